@@ -1,0 +1,207 @@
+/*
+ * gkr_mi355x.h -- C ABI of the MI355X GKR sumcheck prover (matmul + LogUp layers).
+ *
+ * Plain C types only: pointers, sizes and the two value structs below.
+ * Every function returns GKR_OK (0) on success or a GKR_ERR_* code; the
+ * message of the last failure on the calling thread is gkr_last_error().
+ * This mirrors the reference's Result<_, String> convention
+ * (engine/src/backend.rs:85-107, engine/src/gkr/prover.rs:6017-6022).
+ *
+ * Value conventions
+ *   gkr_qm31  {v0, v1, v2, v3} = (v0 + v1*i) + (v2 + v3*i)*u, each word a
+ *             canonical M31 in [0, 2^31 - 1)  (stwo core/fields/qm31.rs:14-33)
+ *   gkr_felt  a canonical felt252 (< 2^251 + 17*2^192 + 1) as 8 little-endian
+ *             u32 words (engine/src/crypto/poseidon_constants.rs:75-86)
+ *   matrices  row-major canonical M31 words (components/matmul.rs:85-107)
+ *   MLE index order: the first variable of a point is the most significant
+ *             index bit (components/matmul.rs:118-136, 342-355).
+ *
+ * Threading: a gkr_ctx owns one HIP stream and its device buffers and is not
+ * re-entrant; use one context per thread, as the reference uses one
+ * executor per thread (engine/src/gpu_sumcheck.rs:1365-1380).
+ */
+#ifndef GKR_MI355X_H
+#define GKR_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+  uint32_t v[4];
+} gkr_qm31;
+
+typedef struct {
+  uint32_t w[8];
+} gkr_felt;
+
+enum {
+  GKR_OK = 0,
+  GKR_ERR_INVALID = 1, /* bad argument or shape */
+  GKR_ERR_DEVICE = 2,  /* HIP runtime failure */
+  GKR_ERR_LOGUP = 3,   /* LogUp trace/table sums disagree (prover.rs:6488-6495) */
+  GKR_ERR_NOMEM = 4,
+  GKR_ERR_BUFFER = 5   /* caller buffer too small */
+};
+
+/* Message of the last error on this thread (never NULL). */
+const char* gkr_last_error(void);
+const char* gkr_version(void);
+
+/* ------------------------------------------------------------------ Poseidon
+ * Replaces starknet_crypto::poseidon_permute_comp / poseidon_hash /
+ * poseidon_hash_many (called at engine/src/crypto/hades.rs:22,
+ * poseidon_channel.rs:222, 249, 294).                                        */
+int gkr_hades_permute(gkr_felt state[3]);
+int gkr_poseidon_hash(const gkr_felt* a, const gkr_felt* b, gkr_felt* out);
+int gkr_poseidon_hash_many(const gkr_felt* in, size_t n, gkr_felt* out);
+
+/* ------------------------------------------------------------------ channel
+ * Replaces PoseidonChannel (engine/src/crypto/poseidon_channel.rs:83-308).   */
+typedef struct gkr_channel gkr_channel;
+int gkr_channel_new(gkr_channel** out);                                    /* PoseidonChannel::new, :98-104 */
+void gkr_channel_free(gkr_channel* ch);
+int gkr_channel_clone(const gkr_channel* ch, gkr_channel** out);           /* #[derive(Clone)], :80 */
+int gkr_channel_mix_u64(gkr_channel* ch, uint64_t v);                      /* mix_u64, :140-142 */
+int gkr_channel_mix_felt(gkr_channel* ch, const gkr_felt* v);              /* mix_felt, :145-151 */
+int gkr_channel_mix_secure_field(gkr_channel* ch, const gkr_qm31* v);      /* gkr/prover.rs:9434-9436 */
+int gkr_channel_mix_felts(gkr_channel* ch, const gkr_qm31* v, size_t n);   /* mix_felts, :261-297 */
+int gkr_channel_mix_poly_coeffs(gkr_channel* ch, const gkr_qm31 c[3]);     /* mix_poly_coeffs, :213-226 */
+int gkr_channel_mix_poly_coeffs_deg3(gkr_channel* ch, const gkr_qm31 c[4]);/* :234-253 */
+int gkr_channel_draw_felt252(gkr_channel* ch, gkr_felt* out);              /* draw_felt252, :156-166 */
+int gkr_channel_draw_qm31(gkr_channel* ch, gkr_qm31* out);                 /* draw_qm31, :176-200 */
+int gkr_channel_draw_qm31s(gkr_channel* ch, size_t n, gkr_qm31* out);      /* draw_qm31s, :203-205 */
+int gkr_channel_digest(const gkr_channel* ch, gkr_felt* out);              /* digest(), :300-302 */
+uint64_t gkr_channel_hash_count(const gkr_channel* ch);                    /* hash_count(), :108-110 */
+/* State as [8 digest words LE, n_draws, hash_count lo, hash_count hi]
+ * (to_gpu_state / from_gpu_state, :115-135): lets a Rust caller hand its
+ * PoseidonChannel over and take it back around each call.                   */
+int gkr_channel_export(const gkr_channel* ch, uint32_t state[11]);
+int gkr_channel_import(gkr_channel* ch, const uint32_t state[11]);
+
+/* ------------------------------------------------------------------ device context */
+typedef struct gkr_ctx gkr_ctx;
+int gkr_ctx_create(int device, gkr_ctx** out);  /* replaces GpuSumcheckExecutor::new/cached, gpu_sumcheck.rs:1309-1380 */
+void gkr_ctx_destroy(gkr_ctx* ctx);
+int gkr_ctx_synchronize(gkr_ctx* ctx);
+/* Per-kernel timing (HIP events on the context stream), for benchmarks.
+ * kernel ids: 0 restrict_cols, 1 restrict_rows, 2 matmul round, 3 eq3 round,
+ * 4 logup prepare, 5 eq table.  Timing adds one event pair per launch.     */
+int gkr_ctx_set_timing(gkr_ctx* ctx, int enabled);
+int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);
+int gkr_ctx_reset_timing(gkr_ctx* ctx);
+
+/* ------------------------------------------------------------------ resident matrices
+ * The reference re-uploads A and B on every restriction
+ * (gpu_sumcheck.rs:2012-2015, 2079-2082); here a matrix is uploaded once
+ * and stays in HBM.  Values must be canonical M31 (< 2^31 - 1).              */
+typedef struct gkr_matrix gkr_matrix;
+int gkr_matrix_upload(gkr_ctx* ctx, const uint32_t* host, uint64_t rows, uint64_t cols, gkr_matrix** out);
+/* Borrow device memory the caller owns (e.g. a torch tensor); not freed here.
+ * The contents must stay unchanged while the matrix is in use.               */
+int gkr_matrix_wrap_device(gkr_ctx* ctx, const uint32_t* device_ptr, uint64_t rows, uint64_t cols,
+                           gkr_matrix** out);
+/* Fill a new resident matrix on the device from the documented synthetic
+ * generator (counter-mode SplitMix64; kind 0 uniform M31, kind 1 int8-range). */
+int gkr_matrix_synthetic(gkr_ctx* ctx, uint64_t rows, uint64_t cols, int kind, uint64_t seed, gkr_matrix** out);
+int gkr_matrix_download(gkr_ctx* ctx, const gkr_matrix* m, uint32_t* host);
+void gkr_matrix_free(gkr_matrix* m);
+/* Host-side copy of the synthetic generator, for callers that need the same
+ * values without a device (value i of the row-major stream).               */
+uint32_t gkr_synthetic_value(int kind, uint64_t seed, uint64_t i);
+
+/* ------------------------------------------------------------------ ZkmlOps
+ * trait ZkmlOps, engine/src/backend.rs:85-107 (CPU impl :110-215, GPU impl
+ * gpu_sumcheck.rs:4484-4525).                                                */
+
+/* ZkmlOps::reduce_matmul_layer (backend.rs:87-94).  A is m x k, B is k x n;
+ * n_r_i = log2(next_pow2(m)), n_r_j = log2(next_pow2(n)),
+ * pk = next_pow2(k).  The transcript (mix_poly_coeffs + draw_qm31 per
+ * round) is applied to `ch` inside, as in the reference.  Outputs:
+ * round_polys[3*t + {0,1,2}] = (c0, c1, c2) of round t, challenges[t],
+ * final_a, final_b; log2(pk) rounds.                                         */
+int gkr_reduce_matmul_layer(gkr_ctx* ctx, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i,
+                            uint32_t n_r_i, const gkr_qm31* r_j, uint32_t n_r_j, uint64_t pk, gkr_channel* ch,
+                            gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b);
+/* ZkmlOps::evaluate_mle_at_point (backend.rs:97-100); len == 2^n_vars. */
+int gkr_evaluate_mle_at_point(gkr_ctx* ctx, const gkr_qm31* mle, uint64_t len, const gkr_qm31* point,
+                              uint32_t n_vars, gkr_qm31* out);
+/* ZkmlOps::restrict_mle (backend.rs:103-106): fixes the first n_assign
+ * variables; out has len >> n_assign entries.                                */
+int gkr_restrict_mle(gkr_ctx* ctx, const gkr_qm31* mle, uint64_t len, const gkr_qm31* assignments,
+                     uint32_t n_assign, gkr_qm31* out);
+
+/* ------------------------------------------------------------------ GKR layer reducers
+ * Proof container (GKRProof, engine/src/gkr/types.rs:589-643).  Layer
+ * reducers append their LayerProof when given a non-NULL proof.              */
+typedef struct gkr_proof gkr_proof;
+int gkr_proof_new(gkr_proof** out);
+void gkr_proof_free(gkr_proof* p);
+size_t gkr_proof_num_layers(const gkr_proof* p);
+int gkr_proof_set_input_claim(gkr_proof* p, const gkr_qm31* point, uint32_t n_vars, const gkr_qm31* value);
+int gkr_proof_add_weight_commitment(gkr_proof* p, const gkr_felt* c);
+int gkr_proof_set_io_commitment(gkr_proof* p, const gkr_felt* c);
+/* serialize_gkr_model_proof (engine/src/cairo_serde.rs:1307-1772) for MatMul
+ * (tag 0) and Activation (tag 3) layers, followed by the input claim, the
+ * weight commitments, the count of weight openings (0: opening proofs are
+ * not produced by this library) and the IO commitment.  Writes up to `cap`
+ * felts; *n_out receives the full length (GKR_ERR_BUFFER when cap is short). */
+int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out);
+
+/* GKR driver seeding (gkr/prover.rs:1527-1560): mix_u64(num_layers),
+ * mix_u64(in_rows), mix_u64(in_cols), then mix_felt(policy_commitment) when
+ * policy != NULL and non-zero (prover.rs:1533-1537).                         */
+int gkr_seed_channel(gkr_channel* ch, uint64_t num_layers, uint64_t in_rows, uint64_t in_cols,
+                     const gkr_felt* policy_commitment);
+
+/* MLE of C = A*B at r_out = (r_i || r_j), computed as sum_l f_a[l]*f_b[l]
+ * from the two restrictions (equal to evaluate_mle(pad(C), r_out) as used
+ * by the driver, prover.rs:1543-1553).  The restrictions are kept and reused
+ * by a following reduce on the same (a, b, r_i, r_j).                       */
+int gkr_matmul_output_claim(gkr_ctx* ctx, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_out,
+                            uint32_t n_vars, gkr_qm31* value);
+
+/* reduce_matmul_layer_with_backend (gkr/prover.rs:5959-6070): mixes m, k, n
+ * and the claim, runs the backend reduction, mixes final_a and final_b.
+ * claim point = r_i || r_j (log2 pm + log2 pn entries).  Outputs the round
+ * polys (3 per round), final evals, and the next claim: point r_i ||
+ * challenges (n_next_point = log2 pm + log2 pk entries) and value final_a.  */
+int gkr_prove_matmul_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                           const gkr_matrix* a, const gkr_matrix* b, gkr_channel* ch, gkr_proof* proof,
+                           gkr_qm31* round_polys, gkr_qm31* final_a, gkr_qm31* final_b, gkr_qm31* next_point,
+                           gkr_qm31* next_value);
+
+/* Outputs of reduce_activation_layer (gkr/prover.rs:6400-6600).  The caller
+ * provides the arrays; sizes: eq_round_polys 4*n_vars, multiplicities
+ * 2^table_log_size, mult_round_polys 2*table_log_size.                       */
+typedef struct {
+  gkr_qm31 claimed_sum;       /* trace-side LogUp sum (LogUpProof::claimed_sum) */
+  gkr_qm31* eq_round_polys;   /* [4*t + {0..3}] = c0..c3 of eq round t */
+  gkr_qm31 w_eval, in_eval, out_eval;   /* LogUpProof::final_evals */
+  uint32_t* multiplicities;
+  gkr_qm31* mult_round_polys; /* [2*t + {0,1}] = (c0, c1) of multiplicity round t */
+  gkr_qm31 mult_final_eval, mult_claimed_sum;
+  gkr_qm31 input_eval, output_eval;
+  gkr_felt table_commitment;
+  gkr_qm31 gamma, beta;       /* LogUp encoding challenges (not serialized) */
+} gkr_logup_out;
+
+/* reduce_activation_layer: input is the rows x cols activation matrix,
+ * activation_type the reference type tag (1 ReLU, 2 GELU, 3 Sigmoid,
+ * 4 Softmax, 5 SiLU), table_log_size the lookup table size (0 = the
+ * reference default: 20 for Softmax, 16 otherwise).  claim_point has
+ * log2(next_pow2(rows) * next_pow2(cols)) entries.                           */
+int gkr_prove_activation_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_point,
+                               const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t activation_type,
+                               uint32_t table_log_size, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out);
+
+/* Activation table output column, f(j) for j < 2^log_size (host). */
+int gkr_activation_table(uint32_t activation_type, uint32_t log_size, uint32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GKR_MI355X_H */

@@ -1,0 +1,345 @@
+"""ctypes wrapper of the CPU oracle (_build/liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Imported only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg, as the checker and the timed CPU baseline.  QM31 values are 4-tuples,
+felts are Python ints, matrices are numpy uint32 arrays.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import List, Sequence
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboracle.so")
+P = (1 << 31) - 1
+
+_lib = None
+_U32P = C.POINTER(C.c_uint32)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = C.CDLL(LIB_PATH)
+        L.orc_channel_size.restype = C.c_size_t
+        L.orc_synthetic_value.restype = C.c_uint32
+        L.orc_synthetic_value.argtypes = [C.c_int, C.c_uint64, C.c_uint64]
+        L.orc_synthetic_fill.argtypes = [_U32P, C.c_size_t, C.c_int, C.c_uint64]
+        L.orc_mix_u64.argtypes = [C.c_void_p, C.c_uint64]
+        L.orc_activation.restype = C.c_uint32
+        L.orc_activation.argtypes = [C.c_uint32, C.c_uint32]
+        for name in ("orc_m31_add", "orc_m31_sub", "orc_m31_mul"):
+            getattr(L, name).restype = C.c_uint32
+            getattr(L, name).argtypes = [C.c_uint32, C.c_uint32]
+        L.orc_m31_inv.restype = C.c_uint32
+        L.orc_m31_inv.argtypes = [C.c_uint32]
+        L.orc_reduce_matmul_layer.argtypes = [_U32P, C.c_size_t, C.c_size_t, _U32P, C.c_size_t, _U32P, C.c_int,
+                                              _U32P, C.c_int, C.c_size_t, C.c_void_p, _U32P, _U32P, _U32P, _U32P]
+        L.orc_prove_matmul_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, C.c_size_t, C.c_size_t, _U32P,
+                                             C.c_size_t, C.c_void_p, _U32P, _U32P, _U32P, _U32P, _U32P]
+        L.orc_matmul_output_claim.argtypes = [_U32P, C.c_size_t, C.c_size_t, _U32P, C.c_size_t, _U32P, C.c_int,
+                                              _U32P]
+        L.orc_matmul_forward.argtypes = [_U32P, C.c_size_t, C.c_size_t, _U32P, C.c_size_t, _U32P]
+        L.orc_restrict_cols_fused.argtypes = [_U32P, C.c_size_t, C.c_size_t, _U32P, C.c_int, C.c_size_t, _U32P]
+        L.orc_restrict_rows_fused.argtypes = [_U32P, C.c_size_t, C.c_size_t, _U32P, C.c_int, C.c_size_t, _U32P]
+        L.orc_restrict_mle.argtypes = [_U32P, C.c_size_t, _U32P, C.c_int, _U32P]
+        L.orc_evaluate_mle.argtypes = [_U32P, C.c_int, _U32P, _U32P]
+        L.orc_prove_activation_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, C.c_size_t, C.c_size_t, C.c_uint32,
+                                                 C.c_uint32, C.c_void_p] + [_U32P] * 9
+        L.orc_verify_matmul_layer.argtypes = [_U32P, C.c_int, _U32P, C.c_size_t, C.c_size_t, C.c_size_t, _U32P,
+                                              C.c_int, _U32P, _U32P, C.c_void_p, _U32P, _U32P]
+        L.orc_verify_activation_layer.argtypes = [_U32P, C.c_int, _U32P, C.c_uint32, C.c_uint32, _U32P, _U32P,
+                                                  C.c_int] + [_U32P] * 6 + [C.c_void_p]
+        _lib = L
+    return _lib
+
+
+def _qa(qs: Sequence[Sequence[int]]) -> np.ndarray:
+    a = np.zeros((max(1, len(qs)), 4), dtype=np.uint32)
+    for i, q in enumerate(qs):
+        a[i] = q
+    return a
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_U32P)
+
+
+def _q(a: np.ndarray, i: int = 0):
+    return tuple(int(x) for x in a.reshape(-1, 4)[i])
+
+
+def felt_words(v: int) -> np.ndarray:
+    return np.array([(v >> (32 * i)) & 0xFFFFFFFF for i in range(8)], dtype=np.uint32)
+
+
+def felt_int(w) -> int:
+    return sum(int(w[i]) << (32 * i) for i in range(8))
+
+
+class Channel:
+    """Oracle PoseidonChannel (engine/src/crypto/poseidon_channel.rs:83-308)."""
+
+    def __init__(self):
+        self.buf = (C.c_uint8 * int(lib().orc_channel_size()))()
+        lib().orc_channel_init(self.buf)
+
+    def clone(self) -> "Channel":
+        c = Channel()
+        C.memmove(c.buf, self.buf, len(self.buf))
+        return c
+
+    def mix_u64(self, v: int):
+        lib().orc_mix_u64(self.buf, v)
+
+    def mix_felt(self, v: int):
+        lib().orc_mix_felt(self.buf, _p(felt_words(v)))
+
+    def mix_secure_field(self, q):
+        lib().orc_mix_secure_field(self.buf, _p(_qa([q])))
+
+    def mix_felts(self, qs):
+        lib().orc_mix_felts(self.buf, _p(_qa(qs)), C.c_size_t(len(qs)))
+
+    def mix_poly_coeffs(self, c0, c1, c2):
+        lib().orc_mix_poly_coeffs(self.buf, _p(_qa([c0, c1, c2])))
+
+    def mix_poly_coeffs_deg3(self, c0, c1, c2, c3):
+        lib().orc_mix_poly_coeffs_deg3(self.buf, _p(_qa([c0, c1, c2, c3])))
+
+    def draw_qm31(self):
+        out = np.zeros(4, dtype=np.uint32)
+        lib().orc_draw_qm31(self.buf, _p(out))
+        return _q(out)
+
+    def draw_qm31s(self, n: int):
+        return [self.draw_qm31() for _ in range(n)]
+
+    def draw_felt252(self) -> int:
+        out = np.zeros(8, dtype=np.uint32)
+        lib().orc_draw_felt252(self.buf, _p(out))
+        return felt_int(out)
+
+    def digest(self) -> int:
+        out = np.zeros(8, dtype=np.uint32)
+        lib().orc_digest(self.buf, _p(out))
+        return felt_int(out)
+
+
+def hash_many(xs: Sequence[int]) -> int:
+    a = np.concatenate([felt_words(x) for x in xs]) if xs else np.zeros(8, dtype=np.uint32)
+    out = np.zeros(8, dtype=np.uint32)
+    lib().orc_hash_many(_p(a), C.c_size_t(len(xs)), _p(out))
+    return felt_int(out)
+
+
+def hades(state: Sequence[int]) -> List[int]:
+    a = np.concatenate([felt_words(x) for x in state])
+    lib().orc_hades(_p(a))
+    return [felt_int(a[8 * i:8 * i + 8]) for i in range(3)]
+
+
+def hades_constant(idx: int) -> int:
+    out = np.zeros(8, dtype=np.uint32)
+    lib().orc_hades_constant(idx, _p(out))
+    return felt_int(out)
+
+
+def qmul(x, y):
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_qm31_mul(_p(_qa([x])), _p(_qa([y])), _p(out))
+    return _q(out)
+
+
+def qadd(x, y):
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_qm31_add(_p(_qa([x])), _p(_qa([y])), _p(out))
+    return _q(out)
+
+
+def qsub(x, y):
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_qm31_sub(_p(_qa([x])), _p(_qa([y])), _p(out))
+    return _q(out)
+
+
+def qinv(x):
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_qm31_inv(_p(_qa([x])), _p(out))
+    return _q(out)
+
+
+def evaluate_mle(evals: Sequence, point: Sequence):
+    e = _qa(evals)
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_evaluate_mle(_p(e), len(point), _p(_qa(point)), _p(out))
+    return _q(out)
+
+
+def restrict_mle(evals: Sequence, assign: Sequence):
+    e = _qa(evals)
+    out = np.zeros((len(evals) >> len(assign), 4), dtype=np.uint32)
+    lib().orc_restrict_mle(_p(e), len(evals), _p(_qa(assign)), len(assign), _p(out))
+    return [_q(out, i) for i in range(out.shape[0])]
+
+
+def eq_evals(r: Sequence):
+    out = np.zeros((1 << len(r), 4), dtype=np.uint32)
+    lib().orc_eq_evals(_p(_qa(r)), len(r), _p(out))
+    return out
+
+
+def lagrange_basis(c: Sequence):
+    out = np.zeros((1 << len(c), 4), dtype=np.uint32)
+    lib().orc_lagrange_basis(_p(_qa(c)), len(c), _p(out))
+    return out
+
+
+def _next_pow2(v: int) -> int:
+    return 1 << max(0, (v - 1).bit_length())
+
+
+def matmul_forward(A: np.ndarray, B: np.ndarray) -> np.ndarray:
+    A = np.ascontiguousarray(A, dtype=np.uint32)
+    B = np.ascontiguousarray(B, dtype=np.uint32)
+    out = np.zeros((A.shape[0], B.shape[1]), dtype=np.uint32)
+    lib().orc_matmul_forward(_p(A), A.shape[0], A.shape[1], _p(B), B.shape[1], _p(out))
+    return out
+
+
+def matmul_output_claim(A: np.ndarray, B: np.ndarray, r_out):
+    A = np.ascontiguousarray(A, dtype=np.uint32)
+    B = np.ascontiguousarray(B, dtype=np.uint32)
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_matmul_output_claim(_p(A), A.shape[0], A.shape[1], _p(B), B.shape[1], _p(_qa(r_out)), len(r_out),
+                                  _p(out))
+    return _q(out)
+
+
+def restrict_cols_fused(B: np.ndarray, r_j, pk: int):
+    B = np.ascontiguousarray(B, dtype=np.uint32)
+    out = np.zeros((pk, 4), dtype=np.uint32)
+    lib().orc_restrict_cols_fused(_p(B), B.shape[0], B.shape[1], _p(_qa(r_j)), len(r_j), pk, _p(out))
+    return out
+
+
+def restrict_rows_fused(A: np.ndarray, r_i, pk: int):
+    A = np.ascontiguousarray(A, dtype=np.uint32)
+    out = np.zeros((pk, 4), dtype=np.uint32)
+    lib().orc_restrict_rows_fused(_p(A), A.shape[0], A.shape[1], _p(_qa(r_i)), len(r_i), pk, _p(out))
+    return out
+
+
+def reduce_matmul_layer(A: np.ndarray, B: np.ndarray, r_i, r_j, pk: int, ch: Channel):
+    """SimdBackend::reduce_matmul_layer (engine/src/backend.rs:111-197)."""
+    A = np.ascontiguousarray(A, dtype=np.uint32)
+    B = np.ascontiguousarray(B, dtype=np.uint32)
+    T = pk.bit_length() - 1
+    rp = np.zeros((max(1, 3 * T), 4), dtype=np.uint32)
+    chal = np.zeros((max(1, T), 4), dtype=np.uint32)
+    fa = np.zeros(4, dtype=np.uint32)
+    fb = np.zeros(4, dtype=np.uint32)
+    rc = lib().orc_reduce_matmul_layer(_p(A), A.shape[0], A.shape[1], _p(B), B.shape[1], _p(_qa(r_i)), len(r_i),
+                                       _p(_qa(r_j)), len(r_j), pk, ch.buf, _p(rp), _p(chal), _p(fa), _p(fb))
+    if rc:
+        raise ValueError(f"oracle reduce_matmul_layer failed ({rc})")
+    return {"round_polys": [(_q(rp, 3 * t), _q(rp, 3 * t + 1), _q(rp, 3 * t + 2)) for t in range(T)],
+            "challenges": [_q(chal, t) for t in range(T)], "final_a_eval": _q(fa), "final_b_eval": _q(fb)}
+
+
+def prove_matmul_layer(claim_point, claim_value, A: np.ndarray, B: np.ndarray, ch: Channel):
+    """reduce_matmul_layer_with_backend (engine/src/gkr/prover.rs:5959-6070)."""
+    A = np.ascontiguousarray(A, dtype=np.uint32)
+    B = np.ascontiguousarray(B, dtype=np.uint32)
+    m, k = A.shape
+    n = B.shape[1]
+    T = _next_pow2(k).bit_length() - 1
+    lm = _next_pow2(m).bit_length() - 1
+    rp = np.zeros((max(1, 3 * T), 4), dtype=np.uint32)
+    fa = np.zeros(4, dtype=np.uint32)
+    fb = np.zeros(4, dtype=np.uint32)
+    npnt = np.zeros((max(1, lm + T), 4), dtype=np.uint32)
+    nv = np.zeros(4, dtype=np.uint32)
+    rc = lib().orc_prove_matmul_layer(_p(_qa(claim_point)), len(claim_point), _p(_qa([claim_value])), _p(A), m, k,
+                                      _p(B), n, ch.buf, _p(rp), _p(fa), _p(fb), _p(npnt), _p(nv))
+    if rc:
+        raise ValueError(f"oracle prove_matmul_layer failed ({rc})")
+    return {"round_polys": [(_q(rp, 3 * t), _q(rp, 3 * t + 1), _q(rp, 3 * t + 2)) for t in range(T)],
+            "final_a_eval": _q(fa), "final_b_eval": _q(fb),
+            "next_point": [_q(npnt, i) for i in range(lm + T)], "next_value": _q(nv)}
+
+
+def prove_activation_layer(claim_point, claim_value, X: np.ndarray, act_type: int, ch: Channel,
+                           table_log_size: int = 0):
+    """reduce_activation_layer (engine/src/gkr/prover.rs:6400-6600)."""
+    if table_log_size == 0:
+        table_log_size = 20 if act_type == 4 else 16
+    X = np.ascontiguousarray(X, dtype=np.uint32)
+    nv = len(claim_point)
+    cs = np.zeros(4, dtype=np.uint32)
+    eq = np.zeros((max(1, 4 * nv), 4), dtype=np.uint32)
+    fe = np.zeros((3, 4), dtype=np.uint32)
+    mults = np.zeros(1 << table_log_size, dtype=np.uint32)
+    mrp = np.zeros((2 * table_log_size, 4), dtype=np.uint32)
+    mfin = np.zeros(4, dtype=np.uint32)
+    msum = np.zeros(4, dtype=np.uint32)
+    ie = np.zeros(4, dtype=np.uint32)
+    tc = np.zeros(8, dtype=np.uint32)
+    rc = lib().orc_prove_activation_layer(_p(_qa(claim_point)), nv, _p(_qa([claim_value])), _p(X), X.shape[0],
+                                          X.shape[1], act_type, table_log_size, ch.buf, _p(cs), _p(eq), _p(fe),
+                                          _p(mults), _p(mrp), _p(mfin), _p(msum), _p(ie), _p(tc))
+    if rc:
+        raise ValueError(f"oracle prove_activation_layer failed ({rc})")
+    return {
+        "claimed_sum": _q(cs),
+        "eq_round_polys": [tuple(_q(eq, 4 * t + j) for j in range(4)) for t in range(nv)],
+        "final_evals": (_q(fe, 0), _q(fe, 1), _q(fe, 2)),
+        "multiplicities": mults,
+        "mult_round_polys": [(_q(mrp, 2 * t), _q(mrp, 2 * t + 1)) for t in range(table_log_size)],
+        "mult_final_eval": _q(mfin),
+        "mult_claimed_sum": _q(msum),
+        "input_eval": _q(ie),
+        "output_eval": tuple(claim_value),
+        "table_commitment": felt_int(tc),
+    }
+
+
+def verify_matmul_layer(claim_point, claim_value, m: int, k: int, n: int, round_polys, final_a, final_b,
+                        ch: Channel) -> int:
+    """verify_matmul_reduction (engine/src/gkr/verifier.rs:2675-2788); 0 = accepted."""
+    c0c2 = _qa([q for rp in round_polys for q in (rp[0], rp[2])])
+    return int(lib().orc_verify_matmul_layer(_p(_qa(claim_point)), len(claim_point), _p(_qa([claim_value])), m, k,
+                                             n, _p(c0c2), len(round_polys), _p(_qa([final_a])), _p(_qa([final_b])),
+                                             ch.buf, None, None))
+
+
+def verify_activation_layer(claim_point, claim_value, act_type: int, table_log: int, proof, ch: Channel) -> int:
+    """verify_activation_reduction, LogUp branch (engine/src/gkr/verifier.rs:3058-3290); 0 = accepted."""
+    c = _qa([q for rp in proof["eq_round_polys"] for q in (rp[0], rp[2], rp[3])])
+    fe = _qa(list(proof["final_evals"]))
+    mults = np.ascontiguousarray(proof["multiplicities"], dtype=np.uint32)
+    mrp = _qa([q for rp in proof["mult_round_polys"] for q in rp])
+    return int(lib().orc_verify_activation_layer(
+        _p(_qa(claim_point)), len(claim_point), _p(_qa([claim_value])), act_type, table_log,
+        _p(_qa([proof["claimed_sum"]])), _p(c), len(proof["eq_round_polys"]), _p(fe), _p(mults), _p(mrp),
+        _p(_qa([proof["mult_final_eval"]])), _p(_qa([proof["mult_claimed_sum"]])), _p(_qa([proof["input_eval"]])),
+        ch.buf))
+
+
+def activation(tag: int, v: int) -> int:
+    return int(lib().orc_activation(tag, v))
+
+
+def synthetic(rows: int, cols: int, kind: int, seed: int) -> np.ndarray:
+    out = np.empty((rows, cols), dtype=np.uint32)
+    lib().orc_synthetic_fill(_p(out), out.size, kind, seed)
+    return out
+
+
+def synthetic_value(kind: int, seed: int, i: int) -> int:
+    return int(lib().orc_synthetic_value(kind, seed, i))

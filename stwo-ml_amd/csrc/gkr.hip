@@ -1,0 +1,1191 @@
+// Host side of the MI355X GKR prover: C ABI (include/gkr_mi355x.h), device
+// context and buffers, the per-round sumcheck loop with the host Poseidon
+// transcript, the LogUp activation reducer and the proof serializer.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/gkr_mi355x.h"
+#include "activations.h"
+#include "field.h"
+#include "kernels.h"
+#include "poseidon.h"
+
+using namespace gkr;
+
+// ------------------------------------------------------------------ errors
+static thread_local std::string g_err = "";
+static int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+#define HIP_TRY(expr)                                                                       \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess) return fail(GKR_ERR_DEVICE, "%s: %s (%s:%d)", #expr,              \
+                                      hipGetErrorString(e_), __FILE__, __LINE__);           \
+  } while (0)
+#define TRY(expr)             \
+  do {                        \
+    int rc_ = (expr);         \
+    if (rc_ != GKR_OK) return rc_; \
+  } while (0)
+
+static inline qm31 Q(const gkr_qm31& x) { return qm31{x.v[0], x.v[1], x.v[2], x.v[3]}; }
+static inline gkr_qm31 G(const qm31& x) {
+  gkr_qm31 r;
+  r.v[0] = x.a; r.v[1] = x.b; r.v[2] = x.c; r.v[3] = x.d;
+  return r;
+}
+static inline bool canonical_q(const gkr_qm31& x) {
+  return x.v[0] < P && x.v[1] < P && x.v[2] < P && x.v[3] < P;
+}
+static inline uint64_t next_pow2(uint64_t v) {
+  uint64_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+static inline int log2_exact(uint64_t v) {
+  int l = 0;
+  while ((1ull << l) < v) l++;
+  return l;
+}
+static inline felt felt_from_abi(const gkr_felt& f) { return felt_to_mont(felt_canon_from_words(f.w)); }
+static inline gkr_felt felt_to_abi(const felt& m) {
+  gkr_felt r;
+  felt_canon_to_words(felt_from_mont(m), r.w);
+  return r;
+}
+static bool felt_abi_canonical(const gkr_felt& f) {
+  felt c = felt_canon_from_words(f.w);
+  return !felt_detail::geq_p(c.l);
+}
+
+// ------------------------------------------------------------------ context
+enum Slot {
+  S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
+  S_TABLE, S_MULT, S_PADIN, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_NSLOTS
+};
+enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
+                K_EQ_TABLE = 5, K_NKERNELS = 6 };
+constexpr int kMaxPartialBlocks = 1024;
+
+struct KernelStat {
+  double ms = 0;
+  uint64_t launches = 0;
+  uint64_t bytes = 0;
+};
+struct PendingTiming {
+  int kid;
+  hipEvent_t e0, e1;
+  uint64_t bytes;
+};
+
+struct MatMulCache {
+  bool valid = false;
+  const gkr_matrix* a = nullptr;
+  const gkr_matrix* b = nullptr;
+  std::vector<gkr_qm31> r_i, r_j;
+  bool have_round0 = false;
+  qm31 round0[3];
+};
+
+struct gkr_matrix {
+  gkr_ctx* ctx;
+  uint32_t* dev;
+  uint64_t rows, cols;
+  bool owned;
+};
+
+struct gkr_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  void* buf[S_NSLOTS] = {};
+  size_t cap[S_NSLOTS] = {};
+  qm31* h_res = nullptr;  // pinned result staging (64 QM31)
+  bool timing = false;
+  KernelStat stats[K_NKERNELS];
+  std::vector<PendingTiming> pending;
+  std::vector<hipEvent_t> free_events;
+  MatMulCache mm;
+  std::map<uint64_t, std::vector<uint32_t>> tables;  // (tag << 32 | log) -> table outputs
+};
+
+static int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
+  if (bytes == 0) bytes = 16;
+  if (c->cap[s] < bytes) {
+    if (c->buf[s]) HIP_TRY(hipFree(c->buf[s]));
+    c->buf[s] = nullptr;
+    c->cap[s] = 0;
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    HIP_TRY(hipMalloc(&c->buf[s], want));
+    c->cap[s] = want;
+  }
+  *out = c->buf[s];
+  return GKR_OK;
+}
+template <typename T>
+static int ensureT(gkr_ctx* c, Slot s, size_t count, T** out) {
+  void* p;
+  TRY(ensure(c, s, count * sizeof(T), &p));
+  *out = (T*)p;
+  return GKR_OK;
+}
+
+static hipEvent_t get_event(gkr_ctx* c) {
+  if (!c->free_events.empty()) {
+    hipEvent_t e = c->free_events.back();
+    c->free_events.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+struct TimedLaunch {
+  gkr_ctx* c;
+  int kid;
+  uint64_t bytes;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
+    if (c->timing) {
+      e0 = get_event(c);
+      e1 = get_event(c);
+      if (e0) (void)hipEventRecord(e0, c->stream);
+    }
+  }
+  ~TimedLaunch() {
+    if (c->timing && e0 && e1) {
+      (void)hipEventRecord(e1, c->stream);
+      c->pending.push_back({kid, e0, e1, bytes});
+    }
+  }
+};
+static void collect_timing(gkr_ctx* c) {
+  for (auto& p : c->pending) {
+    float ms = 0;
+    if (hipEventElapsedTime(&ms, p.e0, p.e1) == hipSuccess) {
+      c->stats[p.kid].ms += ms;
+      c->stats[p.kid].launches++;
+      c->stats[p.kid].bytes += p.bytes;
+    }
+    c->free_events.push_back(p.e0);
+    c->free_events.push_back(p.e1);
+  }
+  c->pending.clear();
+}
+static int sync(gkr_ctx* c) {
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  if (c->timing) collect_timing(c);
+  return GKR_OK;
+}
+static int check_launch() {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(GKR_ERR_DEVICE, "kernel launch: %s", hipGetErrorString(e));
+  return GKR_OK;
+}
+static inline unsigned grid_for(uint64_t n, uint64_t per_block = kBlock) {
+  uint64_t g = (n + per_block - 1) / per_block;
+  return (unsigned)(g == 0 ? 1 : g);
+}
+static inline unsigned partial_grid(uint64_t n) {
+  uint64_t g = (n + kBlock - 1) / kBlock;
+  if (g > kMaxPartialBlocks) g = kMaxPartialBlocks;
+  return (unsigned)(g == 0 ? 1 : g);
+}
+
+static PointArg make_point(const qm31* r, int n) {
+  PointArg p;
+  memset(&p, 0, sizeof p);
+  p.n = n;
+  for (int l = 0; l < n; l++) {
+    p.r[l] = r[l];
+    p.omr[l] = qm31_sub(qm31_one(), r[l]);
+  }
+  return p;
+}
+
+// eq(r, x) for x < count (r[0] on the most significant bit of x).
+static int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out) {
+  if (n > kMaxVars) return fail(GKR_ERR_INVALID, "eq table: %d variables exceeds %d", n, kMaxVars);
+  PointArg pt = make_point(r, n);
+  TimedLaunch t(c, K_EQ_TABLE, 16 * count);
+  if (n <= 10) {
+    hipLaunchKernelGGL(k_eq_direct, dim3(grid_for(count)), dim3(kBlock), 0, c->stream, pt, count, out);
+    return check_launch();
+  }
+  const int h = n / 2;
+  qm31 *hi, *lo;
+  TRY(ensureT(c, S_EQHI, 1ull << (n - h), &hi));
+  TRY(ensureT(c, S_EQLO, 1ull << h, &lo));
+  hipLaunchKernelGGL(k_eq_tables, dim3(grid_for((1ull << (n - h)) + (1ull << h))), dim3(kBlock), 0, c->stream, pt, h,
+                     hi, lo);
+  TRY(check_launch());
+  hipLaunchKernelGGL(k_eq_combine, dim3(grid_for(count)), dim3(kBlock), 0, c->stream, hi, lo, h, count, out);
+  return check_launch();
+}
+
+// Reduce `nblocks` partial rows of NQ QM31 each into h_res[0..NQ) (synchronizes).
+template <int NQ>
+static int finish_partials(gkr_ctx* c, qm31* partials, unsigned nblocks, qm31* host_out) {
+  qm31* d_res;
+  TRY(ensureT(c, S_RES, 64, &d_res));
+  hipLaunchKernelGGL(k_sum_partials<NQ>, dim3(1), dim3(kBlock), 0, c->stream, partials, (int)nblocks, d_res);
+  TRY(check_launch());
+  HIP_TRY(hipMemcpyAsync(c->h_res, d_res, NQ * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
+  TRY(sync(c));
+  for (int q = 0; q < NQ; q++) host_out[q] = c->h_res[q];
+  return GKR_OK;
+}
+static int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out) {
+  HIP_TRY(hipMemcpyAsync(c->h_res, dev, count * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
+  TRY(sync(c));
+  for (int q = 0; q < count; q++) host_out[q] = c->h_res[q];
+  return GKR_OK;
+}
+
+// Partial dot sum_i v[i] * eq[i] (v M31-valued, length n).
+static int dot_m31(gkr_ctx* c, const uint32_t* v, const qm31* eq, uint64_t n, qm31* out) {
+  qm31* part;
+  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
+  unsigned g = partial_grid(n);
+  hipLaunchKernelGGL(k_dot_m31, dim3(g), dim3(kBlock), 0, c->stream, v, eq, n, part);
+  TRY(check_launch());
+  return finish_partials<1>(c, part, g, out);
+}
+
+// ------------------------------------------------------------------ error / version
+extern "C" const char* gkr_last_error(void) { return g_err.c_str(); }
+extern "C" const char* gkr_version(void) { return "gkr_mi355x 0.1 (gfx950)"; }
+
+// ------------------------------------------------------------------ Poseidon ABI
+extern "C" int gkr_hades_permute(gkr_felt state[3]) {
+  if (!state) return fail(GKR_ERR_INVALID, "null state");
+  felt s[3];
+  for (int i = 0; i < 3; i++) {
+    if (!felt_abi_canonical(state[i])) return fail(GKR_ERR_INVALID, "non-canonical felt");
+    s[i] = felt_from_abi(state[i]);
+  }
+  hades_permute(s);
+  for (int i = 0; i < 3; i++) state[i] = felt_to_abi(s[i]);
+  return GKR_OK;
+}
+extern "C" int gkr_poseidon_hash(const gkr_felt* a, const gkr_felt* b, gkr_felt* out) {
+  if (!a || !b || !out) return fail(GKR_ERR_INVALID, "null argument");
+  if (!felt_abi_canonical(*a) || !felt_abi_canonical(*b)) return fail(GKR_ERR_INVALID, "non-canonical felt");
+  *out = felt_to_abi(poseidon_hash(felt_from_abi(*a), felt_from_abi(*b)));
+  return GKR_OK;
+}
+extern "C" int gkr_poseidon_hash_many(const gkr_felt* in, size_t n, gkr_felt* out) {
+  if ((!in && n) || !out) return fail(GKR_ERR_INVALID, "null argument");
+  std::vector<felt> v(n);
+  for (size_t i = 0; i < n; i++) {
+    if (!felt_abi_canonical(in[i])) return fail(GKR_ERR_INVALID, "non-canonical felt at %zu", i);
+    v[i] = felt_from_abi(in[i]);
+  }
+  *out = felt_to_abi(poseidon_hash_many(v.data(), (int)n));
+  return GKR_OK;
+}
+
+// ------------------------------------------------------------------ channel ABI
+struct gkr_channel {
+  PoseidonChannel ch;
+};
+extern "C" int gkr_channel_new(gkr_channel** out) {
+  if (!out) return fail(GKR_ERR_INVALID, "null out");
+  *out = new gkr_channel();
+  return GKR_OK;
+}
+extern "C" void gkr_channel_free(gkr_channel* ch) { delete ch; }
+extern "C" int gkr_channel_clone(const gkr_channel* ch, gkr_channel** out) {
+  if (!ch || !out) return fail(GKR_ERR_INVALID, "null argument");
+  *out = new gkr_channel(*ch);
+  return GKR_OK;
+}
+#define CH_CHECK(ch) \
+  if (!(ch)) return fail(GKR_ERR_INVALID, "null channel")
+extern "C" int gkr_channel_mix_u64(gkr_channel* ch, uint64_t v) {
+  CH_CHECK(ch);
+  ch->ch.mix_u64(v);
+  return GKR_OK;
+}
+extern "C" int gkr_channel_mix_felt(gkr_channel* ch, const gkr_felt* v) {
+  CH_CHECK(ch);
+  if (!v || !felt_abi_canonical(*v)) return fail(GKR_ERR_INVALID, "bad felt");
+  ch->ch.mix_felt(felt_from_abi(*v));
+  return GKR_OK;
+}
+extern "C" int gkr_channel_mix_secure_field(gkr_channel* ch, const gkr_qm31* v) {
+  CH_CHECK(ch);
+  if (!v || !canonical_q(*v)) return fail(GKR_ERR_INVALID, "bad qm31");
+  ch->ch.mix_secure_field(Q(*v));
+  return GKR_OK;
+}
+extern "C" int gkr_channel_mix_felts(gkr_channel* ch, const gkr_qm31* v, size_t n) {
+  CH_CHECK(ch);
+  if (!v && n) return fail(GKR_ERR_INVALID, "null values");
+  std::vector<qm31> q(n);
+  for (size_t i = 0; i < n; i++) {
+    if (!canonical_q(v[i])) return fail(GKR_ERR_INVALID, "non-canonical qm31 at %zu", i);
+    q[i] = Q(v[i]);
+  }
+  ch->ch.mix_felts(q.data(), (int)n);
+  return GKR_OK;
+}
+extern "C" int gkr_channel_mix_poly_coeffs(gkr_channel* ch, const gkr_qm31 c[3]) {
+  CH_CHECK(ch);
+  if (!c) return fail(GKR_ERR_INVALID, "null coefficients");
+  for (int i = 0; i < 3; i++)
+    if (!canonical_q(c[i])) return fail(GKR_ERR_INVALID, "non-canonical coefficient");
+  ch->ch.mix_poly_coeffs(Q(c[0]), Q(c[1]), Q(c[2]));
+  return GKR_OK;
+}
+extern "C" int gkr_channel_mix_poly_coeffs_deg3(gkr_channel* ch, const gkr_qm31 c[4]) {
+  CH_CHECK(ch);
+  if (!c) return fail(GKR_ERR_INVALID, "null coefficients");
+  for (int i = 0; i < 4; i++)
+    if (!canonical_q(c[i])) return fail(GKR_ERR_INVALID, "non-canonical coefficient");
+  ch->ch.mix_poly_coeffs_deg3(Q(c[0]), Q(c[1]), Q(c[2]), Q(c[3]));
+  return GKR_OK;
+}
+extern "C" int gkr_channel_draw_felt252(gkr_channel* ch, gkr_felt* out) {
+  CH_CHECK(ch);
+  if (!out) return fail(GKR_ERR_INVALID, "null out");
+  *out = felt_to_abi(ch->ch.draw_felt252());
+  return GKR_OK;
+}
+extern "C" int gkr_channel_draw_qm31(gkr_channel* ch, gkr_qm31* out) {
+  CH_CHECK(ch);
+  if (!out) return fail(GKR_ERR_INVALID, "null out");
+  *out = G(ch->ch.draw_qm31());
+  return GKR_OK;
+}
+extern "C" int gkr_channel_draw_qm31s(gkr_channel* ch, size_t n, gkr_qm31* out) {
+  CH_CHECK(ch);
+  if (!out && n) return fail(GKR_ERR_INVALID, "null out");
+  for (size_t i = 0; i < n; i++) out[i] = G(ch->ch.draw_qm31());
+  return GKR_OK;
+}
+extern "C" int gkr_channel_digest(const gkr_channel* ch, gkr_felt* out) {
+  CH_CHECK(ch);
+  if (!out) return fail(GKR_ERR_INVALID, "null out");
+  *out = felt_to_abi(ch->ch.digest);
+  return GKR_OK;
+}
+extern "C" uint64_t gkr_channel_hash_count(const gkr_channel* ch) { return ch ? ch->ch.hash_count : 0; }
+extern "C" int gkr_channel_export(const gkr_channel* ch, uint32_t state[11]) {
+  CH_CHECK(ch);
+  if (!state) return fail(GKR_ERR_INVALID, "null state");
+  ch->ch.export_state(state);
+  return GKR_OK;
+}
+extern "C" int gkr_channel_import(gkr_channel* ch, const uint32_t state[11]) {
+  CH_CHECK(ch);
+  if (!state) return fail(GKR_ERR_INVALID, "null state");
+  gkr_felt f;
+  memcpy(f.w, state, sizeof f.w);
+  if (!felt_abi_canonical(f)) return fail(GKR_ERR_INVALID, "non-canonical digest");
+  ch->ch.import_state(state);
+  return GKR_OK;
+}
+extern "C" int gkr_seed_channel(gkr_channel* ch, uint64_t num_layers, uint64_t in_rows, uint64_t in_cols,
+                                const gkr_felt* policy_commitment) {
+  CH_CHECK(ch);
+  ch->ch.mix_u64(num_layers);
+  ch->ch.mix_u64(in_rows);
+  ch->ch.mix_u64(in_cols);
+  if (policy_commitment) {
+    if (!felt_abi_canonical(*policy_commitment)) return fail(GKR_ERR_INVALID, "non-canonical policy commitment");
+    bool zero = true;
+    for (int i = 0; i < 8; i++) zero = zero && policy_commitment->w[i] == 0;
+    if (!zero) ch->ch.mix_felt(felt_from_abi(*policy_commitment));
+  }
+  return GKR_OK;
+}
+
+// ------------------------------------------------------------------ context ABI
+extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
+  if (!out) return fail(GKR_ERR_INVALID, "null out");
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(GKR_ERR_INVALID, "device %d not present (%d devices)", device, n);
+  HIP_TRY(hipSetDevice(device));
+  gkr_ctx* c = new gkr_ctx();
+  c->device = device;
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");
+  }
+  if (hipHostMalloc((void**)&c->h_res, 64 * sizeof(qm31), hipHostMallocDefault) != hipSuccess) {
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return fail(GKR_ERR_DEVICE, "hipHostMalloc failed");
+  }
+  *out = c;
+  return GKR_OK;
+}
+extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (auto& p : c->pending) {
+    (void)hipEventDestroy(p.e0);
+    (void)hipEventDestroy(p.e1);
+  }
+  for (auto e : c->free_events) (void)hipEventDestroy(e);
+  for (int s = 0; s < S_NSLOTS; s++)
+    if (c->buf[s]) (void)hipFree(c->buf[s]);
+  if (c->h_res) (void)hipHostFree(c->h_res);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+extern "C" int gkr_ctx_synchronize(gkr_ctx* c) {
+  if (!c) return fail(GKR_ERR_INVALID, "null ctx");
+  return sync(c);
+}
+extern "C" int gkr_ctx_set_timing(gkr_ctx* c, int enabled) {
+  if (!c) return fail(GKR_ERR_INVALID, "null ctx");
+  TRY(sync(c));
+  c->timing = enabled != 0;
+  return GKR_OK;
+}
+extern "C" int gkr_ctx_kernel_time(gkr_ctx* c, int kid, double* total_ms, uint64_t* launches, uint64_t* bytes) {
+  if (!c || kid < 0 || kid >= K_NKERNELS) return fail(GKR_ERR_INVALID, "bad ctx or kernel id");
+  TRY(sync(c));
+  if (total_ms) *total_ms = c->stats[kid].ms;
+  if (launches) *launches = c->stats[kid].launches;
+  if (bytes) *bytes = c->stats[kid].bytes;
+  return GKR_OK;
+}
+extern "C" int gkr_ctx_reset_timing(gkr_ctx* c) {
+  if (!c) return fail(GKR_ERR_INVALID, "null ctx");
+  TRY(sync(c));
+  for (auto& s : c->stats) s = KernelStat();
+  return GKR_OK;
+}
+
+// ------------------------------------------------------------------ matrices
+extern "C" int gkr_matrix_upload(gkr_ctx* c, const uint32_t* host, uint64_t rows, uint64_t cols, gkr_matrix** out) {
+  if (!c || !out || (!host && rows * cols)) return fail(GKR_ERR_INVALID, "null argument");
+  if (rows == 0 || cols == 0) return fail(GKR_ERR_INVALID, "empty matrix %llux%llu", (unsigned long long)rows,
+                                          (unsigned long long)cols);
+  const uint64_t n = rows * cols;
+  for (uint64_t i = 0; i < n; i++)
+    if (host[i] >= P) return fail(GKR_ERR_INVALID, "matrix value %u at %llu is not a canonical M31", host[i],
+                                  (unsigned long long)i);
+  uint32_t* d = nullptr;
+  HIP_TRY(hipMalloc(&d, n * sizeof(uint32_t)));
+  hipError_t e = hipMemcpyAsync(d, host, n * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return fail(GKR_ERR_DEVICE, "matrix upload: %s", hipGetErrorString(e));
+  }
+  *out = new gkr_matrix{c, d, rows, cols, true};
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_wrap_device(gkr_ctx* c, const uint32_t* dev, uint64_t rows, uint64_t cols, gkr_matrix** out) {
+  if (!c || !out || !dev) return fail(GKR_ERR_INVALID, "null argument");
+  if (rows == 0 || cols == 0) return fail(GKR_ERR_INVALID, "empty matrix");
+  *out = new gkr_matrix{c, const_cast<uint32_t*>(dev), rows, cols, false};
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_synthetic(gkr_ctx* c, uint64_t rows, uint64_t cols, int kind, uint64_t seed,
+                                    gkr_matrix** out) {
+  if (!c || !out) return fail(GKR_ERR_INVALID, "null argument");
+  if (rows == 0 || cols == 0) return fail(GKR_ERR_INVALID, "empty matrix");
+  if (kind != 0 && kind != 1) return fail(GKR_ERR_INVALID, "unknown synthetic kind %d", kind);
+  const uint64_t n = rows * cols;
+  uint32_t* d = nullptr;
+  HIP_TRY(hipMalloc(&d, n * sizeof(uint32_t)));
+  hipLaunchKernelGGL(k_fill_synth, dim3(partial_grid(n) * 8), dim3(kBlock), 0, c->stream, d, n, kind, seed);
+  int rc = check_launch();
+  if (rc == GKR_OK) rc = sync(c);
+  if (rc != GKR_OK) {
+    (void)hipFree(d);
+    return rc;
+  }
+  *out = new gkr_matrix{c, d, rows, cols, true};
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_download(gkr_ctx* c, const gkr_matrix* m, uint32_t* host) {
+  if (!c || !m || !host) return fail(GKR_ERR_INVALID, "null argument");
+  HIP_TRY(hipMemcpyAsync(host, m->dev, m->rows * m->cols * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+  return sync(c);
+}
+extern "C" void gkr_matrix_free(gkr_matrix* m) {
+  if (!m) return;
+  if (m->ctx && m->ctx->mm.a == m) m->ctx->mm.valid = false;
+  if (m->ctx && m->ctx->mm.b == m) m->ctx->mm.valid = false;
+  if (m->owned && m->dev) {
+    (void)hipStreamSynchronize(m->ctx->stream);
+    (void)hipFree(m->dev);
+  }
+  delete m;
+}
+extern "C" uint32_t gkr_synthetic_value(int kind, uint64_t seed, uint64_t i) { return synth_value(kind, seed, i); }
+
+// ------------------------------------------------------------------ matmul reduction
+// Restrict A rows by r_i and B columns by r_j into f_a (S_FA0) and f_b (S_FB0),
+// each of length pk (components/matmul.rs:470-565, backend.rs:127-134).
+static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, const qm31* r_i, int n_ri,
+                         const qm31* r_j, int n_rj, uint64_t pk) {
+  const uint64_t m = A->rows, k = A->cols, n = B->cols;
+  qm31 *Li, *Lj, *fa, *fb;
+  TRY(ensureT(c, S_LI, m, &Li));
+  TRY(ensureT(c, S_LJ, n, &Lj));
+  TRY(ensureT(c, S_FA0, pk, &fa));
+  TRY(ensureT(c, S_FB0, pk, &fb));
+  TRY(eq_table(c, r_i, n_ri, m, Li));
+  TRY(eq_table(c, r_j, n_rj, n, Lj));
+  {
+    TimedLaunch t(c, K_RESTRICT_ROWS, 4 * m * k + 16 * m + 16 * pk);
+    hipLaunchKernelGGL(k_restrict_rows, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, A->dev, m, k, pk, Li, fa);
+    TRY(check_launch());
+  }
+  {
+    TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + 16 * pk);
+    const unsigned g = (unsigned)((k + kRowsPerBlock - 1) / kRowsPerBlock);
+    if (n % 4 == 0)
+      hipLaunchKernelGGL(k_restrict_cols<true>, dim3(g), dim3(kBlock), 0, c->stream, B->dev, k, n, Lj, fb);
+    else
+      hipLaunchKernelGGL(k_restrict_cols<false>, dim3(g), dim3(kBlock), 0, c->stream, B->dev, k, n, Lj, fb);
+    TRY(check_launch());
+  }
+  if (pk > k) {
+    hipLaunchKernelGGL(k_zero_q, dim3(grid_for(pk - k)), dim3(kBlock), 0, c->stream, fb, k, pk);
+    TRY(check_launch());
+  }
+  return GKR_OK;
+}
+
+static int round0_sums(gkr_ctx* c, uint64_t pk, qm31 s[3]) {
+  qm31 *fa, *fb, *part;
+  TRY(ensureT(c, S_FA0, pk, &fa));
+  TRY(ensureT(c, S_FB0, pk, &fb));
+  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
+  const uint64_t half = pk / 2;
+  const unsigned g = partial_grid(half);
+  {
+    TimedLaunch t(c, K_MM_ROUND, 32 * pk);
+    hipLaunchKernelGGL(k_mm_round, dim3(g), dim3(kBlock), 0, c->stream, fa, fb, (qm31*)nullptr, (qm31*)nullptr, half, 0,
+                       qm31_zero(), part);
+    TRY(check_launch());
+  }
+  return finish_partials<3>(c, part, g, s);
+}
+
+static bool cache_matches(const gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, int n_ri,
+                          const gkr_qm31* r_j, int n_rj) {
+  const MatMulCache& mm = c->mm;
+  if (!mm.valid || mm.a != a || mm.b != b || (int)mm.r_i.size() != n_ri || (int)mm.r_j.size() != n_rj) return false;
+  if (n_ri && memcmp(mm.r_i.data(), r_i, n_ri * sizeof(gkr_qm31))) return false;
+  if (n_rj && memcmp(mm.r_j.data(), r_j, n_rj * sizeof(gkr_qm31))) return false;
+  return true;
+}
+
+static int validate_matmul(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, uint32_t n_ri, uint32_t n_rj) {
+  if (!c || !a || !b) return fail(GKR_ERR_INVALID, "null argument");
+  if (a->ctx != c || b->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another context");
+  if (a->cols != b->rows)
+    return fail(GKR_ERR_INVALID, "shape mismatch: A is %llux%llu, B is %llux%llu", (unsigned long long)a->rows,
+                (unsigned long long)a->cols, (unsigned long long)b->rows, (unsigned long long)b->cols);
+  if ((int)n_ri != log2_exact(next_pow2(a->rows)))
+    return fail(GKR_ERR_INVALID, "r_i has %u entries, expected %d", n_ri, log2_exact(next_pow2(a->rows)));
+  if ((int)n_rj != log2_exact(next_pow2(b->cols)))
+    return fail(GKR_ERR_INVALID, "r_j has %u entries, expected %d", n_rj, log2_exact(next_pow2(b->cols)));
+  return GKR_OK;
+}
+
+static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, uint32_t n_ri,
+                             const gkr_qm31* r_j, uint32_t n_rj) {
+  if (cache_matches(c, a, b, r_i, (int)n_ri, r_j, (int)n_rj)) return GKR_OK;
+  std::vector<qm31> ri(n_ri), rj(n_rj);
+  for (uint32_t l = 0; l < n_ri; l++) {
+    if (!canonical_q(r_i[l])) return fail(GKR_ERR_INVALID, "r_i[%u] not canonical", l);
+    ri[l] = Q(r_i[l]);
+  }
+  for (uint32_t l = 0; l < n_rj; l++) {
+    if (!canonical_q(r_j[l])) return fail(GKR_ERR_INVALID, "r_j[%u] not canonical", l);
+    rj[l] = Q(r_j[l]);
+  }
+  c->mm.valid = false;
+  const uint64_t pk = next_pow2(a->cols);
+  TRY(restrict_pair(c, a, b, ri.data(), (int)n_ri, rj.data(), (int)n_rj, pk));
+  c->mm.valid = true;
+  c->mm.a = a;
+  c->mm.b = b;
+  c->mm.r_i.assign(r_i, r_i + n_ri);
+  c->mm.r_j.assign(r_j, r_j + n_rj);
+  c->mm.have_round0 = false;
+  return GKR_OK;
+}
+
+static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, uint32_t n_ri,
+                              const gkr_qm31* r_j, uint32_t n_rj, uint64_t pk, PoseidonChannel& ch,
+                              gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b) {
+  TRY(validate_matmul(c, a, b, n_ri, n_rj));
+  if (pk != next_pow2(a->cols))
+    return fail(GKR_ERR_INVALID, "pk=%llu but next_pow2(k)=%llu", (unsigned long long)pk,
+                (unsigned long long)next_pow2(a->cols));
+  HIP_TRY(hipSetDevice(c->device));
+  TRY(ensure_restricted(c, a, b, r_i, n_ri, r_j, n_rj));
+  const int T = log2_exact(pk);
+  qm31 *fa0, *fa1, *fb0, *fb1, *part, *dres;
+  TRY(ensureT(c, S_FA0, pk, &fa0));
+  TRY(ensureT(c, S_FB0, pk, &fb0));
+  TRY(ensureT(c, S_FA1, pk / 2 + 1, &fa1));
+  TRY(ensureT(c, S_FB1, pk / 2 + 1, &fb1));
+  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
+  TRY(ensureT(c, S_RES, 64, &dres));
+  // The folds below overwrite the restricted vectors' successors only;
+  // S_FA0/S_FB0 keep round 0 input, so a cached restriction stays valid.
+  if (T == 0) {
+    qm31 v[1];
+    TRY(fetch_q(c, fa0, 1, v));
+    *final_a = G(v[0]);
+    TRY(fetch_q(c, fb0, 1, v));
+    *final_b = G(v[0]);
+    return GKR_OK;
+  }
+  const qm31 inv2 = qm31_from_m31(1u << 30);  // 2^-1 mod P
+  const qm31* cur_a = fa0;
+  const qm31* cur_b = fb0;
+  qm31* bufs_a[2] = {fa1, fa0};
+  qm31* bufs_b[2] = {fb1, fb0};
+  // Round t >= 1 folds into bufs[(t-1)&1]; after round 1 the vectors are no
+  // longer needed in S_FA0 except as ping-pong space, so mark the cache stale.
+  qm31 alpha = qm31_zero();
+  for (int t = 0; t < T; t++) {
+    const uint64_t half = (pk >> t) / 2;
+    qm31 s[3];
+    if (t == 0 && c->mm.have_round0) {
+      s[0] = c->mm.round0[0]; s[1] = c->mm.round0[1]; s[2] = c->mm.round0[2];
+    } else if (t == 0) {
+      TRY(round0_sums(c, pk, s));
+    } else {
+      qm31* na = (t == 1) ? fa1 : bufs_a[(t - 1) & 1];
+      qm31* nb = (t == 1) ? fb1 : bufs_b[(t - 1) & 1];
+      if (t == 2) c->mm.valid = false;  // round 2 writes into S_FA0 / S_FB0
+      const unsigned g = partial_grid(half);
+      {
+        // algorithmic bytes: 2 vectors x (read 4*half + write 2*half) QM31 = 48 * n_{t-1}
+        TimedLaunch tl(c, K_MM_ROUND, 192 * half);
+        hipLaunchKernelGGL(k_mm_round, dim3(g), dim3(kBlock), 0, c->stream, cur_a, cur_b, na, nb, half, 1, alpha, part);
+        TRY(check_launch());
+      }
+      TRY(finish_partials<3>(c, part, g, s));
+      cur_a = na;
+      cur_b = nb;
+    }
+    const qm31 c0 = s[0];
+    const qm31 c2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
+    const qm31 c1 = qm31_sub(qm31_sub(s[1], s[0]), c2);
+    round_polys[3 * t + 0] = G(c0);
+    round_polys[3 * t + 1] = G(c1);
+    round_polys[3 * t + 2] = G(c2);
+    ch.mix_poly_coeffs(c0, c1, c2);
+    alpha = ch.draw_qm31();
+    challenges[t] = G(alpha);
+  }
+  c->mm.valid = c->mm.valid && T < 2;
+  hipLaunchKernelGGL(k_mm_final, dim3(1), dim3(64), 0, c->stream, cur_a, cur_b, alpha, dres);
+  TRY(check_launch());
+  qm31 fin[2];
+  TRY(fetch_q(c, dres, 2, fin));
+  *final_a = G(fin[0]);
+  *final_b = G(fin[1]);
+  return GKR_OK;
+}
+
+extern "C" int gkr_reduce_matmul_layer(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i,
+                                       uint32_t n_r_i, const gkr_qm31* r_j, uint32_t n_r_j, uint64_t pk,
+                                       gkr_channel* ch, gkr_qm31* round_polys, gkr_qm31* challenges,
+                                       gkr_qm31* final_a, gkr_qm31* final_b) {
+  CH_CHECK(ch);
+  if (!final_a || !final_b || ((!round_polys || !challenges) && pk > 1) || (!r_i && n_r_i) || (!r_j && n_r_j))
+    return fail(GKR_ERR_INVALID, "null argument");
+  return reduce_matmul_impl(c, a, b, r_i, n_r_i, r_j, n_r_j, pk, ch->ch, round_polys, challenges, final_a, final_b);
+}
+
+extern "C" int gkr_matmul_output_claim(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_out,
+                                       uint32_t n_vars, gkr_qm31* value) {
+  if (!c || !a || !b || !value || (!r_out && n_vars)) return fail(GKR_ERR_INVALID, "null argument");
+  const uint32_t n_ri = (uint32_t)log2_exact(next_pow2(a->rows));
+  if (n_vars < n_ri) return fail(GKR_ERR_INVALID, "point too short");
+  TRY(validate_matmul(c, a, b, n_ri, n_vars - n_ri));
+  HIP_TRY(hipSetDevice(c->device));
+  TRY(ensure_restricted(c, a, b, r_out, n_ri, r_out + n_ri, n_vars - n_ri));
+  const uint64_t pk = next_pow2(a->cols);
+  qm31 s[3];
+  if (pk == 1) {
+    qm31 fa[1], fb[1];
+    qm31 *dfa, *dfb;
+    TRY(ensureT(c, S_FA0, 1, &dfa));
+    TRY(ensureT(c, S_FB0, 1, &dfb));
+    TRY(fetch_q(c, dfa, 1, fa));
+    TRY(fetch_q(c, dfb, 1, fb));
+    *value = G(qm31_mul(fa[0], fb[0]));
+    return GKR_OK;
+  }
+  TRY(round0_sums(c, pk, s));
+  c->mm.have_round0 = true;
+  c->mm.round0[0] = s[0]; c->mm.round0[1] = s[1]; c->mm.round0[2] = s[2];
+  *value = G(qm31_add(s[0], s[1]));
+  return GKR_OK;
+}
+
+// ------------------------------------------------------------------ proof container
+struct LayerRec {
+  uint32_t tag;  // 0 MatMul, 3 Activation
+  std::vector<qm31> rp;  // MatMul: c0,c1,c2 per round; Activation: eq c0..c3 per round
+  qm31 final_a, final_b;
+  uint32_t act_type = 0;
+  qm31 input_eval, output_eval;
+  felt table_commitment;
+  qm31 claimed_sum, w_eval, in_eval, out_eval;
+  std::vector<uint32_t> mults;
+  std::vector<qm31> mult_rp;  // c0,c1 per round
+  qm31 mult_final, mult_sum;
+};
+struct gkr_proof {
+  std::vector<LayerRec> layers;
+  std::vector<qm31> in_point;
+  qm31 in_value = {0, 0, 0, 0};
+  std::vector<felt> weight_commitments;
+  felt io_commitment = {{0, 0, 0, 0}};
+};
+extern "C" int gkr_proof_new(gkr_proof** out) {
+  if (!out) return fail(GKR_ERR_INVALID, "null out");
+  *out = new gkr_proof();
+  return GKR_OK;
+}
+extern "C" void gkr_proof_free(gkr_proof* p) { delete p; }
+extern "C" size_t gkr_proof_num_layers(const gkr_proof* p) { return p ? p->layers.size() : 0; }
+extern "C" int gkr_proof_set_input_claim(gkr_proof* p, const gkr_qm31* point, uint32_t n, const gkr_qm31* value) {
+  if (!p || !value || (!point && n)) return fail(GKR_ERR_INVALID, "null argument");
+  p->in_point.clear();
+  for (uint32_t i = 0; i < n; i++) p->in_point.push_back(Q(point[i]));
+  p->in_value = Q(*value);
+  return GKR_OK;
+}
+extern "C" int gkr_proof_add_weight_commitment(gkr_proof* p, const gkr_felt* cm) {
+  if (!p || !cm || !felt_abi_canonical(*cm)) return fail(GKR_ERR_INVALID, "bad argument");
+  p->weight_commitments.push_back(felt_canon_from_words(cm->w));
+  return GKR_OK;
+}
+extern "C" int gkr_proof_set_io_commitment(gkr_proof* p, const gkr_felt* cm) {
+  if (!p || !cm || !felt_abi_canonical(*cm)) return fail(GKR_ERR_INVALID, "bad argument");
+  p->io_commitment = felt_canon_from_words(cm->w);
+  return GKR_OK;
+}
+
+// serialize_gkr_model_proof (cairo_serde.rs:1307-1772); felts kept canonical.
+struct Ser {
+  std::vector<felt> out;
+  void u(uint64_t v) { out.push_back(felt{{v, 0, 0, 0}}); }
+  void q(const qm31& x) { u(x.a); u(x.b); u(x.c); u(x.d); }
+  void f(const felt& canon) { out.push_back(canon); }
+};
+extern "C" int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out) {
+  if (!p || !n_out || (!out && cap)) return fail(GKR_ERR_INVALID, "null argument");
+  Ser s;
+  s.u(p->layers.size());
+  for (const LayerRec& L : p->layers) {
+    if (L.tag == 0) {
+      s.u(0);
+      const size_t nr = L.rp.size() / 3;
+      s.u(nr);
+      for (size_t r = 0; r < nr; r++) {  // c1 omitted (cairo_serde.rs:1327-1331)
+        s.q(L.rp[3 * r]);
+        s.q(L.rp[3 * r + 2]);
+      }
+      s.q(L.final_a);
+      s.q(L.final_b);
+    } else {
+      s.u(3);
+      s.u(L.act_type);
+      s.q(L.input_eval);
+      s.q(L.output_eval);
+      s.f(L.table_commitment);
+      s.u(1);  // has LogUp proof
+      // serialize_logup_proof_inner with multiplicities (cairo_serde.rs:1080-1105)
+      s.q(L.claimed_sum);
+      const size_t nr = L.rp.size() / 4;
+      s.u(nr);
+      for (size_t r = 0; r < nr; r++) {
+        s.q(L.rp[4 * r]);
+        s.q(L.rp[4 * r + 2]);
+        s.q(L.rp[4 * r + 3]);
+      }
+      s.q(L.w_eval);
+      s.q(L.in_eval);
+      s.q(L.out_eval);
+      s.u(L.mults.size());
+      for (uint32_t m : L.mults) s.u(m);
+      // serialize_multiplicity_sumcheck (cairo_serde.rs:1138-1156)
+      s.u(1);
+      const size_t nm = L.mult_rp.size() / 2;
+      s.u(nm);
+      for (size_t r = 0; r < nm; r++) {
+        s.q(L.mult_rp[2 * r]);
+        s.q(L.mult_rp[2 * r + 1]);
+      }
+      s.q(L.mult_final);
+      s.q(L.mult_sum);
+      s.u(0);  // no activation product proof
+      s.u(0);  // no piecewise proof
+    }
+  }
+  s.u(p->in_point.size());
+  for (const qm31& x : p->in_point) s.q(x);
+  s.q(p->in_value);
+  s.u(p->weight_commitments.size());
+  for (const felt& w : p->weight_commitments) s.f(w);
+  s.u(0);  // weight opening proofs are not produced here
+  s.f(p->io_commitment);
+  *n_out = s.out.size();
+  for (size_t i = 0; i < s.out.size() && i < cap; i++) felt_canon_to_words(s.out[i], out[i].w);
+  if (cap < s.out.size()) return fail(GKR_ERR_BUFFER, "need %zu felts, have %zu", s.out.size(), cap);
+  return GKR_OK;
+}
+
+extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
+                                      const gkr_qm31* claim_value, const gkr_matrix* a, const gkr_matrix* b,
+                                      gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys, gkr_qm31* final_a,
+                                      gkr_qm31* final_b, gkr_qm31* next_point, gkr_qm31* next_value) {
+  CH_CHECK(ch);
+  if (!c || !a || !b || !claim_value || !final_a || !final_b || !next_value || (!claim_point && n_point))
+    return fail(GKR_ERR_INVALID, "null argument");
+  if (!canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
+  const uint64_t pm = next_pow2(a->rows), pk = next_pow2(a->cols), pn = next_pow2(b->cols);
+  const uint32_t log_m = (uint32_t)log2_exact(pm), log_n = (uint32_t)log2_exact(pn);
+  const int T = log2_exact(pk);
+  if (n_point != log_m + log_n)
+    return fail(GKR_ERR_INVALID, "output claim has %u vars, expected exactly %u (log_m=%u + log_n=%u)", n_point,
+                log_m + log_n, log_m, log_n);
+  if (T > 0 && (!round_polys || !next_point)) return fail(GKR_ERR_INVALID, "null output buffer");
+  TRY(validate_matmul(c, a, b, log_m, log_n));
+  PoseidonChannel& C = ch->ch;
+  C.mix_u64(a->rows);
+  C.mix_u64(a->cols);
+  C.mix_u64(b->cols);
+  C.mix_secure_field(Q(*claim_value));
+  std::vector<gkr_qm31> chal(T > 0 ? T : 1);
+  TRY(reduce_matmul_impl(c, a, b, claim_point, log_m, claim_point + log_m, log_n, pk, C, round_polys, chal.data(),
+                         final_a, final_b));
+  C.mix_secure_field(Q(*final_a));
+  C.mix_secure_field(Q(*final_b));
+  if (next_point) {
+    for (uint32_t l = 0; l < log_m; l++) next_point[l] = claim_point[l];
+    for (int t = 0; t < T; t++) next_point[log_m + t] = chal[t];
+  }
+  *next_value = *final_a;
+  if (proof) {
+    LayerRec L;
+    L.tag = 0;
+    for (int t = 0; t < 3 * T; t++) L.rp.push_back(Q(round_polys[t]));
+    L.final_a = Q(*final_a);
+    L.final_b = Q(*final_b);
+    proof->layers.push_back(L);
+  }
+  return GKR_OK;
+}
+
+// ------------------------------------------------------------------ ZkmlOps MLE helpers
+extern "C" int gkr_evaluate_mle_at_point(gkr_ctx* c, const gkr_qm31* mle, uint64_t len, const gkr_qm31* point,
+                                         uint32_t n_vars, gkr_qm31* out) {
+  if (!c || !mle || !out || (!point && n_vars)) return fail(GKR_ERR_INVALID, "null argument");
+  if (n_vars >= 64 || len != (1ull << n_vars))
+    return fail(GKR_ERR_INVALID, "evals length must be 2^n_vars (len=%llu, n_vars=%u)", (unsigned long long)len, n_vars);
+  HIP_TRY(hipSetDevice(c->device));
+  std::vector<qm31> pt(n_vars);
+  for (uint32_t l = 0; l < n_vars; l++) {
+    if (!canonical_q(point[l])) return fail(GKR_ERR_INVALID, "point not canonical");
+    pt[l] = Q(point[l]);
+  }
+  qm31 *dm, *eq, *part;
+  TRY(ensureT(c, S_MLE, len, &dm));
+  TRY(ensureT(c, S_EQ, len, &eq));
+  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
+  HIP_TRY(hipMemcpyAsync(dm, mle, len * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
+  TRY(eq_table(c, pt.data(), (int)n_vars, len, eq));
+  const unsigned g = partial_grid(len);
+  hipLaunchKernelGGL(k_dot_q, dim3(g), dim3(kBlock), 0, c->stream, dm, eq, len, part);
+  TRY(check_launch());
+  qm31 r[1];
+  TRY(finish_partials<1>(c, part, g, r));
+  *out = G(r[0]);
+  return GKR_OK;
+}
+extern "C" int gkr_restrict_mle(gkr_ctx* c, const gkr_qm31* mle, uint64_t len, const gkr_qm31* assign,
+                                uint32_t n_assign, gkr_qm31* out) {
+  if (!c || !mle || !out || (!assign && n_assign)) return fail(GKR_ERR_INVALID, "null argument");
+  if (len == 0 || (len & (len - 1)) || (n_assign >= 64) || (1ull << n_assign) > len)
+    return fail(GKR_ERR_INVALID, "bad MLE length %llu for %u assignments", (unsigned long long)len, n_assign);
+  HIP_TRY(hipSetDevice(c->device));
+  std::vector<qm31> pt(n_assign);
+  for (uint32_t l = 0; l < n_assign; l++) {
+    if (!canonical_q(assign[l])) return fail(GKR_ERR_INVALID, "assignment not canonical");
+    pt[l] = Q(assign[l]);
+  }
+  const uint64_t nx = 1ull << n_assign, rest = len >> n_assign;
+  qm31 *dm, *eq, *dout;
+  TRY(ensureT(c, S_MLE, len, &dm));
+  TRY(ensureT(c, S_EQ, nx, &eq));
+  TRY(ensureT(c, S_OUT, rest, &dout));
+  HIP_TRY(hipMemcpyAsync(dm, mle, len * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
+  TRY(eq_table(c, pt.data(), (int)n_assign, nx, eq));
+  hipLaunchKernelGGL(k_restrict_q, dim3(grid_for(rest)), dim3(kBlock), 0, c->stream, dm, eq, nx, rest, dout);
+  TRY(check_launch());
+  HIP_TRY(hipMemcpyAsync(out, dout, rest * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
+  return sync(c);
+}
+
+// ------------------------------------------------------------------ LogUp activation layer
+extern "C" int gkr_activation_table(uint32_t tag, uint32_t log_size, uint32_t* out) {
+  if (!out || !act_valid(tag) || log_size == 0 || log_size > 24) return fail(GKR_ERR_INVALID, "bad argument");
+  std::vector<uint32_t> t = act_table(tag, log_size);
+  memcpy(out, t.data(), t.size() * sizeof(uint32_t));
+  return GKR_OK;
+}
+
+static const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint32_t log_size) {
+  const uint64_t key = ((uint64_t)tag << 32) | log_size;
+  auto it = c->tables.find(key);
+  if (it == c->tables.end()) it = c->tables.emplace(key, act_table(tag, log_size)).first;
+  return it->second;
+}
+
+extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
+                                          const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t tag,
+                                          uint32_t table_log, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out) {
+  CH_CHECK(ch);
+  if (!c || !input || !claim_value || !out || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
+  if (!act_valid(tag)) return fail(GKR_ERR_INVALID, "unknown activation type %u", tag);
+  if (table_log == 0) table_log = act_default_log_size(tag);
+  if (table_log > 24) return fail(GKR_ERR_INVALID, "table_log_size %u too large", table_log);
+  if (input->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another context");
+  const uint64_t prow = next_pow2(input->rows), pcol = next_pow2(input->cols);
+  const uint64_t n = prow * pcol;
+  const int nv = log2_exact(n);
+  if ((int)n_point != nv)
+    return fail(GKR_ERR_INVALID, "claim point has %u vars, activation MLE has %d", n_point, nv);
+  if (nv > kMaxVars) return fail(GKR_ERR_INVALID, "activation too large");
+  if (!out->eq_round_polys && nv > 0) return fail(GKR_ERR_INVALID, "null eq_round_polys");
+  if (!out->multiplicities || !out->mult_round_polys) return fail(GKR_ERR_INVALID, "null output arrays");
+  if (!canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
+  std::vector<qm31> cpt(n_point);
+  for (uint32_t l = 0; l < n_point; l++) {
+    if (!canonical_q(claim_point[l])) return fail(GKR_ERR_INVALID, "claim point not canonical");
+    cpt[l] = Q(claim_point[l]);
+  }
+  HIP_TRY(hipSetDevice(c->device));
+  c->mm.valid = false;
+  PoseidonChannel& C = ch->ch;
+  const uint64_t tsize = 1ull << table_log;
+  const uint32_t mask = (uint32_t)(tsize - 1);
+  const std::vector<uint32_t>& table = cached_table(c, tag, table_log);
+
+  uint32_t *d_table, *d_mult, *d_pad, *d_min, *d_mout;
+  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *d_e1, *part, *dres;
+  TRY(ensureT(c, S_TABLE, tsize, &d_table));
+  TRY(ensureT(c, S_MULT, tsize, &d_mult));
+  TRY(ensureT(c, S_PADIN, n, &d_pad));
+  TRY(ensureT(c, S_MIN, n, &d_min));
+  TRY(ensureT(c, S_MOUT, n, &d_mout));
+  TRY(ensureT(c, S_D0, n, &d_d0));
+  TRY(ensureT(c, S_D1, n / 2 + 1, &d_d1));
+  TRY(ensureT(c, S_W0, n, &d_w0));
+  TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
+  TRY(ensureT(c, S_E0, n, &d_e0));
+  TRY(ensureT(c, S_E1, n / 2 + 1, &d_e1));
+  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
+  TRY(ensureT(c, S_RES, 64, &dres));
+  HIP_TRY(hipMemcpyAsync(d_table, table.data(), tsize * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
+
+  // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
+  C.mix_u64(0x4C4F47ull);
+  C.mix_u64(tag);
+  const qm31 gamma = C.draw_qm31();
+  const qm31 beta = C.draw_qm31();
+  out->gamma = G(gamma);
+  out->beta = G(beta);
+
+  qm31 trace_sum, table_sum;
+  {
+    const unsigned g = partial_grid(n);
+    {
+      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 12 * n + 32 * n);
+      hipLaunchKernelGGL(k_logup_prepare, dim3(g), dim3(kBlock), 0, c->stream, input->dev, input->rows, input->cols,
+                         log2_exact(pcol), n, d_table, mask, gamma, beta, d_pad, d_min, d_mout, d_d0, d_w0, d_mult,
+                         part);
+      TRY(check_launch());
+    }
+    qm31 r[1];
+    TRY(finish_partials<1>(c, part, g, r));
+    trace_sum = r[0];
+  }
+  {
+    const unsigned g = partial_grid(tsize);
+    hipLaunchKernelGGL(k_logup_table_sum, dim3(g), dim3(kBlock), 0, c->stream, d_table, d_mult, tsize, gamma, beta,
+                       part);
+    TRY(check_launch());
+    qm31 r[1];
+    TRY(finish_partials<1>(c, part, g, r));
+    table_sum = r[0];
+  }
+  if (!qm31_eq(trace_sum, table_sum))
+    return fail(GKR_ERR_LOGUP, "Activation LogUp sum mismatch: trace=(%u,%u,%u,%u) table=(%u,%u,%u,%u)", trace_sum.a,
+                trace_sum.b, trace_sum.c, trace_sum.d, table_sum.a, table_sum.b, table_sum.c, table_sum.d);
+  C.mix_secure_field(trace_sum);
+  out->claimed_sum = G(trace_sum);
+
+  // eq-sumcheck: sum eq(r, x) w(x) d(x) = 1 over the hypercube
+  TRY(eq_table(c, cpt.data(), nv, n, d_e0));
+  const qm31 inv2 = qm31_from_m31(1u << 30);
+  const qm31 inv6 = qm31_from_m31(m31_inv(6));
+  const qm31 two = qm31_from_m31(2), three = qm31_from_m31(3);
+  std::vector<qm31> chal(nv);
+  const qm31 *ce = d_e0, *cw = d_w0, *cd = d_d0;
+  qm31* be[2] = {d_e1, d_e0};
+  qm31* bw[2] = {d_w1, d_w0};
+  qm31* bd[2] = {d_d1, d_d0};
+  qm31 alpha = qm31_zero();
+  for (int t = 0; t < nv; t++) {
+    const uint64_t half = (n >> t) / 2;
+    const unsigned g = partial_grid(half);
+    qm31 s[4];
+    {
+      // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}; round 0 reads only
+      TimedLaunch tl(c, K_EQ3_ROUND, t == 0 ? 96 * half : 288 * half);
+      if (t == 0) {
+        hipLaunchKernelGGL(k_eq3_round, dim3(g), dim3(kBlock), 0, c->stream, ce, cw, cd, (qm31*)nullptr,
+                           (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), part);
+      } else {
+        qm31 *ne = be[(t - 1) & 1], *nw = bw[(t - 1) & 1], *nd = bd[(t - 1) & 1];
+        hipLaunchKernelGGL(k_eq3_round, dim3(g), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw, nd, half, 1, alpha,
+                           part);
+        ce = ne; cw = nw; cd = nd;
+      }
+      TRY(check_launch());
+    }
+    TRY(finish_partials<4>(c, part, g, s));
+    const qm31 dd1 = qm31_sub(s[1], s[0]);
+    const qm31 dd2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
+    const qm31 dd3 = qm31_mul(qm31_sub(qm31_sub(s[3], s[0]), qm31_mul(three, qm31_sub(s[2], s[1]))), inv6);
+    const qm31 c0 = s[0];
+    const qm31 c1 = qm31_add(qm31_sub(dd1, dd2), qm31_mul(two, dd3));
+    const qm31 c2 = qm31_sub(dd2, qm31_mul(three, dd3));
+    const qm31 c3 = dd3;
+    out->eq_round_polys[4 * t + 0] = G(c0);
+    out->eq_round_polys[4 * t + 1] = G(c1);
+    out->eq_round_polys[4 * t + 2] = G(c2);
+    out->eq_round_polys[4 * t + 3] = G(c3);
+    C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
+    alpha = C.draw_qm31();
+    chal[t] = alpha;
+  }
+  qm31 fin[3];
+  if (nv > 0) {
+    hipLaunchKernelGGL(k_eq3_final, dim3(1), dim3(64), 0, c->stream, ce, cw, cd, alpha, dres);
+    TRY(check_launch());
+    TRY(fetch_q(c, dres, 3, fin));
+  } else {
+    TRY(fetch_q(c, d_w0, 1, fin + 1));
+  }
+  const qm31 w_eval = fin[1];
+  // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges
+  qm31 in_eval, out_eval, input_eval;
+  TRY(eq_table(c, chal.data(), nv, n, d_e0));
+  TRY(dot_m31(c, d_min, d_e0, n, &in_eval));
+  TRY(dot_m31(c, d_mout, d_e0, n, &out_eval));
+  // MLE(padded input) at the claim point (prover.rs:6411-6417)
+  TRY(eq_table(c, cpt.data(), nv, n, d_e0));
+  TRY(dot_m31(c, d_pad, d_e0, n, &input_eval));
+  out->w_eval = G(w_eval);
+  out->in_eval = G(in_eval);
+  out->out_eval = G(out_eval);
+
+  // Multiplicity sumcheck (prover.rs:9449-9511): degree-1 rounds over 2^table_log entries.
+  HIP_TRY(hipMemcpyAsync(out->multiplicities, d_mult, tsize * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+  TRY(sync(c));
+  uint64_t msum = 0;
+  for (uint64_t j = 0; j < tsize; j++) msum += out->multiplicities[j];
+  const qm31 mult_sum = qm31_from_m31(m31_reduce64(msum));
+  qm31 *m0, *m1;
+  TRY(ensureT(c, S_M0, tsize, &m0));
+  TRY(ensureT(c, S_M1, tsize / 2 + 1, &m1));
+  hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0);
+  TRY(check_launch());
+  const qm31* cm = m0;
+  qm31* bm[2] = {m1, m0};
+  for (uint32_t t = 0; t < table_log; t++) {
+    const uint64_t half = (tsize >> t) / 2;
+    const unsigned g = partial_grid(half);
+    if (t == 0) {
+      hipLaunchKernelGGL(k_sum_round, dim3(g), dim3(kBlock), 0, c->stream, cm, (qm31*)nullptr, half, 0, qm31_zero(),
+                         part);
+    } else {
+      qm31* nm = bm[(t - 1) & 1];
+      hipLaunchKernelGGL(k_sum_round, dim3(g), dim3(kBlock), 0, c->stream, cm, nm, half, 1, alpha, part);
+      cm = nm;
+    }
+    TRY(check_launch());
+    qm31 s[2];
+    TRY(finish_partials<2>(c, part, g, s));
+    const qm31 c0 = s[0];
+    const qm31 c1 = qm31_sub(s[1], s[0]);
+    out->mult_round_polys[2 * t] = G(c0);
+    out->mult_round_polys[2 * t + 1] = G(c1);
+    C.mix_secure_field(c0);
+    C.mix_secure_field(c1);
+    alpha = C.draw_qm31();
+  }
+  qm31 mfin[1];
+  hipLaunchKernelGGL(k_fold1_final, dim3(1), dim3(64), 0, c->stream, cm, alpha, dres);
+  TRY(check_launch());
+  TRY(fetch_q(c, dres, 1, mfin));
+  out->mult_final_eval = G(mfin[0]);
+  out->mult_claimed_sum = G(mult_sum);
+
+  // Table commitment = poseidon_hash_many([type_tag, log_size]) (prover.rs:8365-8373)
+  felt tc_in[2] = {felt_from_u64(tag), felt_from_u64(table_log)};
+  const felt tc = poseidon_hash_many(tc_in, 2);
+  out->table_commitment = felt_to_abi(tc);
+  C.mix_secure_field(input_eval);
+  C.mix_secure_field(Q(*claim_value));
+  out->input_eval = G(input_eval);
+  out->output_eval = *claim_value;
+
+  if (proof) {
+    LayerRec L;
+    L.tag = 3;
+    L.act_type = tag;
+    for (int t = 0; t < 4 * nv; t++) L.rp.push_back(Q(out->eq_round_polys[t]));
+    L.input_eval = input_eval;
+    L.output_eval = Q(*claim_value);
+    L.table_commitment = felt_from_mont(tc);
+    L.claimed_sum = trace_sum;
+    L.w_eval = w_eval;
+    L.in_eval = in_eval;
+    L.out_eval = out_eval;
+    L.mults.assign(out->multiplicities, out->multiplicities + tsize);
+    for (uint32_t t = 0; t < 2 * table_log; t++) L.mult_rp.push_back(Q(out->mult_round_polys[t]));
+    L.mult_final = mfin[0];
+    L.mult_sum = mult_sum;
+    proof->layers.push_back(L);
+  }
+  return GKR_OK;
+}

@@ -1,0 +1,503 @@
+// gfx950 kernels for the GKR matmul / LogUp sumcheck hot path.
+//
+// All arithmetic is exact M31/QM31 (see field.h).  Memory layout: M31
+// matrices are row-major u32; QM31 vectors are array-of-structs, 16 bytes
+// per element, read and written as one 128-bit access.  Sums of products
+// are accumulated lazily in 64-bit integers and reduced once per thread.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "field.h"
+
+namespace gkr {
+
+constexpr int kBlock = 256;       // threads per workgroup (4 wave64)
+constexpr int kMaxVars = 32;      // largest MLE point handled in one call
+
+// A point (r_0, ..., r_{n-1}) passed by value in the kernel arguments,
+// together with 1 - r_l, so no host-to-device copy is needed per call.
+struct PointArg {
+  qm31 r[kMaxVars];
+  qm31 omr[kMaxVars];
+  int n;
+};
+
+__device__ __forceinline__ qm31 ld_q(const qm31* __restrict__ p, uint64_t i) {
+  uint4 v = reinterpret_cast<const uint4*>(p)[i];
+  return qm31{v.x, v.y, v.z, v.w};
+}
+__device__ __forceinline__ void st_q(qm31* __restrict__ p, uint64_t i, qm31 q) {
+  reinterpret_cast<uint4*>(p)[i] = make_uint4(q.a, q.b, q.c, q.d);
+}
+
+// 64-bit accumulator of canonical QM31 values (up to 2^32 additions).
+struct qacc {
+  uint64_t a, b, c, d;
+  __device__ __forceinline__ void zero() { a = b = c = d = 0; }
+  __device__ __forceinline__ void add(qm31 q) { a += q.a; b += q.b; c += q.c; d += q.d; }
+  __device__ __forceinline__ qm31 reduce() const {
+    return qm31{m31_reduce64(a), m31_reduce64(b), m31_reduce64(c), m31_reduce64(d)};
+  }
+};
+
+__device__ __forceinline__ uint32_t shfl_xor_u32(uint32_t v, int m) {
+  return (uint32_t)__shfl_xor((int)v, m, 64);
+}
+__device__ __forceinline__ qm31 wave_sum(qm31 q) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    qm31 o{shfl_xor_u32(q.a, m), shfl_xor_u32(q.b, m), shfl_xor_u32(q.c, m), shfl_xor_u32(q.d, m)};
+    q = qm31_add(q, o);
+  }
+  return q;
+}
+
+// Block-wide sum of NQ QM31 values per thread; thread 0 writes them to
+// out[0 .. NQ) (as canonical QM31).
+template <int NQ>
+__device__ __forceinline__ void block_sum_store(qm31 (&v)[NQ], qm31* __restrict__ out) {
+  __shared__ qm31 sh[kBlock / 64][NQ];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int q = 0; q < NQ; q++) v[q] = wave_sum(v[q]);
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < NQ; q++) sh[wave][q] = v[q];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+      qm31 s = sh[0][q];
+      for (int w = 1; w < kBlock / 64; w++) s = qm31_add(s, sh[w][q]);
+      out[q] = s;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ eq / Lagrange
+// out[x] = prod_l (bit_l(x) ? r_l : 1 - r_l), with r_0 on the most
+// significant bit of x (components/matmul.rs:342-355, gkr/prover.rs:9201-9233).
+__global__ void k_eq_direct(PointArg pt, uint64_t count, qm31* __restrict__ out) {
+  uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (x >= count) return;
+  qm31 acc = qm31_one();
+  const int n = pt.n;
+  for (int l = 0; l < n; l++) {
+    const uint64_t bit = (x >> (n - 1 - l)) & 1ull;
+    acc = qm31_mul(acc, bit ? pt.r[l] : pt.omr[l]);
+  }
+  st_q(out, x, acc);
+}
+// Split construction: hi table over variables [0, n-h), lo over [n-h, n).
+__global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __restrict__ lo) {
+  const uint64_t n_hi = 1ull << (pt.n - h), n_lo = 1ull << h;
+  uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (x < n_hi) {
+    const int nv = pt.n - h;
+    qm31 acc = qm31_one();
+    for (int l = 0; l < nv; l++) acc = qm31_mul(acc, ((x >> (nv - 1 - l)) & 1ull) ? pt.r[l] : pt.omr[l]);
+    st_q(hi, x, acc);
+  } else if (x < n_hi + n_lo) {
+    const uint64_t y = x - n_hi;
+    qm31 acc = qm31_one();
+    for (int l = 0; l < h; l++) {
+      const int v = pt.n - h + l;
+      acc = qm31_mul(acc, ((y >> (h - 1 - l)) & 1ull) ? pt.r[v] : pt.omr[v]);
+    }
+    st_q(lo, y, acc);
+  }
+}
+__global__ void k_eq_combine(const qm31* __restrict__ hi, const qm31* __restrict__ lo, int h, uint64_t count,
+                             qm31* __restrict__ out) {
+  uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (x >= count) return;
+  st_q(out, x, qm31_mul(ld_q(hi, x >> h), ld_q(lo, x & ((1ull << h) - 1))));
+}
+
+// ------------------------------------------------------------------ restriction
+// Activation side: f_a[j] = sum_{i<m} A[i][j] * L[i] for j < k, 0 for k <= j < pk.
+// One thread per column; consecutive threads read consecutive words of a row.
+__global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint64_t k, uint64_t pk,
+                                const qm31* __restrict__ L, qm31* __restrict__ out) {
+  uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= pk) return;
+  if (j >= k) {
+    st_q(out, j, qm31_zero());
+    return;
+  }
+  // Per component keep lo/hi halves of 4-product partial sums:
+  // 4 * (P-1)^2 < 2^64, and 2^32 == 2 (mod P).
+  uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+  uint64_t i = 0;
+  for (; i + 4 <= m; i += 4) {
+    uint64_t t[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint64_t v = A[(i + u) * k + j];
+      const qm31 l = ld_q(L, i + u);
+      t[0] += v * l.a; t[1] += v * l.b; t[2] += v * l.c; t[3] += v * l.d;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+  }
+  for (; i < m; i++) {
+    const uint64_t v = A[i * k + j];
+    const qm31 l = ld_q(L, i);
+    const uint64_t t[4] = {v * l.a, v * l.b, v * l.c, v * l.d};
+#pragma unroll
+    for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+  }
+  uint32_t r[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
+  st_q(out, j, qm31{r[0], r[1], r[2], r[3]});
+}
+
+// Weight side: f_b[i] = sum_{j<n} B[i][j] * L[j] for i < k, 0 for k <= i < pk.
+// A workgroup owns kRowsPerBlock consecutive rows; its 256 threads stride
+// over the columns 4 at a time (128-bit loads when n % 4 == 0), so each
+// L[j] fetched from L2 is reused for all rows of the group.
+constexpr int kRowsPerBlock = 8;
+template <bool kVec4>
+__global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
+                                                          const qm31* __restrict__ L, qm31* __restrict__ out) {
+  const uint64_t row0 = (uint64_t)blockIdx.x * kRowsPerBlock;
+  const int nrows = (int)((k - row0) < (uint64_t)kRowsPerBlock ? (k - row0) : (uint64_t)kRowsPerBlock);
+  uint64_t lo[kRowsPerBlock][4], hi[kRowsPerBlock][4];
+#pragma unroll
+  for (int r = 0; r < kRowsPerBlock; r++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) lo[r][c] = hi[r][c] = 0;
+
+  for (uint64_t j0 = (uint64_t)threadIdx.x * 4; j0 < n; j0 += (uint64_t)kBlock * 4) {
+    const int cnt = (int)((n - j0) < 4 ? (n - j0) : 4);
+    qm31 l[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) l[u] = (u < cnt) ? ld_q(L, j0 + u) : qm31_zero();
+#pragma unroll
+    for (int r = 0; r < kRowsPerBlock; r++) {
+      if (r < nrows) {
+        const uint32_t* row = B + (row0 + r) * n;
+        uint32_t v[4];
+        if (kVec4 && cnt == 4) {
+          uint4 w = *reinterpret_cast<const uint4*>(row + j0);
+          v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; u++) v[u] = (u < cnt) ? row[j0 + u] : 0u;
+        }
+        uint64_t t[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          t[0] += (uint64_t)v[u] * l[u].a;
+          t[1] += (uint64_t)v[u] * l[u].b;
+          t[2] += (uint64_t)v[u] * l[u].c;
+          t[3] += (uint64_t)v[u] * l[u].d;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) { lo[r][c] += (uint32_t)t[c]; hi[r][c] += t[c] >> 32; }
+      }
+    }
+  }
+  // reduce each row's partial sums over the workgroup
+  __shared__ qm31 sh[kBlock / 64][kRowsPerBlock];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int r = 0; r < kRowsPerBlock; r++) {
+    qm31 s;
+    uint32_t w4[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) w4[c] = m31_add(m31_reduce64(lo[r][c]), m31_mul(m31_reduce64(hi[r][c]), 2u));
+    s = qm31{w4[0], w4[1], w4[2], w4[3]};
+    s = wave_sum(s);
+    if (lane == 0) sh[wave][r] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x < kRowsPerBlock && (int)threadIdx.x < nrows) {
+    qm31 s = sh[0][threadIdx.x];
+    for (int w = 1; w < kBlock / 64; w++) s = qm31_add(s, sh[w][threadIdx.x]);
+    st_q(out, row0 + threadIdx.x, s);
+  }
+}
+__global__ void k_zero_q(qm31* __restrict__ out, uint64_t from, uint64_t to) {
+  uint64_t i = from + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < to) st_q(out, i, qm31_zero());
+}
+
+// ------------------------------------------------------------------ matmul sumcheck round
+// Round t of the degree-2 product sumcheck over f_a, f_b (backend.rs:146-177).
+// When fold != 0 the inputs still have length 4*half and are first folded by
+// alpha (the previous round's challenge): x'[i] = x[i] + alpha*(x[2half+i] - x[i]);
+// the folded vectors (length 2*half) are written to the outputs.  Then, for
+// i < half, with x0 = x'[i], x1 = x'[half+i]:
+//   s0 += a0*b0,  s1 += a1*b1,  s2 += (2a1 - a0)*(2b1 - b0).
+// Each workgroup writes its three partial sums to partials[3*blockIdx ..].
+__global__ void __launch_bounds__(kBlock) k_mm_round(const qm31* __restrict__ a_in, const qm31* __restrict__ b_in,
+                                                     qm31* __restrict__ a_out, qm31* __restrict__ b_out,
+                                                     uint64_t half, int fold, qm31 alpha,
+                                                     qm31* __restrict__ partials) {
+  qacc s0, s1, s2;
+  s0.zero(); s1.zero(); s2.zero();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < half; i += stride) {
+    qm31 a0, a1, b0, b1;
+    if (fold) {
+      a0 = qm31_fold(ld_q(a_in, i), ld_q(a_in, i + 2 * half), alpha);
+      a1 = qm31_fold(ld_q(a_in, i + half), ld_q(a_in, i + 3 * half), alpha);
+      b0 = qm31_fold(ld_q(b_in, i), ld_q(b_in, i + 2 * half), alpha);
+      b1 = qm31_fold(ld_q(b_in, i + half), ld_q(b_in, i + 3 * half), alpha);
+      st_q(a_out, i, a0); st_q(a_out, i + half, a1);
+      st_q(b_out, i, b0); st_q(b_out, i + half, b1);
+    } else {
+      a0 = ld_q(a_in, i); a1 = ld_q(a_in, i + half);
+      b0 = ld_q(b_in, i); b1 = ld_q(b_in, i + half);
+    }
+    s0.add(qm31_mul(a0, b0));
+    s1.add(qm31_mul(a1, b1));
+    const qm31 a2 = qm31_sub(qm31_add(a1, a1), a0);
+    const qm31 b2 = qm31_sub(qm31_add(b1, b1), b0);
+    s2.add(qm31_mul(a2, b2));
+  }
+  qm31 v[3] = {s0.reduce(), s1.reduce(), s2.reduce()};
+  block_sum_store<3>(v, partials + 3 * (uint64_t)blockIdx.x);
+}
+
+// Fold both vectors of length 2 to a single value each: out = {fold(a), fold(b)}.
+__global__ void k_mm_final(const qm31* __restrict__ a, const qm31* __restrict__ b, qm31 alpha,
+                           qm31* __restrict__ out) {
+  if (threadIdx.x == 0) {
+    out[0] = qm31_fold(ld_q(a, 0), ld_q(a, 1), alpha);
+    out[1] = qm31_fold(ld_q(b, 0), ld_q(b, 1), alpha);
+  }
+}
+
+// Sum NQ-wide partial rows: out[q] = sum_b partials[NQ*b + q].  One workgroup.
+template <int NQ>
+__global__ void __launch_bounds__(kBlock) k_sum_partials(const qm31* __restrict__ partials, int nblocks,
+                                                         qm31* __restrict__ out) {
+  qacc acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) acc[q].zero();
+  for (int b = threadIdx.x; b < nblocks; b += blockDim.x)
+#pragma unroll
+    for (int q = 0; q < NQ; q++) acc[q].add(ld_q(partials, (uint64_t)NQ * b + q));
+  qm31 v[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) v[q] = acc[q].reduce();
+  block_sum_store<NQ>(v, out);
+}
+
+// ------------------------------------------------------------------ LogUp
+// Pad the activation matrix to (prow x pcol), mask to the table range, look up
+// the table output, form d = gamma - in - beta*out and w = 1/d, count
+// multiplicities and accumulate sum(w) per workgroup (gkr/prover.rs:6411-6475).
+__global__ void __launch_bounds__(kBlock) k_logup_prepare(
+    const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
+    const uint32_t* __restrict__ table_out, uint32_t mask, qm31 gamma, qm31 beta,
+    uint32_t* __restrict__ padded_in, uint32_t* __restrict__ masked_in, uint32_t* __restrict__ masked_out,
+    qm31* __restrict__ d_out, qm31* __restrict__ w_out, uint32_t* __restrict__ mult, qm31* __restrict__ partials) {
+  qacc acc;
+  acc.zero();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n; p += stride) {
+    const uint64_t r = p >> log_pcol, c = p & ((1ull << log_pcol) - 1);
+    const uint32_t x = (r < rows && c < cols) ? X[r * cols + c] : 0u;
+    const uint32_t mi = x & mask;
+    const uint32_t mo = table_out[mi];
+    padded_in[p] = x;
+    masked_in[p] = mi;
+    masked_out[p] = mo;
+    const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(mi)), qm31_mul_m31(beta, mo));
+    const qm31 w = qm31_inv(d);
+    st_q(d_out, p, d);
+    st_q(w_out, p, w);
+    atomicAdd(&mult[mi], 1u);
+    acc.add(w);
+  }
+  qm31 v[1] = {acc.reduce()};
+  block_sum_store<1>(v, partials + blockIdx.x);
+}
+// Table side: sum_j mult_j / (gamma - j - beta*f(j)) over entries with mult_j > 0.
+__global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __restrict__ table_out,
+                                                            const uint32_t* __restrict__ mult, uint64_t size,
+                                                            qm31 gamma, qm31 beta, qm31* __restrict__ partials) {
+  qacc acc;
+  acc.zero();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; j < size; j += stride) {
+    const uint32_t m = mult[j];
+    if (m == 0) continue;
+    const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(m31_from_u32((uint32_t)j))),
+                            qm31_mul_m31(beta, table_out[j]));
+    acc.add(qm31_mul_m31(qm31_inv(d), m31_from_u32(m)));
+  }
+  qm31 v[1] = {acc.reduce()};
+  block_sum_store<1>(v, partials + blockIdx.x);
+}
+
+// Degree-3 eq-sumcheck round over (eq, w, d) (gkr/prover.rs:6510-6556, 9236-9270):
+// s_t = sum_i eq_t(i) * w_t(i) * d_t(i) at t = 0, 1, 2, 3 where
+// x_t = (1 - t) x[i] + t x[half + i].  Same fused fold as k_mm_round.
+__global__ void __launch_bounds__(kBlock) k_eq3_round(const qm31* __restrict__ e_in, const qm31* __restrict__ w_in,
+                                                      const qm31* __restrict__ d_in, qm31* __restrict__ e_out,
+                                                      qm31* __restrict__ w_out, qm31* __restrict__ d_out,
+                                                      uint64_t half, int fold, qm31 alpha,
+                                                      qm31* __restrict__ partials) {
+  qacc s0, s1, s2, s3;
+  s0.zero(); s1.zero(); s2.zero(); s3.zero();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < half; i += stride) {
+    qm31 e0, e1, w0, w1, d0, d1;
+    if (fold) {
+      e0 = qm31_fold(ld_q(e_in, i), ld_q(e_in, i + 2 * half), alpha);
+      e1 = qm31_fold(ld_q(e_in, i + half), ld_q(e_in, i + 3 * half), alpha);
+      w0 = qm31_fold(ld_q(w_in, i), ld_q(w_in, i + 2 * half), alpha);
+      w1 = qm31_fold(ld_q(w_in, i + half), ld_q(w_in, i + 3 * half), alpha);
+      d0 = qm31_fold(ld_q(d_in, i), ld_q(d_in, i + 2 * half), alpha);
+      d1 = qm31_fold(ld_q(d_in, i + half), ld_q(d_in, i + 3 * half), alpha);
+      st_q(e_out, i, e0); st_q(e_out, i + half, e1);
+      st_q(w_out, i, w0); st_q(w_out, i + half, w1);
+      st_q(d_out, i, d0); st_q(d_out, i + half, d1);
+    } else {
+      e0 = ld_q(e_in, i); e1 = ld_q(e_in, i + half);
+      w0 = ld_q(w_in, i); w1 = ld_q(w_in, i + half);
+      d0 = ld_q(d_in, i); d1 = ld_q(d_in, i + half);
+    }
+    s0.add(qm31_mul(qm31_mul(e0, w0), d0));
+    s1.add(qm31_mul(qm31_mul(e1, w1), d1));
+    const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1, w0), dd = qm31_sub(d1, d0);
+    const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1, dw), d2 = qm31_add(d1, dd);
+    s2.add(qm31_mul(qm31_mul(e2, w2), d2));
+    const qm31 e3 = qm31_add(e2, de), w3 = qm31_add(w2, dw), d3 = qm31_add(d2, dd);
+    s3.add(qm31_mul(qm31_mul(e3, w3), d3));
+  }
+  qm31 v[4] = {s0.reduce(), s1.reduce(), s2.reduce(), s3.reduce()};
+  block_sum_store<4>(v, partials + 4 * (uint64_t)blockIdx.x);
+}
+__global__ void k_eq3_final(const qm31* __restrict__ e, const qm31* __restrict__ w, const qm31* __restrict__ d,
+                            qm31 alpha, qm31* __restrict__ out) {
+  if (threadIdx.x == 0) {
+    out[0] = qm31_fold(ld_q(e, 0), ld_q(e, 1), alpha);
+    out[1] = qm31_fold(ld_q(w, 0), ld_q(w, 1), alpha);
+    out[2] = qm31_fold(ld_q(d, 0), ld_q(d, 1), alpha);
+  }
+}
+
+// Degree-1 sumcheck round over one vector (multiplicities; prover.rs:9449-9511):
+// lo = sum_{i<half} v[i], hi = sum_{i<half} v[half+i], with the same fused fold.
+__global__ void __launch_bounds__(kBlock) k_sum_round(const qm31* __restrict__ v_in, qm31* __restrict__ v_out,
+                                                      uint64_t half, int fold, qm31 alpha,
+                                                      qm31* __restrict__ partials) {
+  qacc lo, hi;
+  lo.zero(); hi.zero();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < half; i += stride) {
+    qm31 x0, x1;
+    if (fold) {
+      x0 = qm31_fold(ld_q(v_in, i), ld_q(v_in, i + 2 * half), alpha);
+      x1 = qm31_fold(ld_q(v_in, i + half), ld_q(v_in, i + 3 * half), alpha);
+      st_q(v_out, i, x0); st_q(v_out, i + half, x1);
+    } else {
+      x0 = ld_q(v_in, i); x1 = ld_q(v_in, i + half);
+    }
+    lo.add(x0);
+    hi.add(x1);
+  }
+  qm31 v[2] = {lo.reduce(), hi.reduce()};
+  block_sum_store<2>(v, partials + 2 * (uint64_t)blockIdx.x);
+}
+__global__ void k_fold1_final(const qm31* __restrict__ v, qm31 alpha, qm31* __restrict__ out) {
+  if (threadIdx.x == 0) out[0] = qm31_fold(ld_q(v, 0), ld_q(v, 1), alpha);
+}
+__global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __restrict__ out) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) st_q(out, i, qm31_from_m31(m31_from_u32(in[i])));
+}
+
+// ------------------------------------------------------------------ MLE evaluation helpers
+// Partial dot products sum_i v[i] * eq[i] for an M31-valued v.
+__global__ void __launch_bounds__(kBlock) k_dot_m31(const uint32_t* __restrict__ v, const qm31* __restrict__ eq,
+                                                    uint64_t n, qm31* __restrict__ partials) {
+  uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint64_t x = m31_from_u32(v[i]);
+    const qm31 e = ld_q(eq, i);
+    const uint64_t t[4] = {x * e.a, x * e.b, x * e.c, x * e.d};
+#pragma unroll
+    for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+  }
+  uint32_t r[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
+  qm31 q[1] = {qm31{r[0], r[1], r[2], r[3]}};
+  block_sum_store<1>(q, partials + blockIdx.x);
+}
+// Partial dot products sum_i v[i] * eq[i] for a QM31-valued v.
+__global__ void __launch_bounds__(kBlock) k_dot_q(const qm31* __restrict__ v, const qm31* __restrict__ eq,
+                                                  uint64_t n, qm31* __restrict__ partials) {
+  qacc acc;
+  acc.zero();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    acc.add(qm31_mul(ld_q(v, i), ld_q(eq, i)));
+  qm31 q[1] = {acc.reduce()};
+  block_sum_store<1>(q, partials + blockIdx.x);
+}
+// restrict_mle: fix the first s variables: out[y] = sum_x eq[x] * mle[x * rest + y].
+__global__ void k_restrict_q(const qm31* __restrict__ mle, const qm31* __restrict__ eq, uint64_t nx,
+                             uint64_t rest, qm31* __restrict__ out) {
+  uint64_t y = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (y >= rest) return;
+  qacc acc;
+  acc.zero();
+  for (uint64_t x = 0; x < nx; x++) acc.add(qm31_mul(ld_q(eq, x), ld_q(mle, x * rest + y)));
+  st_q(out, y, acc.reduce());
+}
+
+// ------------------------------------------------------------------ synthetic inputs
+// Counter-mode SplitMix64: element i of the stream keyed by `seed` is the
+// (i+1)-th output of the sequential generator started at `seed`.
+GKR_HD uint64_t splitmix64_at(uint64_t seed, uint64_t i) {
+  uint64_t z = seed + (i + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+GKR_HD uint64_t splitmix64_mix(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+// kind 0: uniform M31 (31-bit draw, the value P rejected by re-mixing);
+// kind 1: int8-range, uniform in [-127, 127] (as (z >> 32) % 255 - 127), negative v stored as P + v.
+GKR_HD uint32_t synth_value(int kind, uint64_t seed, uint64_t i) {
+  uint64_t z = splitmix64_at(seed, i);
+  if (kind == 0) {
+    uint32_t v = (uint32_t)(z >> 33);
+    while (v == P) {
+      z = splitmix64_mix(z);
+      v = (uint32_t)(z >> 33);
+    }
+    return v;
+  }
+  const int s = (int)((z >> 32) % 255ull) - 127;
+  return s < 0 ? (uint32_t)((int64_t)P + s) : (uint32_t)s;
+}
+__global__ void k_fill_synth(uint32_t* __restrict__ out, uint64_t n, int kind, uint64_t seed) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    out[i] = synth_value(kind, seed, i);
+}
+// Row-major QM31 table: four consecutive draws per element.
+__global__ void k_fill_synth_q(qm31* __restrict__ out, uint64_t n, uint64_t seed) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    st_q(out, i, qm31{synth_value(0, seed, 4 * i), synth_value(0, seed, 4 * i + 1),
+                      synth_value(0, seed, 4 * i + 2), synth_value(0, seed, 4 * i + 3)});
+}
+
+}  // namespace gkr

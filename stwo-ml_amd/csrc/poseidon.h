@@ -1,0 +1,200 @@
+// Starknet Poseidon (Hades over felt252) and the Fiat-Shamir channel of the
+// GKR prover, on the host.
+//
+// Hades: 91 rounds over a 3-element state; rounds 0-3 and 87-90 are full
+// (x^3 on every lane), rounds 4-86 are partial (x^3 on lane 2 only).  Each
+// round adds its three round constants to the three lanes, applies the
+// S-box, then the MDS matrix [[3,1,1],[1,-1,1],[1,1,-2]]
+// (reference: engine/src/recursive/hades_air.rs:1892-2012 for the round
+// structure and MDS; constants per engine/src/crypto/poseidon_constants.rs).
+//
+// Channel semantics follow engine/src/crypto/poseidon_channel.rs:83-308:
+//   mix_felt(v):  digest = hades([digest, v, 2])[0], n_draws = 0
+//   draw_felt252: hades([digest, n_draws, 3])[0],   n_draws += 1
+//   draw_qm31:    four 31-bit limbs of one draw, LSB first, each mod P
+//   mix_poly_coeffs(c0,c1,c2): digest = hash_many([digest, pack(c0,c1), pack(c2)])
+//   mix_poly_coeffs_deg3(c0..c3): hash_many([digest, pack(c0,c1), pack(c2,c3)])
+//   mix_felts(qs): hash_many([digest, pack(pairs)..., pack(last single)])
+// where pack(v...) = fold(1, acc * 2^31 + v) over the M31 words.
+#pragma once
+#include <stdint.h>
+
+#include "felt252.h"
+#include "field.h"
+
+namespace gkr {
+
+#include "hades_constants.inc"
+
+struct hades_rc {
+  felt rc[273];  // Montgomery form
+  hades_rc() {
+    for (int i = 0; i < 273; i++) {
+      felt c{{kHadesRoundConstants[i][0], kHadesRoundConstants[i][1], kHadesRoundConstants[i][2],
+              kHadesRoundConstants[i][3]}};
+      rc[i] = felt_to_mont(c);
+    }
+  }
+};
+inline const hades_rc& hades_constants() {
+  static const hades_rc k;
+  return k;
+}
+
+inline felt felt_cube(const felt& x) { return felt_mul(felt_mul(x, x), x); }
+
+inline void hades_permute(felt s[3]) {
+  const felt* rc = hades_constants().rc;
+  for (int r = 0; r < 91; r++) {
+    s[0] = felt_add(s[0], rc[3 * r]);
+    s[1] = felt_add(s[1], rc[3 * r + 1]);
+    s[2] = felt_add(s[2], rc[3 * r + 2]);
+    const bool full = (r < 4) || (r >= 87);
+    if (full) {
+      s[0] = felt_cube(s[0]);
+      s[1] = felt_cube(s[1]);
+    }
+    s[2] = felt_cube(s[2]);
+    // MDS: t = s0+s1+s2; s0' = t + 2 s0; s1' = t - 2 s1; s2' = t - 3 s2
+    felt t = felt_add(felt_add(s[0], s[1]), s[2]);
+    felt n0 = felt_add(t, felt_add(s[0], s[0]));
+    felt n1 = felt_sub(t, felt_add(s[1], s[1]));
+    felt n2 = felt_sub(t, felt_add(felt_add(s[2], s[2]), s[2]));
+    s[0] = n0;
+    s[1] = n1;
+    s[2] = n2;
+  }
+}
+
+// hash(a, b) = hades([a, b, 2])[0]
+inline felt poseidon_hash(const felt& a, const felt& b) {
+  felt s[3] = {a, b, felt_from_u64(2)};
+  hades_permute(s);
+  return s[0];
+}
+
+// Rate-2 sponge from the zero state.  A trailing single input x absorbs
+// [x, 1]; an even count finishes by absorbing [1, 0].  Output lane 0.
+inline felt poseidon_hash_many(const felt* in, int n) {
+  felt s[3] = {felt_zero(), felt_zero(), felt_zero()};
+  const felt one = felt_one();
+  int i = 0;
+  for (; i + 1 < n; i += 2) {
+    s[0] = felt_add(s[0], in[i]);
+    s[1] = felt_add(s[1], in[i + 1]);
+    hades_permute(s);
+  }
+  if (i < n) {
+    s[0] = felt_add(s[0], in[i]);
+    s[1] = felt_add(s[1], one);
+  } else {
+    s[0] = felt_add(s[0], one);
+  }
+  hades_permute(s);
+  return s[0];
+}
+
+// 1 || v0 || v1 || ... with 31 bits per word (n <= 8 keeps it below 2^249,
+// hence canonical without reduction).  Returns Montgomery form.
+inline felt pack_m31s(const uint32_t* v, int n) {
+  uint64_t l[4] = {1, 0, 0, 0};
+  for (int k = 0; k < n; k++) {
+    // l = l << 31 | v[k]
+    l[3] = (l[3] << 31) | (l[2] >> 33);
+    l[2] = (l[2] << 31) | (l[1] >> 33);
+    l[1] = (l[1] << 31) | (l[0] >> 33);
+    l[0] = (l[0] << 31) | (uint64_t)v[k];
+  }
+  return felt_to_mont(felt{{l[0], l[1], l[2], l[3]}});
+}
+inline felt securefield_to_felt(const qm31& q) {
+  uint32_t w[4] = {q.a, q.b, q.c, q.d};
+  return pack_m31s(w, 4);
+}
+
+class PoseidonChannel {
+ public:
+  felt digest;  // Montgomery form
+  uint32_t n_draws = 0;
+  uint64_t hash_count = 0;
+
+  PoseidonChannel() : digest(felt_zero()) {}
+
+  void mix_felt(const felt& v) {
+    felt s[3] = {digest, v, felt_from_u64(2)};
+    hades_permute(s);
+    digest = s[0];
+    n_draws = 0;
+    hash_count++;
+  }
+  void mix_u64(uint64_t v) { mix_felt(felt_from_u64(v)); }
+  void mix_secure_field(const qm31& v) { mix_felt(securefield_to_felt(v)); }
+
+  felt draw_felt252() {  // returns Montgomery form
+    felt s[3] = {digest, felt_from_u64(n_draws), felt_from_u64(3)};
+    hades_permute(s);
+    n_draws++;
+    hash_count++;
+    return s[0];
+  }
+  qm31 draw_qm31() {
+    felt x = felt_from_mont(draw_felt252());
+    uint32_t m[4];
+    for (int k = 0; k < 4; k++) {
+      const int bit = 31 * k, limb = bit >> 6, off = bit & 63;
+      uint64_t v = x.l[limb] >> off;
+      if (off > 33 && limb < 3) v |= x.l[limb + 1] << (64 - off);
+      m[k] = m31_from_u32((uint32_t)(v & 0x7fffffffull));
+    }
+    return qm31{m[0], m[1], m[2], m[3]};
+  }
+  void mix_poly_coeffs(const qm31& c0, const qm31& c1, const qm31& c2) {
+    const uint32_t w[12] = {c0.a, c0.b, c0.c, c0.d, c1.a, c1.b, c1.c, c1.d, c2.a, c2.b, c2.c, c2.d};
+    felt in[3] = {digest, pack_m31s(w, 8), pack_m31s(w + 8, 4)};
+    digest = poseidon_hash_many(in, 3);
+    n_draws = 0;
+    hash_count++;
+  }
+  void mix_poly_coeffs_deg3(const qm31& c0, const qm31& c1, const qm31& c2, const qm31& c3) {
+    const uint32_t w[16] = {c0.a, c0.b, c0.c, c0.d, c1.a, c1.b, c1.c, c1.d,
+                            c2.a, c2.b, c2.c, c2.d, c3.a, c3.b, c3.c, c3.d};
+    felt in[3] = {digest, pack_m31s(w, 8), pack_m31s(w + 8, 8)};
+    digest = poseidon_hash_many(in, 3);
+    n_draws = 0;
+    hash_count++;
+  }
+  void mix_felts(const qm31* q, int n) {
+    if (n <= 0) return;
+    felt* in = new felt[1 + (n + 1) / 2];
+    int m = 0;
+    in[m++] = digest;
+    for (int i = 0; i < n; i += 2) {
+      if (i + 1 < n) {
+        const uint32_t w[8] = {q[i].a, q[i].b, q[i].c, q[i].d, q[i + 1].a, q[i + 1].b, q[i + 1].c, q[i + 1].d};
+        in[m++] = pack_m31s(w, 8);
+      } else {
+        in[m++] = securefield_to_felt(q[i]);
+      }
+    }
+    digest = poseidon_hash_many(in, m);
+    delete[] in;
+    n_draws = 0;
+    hash_count++;
+  }
+
+  // State in the reference's to_gpu_state layout (poseidon_channel.rs:109-135):
+  // 8 little-endian u32 digest words, n_draws, hash_count lo, hash_count hi.
+  void export_state(uint32_t st[11]) const {
+    felt_canon_to_words(felt_from_mont(digest), st);
+    st[8] = n_draws;
+    st[9] = (uint32_t)hash_count;
+    st[10] = (uint32_t)(hash_count >> 32);
+  }
+  void import_state(const uint32_t st[11]) {
+    digest = felt_to_mont(felt_canon_from_words(st));
+    n_draws = st[8];
+    hash_count = (uint64_t)st[9] | ((uint64_t)st[10] << 32);
+  }
+};
+
+}  // namespace gkr

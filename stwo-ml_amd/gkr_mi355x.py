@@ -1,0 +1,474 @@
+"""ctypes binding of the MI355X GKR prover C ABI (include/gkr_mi355x.h).
+
+The library is lib/libgkr_mi355x.so next to this file (built by the
+package Makefile).  Loading fails loudly when it is missing: there is no
+CPU fallback.  Class and method names follow the reference's Rust API
+(PoseidonChannel in engine/src/crypto/poseidon_channel.rs, ZkmlOps in
+engine/src/backend.rs, the GKR layer reducers in engine/src/gkr/prover.rs).
+QM31 values are 4-tuples (a, b, c, d) = (a + b i) + (c + d i) u; felt252
+values are Python ints.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import List, Optional, Sequence, Tuple
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libgkr_mi355x.so")
+P = (1 << 31) - 1
+FELT_P = 2**251 + 17 * 2**192 + 1
+
+QM31 = Tuple[int, int, int, int]
+
+
+class GkrQM31(C.Structure):
+    _fields_ = [("v", C.c_uint32 * 4)]
+
+
+class GkrFelt(C.Structure):
+    _fields_ = [("w", C.c_uint32 * 8)]
+
+
+class GkrLogupOut(C.Structure):
+    _fields_ = [
+        ("claimed_sum", GkrQM31),
+        ("eq_round_polys", C.POINTER(GkrQM31)),
+        ("w_eval", GkrQM31),
+        ("in_eval", GkrQM31),
+        ("out_eval", GkrQM31),
+        ("multiplicities", C.POINTER(C.c_uint32)),
+        ("mult_round_polys", C.POINTER(GkrQM31)),
+        ("mult_final_eval", GkrQM31),
+        ("mult_claimed_sum", GkrQM31),
+        ("input_eval", GkrQM31),
+        ("output_eval", GkrQM31),
+        ("table_commitment", GkrFelt),
+        ("gamma", GkrQM31),
+        ("beta", GkrQM31),
+    ]
+
+
+class GkrError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"gkr error {code}: {msg}")
+        self.code = code
+
+
+_lib: Optional[C.CDLL] = None
+
+# (name, restype, argtypes) for every symbol of include/gkr_mi355x.h
+_P = C.c_void_p
+_PQ = C.POINTER(GkrQM31)
+_PF = C.POINTER(GkrFelt)
+_U32P = C.POINTER(C.c_uint32)
+SIGNATURES = [
+    ("gkr_last_error", C.c_char_p, []),
+    ("gkr_version", C.c_char_p, []),
+    ("gkr_hades_permute", C.c_int, [_PF]),
+    ("gkr_poseidon_hash", C.c_int, [_PF, _PF, _PF]),
+    ("gkr_poseidon_hash_many", C.c_int, [_PF, C.c_size_t, _PF]),
+    ("gkr_channel_new", C.c_int, [C.POINTER(_P)]),
+    ("gkr_channel_free", None, [_P]),
+    ("gkr_channel_clone", C.c_int, [_P, C.POINTER(_P)]),
+    ("gkr_channel_mix_u64", C.c_int, [_P, C.c_uint64]),
+    ("gkr_channel_mix_felt", C.c_int, [_P, _PF]),
+    ("gkr_channel_mix_secure_field", C.c_int, [_P, _PQ]),
+    ("gkr_channel_mix_felts", C.c_int, [_P, _PQ, C.c_size_t]),
+    ("gkr_channel_mix_poly_coeffs", C.c_int, [_P, _PQ]),
+    ("gkr_channel_mix_poly_coeffs_deg3", C.c_int, [_P, _PQ]),
+    ("gkr_channel_draw_felt252", C.c_int, [_P, _PF]),
+    ("gkr_channel_draw_qm31", C.c_int, [_P, _PQ]),
+    ("gkr_channel_draw_qm31s", C.c_int, [_P, C.c_size_t, _PQ]),
+    ("gkr_channel_digest", C.c_int, [_P, _PF]),
+    ("gkr_channel_hash_count", C.c_uint64, [_P]),
+    ("gkr_channel_export", C.c_int, [_P, _U32P]),
+    ("gkr_channel_import", C.c_int, [_P, _U32P]),
+    ("gkr_ctx_create", C.c_int, [C.c_int, C.POINTER(_P)]),
+    ("gkr_ctx_destroy", None, [_P]),
+    ("gkr_ctx_synchronize", C.c_int, [_P]),
+    ("gkr_ctx_set_timing", C.c_int, [_P, C.c_int]),
+    ("gkr_ctx_kernel_time", C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_uint64),
+                                      C.POINTER(C.c_uint64)]),
+    ("gkr_ctx_reset_timing", C.c_int, [_P]),
+    ("gkr_matrix_upload", C.c_int, [_P, _U32P, C.c_uint64, C.c_uint64, C.POINTER(_P)]),
+    ("gkr_matrix_wrap_device", C.c_int, [_P, _P, C.c_uint64, C.c_uint64, C.POINTER(_P)]),
+    ("gkr_matrix_synthetic", C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_int, C.c_uint64, C.POINTER(_P)]),
+    ("gkr_matrix_download", C.c_int, [_P, _P, _U32P]),
+    ("gkr_matrix_free", None, [_P]),
+    ("gkr_synthetic_value", C.c_uint32, [C.c_int, C.c_uint64, C.c_uint64]),
+    ("gkr_reduce_matmul_layer", C.c_int, [_P, _P, _P, _PQ, C.c_uint32, _PQ, C.c_uint32, C.c_uint64, _P, _PQ, _PQ,
+                                          _PQ, _PQ]),
+    ("gkr_evaluate_mle_at_point", C.c_int, [_P, _PQ, C.c_uint64, _PQ, C.c_uint32, _PQ]),
+    ("gkr_restrict_mle", C.c_int, [_P, _PQ, C.c_uint64, _PQ, C.c_uint32, _PQ]),
+    ("gkr_proof_new", C.c_int, [C.POINTER(_P)]),
+    ("gkr_proof_free", None, [_P]),
+    ("gkr_proof_num_layers", C.c_size_t, [_P]),
+    ("gkr_proof_set_input_claim", C.c_int, [_P, _PQ, C.c_uint32, _PQ]),
+    ("gkr_proof_add_weight_commitment", C.c_int, [_P, _PF]),
+    ("gkr_proof_set_io_commitment", C.c_int, [_P, _PF]),
+    ("gkr_proof_serialize", C.c_int, [_P, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
+    ("gkr_seed_channel", C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_uint64, _PF]),
+    ("gkr_matmul_output_claim", C.c_int, [_P, _P, _P, _PQ, C.c_uint32, _PQ]),
+    ("gkr_prove_matmul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ, _PQ]),
+    ("gkr_prove_activation_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, C.c_uint32, C.c_uint32, _P, _P,
+                                             C.POINTER(GkrLogupOut)]),
+    ("gkr_activation_table", C.c_int, [C.c_uint32, C.c_uint32, _U32P]),
+]
+
+
+def lib() -> C.CDLL:
+    """Load the HIP library (raises when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C stwo-ml_amd` "
+                               "(or __graft_entry__.build()); there is no CPU fallback")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise GkrError(rc, lib().gkr_last_error().decode())
+
+
+# ------------------------------------------------------------------ conversions
+def q_to_c(q: Sequence[int]) -> GkrQM31:
+    x = GkrQM31()
+    for i in range(4):
+        x.v[i] = int(q[i])
+    return x
+
+
+def q_from_c(x: GkrQM31) -> QM31:
+    return (x.v[0], x.v[1], x.v[2], x.v[3])
+
+
+def q_array(qs: Sequence[Sequence[int]]):
+    arr = (GkrQM31 * max(1, len(qs)))()
+    for i, q in enumerate(qs):
+        for j in range(4):
+            arr[i].v[j] = int(q[j])
+    return arr
+
+
+def felt_to_c(v: int) -> GkrFelt:
+    f = GkrFelt()
+    for i in range(8):
+        f.w[i] = (v >> (32 * i)) & 0xFFFFFFFF
+    return f
+
+
+def felt_from_c(f: GkrFelt) -> int:
+    return sum(int(f.w[i]) << (32 * i) for i in range(8))
+
+
+# ------------------------------------------------------------------ Poseidon
+def hades_permute(state: Sequence[int]) -> List[int]:
+    arr = (GkrFelt * 3)(*[felt_to_c(v) for v in state])
+    _check(lib().gkr_hades_permute(arr))
+    return [felt_from_c(arr[i]) for i in range(3)]
+
+
+def poseidon_hash(a: int, b: int) -> int:
+    out = GkrFelt()
+    _check(lib().gkr_poseidon_hash(C.byref(felt_to_c(a)), C.byref(felt_to_c(b)), C.byref(out)))
+    return felt_from_c(out)
+
+
+def poseidon_hash_many(xs: Sequence[int]) -> int:
+    arr = (GkrFelt * max(1, len(xs)))(*[felt_to_c(v) for v in xs])
+    out = GkrFelt()
+    _check(lib().gkr_poseidon_hash_many(arr, len(xs), C.byref(out)))
+    return felt_from_c(out)
+
+
+class PoseidonChannel:
+    """engine/src/crypto/poseidon_channel.rs:83 -- host Fiat-Shamir channel."""
+
+    def __init__(self, _handle: Optional[int] = None):
+        if _handle is None:
+            h = C.c_void_p()
+            _check(lib().gkr_channel_new(C.byref(h)))
+            _handle = h.value
+        self._h = _handle
+
+    def __del__(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.gkr_channel_free(self._h)
+            self._h = None
+
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    def clone(self) -> "PoseidonChannel":
+        h = C.c_void_p()
+        _check(lib().gkr_channel_clone(self._h, C.byref(h)))
+        return PoseidonChannel(h.value)
+
+    def mix_u64(self, v: int) -> None:
+        _check(lib().gkr_channel_mix_u64(self._h, v))
+
+    def mix_felt(self, v: int) -> None:
+        _check(lib().gkr_channel_mix_felt(self._h, C.byref(felt_to_c(v))))
+
+    def mix_secure_field(self, q: Sequence[int]) -> None:
+        _check(lib().gkr_channel_mix_secure_field(self._h, C.byref(q_to_c(q))))
+
+    def mix_felts(self, qs: Sequence[Sequence[int]]) -> None:
+        _check(lib().gkr_channel_mix_felts(self._h, q_array(qs), len(qs)))
+
+    def mix_poly_coeffs(self, c0, c1, c2) -> None:
+        _check(lib().gkr_channel_mix_poly_coeffs(self._h, q_array([c0, c1, c2])))
+
+    def mix_poly_coeffs_deg3(self, c0, c1, c2, c3) -> None:
+        _check(lib().gkr_channel_mix_poly_coeffs_deg3(self._h, q_array([c0, c1, c2, c3])))
+
+    def draw_felt252(self) -> int:
+        out = GkrFelt()
+        _check(lib().gkr_channel_draw_felt252(self._h, C.byref(out)))
+        return felt_from_c(out)
+
+    def draw_qm31(self) -> QM31:
+        out = GkrQM31()
+        _check(lib().gkr_channel_draw_qm31(self._h, C.byref(out)))
+        return q_from_c(out)
+
+    def draw_qm31s(self, n: int) -> List[QM31]:
+        arr = (GkrQM31 * max(1, n))()
+        _check(lib().gkr_channel_draw_qm31s(self._h, n, arr))
+        return [q_from_c(arr[i]) for i in range(n)]
+
+    def digest(self) -> int:
+        out = GkrFelt()
+        _check(lib().gkr_channel_digest(self._h, C.byref(out)))
+        return felt_from_c(out)
+
+    def hash_count(self) -> int:
+        return int(lib().gkr_channel_hash_count(self._h))
+
+    def export_state(self) -> List[int]:
+        st = (C.c_uint32 * 11)()
+        _check(lib().gkr_channel_export(self._h, st))
+        return list(st)
+
+    def import_state(self, st: Sequence[int]) -> None:
+        arr = (C.c_uint32 * 11)(*st)
+        _check(lib().gkr_channel_import(self._h, arr))
+
+    def seed_gkr(self, num_layers: int, in_rows: int, in_cols: int, policy_commitment: Optional[int] = None):
+        pc = C.byref(felt_to_c(policy_commitment)) if policy_commitment is not None else None
+        _check(lib().gkr_seed_channel(self._h, num_layers, in_rows, in_cols, pc))
+
+
+# ------------------------------------------------------------------ device
+class Context:
+    """A device context: one HIP stream plus its device buffers."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        _check(lib().gkr_ctx_create(device, C.byref(h)))
+        self._h = h.value
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().gkr_ctx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        if _lib is not None:
+            self.close()
+
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    def synchronize(self):
+        _check(lib().gkr_ctx_synchronize(self._h))
+
+    def set_timing(self, on: bool):
+        _check(lib().gkr_ctx_set_timing(self._h, 1 if on else 0))
+
+    def reset_timing(self):
+        _check(lib().gkr_ctx_reset_timing(self._h))
+
+    def kernel_time(self, kid: int) -> Tuple[float, int, int]:
+        ms, n, b = C.c_double(), C.c_uint64(), C.c_uint64()
+        _check(lib().gkr_ctx_kernel_time(self._h, kid, C.byref(ms), C.byref(n), C.byref(b)))
+        return ms.value, n.value, b.value
+
+    # matrices
+    def upload(self, m: np.ndarray) -> "Matrix":
+        m = np.ascontiguousarray(m, dtype=np.uint32)
+        assert m.ndim == 2
+        h = C.c_void_p()
+        _check(lib().gkr_matrix_upload(self._h, m.ctypes.data_as(_U32P), m.shape[0], m.shape[1], C.byref(h)))
+        return Matrix(self, h.value, m.shape[0], m.shape[1])
+
+    def wrap_device(self, ptr: int, rows: int, cols: int) -> "Matrix":
+        h = C.c_void_p()
+        _check(lib().gkr_matrix_wrap_device(self._h, C.c_void_p(ptr), rows, cols, C.byref(h)))
+        return Matrix(self, h.value, rows, cols)
+
+    def synthetic(self, rows: int, cols: int, kind: int, seed: int) -> "Matrix":
+        h = C.c_void_p()
+        _check(lib().gkr_matrix_synthetic(self._h, rows, cols, kind, seed, C.byref(h)))
+        return Matrix(self, h.value, rows, cols)
+
+    # ZkmlOps
+    def reduce_matmul_layer(self, a: "Matrix", b: "Matrix", r_i, r_j, pk: int, ch: PoseidonChannel):
+        T = pk.bit_length() - 1
+        rp = (GkrQM31 * max(1, 3 * T))()
+        chal = (GkrQM31 * max(1, T))()
+        fa, fb = GkrQM31(), GkrQM31()
+        _check(lib().gkr_reduce_matmul_layer(self._h, a.handle, b.handle, q_array(r_i), len(r_i), q_array(r_j),
+                                             len(r_j), pk, ch.handle, rp, chal, C.byref(fa), C.byref(fb)))
+        polys = [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2])) for t in range(T)]
+        return {"round_polys": polys, "challenges": [q_from_c(chal[t]) for t in range(T)],
+                "final_a_eval": q_from_c(fa), "final_b_eval": q_from_c(fb)}
+
+    def evaluate_mle_at_point(self, mle, point) -> QM31:
+        out = GkrQM31()
+        _check(lib().gkr_evaluate_mle_at_point(self._h, q_array(mle), len(mle), q_array(point), len(point),
+                                               C.byref(out)))
+        return q_from_c(out)
+
+    def restrict_mle(self, mle, assignments) -> List[QM31]:
+        rest = len(mle) >> len(assignments)
+        out = (GkrQM31 * max(1, rest))()
+        _check(lib().gkr_restrict_mle(self._h, q_array(mle), len(mle), q_array(assignments), len(assignments), out))
+        return [q_from_c(out[i]) for i in range(rest)]
+
+    # GKR layer reducers
+    def matmul_output_claim(self, a: "Matrix", b: "Matrix", r_out) -> QM31:
+        out = GkrQM31()
+        _check(lib().gkr_matmul_output_claim(self._h, a.handle, b.handle, q_array(r_out), len(r_out), C.byref(out)))
+        return q_from_c(out)
+
+    def prove_matmul_layer(self, claim_point, claim_value, a: "Matrix", b: "Matrix", ch: PoseidonChannel,
+                           proof: Optional["Proof"] = None):
+        pm = 1 << (a.rows - 1).bit_length()
+        pk = 1 << (a.cols - 1).bit_length()
+        T = pk.bit_length() - 1
+        lm = pm.bit_length() - 1
+        rp = (GkrQM31 * max(1, 3 * T))()
+        fa, fb, nv = GkrQM31(), GkrQM31(), GkrQM31()
+        npnt = (GkrQM31 * max(1, lm + T))()
+        _check(lib().gkr_prove_matmul_layer(self._h, q_array(claim_point), len(claim_point),
+                                            C.byref(q_to_c(claim_value)), a.handle, b.handle, ch.handle,
+                                            proof.handle if proof else None, rp, C.byref(fa), C.byref(fb), npnt,
+                                            C.byref(nv)))
+        polys = [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2])) for t in range(T)]
+        return {"round_polys": polys, "final_a_eval": q_from_c(fa), "final_b_eval": q_from_c(fb),
+                "next_point": [q_from_c(npnt[i]) for i in range(lm + T)], "next_value": q_from_c(nv)}
+
+    def prove_activation_layer(self, claim_point, claim_value, inp: "Matrix", act_type: int, ch: PoseidonChannel,
+                               table_log_size: int = 0, proof: Optional["Proof"] = None):
+        if table_log_size == 0:
+            table_log_size = 20 if act_type == 4 else 16
+        nv = len(claim_point)
+        eq = (GkrQM31 * max(1, 4 * nv))()
+        mults = (C.c_uint32 * (1 << table_log_size))()
+        mrp = (GkrQM31 * (2 * table_log_size))()
+        out = GkrLogupOut()
+        out.eq_round_polys = C.cast(eq, _PQ)
+        out.multiplicities = C.cast(mults, _U32P)
+        out.mult_round_polys = C.cast(mrp, _PQ)
+        _check(lib().gkr_prove_activation_layer(self._h, q_array(claim_point), nv, C.byref(q_to_c(claim_value)),
+                                                inp.handle, act_type, table_log_size, ch.handle,
+                                                proof.handle if proof else None, C.byref(out)))
+        return {
+            "claimed_sum": q_from_c(out.claimed_sum),
+            "eq_round_polys": [tuple(q_from_c(eq[4 * t + j]) for j in range(4)) for t in range(nv)],
+            "final_evals": (q_from_c(out.w_eval), q_from_c(out.in_eval), q_from_c(out.out_eval)),
+            "multiplicities": np.frombuffer(mults, dtype=np.uint32).copy(),
+            "mult_round_polys": [(q_from_c(mrp[2 * t]), q_from_c(mrp[2 * t + 1])) for t in range(table_log_size)],
+            "mult_final_eval": q_from_c(out.mult_final_eval),
+            "mult_claimed_sum": q_from_c(out.mult_claimed_sum),
+            "input_eval": q_from_c(out.input_eval),
+            "output_eval": q_from_c(out.output_eval),
+            "table_commitment": felt_from_c(out.table_commitment),
+            "gamma": q_from_c(out.gamma),
+            "beta": q_from_c(out.beta),
+        }
+
+
+class Matrix:
+    def __init__(self, ctx: Context, handle: int, rows: int, cols: int):
+        self.ctx, self._h, self.rows, self.cols = ctx, handle, rows, cols
+
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    def download(self) -> np.ndarray:
+        out = np.empty((self.rows, self.cols), dtype=np.uint32)
+        _check(lib().gkr_matrix_download(self.ctx.handle, self._h, out.ctypes.data_as(_U32P)))
+        return out
+
+    def free(self):
+        if self._h:
+            lib().gkr_matrix_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        if _lib is not None and getattr(self, "_h", None):
+            self.free()
+
+
+class Proof:
+    """GKRProof container (engine/src/gkr/types.rs:589-643)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        _check(lib().gkr_proof_new(C.byref(h)))
+        self._h = h.value
+
+    def __del__(self):
+        if _lib is not None and getattr(self, "_h", None):
+            _lib.gkr_proof_free(self._h)
+            self._h = None
+
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    def num_layers(self) -> int:
+        return int(lib().gkr_proof_num_layers(self._h))
+
+    def set_input_claim(self, point, value):
+        _check(lib().gkr_proof_set_input_claim(self._h, q_array(point), len(point), C.byref(q_to_c(value))))
+
+    def add_weight_commitment(self, c: int):
+        _check(lib().gkr_proof_add_weight_commitment(self._h, C.byref(felt_to_c(c))))
+
+    def set_io_commitment(self, c: int):
+        _check(lib().gkr_proof_set_io_commitment(self._h, C.byref(felt_to_c(c))))
+
+    def serialize(self) -> List[int]:
+        n = C.c_size_t()
+        rc = lib().gkr_proof_serialize(self._h, None, 0, C.byref(n))
+        if rc not in (0, 5):
+            _check(rc)
+        arr = (GkrFelt * max(1, n.value))()
+        _check(lib().gkr_proof_serialize(self._h, arr, n.value, C.byref(n)))
+        return [felt_from_c(arr[i]) for i in range(n.value)]
+
+
+def activation_table(act_type: int, log_size: int) -> np.ndarray:
+    out = np.empty(1 << log_size, dtype=np.uint32)
+    _check(lib().gkr_activation_table(act_type, log_size, out.ctypes.data_as(_U32P)))
+    return out
+
+
+def synthetic_value(kind: int, seed: int, i: int) -> int:
+    return int(lib().gkr_synthetic_value(kind, seed, i))
