@@ -1,0 +1,248 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X GKR matmul / LogUp sumcheck prover.
+
+A step is one complete proof of the configured workload over synthetic,
+HBM-resident inputs (weights uploaded once before timing):
+  qwen48 (default): 48 Qwen2.5-14B-shaped layers, 64 tokens;
+  qwen1 (config 4): one such layer;  smollm (config 3): 30 SmolLM2-135M layers,
+  1 token;  cfg1 (config 1): one 256x256x256 matmul layer.
+Per layer, on one Poseidon channel and in this order: q, k, v, o, gate, up
+matmuls, SiLU LogUp, down matmul, softmax-exp LogUp (Qwen only).  Each matmul
+gets a fresh output claim (r_out drawn from the channel, value = MLE of A*B at
+r_out, mixed), then the reference's matmul reduction; each LogUp layer gets a
+drawn claim point and value, then the reference's activation reduction.  The
+proof is serialized at the end of every step.
+
+Prints one JSON line.  value = matmul elements (weights k*n plus activations
+m*k) proved per second, in Melem/s; proved tokens/s and the HBM roofline of the
+dominant kernel (weight-side restriction) are reported beside it, with the CPU
+oracle (the reference's CPU algorithm) timed on a bounded sample.
+"""
+import argparse
+import ctypes as C
+import hashlib
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "stwo-ml_amd"))
+
+import gkr_mi355x as G  # noqa: E402
+
+METRIC = "GKR matmul-sumcheck Melem/s + % HBM peak; proved tokens/s, Qwen2.5-14B shape"
+HBM_PEAK_GBS = 8000.0
+K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE = range(6)
+
+QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
+SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
+
+
+def lg(v):
+    return max(0, (v - 1).bit_length())
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class LayerWeights:
+    def __init__(self, ctx, cfg, layer, seed_base):
+        h, i, q, kv, m = cfg["hidden"], cfg["inter"], cfg["q"], cfg["kv"], cfg["tokens"]
+        s = seed_base + 1000 * layer
+        # int8-range weights and activations (kind 1), resident in HBM
+        self.mats = {
+            "q": (ctx.synthetic(m, h, 1, s + 1), ctx.synthetic(h, q, 1, s + 2)),
+            "k": (None, ctx.synthetic(h, kv, 1, s + 3)),
+            "v": (None, ctx.synthetic(h, kv, 1, s + 4)),
+            "o": (ctx.synthetic(m, q, 1, s + 5), ctx.synthetic(q, h, 1, s + 6)),
+            "gate": (ctx.synthetic(m, h, 1, s + 7), ctx.synthetic(h, i, 1, s + 8)),
+            "up": (None, ctx.synthetic(h, i, 1, s + 9)),
+            "down": (ctx.synthetic(m, i, 1, s + 10), ctx.synthetic(i, h, 1, s + 11)),
+        }
+        # k, v share the attention input with q; up shares gate's input
+        self.mats["k"] = (self.mats["q"][0], self.mats["k"][1])
+        self.mats["v"] = (self.mats["q"][0], self.mats["v"][1])
+        self.mats["up"] = (self.mats["gate"][0], self.mats["up"][1])
+        # LogUp inputs: gate pre-activation (m x inter) and, for multi-token
+        # configs, the attention score tensor (heads*m x m); uniform M31 values
+        self.silu_in = ctx.synthetic(m, i, 0, s + 12)
+        self.scores = ctx.synthetic(cfg["heads"] * m, m, 0, s + 13) if m > 1 else None
+
+
+def matmul_elems(cfg):
+    h, i, q, kv, m = cfg["hidden"], cfg["inter"], cfg["q"], cfg["kv"], cfg["tokens"]
+    shapes = [(m, h, q), (m, h, kv), (m, h, kv), (m, q, h), (m, h, i), (m, h, i), (m, i, h)]
+    return sum(k * n + mm * k for mm, k, n in shapes), shapes
+
+
+def prove_matmul(ctx, ch, a, b, proof):
+    r = ch.draw_qm31s(lg(a.rows) + lg(b.cols))
+    v = ctx.matmul_output_claim(a, b, r)
+    ch.mix_secure_field(v)
+    return ctx.prove_matmul_layer(r, v, a, b, ch, proof)
+
+
+def prove_logup(ctx, ch, x, tag, tlog, proof):
+    r = ch.draw_qm31s(lg(x.rows) + lg(x.cols))
+    v = ch.draw_qm31()
+    return ctx.prove_activation_layer(r, v, x, tag, ch, tlog, proof)
+
+
+def prove_model(ctx, layers, cfg, seed):
+    ch = G.PoseidonChannel()
+    ch.mix_u64(seed)
+    proof = G.Proof()
+    for L in layers:
+        for name in ("q", "k", "v", "o", "gate", "up"):
+            a, b = L.mats[name]
+            prove_matmul(ctx, ch, a, b, proof)
+        prove_logup(ctx, ch, L.silu_in, 5, 16, proof)  # SiLU, 2^16 table
+        a, b = L.mats["down"]
+        prove_matmul(ctx, ch, a, b, proof)
+        if L.scores is not None:
+            prove_logup(ctx, ch, L.scores, 4, 16, proof)  # softmax-exp, 2^16 table
+    # serialize (C side) and fingerprint the felts
+    n = C.c_size_t()
+    G.lib().gkr_proof_serialize(proof.handle, None, 0, C.byref(n))
+    buf = (G.GkrFelt * n.value)()
+    G._check(G.lib().gkr_proof_serialize(proof.handle, buf, n.value, C.byref(n)))
+    fp = hashlib.sha256(bytes(buf)).hexdigest()[:16]
+    return ch.digest(), n.value, fp
+
+
+def cfg1_step(ctx, a, b):
+    ch = G.PoseidonChannel()
+    r = ch.draw_qm31s(16)
+    v = ctx.matmul_output_claim(a, b, r)
+    ch.mix_secure_field(v)
+    proof = G.Proof()
+    ctx.prove_matmul_layer(r, v, a, b, ch, proof)
+    return ch.digest(), 0, ""
+
+
+def cpu_baseline(budget_s=25.0):
+    """The oracle (reference CPU algorithm) on a bounded sample: Qwen q_proj layer reduction."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    m, k, n = 64, 5120, 5120
+    A = O.synthetic(m, k, 1, 1)
+    B = O.synthetic(k, n, 1, 2)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    t0 = time.perf_counter()
+    ch = O.Channel()
+    r = ch.draw_qm31s(lg(m) + lg(n))
+    v = O.matmul_output_claim(A, B, r)
+    ch.mix_secure_field(v)
+    O.prove_matmul_layer(r, v, A, B, ch)
+    dt = time.perf_counter() - t0
+    elems = k * n + m * k
+    return {"value": round(elems / dt / 1e6, 3), "unit": "Melem/s", "cores": threads, "kind": "port",
+            "sample": f"one Qwen2.5-14B q_proj layer (64x5120 . 5120x5120, int8-range) by the reference CPU "
+                      f"algorithm (forward GEMM for the claim, pad, QM31 MLE, restrict_mle, rounds): "
+                      f"{dt:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-timing", action="store_true", help="skip per-kernel HIP events")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(see the sharding design in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    ctx = G.Context(0)
+    if args.config == "cfg1":
+        cfg, n_layers = None, 1
+        a, b = ctx.synthetic(256, 256, 0, 0), ctx.synthetic(256, 256, 0, 1)
+        elems = 256 * 256 * 2
+        step = lambda: cfg1_step(ctx, a, b)  # noqa: E731
+        tokens = 0
+        workload = "config1-matmul-256x256x256-uniform-m31"
+    else:
+        cfg = QWEN if args.config.startswith("qwen") else SMOL
+        n_layers = {"qwen48": 48, "qwen1": 1, "smollm": 30}[args.config]
+        t0 = time.perf_counter()
+        layers = [LayerWeights(ctx, cfg, l, 0) for l in range(n_layers)]
+        ctx.synchronize()
+        log(f"[bench] {n_layers} layers of synthetic weights resident ({time.perf_counter() - t0:.2f} s)")
+        per_layer, shapes = matmul_elems(cfg)
+        elems = per_layer * n_layers
+        tokens = cfg["tokens"]
+        step = lambda: prove_model(ctx, layers, cfg, 7)  # noqa: E731
+        workload = {"qwen48": "qwen2.5-14b-48-layers-64-tokens", "qwen1": "qwen2.5-14b-1-layer-64-tokens",
+                    "smollm": "smollm2-135m-30-layers-1-token"}[args.config]
+
+    for w in range(args.warmup):
+        t0 = time.perf_counter()
+        out = step()
+        log(f"[bench] warmup {w}: {time.perf_counter() - t0:.3f} s digest={out[0]:#x}")
+    ctx.set_timing(not args.no_timing)
+    ctx.reset_timing()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    digests = []
+    for s in range(args.steps):
+        digests.append(step())
+        log(f"[bench] step {s} done ({time.perf_counter() - t0:.3f} s)")
+    ctx.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt / args.steps * 1e3
+    assert all(d == digests[0] for d in digests), "non-deterministic proof"
+
+    kernels = {}
+    for kid, name in [(K_RESTRICT_COLS, "restrict_cols"), (K_RESTRICT_ROWS, "restrict_rows"),
+                      (K_MM_ROUND, "mm_round"), (K_EQ3_ROUND, "eq3_round"), (K_LOGUP_PREP, "logup_prepare"),
+                      (K_EQ_TABLE, "eq_table")]:
+        ms, nl, nb = ctx.kernel_time(kid)
+        if nl:
+            kernels[name] = {"launches": nl, "avg_us": round(ms / nl * 1e3, 3),
+                             "gbps": round(nb / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
+                             "ms_per_step": round(ms / args.steps, 3)}
+    rc = kernels.get("restrict_cols")
+    roofline = None
+    if rc:
+        ms, nl, nb = ctx.kernel_time(K_RESTRICT_COLS)
+        ach = nb / (ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_restrict_cols",
+                    "avg_launch_us": rc["avg_us"], "bytes_per_launch": nb // nl}
+
+    result = {
+        "metric": METRIC,
+        "value": round(elems / (ms_per_step * 1e-3) / 1e6, 1),
+        "unit": "Melem/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u32-m31",
+        "data": "synthetic (counter-mode SplitMix64; int8-range weights/activations, uniform-M31 LogUp inputs)",
+        "config": {"workload": workload, "layers": n_layers, "tokens": tokens,
+                   "matmul_elements_per_step": elems, "logup_tables": "2^16 (SiLU, softmax-exp)"},
+        "proved_tokens_per_s": round(tokens / (ms_per_step * 1e-3), 3) if tokens else None,
+        "roofline": roofline,
+        "kernels": kernels,
+        "proof": {"felts": digests[0][1], "sha256_16": digests[0][2], "final_digest": hex(digests[0][0])},
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] timing CPU baseline sample")
+        result["cpu_baseline"] = cpu_baseline()
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

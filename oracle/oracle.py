@@ -343,3 +343,62 @@ def synthetic(rows: int, cols: int, kind: int, seed: int) -> np.ndarray:
 
 def synthetic_value(kind: int, seed: int, i: int) -> int:
     return int(lib().orc_synthetic_value(kind, seed, i))
+
+
+# ------------------------------------------------------------------ serialization
+def _ser_q(out: list, q) -> None:
+    out.extend(int(x) for x in q)
+
+
+def serialize_matmul_layer(out: list, round_polys, final_a, final_b) -> None:
+    """LayerProof::MatMul in serialize_gkr_model_proof (engine/src/cairo_serde.rs:1321-1336)."""
+    out.append(0)
+    out.append(len(round_polys))
+    for rp in round_polys:  # c1 omitted
+        _ser_q(out, rp[0])
+        _ser_q(out, rp[2])
+    _ser_q(out, final_a)
+    _ser_q(out, final_b)
+
+
+def serialize_activation_layer(out: list, act_type: int, proof) -> None:
+    """LayerProof::Activation with a LogUp proof (cairo_serde.rs:1367-1402, 1071-1105, 1138-1156)."""
+    out.append(3)
+    out.append(act_type)
+    _ser_q(out, proof["input_eval"])
+    _ser_q(out, proof["output_eval"])
+    out.append(int(proof["table_commitment"]))
+    out.append(1)  # has LogUp
+    _ser_q(out, proof["claimed_sum"])
+    out.append(len(proof["eq_round_polys"]))
+    for rp in proof["eq_round_polys"]:
+        _ser_q(out, rp[0])
+        _ser_q(out, rp[2])
+        _ser_q(out, rp[3])
+    for q in proof["final_evals"]:
+        _ser_q(out, q)
+    mults = list(int(x) for x in proof["multiplicities"])
+    out.append(len(mults))
+    out.extend(mults)
+    out.append(1)  # multiplicity sumcheck present
+    out.append(len(proof["mult_round_polys"]))
+    for c0, c1 in proof["mult_round_polys"]:
+        _ser_q(out, c0)
+        _ser_q(out, c1)
+    _ser_q(out, proof["mult_final_eval"])
+    _ser_q(out, proof["mult_claimed_sum"])
+    out.append(0)  # no activation product proof
+    out.append(0)  # no piecewise proof
+
+
+def serialize_tail(out: list, input_point, input_value, weight_commitments, io_commitment,
+                   n_weight_openings: int = 0) -> None:
+    """Input claim, weight commitments, opening count, IO commitment (cairo_serde.rs:1740-1771)."""
+    out.append(len(input_point))
+    for q in input_point:
+        _ser_q(out, q)
+    _ser_q(out, input_value)
+    out.append(len(weight_commitments))
+    out.extend(int(c) for c in weight_commitments)
+    out.append(n_weight_openings)
+    out.append(int(io_commitment))

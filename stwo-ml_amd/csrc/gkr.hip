@@ -7,6 +7,7 @@
 #include <string.h>
 
 #include <map>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -119,6 +120,7 @@ struct gkr_ctx {
   std::vector<hipEvent_t> free_events;
   MatMulCache mm;
   std::map<uint64_t, std::vector<uint32_t>> tables;  // (tag << 32 | log) -> table outputs
+  std::set<gkr_matrix*> matrices;  // live matrices; detached when the context is destroyed
 };
 
 static int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
@@ -321,13 +323,13 @@ extern "C" int gkr_channel_mix_u64(gkr_channel* ch, uint64_t v) {
 }
 extern "C" int gkr_channel_mix_felt(gkr_channel* ch, const gkr_felt* v) {
   CH_CHECK(ch);
-  if (!v || !felt_abi_canonical(*v)) return fail(GKR_ERR_INVALID, "bad felt");
+  if (!v || !felt_abi_canonical(*v)) return fail(GKR_ERR_INVALID, "felt252 value not canonical (must be < p)");
   ch->ch.mix_felt(felt_from_abi(*v));
   return GKR_OK;
 }
 extern "C" int gkr_channel_mix_secure_field(gkr_channel* ch, const gkr_qm31* v) {
   CH_CHECK(ch);
-  if (!v || !canonical_q(*v)) return fail(GKR_ERR_INVALID, "bad qm31");
+  if (!v || !canonical_q(*v)) return fail(GKR_ERR_INVALID, "qm31 value not canonical (each word must be < 2^31 - 1)");
   ch->ch.mix_secure_field(Q(*v));
   return GKR_OK;
 }
@@ -443,6 +445,11 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
     (void)hipEventDestroy(p.e1);
   }
   for (auto e : c->free_events) (void)hipEventDestroy(e);
+  for (gkr_matrix* m : c->matrices) {  // matrices outliving their context keep only the handle
+    if (m->owned && m->dev) (void)hipFree(m->dev);
+    m->dev = nullptr;
+    m->ctx = nullptr;
+  }
   for (int s = 0; s < S_NSLOTS; s++)
     if (c->buf[s]) (void)hipFree(c->buf[s]);
   if (c->h_res) (void)hipHostFree(c->h_res);
@@ -475,6 +482,7 @@ extern "C" int gkr_ctx_reset_timing(gkr_ctx* c) {
 }
 
 // ------------------------------------------------------------------ matrices
+static gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t cols, bool owned);
 extern "C" int gkr_matrix_upload(gkr_ctx* c, const uint32_t* host, uint64_t rows, uint64_t cols, gkr_matrix** out) {
   if (!c || !out || (!host && rows * cols)) return fail(GKR_ERR_INVALID, "null argument");
   if (rows == 0 || cols == 0) return fail(GKR_ERR_INVALID, "empty matrix %llux%llu", (unsigned long long)rows,
@@ -491,13 +499,13 @@ extern "C" int gkr_matrix_upload(gkr_ctx* c, const uint32_t* host, uint64_t rows
     (void)hipFree(d);
     return fail(GKR_ERR_DEVICE, "matrix upload: %s", hipGetErrorString(e));
   }
-  *out = new gkr_matrix{c, d, rows, cols, true};
+  *out = new_matrix(c, d, rows, cols, true);
   return GKR_OK;
 }
 extern "C" int gkr_matrix_wrap_device(gkr_ctx* c, const uint32_t* dev, uint64_t rows, uint64_t cols, gkr_matrix** out) {
   if (!c || !out || !dev) return fail(GKR_ERR_INVALID, "null argument");
   if (rows == 0 || cols == 0) return fail(GKR_ERR_INVALID, "empty matrix");
-  *out = new gkr_matrix{c, const_cast<uint32_t*>(dev), rows, cols, false};
+  *out = new_matrix(c, const_cast<uint32_t*>(dev), rows, cols, false);
   return GKR_OK;
 }
 extern "C" int gkr_matrix_synthetic(gkr_ctx* c, uint64_t rows, uint64_t cols, int kind, uint64_t seed,
@@ -515,23 +523,31 @@ extern "C" int gkr_matrix_synthetic(gkr_ctx* c, uint64_t rows, uint64_t cols, in
     (void)hipFree(d);
     return rc;
   }
-  *out = new gkr_matrix{c, d, rows, cols, true};
+  *out = new_matrix(c, d, rows, cols, true);
   return GKR_OK;
 }
 extern "C" int gkr_matrix_download(gkr_ctx* c, const gkr_matrix* m, uint32_t* host) {
   if (!c || !m || !host) return fail(GKR_ERR_INVALID, "null argument");
+  if (m->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another (or a destroyed) context");
   HIP_TRY(hipMemcpyAsync(host, m->dev, m->rows * m->cols * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
   return sync(c);
 }
 extern "C" void gkr_matrix_free(gkr_matrix* m) {
   if (!m) return;
-  if (m->ctx && m->ctx->mm.a == m) m->ctx->mm.valid = false;
-  if (m->ctx && m->ctx->mm.b == m) m->ctx->mm.valid = false;
-  if (m->owned && m->dev) {
-    (void)hipStreamSynchronize(m->ctx->stream);
-    (void)hipFree(m->dev);
+  if (m->ctx) {
+    if (m->ctx->mm.a == m || m->ctx->mm.b == m) m->ctx->mm.valid = false;
+    m->ctx->matrices.erase(m);
+    if (m->owned && m->dev) {
+      (void)hipStreamSynchronize(m->ctx->stream);
+      (void)hipFree(m->dev);
+    }
   }
   delete m;
+}
+static gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t cols, bool owned) {
+  gkr_matrix* m = new gkr_matrix{c, dev, rows, cols, owned};
+  c->matrices.insert(m);
+  return m;
 }
 extern "C" uint32_t gkr_synthetic_value(int kind, uint64_t seed, uint64_t i) { return synth_value(kind, seed, i); }
 
@@ -556,7 +572,7 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
   {
     TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + 16 * pk);
     const unsigned g = (unsigned)((k + kRowsPerBlock - 1) / kRowsPerBlock);
-    if (n % 4 == 0)
+    if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
       hipLaunchKernelGGL(k_restrict_cols<true>, dim3(g), dim3(kBlock), 0, c->stream, B->dev, k, n, Lj, fb);
     else
       hipLaunchKernelGGL(k_restrict_cols<false>, dim3(g), dim3(kBlock), 0, c->stream, B->dev, k, n, Lj, fb);

@@ -1,0 +1,143 @@
+"""C ABI of the product library: symbols, host-side channel and tables (no GPU)."""
+import os
+import random
+import re
+
+import gkr_mi355x as G
+import numpy as np
+import oracle as O
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+P = (1 << 31) - 1
+
+
+def header_symbols():
+    text = open(os.path.join(ROOT, "include", "gkr_mi355x.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gkr_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = G.lib()
+    syms = header_symbols()
+    assert len(syms) >= 40
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing
+    # and the Python binding declares every one of them
+    bound = {name for name, _, _ in G.SIGNATURES}
+    assert set(syms) <= bound, set(syms) - bound
+
+
+def test_poseidon_kats_through_abi(golden):
+    g = golden["poseidon"]
+    ch = G.PoseidonChannel()
+    ch.mix_u64(g["mix_u64"]["value"])
+    assert ch.digest() == int(g["mix_u64"]["digest"], 16)
+    ch = G.PoseidonChannel()
+    ch.mix_felts([g["mix_felts_qm31_1234"]["value"]])
+    assert ch.digest() == int(g["mix_felts_qm31_1234"]["digest"], 16)
+
+
+def rq(rng):
+    return tuple(rng.randrange(P) for _ in range(4))
+
+
+def test_channel_matches_oracle_on_random_transcripts():
+    rng = random.Random(11)
+    for trial in range(20):
+        a, b = G.PoseidonChannel(), O.Channel()
+        for step in range(25):
+            op = rng.randrange(8)
+            if op == 0:
+                v = rng.getrandbits(64)
+                a.mix_u64(v); b.mix_u64(v)
+            elif op == 1:
+                q = rq(rng)
+                a.mix_secure_field(q); b.mix_secure_field(q)
+            elif op == 2:
+                cs = [rq(rng) for _ in range(3)]
+                a.mix_poly_coeffs(*cs); b.mix_poly_coeffs(*cs)
+            elif op == 3:
+                cs = [rq(rng) for _ in range(4)]
+                a.mix_poly_coeffs_deg3(*cs); b.mix_poly_coeffs_deg3(*cs)
+            elif op == 4:
+                qs = [rq(rng) for _ in range(rng.randrange(0, 6))]
+                a.mix_felts(qs); b.mix_felts(qs)
+            elif op == 5:
+                assert a.draw_qm31() == b.draw_qm31()
+            elif op == 6:
+                assert a.draw_felt252() == b.draw_felt252()
+            else:
+                v = rng.randrange(O_P252())
+                a.mix_felt(v); b.mix_felt(v)
+            assert a.digest() == b.digest()
+
+
+def O_P252():
+    return 2**251 + 17 * 2**192 + 1
+
+
+def test_channel_state_export_import_and_clone():
+    ch = G.PoseidonChannel()
+    ch.mix_u64(7)
+    ch.draw_qm31()
+    st = ch.export_state()
+    assert st[8] == 1 and st[9] == 2 and st[10] == 0  # n_draws, hash_count
+    other = G.PoseidonChannel()
+    other.import_state(st)
+    assert other.digest() == ch.digest() and other.draw_qm31() == ch.clone().draw_qm31()
+    words = [(ch.digest() >> (32 * i)) & 0xFFFFFFFF for i in range(8)]
+    assert st[:8] == words
+
+
+def test_hash_many_and_permutation_match_oracle():
+    rng = random.Random(5)
+    for n in range(0, 7):
+        xs = [rng.randrange(O_P252()) for _ in range(n)]
+        assert G.poseidon_hash_many(xs) == O.hash_many(xs)
+    st = [rng.randrange(O_P252()) for _ in range(3)]
+    assert G.hades_permute(st) == O.hades(st)
+    assert G.poseidon_hash(st[0], st[1]) == O.hades([st[0], st[1], 2])[0]
+
+
+def test_gkr_seeding_with_and_without_policy():
+    a, b = G.PoseidonChannel(), O.Channel()
+    a.seed_gkr(3, 1, 4)
+    for v in (3, 1, 4):
+        b.mix_u64(v)
+    assert a.digest() == b.digest()
+    a.seed_gkr(1, 2, 3, policy_commitment=0)  # zero commitment is skipped
+    for v in (1, 2, 3):
+        b.mix_u64(v)
+    assert a.digest() == b.digest()
+    a.seed_gkr(1, 2, 3, policy_commitment=12345)
+    for v in (1, 2, 3):
+        b.mix_u64(v)
+    b.mix_felt(12345)
+    assert a.digest() == b.digest()
+
+
+@pytest.mark.parametrize("tag", [1, 2, 3, 4, 5])
+def test_activation_tables_match_oracle(tag):
+    t = G.activation_table(tag, 16)
+    ref = np.array([O.activation(tag, j) for j in range(0, 1 << 16)], dtype=np.uint32)
+    assert (t == ref).all()
+
+
+def test_synthetic_generator_matches_oracle():
+    for kind in (0, 1):
+        for seed in (0, 1, 2**63 + 5):
+            for i in list(range(100)) + [10**9, 2**40 + 3]:
+                assert G.synthetic_value(kind, seed, i) == O.synthetic_value(kind, seed, i)
+
+
+def test_errors_are_reported():
+    ch = G.PoseidonChannel()
+    with pytest.raises(G.GkrError) as e:
+        ch.mix_secure_field((P, 0, 0, 0))  # not canonical
+    assert "canonical" in str(e.value)
+    with pytest.raises(G.GkrError):
+        ch.mix_felt(O_P252())
+    with pytest.raises(G.GkrError):
+        G.activation_table(9, 8)

@@ -1,0 +1,282 @@
+"""HIP path (through the C ABI) against the CPU oracle: bit-exact parity.
+
+Small and mid sizes compare every output word with the oracle on the same
+seeded inputs; the Qwen2.5-14B up-projection shape is checked through
+size-independent properties (verifier replay, final evaluations equal the
+MLEs of A and B at the challenge point).
+"""
+import random
+import sys
+
+import gkr_mi355x as G
+import numpy as np
+import oracle as O
+import pytest
+
+pytestmark = pytest.mark.gpu
+P = (1 << 31) - 1
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def npow2(v):
+    return 1 << max(0, (v - 1).bit_length())
+
+
+def lg(v):
+    return npow2(v).bit_length() - 1
+
+
+def test_sp3_fixture_on_gpu(gpu_ctx, golden):
+    sp3 = golden["sp3"]
+    log("case sp3 1x4 . 4x2")
+    A = np.array([[1, 2, 3, 4]], dtype=np.uint32)
+    B = np.array([[2 * i + j + 1 for j in range(2)] for i in range(4)], dtype=np.uint32)
+    a, b = gpu_ctx.upload(A), gpu_ctx.upload(B)
+    ch = G.PoseidonChannel()
+    ch.seed_gkr(1, 1, 4)
+    r_out = ch.draw_qm31s(1)
+    value = gpu_ctx.matmul_output_claim(a, b, r_out)
+    assert value == O.evaluate_mle([(50, 0, 0, 0), (60, 0, 0, 0)], r_out)
+    ch.mix_secure_field(value)
+    proof = G.Proof()
+    res = gpu_ctx.prove_matmul_layer(r_out, value, a, b, ch, proof)
+    assert ch.digest() == int(sp3["post_walk_digest"], 16)
+    assert [list(q) for q in res["next_point"]] == sp3["input_claim_point"]
+    proof.set_input_claim(res["next_point"], res["next_value"])
+    proof.add_weight_commitment(int(sp3["weight_commitments"][0], 16))
+    felts = proof.serialize()
+    cd = [int(x, 16) for x in sp3["calldata_hex"]]
+    # num_layers, MatMul proof, input claim, weight commitments: the first 42 felts
+    assert felts[:42] == cd[:42]
+
+
+def _random_point(rng, n):
+    return [tuple(rng.randrange(P) for _ in range(4)) for _ in range(n)]
+
+
+def _compare_layer(ctx, A, B, seed, label):
+    log(f"case {label} A{A.shape} B{B.shape}")
+    a, b = ctx.upload(A), ctx.upload(B)
+    m, k = A.shape
+    n = B.shape[1]
+    gch, och = G.PoseidonChannel(), O.Channel()
+    gch.mix_u64(seed)
+    och.mix_u64(seed)
+    nv = lg(m) + lg(n)
+    r_g, r_o = gch.draw_qm31s(nv), och.draw_qm31s(nv)
+    assert r_g == r_o
+    v_g = ctx.matmul_output_claim(a, b, r_g)
+    v_o = O.matmul_output_claim(A, B, r_o)
+    assert v_g == v_o
+    gch.mix_secure_field(v_g)
+    och.mix_secure_field(v_o)
+    rg = ctx.prove_matmul_layer(r_g, v_g, a, b, gch)
+    ro = O.prove_matmul_layer(r_o, v_o, A, B, och)
+    assert rg["round_polys"] == ro["round_polys"]
+    assert rg["final_a_eval"] == ro["final_a_eval"] and rg["final_b_eval"] == ro["final_b_eval"]
+    assert rg["next_point"] == ro["next_point"] and rg["next_value"] == ro["next_value"]
+    assert gch.digest() == och.digest()
+    a.free()
+    b.free()
+
+
+def test_config1_uniform_256(gpu_ctx):
+    """A, B 256x256 uniform M31 (A seed 0, B seed 1), channel new()."""
+    A = O.synthetic(256, 256, 0, 0)
+    B = O.synthetic(256, 256, 0, 1)
+    log("case config1 256x256x256")
+    a, b = gpu_ctx.synthetic(256, 256, 0, 0), gpu_ctx.synthetic(256, 256, 0, 1)
+    assert (a.download() == A).all() and (b.download() == B).all()
+    gch, och = G.PoseidonChannel(), O.Channel()
+    r = gch.draw_qm31s(16)
+    assert r == och.draw_qm31s(16)
+    v = gpu_ctx.matmul_output_claim(a, b, r)
+    assert v == O.matmul_output_claim(A, B, r)
+    rg = gpu_ctx.prove_matmul_layer(r, v, a, b, gch)
+    ro = O.prove_matmul_layer(r, v, A, B, och)
+    assert len(rg["round_polys"]) == 8
+    assert rg == ro
+    assert gch.digest() == och.digest()
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (1, 4, 2), (2, 3, 5), (7, 13, 3), (1, 64, 1), (16, 1, 8),
+                                   (33, 100, 70), (64, 300, 257), (5, 1024, 12), (64, 576, 192), (3, 2048, 4)])
+def test_matmul_layer_random_shapes(gpu_ctx, m, k, n):
+    rng = np.random.default_rng(m * 10007 + k * 101 + n)
+    A = rng.integers(0, P, size=(m, k), dtype=np.uint32)
+    B = rng.integers(0, P, size=(k, n), dtype=np.uint32)
+    _compare_layer(gpu_ctx, A, B, m + k + n, "random")
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 576, 576), (1, 1536, 576), (64, 512, 1024)])
+def test_matmul_layer_int8_range(gpu_ctx, m, k, n):
+    A = O.synthetic(m, k, 1, 11)
+    B = O.synthetic(k, n, 1, 12)
+    _compare_layer(gpu_ctx, A, B, 3, "int8")
+
+
+def test_boundary_values(gpu_ctx):
+    # extremes of M31: 0 and P - 1 everywhere
+    A = np.full((4, 8), P - 1, dtype=np.uint32)
+    B = np.full((8, 4), P - 1, dtype=np.uint32)
+    B[::2] = 0
+    _compare_layer(gpu_ctx, A, B, 1, "extremes")
+
+
+def test_zkmlops_reduce_matmul_layer(gpu_ctx):
+    rng = random.Random(4)
+    for (m, k, n) in [(4, 8, 4), (3, 17, 9), (1, 32, 1), (8, 1, 2)]:
+        log(f"case zkmlops {m}x{k}x{n}")
+        nprng = np.random.default_rng(k)
+        A = nprng.integers(0, P, size=(m, k), dtype=np.uint32)
+        B = nprng.integers(0, P, size=(k, n), dtype=np.uint32)
+        r_i, r_j = _random_point(rng, lg(m)), _random_point(rng, lg(n))
+        gch, och = G.PoseidonChannel(), O.Channel()
+        a, b = gpu_ctx.upload(A), gpu_ctx.upload(B)
+        rg = gpu_ctx.reduce_matmul_layer(a, b, r_i, r_j, npow2(k), gch)
+        ro = O.reduce_matmul_layer(A, B, r_i, r_j, npow2(k), och)
+        assert rg == ro
+        assert gch.digest() == och.digest()
+
+
+def test_zkmlops_shape_errors(gpu_ctx):
+    a = gpu_ctx.upload(np.ones((2, 3), dtype=np.uint32))
+    b = gpu_ctx.upload(np.ones((4, 2), dtype=np.uint32))
+    ch = G.PoseidonChannel()
+    with pytest.raises(G.GkrError):
+        gpu_ctx.reduce_matmul_layer(a, b, [(1, 0, 0, 0)], [(1, 0, 0, 0)], 4, ch)
+    b2 = gpu_ctx.upload(np.ones((3, 2), dtype=np.uint32))
+    with pytest.raises(G.GkrError):  # wrong pk
+        gpu_ctx.reduce_matmul_layer(a, b2, [(1, 0, 0, 0)], [(1, 0, 0, 0)], 8, ch)
+    with pytest.raises(G.GkrError):  # non-canonical upload
+        gpu_ctx.upload(np.full((2, 2), P, dtype=np.uint32))
+
+
+def test_mle_ops(gpu_ctx):
+    rng = random.Random(9)
+    for n in (0, 1, 3, 6, 11):
+        log(f"case mle n={n}")
+        evals = _random_point(rng, 1 << n)
+        point = _random_point(rng, n)
+        assert gpu_ctx.evaluate_mle_at_point(evals, point) == O.evaluate_mle(evals, point)
+        for s in range(0, n + 1, max(1, n // 2)):
+            assign = _random_point(rng, s)
+            assert gpu_ctx.restrict_mle(evals, assign) == O.restrict_mle(evals, assign)
+
+
+@pytest.mark.parametrize("rows,cols,tag,tlog", [(1, 8, 5, 8), (4, 16, 5, 10), (3, 5, 1, 6), (2, 32, 4, 8),
+                                                (1, 1536, 5, 16), (8, 96, 2, 12), (16, 64, 3, 16)])
+def test_activation_layer_parity(gpu_ctx, rows, cols, tag, tlog):
+    log(f"case logup {rows}x{cols} tag={tag} table=2^{tlog}")
+    X = O.synthetic(rows, cols, 0, rows * 1000 + cols)
+    nv = lg(rows) + lg(cols)
+    gch, och = G.PoseidonChannel(), O.Channel()
+    pt = gch.draw_qm31s(nv)
+    val = gch.draw_qm31()
+    assert pt == och.draw_qm31s(nv) and val == och.draw_qm31()
+    x = gpu_ctx.upload(X)
+    gp = G.Proof()
+    pg = gpu_ctx.prove_activation_layer(pt, val, x, tag, gch, tlog, gp)
+    po = O.prove_activation_layer(pt, val, X, tag, och, tlog)
+    for key in ("claimed_sum", "eq_round_polys", "final_evals", "mult_round_polys", "mult_final_eval",
+                "mult_claimed_sum", "input_eval", "output_eval", "table_commitment"):
+        assert pg[key] == po[key], key
+    assert (pg["multiplicities"] == po["multiplicities"]).all()
+    assert gch.digest() == och.digest()
+    # serialized layer equals the oracle's serialization
+    gp.set_input_claim(pt, pg["input_eval"])
+    felts = gp.serialize()
+    ref = [1]
+    O.serialize_activation_layer(ref, tag, po)
+    O.serialize_tail(ref, pt, po["input_eval"], [], 0)
+    assert felts == ref
+
+
+def test_two_layer_walk_and_serialization(gpu_ctx):
+    """MatMul -> SiLU(LogUp) -> MatMul walk on one channel, claims chained as in the GKR loop."""
+    log("case walk")
+    X = O.synthetic(4, 64, 1, 21)
+    W1 = O.synthetic(64, 32, 1, 22)
+    H = O.matmul_forward(X, W1)
+    W2 = O.synthetic(32, 16, 1, 23)
+    gx, gw1, gh, gw2 = gpu_ctx.upload(X), gpu_ctx.upload(W1), gpu_ctx.upload(H), gpu_ctx.upload(W2)
+    gch, och = G.PoseidonChannel(), O.Channel()
+    for ch in (gch, och):
+        ch.mix_u64(3); ch.mix_u64(4); ch.mix_u64(64)
+    r = gch.draw_qm31s(lg(4) + lg(16))
+    assert r == och.draw_qm31s(lg(4) + lg(16))
+    # output layer claim on W2's product (the walk's last matmul consumes H directly here)
+    v = gpu_ctx.matmul_output_claim(gh, gw2, r)
+    assert v == O.matmul_output_claim(H, W2, r)
+    gch.mix_secure_field(v); och.mix_secure_field(v)
+    proof = G.Proof()
+    l1 = gpu_ctx.prove_matmul_layer(r, v, gh, gw2, gch, proof)
+    o1 = O.prove_matmul_layer(r, v, H, W2, och)
+    assert l1 == o1
+    l2 = gpu_ctx.prove_activation_layer(l1["next_point"], l1["next_value"], gh, 5, gch, 12, proof)
+    o2 = O.prove_activation_layer(o1["next_point"], o1["next_value"], H, 5, och, 12)
+    assert l2["eq_round_polys"] == o2["eq_round_polys"] and gch.digest() == och.digest()
+    l3 = gpu_ctx.prove_matmul_layer(l1["next_point"], l2["input_eval"], gx, gw1, gch, proof)
+    o3 = O.prove_matmul_layer(o1["next_point"], o2["input_eval"], X, W1, och)
+    assert l3 == o3 and gch.digest() == och.digest()
+    proof.set_input_claim(l3["next_point"], l3["next_value"])
+    ref = [3]
+    O.serialize_matmul_layer(ref, o1["round_polys"], o1["final_a_eval"], o1["final_b_eval"])
+    O.serialize_activation_layer(ref, 5, o2)
+    O.serialize_matmul_layer(ref, o3["round_polys"], o3["final_a_eval"], o3["final_b_eval"])
+    O.serialize_tail(ref, o3["next_point"], o3["next_value"], [], 0)
+    assert proof.serialize() == ref
+
+
+def test_qwen_up_projection_properties(gpu_ctx):
+    """Qwen2.5-14B MLP up projection (64 x 5120 . 5120 x 13824, int8-range): verifier replay and
+    final evaluations equal MLE_A / MLE_B^T at the challenge point (oracle on the CPU)."""
+    m, k, n = 64, 5120, 13824
+    log("case qwen up 64x5120x13824")
+    a = gpu_ctx.synthetic(m, k, 1, 101)
+    b = gpu_ctx.synthetic(k, n, 1, 102)
+    ch = G.PoseidonChannel()
+    ch.mix_u64(42)
+    vch = O.Channel()
+    vch.mix_u64(42)
+    nv = lg(m) + lg(n)
+    r = ch.draw_qm31s(nv)
+    assert r == vch.draw_qm31s(nv)
+    v = gpu_ctx.matmul_output_claim(a, b, r)
+    res = gpu_ctx.prove_matmul_layer(r, v, a, b, ch)
+    assert len(res["round_polys"]) == 13
+    assert O.verify_matmul_layer(r, v, m, k, n, res["round_polys"], res["final_a_eval"], res["final_b_eval"],
+                                 vch) == 0
+    assert vch.digest() == ch.digest()
+    A = O.synthetic(m, k, 1, 101)
+    lm = lg(m)
+    fa = O.restrict_rows_fused(A, r[:lm], npow2(k))
+    assert O.evaluate_mle([tuple(int(x) for x in row) for row in fa], res["next_point"][lm:]) == res["final_a_eval"]
+    B = b.download()
+    assert B[7, 11] == O.synthetic_value(1, 102, 7 * n + 11)
+    fb = O.restrict_cols_fused(B, r[lm:], npow2(k))
+    assert O.evaluate_mle([tuple(int(x) for x in row) for row in fb], res["next_point"][lm:]) == res["final_b_eval"]
+    # the claim is MLE_C(r) = sum_l f_a[l] f_b[l]
+    s = (0, 0, 0, 0)
+    for x, y in zip(fa, fb):
+        s = O.qadd(s, O.qmul(tuple(int(t) for t in x), tuple(int(t) for t in y)))
+    assert v == s
+
+
+def test_matrix_outlives_context():
+    """Freeing a matrix after its context was destroyed is safe; using it is an error."""
+    ctx = G.Context(0)
+    a = ctx.upload(np.ones((2, 2), dtype=np.uint32))
+    b = ctx.upload(np.ones((2, 2), dtype=np.uint32))
+    ctx.close()
+    a.free()
+    other = G.Context(0)
+    ch = G.PoseidonChannel()
+    with pytest.raises(G.GkrError):
+        other.reduce_matmul_layer(b, b, [(1, 0, 0, 0)], [(1, 0, 0, 0)], 2, ch)
+    b.free()
+    other.close()

@@ -1,0 +1,199 @@
+"""The CPU oracle pinned by what the mathematics fixes (no GPU).
+
+Brute-force MLE sums on tiny inputs (pure-Python third implementation),
+fused == naive restriction (the equality the reference relies on in
+components/matmul.rs:2045-2218), sumcheck and LogUp identities, and the
+restated verifier accepting honest proofs and rejecting tampered ones.
+"""
+import random
+
+import numpy as np
+import oracle as O
+import pytest
+import qm31_py as Q
+
+P = (1 << 31) - 1
+
+
+def rq(rng):
+    return tuple(rng.randrange(P) for _ in range(4))
+
+
+def test_qm31_field_axioms():
+    rng = random.Random(1)
+    for _ in range(50):
+        x, y, z = rq(rng), rq(rng), rq(rng)
+        assert O.qmul(x, y) == Q.qmul(x, y)
+        assert O.qmul(O.qmul(x, y), z) == O.qmul(x, O.qmul(y, z))
+        assert O.qmul(x, O.qadd(y, z)) == O.qadd(O.qmul(x, y), O.qmul(x, z))
+        assert O.qmul(x, O.qinv(x)) == (1, 0, 0, 0)
+    # u^2 = 2 + i
+    assert O.qmul((0, 0, 1, 0), (0, 0, 1, 0)) == (2, 1, 0, 0)
+    # inverse through Fermat in the full extension (pure Python)
+    x = rq(rng)
+    assert O.qinv(x) == Q.qinv(x)
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 3, 5])
+def test_evaluate_mle_bruteforce(n):
+    rng = random.Random(n)
+    evals = [rq(rng) for _ in range(1 << n)]
+    point = [rq(rng) for _ in range(n)]
+    assert O.evaluate_mle(evals, point) == Q.mle_bruteforce(evals, point)
+
+
+def test_eq_tables_agree_and_bruteforce():
+    rng = random.Random(7)
+    r = [rq(rng) for _ in range(5)]
+    eq = O.eq_evals(r)
+    lg = O.lagrange_basis(r)
+    assert (eq == lg).all()
+    for x in range(32):
+        assert tuple(int(v) for v in eq[x]) == Q.eq_weight(r, x, 5)
+    s = (0, 0, 0, 0)
+    for x in range(32):
+        s = Q.qadd(s, tuple(int(v) for v in eq[x]))
+    assert s == (1, 0, 0, 0)  # sum of eq over the hypercube
+
+
+def test_restrict_mle_bruteforce():
+    rng = random.Random(3)
+    n, s = 5, 2
+    evals = [rq(rng) for _ in range(1 << n)]
+    assign = [rq(rng) for _ in range(s)]
+    out = O.restrict_mle(evals, assign)
+    rest = 1 << (n - s)
+    for y in range(rest):
+        want = (0, 0, 0, 0)
+        for x in range(1 << s):
+            want = Q.qadd(want, Q.qmul(Q.eq_weight(assign, x, s), evals[x * rest + y]))
+        assert out[y] == want
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4, 2), (3, 5, 7), (8, 16, 4), (5, 1, 3), (16, 33, 9)])
+def test_fused_restrict_equals_naive(m, k, n):
+    rng = np.random.default_rng(m * 100 + k * 10 + n)
+    A = rng.integers(0, P, size=(m, k), dtype=np.uint32)
+    B = rng.integers(0, P, size=(k, n), dtype=np.uint32)
+    pm, pk, pn = [1 << max(0, (v - 1).bit_length()) for v in (m, k, n)]
+    r = random.Random(m + k + n)
+    r_i = [rq(r) for _ in range(pm.bit_length() - 1)]
+    r_j = [rq(r) for _ in range(pn.bit_length() - 1)]
+    # naive: pad -> MLE -> restrict (backend.rs:127-134)
+    Ap = np.zeros((pm, pk), dtype=np.uint32)
+    Ap[:m, :k] = A
+    a_mle = [(int(v), 0, 0, 0) for v in Ap.reshape(-1)]
+    fa = O.restrict_mle(a_mle, r_i)
+    Bp = np.zeros((pk, pn), dtype=np.uint32)
+    Bp[:k, :n] = B
+    b_mle = [(int(v), 0, 0, 0) for v in Bp.T.reshape(-1)]  # column-major
+    fb = O.restrict_mle(b_mle, r_j)
+    fa2 = O.restrict_rows_fused(A, r_i, pk)
+    fb2 = O.restrict_cols_fused(B, r_j, pk)
+    assert [tuple(int(x) for x in row) for row in fa2] == fa
+    assert [tuple(int(x) for x in row) for row in fb2] == fb
+    # MLE_C(r_i || r_j) == sum_l f_a[l] f_b[l]   (C = A B)
+    claim = O.matmul_output_claim(A, B, r_i + r_j)
+    s = (0, 0, 0, 0)
+    for x, y in zip(fa, fb):
+        s = Q.qadd(s, Q.qmul(x, y))
+    assert s == claim
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 4, 2), (4, 8, 4), (3, 7, 5), (1, 1, 1), (2, 1, 3), (6, 3, 1)])
+def test_matmul_sumcheck_identities_and_verifier(m, k, n):
+    rng = np.random.default_rng(k * 31 + m)
+    A = rng.integers(0, P, size=(m, k), dtype=np.uint32)
+    B = rng.integers(0, P, size=(k, n), dtype=np.uint32)
+    ch = O.Channel()
+    ch.mix_u64(99)
+    pm, pk, pn = [1 << max(0, (v - 1).bit_length()) for v in (m, k, n)]
+    nv = (pm.bit_length() - 1) + (pn.bit_length() - 1)
+    r = ch.draw_qm31s(nv)
+    claim = O.matmul_output_claim(A, B, r)
+    vch = ch.clone()
+    res = O.prove_matmul_layer(r, claim, A, B, ch)
+    # each round: p(0) + p(1) = running claim; last: p(r) = final_a * final_b
+    cur = claim
+    for (c0, c1, c2), rr in zip(res["round_polys"], res["next_point"][pm.bit_length() - 1:]):
+        assert Q.qadd(c0, Q.qadd(Q.qadd(c0, c1), c2)) == cur
+        cur = Q.qadd(Q.qadd(c0, Q.qmul(c1, rr)), Q.qmul(Q.qmul(c2, rr), rr))
+    assert cur == Q.qmul(res["final_a_eval"], res["final_b_eval"])
+    # final_a = MLE_A(r_i || challenges), final_b = MLE_B^T(r_j || challenges)
+    Ap = np.zeros((pm, pk), dtype=np.uint32)
+    Ap[:m, :k] = A
+    assert O.evaluate_mle([(int(v), 0, 0, 0) for v in Ap.reshape(-1)], res["next_point"]) == res["final_a_eval"]
+    Bp = np.zeros((pk, pn), dtype=np.uint32)
+    Bp[:k, :n] = B
+    lm = pm.bit_length() - 1
+    bpt = r[lm:] + res["next_point"][lm:]
+    assert O.evaluate_mle([(int(v), 0, 0, 0) for v in Bp.T.reshape(-1)], bpt) == res["final_b_eval"]
+    assert O.verify_matmul_layer(r, claim, m, k, n, res["round_polys"], res["final_a_eval"], res["final_b_eval"],
+                                 vch) == 0
+    assert vch.digest() == ch.digest()
+
+
+def test_activation_functions():
+    # fixed-point scale 2^16; values above P/2 are negative (lookup_table.rs:192-342)
+    assert O.activation(5, 0) == 0
+    big = 20 << 16
+    assert O.activation(5, big) == big  # silu(20) = 20 / (1 + e^-20) rounds to 20
+    assert O.activation(1, 5) == 5 and O.activation(1, P - 5) == 0
+    assert O.activation(3, 0) == 1 << 15 and O.activation(3, 7) == 1 << 16 and O.activation(3, P - 1) == 0
+    assert O.activation(4, 0) == 1 << 16 and O.activation(4, 3 << 16) == 1 << 19
+    assert O.activation(4, P - 1) == 1 << 16  # neg = 0 -> decay 0
+    prev = -1
+    for x in range(0, 1 << 16, 97):  # silu is increasing on x >= 0
+        v = O.activation(5, x)
+        assert v >= prev
+        prev = v
+
+
+@pytest.mark.parametrize("rows,cols,tag,tlog", [(1, 8, 5, 8), (4, 16, 5, 10), (3, 5, 1, 6), (2, 32, 4, 8),
+                                                (1, 1, 2, 4)])
+def test_logup_identities_and_verifier(rows, cols, tag, tlog):
+    rng = np.random.default_rng(rows * 7 + cols)
+    X = rng.integers(0, P, size=(rows, cols), dtype=np.uint32)
+    n = (1 << max(0, (rows - 1).bit_length())) * (1 << max(0, (cols - 1).bit_length()))
+    nv = n.bit_length() - 1
+    ch = O.Channel()
+    ch.mix_u64(5)
+    pt = ch.draw_qm31s(nv)
+    val = ch.draw_qm31()
+    vch = ch.clone()
+    if nv == 0:
+        # the reference prover handles a single element (no eq rounds) but its
+        # verifier rejects a 0-round eq-sumcheck (verifier.rs: "has 0 rounds")
+        proof = O.prove_activation_layer(pt, val, X, tag, ch, tlog)
+        assert proof["eq_round_polys"] == []
+        assert O.verify_activation_layer(pt, val, tag, tlog, proof, vch) != 0
+        return
+    proof = O.prove_activation_layer(pt, val, X, tag, ch, tlog)
+    assert int(proof["multiplicities"].sum()) == n
+    assert proof["mult_claimed_sum"] == (n % P, 0, 0, 0)
+    # multiplicity final eval = MLE of the multiplicities at the round challenges (checked via chain)
+    assert O.verify_activation_layer(pt, val, tag, tlog, proof, vch) == 0
+    assert vch.digest() == ch.digest()
+    # input_eval is MLE(padded input) at the claim point
+    pr, pc = 1 << max(0, (rows - 1).bit_length()), 1 << max(0, (cols - 1).bit_length())
+    Xp = np.zeros((pr, pc), dtype=np.uint32)
+    Xp[:rows, :cols] = X
+    assert O.evaluate_mle([(int(v), 0, 0, 0) for v in Xp.reshape(-1)], pt) == proof["input_eval"]
+    assert proof["table_commitment"] == O.hash_many([tag, tlog])
+    # tampering with the LogUp sum or a round poly is rejected
+    bad = dict(proof)
+    bad["claimed_sum"] = Q.qadd(proof["claimed_sum"], (1, 0, 0, 0))
+    ch2 = O.Channel()
+    ch2.mix_u64(5)
+    ch2.draw_qm31s(nv)
+    ch2.draw_qm31()
+    assert O.verify_activation_layer(pt, val, tag, tlog, bad, ch2) != 0
+    bad = dict(proof)
+    rp = list(proof["eq_round_polys"])
+    rp[0] = (rp[0][0], rp[0][1], Q.qadd(rp[0][2], (1, 0, 0, 0)), rp[0][3])
+    bad["eq_round_polys"] = rp
+    ch3 = O.Channel()
+    ch3.mix_u64(5)
+    ch3.draw_qm31s(nv)
+    ch3.draw_qm31()
+    assert O.verify_activation_layer(pt, val, tag, tlog, bad, ch3) != 0
