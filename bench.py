@@ -33,7 +33,7 @@ import gkr_mi355x as G  # noqa: E402
 
 METRIC = "GKR matmul-sumcheck Melem/s + % HBM peak; proved tokens/s, Qwen2.5-14B shape"
 HBM_PEAK_GBS = 8000.0
-K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE = range(6)
+K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT = range(8)
 
 QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
 SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
@@ -90,7 +90,29 @@ def prove_logup(ctx, ch, x, tag, tlog, proof):
     return ctx.prove_activation_layer(r, v, x, tag, ch, tlog, proof)
 
 
-def prove_model(ctx, layers, cfg, seed):
+class SerialBuffer:
+    """Reused output buffer for the serialized proof (felt252 calldata)."""
+
+    def __init__(self):
+        self.buf, self.cap, self.n = None, 0, 0
+
+    def serialize(self, proof) -> int:
+        n = C.c_size_t()
+        rc = G.lib().gkr_proof_serialize(proof.handle, self.buf, self.cap, C.byref(n))
+        if rc == 5:  # buffer too small: grow once and retry
+            self.cap = int(n.value * 1.25) + 1024
+            self.buf = (G.GkrFelt * self.cap)()
+            rc = G.lib().gkr_proof_serialize(proof.handle, self.buf, self.cap, C.byref(n))
+        G._check(rc)
+        self.n = n.value
+        return self.n
+
+    def fingerprint(self) -> str:
+        view = (C.c_uint8 * (32 * self.n)).from_address(C.addressof(self.buf))
+        return hashlib.sha256(view).hexdigest()[:16]
+
+
+def prove_model(ctx, layers, cfg, seed, sbuf):
     ch = G.PoseidonChannel()
     ch.mix_u64(seed)
     proof = G.Proof()
@@ -103,23 +125,30 @@ def prove_model(ctx, layers, cfg, seed):
         prove_matmul(ctx, ch, a, b, proof)
         if L.scores is not None:
             prove_logup(ctx, ch, L.scores, 4, 16, proof)  # softmax-exp, 2^16 table
-    # serialize (C side) and fingerprint the felts
-    n = C.c_size_t()
-    G.lib().gkr_proof_serialize(proof.handle, None, 0, C.byref(n))
-    buf = (G.GkrFelt * n.value)()
-    G._check(G.lib().gkr_proof_serialize(proof.handle, buf, n.value, C.byref(n)))
-    fp = hashlib.sha256(bytes(buf)).hexdigest()[:16]
-    return ch.digest(), n.value, fp
+    n = sbuf.serialize(proof)  # final proof serialization (C side)
+    return ch.digest(), n
 
 
-def cfg1_step(ctx, a, b):
+def cfg1_step(ctx, a, b, sbuf):
     ch = G.PoseidonChannel()
     r = ch.draw_qm31s(16)
     v = ctx.matmul_output_claim(a, b, r)
     ch.mix_secure_field(v)
     proof = G.Proof()
     ctx.prove_matmul_layer(r, v, a, b, ch, proof)
-    return ch.digest(), 0, ""
+    proof.set_input_claim(r[:8], v)
+    return ch.digest(), sbuf.serialize(proof)
+
+
+def poseidon_round_us(n=500):
+    """Host cost of one degree-2 round of the transcript (mix_poly_coeffs + draw_qm31)."""
+    ch = G.PoseidonChannel()
+    c = [(1, 2, 3, 4), (5, 6, 7, 8), (9, 10, 11, 12)]
+    t0 = time.perf_counter()
+    for _ in range(n):
+        ch.mix_poly_coeffs(*c)
+        ch.draw_qm31()
+    return round((time.perf_counter() - t0) / n * 1e6, 2)
 
 
 def cpu_baseline(budget_s=25.0):
@@ -159,11 +188,12 @@ def main():
         sys.exit(2)
 
     ctx = G.Context(0)
+    sbuf = SerialBuffer()
     if args.config == "cfg1":
         cfg, n_layers = None, 1
         a, b = ctx.synthetic(256, 256, 0, 0), ctx.synthetic(256, 256, 0, 1)
         elems = 256 * 256 * 2
-        step = lambda: cfg1_step(ctx, a, b)  # noqa: E731
+        step = lambda: cfg1_step(ctx, a, b, sbuf)  # noqa: E731
         tokens = 0
         workload = "config1-matmul-256x256x256-uniform-m31"
     else:
@@ -176,7 +206,7 @@ def main():
         per_layer, shapes = matmul_elems(cfg)
         elems = per_layer * n_layers
         tokens = cfg["tokens"]
-        step = lambda: prove_model(ctx, layers, cfg, 7)  # noqa: E731
+        step = lambda: prove_model(ctx, layers, cfg, 7, sbuf)  # noqa: E731
         workload = {"qwen48": "qwen2.5-14b-48-layers-64-tokens", "qwen1": "qwen2.5-14b-1-layer-64-tokens",
                     "smollm": "smollm2-135m-30-layers-1-token"}[args.config]
 
@@ -206,6 +236,11 @@ def main():
             kernels[name] = {"launches": nl, "avg_us": round(ms / nl * 1e3, 3),
                              "gbps": round(nb / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
                              "ms_per_step": round(ms / args.steps, 3)}
+    host = {}
+    for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait")]:
+        ms, nl, _ = ctx.kernel_time(kid)
+        if nl:
+            host[name] = {"ms_per_step": round(ms / args.steps, 3), "avg_us": round(ms / nl * 1e3, 3), "calls": nl}
     rc = kernels.get("restrict_cols")
     roofline = None
     if rc:
@@ -233,7 +268,9 @@ def main():
         "proved_tokens_per_s": round(tokens / (ms_per_step * 1e-3), 3) if tokens else None,
         "roofline": roofline,
         "kernels": kernels,
-        "proof": {"felts": digests[0][1], "sha256_16": digests[0][2], "final_digest": hex(digests[0][0])},
+        "host": host,
+        "host_poseidon_us_per_round": poseidon_round_us(),
+        "proof": {"felts": digests[0][1], "sha256_16": sbuf.fingerprint(), "final_digest": hex(digests[0][0])},
     }
     if not args.no_cpu_baseline:
         log("[bench] timing CPU baseline sample")

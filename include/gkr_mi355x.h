@@ -88,8 +88,10 @@ int gkr_ctx_create(int device, gkr_ctx** out);  /* replaces GpuSumcheckExecutor:
 void gkr_ctx_destroy(gkr_ctx* ctx);
 int gkr_ctx_synchronize(gkr_ctx* ctx);
 /* Per-kernel timing (HIP events on the context stream), for benchmarks.
- * kernel ids: 0 restrict_cols, 1 restrict_rows, 2 matmul round, 3 eq3 round,
- * 4 logup prepare, 5 eq table.  Timing adds one event pair per launch.     */
+ * ids: 0 restrict_cols, 1 restrict_rows, 2 matmul round, 3 eq3 round,
+ * 4 logup prepare, 5 eq table (device kernels: one event pair per launch);
+ * 6 host Fiat-Shamir inside the reducers, 7 host wait for device results
+ * (wall-clock, bytes = 0).                                                  */
 int gkr_ctx_set_timing(gkr_ctx* ctx, int enabled);
 int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);
 int gkr_ctx_reset_timing(gkr_ctx* ctx);

@@ -3,7 +3,8 @@
 // Elements are four little-endian u64 limbs in Montgomery form (R = 2^256).
 // p's limbs are {1, 0, 0, 0x0800000000000011}, so -p^-1 mod 2^64 is
 // 0xffff_ffff_ffff_ffff and each Montgomery reduction step needs only one
-// 64x64 product (m * p3) besides the addition of m itself.  This is the
+// 64x64 product (m * p3) besides the addition of m itself.  Additions and
+// subtractions are branch-free (masked select of the reduced value).  This is the
 // field of the reference's Poseidon channel (engine/src/crypto/
 // poseidon_channel.rs, via starknet-ff 0.3.7).
 #pragma once
@@ -43,59 +44,119 @@ inline bool felt_eq(const felt& x, const felt& y) {
   return x.l[0] == y.l[0] && x.l[1] == y.l[1] && x.l[2] == y.l[2] && x.l[3] == y.l[3];
 }
 
+// Branch-free: r = x + y, s = r - p, keep s when the subtraction did not borrow.
 inline felt felt_add(const felt& x, const felt& y) {
-  felt r;
-  u128 c = 0;
-  for (int i = 0; i < 4; i++) {
-    c = (u128)x.l[i] + y.l[i] + (uint64_t)(c >> 64);
-    r.l[i] = (uint64_t)c;
-  }
-  // x, y < p < 2^252, so no carry out of limb 3.
-  if (felt_detail::geq_p(r.l)) felt_detail::sub_p(r.l);
-  return r;
+  u128 c = (u128)x.l[0] + y.l[0];
+  const uint64_t r0 = (uint64_t)c;
+  c = (u128)x.l[1] + y.l[1] + (uint64_t)(c >> 64);
+  const uint64_t r1 = (uint64_t)c;
+  c = (u128)x.l[2] + y.l[2] + (uint64_t)(c >> 64);
+  const uint64_t r2 = (uint64_t)c;
+  const uint64_t r3 = x.l[3] + y.l[3] + (uint64_t)(c >> 64);  // x, y < p < 2^252: no carry out
+  u128 d = (u128)r0 - felt_detail::P0;
+  const uint64_t s0 = (uint64_t)d;
+  d = (u128)r1 - ((uint64_t)(d >> 64) & 1);
+  const uint64_t s1 = (uint64_t)d;
+  d = (u128)r2 - ((uint64_t)(d >> 64) & 1);
+  const uint64_t s2 = (uint64_t)d;
+  d = (u128)r3 - felt_detail::P3 - ((uint64_t)(d >> 64) & 1);
+  const uint64_t s3 = (uint64_t)d;
+  const uint64_t keep_r = (uint64_t)0 - ((uint64_t)(d >> 64) & 1);  // all ones when r < p
+  return felt{{(r0 & keep_r) | (s0 & ~keep_r), (r1 & keep_r) | (s1 & ~keep_r), (r2 & keep_r) | (s2 & ~keep_r),
+               (r3 & keep_r) | (s3 & ~keep_r)}};
 }
 
+// Branch-free: r = x - y, add p back (masked) when it borrowed.
 inline felt felt_sub(const felt& x, const felt& y) {
-  felt r;
-  uint64_t borrow = 0;
-  for (int i = 0; i < 4; i++) {
-    u128 d = (u128)x.l[i] - y.l[i] - borrow;
-    r.l[i] = (uint64_t)d;
-    borrow = (uint64_t)(d >> 64) & 1;
-  }
-  if (borrow) {  // add p back
-    u128 c = (u128)r.l[0] + felt_detail::P0;
-    r.l[0] = (uint64_t)c;
-    c = (u128)r.l[1] + felt_detail::P1 + (uint64_t)(c >> 64); r.l[1] = (uint64_t)c;
-    c = (u128)r.l[2] + felt_detail::P2 + (uint64_t)(c >> 64); r.l[2] = (uint64_t)c;
-    r.l[3] = r.l[3] + felt_detail::P3 + (uint64_t)(c >> 64);
-  }
-  return r;
+  u128 d = (u128)x.l[0] - y.l[0];
+  const uint64_t r0 = (uint64_t)d;
+  d = (u128)x.l[1] - y.l[1] - ((uint64_t)(d >> 64) & 1);
+  const uint64_t r1 = (uint64_t)d;
+  d = (u128)x.l[2] - y.l[2] - ((uint64_t)(d >> 64) & 1);
+  const uint64_t r2 = (uint64_t)d;
+  d = (u128)x.l[3] - y.l[3] - ((uint64_t)(d >> 64) & 1);
+  const uint64_t r3 = (uint64_t)d;
+  const uint64_t add_p = (uint64_t)0 - ((uint64_t)(d >> 64) & 1);
+  u128 c = (u128)r0 + (felt_detail::P0 & add_p);
+  const uint64_t o0 = (uint64_t)c;
+  c = (u128)r1 + (uint64_t)(c >> 64);
+  const uint64_t o1 = (uint64_t)c;
+  c = (u128)r2 + (uint64_t)(c >> 64);
+  const uint64_t o2 = (uint64_t)c;
+  const uint64_t o3 = r3 + (felt_detail::P3 & add_p) + (uint64_t)(c >> 64);
+  return felt{{o0, o1, o2, o3}};
 }
 
-// Montgomery product x*y*2^-256 mod p (coarsely integrated operand scanning).
+// Montgomery product x*y*2^-256 mod p.  The 512-bit product is formed
+// first (16 independent 64x64 products, so the multiplier pipelines), then
+// reduced word by word: with -p^-1 = -1 mod 2^64, step i takes m = -t[i],
+// which clears limb i with a carry of (t[i] != 0), and adds m*P3 at limb
+// i+3 -- one product per step because p = 1 + P3*2^192.
 inline felt felt_mul(const felt& x, const felt& y) {
-  uint64_t t0 = 0, t1 = 0, t2 = 0, t3 = 0, t4 = 0;
-  for (int i = 0; i < 4; i++) {
-    const uint64_t yi = y.l[i];
-    u128 c = (u128)x.l[0] * yi + t0;
-    t0 = (uint64_t)c;
-    c = (u128)x.l[1] * yi + t1 + (uint64_t)(c >> 64); t1 = (uint64_t)c;
-    c = (u128)x.l[2] * yi + t2 + (uint64_t)(c >> 64); t2 = (uint64_t)c;
-    c = (u128)x.l[3] * yi + t3 + (uint64_t)(c >> 64); t3 = (uint64_t)c;
-    u128 top = (u128)t4 + (uint64_t)(c >> 64);
-    // m = t0 * (-p^-1) = -t0;  t + m*p = t + m + m*P3*2^192, low limb cancels.
-    const uint64_t m = (uint64_t)0 - t0;
-    uint64_t carry = (t0 != 0);  // t0 + m == 2^64 exactly when t0 != 0
-    c = (u128)t1 + carry; uint64_t n0 = (uint64_t)c;
-    c = (u128)t2 + (uint64_t)(c >> 64); uint64_t n1 = (uint64_t)c;
-    c = (u128)t3 + (u128)m * felt_detail::P3 + (uint64_t)(c >> 64); uint64_t n2 = (uint64_t)c;
-    top += (uint64_t)(c >> 64);
-    t0 = n0; t1 = n1; t2 = n2; t3 = (uint64_t)top; t4 = (uint64_t)(top >> 64);
+  const uint64_t* a = x.l;
+  const uint64_t* b = y.l;
+  uint64_t t[8];
+  u128 c;
+  uint64_t k;
+  c = (u128)a[0] * b[0];
+  t[0] = (uint64_t)c;
+  k = (uint64_t)(c >> 64);
+  c = (u128)a[0] * b[1] + k;
+  t[1] = (uint64_t)c;
+  k = (uint64_t)(c >> 64);
+  c = (u128)a[0] * b[2] + k;
+  t[2] = (uint64_t)c;
+  k = (uint64_t)(c >> 64);
+  c = (u128)a[0] * b[3] + k;
+  t[3] = (uint64_t)c;
+  t[4] = (uint64_t)(c >> 64);
+  for (int i = 1; i < 4; i++) {
+    c = (u128)a[i] * b[0] + t[i];
+    t[i] = (uint64_t)c;
+    k = (uint64_t)(c >> 64);
+    c = (u128)a[i] * b[1] + t[i + 1] + k;
+    t[i + 1] = (uint64_t)c;
+    k = (uint64_t)(c >> 64);
+    c = (u128)a[i] * b[2] + t[i + 2] + k;
+    t[i + 2] = (uint64_t)c;
+    k = (uint64_t)(c >> 64);
+    c = (u128)a[i] * b[3] + t[i + 3] + k;
+    t[i + 3] = (uint64_t)c;
+    t[i + 4] = (uint64_t)(c >> 64);
   }
-  felt r{{t0, t1, t2, t3}};
-  // result < 2p < 2^253, so t4 == 0 here
-  if (felt_detail::geq_p(r.l)) felt_detail::sub_p(r.l);
+  for (int i = 0; i < 4; i++) {
+    const uint64_t m = (uint64_t)0 - t[i];
+    uint64_t cc = (t[i] != 0);
+    u128 s = (u128)t[i + 1] + cc;
+    t[i + 1] = (uint64_t)s;
+    cc = (uint64_t)(s >> 64);
+    s = (u128)t[i + 2] + cc;
+    t[i + 2] = (uint64_t)s;
+    cc = (uint64_t)(s >> 64);
+    s = (u128)t[i + 3] + (u128)m * felt_detail::P3 + cc;
+    t[i + 3] = (uint64_t)s;
+    cc = (uint64_t)(s >> 64);
+    for (int j = i + 4; j < 8; j++) {
+      s = (u128)t[j] + cc;
+      t[j] = (uint64_t)s;
+      cc = (uint64_t)(s >> 64);
+    }
+  }
+  felt r{{t[4], t[5], t[6], t[7]}};
+  // r < 2p: one branch-free conditional subtraction
+  u128 d = (u128)r.l[0] - felt_detail::P0;
+  const uint64_t s0 = (uint64_t)d;
+  d = (u128)r.l[1] - ((uint64_t)(d >> 64) & 1);
+  const uint64_t s1 = (uint64_t)d;
+  d = (u128)r.l[2] - ((uint64_t)(d >> 64) & 1);
+  const uint64_t s2 = (uint64_t)d;
+  d = (u128)r.l[3] - felt_detail::P3 - ((uint64_t)(d >> 64) & 1);
+  const uint64_t s3 = (uint64_t)d;
+  const uint64_t keep = (uint64_t)0 - ((uint64_t)(d >> 64) & 1);
+  r.l[0] = (r.l[0] & keep) | (s0 & ~keep);
+  r.l[1] = (r.l[1] & keep) | (s1 & ~keep);
+  r.l[2] = (r.l[2] & keep) | (s2 & ~keep);
+  r.l[3] = (r.l[3] & keep) | (s3 & ~keep);
   return r;
 }
 

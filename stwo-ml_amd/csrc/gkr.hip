@@ -6,6 +6,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <chrono>
+
 #include <map>
 #include <set>
 #include <string>
@@ -75,10 +77,12 @@ static bool felt_abi_canonical(const gkr_felt& f) {
 // ------------------------------------------------------------------ context
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
-  S_TABLE, S_MULT, S_PADIN, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_NSLOTS
+  S_TABLE, S_MULT, S_PADIN, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_COLPART, S_NSLOTS
 };
+// Timer ids: device kernels (HIP events) and two host-side phases
+// (Fiat-Shamir hashing inside the reducers, and waiting for device results).
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
-                K_EQ_TABLE = 5, K_NKERNELS = 6 };
+                K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_NKERNELS = 8 };
 constexpr int kMaxPartialBlocks = 1024;
 
 struct KernelStat {
@@ -114,6 +118,10 @@ struct gkr_ctx {
   void* buf[S_NSLOTS] = {};
   size_t cap[S_NSLOTS] = {};
   qm31* h_res = nullptr;  // pinned result staging (64 QM31)
+  qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
+  uint32_t* h_flag = nullptr; // coherent pinned: sequence number of the last delivery
+  uint32_t* d_counter = nullptr;  // device: workgroup arrival counter of RoundSink
+  uint32_t seq = 0;
   bool timing = false;
   KernelStat stats[K_NKERNELS];
   std::vector<PendingTiming> pending;
@@ -121,11 +129,13 @@ struct gkr_ctx {
   MatMulCache mm;
   std::map<uint64_t, std::vector<uint32_t>> tables;  // (tag << 32 | log) -> table outputs
   std::set<gkr_matrix*> matrices;  // live matrices; detached when the context is destroyed
+  uint64_t table_on_device = 0;    // (tag << 32 | log) of the table held in S_TABLE, 0 = none
 };
 
 static int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
   if (bytes == 0) bytes = 16;
   if (c->cap[s] < bytes) {
+    if (s == S_TABLE) c->table_on_device = 0;
     if (c->buf[s]) HIP_TRY(hipFree(c->buf[s]));
     c->buf[s] = nullptr;
     c->cap[s] = 0;
@@ -170,6 +180,20 @@ struct TimedLaunch {
     if (c->timing && e0 && e1) {
       (void)hipEventRecord(e1, c->stream);
       c->pending.push_back({kid, e0, e1, bytes});
+    }
+  }
+};
+struct HostTimer {
+  gkr_ctx* c;
+  int kid;
+  std::chrono::steady_clock::time_point t0;
+  HostTimer(gkr_ctx* c_, int kid_) : c(c_), kid(kid_) {
+    if (c->timing) t0 = std::chrono::steady_clock::now();
+  }
+  ~HostTimer() {
+    if (c->timing) {
+      c->stats[kid].ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+      c->stats[kid].launches++;
     }
   }
 };
@@ -237,16 +261,34 @@ static int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out)
   return check_launch();
 }
 
-// Reduce `nblocks` partial rows of NQ QM31 each into h_res[0..NQ) (synchronizes).
+static int make_sink(gkr_ctx* c, RoundSink* sk) {
+  qm31* part;
+  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
+  sk->partials = part;
+  sk->counter = c->d_counter;
+  sk->out = c->h_out;
+  sk->flag = c->h_flag;
+  sk->seq = ++c->seq;
+  return GKR_OK;
+}
+// Wait until the kernel launched with `sk` has published its NQ results.
+// The wait spins on the coherent flag; after ~2 s without it the stream is
+// synchronised so that a device error is reported instead of hanging.
 template <int NQ>
-static int finish_partials(gkr_ctx* c, qm31* partials, unsigned nblocks, qm31* host_out) {
-  qm31* d_res;
-  TRY(ensureT(c, S_RES, 64, &d_res));
-  hipLaunchKernelGGL(k_sum_partials<NQ>, dim3(1), dim3(kBlock), 0, c->stream, partials, (int)nblocks, d_res);
+static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
   TRY(check_launch());
-  HIP_TRY(hipMemcpyAsync(c->h_res, d_res, NQ * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
-  TRY(sync(c));
-  for (int q = 0; q < NQ; q++) host_out[q] = c->h_res[q];
+  HostTimer ht(c, K_HOST_WAIT);
+  volatile uint32_t* flag = c->h_flag;
+  uint64_t spins = 0;
+  while (*flag != sk.seq) {
+    if (++spins == (1u << 26)) {
+      HIP_TRY(hipStreamSynchronize(c->stream));
+      if (*flag != sk.seq) return fail(GKR_ERR_DEVICE, "device result %u not delivered", sk.seq);
+      break;
+    }
+  }
+  __atomic_thread_fence(__ATOMIC_ACQUIRE);
+  for (int q = 0; q < NQ; q++) host_out[q] = c->h_out[q];
   return GKR_OK;
 }
 static int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out) {
@@ -256,14 +298,12 @@ static int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out) {
   return GKR_OK;
 }
 
-// Partial dot sum_i v[i] * eq[i] (v M31-valued, length n).
+// sum_i v[i] * eq[i] (v M31-valued, length n).
 static int dot_m31(gkr_ctx* c, const uint32_t* v, const qm31* eq, uint64_t n, qm31* out) {
-  qm31* part;
-  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
-  unsigned g = partial_grid(n);
-  hipLaunchKernelGGL(k_dot_m31, dim3(g), dim3(kBlock), 0, c->stream, v, eq, n, part);
-  TRY(check_launch());
-  return finish_partials<1>(c, part, g, out);
+  RoundSink sk;
+  TRY(make_sink(c, &sk));
+  hipLaunchKernelGGL(k_dot_m31, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, v, eq, n, sk);
+  return wait_sink<1>(c, sk, out);
 }
 
 // ------------------------------------------------------------------ error / version
@@ -416,6 +456,7 @@ extern "C" int gkr_seed_channel(gkr_channel* ch, uint64_t num_layers, uint64_t i
 }
 
 // ------------------------------------------------------------------ context ABI
+extern "C" void gkr_ctx_destroy(gkr_ctx* c);
 extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   if (!out) return fail(GKR_ERR_INVALID, "null out");
   int n = 0;
@@ -428,18 +469,22 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
     delete c;
     return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");
   }
-  if (hipHostMalloc((void**)&c->h_res, 64 * sizeof(qm31), hipHostMallocDefault) != hipSuccess) {
-    (void)hipStreamDestroy(c->stream);
-    delete c;
-    return fail(GKR_ERR_DEVICE, "hipHostMalloc failed");
+  if (hipHostMalloc((void**)&c->h_res, 64 * sizeof(qm31), hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&c->h_out, 64 * sizeof(qm31) + 64, hipHostMallocCoherent | hipHostMallocMapped) !=
+          hipSuccess ||
+      hipMalloc((void**)&c->d_counter, 256) != hipSuccess || hipMemset(c->d_counter, 0, 256) != hipSuccess) {
+    gkr_ctx_destroy(c);
+    return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
   }
+  c->h_flag = reinterpret_cast<uint32_t*>(c->h_out + 64);
+  *c->h_flag = 0;
   *out = c;
   return GKR_OK;
 }
 extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
-  (void)hipStreamSynchronize(c->stream);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
   for (auto& p : c->pending) {
     (void)hipEventDestroy(p.e0);
     (void)hipEventDestroy(p.e1);
@@ -453,7 +498,9 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   for (int s = 0; s < S_NSLOTS; s++)
     if (c->buf[s]) (void)hipFree(c->buf[s]);
   if (c->h_res) (void)hipHostFree(c->h_res);
-  (void)hipStreamDestroy(c->stream);
+  if (c->h_out) (void)hipHostFree(c->h_out);
+  if (c->d_counter) (void)hipFree(c->d_counter);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
 extern "C" int gkr_ctx_synchronize(gkr_ctx* c) {
@@ -570,35 +617,47 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     TRY(check_launch());
   }
   {
-    TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + 16 * pk);
-    const unsigned g = (unsigned)((k + kRowsPerBlock - 1) / kRowsPerBlock);
-    if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
-      hipLaunchKernelGGL(k_restrict_cols<true>, dim3(g), dim3(kBlock), 0, c->stream, B->dev, k, n, Lj, fb);
-    else
-      hipLaunchKernelGGL(k_restrict_cols<false>, dim3(g), dim3(kBlock), 0, c->stream, B->dev, k, n, Lj, fb);
-    TRY(check_launch());
-  }
-  if (pk > k) {
-    hipLaunchKernelGGL(k_zero_q, dim3(grid_for(pk - k)), dim3(kBlock), 0, c->stream, fb, k, pk);
+    // column chunks: enough workgroups to fill the chip (>= 1536), chunks a
+    // multiple of one wave sweep (256 columns) and at least 1024 columns
+    const uint64_t rows_per_block = (uint64_t)kColRows * kColWaves;
+    const uint64_t gr = (k + rows_per_block - 1) / rows_per_block;
+    uint64_t gc = (1536 + gr - 1) / gr;
+    uint64_t chunk = (n + gc - 1) / gc;
+    chunk = (chunk + 255) / 256 * 256;
+    if (chunk < 1024) chunk = 1024;
+    gc = (n + chunk - 1) / chunk;
+    qm31* part;
+    TRY(ensureT(c, S_COLPART, (size_t)gc * k, &part));
+    {
+      TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + 16 * pk);
+      if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
+        hipLaunchKernelGGL(k_restrict_cols<true>, dim3((unsigned)gr, (unsigned)gc), dim3(kBlock), 0, c->stream,
+                           B->dev, k, n, chunk, Lj, (uint32_t*)part);
+      else
+        hipLaunchKernelGGL(k_restrict_cols<false>, dim3((unsigned)gr, (unsigned)gc), dim3(kBlock), 0, c->stream,
+                           B->dev, k, n, chunk, Lj, (uint32_t*)part);
+      TRY(check_launch());
+    }
+    hipLaunchKernelGGL(k_restrict_cols_finish, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, part, k, pk, (int)gc,
+                       fb);
     TRY(check_launch());
   }
   return GKR_OK;
 }
 
 static int round0_sums(gkr_ctx* c, uint64_t pk, qm31 s[3]) {
-  qm31 *fa, *fb, *part;
+  qm31 *fa, *fb;
   TRY(ensureT(c, S_FA0, pk, &fa));
   TRY(ensureT(c, S_FB0, pk, &fb));
-  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
+  RoundSink sk;
+  TRY(make_sink(c, &sk));
   const uint64_t half = pk / 2;
-  const unsigned g = partial_grid(half);
   {
     TimedLaunch t(c, K_MM_ROUND, 32 * pk);
-    hipLaunchKernelGGL(k_mm_round, dim3(g), dim3(kBlock), 0, c->stream, fa, fb, (qm31*)nullptr, (qm31*)nullptr, half, 0,
-                       qm31_zero(), part);
-    TRY(check_launch());
+    hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, fa, fb, (qm31*)nullptr,
+                       (qm31*)nullptr, half, 0, qm31_zero(), sk);
   }
-  return finish_partials<3>(c, part, g, s);
+  return wait_sink<3>(c, sk, s);
 }
 
 static bool cache_matches(const gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, int n_ri,
@@ -657,13 +716,11 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
   HIP_TRY(hipSetDevice(c->device));
   TRY(ensure_restricted(c, a, b, r_i, n_ri, r_j, n_rj));
   const int T = log2_exact(pk);
-  qm31 *fa0, *fa1, *fb0, *fb1, *part, *dres;
+  qm31 *fa0, *fa1, *fb0, *fb1;
   TRY(ensureT(c, S_FA0, pk, &fa0));
   TRY(ensureT(c, S_FB0, pk, &fb0));
   TRY(ensureT(c, S_FA1, pk / 2 + 1, &fa1));
   TRY(ensureT(c, S_FB1, pk / 2 + 1, &fb1));
-  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
-  TRY(ensureT(c, S_RES, 64, &dres));
   // The folds below overwrite the restricted vectors' successors only;
   // S_FA0/S_FB0 keep round 0 input, so a cached restriction stays valid.
   if (T == 0) {
@@ -693,14 +750,15 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
       qm31* na = (t == 1) ? fa1 : bufs_a[(t - 1) & 1];
       qm31* nb = (t == 1) ? fb1 : bufs_b[(t - 1) & 1];
       if (t == 2) c->mm.valid = false;  // round 2 writes into S_FA0 / S_FB0
-      const unsigned g = partial_grid(half);
+      RoundSink sk;
+      TRY(make_sink(c, &sk));
       {
         // algorithmic bytes: 2 vectors x (read 4*half + write 2*half) QM31 = 48 * n_{t-1}
         TimedLaunch tl(c, K_MM_ROUND, 192 * half);
-        hipLaunchKernelGGL(k_mm_round, dim3(g), dim3(kBlock), 0, c->stream, cur_a, cur_b, na, nb, half, 1, alpha, part);
-        TRY(check_launch());
+        hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cur_a, cur_b, na, nb,
+                           half, 1, alpha, sk);
       }
-      TRY(finish_partials<3>(c, part, g, s));
+      TRY(wait_sink<3>(c, sk, s));
       cur_a = na;
       cur_b = nb;
     }
@@ -710,15 +768,19 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
     round_polys[3 * t + 0] = G(c0);
     round_polys[3 * t + 1] = G(c1);
     round_polys[3 * t + 2] = G(c2);
-    ch.mix_poly_coeffs(c0, c1, c2);
-    alpha = ch.draw_qm31();
+    {
+      HostTimer ht(c, K_HOST_FS);
+      ch.mix_poly_coeffs(c0, c1, c2);
+      alpha = ch.draw_qm31();
+    }
     challenges[t] = G(alpha);
   }
   c->mm.valid = c->mm.valid && T < 2;
-  hipLaunchKernelGGL(k_mm_final, dim3(1), dim3(64), 0, c->stream, cur_a, cur_b, alpha, dres);
-  TRY(check_launch());
+  RoundSink fsk;
+  TRY(make_sink(c, &fsk));
+  hipLaunchKernelGGL(k_mm_final, dim3(1), dim3(64), 0, c->stream, cur_a, cur_b, alpha, fsk);
   qm31 fin[2];
-  TRY(fetch_q(c, dres, 2, fin));
+  TRY(wait_sink<2>(c, fsk, fin));
   *final_a = G(fin[0]);
   *final_b = G(fin[1]);
   return GKR_OK;
@@ -807,15 +869,27 @@ extern "C" int gkr_proof_set_io_commitment(gkr_proof* p, const gkr_felt* cm) {
 }
 
 // serialize_gkr_model_proof (cairo_serde.rs:1307-1772); felts kept canonical.
+// Two passes over the proof: the first counts, the second writes straight
+// into the caller's buffer (no intermediate copy of the felt stream).
 struct Ser {
-  std::vector<felt> out;
-  void u(uint64_t v) { out.push_back(felt{{v, 0, 0, 0}}); }
+  gkr_felt* out;  // nullptr: count only
+  size_t n = 0;
+  void u(uint64_t v) {
+    if (out) {
+      gkr_felt& f = out[n];
+      f.w[0] = (uint32_t)v;
+      f.w[1] = (uint32_t)(v >> 32);
+      for (int i = 2; i < 8; i++) f.w[i] = 0;
+    }
+    n++;
+  }
   void q(const qm31& x) { u(x.a); u(x.b); u(x.c); u(x.d); }
-  void f(const felt& canon) { out.push_back(canon); }
+  void f(const felt& canon) {
+    if (out) felt_canon_to_words(canon, out[n].w);
+    n++;
+  }
 };
-extern "C" int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out) {
-  if (!p || !n_out || (!out && cap)) return fail(GKR_ERR_INVALID, "null argument");
-  Ser s;
+static void serialize_proof(const gkr_proof* p, Ser& s) {
   s.u(p->layers.size());
   for (const LayerRec& L : p->layers) {
     if (L.tag == 0) {
@@ -870,9 +944,15 @@ extern "C" int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap
   for (const felt& w : p->weight_commitments) s.f(w);
   s.u(0);  // weight opening proofs are not produced here
   s.f(p->io_commitment);
-  *n_out = s.out.size();
-  for (size_t i = 0; i < s.out.size() && i < cap; i++) felt_canon_to_words(s.out[i], out[i].w);
-  if (cap < s.out.size()) return fail(GKR_ERR_BUFFER, "need %zu felts, have %zu", s.out.size(), cap);
+}
+extern "C" int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out) {
+  if (!p || !n_out || (!out && cap)) return fail(GKR_ERR_INVALID, "null argument");
+  Ser count{nullptr};
+  serialize_proof(p, count);
+  *n_out = count.n;
+  if (cap < count.n) return fail(GKR_ERR_BUFFER, "need %zu felts, have %zu", count.n, cap);
+  Ser write{out};
+  serialize_proof(p, write);
   return GKR_OK;
 }
 
@@ -930,17 +1010,16 @@ extern "C" int gkr_evaluate_mle_at_point(gkr_ctx* c, const gkr_qm31* mle, uint64
     if (!canonical_q(point[l])) return fail(GKR_ERR_INVALID, "point not canonical");
     pt[l] = Q(point[l]);
   }
-  qm31 *dm, *eq, *part;
+  qm31 *dm, *eq;
   TRY(ensureT(c, S_MLE, len, &dm));
   TRY(ensureT(c, S_EQ, len, &eq));
-  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
   HIP_TRY(hipMemcpyAsync(dm, mle, len * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
   TRY(eq_table(c, pt.data(), (int)n_vars, len, eq));
-  const unsigned g = partial_grid(len);
-  hipLaunchKernelGGL(k_dot_q, dim3(g), dim3(kBlock), 0, c->stream, dm, eq, len, part);
-  TRY(check_launch());
+  RoundSink sk;
+  TRY(make_sink(c, &sk));
+  hipLaunchKernelGGL(k_dot_q, dim3(partial_grid(len)), dim3(kBlock), 0, c->stream, dm, eq, len, sk);
   qm31 r[1];
-  TRY(finish_partials<1>(c, part, g, r));
+  TRY(wait_sink<1>(c, sk, r));
   *out = G(r[0]);
   return GKR_OK;
 }
@@ -1014,7 +1093,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   const std::vector<uint32_t>& table = cached_table(c, tag, table_log);
 
   uint32_t *d_table, *d_mult, *d_pad, *d_min, *d_mout;
-  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *d_e1, *part, *dres;
+  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *d_e1;
   TRY(ensureT(c, S_TABLE, tsize, &d_table));
   TRY(ensureT(c, S_MULT, tsize, &d_mult));
   TRY(ensureT(c, S_PADIN, n, &d_pad));
@@ -1026,9 +1105,12 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
   TRY(ensureT(c, S_E0, n, &d_e0));
   TRY(ensureT(c, S_E1, n / 2 + 1, &d_e1));
-  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
-  TRY(ensureT(c, S_RES, 64, &dres));
-  HIP_TRY(hipMemcpyAsync(d_table, table.data(), tsize * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+  const uint64_t table_key = ((uint64_t)tag << 32) | table_log;
+  if (c->table_on_device != table_key) {
+    c->table_on_device = 0;
+    HIP_TRY(hipMemcpyAsync(d_table, table.data(), tsize * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    c->table_on_device = table_key;
+  }
   HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
 
   // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
@@ -1041,25 +1123,25 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
 
   qm31 trace_sum, table_sum;
   {
-    const unsigned g = partial_grid(n);
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
     {
       TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 12 * n + 32 * n);
-      hipLaunchKernelGGL(k_logup_prepare, dim3(g), dim3(kBlock), 0, c->stream, input->dev, input->rows, input->cols,
-                         log2_exact(pcol), n, d_table, mask, gamma, beta, d_pad, d_min, d_mout, d_d0, d_w0, d_mult,
-                         part);
-      TRY(check_launch());
+      hipLaunchKernelGGL(k_logup_prepare, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, input->dev, input->rows,
+                         input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, d_pad, d_min, d_mout, d_d0,
+                         d_w0, d_mult, sk);
     }
     qm31 r[1];
-    TRY(finish_partials<1>(c, part, g, r));
+    TRY(wait_sink<1>(c, sk, r));
     trace_sum = r[0];
   }
   {
-    const unsigned g = partial_grid(tsize);
-    hipLaunchKernelGGL(k_logup_table_sum, dim3(g), dim3(kBlock), 0, c->stream, d_table, d_mult, tsize, gamma, beta,
-                       part);
-    TRY(check_launch());
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
+    hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult,
+                       tsize, gamma, beta, sk);
     qm31 r[1];
-    TRY(finish_partials<1>(c, part, g, r));
+    TRY(wait_sink<1>(c, sk, r));
     table_sum = r[0];
   }
   if (!qm31_eq(trace_sum, table_sum))
@@ -1081,23 +1163,23 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   qm31 alpha = qm31_zero();
   for (int t = 0; t < nv; t++) {
     const uint64_t half = (n >> t) / 2;
-    const unsigned g = partial_grid(half);
     qm31 s[4];
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
     {
       // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}; round 0 reads only
       TimedLaunch tl(c, K_EQ3_ROUND, t == 0 ? 96 * half : 288 * half);
       if (t == 0) {
-        hipLaunchKernelGGL(k_eq3_round, dim3(g), dim3(kBlock), 0, c->stream, ce, cw, cd, (qm31*)nullptr,
-                           (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), part);
+        hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd,
+                           (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
       } else {
         qm31 *ne = be[(t - 1) & 1], *nw = bw[(t - 1) & 1], *nd = bd[(t - 1) & 1];
-        hipLaunchKernelGGL(k_eq3_round, dim3(g), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw, nd, half, 1, alpha,
-                           part);
+        hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw, nd,
+                           half, 1, alpha, sk);
         ce = ne; cw = nw; cd = nd;
       }
-      TRY(check_launch());
     }
-    TRY(finish_partials<4>(c, part, g, s));
+    TRY(wait_sink<4>(c, sk, s));
     const qm31 dd1 = qm31_sub(s[1], s[0]);
     const qm31 dd2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
     const qm31 dd3 = qm31_mul(qm31_sub(qm31_sub(s[3], s[0]), qm31_mul(three, qm31_sub(s[2], s[1]))), inv6);
@@ -1109,15 +1191,19 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     out->eq_round_polys[4 * t + 1] = G(c1);
     out->eq_round_polys[4 * t + 2] = G(c2);
     out->eq_round_polys[4 * t + 3] = G(c3);
-    C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
-    alpha = C.draw_qm31();
+    {
+      HostTimer ht(c, K_HOST_FS);
+      C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
+      alpha = C.draw_qm31();
+    }
     chal[t] = alpha;
   }
   qm31 fin[3];
   if (nv > 0) {
-    hipLaunchKernelGGL(k_eq3_final, dim3(1), dim3(64), 0, c->stream, ce, cw, cd, alpha, dres);
-    TRY(check_launch());
-    TRY(fetch_q(c, dres, 3, fin));
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
+    hipLaunchKernelGGL(k_eq3_final, dim3(1), dim3(64), 0, c->stream, ce, cw, cd, alpha, sk);
+    TRY(wait_sink<3>(c, sk, fin));
   } else {
     TRY(fetch_q(c, d_w0, 1, fin + 1));
   }
@@ -1149,30 +1235,37 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   qm31* bm[2] = {m1, m0};
   for (uint32_t t = 0; t < table_log; t++) {
     const uint64_t half = (tsize >> t) / 2;
-    const unsigned g = partial_grid(half);
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
     if (t == 0) {
-      hipLaunchKernelGGL(k_sum_round, dim3(g), dim3(kBlock), 0, c->stream, cm, (qm31*)nullptr, half, 0, qm31_zero(),
-                         part);
+      hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, (qm31*)nullptr, half,
+                         0, qm31_zero(), sk);
     } else {
       qm31* nm = bm[(t - 1) & 1];
-      hipLaunchKernelGGL(k_sum_round, dim3(g), dim3(kBlock), 0, c->stream, cm, nm, half, 1, alpha, part);
+      hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, nm, half, 1, alpha,
+                         sk);
       cm = nm;
     }
-    TRY(check_launch());
     qm31 s[2];
-    TRY(finish_partials<2>(c, part, g, s));
+    TRY(wait_sink<2>(c, sk, s));
     const qm31 c0 = s[0];
     const qm31 c1 = qm31_sub(s[1], s[0]);
     out->mult_round_polys[2 * t] = G(c0);
     out->mult_round_polys[2 * t + 1] = G(c1);
-    C.mix_secure_field(c0);
-    C.mix_secure_field(c1);
-    alpha = C.draw_qm31();
+    {
+      HostTimer ht(c, K_HOST_FS);
+      C.mix_secure_field(c0);
+      C.mix_secure_field(c1);
+      alpha = C.draw_qm31();
+    }
   }
   qm31 mfin[1];
-  hipLaunchKernelGGL(k_fold1_final, dim3(1), dim3(64), 0, c->stream, cm, alpha, dres);
-  TRY(check_launch());
-  TRY(fetch_q(c, dres, 1, mfin));
+  {
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
+    hipLaunchKernelGGL(k_fold1_final, dim3(1), dim3(64), 0, c->stream, cm, alpha, sk);
+    TRY(wait_sink<1>(c, sk, mfin));
+  }
   out->mult_final_eval = G(mfin[0]);
   out->mult_claimed_sum = G(mult_sum);
 

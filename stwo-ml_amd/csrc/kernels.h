@@ -76,6 +76,60 @@ __device__ __forceinline__ void block_sum_store(qm31 (&v)[NQ], qm31* __restrict_
   }
 }
 
+// Where a reducing kernel delivers its NQ QM31 results: every workgroup
+// stores its partial sums, bumps `counter`, and the last workgroup to arrive
+// adds all partials and writes them to `out` (coherent pinned host memory),
+// then publishes `seq` in `flag` so the host can stop waiting without a
+// stream synchronisation.  The last workgroup resets `counter` to zero.
+struct RoundSink {
+  qm31* partials;          // device, NQ per workgroup
+  uint32_t* counter;       // device, zero between launches
+  qm31* out;               // host-mapped
+  uint32_t* flag;          // host-mapped
+  uint32_t seq;
+};
+
+template <int NQ>
+__device__ __forceinline__ void sink_finish(qm31 (&v)[NQ], const RoundSink& sk) {
+  __shared__ bool last;
+  block_sum_store<NQ>(v, sk.partials + (uint64_t)NQ * blockIdx.x);
+  if (threadIdx.x == 0) {
+    __threadfence();  // release this workgroup's partials (device scope)
+    const uint32_t prev = atomicAdd(sk.counter, 1u);
+    last = (prev == gridDim.x - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();  // acquire the other workgroups' partials
+  qacc acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) acc[q].zero();
+  for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x)
+#pragma unroll
+    for (int q = 0; q < NQ; q++) acc[q].add(ld_q(sk.partials, (uint64_t)NQ * b + q));
+  qm31 tot[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) tot[q] = acc[q].reduce();
+  __shared__ qm31 res[NQ];
+  block_sum_store<NQ>(tot, res);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int q = 0; q < NQ; q++) sk.out[q] = res[q];
+    *sk.counter = 0;
+    __threadfence_system();  // results visible to the host before the flag
+    __atomic_store_n(sk.flag, sk.seq, __ATOMIC_RELEASE);
+  }
+}
+// Single-thread delivery of NQ values computed by one lane.
+template <int NQ>
+__device__ __forceinline__ void sink_single(const qm31 (&v)[NQ], const RoundSink& sk) {
+#pragma unroll
+  for (int q = 0; q < NQ; q++) sk.out[q] = v[q];
+  __threadfence_system();
+  __atomic_store_n(sk.flag, sk.seq, __ATOMIC_RELEASE);
+}
+
 // ------------------------------------------------------------------ eq / Lagrange
 // out[x] = prod_l (bit_l(x) ? r_l : 1 - r_l), with r_0 on the most
 // significant bit of x (components/matmul.rs:342-355, gkr/prover.rs:9201-9233).
@@ -156,70 +210,148 @@ __global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint
 }
 
 // Weight side: f_b[i] = sum_{j<n} B[i][j] * L[j] for i < k, 0 for k <= i < pk.
-// A workgroup owns kRowsPerBlock consecutive rows; its 256 threads stride
-// over the columns 4 at a time (128-bit loads when n % 4 == 0), so each
-// L[j] fetched from L2 is reused for all rows of the group.
-constexpr int kRowsPerBlock = 8;
+// Grid (row blocks of kColWaves * kColRows rows) x (column chunks).  Each
+// wave owns kColRows rows and sweeps the workgroup's column chunk 256
+// columns at a time (4 per lane: one 128-bit load per row when n % 4 == 0),
+// prefetching the next group while it multiplies the current one.  The
+// waves of a workgroup share the chunk, so L[j] comes from L2 once and from
+// L1 for the other waves, and each L[j] held in registers serves kColRows
+// rows.  B is streamed with non-temporal loads.  Each wave reduces its own
+// rows (no LDS, no barrier) and writes one canonical QM31 partial per row to
+// partial[(chunk * k + row) * 4 + component]; k_restrict_cols_finish adds the chunks.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kColRows = 4;
+constexpr int kColWaves = kBlock / 64;
+
+__device__ __forceinline__ void acc_row4(uint64_t (&lo)[4], uint64_t (&hi)[4], const uint32_t (&v)[4],
+                                         const qm31 (&l)[4]) {
+  uint64_t t0 = 0, t1 = 0, t2 = 0, t3 = 0;  // <= 4 products of canonical words: < 2^64
+#pragma unroll
+  for (int u = 0; u < 4; u++) {
+    t0 += (uint64_t)v[u] * l[u].a;
+    t1 += (uint64_t)v[u] * l[u].b;
+    t2 += (uint64_t)v[u] * l[u].c;
+    t3 += (uint64_t)v[u] * l[u].d;
+  }
+  lo[0] += (uint32_t)t0; hi[0] += t0 >> 32;
+  lo[1] += (uint32_t)t1; hi[1] += t1 >> 32;
+  lo[2] += (uint32_t)t2; hi[2] += t2 >> 32;
+  lo[3] += (uint32_t)t3; hi[3] += t3 >> 32;
+}
+
+template <bool kVec4>
+__device__ __forceinline__ void load_row4(const uint32_t* __restrict__ row, uint64_t j0, int cnt, uint32_t (&v)[4]) {
+  if (kVec4) {
+    const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + j0));
+    v[0] = w[0]; v[1] = w[1]; v[2] = w[2]; v[3] = w[3];
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = (u < cnt) ? row[j0 + u] : 0u;
+  }
+}
+
+// Sum 16 canonical M31 values per lane over the 64 lanes of a wave with a
+// transposing butterfly: each step halves the values a lane carries and
+// exchanges the other half with its partner (8+4+2+1 shuffles), two more
+// steps finish the sums.  Lanes with (lane & 3) == 0 end up holding the wave
+// total of value (lane >> 2).
+__device__ __forceinline__ uint32_t wave_sum16(uint32_t (&v)[16]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 8, m = 32; k >= 1; k >>= 1, m >>= 1) {
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int i = 0; i < k; i++) {
+      const uint32_t send = upper ? v[i] : v[i + k];
+      const uint32_t keep = upper ? v[i + k] : v[i];
+      v[i] = m31_add(keep, shfl_xor_u32(send, m));
+    }
+  }
+  uint32_t x = v[0];
+  x = m31_add(x, shfl_xor_u32(x, 2));
+  x = m31_add(x, shfl_xor_u32(x, 1));
+  return x;
+}
+
 template <bool kVec4>
 __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
-                                                          const qm31* __restrict__ L, qm31* __restrict__ out) {
-  const uint64_t row0 = (uint64_t)blockIdx.x * kRowsPerBlock;
-  const int nrows = (int)((k - row0) < (uint64_t)kRowsPerBlock ? (k - row0) : (uint64_t)kRowsPerBlock);
-  uint64_t lo[kRowsPerBlock][4], hi[kRowsPerBlock][4];
+                                                          uint64_t chunk, const qm31* __restrict__ L,
+                                                          uint32_t* __restrict__ partial) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t row0 = ((uint64_t)blockIdx.x * kColWaves + wave) * kColRows;
+  if (row0 >= k) return;  // whole wave leaves; no workgroup barrier follows
+  const int nrows = (int)((k - row0) < (uint64_t)kColRows ? (k - row0) : (uint64_t)kColRows);
+  const uint64_t c0 = (uint64_t)blockIdx.y * chunk;
+  const uint64_t c1 = (c0 + chunk < n) ? c0 + chunk : n;
+  const uint32_t* rows[kColRows];
 #pragma unroll
-  for (int r = 0; r < kRowsPerBlock; r++)
+  for (int r = 0; r < kColRows; r++) rows[r] = B + (row0 + (r < nrows ? r : 0)) * n;
+  uint64_t lo[kColRows][4], hi[kColRows][4];
+#pragma unroll
+  for (int r = 0; r < kColRows; r++)
 #pragma unroll
     for (int c = 0; c < 4; c++) lo[r][c] = hi[r][c] = 0;
 
-  for (uint64_t j0 = (uint64_t)threadIdx.x * 4; j0 < n; j0 += (uint64_t)kBlock * 4) {
-    const int cnt = (int)((n - j0) < 4 ? (n - j0) : 4);
-    qm31 l[4];
+  constexpr uint64_t kStep = 64 * 4;
+  uint64_t j = c0 + (uint64_t)lane * 4;
+  qm31 lc[4];
+  uint32_t vc[kColRows][4];
+  int cnt = (int)(j < c1 ? ((c1 - j) < 4 ? (c1 - j) : 4) : 0);
+  if (cnt) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) l[u] = (u < cnt) ? ld_q(L, j0 + u) : qm31_zero();
+    for (int u = 0; u < 4; u++) lc[u] = (u < cnt) ? ld_q(L, j + u) : qm31_zero();
 #pragma unroll
-    for (int r = 0; r < kRowsPerBlock; r++) {
-      if (r < nrows) {
-        const uint32_t* row = B + (row0 + r) * n;
-        uint32_t v[4];
-        if (kVec4 && cnt == 4) {
-          uint4 w = *reinterpret_cast<const uint4*>(row + j0);
-          v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
-        } else {
+    for (int r = 0; r < kColRows; r++) load_row4<kVec4>(rows[r], j, cnt, vc[r]);
+  }
+  while (cnt) {
+    const uint64_t jn = j + kStep;
+    const int cntn = (int)(jn < c1 ? ((c1 - jn) < 4 ? (c1 - jn) : 4) : 0);
+    qm31 ln[4];
+    uint32_t vn[kColRows][4];
+    if (cntn) {  // prefetch the next column group
 #pragma unroll
-          for (int u = 0; u < 4; u++) v[u] = (u < cnt) ? row[j0 + u] : 0u;
-        }
-        uint64_t t[4] = {0, 0, 0, 0};
+      for (int u = 0; u < 4; u++) ln[u] = (u < cntn) ? ld_q(L, jn + u) : qm31_zero();
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          t[0] += (uint64_t)v[u] * l[u].a;
-          t[1] += (uint64_t)v[u] * l[u].b;
-          t[2] += (uint64_t)v[u] * l[u].c;
-          t[3] += (uint64_t)v[u] * l[u].d;
-        }
-#pragma unroll
-        for (int c = 0; c < 4; c++) { lo[r][c] += (uint32_t)t[c]; hi[r][c] += t[c] >> 32; }
-      }
+      for (int r = 0; r < kColRows; r++) load_row4<kVec4>(rows[r], jn, cntn, vn[r]);
     }
-  }
-  // reduce each row's partial sums over the workgroup
-  __shared__ qm31 sh[kBlock / 64][kRowsPerBlock];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int r = 0; r < kRowsPerBlock; r++) {
-    qm31 s;
-    uint32_t w4[4];
+    for (int r = 0; r < kColRows; r++) acc_row4(lo[r], hi[r], vc[r], lc);
+    if (!cntn) break;
 #pragma unroll
-    for (int c = 0; c < 4; c++) w4[c] = m31_add(m31_reduce64(lo[r][c]), m31_mul(m31_reduce64(hi[r][c]), 2u));
-    s = qm31{w4[0], w4[1], w4[2], w4[3]};
-    s = wave_sum(s);
-    if (lane == 0) sh[wave][r] = s;
+    for (int u = 0; u < 4; u++) lc[u] = ln[u];
+#pragma unroll
+    for (int r = 0; r < kColRows; r++)
+#pragma unroll
+      for (int u = 0; u < 4; u++) vc[r][u] = vn[r][u];
+    j = jn;
+    cnt = cntn;
   }
-  __syncthreads();
-  if (threadIdx.x < kRowsPerBlock && (int)threadIdx.x < nrows) {
-    qm31 s = sh[0][threadIdx.x];
-    for (int w = 1; w < kBlock / 64; w++) s = qm31_add(s, sh[w][threadIdx.x]);
-    st_q(out, row0 + threadIdx.x, s);
+  // canonical per-lane sums (lo + 2*hi < 2^64 because 2^32 == 2 mod P),
+  // then the wave reduction of the 16 (row, component) values
+  uint32_t v[16];
+#pragma unroll
+  for (int r = 0; r < kColRows; r++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) v[4 * r + c] = m31_reduce64(lo[r][c] + (hi[r][c] << 1));
+  const uint32_t w = wave_sum16(v);
+  if ((lane & 3) == 0) {
+    const int slot = lane >> 2, r = slot >> 2, c = slot & 3;
+    if (r < nrows) partial[((uint64_t)blockIdx.y * k + row0 + r) * 4 + c] = w;
   }
+}
+// f_b[i] = sum over column chunks of partial[chunk * k + i] for i < k; 0 for k <= i < pk.
+__global__ void k_restrict_cols_finish(const qm31* __restrict__ partial, uint64_t k, uint64_t pk, int nchunks,
+                                       qm31* __restrict__ out) {
+  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= pk) return;
+  if (i >= k) {
+    st_q(out, i, qm31_zero());
+    return;
+  }
+  qacc acc;
+  acc.zero();
+  for (int c = 0; c < nchunks; c++) acc.add(ld_q(partial, (uint64_t)c * k + i));
+  st_q(out, i, acc.reduce());
 }
 __global__ void k_zero_q(qm31* __restrict__ out, uint64_t from, uint64_t to) {
   uint64_t i = from + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -237,7 +369,7 @@ __global__ void k_zero_q(qm31* __restrict__ out, uint64_t from, uint64_t to) {
 __global__ void __launch_bounds__(kBlock) k_mm_round(const qm31* __restrict__ a_in, const qm31* __restrict__ b_in,
                                                      qm31* __restrict__ a_out, qm31* __restrict__ b_out,
                                                      uint64_t half, int fold, qm31 alpha,
-                                                     qm31* __restrict__ partials) {
+                                                     RoundSink sink) {
   qacc s0, s1, s2;
   s0.zero(); s1.zero(); s2.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -261,32 +393,15 @@ __global__ void __launch_bounds__(kBlock) k_mm_round(const qm31* __restrict__ a_
     s2.add(qm31_mul(a2, b2));
   }
   qm31 v[3] = {s0.reduce(), s1.reduce(), s2.reduce()};
-  block_sum_store<3>(v, partials + 3 * (uint64_t)blockIdx.x);
+  sink_finish<3>(v, sink);
 }
 
 // Fold both vectors of length 2 to a single value each: out = {fold(a), fold(b)}.
-__global__ void k_mm_final(const qm31* __restrict__ a, const qm31* __restrict__ b, qm31 alpha,
-                           qm31* __restrict__ out) {
+__global__ void k_mm_final(const qm31* __restrict__ a, const qm31* __restrict__ b, qm31 alpha, RoundSink sink) {
   if (threadIdx.x == 0) {
-    out[0] = qm31_fold(ld_q(a, 0), ld_q(a, 1), alpha);
-    out[1] = qm31_fold(ld_q(b, 0), ld_q(b, 1), alpha);
+    const qm31 v[2] = {qm31_fold(ld_q(a, 0), ld_q(a, 1), alpha), qm31_fold(ld_q(b, 0), ld_q(b, 1), alpha)};
+    sink_single<2>(v, sink);
   }
-}
-
-// Sum NQ-wide partial rows: out[q] = sum_b partials[NQ*b + q].  One workgroup.
-template <int NQ>
-__global__ void __launch_bounds__(kBlock) k_sum_partials(const qm31* __restrict__ partials, int nblocks,
-                                                         qm31* __restrict__ out) {
-  qacc acc[NQ];
-#pragma unroll
-  for (int q = 0; q < NQ; q++) acc[q].zero();
-  for (int b = threadIdx.x; b < nblocks; b += blockDim.x)
-#pragma unroll
-    for (int q = 0; q < NQ; q++) acc[q].add(ld_q(partials, (uint64_t)NQ * b + q));
-  qm31 v[NQ];
-#pragma unroll
-  for (int q = 0; q < NQ; q++) v[q] = acc[q].reduce();
-  block_sum_store<NQ>(v, out);
 }
 
 // ------------------------------------------------------------------ LogUp
@@ -297,7 +412,7 @@ __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
     const uint32_t* __restrict__ table_out, uint32_t mask, qm31 gamma, qm31 beta,
     uint32_t* __restrict__ padded_in, uint32_t* __restrict__ masked_in, uint32_t* __restrict__ masked_out,
-    qm31* __restrict__ d_out, qm31* __restrict__ w_out, uint32_t* __restrict__ mult, qm31* __restrict__ partials) {
+    qm31* __restrict__ d_out, qm31* __restrict__ w_out, uint32_t* __restrict__ mult, RoundSink sink) {
   qacc acc;
   acc.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -313,16 +428,18 @@ __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     const qm31 w = qm31_inv(d);
     st_q(d_out, p, d);
     st_q(w_out, p, w);
-    atomicAdd(&mult[mi], 1u);
+    // zero padding all lands in bin 0; it is counted once below
+    if (r < rows && c < cols) atomicAdd(&mult[mi], 1u);
     acc.add(w);
   }
+  if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
   qm31 v[1] = {acc.reduce()};
-  block_sum_store<1>(v, partials + blockIdx.x);
+  sink_finish<1>(v, sink);
 }
 // Table side: sum_j mult_j / (gamma - j - beta*f(j)) over entries with mult_j > 0.
 __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __restrict__ table_out,
                                                             const uint32_t* __restrict__ mult, uint64_t size,
-                                                            qm31 gamma, qm31 beta, qm31* __restrict__ partials) {
+                                                            qm31 gamma, qm31 beta, RoundSink sink) {
   qacc acc;
   acc.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -334,7 +451,7 @@ __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __re
     acc.add(qm31_mul_m31(qm31_inv(d), m31_from_u32(m)));
   }
   qm31 v[1] = {acc.reduce()};
-  block_sum_store<1>(v, partials + blockIdx.x);
+  sink_finish<1>(v, sink);
 }
 
 // Degree-3 eq-sumcheck round over (eq, w, d) (gkr/prover.rs:6510-6556, 9236-9270):
@@ -344,7 +461,7 @@ __global__ void __launch_bounds__(kBlock) k_eq3_round(const qm31* __restrict__ e
                                                       const qm31* __restrict__ d_in, qm31* __restrict__ e_out,
                                                       qm31* __restrict__ w_out, qm31* __restrict__ d_out,
                                                       uint64_t half, int fold, qm31 alpha,
-                                                      qm31* __restrict__ partials) {
+                                                      RoundSink sink) {
   qacc s0, s1, s2, s3;
   s0.zero(); s1.zero(); s2.zero(); s3.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -374,14 +491,14 @@ __global__ void __launch_bounds__(kBlock) k_eq3_round(const qm31* __restrict__ e
     s3.add(qm31_mul(qm31_mul(e3, w3), d3));
   }
   qm31 v[4] = {s0.reduce(), s1.reduce(), s2.reduce(), s3.reduce()};
-  block_sum_store<4>(v, partials + 4 * (uint64_t)blockIdx.x);
+  sink_finish<4>(v, sink);
 }
 __global__ void k_eq3_final(const qm31* __restrict__ e, const qm31* __restrict__ w, const qm31* __restrict__ d,
-                            qm31 alpha, qm31* __restrict__ out) {
+                            qm31 alpha, RoundSink sink) {
   if (threadIdx.x == 0) {
-    out[0] = qm31_fold(ld_q(e, 0), ld_q(e, 1), alpha);
-    out[1] = qm31_fold(ld_q(w, 0), ld_q(w, 1), alpha);
-    out[2] = qm31_fold(ld_q(d, 0), ld_q(d, 1), alpha);
+    const qm31 v[3] = {qm31_fold(ld_q(e, 0), ld_q(e, 1), alpha), qm31_fold(ld_q(w, 0), ld_q(w, 1), alpha),
+                       qm31_fold(ld_q(d, 0), ld_q(d, 1), alpha)};
+    sink_single<3>(v, sink);
   }
 }
 
@@ -389,7 +506,7 @@ __global__ void k_eq3_final(const qm31* __restrict__ e, const qm31* __restrict__
 // lo = sum_{i<half} v[i], hi = sum_{i<half} v[half+i], with the same fused fold.
 __global__ void __launch_bounds__(kBlock) k_sum_round(const qm31* __restrict__ v_in, qm31* __restrict__ v_out,
                                                       uint64_t half, int fold, qm31 alpha,
-                                                      qm31* __restrict__ partials) {
+                                                      RoundSink sink) {
   qacc lo, hi;
   lo.zero(); hi.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -406,10 +523,13 @@ __global__ void __launch_bounds__(kBlock) k_sum_round(const qm31* __restrict__ v
     hi.add(x1);
   }
   qm31 v[2] = {lo.reduce(), hi.reduce()};
-  block_sum_store<2>(v, partials + 2 * (uint64_t)blockIdx.x);
+  sink_finish<2>(v, sink);
 }
-__global__ void k_fold1_final(const qm31* __restrict__ v, qm31 alpha, qm31* __restrict__ out) {
-  if (threadIdx.x == 0) out[0] = qm31_fold(ld_q(v, 0), ld_q(v, 1), alpha);
+__global__ void k_fold1_final(const qm31* __restrict__ v, qm31 alpha, RoundSink sink) {
+  if (threadIdx.x == 0) {
+    const qm31 r[1] = {qm31_fold(ld_q(v, 0), ld_q(v, 1), alpha)};
+    sink_single<1>(r, sink);
+  }
 }
 __global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __restrict__ out) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -419,7 +539,7 @@ __global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __
 // ------------------------------------------------------------------ MLE evaluation helpers
 // Partial dot products sum_i v[i] * eq[i] for an M31-valued v.
 __global__ void __launch_bounds__(kBlock) k_dot_m31(const uint32_t* __restrict__ v, const qm31* __restrict__ eq,
-                                                    uint64_t n, qm31* __restrict__ partials) {
+                                                    uint64_t n, RoundSink sink) {
   uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
@@ -433,18 +553,18 @@ __global__ void __launch_bounds__(kBlock) k_dot_m31(const uint32_t* __restrict__
 #pragma unroll
   for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
   qm31 q[1] = {qm31{r[0], r[1], r[2], r[3]}};
-  block_sum_store<1>(q, partials + blockIdx.x);
+  sink_finish<1>(q, sink);
 }
 // Partial dot products sum_i v[i] * eq[i] for a QM31-valued v.
 __global__ void __launch_bounds__(kBlock) k_dot_q(const qm31* __restrict__ v, const qm31* __restrict__ eq,
-                                                  uint64_t n, qm31* __restrict__ partials) {
+                                                  uint64_t n, RoundSink sink) {
   qacc acc;
   acc.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     acc.add(qm31_mul(ld_q(v, i), ld_q(eq, i)));
   qm31 q[1] = {acc.reduce()};
-  block_sum_store<1>(q, partials + blockIdx.x);
+  sink_finish<1>(q, sink);
 }
 // restrict_mle: fix the first s variables: out[y] = sum_x eq[x] * mle[x * rest + y].
 __global__ void k_restrict_q(const qm31* __restrict__ mle, const qm31* __restrict__ eq, uint64_t nx,

@@ -4,7 +4,8 @@
 // Hades: 91 rounds over a 3-element state; rounds 0-3 and 87-90 are full
 // (x^3 on every lane), rounds 4-86 are partial (x^3 on lane 2 only).  Each
 // round adds its three round constants to the three lanes, applies the
-// S-box, then the MDS matrix [[3,1,1],[1,-1,1],[1,1,-2]]
+// S-box, then the MDS matrix [[3,1,1],[1,-1,1],[1,1,-2]] (evaluated below in
+// the equivalent compressed-constant form)
 // (reference: engine/src/recursive/hades_air.rs:1892-2012 for the round
 // structure and MDS; constants per engine/src/crypto/poseidon_constants.rs).
 //
@@ -26,14 +27,44 @@ namespace gkr {
 
 #include "hades_constants.inc"
 
+// Round constants in the compressed form: rounds 0-3 and 88-90 keep their
+// three raw constants; the constants that partial rounds 4-86 add to lanes 0
+// and 1 (which skip the S-box) are pushed through the linear layer and
+// folded into round 87, so a partial round adds a single constant to lane 2.
+// The permutation is unchanged (hades_air.rs:1137-1180 states the same
+// compression).
 struct hades_rc {
-  felt rc[273];  // Montgomery form
+  felt full_first[4][3];
+  felt partial[83];
+  felt full_last[4][3];
+  static void mds(felt s[3]) {
+    felt t = felt_add(felt_add(s[0], s[1]), s[2]);
+    felt n0 = felt_add(t, felt_add(s[0], s[0]));
+    felt n1 = felt_sub(t, felt_add(s[1], s[1]));
+    felt n2 = felt_sub(t, felt_add(felt_add(s[2], s[2]), s[2]));
+    s[0] = n0;
+    s[1] = n1;
+    s[2] = n2;
+  }
   hades_rc() {
-    for (int i = 0; i < 273; i++) {
-      felt c{{kHadesRoundConstants[i][0], kHadesRoundConstants[i][1], kHadesRoundConstants[i][2],
-              kHadesRoundConstants[i][3]}};
-      rc[i] = felt_to_mont(c);
+    felt raw[91][3];
+    for (int r = 0; r < 91; r++)
+      for (int j = 0; j < 3; j++) {
+        const uint64_t* c = kHadesRoundConstants[3 * r + j];
+        raw[r][j] = felt_to_mont(felt{{c[0], c[1], c[2], c[3]}});
+      }
+    for (int r = 0; r < 4; r++)
+      for (int j = 0; j < 3; j++) full_first[r][j] = raw[r][j];
+    felt acc[3] = {felt_zero(), felt_zero(), felt_zero()};
+    for (int r = 0; r < 83; r++) {
+      for (int j = 0; j < 3; j++) acc[j] = felt_add(acc[j], raw[4 + r][j]);
+      partial[r] = acc[2];
+      acc[2] = felt_zero();
+      mds(acc);
     }
+    for (int j = 0; j < 3; j++) full_last[0][j] = felt_add(acc[j], raw[87][j]);
+    for (int r = 1; r < 4; r++)
+      for (int j = 0; j < 3; j++) full_last[r][j] = raw[87 + r][j];
   }
 };
 inline const hades_rc& hades_constants() {
@@ -44,25 +75,22 @@ inline const hades_rc& hades_constants() {
 inline felt felt_cube(const felt& x) { return felt_mul(felt_mul(x, x), x); }
 
 inline void hades_permute(felt s[3]) {
-  const felt* rc = hades_constants().rc;
-  for (int r = 0; r < 91; r++) {
-    s[0] = felt_add(s[0], rc[3 * r]);
-    s[1] = felt_add(s[1], rc[3 * r + 1]);
-    s[2] = felt_add(s[2], rc[3 * r + 2]);
-    const bool full = (r < 4) || (r >= 87);
-    if (full) {
-      s[0] = felt_cube(s[0]);
-      s[1] = felt_cube(s[1]);
-    }
-    s[2] = felt_cube(s[2]);
-    // MDS: t = s0+s1+s2; s0' = t + 2 s0; s1' = t - 2 s1; s2' = t - 3 s2
-    felt t = felt_add(felt_add(s[0], s[1]), s[2]);
-    felt n0 = felt_add(t, felt_add(s[0], s[0]));
-    felt n1 = felt_sub(t, felt_add(s[1], s[1]));
-    felt n2 = felt_sub(t, felt_add(felt_add(s[2], s[2]), s[2]));
-    s[0] = n0;
-    s[1] = n1;
-    s[2] = n2;
+  const hades_rc& k = hades_constants();
+  for (int r = 0; r < 4; r++) {
+    s[0] = felt_cube(felt_add(s[0], k.full_first[r][0]));
+    s[1] = felt_cube(felt_add(s[1], k.full_first[r][1]));
+    s[2] = felt_cube(felt_add(s[2], k.full_first[r][2]));
+    hades_rc::mds(s);
+  }
+  for (int r = 0; r < 83; r++) {
+    s[2] = felt_cube(felt_add(s[2], k.partial[r]));
+    hades_rc::mds(s);
+  }
+  for (int r = 0; r < 4; r++) {
+    s[0] = felt_cube(felt_add(s[0], k.full_last[r][0]));
+    s[1] = felt_cube(felt_add(s[1], k.full_last[r][1]));
+    s[2] = felt_cube(felt_add(s[2], k.full_last[r][2]));
+    hades_rc::mds(s);
   }
 }
 
