@@ -272,6 +272,11 @@ def main():
         "host_poseidon_us_per_round": poseidon_round_us(),
         "proof": {"felts": digests[0][1], "sha256_16": sbuf.fingerprint(), "final_digest": hex(digests[0][0])},
     }
+    cp, rd = ctx.bench_copy(1 << 32, 5)
+    result["hbm_measured"] = {"copy_gbps": round(cp, 1), "read_gbps": round(rd, 1),
+                              "note": "128-bit streaming copy (read+write) / read kernels over 4 GiB"}
+    if rc:
+        result["roofline"]["frac_of_measured_read"] = round(rc["gbps"] / rd, 4)
     if not args.no_cpu_baseline:
         log("[bench] timing CPU baseline sample")
         result["cpu_baseline"] = cpu_baseline()

@@ -203,6 +203,11 @@ int gkr_prove_activation_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32
 /* Activation table output column, f(j) for j < 2^log_size (host). */
 int gkr_activation_table(uint32_t activation_type, uint32_t log_size, uint32_t* out);
 
+/* Bandwidth reference (no counterpart in the reference): a plain 128-bit
+ * device-to-device copy and a read-only stream over `bytes`, `iters` times;
+ * reports (bytes read + written) / time and bytes read / time in GB/s.    */
+int gkr_bench_copy(gkr_ctx* ctx, uint64_t bytes, int iters, double* copy_gbps, double* read_gbps);
+
 #ifdef __cplusplus
 }
 #endif

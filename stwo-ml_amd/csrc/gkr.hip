@@ -1298,3 +1298,45 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   }
   return GKR_OK;
 }
+
+// ------------------------------------------------------------------ bandwidth reference
+extern "C" int gkr_bench_copy(gkr_ctx* c, uint64_t bytes, int iters, double* copy_gbps, double* read_gbps) {
+  if (!c || !copy_gbps || !read_gbps || bytes < 16 || iters < 1) return fail(GKR_ERR_INVALID, "bad argument");
+  HIP_TRY(hipSetDevice(c->device));
+  const uint64_t n = bytes / 16;
+  uint4 *src = nullptr, *dst = nullptr;
+  HIP_TRY(hipMalloc(&src, n * 16));
+  if (hipMalloc(&dst, n * 16) != hipSuccess) {
+    (void)hipFree(src);
+    return fail(GKR_ERR_NOMEM, "copy buffers");
+  }
+  int rc = GKR_OK;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float ms = 0;
+  const unsigned g = 256 * 8;  // 8 workgroups per CU, grid-stride
+  if (hipMemsetAsync(src, 1, n * 16, c->stream) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+      hipEventCreate(&e1) != hipSuccess) {
+    rc = fail(GKR_ERR_DEVICE, "copy setup");
+  } else {
+    hipLaunchKernelGGL(k_copy16, dim3(g), dim3(kBlock), 0, c->stream, src, dst, n);  // warm-up
+    (void)hipEventRecord(e0, c->stream);
+    for (int i = 0; i < iters; i++) hipLaunchKernelGGL(k_copy16, dim3(g), dim3(kBlock), 0, c->stream, src, dst, n);
+    (void)hipEventRecord(e1, c->stream);
+    (void)hipEventSynchronize(e1);
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    *copy_gbps = 2.0 * n * 16 * iters / (ms * 1e-3) / 1e9;
+    (void)hipEventRecord(e0, c->stream);
+    for (int i = 0; i < iters; i++)
+      hipLaunchKernelGGL(k_read16, dim3(g), dim3(kBlock), 0, c->stream, src, n, (uint32_t*)dst);
+    (void)hipEventRecord(e1, c->stream);
+    (void)hipEventSynchronize(e1);
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    *read_gbps = (double)n * 16 * iters / (ms * 1e-3) / 1e9;
+    if (hipGetLastError() != hipSuccess) rc = fail(GKR_ERR_DEVICE, "copy kernels failed");
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  (void)hipFree(src);
+  (void)hipFree(dst);
+  return rc;
+}

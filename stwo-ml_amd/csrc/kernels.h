@@ -577,6 +577,23 @@ __global__ void k_restrict_q(const qm31* __restrict__ mle, const qm31* __restric
   st_q(out, y, acc.reduce());
 }
 
+// ------------------------------------------------------------------ bandwidth reference
+// Plain 128-bit streaming copy and read, used to measure the achievable HBM
+// bandwidth and to calibrate counter-derived traffic.
+__global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, uint64_t n) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+__global__ void k_read16(const uint4* __restrict__ src, uint64_t n, uint32_t* __restrict__ sink) {
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  uint32_t acc = 0;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const uint4 v = src[i];
+    acc ^= v.x + v.y + v.z + v.w;
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;  // keeps the loads live; practically never taken
+}
+
 // ------------------------------------------------------------------ synthetic inputs
 // Counter-mode SplitMix64: element i of the stream keyed by `seed` is the
 // (i+1)-th output of the sequential generator started at `seed`.

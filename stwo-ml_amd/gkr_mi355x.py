@@ -116,6 +116,7 @@ SIGNATURES = [
     ("gkr_prove_activation_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, C.c_uint32, C.c_uint32, _P, _P,
                                              C.POINTER(GkrLogupOut)]),
     ("gkr_activation_table", C.c_int, [C.c_uint32, C.c_uint32, _U32P]),
+    ("gkr_bench_copy", C.c_int, [_P, C.c_uint64, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
 ]
 
 
@@ -305,6 +306,12 @@ class Context:
         ms, n, b = C.c_double(), C.c_uint64(), C.c_uint64()
         _check(lib().gkr_ctx_kernel_time(self._h, kid, C.byref(ms), C.byref(n), C.byref(b)))
         return ms.value, n.value, b.value
+
+    def bench_copy(self, nbytes: int = 1 << 32, iters: int = 5) -> Tuple[float, float]:
+        """(copy GB/s counting read + write, read-only GB/s) of plain 128-bit streaming kernels."""
+        cp, rd = C.c_double(), C.c_double()
+        _check(lib().gkr_bench_copy(self._h, nbytes, iters, C.byref(cp), C.byref(rd)))
+        return cp.value, rd.value
 
     # matrices
     def upload(self, m: np.ndarray) -> "Matrix":
