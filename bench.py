@@ -77,17 +77,28 @@ def matmul_elems(cfg):
     return sum(k * n + mm * k for mm, k, n in shapes), shapes
 
 
+CALL_TIME = {"matmul_claim": 0.0, "matmul_layer": 0.0, "activation_layer": 0.0}
+
+
 def prove_matmul(ctx, ch, a, b, proof):
     r = ch.draw_qm31s(lg(a.rows) + lg(b.cols))
+    t0 = time.perf_counter()
     v = ctx.matmul_output_claim(a, b, r)
+    t1 = time.perf_counter()
     ch.mix_secure_field(v)
-    return ctx.prove_matmul_layer(r, v, a, b, ch, proof)
+    res = ctx.prove_matmul_layer(r, v, a, b, ch, proof)
+    CALL_TIME["matmul_claim"] += t1 - t0
+    CALL_TIME["matmul_layer"] += time.perf_counter() - t1
+    return res
 
 
 def prove_logup(ctx, ch, x, tag, tlog, proof):
     r = ch.draw_qm31s(lg(x.rows) + lg(x.cols))
     v = ch.draw_qm31()
-    return ctx.prove_activation_layer(r, v, x, tag, ch, tlog, proof)
+    t0 = time.perf_counter()
+    res = ctx.prove_activation_layer(r, v, x, tag, ch, tlog, proof)
+    CALL_TIME["activation_layer"] += time.perf_counter() - t0
+    return res
 
 
 class SerialBuffer:
@@ -126,6 +137,33 @@ def prove_model(ctx, layers, cfg, seed, sbuf):
         if L.scores is not None:
             prove_logup(ctx, ch, L.scores, 4, 16, proof)  # softmax-exp, 2^16 table
     n = sbuf.serialize(proof)  # final proof serialization (C side)
+    return ch.digest(), n
+
+
+def model_steps(layers):
+    """The per-layer step list for gkr_prove_walk (same order and claims as prove_model)."""
+    F = G.CLAIM_FRESH
+    steps = []
+    for L in layers:
+        for name in ("q", "k", "v", "o", "gate", "up"):
+            a, b = L.mats[name]
+            steps.append((G.STEP_MATMUL, F, a, b, 0, 0))
+        steps.append((G.STEP_ACTIVATION, F, L.silu_in, None, 5, 16))
+        a, b = L.mats["down"]
+        steps.append((G.STEP_MATMUL, F, a, b, 0, 0))
+        if L.scores is not None:
+            steps.append((G.STEP_ACTIVATION, F, L.scores, None, 4, 16))
+    return G.make_steps(steps), len(steps)
+
+
+def prove_model_walk(ctx, steps, seed, sbuf):
+    """The same proof as prove_model, with the layer loop inside the library (gkr_prove_walk)."""
+    arr, n = steps
+    ch = G.PoseidonChannel()
+    ch.mix_u64(seed)
+    proof = G.Proof()
+    G.prove_walk(ctx, ch, arr, proof, n_steps=n)
+    n = sbuf.serialize(proof)
     return ch.digest(), n
 
 
@@ -181,6 +219,8 @@ def main():
     ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true", help="skip per-kernel HIP events")
+    ap.add_argument("--driver", default="walk", choices=["walk", "calls"],
+                    help="walk: one gkr_prove_walk call per proof; calls: one library call per layer")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -206,7 +246,11 @@ def main():
         per_layer, shapes = matmul_elems(cfg)
         elems = per_layer * n_layers
         tokens = cfg["tokens"]
-        step = lambda: prove_model(ctx, layers, cfg, 7, sbuf)  # noqa: E731
+        if args.driver == "walk":
+            steps = model_steps(layers)
+            step = lambda: prove_model_walk(ctx, steps, 7, sbuf)  # noqa: E731
+        else:
+            step = lambda: prove_model(ctx, layers, cfg, 7, sbuf)  # noqa: E731
         workload = {"qwen48": "qwen2.5-14b-48-layers-64-tokens", "qwen1": "qwen2.5-14b-1-layer-64-tokens",
                     "smollm": "smollm2-135m-30-layers-1-token"}[args.config]
 
@@ -217,6 +261,8 @@ def main():
     ctx.set_timing(not args.no_timing)
     ctx.reset_timing()
     ctx.synchronize()
+    for key in CALL_TIME:
+        CALL_TIME[key] = 0.0
     t0 = time.perf_counter()
     digests = []
     for s in range(args.steps):
@@ -269,6 +315,9 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "host": host,
+        "driver": args.driver,
+        "calls_ms_per_step": ({k: round(v / args.steps * 1e3, 3) for k, v in CALL_TIME.items()}
+                              if args.driver == "calls" else None),
         "host_poseidon_us_per_round": poseidon_round_us(),
         "proof": {"felts": digests[0][1], "sha256_16": sbuf.fingerprint(), "final_digest": hex(digests[0][0])},
     }

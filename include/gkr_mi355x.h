@@ -200,6 +200,30 @@ int gkr_prove_activation_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32
                                const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t activation_type,
                                uint32_t table_log_size, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out);
 
+/* GKR walk over a sequence of layers (the layer loop of prove_gkr_with_cache,
+ * gkr/prover.rs:1500-1660, for MatMul and Activation layers).  Steps run in
+ * order on one channel and append their LayerProof to `proof`.  Each step's
+ * output claim is either chained (the previous step's input claim, or
+ * init_point/init_value for the first step: the reference's walk) or fresh:
+ * a MatMul draws r_out = draw_qm31s(log2 pm + log2 pn), takes value =
+ * MLE of A*B at r_out and mixes it (prover.rs:1543-1560); an Activation
+ * draws its point (log2 of the padded size) and then its value with
+ * draw_qm31.  On return final_point/final_value hold the last input claim
+ * (final_point needs room for 64 entries).                                  */
+enum { GKR_STEP_MATMUL = 0, GKR_STEP_ACTIVATION = 3 };
+enum { GKR_CLAIM_CHAINED = 0, GKR_CLAIM_FRESH = 1 };
+typedef struct {
+  uint32_t kind;             /* GKR_STEP_MATMUL / GKR_STEP_ACTIVATION */
+  uint32_t claim;            /* GKR_CLAIM_CHAINED / GKR_CLAIM_FRESH */
+  const gkr_matrix* a;       /* MatMul: A (m x k); Activation: the input matrix */
+  const gkr_matrix* b;       /* MatMul: B (k x n); Activation: unused */
+  uint32_t activation_type;  /* Activation: reference type tag */
+  uint32_t table_log_size;   /* Activation: 0 = reference default */
+} gkr_step;
+int gkr_prove_walk(gkr_ctx* ctx, gkr_channel* ch, const gkr_step* steps, size_t n_steps, const gkr_qm31* init_point,
+                   uint32_t n_init, const gkr_qm31* init_value, gkr_proof* proof, gkr_qm31* final_point,
+                   uint32_t* n_final, gkr_qm31* final_value);
+
 /* Activation table output column, f(j) for j < 2^log_size (host). */
 int gkr_activation_table(uint32_t activation_type, uint32_t log_size, uint32_t* out);
 

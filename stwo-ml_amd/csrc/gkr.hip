@@ -9,6 +9,7 @@
 #include <chrono>
 
 #include <map>
+#include <memory>
 #include <set>
 #include <string>
 #include <vector>
@@ -120,8 +121,9 @@ struct gkr_ctx {
   qm31* h_res = nullptr;  // pinned result staging (64 QM31)
   qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
   uint32_t* h_flag = nullptr; // coherent pinned: sequence number of the last delivery
-  uint32_t* d_counter = nullptr;  // device: workgroup arrival counter of RoundSink
-  uint32_t seq = 0;
+  Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
+  uint32_t seq = 0;            // last result sequence number handed out
+  uint32_t mb_seq = 0;         // last mailbox sequence number handed out
   bool timing = false;
   KernelStat stats[K_NKERNELS];
   std::vector<PendingTiming> pending;
@@ -265,25 +267,34 @@ static int make_sink(gkr_ctx* c, RoundSink* sk) {
   qm31* part;
   TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
   sk->partials = part;
-  sk->counter = c->d_counter;
   sk->out = c->h_out;
   sk->flag = c->h_flag;
   sk->seq = ++c->seq;
   return GKR_OK;
 }
-// Wait until the kernel launched with `sk` has published its NQ results.
-// The wait spins on the coherent flag; after ~2 s without it the stream is
+// Launch the one-workgroup finisher that adds `nblocks` partial rows and
+// delivers the NQ results (after a multi-workgroup reducing kernel).
+template <int NQ>
+static int launch_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks) {
+  TRY(check_launch());
+  hipLaunchKernelGGL(k_finish<NQ>, dim3(1), dim3(kBlock), 0, c->stream, sk, (uint32_t)nblocks);
+  return check_launch();
+}
+// Wait until result `seq` has been published and copy NQ values.  The wait
+// spins on the coherent flag; after ~2 s without it the stream is
 // synchronised so that a device error is reported instead of hanging.
 template <int NQ>
-static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
+static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out) {
   TRY(check_launch());
   HostTimer ht(c, K_HOST_WAIT);
   volatile uint32_t* flag = c->h_flag;
   uint64_t spins = 0;
-  while (*flag != sk.seq) {
+  uint32_t got;
+  while ((got = *flag) != seq) {
+    if (got == kTailTimeout) return fail(GKR_ERR_DEVICE, "persistent round kernel timed out waiting for a challenge");
     if (++spins == (1u << 26)) {
       HIP_TRY(hipStreamSynchronize(c->stream));
-      if (*flag != sk.seq) return fail(GKR_ERR_DEVICE, "device result %u not delivered", sk.seq);
+      if (*flag != seq) return fail(GKR_ERR_DEVICE, "device result %u not delivered", seq);
       break;
     }
   }
@@ -291,6 +302,34 @@ static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
   for (int q = 0; q < NQ; q++) host_out[q] = c->h_out[q];
   return GKR_OK;
 }
+template <int NQ>
+static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
+  return wait_result<NQ>(c, sk.seq, host_out);
+}
+// Host side of a persistent tail kernel: posts challenges into the mailbox.
+// If the host leaves before the protocol completes (an error), the guard
+// posts the cancel code so the kernel stops waiting at once.
+struct TailSession {
+  gkr_ctx* c;
+  uint32_t res_base, mb_base;
+  bool done = false;
+  TailSession(gkr_ctx* c_, int n_results, int n_posts) : c(c_) {
+    res_base = c->seq + 1;
+    c->seq += (uint32_t)n_results;
+    mb_base = c->mb_seq + 1;
+    c->mb_seq += (uint32_t)n_posts;
+  }
+  void post(uint32_t r, const qm31& alpha) {
+    c->mailbox->alpha = alpha;
+    __atomic_store_n(&c->mailbox->seq, mb_base + r, __ATOMIC_RELEASE);
+  }
+  ~TailSession() {
+    if (!done) {  // error path: release the waiting kernel and let it drain before the mailbox is reused
+      __atomic_store_n(&c->mailbox->seq, kTailCancel, __ATOMIC_RELEASE);
+      (void)hipStreamSynchronize(c->stream);
+    }
+  }
+};
 static int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out) {
   HIP_TRY(hipMemcpyAsync(c->h_res, dev, count * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
   TRY(sync(c));
@@ -303,6 +342,7 @@ static int dot_m31(gkr_ctx* c, const uint32_t* v, const qm31* eq, uint64_t n, qm
   RoundSink sk;
   TRY(make_sink(c, &sk));
   hipLaunchKernelGGL(k_dot_m31, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, v, eq, n, sk);
+  TRY(launch_finish<1>(c, sk, partial_grid(n)));
   return wait_sink<1>(c, sk, out);
 }
 
@@ -470,14 +510,15 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
     return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");
   }
   if (hipHostMalloc((void**)&c->h_res, 64 * sizeof(qm31), hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&c->h_out, 64 * sizeof(qm31) + 64, hipHostMallocCoherent | hipHostMallocMapped) !=
-          hipSuccess ||
-      hipMalloc((void**)&c->d_counter, 256) != hipSuccess || hipMemset(c->d_counter, 0, 256) != hipSuccess) {
+      hipHostMalloc((void**)&c->h_out, 64 * sizeof(qm31) + 256, hipHostMallocCoherent | hipHostMallocMapped) !=
+          hipSuccess) {
     gkr_ctx_destroy(c);
     return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
   }
   c->h_flag = reinterpret_cast<uint32_t*>(c->h_out + 64);
   *c->h_flag = 0;
+  c->mailbox = reinterpret_cast<Mailbox*>(reinterpret_cast<char*>(c->h_out) + 64 * sizeof(qm31) + 128);
+  c->mailbox->seq = 0;
   *out = c;
   return GKR_OK;
 }
@@ -499,7 +540,6 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
     if (c->buf[s]) (void)hipFree(c->buf[s]);
   if (c->h_res) (void)hipHostFree(c->h_res);
   if (c->h_out) (void)hipHostFree(c->h_out);
-  if (c->d_counter) (void)hipFree(c->d_counter);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -657,6 +697,7 @@ static int round0_sums(gkr_ctx* c, uint64_t pk, qm31 s[3]) {
     hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, fa, fb, (qm31*)nullptr,
                        (qm31*)nullptr, half, 0, qm31_zero(), sk);
   }
+  TRY(launch_finish<3>(c, sk, partial_grid(half)));
   return wait_sink<3>(c, sk, s);
 }
 
@@ -734,22 +775,59 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
   const qm31 inv2 = qm31_from_m31(1u << 30);  // 2^-1 mod P
   const qm31* cur_a = fa0;
   const qm31* cur_b = fb0;
+  // Big rounds t < t0 fold into ping-pong buffers (round t >= 1 writes
+  // bufs[(t-1)&1]; round 2 overwrites S_FA0/S_FB0, which ends the cached
+  // restriction).  Rounds t >= t0 (at most kTailMax elements) and the final
+  // fold run in one persistent workgroup (k_mm_tail).
   qm31* bufs_a[2] = {fa1, fa0};
   qm31* bufs_b[2] = {fb1, fb0};
-  // Round t >= 1 folds into bufs[(t-1)&1]; after round 1 the vectors are no
-  // longer needed in S_FA0 except as ping-pong space, so mark the cache stale.
+  int t0 = 0;
+  while ((pk >> t0) > (uint64_t)kTailMax) t0++;
+  const int n_tail = T - t0;
   qm31 alpha = qm31_zero();
-  for (int t = 0; t < T; t++) {
+  auto absorb = [&](int t, const qm31* sums) {
+    const qm31 c0 = sums[0];
+    const qm31 c2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(sums[2], sums[1]), sums[1]), sums[0]), inv2);
+    const qm31 c1 = qm31_sub(qm31_sub(sums[1], sums[0]), c2);
+    round_polys[3 * t + 0] = G(c0);
+    round_polys[3 * t + 1] = G(c1);
+    round_polys[3 * t + 2] = G(c2);
+    HostTimer ht(c, K_HOST_FS);
+    ch.mix_poly_coeffs(c0, c1, c2);
+    alpha = ch.draw_qm31();
+    challenges[t] = G(alpha);
+  };
+  std::unique_ptr<TailSession> tail;
+  auto launch_tail = [&]() -> int {
+    const uint32_t len_in = (uint32_t)(t0 == 0 ? pk : (pk >> (t0 - 1)));
+    tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
+    hipLaunchKernelGGL(k_mm_tail, dim3(1), dim3(kBlock), 0, c->stream, cur_a, cur_b, len_in, t0 > 0 ? 1 : 0,
+                       n_tail, c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base);
+    return check_launch();
+  };
+  for (int t = 0; t < t0; t++) {
     const uint64_t half = (pk >> t) / 2;
-    qm31 s[3];
-    if (t == 0 && c->mm.have_round0) {
-      s[0] = c->mm.round0[0]; s[1] = c->mm.round0[1]; s[2] = c->mm.round0[2];
-    } else if (t == 0) {
-      TRY(round0_sums(c, pk, s));
+    qm31 sums[3];
+    if (t == 0) {
+      if (c->mm.have_round0) {
+        sums[0] = c->mm.round0[0]; sums[1] = c->mm.round0[1]; sums[2] = c->mm.round0[2];
+        if (t0 == 1) TRY(launch_tail());
+      } else {
+        RoundSink sk;
+        TRY(make_sink(c, &sk));
+        {
+          TimedLaunch tl(c, K_MM_ROUND, 32 * pk);
+          hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, fa0, fb0,
+                             (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
+        }
+        TRY(launch_finish<3>(c, sk, partial_grid(half)));
+        if (t0 == 1) TRY(launch_tail());
+        TRY(wait_sink<3>(c, sk, sums));
+      }
     } else {
-      qm31* na = (t == 1) ? fa1 : bufs_a[(t - 1) & 1];
-      qm31* nb = (t == 1) ? fb1 : bufs_b[(t - 1) & 1];
-      if (t == 2) c->mm.valid = false;  // round 2 writes into S_FA0 / S_FB0
+      qm31* na = bufs_a[(t - 1) & 1];
+      qm31* nb = bufs_b[(t - 1) & 1];
+      if (t == 2) c->mm.valid = false;
       RoundSink sk;
       TRY(make_sink(c, &sk));
       {
@@ -758,29 +836,28 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
         hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cur_a, cur_b, na, nb,
                            half, 1, alpha, sk);
       }
-      TRY(wait_sink<3>(c, sk, s));
+      TRY(launch_finish<3>(c, sk, partial_grid(half)));
       cur_a = na;
       cur_b = nb;
+      if (t == t0 - 1) TRY(launch_tail());
+      TRY(wait_sink<3>(c, sk, sums));
     }
-    const qm31 c0 = s[0];
-    const qm31 c2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
-    const qm31 c1 = qm31_sub(qm31_sub(s[1], s[0]), c2);
-    round_polys[3 * t + 0] = G(c0);
-    round_polys[3 * t + 1] = G(c1);
-    round_polys[3 * t + 2] = G(c2);
-    {
-      HostTimer ht(c, K_HOST_FS);
-      ch.mix_poly_coeffs(c0, c1, c2);
-      alpha = ch.draw_qm31();
-    }
-    challenges[t] = G(alpha);
+    absorb(t, sums);
   }
-  c->mm.valid = c->mm.valid && T < 2;
-  RoundSink fsk;
-  TRY(make_sink(c, &fsk));
-  hipLaunchKernelGGL(k_mm_final, dim3(1), dim3(64), 0, c->stream, cur_a, cur_b, alpha, fsk);
+  if (t0 == 0) {
+    TRY(launch_tail());
+  } else {
+    tail->post(0, alpha);  // fold by the challenge of round t0 - 1
+  }
+  for (int r = 0; r < n_tail; r++) {
+    qm31 sums[3];
+    TRY(wait_result<3>(c, tail->res_base + r, sums));
+    absorb(t0 + r, sums);
+    tail->post(r + 1, alpha);
+  }
   qm31 fin[2];
-  TRY(wait_sink<2>(c, fsk, fin));
+  TRY(wait_result<2>(c, tail->res_base + n_tail, fin));
+  tail->done = true;
   *final_a = G(fin[0]);
   *final_b = G(fin[1]);
   return GKR_OK;
@@ -1018,6 +1095,7 @@ extern "C" int gkr_evaluate_mle_at_point(gkr_ctx* c, const gkr_qm31* mle, uint64
   RoundSink sk;
   TRY(make_sink(c, &sk));
   hipLaunchKernelGGL(k_dot_q, dim3(partial_grid(len)), dim3(kBlock), 0, c->stream, dm, eq, len, sk);
+  TRY(launch_finish<1>(c, sk, partial_grid(len)));
   qm31 r[1];
   TRY(wait_sink<1>(c, sk, r));
   *out = G(r[0]);
@@ -1131,6 +1209,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
                          input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, d_pad, d_min, d_mout, d_d0,
                          d_w0, d_mult, sk);
     }
+    TRY(launch_finish<1>(c, sk, partial_grid(n)));
     qm31 r[1];
     TRY(wait_sink<1>(c, sk, r));
     trace_sum = r[0];
@@ -1140,6 +1219,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     TRY(make_sink(c, &sk));
     hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult,
                        tsize, gamma, beta, sk);
+    TRY(launch_finish<1>(c, sk, partial_grid(tsize)));
     qm31 r[1];
     TRY(wait_sink<1>(c, sk, r));
     table_sum = r[0];
@@ -1161,25 +1241,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   qm31* bw[2] = {d_w1, d_w0};
   qm31* bd[2] = {d_d1, d_d0};
   qm31 alpha = qm31_zero();
-  for (int t = 0; t < nv; t++) {
-    const uint64_t half = (n >> t) / 2;
-    qm31 s[4];
-    RoundSink sk;
-    TRY(make_sink(c, &sk));
-    {
-      // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}; round 0 reads only
-      TimedLaunch tl(c, K_EQ3_ROUND, t == 0 ? 96 * half : 288 * half);
-      if (t == 0) {
-        hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd,
-                           (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
-      } else {
-        qm31 *ne = be[(t - 1) & 1], *nw = bw[(t - 1) & 1], *nd = bd[(t - 1) & 1];
-        hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw, nd,
-                           half, 1, alpha, sk);
-        ce = ne; cw = nw; cd = nd;
-      }
-    }
-    TRY(wait_sink<4>(c, sk, s));
+  auto absorb3 = [&](int t, const qm31* s) {
     const qm31 dd1 = qm31_sub(s[1], s[0]);
     const qm31 dd2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
     const qm31 dd3 = qm31_mul(qm31_sub(qm31_sub(s[3], s[0]), qm31_mul(three, qm31_sub(s[2], s[1]))), inv6);
@@ -1191,19 +1253,62 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     out->eq_round_polys[4 * t + 1] = G(c1);
     out->eq_round_polys[4 * t + 2] = G(c2);
     out->eq_round_polys[4 * t + 3] = G(c3);
-    {
-      HostTimer ht(c, K_HOST_FS);
-      C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
-      alpha = C.draw_qm31();
-    }
+    HostTimer ht(c, K_HOST_FS);
+    C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
+    alpha = C.draw_qm31();
     chal[t] = alpha;
-  }
+  };
   qm31 fin[3];
   if (nv > 0) {
-    RoundSink sk;
-    TRY(make_sink(c, &sk));
-    hipLaunchKernelGGL(k_eq3_final, dim3(1), dim3(64), 0, c->stream, ce, cw, cd, alpha, sk);
-    TRY(wait_sink<3>(c, sk, fin));
+    // big rounds t < t0 as grid kernels, rounds t >= t0 (<= kTailMax/2
+    // elements per vector) and the final fold in k_eq3_tail
+    int t0 = 0;
+    while ((n >> t0) > (uint64_t)(kTailMax / 2)) t0++;
+    const int n_tail = nv - t0;
+    std::unique_ptr<TailSession> tail;
+    auto launch_tail = [&]() -> int {
+      const uint32_t len_in = (uint32_t)(t0 == 0 ? n : (n >> (t0 - 1)));
+      tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
+      hipLaunchKernelGGL(k_eq3_tail, dim3(1), dim3(kBlock), 0, c->stream, ce, cw, cd, len_in, t0 > 0 ? 1 : 0,
+                         n_tail, c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base);
+      return check_launch();
+    };
+    for (int t = 0; t < t0; t++) {
+      const uint64_t half = (n >> t) / 2;
+      qm31 sums[4];
+      RoundSink sk;
+      TRY(make_sink(c, &sk));
+      {
+        // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}; round 0 reads only
+        TimedLaunch tl(c, K_EQ3_ROUND, t == 0 ? 96 * half : 288 * half);
+        if (t == 0) {
+          hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd,
+                             (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
+        } else {
+          qm31 *ne = be[(t - 1) & 1], *nw = bw[(t - 1) & 1], *nd = bd[(t - 1) & 1];
+          hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw,
+                             nd, half, 1, alpha, sk);
+          ce = ne; cw = nw; cd = nd;
+        }
+      }
+      TRY(launch_finish<4>(c, sk, partial_grid(half)));
+      if (t == t0 - 1) TRY(launch_tail());
+      TRY(wait_sink<4>(c, sk, sums));
+      absorb3(t, sums);
+    }
+    if (t0 == 0) {
+      TRY(launch_tail());
+    } else {
+      tail->post(0, alpha);
+    }
+    for (int r = 0; r < n_tail; r++) {
+      qm31 sums[4];
+      TRY(wait_result<4>(c, tail->res_base + r, sums));
+      absorb3(t0 + r, sums);
+      tail->post(r + 1, alpha);
+    }
+    TRY(wait_result<3>(c, tail->res_base + n_tail, fin));
+    tail->done = true;
   } else {
     TRY(fetch_q(c, d_w0, 1, fin + 1));
   }
@@ -1233,38 +1338,61 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(check_launch());
   const qm31* cm = m0;
   qm31* bm[2] = {m1, m0};
-  for (uint32_t t = 0; t < table_log; t++) {
-    const uint64_t half = (tsize >> t) / 2;
-    RoundSink sk;
-    TRY(make_sink(c, &sk));
-    if (t == 0) {
-      hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, (qm31*)nullptr, half,
-                         0, qm31_zero(), sk);
-    } else {
-      qm31* nm = bm[(t - 1) & 1];
-      hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, nm, half, 1, alpha,
-                         sk);
-      cm = nm;
-    }
-    qm31 s[2];
-    TRY(wait_sink<2>(c, sk, s));
+  auto absorb1 = [&](uint32_t t, const qm31* s) {
     const qm31 c0 = s[0];
     const qm31 c1 = qm31_sub(s[1], s[0]);
     out->mult_round_polys[2 * t] = G(c0);
     out->mult_round_polys[2 * t + 1] = G(c1);
-    {
-      HostTimer ht(c, K_HOST_FS);
-      C.mix_secure_field(c0);
-      C.mix_secure_field(c1);
-      alpha = C.draw_qm31();
-    }
-  }
+    HostTimer ht(c, K_HOST_FS);
+    C.mix_secure_field(c0);
+    C.mix_secure_field(c1);
+    alpha = C.draw_qm31();
+  };
   qm31 mfin[1];
   {
-    RoundSink sk;
-    TRY(make_sink(c, &sk));
-    hipLaunchKernelGGL(k_fold1_final, dim3(1), dim3(64), 0, c->stream, cm, alpha, sk);
-    TRY(wait_sink<1>(c, sk, mfin));
+    int t0 = 0;
+    while ((tsize >> t0) > (uint64_t)kTailMax) t0++;
+    const int n_tail = (int)table_log - t0;
+    std::unique_ptr<TailSession> tail;
+    auto launch_tail = [&]() -> int {
+      const uint32_t len_in = (uint32_t)(t0 == 0 ? tsize : (tsize >> (t0 - 1)));
+      tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
+      hipLaunchKernelGGL(k_sum_tail, dim3(1), dim3(kBlock), 0, c->stream, cm, len_in, t0 > 0 ? 1 : 0, n_tail,
+                         c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base);
+      return check_launch();
+    };
+    for (int t = 0; t < t0; t++) {
+      const uint64_t half = (tsize >> t) / 2;
+      RoundSink sk;
+      TRY(make_sink(c, &sk));
+      if (t == 0) {
+        hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, (qm31*)nullptr,
+                           half, 0, qm31_zero(), sk);
+      } else {
+        qm31* nm = bm[(t - 1) & 1];
+        hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, nm, half, 1,
+                           alpha, sk);
+        cm = nm;
+      }
+      TRY(launch_finish<2>(c, sk, partial_grid(half)));
+      if (t == t0 - 1) TRY(launch_tail());
+      qm31 sums[2];
+      TRY(wait_sink<2>(c, sk, sums));
+      absorb1((uint32_t)t, sums);
+    }
+    if (t0 == 0) {
+      TRY(launch_tail());
+    } else {
+      tail->post(0, alpha);
+    }
+    for (int r = 0; r < n_tail; r++) {
+      qm31 sums[2];
+      TRY(wait_result<2>(c, tail->res_base + r, sums));
+      absorb1((uint32_t)(t0 + r), sums);
+      tail->post(r + 1, alpha);
+    }
+    TRY(wait_result<1>(c, tail->res_base + n_tail, mfin));
+    tail->done = true;
   }
   out->mult_final_eval = G(mfin[0]);
   out->mult_claimed_sum = G(mult_sum);
@@ -1339,4 +1467,72 @@ extern "C" int gkr_bench_copy(gkr_ctx* c, uint64_t bytes, int iters, double* cop
   (void)hipFree(src);
   (void)hipFree(dst);
   return rc;
+}
+
+// ------------------------------------------------------------------ GKR walk
+extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps, size_t n_steps,
+                              const gkr_qm31* init_point, uint32_t n_init, const gkr_qm31* init_value,
+                              gkr_proof* proof, gkr_qm31* final_point, uint32_t* n_final, gkr_qm31* final_value) {
+  CH_CHECK(ch);
+  if (!c || (!steps && n_steps) || !final_point || !n_final || !final_value)
+    return fail(GKR_ERR_INVALID, "null argument");
+  std::vector<gkr_qm31> point(init_point ? init_point : nullptr, init_point ? init_point + n_init : nullptr);
+  gkr_qm31 value = init_value ? *init_value : G(qm31_zero());
+  bool have_claim = init_value != nullptr;
+  std::vector<gkr_qm31> rp, npnt(64);
+  std::vector<uint32_t> mults;
+  for (size_t si = 0; si < n_steps; si++) {
+    const gkr_step& st = steps[si];
+    if (!st.a) return fail(GKR_ERR_INVALID, "step %zu: null matrix", si);
+    if (st.kind == GKR_STEP_MATMUL) {
+      if (!st.b) return fail(GKR_ERR_INVALID, "step %zu: null weight matrix", si);
+      const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.b->cols)));
+      if (st.claim == GKR_CLAIM_FRESH) {
+        point.resize(nv);
+        for (uint32_t l = 0; l < nv; l++) point[l] = G(ch->ch.draw_qm31());
+        TRY(gkr_matmul_output_claim(c, st.a, st.b, point.data(), nv, &value));
+        ch->ch.mix_secure_field(Q(value));
+      } else if (!have_claim) {
+        return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);
+      }
+      const int T = log2_exact(next_pow2(st.a->cols));
+      rp.resize(3 * (size_t)(T > 0 ? T : 1));
+      gkr_qm31 fa, fb, nval;
+      TRY(gkr_prove_matmul_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.b, ch, proof, rp.data(),
+                                 &fa, &fb, npnt.data(), &nval));
+      const uint32_t nn = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + T);
+      point.assign(npnt.begin(), npnt.begin() + nn);
+      value = nval;
+    } else if (st.kind == GKR_STEP_ACTIVATION) {
+      const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
+      if (st.claim == GKR_CLAIM_FRESH) {
+        point.resize(nv);
+        for (uint32_t l = 0; l < nv; l++) point[l] = G(ch->ch.draw_qm31());
+        value = G(ch->ch.draw_qm31());
+      } else if (!have_claim) {
+        return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);
+      }
+      const uint32_t tl = st.table_log_size ? st.table_log_size : act_default_log_size(st.activation_type);
+      if (tl == 0 || tl > 24) return fail(GKR_ERR_INVALID, "step %zu: bad table size", si);
+      rp.resize(4 * (size_t)(nv ? nv : 1));
+      mults.resize((size_t)1 << tl);
+      std::vector<gkr_qm31> mrp(2 * tl);
+      gkr_logup_out out;
+      memset(&out, 0, sizeof out);
+      out.eq_round_polys = rp.data();
+      out.multiplicities = mults.data();
+      out.mult_round_polys = mrp.data();
+      TRY(gkr_prove_activation_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.activation_type, tl,
+                                     ch, proof, &out));
+      value = out.input_eval;  // the claim point is unchanged (prover.rs:6581-6584)
+    } else {
+      return fail(GKR_ERR_INVALID, "step %zu: unknown kind %u", si, st.kind);
+    }
+    have_claim = true;
+  }
+  if (point.size() > 64) return fail(GKR_ERR_BUFFER, "final claim has %zu variables", point.size());
+  for (size_t l = 0; l < point.size(); l++) final_point[l] = point[l];
+  *n_final = (uint32_t)point.size();
+  *final_value = value;
+  return GKR_OK;
 }

@@ -13,6 +13,7 @@
 namespace gkr {
 
 constexpr int kBlock = 256;       // threads per workgroup (4 wave64)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMaxVars = 32;      // largest MLE point handled in one call
 
 // A point (r_0, ..., r_{n-1}) passed by value in the kernel arguments,
@@ -76,35 +77,34 @@ __device__ __forceinline__ void block_sum_store(qm31 (&v)[NQ], qm31* __restrict_
   }
 }
 
-// Where a reducing kernel delivers its NQ QM31 results: every workgroup
-// stores its partial sums, bumps `counter`, and the last workgroup to arrive
-// adds all partials and writes them to `out` (coherent pinned host memory),
-// then publishes `seq` in `flag` so the host can stop waiting without a
-// stream synchronisation.  The last workgroup resets `counter` to zero.
+// Result delivery.  A reducing kernel stores one partial row of NQ QM31 per
+// workgroup; k_finish (one workgroup, launched right after it) adds the rows
+// and writes the NQ results to `out` in coherent pinned host memory, then
+// publishes `seq` in `flag`.  The host waits on the flag instead of a stream
+// synchronisation.  Kernel boundaries order the partials, so no device-scope
+// fences or atomics are needed.
 struct RoundSink {
   qm31* partials;          // device, NQ per workgroup
-  uint32_t* counter;       // device, zero between launches
   qm31* out;               // host-mapped
   uint32_t* flag;          // host-mapped
   uint32_t seq;
 };
 
+__device__ __forceinline__ void publish_flag(uint32_t* flag, uint32_t seq) {
+  __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 template <int NQ>
 __device__ __forceinline__ void sink_finish(qm31 (&v)[NQ], const RoundSink& sk) {
-  __shared__ bool last;
   block_sum_store<NQ>(v, sk.partials + (uint64_t)NQ * blockIdx.x);
-  if (threadIdx.x == 0) {
-    __threadfence();  // release this workgroup's partials (device scope)
-    const uint32_t prev = atomicAdd(sk.counter, 1u);
-    last = (prev == gridDim.x - 1);
-  }
-  __syncthreads();
-  if (!last) return;
-  __threadfence();  // acquire the other workgroups' partials
+}
+
+template <int NQ>
+__global__ void __launch_bounds__(kBlock) k_finish(RoundSink sk, uint32_t nblocks) {
   qacc acc[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; q++) acc[q].zero();
-  for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x)
+  for (uint32_t b = threadIdx.x; b < nblocks; b += blockDim.x)
 #pragma unroll
     for (int q = 0; q < NQ; q++) acc[q].add(ld_q(sk.partials, (uint64_t)NQ * b + q));
   qm31 tot[NQ];
@@ -116,18 +116,211 @@ __device__ __forceinline__ void sink_finish(qm31 (&v)[NQ], const RoundSink& sk) 
   if (threadIdx.x == 0) {
 #pragma unroll
     for (int q = 0; q < NQ; q++) sk.out[q] = res[q];
-    *sk.counter = 0;
-    __threadfence_system();  // results visible to the host before the flag
-    __atomic_store_n(sk.flag, sk.seq, __ATOMIC_RELEASE);
+    publish_flag(sk.flag, sk.seq);
   }
 }
-// Single-thread delivery of NQ values computed by one lane.
-template <int NQ>
-__device__ __forceinline__ void sink_single(const qm31 (&v)[NQ], const RoundSink& sk) {
-#pragma unroll
-  for (int q = 0; q < NQ; q++) sk.out[q] = v[q];
-  __threadfence_system();
-  __atomic_store_n(sk.flag, sk.seq, __ATOMIC_RELEASE);
+// ------------------------------------------------------------------ persistent tail
+// The last rounds of a sumcheck (vectors of at most kTailMax elements) run in
+// one long-lived workgroup that keeps the vectors in LDS.  Before each fold it
+// waits for the host to post the challenge in the coherent mailbox
+// (sequence number, then alpha); after each evaluation it delivers the round
+// sums like k_finish.  The wait is bounded: after kTailSpinLimit polls
+// without the expected sequence number the kernel publishes kTailTimeout in
+// the result flag and returns, so every wave always exits.
+constexpr int kTailMax = 1024;
+constexpr uint64_t kTailSpinLimit = 1ull << 22;
+constexpr uint32_t kTailTimeout = 0xFFFFFFFFu;
+constexpr uint32_t kTailCancel = 0xFFFFFFFEu;
+
+struct Mailbox {
+  uint32_t seq;
+  uint32_t pad[3];
+  qm31 alpha;
+};
+
+// Thread 0 polls for `want`; the challenge is broadcast through LDS.
+// Returns false (after publishing the timeout code) when the host never posts it.
+__device__ __forceinline__ bool tail_wait(Mailbox* mb, uint32_t want, qm31* sh_alpha, bool* sh_ok, uint32_t* res_flag) {
+  if (threadIdx.x == 0) {
+    bool ok = false;
+    for (uint64_t spins = 0; spins < kTailSpinLimit; spins++) {
+      const uint32_t got = __hip_atomic_load(&mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+      if (got == want) {
+        ok = true;
+        break;
+      }
+      if (got == kTailCancel) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (ok) {  // one 128-bit read of the challenge, ordered after the acquiring read of seq
+      const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&mb->alpha));
+      *sh_alpha = qm31{a[0], a[1], a[2], a[3]};
+    } else {
+      publish_flag(res_flag, kTailTimeout);
+    }
+    *sh_ok = ok;
+  }
+  __syncthreads();
+  return *sh_ok;
+}
+
+// Tail of the product sumcheck (k_mm_round semantics) for rounds
+// round0 .. round0 + n_rounds - 1, then the final fold.  On entry the
+// vectors have length len_in; when fold_first is set they are folded by the
+// challenge of the previous round before the first evaluation.  Result i
+// (round sums, then {final_a, final_b}) is published with seq res_base + i;
+// the challenge folded before result i carries mailbox seq mb_base + i.
+__global__ void __launch_bounds__(kBlock) k_mm_tail(const qm31* __restrict__ a_in, const qm31* __restrict__ b_in,
+                                                    uint32_t len_in, int fold_first, int n_rounds, Mailbox* mb,
+                                                    uint32_t mb_base, qm31* out, uint32_t* flag,
+                                                    uint32_t res_base) {
+  __shared__ qm31 va[2 * kTailMax], vb[2 * kTailMax];
+  __shared__ qm31 sh_alpha;
+  __shared__ bool sh_ok;
+  __shared__ qm31 res[3];
+  for (uint32_t i = threadIdx.x; i < len_in; i += blockDim.x) {
+    va[i] = ld_q(a_in, i);
+    vb[i] = ld_q(b_in, i);
+  }
+  __syncthreads();
+  uint32_t len = len_in;
+  for (int r = 0; r <= n_rounds; r++) {
+    if (r > 0 || fold_first) {
+      if (!tail_wait(mb, mb_base + r, &sh_alpha, &sh_ok, flag)) return;
+      const qm31 al = sh_alpha;
+      const uint32_t h = len / 2;
+      for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) {
+        va[i] = qm31_fold(va[i], va[i + h], al);
+        vb[i] = qm31_fold(vb[i], vb[i + h], al);
+      }
+      len = h;
+      __syncthreads();
+    }
+    if (r == n_rounds) break;
+    const uint32_t half = len / 2;
+    qacc s0, s1, s2;
+    s0.zero(); s1.zero(); s2.zero();
+    for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
+      const qm31 a0 = va[i], a1 = va[i + half], b0 = vb[i], b1 = vb[i + half];
+      s0.add(qm31_mul(a0, b0));
+      s1.add(qm31_mul(a1, b1));
+      s2.add(qm31_mul(qm31_sub(qm31_add(a1, a1), a0), qm31_sub(qm31_add(b1, b1), b0)));
+    }
+    qm31 v[3] = {s0.reduce(), s1.reduce(), s2.reduce()};
+    block_sum_store<3>(v, res);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      out[0] = res[0]; out[1] = res[1]; out[2] = res[2];
+      publish_flag(flag, res_base + r);
+    }
+  }
+  if (threadIdx.x == 0) {  // len == 1 after the final fold
+    out[0] = va[0];
+    out[1] = vb[0];
+    publish_flag(flag, res_base + n_rounds);
+  }
+}
+
+// Tail of the degree-3 eq-sumcheck over (eq, w, d): same protocol, 4 sums per
+// round, final result {eq, w, d} folded to one value each.
+__global__ void __launch_bounds__(kBlock) k_eq3_tail(const qm31* __restrict__ e_in, const qm31* __restrict__ w_in,
+                                                     const qm31* __restrict__ d_in, uint32_t len_in, int fold_first,
+                                                     int n_rounds, Mailbox* mb, uint32_t mb_base, qm31* out,
+                                                     uint32_t* flag, uint32_t res_base) {
+  constexpr int kMax = kTailMax / 2;
+  __shared__ qm31 ve[2 * kMax], vw[2 * kMax], vd[2 * kMax];
+  __shared__ qm31 sh_alpha;
+  __shared__ bool sh_ok;
+  __shared__ qm31 res[4];
+  for (uint32_t i = threadIdx.x; i < len_in; i += blockDim.x) {
+    ve[i] = ld_q(e_in, i);
+    vw[i] = ld_q(w_in, i);
+    vd[i] = ld_q(d_in, i);
+  }
+  __syncthreads();
+  uint32_t len = len_in;
+  for (int r = 0; r <= n_rounds; r++) {
+    if (r > 0 || fold_first) {
+      if (!tail_wait(mb, mb_base + r, &sh_alpha, &sh_ok, flag)) return;
+      const qm31 al = sh_alpha;
+      const uint32_t h = len / 2;
+      for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) {
+        ve[i] = qm31_fold(ve[i], ve[i + h], al);
+        vw[i] = qm31_fold(vw[i], vw[i + h], al);
+        vd[i] = qm31_fold(vd[i], vd[i + h], al);
+      }
+      len = h;
+      __syncthreads();
+    }
+    if (r == n_rounds) break;
+    const uint32_t half = len / 2;
+    qacc s0, s1, s2, s3;
+    s0.zero(); s1.zero(); s2.zero(); s3.zero();
+    for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
+      const qm31 e0 = ve[i], e1 = ve[i + half], w0 = vw[i], w1 = vw[i + half], d0 = vd[i], d1 = vd[i + half];
+      s0.add(qm31_mul(qm31_mul(e0, w0), d0));
+      s1.add(qm31_mul(qm31_mul(e1, w1), d1));
+      const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1, w0), dd = qm31_sub(d1, d0);
+      const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1, dw), d2 = qm31_add(d1, dd);
+      s2.add(qm31_mul(qm31_mul(e2, w2), d2));
+      s3.add(qm31_mul(qm31_mul(qm31_add(e2, de), qm31_add(w2, dw)), qm31_add(d2, dd)));
+    }
+    qm31 v[4] = {s0.reduce(), s1.reduce(), s2.reduce(), s3.reduce()};
+    block_sum_store<4>(v, res);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      out[0] = res[0]; out[1] = res[1]; out[2] = res[2]; out[3] = res[3];
+      publish_flag(flag, res_base + r);
+    }
+  }
+  if (threadIdx.x == 0) {
+    out[0] = ve[0];
+    out[1] = vw[0];
+    out[2] = vd[0];
+    publish_flag(flag, res_base + n_rounds);
+  }
+}
+
+// Tail of the degree-1 multiplicity sumcheck: sums of the low and high halves.
+__global__ void __launch_bounds__(kBlock) k_sum_tail(const qm31* __restrict__ v_in, uint32_t len_in, int fold_first,
+                                                     int n_rounds, Mailbox* mb, uint32_t mb_base, qm31* out,
+                                                     uint32_t* flag, uint32_t res_base) {
+  __shared__ qm31 vv[2 * kTailMax];
+  __shared__ qm31 sh_alpha;
+  __shared__ bool sh_ok;
+  __shared__ qm31 res[2];
+  for (uint32_t i = threadIdx.x; i < len_in; i += blockDim.x) vv[i] = ld_q(v_in, i);
+  __syncthreads();
+  uint32_t len = len_in;
+  for (int r = 0; r <= n_rounds; r++) {
+    if (r > 0 || fold_first) {
+      if (!tail_wait(mb, mb_base + r, &sh_alpha, &sh_ok, flag)) return;
+      const qm31 al = sh_alpha;
+      const uint32_t h = len / 2;
+      for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) vv[i] = qm31_fold(vv[i], vv[i + h], al);
+      len = h;
+      __syncthreads();
+    }
+    if (r == n_rounds) break;
+    const uint32_t half = len / 2;
+    qacc lo, hi;
+    lo.zero(); hi.zero();
+    for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
+      lo.add(vv[i]);
+      hi.add(vv[i + half]);
+    }
+    qm31 v[2] = {lo.reduce(), hi.reduce()};
+    block_sum_store<2>(v, res);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      out[0] = res[0]; out[1] = res[1];
+      publish_flag(flag, res_base + r);
+    }
+  }
+  if (threadIdx.x == 0) {
+    out[0] = vv[0];
+    publish_flag(flag, res_base + n_rounds);
+  }
 }
 
 // ------------------------------------------------------------------ eq / Lagrange
@@ -219,7 +412,6 @@ __global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint
 // rows.  B is streamed with non-temporal loads.  Each wave reduces its own
 // rows (no LDS, no barrier) and writes one canonical QM31 partial per row to
 // partial[(chunk * k + row) * 4 + component]; k_restrict_cols_finish adds the chunks.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kColRows = 4;
 constexpr int kColWaves = kBlock / 64;
 
@@ -396,13 +588,6 @@ __global__ void __launch_bounds__(kBlock) k_mm_round(const qm31* __restrict__ a_
   sink_finish<3>(v, sink);
 }
 
-// Fold both vectors of length 2 to a single value each: out = {fold(a), fold(b)}.
-__global__ void k_mm_final(const qm31* __restrict__ a, const qm31* __restrict__ b, qm31 alpha, RoundSink sink) {
-  if (threadIdx.x == 0) {
-    const qm31 v[2] = {qm31_fold(ld_q(a, 0), ld_q(a, 1), alpha), qm31_fold(ld_q(b, 0), ld_q(b, 1), alpha)};
-    sink_single<2>(v, sink);
-  }
-}
 
 // ------------------------------------------------------------------ LogUp
 // Pad the activation matrix to (prow x pcol), mask to the table range, look up
@@ -493,14 +678,6 @@ __global__ void __launch_bounds__(kBlock) k_eq3_round(const qm31* __restrict__ e
   qm31 v[4] = {s0.reduce(), s1.reduce(), s2.reduce(), s3.reduce()};
   sink_finish<4>(v, sink);
 }
-__global__ void k_eq3_final(const qm31* __restrict__ e, const qm31* __restrict__ w, const qm31* __restrict__ d,
-                            qm31 alpha, RoundSink sink) {
-  if (threadIdx.x == 0) {
-    const qm31 v[3] = {qm31_fold(ld_q(e, 0), ld_q(e, 1), alpha), qm31_fold(ld_q(w, 0), ld_q(w, 1), alpha),
-                       qm31_fold(ld_q(d, 0), ld_q(d, 1), alpha)};
-    sink_single<3>(v, sink);
-  }
-}
 
 // Degree-1 sumcheck round over one vector (multiplicities; prover.rs:9449-9511):
 // lo = sum_{i<half} v[i], hi = sum_{i<half} v[half+i], with the same fused fold.
@@ -524,12 +701,6 @@ __global__ void __launch_bounds__(kBlock) k_sum_round(const qm31* __restrict__ v
   }
   qm31 v[2] = {lo.reduce(), hi.reduce()};
   sink_finish<2>(v, sink);
-}
-__global__ void k_fold1_final(const qm31* __restrict__ v, qm31 alpha, RoundSink sink) {
-  if (threadIdx.x == 0) {
-    const qm31 r[1] = {qm31_fold(ld_q(v, 0), ld_q(v, 1), alpha)};
-    sink_single<1>(r, sink);
-  }
 }
 __global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __restrict__ out) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -51,6 +51,15 @@ class GkrLogupOut(C.Structure):
     ]
 
 
+class GkrStep(C.Structure):
+    _fields_ = [("kind", C.c_uint32), ("claim", C.c_uint32), ("a", C.c_void_p), ("b", C.c_void_p),
+                ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32)]
+
+
+STEP_MATMUL, STEP_ACTIVATION = 0, 3
+CLAIM_CHAINED, CLAIM_FRESH = 0, 1
+
+
 class GkrError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"gkr error {code}: {msg}")
@@ -117,6 +126,8 @@ SIGNATURES = [
                                              C.POINTER(GkrLogupOut)]),
     ("gkr_activation_table", C.c_int, [C.c_uint32, C.c_uint32, _U32P]),
     ("gkr_bench_copy", C.c_int, [_P, C.c_uint64, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    ("gkr_prove_walk", C.c_int, [_P, _P, C.POINTER(GkrStep), C.c_size_t, _PQ, C.c_uint32, _PQ, _P, _PQ,
+                                 C.POINTER(C.c_uint32), _PQ]),
 ]
 
 
@@ -407,6 +418,38 @@ class Context:
             "gamma": q_from_c(out.gamma),
             "beta": q_from_c(out.beta),
         }
+
+
+def make_steps(steps) -> "C.Array":
+    """steps: sequence of (kind, claim, a, b, activation_type, table_log_size) with Matrix objects."""
+    arr = (GkrStep * max(1, len(steps)))()
+    for i, (kind, claim, a, b, act, tlog) in enumerate(steps):
+        arr[i].kind, arr[i].claim = kind, claim
+        arr[i].a = a.handle if a is not None else None
+        arr[i].b = b.handle if b is not None else None
+        arr[i].activation_type, arr[i].table_log_size = act, tlog
+    return arr
+
+
+def prove_walk(ctx: "Context", ch: PoseidonChannel, steps, proof: "Proof", init_point=None, init_value=None,
+               n_steps=None):
+    """gkr_prove_walk: run the layer steps in order; returns the final (point, value) claim.
+
+    `steps` is a list of (kind, claim, a, b, activation_type, table_log_size) tuples or an array
+    from make_steps (then pass n_steps).
+    """
+    if isinstance(steps, (list, tuple)):
+        arr, n = make_steps(steps), len(steps)
+    else:
+        arr, n = steps, (n_steps if n_steps is not None else len(steps))
+    fp = (GkrQM31 * 64)()
+    nf = C.c_uint32()
+    fv = GkrQM31()
+    ip = q_array(init_point) if init_point is not None else None
+    iv = C.byref(q_to_c(init_value)) if init_value is not None else None
+    _check(lib().gkr_prove_walk(ctx.handle, ch.handle, arr, n, ip, len(init_point) if init_point else 0, iv,
+                                proof.handle if proof else None, fp, C.byref(nf), C.byref(fv)))
+    return [q_from_c(fp[i]) for i in range(nf.value)], q_from_c(fv)
 
 
 class Matrix:

@@ -232,6 +232,94 @@ def test_two_layer_walk_and_serialization(gpu_ctx):
     assert proof.serialize() == ref
 
 
+def test_native_walk_chained(gpu_ctx):
+    """gkr_prove_walk over MatMul -> SiLU(LogUp) -> MatMul with chained claims equals the oracle's
+    layer-by-layer walk (final claim, transcript and serialized proof)."""
+    log("case native walk chained")
+    X = O.synthetic(4, 64, 1, 31)
+    W1 = O.synthetic(64, 32, 1, 32)
+    H = O.matmul_forward(X, W1)
+    W2 = O.synthetic(32, 16, 1, 33)
+    gx, gw1, gh, gw2 = gpu_ctx.upload(X), gpu_ctx.upload(W1), gpu_ctx.upload(H), gpu_ctx.upload(W2)
+    och = O.Channel()
+    och.mix_u64(9)
+    r = och.draw_qm31s(lg(4) + lg(16))
+    v = O.matmul_output_claim(H, W2, r)
+    och.mix_secure_field(v)
+    gch = G.PoseidonChannel()
+    gch.mix_u64(9)
+    assert gch.draw_qm31s(lg(4) + lg(16)) == r
+    gch.mix_secure_field(v)
+    proof = G.Proof()
+    C_ = G.CLAIM_CHAINED
+    steps = [(G.STEP_MATMUL, C_, gh, gw2, 0, 0), (G.STEP_ACTIVATION, C_, gh, None, 5, 12),
+             (G.STEP_MATMUL, C_, gx, gw1, 0, 0)]
+    fp, fv = G.prove_walk(gpu_ctx, gch, steps, proof, init_point=r, init_value=v)
+    o1 = O.prove_matmul_layer(r, v, H, W2, och)
+    o2 = O.prove_activation_layer(o1["next_point"], o1["next_value"], H, 5, och, 12)
+    o3 = O.prove_matmul_layer(o1["next_point"], o2["input_eval"], X, W1, och)
+    assert (fp, fv) == (o3["next_point"], o3["next_value"])
+    assert gch.digest() == och.digest()
+    proof.set_input_claim(fp, fv)
+    ref = [3]
+    O.serialize_matmul_layer(ref, o1["round_polys"], o1["final_a_eval"], o1["final_b_eval"])
+    O.serialize_activation_layer(ref, 5, o2)
+    O.serialize_matmul_layer(ref, o3["round_polys"], o3["final_a_eval"], o3["final_b_eval"])
+    O.serialize_tail(ref, o3["next_point"], o3["next_value"], [], 0)
+    assert proof.serialize() == ref
+
+
+def test_native_walk_fresh_claims(gpu_ctx):
+    """gkr_prove_walk with fresh claims (draw point, claim, mix) equals the same sequence driven
+    call by call from the host and the oracle's transcript; ragged shapes, two activations."""
+    log("case native walk fresh")
+    A1, B1 = O.synthetic(3, 50, 1, 41), O.synthetic(50, 20, 1, 42)
+    A2, B2 = O.synthetic(5, 20, 1, 43), O.synthetic(20, 7, 1, 44)
+    S = O.synthetic(6, 40, 0, 45)
+    gs = [gpu_ctx.upload(M) for M in (A1, B1, A2, B2, S)]
+    F = G.CLAIM_FRESH
+    steps = [(G.STEP_MATMUL, F, gs[0], gs[1], 0, 0), (G.STEP_ACTIVATION, F, gs[4], None, 4, 10),
+             (G.STEP_MATMUL, F, gs[2], gs[3], 0, 0), (G.STEP_ACTIVATION, F, gs[4], None, 1, 0)]
+    gch = G.PoseidonChannel()
+    gch.mix_u64(77)
+    proof = G.Proof()
+    fp, fv = G.prove_walk(gpu_ctx, gch, steps, proof)
+    och = O.Channel()
+    och.mix_u64(77)
+    ref = [4]
+    for kind, _, a, b, act, tlog in [(0, 0, A1, B1, 0, 0), (3, 0, S, None, 4, 10), (0, 0, A2, B2, 0, 0),
+                                     (3, 0, S, None, 1, 0)]:
+        if kind == 0:
+            r = och.draw_qm31s(lg(a.shape[0]) + lg(b.shape[1]))
+            v = O.matmul_output_claim(a, b, r)
+            och.mix_secure_field(v)
+            o = O.prove_matmul_layer(r, v, a, b, och)
+            O.serialize_matmul_layer(ref, o["round_polys"], o["final_a_eval"], o["final_b_eval"])
+            last = (o["next_point"], o["next_value"])
+        else:
+            r = och.draw_qm31s(lg(a.shape[0]) + lg(a.shape[1]))
+            v = och.draw_qm31()
+            o = O.prove_activation_layer(r, v, a, act, och, tlog or 16)
+            O.serialize_activation_layer(ref, act, o)
+            last = (r, o["input_eval"])
+    assert (fp, fv) == last
+    assert gch.digest() == och.digest()
+    proof.set_input_claim(fp, fv)
+    O.serialize_tail(ref, fp, fv, [], 0)
+    assert proof.serialize() == ref
+
+
+def test_native_walk_errors(gpu_ctx):
+    """A chained first step without an initial claim and an unknown step kind are rejected."""
+    log("case native walk errors")
+    a = gpu_ctx.upload(O.synthetic(2, 4, 1, 1))
+    b = gpu_ctx.upload(O.synthetic(4, 2, 1, 2))
+    with pytest.raises(G.GkrError, match="no previous claim"):
+        G.prove_walk(gpu_ctx, G.PoseidonChannel(), [(G.STEP_MATMUL, G.CLAIM_CHAINED, a, b, 0, 0)], G.Proof())
+    with pytest.raises(G.GkrError, match="unknown kind"):
+        G.prove_walk(gpu_ctx, G.PoseidonChannel(), [(7, G.CLAIM_FRESH, a, b, 0, 0)], G.Proof())
+
+
 def test_qwen_up_projection_properties(gpu_ctx):
     """Qwen2.5-14B MLP up projection (64 x 5120 . 5120 x 13824, int8-range): verifier replay and
     final evaluations equal MLE_A / MLE_B^T at the challenge point (oracle on the CPU)."""
