@@ -200,6 +200,34 @@ int gkr_prove_activation_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32
                                const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t activation_type,
                                uint32_t table_log_size, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out);
 
+/* Mul layer (element-wise product c = lhs * rhs), reduce_mul_layer
+ * (engine/src/gkr/prover.rs:6172-6271): mix_u64(0x4D554C), mix the claim
+ * value, a degree-3 eq-sumcheck over eq(r[..n_vars], x) * lhs(x) * rhs(x)
+ * (4 coefficients per round, mix_poly_coeffs_deg3 + draw), mix lhs_eval and
+ * rhs_eval, draw alpha; the next claim is (claim_point, alpha * lhs + (1 -
+ * alpha) * rhs).  The claim point may be longer than n_vars; its first n_vars
+ * entries are used.  The caller provides eq_round_polys (4 * n_vars).  */
+typedef struct {
+  gkr_qm31* eq_round_polys;  /* in: caller buffer; out: c0..c3 per round */
+  gkr_qm31 lhs_eval, rhs_eval, alpha, next_value;
+  uint32_t n_vars;
+} gkr_mul_out;
+/* lhs/rhs: resident matrices, padded as pad_matrix_pow2 + matrix_to_mle
+ * (get_binary_op_intermediates, prover.rs:9563-9595); their padded lengths
+ * must agree.  Appends LayerProof::Mul to `proof` when it is non-null. */
+int gkr_prove_mul_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                        const gkr_matrix* lhs, const gkr_matrix* rhs, gkr_channel* ch, gkr_proof* proof,
+                        gkr_mul_out* out);
+/* The reference signature: lhs_vals / rhs_vals are host QM31 slices of length n
+ * (a power of two). */
+int gkr_reduce_mul_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                         const gkr_qm31* lhs_vals, const gkr_qm31* rhs_vals, uint64_t n, gkr_channel* ch,
+                         gkr_proof* proof, gkr_mul_out* out);
+/* MLE of the padded element-wise product at `point` (n_point = log2 of the
+ * padded length): the Mul layer's output claim value (cf. prover.rs:1543-1560). */
+int gkr_mul_output_claim(gkr_ctx* ctx, const gkr_matrix* lhs, const gkr_matrix* rhs, const gkr_qm31* point,
+                         uint32_t n_point, gkr_qm31* out);
+
 /* GKR walk over a sequence of layers (the layer loop of prove_gkr_with_cache,
  * gkr/prover.rs:1500-1660, for MatMul and Activation layers).  Steps run in
  * order on one channel and append their LayerProof to `proof`.  Each step's
@@ -208,15 +236,16 @@ int gkr_prove_activation_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32
  * a MatMul draws r_out = draw_qm31s(log2 pm + log2 pn), takes value =
  * MLE of A*B at r_out and mixes it (prover.rs:1543-1560); an Activation
  * draws its point (log2 of the padded size) and then its value with
- * draw_qm31.  On return final_point/final_value hold the last input claim
+ * draw_qm31; a Mul draws its point (log2 of the padded size), takes the
+ * product MLE there and mixes it.  On return final_point/final_value hold the last input claim
  * (final_point needs room for 64 entries).                                  */
-enum { GKR_STEP_MATMUL = 0, GKR_STEP_ACTIVATION = 3 };
+enum { GKR_STEP_MATMUL = 0, GKR_STEP_MUL = 2, GKR_STEP_ACTIVATION = 3 };
 enum { GKR_CLAIM_CHAINED = 0, GKR_CLAIM_FRESH = 1 };
 typedef struct {
   uint32_t kind;             /* GKR_STEP_MATMUL / GKR_STEP_ACTIVATION */
   uint32_t claim;            /* GKR_CLAIM_CHAINED / GKR_CLAIM_FRESH */
-  const gkr_matrix* a;       /* MatMul: A (m x k); Activation: the input matrix */
-  const gkr_matrix* b;       /* MatMul: B (k x n); Activation: unused */
+  const gkr_matrix* a;       /* MatMul: A (m x k); Mul: lhs; Activation: the input matrix */
+  const gkr_matrix* b;       /* MatMul: B (k x n); Mul: rhs; Activation: unused */
   uint32_t activation_type;  /* Activation: reference type tag */
   uint32_t table_log_size;   /* Activation: 0 = reference default */
 } gkr_step;

@@ -86,6 +86,15 @@ int orc_prove_activation_layer(const uint32_t* claim_point, int n_point, const u
                                uint32_t* input_eval, uint32_t* table_commitment);
 
 /* ---------------------------------------------------------- verifier (verify.c) */
+/* Mul layer (mul.c): lhs/rhs n QM31 each; eq_round_polys 4*log2(n) QM31. */
+int orc_reduce_mul_layer(const uint32_t* claim_point, int n_point, const uint32_t* claim_value,
+                         const uint32_t* lhs, const uint32_t* rhs, size_t n, orc_channel* ch,
+                         uint32_t* eq_round_polys, uint32_t* lhs_eval, uint32_t* rhs_eval, uint32_t* alpha_out,
+                         uint32_t* next_value);
+/* verify_mul_reduction (verify.c); c0c2c3: 3 QM31 per round; writes the next claim value. */
+int orc_verify_mul_layer(const uint32_t* claim_point, int n_point, const uint32_t* claim_value,
+                         const uint32_t* c0c2c3, int n_rounds, const uint32_t* lhs_eval, const uint32_t* rhs_eval,
+                         orc_channel* ch, uint32_t* next_value);
 int orc_verify_matmul_layer(const uint32_t* claim_point, int n_point, const uint32_t* claim_value, size_t m,
                             size_t k, size_t n, const uint32_t* c0c2 /* 8 words per round */, int n_rounds,
                             const uint32_t* final_a, const uint32_t* final_b, orc_channel* ch,

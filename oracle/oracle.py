@@ -55,6 +55,8 @@ def lib():
                                               C.c_int, _U32P, _U32P, C.c_void_p, _U32P, _U32P]
         L.orc_verify_activation_layer.argtypes = [_U32P, C.c_int, _U32P, C.c_uint32, C.c_uint32, _U32P, _U32P,
                                                   C.c_int] + [_U32P] * 6 + [C.c_void_p]
+        L.orc_reduce_mul_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, _U32P, C.c_size_t, C.c_void_p] + [_U32P] * 5
+        L.orc_verify_mul_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, C.c_int, _U32P, _U32P, C.c_void_p, _U32P]
         _lib = L
     return _lib
 
@@ -331,6 +333,54 @@ def verify_activation_layer(claim_point, claim_value, act_type: int, table_log: 
         ch.buf))
 
 
+def padded_mle(X: np.ndarray) -> np.ndarray:
+    """pad_matrix_pow2 + matrix_to_mle (components/matmul.rs:649-664, 174-187): (n, 4) QM31 array."""
+    r, c = X.shape
+    pr, pc = 1 << max(0, (r - 1).bit_length()), 1 << max(0, (c - 1).bit_length())
+    out = np.zeros((pr * pc, 4), dtype=np.uint32)
+    out.reshape(pr, pc, 4)[:r, :c, 0] = np.asarray(X, dtype=np.uint64) % P
+    return out
+
+
+def reduce_mul_layer(claim_point, claim_value, lhs: np.ndarray, rhs: np.ndarray, ch: Channel):
+    """reduce_mul_layer (engine/src/gkr/prover.rs:6172-6271) over QM31 MLEs given as (n, 4) arrays."""
+    lhs = np.ascontiguousarray(lhs, dtype=np.uint32).reshape(-1, 4)
+    rhs = np.ascontiguousarray(rhs, dtype=np.uint32).reshape(-1, 4)
+    n = lhs.shape[0]
+    if rhs.shape[0] != n:
+        raise ValueError("lhs and rhs must have the same length")
+    nv = max(0, (n - 1).bit_length())
+    rp = np.zeros((max(1, 4 * nv), 4), dtype=np.uint32)
+    le, re_, al, nx = (np.zeros(4, dtype=np.uint32) for _ in range(4))
+    rc = lib().orc_reduce_mul_layer(_p(_qa(claim_point)), len(claim_point), _p(_qa([claim_value])), _p(lhs),
+                                    _p(rhs), n, ch.buf, _p(rp), _p(le), _p(re_), _p(al), _p(nx))
+    if rc:
+        raise ValueError(f"oracle reduce_mul_layer failed ({rc})")
+    return {"eq_round_polys": [tuple(_q(rp, 4 * t + j) for j in range(4)) for t in range(nv)],
+            "lhs_eval": _q(le), "rhs_eval": _q(re_), "alpha": _q(al),
+            "next_point": [tuple(q) for q in claim_point], "next_value": _q(nx)}
+
+
+def mul_output_claim(lhs: np.ndarray, rhs: np.ndarray, point) -> tuple:
+    """MLE of the element-wise product of two padded M31 matrices at `point`."""
+    a, b = padded_mle(lhs), padded_mle(rhs)
+    prod = np.zeros_like(a)
+    prod[:, 0] = (a[:, 0].astype(np.uint64) * b[:, 0].astype(np.uint64)) % P
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_evaluate_mle(_p(prod), len(point), _p(_qa(point)), _p(out))
+    return _q(out)
+
+
+def verify_mul_layer(claim_point, claim_value, proof, ch: Channel):
+    """verify_mul_reduction (engine/src/gkr/verifier.rs:2963-3045); returns (status, next_value)."""
+    c = _qa([q for rp in proof["eq_round_polys"] for q in (rp[0], rp[2], rp[3])])
+    nx = np.zeros(4, dtype=np.uint32)
+    rc = lib().orc_verify_mul_layer(_p(_qa(claim_point)), len(claim_point), _p(_qa([claim_value])), _p(c),
+                                    len(proof["eq_round_polys"]), _p(_qa([proof["lhs_eval"]])),
+                                    _p(_qa([proof["rhs_eval"]])), ch.buf, _p(nx))
+    return int(rc), _q(nx)
+
+
 def activation(tag: int, v: int) -> int:
     return int(lib().orc_activation(tag, v))
 
@@ -389,6 +439,18 @@ def serialize_activation_layer(out: list, act_type: int, proof) -> None:
     _ser_q(out, proof["mult_claimed_sum"])
     out.append(0)  # no activation product proof
     out.append(0)  # no piecewise proof
+
+
+def serialize_mul_layer(out: list, proof) -> None:
+    """LayerProof::Mul (cairo_serde.rs:1339-1354): tag 2, rounds, (c0, c2, c3) per round, lhs, rhs."""
+    out.append(2)
+    out.append(len(proof["eq_round_polys"]))
+    for rp in proof["eq_round_polys"]:
+        _ser_q(out, rp[0])
+        _ser_q(out, rp[2])
+        _ser_q(out, rp[3])
+    _ser_q(out, proof["lhs_eval"])
+    _ser_q(out, proof["rhs_eval"])
 
 
 def serialize_tail(out: list, input_point, input_value, weight_commitments, io_commitment,

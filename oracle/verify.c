@@ -135,3 +135,37 @@ int orc_verify_activation_layer(const uint32_t* claim_point, int n_point, const 
   orc_mix_secure_field(ch, claim_value);
   return 0;
 }
+
+/* verify_mul_reduction (verifier.rs:2963-3045): transcript replay, the final
+ * check sum == eq(r, s) * lhs * rhs, then the combiner draw. */
+int orc_verify_mul_layer(const uint32_t* claim_point, int n_point, const uint32_t* claim_value,
+                         const uint32_t* c0c2c3, int n_rounds, const uint32_t* lhs_eval, const uint32_t* rhs_eval,
+                         orc_channel* ch, uint32_t* next_value) {
+  if (n_point < n_rounds) return 1;
+  orc_mix_u64(ch, 0x4D554Cull);
+  orc_mix_secure_field(ch, claim_value);
+  qm sum = q_load(claim_value);
+  qm eq = q_one();
+  const qm* r = (const qm*)claim_point;
+  for (int t = 0; t < n_rounds; t++) {
+    qm c0 = q_load(c0c2c3 + 12 * t), c2 = q_load(c0c2c3 + 12 * t + 4), c3 = q_load(c0c2c3 + 12 * t + 8);
+    qm c1 = q_sub(q_sub(q_sub(q_sub(sum, c0), c0), c2), c3);
+    uint32_t cw[16];
+    q_store(cw, c0);
+    q_store(cw + 4, c1);
+    q_store(cw + 8, c2);
+    q_store(cw + 12, c3);
+    orc_mix_poly_coeffs_deg3(ch, cw);
+    qm s = draw_q(ch);
+    qm s2 = q_mul(s, s);
+    sum = q_add(q_add(c0, q_mul(c1, s)), q_add(q_mul(c2, s2), q_mul(c3, q_mul(s2, s))));
+    eq = q_mul(eq, q_add(q_mul(q_sub(q_one(), r[t]), q_sub(q_one(), s)), q_mul(r[t], s)));
+  }
+  qm le = q_load(lhs_eval), re = q_load(rhs_eval);
+  if (!q_eq(sum, q_mul(q_mul(eq, le), re))) return 2;
+  mix_q(ch, le);
+  mix_q(ch, re);
+  qm alpha = draw_q(ch);
+  q_store(next_value, q_add(q_mul(alpha, le), q_mul(q_sub(q_one(), alpha), re)));
+  return 0;
+}

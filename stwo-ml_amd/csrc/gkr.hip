@@ -902,9 +902,9 @@ extern "C" int gkr_matmul_output_claim(gkr_ctx* c, const gkr_matrix* a, const gk
 
 // ------------------------------------------------------------------ proof container
 struct LayerRec {
-  uint32_t tag;  // 0 MatMul, 3 Activation
-  std::vector<qm31> rp;  // MatMul: c0,c1,c2 per round; Activation: eq c0..c3 per round
-  qm31 final_a, final_b;
+  uint32_t tag;  // 0 MatMul, 2 Mul, 3 Activation
+  std::vector<qm31> rp;  // MatMul: c0,c1,c2 per round; Mul, Activation: eq c0..c3 per round
+  qm31 final_a, final_b;  // MatMul: final a/b evals; Mul: lhs/rhs evals
   uint32_t act_type = 0;
   qm31 input_eval, output_eval;
   felt table_commitment;
@@ -976,6 +976,18 @@ static void serialize_proof(const gkr_proof* p, Ser& s) {
       for (size_t r = 0; r < nr; r++) {  // c1 omitted (cairo_serde.rs:1327-1331)
         s.q(L.rp[3 * r]);
         s.q(L.rp[3 * r + 2]);
+      }
+      s.q(L.final_a);
+      s.q(L.final_b);
+    } else if (L.tag == 2) {
+      // LayerProof::Mul (cairo_serde.rs:1339-1354): c1 omitted
+      s.u(2);
+      const size_t nr = L.rp.size() / 4;
+      s.u(nr);
+      for (size_t r = 0; r < nr; r++) {
+        s.q(L.rp[4 * r]);
+        s.q(L.rp[4 * r + 2]);
+        s.q(L.rp[4 * r + 3]);
       }
       s.q(L.final_a);
       s.q(L.final_b);
@@ -1140,6 +1152,98 @@ static const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint3
   return it->second;
 }
 
+// Eq-weighted degree-3 sumcheck over n = 2^nv entries (the eq-sumcheck of
+// reduce_activation_layer, gkr/prover.rs:6501-6556, and of reduce_mul_layer,
+// 6197-6245): s_t = sum_i eq_t * w_t * d_t at t = 0..3, Newton differences to
+// (c0, c1, c2, c3), mix_poly_coeffs_deg3, draw, fold.  e0/w0/d0 hold the
+// inputs and are overwritten; e1/w1/d1 (n/2 + 1 entries) are the other half of
+// the ping-pong.  Writes 4 * nv round coefficients, nv challenges and the final
+// (eq, w, d) values.
+static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, int nv, qm31* e0, qm31* w0, qm31* d0, qm31* e1, qm31* w1,
+                        qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3]) {
+  const uint64_t n = 1ull << nv;
+  if (nv == 0) {
+    TRY(fetch_q(c, e0, 1, fin + 0));
+    TRY(fetch_q(c, w0, 1, fin + 1));
+    return fetch_q(c, d0, 1, fin + 2);
+  }
+  const qm31 inv2 = qm31_from_m31(1u << 30);
+  const qm31 inv6 = qm31_from_m31(m31_inv(6));
+  const qm31 two = qm31_from_m31(2), three = qm31_from_m31(3);
+  const qm31 *ce = e0, *cw = w0, *cd = d0;
+  qm31* be[2] = {e1, e0};
+  qm31* bw[2] = {w1, w0};
+  qm31* bd[2] = {d1, d0};
+  qm31 alpha = qm31_zero();
+  auto absorb3 = [&](int t, const qm31* s) {
+    const qm31 dd1 = qm31_sub(s[1], s[0]);
+    const qm31 dd2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
+    const qm31 dd3 = qm31_mul(qm31_sub(qm31_sub(s[3], s[0]), qm31_mul(three, qm31_sub(s[2], s[1]))), inv6);
+    const qm31 c0 = s[0];
+    const qm31 c1 = qm31_add(qm31_sub(dd1, dd2), qm31_mul(two, dd3));
+    const qm31 c2 = qm31_sub(dd2, qm31_mul(three, dd3));
+    const qm31 c3 = dd3;
+    rp_out[4 * t + 0] = G(c0);
+    rp_out[4 * t + 1] = G(c1);
+    rp_out[4 * t + 2] = G(c2);
+    rp_out[4 * t + 3] = G(c3);
+    HostTimer ht(c, K_HOST_FS);
+    C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
+    alpha = C.draw_qm31();
+    chal[t] = alpha;
+  };
+  // big rounds t < t0 as grid kernels, rounds t >= t0 (<= kTailMax/2
+  // elements per vector) and the final fold in k_eq3_tail
+  int t0 = 0;
+  while ((n >> t0) > (uint64_t)(kTailMax / 2)) t0++;
+  const int n_tail = nv - t0;
+  std::unique_ptr<TailSession> tail;
+  auto launch_tail = [&]() -> int {
+    const uint32_t len_in = (uint32_t)(t0 == 0 ? n : (n >> (t0 - 1)));
+    tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
+    hipLaunchKernelGGL(k_eq3_tail, dim3(1), dim3(kBlock), 0, c->stream, ce, cw, cd, len_in, t0 > 0 ? 1 : 0, n_tail,
+                       c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base);
+    return check_launch();
+  };
+  for (int t = 0; t < t0; t++) {
+    const uint64_t half = (n >> t) / 2;
+    qm31 sums[4];
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
+    {
+      // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}; round 0 reads only
+      TimedLaunch tl(c, K_EQ3_ROUND, t == 0 ? 96 * half : 288 * half);
+      if (t == 0) {
+        hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd,
+                           (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
+      } else {
+        qm31 *ne = be[(t - 1) & 1], *nw = bw[(t - 1) & 1], *nd = bd[(t - 1) & 1];
+        hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw, nd,
+                           half, 1, alpha, sk);
+        ce = ne; cw = nw; cd = nd;
+      }
+    }
+    TRY(launch_finish<4>(c, sk, partial_grid(half)));
+    if (t == t0 - 1) TRY(launch_tail());
+    TRY(wait_sink<4>(c, sk, sums));
+    absorb3(t, sums);
+  }
+  if (t0 == 0) {
+    TRY(launch_tail());
+  } else {
+    tail->post(0, alpha);
+  }
+  for (int r = 0; r < n_tail; r++) {
+    qm31 sums[4];
+    TRY(wait_result<4>(c, tail->res_base + r, sums));
+    absorb3(t0 + r, sums);
+    tail->post(r + 1, alpha);
+  }
+  TRY(wait_result<3>(c, tail->res_base + n_tail, fin));
+  tail->done = true;
+  return GKR_OK;
+}
+
 extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
                                           const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t tag,
                                           uint32_t table_log, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out) {
@@ -1232,86 +1336,9 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
 
   // eq-sumcheck: sum eq(r, x) w(x) d(x) = 1 over the hypercube
   TRY(eq_table(c, cpt.data(), nv, n, d_e0));
-  const qm31 inv2 = qm31_from_m31(1u << 30);
-  const qm31 inv6 = qm31_from_m31(m31_inv(6));
-  const qm31 two = qm31_from_m31(2), three = qm31_from_m31(3);
   std::vector<qm31> chal(nv);
-  const qm31 *ce = d_e0, *cw = d_w0, *cd = d_d0;
-  qm31* be[2] = {d_e1, d_e0};
-  qm31* bw[2] = {d_w1, d_w0};
-  qm31* bd[2] = {d_d1, d_d0};
-  qm31 alpha = qm31_zero();
-  auto absorb3 = [&](int t, const qm31* s) {
-    const qm31 dd1 = qm31_sub(s[1], s[0]);
-    const qm31 dd2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
-    const qm31 dd3 = qm31_mul(qm31_sub(qm31_sub(s[3], s[0]), qm31_mul(three, qm31_sub(s[2], s[1]))), inv6);
-    const qm31 c0 = s[0];
-    const qm31 c1 = qm31_add(qm31_sub(dd1, dd2), qm31_mul(two, dd3));
-    const qm31 c2 = qm31_sub(dd2, qm31_mul(three, dd3));
-    const qm31 c3 = dd3;
-    out->eq_round_polys[4 * t + 0] = G(c0);
-    out->eq_round_polys[4 * t + 1] = G(c1);
-    out->eq_round_polys[4 * t + 2] = G(c2);
-    out->eq_round_polys[4 * t + 3] = G(c3);
-    HostTimer ht(c, K_HOST_FS);
-    C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
-    alpha = C.draw_qm31();
-    chal[t] = alpha;
-  };
   qm31 fin[3];
-  if (nv > 0) {
-    // big rounds t < t0 as grid kernels, rounds t >= t0 (<= kTailMax/2
-    // elements per vector) and the final fold in k_eq3_tail
-    int t0 = 0;
-    while ((n >> t0) > (uint64_t)(kTailMax / 2)) t0++;
-    const int n_tail = nv - t0;
-    std::unique_ptr<TailSession> tail;
-    auto launch_tail = [&]() -> int {
-      const uint32_t len_in = (uint32_t)(t0 == 0 ? n : (n >> (t0 - 1)));
-      tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
-      hipLaunchKernelGGL(k_eq3_tail, dim3(1), dim3(kBlock), 0, c->stream, ce, cw, cd, len_in, t0 > 0 ? 1 : 0,
-                         n_tail, c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base);
-      return check_launch();
-    };
-    for (int t = 0; t < t0; t++) {
-      const uint64_t half = (n >> t) / 2;
-      qm31 sums[4];
-      RoundSink sk;
-      TRY(make_sink(c, &sk));
-      {
-        // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}; round 0 reads only
-        TimedLaunch tl(c, K_EQ3_ROUND, t == 0 ? 96 * half : 288 * half);
-        if (t == 0) {
-          hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd,
-                             (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
-        } else {
-          qm31 *ne = be[(t - 1) & 1], *nw = bw[(t - 1) & 1], *nd = bd[(t - 1) & 1];
-          hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw,
-                             nd, half, 1, alpha, sk);
-          ce = ne; cw = nw; cd = nd;
-        }
-      }
-      TRY(launch_finish<4>(c, sk, partial_grid(half)));
-      if (t == t0 - 1) TRY(launch_tail());
-      TRY(wait_sink<4>(c, sk, sums));
-      absorb3(t, sums);
-    }
-    if (t0 == 0) {
-      TRY(launch_tail());
-    } else {
-      tail->post(0, alpha);
-    }
-    for (int r = 0; r < n_tail; r++) {
-      qm31 sums[4];
-      TRY(wait_result<4>(c, tail->res_base + r, sums));
-      absorb3(t0 + r, sums);
-      tail->post(r + 1, alpha);
-    }
-    TRY(wait_result<3>(c, tail->res_base + n_tail, fin));
-    tail->done = true;
-  } else {
-    TRY(fetch_q(c, d_w0, 1, fin + 1));
-  }
+  TRY(eq3_sumcheck(c, C, nv, d_e0, d_w0, d_d0, d_e1, d_w1, d_d1, out->eq_round_polys, chal.data(), fin));
   const qm31 w_eval = fin[1];
   // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges
   qm31 in_eval, out_eval, input_eval;
@@ -1338,6 +1365,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(check_launch());
   const qm31* cm = m0;
   qm31* bm[2] = {m1, m0};
+  qm31 alpha = qm31_zero();
   auto absorb1 = [&](uint32_t t, const qm31* s) {
     const qm31 c0 = s[0];
     const qm31 c1 = qm31_sub(s[1], s[0]);
@@ -1469,6 +1497,163 @@ extern "C" int gkr_bench_copy(gkr_ctx* c, uint64_t bytes, int iters, double* cop
   return rc;
 }
 
+
+// ------------------------------------------------------------------ Mul layer
+// reduce_mul_layer (gkr/prover.rs:6172-6271) over the padded QM31 MLEs held in
+// S_W0 (lhs) and S_D0 (rhs), n = 2^nv entries each.
+static int mul_layer_core(gkr_ctx* c, const std::vector<qm31>& cpt, const qm31& claim, int nv, gkr_channel* ch,
+                          gkr_proof* proof, gkr_mul_out* out) {
+  const uint64_t n = 1ull << nv;
+  qm31 *d_e0, *d_e1, *d_w0, *d_w1, *d_d0, *d_d1;
+  TRY(ensureT(c, S_E0, n, &d_e0));
+  TRY(ensureT(c, S_E1, n / 2 + 1, &d_e1));
+  TRY(ensureT(c, S_W0, n, &d_w0));
+  TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
+  TRY(ensureT(c, S_D0, n, &d_d0));
+  TRY(ensureT(c, S_D1, n / 2 + 1, &d_d1));
+  PoseidonChannel& C = ch->ch;
+  TRY(eq_table(c, cpt.data(), nv, n, d_e0));  // eq over the first nv claim coordinates
+  C.mix_u64(0x4D554Cull);                      // "MUL"
+  C.mix_secure_field(claim);
+  std::vector<qm31> chal(nv);
+  qm31 fin[3];
+  TRY(eq3_sumcheck(c, C, nv, d_e0, d_w0, d_d0, d_e1, d_w1, d_d1, out->eq_round_polys, chal.data(), fin));
+  const qm31 lhs = fin[1], rhs = fin[2];
+  C.mix_secure_field(lhs);
+  C.mix_secure_field(rhs);
+  const qm31 alpha = C.draw_qm31();
+  const qm31 comb = qm31_add(qm31_mul(alpha, lhs), qm31_mul(qm31_sub(qm31_one(), alpha), rhs));
+  out->lhs_eval = G(lhs);
+  out->rhs_eval = G(rhs);
+  out->alpha = G(alpha);
+  out->next_value = G(comb);
+  out->n_vars = (uint32_t)nv;
+  if (proof) {
+    LayerRec L;
+    L.tag = 2;
+    L.rp.resize(4 * (size_t)nv);
+    for (size_t i = 0; i < L.rp.size(); i++) L.rp[i] = Q(out->eq_round_polys[i]);
+    L.final_a = lhs;
+    L.final_b = rhs;
+    proof->layers.push_back(std::move(L));
+  }
+  return GKR_OK;
+}
+static int mul_check_claim(const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value, int nv,
+                           gkr_mul_out* out, std::vector<qm31>* cpt) {
+  if (!claim_value || !out || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
+  if (nv > kMaxVars) return fail(GKR_ERR_INVALID, "mul layer too large");
+  if ((int)n_point < nv) return fail(GKR_ERR_INVALID, "claim point too short for MLE size (%u < %d)", n_point, nv);
+  if (!out->eq_round_polys && nv > 0) return fail(GKR_ERR_INVALID, "null eq_round_polys");
+  if (!canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
+  cpt->resize(n_point);
+  for (uint32_t l = 0; l < n_point; l++) {
+    if (!canonical_q(claim_point[l])) return fail(GKR_ERR_INVALID, "claim point not canonical");
+    (*cpt)[l] = Q(claim_point[l]);
+  }
+  return GKR_OK;
+}
+// Padded QM31 MLEs of two resident matrices into S_W0 / S_D0; returns nv.
+static int mul_stage_matrices(gkr_ctx* c, const gkr_matrix* lhs, const gkr_matrix* rhs, int* nv_out) {
+  if (!lhs || !rhs) return fail(GKR_ERR_INVALID, "null matrix");
+  if (lhs->ctx != c || rhs->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another context");
+  const uint64_t nl = next_pow2(lhs->rows) * next_pow2(lhs->cols);
+  const uint64_t nr = next_pow2(rhs->rows) * next_pow2(rhs->cols);
+  if (nl != nr) return fail(GKR_ERR_INVALID, "lhs and rhs must have same length (%llu vs %llu)",
+                            (unsigned long long)nl, (unsigned long long)nr);
+  const int nv = log2_exact(nl);
+  if (nv > kMaxVars) return fail(GKR_ERR_INVALID, "mul layer too large");
+  qm31 *d_w0, *d_d0;
+  TRY(ensureT(c, S_W0, nl, &d_w0));
+  TRY(ensureT(c, S_D0, nl, &d_d0));
+  hipLaunchKernelGGL(k_pad_q, dim3(grid_for(nl)), dim3(kBlock), 0, c->stream, lhs->dev, lhs->rows, lhs->cols,
+                     log2_exact(next_pow2(lhs->cols)), nl, d_w0);
+  TRY(check_launch());
+  hipLaunchKernelGGL(k_pad_q, dim3(grid_for(nl)), dim3(kBlock), 0, c->stream, rhs->dev, rhs->rows, rhs->cols,
+                     log2_exact(next_pow2(rhs->cols)), nl, d_d0);
+  TRY(check_launch());
+  *nv_out = nv;
+  return GKR_OK;
+}
+
+extern "C" int gkr_prove_mul_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
+                                   const gkr_qm31* claim_value, const gkr_matrix* lhs, const gkr_matrix* rhs,
+                                   gkr_channel* ch, gkr_proof* proof, gkr_mul_out* out) {
+  CH_CHECK(ch);
+  if (!c) return fail(GKR_ERR_INVALID, "null context");
+  HIP_TRY(hipSetDevice(c->device));
+  int nv = 0;
+  TRY(mul_stage_matrices(c, lhs, rhs, &nv));
+  std::vector<qm31> cpt;
+  TRY(mul_check_claim(claim_point, n_point, claim_value, nv, out, &cpt));
+  c->mm.valid = false;
+  return mul_layer_core(c, cpt, Q(*claim_value), nv, ch, proof, out);
+}
+
+extern "C" int gkr_reduce_mul_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
+                                    const gkr_qm31* claim_value, const gkr_qm31* lhs_vals, const gkr_qm31* rhs_vals,
+                                    uint64_t n, gkr_channel* ch, gkr_proof* proof, gkr_mul_out* out) {
+  CH_CHECK(ch);
+  if (!c || !lhs_vals || !rhs_vals) return fail(GKR_ERR_INVALID, "null argument");
+  if (n == 0 || (n & (n - 1))) return fail(GKR_ERR_INVALID, "MLE size must be power of 2 (got %llu)",
+                                          (unsigned long long)n);
+  const int nv = log2_exact(n);
+  std::vector<qm31> cpt;
+  TRY(mul_check_claim(claim_point, n_point, claim_value, nv, out, &cpt));
+  for (uint64_t i = 0; i < n; i++)
+    if (!canonical_q(lhs_vals[i]) || !canonical_q(rhs_vals[i]))
+      return fail(GKR_ERR_INVALID, "MLE value %llu not canonical", (unsigned long long)i);
+  HIP_TRY(hipSetDevice(c->device));
+  c->mm.valid = false;
+  qm31 *d_w0, *d_d0;
+  TRY(ensureT(c, S_W0, n, &d_w0));
+  TRY(ensureT(c, S_D0, n, &d_d0));
+  HIP_TRY(hipMemcpyAsync(d_w0, lhs_vals, n * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(hipMemcpyAsync(d_d0, rhs_vals, n * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
+  return mul_layer_core(c, cpt, Q(*claim_value), nv, ch, proof, out);
+}
+
+// MLE of lhs (.) rhs (padded) at `point`: sum_x eq(point, x) lhs(x) rhs(x),
+// as the sum s0 + s1 of an eq3 round-0 pass.
+extern "C" int gkr_mul_output_claim(gkr_ctx* c, const gkr_matrix* lhs, const gkr_matrix* rhs,
+                                    const gkr_qm31* point, uint32_t n_point, gkr_qm31* out) {
+  if (!c || !out || (!point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
+  HIP_TRY(hipSetDevice(c->device));
+  int nv = 0;
+  TRY(mul_stage_matrices(c, lhs, rhs, &nv));
+  if ((int)n_point != nv) return fail(GKR_ERR_INVALID, "point has %u vars, product MLE has %d", n_point, nv);
+  std::vector<qm31> pt(n_point);
+  for (uint32_t l = 0; l < n_point; l++) {
+    if (!canonical_q(point[l])) return fail(GKR_ERR_INVALID, "point not canonical");
+    pt[l] = Q(point[l]);
+  }
+  c->mm.valid = false;
+  const uint64_t n = 1ull << nv;
+  qm31 *d_e0, *d_w0, *d_d0;
+  TRY(ensureT(c, S_E0, n, &d_e0));
+  TRY(ensureT(c, S_W0, n, &d_w0));
+  TRY(ensureT(c, S_D0, n, &d_d0));
+  TRY(eq_table(c, pt.data(), nv, n, d_e0));
+  if (nv == 0) {
+    qm31 e, a, b;
+    TRY(fetch_q(c, d_e0, 1, &e));
+    TRY(fetch_q(c, d_w0, 1, &a));
+    TRY(fetch_q(c, d_d0, 1, &b));
+    *out = G(qm31_mul(qm31_mul(e, a), b));
+    return GKR_OK;
+  }
+  const uint64_t half = n / 2;
+  RoundSink sk;
+  TRY(make_sink(c, &sk));
+  hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, d_e0, d_w0, d_d0,
+                     (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
+  TRY(launch_finish<4>(c, sk, partial_grid(half)));
+  qm31 sums[4];
+  TRY(wait_sink<4>(c, sk, sums));
+  *out = G(qm31_add(sums[0], sums[1]));
+  return GKR_OK;
+}
+
 // ------------------------------------------------------------------ GKR walk
 extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps, size_t n_steps,
                               const gkr_qm31* init_point, uint32_t n_init, const gkr_qm31* init_value,
@@ -1503,6 +1688,23 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       const uint32_t nn = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + T);
       point.assign(npnt.begin(), npnt.begin() + nn);
       value = nval;
+    } else if (st.kind == GKR_STEP_MUL) {
+      if (!st.b) return fail(GKR_ERR_INVALID, "step %zu: null rhs matrix", si);
+      const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
+      if (st.claim == GKR_CLAIM_FRESH) {
+        point.resize(nv);
+        for (uint32_t l = 0; l < nv; l++) point[l] = G(ch->ch.draw_qm31());
+        TRY(gkr_mul_output_claim(c, st.a, st.b, point.data(), nv, &value));
+        ch->ch.mix_secure_field(Q(value));
+      } else if (!have_claim) {
+        return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);
+      }
+      rp.resize(4 * (size_t)(nv ? nv : 1));
+      gkr_mul_out mo;
+      memset(&mo, 0, sizeof mo);
+      mo.eq_round_polys = rp.data();
+      TRY(gkr_prove_mul_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.b, ch, proof, &mo));
+      value = mo.next_value;  // the claim point is unchanged (prover.rs:6260-6263)
     } else if (st.kind == GKR_STEP_ACTIVATION) {
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
       if (st.claim == GKR_CLAIM_FRESH) {

@@ -702,6 +702,15 @@ __global__ void __launch_bounds__(kBlock) k_sum_round(const qm31* __restrict__ v
   qm31 v[2] = {lo.reduce(), hi.reduce()};
   sink_finish<2>(v, sink);
 }
+// pad_matrix_pow2 + matrix_to_mle (components/matmul.rs:649-664, 174-187):
+// out[p] = X[r][c] lifted to QM31 for p = r * pcol + c inside the matrix, 0 outside.
+__global__ void k_pad_q(const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
+                        qm31* __restrict__ out) {
+  const uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  const uint64_t r = p >> log_pcol, c = p & ((1ull << log_pcol) - 1);
+  st_q(out, p, qm31_from_m31((r < rows && c < cols) ? m31_from_u32(X[r * cols + c]) : 0u));
+}
 __global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __restrict__ out) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) st_q(out, i, qm31_from_m31(m31_from_u32(in[i])));

@@ -32,6 +32,11 @@ class GkrFelt(C.Structure):
     _fields_ = [("w", C.c_uint32 * 8)]
 
 
+class GkrMulOut(C.Structure):
+    _fields_ = [("eq_round_polys", C.POINTER(GkrQM31)), ("lhs_eval", GkrQM31), ("rhs_eval", GkrQM31),
+                ("alpha", GkrQM31), ("next_value", GkrQM31), ("n_vars", C.c_uint32)]
+
+
 class GkrLogupOut(C.Structure):
     _fields_ = [
         ("claimed_sum", GkrQM31),
@@ -56,8 +61,12 @@ class GkrStep(C.Structure):
                 ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32)]
 
 
-STEP_MATMUL, STEP_ACTIVATION = 0, 3
+STEP_MATMUL, STEP_MUL, STEP_ACTIVATION = 0, 2, 3
 CLAIM_CHAINED, CLAIM_FRESH = 0, 1
+
+
+def _next_pow2(v: int) -> int:
+    return 1 << max(0, (v - 1).bit_length())
 
 
 class GkrError(RuntimeError):
@@ -126,6 +135,10 @@ SIGNATURES = [
                                              C.POINTER(GkrLogupOut)]),
     ("gkr_activation_table", C.c_int, [C.c_uint32, C.c_uint32, _U32P]),
     ("gkr_bench_copy", C.c_int, [_P, C.c_uint64, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    ("gkr_prove_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, C.POINTER(GkrMulOut)]),
+    ("gkr_reduce_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _PQ, _PQ, C.c_uint64, _P, _P,
+                                       C.POINTER(GkrMulOut)]),
+    ("gkr_mul_output_claim", C.c_int, [_P, _P, _P, _PQ, C.c_uint32, _PQ]),
     ("gkr_prove_walk", C.c_int, [_P, _P, C.POINTER(GkrStep), C.c_size_t, _PQ, C.c_uint32, _PQ, _P, _PQ,
                                  C.POINTER(C.c_uint32), _PQ]),
 ]
@@ -388,6 +401,46 @@ class Context:
         polys = [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2])) for t in range(T)]
         return {"round_polys": polys, "final_a_eval": q_from_c(fa), "final_b_eval": q_from_c(fb),
                 "next_point": [q_from_c(npnt[i]) for i in range(lm + T)], "next_value": q_from_c(nv)}
+
+    def _mul_result(self, out, eq, nv, claim_point):
+        return {"eq_round_polys": [tuple(q_from_c(eq[4 * t + j]) for j in range(4)) for t in range(nv)],
+                "lhs_eval": q_from_c(out.lhs_eval), "rhs_eval": q_from_c(out.rhs_eval),
+                "alpha": q_from_c(out.alpha), "next_point": [tuple(q) for q in claim_point],
+                "next_value": q_from_c(out.next_value)}
+
+    def prove_mul_layer(self, claim_point, claim_value, lhs: "Matrix", rhs: "Matrix", ch: PoseidonChannel,
+                        proof: Optional["Proof"] = None):
+        """gkr_prove_mul_layer: reduce_mul_layer over two resident matrices (padded to powers of two)."""
+        nv = max(0, (_next_pow2(lhs.rows) * _next_pow2(lhs.cols) - 1).bit_length())
+        eq = (GkrQM31 * max(1, 4 * nv))()
+        out = GkrMulOut()
+        out.eq_round_polys = C.cast(eq, _PQ)
+        _check(lib().gkr_prove_mul_layer(self._h, q_array(claim_point), len(claim_point),
+                                         C.byref(q_to_c(claim_value)), lhs.handle, rhs.handle, ch.handle,
+                                         proof.handle if proof else None, C.byref(out)))
+        return self._mul_result(out, eq, out.n_vars, claim_point)
+
+    def reduce_mul_layer(self, claim_point, claim_value, lhs_vals, rhs_vals, ch: PoseidonChannel,
+                         proof: Optional["Proof"] = None):
+        """gkr_reduce_mul_layer: the reference signature, QM31 slices from the host ((n, 4) arrays)."""
+        la = np.ascontiguousarray(lhs_vals, dtype=np.uint32).reshape(-1, 4)
+        lb = np.ascontiguousarray(rhs_vals, dtype=np.uint32).reshape(-1, 4)
+        n = la.shape[0]
+        nv = max(0, (n - 1).bit_length())
+        eq = (GkrQM31 * max(1, 4 * nv))()
+        out = GkrMulOut()
+        out.eq_round_polys = C.cast(eq, _PQ)
+        _check(lib().gkr_reduce_mul_layer(self._h, q_array(claim_point), len(claim_point),
+                                          C.byref(q_to_c(claim_value)), la.ctypes.data_as(_PQ),
+                                          lb.ctypes.data_as(_PQ), n, ch.handle, proof.handle if proof else None,
+                                          C.byref(out)))
+        return self._mul_result(out, eq, out.n_vars, claim_point)
+
+    def mul_output_claim(self, lhs: "Matrix", rhs: "Matrix", point) -> QM31:
+        out = GkrQM31()
+        _check(lib().gkr_mul_output_claim(self._h, lhs.handle, rhs.handle, q_array(point), len(point),
+                                          C.byref(out)))
+        return q_from_c(out)
 
     def prove_activation_layer(self, claim_point, claim_value, inp: "Matrix", act_type: int, ch: PoseidonChannel,
                                table_log_size: int = 0, proof: Optional["Proof"] = None):

@@ -197,3 +197,95 @@ def test_logup_identities_and_verifier(rows, cols, tag, tlog):
     ch3.draw_qm31s(nv)
     ch3.draw_qm31()
     assert O.verify_activation_layer(pt, val, tag, tlog, bad, ch3) != 0
+
+
+def _poly3(c, t):
+    """c0 + c1 t + c2 t^2 + c3 t^3 over QM31."""
+    t2 = Q.qmul(t, t)
+    return Q.qadd(Q.qadd(c[0], Q.qmul(c[1], t)), Q.qadd(Q.qmul(c[2], t2), Q.qmul(c[3], Q.qmul(t2, t))))
+
+
+def test_mul_layer_reference_case_and_bruteforce():
+    """The reference's own test case (prover.rs:10629-10680: a = [2..5], b = [1..4], mix_u64(77),
+    r = draw_qm31s(2)), checked against brute force: each round polynomial evaluated at 0..3 equals
+    the direct sum over the hypercube of eq_t * a_t * b_t; the final evals are MLE_a / MLE_b at the
+    replayed challenges; the combiner is drawn after mixing lhs, rhs; the verifier accepts."""
+    a = [(v, 0, 0, 0) for v in range(2, 6)]
+    b = [(v, 0, 0, 0) for v in range(1, 5)]
+    ch = O.Channel()
+    ch.mix_u64(77)
+    r = ch.draw_qm31s(2)
+    c = [Q.qmul(x, y) for x, y in zip(a, b)]
+    claim = Q.mle_bruteforce(c, r)
+    assert claim == O.evaluate_mle(c, r)
+    replay = ch.clone()
+    vch = ch.clone()
+    proof = O.reduce_mul_layer(r, claim, np.array(a, dtype=np.uint32), np.array(b, dtype=np.uint32), ch)
+    assert len(proof["eq_round_polys"]) == 2
+    # replay the transcript in Python: tag, claim, per-round deg-3 mix + draw
+    replay.mix_u64(0x4D554C)
+    replay.mix_secure_field(claim)
+    eqv = [Q.eq_weight(r, i, 2) for i in range(4)]
+    fa, fb = list(a), list(b)
+    s = []
+    cur = claim
+    for rp in proof["eq_round_polys"]:
+        mid = len(fa) // 2
+        for t in range(4):
+            tq = (t, 0, 0, 0)
+            omt = Q.qsub((1, 0, 0, 0), tq)
+            brute = (0, 0, 0, 0)
+            for i in range(mid):
+                lin = lambda v: Q.qadd(Q.qmul(omt, v[i]), Q.qmul(tq, v[mid + i]))  # noqa: E731
+                brute = Q.qadd(brute, Q.qmul(Q.qmul(lin(eqv), lin(fa)), lin(fb)))
+            assert _poly3(rp, tq) == brute
+        assert Q.qadd(_poly3(rp, (0, 0, 0, 0)), _poly3(rp, (1, 0, 0, 0))) == cur
+        replay.mix_poly_coeffs_deg3(*rp)
+        x = replay.draw_qm31()
+        s.append(x)
+        cur = _poly3(rp, x)
+        fold = lambda v: [Q.qadd(Q.qmul(Q.qsub((1, 0, 0, 0), x), v[i]), Q.qmul(x, v[mid + i]))  # noqa: E731
+                          for i in range(mid)]
+        eqv, fa, fb = fold(eqv), fold(fa), fold(fb)
+    assert proof["lhs_eval"] == Q.mle_bruteforce(a, s)
+    assert proof["rhs_eval"] == Q.mle_bruteforce(b, s)
+    eq_rs = (1, 0, 0, 0)
+    for ri, si in zip(r, s):
+        eq_rs = Q.qmul(eq_rs, Q.qadd(Q.qmul(Q.qsub((1, 0, 0, 0), ri), Q.qsub((1, 0, 0, 0), si)), Q.qmul(ri, si)))
+    assert cur == Q.qmul(Q.qmul(eq_rs, proof["lhs_eval"]), proof["rhs_eval"])
+    replay.mix_secure_field(proof["lhs_eval"])
+    replay.mix_secure_field(proof["rhs_eval"])
+    alpha = replay.draw_qm31()
+    assert proof["alpha"] == alpha
+    assert proof["next_value"] == Q.qadd(Q.qmul(alpha, proof["lhs_eval"]),
+                                         Q.qmul(Q.qsub((1, 0, 0, 0), alpha), proof["rhs_eval"]))
+    assert replay.digest() == ch.digest()
+    st, nxt = O.verify_mul_layer(r, claim, proof, vch)
+    assert st == 0 and nxt == proof["next_value"] and vch.digest() == ch.digest()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 5), (8, 8), (7, 33)])
+def test_mul_layer_matrices_verifier_and_tamper(rows, cols):
+    """Padded-matrix Mul layers (pad_matrix_pow2 + matrix_to_mle) of uniform M31 values: the
+    verifier accepts; a longer claim point uses its first log2(n) entries; tampered evals and
+    claims are rejected."""
+    rng = np.random.default_rng(rows * 131 + cols)
+    A = rng.integers(0, P, size=(rows, cols), dtype=np.uint32)
+    B = rng.integers(0, P, size=(rows, cols), dtype=np.uint32)
+    la, lb = O.padded_mle(A), O.padded_mle(B)
+    nv = la.shape[0].bit_length() - 1
+    ch = O.Channel()
+    ch.mix_u64(rows)
+    r = ch.draw_qm31s(nv + 2)  # two extra trailing coordinates, ignored by the eq table
+    claim = O.mul_output_claim(A, B, r[:nv])
+    vch, tch = ch.clone(), ch.clone()
+    proof = O.reduce_mul_layer(r, claim, la, lb, ch)
+    assert proof["next_point"] == [tuple(q) for q in r]
+    st, nxt = O.verify_mul_layer(r, claim, proof, vch)
+    assert st == 0 and nxt == proof["next_value"] and vch.digest() == ch.digest()
+    if nv > 0:
+        bad = dict(proof)
+        bad["lhs_eval"] = Q.qadd(proof["lhs_eval"], (1, 0, 0, 0))
+        assert O.verify_mul_layer(r, claim, bad, tch.clone())[0] != 0
+        bad_claim = Q.qadd(claim, (0, 0, 1, 0))
+        assert O.verify_mul_layer(r, bad_claim, proof, tch.clone())[0] != 0
