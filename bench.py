@@ -211,12 +211,77 @@ def cpu_baseline(budget_s=25.0):
                       f"{dt:.2f} s"}
 
 
+def bench_c2(ctx, args):
+    """Config 2: the product sumcheck alone over uniform QM31 vectors f_a, f_b of 2^L entries each
+    (channel new(), mix_u64(L); eval -> mix_poly_coeffs -> draw -> fold until size 1).  Algorithmic
+    bytes per sumcheck, as the fused kernels move them: round 0 reads 32 N; grid round t >= 1 reads
+    both vectors at n_(t-1) and writes them at n_t = n_(t-1)/2, 48 n_(t-1); the tail kernel reads
+    its 2 x 16 x n_(t0-1) input once and then works in LDS.  About 128 N in all."""
+    logs = [int(x) for x in args.c2_logs.split(",")]
+    sizes = []
+    for L in logs:
+        n = 1 << L
+        fa, fb = ctx.qvec_synthetic(n, 1000 + L), ctx.qvec_synthetic(n, 2000 + L)
+        ctx.synchronize()
+
+        def run():
+            ch = G.PoseidonChannel()
+            ch.mix_u64(L)
+            res = ctx.sumcheck_product(fa, fb, ch)
+            return ch.digest(), res["final_a_eval"]
+
+        for _ in range(args.warmup):
+            run()
+        ctx.set_timing(not args.no_timing)
+        ctx.reset_timing()
+        t0 = time.perf_counter()
+        outs = [run() for _ in range(args.steps)]
+        ctx.synchronize()
+        dt = (time.perf_counter() - t0) / args.steps
+        assert all(o == outs[0] for o in outs), "non-deterministic proof"
+        ms, nl, nb = ctx.kernel_time(K_MM_ROUND)
+        fs_ms, fs_n, _ = ctx.kernel_time(K_HOST_FS)
+        ctx.set_timing(False)
+        t0 = 0
+        while (n >> t0) > 1024:  # kTailMax: the last rounds run in one workgroup
+            t0 += 1
+        alg = 32 * n + sum(48 * (n >> (t - 1)) for t in range(1, t0)) + (32 * (n >> (t0 - 1)) if t0 else 0)
+        entry = {"log2_n": L, "ms_per_sumcheck": round(dt * 1e3, 3),
+                 "wall_gbps": round(alg / dt / 1e9, 1), "wall_frac": round(alg / dt / 1e9 / HBM_PEAK_GBS, 4),
+                 "qm31_evals_per_s_M": round(2 * (2 * n - 1) / dt / 1e6, 1), "digest": hex(outs[0][0])}
+        if nl:
+            entry["round_kernels"] = {"launches_per_sumcheck": nl // args.steps, "avg_us": round(ms / nl * 1e3, 3),
+                                      "gbps": round(nb / (ms * 1e-3) / 1e9, 1),
+                                      "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "ms_per_sumcheck": round(ms / args.steps, 3)}
+            entry["host_fs_ms_per_sumcheck"] = round(fs_ms / args.steps, 3)
+        sizes.append(entry)
+        log(f"[bench c2] 2^{L}: {entry}")
+        del fa, fb
+    big = sizes[-1]
+    rk = big.get("round_kernels")
+    result = {
+        "metric": METRIC, "value": big["qm31_evals_per_s_M"], "unit": "M QM31 evals/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": big["ms_per_sumcheck"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u32-m31",
+        "data": "synthetic (uniform QM31, SplitMix64)",
+        "config": {"workload": f"config2-product-sumcheck-2^{big['log2_n']}", "log2_sizes": logs},
+        "roofline": ({"bound": "hbm", "achieved": rk["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": rk["frac"], "traffic": None, "kernel": "k_mm_round"} if rk else None),
+        "sizes": sizes, "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1"])
+    ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1", "c2"])
+    ap.add_argument("--c2-logs", default="20,24,28",
+                    help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-timing", action="store_true", help="skip per-kernel HIP events")
     ap.add_argument("--driver", default="walk", choices=["walk", "calls"],
@@ -228,6 +293,8 @@ def main():
         sys.exit(2)
 
     ctx = G.Context(0)
+    if args.config == "c2":
+        return bench_c2(ctx, args)
     sbuf = SerialBuffer()
     if args.config == "cfg1":
         cfg, n_layers = None, 1

@@ -200,6 +200,24 @@ int gkr_prove_activation_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32
                                const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t activation_type,
                                uint32_t table_log_size, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out);
 
+/* Resident QM31 vectors (AoS, 16 B each) and the product sumcheck alone:
+ * the round loop of ZkmlOps::reduce_matmul_layer (engine/src/backend.rs:146-177;
+ * GPU twin gpu_sumcheck.rs:2820-2840) over given f_a, f_b of length 2^T:
+ * per round s0, s1, s2 -> (c0, c1, c2), mix_poly_coeffs, draw_qm31, fold.
+ * No separate reference entry point: this is the part of
+ * gkr_reduce_matmul_layer after the restriction, exported for callers that
+ * already hold the restricted MLEs.  The vectors are left unchanged.
+ * gkr_qvec_synthetic fills n uniform QM31 (four SplitMix64 M31 draws each,
+ * the generator of gkr_matrix_synthetic kind 0 at indices 4i..4i+3). */
+typedef struct gkr_qvec gkr_qvec;
+int gkr_qvec_upload(gkr_ctx* ctx, const gkr_qm31* host, uint64_t n, gkr_qvec** out);
+int gkr_qvec_synthetic(gkr_ctx* ctx, uint64_t n, uint64_t seed, gkr_qvec** out);
+int gkr_qvec_download(gkr_ctx* ctx, const gkr_qvec* v, gkr_qm31* host);
+void gkr_qvec_free(gkr_qvec* v);
+int gkr_sumcheck_product(gkr_ctx* ctx, const gkr_qvec* fa, const gkr_qvec* fb, gkr_channel* ch,
+                         gkr_qm31* round_polys /* 3T: c0, c1, c2 */, gkr_qm31* challenges /* T */,
+                         gkr_qm31* final_a, gkr_qm31* final_b);
+
 /* Mul layer (element-wise product c = lhs * rhs), reduce_mul_layer
  * (engine/src/gkr/prover.rs:6172-6271): mix_u64(0x4D554C), mix the claim
  * value, a degree-3 eq-sumcheck over eq(r[..n_vars], x) * lhs(x) * rhs(x)

@@ -145,25 +145,13 @@ void orc_matmul_output_claim(const uint32_t* A, size_t m, size_t k, const uint32
 }
 
 /* SimdBackend::reduce_matmul_layer (backend.rs:111-197) */
-int orc_reduce_matmul_layer(const uint32_t* A, size_t m, size_t k, const uint32_t* B, size_t n,
-                            const uint32_t* r_i, int n_ri, const uint32_t* r_j, int n_rj, size_t pk,
-                            orc_channel* ch, uint32_t* round_polys, uint32_t* challenges, uint32_t* final_a,
-                            uint32_t* final_b) {
-  size_t la, lb;
-  qm* a_mle = row_major_mle(A, m, k, &la);
-  qm* b_mle = col_major_mle(B, k, n, &lb);
-  qm* fa = restrict_mle(a_mle, la, (const qm*)r_i, n_ri);
-  qm* fb = restrict_mle(b_mle, lb, (const qm*)r_j, n_rj);
-  free(a_mle);
-  free(b_mle);
-  size_t cur = la >> n_ri; /* f_a length */
-  if ((lb >> n_rj) != cur) {
-    free(fa);
-    free(fb);
-    return 1;
-  }
+/* Round loop of SimdBackend::reduce_matmul_layer (backend.rs:146-177):
+ * s0 = sum a0 b0, s1 = sum a1 b1, s2 = sum (2a1 - a0)(2b1 - b0); c0 = s0,
+ * c2 = (s2 - 2 s1 + s0) / 2, c1 = s1 - s0 - c2; mix_poly_coeffs, draw, fold
+ * x + r (y - x).  fa/fb (length cur) are folded in place. */
+static void product_rounds(qm* fa, qm* fb, size_t cur, int log_k, orc_channel* ch, uint32_t* round_polys,
+                           uint32_t* challenges, uint32_t* final_a, uint32_t* final_b) {
   const qm inv2 = q_inv(q_from_m31(2));
-  const int log_k = ilog2(pk);
   for (int t = 0; t < log_k; t++) {
     size_t mid = cur / 2;
     qm s0 = q_zero(), s1 = q_zero(), s2 = q_zero();
@@ -193,6 +181,43 @@ int orc_reduce_matmul_layer(const uint32_t* A, size_t m, size_t k, const uint32_
   }
   q_store(final_a, cur ? fa[0] : q_zero());
   q_store(final_b, cur ? fb[0] : q_zero());
+}
+
+int orc_reduce_matmul_layer(const uint32_t* A, size_t m, size_t k, const uint32_t* B, size_t n,
+                            const uint32_t* r_i, int n_ri, const uint32_t* r_j, int n_rj, size_t pk,
+                            orc_channel* ch, uint32_t* round_polys, uint32_t* challenges, uint32_t* final_a,
+                            uint32_t* final_b) {
+  size_t la, lb;
+  qm* a_mle = row_major_mle(A, m, k, &la);
+  qm* b_mle = col_major_mle(B, k, n, &lb);
+  qm* fa = restrict_mle(a_mle, la, (const qm*)r_i, n_ri);
+  qm* fb = restrict_mle(b_mle, lb, (const qm*)r_j, n_rj);
+  free(a_mle);
+  free(b_mle);
+  size_t cur = la >> n_ri; /* f_a length */
+  if ((lb >> n_rj) != cur) {
+    free(fa);
+    free(fb);
+    return 1;
+  }
+  product_rounds(fa, fb, cur, ilog2(pk), ch, round_polys, challenges, final_a, final_b);
+  free(fa);
+  free(fb);
+  return 0;
+}
+
+/* The round loop alone over given QM31 vectors of length n (a power of two):
+ * config-2 style product sumcheck sum_x f_a(x) f_b(x). */
+int orc_sumcheck_product(const uint32_t* fa_in, const uint32_t* fb_in, size_t n, orc_channel* ch,
+                         uint32_t* round_polys, uint32_t* challenges, uint32_t* final_a, uint32_t* final_b) {
+  if (n == 0 || (n & (n - 1))) return 1;
+  qm* fa = (qm*)malloc(n * sizeof(qm));
+  qm* fb = (qm*)malloc(n * sizeof(qm));
+  for (size_t i = 0; i < n; i++) {
+    fa[i] = q_load(fa_in + 4 * i);
+    fb[i] = q_load(fb_in + 4 * i);
+  }
+  product_rounds(fa, fb, n, ilog2(n), ch, round_polys, challenges, final_a, final_b);
   free(fa);
   free(fb);
   return 0;

@@ -86,6 +86,9 @@ int orc_prove_activation_layer(const uint32_t* claim_point, int n_point, const u
                                uint32_t* input_eval, uint32_t* table_commitment);
 
 /* ---------------------------------------------------------- verifier (verify.c) */
+/* The product-sumcheck round loop over QM31 vectors of length n (matmul.c). */
+int orc_sumcheck_product(const uint32_t* fa, const uint32_t* fb, size_t n, orc_channel* ch, uint32_t* round_polys,
+                         uint32_t* challenges, uint32_t* final_a, uint32_t* final_b);
 /* Mul layer (mul.c): lhs/rhs n QM31 each; eq_round_polys 4*log2(n) QM31. */
 int orc_reduce_mul_layer(const uint32_t* claim_point, int n_point, const uint32_t* claim_value,
                          const uint32_t* lhs, const uint32_t* rhs, size_t n, orc_channel* ch,

@@ -55,6 +55,7 @@ def lib():
                                               C.c_int, _U32P, _U32P, C.c_void_p, _U32P, _U32P]
         L.orc_verify_activation_layer.argtypes = [_U32P, C.c_int, _U32P, C.c_uint32, C.c_uint32, _U32P, _U32P,
                                                   C.c_int] + [_U32P] * 6 + [C.c_void_p]
+        L.orc_sumcheck_product.argtypes = [_U32P, _U32P, C.c_size_t, C.c_void_p, _U32P, _U32P, _U32P, _U32P]
         L.orc_reduce_mul_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, _U32P, C.c_size_t, C.c_void_p] + [_U32P] * 5
         L.orc_verify_mul_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, C.c_int, _U32P, _U32P, C.c_void_p, _U32P]
         _lib = L
@@ -331,6 +332,28 @@ def verify_activation_layer(claim_point, claim_value, act_type: int, table_log: 
         _p(_qa([proof["claimed_sum"]])), _p(c), len(proof["eq_round_polys"]), _p(fe), _p(mults), _p(mrp),
         _p(_qa([proof["mult_final_eval"]])), _p(_qa([proof["mult_claimed_sum"]])), _p(_qa([proof["input_eval"]])),
         ch.buf))
+
+
+def synthetic_q(n: int, seed: int) -> np.ndarray:
+    """n uniform QM31 values, four consecutive kind-0 draws each: (n, 4) array."""
+    out = np.empty((n, 4), dtype=np.uint32)
+    lib().orc_synthetic_fill(_p(out), out.size, 0, seed)
+    return out
+
+
+def sumcheck_product(fa: np.ndarray, fb: np.ndarray, ch: Channel):
+    """The reduce_matmul_layer round loop (engine/src/backend.rs:146-177) over QM31 vectors."""
+    fa = np.ascontiguousarray(fa, dtype=np.uint32).reshape(-1, 4)
+    fb = np.ascontiguousarray(fb, dtype=np.uint32).reshape(-1, 4)
+    n = fa.shape[0]
+    T = max(0, (n - 1).bit_length())
+    rp = np.zeros((max(1, 3 * T), 4), dtype=np.uint32)
+    chal = np.zeros((max(1, T), 4), dtype=np.uint32)
+    a, b = np.zeros(4, dtype=np.uint32), np.zeros(4, dtype=np.uint32)
+    if lib().orc_sumcheck_product(_p(fa), _p(fb), n, ch.buf, _p(rp), _p(chal), _p(a), _p(b)):
+        raise ValueError("oracle sumcheck_product: length must be a power of two")
+    return {"round_polys": [(_q(rp, 3 * t), _q(rp, 3 * t + 1), _q(rp, 3 * t + 2)) for t in range(T)],
+            "challenges": [_q(chal, t) for t in range(T)], "final_a_eval": _q(a), "final_b_eval": _q(b)}
 
 
 def padded_mle(X: np.ndarray) -> np.ndarray:

@@ -113,6 +113,12 @@ struct gkr_matrix {
   bool owned;
 };
 
+struct gkr_qvec {
+  gkr_ctx* ctx;
+  qm31* dev;
+  uint64_t n;
+};
+
 struct gkr_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -131,6 +137,7 @@ struct gkr_ctx {
   MatMulCache mm;
   std::map<uint64_t, std::vector<uint32_t>> tables;  // (tag << 32 | log) -> table outputs
   std::set<gkr_matrix*> matrices;  // live matrices; detached when the context is destroyed
+  std::set<gkr_qvec*> qvecs;       // live QM31 vectors; detached likewise
   uint64_t table_on_device = 0;    // (tag << 32 | log) of the table held in S_TABLE, 0 = none
 };
 
@@ -536,6 +543,11 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
     m->dev = nullptr;
     m->ctx = nullptr;
   }
+  for (gkr_qvec* v : c->qvecs) {
+    if (v->dev) (void)hipFree(v->dev);
+    v->dev = nullptr;
+    v->ctx = nullptr;
+  }
   for (int s = 0; s < S_NSLOTS; s++)
     if (c->buf[s]) (void)hipFree(c->buf[s]);
   if (c->h_res) (void)hipHostFree(c->h_res);
@@ -747,40 +759,24 @@ static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* 
   return GKR_OK;
 }
 
-static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, uint32_t n_ri,
-                              const gkr_qm31* r_j, uint32_t n_rj, uint64_t pk, PoseidonChannel& ch,
-                              gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b) {
-  TRY(validate_matmul(c, a, b, n_ri, n_rj));
-  if (pk != next_pow2(a->cols))
-    return fail(GKR_ERR_INVALID, "pk=%llu but next_pow2(k)=%llu", (unsigned long long)pk,
-                (unsigned long long)next_pow2(a->cols));
-  HIP_TRY(hipSetDevice(c->device));
-  TRY(ensure_restricted(c, a, b, r_i, n_ri, r_j, n_rj));
-  const int T = log2_exact(pk);
-  qm31 *fa0, *fa1, *fb0, *fb1;
-  TRY(ensureT(c, S_FA0, pk, &fa0));
-  TRY(ensureT(c, S_FB0, pk, &fb0));
-  TRY(ensureT(c, S_FA1, pk / 2 + 1, &fa1));
-  TRY(ensureT(c, S_FB1, pk / 2 + 1, &fb1));
-  // The folds below overwrite the restricted vectors' successors only;
-  // S_FA0/S_FB0 keep round 0 input, so a cached restriction stays valid.
-  if (T == 0) {
-    qm31 v[1];
-    TRY(fetch_q(c, fa0, 1, v));
-    *final_a = G(v[0]);
-    TRY(fetch_q(c, fb0, 1, v));
-    *final_b = G(v[0]);
-    return GKR_OK;
-  }
+// Degree-2 product sumcheck sum_x f_a(x) f_b(x) over 2^T entries: the round
+// loop of reduce_matmul_layer (backend.rs:146-177; gpu_sumcheck.rs:2820-2840).
+// in_a/in_b are read by rounds 0 and 1; round t >= 1 folds into
+// bufs[(t - 1) & 1] (bufs[0] holds 2^(T-1) + 1 entries, bufs[1] 2^(T-2) + 1 and
+// may alias the inputs, which round 2 then overwrites: *invalidate_at_round2
+// is cleared at that point).  round0, when given, holds the round-0 sums
+// (s0, s1, s2) already computed for these inputs.
+static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, const qm31* in_b,
+                            qm31* const bufs_a[2], qm31* const bufs_b[2], const qm31* round0,
+                            bool* invalidate_at_round2, gkr_qm31* round_polys, gkr_qm31* challenges,
+                            gkr_qm31* final_a, gkr_qm31* final_b) {
   const qm31 inv2 = qm31_from_m31(1u << 30);  // 2^-1 mod P
-  const qm31* cur_a = fa0;
-  const qm31* cur_b = fb0;
+  const uint64_t pk = 1ull << T;
+  const qm31* cur_a = in_a;
+  const qm31* cur_b = in_b;
   // Big rounds t < t0 fold into ping-pong buffers (round t >= 1 writes
-  // bufs[(t-1)&1]; round 2 overwrites S_FA0/S_FB0, which ends the cached
-  // restriction).  Rounds t >= t0 (at most kTailMax elements) and the final
+  // bufs[(t-1)&1]).  Rounds t >= t0 (at most kTailMax elements) and the final
   // fold run in one persistent workgroup (k_mm_tail).
-  qm31* bufs_a[2] = {fa1, fa0};
-  qm31* bufs_b[2] = {fb1, fb0};
   int t0 = 0;
   while ((pk >> t0) > (uint64_t)kTailMax) t0++;
   const int n_tail = T - t0;
@@ -809,15 +805,15 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
     const uint64_t half = (pk >> t) / 2;
     qm31 sums[3];
     if (t == 0) {
-      if (c->mm.have_round0) {
-        sums[0] = c->mm.round0[0]; sums[1] = c->mm.round0[1]; sums[2] = c->mm.round0[2];
+      if (round0) {
+        sums[0] = round0[0]; sums[1] = round0[1]; sums[2] = round0[2];
         if (t0 == 1) TRY(launch_tail());
       } else {
         RoundSink sk;
         TRY(make_sink(c, &sk));
         {
           TimedLaunch tl(c, K_MM_ROUND, 32 * pk);
-          hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, fa0, fb0,
+          hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, in_a, in_b,
                              (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
         }
         TRY(launch_finish<3>(c, sk, partial_grid(half)));
@@ -827,7 +823,7 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
     } else {
       qm31* na = bufs_a[(t - 1) & 1];
       qm31* nb = bufs_b[(t - 1) & 1];
-      if (t == 2) c->mm.valid = false;
+      if (t == 2 && invalidate_at_round2) *invalidate_at_round2 = false;
       RoundSink sk;
       TRY(make_sink(c, &sk));
       {
@@ -861,6 +857,37 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
   *final_a = G(fin[0]);
   *final_b = G(fin[1]);
   return GKR_OK;
+}
+
+static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, uint32_t n_ri,
+                              const gkr_qm31* r_j, uint32_t n_rj, uint64_t pk, PoseidonChannel& ch,
+                              gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b) {
+  TRY(validate_matmul(c, a, b, n_ri, n_rj));
+  if (pk != next_pow2(a->cols))
+    return fail(GKR_ERR_INVALID, "pk=%llu but next_pow2(k)=%llu", (unsigned long long)pk,
+                (unsigned long long)next_pow2(a->cols));
+  HIP_TRY(hipSetDevice(c->device));
+  TRY(ensure_restricted(c, a, b, r_i, n_ri, r_j, n_rj));
+  const int T = log2_exact(pk);
+  qm31 *fa0, *fa1, *fb0, *fb1;
+  TRY(ensureT(c, S_FA0, pk, &fa0));
+  TRY(ensureT(c, S_FB0, pk, &fb0));
+  TRY(ensureT(c, S_FA1, pk / 2 + 1, &fa1));
+  TRY(ensureT(c, S_FB1, pk / 2 + 1, &fb1));
+  // The folds below overwrite the restricted vectors' successors only;
+  // S_FA0/S_FB0 keep round 0 input, so a cached restriction stays valid.
+  if (T == 0) {
+    qm31 v[1];
+    TRY(fetch_q(c, fa0, 1, v));
+    *final_a = G(v[0]);
+    TRY(fetch_q(c, fb0, 1, v));
+    *final_b = G(v[0]);
+    return GKR_OK;
+  }
+  qm31* bufs_a[2] = {fa1, fa0};
+  qm31* bufs_b[2] = {fb1, fb0};
+  return product_sumcheck(c, ch, T, fa0, fb0, bufs_a, bufs_b, c->mm.have_round0 ? c->mm.round0 : nullptr,
+                          &c->mm.valid, round_polys, challenges, final_a, final_b);
 }
 
 extern "C" int gkr_reduce_matmul_layer(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i,
@@ -1497,6 +1524,94 @@ extern "C" int gkr_bench_copy(gkr_ctx* c, uint64_t bytes, int iters, double* cop
   return rc;
 }
 
+
+
+// ------------------------------------------------------------------ QM31 vectors, product sumcheck
+extern "C" int gkr_qvec_upload(gkr_ctx* c, const gkr_qm31* host, uint64_t n, gkr_qvec** out) {
+  if (!c || !out || !host) return fail(GKR_ERR_INVALID, "null argument");
+  if (n == 0) return fail(GKR_ERR_INVALID, "empty vector");
+  for (uint64_t i = 0; i < n; i++)
+    if (!canonical_q(host[i])) return fail(GKR_ERR_INVALID, "vector value %llu not canonical", (unsigned long long)i);
+  HIP_TRY(hipSetDevice(c->device));
+  qm31* d = nullptr;
+  HIP_TRY(hipMalloc(&d, n * sizeof(qm31)));
+  hipError_t e = hipMemcpyAsync(d, host, n * sizeof(qm31), hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return fail(GKR_ERR_DEVICE, "vector upload: %s", hipGetErrorString(e));
+  }
+  *out = new gkr_qvec{c, d, n};
+  c->qvecs.insert(*out);
+  return GKR_OK;
+}
+extern "C" int gkr_qvec_synthetic(gkr_ctx* c, uint64_t n, uint64_t seed, gkr_qvec** out) {
+  if (!c || !out) return fail(GKR_ERR_INVALID, "null argument");
+  if (n == 0) return fail(GKR_ERR_INVALID, "empty vector");
+  HIP_TRY(hipSetDevice(c->device));
+  qm31* d = nullptr;
+  HIP_TRY(hipMalloc(&d, n * sizeof(qm31)));
+  hipLaunchKernelGGL(k_fill_synth_q, dim3(partial_grid(n) * 8), dim3(kBlock), 0, c->stream, d, n, seed);
+  int rc = check_launch();
+  if (rc == GKR_OK) rc = sync(c);
+  if (rc != GKR_OK) {
+    (void)hipFree(d);
+    return rc;
+  }
+  *out = new gkr_qvec{c, d, n};
+  c->qvecs.insert(*out);
+  return GKR_OK;
+}
+extern "C" int gkr_qvec_download(gkr_ctx* c, const gkr_qvec* v, gkr_qm31* host) {
+  if (!c || !v || !host) return fail(GKR_ERR_INVALID, "null argument");
+  if (v->ctx != c) return fail(GKR_ERR_INVALID, "vector belongs to another (or a destroyed) context");
+  HIP_TRY(hipMemcpyAsync(host, v->dev, v->n * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
+  return sync(c);
+}
+extern "C" void gkr_qvec_free(gkr_qvec* v) {
+  if (!v) return;
+  if (v->ctx) {
+    v->ctx->qvecs.erase(v);
+    if (v->dev) {
+      (void)hipStreamSynchronize(v->ctx->stream);
+      (void)hipFree(v->dev);
+    }
+  }
+  delete v;
+}
+extern "C" int gkr_sumcheck_product(gkr_ctx* c, const gkr_qvec* fa, const gkr_qvec* fb, gkr_channel* ch,
+                                    gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a,
+                                    gkr_qm31* final_b) {
+  CH_CHECK(ch);
+  if (!c || !fa || !fb || !final_a || !final_b) return fail(GKR_ERR_INVALID, "null argument");
+  if (fa->ctx != c || fb->ctx != c) return fail(GKR_ERR_INVALID, "vector belongs to another context");
+  if (fa->n != fb->n) return fail(GKR_ERR_INVALID, "f_a has %llu entries, f_b %llu", (unsigned long long)fa->n,
+                                  (unsigned long long)fb->n);
+  const uint64_t n = fa->n;
+  if (n & (n - 1)) return fail(GKR_ERR_INVALID, "length %llu is not a power of two", (unsigned long long)n);
+  const int T = log2_exact(n);
+  if (T > 0 && (!round_polys || !challenges)) return fail(GKR_ERR_INVALID, "null output arrays");
+  HIP_TRY(hipSetDevice(c->device));
+  if (T == 0) {
+    qm31 v;
+    TRY(fetch_q(c, fa->dev, 1, &v));
+    *final_a = G(v);
+    TRY(fetch_q(c, fb->dev, 1, &v));
+    *final_b = G(v);
+    return GKR_OK;
+  }
+  // scratch: the fold of round 1 (n/2) and of round 2 (n/4); the caller's vectors stay intact
+  c->mm.valid = false;
+  qm31 *a1, *a2, *b1, *b2;
+  TRY(ensureT(c, S_FA1, n / 2 + 1, &a1));
+  TRY(ensureT(c, S_FB1, n / 2 + 1, &b1));
+  TRY(ensureT(c, S_FA0, n / 4 + 1, &a2));
+  TRY(ensureT(c, S_FB0, n / 4 + 1, &b2));
+  qm31* bufs_a[2] = {a1, a2};
+  qm31* bufs_b[2] = {b1, b2};
+  return product_sumcheck(c, ch->ch, T, fa->dev, fb->dev, bufs_a, bufs_b, nullptr, nullptr, round_polys,
+                          challenges, final_a, final_b);
+}
 
 // ------------------------------------------------------------------ Mul layer
 // reduce_mul_layer (gkr/prover.rs:6172-6271) over the padded QM31 MLEs held in

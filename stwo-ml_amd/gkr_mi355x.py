@@ -135,6 +135,11 @@ SIGNATURES = [
                                              C.POINTER(GkrLogupOut)]),
     ("gkr_activation_table", C.c_int, [C.c_uint32, C.c_uint32, _U32P]),
     ("gkr_bench_copy", C.c_int, [_P, C.c_uint64, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    ("gkr_qvec_upload", C.c_int, [_P, _PQ, C.c_uint64, C.POINTER(_P)]),
+    ("gkr_qvec_synthetic", C.c_int, [_P, C.c_uint64, C.c_uint64, C.POINTER(_P)]),
+    ("gkr_qvec_download", C.c_int, [_P, _P, _PQ]),
+    ("gkr_qvec_free", None, [_P]),
+    ("gkr_sumcheck_product", C.c_int, [_P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ]),
     ("gkr_prove_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, C.POINTER(GkrMulOut)]),
     ("gkr_reduce_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _PQ, _PQ, C.c_uint64, _P, _P,
                                        C.POINTER(GkrMulOut)]),
@@ -402,6 +407,30 @@ class Context:
         return {"round_polys": polys, "final_a_eval": q_from_c(fa), "final_b_eval": q_from_c(fb),
                 "next_point": [q_from_c(npnt[i]) for i in range(lm + T)], "next_value": q_from_c(nv)}
 
+    def qvec_upload(self, vals) -> "QVec":
+        a = np.ascontiguousarray(vals, dtype=np.uint32).reshape(-1, 4)
+        h = _P()
+        _check(lib().gkr_qvec_upload(self._h, a.ctypes.data_as(_PQ), a.shape[0], C.byref(h)))
+        return QVec(self, h.value, a.shape[0])
+
+    def qvec_synthetic(self, n: int, seed: int) -> "QVec":
+        h = _P()
+        _check(lib().gkr_qvec_synthetic(self._h, n, seed, C.byref(h)))
+        return QVec(self, h.value, n)
+
+    def sumcheck_product(self, fa: "QVec", fb: "QVec", ch: PoseidonChannel):
+        """gkr_sumcheck_product: the matmul round loop over resident QM31 vectors."""
+        T = max(0, (fa.n - 1).bit_length())
+        rp = (GkrQM31 * max(1, 3 * T))()
+        chal = (GkrQM31 * max(1, T))()
+        a, b = GkrQM31(), GkrQM31()
+        _check(lib().gkr_sumcheck_product(self._h, fa.handle, fb.handle, ch.handle, rp, chal, C.byref(a),
+                                          C.byref(b)))
+        return {"round_polys": [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2]))
+                                for t in range(T)],
+                "challenges": [q_from_c(chal[t]) for t in range(T)],
+                "final_a_eval": q_from_c(a), "final_b_eval": q_from_c(b)}
+
     def _mul_result(self, out, eq, nv, claim_point):
         return {"eq_round_polys": [tuple(q_from_c(eq[4 * t + j]) for j in range(4)) for t in range(nv)],
                 "lhs_eval": q_from_c(out.lhs_eval), "rhs_eval": q_from_c(out.rhs_eval),
@@ -526,6 +555,27 @@ class Matrix:
     def __del__(self):
         if _lib is not None and getattr(self, "_h", None):
             self.free()
+
+
+class QVec:
+    """A resident QM31 vector (gkr_qvec)."""
+
+    def __init__(self, ctx: "Context", handle: int, n: int):
+        self.ctx, self._h, self.n = ctx, handle, n
+
+    @property
+    def handle(self) -> int:
+        return self._h
+
+    def download(self) -> np.ndarray:
+        out = np.empty((self.n, 4), dtype=np.uint32)
+        _check(lib().gkr_qvec_download(self.ctx.handle, self._h, out.ctypes.data_as(_PQ)))
+        return out
+
+    def __del__(self):
+        if self._h and _lib is not None:
+            _lib.gkr_qvec_free(self._h)
+            self._h = None
 
 
 class Proof:

@@ -1,0 +1,76 @@
+"""Product sumcheck alone (gkr_sumcheck_product: the reduce_matmul_layer round loop over resident
+QM31 vectors; the config-2 workload) against the CPU oracle."""
+import sys
+
+import gkr_mi355x as G
+import numpy as np
+import oracle as O
+import pytest
+import qm31_py as Q
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.parametrize("logn", [0, 1, 2, 9, 10, 11, 16, 20, 24])
+def test_sumcheck_product_parity(gpu_ctx, logn):
+    n = 1 << logn
+    log(f"case sumcheck_product 2^{logn}")
+    fa = gpu_ctx.qvec_synthetic(n, 100 + logn)
+    fb = gpu_ctx.qvec_synthetic(n, 200 + logn)
+    ha, hb = O.synthetic_q(n, 100 + logn), O.synthetic_q(n, 200 + logn)
+    assert np.array_equal(fa.download(), ha) and np.array_equal(fb.download(), hb)
+    gch, och = G.PoseidonChannel(), O.Channel()
+    gch.mix_u64(logn)
+    och.mix_u64(logn)
+    got = gpu_ctx.sumcheck_product(fa, fb, gch)
+    ref = O.sumcheck_product(ha, hb, och)
+    assert got == ref
+    assert gch.digest() == och.digest()
+    # the caller's vectors are left unchanged, and a second run repeats the proof
+    assert np.array_equal(fa.download(), ha) and np.array_equal(fb.download(), hb)
+    gch2 = G.PoseidonChannel()
+    gch2.mix_u64(logn)
+    assert gpu_ctx.sumcheck_product(fa, fb, gch2) == got
+
+
+def test_sumcheck_product_uploaded_and_errors(gpu_ctx):
+    log("case sumcheck_product upload/errors")
+    rng = np.random.default_rng(3)
+    ha = rng.integers(0, (1 << 31) - 1, size=(4096, 4), dtype=np.uint32)
+    hb = rng.integers(0, (1 << 31) - 1, size=(4096, 4), dtype=np.uint32)
+    fa, fb = gpu_ctx.qvec_upload(ha), gpu_ctx.qvec_upload(hb)
+    assert gpu_ctx.sumcheck_product(fa, fb, G.PoseidonChannel()) == O.sumcheck_product(ha, hb, O.Channel())
+    with pytest.raises(G.GkrError, match="not canonical"):
+        gpu_ctx.qvec_upload(np.full((2, 4), (1 << 31) - 1, dtype=np.uint32))
+    odd = gpu_ctx.qvec_upload(ha[:3])
+    with pytest.raises(G.GkrError, match="power of two"):
+        gpu_ctx.sumcheck_product(odd, odd, G.PoseidonChannel())
+    with pytest.raises(G.GkrError, match="entries"):
+        gpu_ctx.sumcheck_product(fa, odd, G.PoseidonChannel())
+
+
+def test_sumcheck_product_2_26_chain(gpu_ctx):
+    """2^26 entries (1 GiB per vector): the verifier's chain p_t(0) + p_t(1) = p_{t-1}(r_t-1) with
+    the transcript replayed on the CPU, ending at final_a * final_b."""
+    n = 1 << 26
+    log("case sumcheck_product 2^26 chain")
+    fa, fb = gpu_ctx.qvec_synthetic(n, 7), gpu_ctx.qvec_synthetic(n, 8)
+    gch = G.PoseidonChannel()
+    gch.mix_u64(26)
+    rep = O.Channel()
+    rep.mix_u64(26)
+    got = gpu_ctx.sumcheck_product(fa, fb, gch)
+    cur = None
+    for (c0, c1, c2), r in zip(got["round_polys"], got["challenges"]):
+        if cur is not None:
+            assert Q.qadd(c0, Q.qadd(Q.qadd(c0, c1), c2)) == cur
+        rep.mix_poly_coeffs(c0, c1, c2)
+        assert rep.draw_qm31() == r
+        cur = Q.qadd(Q.qadd(c0, Q.qmul(c1, r)), Q.qmul(c2, Q.qmul(r, r)))
+    assert cur == Q.qmul(got["final_a_eval"], got["final_b_eval"])
+    assert rep.digest() == gch.digest()

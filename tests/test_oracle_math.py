@@ -289,3 +289,29 @@ def test_mul_layer_matrices_verifier_and_tamper(rows, cols):
         assert O.verify_mul_layer(r, claim, bad, tch.clone())[0] != 0
         bad_claim = Q.qadd(claim, (0, 0, 1, 0))
         assert O.verify_mul_layer(r, bad_claim, proof, tch.clone())[0] != 0
+
+
+@pytest.mark.parametrize("n", [1, 2, 16, 64])
+def test_sumcheck_product_identities(n):
+    """The round loop over QM31 vectors: p_0(0) + p_0(1) = sum f_a f_b, p_t(0) + p_t(1) = p_{t-1}(r),
+    the last value equals final_a * final_b, the final evals are the brute-force MLEs at the
+    replayed challenges, and the transcript replays in Python."""
+    fa, fb = O.synthetic_q(n, 5), O.synthetic_q(n, 6)
+    A = [tuple(int(x) for x in row) for row in fa]
+    B = [tuple(int(x) for x in row) for row in fb]
+    ch = O.Channel()
+    ch.mix_u64(n)
+    rep = ch.clone()
+    res = O.sumcheck_product(fa, fb, ch)
+    cur = (0, 0, 0, 0)
+    for x, y in zip(A, B):
+        cur = Q.qadd(cur, Q.qmul(x, y))
+    for (c0, c1, c2), r in zip(res["round_polys"], res["challenges"]):
+        assert Q.qadd(c0, Q.qadd(Q.qadd(c0, c1), c2)) == cur
+        rep.mix_poly_coeffs(c0, c1, c2)
+        assert rep.draw_qm31() == r
+        cur = Q.qadd(Q.qadd(c0, Q.qmul(c1, r)), Q.qmul(c2, Q.qmul(r, r)))
+    assert res["final_a_eval"] == Q.mle_bruteforce(A, res["challenges"])
+    assert res["final_b_eval"] == Q.mle_bruteforce(B, res["challenges"])
+    assert cur == Q.qmul(res["final_a_eval"], res["final_b_eval"])
+    assert rep.digest() == ch.digest()
