@@ -90,7 +90,8 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
 /* Per-kernel timing (HIP events on the context stream), for benchmarks.
  * ids: 0 restrict_cols, 1 restrict_rows, 2 matmul round, 3 eq3 round,
  * 4 logup prepare, 5 eq table (device kernels: one event pair per launch);
- * 6 host Fiat-Shamir inside the reducers, 7 host wait for device results
+ * 6 host Fiat-Shamir inside the reducers, 7 host wait for results of grid
+ * kernels, 8 host wait for results of the persistent tail kernels
  * (wall-clock, bytes = 0).                                                  */
 int gkr_ctx_set_timing(gkr_ctx* ctx, int enabled);
 int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);

@@ -87,77 +87,96 @@ inline felt felt_sub(const felt& x, const felt& y) {
   return felt{{o0, o1, o2, o3}};
 }
 
-// Montgomery product x*y*2^-256 mod p.  The 512-bit product is formed
-// first (16 independent 64x64 products, so the multiplier pipelines), then
-// reduced word by word: with -p^-1 = -1 mod 2^64, step i takes m = -t[i],
-// which clears limb i with a carry of (t[i] != 0), and adds m*P3 at limb
-// i+3 -- one product per step because p = 1 + P3*2^192.
-inline felt felt_mul(const felt& x, const felt& y) {
-  const uint64_t* a = x.l;
-  const uint64_t* b = y.l;
-  uint64_t t[8];
-  u128 c;
-  uint64_t k;
-  c = (u128)a[0] * b[0];
-  t[0] = (uint64_t)c;
-  k = (uint64_t)(c >> 64);
-  c = (u128)a[0] * b[1] + k;
-  t[1] = (uint64_t)c;
-  k = (uint64_t)(c >> 64);
-  c = (u128)a[0] * b[2] + k;
-  t[2] = (uint64_t)c;
-  k = (uint64_t)(c >> 64);
-  c = (u128)a[0] * b[3] + k;
-  t[3] = (uint64_t)c;
-  t[4] = (uint64_t)(c >> 64);
-  for (int i = 1; i < 4; i++) {
-    c = (u128)a[i] * b[0] + t[i];
-    t[i] = (uint64_t)c;
-    k = (uint64_t)(c >> 64);
-    c = (u128)a[i] * b[1] + t[i + 1] + k;
-    t[i + 1] = (uint64_t)c;
-    k = (uint64_t)(c >> 64);
-    c = (u128)a[i] * b[2] + t[i + 2] + k;
-    t[i + 2] = (uint64_t)c;
-    k = (uint64_t)(c >> 64);
-    c = (u128)a[i] * b[3] + t[i + 3] + k;
-    t[i + 3] = (uint64_t)c;
-    t[i + 4] = (uint64_t)(c >> 64);
-  }
-  for (int i = 0; i < 4; i++) {
-    const uint64_t m = (uint64_t)0 - t[i];
-    uint64_t cc = (t[i] != 0);
-    u128 s = (u128)t[i + 1] + cc;
-    t[i + 1] = (uint64_t)s;
-    cc = (uint64_t)(s >> 64);
-    s = (u128)t[i + 2] + cc;
-    t[i + 2] = (uint64_t)s;
-    cc = (uint64_t)(s >> 64);
-    s = (u128)t[i + 3] + (u128)m * felt_detail::P3 + cc;
-    t[i + 3] = (uint64_t)s;
-    cc = (uint64_t)(s >> 64);
-    for (int j = i + 4; j < 8; j++) {
-      s = (u128)t[j] + cc;
-      t[j] = (uint64_t)s;
-      cc = (uint64_t)(s >> 64);
-    }
-  }
-  felt r{{t[4], t[5], t[6], t[7]}};
-  // r < 2p: one branch-free conditional subtraction
-  u128 d = (u128)r.l[0] - felt_detail::P0;
-  const uint64_t s0 = (uint64_t)d;
-  d = (u128)r.l[1] - ((uint64_t)(d >> 64) & 1);
-  const uint64_t s1 = (uint64_t)d;
-  d = (u128)r.l[2] - ((uint64_t)(d >> 64) & 1);
-  const uint64_t s2 = (uint64_t)d;
-  d = (u128)r.l[3] - felt_detail::P3 - ((uint64_t)(d >> 64) & 1);
-  const uint64_t s3 = (uint64_t)d;
-  const uint64_t keep = (uint64_t)0 - ((uint64_t)(d >> 64) & 1);
-  r.l[0] = (r.l[0] & keep) | (s0 & ~keep);
-  r.l[1] = (r.l[1] & keep) | (s1 & ~keep);
-  r.l[2] = (r.l[2] & keep) | (s2 & ~keep);
-  r.l[3] = (r.l[3] & keep) | (s3 & ~keep);
+// Add/subtract with carry (clang builtins; they compile to adc/sbb chains).
+inline uint64_t adc64(uint64_t a, uint64_t b, uint64_t cin, uint64_t* cout) {
+  unsigned long long co;
+  const uint64_t r = __builtin_addcll(a, b, cin, &co);
+  *cout = co;
   return r;
+}
+inline uint64_t sbb64(uint64_t a, uint64_t b, uint64_t bin, uint64_t* bout) {
+  unsigned long long bo;
+  const uint64_t r = __builtin_subcll(a, b, bin, &bo);
+  *bout = bo;
+  return r;
+}
+
+// Montgomery product x*y*2^-256 mod p without the final subtraction,
+// coarsely integrated (row by row): t += x_i * y, then with -p^-1 = -1 mod
+// 2^64 the multiplier is m = -t0, which clears limb 0 with a carry of
+// (t0 != 0), and m*p adds m*P3 at limb 3 because p = 1 + P3*2^192.  For
+// x*y < 8p^2 (e.g. x < 4p, y < 2p) the result is below 2p.
+inline felt felt_mul_lazy(const felt& x, const felt& y) {
+  const uint64_t b0 = y.l[0], b1 = y.l[1], b2 = y.l[2], b3 = y.l[3];
+  uint64_t t0 = 0, t1 = 0, t2 = 0, t3 = 0, t4 = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint64_t ai = x.l[i];
+    const u128 q0 = (u128)ai * b0, q1 = (u128)ai * b1, q2 = (u128)ai * b2, q3 = (u128)ai * b3;
+    uint64_t c, l1, l2, l3, h3 = (uint64_t)(q3 >> 64);
+    l1 = adc64((uint64_t)q1, (uint64_t)(q0 >> 64), 0, &c);
+    l2 = adc64((uint64_t)q2, (uint64_t)(q1 >> 64), c, &c);
+    l3 = adc64((uint64_t)q3, (uint64_t)(q2 >> 64), c, &c);
+    h3 += c;  // x_i * y < 2^64 * 2^254: the top limb cannot overflow
+    t0 = adc64(t0, (uint64_t)q0, 0, &c);
+    t1 = adc64(t1, l1, c, &c);
+    t2 = adc64(t2, l2, c, &c);
+    t3 = adc64(t3, l3, c, &c);
+    t4 += h3 + c;
+    const uint64_t m = (uint64_t)0 - t0;
+    const u128 mp = (u128)m * felt_detail::P3;
+    const uint64_t n1 = adc64(t1, 0, t0 != 0, &c);
+    const uint64_t n2 = adc64(t2, 0, c, &c);
+    const uint64_t n3 = adc64(t3, (uint64_t)mp, c, &c);
+    const uint64_t n4 = adc64(t4, (uint64_t)(mp >> 64), c, &c);
+    t0 = n1; t1 = n2; t2 = n3; t3 = n4; t4 = c;
+  }
+  return felt{{t0, t1, t2, t3}};
+}
+// [0, 2p) -> [0, p): one branch-free conditional subtraction of p.
+inline felt felt_reduce_once(const felt& r) {
+  uint64_t b;
+  const uint64_t s0 = sbb64(r.l[0], felt_detail::P0, 0, &b);
+  const uint64_t s1 = sbb64(r.l[1], 0, b, &b);
+  const uint64_t s2 = sbb64(r.l[2], 0, b, &b);
+  const uint64_t s3 = sbb64(r.l[3], felt_detail::P3, b, &b);
+  const uint64_t keep = (uint64_t)0 - b;  // all ones when r < p
+  return felt{{(r.l[0] & keep) | (s0 & ~keep), (r.l[1] & keep) | (s1 & ~keep), (r.l[2] & keep) | (s2 & ~keep),
+               (r.l[3] & keep) | (s3 & ~keep)}};
+}
+// Montgomery product x*y*2^-256 mod p of canonical inputs, canonical output.
+inline felt felt_mul(const felt& x, const felt& y) { return felt_reduce_once(felt_mul_lazy(x, y)); }
+
+// Lazy domain [0, 2p) for the permutation's inner loop: sums and differences
+// are brought back below 2p with one masked correction by 2p.
+inline felt felt_add_lazy(const felt& x, const felt& y) {
+  constexpr uint64_t TP0 = 2 * felt_detail::P0, TP3 = 2 * felt_detail::P3;
+  uint64_t c, b;
+  const uint64_t r0 = adc64(x.l[0], y.l[0], 0, &c);
+  const uint64_t r1 = adc64(x.l[1], y.l[1], c, &c);
+  const uint64_t r2 = adc64(x.l[2], y.l[2], c, &c);
+  const uint64_t r3 = adc64(x.l[3], y.l[3], c, &c);  // < 4p < 2^254: no carry out
+  const uint64_t s0 = sbb64(r0, TP0, 0, &b);
+  const uint64_t s1 = sbb64(r1, 0, b, &b);
+  const uint64_t s2 = sbb64(r2, 0, b, &b);
+  const uint64_t s3 = sbb64(r3, TP3, b, &b);
+  const uint64_t keep = (uint64_t)0 - b;
+  return felt{{(r0 & keep) | (s0 & ~keep), (r1 & keep) | (s1 & ~keep), (r2 & keep) | (s2 & ~keep),
+               (r3 & keep) | (s3 & ~keep)}};
+}
+inline felt felt_sub_lazy(const felt& x, const felt& y) {
+  constexpr uint64_t TP0 = 2 * felt_detail::P0, TP3 = 2 * felt_detail::P3;
+  uint64_t b, c;
+  const uint64_t r0 = sbb64(x.l[0], y.l[0], 0, &b);
+  const uint64_t r1 = sbb64(x.l[1], y.l[1], b, &b);
+  const uint64_t r2 = sbb64(x.l[2], y.l[2], b, &b);
+  const uint64_t r3 = sbb64(x.l[3], y.l[3], b, &b);
+  const uint64_t m = (uint64_t)0 - b;
+  const uint64_t o0 = adc64(r0, TP0 & m, 0, &c);
+  const uint64_t o1 = adc64(r1, 0, c, &c);
+  const uint64_t o2 = adc64(r2, 0, c, &c);
+  const uint64_t o3 = adc64(r3, TP3 & m, c, &c);
+  return felt{{o0, o1, o2, o3}};
 }
 
 // Montgomery constants.  R mod p and R^2 mod p are derived once by doubling.

@@ -83,7 +83,7 @@ enum Slot {
 // Timer ids: device kernels (HIP events) and two host-side phases
 // (Fiat-Shamir hashing inside the reducers, and waiting for device results).
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
-                K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_NKERNELS = 8 };
+                K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_NKERNELS = 9 };
 constexpr int kMaxPartialBlocks = 1024;
 
 struct KernelStat {
@@ -291,9 +291,9 @@ static int launch_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks) {
 // spins on the coherent flag; after ~2 s without it the stream is
 // synchronised so that a device error is reported instead of hanging.
 template <int NQ>
-static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out) {
+static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_HOST_WAIT_TAIL) {
   TRY(check_launch());
-  HostTimer ht(c, K_HOST_WAIT);
+  HostTimer ht(c, timer);
   volatile uint32_t* flag = c->h_flag;
   uint64_t spins = 0;
   uint32_t got;
@@ -311,7 +311,7 @@ static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out) {
 }
 template <int NQ>
 static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
-  return wait_result<NQ>(c, sk.seq, host_out);
+  return wait_result<NQ>(c, sk.seq, host_out, K_HOST_WAIT);
 }
 // Host side of a persistent tail kernel: posts challenges into the mailbox.
 // If the host leaves before the protocol completes (an error), the guard

@@ -72,26 +72,45 @@ inline const hades_rc& hades_constants() {
   return k;
 }
 
-inline felt felt_cube(const felt& x) { return felt_mul(felt_mul(x, x), x); }
-
+// The permutation with values kept in [0, 2p) inside (felt_*_lazy) and
+// reduced once at the end.  A partial round x = s2 + c, y = x^3 followed by
+// the MDS layer (t = s0 + s1 + y; s0 = t + 2 s0, s1 = t - 2 s1, s2 = t - 3y)
+// is evaluated as s0' = (3 s0 + s1) + y, s1' = (s0 - s1) + y and
+// s2' = (s0 + s1) - 2y, with 2y = x^2 * 2x formed beside y and the next
+// round's constant folded into (s0 + s1): the dependency chain from one
+// round to the next is two products and one subtraction.
 inline void hades_permute(felt s[3]) {
   const hades_rc& k = hades_constants();
-  for (int r = 0; r < 4; r++) {
-    s[0] = felt_cube(felt_add(s[0], k.full_first[r][0]));
-    s[1] = felt_cube(felt_add(s[1], k.full_first[r][1]));
-    s[2] = felt_cube(felt_add(s[2], k.full_first[r][2]));
-    hades_rc::mds(s);
-  }
+  felt a = s[0], b = s[1], c = s[2];
+  auto full = [&](const felt* rc) {
+    const felt x0 = felt_add_lazy(a, rc[0]), x1 = felt_add_lazy(b, rc[1]), x2 = felt_add_lazy(c, rc[2]);
+    const felt y0 = felt_mul_lazy(felt_mul_lazy(x0, x0), x0);
+    const felt y1 = felt_mul_lazy(felt_mul_lazy(x1, x1), x1);
+    const felt y2 = felt_mul_lazy(felt_mul_lazy(x2, x2), x2);
+    const felt t = felt_add_lazy(felt_add_lazy(y0, y1), y2);
+    a = felt_add_lazy(t, felt_add_lazy(y0, y0));
+    b = felt_sub_lazy(t, felt_add_lazy(y1, y1));
+    c = felt_sub_lazy(t, felt_add_lazy(felt_add_lazy(y2, y2), y2));
+  };
+  for (int r = 0; r < 4; r++) full(k.full_first[r]);
+  felt x = felt_add_lazy(c, k.partial[0]);
   for (int r = 0; r < 83; r++) {
-    s[2] = felt_cube(felt_add(s[2], k.partial[r]));
-    hades_rc::mds(s);
+    const felt u = felt_add_lazy(a, b);
+    const felt A = felt_add_lazy(felt_add_lazy(a, a), u);  // 3 s0 + s1
+    const felt B = felt_sub_lazy(a, b);                    // s0 - s1
+    const felt un = r + 1 < 83 ? felt_add_lazy(u, k.partial[r + 1]) : u;
+    const felt x2 = felt_mul_lazy(x, x);
+    const felt y = felt_mul_lazy(x2, x);
+    const felt y2 = felt_mul_lazy(x2, felt_add_lazy(x, x));  // 2 x^3
+    a = felt_add_lazy(A, y);
+    b = felt_add_lazy(B, y);
+    x = felt_sub_lazy(un, y2);
   }
-  for (int r = 0; r < 4; r++) {
-    s[0] = felt_cube(felt_add(s[0], k.full_last[r][0]));
-    s[1] = felt_cube(felt_add(s[1], k.full_last[r][1]));
-    s[2] = felt_cube(felt_add(s[2], k.full_last[r][2]));
-    hades_rc::mds(s);
-  }
+  c = x;
+  for (int r = 0; r < 4; r++) full(k.full_last[r]);
+  s[0] = felt_reduce_once(a);
+  s[1] = felt_reduce_once(b);
+  s[2] = felt_reduce_once(c);
 }
 
 // hash(a, b) = hades([a, b, 2])[0]

@@ -101,6 +101,20 @@ def test_hash_many_and_permutation_match_oracle():
     assert G.poseidon_hash(st[0], st[1]) == O.hades([st[0], st[1], 2])[0]
 
 
+def test_permutation_matches_oracle_on_many_states():
+    """The product's permutation (lazy [0, 2p) arithmetic inside) against the oracle's independent
+    Montgomery implementation on random states and on edge values (0, 1, p - 1, 2^251, limb
+    boundaries)."""
+    p = O_P252()
+    rng = random.Random(11)
+    edges = [0, 1, 2, p - 1, p - 2, 1 << 251, (1 << 251) - 1, (1 << 192) - 1, (1 << 64) - 1, 1 << 128,
+             p - (1 << 192), 17 << 192]
+    states = [[a, b, c] for a in edges[:4] for b in edges[4:8] for c in edges[8:]]
+    states += [[rng.randrange(p) for _ in range(3)] for _ in range(300)]
+    for st in states:
+        assert G.hades_permute(st) == O.hades(st), st
+
+
 def test_gkr_seeding_with_and_without_policy():
     a, b = G.PoseidonChannel(), O.Channel()
     a.seed_gkr(3, 1, 4)
