@@ -133,6 +133,66 @@ inline felt felt_mul_lazy(const felt& x, const felt& y) {
   }
   return felt{{t0, t1, t2, t3}};
 }
+// Montgomery square x*x*2^-256 mod p without the final subtraction, for
+// x < 4p (result < 2p).  The 512-bit square takes 10 products (the six cross
+// products, doubled, plus the four diagonal ones); the reduction is done in
+// one step: the multiplier M with T + M*p = 0 mod 2^256 is
+// M = -L - X*2^192 where L = T mod 2^256 and X = (-t0)*P3 mod 2^64 (because
+// M*p = M + M*P3*2^192 and only M's lowest limb reaches limb 3 of the
+// second term), and the result is T_hi + (M*P3 >> 64) + c with the carry
+// c = (L != 0) + (n3 < X) out of the vanishing low half.
+inline felt felt_sqr_lazy(const felt& x) {
+  const uint64_t a0 = x.l[0], a1 = x.l[1], a2 = x.l[2], a3 = x.l[3];
+  const u128 p01 = (u128)a0 * a1, p02 = (u128)a0 * a2, p03 = (u128)a0 * a3;
+  const u128 p12 = (u128)a1 * a2, p13 = (u128)a1 * a3, p23 = (u128)a2 * a3;
+  uint64_t c;
+  uint64_t c1 = (uint64_t)p01;
+  uint64_t c2 = adc64((uint64_t)(p01 >> 64), (uint64_t)p02, 0, &c);
+  uint64_t c3 = adc64((uint64_t)(p02 >> 64), (uint64_t)p03, c, &c);
+  uint64_t c4 = adc64((uint64_t)(p03 >> 64), (uint64_t)p13, c, &c);
+  uint64_t c5 = adc64((uint64_t)(p13 >> 64), (uint64_t)p23, c, &c);
+  uint64_t c6 = (uint64_t)(p23 >> 64) + c;
+  c3 = adc64(c3, (uint64_t)p12, 0, &c);
+  c4 = adc64(c4, (uint64_t)(p12 >> 64), c, &c);
+  c5 = adc64(c5, 0, c, &c);
+  c6 += c;
+  const uint64_t c7 = c6 >> 63;  // doubling
+  c6 = (c6 << 1) | (c5 >> 63);
+  c5 = (c5 << 1) | (c4 >> 63);
+  c4 = (c4 << 1) | (c3 >> 63);
+  c3 = (c3 << 1) | (c2 >> 63);
+  c2 = (c2 << 1) | (c1 >> 63);
+  c1 = c1 << 1;
+  const u128 d0 = (u128)a0 * a0, d1 = (u128)a1 * a1, d2 = (u128)a2 * a2, d3 = (u128)a3 * a3;
+  const uint64_t t0 = (uint64_t)d0;
+  const uint64_t t1 = adc64(c1, (uint64_t)(d0 >> 64), 0, &c);
+  const uint64_t t2 = adc64(c2, (uint64_t)d1, c, &c);
+  const uint64_t t3 = adc64(c3, (uint64_t)(d1 >> 64), c, &c);
+  const uint64_t t4 = adc64(c4, (uint64_t)d2, c, &c);
+  const uint64_t t5 = adc64(c5, (uint64_t)(d2 >> 64), c, &c);
+  const uint64_t t6 = adc64(c6, (uint64_t)d3, c, &c);
+  const uint64_t t7 = adc64(c7, (uint64_t)(d3 >> 64), c, &c);
+  uint64_t b;
+  const uint64_t n0 = sbb64(0, t0, 0, &b);
+  const uint64_t n1 = sbb64(0, t1, b, &b);
+  const uint64_t n2 = sbb64(0, t2, b, &b);
+  const uint64_t n3 = sbb64(0, t3, b, &b);
+  const uint64_t X = n0 * felt_detail::P3;
+  const uint64_t m3 = n3 - X;
+  const uint64_t cc = b + (n3 < X);
+  const u128 q0 = (u128)n0 * felt_detail::P3, q1 = (u128)n1 * felt_detail::P3;
+  const u128 q2 = (u128)n2 * felt_detail::P3, q3 = (u128)m3 * felt_detail::P3;
+  uint64_t e;
+  const uint64_t w1 = adc64((uint64_t)(q0 >> 64), (uint64_t)q1, 0, &e);
+  const uint64_t w2 = adc64((uint64_t)(q1 >> 64), (uint64_t)q2, e, &e);
+  const uint64_t w3 = adc64((uint64_t)(q2 >> 64), (uint64_t)q3, e, &e);
+  const uint64_t w4 = (uint64_t)(q3 >> 64) + e;
+  const uint64_t r0 = adc64(t4, w1, cc, &e);
+  const uint64_t r1 = adc64(t5, w2, e, &e);
+  const uint64_t r2 = adc64(t6, w3, e, &e);
+  const uint64_t r3 = t7 + w4 + e;
+  return felt{{r0, r1, r2, r3}};
+}
 // [0, 2p) -> [0, p): one branch-free conditional subtraction of p.
 inline felt felt_reduce_once(const felt& r) {
   uint64_t b;

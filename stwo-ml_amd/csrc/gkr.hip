@@ -462,7 +462,9 @@ extern "C" int gkr_channel_draw_qm31(gkr_channel* ch, gkr_qm31* out) {
 extern "C" int gkr_channel_draw_qm31s(gkr_channel* ch, size_t n, gkr_qm31* out) {
   CH_CHECK(ch);
   if (!out && n) return fail(GKR_ERR_INVALID, "null out");
-  for (size_t i = 0; i < n; i++) out[i] = G(ch->ch.draw_qm31());
+  std::vector<qm31> q(n);
+  ch->ch.draw_qm31s(q.data(), n);
+  for (size_t i = 0; i < n; i++) out[i] = G(q[i]);
   return GKR_OK;
 }
 extern "C" int gkr_channel_digest(const gkr_channel* ch, gkr_felt* out) {
@@ -1325,8 +1327,9 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
   C.mix_u64(0x4C4F47ull);
   C.mix_u64(tag);
-  const qm31 gamma = C.draw_qm31();
-  const qm31 beta = C.draw_qm31();
+  qm31 gb[2];
+  C.draw_qm31s(gb, 2);
+  const qm31 gamma = gb[0], beta = gb[1];
   out->gamma = G(gamma);
   out->beta = G(beta);
 
@@ -1789,7 +1792,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.b->cols)));
       if (st.claim == GKR_CLAIM_FRESH) {
         point.resize(nv);
-        for (uint32_t l = 0; l < nv; l++) point[l] = G(ch->ch.draw_qm31());
+        TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
         TRY(gkr_matmul_output_claim(c, st.a, st.b, point.data(), nv, &value));
         ch->ch.mix_secure_field(Q(value));
       } else if (!have_claim) {
@@ -1808,7 +1811,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
       if (st.claim == GKR_CLAIM_FRESH) {
         point.resize(nv);
-        for (uint32_t l = 0; l < nv; l++) point[l] = G(ch->ch.draw_qm31());
+        TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
         TRY(gkr_mul_output_claim(c, st.a, st.b, point.data(), nv, &value));
         ch->ch.mix_secure_field(Q(value));
       } else if (!have_claim) {
@@ -1824,7 +1827,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
       if (st.claim == GKR_CLAIM_FRESH) {
         point.resize(nv);
-        for (uint32_t l = 0; l < nv; l++) point[l] = G(ch->ch.draw_qm31());
+        TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
         value = G(ch->ch.draw_qm31());
       } else if (!have_claim) {
         return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);

@@ -76,17 +76,16 @@ inline const hades_rc& hades_constants() {
 // reduced once at the end.  A partial round x = s2 + c, y = x^3 followed by
 // the MDS layer (t = s0 + s1 + y; s0 = t + 2 s0, s1 = t - 2 s1, s2 = t - 3y)
 // is evaluated as s0' = (3 s0 + s1) + y, s1' = (s0 - s1) + y and
-// s2' = (s0 + s1) - 2y, with 2y = x^2 * 2x formed beside y and the next
-// round's constant folded into (s0 + s1): the dependency chain from one
-// round to the next is two products and one subtraction.
+// s2' = (s0 + s1) - 2y with the next round's constant folded into (s0 + s1):
+// one square, one product and seven additions per partial round.
 inline void hades_permute(felt s[3]) {
   const hades_rc& k = hades_constants();
   felt a = s[0], b = s[1], c = s[2];
   auto full = [&](const felt* rc) {
     const felt x0 = felt_add_lazy(a, rc[0]), x1 = felt_add_lazy(b, rc[1]), x2 = felt_add_lazy(c, rc[2]);
-    const felt y0 = felt_mul_lazy(felt_mul_lazy(x0, x0), x0);
-    const felt y1 = felt_mul_lazy(felt_mul_lazy(x1, x1), x1);
-    const felt y2 = felt_mul_lazy(felt_mul_lazy(x2, x2), x2);
+    const felt y0 = felt_mul_lazy(felt_sqr_lazy(x0), x0);
+    const felt y1 = felt_mul_lazy(felt_sqr_lazy(x1), x1);
+    const felt y2 = felt_mul_lazy(felt_sqr_lazy(x2), x2);
     const felt t = felt_add_lazy(felt_add_lazy(y0, y1), y2);
     a = felt_add_lazy(t, felt_add_lazy(y0, y0));
     b = felt_sub_lazy(t, felt_add_lazy(y1, y1));
@@ -99,12 +98,10 @@ inline void hades_permute(felt s[3]) {
     const felt A = felt_add_lazy(felt_add_lazy(a, a), u);  // 3 s0 + s1
     const felt B = felt_sub_lazy(a, b);                    // s0 - s1
     const felt un = r + 1 < 83 ? felt_add_lazy(u, k.partial[r + 1]) : u;
-    const felt x2 = felt_mul_lazy(x, x);
-    const felt y = felt_mul_lazy(x2, x);
-    const felt y2 = felt_mul_lazy(x2, felt_add_lazy(x, x));  // 2 x^3
+    const felt y = felt_mul_lazy(felt_sqr_lazy(x), x);
     a = felt_add_lazy(A, y);
     b = felt_add_lazy(B, y);
-    x = felt_sub_lazy(un, y2);
+    x = felt_sub_lazy(un, felt_add_lazy(y, y));
   }
   c = x;
   for (int r = 0; r < 4; r++) full(k.full_last[r]);
@@ -184,8 +181,10 @@ class PoseidonChannel {
     hash_count++;
     return s[0];
   }
-  qm31 draw_qm31() {
-    felt x = felt_from_mont(draw_felt252());
+  // draw_qm31: four 31-bit limbs of the drawn felt, LSB first, each mod P
+  // (poseidon_channel.rs:176-200).
+  static qm31 felt_to_qm31(const felt& mont) {
+    const felt x = felt_from_mont(mont);
     uint32_t m[4];
     for (int k = 0; k < 4; k++) {
       const int bit = 31 * k, limb = bit >> 6, off = bit & 63;
@@ -194,6 +193,10 @@ class PoseidonChannel {
       m[k] = m31_from_u32((uint32_t)(v & 0x7fffffffull));
     }
     return qm31{m[0], m[1], m[2], m[3]};
+  }
+  qm31 draw_qm31() { return felt_to_qm31(draw_felt252()); }
+  void draw_qm31s(qm31* out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = draw_qm31();
   }
   void mix_poly_coeffs(const qm31& c0, const qm31& c1, const qm31& c2) {
     const uint32_t w[12] = {c0.a, c0.b, c0.c, c0.d, c1.a, c1.b, c1.c, c1.d, c2.a, c2.b, c2.c, c2.d};

@@ -115,6 +115,23 @@ def test_permutation_matches_oracle_on_many_states():
         assert G.hades_permute(st) == O.hades(st), st
 
 
+def test_batched_draws_equal_sequential_draws():
+    """draw_qm31s(n) runs its independent permutations in lockstep; it must equal n single draws
+    (the oracle draws one at a time) for every remainder modulo the batch width, and leave the
+    same channel state."""
+    for n in range(0, 11):
+        g, o = G.PoseidonChannel(), O.Channel()
+        g.mix_u64(n + 1)
+        o.mix_u64(n + 1)
+        g.draw_qm31()
+        o.draw_qm31()
+        assert g.draw_qm31s(n) == [o.draw_qm31() for _ in range(n)]
+        assert g.draw_qm31() == o.draw_qm31()
+        assert g.digest() == o.digest()
+        st = g.export_state()
+        assert st[8] == n + 2 and (st[9] | (st[10] << 32)) == g.hash_count()
+
+
 def test_gkr_seeding_with_and_without_policy():
     a, b = G.PoseidonChannel(), O.Channel()
     a.seed_gkr(3, 1, 4)
