@@ -78,7 +78,7 @@ static bool felt_abi_canonical(const gkr_felt& f) {
 // ------------------------------------------------------------------ context
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
-  S_TABLE, S_MULT, S_PADIN, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_COLPART, S_NSLOTS
+  S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_COLPART, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and two host-side phases
 // (Fiat-Shamir hashing inside the reducers, and waiting for device results).
@@ -125,6 +125,8 @@ struct gkr_ctx {
   void* buf[S_NSLOTS] = {};
   size_t cap[S_NSLOTS] = {};
   qm31* h_res = nullptr;  // pinned result staging (64 QM31)
+  uint32_t* h_mult = nullptr;  // pinned copy of the LogUp multiplicities
+  size_t h_mult_cap = 0;
   qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
   uint32_t* h_flag = nullptr; // coherent pinned: sequence number of the last delivery
   Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
@@ -160,6 +162,19 @@ static int ensureT(gkr_ctx* c, Slot s, size_t count, T** out) {
   void* p;
   TRY(ensure(c, s, count * sizeof(T), &p));
   *out = (T*)p;
+  return GKR_OK;
+}
+
+static int ensure_host_mult(gkr_ctx* c, uint64_t n) {
+  if (c->h_mult_cap >= n) return GKR_OK;
+  if (c->h_mult) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    (void)hipHostFree(c->h_mult);
+    c->h_mult = nullptr;
+    c->h_mult_cap = 0;
+  }
+  HIP_TRY(hipHostMalloc((void**)&c->h_mult, n * sizeof(uint32_t), hipHostMallocDefault));
+  c->h_mult_cap = n;
   return GKR_OK;
 }
 
@@ -270,13 +285,28 @@ static int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out)
   return check_launch();
 }
 
-static int make_sink(gkr_ctx* c, RoundSink* sk) {
+// Result and mailbox sequence numbers come in consecutive ranges and restart
+// at 1 before they reach the codes reserved at the top of the u32 range
+// (kTailTimeout, kTailCancel); waits compare them modulo 2^32.
+constexpr uint32_t kSeqLimit = 0xFFFFFF00u;
+static uint32_t alloc_seq(uint32_t* counter, uint32_t n) {
+  if (*counter >= kSeqLimit - n) *counter = 0;
+  const uint32_t base = *counter + 1;
+  *counter += n;
+  return base;
+}
+// Partial rows for a reducing kernel.  `slot` selects where in the coherent
+// host buffer the finisher writes its NQ results: slots 0-3 serve the round
+// in flight, higher slots hold results launched ahead of time and read
+// later.  The partial rows are shared: each finisher consumes them before the
+// next reducing kernel on the stream overwrites them.
+static int make_sink(gkr_ctx* c, RoundSink* sk, int slot = 0) {
   qm31* part;
   TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
   sk->partials = part;
-  sk->out = c->h_out;
+  sk->out = c->h_out + slot;
   sk->flag = c->h_flag;
-  sk->seq = ++c->seq;
+  sk->seq = alloc_seq(&c->seq, 1);
   return GKR_OK;
 }
 // Launch the one-workgroup finisher that adds `nblocks` partial rows and
@@ -291,27 +321,28 @@ static int launch_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks) {
 // spins on the coherent flag; after ~2 s without it the stream is
 // synchronised so that a device error is reported instead of hanging.
 template <int NQ>
-static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_HOST_WAIT_TAIL) {
+static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_HOST_WAIT_TAIL, int slot = 0) {
   TRY(check_launch());
   HostTimer ht(c, timer);
   volatile uint32_t* flag = c->h_flag;
   uint64_t spins = 0;
   uint32_t got;
-  while ((got = *flag) != seq) {
+  // the flag only moves forward (mod 2^32): a later delivery implies this one
+  while ((int32_t)((got = *flag) - seq) < 0 || got == kTailTimeout) {
     if (got == kTailTimeout) return fail(GKR_ERR_DEVICE, "persistent round kernel timed out waiting for a challenge");
     if (++spins == (1u << 26)) {
       HIP_TRY(hipStreamSynchronize(c->stream));
-      if (*flag != seq) return fail(GKR_ERR_DEVICE, "device result %u not delivered", seq);
+      if ((int32_t)(*flag - seq) < 0) return fail(GKR_ERR_DEVICE, "device result %u not delivered", seq);
       break;
     }
   }
   __atomic_thread_fence(__ATOMIC_ACQUIRE);
-  for (int q = 0; q < NQ; q++) host_out[q] = c->h_out[q];
+  for (int q = 0; q < NQ; q++) host_out[q] = c->h_out[slot + q];
   return GKR_OK;
 }
 template <int NQ>
 static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
-  return wait_result<NQ>(c, sk.seq, host_out, K_HOST_WAIT);
+  return wait_result<NQ>(c, sk.seq, host_out, K_HOST_WAIT, (int)(sk.out - c->h_out));
 }
 // Host side of a persistent tail kernel: posts challenges into the mailbox.
 // If the host leaves before the protocol completes (an error), the guard
@@ -321,10 +352,8 @@ struct TailSession {
   uint32_t res_base, mb_base;
   bool done = false;
   TailSession(gkr_ctx* c_, int n_results, int n_posts) : c(c_) {
-    res_base = c->seq + 1;
-    c->seq += (uint32_t)n_results;
-    mb_base = c->mb_seq + 1;
-    c->mb_seq += (uint32_t)n_posts;
+    res_base = alloc_seq(&c->seq, (uint32_t)n_results);
+    mb_base = alloc_seq(&c->mb_seq, (uint32_t)n_posts);
   }
   void post(uint32_t r, const qm31& alpha) {
     c->mailbox->alpha = alpha;
@@ -553,6 +582,7 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   for (int s = 0; s < S_NSLOTS; s++)
     if (c->buf[s]) (void)hipFree(c->buf[s]);
   if (c->h_res) (void)hipHostFree(c->h_res);
+  if (c->h_mult) (void)hipHostFree(c->h_mult);
   if (c->h_out) (void)hipHostFree(c->h_out);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
@@ -1188,8 +1218,21 @@ static const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint3
 // inputs and are overwritten; e1/w1/d1 (n/2 + 1 entries) are the other half of
 // the ping-pong.  Writes 4 * nv round coefficients, nv challenges and the final
 // (eq, w, d) values.
+static bool eq3_has_grid_rounds(int nv) { return nv >= 0 && (1ull << nv) > (uint64_t)(kTailMax / 2); }
+// Launch round 0 of eq3_sumcheck ahead of the transcript (it needs no
+// challenge); only when the sumcheck has grid rounds.
+static int eq3_launch_round0(gkr_ctx* c, int nv, const qm31* e0, const qm31* w0, const qm31* d0, RoundSink* sk) {
+  const uint64_t half = (1ull << nv) / 2;
+  TRY(make_sink(c, sk));
+  {
+    TimedLaunch tl(c, K_EQ3_ROUND, 96 * half);
+    hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, e0, w0, d0,
+                       (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), *sk);
+  }
+  return launch_finish<4>(c, *sk, partial_grid(half));
+}
 static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, int nv, qm31* e0, qm31* w0, qm31* d0, qm31* e1, qm31* w1,
-                        qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3]) {
+                        qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3], const RoundSink* pre0 = nullptr) {
   const uint64_t n = 1ull << nv;
   if (nv == 0) {
     TRY(fetch_q(c, e0, 1, fin + 0));
@@ -1238,21 +1281,22 @@ static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, int nv, qm31* e0, qm31* 
     const uint64_t half = (n >> t) / 2;
     qm31 sums[4];
     RoundSink sk;
-    TRY(make_sink(c, &sk));
-    {
-      // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}; round 0 reads only
-      TimedLaunch tl(c, K_EQ3_ROUND, t == 0 ? 96 * half : 288 * half);
-      if (t == 0) {
-        hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd,
-                           (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
-      } else {
+    if (t == 0 && pre0) {
+      sk = *pre0;
+    } else if (t == 0) {
+      TRY(eq3_launch_round0(c, nv, ce, cw, cd, &sk));
+    } else {
+      TRY(make_sink(c, &sk));
+      {
+        // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}
+        TimedLaunch tl(c, K_EQ3_ROUND, 288 * half);
         qm31 *ne = be[(t - 1) & 1], *nw = bw[(t - 1) & 1], *nd = bd[(t - 1) & 1];
         hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw, nd,
                            half, 1, alpha, sk);
         ce = ne; cw = nw; cd = nd;
       }
+      TRY(launch_finish<4>(c, sk, partial_grid(half)));
     }
-    TRY(launch_finish<4>(c, sk, partial_grid(half)));
     if (t == t0 - 1) TRY(launch_tail());
     TRY(wait_sink<4>(c, sk, sums));
     absorb3(t, sums);
@@ -1303,11 +1347,10 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   const uint32_t mask = (uint32_t)(tsize - 1);
   const std::vector<uint32_t>& table = cached_table(c, tag, table_log);
 
-  uint32_t *d_table, *d_mult, *d_pad, *d_min, *d_mout;
-  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *d_e1;
+  uint32_t *d_table, *d_mult, *d_min, *d_mout;
+  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *d_e1, *m0, *m1;
   TRY(ensureT(c, S_TABLE, tsize, &d_table));
   TRY(ensureT(c, S_MULT, tsize, &d_mult));
-  TRY(ensureT(c, S_PADIN, n, &d_pad));
   TRY(ensureT(c, S_MIN, n, &d_min));
   TRY(ensureT(c, S_MOUT, n, &d_mout));
   TRY(ensureT(c, S_D0, n, &d_d0));
@@ -1316,6 +1359,9 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
   TRY(ensureT(c, S_E0, n, &d_e0));
   TRY(ensureT(c, S_E1, n / 2 + 1, &d_e1));
+  TRY(ensureT(c, S_M0, tsize, &m0));
+  TRY(ensureT(c, S_M1, tsize / 2 + 1, &m1));
+  TRY(ensure_host_mult(c, tsize));
   const uint64_t table_key = ((uint64_t)tag << 32) | table_log;
   if (c->table_on_device != table_key) {
     c->table_on_device = 0;
@@ -1323,6 +1369,9 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     c->table_on_device = table_key;
   }
   HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
+  // eq(claim point, x): the input MLE at the claim point (accumulated by the
+  // prepare pass) and the eq vector of the eq-sumcheck
+  TRY(eq_table(c, cpt.data(), nv, n, d_e0));
 
   // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
   C.mix_u64(0x4C4F47ull);
@@ -1333,31 +1382,44 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   out->gamma = G(gamma);
   out->beta = G(beta);
 
-  qm31 trace_sum, table_sum;
+  // Launched back to back, read when needed (results in slots 4-9):
+  //   prepare -> (trace sum, input MLE at the claim point)      slots 4, 5
+  //   table-side sum over the multiplicities                     slot 6
+  //   multiplicities -> pinned host copy
+  //   multiplicity sumcheck round 0 (no challenge needed)        slots 8, 9
+  //   eq-sumcheck round 0                                        slots 0-3
+  RoundSink sk_prep, sk_table, sk_mult0, sk_eq0;
+  TRY(make_sink(c, &sk_prep, 4));
   {
-    RoundSink sk;
-    TRY(make_sink(c, &sk));
-    {
-      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 12 * n + 32 * n);
-      hipLaunchKernelGGL(k_logup_prepare, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, input->dev, input->rows,
-                         input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, d_pad, d_min, d_mout, d_d0,
-                         d_w0, d_mult, sk);
-    }
-    TRY(launch_finish<1>(c, sk, partial_grid(n)));
-    qm31 r[1];
-    TRY(wait_sink<1>(c, sk, r));
-    trace_sum = r[0];
+    TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 16 * n + 8 * n + 32 * n);
+    hipLaunchKernelGGL(k_logup_prepare, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, input->dev, input->rows,
+                       input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, d_e0, d_min, d_mout, d_d0, d_w0,
+                       d_mult, sk_prep);
   }
-  {
-    RoundSink sk;
-    TRY(make_sink(c, &sk));
-    hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult,
-                       tsize, gamma, beta, sk);
-    TRY(launch_finish<1>(c, sk, partial_grid(tsize)));
-    qm31 r[1];
-    TRY(wait_sink<1>(c, sk, r));
-    table_sum = r[0];
+  TRY(launch_finish<2>(c, sk_prep, partial_grid(n)));
+  TRY(make_sink(c, &sk_table, 6));
+  hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult, tsize,
+                     gamma, beta, sk_table);
+  TRY(launch_finish<1>(c, sk_table, partial_grid(tsize)));
+  HIP_TRY(hipMemcpyAsync(c->h_mult, d_mult, tsize * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+  hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0);
+  TRY(check_launch());
+  int mt0 = 0;  // multiplicity sumcheck: grid rounds t < mt0, the rest in k_sum_tail
+  while ((tsize >> mt0) > (uint64_t)kTailMax) mt0++;
+  if (mt0 > 0) {
+    const uint64_t half = tsize / 2;
+    TRY(make_sink(c, &sk_mult0, 8));
+    hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, (const qm31*)m0,
+                       (qm31*)nullptr, half, 0, qm31_zero(), sk_mult0);
+    TRY(launch_finish<2>(c, sk_mult0, partial_grid(half)));
   }
+  const bool eq_pre = eq3_has_grid_rounds(nv) && nv > 0;
+  if (eq_pre) TRY(eq3_launch_round0(c, nv, d_e0, d_w0, d_d0, &sk_eq0));
+
+  qm31 prep[2], tsum[1];
+  TRY(wait_sink<1>(c, sk_table, tsum));  // implies the prepare results (earlier on the stream)
+  for (int q = 0; q < 2; q++) prep[q] = c->h_out[4 + q];
+  const qm31 trace_sum = prep[0], input_eval = prep[1], table_sum = tsum[0];
   if (!qm31_eq(trace_sum, table_sum))
     return fail(GKR_ERR_LOGUP, "Activation LogUp sum mismatch: trace=(%u,%u,%u,%u) table=(%u,%u,%u,%u)", trace_sum.a,
                 trace_sum.b, trace_sum.c, trace_sum.d, table_sum.a, table_sum.b, table_sum.c, table_sum.d);
@@ -1365,34 +1427,32 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   out->claimed_sum = G(trace_sum);
 
   // eq-sumcheck: sum eq(r, x) w(x) d(x) = 1 over the hypercube
-  TRY(eq_table(c, cpt.data(), nv, n, d_e0));
   std::vector<qm31> chal(nv);
   qm31 fin[3];
-  TRY(eq3_sumcheck(c, C, nv, d_e0, d_w0, d_d0, d_e1, d_w1, d_d1, out->eq_round_polys, chal.data(), fin));
+  TRY(eq3_sumcheck(c, C, nv, d_e0, d_w0, d_d0, d_e1, d_w1, d_d1, out->eq_round_polys, chal.data(), fin,
+                   eq_pre ? &sk_eq0 : nullptr));
   const qm31 w_eval = fin[1];
-  // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges
-  qm31 in_eval, out_eval, input_eval;
+  // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass
+  qm31 io[2];
   TRY(eq_table(c, chal.data(), nv, n, d_e0));
-  TRY(dot_m31(c, d_min, d_e0, n, &in_eval));
-  TRY(dot_m31(c, d_mout, d_e0, n, &out_eval));
-  // MLE(padded input) at the claim point (prover.rs:6411-6417)
-  TRY(eq_table(c, cpt.data(), nv, n, d_e0));
-  TRY(dot_m31(c, d_pad, d_e0, n, &input_eval));
+  {
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
+    hipLaunchKernelGGL(k_dot2_m31, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, d_min, d_mout, d_e0, n, sk);
+    TRY(launch_finish<2>(c, sk, partial_grid(n)));
+    TRY(wait_sink<2>(c, sk, io));
+  }
+  const qm31 in_eval = io[0], out_eval = io[1];
   out->w_eval = G(w_eval);
   out->in_eval = G(in_eval);
   out->out_eval = G(out_eval);
 
-  // Multiplicity sumcheck (prover.rs:9449-9511): degree-1 rounds over 2^table_log entries.
-  HIP_TRY(hipMemcpyAsync(out->multiplicities, d_mult, tsize * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
-  TRY(sync(c));
-  uint64_t msum = 0;
-  for (uint64_t j = 0; j < tsize; j++) msum += out->multiplicities[j];
-  const qm31 mult_sum = qm31_from_m31(m31_reduce64(msum));
-  qm31 *m0, *m1;
-  TRY(ensureT(c, S_M0, tsize, &m0));
-  TRY(ensureT(c, S_M1, tsize / 2 + 1, &m1));
-  hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0);
-  TRY(check_launch());
+  // Multiplicity sumcheck (prover.rs:9449-9511): degree-1 rounds over
+  // 2^table_log entries.  The multiplicities reached the pinned copy before
+  // the kernels whose results were waited for above; they count every padded
+  // input once, so their sum is n.
+  memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
+  const qm31 mult_sum = qm31_from_m31(m31_reduce64(n));
   const qm31* cm = m0;
   qm31* bm[2] = {m1, m0};
   qm31 alpha = qm31_zero();
@@ -1408,8 +1468,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   };
   qm31 mfin[1];
   {
-    int t0 = 0;
-    while ((tsize >> t0) > (uint64_t)kTailMax) t0++;
+    const int t0 = mt0;
     const int n_tail = (int)table_log - t0;
     std::unique_ptr<TailSession> tail;
     auto launch_tail = [&]() -> int {
@@ -1422,17 +1481,16 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     for (int t = 0; t < t0; t++) {
       const uint64_t half = (tsize >> t) / 2;
       RoundSink sk;
-      TRY(make_sink(c, &sk));
       if (t == 0) {
-        hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, (qm31*)nullptr,
-                           half, 0, qm31_zero(), sk);
+        sk = sk_mult0;
       } else {
+        TRY(make_sink(c, &sk));
         qm31* nm = bm[(t - 1) & 1];
         hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, nm, half, 1,
                            alpha, sk);
         cm = nm;
+        TRY(launch_finish<2>(c, sk, partial_grid(half)));
       }
-      TRY(launch_finish<2>(c, sk, partial_grid(half)));
       if (t == t0 - 1) TRY(launch_tail());
       qm31 sums[2];
       TRY(wait_sink<2>(c, sk, sums));

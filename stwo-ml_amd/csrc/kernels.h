@@ -590,23 +590,51 @@ __global__ void __launch_bounds__(kBlock) k_mm_round(const qm31* __restrict__ a_
 
 
 // ------------------------------------------------------------------ LogUp
+// M31-by-QM31 dot product accumulator: the four 62-bit products of each term
+// are split into 32-bit halves and summed in 64-bit lanes (no reduction in
+// the loop; 2^32 terms per thread at most).
+struct dot_acc {
+  uint64_t lo[4], hi[4];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int c = 0; c < 4; c++) lo[c] = hi[c] = 0;
+  }
+  __device__ __forceinline__ void add(uint32_t x, const qm31& e) {
+    const uint64_t t[4] = {(uint64_t)x * e.a, (uint64_t)x * e.b, (uint64_t)x * e.c, (uint64_t)x * e.d};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      lo[c] += (uint32_t)t[c];
+      hi[c] += t[c] >> 32;
+    }
+  }
+  __device__ __forceinline__ qm31 reduce() const {  // lo + 2^32 hi with 2^32 = 2 mod P
+    uint32_t r[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
+    return qm31{r[0], r[1], r[2], r[3]};
+  }
+};
+
 // Pad the activation matrix to (prow x pcol), mask to the table range, look up
 // the table output, form d = gamma - in - beta*out and w = 1/d, count
-// multiplicities and accumulate sum(w) per workgroup (gkr/prover.rs:6411-6475).
+// multiplicities (gkr/prover.rs:6411-6475).  Per workgroup it accumulates
+// sum(w) and the MLE of the padded input at the claim point,
+// sum_p x_p * eq[p] (prover.rs:6411-6417), into a 2-value sink.
 __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
-    const uint32_t* __restrict__ table_out, uint32_t mask, qm31 gamma, qm31 beta,
-    uint32_t* __restrict__ padded_in, uint32_t* __restrict__ masked_in, uint32_t* __restrict__ masked_out,
-    qm31* __restrict__ d_out, qm31* __restrict__ w_out, uint32_t* __restrict__ mult, RoundSink sink) {
+    const uint32_t* __restrict__ table_out, uint32_t mask, qm31 gamma, qm31 beta, const qm31* __restrict__ eq,
+    uint32_t* __restrict__ masked_in, uint32_t* __restrict__ masked_out, qm31* __restrict__ d_out,
+    qm31* __restrict__ w_out, uint32_t* __restrict__ mult, RoundSink sink) {
   qacc acc;
   acc.zero();
+  dot_acc ie;
+  ie.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n; p += stride) {
     const uint64_t r = p >> log_pcol, c = p & ((1ull << log_pcol) - 1);
     const uint32_t x = (r < rows && c < cols) ? X[r * cols + c] : 0u;
     const uint32_t mi = x & mask;
     const uint32_t mo = table_out[mi];
-    padded_in[p] = x;
     masked_in[p] = mi;
     masked_out[p] = mo;
     const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(mi)), qm31_mul_m31(beta, mo));
@@ -616,10 +644,11 @@ __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     // zero padding all lands in bin 0; it is counted once below
     if (r < rows && c < cols) atomicAdd(&mult[mi], 1u);
     acc.add(w);
+    ie.add(m31_from_u32(x), ld_q(eq, p));
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
-  qm31 v[1] = {acc.reduce()};
-  sink_finish<1>(v, sink);
+  qm31 v[2] = {acc.reduce(), ie.reduce()};
+  sink_finish<2>(v, sink);
 }
 // Table side: sum_j mult_j / (gamma - j - beta*f(j)) over entries with mult_j > 0.
 __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __restrict__ table_out,
@@ -720,20 +749,29 @@ __global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __
 // Partial dot products sum_i v[i] * eq[i] for an M31-valued v.
 __global__ void __launch_bounds__(kBlock) k_dot_m31(const uint32_t* __restrict__ v, const qm31* __restrict__ eq,
                                                     uint64_t n, RoundSink sink) {
-  uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+  dot_acc acc;
+  acc.zero();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    acc.add(m31_from_u32(v[i]), ld_q(eq, i));
+  qm31 q[1] = {acc.reduce()};
+  sink_finish<1>(q, sink);
+}
+// Two M31 vectors against one eq table in one pass (the masked input and
+// output MLEs at the eq-sumcheck challenges, prover.rs:6558-6579).
+__global__ void __launch_bounds__(kBlock) k_dot2_m31(const uint32_t* __restrict__ v0, const uint32_t* __restrict__ v1,
+                                                     const qm31* __restrict__ eq, uint64_t n, RoundSink sink) {
+  dot_acc a0, a1;
+  a0.zero();
+  a1.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const uint64_t x = m31_from_u32(v[i]);
     const qm31 e = ld_q(eq, i);
-    const uint64_t t[4] = {x * e.a, x * e.b, x * e.c, x * e.d};
-#pragma unroll
-    for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+    a0.add(m31_from_u32(v0[i]), e);
+    a1.add(m31_from_u32(v1[i]), e);
   }
-  uint32_t r[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
-  qm31 q[1] = {qm31{r[0], r[1], r[2], r[3]}};
-  sink_finish<1>(q, sink);
+  qm31 q[2] = {a0.reduce(), a1.reduce()};
+  sink_finish<2>(q, sink);
 }
 // Partial dot products sum_i v[i] * eq[i] for a QM31-valued v.
 __global__ void __launch_bounds__(kBlock) k_dot_q(const qm31* __restrict__ v, const qm31* __restrict__ eq,
