@@ -126,6 +126,7 @@ struct gkr_ctx {
   size_t cap[S_NSLOTS] = {};
   qm31* h_res = nullptr;  // pinned result staging (64 QM31)
   uint32_t* h_mult = nullptr;  // pinned copy of the LogUp multiplicities
+  qm31* h_vec = nullptr;       // coherent pinned: vectors handed over by the tail kernels (3 x kTailMax)
   size_t h_mult_cap = 0;
   qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
   uint32_t* h_flag = nullptr; // coherent pinned: sequence number of the last delivery
@@ -553,6 +554,11 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
     gkr_ctx_destroy(c);
     return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
   }
+  if (hipHostMalloc((void**)&c->h_vec, 3 * kTailMax * sizeof(qm31), hipHostMallocCoherent | hipHostMallocMapped) !=
+      hipSuccess) {
+    gkr_ctx_destroy(c);
+    return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
+  }
   c->h_flag = reinterpret_cast<uint32_t*>(c->h_out + 64);
   *c->h_flag = 0;
   c->mailbox = reinterpret_cast<Mailbox*>(reinterpret_cast<char*>(c->h_out) + 64 * sizeof(qm31) + 128);
@@ -583,6 +589,7 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
     if (c->buf[s]) (void)hipFree(c->buf[s]);
   if (c->h_res) (void)hipHostFree(c->h_res);
   if (c->h_mult) (void)hipHostFree(c->h_mult);
+  if (c->h_vec) (void)hipHostFree(c->h_vec);
   if (c->h_out) (void)hipHostFree(c->h_out);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
@@ -791,6 +798,20 @@ static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* 
   return GKR_OK;
 }
 
+// The last rounds of each sumcheck run on the host once the vectors are this
+// short: a round there costs less than a device round trip (post the
+// challenge, fold and reduce in one workgroup, deliver).  The persistent tail
+// kernel hands its LDS vectors over and exits.
+constexpr uint64_t kHostTailMM = 128;    // product sumcheck: 5 QM31 products per pair
+constexpr uint64_t kHostTailEq3 = 64;    // eq-sumcheck: 11 products per pair
+constexpr uint64_t kHostTailSum = 1024;  // multiplicity sumcheck: 1 product per pair
+// Wait for the vector hand-over `seq` and copy `count` vectors of `len` entries.
+static int fetch_tail_vectors(gkr_ctx* c, uint32_t seq, uint64_t len, int count, std::vector<qm31>* out) {
+  TRY(wait_result<0>(c, seq, nullptr));
+  for (int v = 0; v < count; v++) out[v].assign(c->h_vec + v * len, c->h_vec + (v + 1) * len);
+  return GKR_OK;
+}
+
 // Degree-2 product sumcheck sum_x f_a(x) f_b(x) over 2^T entries: the round
 // loop of reduce_matmul_layer (backend.rs:146-177; gpu_sumcheck.rs:2820-2840).
 // in_a/in_b are read by rounds 0 and 1; round t >= 1 folds into
@@ -811,7 +832,9 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
   // fold run in one persistent workgroup (k_mm_tail).
   int t0 = 0;
   while ((pk >> t0) > (uint64_t)kTailMax) t0++;
-  const int n_tail = T - t0;
+  int t1 = t0;  // rounds t >= t1 on the host
+  while ((pk >> t1) > kHostTailMM) t1++;
+  const int n_tail = t1 - t0;
   qm31 alpha = qm31_zero();
   auto absorb = [&](int t, const qm31* sums) {
     const qm31 c0 = sums[0];
@@ -830,7 +853,7 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
     const uint32_t len_in = (uint32_t)(t0 == 0 ? pk : (pk >> (t0 - 1)));
     tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
     hipLaunchKernelGGL(k_mm_tail, dim3(1), dim3(kBlock), 0, c->stream, cur_a, cur_b, len_in, t0 > 0 ? 1 : 0,
-                       n_tail, c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base);
+                       n_tail, c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base, c->h_vec);
     return check_launch();
   };
   for (int t = 0; t < t0; t++) {
@@ -883,11 +906,30 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
     absorb(t0 + r, sums);
     tail->post(r + 1, alpha);
   }
-  qm31 fin[2];
-  TRY(wait_result<2>(c, tail->res_base + n_tail, fin));
+  std::vector<qm31> v[2];
+  TRY(fetch_tail_vectors(c, tail->res_base + n_tail, pk >> t1, 2, v));
   tail->done = true;
-  *final_a = G(fin[0]);
-  *final_b = G(fin[1]);
+  std::vector<qm31>& A = v[0];
+  std::vector<qm31>& B = v[1];
+  for (int t = t1; t < T; t++) {
+    const size_t half = A.size() / 2;
+    qm31 sums[3] = {qm31_zero(), qm31_zero(), qm31_zero()};
+    for (size_t i = 0; i < half; i++) {
+      const qm31 a0 = A[i], a1 = A[i + half], b0 = B[i], b1 = B[i + half];
+      sums[0] = qm31_add(sums[0], qm31_mul(a0, b0));
+      sums[1] = qm31_add(sums[1], qm31_mul(a1, b1));
+      sums[2] = qm31_add(sums[2], qm31_mul(qm31_sub(qm31_add(a1, a1), a0), qm31_sub(qm31_add(b1, b1), b0)));
+    }
+    absorb(t, sums);
+    for (size_t i = 0; i < half; i++) {
+      A[i] = qm31_fold(A[i], A[i + half], alpha);
+      B[i] = qm31_fold(B[i], B[i + half], alpha);
+    }
+    A.resize(half);
+    B.resize(half);
+  }
+  *final_a = G(A[0]);
+  *final_b = G(B[0]);
   return GKR_OK;
 }
 
@@ -1268,13 +1310,15 @@ static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, int nv, qm31* e0, qm31* 
   // elements per vector) and the final fold in k_eq3_tail
   int t0 = 0;
   while ((n >> t0) > (uint64_t)(kTailMax / 2)) t0++;
-  const int n_tail = nv - t0;
+  int t1 = t0;  // rounds t >= t1 on the host
+  while ((n >> t1) > kHostTailEq3) t1++;
+  const int n_tail = t1 - t0;
   std::unique_ptr<TailSession> tail;
   auto launch_tail = [&]() -> int {
     const uint32_t len_in = (uint32_t)(t0 == 0 ? n : (n >> (t0 - 1)));
     tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
     hipLaunchKernelGGL(k_eq3_tail, dim3(1), dim3(kBlock), 0, c->stream, ce, cw, cd, len_in, t0 > 0 ? 1 : 0, n_tail,
-                       c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base);
+                       c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base, c->h_vec);
     return check_launch();
   };
   for (int t = 0; t < t0; t++) {
@@ -1312,8 +1356,37 @@ static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, int nv, qm31* e0, qm31* 
     absorb3(t0 + r, sums);
     tail->post(r + 1, alpha);
   }
-  TRY(wait_result<3>(c, tail->res_base + n_tail, fin));
+  std::vector<qm31> v[3];
+  TRY(fetch_tail_vectors(c, tail->res_base + n_tail, n >> t1, 3, v));
   tail->done = true;
+  std::vector<qm31>& E = v[0];
+  std::vector<qm31>& W = v[1];
+  std::vector<qm31>& D = v[2];
+  for (int t = t1; t < nv; t++) {
+    const size_t half = E.size() / 2;
+    qm31 sums[4] = {qm31_zero(), qm31_zero(), qm31_zero(), qm31_zero()};
+    for (size_t i = 0; i < half; i++) {
+      const qm31 e0 = E[i], e1 = E[i + half], w0 = W[i], w1 = W[i + half], d0 = D[i], d1 = D[i + half];
+      sums[0] = qm31_add(sums[0], qm31_mul(qm31_mul(e0, w0), d0));
+      sums[1] = qm31_add(sums[1], qm31_mul(qm31_mul(e1, w1), d1));
+      const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1, w0), dd = qm31_sub(d1, d0);
+      const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1, dw), d2 = qm31_add(d1, dd);
+      sums[2] = qm31_add(sums[2], qm31_mul(qm31_mul(e2, w2), d2));
+      sums[3] = qm31_add(sums[3], qm31_mul(qm31_mul(qm31_add(e2, de), qm31_add(w2, dw)), qm31_add(d2, dd)));
+    }
+    absorb3(t, sums);
+    for (size_t i = 0; i < half; i++) {
+      E[i] = qm31_fold(E[i], E[i + half], alpha);
+      W[i] = qm31_fold(W[i], W[i + half], alpha);
+      D[i] = qm31_fold(D[i], D[i + half], alpha);
+    }
+    E.resize(half);
+    W.resize(half);
+    D.resize(half);
+  }
+  fin[0] = E[0];
+  fin[1] = W[0];
+  fin[2] = D[0];
   return GKR_OK;
 }
 
@@ -1469,13 +1542,15 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   qm31 mfin[1];
   {
     const int t0 = mt0;
-    const int n_tail = (int)table_log - t0;
+    int t1 = t0;  // rounds t >= t1 on the host
+    while ((tsize >> t1) > kHostTailSum) t1++;
+    const int n_tail = t1 - t0;
     std::unique_ptr<TailSession> tail;
     auto launch_tail = [&]() -> int {
       const uint32_t len_in = (uint32_t)(t0 == 0 ? tsize : (tsize >> (t0 - 1)));
       tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
       hipLaunchKernelGGL(k_sum_tail, dim3(1), dim3(kBlock), 0, c->stream, cm, len_in, t0 > 0 ? 1 : 0, n_tail,
-                         c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base);
+                         c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base, c->h_vec);
       return check_launch();
     };
     for (int t = 0; t < t0; t++) {
@@ -1507,8 +1582,22 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       absorb1((uint32_t)(t0 + r), sums);
       tail->post(r + 1, alpha);
     }
-    TRY(wait_result<1>(c, tail->res_base + n_tail, mfin));
+    std::vector<qm31> v[1];
+    TRY(fetch_tail_vectors(c, tail->res_base + n_tail, tsize >> t1, 1, v));
     tail->done = true;
+    std::vector<qm31>& V = v[0];
+    for (int t = t1; t < (int)table_log; t++) {
+      const size_t half = V.size() / 2;
+      qm31 sums[2] = {qm31_zero(), qm31_zero()};
+      for (size_t i = 0; i < half; i++) {
+        sums[0] = qm31_add(sums[0], V[i]);
+        sums[1] = qm31_add(sums[1], V[i + half]);
+      }
+      absorb1((uint32_t)t, sums);
+      for (size_t i = 0; i < half; i++) V[i] = qm31_fold(V[i], V[i + half], alpha);
+      V.resize(half);
+    }
+    mfin[0] = V[0];
   }
   out->mult_final_eval = G(mfin[0]);
   out->mult_claimed_sum = G(mult_sum);

@@ -164,16 +164,33 @@ __device__ __forceinline__ bool tail_wait(Mailbox* mb, uint32_t want, qm31* sh_a
   return *sh_ok;
 }
 
-// Tail of the product sumcheck (k_mm_round semantics) for rounds
-// round0 .. round0 + n_rounds - 1, then the final fold.  On entry the
-// vectors have length len_in; when fold_first is set they are folded by the
-// challenge of the previous round before the first evaluation.  Result i
-// (round sums, then {final_a, final_b}) is published with seq res_base + i;
-// the challenge folded before result i carries mailbox seq mb_base + i.
+// Hand the vectors of length len (held in LDS) to the host: every thread
+// stores its share into coherent host memory and makes it visible system-wide
+// before thread 0 publishes `seq`.
+__device__ __forceinline__ void publish_vectors(const qm31* v0, const qm31* v1, const qm31* v2, uint32_t len,
+                                                qm31* vec_out, uint32_t* flag, uint32_t seq) {
+  for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) {
+    vec_out[i] = v0[i];
+    if (v1) vec_out[len + i] = v1[i];
+    if (v2) vec_out[2 * len + i] = v2[i];
+  }
+  __threadfence_system();
+  __syncthreads();
+  if (threadIdx.x == 0) publish_flag(flag, seq);
+}
+
+// Tail of the product sumcheck (k_mm_round semantics) for n_rounds rounds.
+// On entry the vectors have length len_in; when fold_first is set they are
+// folded by the challenge of the previous round before the first
+// evaluation.  Result i < n_rounds (the round sums) is published with seq
+// res_base + i; the challenge folded before result i carries mailbox seq
+// mb_base + i.  After the fold that follows the last round the remaining
+// vectors (a then b, len_in >> (n_rounds + fold_first) entries each) go to
+// vec_out with seq res_base + n_rounds; the host finishes from there.
 __global__ void __launch_bounds__(kBlock) k_mm_tail(const qm31* __restrict__ a_in, const qm31* __restrict__ b_in,
                                                     uint32_t len_in, int fold_first, int n_rounds, Mailbox* mb,
                                                     uint32_t mb_base, qm31* out, uint32_t* flag,
-                                                    uint32_t res_base) {
+                                                    uint32_t res_base, qm31* vec_out) {
   __shared__ qm31 va[2 * kTailMax], vb[2 * kTailMax];
   __shared__ qm31 sh_alpha;
   __shared__ bool sh_ok;
@@ -214,19 +231,15 @@ __global__ void __launch_bounds__(kBlock) k_mm_tail(const qm31* __restrict__ a_i
       publish_flag(flag, res_base + r);
     }
   }
-  if (threadIdx.x == 0) {  // len == 1 after the final fold
-    out[0] = va[0];
-    out[1] = vb[0];
-    publish_flag(flag, res_base + n_rounds);
-  }
+  publish_vectors(va, vb, nullptr, len, vec_out, flag, res_base + n_rounds);
 }
 
 // Tail of the degree-3 eq-sumcheck over (eq, w, d): same protocol, 4 sums per
-// round, final result {eq, w, d} folded to one value each.
+// round; the remaining eq, w and d vectors go to vec_out at the end.
 __global__ void __launch_bounds__(kBlock) k_eq3_tail(const qm31* __restrict__ e_in, const qm31* __restrict__ w_in,
                                                      const qm31* __restrict__ d_in, uint32_t len_in, int fold_first,
                                                      int n_rounds, Mailbox* mb, uint32_t mb_base, qm31* out,
-                                                     uint32_t* flag, uint32_t res_base) {
+                                                     uint32_t* flag, uint32_t res_base, qm31* vec_out) {
   constexpr int kMax = kTailMax / 2;
   __shared__ qm31 ve[2 * kMax], vw[2 * kMax], vd[2 * kMax];
   __shared__ qm31 sh_alpha;
@@ -273,18 +286,13 @@ __global__ void __launch_bounds__(kBlock) k_eq3_tail(const qm31* __restrict__ e_
       publish_flag(flag, res_base + r);
     }
   }
-  if (threadIdx.x == 0) {
-    out[0] = ve[0];
-    out[1] = vw[0];
-    out[2] = vd[0];
-    publish_flag(flag, res_base + n_rounds);
-  }
+  publish_vectors(ve, vw, vd, len, vec_out, flag, res_base + n_rounds);
 }
 
 // Tail of the degree-1 multiplicity sumcheck: sums of the low and high halves.
 __global__ void __launch_bounds__(kBlock) k_sum_tail(const qm31* __restrict__ v_in, uint32_t len_in, int fold_first,
                                                      int n_rounds, Mailbox* mb, uint32_t mb_base, qm31* out,
-                                                     uint32_t* flag, uint32_t res_base) {
+                                                     uint32_t* flag, uint32_t res_base, qm31* vec_out) {
   __shared__ qm31 vv[2 * kTailMax];
   __shared__ qm31 sh_alpha;
   __shared__ bool sh_ok;
@@ -317,10 +325,7 @@ __global__ void __launch_bounds__(kBlock) k_sum_tail(const qm31* __restrict__ v_
       publish_flag(flag, res_base + r);
     }
   }
-  if (threadIdx.x == 0) {
-    out[0] = vv[0];
-    publish_flag(flag, res_base + n_rounds);
-  }
+  publish_vectors(vv, nullptr, nullptr, len, vec_out, flag, res_base + n_rounds);
 }
 
 // ------------------------------------------------------------------ eq / Lagrange
