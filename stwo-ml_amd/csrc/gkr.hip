@@ -802,9 +802,18 @@ static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* 
 // short: a round there costs less than a device round trip (post the
 // challenge, fold and reduce in one workgroup, deliver).  The persistent tail
 // kernel hands its LDS vectors over and exits.
-constexpr uint64_t kHostTailMM = 128;    // product sumcheck: 5 QM31 products per pair
-constexpr uint64_t kHostTailEq3 = 64;    // eq-sumcheck: 11 products per pair
-constexpr uint64_t kHostTailSum = 1024;  // multiplicity sumcheck: 1 product per pair
+#ifndef GKR_HOST_TAIL_MM
+#define GKR_HOST_TAIL_MM 256    // product sumcheck: 5 QM31 products per pair
+#endif
+#ifndef GKR_HOST_TAIL_EQ3
+#define GKR_HOST_TAIL_EQ3 128   // eq-sumcheck: 11 products per pair
+#endif
+#ifndef GKR_HOST_TAIL_SUM
+#define GKR_HOST_TAIL_SUM 1024  // multiplicity sumcheck: 1 product per pair
+#endif
+constexpr uint64_t kHostTailMM = GKR_HOST_TAIL_MM;
+constexpr uint64_t kHostTailEq3 = GKR_HOST_TAIL_EQ3;
+constexpr uint64_t kHostTailSum = GKR_HOST_TAIL_SUM;
 // Wait for the vector hand-over `seq` and copy `count` vectors of `len` entries.
 static int fetch_tail_vectors(gkr_ctx* c, uint32_t seq, uint64_t len, int count, std::vector<qm31>* out) {
   TRY(wait_result<0>(c, seq, nullptr));

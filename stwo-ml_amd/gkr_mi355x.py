@@ -17,7 +17,8 @@ from typing import List, Optional, Sequence, Tuple
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libgkr_mi355x.so")
+# GKR_MI355X_LIB selects another build of the library (e.g. a tuning variant).
+LIB_PATH = os.environ.get("GKR_MI355X_LIB") or os.path.join(HERE, "lib", "libgkr_mi355x.so")
 P = (1 << 31) - 1
 FELT_P = 2**251 + 17 * 2**192 + 1
 
