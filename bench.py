@@ -190,6 +190,20 @@ def poseidon_round_us(n=500):
     return round((time.perf_counter() - t0) / n * 1e6, 2)
 
 
+def measured_traffic(name="restrict_cols_traffic.md"):
+    """HBM bytes per launch of k_restrict_cols from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE runs scaled by the copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(budget_s=25.0):
     """The oracle (reference CPU algorithm) on a bounded sample: Qwen q_proj layer reduction."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -233,7 +247,7 @@ def bench_c2(ctx, args):
 
         for _ in range(args.warmup):
             run()
-        ctx.set_timing(not args.no_timing)
+        ctx.set_timing(0 if args.no_timing else 2)  # the roofline kernel here is k_mm_round
         ctx.reset_timing()
         t0 = time.perf_counter()
         outs = [run() for _ in range(args.steps)]
@@ -284,7 +298,9 @@ def main():
     ap.add_argument("--c2-logs", default="20,24,28",
                     help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-timing", action="store_true", help="skip per-kernel HIP events")
+    ap.add_argument("--no-timing", action="store_true", help="no HIP events and no host timers")
+    ap.add_argument("--timing-all", action="store_true",
+                    help="HIP events on every timed kernel (default: only the roofline kernel k_restrict_cols)")
     ap.add_argument("--driver", default="walk", choices=["walk", "calls"],
                     help="walk: one gkr_prove_walk call per proof; calls: one library call per layer")
     args = ap.parse_args()
@@ -326,7 +342,7 @@ def main():
         t0 = time.perf_counter()
         out = step()
         log(f"[bench] warmup {w}: {time.perf_counter() - t0:.3f} s digest={out[0]:#x}")
-    ctx.set_timing(not args.no_timing)
+    ctx.set_timing(0 if args.no_timing else (2 if args.timing_all else 1))
     ctx.reset_timing()
     ctx.synchronize()
     for key in CALL_TIME:
@@ -361,9 +377,11 @@ def main():
     if rc:
         ms, nl, nb = ctx.kernel_time(K_RESTRICT_COLS)
         ach = nb / (ms * 1e-3) / 1e9
+        traffic = measured_traffic() if cfg is QWEN else None
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_restrict_cols",
-                    "avg_launch_us": rc["avg_us"], "bytes_per_launch": nb // nl}
+                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_restrict_cols",
+                    "avg_launch_us": rc["avg_us"], "bytes_per_launch": nb // nl,
+                    "traffic_source": "profiles/restrict_cols_traffic.md (rocprofv3 PMC, qwen1)" if traffic else None}
 
     result = {
         "metric": METRIC,

@@ -93,7 +93,9 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * 6 host Fiat-Shamir inside the reducers, 7 host wait for results of grid
  * kernels, 8 host wait for results of the persistent tail kernels
  * (wall-clock, bytes = 0).                                                  */
-int gkr_ctx_set_timing(gkr_ctx* ctx, int enabled);
+/* level 0: off; 1: events on k_restrict_cols only, plus the host timers;
+ * 2: events on every timed kernel (adds an event pair per launch). */
+int gkr_ctx_set_timing(gkr_ctx* ctx, int level);
 int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);
 int gkr_ctx_reset_timing(gkr_ctx* ctx);
 

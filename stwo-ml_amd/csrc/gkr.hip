@@ -133,7 +133,7 @@ struct gkr_ctx {
   Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
   uint32_t seq = 0;            // last result sequence number handed out
   uint32_t mb_seq = 0;         // last mailbox sequence number handed out
-  bool timing = false;
+  int timing = 0;  // 0 off; 1: k_restrict_cols events + host timers; 2: events on every timed kernel
   KernelStat stats[K_NKERNELS];
   std::vector<PendingTiming> pending;
   std::vector<hipEvent_t> free_events;
@@ -195,14 +195,14 @@ struct TimedLaunch {
   uint64_t bytes;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
-    if (c->timing) {
+    if (c->timing >= 2 || (c->timing == 1 && kid == K_RESTRICT_COLS)) {
       e0 = get_event(c);
       e1 = get_event(c);
       if (e0) (void)hipEventRecord(e0, c->stream);
     }
   }
   ~TimedLaunch() {
-    if (c->timing && e0 && e1) {
+    if (e0 && e1) {
       (void)hipEventRecord(e1, c->stream);
       c->pending.push_back({kid, e0, e1, bytes});
     }
@@ -598,10 +598,11 @@ extern "C" int gkr_ctx_synchronize(gkr_ctx* c) {
   if (!c) return fail(GKR_ERR_INVALID, "null ctx");
   return sync(c);
 }
-extern "C" int gkr_ctx_set_timing(gkr_ctx* c, int enabled) {
+extern "C" int gkr_ctx_set_timing(gkr_ctx* c, int level) {
+  const int enabled = level;
   if (!c) return fail(GKR_ERR_INVALID, "null ctx");
   TRY(sync(c));
-  c->timing = enabled != 0;
+  c->timing = enabled < 0 ? 0 : (enabled > 2 ? 2 : enabled);
   return GKR_OK;
 }
 extern "C" int gkr_ctx_kernel_time(gkr_ctx* c, int kid, double* total_ms, uint64_t* launches, uint64_t* bytes) {

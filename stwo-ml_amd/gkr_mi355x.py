@@ -326,8 +326,9 @@ class Context:
     def synchronize(self):
         _check(lib().gkr_ctx_synchronize(self._h))
 
-    def set_timing(self, on: bool):
-        _check(lib().gkr_ctx_set_timing(self._h, 1 if on else 0))
+    def set_timing(self, level):
+        """0 off; 1 (or True): k_restrict_cols events + host timers; 2: events on every timed kernel."""
+        _check(lib().gkr_ctx_set_timing(self._h, int(level)))
 
     def reset_timing(self):
         _check(lib().gkr_ctx_reset_timing(self._h))
