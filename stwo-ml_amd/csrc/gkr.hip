@@ -709,14 +709,25 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     TRY(check_launch());
   }
   {
-    // column chunks: enough workgroups to fill the chip (>= 1536), chunks a
-    // multiple of one wave sweep (256 columns) and at least 1024 columns
+    // column chunks: chunks a multiple of one wave sweep (256 columns), at
+    // least GKR_RC_MIN_CHUNK columns, and at most GKR_RC_TARGET workgroups in
+    // all (GKR_RC_CEIL: at least that many)
+#ifndef GKR_RC_TARGET
+#define GKR_RC_TARGET 2560
+#endif
+#ifndef GKR_RC_MIN_CHUNK
+#define GKR_RC_MIN_CHUNK 512
+#endif
+#ifndef GKR_RC_CEIL
+#define GKR_RC_CEIL 1
+#endif
     const uint64_t rows_per_block = (uint64_t)kColRows * kColWaves;
     const uint64_t gr = (k + rows_per_block - 1) / rows_per_block;
-    uint64_t gc = (1536 + gr - 1) / gr;
+    uint64_t gc = GKR_RC_CEIL ? (GKR_RC_TARGET + gr - 1) / gr : GKR_RC_TARGET / gr;
+    if (gc < 1) gc = 1;
     uint64_t chunk = (n + gc - 1) / gc;
     chunk = (chunk + 255) / 256 * 256;
-    if (chunk < 1024) chunk = 1024;
+    if (chunk < GKR_RC_MIN_CHUNK) chunk = GKR_RC_MIN_CHUNK;
     gc = (n + chunk - 1) / chunk;
     qm31* part;
     TRY(ensureT(c, S_COLPART, (size_t)gc * k, &part));

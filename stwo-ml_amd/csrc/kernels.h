@@ -415,8 +415,12 @@ __global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint
 // waves of a workgroup share the chunk, so L[j] comes from L2 once and from
 // L1 for the other waves, and each L[j] held in registers serves kColRows
 // rows.  B is streamed with non-temporal loads.  Each wave reduces its own
-// rows (no LDS, no barrier) and writes one canonical QM31 partial per row to
-// partial[(chunk * k + row) * 4 + component]; k_restrict_cols_finish adds the chunks.
+// rows through a per-wave LDS region (no workgroup barrier) and writes one
+// canonical QM31 partial per row to partial[(chunk * k + row) * 4 + component];
+// k_restrict_cols_finish adds the chunks.  The kernel is VALU-bound (4
+// v_mad_u64_u32 per weight word at ~2.5x the cost of a full-rate op), so the
+// loop keeps the instruction count down: no register copies between steps and
+// a 16-value reduction of ~40 instructions instead of a shuffle butterfly.
 constexpr int kColRows = 4;
 constexpr int kColWaves = kBlock / 64;
 
@@ -447,33 +451,11 @@ __device__ __forceinline__ void load_row4(const uint32_t* __restrict__ row, uint
   }
 }
 
-// Sum 16 canonical M31 values per lane over the 64 lanes of a wave with a
-// transposing butterfly: each step halves the values a lane carries and
-// exchanges the other half with its partner (8+4+2+1 shuffles), two more
-// steps finish the sums.  Lanes with (lane & 3) == 0 end up holding the wave
-// total of value (lane >> 2).
-__device__ __forceinline__ uint32_t wave_sum16(uint32_t (&v)[16]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 8, m = 32; k >= 1; k >>= 1, m >>= 1) {
-    const bool upper = (lane & m) != 0;
-#pragma unroll
-    for (int i = 0; i < k; i++) {
-      const uint32_t send = upper ? v[i] : v[i + k];
-      const uint32_t keep = upper ? v[i + k] : v[i];
-      v[i] = m31_add(keep, shfl_xor_u32(send, m));
-    }
-  }
-  uint32_t x = v[0];
-  x = m31_add(x, shfl_xor_u32(x, 2));
-  x = m31_add(x, shfl_xor_u32(x, 1));
-  return x;
-}
-
 template <bool kVec4>
 __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
                                                           uint64_t chunk, const qm31* __restrict__ L,
                                                           uint32_t* __restrict__ partial) {
+  __shared__ uint32_t sh[kColWaves][64][17];  // epilogue transpose, one region per wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t row0 = ((uint64_t)blockIdx.x * kColWaves + wave) * kColRows;
   if (row0 >= k) return;  // whole wave leaves; no workgroup barrier follows
@@ -489,50 +471,54 @@ __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __rest
 #pragma unroll
     for (int c = 0; c < 4; c++) lo[r][c] = hi[r][c] = 0;
 
+  // Two register sets (a, b) alternate: while one column group is multiplied
+  // the next one is in flight, and no copies are needed between steps.
   constexpr uint64_t kStep = 64 * 4;
+  auto count_at = [&](uint64_t jj) -> int { return (int)(jj < c1 ? ((c1 - jj) < 4 ? (c1 - jj) : 4) : 0); };
+  qm31 la[4], lb[4];
+  uint32_t va[kColRows][4], vb[kColRows][4];
+  auto load = [&](uint64_t jj, int cnt, qm31 (&l)[4], uint32_t (&v)[kColRows][4]) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) l[u] = (u < cnt) ? ld_q(L, jj + u) : qm31_zero();
+#pragma unroll
+    for (int r = 0; r < kColRows; r++) load_row4<kVec4>(rows[r], jj, cnt, v[r]);
+  };
   uint64_t j = c0 + (uint64_t)lane * 4;
-  qm31 lc[4];
-  uint32_t vc[kColRows][4];
-  int cnt = (int)(j < c1 ? ((c1 - j) < 4 ? (c1 - j) : 4) : 0);
-  if (cnt) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) lc[u] = (u < cnt) ? ld_q(L, j + u) : qm31_zero();
-#pragma unroll
-    for (int r = 0; r < kColRows; r++) load_row4<kVec4>(rows[r], j, cnt, vc[r]);
-  }
+  int cnt = count_at(j);
+  if (cnt) load(j, cnt, la, va);
   while (cnt) {
-    const uint64_t jn = j + kStep;
-    const int cntn = (int)(jn < c1 ? ((c1 - jn) < 4 ? (c1 - jn) : 4) : 0);
-    qm31 ln[4];
-    uint32_t vn[kColRows][4];
-    if (cntn) {  // prefetch the next column group
+    const uint64_t j1 = j + kStep;
+    const int cnt1 = count_at(j1);
+    if (cnt1) load(j1, cnt1, lb, vb);
 #pragma unroll
-      for (int u = 0; u < 4; u++) ln[u] = (u < cntn) ? ld_q(L, jn + u) : qm31_zero();
+    for (int r = 0; r < kColRows; r++) acc_row4(lo[r], hi[r], va[r], la);
+    if (!cnt1) break;
+    const uint64_t j2 = j1 + kStep;
+    cnt = count_at(j2);
+    if (cnt) load(j2, cnt, la, va);
 #pragma unroll
-      for (int r = 0; r < kColRows; r++) load_row4<kVec4>(rows[r], jn, cntn, vn[r]);
-    }
-#pragma unroll
-    for (int r = 0; r < kColRows; r++) acc_row4(lo[r], hi[r], vc[r], lc);
-    if (!cntn) break;
-#pragma unroll
-    for (int u = 0; u < 4; u++) lc[u] = ln[u];
-#pragma unroll
-    for (int r = 0; r < kColRows; r++)
-#pragma unroll
-      for (int u = 0; u < 4; u++) vc[r][u] = vn[r][u];
-    j = jn;
-    cnt = cntn;
+    for (int r = 0; r < kColRows; r++) acc_row4(lo[r], hi[r], vb[r], lb);
+    j = j2;
   }
-  // canonical per-lane sums (lo + 2*hi < 2^64 because 2^32 == 2 mod P),
-  // then the wave reduction of the 16 (row, component) values
-  uint32_t v[16];
+  // Canonical per-lane sums (lo + 2*hi < 2^64 because 2^32 == 2 mod P) of
+  // the 16 (row, component) values, then the wave reduction through LDS:
+  // lane l adds value (l & 15) over the 16 lanes of group (l >> 4), two
+  // shuffles add the four groups, lanes 0-15 hold the totals.
 #pragma unroll
   for (int r = 0; r < kColRows; r++)
 #pragma unroll
-    for (int c = 0; c < 4; c++) v[4 * r + c] = m31_reduce64(lo[r][c] + (hi[r][c] << 1));
-  const uint32_t w = wave_sum16(v);
-  if ((lane & 3) == 0) {
-    const int slot = lane >> 2, r = slot >> 2, c = slot & 3;
+    for (int c = 0; c < 4; c++) sh[wave][lane][4 * r + c] = m31_reduce64(lo[r][c] + (hi[r][c] << 1));
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  const int vi = lane & 15, g = lane >> 4;
+  uint64_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < 16; i++) acc += sh[wave][g * 16 + i][vi];
+  uint32_t w = m31_reduce64(acc);
+  w = m31_add(w, shfl_xor_u32(w, 16));
+  w = m31_add(w, shfl_xor_u32(w, 32));
+  if (lane < 16) {
+    const int r = lane >> 2, c = lane & 3;
     if (r < nrows) partial[((uint64_t)blockIdx.y * k + row0 + r) * 4 + c] = w;
   }
 }
