@@ -44,7 +44,8 @@ enum {
   GKR_ERR_DEVICE = 2,  /* HIP runtime failure */
   GKR_ERR_LOGUP = 3,   /* LogUp trace/table sums disagree (prover.rs:6488-6495) */
   GKR_ERR_NOMEM = 4,
-  GKR_ERR_BUFFER = 5   /* caller buffer too small */
+  GKR_ERR_BUFFER = 5,  /* caller buffer too small */
+  GKR_ERR_VERIFY = 6   /* a verifier check failed (reason in gkr_last_error) */
 };
 
 /* Message of the last error on this thread (never NULL). */
@@ -273,6 +274,51 @@ typedef struct {
 int gkr_prove_walk(gkr_ctx* ctx, gkr_channel* ch, const gkr_step* steps, size_t n_steps, const gkr_qm31* init_point,
                    uint32_t n_init, const gkr_qm31* init_value, gkr_proof* proof, gkr_qm31* final_point,
                    uint32_t* n_final, gkr_qm31* final_value);
+
+/* ------------------------------------------------------------------ verifier replay
+ * Host-only: each call replays the layer's transcript on `ch` and returns
+ * GKR_OK with the claim on the layer's input, or GKR_ERR_VERIFY with the
+ * failing check in gkr_last_error. */
+/* verify_matmul_reduction (engine/src/gkr/verifier.rs:2675-2788).
+ * round_polys: (c0, c1, c2) per round; next_point receives log2(pm) +
+ * n_rounds entries (r_i then the challenges); next_value = final_a. */
+int gkr_verify_matmul_layer(const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value, uint64_t m,
+                            uint64_t k, uint64_t n, const gkr_qm31* round_polys, uint32_t n_rounds,
+                            const gkr_qm31* final_a, const gkr_qm31* final_b, gkr_channel* ch, gkr_qm31* next_point,
+                            uint32_t* n_next, gkr_qm31* next_value);
+/* verify_mul_reduction (verifier.rs:2963-3045).  eq_round_polys: (c0..c3)
+ * per round; next_value = alpha * lhs + (1 - alpha) * rhs (the point is
+ * unchanged). */
+int gkr_verify_mul_layer(const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                         const gkr_qm31* eq_round_polys, uint32_t n_rounds, const gkr_qm31* lhs_eval,
+                         const gkr_qm31* rhs_eval, gkr_channel* ch, gkr_qm31* next_value);
+/* verify_activation_reduction, LogUp branch, with verify_multiplicity_sumcheck
+ * (verifier.rs:3058-3290, 5818-5842).  `proof` carries the prover's outputs
+ * (gkr_logup_out: eq_round_polys 4 x n_eq_rounds, 2^table_log_size
+ * multiplicities, 2 x table_log_size multiplicity round polys); next_value =
+ * input_eval.  The reference refuses LogUp-only proofs of non-ReLU
+ * activations unless STWO_ALLOW_LOGUP_ACTIVATION is set; this replay
+ * corresponds to that setting. */
+int gkr_verify_activation_layer(const gkr_qm31* claim_point, uint32_t n_point, uint32_t activation_type,
+                                uint32_t table_log_size, uint32_t n_eq_rounds, const gkr_logup_out* proof,
+                                gkr_channel* ch, gkr_qm31* next_value);
+/* One layer of the circuit a walk is verified against. */
+typedef struct {
+  uint32_t kind;             /* GKR_STEP_MATMUL / GKR_STEP_MUL / GKR_STEP_ACTIVATION */
+  uint64_t rows, cols;       /* MatMul: A is rows x cols (m x k); Mul / Activation: the operand */
+  uint64_t cols_b;           /* MatMul: n (B is cols x cols_b) */
+  uint32_t activation_type;  /* Activation */
+  uint32_t table_log_size;   /* Activation: 0 = reference default */
+} gkr_layer_shape;
+/* A chained walk from serialize_gkr_model_proof calldata (the layer section
+ * and the input claim that follows it): layer i's claim is layer i-1's input
+ * claim, starting from init_point / init_value (the seeded output claim).
+ * Round polynomials are compressed (c1 rebuilt from the running sum).  The
+ * weight commitments, openings and IO commitment after the input claim are
+ * not examined; *n_consumed receives the number of felts read. */
+int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const gkr_layer_shape* layers, size_t n_layers,
+                    const gkr_qm31* init_point, uint32_t n_init, const gkr_qm31* init_value, gkr_channel* ch,
+                    gkr_qm31* final_point, uint32_t* n_final, gkr_qm31* final_value, size_t* n_consumed);
 
 /* Activation table output column, f(j) for j < 2^log_size (host). */
 int gkr_activation_table(uint32_t activation_type, uint32_t log_size, uint32_t* out);

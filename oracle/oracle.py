@@ -134,6 +134,17 @@ class Channel:
         return felt_int(out)
 
 
+def channel_state(ch: "Channel") -> List[int]:
+    """The channel in the reference's to_gpu_state layout (poseidon_channel.rs:109-135): 8 LE u32
+    words of the canonical digest, n_draws, hash_count lo, hash_count hi."""
+    d = ch.digest()
+    words = [(d >> (32 * i)) & 0xFFFFFFFF for i in range(8)]
+    raw = bytes(ch.buf)
+    n_draws = int.from_bytes(raw[32:36], "little")
+    hash_count = int.from_bytes(raw[40:48], "little")
+    return words + [n_draws, hash_count & 0xFFFFFFFF, hash_count >> 32]
+
+
 def hash_many(xs: Sequence[int]) -> int:
     a = np.concatenate([felt_words(x) for x in xs]) if xs else np.zeros(8, dtype=np.uint32)
     out = np.zeros(8, dtype=np.uint32)

@@ -70,6 +70,11 @@ def _next_pow2(v: int) -> int:
     return 1 << max(0, (v - 1).bit_length())
 
 
+class GkrLayerShape(C.Structure):
+    _fields_ = [("kind", C.c_uint32), ("rows", C.c_uint64), ("cols", C.c_uint64), ("cols_b", C.c_uint64),
+                ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32)]
+
+
 class GkrError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"gkr error {code}: {msg}")
@@ -145,6 +150,13 @@ SIGNATURES = [
     ("gkr_reduce_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _PQ, _PQ, C.c_uint64, _P, _P,
                                        C.POINTER(GkrMulOut)]),
     ("gkr_mul_output_claim", C.c_int, [_P, _P, _P, _PQ, C.c_uint32, _PQ]),
+    ("gkr_verify_matmul_layer", C.c_int, [_PQ, C.c_uint32, _PQ, C.c_uint64, C.c_uint64, C.c_uint64, _PQ,
+                                          C.c_uint32, _PQ, _PQ, _P, _PQ, C.POINTER(C.c_uint32), _PQ]),
+    ("gkr_verify_mul_layer", C.c_int, [_PQ, C.c_uint32, _PQ, _PQ, C.c_uint32, _PQ, _PQ, _P, _PQ]),
+    ("gkr_verify_activation_layer", C.c_int, [_PQ, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                              C.POINTER(GkrLogupOut), _P, _PQ]),
+    ("gkr_verify_walk", C.c_int, [C.POINTER(GkrFelt), C.c_size_t, C.POINTER(GkrLayerShape), C.c_size_t, _PQ,
+                                  C.c_uint32, _PQ, _P, _PQ, C.POINTER(C.c_uint32), _PQ, C.POINTER(C.c_size_t)]),
     ("gkr_prove_walk", C.c_int, [_P, _P, C.POINTER(GkrStep), C.c_size_t, _PQ, C.c_uint32, _PQ, _P, _PQ,
                                  C.POINTER(C.c_uint32), _PQ]),
 ]
@@ -534,6 +546,75 @@ def prove_walk(ctx: "Context", ch: PoseidonChannel, steps, proof: "Proof", init_
     _check(lib().gkr_prove_walk(ctx.handle, ch.handle, arr, n, ip, len(init_point) if init_point else 0, iv,
                                 proof.handle if proof else None, fp, C.byref(nf), C.byref(fv)))
     return [q_from_c(fp[i]) for i in range(nf.value)], q_from_c(fv)
+
+
+# ------------------------------------------------------------------ verifier replay (host only)
+def verify_matmul_layer(claim_point, claim_value, m: int, k: int, n: int, round_polys, final_a, final_b,
+                        ch: PoseidonChannel):
+    """gkr_verify_matmul_layer (verify_matmul_reduction); round_polys: (c0, c1, c2) per round.
+    Returns the input claim (point, value); raises GkrError (code 6) when a check fails."""
+    rp = q_array([q for t in round_polys for q in t])
+    npt = (GkrQM31 * 64)()
+    nn = C.c_uint32()
+    nv = GkrQM31()
+    _check(lib().gkr_verify_matmul_layer(q_array(claim_point), len(claim_point), C.byref(q_to_c(claim_value)), m, k,
+                                         n, rp, len(round_polys), C.byref(q_to_c(final_a)),
+                                         C.byref(q_to_c(final_b)), ch.handle, npt, C.byref(nn), C.byref(nv)))
+    return [q_from_c(npt[i]) for i in range(nn.value)], q_from_c(nv)
+
+
+def verify_mul_layer(claim_point, claim_value, proof, ch: PoseidonChannel):
+    """gkr_verify_mul_layer (verify_mul_reduction) on a proof dict as prove_mul_layer returns it."""
+    rp = q_array([q for t in proof["eq_round_polys"] for q in t])
+    nv = GkrQM31()
+    _check(lib().gkr_verify_mul_layer(q_array(claim_point), len(claim_point), C.byref(q_to_c(claim_value)), rp,
+                                      len(proof["eq_round_polys"]), C.byref(q_to_c(proof["lhs_eval"])),
+                                      C.byref(q_to_c(proof["rhs_eval"])), ch.handle, C.byref(nv)))
+    return q_from_c(nv)
+
+
+def verify_activation_layer(claim_point, act_type: int, table_log_size: int, proof, ch: PoseidonChannel):
+    """gkr_verify_activation_layer (LogUp branch of verify_activation_reduction) on a proof dict as
+    prove_activation_layer returns it.  Returns the input claim value."""
+    out = GkrLogupOut()
+    nr = len(proof["eq_round_polys"])
+    eq = q_array([q for t in proof["eq_round_polys"] for q in t])
+    mults = np.ascontiguousarray(proof["multiplicities"], dtype=np.uint32)
+    mrp = q_array([q for t in proof["mult_round_polys"] for q in t])
+    out.claimed_sum = q_to_c(proof["claimed_sum"])
+    out.eq_round_polys = C.cast(eq, _PQ)
+    out.w_eval, out.in_eval, out.out_eval = (q_to_c(x) for x in proof["final_evals"])
+    out.multiplicities = mults.ctypes.data_as(_U32P)
+    out.mult_round_polys = C.cast(mrp, _PQ)
+    out.mult_final_eval = q_to_c(proof["mult_final_eval"])
+    out.mult_claimed_sum = q_to_c(proof["mult_claimed_sum"])
+    out.input_eval = q_to_c(proof["input_eval"])
+    out.output_eval = q_to_c(proof["output_eval"])
+    out.table_commitment = felt_to_c(proof["table_commitment"])
+    nv = GkrQM31()
+    _check(lib().gkr_verify_activation_layer(q_array(claim_point), len(claim_point), act_type, table_log_size, nr,
+                                             C.byref(out), ch.handle, C.byref(nv)))
+    return q_from_c(nv)
+
+
+def verify_walk(calldata, shapes, init_point, init_value, ch: PoseidonChannel):
+    """gkr_verify_walk: a chained walk from serialized calldata (felt ints).  shapes: sequence of
+    (kind, rows, cols, cols_b, activation_type, table_log_size).  Returns (point, value, felts read)."""
+    cd = (GkrFelt * max(1, len(calldata)))()
+    for i, v in enumerate(calldata):
+        cd[i] = felt_to_c(v)
+    sh = (GkrLayerShape * max(1, len(shapes)))()
+    for i, (kind, rows, cols, cols_b, act, tlog) in enumerate(shapes):
+        sh[i].kind, sh[i].rows, sh[i].cols, sh[i].cols_b = kind, rows, cols, cols_b
+        sh[i].activation_type, sh[i].table_log_size = act, tlog
+    fp = (GkrQM31 * 64)()
+    nf = C.c_uint32()
+    fv = GkrQM31()
+    used = C.c_size_t()
+    _check(lib().gkr_verify_walk(cd, len(calldata), sh, len(shapes), q_array(init_point), len(init_point),
+                                 C.byref(q_to_c(init_value)), ch.handle, fp, C.byref(nf), C.byref(fv),
+                                 C.byref(used)))
+    return [q_from_c(fp[i]) for i in range(nf.value)], q_from_c(fv), used.value
 
 
 class Matrix:

@@ -149,3 +149,46 @@ def test_walk_with_mul_step(gpu_ctx):
     proof.set_input_claim(fp, fv)
     O.serialize_tail(ser, fp, fv, [], 0)
     assert proof.serialize() == ser
+
+
+def test_native_walk_proof_verifies(gpu_ctx):
+    """A chained walk proved on the GPU over a consistent circuit (H = X0 . W0, L = relu(H),
+    X = L (.) R, Y = X . W), serialized, then verified by the library's walk verifier from the same
+    starting transcript; a changed felt is rejected."""
+    log("case native walk verifies")
+    rng = np.random.default_rng(8)
+    X0 = rng.integers(0, P, size=(8, 40), dtype=np.uint32)
+    W0 = rng.integers(0, P, size=(40, 32), dtype=np.uint32)
+    H = O.matmul_forward(X0, W0)
+    L = np.vectorize(lambda x: O.activation(1, int(x)), otypes=[np.uint32])(H)
+    R = rng.integers(0, P, size=(8, 32), dtype=np.uint32)
+    X = ((L.astype(np.uint64) * R) % P).astype(np.uint32)
+    W = rng.integers(0, P, size=(32, 24), dtype=np.uint32)
+    gx0, gw0, gh, gl, gr, gx, gw = (gpu_ctx.upload(M) for M in (X0, W0, H, L, R, X, W))
+    ch = G.PoseidonChannel()
+    ch.seed_gkr(4, 8, 40)
+    start = ch.export_state()
+    r = ch.draw_qm31s(lg(8) + lg(24))
+    v = gpu_ctx.matmul_output_claim(gx, gw, r)
+    ch.mix_secure_field(v)
+    after_claim = ch.export_state()
+    steps = [(G.STEP_MATMUL, G.CLAIM_CHAINED, gx, gw, 0, 0), (G.STEP_MUL, G.CLAIM_CHAINED, gl, gr, 0, 0),
+             (G.STEP_ACTIVATION, G.CLAIM_CHAINED, gh, None, 1, 12), (G.STEP_MATMUL, G.CLAIM_CHAINED, gx0, gw0, 0, 0)]
+    proof = G.Proof()
+    fp, fv = G.prove_walk(gpu_ctx, ch, steps, proof, init_point=r, init_value=v)
+    proof.set_input_claim(fp, fv)
+    cd = proof.serialize()
+    shapes = [(G.STEP_MATMUL, 8, 32, 24, 0, 0), (G.STEP_MUL, 8, 32, 0, 0, 0), (G.STEP_ACTIVATION, 8, 32, 0, 1, 12),
+              (G.STEP_MATMUL, 8, 40, 32, 0, 0)]
+    vch = G.PoseidonChannel()
+    vch.import_state(after_claim)
+    pt, val, used = G.verify_walk(cd, shapes, r, v, vch)
+    assert (pt, val) == (fp, fv) and vch.digest() == ch.digest()
+    assert used == len(cd) - 3
+    assert start != after_claim
+    bad = list(cd)
+    bad[used // 2] = (bad[used // 2] + 1) % P
+    vch2 = G.PoseidonChannel()
+    vch2.import_state(after_claim)
+    with pytest.raises(G.GkrError):
+        G.verify_walk(bad, shapes, r, v, vch2)
