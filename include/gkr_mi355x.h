@@ -222,6 +222,21 @@ int gkr_sumcheck_product(gkr_ctx* ctx, const gkr_qvec* fa, const gkr_qvec* fb, g
                          gkr_qm31* round_polys /* 3T: c0, c1, c2 */, gkr_qm31* challenges /* T */,
                          gkr_qm31* final_a, gkr_qm31* final_b);
 
+/* MLE commitments: Poseidon Merkle roots (engine/src/crypto/poseidon_merkle.rs:255-280,
+ * root_only_parallel) over securefield_to_felt leaves (poseidon_channel.rs:59-69),
+ * padded with zero felts to a power of two (at least 2); node = poseidon_hash(l, r).
+ * Roots are canonical felts (8 little-endian u32 words).
+ *
+ * gkr_weight_commitment: the weight commitment of the GKR prover,
+ * commit_mle_root_only(matrix_to_mle_col_major_padded(B)) (engine/src/gkr/prover.rs:1021-1023,
+ * mle_opening.rs:630-641): B[i][j] at index j * next_pow2(rows) + i of the padded grid.
+ * gkr_weight_commitments: the same for `count` matrices in one batch (one root each,
+ * in order), the role of commit_mle_root_only_batch (mle_opening.rs:791-809).
+ * gkr_mle_commitment: commit_mle_root_only over the n QM31 values of `evals`. */
+int gkr_weight_commitment(gkr_ctx* ctx, const gkr_matrix* b, gkr_felt* root);
+int gkr_weight_commitments(gkr_ctx* ctx, const gkr_matrix* const* mats, size_t count, gkr_felt* roots);
+int gkr_mle_commitment(gkr_ctx* ctx, const gkr_qvec* evals, gkr_felt* root);
+
 /* Mul layer (element-wise product c = lhs * rhs), reduce_mul_layer
  * (engine/src/gkr/prover.rs:6172-6271): mix_u64(0x4D554C), mix the claim
  * value, a degree-3 eq-sumcheck over eq(r[..n_vars], x) * lhs(x) * rhs(x)

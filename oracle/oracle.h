@@ -86,6 +86,9 @@ int orc_prove_activation_layer(const uint32_t* claim_point, int n_point, const u
                                uint32_t* input_eval, uint32_t* table_commitment);
 
 /* ---------------------------------------------------------- verifier (verify.c) */
+/* MLE commitments (commit.c): Poseidon Merkle root over securefield_to_felt leaves. */
+void orc_mle_commitment(const uint32_t* evals_qm31, size_t len, uint32_t out[8]);
+void orc_weight_commitment(const uint32_t* B, size_t k, size_t n, uint32_t out[8]);
 /* The product-sumcheck round loop over QM31 vectors of length n (matmul.c). */
 int orc_sumcheck_product(const uint32_t* fa, const uint32_t* fb, size_t n, orc_channel* ch, uint32_t* round_polys,
                          uint32_t* challenges, uint32_t* final_a, uint32_t* final_b);

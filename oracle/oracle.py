@@ -55,6 +55,8 @@ def lib():
                                               C.c_int, _U32P, _U32P, C.c_void_p, _U32P, _U32P]
         L.orc_verify_activation_layer.argtypes = [_U32P, C.c_int, _U32P, C.c_uint32, C.c_uint32, _U32P, _U32P,
                                                   C.c_int] + [_U32P] * 6 + [C.c_void_p]
+        L.orc_mle_commitment.argtypes = [_U32P, C.c_size_t, _U32P]
+        L.orc_weight_commitment.argtypes = [_U32P, C.c_size_t, C.c_size_t, _U32P]
         L.orc_sumcheck_product.argtypes = [_U32P, _U32P, C.c_size_t, C.c_void_p, _U32P, _U32P, _U32P, _U32P]
         L.orc_reduce_mul_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, _U32P, C.c_size_t, C.c_void_p] + [_U32P] * 5
         L.orc_verify_mul_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, C.c_int, _U32P, _U32P, C.c_void_p, _U32P]
@@ -343,6 +345,22 @@ def verify_activation_layer(claim_point, claim_value, act_type: int, table_log: 
         _p(_qa([proof["claimed_sum"]])), _p(c), len(proof["eq_round_polys"]), _p(fe), _p(mults), _p(mrp),
         _p(_qa([proof["mult_final_eval"]])), _p(_qa([proof["mult_claimed_sum"]])), _p(_qa([proof["input_eval"]])),
         ch.buf))
+
+
+def weight_commitment(B: np.ndarray) -> int:
+    """commit_mle_root_only(matrix_to_mle_col_major_padded(B)) (mle_opening.rs:630; prover.rs:1021-1023)."""
+    B = np.ascontiguousarray(B, dtype=np.uint32)
+    out = np.zeros(8, dtype=np.uint32)
+    lib().orc_weight_commitment(_p(B), B.shape[0], B.shape[1], _p(out))
+    return felt_int(out)
+
+
+def mle_commitment(evals: np.ndarray) -> int:
+    """commit_mle_root_only over QM31 evaluations given as an (n, 4) array."""
+    e = np.ascontiguousarray(evals, dtype=np.uint32).reshape(-1, 4)
+    out = np.zeros(8, dtype=np.uint32)
+    lib().orc_mle_commitment(_p(e), e.shape[0], _p(out))
+    return felt_int(out)
 
 
 def synthetic_q(n: int, seed: int) -> np.ndarray:

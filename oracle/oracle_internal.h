@@ -46,6 +46,7 @@ fe fe_from_words(const uint32_t w[8]);
 void fe_to_words(fe x, uint32_t w[8]);
 fe fe_pack_m31s(const uint32_t* v, int n);
 fe fe_hash_many(const fe* in, size_t n);
+fe fe_hash2(fe a, fe b);
 
 /* matmul.c helpers shared with logup.c / verify.c */
 qm mle_evaluate(const qm* evals, int n_vars, const qm* point); /* copies evals */

@@ -245,6 +245,13 @@ static void hades(fe s[3]) {
   }
 }
 
+/* poseidon_hash(a, b) = hades([a, b, 2])[0] */
+fe fe_hash2(fe a, fe b) {
+  ensure_init();
+  fe s[3] = {a, b, fe_from_u64(2)};
+  hades(s);
+  return s[0];
+}
 fe fe_from_u64(uint64_t x) {
   ensure_init();
   uint64_t c[4] = {x, 0, 0, 0};

@@ -19,7 +19,9 @@
 #include "activations.h"
 #include "field.h"
 #include "kernels.h"
+#include "merkle.h"
 #include "poseidon.h"
+#include "poseidon9_host.h"
 #include "verifier.h"
 
 using namespace gkr;
@@ -80,7 +82,8 @@ static bool felt_abi_canonical(const gkr_felt& f) {
 // ------------------------------------------------------------------ context
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
-  S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_COLPART, S_NSLOTS
+  S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_COLPART,
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and two host-side phases
 // (Fiat-Shamir hashing inside the reducers, and waiting for device results).
@@ -144,6 +147,7 @@ struct gkr_ctx {
   std::set<gkr_matrix*> matrices;  // live matrices; detached when the context is destroyed
   std::set<gkr_qvec*> qvecs;       // live QM31 vectors; detached likewise
   uint64_t table_on_device = 0;    // (tag << 32 | log) of the table held in S_TABLE, 0 = none
+  MerkleConsts* merkle_consts = nullptr;  // device copy, built on first use
 };
 
 static int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
@@ -589,6 +593,7 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   }
   for (int s = 0; s < S_NSLOTS; s++)
     if (c->buf[s]) (void)hipFree(c->buf[s]);
+  if (c->merkle_consts) (void)hipFree(c->merkle_consts);
   if (c->h_res) (void)hipHostFree(c->h_res);
   if (c->h_mult) (void)hipHostFree(c->h_mult);
   if (c->h_vec) (void)hipHostFree(c->h_vec);
@@ -1784,6 +1789,193 @@ extern "C" int gkr_sumcheck_product(gkr_ctx* c, const gkr_qvec* fa, const gkr_qv
   qm31* bufs_b[2] = {b1, b2};
   return product_sumcheck(c, ch->ch, T, fa->dev, fb->dev, bufs_a, bufs_b, nullptr, nullptr, round_polys,
                           challenges, final_a, final_b);
+}
+
+/* ------------------------------------------------------------------ MLE commitments
+ * Poseidon Merkle roots (merkle.h).  A batch runs level by level: launch L
+ * moves every unfinished tree from level s to s + d, writing the real nodes
+ * of level s + d into buffer L % 2 and reading level s from the other one.
+ * d is the largest of 4..2 that still gives 2^18 output nodes over the
+ * batch, else 1 (the upper levels are latency-bound: one hash per thread per
+ * launch keeps them short). */
+struct MerkleTreeSpec {
+  uint32_t kind;  // 0 matrix, 1 QM31 vector
+  const uint32_t* src;
+  uint64_t rows, cols;
+  uint32_t log_pk, height;
+  uint64_t mle_len;
+};
+
+static uint32_t log2_ceil(uint64_t v) {
+  uint32_t l = 0;
+  while ((1ull << l) < v) l++;
+  return l;
+}
+
+static int merkle_consts(gkr_ctx* c, const MerkleConsts** out) {
+  if (!c->merkle_consts) {
+    const f9::setup& S = f9::host_setup();
+    std::unique_ptr<MerkleConsts> h(new MerkleConsts());
+    h->hk = S.k;
+    h->r2 = S.r2;
+    h->one = S.one;
+    const felt two124 = felt_to_mont(felt{{0, (uint64_t)1 << 60, 0, 0}});  // securefield_to_felt(0) = 2^124
+    felt z = two124, zz = felt_zero();
+    for (int s = 0; s < 64; s++) {
+      h->z[s] = f9::from_host_mont(z);
+      h->zz[s] = f9::from_host_mont(zz);
+      z = poseidon_hash(z, z);
+      zz = poseidon_hash(zz, zz);
+    }
+    MerkleConsts* d = nullptr;
+    HIP_TRY(hipMalloc(&d, sizeof(MerkleConsts)));
+    if (hipMemcpy(d, h.get(), sizeof(MerkleConsts), hipMemcpyHostToDevice) != hipSuccess) {
+      (void)hipFree(d);
+      return fail(GKR_ERR_DEVICE, "copy of the Merkle constants failed");
+    }
+    c->merkle_consts = d;
+  }
+  *out = c->merkle_consts;
+  return GKR_OK;
+}
+
+static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gkr_felt* roots) {
+  const size_t nt = trees.size();
+  if (nt == 0) return GKR_OK;
+  const MerkleConsts* K;
+  TRY(merkle_consts(c, &K));
+  struct Launch {
+    uint32_t s;
+    size_t first_step, n_steps;
+    uint64_t total;
+  };
+  std::vector<Launch> launches;
+  std::vector<MerkleStep> steps;
+  std::vector<uint64_t> step_off;  // node offset of each step's output in its buffer
+  std::vector<std::pair<size_t, size_t>> root_at(nt);  // (launch, step) producing each root
+  uint64_t need[2] = {1, 1};
+  uint32_t smax = 0;
+  for (const auto& t : trees) smax = std::max(smax, t.height);
+  for (uint32_t s = 0; s < smax;) {
+    auto outputs = [&](uint32_t D) {
+      uint64_t n = 0;
+      for (const auto& t : trees)
+        if (t.height > s) n += merkle_real_count(t.kind, t.rows, t.cols, t.log_pk, s + std::min(D, t.height - s));
+      return n;
+    };
+    uint32_t D = 1;
+    for (uint32_t cand = kMerkleMaxD; cand >= 2; cand--)
+      if (outputs(cand) >= (1ull << 18)) {
+        D = cand;
+        break;
+      }
+    Launch L{s, steps.size(), 0, 0};
+    uint64_t off = 0;
+    for (size_t i = 0; i < nt; i++) {
+      const auto& t = trees[i];
+      if (t.height <= s) continue;
+      MerkleStep st{};
+      st.src = t.src;
+      st.rows = t.rows;
+      st.cols = t.cols;
+      st.mle_len = t.mle_len;
+      st.kind = t.kind;
+      st.log_pk = t.log_pk;
+      st.d = std::min(D, t.height - s);
+      st.n_out = merkle_real_count(t.kind, t.rows, t.cols, t.log_pk, s + st.d);
+      st.thread_begin = L.total;
+      L.total += st.n_out;
+      step_off.push_back(off);
+      off += st.n_out;
+      if (s + st.d == t.height) root_at[i] = {launches.size(), steps.size()};
+      steps.push_back(st);
+    }
+    L.n_steps = steps.size() - L.first_step;
+    need[launches.size() & 1] = std::max(need[launches.size() & 1], off);
+    launches.push_back(L);
+    s += D;
+  }
+  f9::fe* buf[2];
+  TRY(ensureT(c, S_MK0, need[0], &buf[0]));
+  TRY(ensureT(c, S_MK1, need[1], &buf[1]));
+  void* droot;
+  TRY(ensure(c, S_MKROOT, nt * (sizeof(f9::fe) + sizeof(void*) + 32), &droot));
+  f9::fe* root_nodes = (f9::fe*)droot;
+  const f9::fe** dptr = (const f9::fe**)(root_nodes + nt);
+  uint32_t* dwords = (uint32_t*)(dptr + nt);
+  // wire the buffers: launch l writes buf[l & 1]; a tree's input is its previous
+  // output; a tree's last launch writes its root to root_nodes (later launches
+  // reuse the ping-pong buffers)
+  std::vector<const f9::fe*> prev(nt, nullptr);
+  for (size_t l = 0; l < launches.size(); l++) {
+    size_t k = launches[l].first_step;
+    for (size_t i = 0; i < nt; i++) {
+      if (trees[i].height <= launches[l].s) continue;
+      steps[k].in = prev[i];
+      steps[k].out = root_at[i].second == k ? root_nodes + i : buf[l & 1] + step_off[k];
+      prev[i] = steps[k].out;
+      k++;
+    }
+  }
+  MerkleStep* dsteps;
+  TRY(ensureT(c, S_MKSTEP, steps.size(), &dsteps));
+  HIP_TRY(hipMemcpyAsync(dsteps, steps.data(), steps.size() * sizeof(MerkleStep), hipMemcpyHostToDevice, c->stream));
+  for (const auto& L : launches) {
+    const uint64_t blocks = (L.total + kMerkleBlock - 1) / kMerkleBlock;
+    k_merkle_level<<<dim3((uint32_t)blocks), dim3(kMerkleBlock), 0, c->stream>>>(dsteps + L.first_step, (int)L.n_steps,
+                                                                              L.s, L.total, K);
+    HIP_TRY(hipGetLastError());
+  }
+  std::vector<const f9::fe*> rp(nt);
+  for (size_t i = 0; i < nt; i++) rp[i] = root_nodes + i;
+  HIP_TRY(hipMemcpyAsync(dptr, rp.data(), nt * sizeof(void*), hipMemcpyHostToDevice, c->stream));
+  k_merkle_roots<<<dim3((uint32_t)((nt + 63) / 64)), dim3(64), 0, c->stream>>>(dptr, (int)nt, K, dwords);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(hipMemcpyAsync(roots, dwords, nt * 32, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return GKR_OK;
+}
+
+static int weight_tree(const gkr_matrix* m, MerkleTreeSpec* t) {
+  if (!m || !m->dev || m->rows == 0 || m->cols == 0) return fail(GKR_ERR_INVALID, "weight commitment: empty matrix");
+  t->kind = 0;
+  t->src = m->dev;
+  t->rows = m->rows;
+  t->cols = m->cols;
+  t->log_pk = log2_ceil(m->rows);
+  const uint32_t log_pn = log2_ceil(m->cols);
+  if (t->log_pk + log_pn > 48) return fail(GKR_ERR_INVALID, "weight commitment: padded MLE above 2^48 entries");
+  t->mle_len = 1ull << (t->log_pk + log_pn);
+  t->height = std::max(1u, t->log_pk + log_pn);
+  return GKR_OK;
+}
+
+extern "C" int gkr_weight_commitment(gkr_ctx* c, const gkr_matrix* b, gkr_felt* root) {
+  if (!c || !root) return fail(GKR_ERR_INVALID, "null argument");
+  return gkr_weight_commitments(c, &b, 1, root);
+}
+
+extern "C" int gkr_weight_commitments(gkr_ctx* c, const gkr_matrix* const* mats, size_t count, gkr_felt* roots) {
+  if (!c || (count && (!mats || !roots))) return fail(GKR_ERR_INVALID, "null argument");
+  HIP_TRY(hipSetDevice(c->device));
+  std::vector<MerkleTreeSpec> trees(count);
+  for (size_t i = 0; i < count; i++) TRY(weight_tree(mats[i], &trees[i]));
+  return merkle_roots(c, trees, roots);
+}
+
+extern "C" int gkr_mle_commitment(gkr_ctx* c, const gkr_qvec* evals, gkr_felt* root) {
+  if (!c || !evals || !root) return fail(GKR_ERR_INVALID, "null argument");
+  if (evals->n == 0) return fail(GKR_ERR_INVALID, "MLE commitment: empty vector");
+  HIP_TRY(hipSetDevice(c->device));
+  MerkleTreeSpec t{};
+  t.kind = 1;
+  t.src = (const uint32_t*)evals->dev;
+  t.rows = evals->n;
+  t.cols = 1;
+  t.mle_len = evals->n;
+  t.height = std::max(1u, log2_ceil(evals->n));
+  if (t.height > 48) return fail(GKR_ERR_INVALID, "MLE commitment: above 2^48 entries");
+  return merkle_roots(c, {t}, root);
 }
 
 // ------------------------------------------------------------------ Mul layer

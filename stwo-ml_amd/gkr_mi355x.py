@@ -159,6 +159,9 @@ SIGNATURES = [
                                   C.c_uint32, _PQ, _P, _PQ, C.POINTER(C.c_uint32), _PQ, C.POINTER(C.c_size_t)]),
     ("gkr_prove_walk", C.c_int, [_P, _P, C.POINTER(GkrStep), C.c_size_t, _PQ, C.c_uint32, _PQ, _P, _PQ,
                                  C.POINTER(C.c_uint32), _PQ]),
+    ("gkr_weight_commitment", C.c_int, [_P, _P, _PF]),
+    ("gkr_weight_commitments", C.c_int, [_P, C.POINTER(_P), C.c_size_t, _PF]),
+    ("gkr_mle_commitment", C.c_int, [_P, _P, _PF]),
 ]
 
 
@@ -444,6 +447,25 @@ class Context:
                                 for t in range(T)],
                 "challenges": [q_from_c(chal[t]) for t in range(T)],
                 "final_a_eval": q_from_c(a), "final_b_eval": q_from_c(b)}
+
+    def weight_commitment(self, b: "Matrix") -> int:
+        """gkr_weight_commitment: commit_mle_root_only(matrix_to_mle_col_major_padded(B))."""
+        out = GkrFelt()
+        _check(lib().gkr_weight_commitment(self._h, b.handle, C.byref(out)))
+        return felt_from_c(out)
+
+    def weight_commitments(self, mats: Sequence["Matrix"]) -> List[int]:
+        """gkr_weight_commitments: one root per matrix, hashed as one batch."""
+        hs = (_P * max(1, len(mats)))(*[m.handle for m in mats])
+        out = (GkrFelt * max(1, len(mats)))()
+        _check(lib().gkr_weight_commitments(self._h, hs, len(mats), out))
+        return [felt_from_c(out[i]) for i in range(len(mats))]
+
+    def mle_commitment(self, evals: "QVec") -> int:
+        """gkr_mle_commitment: commit_mle_root_only over resident QM31 values."""
+        out = GkrFelt()
+        _check(lib().gkr_mle_commitment(self._h, evals.handle, C.byref(out)))
+        return felt_from_c(out)
 
     def _mul_result(self, out, eq, nv, claim_point):
         return {"eq_round_polys": [tuple(q_from_c(eq[4 * t + j]) for j in range(4)) for t in range(nv)],

@@ -150,3 +150,12 @@ def test_synthetic_generator_is_splitmix64():
         assert O.synthetic_value(0, seed, i) == (z >> 33)  # P is never hit in this range
         s = (z >> 32) % 255 - 127
         assert O.synthetic_value(1, seed, i) == (s if s >= 0 else P + s)
+
+
+def test_sp3_weight_commitment(golden):
+    """commit_mle_root_only(matrix_to_mle_col_major_padded(W)) for the SP3 weight (4 x 2,
+    w[i][j] = 2i + j + 1; engine/tests/artifacts/sp3_matmul_only_proof.json)."""
+    B = np.array([[2 * i + j + 1 for j in range(2)] for i in range(4)], dtype=np.uint32)
+    assert O.weight_commitment(B) == int(golden["sp3"]["weight_commitments"][0], 16)
+    # the row-major layout of the same matrix commits to something else
+    assert O.weight_commitment(np.ascontiguousarray(B.T)) != int(golden["sp3"]["weight_commitments"][0], 16)

@@ -315,3 +315,31 @@ def test_sumcheck_product_identities(n):
     assert res["final_b_eval"] == Q.mle_bruteforce(B, res["challenges"])
     assert cur == Q.qmul(res["final_a_eval"], res["final_b_eval"])
     assert rep.digest() == ch.digest()
+
+
+def _tree_root(leaves):
+    n = 2
+    while n < len(leaves):
+        n *= 2
+    level = list(leaves) + [0] * (n - len(leaves))
+    while len(level) > 1:
+        level = [O.hades([level[i], level[i + 1], 2])[0] for i in range(0, len(level), 2)]
+    return level[0]
+
+
+@pytest.mark.parametrize("k,n", [(1, 1), (1, 2), (3, 1), (3, 5), (4, 4), (6, 3)])
+def test_weight_commitment_bruteforce(k, n):
+    """Merkle root spelled out: leaf (1 << 124) | (v << 93) at index j * pk + i, zero leaves and
+    zero MLE padding, node = hades([l, r, 2])[0]."""
+    rng = np.random.default_rng(k * 10 + n)
+    B = rng.integers(0, P, size=(k, n), dtype=np.uint32)
+    pk = 1 << max(0, (k - 1).bit_length())
+    pn = 1 << max(0, (n - 1).bit_length())
+    leaves = [1 << 124] * (pk * pn)
+    for i in range(k):
+        for j in range(n):
+            leaves[j * pk + i] = (1 << 124) | (int(B[i, j]) << 93)
+    assert O.weight_commitment(B) == _tree_root(leaves)
+    q = rng.integers(0, P, size=(5, 4), dtype=np.uint32)
+    packed = [(1 << 124) | (int(a) << 93) | (int(b) << 62) | (int(c) << 31) | int(d) for a, b, c, d in q]
+    assert O.mle_commitment(q) == _tree_root(packed)
