@@ -237,6 +237,25 @@ int gkr_weight_commitment(gkr_ctx* ctx, const gkr_matrix* b, gkr_felt* root);
 int gkr_weight_commitments(gkr_ctx* ctx, const gkr_matrix* const* mats, size_t count, gkr_felt* roots);
 int gkr_mle_commitment(gkr_ctx* ctx, const gkr_qvec* evals, gkr_felt* root);
 
+/* Weight openings: prove_mle_opening_with_commitment (mle_opening.rs:1654-1915)
+ * over matrix_to_mle_col_major_padded(B) at eval_point (log2(next_pow2(rows)) +
+ * log2(next_pow2(cols)) values, the first folding the top variable): mixes the
+ * commitment and the roots of the folded layers, draws 10 query pairs
+ * (MLE_N_QUERIES, mle_opening.rs:47; fewer when the MLE has under 20 values)
+ * and appends the commitment and the opening (claim point, expected value,
+ * MleOpeningProof, laid out as cairo_serde.rs:1759-1767) to `proof`, so that
+ * gkr_proof_serialize emits them.  expected_value, when not NULL, must equal
+ * the MLE at the point (GKR_ERR_INVALID otherwise).  `commitment` may be NULL.
+ *
+ * gkr_prove_weight_openings: the sequential weight-opening phase of the GKR
+ * prover (prover.rs:2059-2200, main channel, no sub-channels): opens, in
+ * proving order, the claim MLE(B)(r_j || sumcheck challenges) = final_b that
+ * every MatMul layer proved into `proof` recorded (prover.rs:1465-1483), then
+ * forgets the claims.  The weight matrices must still be alive.             */
+int gkr_prove_weight_opening(gkr_ctx* ctx, const gkr_matrix* b, const gkr_qm31* eval_point, uint32_t n_point,
+                             const gkr_qm31* expected_value, gkr_channel* ch, gkr_proof* proof, gkr_felt* commitment);
+int gkr_prove_weight_openings(gkr_ctx* ctx, gkr_channel* ch, gkr_proof* proof);
+
 /* Mul layer (element-wise product c = lhs * rhs), reduce_mul_layer
  * (engine/src/gkr/prover.rs:6172-6271): mix_u64(0x4D554C), mix the claim
  * value, a degree-3 eq-sumcheck over eq(r[..n_vars], x) * lhs(x) * rhs(x)

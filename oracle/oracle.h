@@ -51,6 +51,7 @@ void orc_draw_felt252(orc_channel* ch, uint32_t out[8]);
 void orc_draw_qm31(orc_channel* ch, uint32_t out[4]);
 void orc_draw_qm31s(orc_channel* ch, size_t n, uint32_t* out);
 void orc_digest(const orc_channel* ch, uint32_t out[8]);
+void orc_channel_set_state(orc_channel* ch, const uint32_t st[11]);
 size_t orc_channel_size(void);
 
 /* ---------------------------------------------------------- MLE / matmul (matmul.c) */
@@ -89,6 +90,8 @@ int orc_prove_activation_layer(const uint32_t* claim_point, int n_point, const u
 /* MLE commitments (commit.c): Poseidon Merkle root over securefield_to_felt leaves. */
 void orc_mle_commitment(const uint32_t* evals_qm31, size_t len, uint32_t out[8]);
 void orc_weight_commitment(const uint32_t* B, size_t k, size_t n, uint32_t out[8]);
+size_t orc_mle_opening(const uint32_t* evals, size_t len, const uint32_t* challenges, size_t n_queries_cfg,
+                       orc_channel* ch, uint32_t commitment[8], uint32_t* out, size_t cap);
 /* The product-sumcheck round loop over QM31 vectors of length n (matmul.c). */
 int orc_sumcheck_product(const uint32_t* fa, const uint32_t* fb, size_t n, orc_channel* ch, uint32_t* round_polys,
                          uint32_t* challenges, uint32_t* final_a, uint32_t* final_b);

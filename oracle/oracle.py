@@ -56,6 +56,8 @@ def lib():
         L.orc_verify_activation_layer.argtypes = [_U32P, C.c_int, _U32P, C.c_uint32, C.c_uint32, _U32P, _U32P,
                                                   C.c_int] + [_U32P] * 6 + [C.c_void_p]
         L.orc_mle_commitment.argtypes = [_U32P, C.c_size_t, _U32P]
+        L.orc_mle_opening.restype = C.c_size_t
+        L.orc_mle_opening.argtypes = [_U32P, C.c_size_t, _U32P, C.c_size_t, C.c_void_p, _U32P, _U32P, C.c_size_t]
         L.orc_weight_commitment.argtypes = [_U32P, C.c_size_t, C.c_size_t, _U32P]
         L.orc_sumcheck_product.argtypes = [_U32P, _U32P, C.c_size_t, C.c_void_p, _U32P, _U32P, _U32P, _U32P]
         L.orc_reduce_mul_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, _U32P, C.c_size_t, C.c_void_p] + [_U32P] * 5
@@ -145,6 +147,11 @@ def channel_state(ch: "Channel") -> List[int]:
     n_draws = int.from_bytes(raw[32:36], "little")
     hash_count = int.from_bytes(raw[40:48], "little")
     return words + [n_draws, hash_count & 0xFFFFFFFF, hash_count >> 32]
+
+
+def set_channel_state(ch: "Channel", st) -> None:
+    """Load a to_gpu_state layout (11 words, see channel_state) into an oracle channel."""
+    lib().orc_channel_set_state(ch.buf, _p(np.ascontiguousarray(st, dtype=np.uint32)))
 
 
 def hash_many(xs: Sequence[int]) -> int:
@@ -363,6 +370,27 @@ def mle_commitment(evals: np.ndarray) -> int:
     return felt_int(out)
 
 
+def col_major_mle(B: np.ndarray) -> np.ndarray:
+    """matrix_to_mle_col_major_padded (prover.rs:1021-1023): (pk * pn, 4) QM31 array, B[i][j] at j * pk + i."""
+    r, c = B.shape
+    pk, pn = 1 << max(0, (r - 1).bit_length()), 1 << max(0, (c - 1).bit_length())
+    out = np.zeros((pn, pk, 4), dtype=np.uint32)
+    out[:c, :r, 0] = (np.asarray(B, dtype=np.uint64) % P).T
+    return out.reshape(-1, 4)
+
+
+def mle_opening(evals: np.ndarray, challenges, ch: Channel, n_queries: int = 10):
+    """prove_mle_opening_with_commitment (mle_opening.rs:1654-1915): (commitment, serialized proof felts)."""
+    e = np.ascontiguousarray(evals, dtype=np.uint32).reshape(-1, 4)
+    chal = _qa(challenges) if len(challenges) else np.zeros(4, dtype=np.uint32)
+    cm = np.zeros(8, dtype=np.uint32)
+    probe = ch.clone()  # sizing pass on a copy; the real pass advances ch
+    n = lib().orc_mle_opening(_p(e), e.shape[0], _p(chal), n_queries, probe.buf, _p(cm), None, 0)
+    out = np.zeros((max(1, n), 8), dtype=np.uint32)
+    lib().orc_mle_opening(_p(e), e.shape[0], _p(chal), n_queries, ch.buf, _p(cm), _p(out), n)
+    return felt_int(cm), [felt_int(out[i]) for i in range(n)]
+
+
 def synthetic_q(n: int, seed: int) -> np.ndarray:
     """n uniform QM31 values, four consecutive kind-0 draws each: (n, 4) array."""
     out = np.empty((n, 4), dtype=np.uint32)
@@ -516,3 +544,73 @@ def serialize_tail(out: list, input_point, input_value, weight_commitments, io_c
     out.extend(int(c) for c in weight_commitments)
     out.append(n_weight_openings)
     out.append(int(io_commitment))
+
+
+def parse_mle_opening(felts, pos: int = 0):
+    """Read a serialized MleOpeningProof (cairo_serde.rs:341-369) at felts[pos:]; returns (proof, next pos)."""
+    def u():
+        nonlocal pos
+        pos += 1
+        return int(felts[pos - 1])
+
+    def q():
+        return tuple(u() for _ in range(4))
+
+    roots = [u() for _ in range(u())]
+    queries = []
+    for _ in range(u()):
+        idx, rounds = u(), []
+        for _ in range(u()):
+            lv, rv = q(), q()
+            ls = [u() for _ in range(u())]
+            rs = [u() for _ in range(u())]
+            rounds.append((lv, rv, ls, rs))
+        queries.append((idx, rounds))
+    return {"intermediate_roots": roots, "queries": queries, "final_value": q()}, pos
+
+
+def _securefield_felt(v) -> int:
+    a, b, c, d = (int(x) for x in v)
+    return (1 << 124) | (a << 93) | (b << 62) | (c << 31) | d
+
+
+def _merkle_verify(root: int, index: int, leaf: int, siblings) -> bool:
+    """PoseidonMerkleTree::verify (poseidon_merkle.rs): hash up the path, left/right by the index bits."""
+    cur = leaf
+    for s in siblings:
+        cur = hades([s, cur, 2])[0] if index & 1 else hades([cur, s, 2])[0]
+        index >>= 1
+    return cur == root
+
+
+def verify_mle_opening(commitment: int, proof, challenges, ch: Channel, n_queries: int = 10) -> bool:
+    """verify_mle_opening (mle_opening.rs:1918-2028)."""
+    ch.mix_felt(commitment)
+    for r in proof["intermediate_roots"]:
+        ch.mix_felt(r)
+    n = len(challenges)
+    if n == 0:
+        return not proof["queries"]
+    half = 1 << (n - 1)
+    nq = min(n_queries, half)
+    idxs = [(ch.draw_felt252() & ((1 << 64) - 1)) % half for _ in range(nq)]
+    if len(proof["queries"]) != nq:
+        return False
+    roots = [commitment] + list(proof["intermediate_roots"])
+    for (pair, rounds), want in zip(proof["queries"], idxs):
+        if pair != want or len(rounds) != n:
+            return False
+        cur, size = pair, 1 << n
+        for t, (lv, rv, ls, rs) in enumerate(rounds):
+            mid = size // 2
+            if t < len(roots):
+                if not _merkle_verify(roots[t], cur, _securefield_felt(lv), ls):
+                    return False
+                if not _merkle_verify(roots[t], mid + cur, _securefield_felt(rv), rs):
+                    return False
+            folded = qadd(lv, qmul(challenges[t], qsub(rv, lv)))
+            if t == n - 1 and tuple(folded) != tuple(proof["final_value"]):
+                return False
+            cur %= max(mid // 2, 1)
+            size = mid
+    return True

@@ -392,3 +392,12 @@ void orc_draw_qm31s(orc_channel* ch, size_t n, uint32_t* out) {
   for (size_t i = 0; i < n; i++) orc_draw_qm31(ch, out + 4 * i);
 }
 void orc_digest(const orc_channel* ch, uint32_t out[8]) { fe_to_words(ch_digest(ch), out); }
+/* Channel state in the to_gpu_state layout (poseidon_channel.rs:109-135): 8 LE words of the
+ * canonical digest, n_draws, hash_count lo, hash_count hi. */
+void orc_channel_set_state(orc_channel* ch, const uint32_t st[11]) {
+  ensure_init();
+  const fe d = fe_from_words(st);
+  memcpy(ch->digest, d.v, 32);
+  ch->n_draws = st[8];
+  ch->hash_count = (uint64_t)st[9] | ((uint64_t)st[10] << 32);
+}

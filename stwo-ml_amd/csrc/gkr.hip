@@ -83,7 +83,7 @@ static bool felt_abi_canonical(const gkr_felt& f) {
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_NSLOTS
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and two host-side phases
 // (Fiat-Shamir hashing inside the reducers, and waiting for device results).
@@ -1042,11 +1042,20 @@ struct LayerRec {
   std::vector<qm31> mult_rp;  // c0,c1 per round
   qm31 mult_final, mult_sum;
 };
+// A MatMul layer's claim on its weight: MLE(B)(r_j || sumcheck challenges) =
+// final_b (push_matmul_weight_data, prover.rs:1465-1483).
+struct WeightClaimRec {
+  const gkr_matrix* b;
+  std::vector<qm31> point;
+  qm31 value;
+};
 struct gkr_proof {
   std::vector<LayerRec> layers;
   std::vector<qm31> in_point;
   qm31 in_value = {0, 0, 0, 0};
   std::vector<felt> weight_commitments;
+  std::vector<WeightClaimRec> weight_claims;      // recorded by the MatMul layers, in proving order
+  std::vector<std::vector<felt>> weight_openings;  // serialized opening records (claim + MleOpeningProof)
   felt io_commitment = {{0, 0, 0, 0}};
 };
 extern "C" int gkr_proof_new(gkr_proof** out) {
@@ -1160,7 +1169,9 @@ static void serialize_proof(const gkr_proof* p, Ser& s) {
   s.q(p->in_value);
   s.u(p->weight_commitments.size());
   for (const felt& w : p->weight_commitments) s.f(w);
-  s.u(0);  // weight opening proofs are not produced here
+  s.u(p->weight_openings.size());  // cairo_serde.rs:1756-1767
+  for (const auto& rec : p->weight_openings)
+    for (const felt& f : rec) s.f(f);
   s.f(p->io_commitment);
 }
 extern "C" int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out) {
@@ -1212,6 +1223,12 @@ extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, u
     L.final_a = Q(*final_a);
     L.final_b = Q(*final_b);
     proof->layers.push_back(L);
+    WeightClaimRec w;
+    w.b = b;
+    for (uint32_t l = 0; l < log_n; l++) w.point.push_back(Q(claim_point[log_m + l]));
+    for (int t = 0; t < T; t++) w.point.push_back(Q(chal[t]));
+    w.value = Q(*final_b);
+    proof->weight_claims.push_back(std::move(w));
   }
   return GKR_OK;
 }
@@ -1839,7 +1856,11 @@ static int merkle_consts(gkr_ctx* c, const MerkleConsts** out) {
   return GKR_OK;
 }
 
-static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gkr_felt* roots) {
+// kept == nullptr: roots only (ping-pong level buffers).  Otherwise every level
+// of every tree is kept in one arena (one level per launch) and described in
+// (*kept)[i] for path extraction; the arena stays valid until the next call.
+static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gkr_felt* roots,
+                        std::vector<MerkleKept>* kept = nullptr) {
   const size_t nt = trees.size();
   if (nt == 0) return GKR_OK;
   const MerkleConsts* K;
@@ -1851,9 +1872,9 @@ static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gk
   };
   std::vector<Launch> launches;
   std::vector<MerkleStep> steps;
-  std::vector<uint64_t> step_off;  // node offset of each step's output in its buffer
+  std::vector<uint64_t> step_off;  // node offset of each step's output in its buffer (arena when kept)
   std::vector<std::pair<size_t, size_t>> root_at(nt);  // (launch, step) producing each root
-  uint64_t need[2] = {1, 1};
+  uint64_t need[2] = {1, 1}, arena = 0;
   uint32_t smax = 0;
   for (const auto& t : trees) smax = std::max(smax, t.height);
   for (uint32_t s = 0; s < smax;) {
@@ -1864,11 +1885,12 @@ static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gk
       return n;
     };
     uint32_t D = 1;
-    for (uint32_t cand = kMerkleMaxD; cand >= 2; cand--)
-      if (outputs(cand) >= (1ull << 18)) {
-        D = cand;
-        break;
-      }
+    if (!kept)
+      for (uint32_t cand = kMerkleMaxD; cand >= 2; cand--)
+        if (outputs(cand) >= (1ull << 18)) {
+          D = cand;
+          break;
+        }
     Launch L{s, steps.size(), 0, 0};
     uint64_t off = 0;
     for (size_t i = 0; i < nt; i++) {
@@ -1885,8 +1907,9 @@ static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gk
       st.n_out = merkle_real_count(t.kind, t.rows, t.cols, t.log_pk, s + st.d);
       st.thread_begin = L.total;
       L.total += st.n_out;
-      step_off.push_back(off);
+      step_off.push_back(kept ? arena : off);
       off += st.n_out;
+      arena += st.n_out;
       if (s + st.d == t.height) root_at[i] = {launches.size(), steps.size()};
       steps.push_back(st);
     }
@@ -1895,24 +1918,45 @@ static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gk
     launches.push_back(L);
     s += D;
   }
-  f9::fe* buf[2];
-  TRY(ensureT(c, S_MK0, need[0], &buf[0]));
-  TRY(ensureT(c, S_MK1, need[1], &buf[1]));
+  f9::fe* buf[2] = {nullptr, nullptr};
+  if (kept) {
+    TRY(ensureT(c, S_MK0, arena, &buf[0]));
+    kept->assign(nt, MerkleKept{});
+    for (size_t i = 0; i < nt; i++) {
+      MerkleKept& k = (*kept)[i];
+      k.src = trees[i].src;
+      k.rows = trees[i].rows;
+      k.cols = trees[i].cols;
+      k.mle_len = trees[i].mle_len;
+      k.kind = trees[i].kind;
+      k.log_pk = trees[i].log_pk;
+      k.height = trees[i].height;
+    }
+  } else {
+    TRY(ensureT(c, S_MK0, need[0], &buf[0]));
+    TRY(ensureT(c, S_MK1, need[1], &buf[1]));
+  }
   void* droot;
   TRY(ensure(c, S_MKROOT, nt * (sizeof(f9::fe) + sizeof(void*) + 32), &droot));
   f9::fe* root_nodes = (f9::fe*)droot;
   const f9::fe** dptr = (const f9::fe**)(root_nodes + nt);
   uint32_t* dwords = (uint32_t*)(dptr + nt);
-  // wire the buffers: launch l writes buf[l & 1]; a tree's input is its previous
-  // output; a tree's last launch writes its root to root_nodes (later launches
-  // reuse the ping-pong buffers)
+  // wire the buffers: a tree's input is its previous output.  Roots only:
+  // launch l writes buf[l & 1], and a tree's last launch writes its root to
+  // root_nodes (later launches reuse the ping-pong buffers).  Kept: every
+  // output has its own place in the arena.
   std::vector<const f9::fe*> prev(nt, nullptr);
   for (size_t l = 0; l < launches.size(); l++) {
     size_t k = launches[l].first_step;
     for (size_t i = 0; i < nt; i++) {
       if (trees[i].height <= launches[l].s) continue;
       steps[k].in = prev[i];
-      steps[k].out = root_at[i].second == k ? root_nodes + i : buf[l & 1] + step_off[k];
+      if (kept) {
+        steps[k].out = buf[0] + step_off[k];
+        (*kept)[i].level[launches[l].s + steps[k].d] = steps[k].out;
+      } else {
+        steps[k].out = root_at[i].second == k ? root_nodes + i : buf[l & 1] + step_off[k];
+      }
       prev[i] = steps[k].out;
       k++;
     }
@@ -1927,7 +1971,7 @@ static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gk
     HIP_TRY(hipGetLastError());
   }
   std::vector<const f9::fe*> rp(nt);
-  for (size_t i = 0; i < nt; i++) rp[i] = root_nodes + i;
+  for (size_t i = 0; i < nt; i++) rp[i] = kept ? steps[root_at[i].second].out : root_nodes + i;
   HIP_TRY(hipMemcpyAsync(dptr, rp.data(), nt * sizeof(void*), hipMemcpyHostToDevice, c->stream));
   k_merkle_roots<<<dim3((uint32_t)((nt + 63) / 64)), dim3(64), 0, c->stream>>>(dptr, (int)nt, K, dwords);
   HIP_TRY(hipGetLastError());
@@ -1976,6 +2020,179 @@ extern "C" int gkr_mle_commitment(gkr_ctx* c, const gkr_qvec* evals, gkr_felt* r
   t.height = std::max(1u, log2_ceil(evals->n));
   if (t.height > 48) return fail(GKR_ERR_INVALID, "MLE commitment: above 2^48 entries");
   return merkle_roots(c, {t}, root);
+}
+
+/* ------------------------------------------------------------------ weight openings
+ * prove_mle_opening_with_commitment (engine/src/crypto/mle_opening.rs:1654-1915)
+ * over matrix_to_mle_col_major_padded(B):
+ *   layer 0 = the padded MLE (read from B), layer t+1 = fold of layer t on its
+ *   top variable with eval_point[t]; the Merkle tree of every layer longer
+ *   than 1 is built once with all its levels kept (the reference rebuilds
+ *   them for the query phase); roots are mixed in layer order; query pairs are
+ *   drawn (low 64 bits of draw_felt252 mod len/2, then mod max(mid/2, 1) per
+ *   round); values and auth paths are gathered on the device.
+ * Layers 1..log2(pn) keep B's zero rows (a grid with `rows` real rows, kind 2
+ * trees); later layers are plain QM31 vectors (kind 1).  The record holds the
+ * serialized claim and MleOpeningProof (cairo_serde.rs:341-369, 1759-1767). */
+constexpr size_t kMleQueries = 10;  // MLE_N_QUERIES, mle_opening.rs:47
+
+static int weight_opening(gkr_ctx* c, const gkr_matrix* b, const gkr_qm31* point, uint32_t n_point,
+                          const gkr_qm31* expected, PoseidonChannel& C, felt* commitment, std::vector<felt>& rec) {
+  MerkleTreeSpec t0;
+  TRY(weight_tree(b, &t0));
+  const uint32_t log_pk = t0.log_pk, log_pn = log2_ceil(b->cols), nv = log_pk + log_pn;
+  if (n_point != nv) return fail(GKR_ERR_INVALID, "weight opening: point has %u vars, the padded MLE has %u", n_point, nv);
+  for (uint32_t t = 0; t < nv; t++)
+    if (!canonical_q(point[t])) return fail(GKR_ERR_INVALID, "weight opening: point not canonical");
+  const uint64_t N = 1ull << nv;
+  // folded layers 1..nv, back to back (N - 1 values)
+  qm31* lay = nullptr;
+  TRY(ensureT(c, S_OPL, N, &lay));
+  std::vector<qm31*> L(nv + 1, nullptr);
+  for (uint64_t t = 1, off = 0; t <= nv; t++) {
+    L[t] = lay + off;
+    off += N >> t;
+  }
+  for (uint32_t t = 0; t < nv; t++) {
+    const uint64_t mid = N >> (t + 1);
+    const uint32_t blocks = (uint32_t)((mid + 255) / 256);
+    if (t == 0)
+      k_open_fold_matrix<<<dim3(blocks), dim3(256), 0, c->stream>>>(b->dev, b->rows, b->cols, log_pk, mid,
+                                                                    Q(point[0]), L[1]);
+    else
+      k_open_fold<<<dim3(blocks), dim3(256), 0, c->stream>>>(L[t], mid, Q(point[t]), L[t + 1]);
+    HIP_TRY(hipGetLastError());
+  }
+  // trees of layers 0..nv-1 (layer 0 also when nv == 0: one leaf padded to two)
+  std::vector<MerkleTreeSpec> trees(1, t0);
+  for (uint32_t t = 1; t < nv; t++) {
+    MerkleTreeSpec s{};
+    s.src = (const uint32_t*)L[t];
+    s.mle_len = N >> t;
+    s.height = nv - t;
+    if (t <= log_pn) {
+      s.kind = 2;
+      s.rows = b->rows;
+      s.cols = 1ull << (log_pn - t);
+      s.log_pk = log_pk;
+    } else {
+      s.kind = 1;
+      s.rows = N >> t;
+      s.cols = 1;
+    }
+    trees.push_back(s);
+  }
+  std::vector<gkr_felt> roots(trees.size());
+  std::vector<MerkleKept> kept;
+  TRY(merkle_roots(c, trees, roots.data(), &kept));
+  qm31 final_value;
+  if (nv == 0) {
+    uint32_t v;
+    HIP_TRY(hipMemcpy(&v, b->dev, 4, hipMemcpyDeviceToHost));
+    final_value = qm31_from_m31(v);
+  } else {
+    HIP_TRY(hipMemcpy(&final_value, L[nv], sizeof(qm31), hipMemcpyDeviceToHost));
+  }
+  if (expected && !qm31_eq(final_value, Q(*expected)))
+    return fail(GKR_ERR_INVALID, "weight opening: the MLE at the point differs from the expected value");
+  std::vector<felt> rf(trees.size());
+  for (size_t t = 0; t < trees.size(); t++) rf[t] = felt_canon_from_words(roots[t].w);
+  *commitment = rf[0];
+  for (size_t t = 0; t < trees.size(); t++) C.mix_felt(felt_to_mont(rf[t]));
+  // queries
+  const uint64_t half = N / 2;
+  const size_t nq = (size_t)std::min<uint64_t>(kMleQueries, half);
+  std::vector<uint64_t> pairs(nq);
+  for (size_t q = 0; q < nq; q++) {
+    const felt f = felt_from_mont(C.draw_felt252());
+    pairs[q] = f.l[0] % half;
+  }
+  std::vector<MerkleGather> items;
+  for (size_t q = 0; q < nq; q++) {
+    uint64_t idx = pairs[q];
+    for (uint32_t t = 0; t < nv; t++) {
+      const uint64_t mid = (N >> t) / 2, li = idx, ri = mid + idx;
+      items.push_back(MerkleGather{t, 0, 1, 0, li});
+      items.push_back(MerkleGather{t, 0, 1, 0, ri});
+      for (uint64_t k0 : {li, ri}) {
+        uint64_t k = k0;
+        for (uint32_t lv = 0; lv < trees[t].height; lv++) {
+          items.push_back(MerkleGather{t, lv, 0, 0, k ^ 1});
+          k >>= 1;
+        }
+      }
+      idx %= std::max<uint64_t>(mid / 2, 1);
+    }
+  }
+  std::vector<uint32_t> got(8 * items.size());
+  if (!items.empty()) {
+    void* dio;
+    const size_t kbytes = kept.size() * sizeof(MerkleKept), ibytes = items.size() * sizeof(MerkleGather);
+    TRY(ensure(c, S_OPI, kbytes + ibytes + got.size() * 4, &dio));
+    MerkleKept* dk = (MerkleKept*)dio;
+    MerkleGather* di = (MerkleGather*)((char*)dio + kbytes);
+    uint32_t* dout = (uint32_t*)((char*)dio + kbytes + ibytes);
+    HIP_TRY(hipMemcpyAsync(dk, kept.data(), kbytes, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(di, items.data(), ibytes, hipMemcpyHostToDevice, c->stream));
+    const MerkleConsts* K;
+    TRY(merkle_consts(c, &K));
+    k_merkle_gather<<<dim3((uint32_t)((items.size() + 63) / 64)), dim3(64), 0, c->stream>>>(dk, di, (int)items.size(),
+                                                                                          K, dout);
+    HIP_TRY(hipGetLastError());
+    HIP_TRY(hipMemcpyAsync(got.data(), dout, got.size() * 4, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+  }
+  // record: claim point, expected value, MleOpeningProof
+  auto fu = [&](uint64_t v) { rec.push_back(felt{{v, 0, 0, 0}}); };
+  auto fq = [&](const qm31& x) { fu(x.a); fu(x.b); fu(x.c); fu(x.d); };
+  fu(nv);
+  for (uint32_t t = 0; t < nv; t++) fq(Q(point[t]));
+  fq(expected ? Q(*expected) : final_value);
+  fu(nv > 0 ? nv - 1 : 0);
+  for (uint32_t t = 1; t < nv; t++) rec.push_back(rf[t]);
+  fu(nq);
+  size_t it = 0;
+  for (size_t q = 0; q < nq; q++) {
+    fu(pairs[q]);
+    fu(nv);
+    for (uint32_t t = 0; t < nv; t++) {
+      for (int side = 0; side < 2; side++, it++) fq(qm31{got[8 * it], got[8 * it + 1], got[8 * it + 2], got[8 * it + 3]});
+      for (int side = 0; side < 2; side++) {
+        fu(trees[t].height);
+        for (uint32_t lv = 0; lv < trees[t].height; lv++, it++) rec.push_back(felt_canon_from_words(&got[8 * it]));
+      }
+    }
+  }
+  fq(final_value);
+  return GKR_OK;
+}
+
+extern "C" int gkr_prove_weight_opening(gkr_ctx* c, const gkr_matrix* b, const gkr_qm31* eval_point, uint32_t n_point,
+                                        const gkr_qm31* expected_value, gkr_channel* ch, gkr_proof* proof,
+                                        gkr_felt* commitment) {
+  CH_CHECK(ch);
+  if (!c || !b || !proof || (!eval_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
+  if (expected_value && !canonical_q(*expected_value)) return fail(GKR_ERR_INVALID, "expected value not canonical");
+  HIP_TRY(hipSetDevice(c->device));
+  felt cm;
+  std::vector<felt> rec;
+  TRY(weight_opening(c, b, eval_point, n_point, expected_value, ch->ch, &cm, rec));
+  proof->weight_commitments.push_back(cm);
+  proof->weight_openings.push_back(std::move(rec));
+  if (commitment) felt_canon_to_words(cm, commitment->w);
+  return GKR_OK;
+}
+
+extern "C" int gkr_prove_weight_openings(gkr_ctx* c, gkr_channel* ch, gkr_proof* proof) {
+  CH_CHECK(ch);
+  if (!c || !proof) return fail(GKR_ERR_INVALID, "null argument");
+  for (const WeightClaimRec& w : proof->weight_claims) {
+    const gkr_qm31* pt = reinterpret_cast<const gkr_qm31*>(w.point.data());
+    const gkr_qm31 v = {{w.value.a, w.value.b, w.value.c, w.value.d}};
+    TRY(gkr_prove_weight_opening(c, w.b, pt, (uint32_t)w.point.size(), &v, ch, proof, nullptr));
+  }
+  proof->weight_claims.clear();
+  return GKR_OK;
 }
 
 // ------------------------------------------------------------------ Mul layer

@@ -162,6 +162,8 @@ SIGNATURES = [
     ("gkr_weight_commitment", C.c_int, [_P, _P, _PF]),
     ("gkr_weight_commitments", C.c_int, [_P, C.POINTER(_P), C.c_size_t, _PF]),
     ("gkr_mle_commitment", C.c_int, [_P, _P, _PF]),
+    ("gkr_prove_weight_opening", C.c_int, [_P, _P, _PQ, C.c_uint32, _PQ, _P, _P, _PF]),
+    ("gkr_prove_weight_openings", C.c_int, [_P, _P, _P]),
 ]
 
 
@@ -466,6 +468,19 @@ class Context:
         out = GkrFelt()
         _check(lib().gkr_mle_commitment(self._h, evals.handle, C.byref(out)))
         return felt_from_c(out)
+
+    def prove_weight_opening(self, b: "Matrix", eval_point, ch: PoseidonChannel, proof: "Proof",
+                             expected_value=None) -> int:
+        """gkr_prove_weight_opening: opening appended to proof; returns the commitment."""
+        cm = GkrFelt()
+        ev = C.byref(q_to_c(expected_value)) if expected_value is not None else None
+        _check(lib().gkr_prove_weight_opening(self._h, b.handle, q_array(eval_point), len(eval_point), ev,
+                                              ch.handle, proof.handle, C.byref(cm)))
+        return felt_from_c(cm)
+
+    def prove_weight_openings(self, ch: PoseidonChannel, proof: "Proof") -> None:
+        """gkr_prove_weight_openings: open every weight claim recorded in proof."""
+        _check(lib().gkr_prove_weight_openings(self._h, ch.handle, proof.handle))
 
     def _mul_result(self, out, eq, nv, claim_point):
         return {"eq_round_polys": [tuple(q_from_c(eq[4 * t + j]) for j in range(4)) for t in range(nv)],

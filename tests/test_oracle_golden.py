@@ -159,3 +159,89 @@ def test_sp3_weight_commitment(golden):
     assert O.weight_commitment(B) == int(golden["sp3"]["weight_commitments"][0], 16)
     # the row-major layout of the same matrix commits to something else
     assert O.weight_commitment(np.ascontiguousarray(B.T)) != int(golden["sp3"]["weight_commitments"][0], 16)
+
+
+def test_sp3_weight_opening(golden):
+    """The oracle's MLE opening of the SP3 weight at its claim point reproduces the calldata's
+    opening section felt for felt and the transcript digest after the openings
+    (prove_mle_opening_with_commitment, mle_opening.rs:1654-1915; serialization
+    cairo_serde.rs:341-369, 1756-1767)."""
+    sp3 = golden["sp3"]
+    ch, r_out, value, res = _sp3_prove()
+    assert ch.digest() == int(sp3["post_walk_digest"], 16)
+    cd = [int(x, 16) for x in sp3["calldata_hex"]]
+    W = np.array([[2 * i + j + 1 for j in range(2)] for i in range(4)], dtype=np.uint32)
+    wc = sp3["weight_claims"][0]
+    point = [tuple(q) for q in wc["eval_point"]]
+    cm, felts = O.mle_opening(O.col_major_mle(W), point, ch)
+    assert cm == int(sp3["weight_commitments"][0], 16)
+    assert ch.digest() == int(sp3["final_channel_digest_after_openings"], 16)
+    section = [1, len(point)] + [x for q in point for x in q] + list(wc["expected_value"]) + felts
+    start = cd.index(int(sp3["weight_commitments"][0], 16)) + 1
+    assert cd[start:] == section + [int(sp3["io_commitment"], 16)]
+
+
+def test_sp3_opening_verifies_and_tampering_fails(golden):
+    """verify_mle_opening (mle_opening.rs:1918-2028) restated in the oracle accepts the
+    reference's own SP3 opening (read from its calldata) and rejects changed values,
+    siblings, roots, indices and final values."""
+    sp3 = golden["sp3"]
+    cd = [int(x, 16) for x in sp3["calldata_hex"]]
+    ch, _, _, _ = _sp3_prove()
+    start = cd.index(int(sp3["weight_commitments"][0], 16)) + 1
+    assert cd[start] == 1 and cd[start + 1] == 3
+    point = [tuple(cd[start + 2 + 4 * i:start + 6 + 4 * i]) for i in range(3)]
+    proof, end = O.parse_mle_opening(cd, start + 2 + 12 + 4)
+    assert end == len(cd) - 1
+    commitment = int(sp3["weight_commitments"][0], 16)
+    assert O.verify_mle_opening(commitment, proof, point, ch.clone())
+    import copy
+
+    def tampered(edit):
+        b = copy.deepcopy(proof)
+        edit(b)
+        return b
+
+    def bump_left_value(b):  # query 0, round 1: left value + 1
+        idx, rounds = b["queries"][0]
+        lv, rv, ls, rs = rounds[1]
+        rounds[1] = ((lv[0] + 1,) + tuple(lv[1:]), rv, ls, rs)
+
+    def flip_sibling(b):  # query 2, round 0: a right sibling
+        lv, rv, ls, rs = b["queries"][2][1][0]
+        rs = list(rs)
+        rs[1] ^= 1
+        b["queries"][2][1][0] = (lv, rv, ls, rs)
+
+    def flip_root(b):
+        b["intermediate_roots"][0] ^= 1
+
+    def flip_index(b):
+        b["queries"][3] = (b["queries"][3][0] ^ 1, b["queries"][3][1])
+
+    def change_final(b):
+        b["final_value"] = (1, 2, 3, 4)
+
+    for edit in (bump_left_value, flip_sibling, flip_root, flip_index, change_final):
+        b = tampered(edit)
+        assert not O.verify_mle_opening(commitment, b, point, ch.clone())
+
+
+def test_oracle_opening_round_trip():
+    rng = np.random.default_rng(2)
+    for r, c in [(1, 1), (1, 2), (3, 5), (16, 16), (7, 100)]:
+        B = rng.integers(0, P, size=(r, c), dtype=np.uint32)
+        mle = O.col_major_mle(B)
+        nv = (len(mle) - 1).bit_length()
+        ch = O.Channel()
+        ch.mix_u64(r * 1000 + c)
+        point = ch.draw_qm31s(nv)
+        start = ch.clone()
+        cm, felts = O.mle_opening(mle, point, ch)
+        assert cm == O.weight_commitment(B)
+        proof, end = O.parse_mle_opening(felts)
+        assert end == len(felts)
+        assert tuple(proof["final_value"]) == tuple(O.evaluate_mle([tuple(v) for v in mle], point))
+        vch = start.clone()
+        assert O.verify_mle_opening(cm, proof, point, vch)
+        assert vch.digest() == ch.digest()

@@ -343,3 +343,13 @@ def test_weight_commitment_bruteforce(k, n):
     q = rng.integers(0, P, size=(5, 4), dtype=np.uint32)
     packed = [(1 << 124) | (int(a) << 93) | (int(b) << 62) | (int(c) << 31) | int(d) for a, b, c, d in q]
     assert O.mle_commitment(q) == _tree_root(packed)
+
+
+def test_channel_state_round_trip():
+    a = O.Channel()
+    a.mix_u64(99)
+    a.draw_qm31()
+    b = O.Channel()
+    O.set_channel_state(b, O.channel_state(a))
+    assert b.digest() == a.digest() and O.channel_state(b) == O.channel_state(a)
+    assert b.draw_felt252() == a.draw_felt252()
