@@ -34,7 +34,7 @@ import gkr_mi355x as G  # noqa: E402
 METRIC = "GKR matmul-sumcheck Melem/s + % HBM peak; proved tokens/s, Qwen2.5-14B shape"
 HBM_PEAK_GBS = 8000.0
 (K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT,
- K_HOST_WAIT_TAIL) = range(9)
+ K_HOST_WAIT_TAIL, K_MERKLE) = range(10)
 
 QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
 SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
@@ -226,6 +226,111 @@ def cpu_baseline(budget_s=25.0):
                       f"{dt:.2f} s"}
 
 
+WEIGHT_NAMES = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def merkle_hashes(rows, cols):
+    """Poseidon hashes the commitment of a rows x cols weight computes: the real nodes of levels >= 1
+    (subtrees of grid padding come from a table)."""
+    lpk, lpn = lg(rows), lg(cols)
+    n = 0
+    for s in range(1, max(1, lpk + lpn) + 1):
+        n += cols * -(-rows // (1 << s)) if s <= lpk else -(-cols // (1 << (s - lpk)))
+    return n
+
+
+def merkle_valu_profile(name="merkle_commit.md"):
+    """(VALU wave instructions per Poseidon hash, mix-weighted VALU issue peak in G wave-instr/s)
+    of the Merkle level kernel, from the committed rocprofv3 PMC summary, or (None, None)."""
+    vals = {}
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            for line in f:
+                for key in ("valu_wave_insts_per_hash", "valu_mix_peak_gwips"):
+                    if line.startswith(key + ":"):
+                        vals[key] = float(line.split(":")[1])
+    except OSError:
+        pass
+    return vals.get("valu_wave_insts_per_hash"), vals.get("valu_mix_peak_gwips")
+
+
+def cpu_commit_baseline(budget_rows=256, budget_cols=512):
+    """The oracle's weight commitment (reference algorithm, one thread) on a bounded matrix."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    B = O.synthetic(budget_rows, budget_cols, 1, 3)
+    t0 = time.perf_counter()
+    O.weight_commitment(B)
+    dt = time.perf_counter() - t0
+    h = budget_rows * budget_cols - 1
+    return {"value": round(h / dt / 1e6, 4), "unit": "Mhash/s", "cores": 1, "kind": "port",
+            "sample": f"commit_mle_root_only of a {budget_rows}x{budget_cols} weight (int8-range) by the oracle "
+                      f"(the reference's root_only algorithm, sequential): {h} hashes in {dt:.2f} s"}
+
+
+def bench_commit(ctx, args):
+    """Weight commitments of one Qwen2.5-14B layer: the 7 weights (q, k, v, o, gate, up, down;
+    int8-range synthetic, resident) committed as one batch per step
+    (commit_mle_root_only(matrix_to_mle_col_major_padded(W)) each).  After the timed steps, the
+    layer's 7 weight openings at drawn points are timed once (prove_mle_opening_with_commitment:
+    folds, all folded-layer trees, 10 queries)."""
+    lw = LayerWeights(ctx, QWEN, 0, 0)
+    mats = [lw.mats[k][1] for k in WEIGHT_NAMES]
+    shapes = [(m.rows, m.cols) for m in mats]
+    hashes = sum(merkle_hashes(r, c) for r, c in shapes)
+    padded = sum((1 << lg(r)) * (1 << lg(c)) - 1 for r, c in shapes)
+    ctx.synchronize()
+    for _ in range(args.warmup):
+        roots = ctx.weight_commitments(mats)
+    ctx.set_timing(0 if args.no_timing else 1)
+    ctx.reset_timing()
+    t0 = time.perf_counter()
+    outs = [ctx.weight_commitments(mats) for _ in range(args.steps)]
+    dt = (time.perf_counter() - t0) / args.steps
+    assert all(o == outs[0] for o in outs), "non-deterministic commitment"
+    ms, nl, nh = ctx.kernel_time(K_MERKLE)
+    ctx.set_timing(0)
+    # openings of the same weights at points drawn from a channel
+    ch = G.PoseidonChannel()
+    ch.mix_u64(5120)
+    proof = G.Proof()
+    t1 = time.perf_counter()
+    for m in mats:
+        ctx.prove_weight_opening(m, ch.draw_qm31s(lg(m.rows) + lg(m.cols)), ch, proof)
+    open_s = time.perf_counter() - t1
+    felts = len(proof.serialize())
+    kernel = None
+    roofline = None
+    if nl:
+        kh = nh / (ms * 1e-3)
+        kernel = {"launches_per_step": nl // args.steps, "ms_per_step": round(ms / args.steps, 3),
+                  "hashes_per_s_M": round(kh / 1e6, 1)}
+        ipw, peak = merkle_valu_profile()
+        if ipw and peak:
+            ach = kh / 64 * ipw / 1e9
+            roofline = {"bound": "valu", "achieved": round(ach, 1), "peak": peak,
+                        "unit": "G wave-instr/s", "frac": round(ach / peak, 4), "traffic": None,
+                        "kernel": "k_merkle_level", "valu_wave_insts_per_hash": ipw,
+                        "source": "profiles/merkle_commit.md (rocprofv3 PMC SQ_INSTS_VALU; peak weighted by "
+                                  "the hash's 64-bit/32-bit instruction mix at the published vector rates)"}
+    result = {
+        "metric": "Poseidon Merkle weight commitment, hashes/s (Qwen2.5-14B layer)",
+        "value": round(hashes / dt / 1e6, 1), "unit": "Mhash/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "felt252 (9 x 29-bit limbs)",
+        "data": "synthetic (counter-mode SplitMix64, int8-range weights)",
+        "config": {"workload": "qwen2.5-14b-layer-weight-commitments", "weights": dict(zip(WEIGHT_NAMES, shapes)),
+                   "hashes_per_step": hashes, "padded_tree_hashes_per_step": padded},
+        "padded_tree_equivalent_Mhash_s": round(padded / dt / 1e6, 1),
+        "kernel": kernel, "roofline": roofline,
+        "openings": {"s_per_layer": round(open_s, 3), "felts": felts},
+        "roots_sha256_16": hashlib.sha256(",".join(hex(r) for r in outs[0]).encode()).hexdigest()[:16],
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_commit_baseline(),
+    }
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def bench_c2(ctx, args):
     """Config 2: the product sumcheck alone over uniform QM31 vectors f_a, f_b of 2^L entries each
     (channel new(), mix_u64(L); eval -> mix_poly_coeffs -> draw -> fold until size 1).  Algorithmic
@@ -294,7 +399,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1", "c2"])
+    ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit"])
     ap.add_argument("--c2-logs", default="20,24,28",
                     help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -312,6 +417,8 @@ def main():
     ctx = G.Context(0)
     if args.config == "c2":
         return bench_c2(ctx, args)
+    if args.config == "commit":
+        return bench_commit(ctx, args)
     sbuf = SerialBuffer()
     if args.config == "cfg1":
         cfg, n_layers = None, 1

@@ -93,9 +93,11 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * 4 logup prepare, 5 eq table (device kernels: one event pair per launch);
  * 6 host Fiat-Shamir inside the reducers, 7 host wait for results of grid
  * kernels, 8 host wait for results of the persistent tail kernels
- * (wall-clock, bytes = 0).                                                  */
-/* level 0: off; 1: events on k_restrict_cols only, plus the host timers;
- * 2: events on every timed kernel (adds an event pair per launch). */
+ * (wall-clock, bytes = 0); 9 Merkle level kernel of the commitments, whose
+ * "bytes" count Poseidon hashes instead.                                   */
+/* level 0: off; 1: events on k_restrict_cols and the Merkle level kernel,
+ * plus the host timers; 2: events on every timed kernel (adds an event pair
+ * per launch). */
 int gkr_ctx_set_timing(gkr_ctx* ctx, int level);
 int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);
 int gkr_ctx_reset_timing(gkr_ctx* ctx);

@@ -7,8 +7,8 @@
 // accumulator with no carry handling; carries are resolved once, during the
 // reduction.  The prime has three non-zero limbs (limb 0 = 1, limb 6 =
 // 17*2^18, limb 8 = 2^19) and -p^-1 = -1 mod 2^29, so each of the nine
-// Montgomery steps is m = -t_i mod 2^29, one mad for m*limb6 and one shift-add
-// for m*limb8.
+// Montgomery steps is m = -t_i mod 2^29, a shift for the carry, one mad for
+// m*limb6 and one shift-add for m*limb8.
 //
 // Representation rules (all values are representatives, not canonical):
 //   normalized: limbs in [0, 2^29), value below 2^261;
@@ -52,14 +52,30 @@ struct consts {
   }
 };
 
-// t (18 unnormalized 64-bit columns of a product) -> t / 2^261 mod p, normalized.
+// t (18 unnormalized 64-bit columns of a product, with 1 pre-added to columns
+// 1..9) -> t / 2^261 mod p, normalized.  Step i takes m = 2^29 - (t_i mod 2^29),
+// in [1, 2^29] and congruent to -t_i, so t_i + m = (floor(t_i / 2^29) + 1) 2^29:
+// the carry into t_(i+1) is one shift, its "+1" being the pre-added 1.  The sum
+// of the m's stays below 2^261 (1 + 2^-29), so the result is below p (1 + 2^-29)
+// + t / 2^261.
+// Hides a constant from the optimizer, so that it stays a multiplier or an
+// addend of v_mad_u64_u32 instead of being rewritten as separate shifts/adds.
+template <typename T>
+GKR_HD T opaque(T v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm("" : "+s"(v));
+#endif
+  return v;
+}
+
 GKR_HD void mont_reduce(uint64_t t[18], fe& r) {
+  const uint32_t p6 = opaque(kP6), p8 = opaque(kP8);
 #pragma unroll
   for (int i = 0; i < 9; i++) {
-    const uint32_t m = (0u - (uint32_t)t[i]) & kMask;
-    t[i + 1] += (t[i] + m) >> 29;
-    t[i + 6] += (uint64_t)m * kP6;
-    t[i + 8] += (uint64_t)m << 19;
+    const uint32_t m = (((uint32_t)t[i] & kMask) ^ kMask) + 1u;  // 2^29 - (t_i mod 2^29)
+    t[i + 1] += t[i] >> 29;
+    t[i + 6] += (uint64_t)m * p6;
+    t[i + 8] += (uint64_t)m * p8;
   }
   uint64_t c = t[9];
 #pragma unroll
@@ -70,10 +86,12 @@ GKR_HD void mont_reduce(uint64_t t[18], fe& r) {
   r.l[8] = (uint32_t)c;
 }
 
+// Product columns start at 1 for k = 1..9 (the reduction's carry increments).
 GKR_HD void mul(const fe& a, const fe& b, fe& r) {
   uint64_t t[18];
+  const uint64_t one = opaque((uint64_t)1);
 #pragma unroll
-  for (int k = 0; k < 18; k++) t[k] = 0;
+  for (int k = 0; k < 18; k++) t[k] = (k >= 1 && k <= 9) ? one : 0u;
 #pragma unroll
   for (int i = 0; i < 9; i++)
 #pragma unroll
@@ -81,18 +99,22 @@ GKR_HD void mul(const fe& a, const fe& b, fe& r) {
   mont_reduce(t, r);
 }
 
+// Off-diagonal products taken once against the doubled limbs (2 a_i < 2^31,
+// so a column stays below 4 * 2^61 + 2^60 plus the reduction terms).
 GKR_HD void sqr(const fe& a, fe& r) {
   uint64_t t[18];
+  const uint64_t one = opaque((uint64_t)1);
 #pragma unroll
-  for (int k = 0; k < 18; k++) t[k] = 0;
+  for (int k = 0; k < 18; k++) t[k] = (k >= 1 && k <= 9) ? one : 0u;
+  uint32_t d[9];
 #pragma unroll
-  for (int i = 0; i < 9; i++)
+  for (int i = 0; i < 9; i++) d[i] = a.l[i] << 1;
 #pragma unroll
-    for (int j = i + 1; j < 9; j++) t[i + j] += (uint64_t)a.l[i] * a.l[j];
+  for (int i = 0; i < 9; i++) {
+    t[2 * i] += (uint64_t)a.l[i] * a.l[i];
 #pragma unroll
-  for (int k = 1; k < 16; k++) t[k] <<= 1;
-#pragma unroll
-  for (int i = 0; i < 9; i++) t[2 * i] += (uint64_t)a.l[i] * a.l[i];
+    for (int j = i + 1; j < 9; j++) t[i + j] += (uint64_t)d[i] * a.l[j];
+  }
   mont_reduce(t, r);
 }
 

@@ -88,7 +88,8 @@ enum Slot {
 // Timer ids: device kernels (HIP events) and two host-side phases
 // (Fiat-Shamir hashing inside the reducers, and waiting for device results).
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
-                K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_NKERNELS = 9 };
+                K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
+                K_NKERNELS = 10 };
 constexpr int kMaxPartialBlocks = 1024;
 
 struct KernelStat {
@@ -201,7 +202,7 @@ struct TimedLaunch {
   uint64_t bytes;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
-    if (c->timing >= 2 || (c->timing == 1 && kid == K_RESTRICT_COLS)) {
+    if (c->timing >= 2 || (c->timing == 1 && (kid == K_RESTRICT_COLS || kid == K_MERKLE))) {
       e0 = get_event(c);
       e1 = get_event(c);
       if (e0) (void)hipEventRecord(e0, c->stream);
@@ -1966,6 +1967,9 @@ static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gk
   HIP_TRY(hipMemcpyAsync(dsteps, steps.data(), steps.size() * sizeof(MerkleStep), hipMemcpyHostToDevice, c->stream));
   for (const auto& L : launches) {
     const uint64_t blocks = (L.total + kMerkleBlock - 1) / kMerkleBlock;
+    uint64_t hashes = 0;  // the timer's byte counter holds the hash count of this kernel
+    for (size_t k = L.first_step; k < L.first_step + L.n_steps; k++) hashes += steps[k].n_out * ((1ull << steps[k].d) - 1);
+    TimedLaunch tl(c, K_MERKLE, hashes);
     k_merkle_level<<<dim3((uint32_t)blocks), dim3(kMerkleBlock), 0, c->stream>>>(dsteps + L.first_step, (int)L.n_steps,
                                                                               L.s, L.total, K);
     HIP_TRY(hipGetLastError());
