@@ -257,6 +257,17 @@ int gkr_mle_commitment(gkr_ctx* ctx, const gkr_qvec* evals, gkr_felt* root);
 int gkr_prove_weight_opening(gkr_ctx* ctx, const gkr_matrix* b, const gkr_qm31* eval_point, uint32_t n_point,
                              const gkr_qm31* expected_value, gkr_channel* ch, gkr_proof* proof, gkr_felt* commitment);
 int gkr_prove_weight_openings(gkr_ctx* ctx, gkr_channel* ch, gkr_proof* proof);
+/* The weight phase in one of the reference's transcript modes (prover.rs:2059-2200),
+ * over the claims recorded in `proof`, which are then forgotten:
+ *   GKR_WEIGHT_SEQUENTIAL     = gkr_prove_weight_openings (STWO_WEIGHT_BINDING=sequential);
+ *   GKR_WEIGHT_AGGREGATED_RLC = the reference default (aggregated oracle sumcheck,
+ *     RLC fast path, prover.rs:368-658): the commitment of every claimed weight is
+ *     appended to the proof (one GPU batch), then rho = draw_qm31 and
+ *     mix_secure_field(sum_i rho^i * value_i); no openings;
+ *   GKR_WEIGHT_RLC_DIRECT     = apply_aggregated_rlc_binding (prover.rs:669-699): rho and
+ *     the combined value only.                                                 */
+enum { GKR_WEIGHT_SEQUENTIAL = 0, GKR_WEIGHT_AGGREGATED_RLC = 1, GKR_WEIGHT_RLC_DIRECT = 2 };
+int gkr_prove_weight_binding(gkr_ctx* ctx, gkr_channel* ch, gkr_proof* proof, int mode);
 
 /* Mul layer (element-wise product c = lhs * rhs), reduce_mul_layer
  * (engine/src/gkr/prover.rs:6172-6271): mix_u64(0x4D554C), mix the claim

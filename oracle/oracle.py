@@ -614,3 +614,15 @@ def verify_mle_opening(commitment: int, proof, challenges, ch: Channel, n_querie
             cur %= max(mid // 2, 1)
             size = mid
     return True
+
+
+def rlc_weight_binding(values, ch: Channel):
+    """RLC weight binding (prover.rs:1335-1345, 669-699): rho = draw_qm31;
+    mix_secure_field(sum_i rho^i * value_i)."""
+    rho = ch.draw_qm31()
+    pw, combined = (1, 0, 0, 0), (0, 0, 0, 0)
+    for v in values:
+        combined = qadd(combined, qmul(pw, v))
+        pw = qmul(pw, rho)
+    ch.mix_secure_field(combined)
+    return combined

@@ -2188,14 +2188,53 @@ extern "C" int gkr_prove_weight_opening(gkr_ctx* c, const gkr_matrix* b, const g
 }
 
 extern "C" int gkr_prove_weight_openings(gkr_ctx* c, gkr_channel* ch, gkr_proof* proof) {
+  return gkr_prove_weight_binding(c, ch, proof, GKR_WEIGHT_SEQUENTIAL);
+}
+
+// The weight phase of the GKR prover (prover.rs:2059-2200) over the claims the
+// proof recorded, in recording order.
+//   SEQUENTIAL: one opening per claim on the main channel (prover.rs:2160-2190).
+//   AGGREGATED_RLC: the reference default, the aggregated oracle sumcheck without
+//     the full binding proof (prover.rs:368-658): the commitment of every claimed
+//     weight (one batch) goes into the proof, then rho = draw_qm31 and
+//     mix_secure_field(sum rho^i v_i) (prover.rs:1335-1345); no openings.
+//   RLC_DIRECT: apply_aggregated_rlc_binding (prover.rs:669-699): rho and the
+//     combined value only, no commitments.
+extern "C" int gkr_prove_weight_binding(gkr_ctx* c, gkr_channel* ch, gkr_proof* proof, int mode) {
   CH_CHECK(ch);
   if (!c || !proof) return fail(GKR_ERR_INVALID, "null argument");
-  for (const WeightClaimRec& w : proof->weight_claims) {
-    const gkr_qm31* pt = reinterpret_cast<const gkr_qm31*>(w.point.data());
-    const gkr_qm31 v = {{w.value.a, w.value.b, w.value.c, w.value.d}};
-    TRY(gkr_prove_weight_opening(c, w.b, pt, (uint32_t)w.point.size(), &v, ch, proof, nullptr));
+  if (mode != GKR_WEIGHT_SEQUENTIAL && mode != GKR_WEIGHT_AGGREGATED_RLC && mode != GKR_WEIGHT_RLC_DIRECT)
+    return fail(GKR_ERR_INVALID, "unknown weight binding mode %d", mode);
+  auto& claims = proof->weight_claims;
+  if (mode == GKR_WEIGHT_SEQUENTIAL) {
+    for (const WeightClaimRec& w : claims) {
+      const gkr_qm31* pt = reinterpret_cast<const gkr_qm31*>(w.point.data());
+      const gkr_qm31 v = {{w.value.a, w.value.b, w.value.c, w.value.d}};
+      TRY(gkr_prove_weight_opening(c, w.b, pt, (uint32_t)w.point.size(), &v, ch, proof, nullptr));
+    }
+    claims.clear();
+    return GKR_OK;
   }
-  proof->weight_claims.clear();
+  if (claims.empty()) return GKR_OK;
+  if (mode == GKR_WEIGHT_AGGREGATED_RLC) {
+    // one root per distinct matrix, repeated per claim
+    std::vector<const gkr_matrix*> uniq;
+    std::map<const gkr_matrix*, size_t> at;
+    for (const auto& w : claims)
+      if (at.emplace(w.b, uniq.size()).second) uniq.push_back(w.b);
+    std::vector<gkr_felt> roots(uniq.size());
+    TRY(gkr_weight_commitments(c, uniq.data(), uniq.size(), roots.data()));
+    for (const auto& w : claims) proof->weight_commitments.push_back(felt_canon_from_words(roots[at[w.b]].w));
+  }
+  PoseidonChannel& C = ch->ch;
+  const qm31 rho = C.draw_qm31();
+  qm31 pw = qm31_one(), combined = qm31_zero();
+  for (const auto& w : claims) {
+    combined = qm31_add(combined, qm31_mul(pw, w.value));
+    pw = qm31_mul(pw, rho);
+  }
+  C.mix_secure_field(combined);
+  claims.clear();
   return GKR_OK;
 }
 

@@ -164,7 +164,9 @@ SIGNATURES = [
     ("gkr_mle_commitment", C.c_int, [_P, _P, _PF]),
     ("gkr_prove_weight_opening", C.c_int, [_P, _P, _PQ, C.c_uint32, _PQ, _P, _P, _PF]),
     ("gkr_prove_weight_openings", C.c_int, [_P, _P, _P]),
+    ("gkr_prove_weight_binding", C.c_int, [_P, _P, _P, C.c_int]),
 ]
+WEIGHT_SEQUENTIAL, WEIGHT_AGGREGATED_RLC, WEIGHT_RLC_DIRECT = 0, 1, 2
 
 
 def lib() -> C.CDLL:
@@ -481,6 +483,10 @@ class Context:
     def prove_weight_openings(self, ch: PoseidonChannel, proof: "Proof") -> None:
         """gkr_prove_weight_openings: open every weight claim recorded in proof."""
         _check(lib().gkr_prove_weight_openings(self._h, ch.handle, proof.handle))
+
+    def prove_weight_binding(self, ch: PoseidonChannel, proof: "Proof", mode: int) -> None:
+        """gkr_prove_weight_binding: the weight phase in the given transcript mode."""
+        _check(lib().gkr_prove_weight_binding(self._h, ch.handle, proof.handle, mode))
 
     def _mul_result(self, out, eq, nv, claim_point):
         return {"eq_round_polys": [tuple(q_from_c(eq[4 * t + j]) for j in range(4)) for t in range(nv)],

@@ -137,3 +137,43 @@ def _oracle_channel_from_state(st):
     words = np.array(st, dtype=np.uint32)
     O.set_channel_state(och, words)
     return och
+
+
+@pytest.mark.parametrize("mode", [G.WEIGHT_SEQUENTIAL, G.WEIGHT_AGGREGATED_RLC, G.WEIGHT_RLC_DIRECT])
+def test_weight_binding_modes(gpu_ctx, mode):
+    """Three MatMul layers (one weight used twice), then the weight phase in each of the
+    reference's transcript modes: commitments in claim order (AGGREGATED_RLC) or none
+    (RLC_DIRECT), rho drawn and sum rho^i * final_b_i mixed (oracle replay), or the
+    sequential openings."""
+    rng = np.random.default_rng(11)
+    W1 = rng.integers(0, P, size=(24, 40), dtype=np.uint32)
+    W2 = rng.integers(0, P, size=(40, 9), dtype=np.uint32)
+    X = rng.integers(0, P, size=(3, 24), dtype=np.uint32)
+    x, w1, w2 = gpu_ctx.upload(X), gpu_ctx.upload(W1), gpu_ctx.upload(W2)
+    H = gpu_ctx.upload(O.matmul_forward(X, W1))
+    ch = G.PoseidonChannel()
+    ch.mix_u64(3)
+    proof = G.Proof()
+    finals = []
+    for a, b in [(H, w2), (x, w1), (x, w1)]:
+        r = ch.draw_qm31s(lg(a.rows) + lg(b.cols))
+        v = gpu_ctx.matmul_output_claim(a, b, r)
+        ch.mix_secure_field(v)
+        finals.append(gpu_ctx.prove_matmul_layer(r, v, a, b, ch, proof)["final_b_eval"])
+    och = O.Channel()
+    O.set_channel_state(och, ch.export_state())
+    n_before = len(proof.serialize())
+    gpu_ctx.prove_weight_binding(ch, proof, mode)
+    cd = proof.serialize()
+    if mode == G.WEIGHT_SEQUENTIAL:
+        assert cd[n_before - 3] == 3  # three commitments, then three openings
+        assert cd[n_before - 3 + 4] == 3
+        return
+    O.rlc_weight_binding(finals, och)
+    assert ch.digest() == och.digest()
+    # [.., input point len 0, value, n_commitments, commitments..., 0 openings, io]
+    want = [O.weight_commitment(W2), O.weight_commitment(W1), O.weight_commitment(W1)]
+    if mode == G.WEIGHT_AGGREGATED_RLC:
+        assert cd[n_before - 3:n_before - 3 + 4] == [3] + want and cd[-2] == 0
+    else:
+        assert cd[n_before - 3] == 0 and cd[-2] == 0
