@@ -331,6 +331,45 @@ def bench_commit(ctx, args):
     ctx.close()
 
 
+def bench_forward(ctx, args):
+    """Forward pass of one Qwen2.5-14B layer, 64 tokens: the 7 matmul products C = A * B mod P
+    (int8-range synthetic weights and activations, resident) on the matrix cores, each into a
+    preallocated output.  The weights' digit planes are built during warm-up (once per weight)."""
+    lw = LayerWeights(ctx, QWEN, 0, 0)
+    pairs = [(lw.mats[k][0], lw.mats[k][1]) for k in WEIGHT_NAMES]
+    outs = [ctx.matmul_forward(a, b) for a, b in pairs]
+    for _ in range(max(1, args.warmup)):
+        for (a, b), o in zip(pairs, outs):
+            ctx.matmul_forward_into(a, b, o)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for (a, b), o in zip(pairs, outs):
+            ctx.matmul_forward_into(a, b, o)
+    ctx.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    macs = sum(a.rows * a.cols * b.cols for a, b in pairs)
+    wbytes = sum(b.rows * b.cols for _, b in pairs)  # one digit plane (1 byte per weight) streamed
+    digest = hashlib.sha256(b"".join(o.download().tobytes() for o in outs)).hexdigest()[:16]
+    result = {
+        "metric": "forward M31 GEMM, Qwen2.5-14B layer (64 tokens) on the matrix cores",
+        "value": round(macs / dt / 1e12, 3), "unit": "T M31-MAC/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "i8 digit planes -> i32 -> M31",
+        "data": "synthetic (counter-mode SplitMix64, int8-range weights and activations)",
+        "config": {"workload": "qwen2.5-14b-layer-forward-64-tokens", "weights": dict(zip(WEIGHT_NAMES,
+                   [(b.rows, b.cols) for _, b in pairs])), "macs_per_step": macs},
+        "roofline": {"bound": "hbm", "achieved": round(wbytes / dt / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(wbytes / dt / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_gemm_m31 (whole step incl. packing and split reduction)",
+                     "note": "bytes = the weights' digit plane 0 (int8-range), 1 byte per weight"},
+        "u32_weight_equivalent_gbps": round(4 * wbytes / dt / 1e9, 1),
+        "outputs_sha256_16": digest, "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def bench_c2(ctx, args):
     """Config 2: the product sumcheck alone over uniform QM31 vectors f_a, f_b of 2^L entries each
     (channel new(), mix_u64(L); eval -> mix_poly_coeffs -> draw -> fold until size 1).  Algorithmic
@@ -399,7 +438,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit"])
+    ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward"])
     ap.add_argument("--c2-logs", default="20,24,28",
                     help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -419,6 +458,8 @@ def main():
         return bench_c2(ctx, args)
     if args.config == "commit":
         return bench_commit(ctx, args)
+    if args.config == "forward":
+        return bench_forward(ctx, args)
     sbuf = SerialBuffer()
     if args.config == "cfg1":
         cfg, n_layers = None, 1

@@ -224,6 +224,18 @@ int gkr_sumcheck_product(gkr_ctx* ctx, const gkr_qvec* fa, const gkr_qvec* fb, g
                          gkr_qm31* round_polys /* 3T: c0, c1, c2 */, gkr_qm31* challenges /* T */,
                          gkr_qm31* final_a, gkr_qm31* final_b);
 
+/* Forward-pass matrix product (the witness before the walk): C = A * B mod P
+ * for canonical M31 matrices, a new resident matrix (m x n).  Replaces
+ * gpu_matmul_m31_full (engine/src/gpu_sumcheck.rs:3104) and its GEMM/GEMV
+ * kernels (:418-460); computed on the matrix cores (i8 MFMA on digit planes),
+ * exact for any M31 values.                                                  */
+int gkr_matmul_forward(gkr_ctx* ctx, const gkr_matrix* a, const gkr_matrix* b, gkr_matrix** out);
+/* The same into an existing m x n matrix (no allocation; asynchronous on the
+ * context stream, ordered before the next call that uses `out`).  The first
+ * product with a given B also builds and keeps B's digit planes (one pass
+ * over B plus a host round trip).                                          */
+int gkr_matmul_forward_into(gkr_ctx* ctx, const gkr_matrix* a, const gkr_matrix* b, gkr_matrix* out);
+
 /* MLE commitments: Poseidon Merkle roots (engine/src/crypto/poseidon_merkle.rs:255-280,
  * root_only_parallel) over securefield_to_felt leaves (poseidon_channel.rs:59-69),
  * padded with zero felts to a power of two (at least 2); node = poseidon_hash(l, r).

@@ -159,6 +159,8 @@ SIGNATURES = [
                                   C.c_uint32, _PQ, _P, _PQ, C.POINTER(C.c_uint32), _PQ, C.POINTER(C.c_size_t)]),
     ("gkr_prove_walk", C.c_int, [_P, _P, C.POINTER(GkrStep), C.c_size_t, _PQ, C.c_uint32, _PQ, _P, _PQ,
                                  C.POINTER(C.c_uint32), _PQ]),
+    ("gkr_matmul_forward", C.c_int, [_P, _P, _P, C.POINTER(_P)]),
+    ("gkr_matmul_forward_into", C.c_int, [_P, _P, _P, _P]),
     ("gkr_weight_commitment", C.c_int, [_P, _P, _PF]),
     ("gkr_weight_commitments", C.c_int, [_P, C.POINTER(_P), C.c_size_t, _PF]),
     ("gkr_mle_commitment", C.c_int, [_P, _P, _PF]),
@@ -451,6 +453,16 @@ class Context:
                                 for t in range(T)],
                 "challenges": [q_from_c(chal[t]) for t in range(T)],
                 "final_a_eval": q_from_c(a), "final_b_eval": q_from_c(b)}
+
+    def matmul_forward(self, a: "Matrix", b: "Matrix") -> "Matrix":
+        """gkr_matmul_forward: C = A * B mod P as a new resident matrix."""
+        h = _P()
+        _check(lib().gkr_matmul_forward(self._h, a.handle, b.handle, C.byref(h)))
+        return Matrix(self, h.value, a.rows, b.cols)
+
+    def matmul_forward_into(self, a: "Matrix", b: "Matrix", out: "Matrix") -> None:
+        """gkr_matmul_forward_into: C = A * B mod P written into an existing matrix."""
+        _check(lib().gkr_matmul_forward_into(self._h, a.handle, b.handle, out.handle))
 
     def weight_commitment(self, b: "Matrix") -> int:
         """gkr_weight_commitment: commit_mle_root_only(matrix_to_mle_col_major_padded(B))."""
