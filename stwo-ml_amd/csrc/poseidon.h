@@ -19,6 +19,14 @@
 // where pack(v...) = fold(1, acc * 2^31 + v) over the M31 words.
 #pragma once
 #include <stdint.h>
+#include <stdlib.h>
+
+#include <atomic>
+#include <chrono>
+#include <condition_variable>
+#include <mutex>
+#include <thread>
+#include <vector>
 
 #include "felt252.h"
 #include "field.h"
@@ -156,6 +164,85 @@ inline felt securefield_to_felt(const qm31& q) {
   return pack_m31s(w, 4);
 }
 
+// A batch of draws from one channel state, draw i = hades([digest, base + i, 3])[0],
+// has no dependency between draws: DrawPool spreads them over worker threads
+// (the caller works too).  Items are claimed through one atomic word holding
+// (batch id << 32 | batch size << 16 | next index): every decision of a
+// worker reads only that word, a worker only ever takes items of the batch it
+// has seen, and the batch's fields (read after a successful claim) cannot
+// change before all its items are done.  Workers spin for GKR_DRAW_SPIN_US
+// (default 2000) after a batch, then sleep on a condition variable.  One batch
+// at a time; a second caller (another thread) computes its batch alone.
+// Threads: GKR_DRAW_THREADS, default min(8, hardware threads - 1); 0 disables
+// the pool.
+class DrawPool {
+ public:
+  static DrawPool& instance() {
+    static DrawPool* p = new DrawPool();  // never destroyed: detached workers may still wait at exit
+    return *p;
+  }
+  template <typename F>
+  bool run(const felt& digest, uint64_t base, size_t n, F&& conv, qm31* out) {
+    if (workers_ == 0 || n >= (1u << 16)) return false;
+    std::unique_lock<std::mutex> busy(busy_, std::try_to_lock);
+    if (!busy.owns_lock()) return false;
+    const uint64_t job = ++job_ & 0xffffffffull;
+    digest_ = digest;
+    base_ = base;
+    n_ = n;
+    out_ = out;
+    done_.store(0, std::memory_order_relaxed);
+    claim_.store((job << 32) | ((uint64_t)n << 16), std::memory_order_release);
+    {
+      std::lock_guard<std::mutex> g(sleep_mu_);
+      gen_.store(job, std::memory_order_release);
+    }
+    if (sleepers_.load(std::memory_order_acquire) > 0) sleep_cv_.notify_all();
+    work(job, conv);
+    while (done_.load(std::memory_order_acquire) < n) {
+    }
+    return true;
+  }
+
+ private:
+  DrawPool() {
+    int t = (int)std::thread::hardware_concurrency() - 1;
+    if (t > 8) t = 8;
+    if (const char* e = getenv("GKR_DRAW_THREADS")) t = atoi(e);
+    if (t < 0) t = 0;
+    workers_ = t;
+    if (const char* e = getenv("GKR_DRAW_SPIN_US")) spin_us_ = atoi(e);
+    for (int i = 0; i < t; i++) std::thread([this] { loop(); }).detach();
+  }
+  template <typename F>
+  void work(uint64_t job, F&& conv) {
+    uint64_t c = claim_.load(std::memory_order_acquire);
+    for (;;) {
+      if ((c >> 32) != (job & 0xffffffffull) || (c & 0xffffull) >= ((c >> 16) & 0xffffull)) return;
+      if (!claim_.compare_exchange_weak(c, c + 1, std::memory_order_acq_rel, std::memory_order_acquire)) continue;
+      const size_t i = (size_t)(c & 0xffffull);
+      out_[i] = conv(digest_, base_ + i);
+      done_.fetch_add(1, std::memory_order_release);
+      c = claim_.load(std::memory_order_acquire);
+    }
+  }
+  void loop();
+  int workers_ = 0;
+  int spin_us_ = 2000;  // a prover posts batches a few hundred microseconds apart
+  std::mutex busy_;
+  uint64_t job_ = 0;  // written by the poster only, under busy_
+  felt digest_{};
+  uint64_t base_ = 0;
+  size_t n_ = 0;
+  qm31* out_ = nullptr;
+  std::atomic<uint64_t> claim_{0};
+  std::atomic<size_t> done_{0};
+  std::atomic<uint64_t> gen_{0};
+  std::atomic<int> sleepers_{0};
+  std::mutex sleep_mu_;
+  std::condition_variable sleep_cv_;
+};
+
 class PoseidonChannel {
  public:
   felt digest;  // Montgomery form
@@ -195,7 +282,18 @@ class PoseidonChannel {
     return qm31{m[0], m[1], m[2], m[3]};
   }
   qm31 draw_qm31() { return felt_to_qm31(draw_felt252()); }
+  // One draw without advancing the channel: hades([digest, index, 3])[0].
+  static qm31 draw_at(const felt& digest, uint64_t index) {
+    felt s[3] = {digest, felt_from_u64(index), felt_from_u64(3)};
+    hades_permute(s);
+    return felt_to_qm31(s[0]);
+  }
   void draw_qm31s(qm31* out, size_t n) {
+    if (n >= 4 && DrawPool::instance().run(digest, n_draws, n, draw_at, out)) {
+      n_draws += (uint32_t)n;
+      hash_count += n;
+      return;
+    }
     for (size_t i = 0; i < n; i++) out[i] = draw_qm31();
   }
   void mix_poly_coeffs(const qm31& c0, const qm31& c1, const qm31& c2) {
@@ -246,5 +344,24 @@ class PoseidonChannel {
     hash_count = (uint64_t)st[9] | ((uint64_t)st[10] << 32);
   }
 };
+
+inline void DrawPool::loop() {
+  uint64_t seen = gen_.load(std::memory_order_acquire);
+  for (;;) {
+    // spin for spin_us_ waiting for a batch, then sleep until one is posted
+    const auto t0 = std::chrono::steady_clock::now();
+    uint64_t g;
+    while ((g = gen_.load(std::memory_order_acquire)) == seen) {
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(spin_us_)) {
+        std::unique_lock<std::mutex> lk(sleep_mu_);
+        sleepers_.fetch_add(1, std::memory_order_acq_rel);
+        sleep_cv_.wait(lk, [&] { return gen_.load(std::memory_order_acquire) != seen; });
+        sleepers_.fetch_sub(1, std::memory_order_acq_rel);
+      }
+    }
+    seen = g;
+    work(g, PoseidonChannel::draw_at);
+  }
+}
 
 }  // namespace gkr

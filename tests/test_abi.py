@@ -172,3 +172,35 @@ def test_errors_are_reported():
         ch.mix_felt(O_P252())
     with pytest.raises(G.GkrError):
         G.activation_table(9, 8)
+
+
+def test_parallel_draw_batches_equal_sequential_draws():
+    """draw_qm31s of 4+ values runs on the draw pool's threads; it must equal single draws, also
+    with several Python threads drawing at once (one of them takes the pool, the others draw
+    alone)."""
+    import threading
+    rng = random.Random(17)
+    for trial in range(300):
+        n = rng.choice([4, 5, 8, 19, 20, 64, 257])
+        a = G.PoseidonChannel()
+        a.mix_u64(trial)
+        b = a.clone()
+        assert a.draw_qm31s(n) == [b.draw_qm31() for _ in range(n)]
+        assert a.export_state() == b.export_state()
+    errs = []
+
+    def worker(seed):
+        r = random.Random(seed)
+        for t in range(100):
+            n = r.choice([4, 7, 19, 33])
+            a = G.PoseidonChannel()
+            a.mix_u64(seed * 1000 + t)
+            b = a.clone()
+            if a.draw_qm31s(n) != [b.draw_qm31() for _ in range(n)]:
+                errs.append((seed, t))
+    ts = [threading.Thread(target=worker, args=(s,)) for s in range(4)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errs
