@@ -370,12 +370,26 @@ def bench_forward(ctx, args):
     ctx.close()
 
 
+def trip_plan(T, host_len=128, k0=3, big=1 << 16):
+    """(first round, rounds, vector length) of the device trips of a product sumcheck over 2^T entries
+    (the library's plan_trips: up to 3 rounds per launch, 2 on vectors longer than 2^16)."""
+    if T <= 0:
+        return []
+    t = min(k0, T)
+    out = [(0, t, 1 << T)]
+    while t < T and (1 << (T - t)) > host_len:
+        n = 1 << (T - t)
+        k = min(2 if n > big else 3, T - t)
+        out.append((t, k, n))
+        t += k
+    return out
+
+
 def bench_c2(ctx, args):
     """Config 2: the product sumcheck alone over uniform QM31 vectors f_a, f_b of 2^L entries each
     (channel new(), mix_u64(L); eval -> mix_poly_coeffs -> draw -> fold until size 1).  Algorithmic
-    bytes per sumcheck, as the fused kernels move them: round 0 reads 32 N; grid round t >= 1 reads
-    both vectors at n_(t-1) and writes them at n_t = n_(t-1)/2, 48 n_(t-1); the tail kernel reads
-    its 2 x 16 x n_(t0-1) input once and then works in LDS.  About 128 N in all."""
+    bytes per sumcheck, as the trip kernels move them (trip_plan): the first trip reads both vectors
+    (32 N); trip j >= 1 reads both at its predecessor's length and writes them at its own."""
     logs = [int(x) for x in args.c2_logs.split(",")]
     sizes = []
     for L in logs:
@@ -391,7 +405,7 @@ def bench_c2(ctx, args):
 
         for _ in range(args.warmup):
             run()
-        ctx.set_timing(0 if args.no_timing else 2)  # the roofline kernel here is k_mm_round
+        ctx.set_timing(0 if args.no_timing else 2)  # the roofline kernel here is the product trip
         ctx.reset_timing()
         t0 = time.perf_counter()
         outs = [run() for _ in range(args.steps)]
@@ -401,10 +415,11 @@ def bench_c2(ctx, args):
         ms, nl, nb = ctx.kernel_time(K_MM_ROUND)
         fs_ms, fs_n, _ = ctx.kernel_time(K_HOST_FS)
         ctx.set_timing(False)
-        t0 = 0
-        while (n >> t0) > 1024:  # kTailMax: the last rounds run in one workgroup
-            t0 += 1
-        alg = 32 * n + sum(48 * (n >> (t - 1)) for t in range(1, t0)) + (32 * (n >> (t0 - 1)) if t0 else 0)
+        alg = 0
+        prev = None
+        for _, _, tn in trip_plan(L):
+            alg += 32 * (prev if prev else tn) + (32 * tn if prev else 0)
+            prev = tn
         entry = {"log2_n": L, "ms_per_sumcheck": round(dt * 1e3, 3),
                  "wall_gbps": round(alg / dt / 1e9, 1), "wall_frac": round(alg / dt / 1e9 / HBM_PEAK_GBS, 4),
                  "qm31_evals_per_s_M": round(2 * (2 * n - 1) / dt / 1e6, 1), "digest": hex(outs[0][0])}
@@ -426,7 +441,7 @@ def bench_c2(ctx, args):
         "data": "synthetic (uniform QM31, SplitMix64)",
         "config": {"workload": f"config2-product-sumcheck-2^{big['log2_n']}", "log2_sizes": logs},
         "roofline": ({"bound": "hbm", "achieved": rk["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                      "frac": rk["frac"], "traffic": None, "kernel": "k_mm_round"} if rk else None),
+                      "frac": rk["frac"], "traffic": None, "kernel": "k_trip<0,K> (product trips)"} if rk else None),
         "sizes": sizes, "cpu_baseline": None,
     }
     print(json.dumps(result), flush=True)
@@ -507,7 +522,7 @@ def main():
 
     kernels = {}
     for kid, name in [(K_RESTRICT_COLS, "restrict_cols"), (K_RESTRICT_ROWS, "restrict_rows"),
-                      (K_MM_ROUND, "mm_round"), (K_EQ3_ROUND, "eq3_round"), (K_LOGUP_PREP, "logup_prepare"),
+                      (K_MM_ROUND, "product_trip"), (K_EQ3_ROUND, "eq3_or_sum_trip"), (K_LOGUP_PREP, "logup_prepare"),
                       (K_EQ_TABLE, "eq_table")]:
         ms, nl, nb = ctx.kernel_time(kid)
         if nl:
@@ -515,8 +530,8 @@ def main():
                              "gbps": round(nb / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
                              "ms_per_step": round(ms / args.steps, 3)}
     host = {}
-    for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait_grid"),
-                      (K_HOST_WAIT_TAIL, "device_wait_tail")]:
+    for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait"),
+                      (K_HOST_WAIT_TAIL, "device_wait_handover")]:
         ms, nl, _ = ctx.kernel_time(kid)
         if nl:
             host[name] = {"ms_per_step": round(ms / args.steps, 3), "avg_us": round(ms / nl * 1e3, 3), "calls": nl}

@@ -89,10 +89,11 @@ int gkr_ctx_create(int device, gkr_ctx** out);  /* replaces GpuSumcheckExecutor:
 void gkr_ctx_destroy(gkr_ctx* ctx);
 int gkr_ctx_synchronize(gkr_ctx* ctx);
 /* Per-kernel timing (HIP events on the context stream), for benchmarks.
- * ids: 0 restrict_cols, 1 restrict_rows, 2 matmul round, 3 eq3 round,
- * 4 logup prepare, 5 eq table (device kernels: one event pair per launch);
- * 6 host Fiat-Shamir inside the reducers, 7 host wait for results of grid
- * kernels, 8 host wait for results of the persistent tail kernels
+ * ids: 0 restrict_cols, 1 restrict_rows, 2 product-sumcheck trip (several
+ * rounds per launch), 3 eq-sumcheck or degree-1 trip, 4 logup prepare, 5 eq
+ * tables (device kernels: one event pair per launch); 6 host Fiat-Shamir
+ * inside the reducers, 7 host wait for results of device kernels, 8 host wait
+ * for the hand-over of a sumcheck's last vectors
  * (wall-clock, bytes = 0); 9 Merkle level kernel of the commitments, whose
  * "bytes" count Poseidon hashes instead.                                   */
 /* level 0: off; 1: events on k_restrict_cols and the Merkle level kernel,

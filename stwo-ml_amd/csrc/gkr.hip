@@ -83,15 +83,24 @@ static bool felt_abi_canonical(const gkr_felt& f) {
 // ------------------------------------------------------------------ context
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
-  S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_E1, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_NSLOTS
+  S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_NSLOTS
 };
-// Timer ids: device kernels (HIP events) and two host-side phases
-// (Fiat-Shamir hashing inside the reducers, and waiting for device results).
+// Timer ids: device kernels (HIP events) and host-side phases (Fiat-Shamir
+// hashing inside the reducers, waiting for trip results, waiting for the
+// hand-over of the last vectors).
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
                 K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
                 K_NKERNELS = 10 };
 constexpr int kMaxPartialBlocks = 1024;
+constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
+// Result slots in the coherent host area (h_out): 0 .. 63 serve the result in
+// flight; results launched ahead of time and read later have their own.
+constexpr int kSlotEq0 = 64;     // eq-sumcheck trip 0 (up to 64 values)
+constexpr int kSlotPrep = 128;   // LogUp prepare: trace sum, input MLE
+constexpr int kSlotTable = 130;  // LogUp table-side sum
+constexpr int kSlotMult0 = 136;  // multiplicity sumcheck trip 0 (up to 8 values)
+constexpr int kOutSlots = 192;
 
 struct KernelStat {
   double ms = 0;
@@ -109,8 +118,11 @@ struct MatMulCache {
   const gkr_matrix* a = nullptr;
   const gkr_matrix* b = nullptr;
   std::vector<gkr_qm31> r_i, r_j;
-  bool have_round0 = false;
-  qm31 round0[3];
+  // sums of the product sumcheck's first trip over the restricted vectors
+  // (rounds 0 .. trip0_k - 1), computed with the output claim
+  bool have_trip0 = false;
+  int trip0_k = 0;
+  qm31 trip0[kMaxSums];
 };
 
 struct gkr_matrix {
@@ -137,7 +149,7 @@ struct gkr_ctx {
   size_t cap[S_NSLOTS] = {};
   qm31* h_res = nullptr;  // pinned result staging (64 QM31)
   uint32_t* h_mult = nullptr;  // pinned copy of the LogUp multiplicities
-  qm31* h_vec = nullptr;       // coherent pinned: vectors handed over by the tail kernels (3 x kTailMax)
+  qm31* h_vec = nullptr;       // coherent pinned: vectors handed over by k_handover (2 x kHandMax)
   size_t h_mult_cap = 0;
   qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
   uint32_t* h_flag = nullptr; // coherent pinned: sequence number of the last delivery
@@ -300,7 +312,7 @@ static int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out)
 
 // Result and mailbox sequence numbers come in consecutive ranges and restart
 // at 1 before they reach the codes reserved at the top of the u32 range
-// (kTailTimeout, kTailCancel); waits compare them modulo 2^32.
+// (kWaitTimeout, kWaitCancel); waits compare them modulo 2^32.
 constexpr uint32_t kSeqLimit = 0xFFFFFF00u;
 static uint32_t alloc_seq(uint32_t* counter, uint32_t n) {
   if (*counter >= kSeqLimit - n) *counter = 0;
@@ -315,7 +327,7 @@ static uint32_t alloc_seq(uint32_t* counter, uint32_t n) {
 // next reducing kernel on the stream overwrites them.
 static int make_sink(gkr_ctx* c, RoundSink* sk, int slot = 0) {
   qm31* part;
-  TRY(ensureT(c, S_PART, 4 * kMaxPartialBlocks, &part));
+  TRY(ensureT(c, S_PART, (size_t)kMaxSums * kMaxPartialBlocks, &part));
   sk->partials = part;
   sk->out = c->h_out + slot;
   sk->flag = c->h_flag;
@@ -341,8 +353,8 @@ static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_H
   uint64_t spins = 0;
   uint32_t got;
   // the flag only moves forward (mod 2^32): a later delivery implies this one
-  while ((int32_t)((got = *flag) - seq) < 0 || got == kTailTimeout) {
-    if (got == kTailTimeout) return fail(GKR_ERR_DEVICE, "persistent round kernel timed out waiting for a challenge");
+  while ((int32_t)((got = *flag) - seq) < 0 || got == kWaitTimeout) {
+    if (got == kWaitTimeout) return fail(GKR_ERR_DEVICE, "hand-over kernel timed out waiting for the challenges");
     if (++spins == (1u << 26)) {
       HIP_TRY(hipStreamSynchronize(c->stream));
       if ((int32_t)(*flag - seq) < 0) return fail(GKR_ERR_DEVICE, "device result %u not delivered", seq);
@@ -357,28 +369,199 @@ template <int NQ>
 static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
   return wait_result<NQ>(c, sk.seq, host_out, K_HOST_WAIT, (int)(sk.out - c->h_out));
 }
-// Host side of a persistent tail kernel: posts challenges into the mailbox.
-// If the host leaves before the protocol completes (an error), the guard
-// posts the cancel code so the kernel stops waiting at once.
-struct TailSession {
+// Host side of a k_handover launch: posts the last trip's challenges into
+// the mailbox and receives the folded vectors.  If the host leaves before
+// posting (an error), the guard posts the cancel code so the kernel stops
+// waiting at once, and drains the stream before the mailbox is reused.
+struct HandoverSession {
   gkr_ctx* c;
-  uint32_t res_base, mb_base;
-  bool done = false;
-  TailSession(gkr_ctx* c_, int n_results, int n_posts) : c(c_) {
-    res_base = alloc_seq(&c->seq, (uint32_t)n_results);
-    mb_base = alloc_seq(&c->mb_seq, (uint32_t)n_posts);
+  uint32_t res_seq = 0, mb_seq = 0;
+  bool launched = false, done = false;
+  explicit HandoverSession(gkr_ctx* c_) : c(c_) {}
+  // Launch k_handover<NV> over the vectors a (, b) of length len, to be folded by k challenges.
+  template <int NV>
+  int launch(const qm31* a, const qm31* b, uint64_t len, int k) {
+    if (len > (uint64_t)kHandMax || k < 0 || k > kTripMaxK || (len >> k) == 0)
+      return fail(GKR_ERR_DEVICE, "hand-over of %llu entries folded %d times", (unsigned long long)len, k);
+    res_seq = alloc_seq(&c->seq, 1);
+    mb_seq = alloc_seq(&c->mb_seq, 1);
+    hipLaunchKernelGGL(k_handover<NV>, dim3(1), dim3(kBlock), 0, c->stream, a, b, (uint32_t)len, k, c->mailbox,
+                       mb_seq, c->h_vec, c->h_flag, res_seq);
+    launched = true;
+    return check_launch();
   }
-  void post(uint32_t r, const qm31& alpha) {
-    c->mailbox->alpha = alpha;
-    __atomic_store_n(&c->mailbox->seq, mb_base + r, __ATOMIC_RELEASE);
+  void post(const qm31* chal, int k) {
+    for (int r = 0; r < k; r++) c->mailbox->alpha[r] = chal[r];
+    __atomic_store_n(&c->mailbox->seq, mb_seq, __ATOMIC_RELEASE);
   }
-  ~TailSession() {
-    if (!done) {  // error path: release the waiting kernel and let it drain before the mailbox is reused
-      __atomic_store_n(&c->mailbox->seq, kTailCancel, __ATOMIC_RELEASE);
+  // Wait for the folded vectors: count vectors of len entries each.
+  int fetch(uint64_t len, int count, std::vector<qm31>* out) {
+    TRY(wait_result<0>(c, res_seq, nullptr));
+    for (int v = 0; v < count; v++) out[v].assign(c->h_vec + v * len, c->h_vec + (v + 1) * len);
+    done = true;
+    return GKR_OK;
+  }
+  ~HandoverSession() {
+    if (launched && !done) {
+      __atomic_store_n(&c->mailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
       (void)hipStreamSynchronize(c->stream);
     }
   }
 };
+
+// ------------------------------------------------------------------ multi-round trips (host side)
+// A sumcheck over 2^T entries runs as a few device trips of K <= 3 rounds
+// each (k_trip: one launch plus the finisher per trip), then k_handover
+// folds the last trip's vectors and the host finishes the rounds on vectors
+// of at most host_len entries.  The first trip covers min(k0, T) rounds;
+// trips on vectors longer than kTripBig cover 2 rounds (their sums cost 2^K
+// products per entry), shorter ones 3.  The loop ends once the next trip's
+// vectors would fit the host, so the last trip's vectors have at most
+// host_len * 2^K <= kHandMax entries (host_len <= 256).
+struct Trip {
+  int t, K;    // rounds t .. t + K - 1
+  uint64_t n;  // vector length at round t
+};
+#ifndef GKR_TRIP_BIG
+#define GKR_TRIP_BIG (1ull << 16)
+#endif
+constexpr uint64_t kTripBig = GKR_TRIP_BIG;
+#ifndef GKR_TRIP_MAX_BLOCKS
+#define GKR_TRIP_MAX_BLOCKS 512
+#endif
+constexpr unsigned kTripMaxBlocks = GKR_TRIP_MAX_BLOCKS;  // partial rows per trip (the finisher adds them)
+static std::vector<Trip> plan_trips(int T, uint64_t host_len, int k0) {
+  std::vector<Trip> v;
+  if (T <= 0) return v;
+  int t = k0 < T ? k0 : T;
+  v.push_back({0, t, 1ull << T});
+  while (t < T && (1ull << (T - t)) > host_len) {
+    const uint64_t n = 1ull << (T - t);
+    int k = n > kTripBig ? 2 : 3;
+    if (k > T - t) k = T - t;
+    v.push_back({t, k, n});
+    t += k;
+  }
+  return v;
+}
+static inline int trip_nq(int kind, int K) { return kind == 2 ? (1 << K) : (1 << (2 * K)); }
+// eqlin(z, X) = (1 - z)(1 - X) + z X, the multilinear eq factor of one coordinate.
+static inline qm31 eqlin(const qm31& z, const qm31& x) {
+  const qm31 one = qm31_one();
+  return qm31_add(qm31_mul(qm31_sub(one, z), qm31_sub(one, x)), qm31_mul(z, x));
+}
+// Lagrange weights E[u] (u < 2^j, first challenge on the MSB) of r[0..j).
+static void lagrange_weights(const qm31* r, int j, qm31* E) {
+  E[0] = qm31_one();
+  for (int i = 0; i < j; i++) {
+    const int m = 1 << i;
+    for (int u = m - 1; u >= 0; u--) {
+      const qm31 e = E[u];
+      E[2 * u + 1] = qm31_mul(e, r[i]);
+      E[2 * u] = qm31_sub(e, E[2 * u + 1]);
+    }
+  }
+}
+// Round j (0-based within the trip) of a product-type trip from its cross sums
+// G (4^K, row-major over sub-vectors c, c'), evaluated at the nx points xs:
+//   p(X) = sum_v sum_{u,u',b,b'} E[u] E[u'] eqlin(X,b) eqlin(X,b') G[(u,b,v)][(u',b',v)]
+// with E the Lagrange weights of the trip's challenges r[0..j) and v running
+// over the trip's later variables.  For the eq-sumcheck (zt given: the claim
+// coordinates of the trip's variables; cpre: prod of eqlin(z_l, r_l) over all
+// earlier rounds) the eq factors are applied:
+//   p(X) *= cpre * prod_{i<j} eqlin(zt_i, r_i) * eqlin(zt_j, X),  v weighted by eqlin(zt, v).
+static void trip_round_gram(const qm31* G, int K, int j, const qm31* r, int nx, const qm31* xs, qm31* out,
+                            const qm31* zt, const qm31& cpre) {
+  const int nu = 1 << j, nv = 1 << (K - j - 1), sh_b = K - j - 1, dim = 1 << K;
+  qm31 E[8];
+  lagrange_weights(r, j, E);
+  qm31 H[2][2] = {{qm31_zero(), qm31_zero()}, {qm31_zero(), qm31_zero()}};
+  for (int v = 0; v < nv; v++) {
+    qm31 ez = qm31_one();
+    if (zt)
+      for (int i = 0; i < K - j - 1; i++)
+        ez = qm31_mul(ez, ((v >> (K - j - 2 - i)) & 1) ? zt[j + 1 + i] : qm31_sub(qm31_one(), zt[j + 1 + i]));
+    for (int b = 0; b < 2; b++)
+      for (int b2 = 0; b2 < 2; b2++) {
+        qm31 acc = qm31_zero();
+        for (int u = 0; u < nu; u++) {
+          const int row = (u << (K - j)) | (b << sh_b) | v;
+          qm31 inner = qm31_zero();
+          for (int u2 = 0; u2 < nu; u2++) {
+            const int col = (u2 << (K - j)) | (b2 << sh_b) | v;
+            inner = qm31_add(inner, qm31_mul(E[u2], G[row * dim + col]));
+          }
+          acc = qm31_add(acc, qm31_mul(E[u], inner));
+        }
+        H[b][b2] = qm31_add(H[b][b2], zt ? qm31_mul(ez, acc) : acc);
+      }
+  }
+  qm31 pre = cpre;
+  if (zt)
+    for (int i = 0; i < j; i++) pre = qm31_mul(pre, eqlin(zt[i], r[i]));
+  for (int k = 0; k < nx; k++) {
+    const qm31 x = xs[k];
+    const qm31 e0 = qm31_sub(qm31_one(), x), e1 = x;
+    qm31 p = qm31_add(qm31_mul(qm31_mul(e0, e0), H[0][0]),
+                      qm31_add(qm31_mul(qm31_mul(e0, e1), qm31_add(H[0][1], H[1][0])), qm31_mul(qm31_mul(e1, e1), H[1][1])));
+    if (zt) p = qm31_mul(p, qm31_mul(pre, eqlin(zt[j], x)));
+    out[k] = p;
+  }
+}
+// Round j of a degree-1 trip from its 2^K sums S: p(0), p(1).
+static void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out) {
+  qm31 E[8];
+  lagrange_weights(r, j, E);
+  out[0] = out[1] = qm31_zero();
+  for (int c = 0; c < (1 << K); c++) {
+    const int u = c >> (K - j), b = (c >> (K - j - 1)) & 1;
+    out[b] = qm31_add(out[b], qm31_mul(E[u], S[c]));
+  }
+}
+// Launch k_trip<KIND, K> over sources sa (, sb) of length n << np with the
+// np pending challenges `pend`; folded vectors to da (, db) when given; eq
+// weights (KIND 1) from hi/lo; then the finisher into sink slot `slot`.
+template <int KIND, int K>
+static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n, int np, const TripChal& al,
+                         qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, const RoundSink& sk,
+                         unsigned grid) {
+  hipLaunchKernelGGL((k_trip<KIND, K>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
+                     sk.partials);
+  TRY(check_launch());
+  constexpr int NQ = TripShape<KIND, K>::NQ;
+  hipLaunchKernelGGL(k_finish_wide<NQ>, dim3(1), dim3(kFinishBlock), 0, c->stream, sk, grid);
+  return check_launch();
+}
+static int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
+                       const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
+                       RoundSink* sk) {
+  if (np < 0 || np > kTripMaxK || K < 0 || K > kTripMaxK || (n >> K) == 0 || (kind == 1) != (hi != nullptr))
+    return fail(GKR_ERR_DEVICE, "bad trip (kind %d, K %d, np %d, n %llu)", kind, K, np, (unsigned long long)n);
+  TripChal al;
+  memset(&al, 0, sizeof al);
+  for (int i = 0; i < np; i++) al.c[i] = pend[i];
+  TRY(make_sink(c, sk, slot));
+  unsigned grid = partial_grid(n);  // one entry per thread up to kTripMaxBlocks workgroups
+  if (grid > kTripMaxBlocks) grid = kTripMaxBlocks;
+  const int nvec = kind == 2 ? 1 : 2;
+  TimedLaunch tl(c, kind == 0 ? K_MM_ROUND : K_EQ3_ROUND,
+                 16ull * nvec * ((n << np) + (da ? n : 0)));
+#define GKR_TRIP_CASE(KI, KK) \
+  if (kind == KI && K == KK) return launch_trip_k<KI, KK>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid);
+  GKR_TRIP_CASE(0, 1) GKR_TRIP_CASE(0, 2) GKR_TRIP_CASE(0, 3)
+  GKR_TRIP_CASE(1, 0) GKR_TRIP_CASE(1, 1) GKR_TRIP_CASE(1, 2) GKR_TRIP_CASE(1, 3)
+  GKR_TRIP_CASE(2, 1) GKR_TRIP_CASE(2, 2) GKR_TRIP_CASE(2, 3)
+#undef GKR_TRIP_CASE
+  return fail(GKR_ERR_DEVICE, "no trip kernel for kind %d, K %d", kind, K);
+}
+// Wait for a trip's nq sums.
+static int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out) {
+  TRY(wait_result<0>(c, sk.seq, nullptr, K_HOST_WAIT, 0));
+  const int slot = (int)(sk.out - c->h_out);
+  for (int q = 0; q < nq; q++) out[q] = c->h_out[slot + q];
+  return GKR_OK;
+}
+
 static int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out) {
   HIP_TRY(hipMemcpyAsync(c->h_res, dev, count * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
   TRY(sync(c));
@@ -561,19 +744,19 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
     return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");
   }
   if (hipHostMalloc((void**)&c->h_res, 64 * sizeof(qm31), hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&c->h_out, 64 * sizeof(qm31) + 256, hipHostMallocCoherent | hipHostMallocMapped) !=
+      hipHostMalloc((void**)&c->h_out, kOutSlots * sizeof(qm31) + 256, hipHostMallocCoherent | hipHostMallocMapped) !=
           hipSuccess) {
     gkr_ctx_destroy(c);
     return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
   }
-  if (hipHostMalloc((void**)&c->h_vec, 3 * kTailMax * sizeof(qm31), hipHostMallocCoherent | hipHostMallocMapped) !=
+  if (hipHostMalloc((void**)&c->h_vec, 2 * kHandMax * sizeof(qm31), hipHostMallocCoherent | hipHostMallocMapped) !=
       hipSuccess) {
     gkr_ctx_destroy(c);
     return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
   }
-  c->h_flag = reinterpret_cast<uint32_t*>(c->h_out + 64);
+  c->h_flag = reinterpret_cast<uint32_t*>(c->h_out + kOutSlots);
   *c->h_flag = 0;
-  c->mailbox = reinterpret_cast<Mailbox*>(reinterpret_cast<char*>(c->h_out) + 64 * sizeof(qm31) + 128);
+  c->mailbox = reinterpret_cast<Mailbox*>(reinterpret_cast<char*>(c->h_out) + kOutSlots * sizeof(qm31) + 128);
   c->mailbox->seq = 0;
   *out = c;
   return GKR_OK;
@@ -762,20 +945,17 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
   return GKR_OK;
 }
 
-static int round0_sums(gkr_ctx* c, uint64_t pk, qm31 s[3]) {
+// First trip of the product sumcheck (rounds 0 .. K-1, K = min(3, log pk)):
+// the 4^K cross sums of the restricted vectors f_a, f_b (S_FA0, S_FB0).
+static int first_product_trip(gkr_ctx* c, uint64_t pk, int* K, qm31* g) {
   qm31 *fa, *fb;
   TRY(ensureT(c, S_FA0, pk, &fa));
   TRY(ensureT(c, S_FB0, pk, &fb));
+  const int T = log2_exact(pk);
+  *K = T < kTripMaxK ? T : kTripMaxK;
   RoundSink sk;
-  TRY(make_sink(c, &sk));
-  const uint64_t half = pk / 2;
-  {
-    TimedLaunch t(c, K_MM_ROUND, 32 * pk);
-    hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, fa, fb, (qm31*)nullptr,
-                       (qm31*)nullptr, half, 0, qm31_zero(), sk);
-  }
-  TRY(launch_finish<3>(c, sk, partial_grid(half)));
-  return wait_sink<3>(c, sk, s);
+  TRY(launch_trip(c, 0, *K, fa, fb, pk, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, &sk));
+  return wait_trip(c, sk, trip_nq(0, *K), g);
 }
 
 static bool cache_matches(const gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, int n_ri,
@@ -820,57 +1000,42 @@ static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* 
   c->mm.b = b;
   c->mm.r_i.assign(r_i, r_i + n_ri);
   c->mm.r_j.assign(r_j, r_j + n_rj);
-  c->mm.have_round0 = false;
+  c->mm.have_trip0 = false;
   return GKR_OK;
 }
 
 // The last rounds of each sumcheck run on the host once the vectors are this
-// short: a round there costs less than a device round trip (post the
-// challenge, fold and reduce in one workgroup, deliver).  The persistent tail
-// kernel hands its LDS vectors over and exits.
+// short (the device trips stop there; k_handover folds the last trip's
+// vectors and hands them over).
 #ifndef GKR_HOST_TAIL_MM
-#define GKR_HOST_TAIL_MM 256    // product sumcheck: 5 QM31 products per pair
+#define GKR_HOST_TAIL_MM 128   // product sumcheck: 5 QM31 products per pair
 #endif
 #ifndef GKR_HOST_TAIL_EQ3
-#define GKR_HOST_TAIL_EQ3 128   // eq-sumcheck: 11 products per pair
+#define GKR_HOST_TAIL_EQ3 128  // eq-sumcheck: 11 products per pair
 #endif
 #ifndef GKR_HOST_TAIL_SUM
-#define GKR_HOST_TAIL_SUM 1024  // multiplicity sumcheck: 1 product per pair
+#define GKR_HOST_TAIL_SUM 256  // multiplicity sumcheck: 1 product per pair
 #endif
 constexpr uint64_t kHostTailMM = GKR_HOST_TAIL_MM;
 constexpr uint64_t kHostTailEq3 = GKR_HOST_TAIL_EQ3;
 constexpr uint64_t kHostTailSum = GKR_HOST_TAIL_SUM;
-// Wait for the vector hand-over `seq` and copy `count` vectors of `len` entries.
-static int fetch_tail_vectors(gkr_ctx* c, uint32_t seq, uint64_t len, int count, std::vector<qm31>* out) {
-  TRY(wait_result<0>(c, seq, nullptr));
-  for (int v = 0; v < count; v++) out[v].assign(c->h_vec + v * len, c->h_vec + (v + 1) * len);
-  return GKR_OK;
-}
+static_assert(kHostTailMM * 8 <= (uint64_t)kHandMax && kHostTailEq3 * 8 <= (uint64_t)kHandMax &&
+                  kHostTailSum * 8 <= (uint64_t)kHandMax,
+              "the last trip's vectors must fit k_handover");
 
 // Degree-2 product sumcheck sum_x f_a(x) f_b(x) over 2^T entries: the round
-// loop of reduce_matmul_layer (backend.rs:146-177; gpu_sumcheck.rs:2820-2840).
-// in_a/in_b are read by rounds 0 and 1; round t >= 1 folds into
-// bufs[(t - 1) & 1] (bufs[0] holds 2^(T-1) + 1 entries, bufs[1] 2^(T-2) + 1 and
-// may alias the inputs, which round 2 then overwrites: *invalidate_at_round2
-// is cleared at that point).  round0, when given, holds the round-0 sums
-// (s0, s1, s2) already computed for these inputs.
+// loop of reduce_matmul_layer (backend.rs:146-177; gpu_sumcheck.rs:2820-2840),
+// as device trips of up to 3 rounds (plan_trips), then the host.  in_a/in_b
+// are only read; trip j >= 1 writes its folded vectors to bufs[(j - 1) & 1]
+// (bufs[0] holds 2^(T-1) entries, bufs[1] 2^(T-2)).  g0, when given, holds
+// the first trip's sums (rounds 0 .. k0 - 1) already computed for these inputs.
 static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, const qm31* in_b,
-                            qm31* const bufs_a[2], qm31* const bufs_b[2], const qm31* round0,
-                            bool* invalidate_at_round2, gkr_qm31* round_polys, gkr_qm31* challenges,
-                            gkr_qm31* final_a, gkr_qm31* final_b) {
+                            qm31* const bufs_a[2], qm31* const bufs_b[2], const qm31* g0, int k0,
+                            gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b) {
   const qm31 inv2 = qm31_from_m31(1u << 30);  // 2^-1 mod P
   const uint64_t pk = 1ull << T;
-  const qm31* cur_a = in_a;
-  const qm31* cur_b = in_b;
-  // Big rounds t < t0 fold into ping-pong buffers (round t >= 1 writes
-  // bufs[(t-1)&1]).  Rounds t >= t0 (at most kTailMax elements) and the final
-  // fold run in one persistent workgroup (k_mm_tail).
-  int t0 = 0;
-  while ((pk >> t0) > (uint64_t)kTailMax) t0++;
-  int t1 = t0;  // rounds t >= t1 on the host
-  while ((pk >> t1) > kHostTailMM) t1++;
-  const int n_tail = t1 - t0;
-  qm31 alpha = qm31_zero();
+  const std::vector<Trip> trips = plan_trips(T, kHostTailMM, g0 ? k0 : kTripMaxK);
+  std::vector<qm31> chal(T);
   auto absorb = [&](int t, const qm31* sums) {
     const qm31 c0 = sums[0];
     const qm31 c2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(sums[2], sums[1]), sums[1]), sums[0]), inv2);
@@ -880,73 +1045,50 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
     round_polys[3 * t + 2] = G(c2);
     HostTimer ht(c, K_HOST_FS);
     ch.mix_poly_coeffs(c0, c1, c2);
-    alpha = ch.draw_qm31();
-    challenges[t] = G(alpha);
+    chal[t] = ch.draw_qm31();
+    challenges[t] = G(chal[t]);
   };
-  std::unique_ptr<TailSession> tail;
-  auto launch_tail = [&]() -> int {
-    const uint32_t len_in = (uint32_t)(t0 == 0 ? pk : (pk >> (t0 - 1)));
-    tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
-    hipLaunchKernelGGL(k_mm_tail, dim3(1), dim3(kBlock), 0, c->stream, cur_a, cur_b, len_in, t0 > 0 ? 1 : 0,
-                       n_tail, c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base, c->h_vec);
-    return check_launch();
-  };
-  for (int t = 0; t < t0; t++) {
-    const uint64_t half = (pk >> t) / 2;
-    qm31 sums[3];
-    if (t == 0) {
-      if (round0) {
-        sums[0] = round0[0]; sums[1] = round0[1]; sums[2] = round0[2];
-        if (t0 == 1) TRY(launch_tail());
-      } else {
-        RoundSink sk;
-        TRY(make_sink(c, &sk));
-        {
-          TimedLaunch tl(c, K_MM_ROUND, 32 * pk);
-          hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, in_a, in_b,
-                             (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
-        }
-        TRY(launch_finish<3>(c, sk, partial_grid(half)));
-        if (t0 == 1) TRY(launch_tail());
-        TRY(wait_sink<3>(c, sk, sums));
-      }
+  const qm31 xs[3] = {qm31_zero(), qm31_one(), qm31_from_m31(2)};
+  HandoverSession ho(c);
+  const qm31* src_a = in_a;
+  const qm31* src_b = in_b;
+  int np = 0;
+  const qm31* pend = nullptr;
+  for (size_t j = 0; j < trips.size(); j++) {
+    const Trip& tr = trips[j];
+    const bool last = j + 1 == trips.size();
+    qm31 g[kMaxSums];
+    if (j == 0 && g0) {
+      for (int q = 0; q < trip_nq(0, tr.K); q++) g[q] = g0[q];
+      if (last) TRY(ho.launch<2>(in_a, in_b, tr.n, tr.K));
     } else {
-      qm31* na = bufs_a[(t - 1) & 1];
-      qm31* nb = bufs_b[(t - 1) & 1];
-      if (t == 2 && invalidate_at_round2) *invalidate_at_round2 = false;
+      qm31* da = j == 0 ? nullptr : bufs_a[(j - 1) & 1];
+      qm31* db = j == 0 ? nullptr : bufs_b[(j - 1) & 1];
       RoundSink sk;
-      TRY(make_sink(c, &sk));
-      {
-        // algorithmic bytes: 2 vectors x (read 4*half + write 2*half) QM31 = 48 * n_{t-1}
-        TimedLaunch tl(c, K_MM_ROUND, 192 * half);
-        hipLaunchKernelGGL(k_mm_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cur_a, cur_b, na, nb,
-                           half, 1, alpha, sk);
+      TRY(launch_trip(c, 0, tr.K, src_a, src_b, tr.n, np, pend, da, db, nullptr, nullptr, 0, 0, &sk));
+      if (j > 0) {
+        src_a = da;
+        src_b = db;
       }
-      TRY(launch_finish<3>(c, sk, partial_grid(half)));
-      cur_a = na;
-      cur_b = nb;
-      if (t == t0 - 1) TRY(launch_tail());
-      TRY(wait_sink<3>(c, sk, sums));
+      if (last) TRY(ho.launch<2>(src_a, src_b, tr.n, tr.K));
+      TRY(wait_trip(c, sk, trip_nq(0, tr.K), g));
     }
-    absorb(t, sums);
+    for (int i = 0; i < tr.K; i++) {
+      qm31 sums[3];
+      trip_round_gram(g, tr.K, i, chal.data() + tr.t, 3, xs, sums, nullptr, qm31_zero());
+      absorb(tr.t + i, sums);
+    }
+    np = tr.K;
+    pend = chal.data() + tr.t;
   }
-  if (t0 == 0) {
-    TRY(launch_tail());
-  } else {
-    tail->post(0, alpha);  // fold by the challenge of round t0 - 1
-  }
-  for (int r = 0; r < n_tail; r++) {
-    qm31 sums[3];
-    TRY(wait_result<3>(c, tail->res_base + r, sums));
-    absorb(t0 + r, sums);
-    tail->post(r + 1, alpha);
-  }
+  const int t_end = trips.empty() ? 0 : trips.back().t + trips.back().K;
+  const uint64_t hlen = pk >> t_end;
   std::vector<qm31> v[2];
-  TRY(fetch_tail_vectors(c, tail->res_base + n_tail, pk >> t1, 2, v));
-  tail->done = true;
+  ho.post(pend, np);
+  TRY(ho.fetch(hlen, 2, v));
   std::vector<qm31>& A = v[0];
   std::vector<qm31>& B = v[1];
-  for (int t = t1; t < T; t++) {
+  for (int t = t_end; t < T; t++) {
     const size_t half = A.size() / 2;
     qm31 sums[3] = {qm31_zero(), qm31_zero(), qm31_zero()};
     for (size_t i = 0; i < half; i++) {
@@ -957,8 +1099,8 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
     }
     absorb(t, sums);
     for (size_t i = 0; i < half; i++) {
-      A[i] = qm31_fold(A[i], A[i + half], alpha);
-      B[i] = qm31_fold(B[i], B[i + half], alpha);
+      A[i] = qm31_fold(A[i], A[i + half], chal[t]);
+      B[i] = qm31_fold(B[i], B[i + half], chal[t]);
     }
     A.resize(half);
     B.resize(half);
@@ -978,13 +1120,15 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
   HIP_TRY(hipSetDevice(c->device));
   TRY(ensure_restricted(c, a, b, r_i, n_ri, r_j, n_rj));
   const int T = log2_exact(pk);
-  qm31 *fa0, *fa1, *fb0, *fb1;
+  qm31 *fa0, *fa1, *fb0, *fb1, *fa2, *fb2;
   TRY(ensureT(c, S_FA0, pk, &fa0));
   TRY(ensureT(c, S_FB0, pk, &fb0));
   TRY(ensureT(c, S_FA1, pk / 2 + 1, &fa1));
   TRY(ensureT(c, S_FB1, pk / 2 + 1, &fb1));
-  // The folds below overwrite the restricted vectors' successors only;
-  // S_FA0/S_FB0 keep round 0 input, so a cached restriction stays valid.
+  TRY(ensureT(c, S_FA2, pk / 4 + 1, &fa2));
+  TRY(ensureT(c, S_FB2, pk / 4 + 1, &fb2));
+  // The trips write only S_FA1/S_FB1 and S_FA2/S_FB2; S_FA0/S_FB0 keep the
+  // restricted vectors, so a cached restriction stays valid.
   if (T == 0) {
     qm31 v[1];
     TRY(fetch_q(c, fa0, 1, v));
@@ -993,10 +1137,12 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
     *final_b = G(v[0]);
     return GKR_OK;
   }
-  qm31* bufs_a[2] = {fa1, fa0};
-  qm31* bufs_b[2] = {fb1, fb0};
-  return product_sumcheck(c, ch, T, fa0, fb0, bufs_a, bufs_b, c->mm.have_round0 ? c->mm.round0 : nullptr,
-                          &c->mm.valid, round_polys, challenges, final_a, final_b);
+  qm31* bufs_a[2] = {fa1, fa2};
+  qm31* bufs_b[2] = {fb1, fb2};
+  const bool have = c->mm.have_trip0;
+  c->mm.have_trip0 = false;  // used once: the transcript moves on
+  return product_sumcheck(c, ch, T, fa0, fb0, bufs_a, bufs_b, have ? c->mm.trip0 : nullptr, c->mm.trip0_k,
+                          round_polys, challenges, final_a, final_b);
 }
 
 extern "C" int gkr_reduce_matmul_layer(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i,
@@ -1018,7 +1164,6 @@ extern "C" int gkr_matmul_output_claim(gkr_ctx* c, const gkr_matrix* a, const gk
   HIP_TRY(hipSetDevice(c->device));
   TRY(ensure_restricted(c, a, b, r_out, n_ri, r_out + n_ri, n_vars - n_ri));
   const uint64_t pk = next_pow2(a->cols);
-  qm31 s[3];
   if (pk == 1) {
     qm31 fa[1], fb[1];
     qm31 *dfa, *dfb;
@@ -1029,10 +1174,13 @@ extern "C" int gkr_matmul_output_claim(gkr_ctx* c, const gkr_matrix* a, const gk
     *value = G(qm31_mul(fa[0], fb[0]));
     return GKR_OK;
   }
-  TRY(round0_sums(c, pk, s));
-  c->mm.have_round0 = true;
-  c->mm.round0[0] = s[0]; c->mm.round0[1] = s[1]; c->mm.round0[2] = s[2];
-  *value = G(qm31_add(s[0], s[1]));
+  int K = 0;
+  TRY(first_product_trip(c, pk, &K, c->mm.trip0));
+  c->mm.trip0_k = K;
+  c->mm.have_trip0 = true;
+  qm31 v = qm31_zero();  // sum_x f_a(x) f_b(x) = trace of the cross sums
+  for (int q = 0; q < (1 << K); q++) v = qm31_add(v, c->mm.trip0[q * ((1 << K) + 1)]);
+  *value = G(v);
   return GKR_OK;
 }
 
@@ -1307,40 +1455,88 @@ static const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint3
 
 // Eq-weighted degree-3 sumcheck over n = 2^nv entries (the eq-sumcheck of
 // reduce_activation_layer, gkr/prover.rs:6501-6556, and of reduce_mul_layer,
-// 6197-6245): s_t = sum_i eq_t * w_t * d_t at t = 0..3, Newton differences to
-// (c0, c1, c2, c3), mix_poly_coeffs_deg3, draw, fold.  e0/w0/d0 hold the
-// inputs and are overwritten; e1/w1/d1 (n/2 + 1 entries) are the other half of
-// the ping-pong.  Writes 4 * nv round coefficients, nv challenges and the final
-// (eq, w, d) values.
-static bool eq3_has_grid_rounds(int nv) { return nv >= 0 && (1ull << nv) > (uint64_t)(kTailMax / 2); }
-// Launch round 0 of eq3_sumcheck ahead of the transcript (it needs no
-// challenge); only when the sumcheck has grid rounds.
-static int eq3_launch_round0(gkr_ctx* c, int nv, const qm31* e0, const qm31* w0, const qm31* d0, RoundSink* sk) {
-  const uint64_t half = (1ull << nv) / 2;
-  TRY(make_sink(c, sk));
-  {
-    TimedLaunch tl(c, K_EQ3_ROUND, 96 * half);
-    hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, e0, w0, d0,
-                       (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), *sk);
+// 6197-6245): s_t = sum_x eq_t * w_t * d_t at t = 0..3, Newton differences to
+// (c0, c1, c2, c3), mix_poly_coeffs_deg3, draw, fold.
+//
+// eq(z, x) = prod_l eqlin(z_l, x_l) is kept factored: only w and d are stored
+// and folded.  Round t's polynomial is eqlin(z_t, X) times the product of
+// eqlin(z_l, r_l) over the earlier rounds times sum_x eq(z_{>t}, x) w d; the
+// trips weight their cross sums by the eq part below their variables (two
+// small tables per trip, built at the start), and the host finish rebuilds
+// the eq vector of the remaining variables.  The polynomials, challenges and
+// final values equal those of folding eq like w and d (the polynomial of each
+// round is unique).
+constexpr int kEqLoMax = 10;  // variables in the lower eq table of a trip
+struct Eq3Plan {
+  int nv = 0;
+  std::vector<Trip> trips;
+  std::vector<uint32_t> hi_off, lo_off;  // per trip, offsets into S_EQPARTS
+  std::vector<int> h;                    // per trip, variables in the lower table
+};
+// Plan the trips of an eq-sumcheck over 2^nv entries for claim point z and
+// launch the kernel that builds their eq tables (S_EQPARTS).
+static int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
+  pl->nv = nv;
+  pl->trips = plan_trips(nv, kHostTailEq3, (1ull << nv) > kTripBig ? 2 : kTripMaxK);
+  pl->hi_off.clear();
+  pl->lo_off.clear();
+  pl->h.clear();
+  if (pl->trips.empty()) return GKR_OK;
+  EqPartsArg arg;
+  memset(&arg, 0, sizeof arg);
+  arg.z = make_point(z, nv);
+  uint32_t total = 0;
+  auto table = [&](int s0, int m) -> uint32_t {
+    for (int i = 0; i < arg.count; i++)
+      if (arg.s[i] == s0 && arg.m[i] == m) return arg.off[i];
+    const int i = arg.count++;
+    arg.s[i] = s0;
+    arg.m[i] = m;
+    arg.off[i] = total;
+    total += 1u << m;
+    return arg.off[i];
+  };
+  for (const Trip& tr : pl->trips) {
+    if (arg.count + 2 > kEqPartsMax) return fail(GKR_ERR_DEVICE, "too many eq tables");
+    const int m = nv - tr.t - tr.K;  // coordinates below the trip's variables
+    const int h = m < kEqLoMax ? m : kEqLoMax;
+    pl->hi_off.push_back(table(tr.t + tr.K, m - h));
+    pl->lo_off.push_back(table(nv - h, h));
+    pl->h.push_back(h);
   }
-  return launch_finish<4>(c, *sk, partial_grid(half));
+  qm31* parts;
+  TRY(ensureT(c, S_EQPARTS, total, &parts));
+  {
+    TimedLaunch tl(c, K_EQ_TABLE, 16ull * total);
+    hipLaunchKernelGGL(k_eq_parts, dim3(grid_for(total)), dim3(kBlock), 0, c->stream, arg, total, parts);
+  }
+  return check_launch();
 }
-static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, int nv, qm31* e0, qm31* w0, qm31* d0, qm31* e1, qm31* w1,
-                        qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3], const RoundSink* pre0 = nullptr) {
-  const uint64_t n = 1ull << nv;
+// Launch trip j of the plan over sources w, d (np pending challenges pend),
+// folded vectors to dw, dd when given.
+static int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, const qm31* d, int np,
+                           const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk) {
+  qm31* parts = (qm31*)c->buf[S_EQPARTS];
+  const Trip& tr = pl.trips[j];
+  return launch_trip(c, 1, tr.K, w, d, tr.n, np, pend, dw, dd, parts + pl.hi_off[j], parts + pl.lo_off[j], pl.h[j],
+                     slot, sk);
+}
+// The sumcheck for claim point z over w0, d0 (overwritten: the trips' folded
+// vectors go to w1/d1 (n/2 entries) and w0/d0 alternately).  pre0: trip 0
+// already launched (eq3_launch_trip, any slot).  Writes 4 * nv round
+// coefficients, nv challenges and the final (eq, w, d) values.
+static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& pl, qm31* w0, qm31* d0,
+                        qm31* w1, qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3],
+                        const RoundSink* pre0 = nullptr) {
+  const int nv = pl.nv;
   if (nv == 0) {
-    TRY(fetch_q(c, e0, 1, fin + 0));
+    fin[0] = qm31_one();
     TRY(fetch_q(c, w0, 1, fin + 1));
     return fetch_q(c, d0, 1, fin + 2);
   }
   const qm31 inv2 = qm31_from_m31(1u << 30);
   const qm31 inv6 = qm31_from_m31(m31_inv(6));
   const qm31 two = qm31_from_m31(2), three = qm31_from_m31(3);
-  const qm31 *ce = e0, *cw = w0, *cd = d0;
-  qm31* be[2] = {e1, e0};
-  qm31* bw[2] = {w1, w0};
-  qm31* bd[2] = {d1, d0};
-  qm31 alpha = qm31_zero();
   auto absorb3 = [&](int t, const qm31* s) {
     const qm31 dd1 = qm31_sub(s[1], s[0]);
     const qm31 dd2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
@@ -1355,82 +1551,78 @@ static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, int nv, qm31* e0, qm31* 
     rp_out[4 * t + 3] = G(c3);
     HostTimer ht(c, K_HOST_FS);
     C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
-    alpha = C.draw_qm31();
-    chal[t] = alpha;
+    chal[t] = C.draw_qm31();
   };
-  // big rounds t < t0 as grid kernels, rounds t >= t0 (<= kTailMax/2
-  // elements per vector) and the final fold in k_eq3_tail
-  int t0 = 0;
-  while ((n >> t0) > (uint64_t)(kTailMax / 2)) t0++;
-  int t1 = t0;  // rounds t >= t1 on the host
-  while ((n >> t1) > kHostTailEq3) t1++;
-  const int n_tail = t1 - t0;
-  std::unique_ptr<TailSession> tail;
-  auto launch_tail = [&]() -> int {
-    const uint32_t len_in = (uint32_t)(t0 == 0 ? n : (n >> (t0 - 1)));
-    tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
-    hipLaunchKernelGGL(k_eq3_tail, dim3(1), dim3(kBlock), 0, c->stream, ce, cw, cd, len_in, t0 > 0 ? 1 : 0, n_tail,
-                       c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base, c->h_vec);
-    return check_launch();
-  };
-  for (int t = 0; t < t0; t++) {
-    const uint64_t half = (n >> t) / 2;
-    qm31 sums[4];
+  const qm31 xs[4] = {qm31_zero(), qm31_one(), two, three};
+  qm31* bw[2] = {w1, w0};
+  qm31* bd[2] = {d1, d0};
+  HandoverSession ho(c);
+  const qm31* sw = w0;
+  const qm31* sd = d0;
+  int np = 0;
+  const qm31* pend = nullptr;
+  qm31 cpre = qm31_one();  // prod of eqlin(z_l, r_l) over the rounds done
+  for (size_t j = 0; j < pl.trips.size(); j++) {
+    const Trip& tr = pl.trips[j];
+    const bool last = j + 1 == pl.trips.size();
+    qm31 g[kMaxSums];
     RoundSink sk;
-    if (t == 0 && pre0) {
+    if (j == 0 && pre0) {
       sk = *pre0;
-    } else if (t == 0) {
-      TRY(eq3_launch_round0(c, nv, ce, cw, cd, &sk));
     } else {
-      TRY(make_sink(c, &sk));
-      {
-        // 3 vectors x (read 4*half + write 2*half) QM31 = 72 * n_{t-1}
-        TimedLaunch tl(c, K_EQ3_ROUND, 288 * half);
-        qm31 *ne = be[(t - 1) & 1], *nw = bw[(t - 1) & 1], *nd = bd[(t - 1) & 1];
-        hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, ce, cw, cd, ne, nw, nd,
-                           half, 1, alpha, sk);
-        ce = ne; cw = nw; cd = nd;
+      qm31* dw = j == 0 ? nullptr : bw[(j - 1) & 1];
+      qm31* dd = j == 0 ? nullptr : bd[(j - 1) & 1];
+      TRY(eq3_launch_trip(c, pl, j, sw, sd, np, pend, dw, dd, 0, &sk));
+      if (j > 0) {
+        sw = dw;
+        sd = dd;
       }
-      TRY(launch_finish<4>(c, sk, partial_grid(half)));
     }
-    if (t == t0 - 1) TRY(launch_tail());
-    TRY(wait_sink<4>(c, sk, sums));
-    absorb3(t, sums);
+    if (last) TRY(ho.launch<2>(sw, sd, tr.n, tr.K));
+    TRY(wait_trip(c, sk, trip_nq(1, tr.K), g));
+    for (int i = 0; i < tr.K; i++) {
+      qm31 sums[4];
+      trip_round_gram(g, tr.K, i, chal + tr.t, 4, xs, sums, z + tr.t, cpre);
+      absorb3(tr.t + i, sums);
+    }
+    for (int i = 0; i < tr.K; i++) cpre = qm31_mul(cpre, eqlin(z[tr.t + i], chal[tr.t + i]));
+    np = tr.K;
+    pend = chal + tr.t;
   }
-  if (t0 == 0) {
-    TRY(launch_tail());
-  } else {
-    tail->post(0, alpha);
+  const int t_end = pl.trips.back().t + pl.trips.back().K;
+  const uint64_t hlen = 1ull << (nv - t_end);
+  std::vector<qm31> v[2];
+  ho.post(pend, np);
+  TRY(ho.fetch(hlen, 2, v));
+  std::vector<qm31>& W = v[0];
+  std::vector<qm31>& D = v[1];
+  // eq of the remaining coordinates, scaled by the factors already fixed
+  std::vector<qm31> E(1, cpre);
+  for (int l = t_end; l < nv; l++) {
+    std::vector<qm31> nE(2 * E.size());
+    for (size_t x = 0; x < E.size(); x++) {
+      nE[2 * x + 1] = qm31_mul(E[x], z[l]);
+      nE[2 * x] = qm31_sub(E[x], nE[2 * x + 1]);
+    }
+    E.swap(nE);
   }
-  for (int r = 0; r < n_tail; r++) {
-    qm31 sums[4];
-    TRY(wait_result<4>(c, tail->res_base + r, sums));
-    absorb3(t0 + r, sums);
-    tail->post(r + 1, alpha);
-  }
-  std::vector<qm31> v[3];
-  TRY(fetch_tail_vectors(c, tail->res_base + n_tail, n >> t1, 3, v));
-  tail->done = true;
-  std::vector<qm31>& E = v[0];
-  std::vector<qm31>& W = v[1];
-  std::vector<qm31>& D = v[2];
-  for (int t = t1; t < nv; t++) {
+  for (int t = t_end; t < nv; t++) {
     const size_t half = E.size() / 2;
     qm31 sums[4] = {qm31_zero(), qm31_zero(), qm31_zero(), qm31_zero()};
     for (size_t i = 0; i < half; i++) {
-      const qm31 e0 = E[i], e1 = E[i + half], w0 = W[i], w1 = W[i + half], d0 = D[i], d1 = D[i + half];
-      sums[0] = qm31_add(sums[0], qm31_mul(qm31_mul(e0, w0), d0));
-      sums[1] = qm31_add(sums[1], qm31_mul(qm31_mul(e1, w1), d1));
-      const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1, w0), dd = qm31_sub(d1, d0);
-      const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1, dw), d2 = qm31_add(d1, dd);
+      const qm31 e0 = E[i], e1 = E[i + half], w0v = W[i], w1v = W[i + half], d0v = D[i], d1v = D[i + half];
+      sums[0] = qm31_add(sums[0], qm31_mul(qm31_mul(e0, w0v), d0v));
+      sums[1] = qm31_add(sums[1], qm31_mul(qm31_mul(e1, w1v), d1v));
+      const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1v, w0v), dd = qm31_sub(d1v, d0v);
+      const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1v, dw), d2 = qm31_add(d1v, dd);
       sums[2] = qm31_add(sums[2], qm31_mul(qm31_mul(e2, w2), d2));
       sums[3] = qm31_add(sums[3], qm31_mul(qm31_mul(qm31_add(e2, de), qm31_add(w2, dw)), qm31_add(d2, dd)));
     }
     absorb3(t, sums);
     for (size_t i = 0; i < half; i++) {
-      E[i] = qm31_fold(E[i], E[i + half], alpha);
-      W[i] = qm31_fold(W[i], W[i + half], alpha);
-      D[i] = qm31_fold(D[i], D[i + half], alpha);
+      E[i] = qm31_fold(E[i], E[i + half], chal[t]);
+      W[i] = qm31_fold(W[i], W[i + half], chal[t]);
+      D[i] = qm31_fold(D[i], D[i + half], chal[t]);
     }
     E.resize(half);
     W.resize(half);
@@ -1473,7 +1665,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   const std::vector<uint32_t>& table = cached_table(c, tag, table_log);
 
   uint32_t *d_table, *d_mult, *d_min, *d_mout;
-  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *d_e1, *m0, *m1;
+  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *m0, *m1;
   TRY(ensureT(c, S_TABLE, tsize, &d_table));
   TRY(ensureT(c, S_MULT, tsize, &d_mult));
   TRY(ensureT(c, S_MIN, n, &d_min));
@@ -1483,7 +1675,6 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(ensureT(c, S_W0, n, &d_w0));
   TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
   TRY(ensureT(c, S_E0, n, &d_e0));
-  TRY(ensureT(c, S_E1, n / 2 + 1, &d_e1));
   TRY(ensureT(c, S_M0, tsize, &m0));
   TRY(ensureT(c, S_M1, tsize / 2 + 1, &m1));
   TRY(ensure_host_mult(c, tsize));
@@ -1507,14 +1698,14 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   out->gamma = G(gamma);
   out->beta = G(beta);
 
-  // Launched back to back, read when needed (results in slots 4-9):
-  //   prepare -> (trace sum, input MLE at the claim point)      slots 4, 5
-  //   table-side sum over the multiplicities                     slot 6
+  // Launched back to back, read when needed (each result in its own slot):
+  //   prepare -> (trace sum, input MLE at the claim point)      kSlotPrep
+  //   table-side sum over the multiplicities                     kSlotTable
   //   multiplicities -> pinned host copy
-  //   multiplicity sumcheck round 0 (no challenge needed)        slots 8, 9
-  //   eq-sumcheck round 0                                        slots 0-3
+  //   multiplicity sumcheck trip 0 (no challenge needed)         kSlotMult0
+  //   eq tables of the eq-sumcheck trips, eq-sumcheck trip 0     kSlotEq0
   RoundSink sk_prep, sk_table, sk_mult0, sk_eq0;
-  TRY(make_sink(c, &sk_prep, 4));
+  TRY(make_sink(c, &sk_prep, kSlotPrep));
   {
     TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 16 * n + 8 * n + 32 * n);
     hipLaunchKernelGGL(k_logup_prepare, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, input->dev, input->rows,
@@ -1522,28 +1713,24 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
                        d_mult, sk_prep);
   }
   TRY(launch_finish<2>(c, sk_prep, partial_grid(n)));
-  TRY(make_sink(c, &sk_table, 6));
+  TRY(make_sink(c, &sk_table, kSlotTable));
   hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult, tsize,
                      gamma, beta, sk_table);
   TRY(launch_finish<1>(c, sk_table, partial_grid(tsize)));
   HIP_TRY(hipMemcpyAsync(c->h_mult, d_mult, tsize * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
   hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0);
   TRY(check_launch());
-  int mt0 = 0;  // multiplicity sumcheck: grid rounds t < mt0, the rest in k_sum_tail
-  while ((tsize >> mt0) > (uint64_t)kTailMax) mt0++;
-  if (mt0 > 0) {
-    const uint64_t half = tsize / 2;
-    TRY(make_sink(c, &sk_mult0, 8));
-    hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, (const qm31*)m0,
-                       (qm31*)nullptr, half, 0, qm31_zero(), sk_mult0);
-    TRY(launch_finish<2>(c, sk_mult0, partial_grid(half)));
-  }
-  const bool eq_pre = eq3_has_grid_rounds(nv) && nv > 0;
-  if (eq_pre) TRY(eq3_launch_round0(c, nv, d_e0, d_w0, d_d0, &sk_eq0));
+  const std::vector<Trip> mtrips = plan_trips((int)table_log, kHostTailSum, kTripMaxK);
+  TRY(launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
+                  kSlotMult0, &sk_mult0));
+  Eq3Plan epl;
+  TRY(eq3_prepare(c, cpt.data(), nv, &epl));
+  const bool eq_pre = nv > 0;
+  if (eq_pre) TRY(eq3_launch_trip(c, epl, 0, d_w0, d_d0, 0, nullptr, nullptr, nullptr, kSlotEq0, &sk_eq0));
 
   qm31 prep[2], tsum[1];
   TRY(wait_sink<1>(c, sk_table, tsum));  // implies the prepare results (earlier on the stream)
-  for (int q = 0; q < 2; q++) prep[q] = c->h_out[4 + q];
+  for (int q = 0; q < 2; q++) prep[q] = c->h_out[kSlotPrep + q];
   const qm31 trace_sum = prep[0], input_eval = prep[1], table_sum = tsum[0];
   if (!qm31_eq(trace_sum, table_sum))
     return fail(GKR_ERR_LOGUP, "Activation LogUp sum mismatch: trace=(%u,%u,%u,%u) table=(%u,%u,%u,%u)", trace_sum.a,
@@ -1554,7 +1741,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   // eq-sumcheck: sum eq(r, x) w(x) d(x) = 1 over the hypercube
   std::vector<qm31> chal(nv);
   qm31 fin[3];
-  TRY(eq3_sumcheck(c, C, nv, d_e0, d_w0, d_d0, d_e1, d_w1, d_d1, out->eq_round_polys, chal.data(), fin,
+  TRY(eq3_sumcheck(c, C, cpt.data(), epl, d_w0, d_d0, d_w1, d_d1, out->eq_round_polys, chal.data(), fin,
                    eq_pre ? &sk_eq0 : nullptr));
   const qm31 w_eval = fin[1];
   // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass
@@ -1578,7 +1765,6 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   // input once, so their sum is n.
   memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
   const qm31 mult_sum = qm31_from_m31(m31_reduce64(n));
-  const qm31* cm = m0;
   qm31* bm[2] = {m1, m0};
   qm31 alpha = qm31_zero();
   auto absorb1 = [&](uint32_t t, const qm31* s) {
@@ -1593,52 +1779,41 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   };
   qm31 mfin[1];
   {
-    const int t0 = mt0;
-    int t1 = t0;  // rounds t >= t1 on the host
-    while ((tsize >> t1) > kHostTailSum) t1++;
-    const int n_tail = t1 - t0;
-    std::unique_ptr<TailSession> tail;
-    auto launch_tail = [&]() -> int {
-      const uint32_t len_in = (uint32_t)(t0 == 0 ? tsize : (tsize >> (t0 - 1)));
-      tail.reset(new TailSession(c, n_tail + 1, n_tail + 1));
-      hipLaunchKernelGGL(k_sum_tail, dim3(1), dim3(kBlock), 0, c->stream, cm, len_in, t0 > 0 ? 1 : 0, n_tail,
-                         c->mailbox, tail->mb_base, c->h_out, c->h_flag, tail->res_base, c->h_vec);
-      return check_launch();
-    };
-    for (int t = 0; t < t0; t++) {
-      const uint64_t half = (tsize >> t) / 2;
+    // trips of up to 3 rounds (the first launched ahead above), then the host
+    HandoverSession ho(c);
+    const qm31* src = m0;
+    int np = 0;
+    const qm31* pend = nullptr;
+    std::vector<qm31> mchal(table_log);
+    for (size_t j = 0; j < mtrips.size(); j++) {
+      const Trip& tr = mtrips[j];
+      const bool last = j + 1 == mtrips.size();
       RoundSink sk;
-      if (t == 0) {
+      if (j == 0) {
         sk = sk_mult0;
       } else {
-        TRY(make_sink(c, &sk));
-        qm31* nm = bm[(t - 1) & 1];
-        hipLaunchKernelGGL(k_sum_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, cm, nm, half, 1,
-                           alpha, sk);
-        cm = nm;
-        TRY(launch_finish<2>(c, sk, partial_grid(half)));
+        qm31* dst = bm[(j - 1) & 1];
+        TRY(launch_trip(c, 2, tr.K, src, nullptr, tr.n, np, pend, dst, nullptr, nullptr, nullptr, 0, 0, &sk));
+        src = dst;
       }
-      if (t == t0 - 1) TRY(launch_tail());
-      qm31 sums[2];
-      TRY(wait_sink<2>(c, sk, sums));
-      absorb1((uint32_t)t, sums);
+      if (last) TRY(ho.launch<1>(src, nullptr, tr.n, tr.K));
+      qm31 g[kMaxSums];
+      TRY(wait_trip(c, sk, trip_nq(2, tr.K), g));
+      for (int i = 0; i < tr.K; i++) {
+        qm31 sums[2];
+        trip_round_sum(g, tr.K, i, mchal.data() + tr.t, sums);
+        absorb1((uint32_t)(tr.t + i), sums);
+        mchal[tr.t + i] = alpha;
+      }
+      np = tr.K;
+      pend = mchal.data() + tr.t;
     }
-    if (t0 == 0) {
-      TRY(launch_tail());
-    } else {
-      tail->post(0, alpha);
-    }
-    for (int r = 0; r < n_tail; r++) {
-      qm31 sums[2];
-      TRY(wait_result<2>(c, tail->res_base + r, sums));
-      absorb1((uint32_t)(t0 + r), sums);
-      tail->post(r + 1, alpha);
-    }
+    const int t_end = mtrips.back().t + mtrips.back().K;
     std::vector<qm31> v[1];
-    TRY(fetch_tail_vectors(c, tail->res_base + n_tail, tsize >> t1, 1, v));
-    tail->done = true;
+    ho.post(pend, np);
+    TRY(ho.fetch(tsize >> t_end, 1, v));
     std::vector<qm31>& V = v[0];
-    for (int t = t1; t < (int)table_log; t++) {
+    for (int t = t_end; t < (int)table_log; t++) {
       const size_t half = V.size() / 2;
       qm31 sums[2] = {qm31_zero(), qm31_zero()};
       for (size_t i = 0; i < half; i++) {
@@ -1811,8 +1986,8 @@ extern "C" int gkr_sumcheck_product(gkr_ctx* c, const gkr_qvec* fa, const gkr_qv
   TRY(ensureT(c, S_FB0, n / 4 + 1, &b2));
   qm31* bufs_a[2] = {a1, a2};
   qm31* bufs_b[2] = {b1, b2};
-  return product_sumcheck(c, ch->ch, T, fa->dev, fb->dev, bufs_a, bufs_b, nullptr, nullptr, round_polys,
-                          challenges, final_a, final_b);
+  return product_sumcheck(c, ch->ch, T, fa->dev, fb->dev, bufs_a, bufs_b, nullptr, 0, round_polys, challenges,
+                          final_a, final_b);
 }
 
 /* ------------------------------------------------------------------ MLE commitments
@@ -2394,20 +2569,19 @@ extern "C" int gkr_prove_weight_binding(gkr_ctx* c, gkr_channel* ch, gkr_proof* 
 static int mul_layer_core(gkr_ctx* c, const std::vector<qm31>& cpt, const qm31& claim, int nv, gkr_channel* ch,
                           gkr_proof* proof, gkr_mul_out* out) {
   const uint64_t n = 1ull << nv;
-  qm31 *d_e0, *d_e1, *d_w0, *d_w1, *d_d0, *d_d1;
-  TRY(ensureT(c, S_E0, n, &d_e0));
-  TRY(ensureT(c, S_E1, n / 2 + 1, &d_e1));
+  qm31 *d_w0, *d_w1, *d_d0, *d_d1;
   TRY(ensureT(c, S_W0, n, &d_w0));
   TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
   TRY(ensureT(c, S_D0, n, &d_d0));
   TRY(ensureT(c, S_D1, n / 2 + 1, &d_d1));
   PoseidonChannel& C = ch->ch;
-  TRY(eq_table(c, cpt.data(), nv, n, d_e0));  // eq over the first nv claim coordinates
-  C.mix_u64(0x4D554Cull);                      // "MUL"
+  Eq3Plan epl;  // eq over the first nv claim coordinates, kept factored
+  TRY(eq3_prepare(c, cpt.data(), nv, &epl));
+  C.mix_u64(0x4D554Cull);  // "MUL"
   C.mix_secure_field(claim);
   std::vector<qm31> chal(nv);
   qm31 fin[3];
-  TRY(eq3_sumcheck(c, C, nv, d_e0, d_w0, d_d0, d_e1, d_w1, d_d1, out->eq_round_polys, chal.data(), fin));
+  TRY(eq3_sumcheck(c, C, cpt.data(), epl, d_w0, d_d0, d_w1, d_d1, out->eq_round_polys, chal.data(), fin));
   const qm31 lhs = fin[1], rhs = fin[2];
   C.mix_secure_field(lhs);
   C.mix_secure_field(rhs);
@@ -2504,7 +2678,7 @@ extern "C" int gkr_reduce_mul_layer(gkr_ctx* c, const gkr_qm31* claim_point, uin
 }
 
 // MLE of lhs (.) rhs (padded) at `point`: sum_x eq(point, x) lhs(x) rhs(x),
-// as the sum s0 + s1 of an eq3 round-0 pass.
+// one eq-weighted pass (a trip of no rounds; eq as a product of two tables).
 extern "C" int gkr_mul_output_claim(gkr_ctx* c, const gkr_matrix* lhs, const gkr_matrix* rhs,
                                     const gkr_qm31* point, uint32_t n_point, gkr_qm31* out) {
   if (!c || !out || (!point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
@@ -2519,28 +2693,30 @@ extern "C" int gkr_mul_output_claim(gkr_ctx* c, const gkr_matrix* lhs, const gkr
   }
   c->mm.valid = false;
   const uint64_t n = 1ull << nv;
-  qm31 *d_e0, *d_w0, *d_d0;
-  TRY(ensureT(c, S_E0, n, &d_e0));
+  qm31 *d_w0, *d_d0;
   TRY(ensureT(c, S_W0, n, &d_w0));
   TRY(ensureT(c, S_D0, n, &d_d0));
-  TRY(eq_table(c, pt.data(), nv, n, d_e0));
-  if (nv == 0) {
-    qm31 e, a, b;
-    TRY(fetch_q(c, d_e0, 1, &e));
-    TRY(fetch_q(c, d_w0, 1, &a));
-    TRY(fetch_q(c, d_d0, 1, &b));
-    *out = G(qm31_mul(qm31_mul(e, a), b));
-    return GKR_OK;
-  }
-  const uint64_t half = n / 2;
+  const int h = nv < kEqLoMax ? nv : kEqLoMax;
+  EqPartsArg arg;
+  memset(&arg, 0, sizeof arg);
+  arg.z = make_point(pt.data(), nv);
+  arg.count = 2;
+  arg.s[0] = 0;
+  arg.m[0] = nv - h;
+  arg.off[0] = 0;
+  arg.s[1] = nv - h;
+  arg.m[1] = h;
+  arg.off[1] = 1u << (nv - h);
+  const uint32_t total = arg.off[1] + (1u << h);
+  qm31* parts;
+  TRY(ensureT(c, S_EQPARTS, total, &parts));
+  hipLaunchKernelGGL(k_eq_parts, dim3(grid_for(total)), dim3(kBlock), 0, c->stream, arg, total, parts);
+  TRY(check_launch());
   RoundSink sk;
-  TRY(make_sink(c, &sk));
-  hipLaunchKernelGGL(k_eq3_round, dim3(partial_grid(half)), dim3(kBlock), 0, c->stream, d_e0, d_w0, d_d0,
-                     (qm31*)nullptr, (qm31*)nullptr, (qm31*)nullptr, half, 0, qm31_zero(), sk);
-  TRY(launch_finish<4>(c, sk, partial_grid(half)));
-  qm31 sums[4];
-  TRY(wait_sink<4>(c, sk, sums));
-  *out = G(qm31_add(sums[0], sums[1]));
+  TRY(launch_trip(c, 1, 0, d_w0, d_d0, n, 0, nullptr, nullptr, nullptr, parts, parts + arg.off[1], h, 0, &sk));
+  qm31 v[1];
+  TRY(wait_trip(c, sk, 1, v));
+  *out = G(v[0]);
   return GKR_OK;
 }
 

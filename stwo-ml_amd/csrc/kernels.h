@@ -119,213 +119,265 @@ __global__ void __launch_bounds__(kBlock) k_finish(RoundSink sk, uint32_t nblock
     publish_flag(sk.flag, sk.seq);
   }
 }
-// ------------------------------------------------------------------ persistent tail
-// The last rounds of a sumcheck (vectors of at most kTailMax elements) run in
-// one long-lived workgroup that keeps the vectors in LDS.  Before each fold it
-// waits for the host to post the challenge in the coherent mailbox
-// (sequence number, then alpha); after each evaluation it delivers the round
-// sums like k_finish.  The wait is bounded: after kTailSpinLimit polls
-// without the expected sequence number the kernel publishes kTailTimeout in
-// the result flag and returns, so every wave always exits.
-constexpr int kTailMax = 1024;
-constexpr uint64_t kTailSpinLimit = 1ull << 22;
-constexpr uint32_t kTailTimeout = 0xFFFFFFFFu;
-constexpr uint32_t kTailCancel = 0xFFFFFFFEu;
+// ------------------------------------------------------------------ multi-round trips
+// One launch serves K consecutive rounds of a sumcheck (K <= kTripMaxK).
+// Seen through its top K variables (MSB first), a vector f of length n splits
+// into 2^K sub-vectors f_c(x) = f[c * nb + x], nb = n >> K.  k_trip returns,
+// summed over x < nb:
+//   KIND 0, product f_a f_b (backend.rs:146-177):
+//     G[c][c'] = sum_x a_c(x) b_c'(x)                        4^K values
+//   KIND 1, eq-sumcheck eq w d (prover.rs:6510-6556, 9236-9270), eq factored:
+//     G[c][c'] = sum_x eq(x) w_c(x) d_c'(x)                  4^K values
+//     where eq(x) = hi[x >> h] * lo[x & (2^h - 1)] is the part of eq(z, .)
+//     over the claim coordinates below the trip's variables
+//   KIND 2, degree-1 sum (prover.rs:9449-9511):
+//     S[c] = sum_x v_c(x)                                     2^K values
+// The host derives the K round polynomials from these sums one after
+// another, drawing each challenge before the next (round polynomials are
+// unique, so they are the same as round by round).  The inputs carry np <= 3
+// pending folds: sources of length n << np are folded on the fly by
+// al[0..np) (MSB first: al[0] on the top variable) and, when d_a / d_b are
+// given, the folded vectors (the next trip's sources) are written there.
+//
+// Lanes: groups of 2^K consecutive lanes share one x; lane c of a group
+// holds a_c (and b_c), the b's of the group are exchanged by shuffles and
+// lane c accumulates row c of G.  Rows are reduced across the wave and the
+// workgroup into one partial row per workgroup; k_finish_wide adds the rows.
+constexpr int kTripMaxK = 3;
+struct TripChal {
+  qm31 c[kTripMaxK];
+};
+
+__device__ __forceinline__ qm31 shfl_q(qm31 q, int src) {
+  return qm31{(uint32_t)__shfl((int)q.a, src, 64), (uint32_t)__shfl((int)q.b, src, 64),
+              (uint32_t)__shfl((int)q.c, src, 64), (uint32_t)__shfl((int)q.d, src, 64)};
+}
+
+// Entry pos of a vector of length n held as a source with NP pending folds.
+template <int NP>
+__device__ __forceinline__ qm31 fold_pending(const qm31* __restrict__ src, uint64_t pos, uint64_t n,
+                                             const TripChal& al) {
+  if constexpr (NP == 0) {
+    return ld_q(src, pos);
+  } else {
+    qm31 v[1 << NP];
+#pragma unroll
+    for (int s = 0; s < (1 << NP); s++) v[s] = ld_q(src, pos + (uint64_t)s * n);
+#pragma unroll
+    for (int l = 0; l < NP; l++) {
+#pragma unroll
+      for (int j = 0; j < (1 << (NP - 1 - l)); j++) v[j] = qm31_fold(v[j], v[j + (1 << (NP - 1 - l))], al.c[l]);
+    }
+    return v[0];
+  }
+}
+__device__ __forceinline__ qm31 load_pending(const qm31* __restrict__ src, uint64_t pos, uint64_t n, int np,
+                                             const TripChal& al) {
+  switch (np) {
+    case 0: return fold_pending<0>(src, pos, n, al);
+    case 1: return fold_pending<1>(src, pos, n, al);
+    case 2: return fold_pending<2>(src, pos, n, al);
+    default: return fold_pending<3>(src, pos, n, al);
+  }
+}
+
+template <int KIND, int K>
+struct TripShape {
+  static constexpr int G = 1 << K;                        // sub-vectors
+  static constexpr int NQ = KIND == 2 ? G : G * G;        // sums per launch
+  static constexpr int NA = KIND == 2 ? 1 : G;            // accumulators per lane
+};
+
+// Requirements (checked by the host): np <= 3, n a power of two >= 2^K.
+template <int KIND, int K>
+__global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, const qm31* __restrict__ sb,
+                                                 uint64_t n, int np, TripChal al, qm31* __restrict__ da,
+                                                 qm31* __restrict__ db, const qm31* __restrict__ eq_hi,
+                                                 const qm31* __restrict__ eq_lo, int eq_h,
+                                                 qm31* __restrict__ partials) {
+  using S = TripShape<KIND, K>;
+  constexpr int G = S::G;
+  const uint64_t nb = n >> K;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & (G - 1);
+  const uint64_t groups = ((uint64_t)gridDim.x * blockDim.x) >> K;
+  qacc acc[S::NA];
+#pragma unroll
+  for (int i = 0; i < S::NA; i++) acc[i].zero();
+  for (uint64_t x = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> K; x < nb; x += groups) {
+    const uint64_t pos = (uint64_t)c * nb + x;
+    qm31 a = load_pending(sa, pos, n, np, al);
+    if (da) st_q(da, pos, a);
+    if constexpr (KIND == 2) {
+      acc[0].add(a);
+    } else {
+      const qm31 b = load_pending(sb, pos, n, np, al);
+      if (db) st_q(db, pos, b);
+      if constexpr (KIND == 1) {
+        const uint64_t mask = (1ull << eq_h) - 1;
+        a = qm31_mul(a, qm31_mul(ld_q(eq_hi, x >> eq_h), ld_q(eq_lo, x & mask)));
+      }
+      const int base = lane & ~(G - 1);
+#pragma unroll
+      for (int d = 0; d < G; d++) acc[d].add(qm31_mul(a, shfl_q(b, base + d)));
+    }
+  }
+  qm31 t[S::NA];
+#pragma unroll
+  for (int i = 0; i < S::NA; i++) t[i] = acc[i].reduce();
+#pragma unroll
+  for (int m = G; m < 64; m <<= 1)
+#pragma unroll
+    for (int i = 0; i < S::NA; i++) {
+      const qm31 o{shfl_xor_u32(t[i].a, m), shfl_xor_u32(t[i].b, m), shfl_xor_u32(t[i].c, m),
+                   shfl_xor_u32(t[i].d, m)};
+      t[i] = qm31_add(t[i], o);
+    }
+  __shared__ qm31 sh[kBlock / 64][S::NQ];
+  const int wave = threadIdx.x >> 6;
+  if (lane < G) {
+#pragma unroll
+    for (int i = 0; i < S::NA; i++) sh[wave][lane * S::NA + i] = t[i];
+  }
+  __syncthreads();
+  for (int q = threadIdx.x; q < S::NQ; q += blockDim.x) {
+    qm31 s = sh[0][q];
+#pragma unroll
+    for (int w = 1; w < kBlock / 64; w++) s = qm31_add(s, sh[w][q]);
+    st_q(partials, (uint64_t)blockIdx.x * S::NQ + q, s);
+  }
+}
+
+// Adds nblocks partial rows of NQ values and delivers them like k_finish.
+// kFinishBlock threads: thread t sums column t % NQ over every
+// (kFinishBlock / NQ)-th row, four independent loads in flight.
+constexpr int kFinishBlock = 1024;
+template <int NQ>
+__global__ void __launch_bounds__(kFinishBlock) k_finish_wide(RoundSink sk, uint32_t nblocks) {
+  constexpr int RG = kFinishBlock / NQ;
+  const int q = threadIdx.x % NQ, g = threadIdx.x / NQ;
+  qacc acc;
+  acc.zero();
+  uint32_t b = g;
+  for (; b + 3 * RG < nblocks; b += 4 * RG) {
+    const qm31 v0 = ld_q(sk.partials, (uint64_t)NQ * b + q);
+    const qm31 v1 = ld_q(sk.partials, (uint64_t)NQ * (b + RG) + q);
+    const qm31 v2 = ld_q(sk.partials, (uint64_t)NQ * (b + 2 * RG) + q);
+    const qm31 v3 = ld_q(sk.partials, (uint64_t)NQ * (b + 3 * RG) + q);
+    acc.add(v0);
+    acc.add(v1);
+    acc.add(v2);
+    acc.add(v3);
+  }
+  for (; b < nblocks; b += RG) acc.add(ld_q(sk.partials, (uint64_t)NQ * b + q));
+  __shared__ qm31 sh[kFinishBlock];
+  sh[threadIdx.x] = acc.reduce();
+  __syncthreads();
+  for (int step = RG / 2; step >= 1; step /= 2) {  // tree over the row groups
+    if (g < step) sh[threadIdx.x] = qm31_add(sh[threadIdx.x], sh[threadIdx.x + step * NQ]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    for (int i = 0; i < NQ; i++) sk.out[i] = sh[i];
+    publish_flag(sk.flag, sk.seq);
+  }
+}
+
+// ------------------------------------------------------------------ hand-over to the host
+// The end of a sumcheck's device part: one workgroup loads the NV vectors the
+// last trip left (length len <= kHandMax, not yet folded by that trip's k
+// challenges) into LDS while the host works on the trip's rounds, waits for
+// the k challenges (mailbox seq `want`), folds, and hands the vectors
+// (len >> k entries each, one after another) to vec_out in coherent host
+// memory, then publishes `seq`.  The wait is bounded: after kWaitSpinLimit
+// polls without `want` (or on the cancel code) the kernel publishes
+// kWaitTimeout in the result flag and returns, so every wave always exits.
+constexpr int kHandMax = 2048;
+constexpr uint64_t kWaitSpinLimit = 1ull << 22;
+constexpr uint32_t kWaitTimeout = 0xFFFFFFFFu;
+constexpr uint32_t kWaitCancel = 0xFFFFFFFEu;
 
 struct Mailbox {
   uint32_t seq;
   uint32_t pad[3];
-  qm31 alpha;
+  qm31 alpha[kTripMaxK];
 };
 
-// Thread 0 polls for `want`; the challenge is broadcast through LDS.
-// Returns false (after publishing the timeout code) when the host never posts it.
-__device__ __forceinline__ bool tail_wait(Mailbox* mb, uint32_t want, qm31* sh_alpha, bool* sh_ok, uint32_t* res_flag) {
+template <int NV>
+__global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a, const qm31* __restrict__ b,
+                                                     uint32_t len, int k, Mailbox* mb, uint32_t want,
+                                                     qm31* vec_out, uint32_t* flag, uint32_t seq) {
+  __shared__ qm31 v[NV][kHandMax];
+  __shared__ qm31 sh_al[kTripMaxK];
+  __shared__ bool sh_ok;
+  for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) {
+    v[0][i] = ld_q(a, i);
+    if constexpr (NV > 1) v[1][i] = ld_q(b, i);
+  }
   if (threadIdx.x == 0) {
     bool ok = false;
-    for (uint64_t spins = 0; spins < kTailSpinLimit; spins++) {
+    for (uint64_t spins = 0; spins < kWaitSpinLimit; spins++) {
       const uint32_t got = __hip_atomic_load(&mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
       if (got == want) {
         ok = true;
         break;
       }
-      if (got == kTailCancel) break;
+      if (got == kWaitCancel) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    if (ok) {  // one 128-bit read of the challenge, ordered after the acquiring read of seq
-      const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&mb->alpha));
-      *sh_alpha = qm31{a[0], a[1], a[2], a[3]};
+    if (ok) {  // the challenges, read after the acquiring read of seq
+      for (int r = 0; r < k; r++) {
+        const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&mb->alpha[r]));
+        sh_al[r] = qm31{q[0], q[1], q[2], q[3]};
+      }
     } else {
-      publish_flag(res_flag, kTailTimeout);
+      publish_flag(flag, kWaitTimeout);
     }
-    *sh_ok = ok;
+    sh_ok = ok;
   }
   __syncthreads();
-  return *sh_ok;
-}
-
-// Hand the vectors of length len (held in LDS) to the host: every thread
-// stores its share into coherent host memory and makes it visible system-wide
-// before thread 0 publishes `seq`.
-__device__ __forceinline__ void publish_vectors(const qm31* v0, const qm31* v1, const qm31* v2, uint32_t len,
-                                                qm31* vec_out, uint32_t* flag, uint32_t seq) {
-  for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) {
-    vec_out[i] = v0[i];
-    if (v1) vec_out[len + i] = v1[i];
-    if (v2) vec_out[2 * len + i] = v2[i];
+  if (!sh_ok) return;
+  uint32_t l = len;
+  for (int r = 0; r < k; r++) {
+    const uint32_t h = l / 2;
+    const qm31 al = sh_al[r];
+    for (uint32_t i = threadIdx.x; i < h; i += blockDim.x)
+#pragma unroll
+      for (int j = 0; j < NV; j++) v[j][i] = qm31_fold(v[j][i], v[j][i + h], al);
+    l = h;
+    __syncthreads();
   }
+  for (uint32_t i = threadIdx.x; i < l; i += blockDim.x)
+#pragma unroll
+    for (int j = 0; j < NV; j++) vec_out[(uint64_t)j * l + i] = v[j][i];
   __threadfence_system();
   __syncthreads();
   if (threadIdx.x == 0) publish_flag(flag, seq);
 }
 
-// Tail of the product sumcheck (k_mm_round semantics) for n_rounds rounds.
-// On entry the vectors have length len_in; when fold_first is set they are
-// folded by the challenge of the previous round before the first
-// evaluation.  Result i < n_rounds (the round sums) is published with seq
-// res_base + i; the challenge folded before result i carries mailbox seq
-// mb_base + i.  After the fold that follows the last round the remaining
-// vectors (a then b, len_in >> (n_rounds + fold_first) entries each) go to
-// vec_out with seq res_base + n_rounds; the host finishes from there.
-__global__ void __launch_bounds__(kBlock) k_mm_tail(const qm31* __restrict__ a_in, const qm31* __restrict__ b_in,
-                                                    uint32_t len_in, int fold_first, int n_rounds, Mailbox* mb,
-                                                    uint32_t mb_base, qm31* out, uint32_t* flag,
-                                                    uint32_t res_base, qm31* vec_out) {
-  __shared__ qm31 va[2 * kTailMax], vb[2 * kTailMax];
-  __shared__ qm31 sh_alpha;
-  __shared__ bool sh_ok;
-  __shared__ qm31 res[3];
-  for (uint32_t i = threadIdx.x; i < len_in; i += blockDim.x) {
-    va[i] = ld_q(a_in, i);
-    vb[i] = ld_q(b_in, i);
-  }
-  __syncthreads();
-  uint32_t len = len_in;
-  for (int r = 0; r <= n_rounds; r++) {
-    if (r > 0 || fold_first) {
-      if (!tail_wait(mb, mb_base + r, &sh_alpha, &sh_ok, flag)) return;
-      const qm31 al = sh_alpha;
-      const uint32_t h = len / 2;
-      for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) {
-        va[i] = qm31_fold(va[i], va[i + h], al);
-        vb[i] = qm31_fold(vb[i], vb[i + h], al);
-      }
-      len = h;
-      __syncthreads();
-    }
-    if (r == n_rounds) break;
-    const uint32_t half = len / 2;
-    qacc s0, s1, s2;
-    s0.zero(); s1.zero(); s2.zero();
-    for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
-      const qm31 a0 = va[i], a1 = va[i + half], b0 = vb[i], b1 = vb[i + half];
-      s0.add(qm31_mul(a0, b0));
-      s1.add(qm31_mul(a1, b1));
-      s2.add(qm31_mul(qm31_sub(qm31_add(a1, a1), a0), qm31_sub(qm31_add(b1, b1), b0)));
-    }
-    qm31 v[3] = {s0.reduce(), s1.reduce(), s2.reduce()};
-    block_sum_store<3>(v, res);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      out[0] = res[0]; out[1] = res[1]; out[2] = res[2];
-      publish_flag(flag, res_base + r);
-    }
-  }
-  publish_vectors(va, vb, nullptr, len, vec_out, flag, res_base + n_rounds);
-}
-
-// Tail of the degree-3 eq-sumcheck over (eq, w, d): same protocol, 4 sums per
-// round; the remaining eq, w and d vectors go to vec_out at the end.
-__global__ void __launch_bounds__(kBlock) k_eq3_tail(const qm31* __restrict__ e_in, const qm31* __restrict__ w_in,
-                                                     const qm31* __restrict__ d_in, uint32_t len_in, int fold_first,
-                                                     int n_rounds, Mailbox* mb, uint32_t mb_base, qm31* out,
-                                                     uint32_t* flag, uint32_t res_base, qm31* vec_out) {
-  constexpr int kMax = kTailMax / 2;
-  __shared__ qm31 ve[2 * kMax], vw[2 * kMax], vd[2 * kMax];
-  __shared__ qm31 sh_alpha;
-  __shared__ bool sh_ok;
-  __shared__ qm31 res[4];
-  for (uint32_t i = threadIdx.x; i < len_in; i += blockDim.x) {
-    ve[i] = ld_q(e_in, i);
-    vw[i] = ld_q(w_in, i);
-    vd[i] = ld_q(d_in, i);
-  }
-  __syncthreads();
-  uint32_t len = len_in;
-  for (int r = 0; r <= n_rounds; r++) {
-    if (r > 0 || fold_first) {
-      if (!tail_wait(mb, mb_base + r, &sh_alpha, &sh_ok, flag)) return;
-      const qm31 al = sh_alpha;
-      const uint32_t h = len / 2;
-      for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) {
-        ve[i] = qm31_fold(ve[i], ve[i + h], al);
-        vw[i] = qm31_fold(vw[i], vw[i + h], al);
-        vd[i] = qm31_fold(vd[i], vd[i + h], al);
-      }
-      len = h;
-      __syncthreads();
-    }
-    if (r == n_rounds) break;
-    const uint32_t half = len / 2;
-    qacc s0, s1, s2, s3;
-    s0.zero(); s1.zero(); s2.zero(); s3.zero();
-    for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
-      const qm31 e0 = ve[i], e1 = ve[i + half], w0 = vw[i], w1 = vw[i + half], d0 = vd[i], d1 = vd[i + half];
-      s0.add(qm31_mul(qm31_mul(e0, w0), d0));
-      s1.add(qm31_mul(qm31_mul(e1, w1), d1));
-      const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1, w0), dd = qm31_sub(d1, d0);
-      const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1, dw), d2 = qm31_add(d1, dd);
-      s2.add(qm31_mul(qm31_mul(e2, w2), d2));
-      s3.add(qm31_mul(qm31_mul(qm31_add(e2, de), qm31_add(w2, dw)), qm31_add(d2, dd)));
-    }
-    qm31 v[4] = {s0.reduce(), s1.reduce(), s2.reduce(), s3.reduce()};
-    block_sum_store<4>(v, res);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      out[0] = res[0]; out[1] = res[1]; out[2] = res[2]; out[3] = res[3];
-      publish_flag(flag, res_base + r);
-    }
-  }
-  publish_vectors(ve, vw, vd, len, vec_out, flag, res_base + n_rounds);
-}
-
-// Tail of the degree-1 multiplicity sumcheck: sums of the low and high halves.
-__global__ void __launch_bounds__(kBlock) k_sum_tail(const qm31* __restrict__ v_in, uint32_t len_in, int fold_first,
-                                                     int n_rounds, Mailbox* mb, uint32_t mb_base, qm31* out,
-                                                     uint32_t* flag, uint32_t res_base, qm31* vec_out) {
-  __shared__ qm31 vv[2 * kTailMax];
-  __shared__ qm31 sh_alpha;
-  __shared__ bool sh_ok;
-  __shared__ qm31 res[2];
-  for (uint32_t i = threadIdx.x; i < len_in; i += blockDim.x) vv[i] = ld_q(v_in, i);
-  __syncthreads();
-  uint32_t len = len_in;
-  for (int r = 0; r <= n_rounds; r++) {
-    if (r > 0 || fold_first) {
-      if (!tail_wait(mb, mb_base + r, &sh_alpha, &sh_ok, flag)) return;
-      const qm31 al = sh_alpha;
-      const uint32_t h = len / 2;
-      for (uint32_t i = threadIdx.x; i < h; i += blockDim.x) vv[i] = qm31_fold(vv[i], vv[i + h], al);
-      len = h;
-      __syncthreads();
-    }
-    if (r == n_rounds) break;
-    const uint32_t half = len / 2;
-    qacc lo, hi;
-    lo.zero(); hi.zero();
-    for (uint32_t i = threadIdx.x; i < half; i += blockDim.x) {
-      lo.add(vv[i]);
-      hi.add(vv[i + half]);
-    }
-    qm31 v[2] = {lo.reduce(), hi.reduce()};
-    block_sum_store<2>(v, res);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      out[0] = res[0]; out[1] = res[1];
-      publish_flag(flag, res_base + r);
-    }
-  }
-  publish_vectors(vv, nullptr, nullptr, len, vec_out, flag, res_base + n_rounds);
+// ------------------------------------------------------------------ eq parts
+// Small eq tables over runs of the claim point: table i covers coordinates
+// z[s_i .. s_i + m_i) (the first on the most significant bit) and has 2^m_i
+// entries at out + off_i; the eq-sumcheck trips read their eq weights as
+// products of two such tables.
+constexpr int kEqPartsMax = 48;
+struct EqPartsArg {
+  PointArg z;
+  int count;
+  int s[kEqPartsMax];
+  int m[kEqPartsMax];
+  uint32_t off[kEqPartsMax];
+};
+__global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  int t = 0;
+  while (t + 1 < a.count && i >= a.off[t + 1]) t++;
+  const uint32_t x = i - a.off[t];
+  const int s = a.s[t], m = a.m[t];
+  qm31 acc = qm31_one();
+  for (int l = 0; l < m; l++) acc = qm31_mul(acc, ((x >> (m - 1 - l)) & 1u) ? a.z.r[s + l] : a.z.omr[s + l]);
+  out[i] = acc;
 }
 
 // ------------------------------------------------------------------ eq / Lagrange
@@ -541,45 +593,6 @@ __global__ void k_zero_q(qm31* __restrict__ out, uint64_t from, uint64_t to) {
   if (i < to) st_q(out, i, qm31_zero());
 }
 
-// ------------------------------------------------------------------ matmul sumcheck round
-// Round t of the degree-2 product sumcheck over f_a, f_b (backend.rs:146-177).
-// When fold != 0 the inputs still have length 4*half and are first folded by
-// alpha (the previous round's challenge): x'[i] = x[i] + alpha*(x[2half+i] - x[i]);
-// the folded vectors (length 2*half) are written to the outputs.  Then, for
-// i < half, with x0 = x'[i], x1 = x'[half+i]:
-//   s0 += a0*b0,  s1 += a1*b1,  s2 += (2a1 - a0)*(2b1 - b0).
-// Each workgroup writes its three partial sums to partials[3*blockIdx ..].
-__global__ void __launch_bounds__(kBlock) k_mm_round(const qm31* __restrict__ a_in, const qm31* __restrict__ b_in,
-                                                     qm31* __restrict__ a_out, qm31* __restrict__ b_out,
-                                                     uint64_t half, int fold, qm31 alpha,
-                                                     RoundSink sink) {
-  qacc s0, s1, s2;
-  s0.zero(); s1.zero(); s2.zero();
-  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < half; i += stride) {
-    qm31 a0, a1, b0, b1;
-    if (fold) {
-      a0 = qm31_fold(ld_q(a_in, i), ld_q(a_in, i + 2 * half), alpha);
-      a1 = qm31_fold(ld_q(a_in, i + half), ld_q(a_in, i + 3 * half), alpha);
-      b0 = qm31_fold(ld_q(b_in, i), ld_q(b_in, i + 2 * half), alpha);
-      b1 = qm31_fold(ld_q(b_in, i + half), ld_q(b_in, i + 3 * half), alpha);
-      st_q(a_out, i, a0); st_q(a_out, i + half, a1);
-      st_q(b_out, i, b0); st_q(b_out, i + half, b1);
-    } else {
-      a0 = ld_q(a_in, i); a1 = ld_q(a_in, i + half);
-      b0 = ld_q(b_in, i); b1 = ld_q(b_in, i + half);
-    }
-    s0.add(qm31_mul(a0, b0));
-    s1.add(qm31_mul(a1, b1));
-    const qm31 a2 = qm31_sub(qm31_add(a1, a1), a0);
-    const qm31 b2 = qm31_sub(qm31_add(b1, b1), b0);
-    s2.add(qm31_mul(a2, b2));
-  }
-  qm31 v[3] = {s0.reduce(), s1.reduce(), s2.reduce()};
-  sink_finish<3>(v, sink);
-}
-
-
 // ------------------------------------------------------------------ LogUp
 // M31-by-QM31 dot product accumulator: the four 62-bit products of each term
 // are split into 32-bit halves and summed in 64-bit lanes (no reduction in
@@ -659,69 +672,6 @@ __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __re
   sink_finish<1>(v, sink);
 }
 
-// Degree-3 eq-sumcheck round over (eq, w, d) (gkr/prover.rs:6510-6556, 9236-9270):
-// s_t = sum_i eq_t(i) * w_t(i) * d_t(i) at t = 0, 1, 2, 3 where
-// x_t = (1 - t) x[i] + t x[half + i].  Same fused fold as k_mm_round.
-__global__ void __launch_bounds__(kBlock) k_eq3_round(const qm31* __restrict__ e_in, const qm31* __restrict__ w_in,
-                                                      const qm31* __restrict__ d_in, qm31* __restrict__ e_out,
-                                                      qm31* __restrict__ w_out, qm31* __restrict__ d_out,
-                                                      uint64_t half, int fold, qm31 alpha,
-                                                      RoundSink sink) {
-  qacc s0, s1, s2, s3;
-  s0.zero(); s1.zero(); s2.zero(); s3.zero();
-  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < half; i += stride) {
-    qm31 e0, e1, w0, w1, d0, d1;
-    if (fold) {
-      e0 = qm31_fold(ld_q(e_in, i), ld_q(e_in, i + 2 * half), alpha);
-      e1 = qm31_fold(ld_q(e_in, i + half), ld_q(e_in, i + 3 * half), alpha);
-      w0 = qm31_fold(ld_q(w_in, i), ld_q(w_in, i + 2 * half), alpha);
-      w1 = qm31_fold(ld_q(w_in, i + half), ld_q(w_in, i + 3 * half), alpha);
-      d0 = qm31_fold(ld_q(d_in, i), ld_q(d_in, i + 2 * half), alpha);
-      d1 = qm31_fold(ld_q(d_in, i + half), ld_q(d_in, i + 3 * half), alpha);
-      st_q(e_out, i, e0); st_q(e_out, i + half, e1);
-      st_q(w_out, i, w0); st_q(w_out, i + half, w1);
-      st_q(d_out, i, d0); st_q(d_out, i + half, d1);
-    } else {
-      e0 = ld_q(e_in, i); e1 = ld_q(e_in, i + half);
-      w0 = ld_q(w_in, i); w1 = ld_q(w_in, i + half);
-      d0 = ld_q(d_in, i); d1 = ld_q(d_in, i + half);
-    }
-    s0.add(qm31_mul(qm31_mul(e0, w0), d0));
-    s1.add(qm31_mul(qm31_mul(e1, w1), d1));
-    const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1, w0), dd = qm31_sub(d1, d0);
-    const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1, dw), d2 = qm31_add(d1, dd);
-    s2.add(qm31_mul(qm31_mul(e2, w2), d2));
-    const qm31 e3 = qm31_add(e2, de), w3 = qm31_add(w2, dw), d3 = qm31_add(d2, dd);
-    s3.add(qm31_mul(qm31_mul(e3, w3), d3));
-  }
-  qm31 v[4] = {s0.reduce(), s1.reduce(), s2.reduce(), s3.reduce()};
-  sink_finish<4>(v, sink);
-}
-
-// Degree-1 sumcheck round over one vector (multiplicities; prover.rs:9449-9511):
-// lo = sum_{i<half} v[i], hi = sum_{i<half} v[half+i], with the same fused fold.
-__global__ void __launch_bounds__(kBlock) k_sum_round(const qm31* __restrict__ v_in, qm31* __restrict__ v_out,
-                                                      uint64_t half, int fold, qm31 alpha,
-                                                      RoundSink sink) {
-  qacc lo, hi;
-  lo.zero(); hi.zero();
-  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < half; i += stride) {
-    qm31 x0, x1;
-    if (fold) {
-      x0 = qm31_fold(ld_q(v_in, i), ld_q(v_in, i + 2 * half), alpha);
-      x1 = qm31_fold(ld_q(v_in, i + half), ld_q(v_in, i + 3 * half), alpha);
-      st_q(v_out, i, x0); st_q(v_out, i + half, x1);
-    } else {
-      x0 = ld_q(v_in, i); x1 = ld_q(v_in, i + half);
-    }
-    lo.add(x0);
-    hi.add(x1);
-  }
-  qm31 v[2] = {lo.reduce(), hi.reduce()};
-  sink_finish<2>(v, sink);
-}
 // pad_matrix_pow2 + matrix_to_mle (components/matmul.rs:649-664, 174-187):
 // out[p] = X[r][c] lifted to QM31 for p = r * pcol + c inside the matrix, 0 outside.
 __global__ void k_pad_q(const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
