@@ -34,7 +34,7 @@ import gkr_mi355x as G  # noqa: E402
 METRIC = "GKR matmul-sumcheck Melem/s + % HBM peak; proved tokens/s, Qwen2.5-14B shape"
 HBM_PEAK_GBS = 8000.0
 (K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT,
- K_HOST_WAIT_TAIL, K_MERKLE) = range(10)
+ K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH) = range(13)
 
 QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
 SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
@@ -531,7 +531,8 @@ def main():
                              "ms_per_step": round(ms / args.steps, 3)}
     host = {}
     for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait"),
-                      (K_HOST_WAIT_TAIL, "device_wait_handover")]:
+                      (K_HOST_WAIT_TAIL, "device_wait_handover"), (K_HOST_DRAW, "claim_draws"),
+                      (K_HOST_LAUNCH, "launch_calls"), (K_HOST_FINISH, "host_finish")]:
         ms, nl, _ = ctx.kernel_time(kid)
         if nl:
             host[name] = {"ms_per_step": round(ms / args.steps, 3), "avg_us": round(ms / nl * 1e3, 3), "calls": nl}

@@ -95,7 +95,9 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * inside the reducers, 7 host wait for results of device kernels, 8 host wait
  * for the hand-over of a sumcheck's last vectors
  * (wall-clock, bytes = 0); 9 Merkle level kernel of the commitments, whose
- * "bytes" count Poseidon hashes instead.                                   */
+ * "bytes" count Poseidon hashes instead; 10 host: claim-point draws in the
+ * walk, 11 host: time inside kernel-launch calls of the reducers, 12 host:
+ * the host-finish rounds' arithmetic (wall-clock, bytes = 0).              */
 /* level 0: off; 1: events on k_restrict_cols and the Merkle level kernel,
  * plus the host timers; 2: events on every timed kernel (adds an event pair
  * per launch). */

@@ -84,14 +84,14 @@ static bool felt_abi_canonical(const gkr_felt& f) {
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_NSLOTS
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and host-side phases (Fiat-Shamir
 // hashing inside the reducers, waiting for trip results, waiting for the
 // hand-over of the last vectors).
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
                 K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
-                K_NKERNELS = 10 };
+                K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NKERNELS = 13 };
 constexpr int kMaxPartialBlocks = 1024;
 constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
 // Result slots in the coherent host area (h_out): 0 .. 63 serve the result in
@@ -166,12 +166,18 @@ struct gkr_ctx {
   std::set<gkr_qvec*> qvecs;       // live QM31 vectors; detached likewise
   uint64_t table_on_device = 0;    // (tag << 32 | log) of the table held in S_TABLE, 0 = none
   MerkleConsts* merkle_consts = nullptr;  // device copy, built on first use
+  bool fb_pending = false;  // f_b of the last restriction still as column-chunk partials (S_COLPART)
+  uint64_t fb_rows = 0, fb_pk = 0;
+  int fb_chunks = 0;
+  uint32_t trip_count = 0;         // value of the fused trips' arrival counter (S_TRIPCNT) after the queued launches
+  bool trip_count_valid = false;   // false: zero the counter before the next fused trip
 };
 
 static int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
   if (bytes == 0) bytes = 16;
   if (c->cap[s] < bytes) {
     if (s == S_TABLE) c->table_on_device = 0;
+    if (s == S_TRIPCNT) c->trip_count_valid = false;  // fresh memory must be zeroed
     if (c->buf[s]) HIP_TRY(hipFree(c->buf[s]));
     c->buf[s] = nullptr;
     c->cap[s] = 0;
@@ -381,6 +387,7 @@ struct HandoverSession {
   // Launch k_handover<NV> over the vectors a (, b) of length len, to be folded by k challenges.
   template <int NV>
   int launch(const qm31* a, const qm31* b, uint64_t len, int k) {
+    HostTimer ht(c, K_HOST_LAUNCH);
     if (len > (uint64_t)kHandMax || k < 0 || k > kTripMaxK || (len >> k) == 0)
       return fail(GKR_ERR_DEVICE, "hand-over of %llu entries folded %d times", (unsigned long long)len, k);
     res_seq = alloc_seq(&c->seq, 1);
@@ -430,6 +437,15 @@ constexpr uint64_t kTripBig = GKR_TRIP_BIG;
 #define GKR_TRIP_MAX_BLOCKS 512
 #endif
 constexpr unsigned kTripMaxBlocks = GKR_TRIP_MAX_BLOCKS;  // partial rows per trip (the finisher adds them)
+// Trips whose one-entry-per-thread grid is at most kTripFusedGrid workgroups
+// run on at most kTripFusedMax workgroups and finish in the kernel itself.
+#ifndef GKR_TRIP_FUSED
+#define GKR_TRIP_FUSED 1
+#endif
+#ifndef GKR_TRIP_FUSED_GRID
+#define GKR_TRIP_FUSED_GRID 256
+#endif
+constexpr unsigned kTripFusedGrid = GKR_TRIP_FUSED_GRID;
 static std::vector<Trip> plan_trips(int T, uint64_t host_len, int k0) {
   std::vector<Trip> v;
   if (T <= 0) return v;
@@ -524,30 +540,47 @@ static void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out
 template <int KIND, int K>
 static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n, int np, const TripChal& al,
                          qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, const RoundSink& sk,
-                         unsigned grid) {
+                         unsigned grid, uint64_t b_rows, int b_chunks) {
+  uint32_t* counter = nullptr;
+  uint32_t base = 0;
+  if (GKR_TRIP_FUSED && grid <= kTripFusedMax) {  // one launch: the last workgroup finishes
+    TRY(ensureT(c, S_TRIPCNT, 1, &counter));
+    if (!c->trip_count_valid) {
+      HIP_TRY(hipMemsetAsync(counter, 0, sizeof(uint32_t), c->stream));
+      c->trip_count = 0;
+      c->trip_count_valid = true;
+    }
+    base = c->trip_count;
+    c->trip_count += grid;
+  }
   hipLaunchKernelGGL((k_trip<KIND, K>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
-                     sk.partials);
+                     sk, counter, base, b_rows, b_chunks);
   TRY(check_launch());
+  if (counter) return GKR_OK;
   constexpr int NQ = TripShape<KIND, K>::NQ;
   hipLaunchKernelGGL(k_finish_wide<NQ>, dim3(1), dim3(kFinishBlock), 0, c->stream, sk, grid);
   return check_launch();
 }
 static int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
                        const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
-                       RoundSink* sk) {
-  if (np < 0 || np > kTripMaxK || K < 0 || K > kTripMaxK || (n >> K) == 0 || (kind == 1) != (hi != nullptr))
+                       RoundSink* sk, uint64_t b_rows = 0, int b_chunks = 0) {
+  if (np < 0 || np > kTripMaxK || K < 0 || K > kTripMaxK || (n >> K) == 0 || (kind == 1) != (hi != nullptr) ||
+      (b_chunks && (kind != 0 || np != 0 || b_rows > n)))
     return fail(GKR_ERR_DEVICE, "bad trip (kind %d, K %d, np %d, n %llu)", kind, K, np, (unsigned long long)n);
+  HostTimer ht(c, K_HOST_LAUNCH);
   TripChal al;
   memset(&al, 0, sizeof al);
   for (int i = 0; i < np; i++) al.c[i] = pend[i];
   TRY(make_sink(c, sk, slot));
   unsigned grid = partial_grid(n);  // one entry per thread up to kTripMaxBlocks workgroups
   if (grid > kTripMaxBlocks) grid = kTripMaxBlocks;
+  if (GKR_TRIP_FUSED && grid <= kTripFusedGrid) grid = grid < kTripFusedMax ? grid : kTripFusedMax;
   const int nvec = kind == 2 ? 1 : 2;
   TimedLaunch tl(c, kind == 0 ? K_MM_ROUND : K_EQ3_ROUND,
                  16ull * nvec * ((n << np) + (da ? n : 0)));
-#define GKR_TRIP_CASE(KI, KK) \
-  if (kind == KI && K == KK) return launch_trip_k<KI, KK>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid);
+#define GKR_TRIP_CASE(KI, KK)                                                                                 \
+  if (kind == KI && K == KK)                                                                                  \
+    return launch_trip_k<KI, KK>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks);
   GKR_TRIP_CASE(0, 1) GKR_TRIP_CASE(0, 2) GKR_TRIP_CASE(0, 3)
   GKR_TRIP_CASE(1, 0) GKR_TRIP_CASE(1, 1) GKR_TRIP_CASE(1, 2) GKR_TRIP_CASE(1, 3)
   GKR_TRIP_CASE(2, 1) GKR_TRIP_CASE(2, 2) GKR_TRIP_CASE(2, 3)
@@ -888,22 +921,42 @@ static gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t
 extern "C" uint32_t gkr_synthetic_value(int kind, uint64_t seed, uint64_t i) { return synth_value(kind, seed, i); }
 
 // ------------------------------------------------------------------ matmul reduction
+// The weight-side restriction leaves f_b as column-chunk partials; the first
+// product trip adds them (and stores f_b), or finish_fb does when another
+// consumer comes first.
+static int finish_fb(gkr_ctx* c) {
+  if (!c->fb_pending) return GKR_OK;
+  qm31* fb;
+  TRY(ensureT(c, S_FB0, c->fb_pk, &fb));
+  hipLaunchKernelGGL(k_restrict_cols_finish, dim3(grid_for(c->fb_pk)), dim3(kBlock), 0, c->stream,
+                     (const qm31*)c->buf[S_COLPART], c->fb_rows, c->fb_pk, c->fb_chunks, fb);
+  c->fb_pending = false;
+  return check_launch();
+}
 // Restrict A rows by r_i and B columns by r_j into f_a (S_FA0) and f_b (S_FB0),
-// each of length pk (components/matmul.rs:470-565, backend.rs:127-134).
+// each of length pk (components/matmul.rs:470-565, backend.rs:127-134): one
+// launch for both Lagrange tables, one for both restrictions (f_a directly,
+// f_b as column-chunk partials in S_COLPART, pending until added).
 static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, const qm31* r_i, int n_ri,
                          const qm31* r_j, int n_rj, uint64_t pk) {
+  HostTimer ht(c, K_HOST_LAUNCH);
   const uint64_t m = A->rows, k = A->cols, n = B->cols;
   qm31 *Li, *Lj, *fa, *fb;
   TRY(ensureT(c, S_LI, m, &Li));
   TRY(ensureT(c, S_LJ, n, &Lj));
   TRY(ensureT(c, S_FA0, pk, &fa));
   TRY(ensureT(c, S_FB0, pk, &fb));
-  TRY(eq_table(c, r_i, n_ri, m, Li));
-  TRY(eq_table(c, r_j, n_rj, n, Lj));
-  {
-    TimedLaunch t(c, K_RESTRICT_ROWS, 4 * m * k + 16 * m + 16 * pk);
-    hipLaunchKernelGGL(k_restrict_rows, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, A->dev, m, k, pk, Li, fa);
+  c->fb_pending = false;
+  if (n_ri + n_rj <= kMaxVars) {
+    std::vector<qm31> both(r_i, r_i + n_ri);
+    both.insert(both.end(), r_j, r_j + n_rj);
+    PointArg pt = make_point(both.data(), n_ri + n_rj);
+    TimedLaunch tl(c, K_EQ_TABLE, 16 * (m + n));
+    hipLaunchKernelGGL(k_eq_two, dim3(grid_for(m + n)), dim3(kBlock), 0, c->stream, pt, n_ri, m, n, Li, Lj);
     TRY(check_launch());
+  } else {
+    TRY(eq_table(c, r_i, n_ri, m, Li));
+    TRY(eq_table(c, r_j, n_rj, n, Lj));
   }
   {
     // column chunks: chunks a multiple of one wave sweep (256 columns), at
@@ -928,19 +981,24 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     gc = (n + chunk - 1) / chunk;
     qm31* part;
     TRY(ensureT(c, S_COLPART, (size_t)gc * k, &part));
+    // the activation side rides in one more column-chunk slice (one column per thread)
+    RowsJob rows{A->dev, m, k, pk, Li, fa};
+    if (gr * kBlock < pk) return fail(GKR_ERR_DEVICE, "restriction grid too small for f_a");
     {
-      TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + 16 * pk);
+      // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
+      TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + 4 * m * k + 16 * m + 16 * pk);
       if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
-        hipLaunchKernelGGL(k_restrict_cols<true>, dim3((unsigned)gr, (unsigned)gc), dim3(kBlock), 0, c->stream,
-                           B->dev, k, n, chunk, Lj, (uint32_t*)part);
+        hipLaunchKernelGGL(k_restrict_cols<true>, dim3((unsigned)gr, (unsigned)gc + 1), dim3(kBlock), 0, c->stream,
+                           B->dev, k, n, chunk, Lj, (uint32_t*)part, rows);
       else
-        hipLaunchKernelGGL(k_restrict_cols<false>, dim3((unsigned)gr, (unsigned)gc), dim3(kBlock), 0, c->stream,
-                           B->dev, k, n, chunk, Lj, (uint32_t*)part);
+        hipLaunchKernelGGL(k_restrict_cols<false>, dim3((unsigned)gr, (unsigned)gc + 1), dim3(kBlock), 0,
+                           c->stream, B->dev, k, n, chunk, Lj, (uint32_t*)part, rows);
       TRY(check_launch());
     }
-    hipLaunchKernelGGL(k_restrict_cols_finish, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, part, k, pk, (int)gc,
-                       fb);
-    TRY(check_launch());
+    c->fb_pending = true;
+    c->fb_rows = k;
+    c->fb_pk = pk;
+    c->fb_chunks = (int)gc;
   }
   return GKR_OK;
 }
@@ -954,7 +1012,13 @@ static int first_product_trip(gkr_ctx* c, uint64_t pk, int* K, qm31* g) {
   const int T = log2_exact(pk);
   *K = T < kTripMaxK ? T : kTripMaxK;
   RoundSink sk;
-  TRY(launch_trip(c, 0, *K, fa, fb, pk, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, &sk));
+  if (c->fb_pending) {  // add the chunk partials on the fly and store f_b
+    TRY(launch_trip(c, 0, *K, fa, (const qm31*)c->buf[S_COLPART], pk, 0, nullptr, nullptr, fb, nullptr, nullptr, 0,
+                    0, &sk, c->fb_rows, c->fb_chunks));
+    c->fb_pending = false;
+  } else {
+    TRY(launch_trip(c, 0, *K, fa, fb, pk, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 0, &sk));
+  }
   return wait_trip(c, sk, trip_nq(0, *K), g);
 }
 
@@ -1091,13 +1155,17 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
   for (int t = t_end; t < T; t++) {
     const size_t half = A.size() / 2;
     qm31 sums[3] = {qm31_zero(), qm31_zero(), qm31_zero()};
-    for (size_t i = 0; i < half; i++) {
-      const qm31 a0 = A[i], a1 = A[i + half], b0 = B[i], b1 = B[i + half];
-      sums[0] = qm31_add(sums[0], qm31_mul(a0, b0));
-      sums[1] = qm31_add(sums[1], qm31_mul(a1, b1));
-      sums[2] = qm31_add(sums[2], qm31_mul(qm31_sub(qm31_add(a1, a1), a0), qm31_sub(qm31_add(b1, b1), b0)));
+    {
+      HostTimer ht(c, K_HOST_FINISH);
+      for (size_t i = 0; i < half; i++) {
+        const qm31 a0 = A[i], a1 = A[i + half], b0 = B[i], b1 = B[i + half];
+        sums[0] = qm31_add(sums[0], qm31_mul(a0, b0));
+        sums[1] = qm31_add(sums[1], qm31_mul(a1, b1));
+        sums[2] = qm31_add(sums[2], qm31_mul(qm31_sub(qm31_add(a1, a1), a0), qm31_sub(qm31_add(b1, b1), b0)));
+      }
     }
     absorb(t, sums);
+    HostTimer ht(c, K_HOST_FINISH);
     for (size_t i = 0; i < half; i++) {
       A[i] = qm31_fold(A[i], A[i + half], chal[t]);
       B[i] = qm31_fold(B[i], B[i + half], chal[t]);
@@ -1119,6 +1187,7 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
                 (unsigned long long)next_pow2(a->cols));
   HIP_TRY(hipSetDevice(c->device));
   TRY(ensure_restricted(c, a, b, r_i, n_ri, r_j, n_rj));
+  if (!c->mm.have_trip0) TRY(finish_fb(c));  // the sumcheck reads f_b from S_FB0
   const int T = log2_exact(pk);
   qm31 *fa0, *fa1, *fb0, *fb1, *fa2, *fb2;
   TRY(ensureT(c, S_FA0, pk, &fa0));
@@ -1165,6 +1234,7 @@ extern "C" int gkr_matmul_output_claim(gkr_ctx* c, const gkr_matrix* a, const gk
   TRY(ensure_restricted(c, a, b, r_out, n_ri, r_out + n_ri, n_vars - n_ri));
   const uint64_t pk = next_pow2(a->cols);
   if (pk == 1) {
+    TRY(finish_fb(c));
     qm31 fa[1], fb[1];
     qm31 *dfa, *dfb;
     TRY(ensureT(c, S_FA0, 1, &dfa));
@@ -1504,6 +1574,7 @@ static int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
     pl->lo_off.push_back(table(nv - h, h));
     pl->h.push_back(h);
   }
+  HostTimer ht(c, K_HOST_LAUNCH);
   qm31* parts;
   TRY(ensureT(c, S_EQPARTS, total, &parts));
   {
@@ -1609,16 +1680,20 @@ static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3
   for (int t = t_end; t < nv; t++) {
     const size_t half = E.size() / 2;
     qm31 sums[4] = {qm31_zero(), qm31_zero(), qm31_zero(), qm31_zero()};
-    for (size_t i = 0; i < half; i++) {
-      const qm31 e0 = E[i], e1 = E[i + half], w0v = W[i], w1v = W[i + half], d0v = D[i], d1v = D[i + half];
-      sums[0] = qm31_add(sums[0], qm31_mul(qm31_mul(e0, w0v), d0v));
-      sums[1] = qm31_add(sums[1], qm31_mul(qm31_mul(e1, w1v), d1v));
-      const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1v, w0v), dd = qm31_sub(d1v, d0v);
-      const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1v, dw), d2 = qm31_add(d1v, dd);
-      sums[2] = qm31_add(sums[2], qm31_mul(qm31_mul(e2, w2), d2));
-      sums[3] = qm31_add(sums[3], qm31_mul(qm31_mul(qm31_add(e2, de), qm31_add(w2, dw)), qm31_add(d2, dd)));
+    {
+      HostTimer ht(c, K_HOST_FINISH);
+      for (size_t i = 0; i < half; i++) {
+        const qm31 e0 = E[i], e1 = E[i + half], w0v = W[i], w1v = W[i + half], d0v = D[i], d1v = D[i + half];
+        sums[0] = qm31_add(sums[0], qm31_mul(qm31_mul(e0, w0v), d0v));
+        sums[1] = qm31_add(sums[1], qm31_mul(qm31_mul(e1, w1v), d1v));
+        const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1v, w0v), dd = qm31_sub(d1v, d0v);
+        const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1v, dw), d2 = qm31_add(d1v, dd);
+        sums[2] = qm31_add(sums[2], qm31_mul(qm31_mul(e2, w2), d2));
+        sums[3] = qm31_add(sums[3], qm31_mul(qm31_mul(qm31_add(e2, de), qm31_add(w2, dw)), qm31_add(d2, dd)));
+      }
     }
     absorb3(t, sums);
+    HostTimer ht(c, K_HOST_FINISH);
     for (size_t i = 0; i < half; i++) {
       E[i] = qm31_fold(E[i], E[i + half], chal[t]);
       W[i] = qm31_fold(W[i], W[i + half], chal[t]);
@@ -1705,21 +1780,24 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   //   multiplicity sumcheck trip 0 (no challenge needed)         kSlotMult0
   //   eq tables of the eq-sumcheck trips, eq-sumcheck trip 0     kSlotEq0
   RoundSink sk_prep, sk_table, sk_mult0, sk_eq0;
-  TRY(make_sink(c, &sk_prep, kSlotPrep));
   {
-    TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 16 * n + 8 * n + 32 * n);
-    hipLaunchKernelGGL(k_logup_prepare, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, input->dev, input->rows,
-                       input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, d_e0, d_min, d_mout, d_d0, d_w0,
-                       d_mult, sk_prep);
+    HostTimer ht(c, K_HOST_LAUNCH);
+    TRY(make_sink(c, &sk_prep, kSlotPrep));
+    {
+      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 16 * n + 8 * n + 32 * n);
+      hipLaunchKernelGGL(k_logup_prepare, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, input->dev,
+                         input->rows, input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, d_e0, d_min,
+                         d_mout, d_d0, d_w0, d_mult, sk_prep);
+    }
+    TRY(launch_finish<2>(c, sk_prep, partial_grid(n)));
+    TRY(make_sink(c, &sk_table, kSlotTable));
+    hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult,
+                       tsize, gamma, beta, sk_table);
+    TRY(launch_finish<1>(c, sk_table, partial_grid(tsize)));
+    HIP_TRY(hipMemcpyAsync(c->h_mult, d_mult, tsize * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+    hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0);
+    TRY(check_launch());
   }
-  TRY(launch_finish<2>(c, sk_prep, partial_grid(n)));
-  TRY(make_sink(c, &sk_table, kSlotTable));
-  hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult, tsize,
-                     gamma, beta, sk_table);
-  TRY(launch_finish<1>(c, sk_table, partial_grid(tsize)));
-  HIP_TRY(hipMemcpyAsync(c->h_mult, d_mult, tsize * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
-  hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0);
-  TRY(check_launch());
   const std::vector<Trip> mtrips = plan_trips((int)table_log, kHostTailSum, kTripMaxK);
   TRY(launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
                   kSlotMult0, &sk_mult0));
@@ -1816,11 +1894,15 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     for (int t = t_end; t < (int)table_log; t++) {
       const size_t half = V.size() / 2;
       qm31 sums[2] = {qm31_zero(), qm31_zero()};
-      for (size_t i = 0; i < half; i++) {
-        sums[0] = qm31_add(sums[0], V[i]);
-        sums[1] = qm31_add(sums[1], V[i + half]);
+      {
+        HostTimer ht(c, K_HOST_FINISH);
+        for (size_t i = 0; i < half; i++) {
+          sums[0] = qm31_add(sums[0], V[i]);
+          sums[1] = qm31_add(sums[1], V[i + half]);
+        }
       }
       absorb1((uint32_t)t, sums);
+      HostTimer ht(c, K_HOST_FINISH);
       for (size_t i = 0; i < half; i++) V[i] = qm31_fold(V[i], V[i + half], alpha);
       V.resize(half);
     }
@@ -2740,7 +2822,10 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.b->cols)));
       if (st.claim == GKR_CLAIM_FRESH) {
         point.resize(nv);
-        TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        {
+          HostTimer ht(c, K_HOST_DRAW);
+          TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        }
         TRY(gkr_matmul_output_claim(c, st.a, st.b, point.data(), nv, &value));
         ch->ch.mix_secure_field(Q(value));
       } else if (!have_claim) {
@@ -2759,7 +2844,10 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
       if (st.claim == GKR_CLAIM_FRESH) {
         point.resize(nv);
-        TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        {
+          HostTimer ht(c, K_HOST_DRAW);
+          TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        }
         TRY(gkr_mul_output_claim(c, st.a, st.b, point.data(), nv, &value));
         ch->ch.mix_secure_field(Q(value));
       } else if (!have_claim) {
@@ -2775,7 +2863,10 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
       if (st.claim == GKR_CLAIM_FRESH) {
         point.resize(nv);
-        TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        {
+          HostTimer ht(c, K_HOST_DRAW);
+          TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        }
         value = G(ch->ch.draw_qm31());
       } else if (!have_claim) {
         return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);

@@ -119,6 +119,28 @@ __global__ void __launch_bounds__(kBlock) k_finish(RoundSink sk, uint32_t nblock
     publish_flag(sk.flag, sk.seq);
   }
 }
+// Device-scope (all XCDs) stores and loads: they bypass the XCD-private L2
+// caches, so workgroups of one grid exchange values without cache
+// maintenance.
+__device__ __forceinline__ void st_q_dev(qm31* p, qm31 v) {
+  uint64_t* w = reinterpret_cast<uint64_t*>(p);
+  __hip_atomic_store(w + 0, (uint64_t)v.a | ((uint64_t)v.b << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(w + 1, (uint64_t)v.c | ((uint64_t)v.d << 32), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ qm31 ld_q_dev(const qm31* p) {
+  const uint64_t* w = reinterpret_cast<const uint64_t*>(p);
+  const uint64_t lo = __hip_atomic_load(w + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load(w + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return qm31{(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+}
+// Wait until every memory operation this wave issued has completed (the
+// signal fences keep the compiler from moving memory accesses across it).
+__device__ __forceinline__ void wait_memory() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // ------------------------------------------------------------------ multi-round trips
 // One launch serves K consecutive rounds of a sumcheck (K <= kTripMaxK).
 // Seen through its top K variables (MSB first), a vector f of length n splits
@@ -142,7 +164,13 @@ __global__ void __launch_bounds__(kBlock) k_finish(RoundSink sk, uint32_t nblock
 // Lanes: groups of 2^K consecutive lanes share one x; lane c of a group
 // holds a_c (and b_c), the b's of the group are exchanged by shuffles and
 // lane c accumulates row c of G.  Rows are reduced across the wave and the
-// workgroup into one partial row per workgroup; k_finish_wide adds the rows.
+// workgroup into one partial row per workgroup.  Then either k_finish_wide
+// (launched behind) adds the rows, or, when `counter` is given (grids of at
+// most kTripFusedMax workgroups), the rows are stored with device-scope
+// stores, each workgroup counts itself on the device-scope counter once its
+// row is in memory, and the last to arrive (the counter reaches
+// count_base + gridDim.x, mod 2^32; the host tracks the value) adds the rows
+// and delivers them to sk like k_finish: one launch per trip.
 constexpr int kTripMaxK = 3;
 struct TripChal {
   qm31 c[kTripMaxK];
@@ -189,12 +217,18 @@ struct TripShape {
 };
 
 // Requirements (checked by the host): np <= 3, n a power of two >= 2^K.
+constexpr unsigned kTripFusedMax = 64;
+// b_chunks > 0 (first trip of a matmul, np = 0): sb holds the column-chunk
+// partials of the weight-side restriction (k_restrict_cols) and b is their
+// sum, b[pos] = sum_c sb[c * b_rows + pos] for pos < b_rows and 0 above
+// (the zero padding to n); with db the sums are stored as f_b.
 template <int KIND, int K>
 __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, const qm31* __restrict__ sb,
                                                  uint64_t n, int np, TripChal al, qm31* __restrict__ da,
                                                  qm31* __restrict__ db, const qm31* __restrict__ eq_hi,
-                                                 const qm31* __restrict__ eq_lo, int eq_h,
-                                                 qm31* __restrict__ partials) {
+                                                 const qm31* __restrict__ eq_lo, int eq_h, RoundSink sk,
+                                                 uint32_t* counter, uint32_t count_base, uint64_t b_rows,
+                                                 int b_chunks) {
   using S = TripShape<KIND, K>;
   constexpr int G = S::G;
   const uint64_t nb = n >> K;
@@ -211,7 +245,16 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
     if constexpr (KIND == 2) {
       acc[0].add(a);
     } else {
-      const qm31 b = load_pending(sb, pos, n, np, al);
+      qm31 b;
+      if (b_chunks) {
+        qacc bs;
+        bs.zero();
+        if (pos < b_rows)
+          for (int ch = 0; ch < b_chunks; ch++) bs.add(ld_q(sb, (uint64_t)ch * b_rows + pos));
+        b = bs.reduce();
+      } else {
+        b = load_pending(sb, pos, n, np, al);
+      }
       if (db) st_q(db, pos, b);
       if constexpr (KIND == 1) {
         const uint64_t mask = (1ull << eq_h) - 1;
@@ -244,7 +287,38 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
     qm31 s = sh[0][q];
 #pragma unroll
     for (int w = 1; w < kBlock / 64; w++) s = qm31_add(s, sh[w][q]);
-    st_q(partials, (uint64_t)blockIdx.x * S::NQ + q, s);
+    if (counter)
+      st_q_dev(sk.partials + (uint64_t)blockIdx.x * S::NQ + q, s);
+    else
+      st_q(sk.partials, (uint64_t)blockIdx.x * S::NQ + q, s);
+  }
+  if (!counter) return;
+  __shared__ bool sh_last;
+  wait_memory();  // this workgroup's row is in memory before it is counted
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_last = old == count_base + gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!sh_last) return;
+  // the last workgroup: thread t adds column t % NQ over every (kBlock / NQ)-th row
+  constexpr int RG = S::NQ < kBlock ? kBlock / S::NQ : 1;
+  const int q = threadIdx.x % S::NQ, g = threadIdx.x / S::NQ;
+  qacc col;
+  col.zero();
+  if (g < RG)
+    for (uint32_t b = g; b < gridDim.x; b += RG) col.add(ld_q_dev(sk.partials + (uint64_t)S::NQ * b + q));
+  __shared__ qm31 tot[kBlock];
+  tot[threadIdx.x] = col.reduce();
+  __syncthreads();
+  for (int step = RG / 2; step >= 1; step /= 2) {
+    if (g < step) tot[threadIdx.x] = qm31_add(tot[threadIdx.x], tot[threadIdx.x + step * S::NQ]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    for (int i = 0; i < S::NQ; i++) sk.out[i] = tot[i];
+    publish_flag(sk.flag, sk.seq);
   }
 }
 
@@ -394,6 +468,25 @@ __global__ void k_eq_direct(PointArg pt, uint64_t count, qm31* __restrict__ out)
   }
   st_q(out, x, acc);
 }
+// Both Lagrange tables of a matmul restriction in one launch: out1[x] over
+// coordinates [0, n1) of pt (count1 entries), out2[x] over [n1, pt.n)
+// (count2 entries), one thread per entry.
+__global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, qm31* __restrict__ out1,
+                         qm31* __restrict__ out2) {
+  uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int s = 0, n = n1;
+  qm31* out = out1;
+  if (x >= count1) {
+    x -= count1;
+    if (x >= count2) return;
+    s = n1;
+    n = pt.n - n1;
+    out = out2;
+  }
+  qm31 acc = qm31_one();
+  for (int l = 0; l < n; l++) acc = qm31_mul(acc, ((x >> (n - 1 - l)) & 1ull) ? pt.r[s + l] : pt.omr[s + l]);
+  st_q(out, x, acc);
+}
 // Split construction: hi table over variables [0, n-h), lo over [n-h, n).
 __global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __restrict__ lo) {
   const uint64_t n_hi = 1ull << (pt.n - h), n_lo = 1ull << h;
@@ -423,9 +516,8 @@ __global__ void k_eq_combine(const qm31* __restrict__ hi, const qm31* __restrict
 // ------------------------------------------------------------------ restriction
 // Activation side: f_a[j] = sum_{i<m} A[i][j] * L[i] for j < k, 0 for k <= j < pk.
 // One thread per column; consecutive threads read consecutive words of a row.
-__global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint64_t k, uint64_t pk,
-                                const qm31* __restrict__ L, qm31* __restrict__ out) {
-  uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void restrict_rows_col(const uint32_t* __restrict__ A, uint64_t m, uint64_t k, uint64_t pk,
+                                                  const qm31* __restrict__ L, qm31* __restrict__ out, uint64_t j) {
   if (j >= pk) return;
   if (j >= k) {
     st_q(out, j, qm31_zero());
@@ -457,6 +549,10 @@ __global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint
 #pragma unroll
   for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
   st_q(out, j, qm31{r[0], r[1], r[2], r[3]});
+}
+__global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint64_t k, uint64_t pk,
+                                const qm31* __restrict__ L, qm31* __restrict__ out) {
+  restrict_rows_col(A, m, k, pk, L, out, (uint64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // Weight side: f_b[i] = sum_{j<n} B[i][j] * L[j] for i < k, 0 for k <= i < pk.
@@ -503,16 +599,33 @@ __device__ __forceinline__ void load_row4(const uint32_t* __restrict__ row, uint
   }
 }
 
+// The activation-side restriction of the same matmul rides along: when
+// act.A is set, the grid has one extra column-chunk slice (the first, so it
+// is dispatched alongside the weight side's first workgroups) whose
+// workgroups compute f_a (one column per thread, restrict_rows_col) instead,
+// so both restrictions run in one launch (the host checks
+// gridDim.x * kBlock >= pk).
+struct RowsJob {
+  const uint32_t* A;
+  uint64_t m, k, pk;
+  const qm31* L;
+  qm31* out;
+};
 template <bool kVec4>
 __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
                                                           uint64_t chunk, const qm31* __restrict__ L,
-                                                          uint32_t* __restrict__ partial) {
+                                                          uint32_t* __restrict__ partial, RowsJob act) {
+  if (act.A && blockIdx.y == 0) {
+    restrict_rows_col(act.A, act.m, act.k, act.pk, act.L, act.out, (uint64_t)blockIdx.x * blockDim.x + threadIdx.x);
+    return;
+  }
+  const uint32_t chunk_id = blockIdx.y - (act.A ? 1 : 0);
   __shared__ uint32_t sh[kColWaves][64][17];  // epilogue transpose, one region per wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t row0 = ((uint64_t)blockIdx.x * kColWaves + wave) * kColRows;
   if (row0 >= k) return;  // whole wave leaves; no workgroup barrier follows
   const int nrows = (int)((k - row0) < (uint64_t)kColRows ? (k - row0) : (uint64_t)kColRows);
-  const uint64_t c0 = (uint64_t)blockIdx.y * chunk;
+  const uint64_t c0 = (uint64_t)chunk_id * chunk;
   const uint64_t c1 = (c0 + chunk < n) ? c0 + chunk : n;
   const uint32_t* rows[kColRows];
 #pragma unroll
@@ -571,7 +684,7 @@ __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __rest
   w = m31_add(w, shfl_xor_u32(w, 32));
   if (lane < 16) {
     const int r = lane >> 2, c = lane & 3;
-    if (r < nrows) partial[((uint64_t)blockIdx.y * k + row0 + r) * 4 + c] = w;
+    if (r < nrows) partial[((uint64_t)chunk_id * k + row0 + r) * 4 + c] = w;
   }
 }
 // f_b[i] = sum over column chunks of partial[chunk * k + i] for i < k; 0 for k <= i < pk.
