@@ -84,7 +84,7 @@ static bool felt_abi_canonical(const gkr_felt& f) {
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_NSLOTS
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and host-side phases (Fiat-Shamir
 // hashing inside the reducers, waiting for trip results, waiting for the
@@ -134,6 +134,12 @@ struct gkr_matrix {
   // (gemm.h), built on first use; the contents of a matrix never change
   int8_t* bplanes = nullptr;
   int bnplanes = 0;
+  // row-major int8 copy for the weight-side restriction (rows padded to
+  // r8_stride bytes), built on first use when every entry is int8-range;
+  // r8_state: 0 not yet checked, 1 copy present, -1 not int8-range
+  int8_t* r8 = nullptr;
+  uint64_t r8_stride = 0;
+  int r8_state = 0;
 };
 
 struct gkr_qvec {
@@ -806,7 +812,9 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   for (gkr_matrix* m : c->matrices) {  // matrices outliving their context keep only the handle
     if (m->owned && m->dev) (void)hipFree(m->dev);
     if (m->bplanes) (void)hipFree(m->bplanes);
+    if (m->r8) (void)hipFree(m->r8);
     m->bplanes = nullptr;
+    m->r8 = nullptr;
     m->dev = nullptr;
     m->ctx = nullptr;
   }
@@ -907,14 +915,15 @@ extern "C" void gkr_matrix_free(gkr_matrix* m) {
   if (m->ctx) {
     if (m->ctx->mm.a == m || m->ctx->mm.b == m) m->ctx->mm.valid = false;
     m->ctx->matrices.erase(m);
-    if ((m->owned && m->dev) || m->bplanes) (void)hipStreamSynchronize(m->ctx->stream);
+    if ((m->owned && m->dev) || m->bplanes || m->r8) (void)hipStreamSynchronize(m->ctx->stream);
     if (m->owned && m->dev) (void)hipFree(m->dev);
     if (m->bplanes) (void)hipFree(m->bplanes);
+    if (m->r8) (void)hipFree(m->r8);
   }
   delete m;
 }
 static gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t cols, bool owned) {
-  gkr_matrix* m = new gkr_matrix{c, dev, rows, cols, owned, nullptr, 0};
+  gkr_matrix* m = new gkr_matrix{c, dev, rows, cols, owned};
   c->matrices.insert(m);
   return m;
 }
@@ -933,14 +942,62 @@ static int finish_fb(gkr_ctx* c) {
   c->fb_pending = false;
   return check_launch();
 }
+// The int8 copy of weight B for the restriction (k_to_int8), on first use:
+// one pass over B and a 4-byte read-back of the range flag.
+#ifndef GKR_INT8_WEIGHTS
+#define GKR_INT8_WEIGHTS 1
+#endif
+#ifndef GKR_R8_ROWS
+#define GKR_R8_ROWS 4
+#endif
+constexpr int kR8Rows = GKR_R8_ROWS;  // weight rows per wave in k_restrict_cols8 (4 or 8)
+static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
+  if (B->r8_state || !GKR_INT8_WEIGHTS) return GKR_OK;
+  const uint64_t stride = (B->cols + 15) / 16 * 16;
+  if (B->rows == 0 || stride == 0 || B->rows * stride > (1ull << 40)) {
+    B->r8_state = -1;
+    return GKR_OK;
+  }
+  int8_t* r8 = nullptr;
+  if (hipMalloc(&r8, B->rows * stride) != hipSuccess) {  // no room: keep the u32 path
+    (void)hipGetLastError();
+    B->r8_state = -1;
+    return GKR_OK;
+  }
+  uint32_t* bad;
+  TRY(ensureT(c, S_R8FLAG, 1, &bad));
+  HIP_TRY(hipMemsetAsync(bad, 0, sizeof(uint32_t), c->stream));
+  const uint64_t words = B->rows * stride / 4;
+  const unsigned grid = (unsigned)std::min<uint64_t>((words + kBlock - 1) / kBlock, 4096);
+  hipLaunchKernelGGL(k_to_int8, dim3(grid), dim3(kBlock), 0, c->stream, B->dev, B->rows, B->cols, stride,
+                     (uint32_t*)r8, bad);
+  TRY(check_launch());
+  uint32_t flag = 1;
+  HIP_TRY(hipMemcpyAsync(c->h_res, bad, sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+  TRY(sync(c));
+  memcpy(&flag, c->h_res, sizeof flag);
+  if (flag) {
+    (void)hipFree(r8);
+    B->r8_state = -1;
+  } else {
+    B->r8 = r8;
+    B->r8_stride = stride;
+    B->r8_state = 1;
+  }
+  return GKR_OK;
+}
 // Restrict A rows by r_i and B columns by r_j into f_a (S_FA0) and f_b (S_FB0),
 // each of length pk (components/matmul.rs:470-565, backend.rs:127-134): one
 // launch for both Lagrange tables, one for both restrictions (f_a directly,
 // f_b as column-chunk partials in S_COLPART, pending until added).
 static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, const qm31* r_i, int n_ri,
                          const qm31* r_j, int n_rj, uint64_t pk) {
+  TRY(prepare_r8(c, const_cast<gkr_matrix*>(B)));  // the matrix's contents never change; r8 is derived
   HostTimer ht(c, K_HOST_LAUNCH);
   const uint64_t m = A->rows, k = A->cols, n = B->cols;
+  const bool use8 = B->r8_state == 1 && n < (1ull << 17);  // int32 digit sums stay exact below 2^17 columns
+  uint8_t* ldig = nullptr;
+  if (use8) TRY(ensureT(c, S_LDIG, ((n + 3) / 4) * 64, &ldig));
   qm31 *Li, *Lj, *fa, *fb;
   TRY(ensureT(c, S_LI, m, &Li));
   TRY(ensureT(c, S_LJ, n, &Lj));
@@ -952,9 +1009,10 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     both.insert(both.end(), r_j, r_j + n_rj);
     PointArg pt = make_point(both.data(), n_ri + n_rj);
     TimedLaunch tl(c, K_EQ_TABLE, 16 * (m + n));
-    hipLaunchKernelGGL(k_eq_two, dim3(grid_for(m + n)), dim3(kBlock), 0, c->stream, pt, n_ri, m, n, Li, Lj);
+    hipLaunchKernelGGL(k_eq_two, dim3(grid_for(m + n)), dim3(kBlock), 0, c->stream, pt, n_ri, m, n, Li, Lj, ldig);
     TRY(check_launch());
   } else {
+    if (use8) return fail(GKR_ERR_DEVICE, "int8 restriction needs the combined eq launch");
     TRY(eq_table(c, r_i, n_ri, m, Li));
     TRY(eq_table(c, r_j, n_rj, n, Lj));
   }
@@ -983,16 +1041,26 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     TRY(ensureT(c, S_COLPART, (size_t)gc * k, &part));
     // the activation side rides in one more column-chunk slice (one column per thread)
     RowsJob rows{A->dev, m, k, pk, Li, fa};
-    if (gr * kBlock < pk) return fail(GKR_ERR_DEVICE, "restriction grid too small for f_a");
-    {
+    const uint64_t act_blocks = (pk + 63) / 64;  // 64 columns of A per workgroup
+    if (act_blocks + gr * gc > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
+    const dim3 grid((unsigned)(act_blocks + gr * gc));
+    if (use8) {
+      // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
+      TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + 4 * m * k + 16 * m + 16 * pk);
+      const uint64_t gr8 = (k + kR8Rows * kColWaves - 1) / (kR8Rows * kColWaves);
+      const dim3 grid8((unsigned)(act_blocks + gr8 * gc));
+      hipLaunchKernelGGL(k_restrict_cols8<kR8Rows>, grid8, dim3(kBlock), 0, c->stream, B->r8, B->r8_stride, k, n,
+                         chunk, (const uint32_t*)ldig, (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr8);
+      TRY(check_launch());
+    } else {
       // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
       TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + 4 * m * k + 16 * m + 16 * pk);
       if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
-        hipLaunchKernelGGL(k_restrict_cols<true>, dim3((unsigned)gr, (unsigned)gc + 1), dim3(kBlock), 0, c->stream,
-                           B->dev, k, n, chunk, Lj, (uint32_t*)part, rows);
+        hipLaunchKernelGGL(k_restrict_cols<true>, grid, dim3(kBlock), 0, c->stream, B->dev, k, n, chunk, Lj,
+                           (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr);
       else
-        hipLaunchKernelGGL(k_restrict_cols<false>, dim3((unsigned)gr, (unsigned)gc + 1), dim3(kBlock), 0,
-                           c->stream, B->dev, k, n, chunk, Lj, (uint32_t*)part, rows);
+        hipLaunchKernelGGL(k_restrict_cols<false>, grid, dim3(kBlock), 0, c->stream, B->dev, k, n, chunk, Lj,
+                           (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr);
       TRY(check_launch());
     }
     c->fb_pending = true;
@@ -2404,11 +2472,14 @@ extern "C" int gkr_matmul_forward_into(gkr_ctx* c, const gkr_matrix* a, const gk
                 (unsigned long long)out->rows, (unsigned long long)out->cols);
   if (out == a || out == b) return fail(GKR_ERR_INVALID, "forward GEMM: output aliases an input");
   HIP_TRY(hipSetDevice(c->device));
-  if (out->bplanes) {  // the contents change: drop the cached planes
+  if (out->bplanes || out->r8 || out->r8_state) {  // the contents change: drop the derived copies
     HIP_TRY(hipStreamSynchronize(c->stream));
-    (void)hipFree(out->bplanes);
+    if (out->bplanes) (void)hipFree(out->bplanes);
+    if (out->r8) (void)hipFree(out->r8);
     out->bplanes = nullptr;
     out->bnplanes = 0;
+    out->r8 = nullptr;
+    out->r8_state = 0;
   }
   if (c->mm.a == out || c->mm.b == out) c->mm.valid = false;
   return matmul_forward(c, a, const_cast<gkr_matrix*>(b), out->dev);

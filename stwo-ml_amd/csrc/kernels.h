@@ -23,6 +23,19 @@ struct PointArg {
   qm31 omr[kMaxVars];
   int n;
 };
+// The point's coordinates (r, 1 - r) staged in LDS once per workgroup: the
+// eq kernels index them per thread, which would otherwise be one load from
+// the kernel-argument segment per coordinate and thread.
+struct PointLds {
+  qm31 r[kMaxVars], omr[kMaxVars];
+};
+__device__ __forceinline__ void stage_point(const PointArg& pt, PointLds* sp) {
+  for (int l = threadIdx.x; l < pt.n; l += blockDim.x) {
+    sp->r[l] = pt.r[l];
+    sp->omr[l] = pt.omr[l];
+  }
+  __syncthreads();
+}
 
 __device__ __forceinline__ qm31 ld_q(const qm31* __restrict__ p, uint64_t i) {
   uint4 v = reinterpret_cast<const uint4*>(p)[i];
@@ -304,11 +317,18 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
   if (!sh_last) return;
   // the last workgroup: thread t adds column t % NQ over every (kBlock / NQ)-th row
   constexpr int RG = S::NQ < kBlock ? kBlock / S::NQ : 1;
+  constexpr int MR = (int)((kTripFusedMax + RG - 1) / RG);  // rows per thread, all loads in flight at once
   const int q = threadIdx.x % S::NQ, g = threadIdx.x / S::NQ;
+  qm31 rv[MR];
+#pragma unroll
+  for (int i = 0; i < MR; i++) {
+    const uint32_t b = g + i * RG;
+    rv[i] = b < gridDim.x ? ld_q_dev(sk.partials + (uint64_t)S::NQ * b + q) : qm31_zero();
+  }
   qacc col;
   col.zero();
-  if (g < RG)
-    for (uint32_t b = g; b < gridDim.x; b += RG) col.add(ld_q_dev(sk.partials + (uint64_t)S::NQ * b + q));
+#pragma unroll
+  for (int i = 0; i < MR; i++) col.add(rv[i]);
   __shared__ qm31 tot[kBlock];
   tot[threadIdx.x] = col.reduce();
   __syncthreads();
@@ -443,6 +463,8 @@ struct EqPartsArg {
   uint32_t off[kEqPartsMax];
 };
 __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out) {
+  __shared__ PointLds sp;
+  stage_point(a.z, &sp);
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   int t = 0;
@@ -450,7 +472,7 @@ __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out)
   const uint32_t x = i - a.off[t];
   const int s = a.s[t], m = a.m[t];
   qm31 acc = qm31_one();
-  for (int l = 0; l < m; l++) acc = qm31_mul(acc, ((x >> (m - 1 - l)) & 1u) ? a.z.r[s + l] : a.z.omr[s + l]);
+  for (int l = 0; l < m; l++) acc = qm31_mul(acc, ((x >> (m - 1 - l)) & 1u) ? sp.r[s + l] : sp.omr[s + l]);
   out[i] = acc;
 }
 
@@ -458,21 +480,42 @@ __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out)
 // out[x] = prod_l (bit_l(x) ? r_l : 1 - r_l), with r_0 on the most
 // significant bit of x (components/matmul.rs:342-355, gkr/prover.rs:9201-9233).
 __global__ void k_eq_direct(PointArg pt, uint64_t count, qm31* __restrict__ out) {
+  __shared__ PointLds sp;
+  stage_point(pt, &sp);
   uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (x >= count) return;
   qm31 acc = qm31_one();
   const int n = pt.n;
   for (int l = 0; l < n; l++) {
     const uint64_t bit = (x >> (n - 1 - l)) & 1ull;
-    acc = qm31_mul(acc, bit ? pt.r[l] : pt.omr[l]);
+    acc = qm31_mul(acc, bit ? sp.r[l] : sp.omr[l]);
   }
   st_q(out, x, acc);
 }
+// Balanced base-256 digits of a canonical M31 value: centered to
+// v in (-P/2, P/2], v = sum_q d_q 256^q with d_q in [-128, 127].
+__device__ __forceinline__ int32_t m31_centered(uint32_t x) {
+  return x > (P >> 1) ? (int32_t)x - (int32_t)P : (int32_t)x;
+}
+__device__ __forceinline__ void m31_digits(uint32_t x, int32_t (&d)[4]) {
+  int32_t v = m31_centered(x);
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    d[q] = (int32_t)(int8_t)(v & 0xff);
+    v = (v - d[q]) >> 8;  // exact
+  }
+}
+
 // Both Lagrange tables of a matmul restriction in one launch: out1[x] over
 // coordinates [0, n1) of pt (count1 entries), out2[x] over [n1, pt.n)
-// (count2 entries), one thread per entry.
+// (count2 entries), one thread per entry.  With ldig, the second table is
+// also written as digits for the int8 weight-side restriction: for column x,
+// byte x % 4 of word 16 (x / 4) + 4 c + q holds digit q of component c (so
+// one word carries a digit of four consecutive columns, a v_dot4 operand).
 __global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, qm31* __restrict__ out1,
-                         qm31* __restrict__ out2) {
+                         qm31* __restrict__ out2, uint8_t* __restrict__ ldig) {
+  __shared__ PointLds sp;
+  stage_point(pt, &sp);
   uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   int s = 0, n = n1;
   qm31* out = out1;
@@ -484,24 +527,37 @@ __global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, 
     out = out2;
   }
   qm31 acc = qm31_one();
-  for (int l = 0; l < n; l++) acc = qm31_mul(acc, ((x >> (n - 1 - l)) & 1ull) ? pt.r[s + l] : pt.omr[s + l]);
+  for (int l = 0; l < n; l++) acc = qm31_mul(acc, ((x >> (n - 1 - l)) & 1ull) ? sp.r[s + l] : sp.omr[s + l]);
   st_q(out, x, acc);
+  if (ldig && out == out2) {
+    const uint32_t comp[4] = {acc.a, acc.b, acc.c, acc.d};
+    uint8_t* base = ldig + (x >> 2) * 64 + (x & 3);
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      int32_t d[4];
+      m31_digits(comp[c], d);
+#pragma unroll
+      for (int q = 0; q < 4; q++) base[(4 * c + q) * 4] = (uint8_t)d[q];
+    }
+  }
 }
 // Split construction: hi table over variables [0, n-h), lo over [n-h, n).
 __global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __restrict__ lo) {
+  __shared__ PointLds sp;
+  stage_point(pt, &sp);
   const uint64_t n_hi = 1ull << (pt.n - h), n_lo = 1ull << h;
   uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (x < n_hi) {
     const int nv = pt.n - h;
     qm31 acc = qm31_one();
-    for (int l = 0; l < nv; l++) acc = qm31_mul(acc, ((x >> (nv - 1 - l)) & 1ull) ? pt.r[l] : pt.omr[l]);
+    for (int l = 0; l < nv; l++) acc = qm31_mul(acc, ((x >> (nv - 1 - l)) & 1ull) ? sp.r[l] : sp.omr[l]);
     st_q(hi, x, acc);
   } else if (x < n_hi + n_lo) {
     const uint64_t y = x - n_hi;
     qm31 acc = qm31_one();
     for (int l = 0; l < h; l++) {
       const int v = pt.n - h + l;
-      acc = qm31_mul(acc, ((y >> (h - 1 - l)) & 1ull) ? pt.r[v] : pt.omr[v]);
+      acc = qm31_mul(acc, ((y >> (h - 1 - l)) & 1ull) ? sp.r[v] : sp.omr[v]);
     }
     st_q(lo, y, acc);
   }
@@ -514,46 +570,6 @@ __global__ void k_eq_combine(const qm31* __restrict__ hi, const qm31* __restrict
 }
 
 // ------------------------------------------------------------------ restriction
-// Activation side: f_a[j] = sum_{i<m} A[i][j] * L[i] for j < k, 0 for k <= j < pk.
-// One thread per column; consecutive threads read consecutive words of a row.
-__device__ __forceinline__ void restrict_rows_col(const uint32_t* __restrict__ A, uint64_t m, uint64_t k, uint64_t pk,
-                                                  const qm31* __restrict__ L, qm31* __restrict__ out, uint64_t j) {
-  if (j >= pk) return;
-  if (j >= k) {
-    st_q(out, j, qm31_zero());
-    return;
-  }
-  // Per component keep lo/hi halves of 4-product partial sums:
-  // 4 * (P-1)^2 < 2^64, and 2^32 == 2 (mod P).
-  uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
-  uint64_t i = 0;
-  for (; i + 4 <= m; i += 4) {
-    uint64_t t[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const uint64_t v = A[(i + u) * k + j];
-      const qm31 l = ld_q(L, i + u);
-      t[0] += v * l.a; t[1] += v * l.b; t[2] += v * l.c; t[3] += v * l.d;
-    }
-#pragma unroll
-    for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
-  }
-  for (; i < m; i++) {
-    const uint64_t v = A[i * k + j];
-    const qm31 l = ld_q(L, i);
-    const uint64_t t[4] = {v * l.a, v * l.b, v * l.c, v * l.d};
-#pragma unroll
-    for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
-  }
-  uint32_t r[4];
-#pragma unroll
-  for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
-  st_q(out, j, qm31{r[0], r[1], r[2], r[3]});
-}
-__global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint64_t k, uint64_t pk,
-                                const qm31* __restrict__ L, qm31* __restrict__ out) {
-  restrict_rows_col(A, m, k, pk, L, out, (uint64_t)blockIdx.x * blockDim.x + threadIdx.x);
-}
 
 // Weight side: f_b[i] = sum_{j<n} B[i][j] * L[j] for i < k, 0 for k <= i < pk.
 // Grid (row blocks of kColWaves * kColRows rows) x (column chunks).  Each
@@ -571,6 +587,10 @@ __global__ void k_restrict_rows(const uint32_t* __restrict__ A, uint64_t m, uint
 // a 16-value reduction of ~40 instructions instead of a shuffle butterfly.
 constexpr int kColRows = 4;
 constexpr int kColWaves = kBlock / 64;
+#ifndef GKR_R8_DEPTH
+#define GKR_R8_DEPTH 8
+#endif
+constexpr int kR8Depth = GKR_R8_DEPTH;  // k_restrict_cols8: steps of weights in flight per wave (even)
 
 __device__ __forceinline__ void acc_row4(uint64_t (&lo)[4], uint64_t (&hi)[4], const uint32_t (&v)[4],
                                          const qm31 (&l)[4]) {
@@ -600,29 +620,67 @@ __device__ __forceinline__ void load_row4(const uint32_t* __restrict__ row, uint
 }
 
 // The activation-side restriction of the same matmul rides along: when
-// act.A is set, the grid has one extra column-chunk slice (the first, so it
-// is dispatched alongside the weight side's first workgroups) whose
-// workgroups compute f_a (one column per thread, restrict_rows_col) instead,
-// so both restrictions run in one launch (the host checks
-// gridDim.x * kBlock >= pk).
+// act.A is set, the first act_blocks workgroups of the (one-dimensional)
+// grid compute f_a (64 columns each, restrict_rows_block; dispatched first,
+// alongside the weight side's first workgroups) and the remaining
+// row_blocks * chunks workgroups the weight side, so both restrictions run
+// in one launch (the host checks act_blocks * 64 >= pk).
 struct RowsJob {
   const uint32_t* A;
   uint64_t m, k, pk;
   const qm31* L;
   qm31* out;
 };
+// Activation side within the fused restriction: a workgroup takes 64
+// consecutive columns; wave w adds the rows i = w, w + kColWaves, ... (each
+// row read is 64 consecutive words), and the waves' sums meet in LDS.
+__device__ __forceinline__ void restrict_rows_block(const RowsJob& act, uint64_t col0, qm31 (*part)[64]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t j = col0 + lane;
+  uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+  if (j < act.k) {
+    for (uint64_t i = wave; i < act.m; i += 4 * kColWaves) {
+      uint64_t t[4] = {0, 0, 0, 0};  // up to 4 rows: 4 * (P-1)^2 < 2^64
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const uint64_t iu = i + (uint64_t)u * kColWaves;
+        if (iu < act.m) {
+          const uint64_t v = act.A[iu * act.k + j];
+          const qm31 l = ld_q(act.L, iu);
+          t[0] += v * l.a; t[1] += v * l.b; t[2] += v * l.c; t[3] += v * l.d;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+    }
+  }
+  uint32_t r[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
+  part[wave][lane] = qm31{r[0], r[1], r[2], r[3]};
+  __syncthreads();
+  if (wave == 0 && j < act.pk) {
+    qm31 sum = part[0][lane];
+#pragma unroll
+    for (int w = 1; w < kColWaves; w++) sum = qm31_add(sum, part[w][lane]);
+    st_q(act.out, j, sum);  // columns k <= j < pk: zero padding (no rows added)
+  }
+}
+
 template <bool kVec4>
 __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
                                                           uint64_t chunk, const qm31* __restrict__ L,
-                                                          uint32_t* __restrict__ partial, RowsJob act) {
-  if (act.A && blockIdx.y == 0) {
-    restrict_rows_col(act.A, act.m, act.k, act.pk, act.L, act.out, (uint64_t)blockIdx.x * blockDim.x + threadIdx.x);
+                                                          uint32_t* __restrict__ partial, RowsJob act,
+                                                          uint32_t act_blocks, uint32_t row_blocks) {
+  __shared__ uint32_t sh[kColWaves][64][17];  // epilogue transpose, one region per wave
+  if (blockIdx.x < act_blocks) {
+    restrict_rows_block(act, (uint64_t)blockIdx.x * 64, reinterpret_cast<qm31(*)[64]>(&sh[0][0][0]));
     return;
   }
-  const uint32_t chunk_id = blockIdx.y - (act.A ? 1 : 0);
-  __shared__ uint32_t sh[kColWaves][64][17];  // epilogue transpose, one region per wave
+  const uint32_t wb = blockIdx.x - act_blocks;
+  const uint32_t row_block = wb % row_blocks, chunk_id = wb / row_blocks;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t row0 = ((uint64_t)blockIdx.x * kColWaves + wave) * kColRows;
+  const uint64_t row0 = ((uint64_t)row_block * kColWaves + wave) * kColRows;
   if (row0 >= k) return;  // whole wave leaves; no workgroup barrier follows
   const int nrows = (int)((k - row0) < (uint64_t)kColRows ? (k - row0) : (uint64_t)kColRows);
   const uint64_t c0 = (uint64_t)chunk_id * chunk;
@@ -687,6 +745,146 @@ __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __rest
     if (r < nrows) partial[((uint64_t)chunk_id * k + row0 + r) * 4 + c] = w;
   }
 }
+// ------------------------------------------------------------------ int8 weights
+// A weight whose entries are all int8-range (centered |v| <= 127: the
+// configs' weights) keeps a row-major int8 copy, rows padded to a multiple of
+// 16 bytes (zeros), built once.  The weight-side restriction then streams one
+// byte per entry: with L_j's components in balanced base-256 digits,
+//   sum_j B[i][j] L_j.c = sum_q 256^q sum_j B[i][j] d_q(L_j.c),
+// and each inner sum is v_dot4_i32_i8 over four columns (|B d| <= 127 * 128,
+// so an int32 lane holds the sum of any chunk below 2^17 columns).
+__global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
+                                                    uint64_t stride, uint32_t* __restrict__ out,
+                                                    uint32_t* __restrict__ bad) {
+  const uint64_t wpr = stride / 4, words = k * wpr;
+  uint32_t any = 0;
+  for (uint64_t w = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; w < words;
+       w += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t i = w / wpr, j0 = (w - i * wpr) * 4;
+    uint32_t packed = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int32_t v = j0 + u < n ? m31_centered(B[i * n + j0 + u]) : 0;
+      any |= (v < -127 || v > 127) ? 1u : 0u;
+      packed |= ((uint32_t)v & 0xffu) << (8 * u);
+    }
+    out[w] = packed;
+  }
+  __shared__ uint32_t sh_any;
+  if (threadIdx.x == 0) sh_any = 0;
+  __syncthreads();
+  if (any) sh_any = 1;  // benign race: any writer stores 1
+  __syncthreads();
+  if (threadIdx.x == 0 && sh_any) atomicOr(bad, 1u);
+}
+
+// Same grid and partition as k_restrict_cols (activation side first, then
+// row blocks x column chunks), with R rows per wave (4 * R per row block);
+// each wave owns R rows and sweeps its
+// chunk 256 columns a step, 4 per lane: one 32-bit word of int8 weights per
+// row and the 16 digit words of L for those 4 columns (shared by the rows),
+// then 16 v_dot4 per row.
+// Per lane and row the 16 sums recombine to the 4 components
+// (sum_q 256^q acc_q, reduced once), and the wave reduction and partial rows
+// are those of k_restrict_cols.
+template <int R>
+__global__ void __launch_bounds__(kBlock) k_restrict_cols8(const int8_t* __restrict__ B8, uint64_t stride, uint64_t k,
+                                                           uint64_t n, uint64_t chunk,
+                                                           const uint32_t* __restrict__ ldig,
+                                                           uint32_t* __restrict__ partial, RowsJob act,
+                                                           uint32_t act_blocks, uint32_t row_blocks) {
+  __shared__ uint32_t sh[kColWaves][64][17];  // epilogue transpose, one region per wave
+  if (blockIdx.x < act_blocks) {
+    restrict_rows_block(act, (uint64_t)blockIdx.x * 64, reinterpret_cast<qm31(*)[64]>(&sh[0][0][0]));
+    return;
+  }
+  const uint32_t wb = blockIdx.x - act_blocks;
+  const uint32_t row_block = wb % row_blocks, chunk_id = wb / row_blocks;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t row0 = ((uint64_t)row_block * kColWaves + wave) * R;
+  if (row0 >= k) return;  // whole wave leaves; no workgroup barrier follows
+  const int nrows = (int)((k - row0) < (uint64_t)R ? (k - row0) : (uint64_t)R);
+  const uint64_t c0 = (uint64_t)chunk_id * chunk;
+  const uint64_t c1 = (c0 + chunk < n) ? c0 + chunk : n;
+  const uint32_t* rows[R];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    rows[r] = reinterpret_cast<const uint32_t*>(B8 + (row0 + (r < nrows ? r : 0)) * stride);
+  int32_t acc[R][16];
+#pragma unroll
+  for (int r = 0; r < R; r++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[r][i] = 0;
+  constexpr uint64_t kStep = 64 * 4;
+  // At one byte per weight a step moves little, so the weights of the next
+  // kR8Depth steps are kept in flight (a register ring, indices fixed by
+  // unrolling); the L digit words (L1-resident, shared by the workgroup's
+  // waves) are double-buffered one step ahead.
+  constexpr int D = kR8Depth;
+  const uint64_t jb = c0 + (uint64_t)lane * 4;
+  const int nsteps = jb < c1 ? (int)((c1 - jb + kStep - 1) / kStep) : 0;
+  uint32_t w[D][R];
+  u32x4 l[2][4];
+  auto load_w = [&](int st, uint32_t (&dst)[R]) {
+    const uint64_t word = (jb + (uint64_t)st * kStep) >> 2;
+#pragma unroll
+    for (int r = 0; r < R; r++) dst[r] = __builtin_nontemporal_load(rows[r] + word);
+  };
+  auto load_l = [&](int st, u32x4 (&dst)[4]) {
+    const u32x4* lp = reinterpret_cast<const u32x4*>(ldig) + ((jb + (uint64_t)st * kStep) >> 2) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; i++) dst[i] = lp[i];
+  };
+#pragma unroll
+  for (int d = 0; d < D; d++)
+    if (d < nsteps) load_w(d, w[d]);
+  if (nsteps > 0) load_l(0, l[0]);
+  for (int s0 = 0; s0 < nsteps; s0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      const int st = s0 + d;
+      if (st < nsteps) {
+        if (st + 1 < nsteps) load_l(st + 1, l[(d + 1) & 1]);
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+          for (int i = 0; i < 16; i++)
+            acc[r][i] = __builtin_amdgcn_sdot4((int)w[d][r], (int)l[d & 1][i >> 2][i & 3], acc[r][i], false);
+        if (st + D < nsteps) load_w(st + D, w[d]);
+      }
+    }
+  }
+  // recombine the digits per (row, component), then the wave reduction of
+  // k_restrict_cols, four rows at a time
+  constexpr uint64_t kOffset = (uint64_t)P << 26;  // > |sum_q 256^q acc_q|, a multiple of P
+  const int vi = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int r0 = 0; r0 < R; r0 += 4) {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int64_t v = (int64_t)acc[r0 + r][4 * c] + ((int64_t)acc[r0 + r][4 * c + 1] << 8) +
+                          ((int64_t)acc[r0 + r][4 * c + 2] << 16) + ((int64_t)acc[r0 + r][4 * c + 3] << 24);
+        sh[wave][lane][4 * r + c] = m31_reduce64((uint64_t)(v + (int64_t)kOffset));
+      }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    uint64_t sum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) sum += sh[wave][g * 16 + i][vi];
+    uint32_t w = m31_reduce64(sum);
+    w = m31_add(w, shfl_xor_u32(w, 16));
+    w = m31_add(w, shfl_xor_u32(w, 32));
+    if (lane < 16) {
+      const int r = r0 + (lane >> 2), c = lane & 3;
+      if (r < nrows) partial[((uint64_t)chunk_id * k + row0 + r) * 4 + c] = w;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  }
+}
+
 // f_b[i] = sum over column chunks of partial[chunk * k + i] for i < k; 0 for k <= i < pk.
 __global__ void k_restrict_cols_finish(const qm31* __restrict__ partial, uint64_t k, uint64_t pk, int nchunks,
                                        qm31* __restrict__ out) {
