@@ -460,6 +460,9 @@ def main():
     ap.add_argument("--no-timing", action="store_true", help="no HIP events and no host timers")
     ap.add_argument("--timing-all", action="store_true",
                     help="HIP events on every timed kernel (default: only the roofline kernel k_restrict_cols)")
+    ap.add_argument("--int8-weights", action="store_true",
+                    help="int8 weight-side restriction (GKR_INT8_WEIGHTS=1): a quarter of the weight bytes, "
+                         "bound by v_dot4 issue rather than HBM")
     ap.add_argument("--driver", default="walk", choices=["walk", "calls"],
                     help="walk: one gkr_prove_walk call per proof; calls: one library call per layer")
     args = ap.parse_args()
@@ -468,6 +471,8 @@ def main():
               "(see the sharding design in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
 
+    if args.int8_weights:
+        os.environ["GKR_INT8_WEIGHTS"] = "1"
     ctx = G.Context(0)
     if args.config == "c2":
         return bench_c2(ctx, args)
@@ -561,6 +566,7 @@ def main():
         "dtype": "u32-m31",
         "data": "synthetic (counter-mode SplitMix64; int8-range weights/activations, uniform-M31 LogUp inputs)",
         "config": {"workload": workload, "layers": n_layers, "tokens": tokens,
+                   "weight_restriction": "int8" if args.int8_weights else "u32",
                    "matmul_elements_per_step": elems, "logup_tables": "2^16 (SiLU, softmax-exp)"},
         "proved_tokens_per_s": round(tokens / (ms_per_step * 1e-3), 3) if tokens else None,
         "roofline": roofline,

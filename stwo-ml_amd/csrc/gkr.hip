@@ -134,8 +134,9 @@ struct gkr_matrix {
   // (gemm.h), built on first use; the contents of a matrix never change
   int8_t* bplanes = nullptr;
   int bnplanes = 0;
-  // row-major int8 copy for the weight-side restriction (rows padded to
-  // r8_stride bytes), built on first use when every entry is int8-range;
+  // int8 copy for the weight-side restriction (rows of kR8Block-byte
+  // blocks in k_restrict_cols8's permuted order, padded to r8_stride bytes),
+  // built on first use when every entry is int8-range;
   // r8_state: 0 not yet checked, 1 copy present, -1 not int8-range
   int8_t* r8 = nullptr;
   uint64_t r8_stride = 0;
@@ -177,6 +178,7 @@ struct gkr_ctx {
   int fb_chunks = 0;
   uint32_t trip_count = 0;         // value of the fused trips' arrival counter (S_TRIPCNT) after the queued launches
   bool trip_count_valid = false;   // false: zero the counter before the next fused trip
+  bool int8_weights = false;       // GKR_INT8_WEIGHTS=1 at creation: int8 weight-side restriction
 };
 
 static int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
@@ -778,6 +780,8 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   HIP_TRY(hipSetDevice(device));
   gkr_ctx* c = new gkr_ctx();
   c->device = device;
+  const char* i8 = getenv("GKR_INT8_WEIGHTS");
+  c->int8_weights = i8 && i8[0] == '1' && i8[1] == 0;
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
     delete c;
     return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");
@@ -943,17 +947,13 @@ static int finish_fb(gkr_ctx* c) {
   return check_launch();
 }
 // The int8 copy of weight B for the restriction (k_to_int8), on first use:
-// one pass over B and a 4-byte read-back of the range flag.
-#ifndef GKR_INT8_WEIGHTS
-#define GKR_INT8_WEIGHTS 1
-#endif
-#ifndef GKR_R8_ROWS
-#define GKR_R8_ROWS 4
-#endif
-constexpr int kR8Rows = GKR_R8_ROWS;  // weight rows per wave in k_restrict_cols8 (4 or 8)
+// one pass over B and a 4-byte read-back of the range flag.  Used only when
+// the context was created with GKR_INT8_WEIGHTS=1 in the environment: the
+// int8 restriction moves a quarter of the bytes but is bound by v_dot4 issue
+// (about 2.8 TB/s of int8 weights on the config shapes), the u32 one by HBM.
 static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
-  if (B->r8_state || !GKR_INT8_WEIGHTS) return GKR_OK;
-  const uint64_t stride = (B->cols + 15) / 16 * 16;
+  if (B->r8_state || !c->int8_weights) return GKR_OK;
+  const uint64_t stride = (B->cols + kR8Block - 1) / kR8Block * kR8Block;
   if (B->rows == 0 || stride == 0 || B->rows * stride > (1ull << 40)) {
     B->r8_state = -1;
     return GKR_OK;
@@ -1045,12 +1045,21 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     if (act_blocks + gr * gc > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
     const dim3 grid((unsigned)(act_blocks + gr * gc));
     if (use8) {
+      // column chunks of kR8ChunkBlocks blocks; passes per wave chosen for
+      // about 512 weight-side workgroups (measured best on the config shapes)
+      const uint64_t nblocks = B->r8_stride / kR8Block;
+      const uint64_t gc8 = (nblocks + kR8ChunkBlocks - 1) / kR8ChunkBlocks;
+      const uint64_t groups = (k + kColWaves * kR8Rows - 1) / (kColWaves * kR8Rows);
+      const int passes = (int)std::max<uint64_t>(1, std::min<uint64_t>(kR8MaxPasses, groups * gc8 / 512));
+      const uint64_t gr8 = (k + (uint64_t)kColWaves * kR8Rows * passes - 1) / ((uint64_t)kColWaves * kR8Rows * passes);
+      if (gc8 > gc) TRY(ensureT(c, S_COLPART, (size_t)gc8 * k, &part));
+      gc = gc8;
+      if (act_blocks + gr8 * gc8 > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
       // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
       TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + 4 * m * k + 16 * m + 16 * pk);
-      const uint64_t gr8 = (k + kR8Rows * kColWaves - 1) / (kR8Rows * kColWaves);
-      const dim3 grid8((unsigned)(act_blocks + gr8 * gc));
-      hipLaunchKernelGGL(k_restrict_cols8<kR8Rows>, grid8, dim3(kBlock), 0, c->stream, B->r8, B->r8_stride, k, n,
-                         chunk, (const uint32_t*)ldig, (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr8);
+      hipLaunchKernelGGL(k_restrict_cols8, dim3((unsigned)(act_blocks + gr8 * gc8)), dim3(kBlock), 0, c->stream,
+                         B->r8, B->r8_stride, k, (const u32x4*)ldig, (n + 3) / 4, passes, (uint32_t*)part, rows,
+                         (uint32_t)act_blocks, (uint32_t)gr8);
       TRY(check_launch());
     } else {
       // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written

@@ -509,9 +509,11 @@ __device__ __forceinline__ void m31_digits(uint32_t x, int32_t (&d)[4]) {
 // Both Lagrange tables of a matmul restriction in one launch: out1[x] over
 // coordinates [0, n1) of pt (count1 entries), out2[x] over [n1, pt.n)
 // (count2 entries), one thread per entry.  With ldig, the second table is
-// also written as digits for the int8 weight-side restriction: for column x,
-// byte x % 4 of word 16 (x / 4) + 4 c + q holds digit q of component c (so
-// one word carries a digit of four consecutive columns, a v_dot4 operand).
+// also written as digits for the int8 weight-side restriction, in four
+// planes (one per component c) of nq = ceil(count2 / 4) 16-byte entries: for
+// column x, byte x % 4 of word q of entry c * nq + x / 4 holds digit q of
+// component c, so one word carries a digit of four consecutive columns (a
+// v_dot4 operand) and a wave reads 64 consecutive entries of a plane.
 __global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, qm31* __restrict__ out1,
                          qm31* __restrict__ out2, uint8_t* __restrict__ ldig) {
   __shared__ PointLds sp;
@@ -531,13 +533,14 @@ __global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, 
   st_q(out, x, acc);
   if (ldig && out == out2) {
     const uint32_t comp[4] = {acc.a, acc.b, acc.c, acc.d};
-    uint8_t* base = ldig + (x >> 2) * 64 + (x & 3);
+    const uint64_t nq = (count2 + 3) >> 2;
 #pragma unroll
     for (int c = 0; c < 4; c++) {
+      uint8_t* base = ldig + ((uint64_t)c * nq + (x >> 2)) * 16 + (x & 3);
       int32_t d[4];
       m31_digits(comp[c], d);
 #pragma unroll
-      for (int q = 0; q < 4; q++) base[(4 * c + q) * 4] = (uint8_t)d[q];
+      for (int q = 0; q < 4; q++) base[q * 4] = (uint8_t)d[q];
     }
   }
 }
@@ -587,10 +590,6 @@ __global__ void k_eq_combine(const qm31* __restrict__ hi, const qm31* __restrict
 // a 16-value reduction of ~40 instructions instead of a shuffle butterfly.
 constexpr int kColRows = 4;
 constexpr int kColWaves = kBlock / 64;
-#ifndef GKR_R8_DEPTH
-#define GKR_R8_DEPTH 8
-#endif
-constexpr int kR8Depth = GKR_R8_DEPTH;  // k_restrict_cols8: steps of weights in flight per wave (even)
 
 __device__ __forceinline__ void acc_row4(uint64_t (&lo)[4], uint64_t (&hi)[4], const uint32_t (&v)[4],
                                          const qm31 (&l)[4]) {
@@ -747,12 +746,24 @@ __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __rest
 }
 // ------------------------------------------------------------------ int8 weights
 // A weight whose entries are all int8-range (centered |v| <= 127: the
-// configs' weights) keeps a row-major int8 copy, rows padded to a multiple of
-// 16 bytes (zeros), built once.  The weight-side restriction then streams one
-// byte per entry: with L_j's components in balanced base-256 digits,
+// configs' weights) keeps an int8 copy, built once, that the weight-side
+// restriction streams at one byte per entry.  With L_j's components in
+// balanced base-256 digits,
 //   sum_j B[i][j] L_j.c = sum_q 256^q sum_j B[i][j] d_q(L_j.c),
-// and each inner sum is v_dot4_i32_i8 over four columns (|B d| <= 127 * 128,
-// so an int32 lane holds the sum of any chunk below 2^17 columns).
+// each inner sum is v_dot4_i32_i8 over four columns; |B d| <= 127 * 128, so
+// an int32 lane holds the sum of any chunk below 2^17 columns.
+//
+// Layout: rows of kR8Block-byte blocks (stride a multiple of kR8Block, zero
+// padded).  Block b of a row holds the 256 four-column groups ("quads")
+// 256 b .. 256 b + 255 permuted so that lane l's 16 bytes at offset 16 l are
+// quads l, l + 64, l + 128, l + 192: one coalesced 16-byte load per lane
+// gives each lane four quads whose L digits sit at consecutive LDS entries
+// across the wave.
+constexpr uint64_t kR8Block = 1024;
+constexpr int kR8Rows = 4;       // rows a wave carries through one pass
+constexpr int kR8ChunkBlocks = 2;  // column chunk: 2 blocks (2048 columns), L digits 32 KB of LDS
+constexpr int kR8MaxPasses = 8;  // row passes per wave
+
 __global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
                                                     uint64_t stride, uint32_t* __restrict__ out,
                                                     uint32_t* __restrict__ bad) {
@@ -760,7 +771,9 @@ __global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __restrict__
   uint32_t any = 0;
   for (uint64_t w = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; w < words;
        w += (uint64_t)gridDim.x * blockDim.x) {
-    const uint64_t i = w / wpr, j0 = (w - i * wpr) * 4;
+    const uint64_t i = w / wpr, wr = w - i * wpr;
+    const uint64_t blk = wr >> 8, l = (wr & 255) >> 2, t = wr & 3;  // word 4 l + t of the block
+    const uint64_t j0 = 4 * (blk * 256 + t * 64 + l);
     uint32_t packed = 0;
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -778,94 +791,86 @@ __global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __restrict__
   if (threadIdx.x == 0 && sh_any) atomicOr(bad, 1u);
 }
 
-// Same grid and partition as k_restrict_cols (activation side first, then
-// row blocks x column chunks), with R rows per wave (4 * R per row block);
-// each wave owns R rows and sweeps its
-// chunk 256 columns a step, 4 per lane: one 32-bit word of int8 weights per
-// row and the 16 digit words of L for those 4 columns (shared by the rows),
-// then 16 v_dot4 per row.
-// Per lane and row the 16 sums recombine to the 4 components
-// (sum_q 256^q acc_q, reduced once), and the wave reduction and partial rows
-// are those of k_restrict_cols.
-template <int R>
+// Weight side of the fused restriction over the int8 copy.  The grid is the
+// activation side's act_blocks workgroups, then row_blocks x chunks
+// workgroups; a workgroup copies its chunk's L digits (4 planes x 512
+// entries) into LDS, and each wave then runs `passes` passes of kR8Rows rows
+// over the chunk's blocks: per block and row one 16-byte weight load (the
+// next block's loads are issued before the current block is multiplied) and
+// 64 v_dot4 against digits read from LDS.  After each pass the 16 digit sums
+// per (row, component) recombine (sum_q 256^q acc_q, reduced once) and the
+// wave reduction of k_restrict_cols leaves one value per (row, component),
+// kept in LDS until the wave writes its partial rows at the end.
 __global__ void __launch_bounds__(kBlock) k_restrict_cols8(const int8_t* __restrict__ B8, uint64_t stride, uint64_t k,
-                                                           uint64_t n, uint64_t chunk,
-                                                           const uint32_t* __restrict__ ldig,
+                                                           const u32x4* __restrict__ ldig, uint64_t nq, int passes,
                                                            uint32_t* __restrict__ partial, RowsJob act,
                                                            uint32_t act_blocks, uint32_t row_blocks) {
+  constexpr int QCH = kR8ChunkBlocks * 256;  // quads per chunk
+  __shared__ u32x4 sl[4][QCH];
   __shared__ uint32_t sh[kColWaves][64][17];  // epilogue transpose, one region per wave
+  __shared__ uint32_t sres[kColWaves][kR8MaxPasses][16];
   if (blockIdx.x < act_blocks) {
     restrict_rows_block(act, (uint64_t)blockIdx.x * 64, reinterpret_cast<qm31(*)[64]>(&sh[0][0][0]));
     return;
   }
   const uint32_t wb = blockIdx.x - act_blocks;
   const uint32_t row_block = wb % row_blocks, chunk_id = wb / row_blocks;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t row0 = ((uint64_t)row_block * kColWaves + wave) * R;
-  if (row0 >= k) return;  // whole wave leaves; no workgroup barrier follows
-  const int nrows = (int)((k - row0) < (uint64_t)R ? (k - row0) : (uint64_t)R);
-  const uint64_t c0 = (uint64_t)chunk_id * chunk;
-  const uint64_t c1 = (c0 + chunk < n) ? c0 + chunk : n;
-  const uint32_t* rows[R];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint64_t q0 = (uint64_t)chunk_id * QCH;
+  const uint64_t nblocks = stride / kR8Block, blk0 = (uint64_t)chunk_id * kR8ChunkBlocks;
+  const int nb = (int)((nblocks - blk0) < (uint64_t)kR8ChunkBlocks ? (nblocks - blk0) : (uint64_t)kR8ChunkBlocks);
+  for (int idx = threadIdx.x; idx < 4 * QCH; idx += kBlock) {
+    const int c = idx / QCH, q = idx - c * QCH;
+    sl[c][q] = (q0 + q < nq) ? ldig[c * nq + q0 + q] : u32x4{0, 0, 0, 0};
+  }
+  __syncthreads();
+  const uint64_t wrow0 = ((uint64_t)row_block * kColWaves + wave) * (uint64_t)(kR8Rows * passes);
+  if (wrow0 >= k) return;  // whole wave leaves; no workgroup barrier follows
+  const uint64_t left = (k - wrow0 + kR8Rows - 1) / kR8Rows;
+  const int npass = (int)(left < (uint64_t)passes ? left : (uint64_t)passes);
+  const int iters = npass * nb;
+  const int8_t* base = B8 + blk0 * kR8Block;
+  const uint32_t loff = 16 * lane;
+  // weights of iteration it (pass it / nb, block it % nb); rows past k re-read row k - 1 (not stored)
+  auto load = [&](int it, u32x4 (&w)[kR8Rows]) {
+    const int pass = it / nb, b = it - pass * nb;
 #pragma unroll
-  for (int r = 0; r < R; r++)
-    rows[r] = reinterpret_cast<const uint32_t*>(B8 + (row0 + (r < nrows ? r : 0)) * stride);
-  int32_t acc[R][16];
+    for (int r = 0; r < kR8Rows; r++) {
+      uint64_t row = wrow0 + (uint64_t)pass * kR8Rows + r;
+      row = row < k ? row : k - 1;
+      w[r] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(base + row * stride + (uint64_t)b * kR8Block + loff));
+    }
+  };
+  int32_t acc[kR8Rows][16];
 #pragma unroll
-  for (int r = 0; r < R; r++)
+  for (int r = 0; r < kR8Rows; r++)
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[r][i] = 0;
-  constexpr uint64_t kStep = 64 * 4;
-  // At one byte per weight a step moves little, so the weights of the next
-  // kR8Depth steps are kept in flight (a register ring, indices fixed by
-  // unrolling); the L digit words (L1-resident, shared by the workgroup's
-  // waves) are double-buffered one step ahead.
-  constexpr int D = kR8Depth;
-  const uint64_t jb = c0 + (uint64_t)lane * 4;
-  const int nsteps = jb < c1 ? (int)((c1 - jb + kStep - 1) / kStep) : 0;
-  uint32_t w[D][R];
-  u32x4 l[2][4];
-  auto load_w = [&](int st, uint32_t (&dst)[R]) {
-    const uint64_t word = (jb + (uint64_t)st * kStep) >> 2;
-#pragma unroll
-    for (int r = 0; r < R; r++) dst[r] = __builtin_nontemporal_load(rows[r] + word);
-  };
-  auto load_l = [&](int st, u32x4 (&dst)[4]) {
-    const u32x4* lp = reinterpret_cast<const u32x4*>(ldig) + ((jb + (uint64_t)st * kStep) >> 2) * 4;
-#pragma unroll
-    for (int i = 0; i < 4; i++) dst[i] = lp[i];
-  };
-#pragma unroll
-  for (int d = 0; d < D; d++)
-    if (d < nsteps) load_w(d, w[d]);
-  if (nsteps > 0) load_l(0, l[0]);
-  for (int s0 = 0; s0 < nsteps; s0 += D) {
-#pragma unroll
-    for (int d = 0; d < D; d++) {
-      const int st = s0 + d;
-      if (st < nsteps) {
-        if (st + 1 < nsteps) load_l(st + 1, l[(d + 1) & 1]);
-#pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-          for (int i = 0; i < 16; i++)
-            acc[r][i] = __builtin_amdgcn_sdot4((int)w[d][r], (int)l[d & 1][i >> 2][i & 3], acc[r][i], false);
-        if (st + D < nsteps) load_w(st + D, w[d]);
-      }
-    }
-  }
-  // recombine the digits per (row, component), then the wave reduction of
-  // k_restrict_cols, four rows at a time
   constexpr uint64_t kOffset = (uint64_t)P << 26;  // > |sum_q 256^q acc_q|, a multiple of P
   const int vi = lane & 15, g = lane >> 4;
+  auto step = [&](int it, const u32x4 (&w)[kR8Rows]) {
+    const int pass = it / nb, b = it - pass * nb;
 #pragma unroll
-  for (int r0 = 0; r0 < R; r0 += 4) {
+    for (int t = 0; t < 4; t++) {
+      u32x4 l[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+      for (int c = 0; c < 4; c++) l[c] = sl[c][b * 256 + t * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < kR8Rows; r++)
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+          acc[r][i] = __builtin_amdgcn_sdot4((int)w[r][t], (int)l[i >> 2][i & 3], acc[r][i], false);
+    }
+    if (b != nb - 1) return;
+    // end of a pass: lane l adds value (l & 15) over the 16 lanes of group (l >> 4),
+    // two shuffles add the four groups, lanes 0-15 hold the (row, component) totals
+#pragma unroll
+    for (int r = 0; r < kR8Rows; r++)
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        const int64_t v = (int64_t)acc[r0 + r][4 * c] + ((int64_t)acc[r0 + r][4 * c + 1] << 8) +
-                          ((int64_t)acc[r0 + r][4 * c + 2] << 16) + ((int64_t)acc[r0 + r][4 * c + 3] << 24);
+        const int64_t v = (int64_t)acc[r][4 * c] + ((int64_t)acc[r][4 * c + 1] << 8) +
+                          ((int64_t)acc[r][4 * c + 2] << 16) + ((int64_t)acc[r][4 * c + 3] << 24);
         sh[wave][lane][4 * r + c] = m31_reduce64((uint64_t)(v + (int64_t)kOffset));
       }
     __builtin_amdgcn_wave_barrier();
@@ -873,15 +878,34 @@ __global__ void __launch_bounds__(kBlock) k_restrict_cols8(const int8_t* __restr
     uint64_t sum = 0;
 #pragma unroll
     for (int i = 0; i < 16; i++) sum += sh[wave][g * 16 + i][vi];
-    uint32_t w = m31_reduce64(sum);
-    w = m31_add(w, shfl_xor_u32(w, 16));
-    w = m31_add(w, shfl_xor_u32(w, 32));
-    if (lane < 16) {
-      const int r = r0 + (lane >> 2), c = lane & 3;
-      if (r < nrows) partial[((uint64_t)chunk_id * k + row0 + r) * 4 + c] = w;
-    }
+    uint32_t x = m31_reduce64(sum);
+    x = m31_add(x, shfl_xor_u32(x, 16));
+    x = m31_add(x, shfl_xor_u32(x, 32));
+    if (lane < 16) sres[wave][pass][lane] = x;
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int r = 0; r < kR8Rows; r++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc[r][i] = 0;
+  };
+  // two weight register sets alternate, so a block's loads are in flight
+  // while the previous block is multiplied (the last load repeats a valid block)
+  u32x4 wa[kR8Rows], wb2[kR8Rows];
+  load(0, wa);
+  for (int it = 0; it < iters; it += 2) {
+    load(it + 1 < iters ? it + 1 : iters - 1, wb2);
+    step(it, wa);
+    if (it + 1 >= iters) break;
+    load(it + 2 < iters ? it + 2 : iters - 1, wa);
+    step(it + 1, wb2);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  for (int e = lane; e < npass * 16; e += 64) {
+    const int pass = e >> 4, rc = e & 15;
+    const uint64_t row = wrow0 + (uint64_t)pass * kR8Rows + (rc >> 2);
+    if (row < k) partial[((uint64_t)chunk_id * k + row) * 4 + (rc & 3)] = sres[wave][pass][rc];
   }
 }
 

@@ -5,6 +5,7 @@ seeded inputs; the Qwen2.5-14B up-projection shape is checked through
 size-independent properties (verifier replay, final evaluations equal the
 MLEs of A and B at the challenge point).
 """
+import os
 import random
 import sys
 
@@ -112,11 +113,47 @@ def test_matmul_layer_random_shapes(gpu_ctx, m, k, n):
     _compare_layer(gpu_ctx, A, B, m + k + n, "random")
 
 
+@pytest.fixture(scope="module")
+def int8_ctx():
+    """A context created with GKR_INT8_WEIGHTS=1: int8-range weights take the int8 restriction."""
+    old = os.environ.get("GKR_INT8_WEIGHTS")
+    os.environ["GKR_INT8_WEIGHTS"] = "1"
+    try:
+        ctx = G.Context(0)
+    finally:
+        if old is None:
+            del os.environ["GKR_INT8_WEIGHTS"]
+        else:
+            os.environ["GKR_INT8_WEIGHTS"] = old
+    yield ctx
+    ctx.close()
+
+
 @pytest.mark.parametrize("m,k,n", [(1, 576, 576), (1, 1536, 576), (64, 512, 1024)])
 def test_matmul_layer_int8_range(gpu_ctx, m, k, n):
     A = O.synthetic(m, k, 1, 11)
     B = O.synthetic(k, n, 1, 12)
     _compare_layer(gpu_ctx, A, B, 3, "int8")
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 576, 576), (1, 1536, 576), (64, 512, 1024), (3, 700, 3000), (2, 33, 5),
+                                   (5, 4100, 2048), (1, 16, 9000)])
+def test_matmul_layer_int8_weight_path(int8_ctx, m, k, n):
+    """The int8 weight copy (permuted blocks, digit planes, LDS-staged v_dot4 restriction) gives the
+    same proof as the oracle, including ragged rows, partial blocks and chunks."""
+    A = O.synthetic(m, k, 1, 21)
+    B = O.synthetic(k, n, 1, 22)
+    _compare_layer(int8_ctx, A, B, 5, "int8 path")
+
+
+@pytest.mark.parametrize("m,k,n", [(2, 40, 70), (4, 300, 1100)])
+def test_int8_context_full_range_weights(int8_ctx, m, k, n):
+    """Weights outside the int8 range fall back to the u32 restriction under an int8 context."""
+    rng = np.random.default_rng(m + k + n)
+    A = rng.integers(0, P, size=(m, k), dtype=np.uint32)
+    B = rng.integers(0, P, size=(k, n), dtype=np.uint32)
+    B[0, 0] = 200  # out of int8 range even if the rest were small
+    _compare_layer(int8_ctx, A, B, 7, "int8 ctx, full range")
 
 
 def test_boundary_values(gpu_ctx):
@@ -320,11 +357,13 @@ def test_native_walk_errors(gpu_ctx):
         G.prove_walk(gpu_ctx, G.PoseidonChannel(), [(7, G.CLAIM_FRESH, a, b, 0, 0)], G.Proof())
 
 
-def test_qwen_up_projection_properties(gpu_ctx):
+@pytest.mark.parametrize("path", ["u32", "int8"])
+def test_qwen_up_projection_properties(gpu_ctx, int8_ctx, path):
     """Qwen2.5-14B MLP up projection (64 x 5120 . 5120 x 13824, int8-range): verifier replay and
     final evaluations equal MLE_A / MLE_B^T at the challenge point (oracle on the CPU)."""
+    gpu_ctx = int8_ctx if path == "int8" else gpu_ctx
     m, k, n = 64, 5120, 13824
-    log("case qwen up 64x5120x13824")
+    log("case qwen up 64x5120x13824 " + path)
     a = gpu_ctx.synthetic(m, k, 1, 101)
     b = gpu_ctx.synthetic(k, n, 1, 102)
     ch = G.PoseidonChannel()
