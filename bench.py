@@ -370,16 +370,21 @@ def bench_forward(ctx, args):
     ctx.close()
 
 
-def trip_plan(T, host_len=128, k0=3, big=1 << 16):
+def trip_k(n, big=1 << 16, huge=1 << 20):
+    """Rounds per device trip over a vector of n entries (the library's trip_k)."""
+    return 1 if n > huge else 2 if n > big else 3
+
+
+def trip_plan(T, host_len=128):
     """(first round, rounds, vector length) of the device trips of a product sumcheck over 2^T entries
-    (the library's plan_trips: up to 3 rounds per launch, 2 on vectors longer than 2^16)."""
+    (the library's plan_trips with the first trip of trip_k(2^T) rounds)."""
     if T <= 0:
         return []
-    t = min(k0, T)
+    t = min(trip_k(1 << T), T)
     out = [(0, t, 1 << T)]
     while t < T and (1 << (T - t)) > host_len:
         n = 1 << (T - t)
-        k = min(2 if n > big else 3, T - t)
+        k = min(trip_k(n), T - t)
         out.append((t, k, n))
         t += k
     return out

@@ -429,8 +429,9 @@ struct HandoverSession {
 // each (k_trip: one launch plus the finisher per trip), then k_handover
 // folds the last trip's vectors and the host finishes the rounds on vectors
 // of at most host_len entries.  The first trip covers min(k0, T) rounds;
-// trips on vectors longer than kTripBig cover 2 rounds (their sums cost 2^K
-// products per entry), shorter ones 3.  The loop ends once the next trip's
+// later trips cover trip_k(n) rounds: a trip's sums cost 2^K products per
+// entry, so trips over long vectors (bound by HBM and VALU, not by launch
+// latency) take fewer rounds each.  The loop ends once the next trip's
 // vectors would fit the host, so the last trip's vectors have at most
 // host_len * 2^K <= kHandMax entries (host_len <= 256).
 struct Trip {
@@ -441,10 +442,22 @@ struct Trip {
 #define GKR_TRIP_BIG (1ull << 16)
 #endif
 constexpr uint64_t kTripBig = GKR_TRIP_BIG;
+#ifndef GKR_TRIP_HUGE
+#define GKR_TRIP_HUGE (1ull << 20)
+#endif
+constexpr uint64_t kTripHuge = GKR_TRIP_HUGE;
+// Rounds per trip over a vector of n entries: 3 up to kTripBig, 2 up to kTripHuge, then 1.
+static inline int trip_k(uint64_t n) { return n > kTripHuge ? 1 : n > kTripBig ? 2 : 3; }
 #ifndef GKR_TRIP_MAX_BLOCKS
 #define GKR_TRIP_MAX_BLOCKS 512
 #endif
 constexpr unsigned kTripMaxBlocks = GKR_TRIP_MAX_BLOCKS;  // partial rows per trip (the finisher adds them)
+#ifndef GKR_TRIP_MAX_BLOCKS_SHORT
+#define GKR_TRIP_MAX_BLOCKS_SHORT 1024
+#endif
+constexpr unsigned kTripMaxBlocksShort = GKR_TRIP_MAX_BLOCKS_SHORT;  // the same for trips of at most 2 rounds
+static_assert(GKR_TRIP_MAX_BLOCKS_SHORT <= kMaxPartialBlocks && GKR_TRIP_MAX_BLOCKS <= kMaxPartialBlocks,
+              "trip partial rows exceed the partial buffer");
 // Trips whose one-entry-per-thread grid is at most kTripFusedGrid workgroups
 // run on at most kTripFusedMax workgroups and finish in the kernel itself.
 #ifndef GKR_TRIP_FUSED
@@ -461,7 +474,7 @@ static std::vector<Trip> plan_trips(int T, uint64_t host_len, int k0) {
   v.push_back({0, t, 1ull << T});
   while (t < T && (1ull << (T - t)) > host_len) {
     const uint64_t n = 1ull << (T - t);
-    int k = n > kTripBig ? 2 : 3;
+    int k = trip_k(n);
     if (k > T - t) k = T - t;
     v.push_back({t, k, n});
     t += k;
@@ -581,7 +594,8 @@ static int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* 
   for (int i = 0; i < np; i++) al.c[i] = pend[i];
   TRY(make_sink(c, sk, slot));
   unsigned grid = partial_grid(n);  // one entry per thread up to kTripMaxBlocks workgroups
-  if (grid > kTripMaxBlocks) grid = kTripMaxBlocks;
+  const unsigned max_blocks = K <= 2 ? kTripMaxBlocksShort : kTripMaxBlocks;
+  if (grid > max_blocks) grid = max_blocks;
   if (GKR_TRIP_FUSED && grid <= kTripFusedGrid) grid = grid < kTripFusedMax ? grid : kTripFusedMax;
   const int nvec = kind == 2 ? 1 : 2;
   TimedLaunch tl(c, kind == 0 ? K_MM_ROUND : K_EQ3_ROUND,
@@ -1087,7 +1101,7 @@ static int first_product_trip(gkr_ctx* c, uint64_t pk, int* K, qm31* g) {
   TRY(ensureT(c, S_FA0, pk, &fa));
   TRY(ensureT(c, S_FB0, pk, &fb));
   const int T = log2_exact(pk);
-  *K = T < kTripMaxK ? T : kTripMaxK;
+  *K = T < trip_k(pk) ? T : trip_k(pk);
   RoundSink sk;
   if (c->fb_pending) {  // add the chunk partials on the fly and store f_b
     TRY(launch_trip(c, 0, *K, fa, (const qm31*)c->buf[S_COLPART], pk, 0, nullptr, nullptr, fb, nullptr, nullptr, 0,
@@ -1175,7 +1189,7 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
                             gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b) {
   const qm31 inv2 = qm31_from_m31(1u << 30);  // 2^-1 mod P
   const uint64_t pk = 1ull << T;
-  const std::vector<Trip> trips = plan_trips(T, kHostTailMM, g0 ? k0 : kTripMaxK);
+  const std::vector<Trip> trips = plan_trips(T, kHostTailMM, g0 ? k0 : trip_k(1ull << T));
   std::vector<qm31> chal(T);
   auto absorb = [&](int t, const qm31* sums) {
     const qm31 c0 = sums[0];
@@ -1624,7 +1638,7 @@ struct Eq3Plan {
 // launch the kernel that builds their eq tables (S_EQPARTS).
 static int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
   pl->nv = nv;
-  pl->trips = plan_trips(nv, kHostTailEq3, (1ull << nv) > kTripBig ? 2 : kTripMaxK);
+  pl->trips = plan_trips(nv, kHostTailEq3, trip_k(1ull << nv));
   pl->hi_off.clear();
   pl->lo_off.clear();
   pl->h.clear();
