@@ -551,7 +551,7 @@ def main():
     if rc:
         ms, nl, nb = ctx.kernel_time(K_RESTRICT_COLS)
         ach = nb / (ms * 1e-3) / 1e9
-        traffic = measured_traffic() if cfg is QWEN else None
+        traffic = measured_traffic() if cfg is QWEN and not args.int8_weights else None  # u32 restriction
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_restrict_cols",
                     "avg_launch_us": rc["avg_us"], "bytes_per_launch": nb // nl,

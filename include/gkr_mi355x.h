@@ -86,10 +86,15 @@ int gkr_channel_import(gkr_channel* ch, const uint32_t state[11]);
 /* ------------------------------------------------------------------ device context */
 typedef struct gkr_ctx gkr_ctx;
 int gkr_ctx_create(int device, gkr_ctx** out);  /* replaces GpuSumcheckExecutor::new/cached, gpu_sumcheck.rs:1309-1380 */
+/* With GKR_INT8_WEIGHTS=1 in the environment when the context is created, a
+ * weight matrix whose entries are all int8-range gets an int8 copy on first
+ * use and the weight-side restriction reads that copy (one byte per weight,
+ * v_dot4 digit sums); otherwise the u32 matrix is read.  Proofs are identical. */
 void gkr_ctx_destroy(gkr_ctx* ctx);
 int gkr_ctx_synchronize(gkr_ctx* ctx);
 /* Per-kernel timing (HIP events on the context stream), for benchmarks.
- * ids: 0 restrict_cols, 1 restrict_rows, 2 product-sumcheck trip (several
+ * ids: 0 restrict_cols (weight and activation side of a matmul in one
+ * launch), 1 unused, 2 product-sumcheck trip (several
  * rounds per launch), 3 eq-sumcheck or degree-1 trip, 4 logup prepare, 5 eq
  * tables (device kernels: one event pair per launch); 6 host Fiat-Shamir
  * inside the reducers, 7 host wait for results of device kernels, 8 host wait
