@@ -336,10 +336,11 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
     if (g < step) tot[threadIdx.x] = qm31_add(tot[threadIdx.x], tot[threadIdx.x + step * S::NQ]);
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    for (int i = 0; i < S::NQ; i++) sk.out[i] = tot[i];
-    publish_flag(sk.flag, sk.seq);
-  }
+  // the NQ results go out in one store instruction of wave 0, then the flag
+  // (its system-scope release follows the barrier, so it covers every lane's store)
+  if (threadIdx.x < S::NQ) sk.out[threadIdx.x] = tot[threadIdx.x];
+  __syncthreads();
+  if (threadIdx.x == 0) publish_flag(sk.flag, sk.seq);
 }
 
 // Adds nblocks partial rows of NQ values and delivers them like k_finish.
@@ -371,10 +372,9 @@ __global__ void __launch_bounds__(kFinishBlock) k_finish_wide(RoundSink sk, uint
     if (g < step) sh[threadIdx.x] = qm31_add(sh[threadIdx.x], sh[threadIdx.x + step * NQ]);
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    for (int i = 0; i < NQ; i++) sk.out[i] = sh[i];
-    publish_flag(sk.flag, sk.seq);
-  }
+  if (threadIdx.x < NQ) sk.out[threadIdx.x] = sh[threadIdx.x];
+  __syncthreads();
+  if (threadIdx.x == 0) publish_flag(sk.flag, sk.seq);
 }
 
 // ------------------------------------------------------------------ hand-over to the host
@@ -444,7 +444,8 @@ __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a,
   for (uint32_t i = threadIdx.x; i < l; i += blockDim.x)
 #pragma unroll
     for (int j = 0; j < NV; j++) vec_out[(uint64_t)j * l + i] = v[j][i];
-  __threadfence_system();
+  // the barrier orders every thread's stores before thread 0's system-scope
+  // release of the flag, which writes the L2 back to host memory for all of them
   __syncthreads();
   if (threadIdx.x == 0) publish_flag(flag, seq);
 }
