@@ -189,6 +189,28 @@ struct TripChal {
   qm31 c[kTripMaxK];
 };
 
+// t + (t of lane l ^ m), for every lane.  m = 8: DPP row rotation by 8 (the
+// other half of the 16-lane row); m = 16 / 32: the gfx950 row swaps, whose
+// two outputs hold the values of the two halves (their sum is the same in
+// every lane); other m: ds_bpermute.
+template <int M>
+__device__ __forceinline__ uint32_t m31_add_xor(uint32_t v) {
+  if constexpr (M == 8) {
+    return m31_add(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false));  // row_ror:8
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return m31_add(r[0], r[1]);
+  } else if constexpr (M == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return m31_add(r[0], r[1]);
+  } else {
+    return m31_add(v, (uint32_t)__shfl_xor((int)v, M, 64));
+  }
+}
+template <int M>
+__device__ __forceinline__ qm31 qm31_add_xor(qm31 t) {
+  return qm31{m31_add_xor<M>(t.a), m31_add_xor<M>(t.b), m31_add_xor<M>(t.c), m31_add_xor<M>(t.d)};
+}
 __device__ __forceinline__ qm31 shfl_q(qm31 q, int src) {
   return qm31{(uint32_t)__shfl((int)q.a, src, 64), (uint32_t)__shfl((int)q.b, src, 64),
               (uint32_t)__shfl((int)q.c, src, 64), (uint32_t)__shfl((int)q.d, src, 64)};
@@ -251,6 +273,7 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
   qacc acc[S::NA];
 #pragma unroll
   for (int i = 0; i < S::NA; i++) acc[i].zero();
+  __shared__ qm31 shb[kBlock];  // b of the wave's lanes, for the products of a lane group
   for (uint64_t x = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> K; x < nb; x += groups) {
     const uint64_t pos = (uint64_t)c * nb + x;
     qm31 a = load_pending(sa, pos, n, np, al);
@@ -273,22 +296,29 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
         const uint64_t mask = (1ull << eq_h) - 1;
         a = qm31_mul(a, qm31_mul(ld_q(eq_hi, x >> eq_h), ld_q(eq_lo, x & mask)));
       }
-      const int base = lane & ~(G - 1);
+      // the group's G values of b through LDS (one 16-byte write, G broadcast reads)
+      shb[threadIdx.x] = b;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      const int base = threadIdx.x & ~(G - 1);
 #pragma unroll
-      for (int d = 0; d < G; d++) acc[d].add(qm31_mul(a, shfl_q(b, base + d)));
+      for (int d = 0; d < G; d++) acc[d].add(qm31_mul(a, shb[base + d]));
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
   }
   qm31 t[S::NA];
 #pragma unroll
-  for (int i = 0; i < S::NA; i++) t[i] = acc[i].reduce();
-#pragma unroll
-  for (int m = G; m < 64; m <<= 1)
-#pragma unroll
-    for (int i = 0; i < S::NA; i++) {
-      const qm31 o{shfl_xor_u32(t[i].a, m), shfl_xor_u32(t[i].b, m), shfl_xor_u32(t[i].c, m),
-                   shfl_xor_u32(t[i].d, m)};
-      t[i] = qm31_add(t[i], o);
-    }
+  for (int i = 0; i < S::NA; i++) {
+    t[i] = acc[i].reduce();
+    // add the 64 / G lane groups: masks G .. 32
+    if constexpr (G <= 1) t[i] = qm31_add_xor<1>(t[i]);
+    if constexpr (G <= 2) t[i] = qm31_add_xor<2>(t[i]);
+    if constexpr (G <= 4) t[i] = qm31_add_xor<4>(t[i]);
+    if constexpr (G <= 8) t[i] = qm31_add_xor<8>(t[i]);
+    t[i] = qm31_add_xor<16>(t[i]);
+    t[i] = qm31_add_xor<32>(t[i]);
+  }
   __shared__ qm31 sh[kBlock / 64][S::NQ];
   const int wave = threadIdx.x >> 6;
   if (lane < G) {
