@@ -558,7 +558,7 @@ static void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out
 // Launch k_trip<KIND, K> over sources sa (, sb) of length n << np with the
 // np pending challenges `pend`; folded vectors to da (, db) when given; eq
 // weights (KIND 1) from hi/lo; then the finisher into sink slot `slot`.
-template <int KIND, int K>
+template <int KIND, int K, bool SPLIT>
 static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n, int np, const TripChal& al,
                          qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, const RoundSink& sk,
                          unsigned grid, uint64_t b_rows, int b_chunks) {
@@ -574,11 +574,11 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
     base = c->trip_count;
     c->trip_count += grid;
   }
-  hipLaunchKernelGGL((k_trip<KIND, K>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
+  hipLaunchKernelGGL((k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
                      sk, counter, base, b_rows, b_chunks);
   TRY(check_launch());
   if (counter) return GKR_OK;
-  constexpr int NQ = TripShape<KIND, K>::NQ;
+  constexpr int NQ = TripShape<KIND, K, SPLIT>::NQ;
   hipLaunchKernelGGL(k_finish_wide<NQ>, dim3(1), dim3(kFinishBlock), 0, c->stream, sk, grid);
   return check_launch();
 }
@@ -593,7 +593,11 @@ static int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* 
   memset(&al, 0, sizeof al);
   for (int i = 0; i < np; i++) al.c[i] = pend[i];
   TRY(make_sink(c, sk, slot));
-  unsigned grid = partial_grid(n);  // one entry per thread up to kTripMaxBlocks workgroups
+  // short vectors: one lane per entry and vector (KIND 0 / 1: 2n lanes, the
+  // split layout of k_trip); long ones one lane per entry; up to
+  // kTripMaxBlocks workgroups
+  const bool split = kind != 2 && 2 * n <= (uint64_t)kTripFusedGrid * kBlock;
+  unsigned grid = partial_grid(split ? 2 * n : n);
   const unsigned max_blocks = K <= 2 ? kTripMaxBlocksShort : kTripMaxBlocks;
   if (grid > max_blocks) grid = max_blocks;
   if (GKR_TRIP_FUSED && grid <= kTripFusedGrid) grid = grid < kTripFusedMax ? grid : kTripFusedMax;
@@ -602,7 +606,8 @@ static int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* 
                  16ull * nvec * ((n << np) + (da ? n : 0)));
 #define GKR_TRIP_CASE(KI, KK)                                                                                 \
   if (kind == KI && K == KK)                                                                                  \
-    return launch_trip_k<KI, KK>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks);
+    return split ? launch_trip_k<KI, KK, true>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks) \
+                 : launch_trip_k<KI, KK, false>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks);
   GKR_TRIP_CASE(0, 1) GKR_TRIP_CASE(0, 2) GKR_TRIP_CASE(0, 3)
   GKR_TRIP_CASE(1, 0) GKR_TRIP_CASE(1, 1) GKR_TRIP_CASE(1, 2) GKR_TRIP_CASE(1, 3)
   GKR_TRIP_CASE(2, 1) GKR_TRIP_CASE(2, 2) GKR_TRIP_CASE(2, 3)

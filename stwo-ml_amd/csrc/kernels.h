@@ -244,43 +244,56 @@ __device__ __forceinline__ qm31 load_pending(const qm31* __restrict__ src, uint6
   }
 }
 
-template <int KIND, int K>
+template <int KIND, int K, bool SPLIT = true>
 struct TripShape {
-  static constexpr int G = 1 << K;                        // sub-vectors
-  static constexpr int NQ = KIND == 2 ? G : G * G;        // sums per launch
-  static constexpr int NA = KIND == 2 ? 1 : G;            // accumulators per lane
+  static constexpr int G = 1 << K;                                  // sub-vectors
+  static constexpr int NQ = KIND == 2 ? G : G * G;                  // sums per launch
+  static constexpr bool SIDES = KIND != 2 && SPLIT;                 // a and b on separate lanes
+  static constexpr int LX = SIDES ? 2 * G : G;                      // lanes per entry group x
+  static constexpr int NA = KIND == 2 ? 1 : SIDES ? (G > 1 ? G / 2 : 1) : G;  // accumulators per lane
 };
 
 // Requirements (checked by the host): np <= 3, n a power of two >= 2^K.
 constexpr unsigned kTripFusedMax = 64;
+// Lanes: entry group x (the G entries c * (n >> K) + x) takes LX lanes.
+// KIND 2: lane c adds entry c of a.  KIND 0 / 1 with SPLIT (short vectors,
+// where a lane's serial work is the latency): lane c (the "a side") loads
+// and folds a_c (times the eq weight for KIND 1), lane G + c (the "b side")
+// b_c; both go through LDS, and each side forms half of the G products
+// a_c b_d (a side d < G / 2, b side the rest; G = 1: the a side).  Without
+// SPLIT (long vectors, bound by HBM and VALU throughput) lane c does both
+// vectors and all G products.
 // b_chunks > 0 (first trip of a matmul, np = 0): sb holds the column-chunk
 // partials of the weight-side restriction (k_restrict_cols) and b is their
 // sum, b[pos] = sum_c sb[c * b_rows + pos] for pos < b_rows and 0 above
 // (the zero padding to n); with db the sums are stored as f_b.
-template <int KIND, int K>
+template <int KIND, int K, bool SPLIT>
 __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, const qm31* __restrict__ sb,
                                                  uint64_t n, int np, TripChal al, qm31* __restrict__ da,
                                                  qm31* __restrict__ db, const qm31* __restrict__ eq_hi,
                                                  const qm31* __restrict__ eq_lo, int eq_h, RoundSink sk,
                                                  uint32_t* counter, uint32_t count_base, uint64_t b_rows,
                                                  int b_chunks) {
-  using S = TripShape<KIND, K>;
-  constexpr int G = S::G;
+  using S = TripShape<KIND, K, SPLIT>;
+  constexpr int G = S::G, LX = S::LX, NA = S::NA;
   const uint64_t nb = n >> K;
   const int lane = threadIdx.x & 63;
-  const int c = lane & (G - 1);
-  const uint64_t groups = ((uint64_t)gridDim.x * blockDim.x) >> K;
-  qacc acc[S::NA];
+  const int gl = lane & (LX - 1);
+  const int c = gl & (G - 1), side = gl / G;  // side 1: the b side (KIND 0 / 1)
+  const uint64_t groups = ((uint64_t)gridDim.x * blockDim.x) / LX;
+  qacc acc[NA];
 #pragma unroll
-  for (int i = 0; i < S::NA; i++) acc[i].zero();
-  __shared__ qm31 shb[kBlock];  // b of the wave's lanes, for the products of a lane group
-  for (uint64_t x = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) >> K; x < nb; x += groups) {
+  for (int i = 0; i < NA; i++) acc[i].zero();
+  __shared__ qm31 shv[kBlock];  // the wave's folded values, for the products of a lane group
+  for (uint64_t x = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / LX; x < nb; x += groups) {
     const uint64_t pos = (uint64_t)c * nb + x;
-    qm31 a = load_pending(sa, pos, n, np, al);
-    if (da) st_q(da, pos, a);
     if constexpr (KIND == 2) {
+      const qm31 a = load_pending(sa, pos, n, np, al);
+      if (da) st_q(da, pos, a);
       acc[0].add(a);
-    } else {
+    } else if constexpr (!S::SIDES) {
+      qm31 a = load_pending(sa, pos, n, np, al);
+      if (da) st_q(da, pos, a);
       qm31 b;
       if (b_chunks) {
         qacc bs;
@@ -297,33 +310,73 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
         a = qm31_mul(a, qm31_mul(ld_q(eq_hi, x >> eq_h), ld_q(eq_lo, x & mask)));
       }
       // the group's G values of b through LDS (one 16-byte write, G broadcast reads)
-      shb[threadIdx.x] = b;
+      shv[threadIdx.x] = b;
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-      const int base = threadIdx.x & ~(G - 1);
+      const int gb = threadIdx.x & ~(G - 1);
 #pragma unroll
-      for (int d = 0; d < G; d++) acc[d].add(qm31_mul(a, shb[base + d]));
+      for (int d = 0; d < G; d++) acc[d].add(qm31_mul(a, shv[gb + d]));
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    } else {
+      qm31 v;
+      if (side == 0) {
+        v = load_pending(sa, pos, n, np, al);
+        if (da) st_q(da, pos, v);
+        if constexpr (KIND == 1) {
+          const uint64_t mask = (1ull << eq_h) - 1;
+          v = qm31_mul(v, qm31_mul(ld_q(eq_hi, x >> eq_h), ld_q(eq_lo, x & mask)));
+        }
+      } else {
+        if (b_chunks) {
+          qacc bs;
+          bs.zero();
+          if (pos < b_rows)
+            for (int ch = 0; ch < b_chunks; ch++) bs.add(ld_q(sb, (uint64_t)ch * b_rows + pos));
+          v = bs.reduce();
+        } else {
+          v = load_pending(sb, pos, n, np, al);
+        }
+        if (db) st_q(db, pos, v);
+      }
+      // a_c at group base + c, b_d at group base + G + d (one 16-byte write, broadcast reads)
+      shv[threadIdx.x] = v;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      const int gb = threadIdx.x & ~(LX - 1);
+      const qm31 ac = shv[gb + c];
+      if (G > 1 || side == 0) {
+#pragma unroll
+        for (int i = 0; i < NA; i++) acc[i].add(qm31_mul(ac, shv[gb + G + side * NA + i]));
+      }
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
   }
-  qm31 t[S::NA];
+  qm31 t[NA];
 #pragma unroll
-  for (int i = 0; i < S::NA; i++) {
+  for (int i = 0; i < NA; i++) {
     t[i] = acc[i].reduce();
-    // add the 64 / G lane groups: masks G .. 32
-    if constexpr (G <= 1) t[i] = qm31_add_xor<1>(t[i]);
-    if constexpr (G <= 2) t[i] = qm31_add_xor<2>(t[i]);
-    if constexpr (G <= 4) t[i] = qm31_add_xor<4>(t[i]);
-    if constexpr (G <= 8) t[i] = qm31_add_xor<8>(t[i]);
-    t[i] = qm31_add_xor<16>(t[i]);
+    // add the 64 / LX lane groups: masks LX .. 32
+    if constexpr (LX <= 1) t[i] = qm31_add_xor<1>(t[i]);
+    if constexpr (LX <= 2) t[i] = qm31_add_xor<2>(t[i]);
+    if constexpr (LX <= 4) t[i] = qm31_add_xor<4>(t[i]);
+    if constexpr (LX <= 8) t[i] = qm31_add_xor<8>(t[i]);
+    if constexpr (LX <= 16) t[i] = qm31_add_xor<16>(t[i]);
     t[i] = qm31_add_xor<32>(t[i]);
   }
   __shared__ qm31 sh[kBlock / 64][S::NQ];
   const int wave = threadIdx.x >> 6;
-  if (lane < G) {
+  if (lane < LX) {
+    if constexpr (KIND == 2) {
+      sh[wave][c] = t[0];
+    } else if constexpr (!S::SIDES) {
 #pragma unroll
-    for (int i = 0; i < S::NA; i++) sh[wave][lane * S::NA + i] = t[i];
+      for (int i = 0; i < NA; i++) sh[wave][c * G + i] = t[i];
+    } else if (G > 1 || side == 0) {
+#pragma unroll
+      for (int i = 0; i < NA; i++) sh[wave][c * G + side * NA + i] = t[i];
+    }
   }
   __syncthreads();
   for (int q = threadIdx.x; q < S::NQ; q += blockDim.x) {
