@@ -16,7 +16,7 @@ def log(msg):
     sys.stdout.flush()
 
 
-@pytest.mark.parametrize("logn", [0, 1, 2, 9, 10, 11, 16, 20, 24])
+@pytest.mark.parametrize("logn", [0, 1, 2, 9, 10, 11, 15, 16, 17, 20, 21, 24])
 def test_sumcheck_product_parity(gpu_ctx, logn):
     n = 1 << logn
     log(f"case sumcheck_product 2^{logn}")
