@@ -37,6 +37,20 @@ __device__ __forceinline__ void stage_point(const PointArg& pt, PointLds* sp) {
   __syncthreads();
 }
 
+// eq factor product prod_{l < m} (bit m-1-l of x ? r[s+l] : 1 - r[s+l]) from
+// the staged point, as two interleaved chains (even and odd l) so one wave
+// issues the second chain's instructions while the first's results are in
+// flight; the field product does not depend on the order.
+__device__ __forceinline__ qm31 eq_prod(const PointLds& sp, int s, int m, uint64_t x) {
+  qm31 e0 = qm31_one(), e1 = qm31_one();
+  int l = 0;
+  for (; l + 2 <= m; l += 2) {
+    e0 = qm31_mul(e0, ((x >> (m - 1 - l)) & 1ull) ? sp.r[s + l] : sp.omr[s + l]);
+    e1 = qm31_mul(e1, ((x >> (m - 2 - l)) & 1ull) ? sp.r[s + l + 1] : sp.omr[s + l + 1]);
+  }
+  if (l < m) e0 = qm31_mul(e0, (x & 1ull) ? sp.r[s + l] : sp.omr[s + l]);
+  return qm31_mul(e0, e1);
+}
 __device__ __forceinline__ qm31 ld_q(const qm31* __restrict__ p, uint64_t i) {
   uint4 v = reinterpret_cast<const uint4*>(p)[i];
   return qm31{v.x, v.y, v.z, v.w};
@@ -555,9 +569,7 @@ __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out)
   while (t + 1 < a.count && i >= a.off[t + 1]) t++;
   const uint32_t x = i - a.off[t];
   const int s = a.s[t], m = a.m[t];
-  qm31 acc = qm31_one();
-  for (int l = 0; l < m; l++) acc = qm31_mul(acc, ((x >> (m - 1 - l)) & 1u) ? sp.r[s + l] : sp.omr[s + l]);
-  out[i] = acc;
+  out[i] = eq_prod(sp, s, m, x);
 }
 
 // ------------------------------------------------------------------ eq / Lagrange
@@ -568,13 +580,7 @@ __global__ void k_eq_direct(PointArg pt, uint64_t count, qm31* __restrict__ out)
   stage_point(pt, &sp);
   uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (x >= count) return;
-  qm31 acc = qm31_one();
-  const int n = pt.n;
-  for (int l = 0; l < n; l++) {
-    const uint64_t bit = (x >> (n - 1 - l)) & 1ull;
-    acc = qm31_mul(acc, bit ? sp.r[l] : sp.omr[l]);
-  }
-  st_q(out, x, acc);
+  st_q(out, x, eq_prod(sp, 0, pt.n, x));
 }
 // Balanced base-256 digits of a canonical M31 value: centered to
 // v in (-P/2, P/2], v = sum_q d_q 256^q with d_q in [-128, 127].
@@ -612,8 +618,7 @@ __global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, 
     n = pt.n - n1;
     out = out2;
   }
-  qm31 acc = qm31_one();
-  for (int l = 0; l < n; l++) acc = qm31_mul(acc, ((x >> (n - 1 - l)) & 1ull) ? sp.r[s + l] : sp.omr[s + l]);
+  const qm31 acc = eq_prod(sp, s, n, x);
   st_q(out, x, acc);
   if (ldig && out == out2) {
     const uint32_t comp[4] = {acc.a, acc.b, acc.c, acc.d};
@@ -635,18 +640,10 @@ __global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __r
   const uint64_t n_hi = 1ull << (pt.n - h), n_lo = 1ull << h;
   uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (x < n_hi) {
-    const int nv = pt.n - h;
-    qm31 acc = qm31_one();
-    for (int l = 0; l < nv; l++) acc = qm31_mul(acc, ((x >> (nv - 1 - l)) & 1ull) ? sp.r[l] : sp.omr[l]);
-    st_q(hi, x, acc);
+    st_q(hi, x, eq_prod(sp, 0, pt.n - h, x));
   } else if (x < n_hi + n_lo) {
     const uint64_t y = x - n_hi;
-    qm31 acc = qm31_one();
-    for (int l = 0; l < h; l++) {
-      const int v = pt.n - h + l;
-      acc = qm31_mul(acc, ((y >> (h - 1 - l)) & 1ull) ? sp.r[v] : sp.omr[v]);
-    }
-    st_q(lo, y, acc);
+    st_q(lo, y, eq_prod(sp, pt.n - h, h, y));
   }
 }
 __global__ void k_eq_combine(const qm31* __restrict__ hi, const qm31* __restrict__ lo, int h, uint64_t count,
