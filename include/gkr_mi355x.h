@@ -190,6 +190,18 @@ int gkr_prove_matmul_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n
                            gkr_qm31* round_polys, gkr_qm31* final_a, gkr_qm31* final_b, gkr_qm31* next_point,
                            gkr_qm31* next_value);
 
+/* reduce_matmul_layer_simd_gpu (gkr/prover.rs:5422-5600): a shared-weight
+ * SIMD matmul over n_blocks (1 .. 64) activation blocks a_blocks[b] (all
+ * m x k) and one b.  f_a = sum_b block_weights[b] * restrict_rows(A_b, r_i)
+ * (combine_blocks, gpu_sumcheck.rs:1123-1146), f_b = restrict_cols(B, r_j);
+ * transcript, outputs and proof record as gkr_prove_matmul_layer (a MatMul
+ * layer proof).                                                            */
+int gkr_prove_matmul_layer_simd(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_point,
+                                const gkr_qm31* claim_value, const gkr_matrix* const* a_blocks,
+                                const gkr_qm31* block_weights, uint32_t n_blocks, const gkr_matrix* b,
+                                gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys, gkr_qm31* final_a,
+                                gkr_qm31* final_b, gkr_qm31* next_point, gkr_qm31* next_value);
+
 /* Outputs of reduce_activation_layer (gkr/prover.rs:6400-6600).  The caller
  * provides the arrays; sizes: eq_round_polys 4*n_vars, multiplicities
  * 2^table_log_size, mult_round_polys 2*table_log_size.                       */

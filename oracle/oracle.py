@@ -332,6 +332,53 @@ def prove_activation_layer(claim_point, claim_value, X: np.ndarray, act_type: in
     }
 
 
+def qmul_rows(w, X: np.ndarray) -> np.ndarray:
+    """w * X[i] for every QM31 row of X ((n, 4) array), the textbook tower product
+    (u^2 = 2 + i) in uint64 numpy arithmetic; rows canonical in, canonical out."""
+    X = np.asarray(X, dtype=np.uint64).reshape(-1, 4)
+    w0, w1, w2, w3 = (np.uint64(int(v) % P) for v in w)
+    p = np.uint64(P)
+
+    def cm(a, b, c, d):  # (a + b i)(c + d i)
+        return (a * c % p + (p - b * d % p)) % p, (a * d % p + b * c % p) % p
+
+    x0, x1, x2, x3 = X[:, 0], X[:, 1], X[:, 2], X[:, 3]
+    ll = cm(w0, w1, x0, x1)
+    hh = cm(w2, w3, x2, x3)
+    rh = ((2 * hh[0] % p + (p - hh[1])) % p, (hh[0] + 2 * hh[1]) % p)  # (2 + i) * hh
+    lh = cm(w0, w1, x2, x3)
+    hl = cm(w2, w3, x0, x1)
+    out = np.stack([(ll[0] + rh[0]) % p, (ll[1] + rh[1]) % p, (lh[0] + hl[0]) % p, (lh[1] + hl[1]) % p], axis=1)
+    return out.astype(np.uint32)
+
+
+def prove_matmul_layer_simd(claim_point, claim_value, A_blocks, B: np.ndarray, block_weights, ch: Channel):
+    """reduce_matmul_layer_simd_gpu (engine/src/gkr/prover.rs:5422-5600): mix m, k, n and the claim;
+    f_a = sum_b w_b restrict_rows(A_b, r_i) (combine_blocks, gpu_sumcheck.rs:1123-1146); f_b =
+    restrict_cols(B, r_j); the degree-2 round loop; mix final_a, final_b."""
+    A0 = np.asarray(A_blocks[0])
+    m, k = A0.shape
+    n = B.shape[1]
+    pk = _next_pow2(k)
+    lm = _next_pow2(m).bit_length() - 1
+    ln = _next_pow2(n).bit_length() - 1
+    r_i, r_j = list(claim_point[:lm]), list(claim_point[lm:lm + ln])
+    ch.mix_u64(m)
+    ch.mix_u64(k)
+    ch.mix_u64(n)
+    ch.mix_secure_field(claim_value)
+    fa = np.zeros((pk, 4), dtype=np.uint64)
+    for A_b, w in zip(A_blocks, block_weights):
+        fa = (fa + qmul_rows(w, restrict_rows_fused(A_b, r_i, pk))) % P
+    fb = restrict_cols_fused(B, r_j, pk)
+    res = sumcheck_product(fa.astype(np.uint32), fb, ch)
+    ch.mix_secure_field(res["final_a_eval"])
+    ch.mix_secure_field(res["final_b_eval"])
+    return {"round_polys": res["round_polys"], "final_a_eval": res["final_a_eval"],
+            "final_b_eval": res["final_b_eval"], "next_point": r_i + res["challenges"],
+            "next_value": res["final_a_eval"]}
+
+
 def verify_matmul_layer(claim_point, claim_value, m: int, k: int, n: int, round_polys, final_a, final_b,
                         ch: Channel) -> int:
     """verify_matmul_reduction (engine/src/gkr/verifier.rs:2675-2788); 0 = accepted."""

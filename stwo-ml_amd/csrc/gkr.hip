@@ -1009,8 +1009,10 @@ static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
 // each of length pk (components/matmul.rs:470-565, backend.rs:127-134): one
 // launch for both Lagrange tables, one for both restrictions (f_a directly,
 // f_b as column-chunk partials in S_COLPART, pending until added).
+// weight_only: f_a is left to the caller (the SIMD layer combines its blocks'
+// activation sides itself); L_i is still built.
 static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, const qm31* r_i, int n_ri,
-                         const qm31* r_j, int n_rj, uint64_t pk) {
+                         const qm31* r_j, int n_rj, uint64_t pk, bool weight_only = false) {
   TRY(prepare_r8(c, const_cast<gkr_matrix*>(B)));  // the matrix's contents never change; r8 is derived
   HostTimer ht(c, K_HOST_LAUNCH);
   const uint64_t m = A->rows, k = A->cols, n = B->cols;
@@ -1060,7 +1062,7 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     TRY(ensureT(c, S_COLPART, (size_t)gc * k, &part));
     // the activation side rides in one more column-chunk slice (one column per thread)
     RowsJob rows{A->dev, m, k, pk, Li, fa};
-    const uint64_t act_blocks = (pk + 63) / 64;  // 64 columns of A per workgroup
+    const uint64_t act_blocks = weight_only ? 0 : (pk + 63) / 64;  // 64 columns of A per workgroup
     if (act_blocks + gr * gc > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
     const dim3 grid((unsigned)(act_blocks + gr * gc));
     if (use8) {
@@ -1530,6 +1532,114 @@ extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, u
   std::vector<gkr_qm31> chal(T > 0 ? T : 1);
   TRY(reduce_matmul_impl(c, a, b, claim_point, log_m, claim_point + log_m, log_n, pk, C, round_polys, chal.data(),
                          final_a, final_b));
+  C.mix_secure_field(Q(*final_a));
+  C.mix_secure_field(Q(*final_b));
+  if (next_point) {
+    for (uint32_t l = 0; l < log_m; l++) next_point[l] = claim_point[l];
+    for (int t = 0; t < T; t++) next_point[log_m + t] = chal[t];
+  }
+  *next_value = *final_a;
+  if (proof) {
+    LayerRec L;
+    L.tag = 0;
+    for (int t = 0; t < 3 * T; t++) L.rp.push_back(Q(round_polys[t]));
+    L.final_a = Q(*final_a);
+    L.final_b = Q(*final_b);
+    proof->layers.push_back(L);
+    WeightClaimRec w;
+    w.b = b;
+    for (uint32_t l = 0; l < log_n; l++) w.point.push_back(Q(claim_point[log_m + l]));
+    for (int t = 0; t < T; t++) w.point.push_back(Q(chal[t]));
+    w.value = Q(*final_b);
+    proof->weight_claims.push_back(std::move(w));
+  }
+  return GKR_OK;
+}
+
+// SIMD matmul layer with a shared weight: N activation blocks A_b (all m x k)
+// combined with weights w_b against one B (gkr/prover.rs:5422-5600,
+// reduce_matmul_layer_simd_gpu).  Same transcript and proof record as
+// gkr_prove_matmul_layer with f_a = sum_b w_b restrict_rows(A_b, r_i).
+extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
+                                           const gkr_qm31* claim_value, const gkr_matrix* const* a_blocks,
+                                           const gkr_qm31* block_weights, uint32_t n_blocks, const gkr_matrix* b,
+                                           gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys,
+                                           gkr_qm31* final_a, gkr_qm31* final_b, gkr_qm31* next_point,
+                                           gkr_qm31* next_value) {
+  CH_CHECK(ch);
+  if (!c || !a_blocks || !block_weights || !b || !claim_value || !final_a || !final_b || !next_value ||
+      (!claim_point && n_point))
+    return fail(GKR_ERR_INVALID, "null argument");
+  if (n_blocks == 0 || n_blocks > (uint32_t)kSimdMaxBlocks)
+    return fail(GKR_ERR_INVALID, "%u blocks (1 .. %d supported)", n_blocks, kSimdMaxBlocks);
+  if (!canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
+  const gkr_matrix* a = a_blocks[0];
+  if (!a) return fail(GKR_ERR_INVALID, "null block");
+  SimdBlocks blk;
+  memset(&blk, 0, sizeof blk);
+  blk.count = (int)n_blocks;
+  for (uint32_t i = 0; i < n_blocks; i++) {
+    const gkr_matrix* ai = a_blocks[i];
+    if (!ai || ai->ctx != c) return fail(GKR_ERR_INVALID, "block %u missing or from another context", i);
+    if (ai->rows != a->rows || ai->cols != a->cols)
+      return fail(GKR_ERR_INVALID, "block %u is %llux%llu, block 0 %llux%llu", i, (unsigned long long)ai->rows,
+                  (unsigned long long)ai->cols, (unsigned long long)a->rows, (unsigned long long)a->cols);
+    if (!canonical_q(block_weights[i])) return fail(GKR_ERR_INVALID, "block weight %u not canonical", i);
+    blk.a[i] = ai->dev;
+    blk.w[i] = Q(block_weights[i]);
+  }
+  const uint64_t pm = next_pow2(a->rows), pk = next_pow2(a->cols), pn = next_pow2(b->cols);
+  const uint32_t log_m = (uint32_t)log2_exact(pm), log_n = (uint32_t)log2_exact(pn);
+  const int T = log2_exact(pk);
+  if (n_point != log_m + log_n)
+    return fail(GKR_ERR_INVALID, "output claim has %u vars, expected exactly %u (log_m=%u + log_n=%u)", n_point,
+                log_m + log_n, log_m, log_n);
+  if (T > 0 && (!round_polys || !next_point)) return fail(GKR_ERR_INVALID, "null output buffer");
+  TRY(validate_matmul(c, a, b, log_m, log_n));
+  std::vector<qm31> ri(log_m), rj(log_n);
+  for (uint32_t l = 0; l < log_m + log_n; l++)
+    if (!canonical_q(claim_point[l])) return fail(GKR_ERR_INVALID, "claim point coordinate %u not canonical", l);
+  for (uint32_t l = 0; l < log_m; l++) ri[l] = Q(claim_point[l]);
+  for (uint32_t l = 0; l < log_n; l++) rj[l] = Q(claim_point[log_m + l]);
+  HIP_TRY(hipSetDevice(c->device));
+  PoseidonChannel& C = ch->ch;
+  C.mix_u64(a->rows);
+  C.mix_u64(a->cols);
+  C.mix_u64(b->cols);
+  C.mix_secure_field(Q(*claim_value));
+  // the restriction scratch (S_FA0 / S_FB0) is rewritten: no cached restriction survives
+  c->mm.valid = false;
+  c->mm.have_trip0 = false;
+  TRY(restrict_pair(c, a, b, ri.data(), (int)log_m, rj.data(), (int)log_n, pk, true));
+  {
+    HostTimer ht(c, K_HOST_LAUNCH);
+    qm31 *Li, *fa;
+    TRY(ensureT(c, S_LI, a->rows, &Li));
+    TRY(ensureT(c, S_FA0, pk, &fa));
+    hipLaunchKernelGGL(k_restrict_rows_simd, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, blk, a->rows, a->cols,
+                       pk, (const qm31*)Li, fa);
+    TRY(check_launch());
+  }
+  TRY(finish_fb(c));
+  std::vector<gkr_qm31> chal(T > 0 ? T : 1);
+  qm31 *fa0, *fa1, *fb0, *fb1, *fa2, *fb2;
+  TRY(ensureT(c, S_FA0, pk, &fa0));
+  TRY(ensureT(c, S_FB0, pk, &fb0));
+  TRY(ensureT(c, S_FA1, pk / 2 + 1, &fa1));
+  TRY(ensureT(c, S_FB1, pk / 2 + 1, &fb1));
+  TRY(ensureT(c, S_FA2, pk / 4 + 1, &fa2));
+  TRY(ensureT(c, S_FB2, pk / 4 + 1, &fb2));
+  if (T == 0) {
+    qm31 v[1];
+    TRY(fetch_q(c, fa0, 1, v));
+    *final_a = G(v[0]);
+    TRY(fetch_q(c, fb0, 1, v));
+    *final_b = G(v[0]);
+  } else {
+    qm31* bufs_a[2] = {fa1, fa2};
+    qm31* bufs_b[2] = {fb1, fb2};
+    TRY(product_sumcheck(c, C, T, fa0, fb0, bufs_a, bufs_b, nullptr, 0, round_polys, chal.data(), final_a, final_b));
+  }
   C.mix_secure_field(Q(*final_a));
   C.mix_secure_field(Q(*final_b));
   if (next_point) {

@@ -137,6 +137,8 @@ SIGNATURES = [
     ("gkr_seed_channel", C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_uint64, _PF]),
     ("gkr_matmul_output_claim", C.c_int, [_P, _P, _P, _PQ, C.c_uint32, _PQ]),
     ("gkr_prove_matmul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ, _PQ]),
+    ("gkr_prove_matmul_layer_simd", C.c_int,
+     [_P, _PQ, C.c_uint32, _PQ, C.POINTER(_P), _PQ, C.c_uint32, _P, _P, _P, _PQ, _PQ, _PQ, _PQ, _PQ]),
     ("gkr_prove_activation_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, C.c_uint32, C.c_uint32, _P, _P,
                                              C.POINTER(GkrLogupOut)]),
     ("gkr_activation_table", C.c_int, [C.c_uint32, C.c_uint32, _U32P]),
@@ -426,6 +428,28 @@ class Context:
                                             C.byref(q_to_c(claim_value)), a.handle, b.handle, ch.handle,
                                             proof.handle if proof else None, rp, C.byref(fa), C.byref(fb), npnt,
                                             C.byref(nv)))
+        polys = [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2])) for t in range(T)]
+        return {"round_polys": polys, "final_a_eval": q_from_c(fa), "final_b_eval": q_from_c(fb),
+                "next_point": [q_from_c(npnt[i]) for i in range(lm + T)], "next_value": q_from_c(nv)}
+
+    def prove_matmul_layer_simd(self, claim_point, claim_value, a_blocks, block_weights, b: "Matrix",
+                                ch: PoseidonChannel, proof: Optional["Proof"] = None):
+        """gkr_prove_matmul_layer_simd: reduce_matmul_layer_simd_gpu (gkr/prover.rs:5422-5600) over
+        activation blocks a_blocks (Matrix list, same shape) with QM31 block_weights and one weight b."""
+        a0 = a_blocks[0]
+        pm = 1 << (a0.rows - 1).bit_length()
+        pk = 1 << (a0.cols - 1).bit_length()
+        T = pk.bit_length() - 1
+        lm = pm.bit_length() - 1
+        rp = (GkrQM31 * max(1, 3 * T))()
+        fa, fb, nv = GkrQM31(), GkrQM31(), GkrQM31()
+        npnt = (GkrQM31 * max(1, lm + T))()
+        handles = (_P * len(a_blocks))(*[m.handle for m in a_blocks])
+        _check(lib().gkr_prove_matmul_layer_simd(self._h, q_array(claim_point), len(claim_point),
+                                                 C.byref(q_to_c(claim_value)), handles, q_array(block_weights),
+                                                 len(a_blocks), b.handle, ch.handle,
+                                                 proof.handle if proof else None, rp, C.byref(fa), C.byref(fb),
+                                                 npnt, C.byref(nv)))
         polys = [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2])) for t in range(T)]
         return {"round_polys": polys, "final_a_eval": q_from_c(fa), "final_b_eval": q_from_c(fb),
                 "next_point": [q_from_c(npnt[i]) for i in range(lm + T)], "next_value": q_from_c(nv)}
