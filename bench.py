@@ -33,6 +33,7 @@ import gkr_mi355x as G  # noqa: E402
 
 METRIC = "GKR matmul-sumcheck Melem/s + % HBM peak; proved tokens/s, Qwen2.5-14B shape"
 HBM_PEAK_GBS = 8000.0
+P = (1 << 31) - 1  # M31
 (K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT,
  K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH) = range(13)
 
@@ -370,6 +371,75 @@ def bench_forward(ctx, args):
     ctx.close()
 
 
+def bench_simd(ctx, args, blocks=8):
+    """Shared-weight SIMD matmul layer (reduce_matmul_layer_simd_gpu): `blocks` activation blocks of
+    64x5120 (one per transformer block of a batch) against the Qwen2.5-14B MLP gate weight 5120x13824,
+    int8-range synthetic data resident in HBM; a step is one layer proof with a fresh channel."""
+    m, k, n = 64, 5120, 13824
+    a = [ctx.synthetic(m, k, 1, 300 + i) for i in range(blocks)]
+    b = ctx.synthetic(k, n, 1, 400)
+    prng = __import__("random").Random(5)
+    ws = [tuple(prng.randrange(P) for _ in range(4)) for _ in range(blocks)]
+    nv = lg(m) + lg(n)
+
+    def step():
+        ch = G.PoseidonChannel()
+        ch.mix_u64(blocks)
+        r = ch.draw_qm31s(nv)
+        res = ctx.prove_matmul_layer_simd(r, (1, 2, 3, 4), a, ws, b, ch)
+        return ch.digest(), res["final_a_eval"]
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    ctx.set_timing(0 if args.no_timing else 1)
+    ctx.reset_timing()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    outs = [step() for _ in range(args.steps)]
+    ctx.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    assert all(o == outs[0] for o in outs), "non-deterministic proof"
+    elems = blocks * m * k + k * n
+    kernels, roofline = {}, None
+    for kid, name in [(K_RESTRICT_COLS, "restrict_cols (weight side)"), (K_RESTRICT_ROWS, "restrict_rows_simd")]:
+        ms, nl, nb = ctx.kernel_time(kid)
+        if nl:
+            kernels[name] = {"launches": nl, "avg_us": round(ms / nl * 1e3, 3),
+                             "gbps": round(nb / (ms * 1e-3) / 1e9, 1), "bytes_per_launch": nb // nl}
+    rc = kernels.get("restrict_cols (weight side)")
+    if rc:
+        roofline = {"bound": "hbm", "achieved": rc["gbps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(rc["gbps"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_restrict_cols",
+                    "avg_launch_us": rc["avg_us"], "bytes_per_launch": rc["bytes_per_launch"]}
+    ctx.set_timing(0)
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        As = [O.synthetic(m, k, 1, 300 + i) for i in range(blocks)]
+        B = O.synthetic(k, n, 1, 400)
+        ch = O.Channel()
+        ch.mix_u64(blocks)
+        r = ch.draw_qm31s(nv)
+        t1 = time.perf_counter()
+        O.prove_matmul_layer_simd(r, (1, 2, 3, 4), As, B, ws, ch)
+        dtc = time.perf_counter() - t1
+        cpu = {"value": round(elems / dtc / 1e6, 3), "unit": "Melem/s",
+               "cores": int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count(), "kind": "port",
+               "sample": f"the same layer by the oracle (reference CPU algorithm): {dtc:.2f} s"}
+    result = {
+        "metric": "GKR SIMD matmul layer (shared weight) Melem/s + % HBM peak",
+        "value": round(elems / dt / 1e6, 1), "unit": "Melem/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u32-m31", "data": "synthetic (counter-mode SplitMix64, int8-range)",
+        "config": {"workload": f"qwen2.5-14b-gate-simd-{blocks}-blocks", "blocks": blocks, "block_shape": [m, k],
+                   "weight_shape": [k, n]},
+        "roofline": roofline, "kernels": kernels, "digest": hex(outs[0][0]), "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def trip_k(n, big=1 << 16, huge=1 << 20):
     """Rounds per device trip over a vector of n entries (the library's trip_k)."""
     return 1 if n > huge else 2 if n > big else 3
@@ -458,7 +528,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
-    ap.add_argument("--config", default="qwen48", choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward"])
+    ap.add_argument("--config", default="qwen48",
+                    choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward", "simd"])
     ap.add_argument("--c2-logs", default="20,24,28",
                     help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -485,6 +556,8 @@ def main():
         return bench_commit(ctx, args)
     if args.config == "forward":
         return bench_forward(ctx, args)
+    if args.config == "simd":
+        return bench_simd(ctx, args)
     sbuf = SerialBuffer()
     if args.config == "cfg1":
         cfg, n_layers = None, 1

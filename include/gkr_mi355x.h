@@ -94,7 +94,8 @@ void gkr_ctx_destroy(gkr_ctx* ctx);
 int gkr_ctx_synchronize(gkr_ctx* ctx);
 /* Per-kernel timing (HIP events on the context stream), for benchmarks.
  * ids: 0 restrict_cols (weight and activation side of a matmul in one
- * launch), 1 unused, 2 product-sumcheck trip (several
+ * launch), 1 the SIMD layer's weighted activation-side restriction, 2
+ * product-sumcheck trip (several
  * rounds per launch), 3 eq-sumcheck or degree-1 trip, 4 logup prepare, 5 eq
  * tables (device kernels: one event pair per launch); 6 host Fiat-Shamir
  * inside the reducers, 7 host wait for results of device kernels, 8 host wait

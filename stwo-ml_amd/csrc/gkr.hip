@@ -233,7 +233,7 @@ struct TimedLaunch {
   uint64_t bytes;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
-    if (c->timing >= 2 || (c->timing == 1 && (kid == K_RESTRICT_COLS || kid == K_MERKLE))) {
+    if (c->timing >= 2 || (c->timing == 1 && (kid == K_RESTRICT_COLS || kid == K_RESTRICT_ROWS || kid == K_MERKLE))) {
       e0 = get_event(c);
       e1 = get_event(c);
       if (e0) (void)hipEventRecord(e0, c->stream);
@@ -1077,14 +1077,14 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
       gc = gc8;
       if (act_blocks + gr8 * gc8 > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
       // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
-      TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + 4 * m * k + 16 * m + 16 * pk);
+      TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
       hipLaunchKernelGGL(k_restrict_cols8, dim3((unsigned)(act_blocks + gr8 * gc8)), dim3(kBlock), 0, c->stream,
                          B->r8, B->r8_stride, k, (const u32x4*)ldig, (n + 3) / 4, passes, (uint32_t*)part, rows,
                          (uint32_t)act_blocks, (uint32_t)gr8);
       TRY(check_launch());
     } else {
       // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
-      TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + 4 * m * k + 16 * m + 16 * pk);
+      TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
       if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
         hipLaunchKernelGGL(k_restrict_cols<true>, grid, dim3(kBlock), 0, c->stream, B->dev, k, n, chunk, Lj,
                            (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr);
@@ -1616,8 +1616,10 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
     qm31 *Li, *fa;
     TRY(ensureT(c, S_LI, a->rows, &Li));
     TRY(ensureT(c, S_FA0, pk, &fa));
-    hipLaunchKernelGGL(k_restrict_rows_simd, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, blk, a->rows, a->cols,
-                       pk, (const qm31*)Li, fa);
+    // algorithmic bytes: the blocks' activations, L_i, f_a written
+    TimedLaunch t(c, K_RESTRICT_ROWS, 4ull * n_blocks * a->rows * a->cols + 16 * a->rows + 16 * pk);
+    hipLaunchKernelGGL(k_restrict_rows_simd, dim3((unsigned)((pk + 63) / 64)), dim3(kSimdWaves * 64), 0, c->stream, blk,
+                       a->rows, a->cols, pk, (const qm31*)Li, fa);
     TRY(check_launch());
   }
   TRY(finish_fb(c));

@@ -994,46 +994,66 @@ __global__ void __launch_bounds__(kBlock) k_restrict_cols8(const int8_t* __restr
 // Activation side of a shared-weight SIMD matmul (N blocks A_b with one B):
 // f_a[j] = sum_b w_b sum_i L_i A_b[i][j] for j < k, 0 for k <= j < pk, the
 // per-block restrict_rows followed by combine_blocks of the reference
-// (gkr/prover.rs:5471-5506, gpu_sumcheck.rs:1123-1146) in one pass; one
-// thread per column, rows in lazy 64-bit sums as in restrict_rows_block.
+// (gkr/prover.rs:5471-5506, gpu_sumcheck.rs:1123-1146) in one pass.  A
+// workgroup (kSimdWaves waves) takes 64 columns; wave w adds rows w,
+// w + kSimdWaves, ... of every block
+// (eight rows in flight, lazy 64-bit sums as in restrict_rows_block), scales
+// its block sums by w_b (linear, so partial sums may be scaled), and the four
+// waves meet in LDS.
 constexpr int kSimdMaxBlocks = 64;
+constexpr int kSimdWaves = 4;
 struct SimdBlocks {
   const uint32_t* a[kSimdMaxBlocks];
   qm31 w[kSimdMaxBlocks];
   int count;
 };
-__global__ void __launch_bounds__(kBlock) k_restrict_rows_simd(SimdBlocks blk, uint64_t m, uint64_t k, uint64_t pk,
-                                                               const qm31* __restrict__ L, qm31* __restrict__ out) {
-  const uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= pk) return;
-  if (j >= k) {
-    st_q(out, j, qm31_zero());
-    return;
-  }
+__global__ void __launch_bounds__(kSimdWaves * 64) k_restrict_rows_simd(SimdBlocks blk, uint64_t m, uint64_t k,
+                                                                         uint64_t pk, const qm31* __restrict__ L,
+                                                                         qm31* __restrict__ out) {
+  __shared__ qm31 part[kSimdWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t j = (uint64_t)blockIdx.x * 64 + lane;
   qacc acc;
   acc.zero();
-  for (int b = 0; b < blk.count; b++) {
-    const uint32_t* A = blk.a[b];
-    uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
-    for (uint64_t i = 0; i < m; i += 4) {
-      uint64_t t[4] = {0, 0, 0, 0};  // up to 4 rows: 4 * (P-1)^2 < 2^64
+  if (j < k) {
+    for (int b = 0; b < blk.count; b++) {
+      const uint32_t* A = blk.a[b];
+      uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+      for (uint64_t i0 = wave; i0 < m; i0 += 8 * kSimdWaves) {
+        uint32_t v[8];
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        if (i + u < m) {
-          const uint64_t v = A[(i + u) * k + j];
-          const qm31 l = ld_q(L, i + u);
-          t[0] += v * l.a; t[1] += v * l.b; t[2] += v * l.c; t[3] += v * l.d;
+        for (int u = 0; u < 8; u++) {
+          const uint64_t i = i0 + (uint64_t)u * kSimdWaves;
+          v[u] = i < m ? A[i * k + j] : 0u;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          uint64_t t[4] = {0, 0, 0, 0};  // 4 rows: 4 * (P-1)^2 < 2^64
+#pragma unroll
+          for (int u = 4 * h; u < 4 * h + 4; u++) {
+            const uint64_t i = i0 + (uint64_t)u * kSimdWaves;
+            const qm31 l = i < m ? ld_q(L, i) : qm31_zero();
+            t[0] += (uint64_t)v[u] * l.a; t[1] += (uint64_t)v[u] * l.b;
+            t[2] += (uint64_t)v[u] * l.c; t[3] += (uint64_t)v[u] * l.d;
+          }
+#pragma unroll
+          for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
         }
       }
+      uint32_t r[4];
 #pragma unroll
-      for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+      for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
+      acc.add(qm31_mul(blk.w[b], qm31{r[0], r[1], r[2], r[3]}));
     }
-    uint32_t r[4];
-#pragma unroll
-    for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
-    acc.add(qm31_mul(blk.w[b], qm31{r[0], r[1], r[2], r[3]}));
   }
-  st_q(out, j, acc.reduce());
+  part[wave][lane] = acc.reduce();
+  __syncthreads();
+  if (wave == 0 && j < pk) {
+    qm31 sum = part[0][lane];
+#pragma unroll
+    for (int w = 1; w < kSimdWaves; w++) sum = qm31_add(sum, part[w][lane]);
+    st_q(out, j, sum);  // columns k <= j < pk: zero (no rows added)
+  }
 }
 
 // f_b[i] = sum over column chunks of partial[chunk * k + i] for i < k; 0 for k <= i < pk.
