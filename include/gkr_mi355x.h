@@ -203,6 +203,19 @@ int gkr_prove_matmul_layer_simd(gkr_ctx* ctx, const gkr_qm31* claim_point, uint3
                                 gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys, gkr_qm31* final_a,
                                 gkr_qm31* final_b, gkr_qm31* next_point, gkr_qm31* next_value);
 
+/* reduce_matmul_layer_dual_simd_gpu (gkr/prover.rs:5615-5785): n_blocks (a
+ * power of two, up to 64) pairs A_b (m x k), B_b (k x n) with weights w_b.
+ * Mixes m, k, n, n_blocks and the claim, runs the three-factor sumcheck of
+ * sumcheck_3way (gpu_sumcheck.rs:2597-2681) over the block-extended
+ * (w_b, restrict_rows(A_b, r_i), restrict_cols(B_b, r_j)) — block variables
+ * first — and mixes final_a, final_b.  round_polys: 4 per round (c0..c3),
+ * log2(n_blocks) + log2(pk) rounds.  Records a MatMulDualSimd layer.      */
+int gkr_prove_matmul_layer_dual_simd(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_point,
+                                     const gkr_qm31* claim_value, const gkr_matrix* const* a_blocks,
+                                     const gkr_matrix* const* b_blocks, const gkr_qm31* block_weights,
+                                     uint32_t n_blocks, gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys,
+                                     gkr_qm31* final_a, gkr_qm31* final_b);
+
 /* Outputs of reduce_activation_layer (gkr/prover.rs:6400-6600).  The caller
  * provides the arrays; sizes: eq_round_polys 4*n_vars, multiplicities
  * 2^table_log_size, mult_round_polys 2*table_log_size.                       */

@@ -379,6 +379,86 @@ def prove_matmul_layer_simd(claim_point, claim_value, A_blocks, B: np.ndarray, b
             "next_value": res["final_a_eval"]}
 
 
+def _qops():
+    p = np.uint64(P)
+
+    def add(x, y):
+        return (x + y) % p
+
+    def sub(x, y):
+        return (x + (p - y)) % p
+
+    def mul(x, y):  # elementwise QM31 product of (n, 4) uint64 arrays (u^2 = 2 + i)
+        def cm(a, b, c, d):
+            return (a * c % p + (p - b * d % p)) % p, (a * d % p + b * c % p) % p
+        ll = cm(x[:, 0], x[:, 1], y[:, 0], y[:, 1])
+        hh = cm(x[:, 2], x[:, 3], y[:, 2], y[:, 3])
+        rh = ((2 * hh[0] % p + (p - hh[1])) % p, (hh[0] + 2 * hh[1]) % p)
+        lh = cm(x[:, 0], x[:, 1], y[:, 2], y[:, 3])
+        hl = cm(x[:, 2], x[:, 3], y[:, 0], y[:, 1])
+        return np.stack([(ll[0] + rh[0]) % p, (ll[1] + rh[1]) % p, (lh[0] + hl[0]) % p, (lh[1] + hl[1]) % p], axis=1)
+    return add, sub, mul
+
+
+def sumcheck_3way(w: np.ndarray, a: np.ndarray, b: np.ndarray, ch: Channel):
+    """GpuSumcheckExecutor::sumcheck_3way (engine/src/gpu_sumcheck.rs:2597-2681): rounds of
+    sum_x w(x) a(x) b(x) evaluated at t = 0..3 on the top variable (MSB first), Newton differences to
+    c0..c3, mix_poly_coeffs_deg3, draw, fold all three; numpy over (n, 4) QM31 arrays."""
+    add, sub, mul = _qops()
+    w, a, b = (np.asarray(v, dtype=np.uint64).reshape(-1, 4) for v in (w, a, b))
+    rounds, chals = [], []
+    while w.shape[0] > 1:
+        mid = w.shape[0] // 2
+        lo = (w[:mid], a[:mid], b[:mid])
+        dl = tuple(sub(h, l) for h, l in zip((w[mid:], a[mid:], b[mid:]), lo))
+        cur = lo
+        s = []
+        for t in range(4):
+            if t:
+                cur = tuple(add(x, d) for x, d in zip(cur, dl))
+            prod = mul(mul(cur[0], cur[1]), cur[2])
+            s.append(tuple(int(v) for v in (prod.sum(axis=0) % P)))
+        d1 = qsub(s[1], s[0])
+        d2 = qmul(qadd(qsub(qsub(s[2], s[1]), s[1]), s[0]), qinv((2, 0, 0, 0)))
+        d3 = qmul(qsub(qsub(s[3], s[0]), qmul((3, 0, 0, 0), qsub(s[2], s[1]))), qinv((6, 0, 0, 0)))
+        c0, c1 = s[0], qadd(qsub(d1, d2), qmul((2, 0, 0, 0), d3))
+        c2, c3 = qsub(d2, qmul((3, 0, 0, 0), d3)), d3
+        rounds.append((c0, c1, c2, c3))
+        ch.mix_poly_coeffs_deg3(c0, c1, c2, c3)
+        r = ch.draw_qm31()
+        chals.append(r)
+        rr = np.tile(np.array(r, dtype=np.uint64), (mid, 1))
+        w, a, b = (add(l, mul(rr, d)) for l, d in zip(lo, dl))
+    fin = tuple(tuple(int(v) for v in x[0]) for x in (w, a, b))
+    return {"round_polys": rounds, "challenges": chals, "final_w": fin[0], "final_a": fin[1], "final_b": fin[2]}
+
+
+def prove_matmul_layer_dual_simd(claim_point, claim_value, A_blocks, B_blocks, block_weights, ch: Channel):
+    """reduce_matmul_layer_dual_simd_gpu (engine/src/gkr/prover.rs:5615-5785): mix m, k, n, the block count
+    and the claim; ext_w[b pk + x] = w_b, ext_a = restrict_rows(A_b, r_i), ext_b = restrict_cols(B_b, r_j);
+    the three-factor sumcheck; mix final_a, final_b."""
+    m, k = np.asarray(A_blocks[0]).shape
+    n = np.asarray(B_blocks[0]).shape[1]
+    nb = len(A_blocks)
+    pk = _next_pow2(k)
+    lm = _next_pow2(m).bit_length() - 1
+    ln = _next_pow2(n).bit_length() - 1
+    r_i, r_j = list(claim_point[:lm]), list(claim_point[lm:lm + ln])
+    ch.mix_u64(m)
+    ch.mix_u64(k)
+    ch.mix_u64(n)
+    ch.mix_u64(nb)
+    ch.mix_secure_field(claim_value)
+    ew = np.concatenate([np.tile(np.array(w, dtype=np.uint32), (pk, 1)) for w in block_weights])
+    ea = np.concatenate([restrict_rows_fused(A, r_i, pk) for A in A_blocks])
+    eb = np.concatenate([restrict_cols_fused(B, r_j, pk) for B in B_blocks])
+    res = sumcheck_3way(ew, ea, eb, ch)
+    ch.mix_secure_field(res["final_a"])
+    ch.mix_secure_field(res["final_b"])
+    return {"round_polys": res["round_polys"], "final_a_eval": res["final_a"], "final_b_eval": res["final_b"],
+            "n_block_vars": nb.bit_length() - 1, "challenges": res["challenges"], "final_w": res["final_w"]}
+
+
 def verify_matmul_layer(claim_point, claim_value, m: int, k: int, n: int, round_polys, final_a, final_b,
                         ch: Channel) -> int:
     """verify_matmul_reduction (engine/src/gkr/verifier.rs:2675-2788); 0 = accepted."""

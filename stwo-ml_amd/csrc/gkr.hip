@@ -84,7 +84,7 @@ static bool felt_abi_canonical(const gkr_felt& f) {
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_NSLOTS
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and host-side phases (Fiat-Shamir
 // hashing inside the reducers, waiting for trip results, waiting for the
@@ -1191,9 +1191,13 @@ static_assert(kHostTailMM * 8 <= (uint64_t)kHandMax && kHostTailEq3 * 8 <= (uint
 // are only read; trip j >= 1 writes its folded vectors to bufs[(j - 1) & 1]
 // (bufs[0] holds 2^(T-1) entries, bufs[1] 2^(T-2)).  g0, when given, holds
 // the first trip's sums (rounds 0 .. k0 - 1) already computed for these inputs.
+// scale3 set: the rounds of a three-factor sumcheck sum w a b whose w is the
+// constant *scale3 over these variables: each round polynomial is *scale3
+// times the product one, written and mixed as degree 3 (c3 = 0; 4 per round).
 static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, const qm31* in_b,
                             qm31* const bufs_a[2], qm31* const bufs_b[2], const qm31* g0, int k0,
-                            gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b) {
+                            gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b,
+                            const qm31* scale3 = nullptr) {
   const qm31 inv2 = qm31_from_m31(1u << 30);  // 2^-1 mod P
   const uint64_t pk = 1ull << T;
   const std::vector<Trip> trips = plan_trips(T, kHostTailMM, g0 ? k0 : trip_k(1ull << T));
@@ -1202,6 +1206,18 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
     const qm31 c0 = sums[0];
     const qm31 c2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(sums[2], sums[1]), sums[1]), sums[0]), inv2);
     const qm31 c1 = qm31_sub(qm31_sub(sums[1], sums[0]), c2);
+    if (scale3) {
+      const qm31 d0 = qm31_mul(*scale3, c0), d1 = qm31_mul(*scale3, c1), d2 = qm31_mul(*scale3, c2);
+      round_polys[4 * t + 0] = G(d0);
+      round_polys[4 * t + 1] = G(d1);
+      round_polys[4 * t + 2] = G(d2);
+      round_polys[4 * t + 3] = G(qm31_zero());
+      HostTimer ht(c, K_HOST_FS);
+      ch.mix_poly_coeffs_deg3(d0, d1, d2, qm31_zero());
+      chal[t] = ch.draw_qm31();
+      challenges[t] = G(chal[t]);
+      return;
+    }
     round_polys[3 * t + 0] = G(c0);
     round_polys[3 * t + 1] = G(c1);
     round_polys[3 * t + 2] = G(c2);
@@ -1354,7 +1370,8 @@ extern "C" int gkr_matmul_output_claim(gkr_ctx* c, const gkr_matrix* a, const gk
 
 // ------------------------------------------------------------------ proof container
 struct LayerRec {
-  uint32_t tag;  // 0 MatMul, 2 Mul, 3 Activation
+  uint32_t tag;  // 0 MatMul, 2 Mul, 3 Activation, 7 MatMulDualSimd (rp: c0..c3 per round)
+  uint32_t n_block_vars = 0;  // MatMulDualSimd
   std::vector<qm31> rp;  // MatMul: c0,c1,c2 per round; Mul, Activation: eq c0..c3 per round
   qm31 final_a, final_b;  // MatMul: final a/b evals; Mul: lhs/rhs evals
   uint32_t act_type = 0;
@@ -1437,6 +1454,19 @@ static void serialize_proof(const gkr_proof* p, Ser& s) {
       for (size_t r = 0; r < nr; r++) {  // c1 omitted (cairo_serde.rs:1327-1331)
         s.q(L.rp[3 * r]);
         s.q(L.rp[3 * r + 2]);
+      }
+      s.q(L.final_a);
+      s.q(L.final_b);
+    } else if (L.tag == 7) {
+      // LayerProof::MatMulDualSimd (cairo_serde.rs:1629-1646): c1 omitted
+      s.u(7);
+      s.u(L.n_block_vars);
+      const size_t nr = L.rp.size() / 4;
+      s.u(nr);
+      for (size_t r = 0; r < nr; r++) {
+        s.q(L.rp[4 * r]);
+        s.q(L.rp[4 * r + 2]);
+        s.q(L.rp[4 * r + 3]);
       }
       s.q(L.final_a);
       s.q(L.final_b);
@@ -1662,6 +1692,178 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
     for (int t = 0; t < T; t++) w.point.push_back(Q(chal[t]));
     w.value = Q(*final_b);
     proof->weight_claims.push_back(std::move(w));
+  }
+  return GKR_OK;
+}
+
+// Dual-operand SIMD matmul layer (gkr/prover.rs:5615-5785,
+// reduce_matmul_layer_dual_simd_gpu): N = 2^nbv blocks A_b (m x k), B_b
+// (k x n) with weights w_b; the three-factor sumcheck over the block-extended
+// vectors ext_w[b pk + x] = w_b, ext_a = restrict_rows(A_b, r_i),
+// ext_b = restrict_cols(B_b, r_j) (sumcheck_3way, gpu_sumcheck.rs:2597-2681).
+// ext_w is constant over the k variables, so the nbv block rounds (first, MSB)
+// come from the block Gram matrix D[b1][b2] = sum_x fa_b1(x) fb_b2(x) on the
+// host, and the log2 pk remaining rounds are the product sumcheck of the
+// blocks' combinations by the block challenges, scaled by the folded weight.
+extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
+                                                const gkr_qm31* claim_value, const gkr_matrix* const* a_blocks,
+                                                const gkr_matrix* const* b_blocks, const gkr_qm31* block_weights,
+                                                uint32_t n_blocks, gkr_channel* ch, gkr_proof* proof,
+                                                gkr_qm31* round_polys, gkr_qm31* final_a, gkr_qm31* final_b) {
+  CH_CHECK(ch);
+  if (!c || !a_blocks || !b_blocks || !block_weights || !claim_value || !final_a || !final_b ||
+      (!claim_point && n_point))
+    return fail(GKR_ERR_INVALID, "null argument");
+  if (n_blocks == 0 || n_blocks > (uint32_t)kSimdMaxBlocks || (n_blocks & (n_blocks - 1)))
+    return fail(GKR_ERR_INVALID, "%u blocks (a power of two up to %d)", n_blocks, kSimdMaxBlocks);
+  if (!canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
+  const gkr_matrix* a = a_blocks[0];
+  const gkr_matrix* b = b_blocks[0];
+  if (!a || !b) return fail(GKR_ERR_INVALID, "null block");
+  std::vector<qm31> W(n_blocks);
+  for (uint32_t i = 0; i < n_blocks; i++) {
+    const gkr_matrix *ai = a_blocks[i], *bi = b_blocks[i];
+    if (!ai || !bi || ai->ctx != c || bi->ctx != c)
+      return fail(GKR_ERR_INVALID, "block %u missing or from another context", i);
+    if (ai->rows != a->rows || ai->cols != a->cols || bi->rows != b->rows || bi->cols != b->cols)
+      return fail(GKR_ERR_INVALID, "block %u shapes differ from block 0", i);
+    if (!canonical_q(block_weights[i])) return fail(GKR_ERR_INVALID, "block weight %u not canonical", i);
+    W[i] = Q(block_weights[i]);
+  }
+  const uint64_t pm = next_pow2(a->rows), pk = next_pow2(a->cols), pn = next_pow2(b->cols);
+  const uint32_t log_m = (uint32_t)log2_exact(pm), log_n = (uint32_t)log2_exact(pn);
+  const int T = log2_exact(pk), nbv = log2_exact(n_blocks);
+  if (n_point != log_m + log_n)
+    return fail(GKR_ERR_INVALID, "output claim has %u vars, expected exactly %u (log_m=%u + log_n=%u)", n_point,
+                log_m + log_n, log_m, log_n);
+  if (nbv + T > 0 && !round_polys) return fail(GKR_ERR_INVALID, "null output buffer");
+  TRY(validate_matmul(c, a, b, log_m, log_n));
+  std::vector<qm31> ri(log_m), rj(log_n);
+  for (uint32_t l = 0; l < log_m + log_n; l++)
+    if (!canonical_q(claim_point[l])) return fail(GKR_ERR_INVALID, "claim point coordinate %u not canonical", l);
+  for (uint32_t l = 0; l < log_m; l++) ri[l] = Q(claim_point[l]);
+  for (uint32_t l = 0; l < log_n; l++) rj[l] = Q(claim_point[log_m + l]);
+  HIP_TRY(hipSetDevice(c->device));
+  PoseidonChannel& C = ch->ch;
+  C.mix_u64(a->rows);
+  C.mix_u64(a->cols);
+  C.mix_u64(b->cols);
+  C.mix_u64(n_blocks);
+  C.mix_secure_field(Q(*claim_value));
+  c->mm.valid = false;
+  c->mm.have_trip0 = false;
+  // the blocks' restricted vectors, back to back
+  qm31 *ea, *eb, *gram;
+  TRY(ensureT(c, S_EXTA, n_blocks * pk, &ea));
+  TRY(ensureT(c, S_EXTB, n_blocks * pk, &eb));
+  TRY(ensureT(c, S_GRAM, (size_t)n_blocks * n_blocks, &gram));
+  for (uint32_t i = 0; i < n_blocks; i++) {
+    TRY(restrict_pair(c, a_blocks[i], b_blocks[i], ri.data(), (int)log_m, rj.data(), (int)log_n, pk));
+    TRY(finish_fb(c));
+    HIP_TRY(hipMemcpyAsync(ea + (uint64_t)i * pk, c->buf[S_FA0], pk * sizeof(qm31), hipMemcpyDeviceToDevice,
+                           c->stream));
+    HIP_TRY(hipMemcpyAsync(eb + (uint64_t)i * pk, c->buf[S_FB0], pk * sizeof(qm31), hipMemcpyDeviceToDevice,
+                           c->stream));
+  }
+  std::vector<qm31> D((size_t)n_blocks * n_blocks);
+  if (nbv > 0) {
+    hipLaunchKernelGGL(k_block_gram, dim3(n_blocks * n_blocks), dim3(kBlock), 0, c->stream, (const qm31*)ea,
+                       (const qm31*)eb, n_blocks, pk, gram);
+    TRY(check_launch());
+    HIP_TRY(hipMemcpyAsync(D.data(), gram, D.size() * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
+    TRY(sync(c));
+  }
+  // block rounds: for t = 0..3, s(t) = sum_rest W_t(rest) sum_{b1,b2} lam_t(b1) lam_t(b2) D[b1][b2] over the
+  // blocks b = (u, v, rest) with lam_t = eq(r_<j, u) * (v ? t : 1 - t)
+  const qm31 inv2 = qm31_from_m31(1u << 30), inv6 = qm31_from_m31(m31_inv(6));
+  const qm31 two = qm31_from_m31(2), three = qm31_from_m31(3);
+  std::vector<qm31> chal(nbv + T);
+  for (int j = 0; j < nbv; j++) {
+    std::vector<qm31> E((size_t)1 << j);
+    lagrange_weights(chal.data(), j, E.data());
+    const int rb = nbv - j - 1;  // bits below the current variable
+    qm31 sv[4];
+    for (int t = 0; t < 4; t++) {
+      const qm31 xt = qm31_from_m31((uint32_t)t), omt = qm31_sub(qm31_one(), xt);
+      qm31 st = qm31_zero();
+      for (uint32_t rest = 0; rest < (1u << rb); rest++) {
+        std::vector<uint32_t> idx;
+        std::vector<qm31> lam;
+        for (uint32_t u = 0; u < (1u << j); u++)
+          for (uint32_t v = 0; v < 2; v++) {
+            idx.push_back((u << (rb + 1)) | (v << rb) | rest);
+            lam.push_back(qm31_mul(E[u], v ? xt : omt));
+          }
+        qm31 wt = qm31_zero(), gt = qm31_zero();
+        for (size_t p1 = 0; p1 < idx.size(); p1++) {
+          wt = qm31_add(wt, qm31_mul(lam[p1], W[idx[p1]]));
+          qm31 row = qm31_zero();
+          for (size_t p2 = 0; p2 < idx.size(); p2++)
+            row = qm31_add(row, qm31_mul(lam[p2], D[(size_t)idx[p1] * n_blocks + idx[p2]]));
+          gt = qm31_add(gt, qm31_mul(lam[p1], row));
+        }
+        st = qm31_add(st, qm31_mul(wt, gt));
+      }
+      sv[t] = st;
+    }
+    // Newton differences to monomial coefficients (gpu_sumcheck.rs:2632-2640)
+    const qm31 d1 = qm31_sub(sv[1], sv[0]);
+    const qm31 d2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(sv[2], sv[1]), sv[1]), sv[0]), inv2);
+    const qm31 d3 = qm31_mul(qm31_sub(qm31_sub(sv[3], sv[0]), qm31_mul(three, qm31_sub(sv[2], sv[1]))), inv6);
+    const qm31 c0 = sv[0], c1 = qm31_add(qm31_sub(d1, d2), qm31_mul(two, d3)), c2 = qm31_sub(d2, qm31_mul(three, d3));
+    round_polys[4 * j + 0] = G(c0);
+    round_polys[4 * j + 1] = G(c1);
+    round_polys[4 * j + 2] = G(c2);
+    round_polys[4 * j + 3] = G(d3);
+    HostTimer ht(c, K_HOST_FS);
+    C.mix_poly_coeffs_deg3(c0, c1, c2, d3);
+    chal[j] = C.draw_qm31();
+  }
+  // the blocks folded by the block challenges: f_a, f_b and the weight
+  std::vector<qm31> lam((size_t)n_blocks);
+  lagrange_weights(chal.data(), nbv, lam.data());
+  qm31 wf = qm31_zero();
+  QWeights qw;
+  memset(&qw, 0, sizeof qw);
+  for (uint32_t i = 0; i < n_blocks; i++) {
+    wf = qm31_add(wf, qm31_mul(lam[i], W[i]));
+    qw.w[i] = lam[i];
+  }
+  qm31 *fa0, *fb0, *fa1, *fb1, *fa2, *fb2;
+  TRY(ensureT(c, S_FA0, pk, &fa0));
+  TRY(ensureT(c, S_FB0, pk, &fb0));
+  TRY(ensureT(c, S_FA1, pk / 2 + 1, &fa1));
+  TRY(ensureT(c, S_FB1, pk / 2 + 1, &fb1));
+  TRY(ensureT(c, S_FA2, pk / 4 + 1, &fa2));
+  TRY(ensureT(c, S_FB2, pk / 4 + 1, &fb2));
+  hipLaunchKernelGGL(k_combine_q, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, (const qm31*)ea, qw, n_blocks, pk,
+                     fa0);
+  hipLaunchKernelGGL(k_combine_q, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, (const qm31*)eb, qw, n_blocks, pk,
+                     fb0);
+  TRY(check_launch());
+  std::vector<gkr_qm31> kchal(T > 0 ? T : 1);
+  if (T == 0) {
+    qm31 v[1];
+    TRY(fetch_q(c, fa0, 1, v));
+    *final_a = G(v[0]);
+    TRY(fetch_q(c, fb0, 1, v));
+    *final_b = G(v[0]);
+  } else {
+    qm31* bufs_a[2] = {fa1, fa2};
+    qm31* bufs_b[2] = {fb1, fb2};
+    TRY(product_sumcheck(c, C, T, fa0, fb0, bufs_a, bufs_b, nullptr, 0, round_polys + 4 * nbv, kchal.data(), final_a,
+                         final_b, &wf));
+  }
+  C.mix_secure_field(Q(*final_a));
+  C.mix_secure_field(Q(*final_b));
+  if (proof) {
+    LayerRec L;
+    L.tag = 7;
+    L.n_block_vars = (uint32_t)nbv;
+    for (int t = 0; t < 4 * (nbv + T); t++) L.rp.push_back(Q(round_polys[t]));
+    L.final_a = Q(*final_a);
+    L.final_b = Q(*final_b);
+    proof->layers.push_back(L);
   }
   return GKR_OK;
 }

@@ -1056,6 +1056,34 @@ __global__ void __launch_bounds__(kSimdWaves * 64) k_restrict_rows_simd(SimdBloc
   }
 }
 
+// Dual-operand SIMD layer (both operands per block): the block Gram matrix
+// D[b1][b2] = sum_k fa[b1 pk + k] fb[b2 pk + k] of the blocks' restricted
+// vectors, one workgroup per (b1, b2), and the combination out[k] =
+// sum_b lam_b src[b pk + k] of the blocks' vectors by the block challenges'
+// Lagrange weights.
+__global__ void __launch_bounds__(kBlock) k_block_gram(const qm31* __restrict__ fa, const qm31* __restrict__ fb,
+                                                       uint32_t nb, uint64_t pk, qm31* __restrict__ D) {
+  const uint32_t b1 = blockIdx.x / nb, b2 = blockIdx.x % nb;
+  qacc acc;
+  acc.zero();
+  for (uint64_t k = threadIdx.x; k < pk; k += blockDim.x)
+    acc.add(qm31_mul(ld_q(fa, (uint64_t)b1 * pk + k), ld_q(fb, (uint64_t)b2 * pk + k)));
+  qm31 v[1] = {acc.reduce()};
+  block_sum_store<1>(v, D + blockIdx.x);
+}
+struct QWeights {
+  qm31 w[kSimdMaxBlocks];
+};
+__global__ void __launch_bounds__(kBlock) k_combine_q(const qm31* __restrict__ src, QWeights lam, uint32_t nb,
+                                                      uint64_t pk, qm31* __restrict__ out) {
+  const uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= pk) return;
+  qacc acc;
+  acc.zero();
+  for (uint32_t b = 0; b < nb; b++) acc.add(qm31_mul(lam.w[b], ld_q(src, (uint64_t)b * pk + k)));
+  st_q(out, k, acc.reduce());
+}
+
 // f_b[i] = sum over column chunks of partial[chunk * k + i] for i < k; 0 for k <= i < pk.
 __global__ void k_restrict_cols_finish(const qm31* __restrict__ partial, uint64_t k, uint64_t pk, int nchunks,
                                        qm31* __restrict__ out) {

@@ -137,6 +137,8 @@ SIGNATURES = [
     ("gkr_seed_channel", C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_uint64, _PF]),
     ("gkr_matmul_output_claim", C.c_int, [_P, _P, _P, _PQ, C.c_uint32, _PQ]),
     ("gkr_prove_matmul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ, _PQ]),
+    ("gkr_prove_matmul_layer_dual_simd", C.c_int,
+     [_P, _PQ, C.c_uint32, _PQ, C.POINTER(_P), C.POINTER(_P), _PQ, C.c_uint32, _P, _P, _PQ, _PQ, _PQ]),
     ("gkr_prove_matmul_layer_simd", C.c_int,
      [_P, _PQ, C.c_uint32, _PQ, C.POINTER(_P), _PQ, C.c_uint32, _P, _P, _P, _PQ, _PQ, _PQ, _PQ, _PQ]),
     ("gkr_prove_activation_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, C.c_uint32, C.c_uint32, _P, _P,
@@ -453,6 +455,25 @@ class Context:
         polys = [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2])) for t in range(T)]
         return {"round_polys": polys, "final_a_eval": q_from_c(fa), "final_b_eval": q_from_c(fb),
                 "next_point": [q_from_c(npnt[i]) for i in range(lm + T)], "next_value": q_from_c(nv)}
+
+    def prove_matmul_layer_dual_simd(self, claim_point, claim_value, a_blocks, b_blocks, block_weights,
+                                     ch: PoseidonChannel, proof: Optional["Proof"] = None):
+        """gkr_prove_matmul_layer_dual_simd: reduce_matmul_layer_dual_simd_gpu (gkr/prover.rs:5615-5785);
+        round polys are (c0, c1, c2, c3), block variables first."""
+        nb = len(a_blocks)
+        pk = 1 << (a_blocks[0].cols - 1).bit_length()
+        rounds = (nb.bit_length() - 1) + (pk.bit_length() - 1)
+        rp = (GkrQM31 * max(1, 4 * rounds))()
+        fa, fb = GkrQM31(), GkrQM31()
+        ha = (_P * nb)(*[m.handle for m in a_blocks])
+        hb = (_P * len(b_blocks))(*[m.handle for m in b_blocks])
+        _check(lib().gkr_prove_matmul_layer_dual_simd(self._h, q_array(claim_point), len(claim_point),
+                                                      C.byref(q_to_c(claim_value)), ha, hb, q_array(block_weights),
+                                                      nb, ch.handle, proof.handle if proof else None, rp,
+                                                      C.byref(fa), C.byref(fb)))
+        polys = [tuple(q_from_c(rp[4 * t + i]) for i in range(4)) for t in range(rounds)]
+        return {"round_polys": polys, "final_a_eval": q_from_c(fa), "final_b_eval": q_from_c(fb),
+                "n_block_vars": nb.bit_length() - 1}
 
     def qvec_upload(self, vals) -> "QVec":
         a = np.ascontiguousarray(vals, dtype=np.uint32).reshape(-1, 4)
