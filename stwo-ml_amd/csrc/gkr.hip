@@ -1757,13 +1757,26 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
   TRY(ensureT(c, S_EXTA, n_blocks * pk, &ea));
   TRY(ensureT(c, S_EXTB, n_blocks * pk, &eb));
   TRY(ensureT(c, S_GRAM, (size_t)n_blocks * n_blocks, &gram));
-  for (uint32_t i = 0; i < n_blocks; i++) {
-    TRY(restrict_pair(c, a_blocks[i], b_blocks[i], ri.data(), (int)log_m, rj.data(), (int)log_n, pk));
-    TRY(finish_fb(c));
-    HIP_TRY(hipMemcpyAsync(ea + (uint64_t)i * pk, c->buf[S_FA0], pk * sizeof(qm31), hipMemcpyDeviceToDevice,
-                           c->stream));
-    HIP_TRY(hipMemcpyAsync(eb + (uint64_t)i * pk, c->buf[S_FB0], pk * sizeof(qm31), hipMemcpyDeviceToDevice,
-                           c->stream));
+  {
+    // the blocks share the claim point: both Lagrange tables once, then each side for all blocks
+    HostTimer ht(c, K_HOST_LAUNCH);
+    qm31 *Li, *Lj;
+    TRY(ensureT(c, S_LI, a->rows, &Li));
+    TRY(ensureT(c, S_LJ, b->cols, &Lj));
+    TRY(eq_table(c, ri.data(), (int)log_m, a->rows, Li));
+    TRY(eq_table(c, rj.data(), (int)log_n, b->cols, Lj));
+    BlockPtrs pa, pb;
+    memset(&pa, 0, sizeof pa);
+    memset(&pb, 0, sizeof pb);
+    for (uint32_t i = 0; i < n_blocks; i++) {
+      pa.p[i] = a_blocks[i]->dev;
+      pb.p[i] = b_blocks[i]->dev;
+    }
+    hipLaunchKernelGGL(k_restrict_rows_blocks, dim3(grid_for(pk), n_blocks), dim3(kBlock), 0, c->stream, pa, a->rows,
+                       a->cols, pk, (const qm31*)Li, ea);
+    hipLaunchKernelGGL(k_restrict_cols_blocks, dim3((unsigned)((pk + kColWaves - 1) / kColWaves), n_blocks),
+                       dim3(kBlock), 0, c->stream, pb, b->rows, b->cols, pk, (const qm31*)Lj, eb);
+    TRY(check_launch());
   }
   std::vector<qm31> D((size_t)n_blocks * n_blocks);
   if (nbv > 0) {
@@ -1773,36 +1786,26 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
     HIP_TRY(hipMemcpyAsync(D.data(), gram, D.size() * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
     TRY(sync(c));
   }
-  // block rounds: for t = 0..3, s(t) = sum_rest W_t(rest) sum_{b1,b2} lam_t(b1) lam_t(b2) D[b1][b2] over the
-  // blocks b = (u, v, rest) with lam_t = eq(r_<j, u) * (v ? t : 1 - t)
+  // block rounds on the Gram matrix: with the block variables above bound, D is folded to the remaining
+  // blocks (D'[x][y] = sum_{v,v'} l(v) l(v') D[v h + x][v' h + y], l(0) = 1 - r, l(1) = r) and so is W;
+  // s(t) = sum_{x < h} W_t(x) sum_{v,v'} l_t(v) l_t(v') D[v h + x][v' h + x] with l_t at t = 0..3
   const qm31 inv2 = qm31_from_m31(1u << 30), inv6 = qm31_from_m31(m31_inv(6));
   const qm31 two = qm31_from_m31(2), three = qm31_from_m31(3);
   std::vector<qm31> chal(nbv + T);
+  std::vector<qm31> Wc(W);
+  size_t N = n_blocks;
   for (int j = 0; j < nbv; j++) {
-    std::vector<qm31> E((size_t)1 << j);
-    lagrange_weights(chal.data(), j, E.data());
-    const int rb = nbv - j - 1;  // bits below the current variable
+    const size_t h = N / 2;
     qm31 sv[4];
     for (int t = 0; t < 4; t++) {
-      const qm31 xt = qm31_from_m31((uint32_t)t), omt = qm31_sub(qm31_one(), xt);
+      const qm31 l1 = qm31_from_m31((uint32_t)t), l0 = qm31_sub(qm31_one(), l1);
+      const qm31 l00 = qm31_mul(l0, l0), l01 = qm31_mul(l0, l1), l11 = qm31_mul(l1, l1);
       qm31 st = qm31_zero();
-      for (uint32_t rest = 0; rest < (1u << rb); rest++) {
-        std::vector<uint32_t> idx;
-        std::vector<qm31> lam;
-        for (uint32_t u = 0; u < (1u << j); u++)
-          for (uint32_t v = 0; v < 2; v++) {
-            idx.push_back((u << (rb + 1)) | (v << rb) | rest);
-            lam.push_back(qm31_mul(E[u], v ? xt : omt));
-          }
-        qm31 wt = qm31_zero(), gt = qm31_zero();
-        for (size_t p1 = 0; p1 < idx.size(); p1++) {
-          wt = qm31_add(wt, qm31_mul(lam[p1], W[idx[p1]]));
-          qm31 row = qm31_zero();
-          for (size_t p2 = 0; p2 < idx.size(); p2++)
-            row = qm31_add(row, qm31_mul(lam[p2], D[(size_t)idx[p1] * n_blocks + idx[p2]]));
-          gt = qm31_add(gt, qm31_mul(lam[p1], row));
-        }
-        st = qm31_add(st, qm31_mul(wt, gt));
+      for (size_t x = 0; x < h; x++) {
+        const qm31 wt = qm31_add(qm31_mul(l0, Wc[x]), qm31_mul(l1, Wc[h + x]));
+        const qm31 g = qm31_add(qm31_add(qm31_mul(l00, D[x * N + x]), qm31_mul(l11, D[(h + x) * N + h + x])),
+                                qm31_mul(l01, qm31_add(D[x * N + h + x], D[(h + x) * N + x])));
+        st = qm31_add(st, qm31_mul(wt, g));
       }
       sv[t] = st;
     }
@@ -1815,9 +1818,24 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
     round_polys[4 * j + 1] = G(c1);
     round_polys[4 * j + 2] = G(c2);
     round_polys[4 * j + 3] = G(d3);
-    HostTimer ht(c, K_HOST_FS);
-    C.mix_poly_coeffs_deg3(c0, c1, c2, d3);
-    chal[j] = C.draw_qm31();
+    {
+      HostTimer ht(c, K_HOST_FS);
+      C.mix_poly_coeffs_deg3(c0, c1, c2, d3);
+      chal[j] = C.draw_qm31();
+    }
+    const qm31 r1 = chal[j], r0 = qm31_sub(qm31_one(), r1);
+    std::vector<qm31> Dn(h * h), Wn(h);
+    for (size_t x = 0; x < h; x++) {
+      Wn[x] = qm31_add(qm31_mul(r0, Wc[x]), qm31_mul(r1, Wc[h + x]));
+      for (size_t y = 0; y < h; y++) {
+        const qm31 top = qm31_add(qm31_mul(r0, D[x * N + y]), qm31_mul(r1, D[x * N + h + y]));
+        const qm31 bot = qm31_add(qm31_mul(r0, D[(h + x) * N + y]), qm31_mul(r1, D[(h + x) * N + h + y]));
+        Dn[x * h + y] = qm31_add(qm31_mul(r0, top), qm31_mul(r1, bot));
+      }
+    }
+    D.swap(Dn);
+    Wc.swap(Wn);
+    N = h;
   }
   // the blocks folded by the block challenges: f_a, f_b and the weight
   std::vector<qm31> lam((size_t)n_blocks);

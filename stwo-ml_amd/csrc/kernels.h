@@ -1071,6 +1071,70 @@ __global__ void __launch_bounds__(kBlock) k_block_gram(const qm31* __restrict__ 
   qm31 v[1] = {acc.reduce()};
   block_sum_store<1>(v, D + blockIdx.x);
 }
+// Restrictions of every block of a dual-operand SIMD layer in one launch each
+// (the blocks share the claim point, so L_i and L_j are built once):
+// rows: ea[b pk + x] = sum_i L_i A_b[i][x] (0 for k <= x < pk), one thread per
+// (x, b) with blockIdx.y = b; cols: eb[b pk + x] = sum_j B_b[x][j] L_j, one
+// wave per (x, b) reading row x of B_b with coalesced loads.
+struct BlockPtrs {
+  const uint32_t* p[kSimdMaxBlocks];
+};
+__global__ void __launch_bounds__(kBlock) k_restrict_rows_blocks(BlockPtrs a, uint64_t m, uint64_t k, uint64_t pk,
+                                                                 const qm31* __restrict__ L, qm31* __restrict__ ea) {
+  const uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t b = blockIdx.y;
+  if (x >= pk) return;
+  qm31* out = ea + (uint64_t)b * pk;
+  if (x >= k) {
+    st_q(out, x, qm31_zero());
+    return;
+  }
+  const uint32_t* A = a.p[b];
+  uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+  for (uint64_t i = 0; i < m; i += 4) {
+    uint64_t t[4] = {0, 0, 0, 0};  // 4 rows: 4 * (P-1)^2 < 2^64
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      if (i + u < m) {
+        const uint64_t v = A[(i + u) * k + x];
+        const qm31 l = ld_q(L, i + u);
+        t[0] += v * l.a; t[1] += v * l.b; t[2] += v * l.c; t[3] += v * l.d;
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+  }
+  uint32_t r[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
+  st_q(out, x, qm31{r[0], r[1], r[2], r[3]});
+}
+__global__ void __launch_bounds__(kBlock) k_restrict_cols_blocks(BlockPtrs bm, uint64_t k, uint64_t n, uint64_t pk,
+                                                                 const qm31* __restrict__ L, qm31* __restrict__ eb) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t x = (uint64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  const uint32_t b = blockIdx.y;
+  if (x >= pk) return;  // whole wave
+  qm31* out = eb + (uint64_t)b * pk;
+  uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
+  if (x < k) {
+    const uint32_t* row = bm.p[b] + x * n;
+    for (uint64_t j = lane; j < n; j += 64) {
+      const uint64_t v = row[j];
+      const qm31 l = ld_q(L, j);
+      const uint64_t t0 = v * l.a, t1 = v * l.b, t2 = v * l.c, t3 = v * l.d;  // each < 2^62
+      lo[0] += (uint32_t)t0; hi[0] += t0 >> 32;
+      lo[1] += (uint32_t)t1; hi[1] += t1 >> 32;
+      lo[2] += (uint32_t)t2; hi[2] += t2 >> 32;
+      lo[3] += (uint32_t)t3; hi[3] += t3 >> 32;
+    }
+  }
+  uint32_t r[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
+  qm31 v = wave_sum(qm31{r[0], r[1], r[2], r[3]});
+  if (lane == 0) st_q(out, x, v);
+}
 struct QWeights {
   qm31 w[kSimdMaxBlocks];
 };
