@@ -1854,10 +1854,9 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
   TRY(ensureT(c, S_FB1, pk / 2 + 1, &fb1));
   TRY(ensureT(c, S_FA2, pk / 4 + 1, &fa2));
   TRY(ensureT(c, S_FB2, pk / 4 + 1, &fb2));
-  hipLaunchKernelGGL(k_combine_q, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, (const qm31*)ea, qw, n_blocks, pk,
-                     fa0);
-  hipLaunchKernelGGL(k_combine_q, dim3(grid_for(pk)), dim3(kBlock), 0, c->stream, (const qm31*)eb, qw, n_blocks, pk,
-                     fb0);
+  const dim3 gq((unsigned)((pk + kColWaves - 1) / kColWaves));  // one wave per entry
+  hipLaunchKernelGGL(k_combine_q, gq, dim3(kBlock), 0, c->stream, (const qm31*)ea, qw, n_blocks, pk, fa0);
+  hipLaunchKernelGGL(k_combine_q, gq, dim3(kBlock), 0, c->stream, (const qm31*)eb, qw, n_blocks, pk, fb0);
   TRY(check_launch());
   std::vector<gkr_qm31> kchal(T > 0 ? T : 1);
   if (T == 0) {

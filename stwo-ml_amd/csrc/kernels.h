@@ -1140,12 +1140,13 @@ struct QWeights {
 };
 __global__ void __launch_bounds__(kBlock) k_combine_q(const qm31* __restrict__ src, QWeights lam, uint32_t nb,
                                                       uint64_t pk, qm31* __restrict__ out) {
-  const uint64_t k = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= pk) return;
-  qacc acc;
-  acc.zero();
-  for (uint32_t b = 0; b < nb; b++) acc.add(qm31_mul(lam.w[b], ld_q(src, (uint64_t)b * pk + k)));
-  st_q(out, k, acc.reduce());
+  // one wave per entry k, lane b multiplies block b's entry (nb <= 64), then a wave sum
+  const int lane = threadIdx.x & 63;
+  const uint64_t k = (uint64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+  if (k >= pk) return;  // whole wave
+  const qm31 v = (uint32_t)lane < nb ? qm31_mul(lam.w[lane], ld_q(src, (uint64_t)lane * pk + k)) : qm31_zero();
+  const qm31 sum = wave_sum(v);
+  if (lane == 0) st_q(out, k, sum);
 }
 
 // f_b[i] = sum over column chunks of partial[chunk * k + i] for i < k; 0 for k <= i < pk.
