@@ -566,7 +566,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(see the sharding design in DESIGN.md)", file=sys.stderr)
+              "(the path is measured on one GPU's share)", file=sys.stderr)
         sys.exit(2)
 
     if args.int8_weights:
