@@ -223,8 +223,10 @@ static hipEvent_t get_event(gkr_ctx* c) {
     c->free_events.pop_back();
     return e;
   }
+  // timing-only events: no system-scope fence (cache writeback) when they are
+  // recorded, so the pair brackets the kernel and not the cache maintenance
   hipEvent_t e = nullptr;
-  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
   return e;
 }
 struct TimedLaunch {
