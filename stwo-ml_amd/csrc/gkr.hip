@@ -1172,10 +1172,10 @@ static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* 
 // short (the device trips stop there; k_handover folds the last trip's
 // vectors and hands them over).
 #ifndef GKR_HOST_TAIL_MM
-#define GKR_HOST_TAIL_MM 128   // product sumcheck: 5 QM31 products per pair
+#define GKR_HOST_TAIL_MM 256   // product sumcheck: 5 QM31 products per pair
 #endif
 #ifndef GKR_HOST_TAIL_EQ3
-#define GKR_HOST_TAIL_EQ3 128  // eq-sumcheck: 11 products per pair
+#define GKR_HOST_TAIL_EQ3 256  // eq-sumcheck: 11 products per pair
 #endif
 #ifndef GKR_HOST_TAIL_SUM
 #define GKR_HOST_TAIL_SUM 256  // multiplicity sumcheck: 1 product per pair
