@@ -110,6 +110,16 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
 int gkr_ctx_set_timing(gkr_ctx* ctx, int level);
 int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);
 int gkr_ctx_reset_timing(gkr_ctx* ctx);
+/* Test hooks for the failure paths of the hand-over (no counterpart in the
+ * reference).  Each applies to the next sumcheck hand-over on the context:
+ *   GKR_DEBUG_HANDOVER_CANCEL: the host leaves before posting the last
+ *     challenges, as on an error; the call fails with GKR_ERR_DEVICE and the
+ *     kernel ends on the cancel code;
+ *   GKR_DEBUG_HANDOVER_EXPIRE: the kernel's bounded wait is `arg` polls and
+ *     the host posts only after it expired; the call fails with GKR_ERR_DEVICE.
+ * Every kernel exits normally and the context stays usable.                 */
+enum { GKR_DEBUG_HANDOVER_CANCEL = 1, GKR_DEBUG_HANDOVER_EXPIRE = 2 };
+int gkr_ctx_debug(gkr_ctx* ctx, int op, uint64_t arg);
 
 /* ------------------------------------------------------------------ resident matrices
  * The reference re-uploads A and B on every restriction
@@ -254,6 +264,8 @@ int gkr_qvec_upload(gkr_ctx* ctx, const gkr_qm31* host, uint64_t n, gkr_qvec** o
 int gkr_qvec_synthetic(gkr_ctx* ctx, uint64_t n, uint64_t seed, gkr_qvec** out);
 int gkr_qvec_download(gkr_ctx* ctx, const gkr_qvec* v, gkr_qm31* host);
 void gkr_qvec_free(gkr_qvec* v);
+/* Device address of a vector's n QM31 (for device-pointer entry points). */
+const gkr_qm31* gkr_qvec_device_ptr(const gkr_qvec* v);
 int gkr_sumcheck_product(gkr_ctx* ctx, const gkr_qvec* fa, const gkr_qvec* fb, gkr_channel* ch,
                          gkr_qm31* round_polys /* 3T: c0, c1, c2 */, gkr_qm31* challenges /* T */,
                          gkr_qm31* final_a, gkr_qm31* final_b);

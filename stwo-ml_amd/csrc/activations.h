@@ -88,6 +88,11 @@ inline uint32_t act_silu(uint32_t v) {
 }
 
 inline bool act_valid(uint32_t tag) { return tag >= ACT_RELU && tag <= ACT_SILU; }
+// Activations the reference proves with the LogUp reducer.  ReLU never goes
+// through it: every dispatch sends ReLU to the algebraic proof
+// (engine/src/gkr/prover.rs:1770-1776), so a LogUp proof of ReLU could not be
+// byte-identical to the reference's and is refused.
+inline bool act_logup_valid(uint32_t tag) { return act_valid(tag) && tag != ACT_RELU; }
 
 inline uint32_t act_apply(uint32_t tag, uint32_t v) {
   switch (tag) {

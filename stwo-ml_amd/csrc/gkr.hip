@@ -179,6 +179,9 @@ struct gkr_ctx {
   uint32_t trip_count = 0;         // value of the fused trips' arrival counter (S_TRIPCNT) after the queued launches
   bool trip_count_valid = false;   // false: zero the counter before the next fused trip
   bool int8_weights = false;       // GKR_INT8_WEIGHTS=1 at creation: int8 weight-side restriction
+  // test hooks (gkr_ctx_debug), each consumed by the next hand-over
+  bool debug_handover_cancel = false;  // the host leaves before posting the challenges
+  uint32_t debug_handover_spins = 0;   // nonzero: the kernel's bounded wait, posted only after it expired
 };
 
 static int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
@@ -327,8 +330,8 @@ static int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out)
 }
 
 // Result and mailbox sequence numbers come in consecutive ranges and restart
-// at 1 before they reach the codes reserved at the top of the u32 range
-// (kWaitTimeout, kWaitCancel); waits compare them modulo 2^32.
+// at 1 before they reach the cancel code reserved at the top of the u32 range
+// (kWaitCancel); waits compare them modulo 2^32.
 constexpr uint32_t kSeqLimit = 0xFFFFFF00u;
 static uint32_t alloc_seq(uint32_t* counter, uint32_t n) {
   if (*counter >= kSeqLimit - n) *counter = 0;
@@ -359,23 +362,35 @@ static int launch_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks) {
   return check_launch();
 }
 // Wait until result `seq` has been published and copy NQ values.  The wait
-// spins on the coherent flag; after ~2 s without it the stream is
-// synchronised so that a device error is reported instead of hanging.
+// spins on the coherent flag and never blocks on the stream (a hand-over
+// kernel queued behind the result may be waiting for the host): from time to
+// time it queries the stream, so a device error, or a drained stream without
+// the result, is reported; after kWaitWallSeconds it gives up.  hand_mb != 0:
+// the result comes from the hand-over waiting for mailbox sequence hand_mb,
+// whose expiry is reported at once.
+constexpr double kWaitWallSeconds = 60.0;
 template <int NQ>
-static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_HOST_WAIT_TAIL, int slot = 0) {
+static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_HOST_WAIT_TAIL, int slot = 0,
+                       uint32_t hand_mb = 0) {
   TRY(check_launch());
   HostTimer ht(c, timer);
   volatile uint32_t* flag = c->h_flag;
-  uint64_t spins = 0;
-  uint32_t got;
+  volatile uint32_t* expired = &c->mailbox->expired;
+  std::chrono::steady_clock::time_point t0;
   // the flag only moves forward (mod 2^32): a later delivery implies this one
-  while ((int32_t)((got = *flag) - seq) < 0 || got == kWaitTimeout) {
-    if (got == kWaitTimeout) return fail(GKR_ERR_DEVICE, "hand-over kernel timed out waiting for the challenges");
-    if (++spins == (1u << 26)) {
-      HIP_TRY(hipStreamSynchronize(c->stream));
-      if ((int32_t)(*flag - seq) < 0) return fail(GKR_ERR_DEVICE, "device result %u not delivered", seq);
-      break;
+  for (uint64_t spins = 0; (int32_t)(*flag - seq) < 0; spins++) {
+    if (hand_mb && *expired == hand_mb)
+      return fail(GKR_ERR_DEVICE, "hand-over kernel stopped waiting for the challenges (mailbox %u)", hand_mb);
+    if ((spins & 0xFFFF) != 0xFFFF) continue;
+    if (spins == 0xFFFF) t0 = std::chrono::steady_clock::now();
+    const hipError_t e = hipStreamQuery(c->stream);
+    if (e == hipSuccess) {
+      if ((int32_t)(*flag - seq) >= 0) break;
+      return fail(GKR_ERR_DEVICE, "device result %u not delivered (stream drained)", seq);
     }
+    if (e != hipErrorNotReady) return fail(GKR_ERR_DEVICE, "waiting for device result %u: %s", seq, hipGetErrorString(e));
+    if (std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > kWaitWallSeconds)
+      return fail(GKR_ERR_DEVICE, "device result %u not delivered after %.0f s", seq, kWaitWallSeconds);
   }
   __atomic_thread_fence(__ATOMIC_ACQUIRE);
   for (int q = 0; q < NQ; q++) host_out[q] = c->h_out[slot + q];
@@ -388,11 +403,14 @@ static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
 // Host side of a k_handover launch: posts the last trip's challenges into
 // the mailbox and receives the folded vectors.  If the host leaves before
 // posting (an error), the guard posts the cancel code so the kernel stops
-// waiting at once, and drains the stream before the mailbox is reused.
+// waiting at once, drains the stream, and clears the mailbox so that the
+// next hand-over does not read the cancel code.
 struct HandoverSession {
   gkr_ctx* c;
   uint32_t res_seq = 0, mb_seq = 0;
   bool launched = false, done = false;
+  bool cancel_before_post = false;  // test hook (gkr_ctx_debug): leave without posting
+  bool hold_post = false;           // test hook (gkr_ctx_debug): post only after the kernel's wait expired
   explicit HandoverSession(gkr_ctx* c_) : c(c_) {}
   // Launch k_handover<NV> over the vectors a (, b) of length len, to be folded by k challenges.
   template <int NV>
@@ -402,18 +420,36 @@ struct HandoverSession {
       return fail(GKR_ERR_DEVICE, "hand-over of %llu entries folded %d times", (unsigned long long)len, k);
     res_seq = alloc_seq(&c->seq, 1);
     mb_seq = alloc_seq(&c->mb_seq, 1);
+    uint32_t spin_limit = kWaitSpinLimit;
+    if (c->debug_handover_spins) {  // test hook: a short bounded wait that expires before the post
+      spin_limit = c->debug_handover_spins;
+      c->debug_handover_spins = 0;
+      hold_post = true;
+    }
+    if (c->debug_handover_cancel) {
+      cancel_before_post = true;
+      c->debug_handover_cancel = false;
+    }
     hipLaunchKernelGGL(k_handover<NV>, dim3(1), dim3(kBlock), 0, c->stream, a, b, (uint32_t)len, k, c->mailbox,
-                       mb_seq, c->h_vec, c->h_flag, res_seq);
+                       mb_seq, spin_limit, c->h_vec, c->h_flag, res_seq);
     launched = true;
     return check_launch();
   }
-  void post(const qm31* chal, int k) {
+  int post(const qm31* chal, int k) {
+    if (cancel_before_post) return fail(GKR_ERR_DEVICE, "hand-over cancelled before the challenges were posted");
+    if (hold_post) {
+      const auto t0 = std::chrono::steady_clock::now();
+      volatile uint32_t* expired = &c->mailbox->expired;
+      while (*expired != mb_seq && std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() < 10.0) {
+      }
+    }
     for (int r = 0; r < k; r++) c->mailbox->alpha[r] = chal[r];
     __atomic_store_n(&c->mailbox->seq, mb_seq, __ATOMIC_RELEASE);
+    return GKR_OK;
   }
   // Wait for the folded vectors: count vectors of len entries each.
   int fetch(uint64_t len, int count, std::vector<qm31>* out) {
-    TRY(wait_result<0>(c, res_seq, nullptr));
+    TRY(wait_result<0>(c, res_seq, nullptr, K_HOST_WAIT_TAIL, 0, mb_seq));
     for (int v = 0; v < count; v++) out[v].assign(c->h_vec + v * len, c->h_vec + (v + 1) * len);
     done = true;
     return GKR_OK;
@@ -422,6 +458,7 @@ struct HandoverSession {
     if (launched && !done) {
       __atomic_store_n(&c->mailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
       (void)hipStreamSynchronize(c->stream);
+      __atomic_store_n(&c->mailbox->seq, 0u, __ATOMIC_RELEASE);  // 0 is never a wanted sequence
     }
   }
 };
@@ -569,7 +606,8 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
   if (GKR_TRIP_FUSED && grid <= kTripFusedMax) {  // one launch: the last workgroup finishes
     TRY(ensureT(c, S_TRIPCNT, 1, &counter));
     if (!c->trip_count_valid) {
-      HIP_TRY(hipMemsetAsync(counter, 0, sizeof(uint32_t), c->stream));
+      hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, c->stream, counter, 1u);
+      TRY(check_launch());
       c->trip_count = 0;
       c->trip_count_valid = true;
     }
@@ -822,6 +860,7 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   *c->h_flag = 0;
   c->mailbox = reinterpret_cast<Mailbox*>(reinterpret_cast<char*>(c->h_out) + kOutSlots * sizeof(qm31) + 128);
   c->mailbox->seq = 0;
+  c->mailbox->expired = 0;
   *out = c;
   return GKR_OK;
 }
@@ -857,6 +896,17 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   if (c->h_out) (void)hipHostFree(c->h_out);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
+}
+extern "C" int gkr_ctx_debug(gkr_ctx* c, int op, uint64_t arg) {
+  if (!c) return fail(GKR_ERR_INVALID, "null ctx");
+  switch (op) {
+    case GKR_DEBUG_HANDOVER_CANCEL: c->debug_handover_cancel = true; return GKR_OK;
+    case GKR_DEBUG_HANDOVER_EXPIRE:
+      if (arg == 0 || arg > kWaitSpinLimit) return fail(GKR_ERR_INVALID, "spin limit %llu", (unsigned long long)arg);
+      c->debug_handover_spins = (uint32_t)arg;
+      return GKR_OK;
+    default: return fail(GKR_ERR_INVALID, "unknown debug op %d", op);
+  }
 }
 extern "C" int gkr_ctx_synchronize(gkr_ctx* c) {
   if (!c) return fail(GKR_ERR_INVALID, "null ctx");
@@ -1264,7 +1314,7 @@ static int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* 
   const int t_end = trips.empty() ? 0 : trips.back().t + trips.back().K;
   const uint64_t hlen = pk >> t_end;
   std::vector<qm31> v[2];
-  ho.post(pend, np);
+  TRY(ho.post(pend, np));
   TRY(ho.fetch(hlen, 2, v));
   std::vector<qm31>& A = v[0];
   std::vector<qm31>& B = v[1];
@@ -2092,7 +2142,7 @@ static int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3
   const int t_end = pl.trips.back().t + pl.trips.back().K;
   const uint64_t hlen = 1ull << (nv - t_end);
   std::vector<qm31> v[2];
-  ho.post(pend, np);
+  TRY(ho.post(pend, np));
   TRY(ho.fetch(hlen, 2, v));
   std::vector<qm31>& W = v[0];
   std::vector<qm31>& D = v[1];
@@ -2144,6 +2194,8 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   CH_CHECK(ch);
   if (!c || !input || !claim_value || !out || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
   if (!act_valid(tag)) return fail(GKR_ERR_INVALID, "unknown activation type %u", tag);
+  if (!act_logup_valid(tag))
+    return fail(GKR_ERR_INVALID, "activation type %u (ReLU) is proved algebraically, not by LogUp", tag);
   if (table_log == 0) table_log = act_default_log_size(tag);
   if (table_log > 24) return fail(GKR_ERR_INVALID, "table_log_size %u too large", table_log);
   if (input->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another context");
@@ -2317,7 +2369,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     }
     const int t_end = mtrips.back().t + mtrips.back().K;
     std::vector<qm31> v[1];
-    ho.post(pend, np);
+    TRY(ho.post(pend, np));
     TRY(ho.fetch(tsize >> t_end, 1, v));
     std::vector<qm31>& V = v[0];
     for (int t = t_end; t < (int)table_log; t++) {
@@ -2455,6 +2507,9 @@ extern "C" int gkr_qvec_download(gkr_ctx* c, const gkr_qvec* v, gkr_qm31* host) 
   if (v->ctx != c) return fail(GKR_ERR_INVALID, "vector belongs to another (or a destroyed) context");
   HIP_TRY(hipMemcpyAsync(host, v->dev, v->n * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
   return sync(c);
+}
+extern "C" const gkr_qm31* gkr_qvec_device_ptr(const gkr_qvec* v) {
+  return v ? reinterpret_cast<const gkr_qm31*>(v->dev) : nullptr;
 }
 extern "C" void gkr_qvec_free(gkr_qvec* v) {
   if (!v) return;
@@ -3399,6 +3454,8 @@ extern "C" int gkr_verify_activation_layer(const gkr_qm31* claim_point, uint32_t
   CH_CHECK(ch);
   if (!proof || !next_value || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
   if (!act_valid(activation_type)) return fail(GKR_ERR_INVALID, "unknown activation type %u", activation_type);
+  if (!act_logup_valid(activation_type))
+    return fail(GKR_ERR_INVALID, "activation type %u (ReLU) is proved algebraically, not by LogUp", activation_type);
   if (table_log_size == 0) table_log_size = act_default_log_size(activation_type);
   if (table_log_size > 24) return fail(GKR_ERR_INVALID, "table_log_size %u too large", table_log_size);
   if ((n_eq_rounds && !proof->eq_round_polys) || !proof->multiplicities || !proof->mult_round_polys)
@@ -3492,6 +3549,7 @@ extern "C" int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const g
       if (R.ok && act != L.activation_type)
         return bad(at + "activation type " + std::to_string(act) + ", circuit " + std::to_string(L.activation_type));
       if (!act_valid(act)) return bad(at + "unknown activation type");
+      if (!act_logup_valid(act)) return bad(at + "ReLU is proved algebraically, not by LogUp");
       const uint32_t tlog = L.table_log_size ? L.table_log_size : act_default_log_size(act);
       if (tlog > 24) return bad(at + "table size too large");
       LogUpProofIn p;

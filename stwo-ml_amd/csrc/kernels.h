@@ -406,12 +406,17 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
   __shared__ bool sh_last;
   wait_memory();  // this workgroup's row is in memory before it is counted
   __syncthreads();
+  // The arrival count is an acquire-release operation at agent scope: its
+  // release publishes this workgroup's row (ordered before it by the barrier),
+  // and in the last workgroup its acquire, extended to every wave by the
+  // barrier and an agent-scope acquire fence, makes all rows visible.
   if (threadIdx.x == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     sh_last = old == count_base + gridDim.x - 1;
   }
   __syncthreads();
   if (!sh_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   // the last workgroup: thread t adds column t % NQ over every (kBlock / NQ)-th row
   constexpr int RG = S::NQ < kBlock ? kBlock / S::NQ : 1;
   constexpr int MR = (int)((kTripFusedMax + RG - 1) / RG);  // rows per thread, all loads in flight at once
@@ -480,24 +485,26 @@ __global__ void __launch_bounds__(kFinishBlock) k_finish_wide(RoundSink sk, uint
 // challenges) into LDS while the host works on the trip's rounds, waits for
 // the k challenges (mailbox seq `want`), folds, and hands the vectors
 // (len >> k entries each, one after another) to vec_out in coherent host
-// memory, then publishes `seq`.  The wait is bounded: after kWaitSpinLimit
-// polls without `want` (or on the cancel code) the kernel publishes
-// kWaitTimeout in the result flag and returns, so every wave always exits.
+// memory, then publishes `seq`.  The wait is bounded: after spin_limit
+// polls without `want` (or on the cancel code) the kernel writes `want` into
+// the mailbox's `expired` word and returns without publishing, so every wave
+// always exits and the shared result flag only ever holds sequence numbers.
 constexpr int kHandMax = 2048;
-constexpr uint64_t kWaitSpinLimit = 1ull << 22;
-constexpr uint32_t kWaitTimeout = 0xFFFFFFFFu;
+constexpr uint32_t kWaitSpinLimit = 1u << 22;
 constexpr uint32_t kWaitCancel = 0xFFFFFFFEu;
 
 struct Mailbox {
-  uint32_t seq;
-  uint32_t pad[3];
+  uint32_t seq;      // host -> device: sequence number of the posted challenges
+  uint32_t expired;  // device -> host: the `want` of the last wait that ended without them
+  uint32_t pad[2];
   qm31 alpha[kTripMaxK];
 };
 
 template <int NV>
 __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a, const qm31* __restrict__ b,
                                                      uint32_t len, int k, Mailbox* mb, uint32_t want,
-                                                     qm31* vec_out, uint32_t* flag, uint32_t seq) {
+                                                     uint32_t spin_limit, qm31* vec_out, uint32_t* flag,
+                                                     uint32_t seq) {
   __shared__ qm31 v[NV][kHandMax];
   __shared__ qm31 sh_al[kTripMaxK];
   __shared__ bool sh_ok;
@@ -507,7 +514,7 @@ __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a,
   }
   if (threadIdx.x == 0) {
     bool ok = false;
-    for (uint64_t spins = 0; spins < kWaitSpinLimit; spins++) {
+    for (uint32_t spins = 0; spins < spin_limit; spins++) {
       const uint32_t got = __hip_atomic_load(&mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
       if (got == want) {
         ok = true;
@@ -522,7 +529,7 @@ __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a,
         sh_al[r] = qm31{q[0], q[1], q[2], q[3]};
       }
     } else {
-      publish_flag(flag, kWaitTimeout);
+      __hip_atomic_store(&mb->expired, want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     sh_ok = ok;
   }
@@ -1162,6 +1169,10 @@ __global__ void k_restrict_cols_finish(const qm31* __restrict__ partial, uint64_
   acc.zero();
   for (int c = 0; c < nchunks; c++) acc.add(ld_q(partial, (uint64_t)c * k + i));
   st_q(out, i, acc.reduce());
+}
+__global__ void k_zero_u32(uint32_t* __restrict__ out, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = 0u;
 }
 __global__ void k_zero_q(qm31* __restrict__ out, uint64_t from, uint64_t to) {
   uint64_t i = from + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -117,6 +117,7 @@ SIGNATURES = [
     ("gkr_ctx_kernel_time", C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_uint64),
                                       C.POINTER(C.c_uint64)]),
     ("gkr_ctx_reset_timing", C.c_int, [_P]),
+    ("gkr_ctx_debug", C.c_int, [_P, C.c_int, C.c_uint64]),
     ("gkr_matrix_upload", C.c_int, [_P, _U32P, C.c_uint64, C.c_uint64, C.POINTER(_P)]),
     ("gkr_matrix_wrap_device", C.c_int, [_P, _P, C.c_uint64, C.c_uint64, C.POINTER(_P)]),
     ("gkr_matrix_synthetic", C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_int, C.c_uint64, C.POINTER(_P)]),
@@ -149,6 +150,7 @@ SIGNATURES = [
     ("gkr_qvec_synthetic", C.c_int, [_P, C.c_uint64, C.c_uint64, C.POINTER(_P)]),
     ("gkr_qvec_download", C.c_int, [_P, _P, _PQ]),
     ("gkr_qvec_free", None, [_P]),
+    ("gkr_qvec_device_ptr", _P, [_P]),
     ("gkr_sumcheck_product", C.c_int, [_P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ]),
     ("gkr_prove_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, C.POINTER(GkrMulOut)]),
     ("gkr_reduce_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _PQ, _PQ, C.c_uint64, _P, _P,
@@ -173,6 +175,7 @@ SIGNATURES = [
     ("gkr_prove_weight_binding", C.c_int, [_P, _P, _P, C.c_int]),
 ]
 WEIGHT_SEQUENTIAL, WEIGHT_AGGREGATED_RLC, WEIGHT_RLC_DIRECT = 0, 1, 2
+DEBUG_HANDOVER_CANCEL, DEBUG_HANDOVER_EXPIRE = 1, 2
 
 
 def lib() -> C.CDLL:
@@ -357,6 +360,10 @@ class Context:
 
     def reset_timing(self):
         _check(lib().gkr_ctx_reset_timing(self._h))
+
+    def debug(self, op: int, arg: int = 0) -> None:
+        """Test hook for the hand-over failure paths (DEBUG_HANDOVER_CANCEL / DEBUG_HANDOVER_EXPIRE)."""
+        _check(lib().gkr_ctx_debug(self._h, op, arg))
 
     def kernel_time(self, kid: int) -> Tuple[float, int, int]:
         ms, n, b = C.c_double(), C.c_uint64(), C.c_uint64()
@@ -754,6 +761,11 @@ class QVec:
         out = np.empty((self.n, 4), dtype=np.uint32)
         _check(lib().gkr_qvec_download(self.ctx.handle, self._h, out.ctypes.data_as(_PQ)))
         return out
+
+    @property
+    def device_ptr(self) -> int:
+        """Device address of the n QM31 (gkr_qvec_device_ptr)."""
+        return lib().gkr_qvec_device_ptr(self._h)
 
     def __del__(self):
         if self._h and _lib is not None:

@@ -152,7 +152,7 @@ def test_walk_with_mul_step(gpu_ctx):
 
 
 def test_native_walk_proof_verifies(gpu_ctx):
-    """A chained walk proved on the GPU over a consistent circuit (H = X0 . W0, L = relu(H),
+    """A chained walk proved on the GPU over a consistent circuit (H = X0 . W0, L = sigmoid(H),
     X = L (.) R, Y = X . W), serialized, then verified by the library's walk verifier from the same
     starting transcript; a changed felt is rejected."""
     log("case native walk verifies")
@@ -160,7 +160,7 @@ def test_native_walk_proof_verifies(gpu_ctx):
     X0 = rng.integers(0, P, size=(8, 40), dtype=np.uint32)
     W0 = rng.integers(0, P, size=(40, 32), dtype=np.uint32)
     H = O.matmul_forward(X0, W0)
-    L = np.vectorize(lambda x: O.activation(1, int(x)), otypes=[np.uint32])(H)
+    L = np.vectorize(lambda x: O.activation(3, int(x)), otypes=[np.uint32])(H)
     R = rng.integers(0, P, size=(8, 32), dtype=np.uint32)
     X = ((L.astype(np.uint64) * R) % P).astype(np.uint32)
     W = rng.integers(0, P, size=(32, 24), dtype=np.uint32)
@@ -173,12 +173,12 @@ def test_native_walk_proof_verifies(gpu_ctx):
     ch.mix_secure_field(v)
     after_claim = ch.export_state()
     steps = [(G.STEP_MATMUL, G.CLAIM_CHAINED, gx, gw, 0, 0), (G.STEP_MUL, G.CLAIM_CHAINED, gl, gr, 0, 0),
-             (G.STEP_ACTIVATION, G.CLAIM_CHAINED, gh, None, 1, 12), (G.STEP_MATMUL, G.CLAIM_CHAINED, gx0, gw0, 0, 0)]
+             (G.STEP_ACTIVATION, G.CLAIM_CHAINED, gh, None, 3, 12), (G.STEP_MATMUL, G.CLAIM_CHAINED, gx0, gw0, 0, 0)]
     proof = G.Proof()
     fp, fv = G.prove_walk(gpu_ctx, ch, steps, proof, init_point=r, init_value=v)
     proof.set_input_claim(fp, fv)
     cd = proof.serialize()
-    shapes = [(G.STEP_MATMUL, 8, 32, 24, 0, 0), (G.STEP_MUL, 8, 32, 0, 0, 0), (G.STEP_ACTIVATION, 8, 32, 0, 1, 12),
+    shapes = [(G.STEP_MATMUL, 8, 32, 24, 0, 0), (G.STEP_MUL, 8, 32, 0, 0, 0), (G.STEP_ACTIVATION, 8, 32, 0, 3, 12),
               (G.STEP_MATMUL, 8, 40, 32, 0, 0)]
     vch = G.PoseidonChannel()
     vch.import_state(after_claim)

@@ -205,7 +205,7 @@ def test_mle_ops(gpu_ctx):
             assert gpu_ctx.restrict_mle(evals, assign) == O.restrict_mle(evals, assign)
 
 
-@pytest.mark.parametrize("rows,cols,tag,tlog", [(1, 8, 5, 8), (4, 16, 5, 10), (3, 5, 1, 6), (2, 32, 4, 8),
+@pytest.mark.parametrize("rows,cols,tag,tlog", [(1, 8, 5, 8), (4, 16, 5, 10), (3, 5, 3, 6), (2, 32, 4, 8),
                                                 (1, 1536, 5, 16), (8, 96, 2, 12), (16, 64, 3, 16)])
 def test_activation_layer_parity(gpu_ctx, rows, cols, tag, tlog):
     log(f"case logup {rows}x{cols} tag={tag} table=2^{tlog}")
@@ -231,6 +231,25 @@ def test_activation_layer_parity(gpu_ctx, rows, cols, tag, tlog):
     O.serialize_activation_layer(ref, tag, po)
     O.serialize_tail(ref, pt, po["input_eval"], [], 0)
     assert felts == ref
+
+
+def test_relu_is_not_a_logup_activation(gpu_ctx):
+    """The reference proves ReLU algebraically (prover.rs:1770-1776), never with LogUp: the LogUp
+    reducer and a walk step refuse it before any device work or transcript change."""
+    log("case relu refused")
+    X = O.synthetic(3, 5, 0, 35)
+    x = gpu_ctx.upload(X)
+    gch = G.PoseidonChannel()
+    pt = gch.draw_qm31s(lg(3) + lg(5))
+    val = gch.draw_qm31()
+    d0 = gch.digest()
+    with pytest.raises(G.GkrError) as e:
+        gpu_ctx.prove_activation_layer(pt, val, x, 1, gch, 6)
+    assert e.value.code == 1 and "algebraically" in str(e.value)
+    with pytest.raises(G.GkrError) as e:
+        G.prove_walk(gpu_ctx, gch, [(G.STEP_ACTIVATION, G.CLAIM_CHAINED, x, None, 1, 6)], G.Proof(), pt, val)
+    assert e.value.code == 1
+    assert gch.digest() == d0
 
 
 def test_two_layer_walk_and_serialization(gpu_ctx):
@@ -316,7 +335,7 @@ def test_native_walk_fresh_claims(gpu_ctx):
     gs = [gpu_ctx.upload(M) for M in (A1, B1, A2, B2, S)]
     F = G.CLAIM_FRESH
     steps = [(G.STEP_MATMUL, F, gs[0], gs[1], 0, 0), (G.STEP_ACTIVATION, F, gs[4], None, 4, 10),
-             (G.STEP_MATMUL, F, gs[2], gs[3], 0, 0), (G.STEP_ACTIVATION, F, gs[4], None, 1, 0)]
+             (G.STEP_MATMUL, F, gs[2], gs[3], 0, 0), (G.STEP_ACTIVATION, F, gs[4], None, 2, 0)]
     gch = G.PoseidonChannel()
     gch.mix_u64(77)
     proof = G.Proof()
@@ -325,7 +344,7 @@ def test_native_walk_fresh_claims(gpu_ctx):
     och.mix_u64(77)
     ref = [4]
     for kind, _, a, b, act, tlog in [(0, 0, A1, B1, 0, 0), (3, 0, S, None, 4, 10), (0, 0, A2, B2, 0, 0),
-                                     (3, 0, S, None, 1, 0)]:
+                                     (3, 0, S, None, 2, 0)]:
         if kind == 0:
             r = och.draw_qm31s(lg(a.shape[0]) + lg(b.shape[1]))
             v = O.matmul_output_claim(a, b, r)

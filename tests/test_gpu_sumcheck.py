@@ -74,3 +74,30 @@ def test_sumcheck_product_2_26_chain(gpu_ctx):
         cur = Q.qadd(Q.qadd(c0, Q.qmul(c1, r)), Q.qmul(c2, Q.qmul(r, r)))
     assert cur == Q.qmul(got["final_a_eval"], got["final_b_eval"])
     assert rep.digest() == gch.digest()
+
+
+@pytest.mark.parametrize("op,arg", [(G.DEBUG_HANDOVER_CANCEL, 0), (G.DEBUG_HANDOVER_EXPIRE, 4)])
+def test_handover_failure_leaves_context_usable(gpu_ctx, op, arg):
+    """A hand-over the host cancels before posting its challenges (the error path), or whose
+    bounded wait expires before the post, fails the call with a device error while every kernel
+    exits normally; the next proofs on the same context are correct (no stale cancel code in the
+    mailbox, no timeout code in the shared result flag)."""
+    log(f"case handover failure op={op}")
+    n = 1 << 12
+    fa, fb = gpu_ctx.qvec_synthetic(n, 31), gpu_ctx.qvec_synthetic(n, 32)
+    ha, hb = O.synthetic_q(n, 31), O.synthetic_q(n, 32)
+    gpu_ctx.debug(op, arg)
+    with pytest.raises(G.GkrError) as e:
+        gpu_ctx.sumcheck_product(fa, fb, G.PoseidonChannel())
+    assert e.value.code == 2
+    for rep in range(2):
+        assert gpu_ctx.sumcheck_product(fa, fb, G.PoseidonChannel()) == O.sumcheck_product(ha, hb, O.Channel())
+    # a matmul layer (restriction, trips, hand-over) on the same context
+    A, B = O.synthetic(8, 96, 0, 41), O.synthetic(96, 16, 0, 42)
+    a, b = gpu_ctx.upload(A), gpu_ctx.upload(B)
+    gch, och = G.PoseidonChannel(), O.Channel()
+    r = gch.draw_qm31s(3 + 4)
+    assert r == och.draw_qm31s(7)
+    v = gpu_ctx.matmul_output_claim(a, b, r)
+    assert gpu_ctx.prove_matmul_layer(r, v, a, b, gch) == O.prove_matmul_layer(r, v, A, B, och)
+    assert gch.digest() == och.digest()

@@ -92,7 +92,7 @@ def _export(oracle_channel):
     return O.channel_state(oracle_channel)
 
 
-@pytest.mark.parametrize("rows,cols,tag,tlog", [(4, 64, 5, 10), (3, 5, 1, 8), (8, 8, 4, 6)])
+@pytest.mark.parametrize("rows,cols,tag,tlog", [(4, 64, 5, 10), (3, 5, 3, 8), (8, 8, 4, 6), (2, 8, 2, 8)])
 def test_activation_layer_verifier(rows, cols, tag, tlog):
     rng = np.random.default_rng(rows * 31 + cols)
     X = rng.integers(0, P, size=(rows, cols), dtype=np.uint32)
@@ -132,6 +132,29 @@ def test_activation_layer_verifier(rows, cols, tag, tlog):
         assert e.value.code == 6
 
 
+def test_activation_verifier_refuses_relu():
+    """ReLU is proved algebraically by the reference (prover.rs:1770-1776); the LogUp replay and the
+    walk verifier refuse a LogUp proof of it."""
+    X = np.arange(15, dtype=np.uint32).reshape(3, 5)
+    ch = O.Channel()
+    r = ch.draw_qm31s(lg(3) + lg(5))
+    v = ch.draw_qm31()
+    start = ch.clone()
+    proof = O.prove_activation_layer(r, v, X, 1, ch, 8)
+    gch = G.PoseidonChannel()
+    gch.import_state(_export(start))
+    with pytest.raises(G.GkrError) as e:
+        G.verify_activation_layer(r, 1, 8, proof, gch)
+    assert e.value.code == 1
+    cd = [1]
+    O.serialize_activation_layer(cd, 1, proof)
+    O.serialize_tail(cd, r, proof["input_eval"], [], 0)
+    g2 = G.PoseidonChannel()
+    g2.import_state(_export(start))
+    with pytest.raises(G.GkrError, match="algebraically"):
+        G.verify_walk(cd, [(G.STEP_ACTIVATION, 3, 5, 0, 1, 8)], r, v, g2)
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 2), (3, 5), (8, 16)])
 def test_mul_layer_verifier(rows, cols):
     rng = np.random.default_rng(rows * 7 + cols)
@@ -162,11 +185,11 @@ def test_serialized_chained_walk():
     serialized as the reference does; the product's walk verifier accepts it and rejects any
     changed felt among a sample of positions."""
     rng = np.random.default_rng(5)
-    # circuit (input to output): H = X0 . W0; L = relu(H); X = L (.) R; Y = X . W
+    # circuit (input to output): H = X0 . W0; L = sigmoid(H); X = L (.) R; Y = X . W
     X0 = rng.integers(0, P, size=(4, 12), dtype=np.uint32)
     W0 = rng.integers(0, P, size=(12, 16), dtype=np.uint32)
     H = O.matmul_forward(X0, W0)
-    L = np.vectorize(lambda x: O.activation(1, int(x)), otypes=[np.uint32])(H)
+    L = np.vectorize(lambda x: O.activation(3, int(x)), otypes=[np.uint32])(H)
     R = rng.integers(0, P, size=(4, 16), dtype=np.uint32)
     X = ((L.astype(np.uint64) * R) % P).astype(np.uint32)
     W = rng.integers(0, P, size=(16, 8), dtype=np.uint32)
@@ -178,15 +201,15 @@ def test_serialized_chained_walk():
     start = ch.clone()
     o1 = O.prove_matmul_layer(r, v, X, W, ch)
     o2 = O.reduce_mul_layer(o1["next_point"], o1["next_value"], O.padded_mle(L), O.padded_mle(R), ch)
-    o3 = O.prove_activation_layer(o2["next_point"], o2["next_value"], H, 1, ch, 8)
+    o3 = O.prove_activation_layer(o2["next_point"], o2["next_value"], H, 3, ch, 8)
     o4 = O.prove_matmul_layer(o2["next_point"], o3["input_eval"], X0, W0, ch)
     cd = [4]
     O.serialize_matmul_layer(cd, o1["round_polys"], o1["final_a_eval"], o1["final_b_eval"])
     O.serialize_mul_layer(cd, o2)
-    O.serialize_activation_layer(cd, 1, o3)
+    O.serialize_activation_layer(cd, 3, o3)
     O.serialize_matmul_layer(cd, o4["round_polys"], o4["final_a_eval"], o4["final_b_eval"])
     O.serialize_tail(cd, o4["next_point"], o4["next_value"], [], 0)
-    shapes = [(G.STEP_MATMUL, 4, 16, 8, 0, 0), (G.STEP_MUL, 4, 16, 0, 0, 0), (G.STEP_ACTIVATION, 4, 16, 0, 1, 8),
+    shapes = [(G.STEP_MATMUL, 4, 16, 8, 0, 0), (G.STEP_MUL, 4, 16, 0, 0, 0), (G.STEP_ACTIVATION, 4, 16, 0, 3, 8),
               (G.STEP_MATMUL, 4, 12, 16, 0, 0)]
     gch = G.PoseidonChannel()
     gch.import_state(_export(start))
