@@ -270,6 +270,20 @@ int gkr_sumcheck_product(gkr_ctx* ctx, const gkr_qvec* fa, const gkr_qvec* fb, g
                          gkr_qm31* round_polys /* 3T: c0, c1, c2 */, gkr_qm31* challenges /* T */,
                          gkr_qm31* final_a, gkr_qm31* final_b);
 
+/* Allocation-free variant of gkr_sumcheck_product (no counterpart in the
+ * reference): for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  fa
+ * and fb are device pointers of the context's GPU holding n canonical QM31
+ * each (n a power of two, at most 2^20); outputs as gkr_sumcheck_product.
+ * Every device buffer the kernels need (fold levels, partial rows, arrival
+ * counter) lives in a static 25 MiB device array, one per GPU, held until
+ * the process ends; no hipMalloc or hipFree is called.  All calls on one GPU
+ * share that array, so calls that overlap on one GPU (two contexts, two
+ * threads) race.  Longer vectors fail with GKR_ERR_INVALID.               */
+int gkr_sumcheck_product_noalloc(gkr_ctx* ctx, const gkr_qm31* fa, const gkr_qm31* fb, uint64_t n, gkr_channel* ch,
+                                 gkr_qm31* round_polys /* 3T */, gkr_qm31* challenges /* T */, gkr_qm31* final_a,
+                                 gkr_qm31* final_b);
+
 /* Forward-pass matrix product (the witness before the walk): C = A * B mod P
  * for canonical M31 matrices, a new resident matrix (m x n).  Replaces
  * gpu_matmul_m31_full (engine/src/gpu_sumcheck.rs:3104) and its GEMM/GEMV

@@ -179,13 +179,47 @@ struct gkr_ctx {
   uint32_t trip_count = 0;         // value of the fused trips' arrival counter (S_TRIPCNT) after the queued launches
   bool trip_count_valid = false;   // false: zero the counter before the next fused trip
   bool int8_weights = false;       // GKR_INT8_WEIGHTS=1 at creation: int8 weight-side restriction
+  // allocation-free mode (gkr_sumcheck_product_noalloc): ensure() hands out
+  // the partial rows and the arrival counter from the device's static
+  // scratch array (scratch_dev: its address on this context's device) and
+  // refuses every other slot
+  uint8_t* scratch_dev = nullptr;
+  bool noalloc = false;
   // test hooks (gkr_ctx_debug), each consumed by the next hand-over
   bool debug_handover_cancel = false;  // the host leaves before posting the challenges
   uint32_t debug_handover_spins = 0;   // nonzero: the kernel's bounded wait, posted only after it expired
 };
 
+// ------------------------------------------------------------------ static scratch (allocation-free entry point)
+// Device memory of gkr_sumcheck_product_noalloc, one copy per GPU for the
+// life of the process: the two fold levels of each vector (n/2 and n/4
+// entries), the trips' partial rows and their arrival counter.  Host code
+// never uses the array's name as an address: gkr_ctx_create looks up its
+// address on the context's device (hipGetSymbolAddress) and everything
+// else goes through gkr_ctx::scratch_dev.
+constexpr uint64_t kNoAllocMaxN = 1ull << 20;  // longest vectors of the allocation-free sumcheck
+constexpr size_t kScratchFold1 = (kNoAllocMaxN / 2) * sizeof(qm31);
+constexpr size_t kScratchFold2 = (kNoAllocMaxN / 4) * sizeof(qm31);
+constexpr size_t kScratchOffA1 = 0, kScratchOffB1 = kScratchFold1, kScratchOffA2 = 2 * kScratchFold1,
+                 kScratchOffB2 = 2 * kScratchFold1 + kScratchFold2, kScratchOffPart = 2 * kScratchFold1 + 2 * kScratchFold2;
+constexpr size_t kScratchPartBytes = (size_t)kMaxSums * kMaxPartialBlocks * sizeof(qm31);
+constexpr size_t kScratchOffCount = kScratchOffPart + kScratchPartBytes;
+constexpr size_t kScratchBytes = kScratchOffCount + 256;  // 25 MiB + 256 B
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 static int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
   if (bytes == 0) bytes = 16;
+  if (c->noalloc) {
+    if (s == S_PART && bytes <= kScratchPartBytes) {
+      *out = c->scratch_dev + kScratchOffPart;
+      return GKR_OK;
+    }
+    if (s == S_TRIPCNT && bytes <= 256) {
+      *out = c->scratch_dev + kScratchOffCount;
+      return GKR_OK;
+    }
+    return fail(GKR_ERR_NOMEM, "the allocation-free entry point needs device buffer %d (%zu bytes)", (int)s, bytes);
+  }
   if (c->cap[s] < bytes) {
     if (s == S_TABLE) c->table_on_device = 0;
     if (s == S_TRIPCNT) c->trip_count_valid = false;  // fresh memory must be zeroed
@@ -855,6 +889,15 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
       hipSuccess) {
     gkr_ctx_destroy(c);
     return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
+  }
+  {  // this device's copy of the static scratch array (gkr_sumcheck_product_noalloc)
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      gkr_ctx_destroy(c);
+      return fail(GKR_ERR_DEVICE, "scratch address on device %d: %s", device, hipGetErrorString(e));
+    }
+    c->scratch_dev = static_cast<uint8_t*>(p);
   }
   c->h_flag = reinterpret_cast<uint32_t*>(c->h_out + kOutSlots);
   *c->h_flag = 0;
@@ -2554,6 +2597,59 @@ extern "C" int gkr_sumcheck_product(gkr_ctx* c, const gkr_qvec* fa, const gkr_qv
   qm31* bufs_b[2] = {b1, b2};
   return product_sumcheck(c, ch->ch, T, fa->dev, fb->dev, bufs_a, bufs_b, nullptr, 0, round_polys, challenges,
                           final_a, final_b);
+}
+
+// The allocation-free variant: the caller's vectors are device pointers and
+// every device buffer comes from the static scratch array.  The arrival
+// counter's expected value belongs to the scratch copy, so the context's
+// own counter state is set aside for the call and restored afterwards.
+extern "C" int gkr_sumcheck_product_noalloc(gkr_ctx* c, const gkr_qm31* fa, const gkr_qm31* fb, uint64_t n,
+                                            gkr_channel* ch, gkr_qm31* round_polys, gkr_qm31* challenges,
+                                            gkr_qm31* final_a, gkr_qm31* final_b) {
+  CH_CHECK(ch);
+  if (!c || !fa || !fb || !final_a || !final_b) return fail(GKR_ERR_INVALID, "null argument");
+  if (n == 0 || (n & (n - 1))) return fail(GKR_ERR_INVALID, "length %llu is not a power of two", (unsigned long long)n);
+  if (n > kNoAllocMaxN)
+    return fail(GKR_ERR_INVALID, "length %llu exceeds the allocation-free maximum of %llu entries",
+                (unsigned long long)n, (unsigned long long)kNoAllocMaxN);
+  const int T = log2_exact(n);
+  if (T > 0 && (!round_polys || !challenges)) return fail(GKR_ERR_INVALID, "null output arrays");
+  HIP_TRY(hipSetDevice(c->device));
+  for (const gkr_qm31* p : {fa, fb}) {  // device memory of this context's GPU, or the kernels would fault
+    hipPointerAttribute_t at;
+    if (hipPointerGetAttributes(&at, p) != hipSuccess || at.type != hipMemoryTypeDevice || at.device != c->device) {
+      (void)hipGetLastError();
+      return fail(GKR_ERR_INVALID, "vector %p is not device memory of device %d", (const void*)p, c->device);
+    }
+  }
+  const qm31* da = reinterpret_cast<const qm31*>(fa);
+  const qm31* db = reinterpret_cast<const qm31*>(fb);
+  if (T == 0) {
+    qm31 v;
+    TRY(fetch_q(c, da, 1, &v));
+    *final_a = G(v);
+    TRY(fetch_q(c, db, 1, &v));
+    *final_b = G(v);
+    return GKR_OK;
+  }
+  c->mm.valid = false;
+  qm31* bufs_a[2] = {reinterpret_cast<qm31*>(c->scratch_dev + kScratchOffA1),
+                     reinterpret_cast<qm31*>(c->scratch_dev + kScratchOffA2)};
+  qm31* bufs_b[2] = {reinterpret_cast<qm31*>(c->scratch_dev + kScratchOffB1),
+                     reinterpret_cast<qm31*>(c->scratch_dev + kScratchOffB2)};
+  const uint32_t saved_count = c->trip_count;
+  const bool saved_valid = c->trip_count_valid;
+  const int saved_timing = c->timing;  // timing events would be created on demand
+  c->noalloc = true;
+  c->trip_count_valid = false;  // the scratch counter starts from zero (a fill kernel, queued first)
+  c->timing = 0;
+  const int rc = product_sumcheck(c, ch->ch, T, da, db, bufs_a, bufs_b, nullptr, 0, round_polys, challenges, final_a,
+                                  final_b);
+  c->noalloc = false;
+  c->trip_count = saved_count;
+  c->trip_count_valid = saved_valid;
+  c->timing = saved_timing;
+  return rc;
 }
 
 /* ------------------------------------------------------------------ MLE commitments

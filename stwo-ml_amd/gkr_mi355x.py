@@ -152,6 +152,7 @@ SIGNATURES = [
     ("gkr_qvec_free", None, [_P]),
     ("gkr_qvec_device_ptr", _P, [_P]),
     ("gkr_sumcheck_product", C.c_int, [_P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ]),
+    ("gkr_sumcheck_product_noalloc", C.c_int, [_P, _PQ, _PQ, C.c_uint64, _P, _PQ, _PQ, _PQ, _PQ]),
     ("gkr_prove_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, C.POINTER(GkrMulOut)]),
     ("gkr_reduce_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _PQ, _PQ, C.c_uint64, _P, _P,
                                        C.POINTER(GkrMulOut)]),
@@ -501,6 +502,21 @@ class Context:
         a, b = GkrQM31(), GkrQM31()
         _check(lib().gkr_sumcheck_product(self._h, fa.handle, fb.handle, ch.handle, rp, chal, C.byref(a),
                                           C.byref(b)))
+        return {"round_polys": [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2]))
+                                for t in range(T)],
+                "challenges": [q_from_c(chal[t]) for t in range(T)],
+                "final_a_eval": q_from_c(a), "final_b_eval": q_from_c(b)}
+
+    def sumcheck_product_noalloc(self, fa_ptr: int, fb_ptr: int, n: int, ch: PoseidonChannel):
+        """gkr_sumcheck_product_noalloc: the same round loop over caller-owned device memory (n canonical
+        QM31 at each device pointer), with every device buffer in the library's static scratch array."""
+        T = max(0, (n - 1).bit_length())
+        rp = (GkrQM31 * max(1, 3 * T))()
+        chal = (GkrQM31 * max(1, T))()
+        a, b = GkrQM31(), GkrQM31()
+        _check(lib().gkr_sumcheck_product_noalloc(self._h, C.cast(C.c_void_p(fa_ptr), _PQ),
+                                                  C.cast(C.c_void_p(fb_ptr), _PQ), n, ch.handle, rp, chal,
+                                                  C.byref(a), C.byref(b)))
         return {"round_polys": [(q_from_c(rp[3 * t]), q_from_c(rp[3 * t + 1]), q_from_c(rp[3 * t + 2]))
                                 for t in range(T)],
                 "challenges": [q_from_c(chal[t]) for t in range(T)],
