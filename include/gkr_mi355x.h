@@ -169,6 +169,8 @@ int gkr_proof_new(gkr_proof** out);
 void gkr_proof_free(gkr_proof* p);
 size_t gkr_proof_num_layers(const gkr_proof* p);
 int gkr_proof_set_input_claim(gkr_proof* p, const gkr_qm31* point, uint32_t n_vars, const gkr_qm31* value);
+/* The value of the output claim layer `layer` (proving order) was proved against. */
+int gkr_proof_layer_claim_value(const gkr_proof* p, size_t layer, gkr_qm31* value);
 int gkr_proof_add_weight_commitment(gkr_proof* p, const gkr_felt* c);
 int gkr_proof_set_io_commitment(gkr_proof* p, const gkr_felt* c);
 /* serialize_gkr_model_proof (engine/src/cairo_serde.rs:1307-1772) for MatMul
@@ -428,16 +430,23 @@ typedef struct {
   uint64_t cols_b;           /* MatMul: n (B is cols x cols_b) */
   uint32_t activation_type;  /* Activation */
   uint32_t table_log_size;   /* Activation: 0 = reference default */
+  uint32_t claim;            /* GKR_CLAIM_CHAINED / GKR_CLAIM_FRESH, as the walk that proved it */
 } gkr_layer_shape;
-/* A chained walk from serialize_gkr_model_proof calldata (the layer section
- * and the input claim that follows it): layer i's claim is layer i-1's input
- * claim, starting from init_point / init_value (the seeded output claim).
- * Round polynomials are compressed (c1 rebuilt from the running sum).  The
- * weight commitments, openings and IO commitment after the input claim are
- * not examined; *n_consumed receives the number of felts read. */
+/* A walk from serialize_gkr_model_proof calldata (the layer section and the
+ * input claim that follows it).  A chained layer's claim is the previous
+ * layer's input claim, starting from init_point / init_value (the seeded
+ * output claim; both may be absent when the first layer is fresh).  A fresh
+ * layer replays gkr_prove_walk's rule: its point is drawn from the channel;
+ * an Activation draws its value, a MatMul or Mul takes the next of the
+ * fresh_values (the values its prover computed from the witness, public to
+ * this verifier like the model output; gkr_proof_layer_claim_value) and mixes
+ * it.  Round polynomials are compressed (c1 rebuilt from the running sum).
+ * The weight commitments, openings and IO commitment after the input claim
+ * are not examined; *n_consumed receives the number of felts read. */
 int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const gkr_layer_shape* layers, size_t n_layers,
-                    const gkr_qm31* init_point, uint32_t n_init, const gkr_qm31* init_value, gkr_channel* ch,
-                    gkr_qm31* final_point, uint32_t* n_final, gkr_qm31* final_value, size_t* n_consumed);
+                    const gkr_qm31* init_point, uint32_t n_init, const gkr_qm31* init_value,
+                    const gkr_qm31* fresh_values, size_t n_fresh, gkr_channel* ch, gkr_qm31* final_point,
+                    uint32_t* n_final, gkr_qm31* final_value, size_t* n_consumed);
 
 /* Activation table output column, f(j) for j < 2^log_size (host). */
 int gkr_activation_table(uint32_t activation_type, uint32_t log_size, uint32_t* out);

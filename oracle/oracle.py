@@ -67,6 +67,8 @@ def lib():
 
 
 def _qa(qs: Sequence[Sequence[int]]) -> np.ndarray:
+    if isinstance(qs, np.ndarray) and qs.dtype == np.uint32 and qs.ndim == 2 and qs.shape[1] == 4 and len(qs):
+        return np.ascontiguousarray(qs)
     a = np.zeros((max(1, len(qs)), 4), dtype=np.uint32)
     for i, q in enumerate(qs):
         a[i] = q

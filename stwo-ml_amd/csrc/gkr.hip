@@ -1467,6 +1467,7 @@ extern "C" int gkr_matmul_output_claim(gkr_ctx* c, const gkr_matrix* a, const gk
 struct LayerRec {
   uint32_t tag;  // 0 MatMul, 2 Mul, 3 Activation, 7 MatMulDualSimd (rp: c0..c3 per round)
   uint32_t n_block_vars = 0;  // MatMulDualSimd
+  qm31 claim_value = {0, 0, 0, 0};  // the output claim's value the layer was proved against
   std::vector<qm31> rp;  // MatMul: c0,c1,c2 per round; Mul, Activation: eq c0..c3 per round
   qm31 final_a, final_b;  // MatMul: final a/b evals; Mul: lhs/rhs evals
   uint32_t act_type = 0;
@@ -1500,6 +1501,12 @@ extern "C" int gkr_proof_new(gkr_proof** out) {
 }
 extern "C" void gkr_proof_free(gkr_proof* p) { delete p; }
 extern "C" size_t gkr_proof_num_layers(const gkr_proof* p) { return p ? p->layers.size() : 0; }
+extern "C" int gkr_proof_layer_claim_value(const gkr_proof* p, size_t layer, gkr_qm31* value) {
+  if (!p || !value) return fail(GKR_ERR_INVALID, "null argument");
+  if (layer >= p->layers.size()) return fail(GKR_ERR_INVALID, "layer %zu of %zu", layer, p->layers.size());
+  *value = G(p->layers[layer].claim_value);
+  return GKR_OK;
+}
 extern "C" int gkr_proof_set_input_claim(gkr_proof* p, const gkr_qm31* point, uint32_t n, const gkr_qm31* value) {
   if (!p || !value || (!point && n)) return fail(GKR_ERR_INVALID, "null argument");
   p->in_point.clear();
@@ -1667,6 +1674,7 @@ extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, u
   if (proof) {
     LayerRec L;
     L.tag = 0;
+    L.claim_value = Q(*claim_value);
     for (int t = 0; t < 3 * T; t++) L.rp.push_back(Q(round_polys[t]));
     L.final_a = Q(*final_a);
     L.final_b = Q(*final_b);
@@ -1777,6 +1785,7 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
   if (proof) {
     LayerRec L;
     L.tag = 0;
+    L.claim_value = Q(*claim_value);
     for (int t = 0; t < 3 * T; t++) L.rp.push_back(Q(round_polys[t]));
     L.final_a = Q(*final_a);
     L.final_b = Q(*final_b);
@@ -1971,6 +1980,7 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
   if (proof) {
     LayerRec L;
     L.tag = 7;
+    L.claim_value = Q(*claim_value);
     L.n_block_vars = (uint32_t)nbv;
     for (int t = 0; t < 4 * (nbv + T); t++) L.rp.push_back(Q(round_polys[t]));
     L.final_a = Q(*final_a);
@@ -2451,6 +2461,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     for (int t = 0; t < 4 * nv; t++) L.rp.push_back(Q(out->eq_round_polys[t]));
     L.input_eval = input_eval;
     L.output_eval = Q(*claim_value);
+    L.claim_value = Q(*claim_value);
     L.table_commitment = felt_from_mont(tc);
     L.claimed_sum = trace_sum;
     L.w_eval = w_eval;
@@ -3260,6 +3271,7 @@ static int mul_layer_core(gkr_ctx* c, const std::vector<qm31>& cpt, const qm31& 
   if (proof) {
     LayerRec L;
     L.tag = 2;
+    L.claim_value = claim;
     L.rp.resize(4 * (size_t)nv);
     for (size_t i = 0; i < L.rp.size(); i++) L.rp[i] = Q(out->eq_round_polys[i]);
     L.final_a = lhs;
@@ -3587,14 +3599,19 @@ extern "C" int gkr_verify_activation_layer(const gkr_qm31* claim_point, uint32_t
 // openings and IO commitment that follow are not examined.
 extern "C" int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const gkr_layer_shape* layers,
                                size_t n_layers, const gkr_qm31* init_point, uint32_t n_init,
-                               const gkr_qm31* init_value, gkr_channel* ch, gkr_qm31* final_point, uint32_t* n_final,
-                               gkr_qm31* final_value, size_t* n_consumed) {
+                               const gkr_qm31* init_value, const gkr_qm31* fresh_values, size_t n_fresh,
+                               gkr_channel* ch, gkr_qm31* final_point, uint32_t* n_final, gkr_qm31* final_value,
+                               size_t* n_consumed) {
   CH_CHECK(ch);
-  if (!calldata || !layers || !init_value || !final_point || !n_final || !final_value || (!init_point && n_init))
+  if (!calldata || !layers || !final_point || !n_final || !final_value || (!init_point && n_init) ||
+      (!fresh_values && n_fresh))
     return fail(GKR_ERR_INVALID, "null argument");
+  if (n_layers && layers[0].claim != GKR_CLAIM_FRESH && !init_value)
+    return fail(GKR_ERR_INVALID, "the first layer's claim is chained but no initial claim is given");
   std::vector<qm31> point;
   if (!read_point(init_point, n_init, &point)) return fail(GKR_ERR_INVALID, "initial point not canonical");
-  qm31 value = Q(*init_value);
+  qm31 value = init_value ? Q(*init_value) : qm31_zero();
+  size_t fresh_used = 0;
   FeltReader R{reinterpret_cast<const uint32_t*>(calldata), n_felts};
   auto bad = [&](const std::string& why) { return fail(GKR_ERR_VERIFY, "%s", why.c_str()); };
   const uint64_t nl = R.u();
@@ -3605,6 +3622,25 @@ extern "C" int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const g
     const std::string at = "layer " + std::to_string(li) + ": ";
     const uint64_t tag = R.u();
     if (!R.ok) return bad(R.why);
+    if (L.claim == GKR_CLAIM_FRESH) {  // the prover's fresh-claim rule (gkr_prove_walk)
+      if (L.kind != GKR_STEP_MATMUL && L.kind != GKR_STEP_MUL && L.kind != GKR_STEP_ACTIVATION)
+        return fail(GKR_ERR_INVALID, "layer %zu: unknown kind %u", li, L.kind);
+      const uint64_t out_cols = L.kind == GKR_STEP_MATMUL ? L.cols_b : L.cols;
+      const int nv = v_log2(v_next_pow2(L.rows)) + v_log2(v_next_pow2(out_cols));
+      if (nv > 64) return fail(GKR_ERR_INVALID, "layer %zu: output claim of %d variables", li, nv);
+      point.resize(nv);
+      ch->ch.draw_qm31s(point.data(), (size_t)nv);
+      if (L.kind == GKR_STEP_ACTIVATION) {
+        value = ch->ch.draw_qm31();
+      } else {
+        if (fresh_used >= n_fresh) return fail(GKR_ERR_INVALID, "layer %zu: no fresh claim value left", li);
+        if (!canonical_q(fresh_values[fresh_used])) return fail(GKR_ERR_INVALID, "fresh claim value not canonical");
+        value = Q(fresh_values[fresh_used++]);
+        ch->ch.mix_secure_field(value);
+      }
+    } else if (L.claim != GKR_CLAIM_CHAINED) {
+      return fail(GKR_ERR_INVALID, "layer %zu: unknown claim rule %u", li, L.claim);
+    }
     VerifyError e;
     if (L.kind == GKR_STEP_MATMUL) {
       if (tag != 0) return bad(at + "expected a MatMul proof (tag 0), found tag " + std::to_string(tag));
@@ -3697,6 +3733,8 @@ extern "C" int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const g
   bool same = ipt.size() == point.size() && qm31_eq(ival, value);
   for (size_t l = 0; same && l < ipt.size(); l++) same = qm31_eq(ipt[l], point[l]);
   if (!same) return bad("input claim in the proof differs from the claim the walk reached");
+  if (fresh_used != n_fresh)
+    return fail(GKR_ERR_INVALID, "%zu fresh claim values given, the circuit uses %zu", n_fresh, fresh_used);
   if (point.size() > 64) return fail(GKR_ERR_BUFFER, "final claim has %zu variables", point.size());
   for (size_t l = 0; l < point.size(); l++) final_point[l] = G(point[l]);
   *n_final = (uint32_t)point.size();

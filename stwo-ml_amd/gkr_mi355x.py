@@ -72,7 +72,7 @@ def _next_pow2(v: int) -> int:
 
 class GkrLayerShape(C.Structure):
     _fields_ = [("kind", C.c_uint32), ("rows", C.c_uint64), ("cols", C.c_uint64), ("cols_b", C.c_uint64),
-                ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32)]
+                ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32), ("claim", C.c_uint32)]
 
 
 class GkrError(RuntimeError):
@@ -132,6 +132,7 @@ SIGNATURES = [
     ("gkr_proof_free", None, [_P]),
     ("gkr_proof_num_layers", C.c_size_t, [_P]),
     ("gkr_proof_set_input_claim", C.c_int, [_P, _PQ, C.c_uint32, _PQ]),
+    ("gkr_proof_layer_claim_value", C.c_int, [_P, C.c_size_t, _PQ]),
     ("gkr_proof_add_weight_commitment", C.c_int, [_P, _PF]),
     ("gkr_proof_set_io_commitment", C.c_int, [_P, _PF]),
     ("gkr_proof_serialize", C.c_int, [_P, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -163,7 +164,8 @@ SIGNATURES = [
     ("gkr_verify_activation_layer", C.c_int, [_PQ, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                               C.POINTER(GkrLogupOut), _P, _PQ]),
     ("gkr_verify_walk", C.c_int, [C.POINTER(GkrFelt), C.c_size_t, C.POINTER(GkrLayerShape), C.c_size_t, _PQ,
-                                  C.c_uint32, _PQ, _P, _PQ, C.POINTER(C.c_uint32), _PQ, C.POINTER(C.c_size_t)]),
+                                  C.c_uint32, _PQ, _PQ, C.c_size_t, _P, _PQ, C.POINTER(C.c_uint32), _PQ,
+                                  C.POINTER(C.c_size_t)]),
     ("gkr_prove_walk", C.c_int, [_P, _P, C.POINTER(GkrStep), C.c_size_t, _PQ, C.c_uint32, _PQ, _P, _PQ,
                                  C.POINTER(C.c_uint32), _PQ]),
     ("gkr_matmul_forward", C.c_int, [_P, _P, _P, C.POINTER(_P)]),
@@ -720,23 +722,44 @@ def verify_activation_layer(claim_point, act_type: int, table_log_size: int, pro
     return q_from_c(nv)
 
 
-def verify_walk(calldata, shapes, init_point, init_value, ch: PoseidonChannel):
-    """gkr_verify_walk: a chained walk from serialized calldata (felt ints).  shapes: sequence of
-    (kind, rows, cols, cols_b, activation_type, table_log_size).  Returns (point, value, felts read)."""
-    cd = (GkrFelt * max(1, len(calldata)))()
-    for i, v in enumerate(calldata):
-        cd[i] = felt_to_c(v)
+def felts_to_words(felts) -> np.ndarray:
+    """felt252 ints -> (n, 8) little-endian u32 words."""
+    out = np.zeros((len(felts), 8), dtype=np.uint32)
+    for i, v in enumerate(felts):
+        for j in range(8):
+            out[i, j] = (v >> (32 * j)) & 0xFFFFFFFF
+    return out
+
+
+def verify_walk(calldata, shapes, init_point, init_value, ch: PoseidonChannel, fresh_values=()):
+    """gkr_verify_walk: a walk from serialized calldata (felt ints, or an (n, 8) u32 word array).
+    shapes: sequence of (kind, rows, cols, cols_b, activation_type, table_log_size[, claim]);
+    fresh_values: the claim values of the fresh MatMul / Mul layers, in order.  Returns
+    (point, value, felts read)."""
+    if isinstance(calldata, np.ndarray):
+        words = np.ascontiguousarray(calldata, dtype=np.uint32).reshape(-1, 8)
+        n_felts = len(words)
+        cd = words.ctypes.data_as(C.POINTER(GkrFelt))
+    else:
+        n_felts = len(calldata)
+        cd = (GkrFelt * max(1, n_felts))()
+        for i, v in enumerate(calldata):
+            cd[i] = felt_to_c(v)
     sh = (GkrLayerShape * max(1, len(shapes)))()
-    for i, (kind, rows, cols, cols_b, act, tlog) in enumerate(shapes):
+    for i, shp in enumerate(shapes):
+        kind, rows, cols, cols_b, act, tlog = shp[:6]
         sh[i].kind, sh[i].rows, sh[i].cols, sh[i].cols_b = kind, rows, cols, cols_b
         sh[i].activation_type, sh[i].table_log_size = act, tlog
+        sh[i].claim = shp[6] if len(shp) > 6 else CLAIM_CHAINED
     fp = (GkrQM31 * 64)()
     nf = C.c_uint32()
     fv = GkrQM31()
     used = C.c_size_t()
-    _check(lib().gkr_verify_walk(cd, len(calldata), sh, len(shapes), q_array(init_point), len(init_point),
-                                 C.byref(q_to_c(init_value)), ch.handle, fp, C.byref(nf), C.byref(fv),
-                                 C.byref(used)))
+    ip = init_point or []
+    _check(lib().gkr_verify_walk(cd, n_felts, sh, len(shapes), q_array(ip), len(ip),
+                                 C.byref(q_to_c(init_value)) if init_value is not None else None,
+                                 q_array(fresh_values), len(fresh_values), ch.handle, fp, C.byref(nf),
+                                 C.byref(fv), C.byref(used)))
     return [q_from_c(fp[i]) for i in range(nf.value)], q_from_c(fv), used.value
 
 
@@ -826,6 +849,22 @@ class Proof:
         arr = (GkrFelt * max(1, n.value))()
         _check(lib().gkr_proof_serialize(self._h, arr, n.value, C.byref(n)))
         return [felt_from_c(arr[i]) for i in range(n.value)]
+
+    def serialize_words(self) -> np.ndarray:
+        """The serialized proof as an (n, 8) array of little-endian u32 felt words (no int conversion)."""
+        n = C.c_size_t()
+        rc = lib().gkr_proof_serialize(self._h, None, 0, C.byref(n))
+        if rc not in (0, 5):
+            _check(rc)
+        out = np.zeros((max(1, n.value), 8), dtype=np.uint32)
+        _check(lib().gkr_proof_serialize(self._h, out.ctypes.data_as(C.POINTER(GkrFelt)), n.value, C.byref(n)))
+        return out[:n.value]
+
+    def layer_claim_value(self, layer: int) -> QM31:
+        """The output-claim value layer `layer` was proved against (gkr_proof_layer_claim_value)."""
+        v = GkrQM31()
+        _check(lib().gkr_proof_layer_claim_value(self._h, layer, C.byref(v)))
+        return q_from_c(v)
 
 
 def activation_table(act_type: int, log_size: int) -> np.ndarray:

@@ -1,0 +1,235 @@
+"""The BASELINE configurations at their full shapes on the GPU, checked against the CPU oracle
+(the reference's CPU algorithm): config 4 (one Qwen2.5-14B layer, the bench's workload), config 3
+(the 30-layer SmolLM2-135M walk), config 2 at 2^28, and the reference-default 2^20 softmax table on
+the Qwen score shape.  Inputs come from the bench's own generator (bench.LayerWeights), so these
+tests prove exactly what bench.py times."""
+import os
+import sys
+import time
+
+import gkr_mi355x as G
+import numpy as np
+import oracle as O
+import pytest
+import qm31_py as Q
+
+sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+import bench  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def lg(v):
+    return max(0, (v - 1).bit_length())
+
+
+def host_layer(cfg, layer, seed_base=0):
+    """Host copies of bench.LayerWeights(ctx, cfg, layer, seed_base): same generator, same seeds."""
+    h, i, q, kv, m = cfg["hidden"], cfg["inter"], cfg["q"], cfg["kv"], cfg["tokens"]
+    s = seed_base + 1000 * layer
+    xq, xo, xg, xd = (O.synthetic(m, h, 1, s + 1), O.synthetic(m, q, 1, s + 5), O.synthetic(m, h, 1, s + 7),
+                      O.synthetic(m, i, 1, s + 10))
+    mats = {"q": (xq, O.synthetic(h, q, 1, s + 2)), "k": (xq, O.synthetic(h, kv, 1, s + 3)),
+            "v": (xq, O.synthetic(h, kv, 1, s + 4)), "o": (xo, O.synthetic(q, h, 1, s + 6)),
+            "gate": (xg, O.synthetic(h, i, 1, s + 8)), "up": (xg, O.synthetic(h, i, 1, s + 9)),
+            "down": (xd, O.synthetic(i, h, 1, s + 11))}
+    silu = O.synthetic(m, i, 0, s + 12)
+    scores = O.synthetic(cfg["heads"] * m, m, 0, s + 13) if m > 1 else None
+    return mats, silu, scores
+
+
+def oracle_layer(och, cfg, layer, out, seed_base=0):
+    """The bench's per-layer sequence (bench.model_steps) on the oracle: fresh claims, q k v o gate up
+    matmuls, SiLU LogUp (2^16), down, softmax-exp LogUp (2^16); serialized felts appended to out."""
+    mats, silu, scores = host_layer(cfg, layer, seed_base)
+
+    def matmul(A, B):
+        r = och.draw_qm31s(lg(A.shape[0]) + lg(B.shape[1]))
+        v = O.matmul_output_claim(A, B, r)
+        och.mix_secure_field(v)
+        o = O.prove_matmul_layer(r, v, A, B, och)
+        O.serialize_matmul_layer(out, o["round_polys"], o["final_a_eval"], o["final_b_eval"])
+
+    def logup(X, tag):
+        r = och.draw_qm31s(lg(X.shape[0]) + lg(X.shape[1]))
+        v = och.draw_qm31()
+        o = O.prove_activation_layer(r, v, X, tag, och, 16)
+        O.serialize_activation_layer(out, tag, o)
+
+    for name in ("q", "k", "v", "o", "gate", "up"):
+        matmul(*mats[name])
+    logup(silu, 5)
+    matmul(*mats["down"])
+    if scores is not None:
+        logup(scores, 4)
+
+
+def gpu_walk(ctx, layers, seed=7):
+    """bench.prove_model_walk: one gkr_prove_walk over the layers' steps; returns the serialized proof
+    (without the input-claim tail) and the channel."""
+    arr, n = bench.model_steps(layers)
+    ch = G.PoseidonChannel()
+    ch.mix_u64(seed)
+    proof = G.Proof()
+    G.prove_walk(ctx, ch, arr, proof, n_steps=n)
+    return proof, ch
+
+
+def test_config4_qwen_layer_matches_oracle(gpu_ctx):
+    """Config 4: one Qwen2.5-14B layer, 64 tokens (q/o 5120x5120, k/v 5120x1024, gate/up 5120x13824,
+    down 13824x5120; SiLU LogUp over 64x13824 -> 2^20 with a 2^16 table; softmax-exp over 2560x64 ->
+    2^18).  Every serialized felt (round polynomials, final evaluations, LogUp sums, multiplicities,
+    multiplicity rounds, table commitments) and the final digest equal the oracle's."""
+    log("case config4 qwen layer")
+    layers = [bench.LayerWeights(gpu_ctx, bench.QWEN, 0, 0)]
+    proof, gch = gpu_walk(gpu_ctx, layers)
+    felts = proof.serialize()
+    t0 = time.time()
+    och = O.Channel()
+    och.mix_u64(7)
+    ref = [9]
+    oracle_layer(och, bench.QWEN, 0, ref)
+    log(f"  oracle layer {time.time() - t0:.1f} s")
+    n = len(ref)
+    assert felts[:n] == ref
+    assert gch.digest() == och.digest()
+
+
+def test_config3_smollm_30_layers_matches_oracle(gpu_ctx):
+    """Config 3: the 30-layer SmolLM2-135M decode walk (1 token; q 576x576, k/v 576x192, o 576x576,
+    gate/up 576x1536, down 1536x576; SiLU LogUp over 1x1536 with a 2^16 table): the whole serialized
+    proof and the digest equal the oracle's."""
+    log("case config3 smollm 30 layers")
+    layers = [bench.LayerWeights(gpu_ctx, bench.SMOL, l, 0) for l in range(30)]
+    proof, gch = gpu_walk(gpu_ctx, layers)
+    felts = proof.serialize()
+    och = O.Channel()
+    och.mix_u64(7)
+    ref = [30 * 8]
+    for l in range(30):
+        oracle_layer(och, bench.SMOL, l, ref)
+    assert felts[:len(ref)] == ref
+    assert gch.digest() == och.digest()
+
+
+def test_config2_product_sumcheck_2_28_chain(gpu_ctx):
+    """Config 2 at its largest size: f_a, f_b of 2^28 QM31 each (4 GiB per vector).  The verifier's
+    chain p_t(0) + p_t(1) = p_{t-1}(r_{t-1}) with the transcript replayed on the CPU, ending at
+    final_a * final_b; final_a equals the oracle's MLE of the downloaded f_a at the challenges."""
+    n = 1 << 28
+    log("case config2 2^28 chain")
+    fa, fb = gpu_ctx.qvec_synthetic(n, 28), gpu_ctx.qvec_synthetic(n, 29)
+    gch = G.PoseidonChannel()
+    gch.mix_u64(28)
+    rep = O.Channel()
+    rep.mix_u64(28)
+    got = gpu_ctx.sumcheck_product(fa, fb, gch)
+    assert len(got["round_polys"]) == 28
+    cur = None
+    for (c0, c1, c2), r in zip(got["round_polys"], got["challenges"]):
+        if cur is not None:
+            assert Q.qadd(c0, Q.qadd(Q.qadd(c0, c1), c2)) == cur
+        rep.mix_poly_coeffs(c0, c1, c2)
+        assert rep.draw_qm31() == r
+        cur = Q.qadd(Q.qadd(c0, Q.qmul(c1, r)), Q.qmul(c2, Q.qmul(r, r)))
+    assert cur == Q.qmul(got["final_a_eval"], got["final_b_eval"])
+    assert rep.digest() == gch.digest()
+    del fb
+    ha = fa.download()
+    del fa
+    assert tuple(O.evaluate_mle(ha, got["challenges"])) == got["final_a_eval"]
+
+
+def test_softmax_reference_table_qwen_scores(gpu_ctx):
+    """The reference-default softmax-exp table (2^20 entries, table_log_size 0) over the Qwen score
+    tensor 2560x64 (2^18 inputs): 20 multiplicity rounds, the 2^20 table commitment, bit-exact."""
+    log("case softmax 2^20 table")
+    X = O.synthetic(2560, 64, 0, 4)
+    x = gpu_ctx.upload(X)
+    gch, och = G.PoseidonChannel(), O.Channel()
+    pt = gch.draw_qm31s(18)
+    val = gch.draw_qm31()
+    assert pt == och.draw_qm31s(18) and val == och.draw_qm31()
+    gp = G.Proof()
+    pg = gpu_ctx.prove_activation_layer(pt, val, x, 4, gch, 0, gp)
+    po = O.prove_activation_layer(pt, val, X, 4, och, 0)
+    assert len(po["mult_round_polys"]) == 20
+    for key in ("claimed_sum", "eq_round_polys", "final_evals", "mult_round_polys", "mult_final_eval",
+                "mult_claimed_sum", "input_eval", "output_eval", "table_commitment"):
+        assert pg[key] == po[key], key
+    assert (pg["multiplicities"] == po["multiplicities"]).all()
+    assert gch.digest() == och.digest()
+
+
+def layer_shapes(cfg):
+    """The circuit of one bench layer for gkr_verify_walk (fresh claims, bench.model_steps order)."""
+    h, i, q, kv, m = cfg["hidden"], cfg["inter"], cfg["q"], cfg["kv"], cfg["tokens"]
+    F, MM, ACT = G.CLAIM_FRESH, G.STEP_MATMUL, G.STEP_ACTIVATION
+    out = [(MM, m, h, q, 0, 0, F), (MM, m, h, kv, 0, 0, F), (MM, m, h, kv, 0, 0, F), (MM, m, q, h, 0, 0, F),
+           (MM, m, h, i, 0, 0, F), (MM, m, h, i, 0, 0, F), (ACT, m, i, 0, 5, 16, F), (MM, m, i, h, 0, 0, F)]
+    if m > 1:
+        out.append((ACT, cfg["heads"] * m, m, 0, 4, 16, F))
+    return out
+
+
+def test_config5_qwen_48_layers(gpu_ctx):
+    """Config 5: the bench's 48-layer Qwen2.5-14B proof (52.9 GB of weights resident).  The proof
+    bytes equal the bench's recorded fingerprint; the whole serialized proof (432 layer proofs) is
+    replayed by the host verifier with the fresh-claim rule; layers 0, 23 and 47 are proved again
+    by the oracle from the channel state exported before each and equal the GPU's felts and the
+    state after them; a changed felt in layer 30 is rejected."""
+    import hashlib
+    log("case config5 48 layers")
+    layers = [bench.LayerWeights(gpu_ctx, bench.QWEN, l, 0) for l in range(48)]
+    sample = (0, 23, 47)
+    ch = G.PoseidonChannel()
+    ch.mix_u64(7)
+    proof = G.Proof()
+    states = {}
+    for l, L in enumerate(layers):
+        if l in sample or l - 1 in sample:
+            states[l] = ch.export_state()
+        arr, n = bench.model_steps([L])
+        fp, fv = G.prove_walk(gpu_ctx, ch, arr, proof, n_steps=n)
+    states[48] = ch.export_state()
+    words = proof.serialize_words()
+    assert len(words) == 6368361
+    assert hashlib.sha256(words.tobytes()).hexdigest()[:16] == "7553e0f9af527f9a"  # bench.py's proof
+    # layer count, then 48 equal layers, then the tail: input claim (no point: 1 + 4 felts), commitment
+    # count, opening count, IO commitment
+    per, rem = divmod(len(words) - 1 - 8, 48)
+    assert rem == 0
+    for l in sample:
+        t0 = time.time()
+        och = O.Channel()
+        O.set_channel_state(och, states[l])
+        ref = []
+        oracle_layer(och, bench.QWEN, l, ref)
+        log(f"  oracle layer {l}: {time.time() - t0:.1f} s")
+        assert len(ref) == per
+        assert np.array_equal(words[1 + l * per:1 + (l + 1) * per], G.felts_to_words(ref)), f"layer {l}"
+        assert O.channel_state(och) == list(states[l + 1]), f"channel after layer {l}"
+    # host replay of the whole proof
+    proof.set_input_claim(fp, fv)
+    full = proof.serialize_words()
+    shapes = layer_shapes(bench.QWEN) * 48
+    fresh = [proof.layer_claim_value(i) for i, s in enumerate(shapes) if s[0] == G.STEP_MATMUL]
+    vch = G.PoseidonChannel()
+    vch.mix_u64(7)
+    t0 = time.time()
+    pt, val, used = G.verify_walk(full, shapes, None, None, vch, fresh)
+    log(f"  host verifier: {time.time() - t0:.1f} s")
+    assert (pt, val) == (fp, fv) and vch.digest() == ch.digest()
+    bad = full.copy()
+    pos = 1 + 30 * per + 5  # a round-polynomial word of layer 30's q matmul
+    bad[pos, 0] ^= 1
+    v2 = G.PoseidonChannel()
+    v2.mix_u64(7)
+    with pytest.raises(G.GkrError) as e:
+        G.verify_walk(bad, shapes, None, None, v2, fresh)
+    assert e.value.code == 6

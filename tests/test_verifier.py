@@ -225,3 +225,62 @@ def test_serialized_chained_walk():
         g2.import_state(_export(start))
         with pytest.raises(G.GkrError):
             G.verify_walk(bad, shapes, r, v, g2)
+
+
+def test_fresh_claim_walk_verifier():
+    """A fresh-claim walk (the configs 3-5 driver: every layer draws its output point; a MatMul or Mul
+    takes MLE(output) there and mixes it, an Activation draws its value) proved by the oracle and
+    serialized; the walk verifier replays it from the fresh values alone and ends at the same
+    transcript; a changed fresh value or felt is rejected."""
+    rng = np.random.default_rng(9)
+    A1, B1 = rng.integers(0, P, size=(3, 20), dtype=np.uint32), rng.integers(0, P, size=(20, 6), dtype=np.uint32)
+    S = rng.integers(0, P, size=(4, 12), dtype=np.uint32)
+    L, R = rng.integers(0, P, size=(2, 9), dtype=np.uint32), rng.integers(0, P, size=(2, 9), dtype=np.uint32)
+    ch = O.Channel()
+    ch.mix_u64(3)
+    start = ch.clone()
+    cd = [4]
+    fresh = []
+    r = ch.draw_qm31s(lg(3) + lg(6))
+    v = O.matmul_output_claim(A1, B1, r)
+    fresh.append(v)
+    ch.mix_secure_field(v)
+    o = O.prove_matmul_layer(r, v, A1, B1, ch)
+    O.serialize_matmul_layer(cd, o["round_polys"], o["final_a_eval"], o["final_b_eval"])
+    r = ch.draw_qm31s(lg(4) + lg(12))
+    v = ch.draw_qm31()
+    o = O.prove_activation_layer(r, v, S, 2, ch, 8)
+    O.serialize_activation_layer(cd, 2, o)
+    r = ch.draw_qm31s(lg(2) + lg(9))
+    v = O.mul_output_claim(L, R, r)
+    fresh.append(v)
+    ch.mix_secure_field(v)
+    o = O.reduce_mul_layer(r, v, O.padded_mle(L), O.padded_mle(R), ch)
+    O.serialize_mul_layer(cd, o)
+    r = ch.draw_qm31s(lg(3) + lg(6))
+    v = O.matmul_output_claim(A1, B1, r)
+    fresh.append(v)
+    ch.mix_secure_field(v)
+    o = O.prove_matmul_layer(r, v, A1, B1, ch)
+    O.serialize_matmul_layer(cd, o["round_polys"], o["final_a_eval"], o["final_b_eval"])
+    O.serialize_tail(cd, o["next_point"], o["next_value"], [], 0)
+    F = G.CLAIM_FRESH
+    shapes = [(G.STEP_MATMUL, 3, 20, 6, 0, 0, F), (G.STEP_ACTIVATION, 4, 12, 0, 2, 8, F),
+              (G.STEP_MUL, 2, 9, 0, 0, 0, F), (G.STEP_MATMUL, 3, 20, 6, 0, 0, F)]
+    gch = G.PoseidonChannel()
+    gch.import_state(_export(start))
+    pt, val, used = G.verify_walk(cd, shapes, None, None, gch, fresh)
+    assert (pt, val) == (o["next_point"], o["next_value"])
+    assert gch.digest() == ch.digest()
+    bad_fresh = list(fresh)
+    bad_fresh[1] = Q.qadd(bad_fresh[1], (1, 0, 0, 0))
+    g2 = G.PoseidonChannel()
+    g2.import_state(_export(start))
+    with pytest.raises(G.GkrError) as e:
+        G.verify_walk(cd, shapes, None, None, g2, bad_fresh)
+    assert e.value.code == 6
+    g3 = G.PoseidonChannel()
+    g3.import_state(_export(start))
+    with pytest.raises(G.GkrError) as e:
+        G.verify_walk(cd, shapes, None, None, g3, fresh[:2])
+    assert e.value.code == 1
