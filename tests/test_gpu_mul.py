@@ -192,3 +192,18 @@ def test_native_walk_proof_verifies(gpu_ctx):
     vch2.import_state(after_claim)
     with pytest.raises(G.GkrError):
         G.verify_walk(bad, shapes, r, v, vch2)
+
+
+def test_cairo_mul_case_gpu_prover(gpu_ctx):
+    """The reference's hand-built one-variable Mul proof (elo-cairo-verifier/tests/
+    test_layer_verifiers.cairo:143-214): the GPU prover, from a fresh channel, gives exactly its
+    round polynomial and its lhs/rhs evaluations at the challenge drawn after mix_u64(0x4D554C),
+    the claim value and the round polynomial."""
+    from test_reference_cases import cairo_mul_case
+    log("case cairo mul")
+    c = cairo_mul_case()
+    lhs = np.array(c["lhs_mle"], dtype=np.uint32)
+    rhs = np.array(c["rhs_mle"], dtype=np.uint32)
+    g = gpu_ctx.reduce_mul_layer(c["point"], c["value"], lhs, rhs, G.PoseidonChannel())
+    assert g["eq_round_polys"] == [c["poly"]]
+    assert (g["lhs_eval"], g["rhs_eval"]) == (c["lhs"], c["rhs"])

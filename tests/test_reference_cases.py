@@ -1,0 +1,204 @@
+"""Cases the reference itself holds for the LogUp and Mul transcripts and the activation tables,
+ported to this build's verifier (the C ABI's host replay), the oracle's verifier and the provers.
+
+* Mul layer: elo-cairo-verifier/tests/test_layer_verifiers.cairo:143-241 — a one-variable Mul
+  proof written out by hand: c0..c3 from the eq / lhs / rhs coefficients, the challenge drawn after
+  mix_u64(0x4D554C), mix(claim value), mix_poly_coeffs_deg3, and lhs_eval = a0 + (a1 - a0) s.  The
+  verifiers must accept it (and reject the case's bad round polynomial), and the provers must
+  produce exactly those coefficients and evaluations on the same inputs.
+* Activation (LogUp) layer: test_layer_verifiers.cairo:443-580 — a one-variable eq-sumcheck whose
+  round polynomial is eq(r0, X) itself (sum 1), with gamma and beta drawn after
+  mix_u64(0x4C4F47), mix_u64(type tag), the claimed sum mixed before the round, and
+  final_w_eval = 1 / gamma with zero input and output evaluations.  The Cairo verifier checks no
+  table side; the reference's Rust verifier (verifier.rs:3058-3290) and this build's do, so the
+  port takes all-zero multiplicities (table-side sum 0 = the claimed sum) and the matching
+  all-zero multiplicity sumcheck; everything the Cairo case's acceptance depends on is kept.
+* Activation tables: engine/src/gadgets/lookup_table.rs:466-633 (GELU against its f64 formula
+  at 200 points, known values, limits, monotonicity; SiLU(0) and SiLU(1.0))."""
+import math
+
+import gkr_mi355x as G
+import numpy as np
+import oracle as O
+import pytest
+import qm31_py as Q
+
+P = (1 << 31) - 1
+ONE, ZERO = (1, 0, 0, 0), (0, 0, 0, 0)
+
+
+def _q(v):
+    return (v % P, 0, 0, 0)
+
+
+def cairo_mul_case():
+    """test_verify_mul_layer_single_var: the hand-built proof and its channel replay."""
+    r0 = _q(3)
+    a0, a1, b0, b1 = _q(2), _q(5), _q(3), _q(7)
+    eq0, eq1 = Q.qsub(ONE, r0), r0
+    v = Q.qadd(Q.qmul(eq0, Q.qmul(a0, b0)), Q.qmul(eq1, Q.qmul(a1, b1)))
+    eqc0 = Q.qsub(ONE, r0)
+    eqc1 = Q.qsub(Q.qadd(r0, r0), ONE)
+    da, db = Q.qsub(a1, a0), Q.qsub(b1, b0)
+    ea0 = Q.qmul(eqc0, a0)
+    ea1 = Q.qadd(Q.qmul(eqc0, da), Q.qmul(eqc1, a0))
+    ea2 = Q.qmul(eqc1, da)
+    c0 = Q.qmul(ea0, b0)
+    c1 = Q.qadd(Q.qmul(ea0, db), Q.qmul(ea1, b0))
+    c2 = Q.qadd(Q.qmul(ea1, db), Q.qmul(ea2, b0))
+    c3 = Q.qmul(ea2, db)
+    assert c0 == Q.qmul(eq0, Q.qmul(a0, b0))
+    assert Q.qadd(Q.qadd(Q.qadd(c0, c1), c2), c3) == Q.qmul(eq1, Q.qmul(a1, b1))
+    ch = G.PoseidonChannel()  # the prover's Fiat-Shamir, replayed as the case does
+    ch.mix_u64(0x4D554C)
+    ch.mix_secure_field(v)
+    ch.mix_poly_coeffs_deg3(c0, c1, c2, c3)
+    s0 = ch.draw_qm31()
+    lhs = Q.qadd(a0, Q.qmul(da, s0))
+    rhs = Q.qadd(b0, Q.qmul(db, s0))
+    return {"point": [r0], "value": v, "poly": (c0, c1, c2, c3), "lhs": lhs, "rhs": rhs,
+            "lhs_mle": [a0, a1], "rhs_mle": [b0, b1]}
+
+
+def test_cairo_mul_case_accepted_by_both_verifiers():
+    c = cairo_mul_case()
+    proof = {"eq_round_polys": [c["poly"]], "lhs_eval": c["lhs"], "rhs_eval": c["rhs"]}
+    G.verify_mul_layer(c["point"], c["value"], proof, G.PoseidonChannel())
+    rc, _ = O.verify_mul_layer(c["point"], c["value"], proof, O.Channel())
+    assert rc == 0
+
+
+def test_cairo_mul_case_bad_round_poly_rejected():
+    """test_verify_mul_layer_bad_round_poly: c1 is rebuilt from the claim, so the round sum holds,
+    and the final check (MUL_FINAL_MISMATCH) fails."""
+    v = _q(100)
+    bad = {"eq_round_polys": [(_q(10), ZERO, _q(30), _q(40))], "lhs_eval": ZERO, "rhs_eval": ZERO}
+    with pytest.raises(G.GkrError) as e:
+        G.verify_mul_layer([_q(3)], v, bad, G.PoseidonChannel())
+    assert e.value.code == 6
+    rc, _ = O.verify_mul_layer([_q(3)], v, bad, O.Channel())
+    assert rc != 0
+
+
+def test_cairo_mul_case_oracle_prover():
+    """The oracle's reduce_mul_layer on the case's operands gives the case's coefficients and
+    evaluations (the round polynomial is unique; the transcript order fixes s0)."""
+    c = cairo_mul_case()
+    lhs = np.array(c["lhs_mle"], dtype=np.uint32)
+    rhs = np.array(c["rhs_mle"], dtype=np.uint32)
+    o = O.reduce_mul_layer(c["point"], c["value"], lhs, rhs, O.Channel())
+    assert o["eq_round_polys"] == [c["poly"]]
+    assert (o["lhs_eval"], o["rhs_eval"]) == (c["lhs"], c["rhs"])
+
+
+def cairo_activation_case(tag, table_log, r0=_q(5), poly=None, claimed_sum=ZERO):
+    """test_verify_activation_layer_single_var / test_activation_channel_state_changes, with the
+    table side made consistent (zero multiplicities: table sum 0 = claimed sum; a zero multiplicity
+    sumcheck).  Returns the claim point and the proof dict in prove_activation_layer's layout."""
+    sim = G.PoseidonChannel()
+    sim.mix_u64(0x4C4F47)
+    sim.mix_u64(tag)
+    gamma = sim.draw_qm31()
+    sim.draw_qm31()  # beta
+    if poly is None:  # the eq polynomial of the one variable: (1 - r0) + (2 r0 - 1) X
+        poly = (Q.qsub(ONE, r0), Q.qsub(Q.qadd(r0, r0), ONE), ZERO, ZERO)
+    sim.mix_secure_field(claimed_sum)
+    sim.mix_poly_coeffs_deg3(*poly)
+    sim.draw_qm31()
+    mult_rounds = [(ZERO, ZERO)] * table_log
+    return [r0], {
+        "claimed_sum": claimed_sum, "eq_round_polys": [poly],
+        "final_evals": (Q.qinv(gamma), ZERO, ZERO),
+        "multiplicities": np.zeros(1 << table_log, dtype=np.uint32),
+        "mult_round_polys": mult_rounds, "mult_final_eval": ZERO, "mult_claimed_sum": ZERO,
+        "input_eval": _q(42), "output_eval": _q(99),
+        "table_commitment": O.hash_many([tag, table_log]),
+    }
+
+
+@pytest.mark.parametrize("tag,table_log", [(5, 4), (2, 6), (4, 5)])
+def test_cairo_activation_case_accepted(tag, table_log):
+    pt, proof = cairo_activation_case(tag, table_log)
+    ch = G.PoseidonChannel()
+    d0 = ch.digest()
+    assert G.verify_activation_layer(pt, tag, table_log, proof, ch) == _q(42)
+    assert ch.digest() != d0
+    assert O.verify_activation_layer(pt, ZERO, tag, table_log, proof, O.Channel()) == 0
+
+
+def test_cairo_activation_case_zero_point():
+    """test_activation_channel_state_changes: r0 = 0, round polynomial (1, -1, 0, 0)."""
+    pt, proof = cairo_activation_case(3, 4, r0=ZERO, poly=(ONE, Q.qsub(ZERO, ONE), ZERO, ZERO))
+    assert G.verify_activation_layer(pt, 3, 4, proof, G.PoseidonChannel()) == _q(42)
+    assert O.verify_activation_layer(pt, ZERO, 3, 4, proof, O.Channel()) == 0
+
+
+def test_cairo_activation_case_rejections():
+    """test_verify_activation_layer_bad_round_poly (LOGUP_FINAL_MISMATCH), and the case with gamma
+    drawn in another order (tag mixed once) or w = 1 / beta: all rejected."""
+    pt, proof = cairo_activation_case(5, 4)
+    bad = dict(proof)
+    bad["eq_round_polys"] = [(_q(10), ZERO, _q(30), _q(40))]
+    for p in (bad,):
+        with pytest.raises(G.GkrError) as e:
+            G.verify_activation_layer(pt, 5, 4, p, G.PoseidonChannel())
+        assert e.value.code == 6
+        assert O.verify_activation_layer(pt, ZERO, 5, 4, p, O.Channel()) != 0
+    # w = 1 / gamma' with gamma' from a transcript that skips the type tag
+    sim = G.PoseidonChannel()
+    sim.mix_u64(0x4C4F47)
+    g_wrong = sim.draw_qm31()
+    wrong = dict(proof)
+    wrong["final_evals"] = (Q.qinv(g_wrong), ZERO, ZERO)
+    with pytest.raises(G.GkrError) as e:
+        G.verify_activation_layer(pt, 5, 4, wrong, G.PoseidonChannel())
+    assert e.value.code == 6
+    assert O.verify_activation_layer(pt, ZERO, 5, 4, wrong, O.Channel()) != 0
+
+
+# ------------------------------------------------------------------ lookup_table.rs cases
+SCALE = 1 << 16
+
+
+def _tables():
+    return {2: G.activation_table(2, 17), 5: G.activation_table(5, 17)}
+
+
+def test_gelu_matches_f64_reference():
+    """lookup_table.rs test_gelu_matches_f64_reference: exact equality at i = 0, 500, ..., 99500
+    with the test's own f64 formula (x_real.powi(3) = (x * x) * x)."""
+    gelu = _tables()[2]
+    k = math.sqrt(2.0 / math.pi)
+    for i in range(0, 200 * 500, 500):
+        x = i / SCALE
+        inner = k * (x + 0.044715 * (x * x * x))
+        expected = round(0.5 * x * (1.0 + math.tanh(inner)) * SCALE)
+        assert int(gelu[i]) == expected == O.activation(2, i), i
+
+
+def test_gelu_known_values_and_limits():
+    """test_gelu_known_values (1% tolerance), test_gelu_converges_to_identity_for_large_x,
+    test_gelu_negative_returns_near_zero, test_gelu_monotonic_positive, GELU vs ReLU at 0.5/1.0."""
+    for x, y in [(0.0, 0.0), (0.5, 0.3457), (1.0, 0.8412), (2.0, 1.9545), (3.0, 2.9964)]:
+        out = O.activation(2, round(x * SCALE))
+        assert abs(out - round(y * SCALE)) <= round(0.01 * SCALE), x
+    big = 5 * SCALE
+    assert abs(O.activation(2, big) - big) <= SCALE // 100
+    assert O.activation(2, P - 5 * SCALE) == 0
+    r3 = O.activation(2, P - 3 * SCALE)
+    assert r3 == 0 or r3 > P - SCALE
+    prev = 0
+    for i in range(100):
+        out = O.activation(2, i * (SCALE // 10))
+        assert out >= prev
+        prev = out
+    assert O.activation(2, SCALE // 2) < SCALE // 2 and O.activation(2, SCALE) < SCALE
+
+
+def test_silu_cases():
+    """test_silu_zero and test_silu_positive (SiLU(1.0) within 1 of round(2^16 / (1 + e^-1)))."""
+    silu = _tables()[5]
+    assert int(silu[0]) == 0 == O.activation(5, 0)
+    expected = round(1.0 / (1.0 + math.exp(-1.0)) * 65536.0)
+    assert abs(int(silu[65536]) - expected) <= 1
+    assert O.activation(5, 65536) == int(silu[65536])
