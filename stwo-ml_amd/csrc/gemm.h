@@ -51,7 +51,7 @@ __device__ __forceinline__ void balanced_digits(int32_t v, int32_t (&d)[4]) {
 // Which planes of X (count canonical M31 values) are non-zero: bit p of
 // *mask.  Grid-stride, an OR across the workgroup in LDS, then one vector
 // atomic per workgroup (launch at most a few hundred workgroups).
-__global__ void __launch_bounds__(256) k_digit_mask(const uint32_t* __restrict__ X, uint64_t count,
+static __global__ void __launch_bounds__(256) k_digit_mask(const uint32_t* __restrict__ X, uint64_t count,
                                                     uint32_t* __restrict__ mask) {
   __shared__ uint32_t wave_bits[4];
   uint32_t bits = 0;
@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(256) k_digit_mask(const uint32_t* __restrict__
 // row-major (B: outer = column).  One thread fills one lane slot (16 bytes
 // per plane) of one block; K and outer beyond the matrix are zero.  When mask
 // is given (zeroed by the caller), bit p is set if plane p is non-zero.
-__global__ void __launch_bounds__(256) k_digit_pack(const uint32_t* __restrict__ X, uint64_t outer, uint64_t K,
+static __global__ void __launch_bounds__(256) k_digit_pack(const uint32_t* __restrict__ X, uint64_t outer, uint64_t K,
                                                     bool kmajor, int nplanes, uint64_t ntiles, uint64_t nsteps,
                                                     int8_t* __restrict__ planes, uint32_t* __restrict__ mask) {
   __shared__ uint32_t wave_bits[4];
@@ -137,7 +137,7 @@ __device__ __forceinline__ uint32_t gemm_mod_p(int64_t x) {
 // variants back to back; *amask (A's non-zero planes, written by the A
 // packing) makes exactly one of them work, so no host round trip decides.
 template <int PA, int PB, int U>
-__global__ void __launch_bounds__(256) k_gemm_m31(const int8_t* __restrict__ Ap, uint64_t a_plane_bytes,
+static __global__ void __launch_bounds__(256) k_gemm_m31(const int8_t* __restrict__ Ap, uint64_t a_plane_bytes,
                                                   const uint32_t* __restrict__ amask,
                                                   const int8_t* __restrict__ Bp, uint64_t b_plane_bytes,
                                                   uint64_t m, uint64_t n, uint64_t nsteps, uint64_t rtiles,
@@ -205,7 +205,7 @@ __global__ void __launch_bounds__(256) k_gemm_m31(const int8_t* __restrict__ Ap,
 }
 
 // C = sum over splits of the partials, mod P.
-__global__ void k_gemm_reduce(const uint32_t* __restrict__ part, uint64_t count, int splits, uint32_t* __restrict__ C) {
+static __global__ void k_gemm_reduce(const uint32_t* __restrict__ part, uint64_t count, int splits, uint32_t* __restrict__ C) {
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= count) return;
   uint64_t s = 0;

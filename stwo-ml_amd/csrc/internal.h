@@ -1,0 +1,555 @@
+// Shared internals of the host side of the MI355X GKR prover (not part of
+// the C ABI): the error convention, the device context and its buffers, the
+// result sinks and waits, the hand-over session, the multi-round trip
+// planner and launcher, the channel and proof records, and the functions
+// one translation unit provides to the others.  Each .hip file of this
+// directory implements one part of include/gkr_mi355x.h on top of it.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <chrono>
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/gkr_mi355x.h"
+#include "field.h"
+#include "kernels.h"
+#include "poseidon.h"
+
+namespace gkr {
+struct MerkleConsts;  // merkle.h
+}
+using namespace gkr;
+
+// ------------------------------------------------------------------ errors
+// Records the message of a failure for gkr_last_error() and returns code.
+int fail(int code, const char* fmt, ...);
+#define HIP_TRY(expr)                                                                       \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess) return fail(GKR_ERR_DEVICE, "%s: %s (%s:%d)", #expr,              \
+                                      hipGetErrorString(e_), __FILE__, __LINE__);           \
+  } while (0)
+#define TRY(expr)             \
+  do {                        \
+    int rc_ = (expr);         \
+    if (rc_ != GKR_OK) return rc_; \
+  } while (0)
+
+static inline qm31 Q(const gkr_qm31& x) { return qm31{x.v[0], x.v[1], x.v[2], x.v[3]}; }
+static inline gkr_qm31 G(const qm31& x) {
+  gkr_qm31 r;
+  r.v[0] = x.a; r.v[1] = x.b; r.v[2] = x.c; r.v[3] = x.d;
+  return r;
+}
+static inline bool canonical_q(const gkr_qm31& x) {
+  return x.v[0] < P && x.v[1] < P && x.v[2] < P && x.v[3] < P;
+}
+static inline uint64_t next_pow2(uint64_t v) {
+  uint64_t p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+static inline int log2_exact(uint64_t v) {
+  int l = 0;
+  while ((1ull << l) < v) l++;
+  return l;
+}
+static inline felt felt_from_abi(const gkr_felt& f) { return felt_to_mont(felt_canon_from_words(f.w)); }
+static inline gkr_felt felt_to_abi(const felt& m) {
+  gkr_felt r;
+  felt_canon_to_words(felt_from_mont(m), r.w);
+  return r;
+}
+inline bool felt_abi_canonical(const gkr_felt& f) {
+  felt c = felt_canon_from_words(f.w);
+  return !felt_detail::geq_p(c.l);
+}
+
+// ------------------------------------------------------------------ context
+enum Slot {
+  S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
+  S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NSLOTS
+};
+// Timer ids: device kernels (HIP events) and host-side phases (Fiat-Shamir
+// hashing inside the reducers, waiting for trip results, waiting for the
+// hand-over of the last vectors).
+enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
+                K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
+                K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NKERNELS = 13 };
+constexpr int kMaxPartialBlocks = 1024;
+constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
+// Result slots in the coherent host area (h_out): 0 .. 63 serve the result in
+// flight; results launched ahead of time and read later have their own.
+constexpr int kSlotEq0 = 64;     // eq-sumcheck trip 0 (up to 64 values)
+constexpr int kSlotPrep = 128;   // LogUp prepare: trace sum, input MLE
+constexpr int kSlotTable = 130;  // LogUp table-side sum
+constexpr int kSlotMult0 = 136;  // multiplicity sumcheck trip 0 (up to 8 values)
+constexpr int kOutSlots = 192;
+
+struct KernelStat {
+  double ms = 0;
+  uint64_t launches = 0;
+  uint64_t bytes = 0;
+};
+struct PendingTiming {
+  int kid;
+  hipEvent_t e0, e1;
+  uint64_t bytes;
+};
+
+struct MatMulCache {
+  bool valid = false;
+  const gkr_matrix* a = nullptr;
+  const gkr_matrix* b = nullptr;
+  std::vector<gkr_qm31> r_i, r_j;
+  // sums of the product sumcheck's first trip over the restricted vectors
+  // (rounds 0 .. trip0_k - 1), computed with the output claim
+  bool have_trip0 = false;
+  int trip0_k = 0;
+  qm31 trip0[kMaxSums];
+};
+
+struct gkr_matrix {
+  gkr_ctx* ctx;
+  uint32_t* dev;
+  uint64_t rows, cols;
+  bool owned;
+  // digit planes of the matrix as the B operand of the forward product
+  // (gemm.h), built on first use; the contents of a matrix never change
+  int8_t* bplanes = nullptr;
+  int bnplanes = 0;
+  // int8 copy for the weight-side restriction (rows of kR8Block-byte
+  // blocks in k_restrict_cols8's permuted order, padded to r8_stride bytes),
+  // built on first use when every entry is int8-range;
+  // r8_state: 0 not yet checked, 1 copy present, -1 not int8-range
+  int8_t* r8 = nullptr;
+  uint64_t r8_stride = 0;
+  int r8_state = 0;
+};
+
+struct gkr_qvec {
+  gkr_ctx* ctx;
+  qm31* dev;
+  uint64_t n;
+};
+
+struct gkr_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  void* buf[S_NSLOTS] = {};
+  size_t cap[S_NSLOTS] = {};
+  qm31* h_res = nullptr;  // pinned result staging (64 QM31)
+  uint32_t* h_mult = nullptr;  // pinned copy of the LogUp multiplicities
+  qm31* h_vec = nullptr;       // coherent pinned: vectors handed over by k_handover (2 x kHandMax)
+  size_t h_mult_cap = 0;
+  qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
+  uint32_t* h_flag = nullptr; // coherent pinned: sequence number of the last delivery
+  Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
+  uint32_t seq = 0;            // last result sequence number handed out
+  uint32_t mb_seq = 0;         // last mailbox sequence number handed out
+  int timing = 0;  // 0 off; 1: k_restrict_cols events + host timers; 2: events on every timed kernel
+  KernelStat stats[K_NKERNELS];
+  std::vector<PendingTiming> pending;
+  std::vector<hipEvent_t> free_events;
+  MatMulCache mm;
+  std::map<uint64_t, std::vector<uint32_t>> tables;  // (tag << 32 | log) -> table outputs
+  std::set<gkr_matrix*> matrices;  // live matrices; detached when the context is destroyed
+  std::set<gkr_qvec*> qvecs;       // live QM31 vectors; detached likewise
+  uint64_t table_on_device = 0;    // (tag << 32 | log) of the table held in S_TABLE, 0 = none
+  MerkleConsts* merkle_consts = nullptr;  // device copy, built on first use
+  bool fb_pending = false;  // f_b of the last restriction still as column-chunk partials (S_COLPART)
+  uint64_t fb_rows = 0, fb_pk = 0;
+  int fb_chunks = 0;
+  uint32_t trip_count = 0;         // value of the fused trips' arrival counter (S_TRIPCNT) after the queued launches
+  bool trip_count_valid = false;   // false: zero the counter before the next fused trip
+  bool int8_weights = false;       // GKR_INT8_WEIGHTS=1 at creation: int8 weight-side restriction
+  // allocation-free mode (gkr_sumcheck_product_noalloc): ensure() hands out
+  // the partial rows and the arrival counter from the device's static
+  // scratch array (scratch_dev: its address on this context's device) and
+  // refuses every other slot
+  uint8_t* scratch_dev = nullptr;
+  bool noalloc = false;
+  // test hooks (gkr_ctx_debug), each consumed by the next hand-over
+  bool debug_handover_cancel = false;  // the host leaves before posting the challenges
+  uint32_t debug_handover_spins = 0;   // nonzero: the kernel's bounded wait, posted only after it expired
+};
+
+// ------------------------------------------------------------------ static scratch (allocation-free entry point)
+// Device memory of gkr_sumcheck_product_noalloc, one copy per GPU for the
+// life of the process: the two fold levels of each vector (n/2 and n/4
+// entries), the trips' partial rows and their arrival counter.  Host code
+// never uses the array's name as an address: gkr_ctx_create looks up its
+// address on the context's device (hipGetSymbolAddress) and everything
+// else goes through gkr_ctx::scratch_dev.
+constexpr uint64_t kNoAllocMaxN = 1ull << 20;  // longest vectors of the allocation-free sumcheck
+constexpr size_t kScratchFold1 = (kNoAllocMaxN / 2) * sizeof(qm31);
+constexpr size_t kScratchFold2 = (kNoAllocMaxN / 4) * sizeof(qm31);
+constexpr size_t kScratchOffA1 = 0, kScratchOffB1 = kScratchFold1, kScratchOffA2 = 2 * kScratchFold1,
+                 kScratchOffB2 = 2 * kScratchFold1 + kScratchFold2, kScratchOffPart = 2 * kScratchFold1 + 2 * kScratchFold2;
+constexpr size_t kScratchPartBytes = (size_t)kMaxSums * kMaxPartialBlocks * sizeof(qm31);
+constexpr size_t kScratchOffCount = kScratchOffPart + kScratchPartBytes;
+constexpr size_t kScratchBytes = kScratchOffCount + 256;  // 25 MiB + 256 B
+
+int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out);
+template <typename T>
+inline int ensureT(gkr_ctx* c, Slot s, size_t count, T** out) {
+  void* p;
+  TRY(ensure(c, s, count * sizeof(T), &p));
+  *out = (T*)p;
+  return GKR_OK;
+}
+
+int ensure_host_mult(gkr_ctx* c, uint64_t n);
+
+hipEvent_t get_event(gkr_ctx* c);
+struct TimedLaunch {
+  gkr_ctx* c;
+  int kid;
+  uint64_t bytes;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
+    if (c->timing >= 2 || (c->timing == 1 && (kid == K_RESTRICT_COLS || kid == K_RESTRICT_ROWS || kid == K_MERKLE))) {
+      e0 = get_event(c);
+      e1 = get_event(c);
+      if (e0) (void)hipEventRecord(e0, c->stream);
+    }
+  }
+  ~TimedLaunch() {
+    if (e0 && e1) {
+      (void)hipEventRecord(e1, c->stream);
+      c->pending.push_back({kid, e0, e1, bytes});
+    }
+  }
+};
+struct HostTimer {
+  gkr_ctx* c;
+  int kid;
+  std::chrono::steady_clock::time_point t0;
+  HostTimer(gkr_ctx* c_, int kid_) : c(c_), kid(kid_) {
+    if (c->timing) t0 = std::chrono::steady_clock::now();
+  }
+  ~HostTimer() {
+    if (c->timing) {
+      c->stats[kid].ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+      c->stats[kid].launches++;
+    }
+  }
+};
+void collect_timing(gkr_ctx* c);
+int sync(gkr_ctx* c);
+inline int check_launch() {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(GKR_ERR_DEVICE, "kernel launch: %s", hipGetErrorString(e));
+  return GKR_OK;
+}
+static inline unsigned grid_for(uint64_t n, uint64_t per_block = kBlock) {
+  uint64_t g = (n + per_block - 1) / per_block;
+  return (unsigned)(g == 0 ? 1 : g);
+}
+static inline unsigned partial_grid(uint64_t n) {
+  uint64_t g = (n + kBlock - 1) / kBlock;
+  if (g > kMaxPartialBlocks) g = kMaxPartialBlocks;
+  return (unsigned)(g == 0 ? 1 : g);
+}
+
+PointArg make_point(const qm31* r, int n);
+
+// eq(r, x) for x < count (r[0] on the most significant bit of x).
+int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out);
+
+// Result and mailbox sequence numbers come in consecutive ranges and restart
+// at 1 before they reach the cancel code reserved at the top of the u32 range
+// (kWaitCancel); waits compare them modulo 2^32.
+constexpr uint32_t kSeqLimit = 0xFFFFFF00u;
+inline uint32_t alloc_seq(uint32_t* counter, uint32_t n) {
+  if (*counter >= kSeqLimit - n) *counter = 0;
+  const uint32_t base = *counter + 1;
+  *counter += n;
+  return base;
+}
+// Partial rows for a reducing kernel.  `slot` selects where in the coherent
+// host buffer the finisher writes its NQ results: slots 0-3 serve the round
+// in flight, higher slots hold results launched ahead of time and read
+// later.  The partial rows are shared: each finisher consumes them before the
+// next reducing kernel on the stream overwrites them.
+int make_sink(gkr_ctx* c, RoundSink* sk, int slot = 0);
+// Launch the one-workgroup finisher that adds `nblocks` partial rows and
+// delivers the NQ results (after a multi-workgroup reducing kernel).
+template <int NQ>
+static int launch_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks) {
+  TRY(check_launch());
+  hipLaunchKernelGGL(k_finish<NQ>, dim3(1), dim3(kBlock), 0, c->stream, sk, (uint32_t)nblocks);
+  return check_launch();
+}
+// Wait until result `seq` has been published and copy NQ values.  The wait
+// spins on the coherent flag and never blocks on the stream (a hand-over
+// kernel queued behind the result may be waiting for the host): from time to
+// time it queries the stream, so a device error, or a drained stream without
+// the result, is reported; after kWaitWallSeconds it gives up.  hand_mb != 0:
+// the result comes from the hand-over waiting for mailbox sequence hand_mb,
+// whose expiry is reported at once.
+constexpr double kWaitWallSeconds = 60.0;
+template <int NQ>
+static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_HOST_WAIT_TAIL, int slot = 0,
+                       uint32_t hand_mb = 0) {
+  TRY(check_launch());
+  HostTimer ht(c, timer);
+  volatile uint32_t* flag = c->h_flag;
+  volatile uint32_t* expired = &c->mailbox->expired;
+  std::chrono::steady_clock::time_point t0;
+  // the flag only moves forward (mod 2^32): a later delivery implies this one
+  for (uint64_t spins = 0; (int32_t)(*flag - seq) < 0; spins++) {
+    if (hand_mb && *expired == hand_mb)
+      return fail(GKR_ERR_DEVICE, "hand-over kernel stopped waiting for the challenges (mailbox %u)", hand_mb);
+    if ((spins & 0xFFFF) != 0xFFFF) continue;
+    if (spins == 0xFFFF) t0 = std::chrono::steady_clock::now();
+    const hipError_t e = hipStreamQuery(c->stream);
+    if (e == hipSuccess) {
+      if ((int32_t)(*flag - seq) >= 0) break;
+      return fail(GKR_ERR_DEVICE, "device result %u not delivered (stream drained)", seq);
+    }
+    if (e != hipErrorNotReady) return fail(GKR_ERR_DEVICE, "waiting for device result %u: %s", seq, hipGetErrorString(e));
+    if (std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > kWaitWallSeconds)
+      return fail(GKR_ERR_DEVICE, "device result %u not delivered after %.0f s", seq, kWaitWallSeconds);
+  }
+  __atomic_thread_fence(__ATOMIC_ACQUIRE);
+  for (int q = 0; q < NQ; q++) host_out[q] = c->h_out[slot + q];
+  return GKR_OK;
+}
+template <int NQ>
+static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
+  return wait_result<NQ>(c, sk.seq, host_out, K_HOST_WAIT, (int)(sk.out - c->h_out));
+}
+// Host side of a k_handover launch: posts the last trip's challenges into
+// the mailbox and receives the folded vectors.  If the host leaves before
+// posting (an error), the guard posts the cancel code so the kernel stops
+// waiting at once, drains the stream, and clears the mailbox so that the
+// next hand-over does not read the cancel code.
+struct HandoverSession {
+  gkr_ctx* c;
+  uint32_t res_seq = 0, mb_seq = 0;
+  bool launched = false, done = false;
+  bool cancel_before_post = false;  // test hook (gkr_ctx_debug): leave without posting
+  bool hold_post = false;           // test hook (gkr_ctx_debug): post only after the kernel's wait expired
+  explicit HandoverSession(gkr_ctx* c_) : c(c_) {}
+  // Launch k_handover<NV> over the vectors a (, b) of length len, to be folded by k challenges.
+  template <int NV>
+  int launch(const qm31* a, const qm31* b, uint64_t len, int k) {
+    HostTimer ht(c, K_HOST_LAUNCH);
+    if (len > (uint64_t)kHandMax || k < 0 || k > kTripMaxK || (len >> k) == 0)
+      return fail(GKR_ERR_DEVICE, "hand-over of %llu entries folded %d times", (unsigned long long)len, k);
+    res_seq = alloc_seq(&c->seq, 1);
+    mb_seq = alloc_seq(&c->mb_seq, 1);
+    uint32_t spin_limit = kWaitSpinLimit;
+    if (c->debug_handover_spins) {  // test hook: a short bounded wait that expires before the post
+      spin_limit = c->debug_handover_spins;
+      c->debug_handover_spins = 0;
+      hold_post = true;
+    }
+    if (c->debug_handover_cancel) {
+      cancel_before_post = true;
+      c->debug_handover_cancel = false;
+    }
+    hipLaunchKernelGGL(k_handover<NV>, dim3(1), dim3(kBlock), 0, c->stream, a, b, (uint32_t)len, k, c->mailbox,
+                       mb_seq, spin_limit, c->h_vec, c->h_flag, res_seq);
+    launched = true;
+    return check_launch();
+  }
+  int post(const qm31* chal, int k) {
+    if (cancel_before_post) return fail(GKR_ERR_DEVICE, "hand-over cancelled before the challenges were posted");
+    if (hold_post) {
+      const auto t0 = std::chrono::steady_clock::now();
+      volatile uint32_t* expired = &c->mailbox->expired;
+      while (*expired != mb_seq && std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() < 10.0) {
+      }
+    }
+    for (int r = 0; r < k; r++) c->mailbox->alpha[r] = chal[r];
+    __atomic_store_n(&c->mailbox->seq, mb_seq, __ATOMIC_RELEASE);
+    return GKR_OK;
+  }
+  // Wait for the folded vectors: count vectors of len entries each.
+  int fetch(uint64_t len, int count, std::vector<qm31>* out) {
+    TRY(wait_result<0>(c, res_seq, nullptr, K_HOST_WAIT_TAIL, 0, mb_seq));
+    for (int v = 0; v < count; v++) out[v].assign(c->h_vec + v * len, c->h_vec + (v + 1) * len);
+    done = true;
+    return GKR_OK;
+  }
+  ~HandoverSession() {
+    if (launched && !done) {
+      __atomic_store_n(&c->mailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
+      (void)hipStreamSynchronize(c->stream);
+      __atomic_store_n(&c->mailbox->seq, 0u, __ATOMIC_RELEASE);  // 0 is never a wanted sequence
+    }
+  }
+};
+
+// ------------------------------------------------------------------ multi-round trips (host side)
+// A sumcheck over 2^T entries runs as a few device trips of K <= 3 rounds
+// each (k_trip: one launch plus the finisher per trip), then k_handover
+// folds the last trip's vectors and the host finishes the rounds on vectors
+// of at most host_len entries.  The first trip covers min(k0, T) rounds;
+// later trips cover trip_k(n) rounds: a trip's sums cost 2^K products per
+// entry, so trips over long vectors (bound by HBM and VALU, not by launch
+// latency) take fewer rounds each.  The loop ends once the next trip's
+// vectors would fit the host, so the last trip's vectors have at most
+// host_len * 2^K <= kHandMax entries (host_len <= 256).
+struct Trip {
+  int t, K;    // rounds t .. t + K - 1
+  uint64_t n;  // vector length at round t
+};
+#ifndef GKR_TRIP_BIG
+#define GKR_TRIP_BIG (1ull << 16)
+#endif
+constexpr uint64_t kTripBig = GKR_TRIP_BIG;
+#ifndef GKR_TRIP_HUGE
+#define GKR_TRIP_HUGE (1ull << 20)
+#endif
+constexpr uint64_t kTripHuge = GKR_TRIP_HUGE;
+// Rounds per trip over a vector of n entries: 3 up to kTripBig, 2 up to kTripHuge, then 1.
+static inline int trip_k(uint64_t n) { return n > kTripHuge ? 1 : n > kTripBig ? 2 : 3; }
+#ifndef GKR_TRIP_MAX_BLOCKS
+#define GKR_TRIP_MAX_BLOCKS 512
+#endif
+constexpr unsigned kTripMaxBlocks = GKR_TRIP_MAX_BLOCKS;  // partial rows per trip (the finisher adds them)
+#ifndef GKR_TRIP_MAX_BLOCKS_SHORT
+#define GKR_TRIP_MAX_BLOCKS_SHORT 1024
+#endif
+constexpr unsigned kTripMaxBlocksShort = GKR_TRIP_MAX_BLOCKS_SHORT;  // the same for trips of at most 2 rounds
+static_assert(GKR_TRIP_MAX_BLOCKS_SHORT <= kMaxPartialBlocks && GKR_TRIP_MAX_BLOCKS <= kMaxPartialBlocks,
+              "trip partial rows exceed the partial buffer");
+// Trips whose one-entry-per-thread grid is at most kTripFusedGrid workgroups
+// run on at most kTripFusedMax workgroups and finish in the kernel itself.
+#ifndef GKR_TRIP_FUSED
+#define GKR_TRIP_FUSED 1
+#endif
+#ifndef GKR_TRIP_FUSED_GRID
+#define GKR_TRIP_FUSED_GRID 256
+#endif
+constexpr unsigned kTripFusedGrid = GKR_TRIP_FUSED_GRID;
+std::vector<Trip> plan_trips(int T, uint64_t host_len, int k0);
+static inline int trip_nq(int kind, int K) { return kind == 2 ? (1 << K) : (1 << (2 * K)); }
+// eqlin(z, X) = (1 - z)(1 - X) + z X, the multilinear eq factor of one coordinate.
+static inline qm31 eqlin(const qm31& z, const qm31& x) {
+  const qm31 one = qm31_one();
+  return qm31_add(qm31_mul(qm31_sub(one, z), qm31_sub(one, x)), qm31_mul(z, x));
+}
+// Lagrange weights E[u] (u < 2^j, first challenge on the MSB) of r[0..j).
+void lagrange_weights(const qm31* r, int j, qm31* E);
+// Round j (0-based within the trip) of a product-type trip from its cross sums
+// G (4^K, row-major over sub-vectors c, c'), evaluated at the nx points xs:
+//   p(X) = sum_v sum_{u,u',b,b'} E[u] E[u'] eqlin(X,b) eqlin(X,b') G[(u,b,v)][(u',b',v)]
+// with E the Lagrange weights of the trip's challenges r[0..j) and v running
+// over the trip's later variables.  For the eq-sumcheck (zt given: the claim
+// coordinates of the trip's variables; cpre: prod of eqlin(z_l, r_l) over all
+// earlier rounds) the eq factors are applied:
+//   p(X) *= cpre * prod_{i<j} eqlin(zt_i, r_i) * eqlin(zt_j, X),  v weighted by eqlin(zt, v).
+void trip_round_gram(const qm31* G, int K, int j, const qm31* r, int nx, const qm31* xs, qm31* out,
+                            const qm31* zt, const qm31& cpre);
+// Round j of a degree-1 trip from its 2^K sums S: p(0), p(1).
+void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out);
+int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
+                       const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
+                       RoundSink* sk, uint64_t b_rows = 0, int b_chunks = 0);
+// Wait for a trip's nq sums.
+int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out);
+
+int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out);
+
+// sum_i v[i] * eq[i] (v M31-valued, length n).
+int dot_m31(gkr_ctx* c, const uint32_t* v, const qm31* eq, uint64_t n, qm31* out);
+
+
+// ------------------------------------------------------------------ channel and proof records
+struct gkr_channel {
+  PoseidonChannel ch;
+};
+#define CH_CHECK(ch) \
+  if (!(ch)) return fail(GKR_ERR_INVALID, "null channel")
+
+struct LayerRec {
+  uint32_t tag;  // 0 MatMul, 2 Mul, 3 Activation, 7 MatMulDualSimd (rp: c0..c3 per round)
+  uint32_t n_block_vars = 0;  // MatMulDualSimd
+  qm31 claim_value = {0, 0, 0, 0};  // the output claim's value the layer was proved against
+  std::vector<qm31> rp;  // MatMul: c0,c1,c2 per round; Mul, Activation: eq c0..c3 per round
+  qm31 final_a, final_b;  // MatMul: final a/b evals; Mul: lhs/rhs evals
+  uint32_t act_type = 0;
+  qm31 input_eval, output_eval;
+  felt table_commitment;
+  qm31 claimed_sum, w_eval, in_eval, out_eval;
+  std::vector<uint32_t> mults;
+  std::vector<qm31> mult_rp;  // c0,c1 per round
+  qm31 mult_final, mult_sum;
+};
+// A MatMul layer's claim on its weight: MLE(B)(r_j || sumcheck challenges) =
+// final_b (push_matmul_weight_data, prover.rs:1465-1483).
+struct WeightClaimRec {
+  const gkr_matrix* b;
+  std::vector<qm31> point;
+  qm31 value;
+};
+struct gkr_proof {
+  std::vector<LayerRec> layers;
+  std::vector<qm31> in_point;
+  qm31 in_value = {0, 0, 0, 0};
+  std::vector<felt> weight_commitments;
+  std::vector<WeightClaimRec> weight_claims;      // recorded by the MatMul layers, in proving order
+  std::vector<std::vector<felt>> weight_openings;  // serialized opening records (claim + MleOpeningProof)
+  felt io_commitment = {{0, 0, 0, 0}};
+};
+
+// ------------------------------------------------------------------ provided by one unit to the others
+// The last rounds of each sumcheck run on the host once the vectors are this
+// short (the device trips stop there; k_handover folds the last trip's
+// vectors and hands them over).
+#ifndef GKR_HOST_TAIL_MM
+#define GKR_HOST_TAIL_MM 256   // product sumcheck: 5 QM31 products per pair
+#endif
+#ifndef GKR_HOST_TAIL_EQ3
+#define GKR_HOST_TAIL_EQ3 256  // eq-sumcheck: 11 products per pair
+#endif
+#ifndef GKR_HOST_TAIL_SUM
+#define GKR_HOST_TAIL_SUM 256  // multiplicity sumcheck: 1 product per pair
+#endif
+constexpr uint64_t kHostTailMM = GKR_HOST_TAIL_MM;
+constexpr uint64_t kHostTailEq3 = GKR_HOST_TAIL_EQ3;
+constexpr uint64_t kHostTailSum = GKR_HOST_TAIL_SUM;
+static_assert(kHostTailMM * 8 <= (uint64_t)kHandMax && kHostTailEq3 * 8 <= (uint64_t)kHandMax &&
+                  kHostTailSum * 8 <= (uint64_t)kHandMax,
+              "the last trip's vectors must fit k_handover");
+
+constexpr int kEqLoMax = 10;  // variables in the lower eq table of a trip
+struct Eq3Plan {
+  int nv = 0;
+  std::vector<Trip> trips;
+  std::vector<uint32_t> hi_off, lo_off;  // per trip, offsets into S_EQPARTS
+  std::vector<int> h;                    // per trip, variables in the lower table
+};
+
+// A new matrix handle (owned: freed with the handle).
+gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t cols, bool owned);
+// Degree-2 product sumcheck over 2^T entries (matmul.hip).
+int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, const qm31* in_b,
+                            qm31* const bufs_a[2], qm31* const bufs_b[2], const qm31* g0, int k0,
+                            gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b,
+                            const qm31* scale3 = nullptr);
+// Eq-weighted degree-3 sumcheck sum_x eq(z, x) w(x) d(x) (logup.hip): plan and eq tables,
+int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl);
+// one trip,
+int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, const qm31* d, int np,
+                           const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk);
+// the whole sumcheck.
+int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& pl, qm31* w0, qm31* d0,
+                        qm31* w1, qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3],
+                        const RoundSink* pre0 = nullptr);
+// Activation table outputs (host copy, cached per context).
+const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint32_t log_size);

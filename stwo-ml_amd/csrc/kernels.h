@@ -127,7 +127,7 @@ __device__ __forceinline__ void sink_finish(qm31 (&v)[NQ], const RoundSink& sk) 
 }
 
 template <int NQ>
-__global__ void __launch_bounds__(kBlock) k_finish(RoundSink sk, uint32_t nblocks) {
+static __global__ void __launch_bounds__(kBlock) k_finish(RoundSink sk, uint32_t nblocks) {
   qacc acc[NQ];
 #pragma unroll
   for (int q = 0; q < NQ; q++) acc[q].zero();
@@ -282,7 +282,7 @@ constexpr unsigned kTripFusedMax = 64;
 // sum, b[pos] = sum_c sb[c * b_rows + pos] for pos < b_rows and 0 above
 // (the zero padding to n); with db the sums are stored as f_b.
 template <int KIND, int K, bool SPLIT>
-__global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, const qm31* __restrict__ sb,
+static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, const qm31* __restrict__ sb,
                                                  uint64_t n, int np, TripChal al, qm31* __restrict__ da,
                                                  qm31* __restrict__ db, const qm31* __restrict__ eq_hi,
                                                  const qm31* __restrict__ eq_lo, int eq_h, RoundSink sk,
@@ -450,7 +450,7 @@ __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__ sa, co
 // (kFinishBlock / NQ)-th row, four independent loads in flight.
 constexpr int kFinishBlock = 1024;
 template <int NQ>
-__global__ void __launch_bounds__(kFinishBlock) k_finish_wide(RoundSink sk, uint32_t nblocks) {
+static __global__ void __launch_bounds__(kFinishBlock) k_finish_wide(RoundSink sk, uint32_t nblocks) {
   constexpr int RG = kFinishBlock / NQ;
   const int q = threadIdx.x % NQ, g = threadIdx.x / NQ;
   qacc acc;
@@ -501,7 +501,7 @@ struct Mailbox {
 };
 
 template <int NV>
-__global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a, const qm31* __restrict__ b,
+static __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a, const qm31* __restrict__ b,
                                                      uint32_t len, int k, Mailbox* mb, uint32_t want,
                                                      uint32_t spin_limit, qm31* vec_out, uint32_t* flag,
                                                      uint32_t seq) {
@@ -567,7 +567,7 @@ struct EqPartsArg {
   int m[kEqPartsMax];
   uint32_t off[kEqPartsMax];
 };
-__global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out) {
+static __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out) {
   __shared__ PointLds sp;
   stage_point(a.z, &sp);
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -582,7 +582,7 @@ __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out)
 // ------------------------------------------------------------------ eq / Lagrange
 // out[x] = prod_l (bit_l(x) ? r_l : 1 - r_l), with r_0 on the most
 // significant bit of x (components/matmul.rs:342-355, gkr/prover.rs:9201-9233).
-__global__ void k_eq_direct(PointArg pt, uint64_t count, qm31* __restrict__ out) {
+static __global__ void k_eq_direct(PointArg pt, uint64_t count, qm31* __restrict__ out) {
   __shared__ PointLds sp;
   stage_point(pt, &sp);
   uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -611,7 +611,7 @@ __device__ __forceinline__ void m31_digits(uint32_t x, int32_t (&d)[4]) {
 // column x, byte x % 4 of word q of entry c * nq + x / 4 holds digit q of
 // component c, so one word carries a digit of four consecutive columns (a
 // v_dot4 operand) and a wave reads 64 consecutive entries of a plane.
-__global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, qm31* __restrict__ out1,
+static __global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, qm31* __restrict__ out1,
                          qm31* __restrict__ out2, uint8_t* __restrict__ ldig) {
   __shared__ PointLds sp;
   stage_point(pt, &sp);
@@ -641,7 +641,7 @@ __global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, 
   }
 }
 // Split construction: hi table over variables [0, n-h), lo over [n-h, n).
-__global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __restrict__ lo) {
+static __global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __restrict__ lo) {
   __shared__ PointLds sp;
   stage_point(pt, &sp);
   const uint64_t n_hi = 1ull << (pt.n - h), n_lo = 1ull << h;
@@ -653,7 +653,7 @@ __global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __r
     st_q(lo, y, eq_prod(sp, pt.n - h, h, y));
   }
 }
-__global__ void k_eq_combine(const qm31* __restrict__ hi, const qm31* __restrict__ lo, int h, uint64_t count,
+static __global__ void k_eq_combine(const qm31* __restrict__ hi, const qm31* __restrict__ lo, int h, uint64_t count,
                              qm31* __restrict__ out) {
   uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (x >= count) return;
@@ -755,7 +755,7 @@ __device__ __forceinline__ void restrict_rows_block(const RowsJob& act, uint64_t
 }
 
 template <bool kVec4>
-__global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
+static __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
                                                           uint64_t chunk, const qm31* __restrict__ L,
                                                           uint32_t* __restrict__ partial, RowsJob act,
                                                           uint32_t act_blocks, uint32_t row_blocks) {
@@ -852,7 +852,7 @@ constexpr int kR8Rows = 4;       // rows a wave carries through one pass
 constexpr int kR8ChunkBlocks = 2;  // column chunk: 2 blocks (2048 columns), L digits 32 KB of LDS
 constexpr int kR8MaxPasses = 8;  // row passes per wave
 
-__global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
+static __global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
                                                     uint64_t stride, uint32_t* __restrict__ out,
                                                     uint32_t* __restrict__ bad) {
   const uint64_t wpr = stride / 4, words = k * wpr;
@@ -889,7 +889,7 @@ __global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __restrict__
 // per (row, component) recombine (sum_q 256^q acc_q, reduced once) and the
 // wave reduction of k_restrict_cols leaves one value per (row, component),
 // kept in LDS until the wave writes its partial rows at the end.
-__global__ void __launch_bounds__(kBlock) k_restrict_cols8(const int8_t* __restrict__ B8, uint64_t stride, uint64_t k,
+static __global__ void __launch_bounds__(kBlock) k_restrict_cols8(const int8_t* __restrict__ B8, uint64_t stride, uint64_t k,
                                                            const u32x4* __restrict__ ldig, uint64_t nq, int passes,
                                                            uint32_t* __restrict__ partial, RowsJob act,
                                                            uint32_t act_blocks, uint32_t row_blocks) {
@@ -1014,7 +1014,7 @@ struct SimdBlocks {
   qm31 w[kSimdMaxBlocks];
   int count;
 };
-__global__ void __launch_bounds__(kSimdWaves * 64) k_restrict_rows_simd(SimdBlocks blk, uint64_t m, uint64_t k,
+static __global__ void __launch_bounds__(kSimdWaves * 64) k_restrict_rows_simd(SimdBlocks blk, uint64_t m, uint64_t k,
                                                                          uint64_t pk, const qm31* __restrict__ L,
                                                                          qm31* __restrict__ out) {
   __shared__ qm31 part[kSimdWaves][64];
@@ -1068,7 +1068,7 @@ __global__ void __launch_bounds__(kSimdWaves * 64) k_restrict_rows_simd(SimdBloc
 // vectors, one workgroup per (b1, b2), and the combination out[k] =
 // sum_b lam_b src[b pk + k] of the blocks' vectors by the block challenges'
 // Lagrange weights.
-__global__ void __launch_bounds__(kBlock) k_block_gram(const qm31* __restrict__ fa, const qm31* __restrict__ fb,
+static __global__ void __launch_bounds__(kBlock) k_block_gram(const qm31* __restrict__ fa, const qm31* __restrict__ fb,
                                                        uint32_t nb, uint64_t pk, qm31* __restrict__ D) {
   const uint32_t b1 = blockIdx.x / nb, b2 = blockIdx.x % nb;
   qacc acc;
@@ -1086,7 +1086,7 @@ __global__ void __launch_bounds__(kBlock) k_block_gram(const qm31* __restrict__ 
 struct BlockPtrs {
   const uint32_t* p[kSimdMaxBlocks];
 };
-__global__ void __launch_bounds__(kBlock) k_restrict_rows_blocks(BlockPtrs a, uint64_t m, uint64_t k, uint64_t pk,
+static __global__ void __launch_bounds__(kBlock) k_restrict_rows_blocks(BlockPtrs a, uint64_t m, uint64_t k, uint64_t pk,
                                                                  const qm31* __restrict__ L, qm31* __restrict__ ea) {
   const uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const uint32_t b = blockIdx.y;
@@ -1116,7 +1116,7 @@ __global__ void __launch_bounds__(kBlock) k_restrict_rows_blocks(BlockPtrs a, ui
   for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
   st_q(out, x, qm31{r[0], r[1], r[2], r[3]});
 }
-__global__ void __launch_bounds__(kBlock) k_restrict_cols_blocks(BlockPtrs bm, uint64_t k, uint64_t n, uint64_t pk,
+static __global__ void __launch_bounds__(kBlock) k_restrict_cols_blocks(BlockPtrs bm, uint64_t k, uint64_t n, uint64_t pk,
                                                                  const qm31* __restrict__ L, qm31* __restrict__ eb) {
   const int lane = threadIdx.x & 63;
   const uint64_t x = (uint64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
@@ -1145,7 +1145,7 @@ __global__ void __launch_bounds__(kBlock) k_restrict_cols_blocks(BlockPtrs bm, u
 struct QWeights {
   qm31 w[kSimdMaxBlocks];
 };
-__global__ void __launch_bounds__(kBlock) k_combine_q(const qm31* __restrict__ src, QWeights lam, uint32_t nb,
+static __global__ void __launch_bounds__(kBlock) k_combine_q(const qm31* __restrict__ src, QWeights lam, uint32_t nb,
                                                       uint64_t pk, qm31* __restrict__ out) {
   // one wave per entry k, lane b multiplies block b's entry (nb <= 64), then a wave sum
   const int lane = threadIdx.x & 63;
@@ -1157,7 +1157,7 @@ __global__ void __launch_bounds__(kBlock) k_combine_q(const qm31* __restrict__ s
 }
 
 // f_b[i] = sum over column chunks of partial[chunk * k + i] for i < k; 0 for k <= i < pk.
-__global__ void k_restrict_cols_finish(const qm31* __restrict__ partial, uint64_t k, uint64_t pk, int nchunks,
+static __global__ void k_restrict_cols_finish(const qm31* __restrict__ partial, uint64_t k, uint64_t pk, int nchunks,
                                        qm31* __restrict__ out) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= pk) return;
@@ -1170,11 +1170,11 @@ __global__ void k_restrict_cols_finish(const qm31* __restrict__ partial, uint64_
   for (int c = 0; c < nchunks; c++) acc.add(ld_q(partial, (uint64_t)c * k + i));
   st_q(out, i, acc.reduce());
 }
-__global__ void k_zero_u32(uint32_t* __restrict__ out, uint32_t n) {
+static __global__ void k_zero_u32(uint32_t* __restrict__ out, uint32_t n) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) out[i] = 0u;
 }
-__global__ void k_zero_q(qm31* __restrict__ out, uint64_t from, uint64_t to) {
+static __global__ void k_zero_q(qm31* __restrict__ out, uint64_t from, uint64_t to) {
   uint64_t i = from + (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < to) st_q(out, i, qm31_zero());
 }
@@ -1210,7 +1210,7 @@ struct dot_acc {
 // multiplicities (gkr/prover.rs:6411-6475).  Per workgroup it accumulates
 // sum(w) and the MLE of the padded input at the claim point,
 // sum_p x_p * eq[p] (prover.rs:6411-6417), into a 2-value sink.
-__global__ void __launch_bounds__(kBlock) k_logup_prepare(
+static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
     const uint32_t* __restrict__ table_out, uint32_t mask, qm31 gamma, qm31 beta, const qm31* __restrict__ eq,
     uint32_t* __restrict__ masked_in, uint32_t* __restrict__ masked_out, qm31* __restrict__ d_out,
@@ -1241,7 +1241,7 @@ __global__ void __launch_bounds__(kBlock) k_logup_prepare(
   sink_finish<2>(v, sink);
 }
 // Table side: sum_j mult_j / (gamma - j - beta*f(j)) over entries with mult_j > 0.
-__global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __restrict__ table_out,
+static __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __restrict__ table_out,
                                                             const uint32_t* __restrict__ mult, uint64_t size,
                                                             qm31 gamma, qm31 beta, RoundSink sink) {
   qacc acc;
@@ -1260,21 +1260,21 @@ __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __re
 
 // pad_matrix_pow2 + matrix_to_mle (components/matmul.rs:649-664, 174-187):
 // out[p] = X[r][c] lifted to QM31 for p = r * pcol + c inside the matrix, 0 outside.
-__global__ void k_pad_q(const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
+static __global__ void k_pad_q(const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
                         qm31* __restrict__ out) {
   const uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= n) return;
   const uint64_t r = p >> log_pcol, c = p & ((1ull << log_pcol) - 1);
   st_q(out, p, qm31_from_m31((r < rows && c < cols) ? m31_from_u32(X[r * cols + c]) : 0u));
 }
-__global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __restrict__ out) {
+static __global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __restrict__ out) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) st_q(out, i, qm31_from_m31(m31_from_u32(in[i])));
 }
 
 // ------------------------------------------------------------------ MLE evaluation helpers
 // Partial dot products sum_i v[i] * eq[i] for an M31-valued v.
-__global__ void __launch_bounds__(kBlock) k_dot_m31(const uint32_t* __restrict__ v, const qm31* __restrict__ eq,
+static __global__ void __launch_bounds__(kBlock) k_dot_m31(const uint32_t* __restrict__ v, const qm31* __restrict__ eq,
                                                     uint64_t n, RoundSink sink) {
   dot_acc acc;
   acc.zero();
@@ -1286,7 +1286,7 @@ __global__ void __launch_bounds__(kBlock) k_dot_m31(const uint32_t* __restrict__
 }
 // Two M31 vectors against one eq table in one pass (the masked input and
 // output MLEs at the eq-sumcheck challenges, prover.rs:6558-6579).
-__global__ void __launch_bounds__(kBlock) k_dot2_m31(const uint32_t* __restrict__ v0, const uint32_t* __restrict__ v1,
+static __global__ void __launch_bounds__(kBlock) k_dot2_m31(const uint32_t* __restrict__ v0, const uint32_t* __restrict__ v1,
                                                      const qm31* __restrict__ eq, uint64_t n, RoundSink sink) {
   dot_acc a0, a1;
   a0.zero();
@@ -1301,7 +1301,7 @@ __global__ void __launch_bounds__(kBlock) k_dot2_m31(const uint32_t* __restrict_
   sink_finish<2>(q, sink);
 }
 // Partial dot products sum_i v[i] * eq[i] for a QM31-valued v.
-__global__ void __launch_bounds__(kBlock) k_dot_q(const qm31* __restrict__ v, const qm31* __restrict__ eq,
+static __global__ void __launch_bounds__(kBlock) k_dot_q(const qm31* __restrict__ v, const qm31* __restrict__ eq,
                                                   uint64_t n, RoundSink sink) {
   qacc acc;
   acc.zero();
@@ -1312,7 +1312,7 @@ __global__ void __launch_bounds__(kBlock) k_dot_q(const qm31* __restrict__ v, co
   sink_finish<1>(q, sink);
 }
 // restrict_mle: fix the first s variables: out[y] = sum_x eq[x] * mle[x * rest + y].
-__global__ void k_restrict_q(const qm31* __restrict__ mle, const qm31* __restrict__ eq, uint64_t nx,
+static __global__ void k_restrict_q(const qm31* __restrict__ mle, const qm31* __restrict__ eq, uint64_t nx,
                              uint64_t rest, qm31* __restrict__ out) {
   uint64_t y = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (y >= rest) return;
@@ -1325,11 +1325,11 @@ __global__ void k_restrict_q(const qm31* __restrict__ mle, const qm31* __restric
 // ------------------------------------------------------------------ bandwidth reference
 // Plain 128-bit streaming copy and read, used to measure the achievable HBM
 // bandwidth and to calibrate counter-derived traffic.
-__global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, uint64_t n) {
+static __global__ void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, uint64_t n) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
-__global__ void k_read16(const uint4* __restrict__ src, uint64_t n, uint32_t* __restrict__ sink) {
+static __global__ void k_read16(const uint4* __restrict__ src, uint64_t n, uint32_t* __restrict__ sink) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   uint32_t acc = 0;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
@@ -1369,13 +1369,13 @@ GKR_HD uint32_t synth_value(int kind, uint64_t seed, uint64_t i) {
   const int s = (int)((z >> 32) % 255ull) - 127;
   return s < 0 ? (uint32_t)((int64_t)P + s) : (uint32_t)s;
 }
-__global__ void k_fill_synth(uint32_t* __restrict__ out, uint64_t n, int kind, uint64_t seed) {
+static __global__ void k_fill_synth(uint32_t* __restrict__ out, uint64_t n, int kind, uint64_t seed) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     out[i] = synth_value(kind, seed, i);
 }
 // Row-major QM31 table: four consecutive draws per element.
-__global__ void k_fill_synth_q(qm31* __restrict__ out, uint64_t n, uint64_t seed) {
+static __global__ void k_fill_synth_q(qm31* __restrict__ out, uint64_t n, uint64_t seed) {
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
     st_q(out, i, qm31{synth_value(0, seed, 4 * i), synth_value(0, seed, 4 * i + 1),

@@ -1,0 +1,433 @@
+// LogUp activation layer (reduce_activation_layer, gkr/prover.rs:6400-6600):
+// tables, the eq-weighted degree-3 sumcheck and the multiplicity sumcheck.
+#include "internal.h"
+#include "activations.h"
+// ------------------------------------------------------------------ LogUp activation layer
+extern "C" int gkr_activation_table(uint32_t tag, uint32_t log_size, uint32_t* out) {
+  if (!out || !act_valid(tag) || log_size == 0 || log_size > 24) return fail(GKR_ERR_INVALID, "bad argument");
+  std::vector<uint32_t> t = act_table(tag, log_size);
+  memcpy(out, t.data(), t.size() * sizeof(uint32_t));
+  return GKR_OK;
+}
+
+const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint32_t log_size) {
+  const uint64_t key = ((uint64_t)tag << 32) | log_size;
+  auto it = c->tables.find(key);
+  if (it == c->tables.end()) it = c->tables.emplace(key, act_table(tag, log_size)).first;
+  return it->second;
+}
+
+// Eq-weighted degree-3 sumcheck over n = 2^nv entries (the eq-sumcheck of
+// reduce_activation_layer, gkr/prover.rs:6501-6556, and of reduce_mul_layer,
+// 6197-6245): s_t = sum_x eq_t * w_t * d_t at t = 0..3, Newton differences to
+// (c0, c1, c2, c3), mix_poly_coeffs_deg3, draw, fold.
+//
+// eq(z, x) = prod_l eqlin(z_l, x_l) is kept factored: only w and d are stored
+// and folded.  Round t's polynomial is eqlin(z_t, X) times the product of
+// eqlin(z_l, r_l) over the earlier rounds times sum_x eq(z_{>t}, x) w d; the
+// trips weight their cross sums by the eq part below their variables (two
+// small tables per trip, built at the start), and the host finish rebuilds
+// the eq vector of the remaining variables.  The polynomials, challenges and
+// final values equal those of folding eq like w and d (the polynomial of each
+// round is unique).
+// Plan the trips of an eq-sumcheck over 2^nv entries for claim point z and
+// launch the kernel that builds their eq tables (S_EQPARTS).
+int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
+  pl->nv = nv;
+  pl->trips = plan_trips(nv, kHostTailEq3, trip_k(1ull << nv));
+  pl->hi_off.clear();
+  pl->lo_off.clear();
+  pl->h.clear();
+  if (pl->trips.empty()) return GKR_OK;
+  EqPartsArg arg;
+  memset(&arg, 0, sizeof arg);
+  arg.z = make_point(z, nv);
+  uint32_t total = 0;
+  auto table = [&](int s0, int m) -> uint32_t {
+    for (int i = 0; i < arg.count; i++)
+      if (arg.s[i] == s0 && arg.m[i] == m) return arg.off[i];
+    const int i = arg.count++;
+    arg.s[i] = s0;
+    arg.m[i] = m;
+    arg.off[i] = total;
+    total += 1u << m;
+    return arg.off[i];
+  };
+  for (const Trip& tr : pl->trips) {
+    if (arg.count + 2 > kEqPartsMax) return fail(GKR_ERR_DEVICE, "too many eq tables");
+    const int m = nv - tr.t - tr.K;  // coordinates below the trip's variables
+    const int h = m < kEqLoMax ? m : kEqLoMax;
+    pl->hi_off.push_back(table(tr.t + tr.K, m - h));
+    pl->lo_off.push_back(table(nv - h, h));
+    pl->h.push_back(h);
+  }
+  HostTimer ht(c, K_HOST_LAUNCH);
+  qm31* parts;
+  TRY(ensureT(c, S_EQPARTS, total, &parts));
+  {
+    TimedLaunch tl(c, K_EQ_TABLE, 16ull * total);
+    hipLaunchKernelGGL(k_eq_parts, dim3(grid_for(total)), dim3(kBlock), 0, c->stream, arg, total, parts);
+  }
+  return check_launch();
+}
+// Launch trip j of the plan over sources w, d (np pending challenges pend),
+// folded vectors to dw, dd when given.
+int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, const qm31* d, int np,
+                           const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk) {
+  qm31* parts = (qm31*)c->buf[S_EQPARTS];
+  const Trip& tr = pl.trips[j];
+  return launch_trip(c, 1, tr.K, w, d, tr.n, np, pend, dw, dd, parts + pl.hi_off[j], parts + pl.lo_off[j], pl.h[j],
+                     slot, sk);
+}
+// The sumcheck for claim point z over w0, d0 (overwritten: the trips' folded
+// vectors go to w1/d1 (n/2 entries) and w0/d0 alternately).  pre0: trip 0
+// already launched (eq3_launch_trip, any slot).  Writes 4 * nv round
+// coefficients, nv challenges and the final (eq, w, d) values.
+int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& pl, qm31* w0, qm31* d0,
+                        qm31* w1, qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3],
+                        const RoundSink* pre0) {
+  const int nv = pl.nv;
+  if (nv == 0) {
+    fin[0] = qm31_one();
+    TRY(fetch_q(c, w0, 1, fin + 1));
+    return fetch_q(c, d0, 1, fin + 2);
+  }
+  const qm31 inv2 = qm31_from_m31(1u << 30);
+  const qm31 inv6 = qm31_from_m31(m31_inv(6));
+  const qm31 two = qm31_from_m31(2), three = qm31_from_m31(3);
+  auto absorb3 = [&](int t, const qm31* s) {
+    const qm31 dd1 = qm31_sub(s[1], s[0]);
+    const qm31 dd2 = qm31_mul(qm31_add(qm31_sub(qm31_sub(s[2], s[1]), s[1]), s[0]), inv2);
+    const qm31 dd3 = qm31_mul(qm31_sub(qm31_sub(s[3], s[0]), qm31_mul(three, qm31_sub(s[2], s[1]))), inv6);
+    const qm31 c0 = s[0];
+    const qm31 c1 = qm31_add(qm31_sub(dd1, dd2), qm31_mul(two, dd3));
+    const qm31 c2 = qm31_sub(dd2, qm31_mul(three, dd3));
+    const qm31 c3 = dd3;
+    rp_out[4 * t + 0] = G(c0);
+    rp_out[4 * t + 1] = G(c1);
+    rp_out[4 * t + 2] = G(c2);
+    rp_out[4 * t + 3] = G(c3);
+    HostTimer ht(c, K_HOST_FS);
+    C.mix_poly_coeffs_deg3(c0, c1, c2, c3);
+    chal[t] = C.draw_qm31();
+  };
+  const qm31 xs[4] = {qm31_zero(), qm31_one(), two, three};
+  qm31* bw[2] = {w1, w0};
+  qm31* bd[2] = {d1, d0};
+  HandoverSession ho(c);
+  const qm31* sw = w0;
+  const qm31* sd = d0;
+  int np = 0;
+  const qm31* pend = nullptr;
+  qm31 cpre = qm31_one();  // prod of eqlin(z_l, r_l) over the rounds done
+  for (size_t j = 0; j < pl.trips.size(); j++) {
+    const Trip& tr = pl.trips[j];
+    const bool last = j + 1 == pl.trips.size();
+    qm31 g[kMaxSums];
+    RoundSink sk;
+    if (j == 0 && pre0) {
+      sk = *pre0;
+    } else {
+      qm31* dw = j == 0 ? nullptr : bw[(j - 1) & 1];
+      qm31* dd = j == 0 ? nullptr : bd[(j - 1) & 1];
+      TRY(eq3_launch_trip(c, pl, j, sw, sd, np, pend, dw, dd, 0, &sk));
+      if (j > 0) {
+        sw = dw;
+        sd = dd;
+      }
+    }
+    if (last) TRY(ho.launch<2>(sw, sd, tr.n, tr.K));
+    TRY(wait_trip(c, sk, trip_nq(1, tr.K), g));
+    for (int i = 0; i < tr.K; i++) {
+      qm31 sums[4];
+      trip_round_gram(g, tr.K, i, chal + tr.t, 4, xs, sums, z + tr.t, cpre);
+      absorb3(tr.t + i, sums);
+    }
+    for (int i = 0; i < tr.K; i++) cpre = qm31_mul(cpre, eqlin(z[tr.t + i], chal[tr.t + i]));
+    np = tr.K;
+    pend = chal + tr.t;
+  }
+  const int t_end = pl.trips.back().t + pl.trips.back().K;
+  const uint64_t hlen = 1ull << (nv - t_end);
+  std::vector<qm31> v[2];
+  TRY(ho.post(pend, np));
+  TRY(ho.fetch(hlen, 2, v));
+  std::vector<qm31>& W = v[0];
+  std::vector<qm31>& D = v[1];
+  // eq of the remaining coordinates, scaled by the factors already fixed
+  std::vector<qm31> E(1, cpre);
+  for (int l = t_end; l < nv; l++) {
+    std::vector<qm31> nE(2 * E.size());
+    for (size_t x = 0; x < E.size(); x++) {
+      nE[2 * x + 1] = qm31_mul(E[x], z[l]);
+      nE[2 * x] = qm31_sub(E[x], nE[2 * x + 1]);
+    }
+    E.swap(nE);
+  }
+  for (int t = t_end; t < nv; t++) {
+    const size_t half = E.size() / 2;
+    qm31 sums[4] = {qm31_zero(), qm31_zero(), qm31_zero(), qm31_zero()};
+    {
+      HostTimer ht(c, K_HOST_FINISH);
+      for (size_t i = 0; i < half; i++) {
+        const qm31 e0 = E[i], e1 = E[i + half], w0v = W[i], w1v = W[i + half], d0v = D[i], d1v = D[i + half];
+        sums[0] = qm31_add(sums[0], qm31_mul(qm31_mul(e0, w0v), d0v));
+        sums[1] = qm31_add(sums[1], qm31_mul(qm31_mul(e1, w1v), d1v));
+        const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1v, w0v), dd = qm31_sub(d1v, d0v);
+        const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1v, dw), d2 = qm31_add(d1v, dd);
+        sums[2] = qm31_add(sums[2], qm31_mul(qm31_mul(e2, w2), d2));
+        sums[3] = qm31_add(sums[3], qm31_mul(qm31_mul(qm31_add(e2, de), qm31_add(w2, dw)), qm31_add(d2, dd)));
+      }
+    }
+    absorb3(t, sums);
+    HostTimer ht(c, K_HOST_FINISH);
+    for (size_t i = 0; i < half; i++) {
+      E[i] = qm31_fold(E[i], E[i + half], chal[t]);
+      W[i] = qm31_fold(W[i], W[i + half], chal[t]);
+      D[i] = qm31_fold(D[i], D[i + half], chal[t]);
+    }
+    E.resize(half);
+    W.resize(half);
+    D.resize(half);
+  }
+  fin[0] = E[0];
+  fin[1] = W[0];
+  fin[2] = D[0];
+  return GKR_OK;
+}
+
+extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
+                                          const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t tag,
+                                          uint32_t table_log, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out) {
+  CH_CHECK(ch);
+  if (!c || !input || !claim_value || !out || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
+  if (!act_valid(tag)) return fail(GKR_ERR_INVALID, "unknown activation type %u", tag);
+  if (!act_logup_valid(tag))
+    return fail(GKR_ERR_INVALID, "activation type %u (ReLU) is proved algebraically, not by LogUp", tag);
+  if (table_log == 0) table_log = act_default_log_size(tag);
+  if (table_log > 24) return fail(GKR_ERR_INVALID, "table_log_size %u too large", table_log);
+  if (input->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another context");
+  const uint64_t prow = next_pow2(input->rows), pcol = next_pow2(input->cols);
+  const uint64_t n = prow * pcol;
+  const int nv = log2_exact(n);
+  if ((int)n_point != nv)
+    return fail(GKR_ERR_INVALID, "claim point has %u vars, activation MLE has %d", n_point, nv);
+  if (nv > kMaxVars) return fail(GKR_ERR_INVALID, "activation too large");
+  if (!out->eq_round_polys && nv > 0) return fail(GKR_ERR_INVALID, "null eq_round_polys");
+  if (!out->multiplicities || !out->mult_round_polys) return fail(GKR_ERR_INVALID, "null output arrays");
+  if (!canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
+  std::vector<qm31> cpt(n_point);
+  for (uint32_t l = 0; l < n_point; l++) {
+    if (!canonical_q(claim_point[l])) return fail(GKR_ERR_INVALID, "claim point not canonical");
+    cpt[l] = Q(claim_point[l]);
+  }
+  HIP_TRY(hipSetDevice(c->device));
+  c->mm.valid = false;
+  PoseidonChannel& C = ch->ch;
+  const uint64_t tsize = 1ull << table_log;
+  const uint32_t mask = (uint32_t)(tsize - 1);
+  const std::vector<uint32_t>& table = cached_table(c, tag, table_log);
+
+  uint32_t *d_table, *d_mult, *d_min, *d_mout;
+  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *m0, *m1;
+  TRY(ensureT(c, S_TABLE, tsize, &d_table));
+  TRY(ensureT(c, S_MULT, tsize, &d_mult));
+  TRY(ensureT(c, S_MIN, n, &d_min));
+  TRY(ensureT(c, S_MOUT, n, &d_mout));
+  TRY(ensureT(c, S_D0, n, &d_d0));
+  TRY(ensureT(c, S_D1, n / 2 + 1, &d_d1));
+  TRY(ensureT(c, S_W0, n, &d_w0));
+  TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
+  TRY(ensureT(c, S_E0, n, &d_e0));
+  TRY(ensureT(c, S_M0, tsize, &m0));
+  TRY(ensureT(c, S_M1, tsize / 2 + 1, &m1));
+  TRY(ensure_host_mult(c, tsize));
+  const uint64_t table_key = ((uint64_t)tag << 32) | table_log;
+  if (c->table_on_device != table_key) {
+    c->table_on_device = 0;
+    HIP_TRY(hipMemcpyAsync(d_table, table.data(), tsize * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
+    c->table_on_device = table_key;
+  }
+  HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
+  // eq(claim point, x): the input MLE at the claim point (accumulated by the
+  // prepare pass) and the eq vector of the eq-sumcheck
+  TRY(eq_table(c, cpt.data(), nv, n, d_e0));
+
+  // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
+  C.mix_u64(0x4C4F47ull);
+  C.mix_u64(tag);
+  qm31 gb[2];
+  C.draw_qm31s(gb, 2);
+  const qm31 gamma = gb[0], beta = gb[1];
+  out->gamma = G(gamma);
+  out->beta = G(beta);
+
+  // Launched back to back, read when needed (each result in its own slot):
+  //   prepare -> (trace sum, input MLE at the claim point)      kSlotPrep
+  //   table-side sum over the multiplicities                     kSlotTable
+  //   multiplicities -> pinned host copy
+  //   multiplicity sumcheck trip 0 (no challenge needed)         kSlotMult0
+  //   eq tables of the eq-sumcheck trips, eq-sumcheck trip 0     kSlotEq0
+  RoundSink sk_prep, sk_table, sk_mult0, sk_eq0;
+  {
+    HostTimer ht(c, K_HOST_LAUNCH);
+    TRY(make_sink(c, &sk_prep, kSlotPrep));
+    {
+      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 16 * n + 8 * n + 32 * n);
+      hipLaunchKernelGGL(k_logup_prepare, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, input->dev,
+                         input->rows, input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, d_e0, d_min,
+                         d_mout, d_d0, d_w0, d_mult, sk_prep);
+    }
+    TRY(launch_finish<2>(c, sk_prep, partial_grid(n)));
+    TRY(make_sink(c, &sk_table, kSlotTable));
+    hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult,
+                       tsize, gamma, beta, sk_table);
+    TRY(launch_finish<1>(c, sk_table, partial_grid(tsize)));
+    HIP_TRY(hipMemcpyAsync(c->h_mult, d_mult, tsize * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+    hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0);
+    TRY(check_launch());
+  }
+  const std::vector<Trip> mtrips = plan_trips((int)table_log, kHostTailSum, kTripMaxK);
+  TRY(launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
+                  kSlotMult0, &sk_mult0));
+  Eq3Plan epl;
+  TRY(eq3_prepare(c, cpt.data(), nv, &epl));
+  const bool eq_pre = nv > 0;
+  if (eq_pre) TRY(eq3_launch_trip(c, epl, 0, d_w0, d_d0, 0, nullptr, nullptr, nullptr, kSlotEq0, &sk_eq0));
+
+  qm31 prep[2], tsum[1];
+  TRY(wait_sink<1>(c, sk_table, tsum));  // implies the prepare results (earlier on the stream)
+  for (int q = 0; q < 2; q++) prep[q] = c->h_out[kSlotPrep + q];
+  const qm31 trace_sum = prep[0], input_eval = prep[1], table_sum = tsum[0];
+  if (!qm31_eq(trace_sum, table_sum))
+    return fail(GKR_ERR_LOGUP, "Activation LogUp sum mismatch: trace=(%u,%u,%u,%u) table=(%u,%u,%u,%u)", trace_sum.a,
+                trace_sum.b, trace_sum.c, trace_sum.d, table_sum.a, table_sum.b, table_sum.c, table_sum.d);
+  C.mix_secure_field(trace_sum);
+  out->claimed_sum = G(trace_sum);
+
+  // eq-sumcheck: sum eq(r, x) w(x) d(x) = 1 over the hypercube
+  std::vector<qm31> chal(nv);
+  qm31 fin[3];
+  TRY(eq3_sumcheck(c, C, cpt.data(), epl, d_w0, d_d0, d_w1, d_d1, out->eq_round_polys, chal.data(), fin,
+                   eq_pre ? &sk_eq0 : nullptr));
+  const qm31 w_eval = fin[1];
+  // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass
+  qm31 io[2];
+  TRY(eq_table(c, chal.data(), nv, n, d_e0));
+  {
+    RoundSink sk;
+    TRY(make_sink(c, &sk));
+    hipLaunchKernelGGL(k_dot2_m31, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, d_min, d_mout, d_e0, n, sk);
+    TRY(launch_finish<2>(c, sk, partial_grid(n)));
+    TRY(wait_sink<2>(c, sk, io));
+  }
+  const qm31 in_eval = io[0], out_eval = io[1];
+  out->w_eval = G(w_eval);
+  out->in_eval = G(in_eval);
+  out->out_eval = G(out_eval);
+
+  // Multiplicity sumcheck (prover.rs:9449-9511): degree-1 rounds over
+  // 2^table_log entries.  The multiplicities reached the pinned copy before
+  // the kernels whose results were waited for above; they count every padded
+  // input once, so their sum is n.
+  memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
+  const qm31 mult_sum = qm31_from_m31(m31_reduce64(n));
+  qm31* bm[2] = {m1, m0};
+  qm31 alpha = qm31_zero();
+  auto absorb1 = [&](uint32_t t, const qm31* s) {
+    const qm31 c0 = s[0];
+    const qm31 c1 = qm31_sub(s[1], s[0]);
+    out->mult_round_polys[2 * t] = G(c0);
+    out->mult_round_polys[2 * t + 1] = G(c1);
+    HostTimer ht(c, K_HOST_FS);
+    C.mix_secure_field(c0);
+    C.mix_secure_field(c1);
+    alpha = C.draw_qm31();
+  };
+  qm31 mfin[1];
+  {
+    // trips of up to 3 rounds (the first launched ahead above), then the host
+    HandoverSession ho(c);
+    const qm31* src = m0;
+    int np = 0;
+    const qm31* pend = nullptr;
+    std::vector<qm31> mchal(table_log);
+    for (size_t j = 0; j < mtrips.size(); j++) {
+      const Trip& tr = mtrips[j];
+      const bool last = j + 1 == mtrips.size();
+      RoundSink sk;
+      if (j == 0) {
+        sk = sk_mult0;
+      } else {
+        qm31* dst = bm[(j - 1) & 1];
+        TRY(launch_trip(c, 2, tr.K, src, nullptr, tr.n, np, pend, dst, nullptr, nullptr, nullptr, 0, 0, &sk));
+        src = dst;
+      }
+      if (last) TRY(ho.launch<1>(src, nullptr, tr.n, tr.K));
+      qm31 g[kMaxSums];
+      TRY(wait_trip(c, sk, trip_nq(2, tr.K), g));
+      for (int i = 0; i < tr.K; i++) {
+        qm31 sums[2];
+        trip_round_sum(g, tr.K, i, mchal.data() + tr.t, sums);
+        absorb1((uint32_t)(tr.t + i), sums);
+        mchal[tr.t + i] = alpha;
+      }
+      np = tr.K;
+      pend = mchal.data() + tr.t;
+    }
+    const int t_end = mtrips.back().t + mtrips.back().K;
+    std::vector<qm31> v[1];
+    TRY(ho.post(pend, np));
+    TRY(ho.fetch(tsize >> t_end, 1, v));
+    std::vector<qm31>& V = v[0];
+    for (int t = t_end; t < (int)table_log; t++) {
+      const size_t half = V.size() / 2;
+      qm31 sums[2] = {qm31_zero(), qm31_zero()};
+      {
+        HostTimer ht(c, K_HOST_FINISH);
+        for (size_t i = 0; i < half; i++) {
+          sums[0] = qm31_add(sums[0], V[i]);
+          sums[1] = qm31_add(sums[1], V[i + half]);
+        }
+      }
+      absorb1((uint32_t)t, sums);
+      HostTimer ht(c, K_HOST_FINISH);
+      for (size_t i = 0; i < half; i++) V[i] = qm31_fold(V[i], V[i + half], alpha);
+      V.resize(half);
+    }
+    mfin[0] = V[0];
+  }
+  out->mult_final_eval = G(mfin[0]);
+  out->mult_claimed_sum = G(mult_sum);
+
+  // Table commitment = poseidon_hash_many([type_tag, log_size]) (prover.rs:8365-8373)
+  felt tc_in[2] = {felt_from_u64(tag), felt_from_u64(table_log)};
+  const felt tc = poseidon_hash_many(tc_in, 2);
+  out->table_commitment = felt_to_abi(tc);
+  C.mix_secure_field(input_eval);
+  C.mix_secure_field(Q(*claim_value));
+  out->input_eval = G(input_eval);
+  out->output_eval = *claim_value;
+
+  if (proof) {
+    LayerRec L;
+    L.tag = 3;
+    L.act_type = tag;
+    for (int t = 0; t < 4 * nv; t++) L.rp.push_back(Q(out->eq_round_polys[t]));
+    L.input_eval = input_eval;
+    L.output_eval = Q(*claim_value);
+    L.claim_value = Q(*claim_value);
+    L.table_commitment = felt_from_mont(tc);
+    L.claimed_sum = trace_sum;
+    L.w_eval = w_eval;
+    L.in_eval = in_eval;
+    L.out_eval = out_eval;
+    L.mults.assign(out->multiplicities, out->multiplicities + tsize);
+    for (uint32_t t = 0; t < 2 * table_log; t++) L.mult_rp.push_back(Q(out->mult_round_polys[t]));
+    L.mult_final = mfin[0];
+    L.mult_sum = mult_sum;
+    proof->layers.push_back(L);
+  }
+  return GKR_OK;
+}
+

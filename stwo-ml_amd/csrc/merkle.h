@@ -134,7 +134,7 @@ __device__ __forceinline__ void merkle_child(const MerkleStep& T, uint32_t s, ui
 constexpr int kMerkleBlock = 256;
 constexpr int kMerkleMaxD = 4;
 
-__global__ void __launch_bounds__(kMerkleBlock) k_merkle_level(const MerkleStep* __restrict__ steps, int n_steps,
+static __global__ void __launch_bounds__(kMerkleBlock) k_merkle_level(const MerkleStep* __restrict__ steps, int n_steps,
                                                                uint32_t s, uint64_t total,
                                                                const MerkleConsts* __restrict__ Cp) {
   __shared__ f9::fe stack[kMerkleMaxD][kMerkleBlock];
@@ -185,7 +185,7 @@ struct MerkleGather {
   uint64_t index;
 };
 
-__global__ void k_merkle_gather(const MerkleKept* __restrict__ trees, const MerkleGather* __restrict__ items, int n,
+static __global__ void k_merkle_gather(const MerkleKept* __restrict__ trees, const MerkleGather* __restrict__ items, int n,
                                 const MerkleConsts* __restrict__ Cp, uint32_t* __restrict__ out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -227,7 +227,7 @@ __global__ void k_merkle_gather(const MerkleKept* __restrict__ trees, const Merk
 // Folds of a weight opening, f'[x] = f[x] + r (f[x + mid] - f[x]) on the top
 // variable.  The first fold reads the column-major padded MLE of B (B[i][j] at
 // j * pk + i, zero outside B) straight from the row-major matrix.
-__global__ void k_open_fold_matrix(const uint32_t* __restrict__ B, uint64_t rows, uint64_t cols, uint32_t log_pk,
+static __global__ void k_open_fold_matrix(const uint32_t* __restrict__ B, uint64_t rows, uint64_t cols, uint32_t log_pk,
                                    uint64_t mid, qm31 r, qm31* __restrict__ out) {
   const uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (x >= mid) return;
@@ -237,14 +237,14 @@ __global__ void k_open_fold_matrix(const uint32_t* __restrict__ B, uint64_t rows
   };
   out[x] = qm31_fold(qm31_from_m31(at(x)), qm31_from_m31(at(x + mid)), r);
 }
-__global__ void k_open_fold(const qm31* __restrict__ in, uint64_t mid, qm31 r, qm31* __restrict__ out) {
+static __global__ void k_open_fold(const qm31* __restrict__ in, uint64_t mid, qm31 r, qm31* __restrict__ out) {
   const uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (x >= mid) return;
   out[x] = qm31_fold(in[x], in[x + mid], r);
 }
 
 // Montgomery roots -> canonical 8-word felts.
-__global__ void k_merkle_roots(const f9::fe* const* __restrict__ roots, int n, const MerkleConsts* __restrict__ Cp,
+static __global__ void k_merkle_roots(const f9::fe* const* __restrict__ roots, int n, const MerkleConsts* __restrict__ Cp,
                                uint32_t* __restrict__ out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;

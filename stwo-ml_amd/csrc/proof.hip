@@ -1,0 +1,149 @@
+// Proof container and serialize_gkr_model_proof (engine/src/cairo_serde.rs).
+#include "internal.h"
+// ------------------------------------------------------------------ proof container
+extern "C" int gkr_proof_new(gkr_proof** out) {
+  if (!out) return fail(GKR_ERR_INVALID, "null out");
+  *out = new gkr_proof();
+  return GKR_OK;
+}
+extern "C" void gkr_proof_free(gkr_proof* p) { delete p; }
+extern "C" size_t gkr_proof_num_layers(const gkr_proof* p) { return p ? p->layers.size() : 0; }
+extern "C" int gkr_proof_layer_claim_value(const gkr_proof* p, size_t layer, gkr_qm31* value) {
+  if (!p || !value) return fail(GKR_ERR_INVALID, "null argument");
+  if (layer >= p->layers.size()) return fail(GKR_ERR_INVALID, "layer %zu of %zu", layer, p->layers.size());
+  *value = G(p->layers[layer].claim_value);
+  return GKR_OK;
+}
+extern "C" int gkr_proof_set_input_claim(gkr_proof* p, const gkr_qm31* point, uint32_t n, const gkr_qm31* value) {
+  if (!p || !value || (!point && n)) return fail(GKR_ERR_INVALID, "null argument");
+  p->in_point.clear();
+  for (uint32_t i = 0; i < n; i++) p->in_point.push_back(Q(point[i]));
+  p->in_value = Q(*value);
+  return GKR_OK;
+}
+extern "C" int gkr_proof_add_weight_commitment(gkr_proof* p, const gkr_felt* cm) {
+  if (!p || !cm || !felt_abi_canonical(*cm)) return fail(GKR_ERR_INVALID, "bad argument");
+  p->weight_commitments.push_back(felt_canon_from_words(cm->w));
+  return GKR_OK;
+}
+extern "C" int gkr_proof_set_io_commitment(gkr_proof* p, const gkr_felt* cm) {
+  if (!p || !cm || !felt_abi_canonical(*cm)) return fail(GKR_ERR_INVALID, "bad argument");
+  p->io_commitment = felt_canon_from_words(cm->w);
+  return GKR_OK;
+}
+
+// serialize_gkr_model_proof (cairo_serde.rs:1307-1772); felts kept canonical.
+// Two passes over the proof: the first counts, the second writes straight
+// into the caller's buffer (no intermediate copy of the felt stream).
+struct Ser {
+  gkr_felt* out;  // nullptr: count only
+  size_t n = 0;
+  void u(uint64_t v) {
+    if (out) {
+      gkr_felt& f = out[n];
+      f.w[0] = (uint32_t)v;
+      f.w[1] = (uint32_t)(v >> 32);
+      for (int i = 2; i < 8; i++) f.w[i] = 0;
+    }
+    n++;
+  }
+  void q(const qm31& x) { u(x.a); u(x.b); u(x.c); u(x.d); }
+  void f(const felt& canon) {
+    if (out) felt_canon_to_words(canon, out[n].w);
+    n++;
+  }
+};
+static void serialize_proof(const gkr_proof* p, Ser& s) {
+  s.u(p->layers.size());
+  for (const LayerRec& L : p->layers) {
+    if (L.tag == 0) {
+      s.u(0);
+      const size_t nr = L.rp.size() / 3;
+      s.u(nr);
+      for (size_t r = 0; r < nr; r++) {  // c1 omitted (cairo_serde.rs:1327-1331)
+        s.q(L.rp[3 * r]);
+        s.q(L.rp[3 * r + 2]);
+      }
+      s.q(L.final_a);
+      s.q(L.final_b);
+    } else if (L.tag == 7) {
+      // LayerProof::MatMulDualSimd (cairo_serde.rs:1629-1646): c1 omitted
+      s.u(7);
+      s.u(L.n_block_vars);
+      const size_t nr = L.rp.size() / 4;
+      s.u(nr);
+      for (size_t r = 0; r < nr; r++) {
+        s.q(L.rp[4 * r]);
+        s.q(L.rp[4 * r + 2]);
+        s.q(L.rp[4 * r + 3]);
+      }
+      s.q(L.final_a);
+      s.q(L.final_b);
+    } else if (L.tag == 2) {
+      // LayerProof::Mul (cairo_serde.rs:1339-1354): c1 omitted
+      s.u(2);
+      const size_t nr = L.rp.size() / 4;
+      s.u(nr);
+      for (size_t r = 0; r < nr; r++) {
+        s.q(L.rp[4 * r]);
+        s.q(L.rp[4 * r + 2]);
+        s.q(L.rp[4 * r + 3]);
+      }
+      s.q(L.final_a);
+      s.q(L.final_b);
+    } else {
+      s.u(3);
+      s.u(L.act_type);
+      s.q(L.input_eval);
+      s.q(L.output_eval);
+      s.f(L.table_commitment);
+      s.u(1);  // has LogUp proof
+      // serialize_logup_proof_inner with multiplicities (cairo_serde.rs:1080-1105)
+      s.q(L.claimed_sum);
+      const size_t nr = L.rp.size() / 4;
+      s.u(nr);
+      for (size_t r = 0; r < nr; r++) {
+        s.q(L.rp[4 * r]);
+        s.q(L.rp[4 * r + 2]);
+        s.q(L.rp[4 * r + 3]);
+      }
+      s.q(L.w_eval);
+      s.q(L.in_eval);
+      s.q(L.out_eval);
+      s.u(L.mults.size());
+      for (uint32_t m : L.mults) s.u(m);
+      // serialize_multiplicity_sumcheck (cairo_serde.rs:1138-1156)
+      s.u(1);
+      const size_t nm = L.mult_rp.size() / 2;
+      s.u(nm);
+      for (size_t r = 0; r < nm; r++) {
+        s.q(L.mult_rp[2 * r]);
+        s.q(L.mult_rp[2 * r + 1]);
+      }
+      s.q(L.mult_final);
+      s.q(L.mult_sum);
+      s.u(0);  // no activation product proof
+      s.u(0);  // no piecewise proof
+    }
+  }
+  s.u(p->in_point.size());
+  for (const qm31& x : p->in_point) s.q(x);
+  s.q(p->in_value);
+  s.u(p->weight_commitments.size());
+  for (const felt& w : p->weight_commitments) s.f(w);
+  s.u(p->weight_openings.size());  // cairo_serde.rs:1756-1767
+  for (const auto& rec : p->weight_openings)
+    for (const felt& f : rec) s.f(f);
+  s.f(p->io_commitment);
+}
+extern "C" int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out) {
+  if (!p || !n_out || (!out && cap)) return fail(GKR_ERR_INVALID, "null argument");
+  Ser count{nullptr};
+  serialize_proof(p, count);
+  *n_out = count.n;
+  if (cap < count.n) return fail(GKR_ERR_BUFFER, "need %zu felts, have %zu", count.n, cap);
+  Ser write{out};
+  serialize_proof(p, write);
+  return GKR_OK;
+}
+

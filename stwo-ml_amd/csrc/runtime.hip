@@ -1,0 +1,508 @@
+// Device context, resident matrices, scratch buffers, result sinks and the
+// multi-round trip launcher shared by the layer reducers; the bandwidth
+// reference kernels.
+#include "internal.h"
+
+// ------------------------------------------------------------------ errors, version
+thread_local std::string g_err = "";
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+extern "C" const char* gkr_last_error(void) { return g_err.c_str(); }
+extern "C" const char* gkr_version(void) { return "gkr_mi355x 0.1 (gfx950)"; }
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
+  if (bytes == 0) bytes = 16;
+  if (c->noalloc) {
+    if (s == S_PART && bytes <= kScratchPartBytes) {
+      *out = c->scratch_dev + kScratchOffPart;
+      return GKR_OK;
+    }
+    if (s == S_TRIPCNT && bytes <= 256) {
+      *out = c->scratch_dev + kScratchOffCount;
+      return GKR_OK;
+    }
+    return fail(GKR_ERR_NOMEM, "the allocation-free entry point needs device buffer %d (%zu bytes)", (int)s, bytes);
+  }
+  if (c->cap[s] < bytes) {
+    if (s == S_TABLE) c->table_on_device = 0;
+    if (s == S_TRIPCNT) c->trip_count_valid = false;  // fresh memory must be zeroed
+    if (c->buf[s]) HIP_TRY(hipFree(c->buf[s]));
+    c->buf[s] = nullptr;
+    c->cap[s] = 0;
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    HIP_TRY(hipMalloc(&c->buf[s], want));
+    c->cap[s] = want;
+  }
+  *out = c->buf[s];
+  return GKR_OK;
+}
+
+int ensure_host_mult(gkr_ctx* c, uint64_t n) {
+  if (c->h_mult_cap >= n) return GKR_OK;
+  if (c->h_mult) {
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    (void)hipHostFree(c->h_mult);
+    c->h_mult = nullptr;
+    c->h_mult_cap = 0;
+  }
+  HIP_TRY(hipHostMalloc((void**)&c->h_mult, n * sizeof(uint32_t), hipHostMallocDefault));
+  c->h_mult_cap = n;
+  return GKR_OK;
+}
+
+hipEvent_t get_event(gkr_ctx* c) {
+  if (!c->free_events.empty()) {
+    hipEvent_t e = c->free_events.back();
+    c->free_events.pop_back();
+    return e;
+  }
+  // timing-only events: no system-scope fence (cache writeback) when they are
+  // recorded, so the pair brackets the kernel and not the cache maintenance
+  hipEvent_t e = nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
+  return e;
+}
+void collect_timing(gkr_ctx* c) {
+  for (auto& p : c->pending) {
+    float ms = 0;
+    if (hipEventElapsedTime(&ms, p.e0, p.e1) == hipSuccess) {
+      c->stats[p.kid].ms += ms;
+      c->stats[p.kid].launches++;
+      c->stats[p.kid].bytes += p.bytes;
+    }
+    c->free_events.push_back(p.e0);
+    c->free_events.push_back(p.e1);
+  }
+  c->pending.clear();
+}
+int sync(gkr_ctx* c) {
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  if (c->timing) collect_timing(c);
+  return GKR_OK;
+}
+
+PointArg make_point(const qm31* r, int n) {
+  PointArg p;
+  memset(&p, 0, sizeof p);
+  p.n = n;
+  for (int l = 0; l < n; l++) {
+    p.r[l] = r[l];
+    p.omr[l] = qm31_sub(qm31_one(), r[l]);
+  }
+  return p;
+}
+int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out) {
+  if (n > kMaxVars) return fail(GKR_ERR_INVALID, "eq table: %d variables exceeds %d", n, kMaxVars);
+  PointArg pt = make_point(r, n);
+  TimedLaunch t(c, K_EQ_TABLE, 16 * count);
+  if (n <= 10) {
+    hipLaunchKernelGGL(k_eq_direct, dim3(grid_for(count)), dim3(kBlock), 0, c->stream, pt, count, out);
+    return check_launch();
+  }
+  const int h = n / 2;
+  qm31 *hi, *lo;
+  TRY(ensureT(c, S_EQHI, 1ull << (n - h), &hi));
+  TRY(ensureT(c, S_EQLO, 1ull << h, &lo));
+  hipLaunchKernelGGL(k_eq_tables, dim3(grid_for((1ull << (n - h)) + (1ull << h))), dim3(kBlock), 0, c->stream, pt, h,
+                     hi, lo);
+  TRY(check_launch());
+  hipLaunchKernelGGL(k_eq_combine, dim3(grid_for(count)), dim3(kBlock), 0, c->stream, hi, lo, h, count, out);
+  return check_launch();
+}
+int make_sink(gkr_ctx* c, RoundSink* sk, int slot) {
+  qm31* part;
+  TRY(ensureT(c, S_PART, (size_t)kMaxSums * kMaxPartialBlocks, &part));
+  sk->partials = part;
+  sk->out = c->h_out + slot;
+  sk->flag = c->h_flag;
+  sk->seq = alloc_seq(&c->seq, 1);
+  return GKR_OK;
+}
+std::vector<Trip> plan_trips(int T, uint64_t host_len, int k0) {
+  std::vector<Trip> v;
+  if (T <= 0) return v;
+  int t = k0 < T ? k0 : T;
+  v.push_back({0, t, 1ull << T});
+  while (t < T && (1ull << (T - t)) > host_len) {
+    const uint64_t n = 1ull << (T - t);
+    int k = trip_k(n);
+    if (k > T - t) k = T - t;
+    v.push_back({t, k, n});
+    t += k;
+  }
+  return v;
+}
+void lagrange_weights(const qm31* r, int j, qm31* E) {
+  E[0] = qm31_one();
+  for (int i = 0; i < j; i++) {
+    const int m = 1 << i;
+    for (int u = m - 1; u >= 0; u--) {
+      const qm31 e = E[u];
+      E[2 * u + 1] = qm31_mul(e, r[i]);
+      E[2 * u] = qm31_sub(e, E[2 * u + 1]);
+    }
+  }
+}
+void trip_round_gram(const qm31* G, int K, int j, const qm31* r, int nx, const qm31* xs, qm31* out,
+                            const qm31* zt, const qm31& cpre) {
+  const int nu = 1 << j, nv = 1 << (K - j - 1), sh_b = K - j - 1, dim = 1 << K;
+  qm31 E[8];
+  lagrange_weights(r, j, E);
+  qm31 H[2][2] = {{qm31_zero(), qm31_zero()}, {qm31_zero(), qm31_zero()}};
+  for (int v = 0; v < nv; v++) {
+    qm31 ez = qm31_one();
+    if (zt)
+      for (int i = 0; i < K - j - 1; i++)
+        ez = qm31_mul(ez, ((v >> (K - j - 2 - i)) & 1) ? zt[j + 1 + i] : qm31_sub(qm31_one(), zt[j + 1 + i]));
+    for (int b = 0; b < 2; b++)
+      for (int b2 = 0; b2 < 2; b2++) {
+        qm31 acc = qm31_zero();
+        for (int u = 0; u < nu; u++) {
+          const int row = (u << (K - j)) | (b << sh_b) | v;
+          qm31 inner = qm31_zero();
+          for (int u2 = 0; u2 < nu; u2++) {
+            const int col = (u2 << (K - j)) | (b2 << sh_b) | v;
+            inner = qm31_add(inner, qm31_mul(E[u2], G[row * dim + col]));
+          }
+          acc = qm31_add(acc, qm31_mul(E[u], inner));
+        }
+        H[b][b2] = qm31_add(H[b][b2], zt ? qm31_mul(ez, acc) : acc);
+      }
+  }
+  qm31 pre = cpre;
+  if (zt)
+    for (int i = 0; i < j; i++) pre = qm31_mul(pre, eqlin(zt[i], r[i]));
+  for (int k = 0; k < nx; k++) {
+    const qm31 x = xs[k];
+    const qm31 e0 = qm31_sub(qm31_one(), x), e1 = x;
+    qm31 p = qm31_add(qm31_mul(qm31_mul(e0, e0), H[0][0]),
+                      qm31_add(qm31_mul(qm31_mul(e0, e1), qm31_add(H[0][1], H[1][0])), qm31_mul(qm31_mul(e1, e1), H[1][1])));
+    if (zt) p = qm31_mul(p, qm31_mul(pre, eqlin(zt[j], x)));
+    out[k] = p;
+  }
+}
+void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out) {
+  qm31 E[8];
+  lagrange_weights(r, j, E);
+  out[0] = out[1] = qm31_zero();
+  for (int c = 0; c < (1 << K); c++) {
+    const int u = c >> (K - j), b = (c >> (K - j - 1)) & 1;
+    out[b] = qm31_add(out[b], qm31_mul(E[u], S[c]));
+  }
+}
+// Launch k_trip<KIND, K> over sources sa (, sb) of length n << np with the
+// np pending challenges `pend`; folded vectors to da (, db) when given; eq
+// weights (KIND 1) from hi/lo; then the finisher into sink slot `slot`.
+template <int KIND, int K, bool SPLIT>
+static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n, int np, const TripChal& al,
+                         qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, const RoundSink& sk,
+                         unsigned grid, uint64_t b_rows, int b_chunks) {
+  uint32_t* counter = nullptr;
+  uint32_t base = 0;
+  if (GKR_TRIP_FUSED && grid <= kTripFusedMax) {  // one launch: the last workgroup finishes
+    TRY(ensureT(c, S_TRIPCNT, 1, &counter));
+    if (!c->trip_count_valid) {
+      hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, c->stream, counter, 1u);
+      TRY(check_launch());
+      c->trip_count = 0;
+      c->trip_count_valid = true;
+    }
+    base = c->trip_count;
+    c->trip_count += grid;
+  }
+  hipLaunchKernelGGL((k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
+                     sk, counter, base, b_rows, b_chunks);
+  TRY(check_launch());
+  if (counter) return GKR_OK;
+  constexpr int NQ = TripShape<KIND, K, SPLIT>::NQ;
+  hipLaunchKernelGGL(k_finish_wide<NQ>, dim3(1), dim3(kFinishBlock), 0, c->stream, sk, grid);
+  return check_launch();
+}
+int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
+                       const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
+                       RoundSink* sk, uint64_t b_rows, int b_chunks) {
+  if (np < 0 || np > kTripMaxK || K < 0 || K > kTripMaxK || (n >> K) == 0 || (kind == 1) != (hi != nullptr) ||
+      (b_chunks && (kind != 0 || np != 0 || b_rows > n)))
+    return fail(GKR_ERR_DEVICE, "bad trip (kind %d, K %d, np %d, n %llu)", kind, K, np, (unsigned long long)n);
+  HostTimer ht(c, K_HOST_LAUNCH);
+  TripChal al;
+  memset(&al, 0, sizeof al);
+  for (int i = 0; i < np; i++) al.c[i] = pend[i];
+  TRY(make_sink(c, sk, slot));
+  // short vectors: one lane per entry and vector (KIND 0 / 1: 2n lanes, the
+  // split layout of k_trip); long ones one lane per entry; up to
+  // kTripMaxBlocks workgroups
+  const bool split = kind != 2 && 2 * n <= (uint64_t)kTripFusedGrid * kBlock;
+  unsigned grid = partial_grid(split ? 2 * n : n);
+  const unsigned max_blocks = K <= 2 ? kTripMaxBlocksShort : kTripMaxBlocks;
+  if (grid > max_blocks) grid = max_blocks;
+  if (GKR_TRIP_FUSED && grid <= kTripFusedGrid) grid = grid < kTripFusedMax ? grid : kTripFusedMax;
+  const int nvec = kind == 2 ? 1 : 2;
+  TimedLaunch tl(c, kind == 0 ? K_MM_ROUND : K_EQ3_ROUND,
+                 16ull * nvec * ((n << np) + (da ? n : 0)));
+#define GKR_TRIP_CASE(KI, KK)                                                                                 \
+  if (kind == KI && K == KK)                                                                                  \
+    return split ? launch_trip_k<KI, KK, true>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks) \
+                 : launch_trip_k<KI, KK, false>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks);
+  GKR_TRIP_CASE(0, 1) GKR_TRIP_CASE(0, 2) GKR_TRIP_CASE(0, 3)
+  GKR_TRIP_CASE(1, 0) GKR_TRIP_CASE(1, 1) GKR_TRIP_CASE(1, 2) GKR_TRIP_CASE(1, 3)
+  GKR_TRIP_CASE(2, 1) GKR_TRIP_CASE(2, 2) GKR_TRIP_CASE(2, 3)
+#undef GKR_TRIP_CASE
+  return fail(GKR_ERR_DEVICE, "no trip kernel for kind %d, K %d", kind, K);
+}
+int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out) {
+  TRY(wait_result<0>(c, sk.seq, nullptr, K_HOST_WAIT, 0));
+  const int slot = (int)(sk.out - c->h_out);
+  for (int q = 0; q < nq; q++) out[q] = c->h_out[slot + q];
+  return GKR_OK;
+}
+
+int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out) {
+  HIP_TRY(hipMemcpyAsync(c->h_res, dev, count * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
+  TRY(sync(c));
+  for (int q = 0; q < count; q++) host_out[q] = c->h_res[q];
+  return GKR_OK;
+}
+int dot_m31(gkr_ctx* c, const uint32_t* v, const qm31* eq, uint64_t n, qm31* out) {
+  RoundSink sk;
+  TRY(make_sink(c, &sk));
+  hipLaunchKernelGGL(k_dot_m31, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, v, eq, n, sk);
+  TRY(launch_finish<1>(c, sk, partial_grid(n)));
+  return wait_sink<1>(c, sk, out);
+}
+// ------------------------------------------------------------------ context ABI
+extern "C" void gkr_ctx_destroy(gkr_ctx* c);
+extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
+  if (!out) return fail(GKR_ERR_INVALID, "null out");
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(GKR_ERR_INVALID, "device %d not present (%d devices)", device, n);
+  HIP_TRY(hipSetDevice(device));
+  gkr_ctx* c = new gkr_ctx();
+  c->device = device;
+  const char* i8 = getenv("GKR_INT8_WEIGHTS");
+  c->int8_weights = i8 && i8[0] == '1' && i8[1] == 0;
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete c;
+    return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");
+  }
+  if (hipHostMalloc((void**)&c->h_res, 64 * sizeof(qm31), hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&c->h_out, kOutSlots * sizeof(qm31) + 256, hipHostMallocCoherent | hipHostMallocMapped) !=
+          hipSuccess) {
+    gkr_ctx_destroy(c);
+    return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
+  }
+  if (hipHostMalloc((void**)&c->h_vec, 2 * kHandMax * sizeof(qm31), hipHostMallocCoherent | hipHostMallocMapped) !=
+      hipSuccess) {
+    gkr_ctx_destroy(c);
+    return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
+  }
+  {  // this device's copy of the static scratch array (gkr_sumcheck_product_noalloc)
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      gkr_ctx_destroy(c);
+      return fail(GKR_ERR_DEVICE, "scratch address on device %d: %s", device, hipGetErrorString(e));
+    }
+    c->scratch_dev = static_cast<uint8_t*>(p);
+  }
+  c->h_flag = reinterpret_cast<uint32_t*>(c->h_out + kOutSlots);
+  *c->h_flag = 0;
+  c->mailbox = reinterpret_cast<Mailbox*>(reinterpret_cast<char*>(c->h_out) + kOutSlots * sizeof(qm31) + 128);
+  c->mailbox->seq = 0;
+  c->mailbox->expired = 0;
+  *out = c;
+  return GKR_OK;
+}
+extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  for (auto& p : c->pending) {
+    (void)hipEventDestroy(p.e0);
+    (void)hipEventDestroy(p.e1);
+  }
+  for (auto e : c->free_events) (void)hipEventDestroy(e);
+  for (gkr_matrix* m : c->matrices) {  // matrices outliving their context keep only the handle
+    if (m->owned && m->dev) (void)hipFree(m->dev);
+    if (m->bplanes) (void)hipFree(m->bplanes);
+    if (m->r8) (void)hipFree(m->r8);
+    m->bplanes = nullptr;
+    m->r8 = nullptr;
+    m->dev = nullptr;
+    m->ctx = nullptr;
+  }
+  for (gkr_qvec* v : c->qvecs) {
+    if (v->dev) (void)hipFree(v->dev);
+    v->dev = nullptr;
+    v->ctx = nullptr;
+  }
+  for (int s = 0; s < S_NSLOTS; s++)
+    if (c->buf[s]) (void)hipFree(c->buf[s]);
+  if (c->merkle_consts) (void)hipFree(c->merkle_consts);
+  if (c->h_res) (void)hipHostFree(c->h_res);
+  if (c->h_mult) (void)hipHostFree(c->h_mult);
+  if (c->h_vec) (void)hipHostFree(c->h_vec);
+  if (c->h_out) (void)hipHostFree(c->h_out);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+extern "C" int gkr_ctx_debug(gkr_ctx* c, int op, uint64_t arg) {
+  if (!c) return fail(GKR_ERR_INVALID, "null ctx");
+  switch (op) {
+    case GKR_DEBUG_HANDOVER_CANCEL: c->debug_handover_cancel = true; return GKR_OK;
+    case GKR_DEBUG_HANDOVER_EXPIRE:
+      if (arg == 0 || arg > kWaitSpinLimit) return fail(GKR_ERR_INVALID, "spin limit %llu", (unsigned long long)arg);
+      c->debug_handover_spins = (uint32_t)arg;
+      return GKR_OK;
+    default: return fail(GKR_ERR_INVALID, "unknown debug op %d", op);
+  }
+}
+extern "C" int gkr_ctx_synchronize(gkr_ctx* c) {
+  if (!c) return fail(GKR_ERR_INVALID, "null ctx");
+  return sync(c);
+}
+extern "C" int gkr_ctx_set_timing(gkr_ctx* c, int level) {
+  const int enabled = level;
+  if (!c) return fail(GKR_ERR_INVALID, "null ctx");
+  TRY(sync(c));
+  c->timing = enabled < 0 ? 0 : (enabled > 2 ? 2 : enabled);
+  return GKR_OK;
+}
+extern "C" int gkr_ctx_kernel_time(gkr_ctx* c, int kid, double* total_ms, uint64_t* launches, uint64_t* bytes) {
+  if (!c || kid < 0 || kid >= K_NKERNELS) return fail(GKR_ERR_INVALID, "bad ctx or kernel id");
+  TRY(sync(c));
+  if (total_ms) *total_ms = c->stats[kid].ms;
+  if (launches) *launches = c->stats[kid].launches;
+  if (bytes) *bytes = c->stats[kid].bytes;
+  return GKR_OK;
+}
+extern "C" int gkr_ctx_reset_timing(gkr_ctx* c) {
+  if (!c) return fail(GKR_ERR_INVALID, "null ctx");
+  TRY(sync(c));
+  for (auto& s : c->stats) s = KernelStat();
+  return GKR_OK;
+}
+
+// ------------------------------------------------------------------ matrices
+gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t cols, bool owned);
+extern "C" int gkr_matrix_upload(gkr_ctx* c, const uint32_t* host, uint64_t rows, uint64_t cols, gkr_matrix** out) {
+  if (!c || !out || (!host && rows * cols)) return fail(GKR_ERR_INVALID, "null argument");
+  if (rows == 0 || cols == 0) return fail(GKR_ERR_INVALID, "empty matrix %llux%llu", (unsigned long long)rows,
+                                          (unsigned long long)cols);
+  const uint64_t n = rows * cols;
+  for (uint64_t i = 0; i < n; i++)
+    if (host[i] >= P) return fail(GKR_ERR_INVALID, "matrix value %u at %llu is not a canonical M31", host[i],
+                                  (unsigned long long)i);
+  uint32_t* d = nullptr;
+  HIP_TRY(hipMalloc(&d, n * sizeof(uint32_t)));
+  hipError_t e = hipMemcpyAsync(d, host, n * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return fail(GKR_ERR_DEVICE, "matrix upload: %s", hipGetErrorString(e));
+  }
+  *out = new_matrix(c, d, rows, cols, true);
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_wrap_device(gkr_ctx* c, const uint32_t* dev, uint64_t rows, uint64_t cols, gkr_matrix** out) {
+  if (!c || !out || !dev) return fail(GKR_ERR_INVALID, "null argument");
+  if (rows == 0 || cols == 0) return fail(GKR_ERR_INVALID, "empty matrix");
+  *out = new_matrix(c, const_cast<uint32_t*>(dev), rows, cols, false);
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_synthetic(gkr_ctx* c, uint64_t rows, uint64_t cols, int kind, uint64_t seed,
+                                    gkr_matrix** out) {
+  if (!c || !out) return fail(GKR_ERR_INVALID, "null argument");
+  if (rows == 0 || cols == 0) return fail(GKR_ERR_INVALID, "empty matrix");
+  if (kind != 0 && kind != 1) return fail(GKR_ERR_INVALID, "unknown synthetic kind %d", kind);
+  const uint64_t n = rows * cols;
+  uint32_t* d = nullptr;
+  HIP_TRY(hipMalloc(&d, n * sizeof(uint32_t)));
+  hipLaunchKernelGGL(k_fill_synth, dim3(partial_grid(n) * 8), dim3(kBlock), 0, c->stream, d, n, kind, seed);
+  int rc = check_launch();
+  if (rc == GKR_OK) rc = sync(c);
+  if (rc != GKR_OK) {
+    (void)hipFree(d);
+    return rc;
+  }
+  *out = new_matrix(c, d, rows, cols, true);
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_download(gkr_ctx* c, const gkr_matrix* m, uint32_t* host) {
+  if (!c || !m || !host) return fail(GKR_ERR_INVALID, "null argument");
+  if (m->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another (or a destroyed) context");
+  HIP_TRY(hipMemcpyAsync(host, m->dev, m->rows * m->cols * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
+  return sync(c);
+}
+extern "C" void gkr_matrix_free(gkr_matrix* m) {
+  if (!m) return;
+  if (m->ctx) {
+    if (m->ctx->mm.a == m || m->ctx->mm.b == m) m->ctx->mm.valid = false;
+    m->ctx->matrices.erase(m);
+    if ((m->owned && m->dev) || m->bplanes || m->r8) (void)hipStreamSynchronize(m->ctx->stream);
+    if (m->owned && m->dev) (void)hipFree(m->dev);
+    if (m->bplanes) (void)hipFree(m->bplanes);
+    if (m->r8) (void)hipFree(m->r8);
+  }
+  delete m;
+}
+gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t cols, bool owned) {
+  gkr_matrix* m = new gkr_matrix{c, dev, rows, cols, owned};
+  c->matrices.insert(m);
+  return m;
+}
+extern "C" uint32_t gkr_synthetic_value(int kind, uint64_t seed, uint64_t i) { return synth_value(kind, seed, i); }
+
+// ------------------------------------------------------------------ bandwidth reference
+extern "C" int gkr_bench_copy(gkr_ctx* c, uint64_t bytes, int iters, double* copy_gbps, double* read_gbps) {
+  if (!c || !copy_gbps || !read_gbps || bytes < 16 || iters < 1) return fail(GKR_ERR_INVALID, "bad argument");
+  HIP_TRY(hipSetDevice(c->device));
+  const uint64_t n = bytes / 16;
+  uint4 *src = nullptr, *dst = nullptr;
+  HIP_TRY(hipMalloc(&src, n * 16));
+  if (hipMalloc(&dst, n * 16) != hipSuccess) {
+    (void)hipFree(src);
+    return fail(GKR_ERR_NOMEM, "copy buffers");
+  }
+  int rc = GKR_OK;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  float ms = 0;
+  const unsigned g = 256 * 8;  // 8 workgroups per CU, grid-stride
+  if (hipMemsetAsync(src, 1, n * 16, c->stream) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+      hipEventCreate(&e1) != hipSuccess) {
+    rc = fail(GKR_ERR_DEVICE, "copy setup");
+  } else {
+    hipLaunchKernelGGL(k_copy16, dim3(g), dim3(kBlock), 0, c->stream, src, dst, n);  // warm-up
+    (void)hipEventRecord(e0, c->stream);
+    for (int i = 0; i < iters; i++) hipLaunchKernelGGL(k_copy16, dim3(g), dim3(kBlock), 0, c->stream, src, dst, n);
+    (void)hipEventRecord(e1, c->stream);
+    (void)hipEventSynchronize(e1);
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    *copy_gbps = 2.0 * n * 16 * iters / (ms * 1e-3) / 1e9;
+    (void)hipEventRecord(e0, c->stream);
+    for (int i = 0; i < iters; i++)
+      hipLaunchKernelGGL(k_read16, dim3(g), dim3(kBlock), 0, c->stream, src, n, (uint32_t*)dst);
+    (void)hipEventRecord(e1, c->stream);
+    (void)hipEventSynchronize(e1);
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    *read_gbps = (double)n * 16 * iters / (ms * 1e-3) / 1e9;
+    if (hipGetLastError() != hipSuccess) rc = fail(GKR_ERR_DEVICE, "copy kernels failed");
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  (void)hipFree(src);
+  (void)hipFree(dst);
+  return rc;
+}
+
+
+

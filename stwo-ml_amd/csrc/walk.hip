@@ -1,0 +1,97 @@
+// The GKR walk: a list of layer steps proved on one channel.
+#include "internal.h"
+#include "activations.h"
+// ------------------------------------------------------------------ GKR walk
+extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps, size_t n_steps,
+                              const gkr_qm31* init_point, uint32_t n_init, const gkr_qm31* init_value,
+                              gkr_proof* proof, gkr_qm31* final_point, uint32_t* n_final, gkr_qm31* final_value) {
+  CH_CHECK(ch);
+  if (!c || (!steps && n_steps) || !final_point || !n_final || !final_value)
+    return fail(GKR_ERR_INVALID, "null argument");
+  std::vector<gkr_qm31> point(init_point ? init_point : nullptr, init_point ? init_point + n_init : nullptr);
+  gkr_qm31 value = init_value ? *init_value : G(qm31_zero());
+  bool have_claim = init_value != nullptr;
+  std::vector<gkr_qm31> rp, npnt(64);
+  std::vector<uint32_t> mults;
+  for (size_t si = 0; si < n_steps; si++) {
+    const gkr_step& st = steps[si];
+    if (!st.a) return fail(GKR_ERR_INVALID, "step %zu: null matrix", si);
+    if (st.kind == GKR_STEP_MATMUL) {
+      if (!st.b) return fail(GKR_ERR_INVALID, "step %zu: null weight matrix", si);
+      const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.b->cols)));
+      if (st.claim == GKR_CLAIM_FRESH) {
+        point.resize(nv);
+        {
+          HostTimer ht(c, K_HOST_DRAW);
+          TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        }
+        TRY(gkr_matmul_output_claim(c, st.a, st.b, point.data(), nv, &value));
+        ch->ch.mix_secure_field(Q(value));
+      } else if (!have_claim) {
+        return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);
+      }
+      const int T = log2_exact(next_pow2(st.a->cols));
+      rp.resize(3 * (size_t)(T > 0 ? T : 1));
+      gkr_qm31 fa, fb, nval;
+      TRY(gkr_prove_matmul_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.b, ch, proof, rp.data(),
+                                 &fa, &fb, npnt.data(), &nval));
+      const uint32_t nn = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + T);
+      point.assign(npnt.begin(), npnt.begin() + nn);
+      value = nval;
+    } else if (st.kind == GKR_STEP_MUL) {
+      if (!st.b) return fail(GKR_ERR_INVALID, "step %zu: null rhs matrix", si);
+      const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
+      if (st.claim == GKR_CLAIM_FRESH) {
+        point.resize(nv);
+        {
+          HostTimer ht(c, K_HOST_DRAW);
+          TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        }
+        TRY(gkr_mul_output_claim(c, st.a, st.b, point.data(), nv, &value));
+        ch->ch.mix_secure_field(Q(value));
+      } else if (!have_claim) {
+        return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);
+      }
+      rp.resize(4 * (size_t)(nv ? nv : 1));
+      gkr_mul_out mo;
+      memset(&mo, 0, sizeof mo);
+      mo.eq_round_polys = rp.data();
+      TRY(gkr_prove_mul_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.b, ch, proof, &mo));
+      value = mo.next_value;  // the claim point is unchanged (prover.rs:6260-6263)
+    } else if (st.kind == GKR_STEP_ACTIVATION) {
+      const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
+      if (st.claim == GKR_CLAIM_FRESH) {
+        point.resize(nv);
+        {
+          HostTimer ht(c, K_HOST_DRAW);
+          TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        }
+        value = G(ch->ch.draw_qm31());
+      } else if (!have_claim) {
+        return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);
+      }
+      const uint32_t tl = st.table_log_size ? st.table_log_size : act_default_log_size(st.activation_type);
+      if (tl == 0 || tl > 24) return fail(GKR_ERR_INVALID, "step %zu: bad table size", si);
+      rp.resize(4 * (size_t)(nv ? nv : 1));
+      mults.resize((size_t)1 << tl);
+      std::vector<gkr_qm31> mrp(2 * tl);
+      gkr_logup_out out;
+      memset(&out, 0, sizeof out);
+      out.eq_round_polys = rp.data();
+      out.multiplicities = mults.data();
+      out.mult_round_polys = mrp.data();
+      TRY(gkr_prove_activation_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.activation_type, tl,
+                                     ch, proof, &out));
+      value = out.input_eval;  // the claim point is unchanged (prover.rs:6581-6584)
+    } else {
+      return fail(GKR_ERR_INVALID, "step %zu: unknown kind %u", si, st.kind);
+    }
+    have_claim = true;
+  }
+  if (point.size() > 64) return fail(GKR_ERR_BUFFER, "final claim has %zu variables", point.size());
+  for (size_t l = 0; l < point.size(); l++) final_point[l] = point[l];
+  *n_final = (uint32_t)point.size();
+  *final_value = value;
+  return GKR_OK;
+}
+
