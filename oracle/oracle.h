@@ -115,6 +115,51 @@ int orc_verify_activation_layer(const uint32_t* claim_point, int n_point, const 
                                 const uint32_t* mult_round_polys, const uint32_t* mult_final,
                                 const uint32_t* mult_sum, const uint32_t* input_eval, orc_channel* ch);
 
+/* ---------------------------------------------------------- LayerNorm / RMSNorm (norm.c) */
+/* Outputs of reduce_layernorm_layer / reduce_rmsnorm_layer_with_gamma
+ * (prover.rs:7944-8395, 8407-8801).  Caller-provided arrays: the three
+ * round-polynomial arrays hold 16 words (c0..c3) per round (nv rounds),
+ * multiplicities 2^16, mult_round_polys 16 x (c0, c1), row_stats0/1 one word
+ * per padded row.  RMSNorm uses mean_eval for rms_sq_eval, sum0 for the
+ * square sum, p0_final0 for its final input value, lin_final0/1 for
+ * (input_final, scale_final), row_stats0 for the per-row rms_sq; var_eval,
+ * sum1, p0_final1, cb_input, cb_mean and row_stats1 are LayerNorm-only. */
+typedef struct {
+  uint32_t input_eval[4], output_eval[4], mean_eval[4], rsqrt_eval[4], var_eval[4];
+  uint32_t n_active;
+  uint32_t sum0[4], sum1[4];
+  uint32_t* p0_round_polys;
+  uint32_t p0_final0[4], p0_final1[4];
+  uint32_t* lin_round_polys;
+  uint32_t lin_final0[4], lin_final1[4];
+  uint32_t cb_input[4], cb_mean[4];
+  uint32_t claimed_sum[4];
+  uint32_t* logup_round_polys;
+  uint32_t w_eval[4], in_eval[4], out_eval[4];
+  uint32_t* multiplicities;
+  uint32_t* mult_round_polys;
+  uint32_t mult_final[4], mult_sum[4];
+  uint32_t table_commitment[8];
+  uint32_t n_rows;
+  uint32_t* row_stats0;
+  uint32_t* row_stats1;
+  uint32_t gamma_commitment[8], gamma_eval[4];
+} orc_norm_out;
+uint32_t orc_rsqrt(uint32_t v); /* build_rsqrt_table entry (layernorm.rs:116-135) */
+void orc_layernorm_forward(const uint32_t* X, size_t rows, size_t cols, size_t dim, uint32_t* out_padded);
+void orc_rmsnorm_forward(const uint32_t* X, size_t rows, size_t cols, size_t dim, const uint32_t* gamma, size_t ng,
+                         uint32_t* out_padded);
+int orc_prove_layernorm_layer(const uint32_t* claim_point, int n_point, const uint32_t* claim_value,
+                              const uint32_t* X, size_t rows, size_t cols, size_t dim, orc_channel* ch,
+                              orc_norm_out* out);
+int orc_prove_rmsnorm_layer(const uint32_t* claim_point, int n_point, const uint32_t* claim_value, const uint32_t* X,
+                            size_t rows, size_t cols, size_t dim, const uint32_t* gamma, size_t ng, orc_channel* ch,
+                            orc_norm_out* out);
+int orc_verify_layernorm_layer(const uint32_t* claim_point, int nv, const uint32_t* claim_value, size_t dim,
+                               const orc_norm_out* p, orc_channel* ch, uint32_t next_value[4]);
+int orc_verify_rmsnorm_layer(const uint32_t* claim_point, int nv, const uint32_t* claim_value, size_t dim,
+                             const orc_norm_out* p, orc_channel* ch, uint32_t next_value[4]);
+
 #ifdef __cplusplus
 }
 #endif

@@ -755,3 +755,241 @@ def rlc_weight_binding(values, ch: Channel):
         pw = qmul(pw, rho)
     ch.mix_secure_field(combined)
     return combined
+
+
+# ------------------------------------------------------------------ LayerNorm / RMSNorm (norm.c)
+NORM_TABLE_LOG = 16
+
+
+class NormOut(C.Structure):
+    """orc_norm_out (oracle.h)."""
+    _fields_ = [("input_eval", C.c_uint32 * 4), ("output_eval", C.c_uint32 * 4), ("mean_eval", C.c_uint32 * 4),
+                ("rsqrt_eval", C.c_uint32 * 4), ("var_eval", C.c_uint32 * 4), ("n_active", C.c_uint32),
+                ("sum0", C.c_uint32 * 4), ("sum1", C.c_uint32 * 4), ("p0_round_polys", _U32P),
+                ("p0_final0", C.c_uint32 * 4), ("p0_final1", C.c_uint32 * 4), ("lin_round_polys", _U32P),
+                ("lin_final0", C.c_uint32 * 4), ("lin_final1", C.c_uint32 * 4), ("cb_input", C.c_uint32 * 4),
+                ("cb_mean", C.c_uint32 * 4), ("claimed_sum", C.c_uint32 * 4), ("logup_round_polys", _U32P),
+                ("w_eval", C.c_uint32 * 4), ("in_eval", C.c_uint32 * 4), ("out_eval", C.c_uint32 * 4),
+                ("multiplicities", _U32P), ("mult_round_polys", _U32P), ("mult_final", C.c_uint32 * 4),
+                ("mult_sum", C.c_uint32 * 4), ("table_commitment", C.c_uint32 * 8), ("n_rows", C.c_uint32),
+                ("row_stats0", _U32P), ("row_stats1", _U32P), ("gamma_commitment", C.c_uint32 * 8),
+                ("gamma_eval", C.c_uint32 * 4)]
+
+
+NORM_SCALAR_KEYS = ("input_eval", "output_eval", "mean_eval", "rsqrt_eval", "var_eval", "sum0", "sum1", "p0_final0",
+                    "p0_final1", "lin_final0", "lin_final1", "cb_input", "cb_mean", "claimed_sum", "w_eval",
+                    "in_eval", "out_eval", "mult_final", "mult_sum", "gamma_eval")
+
+
+def _norm_lib():
+    L = lib()
+    if not getattr(L, "_norm_ready", False):
+        L.orc_rsqrt.restype = C.c_uint32
+        L.orc_rsqrt.argtypes = [C.c_uint32]
+        L.orc_layernorm_forward.argtypes = [_U32P, C.c_size_t, C.c_size_t, C.c_size_t, _U32P]
+        L.orc_rmsnorm_forward.argtypes = [_U32P, C.c_size_t, C.c_size_t, C.c_size_t, _U32P, C.c_size_t, _U32P]
+        L.orc_prove_layernorm_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, C.c_size_t, C.c_size_t, C.c_size_t,
+                                                C.c_void_p, C.POINTER(NormOut)]
+        L.orc_prove_rmsnorm_layer.argtypes = [_U32P, C.c_int, _U32P, _U32P, C.c_size_t, C.c_size_t, C.c_size_t,
+                                              _U32P, C.c_size_t, C.c_void_p, C.POINTER(NormOut)]
+        for name in ("orc_verify_layernorm_layer", "orc_verify_rmsnorm_layer"):
+            getattr(L, name).argtypes = [_U32P, C.c_int, _U32P, C.c_size_t, C.POINTER(NormOut), C.c_void_p, _U32P]
+        L._norm_ready = True
+    return L
+
+
+def rsqrt_table_value(v: int) -> int:
+    return int(_norm_lib().orc_rsqrt(v))
+
+
+def layernorm_forward(X: np.ndarray, dim: int) -> np.ndarray:
+    """The LayerNorm output as reduce_layernorm_layer defines it, on the padded matrix."""
+    X = np.ascontiguousarray(X, dtype=np.uint32)
+    out = np.zeros((_next_pow2(X.shape[0]), _next_pow2(X.shape[1])), dtype=np.uint32)
+    _norm_lib().orc_layernorm_forward(_p(X), X.shape[0], X.shape[1], dim, _p(out))
+    return out
+
+
+def rmsnorm_forward(X: np.ndarray, dim: int, gamma=None) -> np.ndarray:
+    X = np.ascontiguousarray(X, dtype=np.uint32)
+    g = np.ascontiguousarray(gamma if gamma is not None else np.zeros(1), dtype=np.uint32)
+    out = np.zeros((_next_pow2(X.shape[0]), _next_pow2(X.shape[1])), dtype=np.uint32)
+    _norm_lib().orc_rmsnorm_forward(_p(X), X.shape[0], X.shape[1], dim, _p(g), 0 if gamma is None else len(g),
+                                    _p(out))
+    return out
+
+
+def _norm_buffers(nv: int, prow: int):
+    bufs = {"p0": np.zeros(16 * nv, dtype=np.uint32), "lin": np.zeros(16 * nv, dtype=np.uint32),
+            "lg": np.zeros(16 * nv, dtype=np.uint32), "mult": np.zeros(1 << NORM_TABLE_LOG, dtype=np.uint32),
+            "mrp": np.zeros(8 * NORM_TABLE_LOG, dtype=np.uint32), "rs0": np.zeros(max(1, prow), dtype=np.uint32),
+            "rs1": np.zeros(max(1, prow), dtype=np.uint32)}
+    o = NormOut()
+    o.p0_round_polys, o.lin_round_polys, o.logup_round_polys = _p(bufs["p0"]), _p(bufs["lin"]), _p(bufs["lg"])
+    o.multiplicities, o.mult_round_polys = _p(bufs["mult"]), _p(bufs["mrp"])
+    o.row_stats0, o.row_stats1 = _p(bufs["rs0"]), _p(bufs["rs1"])
+    return o, bufs
+
+
+def _norm_dict(o: "NormOut", bufs, nv: int) -> dict:
+    d = {k: tuple(int(x) for x in getattr(o, k)) for k in NORM_SCALAR_KEYS}
+    polys = lambda a: [tuple(tuple(int(x) for x in a[16 * t + 4 * j:16 * t + 4 * j + 4]) for j in range(4))
+                       for t in range(nv)]  # noqa: E731
+    d["p0_round_polys"], d["lin_round_polys"], d["logup_round_polys"] = (polys(bufs["p0"]), polys(bufs["lin"]),
+                                                                         polys(bufs["lg"]))
+    d["multiplicities"] = bufs["mult"].copy()
+    d["mult_round_polys"] = [(tuple(int(x) for x in bufs["mrp"][8 * t:8 * t + 4]),
+                              tuple(int(x) for x in bufs["mrp"][8 * t + 4:8 * t + 8])) for t in range(NORM_TABLE_LOG)]
+    d["table_commitment"] = felt_int(o.table_commitment)
+    d["gamma_commitment"] = felt_int(o.gamma_commitment)
+    d["n_active"], d["n_rows"] = int(o.n_active), int(o.n_rows)
+    d["row_stats0"] = [int(x) for x in bufs["rs0"][:o.n_rows]]
+    d["row_stats1"] = [int(x) for x in bufs["rs1"][:o.n_rows]]
+    return d
+
+
+def prove_layernorm_layer(claim_point, claim_value, X: np.ndarray, dim: int, ch: Channel) -> dict:
+    """reduce_layernorm_layer (engine/src/gkr/prover.rs:7944-8395)."""
+    X = np.ascontiguousarray(X, dtype=np.uint32)
+    nv = len(claim_point)
+    o, bufs = _norm_buffers(nv, _next_pow2(X.shape[0]))
+    rc = _norm_lib().orc_prove_layernorm_layer(_p(_qa(claim_point)), nv, _p(_qa([claim_value])), _p(X), X.shape[0],
+                                               X.shape[1], dim, ch.buf, C.byref(o))
+    if rc:
+        raise ValueError(f"oracle prove_layernorm_layer failed ({rc})")
+    return _norm_dict(o, bufs, nv)
+
+
+def prove_rmsnorm_layer(claim_point, claim_value, X: np.ndarray, dim: int, ch: Channel, gamma=None) -> dict:
+    """reduce_rmsnorm_layer_with_gamma (engine/src/gkr/prover.rs:8407-8801)."""
+    X = np.ascontiguousarray(X, dtype=np.uint32)
+    g = np.ascontiguousarray(gamma if gamma is not None else np.zeros(1), dtype=np.uint32)
+    nv = len(claim_point)
+    o, bufs = _norm_buffers(nv, _next_pow2(X.shape[0]))
+    rc = _norm_lib().orc_prove_rmsnorm_layer(_p(_qa(claim_point)), nv, _p(_qa([claim_value])), _p(X), X.shape[0],
+                                             X.shape[1], dim, _p(g), 0 if gamma is None else len(g), ch.buf,
+                                             C.byref(o))
+    if rc:
+        raise ValueError(f"oracle prove_rmsnorm_layer failed ({rc})")
+    return _norm_dict(o, bufs, nv)
+
+
+def _norm_struct(proof: dict):
+    nv = len(proof["lin_round_polys"])
+    o, bufs = _norm_buffers(nv, max(1, proof["n_rows"]))
+    for k in NORM_SCALAR_KEYS:
+        getattr(o, k)[:] = list(proof[k])
+    flat = lambda polys: [x for rp in polys for q in rp for x in q]  # noqa: E731
+    bufs["p0"][:] = flat(proof["p0_round_polys"])
+    bufs["lin"][:] = flat(proof["lin_round_polys"])
+    bufs["lg"][:] = flat(proof["logup_round_polys"])
+    bufs["mult"][:] = proof["multiplicities"]
+    bufs["mrp"][:] = [x for c0, c1 in proof["mult_round_polys"] for x in (*c0, *c1)]
+    bufs["rs0"][:len(proof["row_stats0"])] = proof["row_stats0"]
+    bufs["rs1"][:len(proof["row_stats1"])] = proof["row_stats1"]
+    o.table_commitment[:] = list(felt_words(proof["table_commitment"]))
+    o.n_active, o.n_rows = proof["n_active"], proof["n_rows"]
+    return o, bufs, nv
+
+
+def verify_norm_layer(kind: str, claim_point, claim_value, dim: int, proof: dict, ch: Channel):
+    """verify_layernorm_reduction / verify_rmsnorm_reduction (verifier.rs:4153-4690, 4693-5076).
+    Returns (status, next_value); status 0 = accepted."""
+    o, bufs, nv = _norm_struct(proof)
+    nx = np.zeros(4, dtype=np.uint32)
+    f = _norm_lib().orc_verify_layernorm_layer if kind == "layernorm" else _norm_lib().orc_verify_rmsnorm_layer
+    rc = f(_p(_qa(claim_point)), len(claim_point), _p(_qa([claim_value])), dim, C.byref(o), ch.buf, _p(nx))
+    return int(rc), _q(nx)
+
+
+def _ser_norm_logup(out: list, proof: dict) -> None:
+    """serialize_logup_proof with multiplicities (cairo_serde.rs:1071-1105)."""
+    out.append(1)
+    _ser_q(out, proof["claimed_sum"])
+    out.append(len(proof["logup_round_polys"]))
+    for rp in proof["logup_round_polys"]:
+        _ser_q(out, rp[0])
+        _ser_q(out, rp[2])
+        _ser_q(out, rp[3])
+    for k in ("w_eval", "in_eval", "out_eval"):
+        _ser_q(out, proof[k])
+    out.append(len(proof["multiplicities"]))
+    out.extend(int(x) for x in proof["multiplicities"])
+
+
+def serialize_layernorm_layer(out: list, proof: dict) -> None:
+    """LayerProof::LayerNorm in serialize_gkr_model_proof (cairo_serde.rs:1388-1484)."""
+    out.append(4)
+    for k in ("input_eval", "output_eval", "mean_eval", "rsqrt_eval"):
+        _ser_q(out, proof[k])
+    out.append(int(proof["table_commitment"]))
+    out.append(0)  # simd_combined
+    out.append(1)  # has the mean-variance part
+    out.append(proof["n_active"])
+    _ser_q(out, proof["sum0"])
+    _ser_q(out, proof["sum1"])
+    out.append(len(proof["p0_round_polys"]))
+    for rp in proof["p0_round_polys"]:
+        _ser_q(out, rp[0])
+        _ser_q(out, rp[2])
+        _ser_q(out, rp[3])
+    _ser_q(out, proof["p0_final0"])
+    _ser_q(out, proof["p0_final1"])
+    out.append(len(proof["lin_round_polys"]))
+    for rp in proof["lin_round_polys"]:
+        _ser_q(out, rp[0])
+        _ser_q(out, rp[2])
+        _ser_q(out, rp[3])
+    _ser_q(out, proof["lin_final0"])
+    _ser_q(out, proof["lin_final1"])
+    _ser_q(out, proof["cb_input"])
+    _ser_q(out, proof["cb_mean"])
+    _ser_norm_logup(out, proof)
+    out.append(1)  # multiplicity sumcheck (cairo_serde.rs:1138-1156)
+    out.append(len(proof["mult_round_polys"]))
+    for c0, c1 in proof["mult_round_polys"]:
+        _ser_q(out, c0)
+        _ser_q(out, c1)
+    _ser_q(out, proof["mult_final"])
+    _ser_q(out, proof["mult_sum"])
+    _ser_q(out, proof["var_eval"])
+    for key in ("row_stats0", "row_stats1"):
+        if proof["n_rows"] > 1:
+            out.append(1)
+            out.append(len(proof[key]))
+            out.extend(proof[key])
+        else:
+            out.append(0)
+
+
+def serialize_rmsnorm_layer(out: list, proof: dict) -> None:
+    """LayerProof::RMSNorm in serialize_gkr_model_proof (cairo_serde.rs:1648-1720): no multiplicity
+    sumcheck in this format."""
+    out.append(8)
+    for k in ("input_eval", "output_eval", "mean_eval", "rsqrt_eval"):
+        _ser_q(out, proof[k])
+    out.append(int(proof["table_commitment"]))
+    out.append(0)  # simd_combined
+    out.append(1)  # has the RMS^2 part
+    out.append(proof["n_active"])
+    _ser_q(out, proof["sum0"])
+    out.append(len(proof["p0_round_polys"]))
+    for rp in proof["p0_round_polys"]:
+        _ser_q(out, rp[0])
+        _ser_q(out, rp[2])
+        _ser_q(out, rp[3])
+    _ser_q(out, proof["p0_final0"])
+    out.append(len(proof["lin_round_polys"]))
+    for rp in proof["lin_round_polys"]:
+        _ser_q(out, rp[0])
+        _ser_q(out, rp[2])
+        _ser_q(out, rp[3])
+    _ser_q(out, proof["lin_final0"])
+    _ser_q(out, proof["lin_final1"])
+    _ser_norm_logup(out, proof)
+    if proof["n_rows"] > 1:
+        out.append(1)
+        out.append(len(proof["row_stats0"]))
+        out.extend(proof["row_stats0"])
+    else:
+        out.append(0)

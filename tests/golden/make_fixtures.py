@@ -13,6 +13,8 @@ tests and artifacts hold.  Sources:
   - elo-cairo-verifier/tests/test_field.cairo:14-142 (M31 / CM31 vectors)
   - engine/src/crypto/poseidon_constants.rs:98-191 (round constants: only a
     SHA-256 digest of the decimal list and the first/last value are kept)
+  - engine/tests/artifacts/d10_verify_gkr_calldata.txt and d10_onchain_summary.json
+    (MatMul -> LayerNorm -> MatMul on-chain calldata, e2e_cairo_verify.rs:312, 1479)
 """
 import hashlib
 import json
@@ -85,6 +87,14 @@ def main() -> None:
                      "source": "elo-cairo-verifier/tests/test_field.cairo"},
         "cm31_i_squared": {"x": [0, 1], "xx": [P - 1, 0]},
         "m31_inv2": {"x": 2, "inv": 0x40000000},
+    }
+    d10 = read("engine/tests/artifacts/d10_verify_gkr_calldata.txt").split()
+    out["d10"] = {
+        "source": "engine/tests/artifacts/d10_verify_gkr_calldata.txt",
+        "model": "build_gkr_mlp_layernorm (engine/tests/e2e_cairo_verify.rs:312-351): 2x4 input "
+                 "[[7,9,11,13],[17,19,21,23]], identity 4x4 W0, W2[i][j] = i+j+1 (4x2)",
+        "verify_calldata": [int(x, 16) if x.startswith("0x") else int(x) for x in d10],
+        "summary": json.loads(read("engine/tests/artifacts/d10_onchain_summary.json")),
     }
     with open(os.path.join(HERE, "reference_vectors.json"), "w") as f:
         json.dump(out, f, indent=1)
