@@ -371,26 +371,78 @@ int gkr_reduce_mul_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_p
 int gkr_mul_output_claim(gkr_ctx* ctx, const gkr_matrix* lhs, const gkr_matrix* rhs, const gkr_qm31* point,
                          uint32_t n_point, gkr_qm31* out);
 
+/* LayerNorm and RMSNorm layers (reduce_layernorm_layer, gkr/prover.rs:7944-8395;
+ * reduce_rmsnorm_layer_with_gamma, 8407-8801): Part 0 a plain sumcheck
+ * (LayerNorm: eta0 input + eta1 centered^2, tag 0x4D56; RMSNorm: input^2, tag
+ * 0x5251), Part 1 the eq-sumcheck of output = centered * rsqrt (LayerNorm, tag
+ * 0x4C4E) or input * scale (RMSNorm, tag 0x524E; scale = rsqrt * gamma), Part 2
+ * the LogUp of (variance or rms^2, rsqrt) in the 2^16-entry rsqrt table with
+ * its multiplicity sumcheck.  dim: the normalized width (the first
+ * min(dim, padded cols) columns); the claim point has log2 of the padded size
+ * entries.  The caller provides p0/lin/logup_round_polys (4 * n_vars each,
+ * c0..c3), multiplicities (2^16), mult_round_polys (2 * 16) and row_stats0/1
+ * (next_pow2(rows) each).  RMSNorm reports rms^2 in mean_eval, the square sum
+ * in sum0, its Part 0 final input in p0_final0, (input, scale) finals in
+ * lin_final0/1 and the per-row rms^2 in row_stats0; var_eval, sum1,
+ * p0_final1, cb_input, cb_mean and row_stats1 are LayerNorm's only, and
+ * gamma_commitment / gamma_eval RMSNorm's (not mixed, not serialized). */
+typedef struct {
+  gkr_qm31 input_eval, output_eval, mean_eval, rsqrt_eval, var_eval;
+  uint32_t n_active;
+  gkr_qm31 sum0, sum1;        /* LayerNorm: input sum, centered^2 sum; RMSNorm: input^2 sum */
+  gkr_qm31* p0_round_polys;   /* Part 0 */
+  gkr_qm31 p0_final0, p0_final1;
+  gkr_qm31* lin_round_polys;  /* Part 1 */
+  gkr_qm31 lin_final0, lin_final1;
+  gkr_qm31 cb_input, cb_mean; /* LayerNorm centered binding (input - mean = centered) */
+  gkr_qm31 claimed_sum;       /* Part 2: LogUp trace sum */
+  gkr_qm31* logup_round_polys;
+  gkr_qm31 w_eval, in_eval, out_eval;
+  uint32_t* multiplicities;
+  gkr_qm31* mult_round_polys;
+  gkr_qm31 mult_final_eval, mult_claimed_sum;
+  gkr_felt table_commitment;  /* hash_many([0x5253, 16]) (prover.rs:8357-8363) */
+  uint32_t n_rows;            /* padded rows */
+  uint32_t* row_stats0;       /* LayerNorm per-row means, RMSNorm per-row rms^2 */
+  uint32_t* row_stats1;       /* LayerNorm per-row variances */
+  gkr_felt gamma_commitment;
+  gkr_qm31 gamma_eval;
+} gkr_norm_out;
+int gkr_prove_layernorm_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                              const gkr_matrix* input, uint64_t dim, gkr_channel* ch, gkr_proof* proof,
+                              gkr_norm_out* out);
+/* gamma: host array of n_gamma canonical M31 (the learned per-column scale), or NULL. */
+int gkr_prove_rmsnorm_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                            const gkr_matrix* input, uint64_t dim, const uint32_t* gamma, uint64_t n_gamma,
+                            gkr_channel* ch, gkr_proof* proof, gkr_norm_out* out);
+/* MLE at `point` of the layer's output as the reducers define it (kind
+ * GKR_STEP_LAYERNORM or GKR_STEP_RMSNORM): LayerNorm (x - mean) * rsqrt on
+ * every padded entry; RMSNorm x * scale on the active columns, x elsewhere. */
+int gkr_norm_output_claim(gkr_ctx* ctx, uint32_t kind, const gkr_matrix* input, uint64_t dim, const uint32_t* gamma,
+                          uint64_t n_gamma, const gkr_qm31* point, uint32_t n_point, gkr_qm31* value);
+
 /* GKR walk over a sequence of layers (the layer loop of prove_gkr_with_cache,
- * gkr/prover.rs:1500-1660, for MatMul and Activation layers).  Steps run in
- * order on one channel and append their LayerProof to `proof`.  Each step's
- * output claim is either chained (the previous step's input claim, or
- * init_point/init_value for the first step: the reference's walk) or fresh:
- * a MatMul draws r_out = draw_qm31s(log2 pm + log2 pn), takes value =
- * MLE of A*B at r_out and mixes it (prover.rs:1543-1560); an Activation
- * draws its point (log2 of the padded size) and then its value with
- * draw_qm31; a Mul draws its point (log2 of the padded size), takes the
- * product MLE there and mixes it.  On return final_point/final_value hold the last input claim
- * (final_point needs room for 64 entries).                                  */
-enum { GKR_STEP_MATMUL = 0, GKR_STEP_MUL = 2, GKR_STEP_ACTIVATION = 3 };
+ * gkr/prover.rs:1500-1660, for MatMul, Mul, Activation, LayerNorm and RMSNorm
+ * layers).  Steps run in order on one channel and append their LayerProof to
+ * `proof`.  Each step's output claim is either chained (the previous step's
+ * input claim, or init_point/init_value for the first step: the reference's
+ * walk) or fresh: a MatMul draws r_out = draw_qm31s(log2 pm + log2 pn), takes
+ * value = MLE of A*B at r_out and mixes it (prover.rs:1543-1560); an
+ * Activation draws its point (log2 of the padded size) and then its value
+ * with draw_qm31; a Mul, LayerNorm or RMSNorm draws its point (log2 of the
+ * padded size), takes the MLE of its output there and mixes it.  On return
+ * final_point/final_value hold the last input claim (final_point needs room
+ * for 64 entries).                                                          */
+enum { GKR_STEP_MATMUL = 0, GKR_STEP_MUL = 2, GKR_STEP_ACTIVATION = 3, GKR_STEP_LAYERNORM = 4, GKR_STEP_RMSNORM = 8 };
 enum { GKR_CLAIM_CHAINED = 0, GKR_CLAIM_FRESH = 1 };
 typedef struct {
-  uint32_t kind;             /* GKR_STEP_MATMUL / GKR_STEP_ACTIVATION */
+  uint32_t kind;             /* GKR_STEP_* */
   uint32_t claim;            /* GKR_CLAIM_CHAINED / GKR_CLAIM_FRESH */
-  const gkr_matrix* a;       /* MatMul: A (m x k); Mul: lhs; Activation: the input matrix */
-  const gkr_matrix* b;       /* MatMul: B (k x n); Mul: rhs; Activation: unused */
+  const gkr_matrix* a;       /* MatMul: A (m x k); Mul: lhs; Activation / norms: the input matrix */
+  const gkr_matrix* b;       /* MatMul: B (k x n); Mul: rhs; RMSNorm: gamma (1 x n_gamma) or NULL */
   uint32_t activation_type;  /* Activation: reference type tag */
   uint32_t table_log_size;   /* Activation: 0 = reference default */
+  uint64_t dim;              /* LayerNorm / RMSNorm: normalized width (0: the input's columns) */
 } gkr_step;
 int gkr_prove_walk(gkr_ctx* ctx, gkr_channel* ch, const gkr_step* steps, size_t n_steps, const gkr_qm31* init_point,
                    uint32_t n_init, const gkr_qm31* init_value, gkr_proof* proof, gkr_qm31* final_point,
@@ -423,6 +475,14 @@ int gkr_verify_mul_layer(const gkr_qm31* claim_point, uint32_t n_point, const gk
 int gkr_verify_activation_layer(const gkr_qm31* claim_point, uint32_t n_point, uint32_t activation_type,
                                 uint32_t table_log_size, uint32_t n_eq_rounds, const gkr_logup_out* proof,
                                 gkr_channel* ch, gkr_qm31* next_value);
+/* verify_layernorm_reduction / verify_rmsnorm_reduction (verifier.rs:4153-4690,
+ * 4693-5076), non-SIMD with the Part 0 proof: `proof` as the reducers fill it
+ * (round polynomials in full, n_rows padded rows).  The multi-row LayerNorm
+ * variance binding is the reference's (rows with equal variances pass). */
+int gkr_verify_layernorm_layer(const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                               uint64_t dim, const gkr_norm_out* proof, gkr_channel* ch, gkr_qm31* next_value);
+int gkr_verify_rmsnorm_layer(const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                             uint64_t dim, const gkr_norm_out* proof, gkr_channel* ch, gkr_qm31* next_value);
 /* One layer of the circuit a walk is verified against. */
 typedef struct {
   uint32_t kind;             /* GKR_STEP_MATMUL / GKR_STEP_MUL / GKR_STEP_ACTIVATION */
@@ -431,6 +491,7 @@ typedef struct {
   uint32_t activation_type;  /* Activation */
   uint32_t table_log_size;   /* Activation: 0 = reference default */
   uint32_t claim;            /* GKR_CLAIM_CHAINED / GKR_CLAIM_FRESH, as the walk that proved it */
+  uint64_t dim;              /* LayerNorm: normalized width (0: cols) */
 } gkr_layer_shape;
 /* A walk from serialize_gkr_model_proof calldata (the layer section and the
  * input claim that follows it).  A chained layer's claim is the previous

@@ -78,7 +78,7 @@ inline bool felt_abi_canonical(const gkr_felt& f) {
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NSLOTS
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and host-side phases (Fiat-Shamir
 // hashing inside the reducers, waiting for trip results, waiting for the
@@ -476,6 +476,23 @@ struct gkr_channel {
 #define CH_CHECK(ch) \
   if (!(ch)) return fail(GKR_ERR_INVALID, "null channel")
 
+// A LayerNorm (tag 4) or RMSNorm (tag 8) layer's proof fields (types.rs
+// LayerProof::LayerNorm / RMSNorm): RMSNorm keeps rms^2 in mean_eval, the
+// square sum in sum0, its final input in p0_final0, (input, scale) finals in
+// lin_final0/1, the per-row rms^2 in rows0.
+struct NormRec {
+  qm31 input_eval, output_eval, mean_eval, rsqrt_eval, var_eval;
+  uint32_t n_active = 0;
+  qm31 sum0, sum1;
+  std::vector<qm31> p0, lin, logup;  // c0..c3 per round
+  qm31 p0_final0, p0_final1, lin_final0, lin_final1, cb_input, cb_mean;
+  qm31 claimed_sum, w_eval, in_eval, out_eval;
+  std::vector<uint32_t> mults;
+  std::vector<qm31> mult_rp;  // c0, c1 per round
+  qm31 mult_final, mult_sum;
+  felt table_commitment;
+  std::vector<uint32_t> rows0, rows1;  // per padded row
+};
 struct LayerRec {
   uint32_t tag;  // 0 MatMul, 2 Mul, 3 Activation, 7 MatMulDualSimd (rp: c0..c3 per round)
   uint32_t n_block_vars = 0;  // MatMulDualSimd
@@ -489,6 +506,7 @@ struct LayerRec {
   std::vector<uint32_t> mults;
   std::vector<qm31> mult_rp;  // c0,c1 per round
   qm31 mult_final, mult_sum;
+  NormRec norm;  // tags 4 (LayerNorm) and 8 (RMSNorm)
 };
 // A MatMul layer's claim on its weight: MLE(B)(r_j || sumcheck challenges) =
 // final_b (push_matmul_weight_data, prover.rs:1465-1483).

@@ -53,6 +53,74 @@ struct Ser {
     n++;
   }
 };
+// (c0, c2, c3) per round, c1 omitted
+static void ser_deg3(const std::vector<qm31>& rp, Ser& s) {
+  const size_t nr = rp.size() / 4;
+  s.u(nr);
+  for (size_t r = 0; r < nr; r++) {
+    s.q(rp[4 * r]);
+    s.q(rp[4 * r + 2]);
+    s.q(rp[4 * r + 3]);
+  }
+}
+// LayerProof::LayerNorm (cairo_serde.rs:1388-1484) and LayerProof::RMSNorm
+// (1648-1720; no multiplicity sumcheck in this format), non-SIMD, with their
+// Part 0 proofs; per-row statistics only for more than one padded row.
+static void serialize_norm(const LayerRec& L, Ser& s) {
+  const NormRec& N = L.norm;
+  const bool ln = L.tag == 4;
+  s.u(L.tag);
+  s.q(N.input_eval);
+  s.q(N.output_eval);
+  s.q(N.mean_eval);
+  s.q(N.rsqrt_eval);
+  s.f(N.table_commitment);
+  s.u(0);  // simd_combined
+  s.u(1);  // Part 0 present
+  s.u(N.n_active);
+  s.q(N.sum0);
+  if (ln) s.q(N.sum1);
+  ser_deg3(N.p0, s);
+  s.q(N.p0_final0);
+  if (ln) s.q(N.p0_final1);
+  ser_deg3(N.lin, s);
+  s.q(N.lin_final0);
+  s.q(N.lin_final1);
+  if (ln) {
+    s.q(N.cb_input);
+    s.q(N.cb_mean);
+  }
+  s.u(1);  // LogUp proof (serialize_logup_proof, with multiplicities: cairo_serde.rs:1071-1105)
+  s.q(N.claimed_sum);
+  ser_deg3(N.logup, s);
+  s.q(N.w_eval);
+  s.q(N.in_eval);
+  s.q(N.out_eval);
+  s.u(N.mults.size());
+  for (uint32_t m : N.mults) s.u(m);
+  const bool multi_row = N.rows0.size() > 1;
+  if (ln) {
+    s.u(1);  // serialize_multiplicity_sumcheck (cairo_serde.rs:1138-1156)
+    s.u(N.mult_rp.size() / 2);
+    for (const qm31& c : N.mult_rp) s.q(c);
+    s.q(N.mult_final);
+    s.q(N.mult_sum);
+    s.q(N.var_eval);
+    for (const std::vector<uint32_t>* rv : {&N.rows0, &N.rows1}) {
+      s.u(multi_row ? 1 : 0);
+      if (multi_row) {
+        s.u(rv->size());
+        for (uint32_t v : *rv) s.u(v);
+      }
+    }
+  } else {
+    s.u(multi_row ? 1 : 0);
+    if (multi_row) {
+      s.u(N.rows0.size());
+      for (uint32_t v : N.rows0) s.u(v);
+    }
+  }
+}
 static void serialize_proof(const gkr_proof* p, Ser& s) {
   s.u(p->layers.size());
   for (const LayerRec& L : p->layers) {
@@ -79,6 +147,8 @@ static void serialize_proof(const gkr_proof* p, Ser& s) {
       }
       s.q(L.final_a);
       s.q(L.final_b);
+    } else if (L.tag == 4 || L.tag == 8) {
+      serialize_norm(L, s);
     } else if (L.tag == 2) {
       // LayerProof::Mul (cairo_serde.rs:1339-1354): c1 omitted
       s.u(2);

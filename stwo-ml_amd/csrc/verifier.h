@@ -247,6 +247,226 @@ inline bool verify_activation(const std::vector<qm31>& point, uint32_t tag, uint
   return true;
 }
 
+// A LayerNorm / RMSNorm layer proof (types.rs LayerProof::LayerNorm /
+// RMSNorm) with full round polynomials (c0..c3 per round).  RMSNorm keeps
+// rms^2 in key_eval, the square sum in sum0, the Part 0 final input in
+// p0_final0, the per-row rms^2 in rows0; has_mult is false when the format
+// carries no multiplicity sumcheck (serialize_gkr_model_proof's RMSNorm).
+struct NormProofIn {
+  qm31 input_eval, output_eval, key_eval /* LN mean, RMS rms^2 */, rsqrt_eval, var_eval;
+  uint64_t n_active = 0;
+  qm31 sum0, sum1;
+  std::vector<qm31> p0, lin;
+  qm31 p0_final0, p0_final1, lin_final0, lin_final1, cb_input, cb_mean;
+  LogUpProofIn lu;  // claimed_sum, eq_polys, w/in/out evals, mults, mult_polys, mult_final/sum, table_commitment
+  bool has_mult = true;
+  std::vector<uint32_t> rows0, rows1;
+};
+
+inline uint32_t norm_inv_or_zero(uint64_t n) { return n ? m31_inv(m31_from_u32((uint32_t)(n % P))) : 0u; }
+inline qm31 norm_row_mle(const std::vector<uint32_t>& v, int log_rows, const qm31* s) {
+  qm31 acc = qm31_zero();
+  for (size_t r = 0; r < v.size(); r++) {
+    qm31 e = qm31_one();
+    for (int k = 0; k < log_rows; k++) e = qm31_mul(e, ((r >> (log_rows - 1 - k)) & 1) ? s[k] : qm31_sub(qm31_one(), s[k]));
+    acc = qm31_add(acc, qm31_mul(e, qm31_from_m31(v[r])));
+  }
+  return acc;
+}
+// p(0) + p(1) = sum per round, mix, draw; the challenges and the final sum.
+inline bool norm_rounds(const std::vector<qm31>& polys, qm31* sum, PoseidonChannel& ch, std::vector<qm31>* chal,
+                        const char* what, VerifyError* err, bool compressed) {
+  for (size_t t = 0; t < polys.size() / 4; t++) {
+    qm31 c[4] = {polys[4 * t], polys[4 * t + 1], polys[4 * t + 2], polys[4 * t + 3]};
+    if (compressed) c[1] = qm31_sub(qm31_sub(qm31_sub(qm31_sub(*sum, c[0]), c[0]), c[2]), c[3]);
+    const qm31 p01 = qm31_add(c[0], qm31_add(qm31_add(qm31_add(c[0], c[1]), c[2]), c[3]));
+    if (!qm31_eq(p01, *sum)) {
+      err->why = std::string(what) + " round " + std::to_string(t) + ": p(0)+p(1) = " + q_str(p01) + " != sum " +
+                 q_str(*sum);
+      return false;
+    }
+    ch.mix_poly_coeffs_deg3(c[0], c[1], c[2], c[3]);
+    const qm31 r = ch.draw_qm31();
+    if (chal) chal->push_back(r);
+    *sum = poly_eval(c, 3, r);
+  }
+  return true;
+}
+
+// verify_layernorm_reduction (verifier.rs:4153-4690) and verify_rmsnorm_reduction
+// (4693-5076), non-SIMD, with the Part 0 proof present.  The multi-row
+// LayerNorm variance binding is the reference's: the row variances weighted at
+// the mean-variance challenges must equal var_eval at the claim point, which
+// holds when every row has the same variance.
+inline bool verify_norm(bool ln, const std::vector<qm31>& point, const qm31& value, uint64_t dim, const NormProofIn& p,
+                        const std::vector<uint32_t>& rsqrt_table, PoseidonChannel& ch, qm31* next_value,
+                        VerifyError* err, bool compressed = false) {
+  const char* name = ln ? "layernorm" : "rmsnorm";
+  const size_t nv = p.lin.size() / 4;
+  if (nv == 0) {
+    err->why = std::string(name) + " linear eq-sumcheck has 0 rounds";
+    return false;
+  }
+  if (point.size() < nv) {
+    err->why = std::string(name) + ": claim point too short";
+    return false;
+  }
+  if (p.lu.eq_polys.size() / 4 != nv || p.p0.size() / 4 != nv) {
+    err->why = std::string(name) + ": part 0 / LogUp round counts differ from the linear sumcheck";
+    return false;
+  }
+  const uint64_t total = 1ull << nv;
+  const uint64_t n_active = dim < total ? dim : total;
+  const uint64_t cols_padded = v_next_pow2(dim);
+  const uint64_t rows = total / cols_padded;
+  const int log_rows = (int)nv - v_log2(cols_padded);
+  // Part 0
+  std::vector<qm31> mv;
+  qm31 sum;
+  if (ln) {
+    ch.mix_u64(0x4D56ull);
+    ch.mix_u64(n_active);
+    ch.mix_secure_field(p.sum0);
+    ch.mix_secure_field(p.sum1);
+    const qm31 eta0 = ch.draw_qm31(), eta1 = qm31_mul(eta0, eta0);
+    sum = qm31_add(qm31_mul(eta0, p.sum0), qm31_mul(eta1, p.sum1));
+    if (!norm_rounds(p.p0, &sum, ch, &mv, "layernorm mean-variance", err, compressed)) return false;
+    ch.mix_secure_field(p.p0_final0);
+    ch.mix_secure_field(p.p0_final1);
+    const qm31 cf = qm31_sub(p.p0_final0, p.p0_final1);
+    if (!qm31_eq(sum, qm31_add(qm31_mul(eta0, p.p0_final0), qm31_mul(eta1, qm31_sqr(cf))))) {
+      err->why = "layernorm mean-variance final check failed";
+      return false;
+    }
+    if (rows == 1) {
+      const uint32_t inv_n = norm_inv_or_zero(n_active);
+      if (m31_mul(p.sum0.a, inv_n) != p.key_eval.a) {
+        err->why = "layernorm mean derivation mismatch";
+        return false;
+      }
+      if (n_active == cols_padded && (m31_mul(p.sum1.a, inv_n) & 0xFFFFu) != p.var_eval.a) {
+        err->why = "layernorm variance derivation mismatch";
+        return false;
+      }
+    } else {
+      if (p.rows0.size() != rows || p.rows1.size() != rows) {
+        err->why = "layernorm row statistics length differs from " + std::to_string(rows) + " rows";
+        return false;
+      }
+      if (!qm31_eq(p.p0_final1, norm_row_mle(p.rows0, log_rows, mv.data()))) {
+        err->why = "layernorm multi-row mean binding failed";
+        return false;
+      }
+      if (!qm31_eq(p.var_eval, norm_row_mle(p.rows1, log_rows, mv.data()))) {
+        err->why = "layernorm multi-row variance binding failed";
+        return false;
+      }
+    }
+  } else {
+    ch.mix_u64(0x5251ull);
+    ch.mix_u64(n_active);
+    ch.mix_secure_field(p.sum0);
+    sum = p.sum0;
+    if (!norm_rounds(p.p0, &sum, ch, nullptr, "rmsnorm RMS^2", err, compressed)) return false;
+    ch.mix_secure_field(p.p0_final0);
+    if (!qm31_eq(qm31_sqr(p.p0_final0), sum)) {
+      err->why = "rmsnorm RMS^2 final check failed";
+      return false;
+    }
+    if (rows == 1) {
+      if ((m31_mul(p.sum0.a, norm_inv_or_zero(n_active)) & 0xFFFFu) != p.key_eval.a) {
+        err->why = "rmsnorm RMS^2 derivation mismatch";
+        return false;
+      }
+    } else {
+      if (p.rows0.size() != rows) {
+        err->why = "rmsnorm row_rms_sq length differs from " + std::to_string(rows) + " rows";
+        return false;
+      }
+      if (!qm31_eq(p.key_eval, norm_row_mle(p.rows0, log_rows, point.data()))) {
+        err->why = "rmsnorm multi-row rms_sq binding failed";
+        return false;
+      }
+    }
+  }
+  // Part 1
+  ch.mix_u64(ln ? 0x4C4Eull : 0x524Eull);
+  ch.mix_secure_field(p.key_eval);
+  ch.mix_secure_field(p.rsqrt_eval);
+  ch.mix_secure_field(value);
+  sum = value;
+  std::vector<qm31> chal;
+  if (!norm_rounds(p.lin, &sum, ch, &chal, ln ? "layernorm linear" : "rmsnorm linear", err, compressed)) return false;
+  if (!qm31_eq(sum, qm31_mul(qm31_mul(eq_eval(point.data(), chal.data(), nv), p.lin_final0), p.lin_final1))) {
+    err->why = std::string(name) + " linear final check failed";
+    return false;
+  }
+  ch.mix_secure_field(p.lin_final0);
+  ch.mix_secure_field(p.lin_final1);
+  if (ln) {
+    ch.mix_secure_field(p.cb_input);
+    ch.mix_secure_field(p.cb_mean);
+    if (!qm31_eq(p.lin_final0, qm31_sub(p.cb_input, p.cb_mean))) {
+      err->why = "layernorm centered binding failed";
+      return false;
+    }
+  }
+  // Part 2: rsqrt LogUp
+  ch.mix_u64(0x4C4F47ull);
+  ch.mix_u64(ln ? 0x5253ull : 0x524Eull);
+  const qm31 gamma = ch.draw_qm31(), beta = ch.draw_qm31();
+  felt tc_in[2] = {felt_from_u64(0x5253), felt_from_u64(16)};
+  if (!felt_eq(felt_from_mont(poseidon_hash_many(tc_in, 2)), p.lu.table_commitment)) {
+    err->why = std::string(name) + " rsqrt table commitment mismatch";
+    return false;
+  }
+  if (p.lu.mults.size() != rsqrt_table.size()) {
+    err->why = std::string(name) + " rsqrt multiplicities length " + std::to_string(p.lu.mults.size());
+    return false;
+  }
+  qm31 table_sum = qm31_zero();
+  for (size_t j = 0; j < rsqrt_table.size(); j++) {
+    if (!p.lu.mults[j]) continue;
+    const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31((uint32_t)j)), qm31_mul(beta, qm31_from_m31(rsqrt_table[j])));
+    table_sum = qm31_add(table_sum, qm31_mul(qm31_from_m31(m31_from_u32(p.lu.mults[j])), qm31_inv(d)));
+  }
+  if (!qm31_eq(p.lu.claimed_sum, table_sum)) {
+    err->why = std::string(name) + " rsqrt LogUp sum mismatch";
+    return false;
+  }
+  ch.mix_secure_field(p.lu.claimed_sum);
+  sum = qm31_one();
+  std::vector<qm31> lchal;
+  if (!norm_rounds(p.lu.eq_polys, &sum, ch, &lchal, ln ? "layernorm LogUp" : "rmsnorm LogUp", err, compressed))
+    return false;
+  const qm31 d_eval = qm31_sub(qm31_sub(gamma, p.lu.in_eval), qm31_mul(beta, p.lu.out_eval));
+  if (!qm31_eq(sum, qm31_mul(qm31_mul(eq_eval(point.data(), lchal.data(), nv), p.lu.w_eval), d_eval))) {
+    err->why = std::string(name) + " LogUp final check failed";
+    return false;
+  }
+  if (p.has_mult) {  // verify_multiplicity_sumcheck
+    qm31 msum = p.lu.mult_sum;
+    for (size_t t = 0; t < p.lu.mult_polys.size() / 2; t++) {
+      const qm31 c0 = p.lu.mult_polys[2 * t], c1 = p.lu.mult_polys[2 * t + 1];
+      if (!qm31_eq(qm31_add(c0, qm31_add(c0, c1)), msum)) {
+        err->why = "multiplicity sumcheck round check failed";
+        return false;
+      }
+      ch.mix_secure_field(c0);
+      ch.mix_secure_field(c1);
+      msum = qm31_add(c0, qm31_mul(c1, ch.draw_qm31()));
+    }
+    if (!qm31_eq(msum, p.lu.mult_final)) {
+      err->why = "multiplicity sumcheck final eval mismatch";
+      return false;
+    }
+  }
+  ch.mix_secure_field(p.input_eval);
+  ch.mix_secure_field(p.output_eval);
+  *next_value = p.input_eval;
+  return true;
+}
+
 // Reader of serialize_gkr_model_proof calldata (felt252 words).
 struct FeltReader {
   const uint32_t* w;  // 8 words per felt

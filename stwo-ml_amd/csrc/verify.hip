@@ -2,6 +2,7 @@
 // (engine/src/gkr/verifier.rs).
 #include "internal.h"
 #include "activations.h"
+#include "norm.h"
 #include "verifier.h"
 // ------------------------------------------------------------------ verifier replay
 static bool read_point(const gkr_qm31* p, uint32_t n, std::vector<qm31>* out) {
@@ -105,6 +106,74 @@ extern "C" int gkr_verify_activation_layer(const gkr_qm31* claim_point, uint32_t
   return GKR_OK;
 }
 
+static const std::vector<uint32_t>& rsqrt_table() {
+  static const std::vector<uint32_t> t = [] {
+    std::vector<uint32_t> v(1u << kNormTableLog);
+    for (uint32_t j = 0; j < v.size(); j++) v[j] = norm_rsqrt(j);
+    return v;
+  }();
+  return t;
+}
+static int verify_norm_abi(bool ln, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                           uint64_t dim, const gkr_norm_out* o, gkr_channel* ch, gkr_qm31* next_value) {
+  CH_CHECK(ch);
+  if (!o || !claim_value || !next_value || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
+  if (!o->p0_round_polys || !o->lin_round_polys || !o->logup_round_polys || !o->multiplicities ||
+      !o->mult_round_polys || (o->n_rows && (!o->row_stats0 || !o->row_stats1)))
+    return fail(GKR_ERR_INVALID, "null proof arrays");
+  std::vector<qm31> pt;
+  if (!read_point(claim_point, n_point, &pt)) return fail(GKR_ERR_INVALID, "claim point not canonical");
+  NormProofIn p;
+  p.input_eval = Q(o->input_eval);
+  p.output_eval = Q(o->output_eval);
+  p.key_eval = Q(o->mean_eval);
+  p.rsqrt_eval = Q(o->rsqrt_eval);
+  p.var_eval = Q(o->var_eval);
+  p.n_active = o->n_active;
+  p.sum0 = Q(o->sum0);
+  p.sum1 = Q(o->sum1);
+  for (uint32_t i = 0; i < 4 * n_point; i++) {
+    p.p0.push_back(Q(o->p0_round_polys[i]));
+    p.lin.push_back(Q(o->lin_round_polys[i]));
+    p.lu.eq_polys.push_back(Q(o->logup_round_polys[i]));
+  }
+  p.p0_final0 = Q(o->p0_final0);
+  p.p0_final1 = Q(o->p0_final1);
+  p.lin_final0 = Q(o->lin_final0);
+  p.lin_final1 = Q(o->lin_final1);
+  p.cb_input = Q(o->cb_input);
+  p.cb_mean = Q(o->cb_mean);
+  p.lu.claimed_sum = Q(o->claimed_sum);
+  p.lu.w_eval = Q(o->w_eval);
+  p.lu.in_eval = Q(o->in_eval);
+  p.lu.out_eval = Q(o->out_eval);
+  p.lu.mults.assign(o->multiplicities, o->multiplicities + (1u << kNormTableLog));
+  for (uint32_t i = 0; i < 2 * kNormTableLog; i++) p.lu.mult_polys.push_back(Q(o->mult_round_polys[i]));
+  p.lu.mult_final = Q(o->mult_final_eval);
+  p.lu.mult_sum = Q(o->mult_claimed_sum);
+  if (!felt_abi_canonical(o->table_commitment)) return fail(GKR_ERR_INVALID, "table commitment not canonical");
+  p.lu.table_commitment = felt_canon_from_words(o->table_commitment.w);
+  if (o->n_rows > 1) {  // per-row statistics are part of the proof only for several rows
+    p.rows0.assign(o->row_stats0, o->row_stats0 + o->n_rows);
+    p.rows1.assign(o->row_stats1, o->row_stats1 + o->n_rows);
+  }
+  qm31 nv;
+  VerifyError e;
+  if (!verify_norm(ln, pt, Q(*claim_value), dim, p, rsqrt_table(), ch->ch, &nv, &e)) return verify_fail(e);
+  *next_value = G(nv);
+  return GKR_OK;
+}
+extern "C" int gkr_verify_layernorm_layer(const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                                          uint64_t dim, const gkr_norm_out* proof, gkr_channel* ch,
+                                          gkr_qm31* next_value) {
+  return verify_norm_abi(true, claim_point, n_point, claim_value, dim, proof, ch, next_value);
+}
+extern "C" int gkr_verify_rmsnorm_layer(const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                                        uint64_t dim, const gkr_norm_out* proof, gkr_channel* ch,
+                                        gkr_qm31* next_value) {
+  return verify_norm_abi(false, claim_point, n_point, claim_value, dim, proof, ch, next_value);
+}
+
 // A chained walk from serialize_gkr_model_proof calldata: every layer's
 // claim is the previous layer's input claim, starting from init_*.  Checks
 // the layer proofs and the input-claim section; the weight commitments,
@@ -135,7 +204,8 @@ extern "C" int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const g
     const uint64_t tag = R.u();
     if (!R.ok) return bad(R.why);
     if (L.claim == GKR_CLAIM_FRESH) {  // the prover's fresh-claim rule (gkr_prove_walk)
-      if (L.kind != GKR_STEP_MATMUL && L.kind != GKR_STEP_MUL && L.kind != GKR_STEP_ACTIVATION)
+      if (L.kind != GKR_STEP_MATMUL && L.kind != GKR_STEP_MUL && L.kind != GKR_STEP_ACTIVATION &&
+          L.kind != GKR_STEP_LAYERNORM && L.kind != GKR_STEP_RMSNORM)
         return fail(GKR_ERR_INVALID, "layer %zu: unknown kind %u", li, L.kind);
       const uint64_t out_cols = L.kind == GKR_STEP_MATMUL ? L.cols_b : L.cols;
       const int nv = v_log2(v_next_pow2(L.rows)) + v_log2(v_next_pow2(out_cols));
@@ -232,6 +302,66 @@ extern "C" int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const g
       if (nmr != tlog) return bad(at + "multiplicity sumcheck has " + std::to_string(nmr) + " rounds");
       if (!verify_activation(point, act, tlog, verifier_table(act, tlog), p, ch->ch, &value, &e, true))
         return bad(at + e.why);
+    } else if (L.kind == GKR_STEP_LAYERNORM) {
+      if (tag != 4) return bad(at + "expected a LayerNorm proof (tag 4), found tag " + std::to_string(tag));
+      NormProofIn p;
+      p.input_eval = R.q();
+      p.output_eval = R.q();
+      p.key_eval = R.q();
+      p.rsqrt_eval = R.q();
+      p.lu.table_commitment = R.f();
+      if (R.u(1) != 0) return bad(at + "SIMD-combined LayerNorm proofs are not supported");
+      if (R.u(1) != 1) return bad(at + "LayerNorm proof without the mean-variance part");
+      p.n_active = R.u(0xFFFFFFFFull);
+      p.sum0 = R.q();
+      p.sum1 = R.q();
+      auto rounds = [&](std::vector<qm31>* v) {
+        const uint64_t nr = R.u(64);
+        for (uint64_t t = 0; t < nr && R.ok; t++) {
+          const qm31 c0 = R.q(), c2 = R.q(), c3 = R.q();
+          v->insert(v->end(), {c0, qm31_zero(), c2, c3});
+        }
+      };
+      rounds(&p.p0);
+      p.p0_final0 = R.q();
+      p.p0_final1 = R.q();
+      rounds(&p.lin);
+      p.lin_final0 = R.q();
+      p.lin_final1 = R.q();
+      p.cb_input = R.q();
+      p.cb_mean = R.q();
+      if (R.u(1) != 1) return bad(at + "LayerNorm proof without the rsqrt LogUp");
+      p.lu.claimed_sum = R.q();
+      rounds(&p.lu.eq_polys);
+      p.lu.w_eval = R.q();
+      p.lu.in_eval = R.q();
+      p.lu.out_eval = R.q();
+      const uint64_t nm = R.u(1ull << 24);
+      for (uint64_t j = 0; j < nm && R.ok; j++) p.lu.mults.push_back((uint32_t)R.u(0xFFFFFFFFull));
+      if (R.u(1) != 1) return bad(at + "LayerNorm proof without the multiplicity sumcheck");
+      const uint64_t nmr = R.u(64);
+      for (uint64_t t = 0; t < nmr && R.ok; t++) {
+        p.lu.mult_polys.push_back(R.q());
+        p.lu.mult_polys.push_back(R.q());
+      }
+      p.lu.mult_final = R.q();
+      p.lu.mult_sum = R.q();
+      p.var_eval = R.q();
+      for (std::vector<uint32_t>* rv : {&p.rows0, &p.rows1})
+        if (R.u(1)) {
+          const uint64_t nr = R.u(1ull << 24);
+          for (uint64_t i = 0; i < nr && R.ok; i++) rv->push_back((uint32_t)R.u(P - 1));
+        }
+      if (!R.ok) return bad(at + R.why);
+      if (p.lin.size() / 4 != (uint64_t)v_log2(v_next_pow2(L.rows) * v_next_pow2(L.cols)))
+        return bad(at + "LayerNorm proof has " + std::to_string(p.lin.size() / 4) + " rounds for a " +
+                   std::to_string(L.rows) + " x " + std::to_string(L.cols) + " input");
+      if (nmr != kNormTableLog) return bad(at + "multiplicity sumcheck has " + std::to_string(nmr) + " rounds");
+      const uint64_t dim = L.dim ? L.dim : L.cols;
+      if (!verify_norm(true, point, value, dim, p, rsqrt_table(), ch->ch, &value, &e, true)) return bad(at + e.why);
+    } else if (L.kind == GKR_STEP_RMSNORM) {
+      return bad(at + "RMSNorm proofs cannot be replayed from serialize_gkr_model_proof calldata: the format omits "
+                      "their multiplicity sumcheck (cairo_serde.rs:1648-1720); use gkr_verify_rmsnorm_layer");
     } else {
       return fail(GKR_ERR_INVALID, "layer %zu: unknown kind %u", li, L.kind);
     }

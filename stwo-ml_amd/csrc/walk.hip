@@ -83,6 +83,43 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       TRY(gkr_prove_activation_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.activation_type, tl,
                                      ch, proof, &out));
       value = out.input_eval;  // the claim point is unchanged (prover.rs:6581-6584)
+    } else if (st.kind == GKR_STEP_LAYERNORM || st.kind == GKR_STEP_RMSNORM) {
+      const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
+      const uint64_t dim = st.dim ? st.dim : st.a->cols;
+      std::vector<uint32_t> gamma;
+      if (st.kind == GKR_STEP_RMSNORM && st.b) {  // the learned scale, one row
+        if (st.b->rows != 1) return fail(GKR_ERR_INVALID, "step %zu: gamma must be a 1 x n matrix", si);
+        gamma.resize(st.b->cols);
+        TRY(gkr_matrix_download(c, st.b, gamma.data()));
+      }
+      if (st.claim == GKR_CLAIM_FRESH) {
+        point.resize(nv);
+        {
+          HostTimer ht(c, K_HOST_DRAW);
+          TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
+        }
+        TRY(gkr_norm_output_claim(c, st.kind, st.a, dim, gamma.data(), gamma.size(), point.data(), nv, &value));
+        ch->ch.mix_secure_field(Q(value));
+      } else if (!have_claim) {
+        return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);
+      }
+      std::vector<gkr_qm31> p0(4 * nv), lin(4 * nv), lg(4 * nv), mrp(32);
+      std::vector<uint32_t> nm(1u << 16), r0(next_pow2(st.a->rows)), r1(next_pow2(st.a->rows));
+      gkr_norm_out out;
+      memset(&out, 0, sizeof out);
+      out.p0_round_polys = p0.data();
+      out.lin_round_polys = lin.data();
+      out.logup_round_polys = lg.data();
+      out.multiplicities = nm.data();
+      out.mult_round_polys = mrp.data();
+      out.row_stats0 = r0.data();
+      out.row_stats1 = r1.data();
+      if (st.kind == GKR_STEP_LAYERNORM)
+        TRY(gkr_prove_layernorm_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, dim, ch, proof, &out));
+      else
+        TRY(gkr_prove_rmsnorm_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, dim,
+                                    gamma.empty() ? nullptr : gamma.data(), gamma.size(), ch, proof, &out));
+      value = out.input_eval;  // the claim point is unchanged (prover.rs:8351-8354)
     } else {
       return fail(GKR_ERR_INVALID, "step %zu: unknown kind %u", si, st.kind);
     }

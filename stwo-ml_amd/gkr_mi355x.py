@@ -59,10 +59,32 @@ class GkrLogupOut(C.Structure):
 
 class GkrStep(C.Structure):
     _fields_ = [("kind", C.c_uint32), ("claim", C.c_uint32), ("a", C.c_void_p), ("b", C.c_void_p),
-                ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32)]
+                ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32), ("dim", C.c_uint64)]
 
 
-STEP_MATMUL, STEP_MUL, STEP_ACTIVATION = 0, 2, 3
+class GkrNormOut(C.Structure):
+    _fields_ = [("input_eval", GkrQM31), ("output_eval", GkrQM31), ("mean_eval", GkrQM31),
+                ("rsqrt_eval", GkrQM31), ("var_eval", GkrQM31), ("n_active", C.c_uint32), ("sum0", GkrQM31),
+                ("sum1", GkrQM31), ("p0_round_polys", C.POINTER(GkrQM31)), ("p0_final0", GkrQM31),
+                ("p0_final1", GkrQM31), ("lin_round_polys", C.POINTER(GkrQM31)), ("lin_final0", GkrQM31),
+                ("lin_final1", GkrQM31), ("cb_input", GkrQM31), ("cb_mean", GkrQM31), ("claimed_sum", GkrQM31),
+                ("logup_round_polys", C.POINTER(GkrQM31)), ("w_eval", GkrQM31), ("in_eval", GkrQM31),
+                ("out_eval", GkrQM31), ("multiplicities", C.POINTER(C.c_uint32)),
+                ("mult_round_polys", C.POINTER(GkrQM31)), ("mult_final_eval", GkrQM31),
+                ("mult_claimed_sum", GkrQM31), ("table_commitment", GkrFelt), ("n_rows", C.c_uint32),
+                ("row_stats0", C.POINTER(C.c_uint32)), ("row_stats1", C.POINTER(C.c_uint32)),
+                ("gamma_commitment", GkrFelt), ("gamma_eval", GkrQM31)]
+
+
+STEP_MATMUL, STEP_MUL, STEP_ACTIVATION, STEP_LAYERNORM, STEP_RMSNORM = 0, 2, 3, 4, 8
+NORM_TABLE_LOG = 16
+# norm proof dict keys holding one QM31 (the oracle's norm proof dicts use the same names)
+NORM_Q_KEYS = (("input_eval", "input_eval"), ("output_eval", "output_eval"), ("mean_eval", "mean_eval"),
+               ("rsqrt_eval", "rsqrt_eval"), ("var_eval", "var_eval"), ("sum0", "sum0"), ("sum1", "sum1"),
+               ("p0_final0", "p0_final0"), ("p0_final1", "p0_final1"), ("lin_final0", "lin_final0"),
+               ("lin_final1", "lin_final1"), ("cb_input", "cb_input"), ("cb_mean", "cb_mean"),
+               ("claimed_sum", "claimed_sum"), ("w_eval", "w_eval"), ("in_eval", "in_eval"), ("out_eval", "out_eval"),
+               ("mult_final_eval", "mult_final"), ("mult_claimed_sum", "mult_sum"), ("gamma_eval", "gamma_eval"))
 CLAIM_CHAINED, CLAIM_FRESH = 0, 1
 
 
@@ -72,7 +94,8 @@ def _next_pow2(v: int) -> int:
 
 class GkrLayerShape(C.Structure):
     _fields_ = [("kind", C.c_uint32), ("rows", C.c_uint64), ("cols", C.c_uint64), ("cols_b", C.c_uint64),
-                ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32), ("claim", C.c_uint32)]
+                ("activation_type", C.c_uint32), ("table_log_size", C.c_uint32), ("claim", C.c_uint32),
+                ("dim", C.c_uint64)]
 
 
 class GkrError(RuntimeError):
@@ -163,6 +186,12 @@ SIGNATURES = [
     ("gkr_verify_mul_layer", C.c_int, [_PQ, C.c_uint32, _PQ, _PQ, C.c_uint32, _PQ, _PQ, _P, _PQ]),
     ("gkr_verify_activation_layer", C.c_int, [_PQ, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
                                               C.POINTER(GkrLogupOut), _P, _PQ]),
+    ("gkr_prove_layernorm_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, C.c_uint64, _P, _P, C.POINTER(GkrNormOut)]),
+    ("gkr_prove_rmsnorm_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, C.c_uint64, _U32P, C.c_uint64, _P, _P,
+                                          C.POINTER(GkrNormOut)]),
+    ("gkr_norm_output_claim", C.c_int, [_P, C.c_uint32, _P, C.c_uint64, _U32P, C.c_uint64, _PQ, C.c_uint32, _PQ]),
+    ("gkr_verify_layernorm_layer", C.c_int, [_PQ, C.c_uint32, _PQ, C.c_uint64, C.POINTER(GkrNormOut), _P, _PQ]),
+    ("gkr_verify_rmsnorm_layer", C.c_int, [_PQ, C.c_uint32, _PQ, C.c_uint64, C.POINTER(GkrNormOut), _P, _PQ]),
     ("gkr_verify_walk", C.c_int, [C.POINTER(GkrFelt), C.c_size_t, C.POINTER(GkrLayerShape), C.c_size_t, _PQ,
                                   C.c_uint32, _PQ, _PQ, C.c_size_t, _P, _PQ, C.POINTER(C.c_uint32), _PQ,
                                   C.POINTER(C.c_size_t)]),
@@ -610,6 +639,31 @@ class Context:
                                           C.byref(out)))
         return q_from_c(out)
 
+    def prove_norm_layer(self, kind: int, claim_point, claim_value, inp: "Matrix", dim: int, ch: PoseidonChannel,
+                         gamma=None, proof: Optional["Proof"] = None) -> dict:
+        """gkr_prove_layernorm_layer (kind STEP_LAYERNORM) / gkr_prove_rmsnorm_layer (STEP_RMSNORM): a dict with
+        the oracle's norm proof keys."""
+        nv = len(claim_point)
+        o, keep = _norm_struct(nv, _next_pow2(inp.rows))
+        if kind == STEP_LAYERNORM:
+            _check(lib().gkr_prove_layernorm_layer(self._h, q_array(claim_point), nv, C.byref(q_to_c(claim_value)),
+                                                   inp.handle, dim, ch.handle, proof.handle if proof else None,
+                                                   C.byref(o)))
+        else:
+            g = np.ascontiguousarray(gamma if gamma is not None else np.zeros(1), dtype=np.uint32)
+            _check(lib().gkr_prove_rmsnorm_layer(self._h, q_array(claim_point), nv, C.byref(q_to_c(claim_value)),
+                                                 inp.handle, dim, g.ctypes.data_as(_U32P),
+                                                 0 if gamma is None else len(g), ch.handle,
+                                                 proof.handle if proof else None, C.byref(o)))
+        return _norm_dict(o, keep, nv)
+
+    def norm_output_claim(self, kind: int, inp: "Matrix", dim: int, point, gamma=None) -> QM31:
+        g = np.ascontiguousarray(gamma if gamma is not None else np.zeros(1), dtype=np.uint32)
+        v = GkrQM31()
+        _check(lib().gkr_norm_output_claim(self._h, kind, inp.handle, dim, g.ctypes.data_as(_U32P),
+                                           0 if gamma is None else len(g), q_array(point), len(point), C.byref(v)))
+        return q_from_c(v)
+
     def prove_activation_layer(self, claim_point, claim_value, inp: "Matrix", act_type: int, ch: PoseidonChannel,
                                table_log_size: int = 0, proof: Optional["Proof"] = None):
         if table_log_size == 0:
@@ -642,13 +696,15 @@ class Context:
 
 
 def make_steps(steps) -> "C.Array":
-    """steps: sequence of (kind, claim, a, b, activation_type, table_log_size) with Matrix objects."""
+    """steps: sequence of (kind, claim, a, b, activation_type, table_log_size[, dim]) with Matrix objects."""
     arr = (GkrStep * max(1, len(steps)))()
-    for i, (kind, claim, a, b, act, tlog) in enumerate(steps):
+    for i, st in enumerate(steps):
+        kind, claim, a, b, act, tlog = st[:6]
         arr[i].kind, arr[i].claim = kind, claim
         arr[i].a = a.handle if a is not None else None
         arr[i].b = b.handle if b is not None else None
         arr[i].activation_type, arr[i].table_log_size = act, tlog
+        arr[i].dim = st[6] if len(st) > 6 else 0
     return arr
 
 
@@ -722,6 +778,58 @@ def verify_activation_layer(claim_point, act_type: int, table_log_size: int, pro
     return q_from_c(nv)
 
 
+def _norm_struct(nv: int, prow: int):
+    keep = {"p0": (GkrQM31 * max(1, 4 * nv))(), "lin": (GkrQM31 * max(1, 4 * nv))(),
+            "lg": (GkrQM31 * max(1, 4 * nv))(), "mult": np.zeros(1 << NORM_TABLE_LOG, dtype=np.uint32),
+            "mrp": (GkrQM31 * (2 * NORM_TABLE_LOG))(), "rs0": np.zeros(max(1, prow), dtype=np.uint32),
+            "rs1": np.zeros(max(1, prow), dtype=np.uint32)}
+    o = GkrNormOut()
+    o.p0_round_polys, o.lin_round_polys = C.cast(keep["p0"], C.POINTER(GkrQM31)), C.cast(keep["lin"], C.POINTER(GkrQM31))
+    o.logup_round_polys = C.cast(keep["lg"], C.POINTER(GkrQM31))
+    o.multiplicities = keep["mult"].ctypes.data_as(_U32P)
+    o.mult_round_polys = C.cast(keep["mrp"], C.POINTER(GkrQM31))
+    o.row_stats0, o.row_stats1 = keep["rs0"].ctypes.data_as(_U32P), keep["rs1"].ctypes.data_as(_U32P)
+    return o, keep
+
+
+def _norm_dict(o: GkrNormOut, keep, nv: int) -> dict:
+    d = {dk: q_from_c(getattr(o, ck)) for ck, dk in NORM_Q_KEYS}
+    for key, arr in (("p0_round_polys", "p0"), ("lin_round_polys", "lin"), ("logup_round_polys", "lg")):
+        d[key] = [tuple(q_from_c(keep[arr][4 * t + j]) for j in range(4)) for t in range(nv)]
+    d["multiplicities"] = keep["mult"].copy()
+    d["mult_round_polys"] = [(q_from_c(keep["mrp"][2 * t]), q_from_c(keep["mrp"][2 * t + 1]))
+                             for t in range(NORM_TABLE_LOG)]
+    d["table_commitment"] = felt_from_c(o.table_commitment)
+    d["gamma_commitment"] = felt_from_c(o.gamma_commitment)
+    d["n_active"], d["n_rows"] = int(o.n_active), int(o.n_rows)
+    d["row_stats0"] = [int(x) for x in keep["rs0"][:o.n_rows]]
+    d["row_stats1"] = [int(x) for x in keep["rs1"][:o.n_rows]]
+    return d
+
+
+def verify_norm_layer(kind: int, claim_point, claim_value, dim: int, proof: dict, ch: PoseidonChannel) -> QM31:
+    """gkr_verify_layernorm_layer / gkr_verify_rmsnorm_layer on a norm proof dict; returns the input claim value."""
+    nv = len(claim_point)
+    o, keep = _norm_struct(nv, max(1, proof["n_rows"]))
+    for ck, dk in NORM_Q_KEYS:
+        setattr(o, ck, q_to_c(proof[dk]))
+    for key, arr in (("p0_round_polys", "p0"), ("lin_round_polys", "lin"), ("logup_round_polys", "lg")):
+        for t, rp in enumerate(proof[key]):
+            for j in range(4):
+                keep[arr][4 * t + j] = q_to_c(rp[j])
+    keep["mult"][:] = proof["multiplicities"]
+    for t, (c0, c1) in enumerate(proof["mult_round_polys"]):
+        keep["mrp"][2 * t], keep["mrp"][2 * t + 1] = q_to_c(c0), q_to_c(c1)
+    keep["rs0"][:len(proof["row_stats0"])] = proof["row_stats0"]
+    keep["rs1"][:len(proof["row_stats1"])] = proof["row_stats1"]
+    o.table_commitment = felt_to_c(proof["table_commitment"])
+    o.n_active, o.n_rows = proof["n_active"], proof["n_rows"]
+    nx = GkrQM31()
+    f = lib().gkr_verify_layernorm_layer if kind == STEP_LAYERNORM else lib().gkr_verify_rmsnorm_layer
+    _check(f(q_array(claim_point), nv, C.byref(q_to_c(claim_value)), dim, C.byref(o), ch.handle, C.byref(nx)))
+    return q_from_c(nx)
+
+
 def felts_to_words(felts) -> np.ndarray:
     """felt252 ints -> (n, 8) little-endian u32 words."""
     out = np.zeros((len(felts), 8), dtype=np.uint32)
@@ -751,6 +859,7 @@ def verify_walk(calldata, shapes, init_point, init_value, ch: PoseidonChannel, f
         sh[i].kind, sh[i].rows, sh[i].cols, sh[i].cols_b = kind, rows, cols, cols_b
         sh[i].activation_type, sh[i].table_log_size = act, tlog
         sh[i].claim = shp[6] if len(shp) > 6 else CLAIM_CHAINED
+        sh[i].dim = shp[7] if len(shp) > 7 else 0
     fp = (GkrQM31 * 64)()
     nf = C.c_uint32()
     fv = GkrQM31()
