@@ -35,7 +35,7 @@ METRIC = "GKR matmul-sumcheck Melem/s + % HBM peak; proved tokens/s, Qwen2.5-14B
 HBM_PEAK_GBS = 8000.0
 P = (1 << 31) - 1  # M31
 (K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT,
- K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH) = range(13)
+ K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH, K_NORM) = range(14)
 
 QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
 SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
@@ -462,6 +462,92 @@ def bench_simd(ctx, args, blocks=8):
     ctx.close()
 
 
+def bench_norm(ctx, args):
+    """The two RMSNorm layers of one Qwen2.5-14B block (input and post-attention: 64 tokens x 5120,
+    learned per-column scale), each with a fresh output claim on one channel through
+    gkr_prove_walk (reduce_rmsnorm_layer_with_gamma, prover.rs:8407-8801); a LayerNorm layer of the
+    same shape (reduce_layernorm_layer, prover.rs:7944-8395) is timed beside it.  int8-range
+    synthetic activations resident in HBM."""
+    import numpy as np
+    m, h = QWEN["tokens"], QWEN["hidden"]
+    xs = [ctx.synthetic(m, h, 1, 700 + i) for i in range(2)]
+    gv = [np.random.default_rng(7 + i).integers(1, 1 << 12, size=(1, h), dtype=np.uint32) for i in range(2)]
+    gam = [ctx.upload(g) for g in gv]
+    steps = G.make_steps([(G.STEP_RMSNORM, G.CLAIM_FRESH, xs[i], gam[i], 0, 0, h) for i in range(2)])
+    ln_steps = G.make_steps([(G.STEP_LAYERNORM, G.CLAIM_FRESH, xs[0], None, 0, 0, h)])
+
+    def run(arr, n):
+        ch = G.PoseidonChannel()
+        ch.mix_u64(m)
+        proof = G.Proof()
+        G.prove_walk(ctx, ch, arr, proof, n_steps=n)
+        return ch.digest()
+
+    for _ in range(max(1, args.warmup)):
+        run(steps, 2)
+    ctx.set_timing(0 if args.no_timing else 2 if args.timing_all else 1)
+    ctx.reset_timing()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    outs = [run(steps, 2) for _ in range(args.steps)]
+    ctx.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    assert all(o == outs[0] for o in outs), "non-deterministic proof"
+    ms, nl, nb = ctx.kernel_time(K_NORM)
+    kernels = {}
+    for kid, name in [(K_NORM, "norm_rows+prepare"), (K_MM_ROUND, "product_trips"), (K_EQ3_ROUND, "eq3_trips"),
+                      (K_EQ_TABLE, "eq_tables")]:
+        km, kn, kb = ctx.kernel_time(kid)
+        if kn:
+            kernels[name] = {"launches": kn // args.steps, "avg_us": round(km / kn * 1e3, 3),
+                             "ms_per_step": round(km / args.steps, 3)}
+    host = {}
+    for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait"), (K_HOST_WAIT_TAIL, "device_wait_handover"),
+                      (K_HOST_DRAW, "claim_draws"), (K_HOST_LAUNCH, "launch_calls"), (K_HOST_FINISH, "host_finish")]:
+        hm, hn, _ = ctx.kernel_time(kid)
+        if hn:
+            host[name] = {"ms_per_step": round(hm / args.steps, 3), "calls": hn // args.steps}
+    roofline = None
+    if nl:
+        gbps = nb / (ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbps / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_norm_rows + k_norm_prepare",
+                    "avg_launch_us": round(ms / nl * 1e3, 3), "bytes_per_launch": nb // nl}
+    ctx.set_timing(0)
+    run(ln_steps, 1)
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    ln = [run(ln_steps, 1) for _ in range(args.steps)]
+    ctx.synchronize()
+    ln_ms = (time.perf_counter() - t1) / args.steps * 1e3
+    assert all(x == ln[0] for x in ln), "non-deterministic proof"
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        X = O.synthetic(m, h, 1, 700)
+        g = gv[0].reshape(-1)
+        ch = O.Channel()
+        r = ch.draw_qm31s(lg(m) + lg(h))
+        t2 = time.perf_counter()
+        O.prove_rmsnorm_layer(r, (1, 2, 3, 4), X, h, ch, g)
+        dtc = time.perf_counter() - t2
+        cpu = {"value": round(m * h / dtc / 1e6, 4), "unit": "Melem/s", "cores": 1, "kind": "port",
+               "sample": f"one RMSNorm layer {m}x{h} by the oracle (reference CPU algorithm, one core): {dtc:.2f} s"}
+    result = {
+        "metric": "GKR RMSNorm layer proving, normalized Melem/s", "value": round(2 * m * h / dt / 1e6, 2),
+        "unit": "Melem/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u32-m31", "data": "synthetic (counter-mode SplitMix64, int8-range activations, 12-bit scales)",
+        "config": {"workload": "qwen2.5-14b-block-rmsnorms-64-tokens", "layers": 2, "shape": [m, h]},
+        "roofline": roofline, "kernels": kernels, "host": host, "layernorm_ms_per_layer": round(ln_ms, 3),
+        "digest": hex(outs[0]),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def trip_k(n, big=1 << 16, huge=1 << 20):
     """Rounds per device trip over a vector of n entries (the library's trip_k)."""
     return 1 if n > huge else 2 if n > big else 3
@@ -551,7 +637,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="qwen48",
-                    choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward", "simd"])
+                    choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward", "simd", "norm"])
     ap.add_argument("--c2-logs", default="20,24,28",
                     help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -580,6 +666,8 @@ def main():
         return bench_forward(ctx, args)
     if args.config == "simd":
         return bench_simd(ctx, args)
+    if args.config == "norm":
+        return bench_norm(ctx, args)
     sbuf = SerialBuffer()
     if args.config == "cfg1":
         cfg, n_layers = None, 1

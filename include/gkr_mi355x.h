@@ -103,8 +103,10 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * (wall-clock, bytes = 0); 9 Merkle level kernel of the commitments, whose
  * "bytes" count Poseidon hashes instead; 10 host: claim-point draws in the
  * walk, 11 host: time inside kernel-launch calls of the reducers, 12 host:
- * the host-finish rounds' arithmetic (wall-clock, bytes = 0).              */
-/* level 0: off; 1: events on k_restrict_cols and the Merkle level kernel,
+ * the host-finish rounds' arithmetic (wall-clock, bytes = 0); 13 the norm
+ * layers' row statistics and padded-vector kernels (device). */
+/* level 0: off; 1: events on k_restrict_cols, the Merkle level kernel and
+ * the norm kernels,
  * plus the host timers; 2: events on every timed kernel (adds an event pair
  * per launch). */
 int gkr_ctx_set_timing(gkr_ctx* ctx, int level);
@@ -385,7 +387,9 @@ int gkr_mul_output_claim(gkr_ctx* ctx, const gkr_matrix* lhs, const gkr_matrix* 
  * in sum0, its Part 0 final input in p0_final0, (input, scale) finals in
  * lin_final0/1 and the per-row rms^2 in row_stats0; var_eval, sum1,
  * p0_final1, cb_input, cb_mean and row_stats1 are LayerNorm's only, and
- * gamma_commitment / gamma_eval RMSNorm's (not mixed, not serialized). */
+ * gamma_commitment / gamma_eval RMSNorm's (not mixed, not serialized;
+ * gkr_prove_walk does not compute the commitment, a chain of one Poseidon
+ * mix per scale entry). */
 typedef struct {
   gkr_qm31 input_eval, output_eval, mean_eval, rsqrt_eval, var_eval;
   uint32_t n_active;

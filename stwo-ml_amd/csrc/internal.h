@@ -85,7 +85,7 @@ enum Slot {
 // hand-over of the last vectors).
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
                 K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
-                K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NKERNELS = 13 };
+                K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NORM = 13, K_NKERNELS = 14 };
 constexpr int kMaxPartialBlocks = 1024;
 constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
 // Result slots in the coherent host area (h_out): 0 .. 63 serve the result in
@@ -218,7 +218,8 @@ struct TimedLaunch {
   uint64_t bytes;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
-    if (c->timing >= 2 || (c->timing == 1 && (kid == K_RESTRICT_COLS || kid == K_RESTRICT_ROWS || kid == K_MERKLE))) {
+    if (c->timing >= 2 || (c->timing == 1 && (kid == K_RESTRICT_COLS || kid == K_RESTRICT_ROWS || kid == K_MERKLE ||
+                                              kid == K_NORM))) {
       e0 = get_event(c);
       e1 = get_event(c);
       if (e0) (void)hipEventRecord(e0, c->stream);
@@ -569,5 +570,11 @@ int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, cons
 int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& pl, qm31* w0, qm31* d0,
                         qm31* w1, qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3],
                         const RoundSink* pre0 = nullptr);
+// LayerNorm (ln) or RMSNorm layer reducer (norm.hip); commit_gamma: fill
+// gamma_commitment (one Poseidon mix per scale entry; the walk, which neither
+// mixes nor serializes it, skips it).
+int prove_norm(gkr_ctx* c, bool ln, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+               const gkr_matrix* X, uint64_t dim, const uint32_t* gamma, uint64_t ng, gkr_channel* ch,
+               gkr_proof* proof, gkr_norm_out* out, bool commit_gamma);
 // Activation table outputs (host copy, cached per context).
 const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint32_t log_size);

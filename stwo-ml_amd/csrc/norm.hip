@@ -133,8 +133,11 @@ int norm_stats(gkr_ctx* c, const gkr_matrix* X, bool ln, uint64_t dim, NormShape
   uint32_t* d_sums;
   TRY(ensureT(c, S_NORMSUM, 4 * X->rows, &d_sums));
   const uint64_t act_real = S->active < X->cols ? S->active : X->cols;
-  hipLaunchKernelGGL(k_norm_rows, dim3((unsigned)X->rows), dim3(kBlock), 0, c->stream, X->dev, X->cols, act_real,
-                     d_sums);
+  {
+    TimedLaunch tl(c, K_NORM, 4 * X->rows * X->cols + 16 * X->rows);
+    hipLaunchKernelGGL(k_norm_rows, dim3((unsigned)X->rows), dim3(kBlock), 0, c->stream, X->dev, X->cols, act_real,
+                       d_sums);
+  }
   TRY(check_launch());
   HIP_TRY(hipMemcpyAsync(sums.data(), d_sums, sums.size() * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
   TRY(sync(c));
@@ -194,9 +197,12 @@ int norm_prepare(gkr_ctx* c, const gkr_matrix* X, const NormShape& S, const uint
   HIP_TRY(hipMemcpyAsync(d_rowv, rowv.data(), rowv.size() * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
   if (d_gamma)
     HIP_TRY(hipMemcpyAsync(d_gamma, gamma, ng * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
-  hipLaunchKernelGGL(k_norm_prepare, dim3(grid_for(S.n)), dim3(kBlock), 0, c->stream, X->dev, S.rows, S.cols,
-                     log2_exact(S.pcol), S.n, S.ln ? 1 : 0, S.active, d_rowv, d_gamma, d_gamma ? ng : 0, w, d,
-                     in_q, in_u, out_u);
+  {  // reads X once; writes w, d (and the LayerNorm input) as QM31, input and output as u32
+    TimedLaunch tl(c, K_NORM, 4 * S.rows * S.cols + (S.ln ? 56 : 40) * S.n);
+    hipLaunchKernelGGL(k_norm_prepare, dim3(grid_for(S.n)), dim3(kBlock), 0, c->stream, X->dev, S.rows, S.cols,
+                       log2_exact(S.pcol), S.n, S.ln ? 1 : 0, S.active, d_rowv, d_gamma, d_gamma ? ng : 0, w, d,
+                       in_q, in_u, out_u);
+  }
   TRY(check_launch());
   // the host copies of rowv / gamma must outlive the copies
   return sync(c);
@@ -507,11 +513,13 @@ void record_norm(gkr_proof* proof, bool ln, const qm31& claim, const NormShape& 
   proof->layers.push_back(std::move(L));
 }
 
+}  // namespace
+
 // Both reducers: ln selects LayerNorm (prover.rs:7944-8395) or RMSNorm
 // (8407-8801, with the optional per-column gamma).
 int prove_norm(gkr_ctx* c, bool ln, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
                const gkr_matrix* X, uint64_t dim, const uint32_t* gamma, uint64_t ng, gkr_channel* ch,
-               gkr_proof* proof, gkr_norm_out* out) {
+               gkr_proof* proof, gkr_norm_out* out, bool commit_gamma) {
   CH_CHECK(ch);
   std::vector<qm31> z;
   TRY(norm_check(c, claim_point, n_point, claim_value, X, out, &z));
@@ -538,10 +546,12 @@ int prove_norm(gkr_ctx* c, bool ln, const gkr_qm31* claim_point, uint32_t n_poin
   out->gamma_commitment = felt_to_abi(felt_zero());
   out->gamma_eval = G(qm31_zero());
   if (!ln && gamma && ng) {  // gamma commitment and evaluation (prover.rs:8758-8781), neither mixed nor serialized
-    PoseidonChannel g;
-    g.mix_u64(kNormTagGamma);
-    for (uint64_t i = 0; i < ng; i++) g.mix_secure_field(qm31_from_m31(gamma[i]));
-    out->gamma_commitment = felt_to_abi(g.digest);
+    if (commit_gamma) {
+      PoseidonChannel g;
+      g.mix_u64(kNormTagGamma);
+      for (uint64_t i = 0; i < ng; i++) g.mix_secure_field(qm31_from_m31(gamma[i]));
+      out->gamma_commitment = felt_to_abi(g.digest);
+    }
     std::vector<qm31> gcol(S.pcol);
     for (uint64_t col = 0; col < S.pcol; col++) gcol[col] = col < ng ? qm31_from_m31(gamma[col]) : qm31_one();
     // MLE at z of gamma broadcast over rows: the row variables sum to one
@@ -636,18 +646,16 @@ int prove_norm(gkr_ctx* c, bool ln, const gkr_qm31* claim_point, uint32_t n_poin
   return GKR_OK;
 }
 
-}  // namespace
-
 extern "C" int gkr_prove_layernorm_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
                                          const gkr_qm31* claim_value, const gkr_matrix* input, uint64_t dim,
                                          gkr_channel* ch, gkr_proof* proof, gkr_norm_out* out) {
-  return prove_norm(c, true, claim_point, n_point, claim_value, input, dim, nullptr, 0, ch, proof, out);
+  return prove_norm(c, true, claim_point, n_point, claim_value, input, dim, nullptr, 0, ch, proof, out, false);
 }
 extern "C" int gkr_prove_rmsnorm_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
                                        const gkr_qm31* claim_value, const gkr_matrix* input, uint64_t dim,
                                        const uint32_t* gamma, uint64_t n_gamma, gkr_channel* ch, gkr_proof* proof,
                                        gkr_norm_out* out) {
-  return prove_norm(c, false, claim_point, n_point, claim_value, input, dim, gamma, n_gamma, ch, proof, out);
+  return prove_norm(c, false, claim_point, n_point, claim_value, input, dim, gamma, n_gamma, ch, proof, out, true);
 }
 
 // The layer output's MLE at `point` (the value a fresh claim on the layer takes).

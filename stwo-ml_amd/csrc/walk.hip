@@ -114,11 +114,8 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       out.mult_round_polys = mrp.data();
       out.row_stats0 = r0.data();
       out.row_stats1 = r1.data();
-      if (st.kind == GKR_STEP_LAYERNORM)
-        TRY(gkr_prove_layernorm_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, dim, ch, proof, &out));
-      else
-        TRY(gkr_prove_rmsnorm_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, dim,
-                                    gamma.empty() ? nullptr : gamma.data(), gamma.size(), ch, proof, &out));
+      TRY(prove_norm(c, st.kind == GKR_STEP_LAYERNORM, point.data(), (uint32_t)point.size(), &value, st.a, dim,
+                     gamma.empty() ? nullptr : gamma.data(), gamma.size(), ch, proof, &out, false));
       value = out.input_eval;  // the claim point is unchanged (prover.rs:8351-8354)
     } else {
       return fail(GKR_ERR_INVALID, "step %zu: unknown kind %u", si, st.kind);
