@@ -163,4 +163,30 @@ int orc_verify_rmsnorm_layer(const uint32_t* claim_point, int nv, const uint32_t
 #ifdef __cplusplus
 }
 #endif
+
+/* STWO LogUp-GKR / grand-product batch (lookup_gkr.c).  kind: 0 grand
+ * product (den = the column), 1 LogUp generic (num QM31), 2 LogUp with M31
+ * multiplicities (num u32), 3 LogUp singles (numerators 1). */
+typedef struct {
+  uint32_t kind, n_vars;
+  const uint32_t* num;
+  const uint32_t* den;
+} orc_lookup_layer;
+/* Dense proof layout: output_claims / claims_to_verify 2 QM31 per instance;
+ * round_polys 4 QM31 per round (layers 0.. n_layers-1, `layer` rounds each)
+ * with round_poly_lens the coefficient counts; masks 4 QM31 per (layer,
+ * instance), zero where the instance is not active; ood_point n_layers QM31. */
+typedef struct {
+  uint32_t* output_claims;
+  uint32_t* round_polys;
+  uint32_t* round_poly_lens;
+  uint32_t* masks;
+  uint32_t* ood_point;
+  uint32_t* claims_to_verify;
+  uint32_t n_layers;
+} orc_lookup_out;
+int orc_prove_lookup_batch(orc_channel* ch, const orc_lookup_layer* inst, size_t n_inst, orc_lookup_out* out);
+int orc_verify_lookup_batch(const uint32_t* gates, const uint32_t* n_vars, size_t n_inst, const orc_lookup_out* p,
+                            orc_channel* ch, uint32_t* ood_out, uint32_t* claims_out);
+
 #endif

@@ -993,3 +993,170 @@ def serialize_rmsnorm_layer(out: list, proof: dict) -> None:
         out.extend(proof["row_stats0"])
     else:
         out.append(0)
+
+
+# ------------------------------------------------------------------ STWO LogUp-GKR batch (lookup_gkr.c)
+LOOKUP_GRAND_PRODUCT, LOOKUP_LOGUP_GENERIC, LOOKUP_LOGUP_MULTIPLICITIES, LOOKUP_LOGUP_SINGLES = 0, 1, 2, 3
+
+
+class LookupLayer(C.Structure):
+    """orc_lookup_layer (oracle.h)."""
+    _fields_ = [("kind", C.c_uint32), ("n_vars", C.c_uint32), ("num", _U32P), ("den", _U32P)]
+
+
+class LookupOut(C.Structure):
+    """orc_lookup_out (oracle.h)."""
+    _fields_ = [("output_claims", _U32P), ("round_polys", _U32P), ("round_poly_lens", _U32P), ("masks", _U32P),
+                ("ood_point", _U32P), ("claims_to_verify", _U32P), ("n_layers", C.c_uint32)]
+
+
+def _lookup_lib():
+    L = lib()
+    if not getattr(L, "_lookup_ready", False):
+        L.orc_prove_lookup_batch.argtypes = [C.c_void_p, C.POINTER(LookupLayer), C.c_size_t, C.POINTER(LookupOut)]
+        L.orc_verify_lookup_batch.argtypes = [_U32P, _U32P, C.c_size_t, C.POINTER(LookupOut), C.c_void_p, _U32P,
+                                              _U32P]
+        L._lookup_ready = True
+    return L
+
+
+def lookup_gate(kind: int) -> int:
+    """Gate of an instance: 0 grand product, 1 LogUp."""
+    return 0 if kind == LOOKUP_GRAND_PRODUCT else 1
+
+
+def _lookup_bufs(n_inst: int, n_layers: int):
+    n_rounds = max(1, n_layers * (n_layers - 1) // 2)
+    return {"oc": np.zeros(8 * n_inst, dtype=np.uint32), "rp": np.zeros(16 * n_rounds, dtype=np.uint32),
+            "rl": np.zeros(n_rounds, dtype=np.uint32), "mk": np.zeros(16 * max(1, n_layers) * n_inst, dtype=np.uint32),
+            "ood": np.zeros(4 * max(1, n_layers), dtype=np.uint32), "cv": np.zeros(8 * n_inst, dtype=np.uint32)}
+
+
+def _lookup_struct(b) -> "LookupOut":
+    o = LookupOut()
+    o.output_claims, o.round_polys, o.round_poly_lens = _p(b["oc"]), _p(b["rp"]), _p(b["rl"])
+    o.masks, o.ood_point, o.claims_to_verify = _p(b["mk"]), _p(b["ood"]), _p(b["cv"])
+    return o
+
+
+def prove_lookup_batch(ch: "Channel", instances) -> dict:
+    """prove_batch (stwo-gpu/crates/stwo/src/prover/lookups/gkr_prover.rs:396-500).  instances:
+    (kind, numerators, denominators) with numerators a QM31 (n, 4) array (generic), an M31 (n,)
+    array (multiplicities) or None, denominators a QM31 (n, 4) array (grand product: the column)."""
+    arrs, layers = [], (LookupLayer * len(instances))()
+    n_layers = 0
+    for i, (kind, num, den) in enumerate(instances):
+        den = _qa(den)
+        nv = max(0, (len(den) - 1).bit_length())
+        n_layers = max(n_layers, nv)
+        layers[i].kind, layers[i].n_vars, layers[i].den = kind, nv, _p(den)
+        arrs.append(den)
+        if kind == LOOKUP_LOGUP_GENERIC:
+            nq = _qa(num)
+            layers[i].num = _p(nq)
+            arrs.append(nq)
+        elif kind == LOOKUP_LOGUP_MULTIPLICITIES:
+            nm = np.ascontiguousarray(num, dtype=np.uint32)
+            layers[i].num = _p(nm)
+            arrs.append(nm)
+    b = _lookup_bufs(len(instances), n_layers)
+    o = _lookup_struct(b)
+    rc = _lookup_lib().orc_prove_lookup_batch(ch.buf, layers, len(instances), C.byref(o))
+    if rc:
+        raise ValueError(f"oracle prove_lookup_batch failed ({rc})")
+    kinds = [k for k, _, _ in instances]
+    nvs = [layers[i].n_vars for i in range(len(instances))]
+    return _lookup_dict(b, kinds, nvs, n_layers)
+
+
+def _lookup_dict(b, kinds, nvs, n_layers) -> dict:
+    """The dense proof arrays as a dict: output_claims[i] and claims_to_verify[i] (1 or 2 QM31),
+    round_polys[layer] (coefficient lists, leading zeros dropped), masks[layer][i] (2 values per
+    column; None before instance i joins), ood_point."""
+    n_inst = len(kinds)
+    ncl = [1 if k == LOOKUP_GRAND_PRODUCT else 2 for k in kinds]
+    q = lambda a, i: tuple(int(x) for x in a[4 * i:4 * i + 4])  # noqa: E731
+    d = {"kinds": list(kinds), "n_vars": list(nvs), "n_layers": n_layers,
+         "output_claims": [[q(b["oc"], 2 * i + c) for c in range(ncl[i])] for i in range(n_inst)],
+         "claims_to_verify": [[q(b["cv"], 2 * i + c) for c in range(ncl[i])] for i in range(n_inst)],
+         "ood_point": [q(b["ood"], k) for k in range(n_layers)], "round_polys": [], "masks": []}
+    r = 0
+    for layer in range(n_layers):
+        polys = []
+        for _ in range(layer):
+            polys.append([q(b["rp"], 4 * r + c) for c in range(int(b["rl"][r]))])
+            r += 1
+        d["round_polys"].append(polys)
+    for layer in range(n_layers):
+        d["masks"].append([[q(b["mk"], 4 * (layer * n_inst + i) + c) for c in range(2 * ncl[i])]
+                           if layer >= n_layers - nvs[i] else None for i in range(n_inst)])
+    return d
+
+
+def _lookup_arrays(d) -> dict:
+    n_inst, n_layers = len(d["kinds"]), d["n_layers"]
+    b = _lookup_bufs(n_inst, n_layers)
+    for i in range(n_inst):
+        for c, v in enumerate(d["output_claims"][i]):
+            b["oc"][8 * i + 4 * c:8 * i + 4 * c + 4] = v
+    r = 0
+    for layer in range(n_layers):
+        for poly in d["round_polys"][layer]:
+            b["rl"][r] = len(poly)
+            for c, v in enumerate(poly):
+                b["rp"][16 * r + 4 * c:16 * r + 4 * c + 4] = v
+            r += 1
+        for i in range(n_inst):
+            m = d["masks"][layer][i]
+            if m is not None:
+                for c, v in enumerate(m):
+                    b["mk"][16 * (layer * n_inst + i) + 4 * c:16 * (layer * n_inst + i) + 4 * c + 4] = v
+    return b
+
+
+def verify_lookup_batch(d: dict, ch: "Channel"):
+    """partially_verify_batch (gkr_verifier.rs:17-157) on a proof dict.  Returns (status,
+    ood_point, claims_to_verify); status 0 = accepted."""
+    b = _lookup_arrays(d)
+    o = _lookup_struct(b)
+    o.n_layers = d["n_layers"]
+    gates = np.array([lookup_gate(k) for k in d["kinds"]], dtype=np.uint32)
+    nvs = np.array(d["n_vars"], dtype=np.uint32)
+    ood = np.zeros(4 * max(1, d["n_layers"]), dtype=np.uint32)
+    cv = np.zeros(8 * len(gates), dtype=np.uint32)
+    rc = _lookup_lib().orc_verify_lookup_batch(_p(gates), _p(nvs), len(gates), C.byref(o), ch.buf, _p(ood), _p(cv))
+    ncl = [1 if g == 0 else 2 for g in gates]
+    return (int(rc), [_q(ood, k) for k in range(d["n_layers"])],
+            [[_q(cv, 2 * i + c) for c in range(ncl[i])] for i in range(len(gates))])
+
+
+def serialize_lookup_batch(out: list, d: dict) -> None:
+    """serialize_stwo_gkr_batch_proof (engine/src/cairo_serde.rs:3330-3420)."""
+    n_inst = len(d["kinds"])
+    out.append(n_inst)
+    for i in range(n_inst):
+        out.append(lookup_gate(d["kinds"][i]))
+        out.append(d["n_vars"][i])
+        out.append(len(d["output_claims"][i]))
+        for v in d["output_claims"][i]:
+            _ser_q(out, v)
+    out.append(d["n_layers"])
+    for layer in range(d["n_layers"]):
+        polys = d["round_polys"][layer]
+        out.append(len(polys))
+        for poly in polys:
+            for c in range(4):
+                _ser_q(out, poly[c] if c < len(poly) else (0, 0, 0, 0))
+            out.append(len(poly))
+        # masks: layer_masks_by_instance[i][layer], the instance's own layer index (cairo_serde.rs:3403-3416):
+        # instances of different sizes would index past their masks, so the reference only serializes
+        # batches of one size
+        out.append(n_inst)
+        for i in range(n_inst):
+            if d["n_vars"][i] != d["n_layers"]:
+                raise ValueError("serialize_stwo_gkr_batch_proof indexes masks by layer: instances must share n_vars")
+            m = d["masks"][layer][i]
+            out.append(len(m))
+            for v in m:
+                _ser_q(out, v)
+            out.append(len(m) // 2)
