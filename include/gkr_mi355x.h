@@ -425,6 +425,64 @@ int gkr_prove_rmsnorm_layer(gkr_ctx* ctx, const gkr_qm31* claim_point, uint32_t 
 int gkr_norm_output_claim(gkr_ctx* ctx, uint32_t kind, const gkr_matrix* input, uint64_t dim, const uint32_t* gamma,
                           uint64_t n_gamma, const gkr_qm31* point, uint32_t n_point, gkr_qm31* value);
 
+/* ------------------------------------------------------------------ STWO LogUp-GKR batch
+ * prove_batch (stwo-gpu/crates/stwo/src/prover/lookups/gkr_prover.rs:396-500)
+ * over device columns, with the Poseidon252 channel (the engine calls it from
+ * prove_logup_gkr, engine/src/aggregation.rs:3926-4062, after drawing the
+ * LogUp alpha).  An instance is one binary-tree circuit over 2^n_vars
+ * entries: GKR_LOOKUP_GRAND_PRODUCT (`denominators` holds the column),
+ * _LOGUP_GENERIC (QM31 numerators), _LOGUP_MULTIPLICITIES (u32 M31
+ * numerators; n_vars >= 2) or _LOGUP_SINGLES (numerators 1).  Columns are
+ * device pointers in the reference's Mle order (first variable on the most
+ * significant bit of the index).  n_layers = the largest n_vars; the caller
+ * provides output_claims and claims_to_verify (2 QM31 per instance; a grand
+ * product uses the first), round_polys (4 QM31 per round, n_layers *
+ * (n_layers - 1) / 2 rounds: layer 0's, then layer 1's ...), round_poly_lens
+ * (one per round: the coefficients the reference keeps, leading zeros
+ * dropped), masks (4 QM31 per (layer, instance): instance i of layer l at
+ * 4 * (l * n_instances + i), LogUp: num(0), num(1), den(0), den(1), grand
+ * product: the two values; zero before the instance joins) and ood_point
+ * (n_layers).  The claims are the artifact's claims_to_verify_by_instance:
+ * the input columns at the last n_vars coordinates of ood_point. */
+enum {
+  GKR_LOOKUP_GRAND_PRODUCT = 0,
+  GKR_LOOKUP_LOGUP_GENERIC = 1,
+  GKR_LOOKUP_LOGUP_MULTIPLICITIES = 2,
+  GKR_LOOKUP_LOGUP_SINGLES = 3
+};
+typedef struct {
+  uint32_t kind;
+  uint32_t n_vars;
+  const void* numerators;         /* device: gkr_qm31 (generic) or uint32_t (multiplicities); else NULL */
+  const gkr_qm31* denominators;   /* device */
+} gkr_lookup_instance;
+typedef struct {
+  gkr_qm31* output_claims;
+  gkr_qm31* round_polys;
+  uint32_t* round_poly_lens;
+  gkr_qm31* masks;
+  gkr_qm31* ood_point;
+  gkr_qm31* claims_to_verify;
+  uint32_t n_layers;
+} gkr_lookup_batch;
+int gkr_prove_lookup_batch(gkr_ctx* ctx, gkr_channel* ch, const gkr_lookup_instance* instances, size_t n_instances,
+                           gkr_lookup_batch* out);
+/* partially_verify_batch (stwo-gpu/crates/stwo/src/prover/lookups/gkr_verifier.rs:17-157),
+ * host only.  gates: 0 grand product, 1 LogUp, per instance; proof as
+ * gkr_prove_lookup_batch writes it (n_layers set).  Returns the artifact's
+ * OOD point (n_layers) and claims (2 per instance), or GKR_ERR_VERIFY. */
+int gkr_verify_lookup_batch(const uint32_t* gates, const uint32_t* n_vars, size_t n_instances,
+                            const gkr_lookup_batch* proof, gkr_channel* ch, gkr_qm31* ood_point,
+                            gkr_qm31* claims_to_verify);
+/* serialize_stwo_gkr_batch_proof (engine/src/cairo_serde.rs:3330-3420).  It
+ * indexes each instance's masks by the global layer, so every instance must
+ * have n_vars = n_layers (GKR_ERR_INVALID otherwise).  *n_felts receives the
+ * full length (GKR_ERR_BUFFER when cap is short). */
+int gkr_serialize_lookup_batch(const uint32_t* gates, const uint32_t* n_vars, size_t n_instances,
+                               const gkr_lookup_batch* proof, gkr_felt* out, size_t cap, size_t* n_felts);
+/* Device address of a matrix's u32 entries (row-major), e.g. multiplicities for a lookup instance. */
+const uint32_t* gkr_matrix_device_ptr(const gkr_matrix* m);
+
 /* GKR walk over a sequence of layers (the layer loop of prove_gkr_with_cache,
  * gkr/prover.rs:1500-1660, for MatMul, Mul, Activation, LayerNorm and RMSNorm
  * layers).  Steps run in order on one channel and append their LayerProof to

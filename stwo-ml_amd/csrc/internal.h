@@ -78,14 +78,16 @@ inline bool felt_abi_canonical(const gkr_felt& f) {
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW, S_NSLOTS
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW,
+  S_LKARENA, S_LKFOLD, S_LKDESC, S_LKPART, S_LKRES, S_LKTAB, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and host-side phases (Fiat-Shamir
 // hashing inside the reducers, waiting for trip results, waiting for the
 // hand-over of the last vectors).
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
                 K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
-                K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NORM = 13, K_NKERNELS = 14 };
+                K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NORM = 13, K_LOOKUP = 14,
+                K_NKERNELS = 15 };
 constexpr int kMaxPartialBlocks = 1024;
 constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
 // Result slots in the coherent host area (h_out): 0 .. 63 serve the result in
@@ -143,8 +145,13 @@ struct gkr_qvec {
   uint64_t n;
 };
 
+// Pinned host staging buffers (grow-only, hipHostMalloc).
+enum HostSlot { H_LKDESC, H_LKRES, H_LKTAB, H_NSLOTS };
+
 struct gkr_ctx {
   int device = 0;
+  void* hbuf[H_NSLOTS] = {};
+  size_t hcap[H_NSLOTS] = {};
   hipStream_t stream = nullptr;
   void* buf[S_NSLOTS] = {};
   size_t cap[S_NSLOTS] = {};
@@ -219,7 +226,7 @@ struct TimedLaunch {
   hipEvent_t e0 = nullptr, e1 = nullptr;
   TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
     if (c->timing >= 2 || (c->timing == 1 && (kid == K_RESTRICT_COLS || kid == K_RESTRICT_ROWS || kid == K_MERKLE ||
-                                              kid == K_NORM))) {
+                                              kid == K_NORM || kid == K_LOOKUP))) {
       e0 = get_event(c);
       e1 = get_event(c);
       if (e0) (void)hipEventRecord(e0, c->stream);

@@ -350,6 +350,8 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   if (c->merkle_consts) (void)hipFree(c->merkle_consts);
   if (c->h_res) (void)hipHostFree(c->h_res);
   if (c->h_mult) (void)hipHostFree(c->h_mult);
+  for (int s = 0; s < H_NSLOTS; s++)
+    if (c->hbuf[s]) (void)hipHostFree(c->hbuf[s]);
   if (c->h_vec) (void)hipHostFree(c->h_vec);
   if (c->h_out) (void)hipHostFree(c->h_out);
   if (c->stream) (void)hipStreamDestroy(c->stream);

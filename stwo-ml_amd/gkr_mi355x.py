@@ -175,6 +175,11 @@ SIGNATURES = [
     ("gkr_qvec_download", C.c_int, [_P, _P, _PQ]),
     ("gkr_qvec_free", None, [_P]),
     ("gkr_qvec_device_ptr", _P, [_P]),
+    ("gkr_matrix_device_ptr", _P, [_P]),
+    ("gkr_prove_lookup_batch", C.c_int, [_P, _P, _P, C.c_size_t, _P]),
+    ("gkr_verify_lookup_batch", C.c_int, [_U32P, _U32P, C.c_size_t, _P, _P, _PQ, _PQ]),
+    ("gkr_serialize_lookup_batch", C.c_int, [_U32P, _U32P, C.c_size_t, _P, _PF, C.c_size_t,
+                                             C.POINTER(C.c_size_t)]),
     ("gkr_sumcheck_product", C.c_int, [_P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ]),
     ("gkr_sumcheck_product_noalloc", C.c_int, [_P, _PQ, _PQ, C.c_uint64, _P, _PQ, _PQ, _PQ, _PQ]),
     ("gkr_prove_mul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, C.POINTER(GkrMulOut)]),
@@ -877,6 +882,11 @@ class Matrix:
         self.ctx, self._h, self.rows, self.cols = ctx, handle, rows, cols
 
     @property
+    def device_ptr(self) -> int:
+        """Device address of the row-major u32 entries (gkr_matrix_device_ptr)."""
+        return lib().gkr_matrix_device_ptr(self._h)
+
+    @property
     def handle(self) -> int:
         return self._h
 
@@ -984,3 +994,119 @@ def activation_table(act_type: int, log_size: int) -> np.ndarray:
 
 def synthetic_value(kind: int, seed: int, i: int) -> int:
     return int(lib().gkr_synthetic_value(kind, seed, i))
+
+
+# ------------------------------------------------------------------ STWO LogUp-GKR batch
+LOOKUP_GRAND_PRODUCT, LOOKUP_LOGUP_GENERIC, LOOKUP_LOGUP_MULTIPLICITIES, LOOKUP_LOGUP_SINGLES = 0, 1, 2, 3
+
+
+class GkrLookupInstance(C.Structure):
+    _fields_ = [("kind", C.c_uint32), ("n_vars", C.c_uint32), ("numerators", C.c_void_p),
+                ("denominators", C.c_void_p)]
+
+
+class GkrLookupBatch(C.Structure):
+    _fields_ = [("output_claims", _PQ), ("round_polys", _PQ), ("round_poly_lens", _U32P), ("masks", _PQ),
+                ("ood_point", _PQ), ("claims_to_verify", _PQ), ("n_layers", C.c_uint32)]
+
+
+def _lookup_buffers(n_inst: int, n_layers: int):
+    n_rounds = max(1, n_layers * (n_layers - 1) // 2)
+    keep = {"oc": (GkrQM31 * (2 * n_inst))(), "rp": (GkrQM31 * (4 * n_rounds))(),
+            "rl": np.zeros(n_rounds, dtype=np.uint32), "mk": (GkrQM31 * (4 * max(1, n_layers) * n_inst))(),
+            "ood": (GkrQM31 * max(1, n_layers))(), "cv": (GkrQM31 * (2 * n_inst))()}
+    b = GkrLookupBatch()
+    b.output_claims, b.round_polys = C.cast(keep["oc"], _PQ), C.cast(keep["rp"], _PQ)
+    b.round_poly_lens = keep["rl"].ctypes.data_as(_U32P)
+    b.masks, b.ood_point, b.claims_to_verify = C.cast(keep["mk"], _PQ), C.cast(keep["ood"], _PQ), C.cast(keep["cv"], _PQ)
+    return b, keep
+
+
+def lookup_gate(kind: int) -> int:
+    return 0 if kind == LOOKUP_GRAND_PRODUCT else 1
+
+
+def _lookup_result(keep, kinds, nvs, n_layers) -> dict:
+    """The proof as a dict with the oracle's keys (oracle.prove_lookup_batch)."""
+    n_inst = len(kinds)
+    ncl = [1 if k == LOOKUP_GRAND_PRODUCT else 2 for k in kinds]
+    d = {"kinds": list(kinds), "n_vars": list(nvs), "n_layers": n_layers,
+         "output_claims": [[q_from_c(keep["oc"][2 * i + c]) for c in range(ncl[i])] for i in range(n_inst)],
+         "claims_to_verify": [[q_from_c(keep["cv"][2 * i + c]) for c in range(ncl[i])] for i in range(n_inst)],
+         "ood_point": [q_from_c(keep["ood"][k]) for k in range(n_layers)], "round_polys": [], "masks": []}
+    r = 0
+    for layer in range(n_layers):
+        polys = []
+        for _ in range(layer):
+            polys.append([q_from_c(keep["rp"][4 * r + c]) for c in range(int(keep["rl"][r]))])
+            r += 1
+        d["round_polys"].append(polys)
+    for layer in range(n_layers):
+        d["masks"].append([[q_from_c(keep["mk"][4 * (layer * n_inst + i) + c]) for c in range(2 * ncl[i])]
+                           if layer >= n_layers - nvs[i] else None for i in range(n_inst)])
+    return d
+
+
+def prove_lookup_batch(ctx: "Context", ch: PoseidonChannel, instances) -> dict:
+    """gkr_prove_lookup_batch.  instances: (kind, n_vars, numerators, denominators) with device
+    columns given as QVec / Matrix objects or device addresses (None where the kind has none)."""
+    arr = (GkrLookupInstance * max(1, len(instances)))()
+    n_layers = 0
+    ptr = lambda v: None if v is None else (v if isinstance(v, int) else v.device_ptr)  # noqa: E731
+    for i, (kind, nv, num, den) in enumerate(instances):
+        arr[i].kind, arr[i].n_vars = kind, nv
+        arr[i].numerators, arr[i].denominators = ptr(num), ptr(den)
+        n_layers = max(n_layers, nv)
+    b, keep = _lookup_buffers(len(instances), n_layers)
+    _check(lib().gkr_prove_lookup_batch(ctx.handle, ch.handle, arr, len(instances), C.byref(b)))
+    return _lookup_result(keep, [x[0] for x in instances], [x[1] for x in instances], n_layers)
+
+
+def _lookup_fill(d):
+    n_inst, n_layers = len(d["kinds"]), d["n_layers"]
+    b, keep = _lookup_buffers(n_inst, n_layers)
+    b.n_layers = n_layers
+    for i in range(n_inst):
+        for c, v in enumerate(d["output_claims"][i]):
+            keep["oc"][2 * i + c] = q_to_c(v)
+    r = 0
+    for layer in range(n_layers):
+        for poly in d["round_polys"][layer]:
+            keep["rl"][r] = len(poly)
+            for c, v in enumerate(poly):
+                keep["rp"][4 * r + c] = q_to_c(v)
+            r += 1
+        for i in range(n_inst):
+            m = d["masks"][layer][i]
+            if m is not None:
+                for c, v in enumerate(m):
+                    keep["mk"][4 * (layer * n_inst + i) + c] = q_to_c(v)
+    gates = np.array([lookup_gate(k) for k in d["kinds"]], dtype=np.uint32)
+    nvs = np.array(d["n_vars"], dtype=np.uint32)
+    return b, keep, gates, nvs
+
+
+def verify_lookup_batch(d: dict, ch: PoseidonChannel):
+    """gkr_verify_lookup_batch on a proof dict; returns (ood_point, claims_to_verify)."""
+    b, keep, gates, nvs = _lookup_fill(d)
+    ood = (GkrQM31 * max(1, d["n_layers"]))()
+    cv = (GkrQM31 * (2 * len(gates)))()
+    _check(lib().gkr_verify_lookup_batch(gates.ctypes.data_as(_U32P), nvs.ctypes.data_as(_U32P), len(gates),
+                                         C.byref(b), ch.handle, ood, cv))
+    ncl = [1 if g == 0 else 2 for g in gates]
+    return ([q_from_c(ood[k]) for k in range(d["n_layers"])],
+            [[q_from_c(cv[2 * i + c]) for c in range(ncl[i])] for i in range(len(gates))])
+
+
+def serialize_lookup_batch(d: dict) -> List[int]:
+    """gkr_serialize_lookup_batch (serialize_stwo_gkr_batch_proof) as felt ints."""
+    b, keep, gates, nvs = _lookup_fill(d)
+    n = C.c_size_t()
+    rc = lib().gkr_serialize_lookup_batch(gates.ctypes.data_as(_U32P), nvs.ctypes.data_as(_U32P), len(gates),
+                                          C.byref(b), None, 0, C.byref(n))
+    if rc not in (0, 5):
+        _check(rc)
+    out = (GkrFelt * max(1, n.value))()
+    _check(lib().gkr_serialize_lookup_batch(gates.ctypes.data_as(_U32P), nvs.ctypes.data_as(_U32P), len(gates),
+                                            C.byref(b), out, n.value, C.byref(n)))
+    return [felt_from_c(out[i]) for i in range(n.value)]
