@@ -35,7 +35,7 @@ METRIC = "GKR matmul-sumcheck Melem/s + % HBM peak; proved tokens/s, Qwen2.5-14B
 HBM_PEAK_GBS = 8000.0
 P = (1 << 31) - 1  # M31
 (K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT,
- K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH, K_NORM) = range(14)
+ K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH, K_NORM, K_LOOKUP) = range(15)
 
 QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
 SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
@@ -548,6 +548,82 @@ def bench_norm(ctx, args):
     ctx.close()
 
 
+def bench_lookup(ctx, args, n_inst=96, log_n=16):
+    """STWO LogUp-GKR batch (prove_batch, stwo-gpu/crates/stwo/src/prover/lookups/gkr_prover.rs:396-500) as
+    prove_logup_gkr (engine/src/aggregation.rs:3926-4062) builds it for a Qwen2.5-14B model: one
+    LogUpMultiplicities instance per activation table of the 48 layers (SiLU and softmax-exp, 2^16 entries
+    each): numerators the table's multiplicities, denominators alpha - table input.  Synthetic tables and
+    counts resident in HBM; a step is one batch proof on a fresh channel."""
+    import numpy as np
+    n = 1 << log_n
+    rng = np.random.default_rng(11)
+    alpha = [int(x) for x in rng.integers(0, P, size=4)]
+    host = []
+    for i in range(n_inst):
+        mult = rng.integers(0, 8, size=n, dtype=np.uint32)
+        tin = rng.integers(0, P, size=n, dtype=np.uint64)
+        den = np.empty((n, 4), dtype=np.uint32)
+        den[:, 0] = (alpha[0] + P - tin) % P
+        den[:, 1:] = alpha[1:]
+        host.append((mult, den))
+    dev = [(G.LOOKUP_LOGUP_MULTIPLICITIES, log_n, ctx.upload(m.reshape(1, -1)), ctx.qvec_upload(d)) for m, d in host]
+
+    def step():
+        ch = G.PoseidonChannel()
+        ch.mix_u64(n_inst)
+        G.prove_lookup_batch(ctx, ch, dev)
+        return ch.digest()
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    ctx.set_timing(0 if args.no_timing else 2 if args.timing_all else 1)
+    ctx.reset_timing()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    outs = [step() for _ in range(args.steps)]
+    ctx.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    assert all(o == outs[0] for o in outs), "non-deterministic proof"
+    ms, nl, nb = ctx.kernel_time(K_LOOKUP)
+    hostt = {}
+    for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait"), (K_HOST_LAUNCH, "launch_calls")]:
+        hm, hn, _ = ctx.kernel_time(kid)
+        if hn:
+            hostt[name] = {"ms_per_step": round(hm / args.steps, 3), "calls": hn // args.steps}
+    roofline = None
+    if nl:
+        gbps = nb / (ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(gbps / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_lk_tree + k_lk_round",
+                    "avg_launch_us": round(ms / nl * 1e3, 3), "bytes_per_launch": nb // nl,
+                    "launches_per_step": nl // args.steps, "device_ms_per_step": round(ms / args.steps, 3)}
+    ctx.set_timing(0)
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+        k = 8
+        sample = [(O.LOOKUP_LOGUP_MULTIPLICITIES, m, d) for m, d in host[:k]]
+        ch = O.Channel()
+        ch.mix_u64(k)
+        t1 = time.perf_counter()
+        O.prove_lookup_batch(ch, sample)
+        dtc = time.perf_counter() - t1
+        cpu = {"value": round(k * n / dtc / 1e6, 3), "unit": "Mentries/s", "cores": 1, "kind": "port",
+               "sample": f"{k} of the {n_inst} instances by the oracle (reference CPU algorithm, one core): {dtc:.2f} s"}
+    result = {
+        "metric": "STWO LogUp-GKR batch proving, table entries/s", "value": round(n_inst * n / dt / 1e6, 2),
+        "unit": "Mentries/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u32-m31/qm31", "data": "synthetic (uniform table inputs, multiplicities 0..7)",
+        "config": {"workload": f"qwen2.5-14b-logup-gkr-{n_inst}-tables-2^{log_n}", "instances": n_inst,
+                   "log_size": log_n},
+        "roofline": roofline, "host": hostt, "digest": hex(outs[0]), "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def trip_k(n, big=1 << 16, huge=1 << 20):
     """Rounds per device trip over a vector of n entries (the library's trip_k)."""
     return 1 if n > huge else 2 if n > big else 3
@@ -637,7 +713,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="qwen48",
-                    choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward", "simd", "norm"])
+                    choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward", "simd", "norm", "lookup"])
     ap.add_argument("--c2-logs", default="20,24,28",
                     help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -668,6 +744,8 @@ def main():
         return bench_simd(ctx, args)
     if args.config == "norm":
         return bench_norm(ctx, args)
+    if args.config == "lookup":
+        return bench_lookup(ctx, args)
     sbuf = SerialBuffer()
     if args.config == "cfg1":
         cfg, n_layers = None, 1

@@ -270,25 +270,39 @@ struct Poly {
   }
 };
 
-// The unique polynomial of degree <= 3 through (xs[i], ys[i]) (Lagrange form expanded).
-Poly interpolate4(const qm31 xs[4], const qm31 ys[4]) {
+// The round polynomial of correct_sum_as_poly_in_first_variable
+// (gkr_prover.rs:518-566) is the unique cubic r with r(0), r(1), r(2) given and
+// r(b) = 0, b = (1 - y) / (1 - 2 y) the root of eq(t, y).  Written as
+// r(t) = (t - b) q(t) with q the quadratic through q(k) = r(k) / (k - b),
+// k = 0, 1, 2; the reciprocals depend only on y, so instances of one size
+// share them within a round.
+struct RootInv {
+  qm31 y, b, i0, i1, i2;  // i_k = 1 / (k - b)
+  bool valid = false;
+};
+RootInv root_inv(const qm31& y) {
+  RootInv r;
+  r.y = y;
+  r.b = qm31_mul(qm31_sub(qm31_one(), y), qm31_inv(qm31_sub(qm31_one(), qm31_add(y, y))));
+  const qm31 d0 = qm31_neg(r.b), d1 = qm31_sub(qm31_one(), r.b), d2 = qm31_sub(qm31_from_m31(2), r.b);
+  const qm31 p01 = qm31_mul(d0, d1), inv = qm31_inv(qm31_mul(p01, d2)), t = qm31_mul(inv, d2);
+  r.i2 = qm31_mul(inv, p01);
+  r.i1 = qm31_mul(t, d0);
+  r.i0 = qm31_mul(t, d1);
+  r.valid = true;
+  return r;
+}
+Poly cubic_with_root(const qm31& r0, const qm31& r1, const qm31& r2, const RootInv& ri) {
+  const qm31 inv2 = qm31_from_m31(1u << 30);
+  const qm31 q0 = qm31_mul(r0, ri.i0), q1 = qm31_mul(r1, ri.i1), q2 = qm31_mul(r2, ri.i2);
+  const qm31 a2 = qm31_mul(qm31_add(qm31_sub(q2, qm31_add(q1, q1)), q0), inv2);  // q = a0 + a1 t + a2 t^2
+  const qm31 a1 = qm31_sub(qm31_sub(q1, q0), a2), a0 = q0;
   Poly p;
-  for (int k = 0; k < 4; k++) p.c[k] = qm31_zero();
+  p.c[0] = qm31_neg(qm31_mul(ri.b, a0));
+  p.c[1] = qm31_sub(a0, qm31_mul(ri.b, a1));
+  p.c[2] = qm31_sub(a1, qm31_mul(ri.b, a2));
+  p.c[3] = a2;
   p.len = 4;
-  for (int i = 0; i < 4; i++) {
-    qm31 den = qm31_one();
-    for (int j = 0; j < 4; j++)
-      if (j != i) den = qm31_mul(den, qm31_sub(xs[i], xs[j]));
-    qm31 t[4] = {qm31_mul(ys[i], qm31_inv(den)), qm31_zero(), qm31_zero(), qm31_zero()};
-    int deg = 0;
-    for (int j = 0; j < 4; j++) {
-      if (j == i) continue;
-      for (int k = deg + 1; k >= 1; k--) t[k] = qm31_sub(t[k - 1], qm31_mul(xs[j], t[k]));
-      t[0] = qm31_neg(qm31_mul(xs[j], t[0]));
-      deg++;
-    }
-    for (int k = 0; k < 4; k++) p.c[k] = qm31_add(p.c[k], t[k]);
-  }
   p.trunc();
   return p;
 }
@@ -643,6 +657,7 @@ extern "C" int gkr_prove_lookup_batch(gkr_ctx* c, gkr_channel* ch, const gkr_loo
           TRY(sync(c));
         }
         const qm31* rv = static_cast<const qm31*>(hr);
+        RootInv roots[kLkMaxVars + 2];
         for (size_t a = 0; a < real.size(); a++) {
           const size_t i = real[a];
           const qm31* s = rv + (size_t)kLkRes * a;
@@ -652,10 +667,8 @@ extern "C" int gkr_prove_lookup_batch(gkr_ctx* c, gkr_channel* ch, const gkr_loo
           const qm31 yc = ood[layer - m + 1];
           const qm31 r0 = qm31_mul(qm31_mul(S0, corr[i]), eq1(qm31_zero(), yc));
           const qm31 r2 = qm31_mul(qm31_mul(S2, corr[i]), eq1(two, yc));
-          const qm31 bx = qm31_mul(qm31_sub(qm31_one(), yc), qm31_inv(qm31_sub(qm31_one(), qm31_add(yc, yc))));
-          const qm31 xs[4] = {qm31_zero(), qm31_one(), two, bx};
-          const qm31 ys[4] = {r0, qm31_sub(sc[i], r0), r2, qm31_zero()};
-          polys[i] = interpolate4(xs, ys);
+          if (!roots[m].valid) roots[m] = root_inv(yc);
+          polys[i] = cubic_with_root(r0, qm31_sub(sc[i], r0), r2, roots[m]);
           if (m == 2)
             for (int q = 0; q < 8; q++) snap[8 * i + q] = s[4 + q];
         }
