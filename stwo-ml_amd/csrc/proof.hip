@@ -1,5 +1,8 @@
 // Proof container and serialize_gkr_model_proof (engine/src/cairo_serde.rs).
 #include "internal.h"
+
+#include <algorithm>
+#include <thread>
 // ------------------------------------------------------------------ proof container
 extern "C" int gkr_proof_new(gkr_proof** out) {
   if (!out) return fail(GKR_ERR_INVALID, "null out");
@@ -33,8 +36,9 @@ extern "C" int gkr_proof_set_io_commitment(gkr_proof* p, const gkr_felt* cm) {
 }
 
 // serialize_gkr_model_proof (cairo_serde.rs:1307-1772); felts kept canonical.
-// Two passes over the proof: the first counts, the second writes straight
-// into the caller's buffer (no intermediate copy of the felt stream).
+// A counting pass (constant time per layer: runs of u32 values are counted,
+// not visited) gives every layer's offset; the layers are then written
+// straight into the caller's buffer by several threads.
 struct Ser {
   gkr_felt* out;  // nullptr: count only
   size_t n = 0;
@@ -46,6 +50,15 @@ struct Ser {
       for (int i = 2; i < 8; i++) f.w[i] = 0;
     }
     n++;
+  }
+  void us(const uint32_t* v, size_t count) {  // count felts of u32 values
+    if (out)
+      for (size_t i = 0; i < count; i++) {
+        gkr_felt& f = out[n + i];
+        f.w[0] = v[i];
+        for (int k = 1; k < 8; k++) f.w[k] = 0;
+      }
+    n += count;
   }
   void q(const qm31& x) { u(x.a); u(x.b); u(x.c); u(x.d); }
   void f(const felt& canon) {
@@ -97,7 +110,7 @@ static void serialize_norm(const LayerRec& L, Ser& s) {
   s.q(N.in_eval);
   s.q(N.out_eval);
   s.u(N.mults.size());
-  for (uint32_t m : N.mults) s.u(m);
+  s.us(N.mults.data(), N.mults.size());
   const bool multi_row = N.rows0.size() > 1;
   if (ln) {
     s.u(1);  // serialize_multiplicity_sumcheck (cairo_serde.rs:1138-1156)
@@ -110,20 +123,19 @@ static void serialize_norm(const LayerRec& L, Ser& s) {
       s.u(multi_row ? 1 : 0);
       if (multi_row) {
         s.u(rv->size());
-        for (uint32_t v : *rv) s.u(v);
+        s.us(rv->data(), rv->size());
       }
     }
   } else {
     s.u(multi_row ? 1 : 0);
     if (multi_row) {
       s.u(N.rows0.size());
-      for (uint32_t v : N.rows0) s.u(v);
+      s.us(N.rows0.data(), N.rows0.size());
     }
   }
 }
-static void serialize_proof(const gkr_proof* p, Ser& s) {
-  s.u(p->layers.size());
-  for (const LayerRec& L : p->layers) {
+static void serialize_layer(const LayerRec& L, Ser& s) {
+  {
     if (L.tag == 0) {
       s.u(0);
       const size_t nr = L.rp.size() / 3;
@@ -181,7 +193,7 @@ static void serialize_proof(const gkr_proof* p, Ser& s) {
       s.q(L.in_eval);
       s.q(L.out_eval);
       s.u(L.mults.size());
-      for (uint32_t m : L.mults) s.u(m);
+      s.us(L.mults.data(), L.mults.size());
       // serialize_multiplicity_sumcheck (cairo_serde.rs:1138-1156)
       s.u(1);
       const size_t nm = L.mult_rp.size() / 2;
@@ -196,6 +208,8 @@ static void serialize_proof(const gkr_proof* p, Ser& s) {
       s.u(0);  // no piecewise proof
     }
   }
+}
+static void serialize_tail(const gkr_proof* p, Ser& s) {
   s.u(p->in_point.size());
   for (const qm31& x : p->in_point) s.q(x);
   s.q(p->in_value);
@@ -208,12 +222,49 @@ static void serialize_proof(const gkr_proof* p, Ser& s) {
 }
 extern "C" int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out) {
   if (!p || !n_out || (!out && cap)) return fail(GKR_ERR_INVALID, "null argument");
-  Ser count{nullptr};
-  serialize_proof(p, count);
-  *n_out = count.n;
-  if (cap < count.n) return fail(GKR_ERR_BUFFER, "need %zu felts, have %zu", count.n, cap);
-  Ser write{out};
-  serialize_proof(p, write);
+  const size_t nl = p->layers.size();
+  std::vector<size_t> off(nl + 1);
+  off[0] = 1;  // the layer count
+  for (size_t l = 0; l < nl; l++) {
+    Ser count{nullptr};
+    serialize_layer(p->layers[l], count);
+    off[l + 1] = off[l] + count.n;
+  }
+  Ser tail_count{nullptr};
+  serialize_tail(p, tail_count);
+  *n_out = off[nl] + tail_count.n;
+  if (cap < *n_out) return fail(GKR_ERR_BUFFER, "need %zu felts, have %zu", *n_out, cap);
+  Ser head{out};
+  head.u(nl);
+  // layers in contiguous chunks of about equal felt counts, one per thread
+  const size_t total = off[nl] - off[0];
+  const unsigned hw = std::thread::hardware_concurrency();
+  const size_t nt = std::min<size_t>({(size_t)(hw ? hw : 1), (size_t)8, nl ? nl : 1, total / (1u << 16) + 1});
+  auto write_range = [&](size_t l0, size_t l1) {
+    for (size_t l = l0; l < l1; l++) {
+      Ser w{out};
+      w.n = off[l];
+      serialize_layer(p->layers[l], w);
+    }
+  };
+  if (nt <= 1) {
+    write_range(0, nl);
+  } else {
+    std::vector<std::thread> th;
+    size_t l0 = 0;
+    for (size_t t = 0; t < nt && l0 < nl; t++) {
+      const size_t target = off[0] + total * (t + 1) / nt;
+      size_t l1 = l0;
+      while (l1 < nl && (off[l1 + 1] <= target || l1 == l0)) l1++;
+      if (t + 1 == nt) l1 = nl;
+      th.emplace_back(write_range, l0, l1);
+      l0 = l1;
+    }
+    for (auto& x : th) x.join();
+  }
+  Ser tail{out};
+  tail.n = off[nl];
+  serialize_tail(p, tail);
   return GKR_OK;
 }
 
