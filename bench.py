@@ -227,6 +227,103 @@ def cpu_baseline(budget_s=25.0):
                       f"{dt:.2f} s"}
 
 
+def oracle_host_layer(O, cfg, layer, seed_base=0):
+    """Host copies of LayerWeights(ctx, cfg, layer, seed_base): the same generator and seeds."""
+    h, i, q, kv, m = cfg["hidden"], cfg["inter"], cfg["q"], cfg["kv"], cfg["tokens"]
+    s = seed_base + 1000 * layer
+    xq, xo, xg, xd = (O.synthetic(m, h, 1, s + 1), O.synthetic(m, q, 1, s + 5), O.synthetic(m, h, 1, s + 7),
+                      O.synthetic(m, i, 1, s + 10))
+    mats = {"q": (xq, O.synthetic(h, q, 1, s + 2)), "k": (xq, O.synthetic(h, kv, 1, s + 3)),
+            "v": (xq, O.synthetic(h, kv, 1, s + 4)), "o": (xo, O.synthetic(q, h, 1, s + 6)),
+            "gate": (xg, O.synthetic(h, i, 1, s + 8)), "up": (xg, O.synthetic(h, i, 1, s + 9)),
+            "down": (xd, O.synthetic(i, h, 1, s + 11))}
+    silu = O.synthetic(m, i, 0, s + 12)
+    scores = O.synthetic(cfg["heads"] * m, m, 0, s + 13) if m > 1 else None
+    return mats, silu, scores
+
+
+def oracle_layer(O, och, cfg, layer, out, seed_base=0):
+    """The per-layer sequence of model_steps on the oracle (the reference's CPU algorithm): fresh
+    claims, q k v o gate up matmuls, SiLU LogUp (2^16), down, softmax-exp LogUp (2^16); the serialized
+    felts are appended to out."""
+    mats, silu, scores = oracle_host_layer(O, cfg, layer, seed_base)
+
+    def matmul(A, B):
+        r = och.draw_qm31s(lg(A.shape[0]) + lg(B.shape[1]))
+        v = O.matmul_output_claim(A, B, r)
+        och.mix_secure_field(v)
+        o = O.prove_matmul_layer(r, v, A, B, och)
+        O.serialize_matmul_layer(out, o["round_polys"], o["final_a_eval"], o["final_b_eval"])
+
+    def logup(X, tag):
+        r = och.draw_qm31s(lg(X.shape[0]) + lg(X.shape[1]))
+        v = och.draw_qm31()
+        o = O.prove_activation_layer(r, v, X, tag, och, 16)
+        O.serialize_activation_layer(out, tag, o)
+
+    for name in ("q", "k", "v", "o", "gate", "up"):
+        matmul(*mats[name])
+    logup(silu, 5)
+    matmul(*mats["down"])
+    if scores is not None:
+        logup(scores, 4)
+
+
+def host_info():
+    """CPU model, threads and the oracle's compiler, for the CPU baseline records."""
+    import platform
+    import subprocess
+    model = platform.processor()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        cc = subprocess.run(["gcc", "--version"], capture_output=True, text=True, timeout=10).stdout.splitlines()[0]
+    except (OSError, IndexError, subprocess.SubprocessError):
+        cc = None
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    return {"cpu_model": model, "nproc": os.cpu_count(), "omp_threads": threads, "oracle_compiler": cc}
+
+
+def cpu_configs():
+    """The oracle (reference CPU algorithm) on whole configurations: config 1 (256^3 uniform matmul),
+    config 3 (the 30-layer SmolLM2 walk, 1 token) and config 4 (one Qwen2.5-14B layer, 64 tokens: 7
+    matmuls, the SiLU and softmax-exp LogUps), each the workload the GPU bench times for that config."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    res = {"host": host_info()}
+    t0 = time.perf_counter()
+    A, B = O.synthetic(256, 256, 0, 0), O.synthetic(256, 256, 0, 1)
+    ch = O.Channel()
+    r = ch.draw_qm31s(16)
+    v = O.matmul_output_claim(A, B, r)
+    ch.mix_secure_field(v)
+    O.prove_matmul_layer(r, v, A, B, ch)
+    res["cfg1"] = {"s_per_proof": round(time.perf_counter() - t0, 4)}
+    log("[cpu] config 1 done")
+    t0 = time.perf_counter()
+    och = O.Channel()
+    out = [0]
+    for layer in range(30):
+        oracle_layer(O, och, SMOL, layer, out)
+    res["smollm"] = {"s_per_proof": round(time.perf_counter() - t0, 3), "tokens": 1}
+    log("[cpu] config 3 done")
+    t0 = time.perf_counter()
+    och = O.Channel()
+    out = [0]
+    oracle_layer(O, och, QWEN, 0, out)
+    dt = time.perf_counter() - t0
+    res["qwen1"] = {"s_per_layer": round(dt, 3), "tokens": QWEN["tokens"],
+                    "qwen48_extrapolated_s": round(48 * dt, 1)}
+    log("[cpu] config 4 done")
+    return res
+
+
 WEIGHT_NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
 
@@ -717,6 +814,8 @@ def main():
     ap.add_argument("--c2-logs", default="20,24,28",
                     help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="time the oracle (reference CPU algorithm) on configs 1, 3 and 4 and print one JSON line")
     ap.add_argument("--no-timing", action="store_true", help="no HIP events and no host timers")
     ap.add_argument("--timing-all", action="store_true",
                     help="HIP events on every timed kernel (default: only the roofline kernel k_restrict_cols)")
@@ -731,6 +830,9 @@ def main():
               "(the path is measured on one GPU's share)", file=sys.stderr)
         sys.exit(2)
 
+    if args.cpu_configs:
+        print(json.dumps({"cpu_configs": cpu_configs()}), flush=True)
+        return
     if args.int8_weights:
         os.environ["GKR_INT8_WEIGHTS"] = "1"
     ctx = G.Context(0)

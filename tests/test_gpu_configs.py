@@ -28,45 +28,9 @@ def lg(v):
     return max(0, (v - 1).bit_length())
 
 
-def host_layer(cfg, layer, seed_base=0):
-    """Host copies of bench.LayerWeights(ctx, cfg, layer, seed_base): same generator, same seeds."""
-    h, i, q, kv, m = cfg["hidden"], cfg["inter"], cfg["q"], cfg["kv"], cfg["tokens"]
-    s = seed_base + 1000 * layer
-    xq, xo, xg, xd = (O.synthetic(m, h, 1, s + 1), O.synthetic(m, q, 1, s + 5), O.synthetic(m, h, 1, s + 7),
-                      O.synthetic(m, i, 1, s + 10))
-    mats = {"q": (xq, O.synthetic(h, q, 1, s + 2)), "k": (xq, O.synthetic(h, kv, 1, s + 3)),
-            "v": (xq, O.synthetic(h, kv, 1, s + 4)), "o": (xo, O.synthetic(q, h, 1, s + 6)),
-            "gate": (xg, O.synthetic(h, i, 1, s + 8)), "up": (xg, O.synthetic(h, i, 1, s + 9)),
-            "down": (xd, O.synthetic(i, h, 1, s + 11))}
-    silu = O.synthetic(m, i, 0, s + 12)
-    scores = O.synthetic(cfg["heads"] * m, m, 0, s + 13) if m > 1 else None
-    return mats, silu, scores
-
-
 def oracle_layer(och, cfg, layer, out, seed_base=0):
-    """The bench's per-layer sequence (bench.model_steps) on the oracle: fresh claims, q k v o gate up
-    matmuls, SiLU LogUp (2^16), down, softmax-exp LogUp (2^16); serialized felts appended to out."""
-    mats, silu, scores = host_layer(cfg, layer, seed_base)
-
-    def matmul(A, B):
-        r = och.draw_qm31s(lg(A.shape[0]) + lg(B.shape[1]))
-        v = O.matmul_output_claim(A, B, r)
-        och.mix_secure_field(v)
-        o = O.prove_matmul_layer(r, v, A, B, och)
-        O.serialize_matmul_layer(out, o["round_polys"], o["final_a_eval"], o["final_b_eval"])
-
-    def logup(X, tag):
-        r = och.draw_qm31s(lg(X.shape[0]) + lg(X.shape[1]))
-        v = och.draw_qm31()
-        o = O.prove_activation_layer(r, v, X, tag, och, 16)
-        O.serialize_activation_layer(out, tag, o)
-
-    for name in ("q", "k", "v", "o", "gate", "up"):
-        matmul(*mats[name])
-    logup(silu, 5)
-    matmul(*mats["down"])
-    if scores is not None:
-        logup(scores, 4)
+    """bench.oracle_layer: the bench's per-layer sequence on the oracle."""
+    bench.oracle_layer(O, och, cfg, layer, out, seed_base)
 
 
 def gpu_walk(ctx, layers, seed=7):
