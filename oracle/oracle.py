@@ -1160,3 +1160,181 @@ def serialize_lookup_batch(out: list, d: dict) -> None:
             for v in m:
                 _ser_q(out, v)
             out.append(len(m) // 2)
+
+
+# ------------------------------------------------------------------ aggregated weight binding
+# crypto/aggregated_opening.rs: prove_aggregated_binding(_streaming) (:681-730, :1647-1720),
+# verify_aggregated_binding (:1774-1905), serialize_aggregated_binding_proof (cairo_serde.rs:3885-3920).
+# Pure Python over the oracle's field, hash and MLE primitives: small cases only.
+BINDING_GROUP_SIZE = 4  # gkr/prover.rs:366
+
+
+def poseidon_hash(a: int, b: int) -> int:
+    """starknet_crypto::poseidon_hash(a, b) = hades([a, b, 2])[0]."""
+    return hades([a, b, 2])[0]
+
+
+def binding_config(n_vars):
+    """AggregatedBindingConfig::from_claims (:70-95) from the claims' local variable counts."""
+    n_max = max(n_vars)
+    m_padded = 1 << max(0, (len(n_vars) - 1).bit_length())
+    sel = m_padded.bit_length() - 1
+    return {"selector_bits": sel, "n_max": n_max, "m_padded": m_padded, "n_global": sel + n_max,
+            "n_claims": len(n_vars)}
+
+
+def compute_zero_tree_root(n_vars: int) -> int:
+    """:157-171: the root of 2^n_vars zero leaves (securefield_to_felt(0) = 2^124)."""
+    h = 1 << 124
+    for _ in range(n_vars):
+        h = poseidon_hash(h, h)
+    return h
+
+
+def build_super_root(claims, cfg) -> dict:
+    """:181-227: subtree roots (a smaller matrix's root hashed up with zero trees), zero-tree padding to
+    m_padded slots, then a Merkle tree over them."""
+    zeros = [compute_zero_tree_root(k) for k in range(cfg["n_max"] + 1)]
+    subs = []
+    for c in claims:
+        r = c["commitment"]
+        for k in range(cfg["n_max"] - c["n_vars"]):
+            r = poseidon_hash(r, zeros[c["n_vars"] + k])
+        subs.append(r)
+    subs += [zeros[cfg["n_max"]]] * (cfg["m_padded"] - len(subs))
+    cur = list(subs)
+    while len(cur) > 1:
+        cur = [poseidon_hash(cur[2 * i], cur[2 * i + 1]) for i in range(len(cur) // 2)]
+    return {"root": cur[0], "subtree_roots": subs}
+
+
+def _eq1(a, b):
+    one = (1, 0, 0, 0)
+    return qadd(qmul(a, b), qmul(qsub(one, a), qsub(one, b)))
+
+
+def _selector_weight(k: int, selector, sel_bits: int):
+    """compute_selector_weight (:289-309): bits of k, most significant first."""
+    w = (1, 0, 0, 0)
+    for j, s in enumerate(selector):
+        bit = (k >> (sel_bits - 1 - j)) & 1
+        w = qmul(w, _eq1(s, (bit, 0, 0, 0)))
+    return w
+
+
+def _global_point(index: int, n_vars: int, point, cfg):
+    """global_point (:328-356): selector bits of the claim's matrix index, zeros, the local point."""
+    g = [(((index >> b) & 1), 0, 0, 0) for b in range(cfg["selector_bits"] - 1, -1, -1)]
+    g += [(0, 0, 0, 0)] * (cfg["n_max"] - n_vars)
+    return g + [tuple(q) for q in point]
+
+
+def _unified_oracle(t, mles, cfg):
+    """eval_unified_oracle (:364-393): sum_k sel_k(t_sel) W_k(t_loc[n_max - n_k ..])."""
+    sb = cfg["selector_bits"]
+    sel, loc = t[:sb], t[sb:]
+    acc = (0, 0, 0, 0)
+    for k, mle in enumerate(mles):
+        w = _selector_weight(k, sel, sb)
+        if w == (0, 0, 0, 0):
+            continue
+        nk = (len(mle) - 1).bit_length()
+        acc = qadd(acc, qmul(w, evaluate_mle([tuple(int(x) for x in v) for v in mle], loc[cfg["n_max"] - nk:])))
+    return acc
+
+
+def prove_aggregated_binding(claims, mles, ch: Channel) -> dict:
+    """prove_aggregated_binding_streaming (:1647-1720) / prove_aggregated_binding (:681-730).
+    claims: dicts (n_vars, point, value, commitment), one per matrix, in slot order; mles: the
+    matrices' MLEs (matrix_to_mle_col_major_padded) as (2^n_vars, 4) arrays."""
+    cfg = binding_config([c["n_vars"] for c in claims])
+    sr = build_super_root(claims, cfg)
+    ch.mix_felt(sr["root"])
+    rho = ch.draw_qm31()
+    betas, pw = [], (1, 0, 0, 0)
+    for _ in claims:
+        betas.append(pw)
+        pw = qmul(pw, rho)
+    gps = [_global_point(i, c["n_vars"], c["point"], cfg) for i, c in enumerate(claims)]
+    n = cfg["n_global"]
+    eqp = [(1, 0, 0, 0)] * len(claims)
+    chal, polys = [], []
+    inv2 = qinv((2, 0, 0, 0))
+    for rnd in range(n):
+        s = []
+        for x in range(3):
+            xv = (x, 0, 0, 0)
+            tot = (0, 0, 0, 0)
+            for i, c in enumerate(claims):
+                pt = chal + [xv] + gps[i][rnd + 1:]
+                mis = qsub(_unified_oracle(pt, mles, cfg), tuple(c["value"]))
+                tot = qadd(tot, qmul(qmul(betas[i], eqp[i]), qmul(_eq1(gps[i][rnd], xv), mis)))
+            s.append(tot)
+        c0 = s[0]
+        c2 = qmul(qadd(qsub(s[0], qadd(s[1], s[1])), s[2]), inv2)
+        c1 = qsub(qsub(s[1], s[0]), c2)
+        ch.mix_poly_coeffs(c0, c1, c2)
+        polys.append((c0, c1, c2))
+        r = ch.draw_qm31()
+        chal.append(r)
+        eqp = [qmul(eqp[i], _eq1(r, gps[i][rnd])) for i in range(len(claims))]
+    oracle_eval = _unified_oracle(chal, mles, cfg)
+    ch.mix_felts([oracle_eval])
+    slot = 1 << cfg["n_max"]
+    virtual = np.zeros((cfg["m_padded"] * slot, 4), dtype=np.uint32)
+    for k, mle in enumerate(mles):
+        virtual[k * slot:k * slot + len(mle)] = mle
+    cm, felts = mle_opening(virtual, chal, ch)
+    return {"config": cfg, "round_polys": polys, "oracle_eval": oracle_eval, "super_root": sr,
+            "opening": parse_mle_opening(felts)[0], "opening_felts": felts, "opening_commitment": cm,
+            "challenges": chal}
+
+
+def verify_aggregated_binding(proof, claims, ch: Channel) -> bool:
+    """verify_aggregated_binding (:1774-1905), single-opening path."""
+    cfg = proof["config"]
+    if build_super_root(claims, cfg)["root"] != proof["super_root"]["root"]:
+        return False
+    ch.mix_felt(proof["super_root"]["root"])
+    rho = ch.draw_qm31()
+    betas, pw = [], (1, 0, 0, 0)
+    for _ in claims:
+        betas.append(pw)
+        pw = qmul(pw, rho)
+    gps = [_global_point(i, c["n_vars"], c["point"], cfg) for i, c in enumerate(claims)]
+    if len(proof["round_polys"]) != cfg["n_global"]:
+        return False
+    cur, chal = (0, 0, 0, 0), []
+    for c0, c1, c2 in proof["round_polys"]:
+        if qadd(c0, qadd(qadd(c0, c1), c2)) != cur:
+            return False
+        ch.mix_poly_coeffs(c0, c1, c2)
+        r = ch.draw_qm31()
+        chal.append(r)
+        cur = qadd(c0, qmul(r, qadd(c1, qmul(r, c2))))
+    tot = (0, 0, 0, 0)
+    for i, c in enumerate(claims):
+        e = (1, 0, 0, 0)
+        for a, b in zip(gps[i], chal):
+            e = qmul(e, _eq1(a, b))
+        tot = qadd(tot, qmul(qmul(betas[i], e), qsub(tuple(proof["oracle_eval"]), tuple(c["value"]))))
+    if tot != cur:
+        return False
+    ch.mix_felts([proof["oracle_eval"]])
+    return verify_mle_opening(proof["super_root"]["root"], proof["opening"], chal, ch)
+
+
+def serialize_aggregated_binding_proof(out: list, proof) -> None:
+    """serialize_aggregated_binding_proof (cairo_serde.rs:3885-3920)."""
+    cfg = proof["config"]
+    for k in ("selector_bits", "n_max", "m_padded", "n_global", "n_claims"):
+        out.append(cfg[k])
+    out.append(len(proof["round_polys"]))
+    for c0, c1, c2 in proof["round_polys"]:
+        for q in (c0, c1, c2):
+            _ser_q(out, q)
+    _ser_q(out, proof["oracle_eval"])
+    out.append(proof["super_root"]["root"])
+    out.append(len(proof["super_root"]["subtree_roots"]))
+    out.extend(proof["super_root"]["subtree_roots"])
+    out.extend(proof["opening_felts"])
