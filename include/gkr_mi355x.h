@@ -483,6 +483,27 @@ int gkr_serialize_lookup_batch(const uint32_t* gates, const uint32_t* n_vars, si
 /* Device address of a matrix's u32 entries (row-major), e.g. multiplicities for a lookup instance. */
 const uint32_t* gkr_matrix_device_ptr(const gkr_matrix* m);
 
+/* ------------------------------------------------------------------ aggregated weight binding
+ * prove_aggregated_binding_streaming (engine/src/crypto/aggregated_opening.rs:1647-1720),
+ * the full binding proof of STWO_AGGREGATED_FULL_BINDING=1 (gkr/prover.rs:1233-1330): one
+ * AggregatedWeightBindingProof over up to 8 claims (the prover groups them by 4,
+ * BINDING_GROUP_SIZE).  Claim i sits in selector slot i; its weight's MLE is
+ * matrix_to_mle_col_major_padded(B) (log2 pk + log2 pn variables = n_point);
+ * commitment = that MLE's root (gkr_weight_commitment).  The proof is written as
+ * serialize_aggregated_binding_proof (cairo_serde.rs:3885-3920): config, sumcheck
+ * round polynomials, oracle value, super root, subtree roots, the opening of the
+ * virtual MLE.  *n_felts receives its length (GKR_ERR_BUFFER, channel untouched,
+ * when cap is short). */
+typedef struct {
+  const gkr_matrix* weight;
+  const gkr_qm31* eval_point;
+  uint32_t n_point;
+  gkr_qm31 expected_value;
+  gkr_felt commitment;
+} gkr_binding_claim;
+int gkr_prove_aggregated_binding(gkr_ctx* ctx, gkr_channel* ch, const gkr_binding_claim* claims, size_t n_claims,
+                                 gkr_felt* out, size_t cap, size_t* n_felts);
+
 /* GKR walk over a sequence of layers (the layer loop of prove_gkr_with_cache,
  * gkr/prover.rs:1500-1660, for MatMul, Mul, Activation, LayerNorm and RMSNorm
  * layers).  Steps run in order on one channel and append their LayerProof to

@@ -234,11 +234,30 @@ extern "C" int gkr_mle_commitment(gkr_ctx* c, const gkr_qvec* evals, gkr_felt* r
  * serialized claim and MleOpeningProof (cairo_serde.rs:341-369, 1759-1767). */
 constexpr size_t kMleQueries = 10;  // MLE_N_QUERIES, mle_opening.rs:47
 
-static int weight_opening(gkr_ctx* c, const gkr_matrix* b, const gkr_qm31* point, uint32_t n_point,
-                          const gkr_qm31* expected, PoseidonChannel& C, felt* commitment, std::vector<felt>& rec) {
-  MerkleTreeSpec t0;
-  TRY(weight_tree(b, &t0));
-  const uint32_t log_pk = t0.log_pk, log_pn = log2_ceil(b->cols), nv = log_pk + log_pn;
+// src: a weight matrix (its column-major padded MLE) or a resident QM31
+// vector of a power-of-two length.  with_claim: the record starts with the
+// claim (point, expected value) as serialize_gkr_model_proof writes openings;
+// otherwise it holds the MleOpeningProof alone.
+int mle_opening(gkr_ctx* c, const OpenSrc& src, const gkr_qm31* point, uint32_t n_point, const gkr_qm31* expected,
+                PoseidonChannel& C, felt* commitment, std::vector<felt>& rec, bool with_claim) {
+  const gkr_matrix* b = src.b;
+  MerkleTreeSpec t0{};
+  uint32_t log_pk = 0, log_pn = 0, nv = 0;
+  if (b) {
+    TRY(weight_tree(b, &t0));
+    log_pk = t0.log_pk;
+    log_pn = log2_ceil(b->cols);
+    nv = log_pk + log_pn;
+  } else {
+    if (!src.q || src.qn == 0 || (src.qn & (src.qn - 1))) return fail(GKR_ERR_INVALID, "MLE opening: bad vector");
+    nv = log2_ceil(src.qn);
+    t0.kind = 1;
+    t0.src = (const uint32_t*)src.q;
+    t0.rows = src.qn;
+    t0.cols = 1;
+    t0.mle_len = src.qn;
+    t0.height = std::max(1u, nv);
+  }
   if (n_point != nv) return fail(GKR_ERR_INVALID, "weight opening: point has %u vars, the padded MLE has %u", n_point, nv);
   for (uint32_t t = 0; t < nv; t++)
     if (!canonical_q(point[t])) return fail(GKR_ERR_INVALID, "weight opening: point not canonical");
@@ -254,9 +273,11 @@ static int weight_opening(gkr_ctx* c, const gkr_matrix* b, const gkr_qm31* point
   for (uint32_t t = 0; t < nv; t++) {
     const uint64_t mid = N >> (t + 1);
     const uint32_t blocks = (uint32_t)((mid + 255) / 256);
-    if (t == 0)
+    if (t == 0 && b)
       k_open_fold_matrix<<<dim3(blocks), dim3(256), 0, c->stream>>>(b->dev, b->rows, b->cols, log_pk, mid,
                                                                     Q(point[0]), L[1]);
+    else if (t == 0)
+      k_open_fold<<<dim3(blocks), dim3(256), 0, c->stream>>>(src.q, mid, Q(point[0]), L[1]);
     else
       k_open_fold<<<dim3(blocks), dim3(256), 0, c->stream>>>(L[t], mid, Q(point[t]), L[t + 1]);
     HIP_TRY(hipGetLastError());
@@ -268,7 +289,7 @@ static int weight_opening(gkr_ctx* c, const gkr_matrix* b, const gkr_qm31* point
     s.src = (const uint32_t*)L[t];
     s.mle_len = N >> t;
     s.height = nv - t;
-    if (t <= log_pn) {
+    if (b && t <= log_pn) {
       s.kind = 2;
       s.rows = b->rows;
       s.cols = 1ull << (log_pn - t);
@@ -284,10 +305,12 @@ static int weight_opening(gkr_ctx* c, const gkr_matrix* b, const gkr_qm31* point
   std::vector<MerkleKept> kept;
   TRY(merkle_roots(c, trees, roots.data(), &kept));
   qm31 final_value;
-  if (nv == 0) {
+  if (nv == 0 && b) {
     uint32_t v;
     HIP_TRY(hipMemcpy(&v, b->dev, 4, hipMemcpyDeviceToHost));
     final_value = qm31_from_m31(v);
+  } else if (nv == 0) {
+    HIP_TRY(hipMemcpy(&final_value, src.q, sizeof(qm31), hipMemcpyDeviceToHost));
   } else {
     HIP_TRY(hipMemcpy(&final_value, L[nv], sizeof(qm31), hipMemcpyDeviceToHost));
   }
@@ -343,9 +366,11 @@ static int weight_opening(gkr_ctx* c, const gkr_matrix* b, const gkr_qm31* point
   // record: claim point, expected value, MleOpeningProof
   auto fu = [&](uint64_t v) { rec.push_back(felt{{v, 0, 0, 0}}); };
   auto fq = [&](const qm31& x) { fu(x.a); fu(x.b); fu(x.c); fu(x.d); };
-  fu(nv);
-  for (uint32_t t = 0; t < nv; t++) fq(Q(point[t]));
-  fq(expected ? Q(*expected) : final_value);
+  if (with_claim) {
+    fu(nv);
+    for (uint32_t t = 0; t < nv; t++) fq(Q(point[t]));
+    fq(expected ? Q(*expected) : final_value);
+  }
   fu(nv > 0 ? nv - 1 : 0);
   for (uint32_t t = 1; t < nv; t++) rec.push_back(rf[t]);
   fu(nq);
@@ -374,7 +399,7 @@ extern "C" int gkr_prove_weight_opening(gkr_ctx* c, const gkr_matrix* b, const g
   HIP_TRY(hipSetDevice(c->device));
   felt cm;
   std::vector<felt> rec;
-  TRY(weight_opening(c, b, eval_point, n_point, expected_value, ch->ch, &cm, rec));
+  TRY(mle_opening(c, OpenSrc{b, nullptr, 0}, eval_point, n_point, expected_value, ch->ch, &cm, rec, true));
   proof->weight_commitments.push_back(cm);
   proof->weight_openings.push_back(std::move(rec));
   if (commitment) felt_canon_to_words(cm, commitment->w);

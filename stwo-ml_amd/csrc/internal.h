@@ -79,7 +79,8 @@ enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
   S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW,
-  S_LKARENA, S_LKFOLD, S_LKDESC, S_LKPART, S_LKRES, S_LKTAB, S_NSLOTS
+  S_LKARENA, S_LKFOLD, S_LKDESC, S_LKPART, S_LKRES, S_LKTAB,
+  S_BIND, S_BINDEQ, S_BINDDESC, S_BINDPART, S_BINDRES, S_BINDVIRT, S_NSLOTS
 };
 // Timer ids: device kernels (HIP events) and host-side phases (Fiat-Shamir
 // hashing inside the reducers, waiting for trip results, waiting for the
@@ -583,5 +584,16 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
 int prove_norm(gkr_ctx* c, bool ln, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
                const gkr_matrix* X, uint64_t dim, const uint32_t* gamma, uint64_t ng, gkr_channel* ch,
                gkr_proof* proof, gkr_norm_out* out, bool commit_gamma);
+// prove_mle_opening_with_commitment (crypto/mle_opening.rs:1654-1915) over
+// a weight's column-major padded MLE (b) or a resident QM31 vector (q, qn
+// entries, a power of two) (commit.hip); the record gets the claim first when
+// with_claim is set, then the MleOpeningProof.
+struct OpenSrc {
+  const gkr_matrix* b;
+  const qm31* q;
+  uint64_t qn;
+};
+int mle_opening(gkr_ctx* c, const OpenSrc& src, const gkr_qm31* point, uint32_t n_point, const gkr_qm31* expected,
+                PoseidonChannel& C, felt* commitment, std::vector<felt>& rec, bool with_claim);
 // Activation table outputs (host copy, cached per context).
 const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint32_t log_size);

@@ -176,6 +176,7 @@ SIGNATURES = [
     ("gkr_qvec_free", None, [_P]),
     ("gkr_qvec_device_ptr", _P, [_P]),
     ("gkr_matrix_device_ptr", _P, [_P]),
+    ("gkr_prove_aggregated_binding", C.c_int, [_P, _P, _P, C.c_size_t, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("gkr_prove_lookup_batch", C.c_int, [_P, _P, _P, C.c_size_t, _P]),
     ("gkr_verify_lookup_batch", C.c_int, [_U32P, _U32P, C.c_size_t, _P, _P, _PQ, _PQ]),
     ("gkr_serialize_lookup_batch", C.c_int, [_U32P, _U32P, C.c_size_t, _P, _PF, C.c_size_t,
@@ -1109,4 +1110,29 @@ def serialize_lookup_batch(d: dict) -> List[int]:
     out = (GkrFelt * max(1, n.value))()
     _check(lib().gkr_serialize_lookup_batch(gates.ctypes.data_as(_U32P), nvs.ctypes.data_as(_U32P), len(gates),
                                             C.byref(b), out, n.value, C.byref(n)))
+    return [felt_from_c(out[i]) for i in range(n.value)]
+
+
+# ------------------------------------------------------------------ aggregated weight binding
+class GkrBindingClaim(C.Structure):
+    _fields_ = [("weight", C.c_void_p), ("eval_point", _PQ), ("n_point", C.c_uint32), ("expected_value", GkrQM31),
+                ("commitment", GkrFelt)]
+
+
+def prove_aggregated_binding(ctx: "Context", ch: PoseidonChannel, claims) -> List[int]:
+    """gkr_prove_aggregated_binding: claims are (weight Matrix, eval point, expected value, commitment int);
+    returns the serialize_aggregated_binding_proof felts."""
+    arr = (GkrBindingClaim * max(1, len(claims)))()
+    keep = []
+    for i, (w, pt, v, cm) in enumerate(claims):
+        qa = q_array(pt)
+        keep.append(qa)
+        arr[i].weight, arr[i].eval_point, arr[i].n_point = w.handle, C.cast(qa, _PQ), len(pt)
+        arr[i].expected_value, arr[i].commitment = q_to_c(v), felt_to_c(cm)
+    n = C.c_size_t()
+    rc = lib().gkr_prove_aggregated_binding(ctx.handle, ch.handle, arr, len(claims), None, 0, C.byref(n))
+    if rc != 5:
+        _check(rc)
+    out = (GkrFelt * max(1, n.value))()
+    _check(lib().gkr_prove_aggregated_binding(ctx.handle, ch.handle, arr, len(claims), out, n.value, C.byref(n)))
     return [felt_from_c(out[i]) for i in range(n.value)]
