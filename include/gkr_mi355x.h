@@ -341,9 +341,18 @@ int gkr_prove_weight_openings(gkr_ctx* ctx, gkr_channel* ch, gkr_proof* proof);
  *     appended to the proof (one GPU batch), then rho = draw_qm31 and
  *     mix_secure_field(sum_i rho^i * value_i); no openings;
  *   GKR_WEIGHT_RLC_DIRECT     = apply_aggregated_rlc_binding (prover.rs:669-699): rho and
- *     the combined value only.                                                 */
-enum { GKR_WEIGHT_SEQUENTIAL = 0, GKR_WEIGHT_AGGREGATED_RLC = 1, GKR_WEIGHT_RLC_DIRECT = 2 };
+ *     the combined value only;
+ *   GKR_WEIGHT_AGGREGATED_FULL = STWO_AGGREGATED_FULL_BINDING=1 (prover.rs:1233-1330): the
+ *     commitments as in AGGREGATED_RLC, then one gkr_prove_aggregated_binding per group of
+ *     4 claims (BINDING_GROUP_SIZE, prover.rs:366) on the channel, in claim order; the
+ *     groups' serialized proofs are kept in `proof` (gkr_proof_binding_group).        */
+enum { GKR_WEIGHT_SEQUENTIAL = 0, GKR_WEIGHT_AGGREGATED_RLC = 1, GKR_WEIGHT_RLC_DIRECT = 2,
+       GKR_WEIGHT_AGGREGATED_FULL = 3 };
 int gkr_prove_weight_binding(gkr_ctx* ctx, gkr_channel* ch, gkr_proof* proof, int mode);
+size_t gkr_proof_num_binding_groups(const gkr_proof* proof);
+/* The serialize_aggregated_binding_proof felts of group g; *n_felts gets the length
+ * (GKR_ERR_BUFFER when cap is short). */
+int gkr_proof_binding_group(const gkr_proof* proof, size_t g, gkr_felt* out, size_t cap, size_t* n_felts);
 
 /* Mul layer (element-wise product c = lhs * rhs), reduce_mul_layer
  * (engine/src/gkr/prover.rs:6172-6271): mix_u64(0x4D554C), mix the claim

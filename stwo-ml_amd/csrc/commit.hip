@@ -422,7 +422,8 @@ extern "C" int gkr_prove_weight_openings(gkr_ctx* c, gkr_channel* ch, gkr_proof*
 extern "C" int gkr_prove_weight_binding(gkr_ctx* c, gkr_channel* ch, gkr_proof* proof, int mode) {
   CH_CHECK(ch);
   if (!c || !proof) return fail(GKR_ERR_INVALID, "null argument");
-  if (mode != GKR_WEIGHT_SEQUENTIAL && mode != GKR_WEIGHT_AGGREGATED_RLC && mode != GKR_WEIGHT_RLC_DIRECT)
+  if (mode != GKR_WEIGHT_SEQUENTIAL && mode != GKR_WEIGHT_AGGREGATED_RLC && mode != GKR_WEIGHT_RLC_DIRECT &&
+      mode != GKR_WEIGHT_AGGREGATED_FULL)
     return fail(GKR_ERR_INVALID, "unknown weight binding mode %d", mode);
   auto& claims = proof->weight_claims;
   if (mode == GKR_WEIGHT_SEQUENTIAL) {
@@ -435,7 +436,8 @@ extern "C" int gkr_prove_weight_binding(gkr_ctx* c, gkr_channel* ch, gkr_proof* 
     return GKR_OK;
   }
   if (claims.empty()) return GKR_OK;
-  if (mode == GKR_WEIGHT_AGGREGATED_RLC) {
+  std::vector<gkr_felt> claim_roots;
+  if (mode == GKR_WEIGHT_AGGREGATED_RLC || mode == GKR_WEIGHT_AGGREGATED_FULL) {
     // one root per distinct matrix, repeated per claim
     std::vector<const gkr_matrix*> uniq;
     std::map<const gkr_matrix*, size_t> at;
@@ -443,7 +445,33 @@ extern "C" int gkr_prove_weight_binding(gkr_ctx* c, gkr_channel* ch, gkr_proof* 
       if (at.emplace(w.b, uniq.size()).second) uniq.push_back(w.b);
     std::vector<gkr_felt> roots(uniq.size());
     TRY(gkr_weight_commitments(c, uniq.data(), uniq.size(), roots.data()));
-    for (const auto& w : claims) proof->weight_commitments.push_back(felt_canon_from_words(roots[at[w.b]].w));
+    for (const auto& w : claims) {
+      proof->weight_commitments.push_back(felt_canon_from_words(roots[at[w.b]].w));
+      claim_roots.push_back(roots[at[w.b]]);
+    }
+  }
+  if (mode == GKR_WEIGHT_AGGREGATED_FULL) {  // groups of BINDING_GROUP_SIZE claims (prover.rs:1276-1300)
+    constexpr size_t kGroup = 4;
+    for (size_t g0 = 0; g0 < claims.size(); g0 += kGroup) {
+      const size_t ng = std::min(kGroup, claims.size() - g0);
+      std::vector<gkr_binding_claim> bc(ng);
+      for (size_t i = 0; i < ng; i++) {
+        const WeightClaimRec& w = claims[g0 + i];
+        bc[i].weight = w.b;
+        bc[i].eval_point = reinterpret_cast<const gkr_qm31*>(w.point.data());
+        bc[i].n_point = (uint32_t)w.point.size();
+        bc[i].expected_value = G(w.value);
+        bc[i].commitment = claim_roots[g0 + i];
+      }
+      size_t n = 0;
+      const int rc = gkr_prove_aggregated_binding(c, ch, bc.data(), ng, nullptr, 0, &n);
+      if (rc != GKR_ERR_BUFFER) return rc == GKR_OK ? fail(GKR_ERR_INVALID, "binding proof size") : rc;
+      std::vector<gkr_felt> out(n);
+      TRY(gkr_prove_aggregated_binding(c, ch, bc.data(), ng, out.data(), n, &n));
+      proof->binding_groups.push_back(std::move(out));
+    }
+    claims.clear();
+    return GKR_OK;
   }
   PoseidonChannel& C = ch->ch;
   const qm31 rho = C.draw_qm31();
@@ -457,3 +485,14 @@ extern "C" int gkr_prove_weight_binding(gkr_ctx* c, gkr_channel* ch, gkr_proof* 
   return GKR_OK;
 }
 
+
+extern "C" size_t gkr_proof_num_binding_groups(const gkr_proof* p) { return p ? p->binding_groups.size() : 0; }
+extern "C" int gkr_proof_binding_group(const gkr_proof* p, size_t g, gkr_felt* out, size_t cap, size_t* n_felts) {
+  if (!p || !n_felts || (!out && cap)) return fail(GKR_ERR_INVALID, "null argument");
+  if (g >= p->binding_groups.size()) return fail(GKR_ERR_INVALID, "binding group %zu of %zu", g, p->binding_groups.size());
+  const auto& v = p->binding_groups[g];
+  *n_felts = v.size();
+  if (cap < v.size()) return fail(GKR_ERR_BUFFER, "need %zu felts, have %zu", v.size(), cap);
+  std::copy(v.begin(), v.end(), out);
+  return GKR_OK;
+}

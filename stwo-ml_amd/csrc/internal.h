@@ -531,6 +531,7 @@ struct gkr_proof {
   std::vector<felt> weight_commitments;
   std::vector<WeightClaimRec> weight_claims;      // recorded by the MatMul layers, in proving order
   std::vector<std::vector<felt>> weight_openings;  // serialized opening records (claim + MleOpeningProof)
+  std::vector<std::vector<gkr_felt>> binding_groups;  // serialized aggregated binding proofs
   felt io_commitment = {{0, 0, 0, 0}};
 };
 

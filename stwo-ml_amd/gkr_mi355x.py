@@ -177,6 +177,8 @@ SIGNATURES = [
     ("gkr_qvec_device_ptr", _P, [_P]),
     ("gkr_matrix_device_ptr", _P, [_P]),
     ("gkr_prove_aggregated_binding", C.c_int, [_P, _P, _P, C.c_size_t, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
+    ("gkr_proof_num_binding_groups", C.c_size_t, [_P]),
+    ("gkr_proof_binding_group", C.c_int, [_P, C.c_size_t, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("gkr_prove_lookup_batch", C.c_int, [_P, _P, _P, C.c_size_t, _P]),
     ("gkr_verify_lookup_batch", C.c_int, [_U32P, _U32P, C.c_size_t, _P, _P, _PQ, _PQ]),
     ("gkr_serialize_lookup_batch", C.c_int, [_U32P, _U32P, C.c_size_t, _P, _PF, C.c_size_t,
@@ -212,7 +214,7 @@ SIGNATURES = [
     ("gkr_prove_weight_openings", C.c_int, [_P, _P, _P]),
     ("gkr_prove_weight_binding", C.c_int, [_P, _P, _P, C.c_int]),
 ]
-WEIGHT_SEQUENTIAL, WEIGHT_AGGREGATED_RLC, WEIGHT_RLC_DIRECT = 0, 1, 2
+WEIGHT_SEQUENTIAL, WEIGHT_AGGREGATED_RLC, WEIGHT_RLC_DIRECT, WEIGHT_AGGREGATED_FULL = 0, 1, 2, 3
 DEBUG_HANDOVER_CANCEL, DEBUG_HANDOVER_EXPIRE = 1, 2
 
 
@@ -979,6 +981,19 @@ class Proof:
         out = np.zeros((max(1, n.value), 8), dtype=np.uint32)
         _check(lib().gkr_proof_serialize(self._h, out.ctypes.data_as(C.POINTER(GkrFelt)), n.value, C.byref(n)))
         return out[:n.value]
+
+    def binding_groups(self) -> List[List[int]]:
+        """The serialized aggregated binding proofs of GKR_WEIGHT_AGGREGATED_FULL, one per group."""
+        out = []
+        for g in range(lib().gkr_proof_num_binding_groups(self._h)):
+            n = C.c_size_t()
+            rc = lib().gkr_proof_binding_group(self._h, g, None, 0, C.byref(n))
+            if rc not in (0, 5):
+                _check(rc)
+            arr = (GkrFelt * max(1, n.value))()
+            _check(lib().gkr_proof_binding_group(self._h, g, arr, n.value, C.byref(n)))
+            out.append([felt_from_c(arr[i]) for i in range(n.value)])
+        return out
 
     def layer_claim_value(self, layer: int) -> QM31:
         """The output-claim value layer `layer` was proved against (gkr_proof_layer_claim_value)."""

@@ -83,3 +83,50 @@ def test_aggregated_binding_errors(gpu_ctx):
         G.prove_aggregated_binding(gpu_ctx, ch, [(m, pt, (0, 0, 0, 0), 0)] * 9)
     with pytest.raises(G.GkrError):
         G.prove_aggregated_binding(gpu_ctx, ch, [])
+
+
+def lg(v):
+    return max(0, (v - 1).bit_length())
+
+
+def test_weight_phase_full_binding(gpu_ctx):
+    """GKR_WEIGHT_AGGREGATED_FULL after five MatMul layers (two weights claimed twice): the
+    commitments in claim order, then groups of 4 and 1 claims proved on the channel, each group's
+    serialized proof equal to the oracle's over the same claims (points r_j || challenges, values
+    final_b) and the same transcript."""
+    log("case weight phase full binding")
+    rng = np.random.default_rng(21)
+    shapes = [(3, 24, 40), (3, 40, 9), (2, 16, 16), (3, 24, 40), (5, 9, 12)]
+    Ws = {}
+    mats = []
+    for m, k, n in shapes:
+        if (k, n) not in Ws:
+            Ws[(k, n)] = rng.integers(0, P, size=(k, n), dtype=np.uint32)
+        X = rng.integers(0, P, size=(m, k), dtype=np.uint32)
+        mats.append((X, Ws[(k, n)]))
+    dev = {key: gpu_ctx.upload(W) for key, W in Ws.items()}
+    ch = G.PoseidonChannel()
+    ch.mix_u64(21)
+    proof = G.Proof()
+    claims = []
+    for (X, W), (m, k, n) in zip(mats, shapes):
+        a = gpu_ctx.upload(X)
+        r = ch.draw_qm31s(lg(m) + lg(n))
+        v = gpu_ctx.matmul_output_claim(a, dev[(k, n)], r)
+        ch.mix_secure_field(v)
+        o = gpu_ctx.prove_matmul_layer(r, v, a, dev[(k, n)], ch, proof)
+        pt = list(r[lg(m):]) + list(o["next_point"][lg(m):])
+        claims.append({"n_vars": lg(k) + lg(n), "point": pt, "value": o["final_b_eval"],
+                       "commitment": O.weight_commitment(W), "mle": O.col_major_mle(W)})
+    och = O.Channel()
+    O.set_channel_state(och, ch.export_state())
+    gpu_ctx.prove_weight_binding(ch, proof, G.WEIGHT_AGGREGATED_FULL)
+    groups = proof.binding_groups()
+    assert len(groups) == 2
+    for g, start in enumerate((0, 4)):
+        part = claims[start:start + 4]
+        p = O.prove_aggregated_binding(part, [c["mle"] for c in part], och)
+        ref = []
+        O.serialize_aggregated_binding_proof(ref, p)
+        assert groups[g] == ref, g
+    assert ch.digest() == och.digest()
