@@ -645,6 +645,53 @@ def bench_norm(ctx, args):
     ctx.close()
 
 
+def bench_binding(ctx, args):
+    """The full aggregated weight binding (STWO_AGGREGATED_FULL_BINDING=1, gkr/prover.rs:1233-1330) of one
+    Qwen2.5-14B layer: the layer's walk (fresh claims, bench order) records its 7 weight claims, then the
+    weight phase proves the commitments and two AggregatedWeightBindingProofs (groups of 4 and 3 claims,
+    aggregated_opening.rs:1647-1720).  Only the weight phase is timed; weights resident in HBM."""
+    lw = LayerWeights(ctx, QWEN, 0, 0)
+    steps = model_steps([lw])
+    weight_elems = sum(lw.mats[k][1].rows * lw.mats[k][1].cols for k in WEIGHT_NAMES)
+
+    def step():
+        ch = G.PoseidonChannel()
+        ch.mix_u64(7)
+        proof = G.Proof()
+        G.prove_walk(ctx, ch, steps[0], proof, n_steps=steps[1])
+        ctx.synchronize()
+        t0 = time.perf_counter()
+        ctx.prove_weight_binding(ch, proof, G.WEIGHT_AGGREGATED_FULL)
+        ctx.synchronize()
+        dt = time.perf_counter() - t0
+        groups = proof.binding_groups()
+        return dt, ch.digest(), [len(g) for g in groups]
+
+    for _ in range(max(1, args.warmup)):
+        step()
+    ctx.set_timing(0 if args.no_timing else 1)
+    ctx.reset_timing()
+    res = [step() for _ in range(args.steps)]
+    dt = sum(r[0] for r in res) / len(res)
+    assert all(r[1] == res[0][1] for r in res), "non-deterministic proof"
+    ms, nl, nh = ctx.kernel_time(K_MERKLE)
+    fs, fsn, _ = ctx.kernel_time(K_HOST_FS)
+    ctx.set_timing(0)
+    result = {
+        "metric": "aggregated weight binding (full), weight elements/s (Qwen2.5-14B layer)",
+        "value": round(weight_elems / dt / 1e6, 1), "unit": "Melem/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u32-m31/qm31", "data": "synthetic (counter-mode SplitMix64, int8-range)",
+        "config": {"workload": "qwen2.5-14b-layer-full-weight-binding", "claims": 7, "groups": res[0][2],
+                   "weight_elements": weight_elems},
+        "merkle": {"ms_per_step": round(ms / args.steps, 3), "Mhash_per_s": round(nh / (ms * 1e-3) / 1e6, 1)} if nl else None,
+        "host_fiat_shamir_ms_per_step": round(fs / args.steps, 3) if fsn else None,
+        "digest": hex(res[0][1]), "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+    ctx.close()
+
+
 def bench_lookup(ctx, args, n_inst=96, log_n=16):
     """STWO LogUp-GKR batch (prove_batch, stwo-gpu/crates/stwo/src/prover/lookups/gkr_prover.rs:396-500) as
     prove_logup_gkr (engine/src/aggregation.rs:3926-4062) builds it for a Qwen2.5-14B model: one
@@ -810,7 +857,7 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--config", default="qwen48",
-                    choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward", "simd", "norm", "lookup"])
+                    choices=["qwen48", "qwen1", "smollm", "cfg1", "c2", "commit", "forward", "simd", "norm", "lookup", "binding"])
     ap.add_argument("--c2-logs", default="20,24,28",
                     help="config 2: log2 sizes of the QM31 vectors f_a, f_b (product sumcheck alone)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -848,6 +895,8 @@ def main():
         return bench_norm(ctx, args)
     if args.config == "lookup":
         return bench_lookup(ctx, args)
+    if args.config == "binding":
+        return bench_binding(ctx, args)
     sbuf = SerialBuffer()
     if args.config == "cfg1":
         cfg, n_layers = None, 1
