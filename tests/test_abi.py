@@ -101,6 +101,14 @@ def test_hash_many_and_permutation_match_oracle():
     assert G.poseidon_hash(st[0], st[1]) == O.hades([st[0], st[1], 2])[0]
 
 
+def test_hash_many_of_twelve_matches_sp3_io_commitment(golden):
+    """The product's hash_many on the SP3 io_commitment preimage (compute_io_commitment,
+    engine/src/aggregation.rs:235-252): rows, cols, len, data of input then output."""
+    sp3 = golden["sp3"]
+    xs = [1, 4, 4] + sp3["input_data"] + [1, 2, 2] + sp3["output_data"]
+    assert G.poseidon_hash_many(xs) == int(sp3["io_commitment"], 16)
+
+
 def test_permutation_matches_oracle_on_many_states():
     """The product's permutation (lazy [0, 2p) arithmetic inside) against the oracle's independent
     Montgomery implementation on random states and on edge values (0, 1, p - 1, 2^251, limb

@@ -181,6 +181,18 @@ def test_sp3_weight_opening(golden):
     assert cd[start:] == section + [int(sp3["io_commitment"], 16)]
 
 
+def test_sp3_io_commitment_is_hash_many_of_twelve(golden):
+    """compute_io_commitment (engine/src/aggregation.rs:235-252) hashes rows, cols, len and the data
+    of the input, then the same of the output, with poseidon_hash_many: the SP3 fixture's
+    io_commitment pins hash_many on 12 inputs (input [[1, 2, 3, 4]], output [[50, 60]])."""
+    sp3 = golden["sp3"]
+    xs = [1, 4, 4] + sp3["input_data"] + [1, 2, 2] + sp3["output_data"]
+    assert xs == [1, 4, 4, 1, 2, 3, 4, 1, 2, 2, 50, 60]
+    want = int(sp3["io_commitment"], 16)
+    assert O.hash_many(xs) == want
+    assert O.hash_many(xs[:-1] + [61]) != want
+
+
 def test_sp3_opening_verifies_and_tampering_fails(golden):
     """verify_mle_opening (mle_opening.rs:1918-2028) restated in the oracle accepts the
     reference's own SP3 opening (read from its calldata) and rejects changed values,
