@@ -35,7 +35,8 @@ METRIC = "GKR matmul-sumcheck Melem/s + % HBM peak; proved tokens/s, Qwen2.5-14B
 HBM_PEAK_GBS = 8000.0
 P = (1 << 31) - 1  # M31
 (K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT,
- K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH, K_NORM, K_LOOKUP) = range(15)
+ K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH, K_NORM, K_LOOKUP, K_HOST_GRAM,
+ K_HOST_PROOF) = range(17)
 
 QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
 SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
@@ -79,7 +80,7 @@ def matmul_elems(cfg):
     return sum(k * n + mm * k for mm, k, n in shapes), shapes
 
 
-CALL_TIME = {"matmul_claim": 0.0, "matmul_layer": 0.0, "activation_layer": 0.0}
+CALL_TIME = {"matmul_claim": 0.0, "matmul_layer": 0.0, "activation_layer": 0.0, "walk": 0.0, "serialize": 0.0}
 
 
 def prove_matmul(ctx, ch, a, b, proof):
@@ -138,7 +139,9 @@ def prove_model(ctx, layers, cfg, seed, sbuf):
         prove_matmul(ctx, ch, a, b, proof)
         if L.scores is not None:
             prove_logup(ctx, ch, L.scores, 4, 16, proof)  # softmax-exp, 2^16 table
+    t1 = time.perf_counter()
     n = sbuf.serialize(proof)  # final proof serialization (C side)
+    CALL_TIME["serialize"] += time.perf_counter() - t1
     return ch.digest(), n
 
 
@@ -164,8 +167,12 @@ def prove_model_walk(ctx, steps, seed, sbuf):
     ch = G.PoseidonChannel()
     ch.mix_u64(seed)
     proof = G.Proof()
+    t0 = time.perf_counter()
     G.prove_walk(ctx, ch, arr, proof, n_steps=n)
+    t1 = time.perf_counter()
     n = sbuf.serialize(proof)
+    CALL_TIME["walk"] += t1 - t0
+    CALL_TIME["serialize"] += time.perf_counter() - t1
     return ch.digest(), n
 
 
@@ -954,7 +961,8 @@ def main():
     host = {}
     for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait"),
                       (K_HOST_WAIT_TAIL, "device_wait_handover"), (K_HOST_DRAW, "claim_draws"),
-                      (K_HOST_LAUNCH, "launch_calls"), (K_HOST_FINISH, "host_finish")]:
+                      (K_HOST_LAUNCH, "launch_calls"), (K_HOST_FINISH, "host_finish"),
+                      (K_HOST_GRAM, "round_polys_from_trip_sums"), (K_HOST_PROOF, "proof_records")]:
         ms, nl, _ = ctx.kernel_time(kid)
         if nl:
             host[name] = {"ms_per_step": round(ms / args.steps, 3), "avg_us": round(ms / nl * 1e3, 3), "calls": nl}
@@ -990,8 +998,7 @@ def main():
         "kernels": kernels,
         "host": host,
         "driver": args.driver,
-        "calls_ms_per_step": ({k: round(v / args.steps * 1e3, 3) for k, v in CALL_TIME.items()}
-                              if args.driver == "calls" else None),
+        "calls_ms_per_step": {k: round(v / args.steps * 1e3, 3) for k, v in CALL_TIME.items() if v},
         "host_poseidon_us_per_round": poseidon_round_us(),
         "proof": {"felts": digests[0][1], "sha256_16": sbuf.fingerprint(), "final_digest": hex(digests[0][0])},
     }

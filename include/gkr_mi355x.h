@@ -104,7 +104,9 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * "bytes" count Poseidon hashes instead; 10 host: claim-point draws in the
  * walk, 11 host: time inside kernel-launch calls of the reducers, 12 host:
  * the host-finish rounds' arithmetic (wall-clock, bytes = 0); 13 the norm
- * layers' row statistics and padded-vector kernels (device). */
+ * layers' row statistics and padded-vector kernels (device); 14 the LogUp-GKR
+ * batch kernels (device); 15 host: round polynomials derived from a trip's
+ * sums; 16 host: proof-record appends (wall-clock, bytes = 0). */
 /* level 0: off; 1: events on k_restrict_cols, the Merkle level kernel and
  * the norm kernels,
  * plus the host timers; 2: events on every timed kernel (adds an event pair

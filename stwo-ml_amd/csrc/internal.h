@@ -21,6 +21,8 @@
 
 #include "../../include/gkr_mi355x.h"
 #include "field.h"
+#include <functional>
+
 #include "kernels.h"
 #include "poseidon.h"
 
@@ -77,8 +79,8 @@ inline bool felt_abi_canonical(const gkr_felt& f) {
 // ------------------------------------------------------------------ context
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
-  S_TABLE, S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW,
+  S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_TRIPMB, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW,
   S_LKARENA, S_LKFOLD, S_LKDESC, S_LKPART, S_LKRES, S_LKTAB,
   S_BIND, S_BINDEQ, S_BINDDESC, S_BINDPART, S_BINDRES, S_BINDVIRT, S_NSLOTS
 };
@@ -88,9 +90,11 @@ enum Slot {
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
                 K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
                 K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NORM = 13, K_LOOKUP = 14,
-                K_NKERNELS = 15 };
+                K_HOST_GRAM = 15, K_HOST_PROOF = 16, K_NKERNELS = 17 };
 constexpr int kMaxPartialBlocks = 1024;
 constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
+static_assert(kMaxPartialBlocks <= kCountedMaxRows && kCountedMaxRows % kBlock == 0,
+              "partial_grid launches must fit the in-kernel finish");
 // Result slots in the coherent host area (h_out): 0 .. 63 serve the result in
 // flight; results launched ahead of time and read later have their own.
 constexpr int kSlotEq0 = 64;     // eq-sumcheck trip 0 (up to 64 values)
@@ -157,7 +161,7 @@ struct gkr_ctx {
   void* buf[S_NSLOTS] = {};
   size_t cap[S_NSLOTS] = {};
   qm31* h_res = nullptr;  // pinned result staging (64 QM31)
-  uint32_t* h_mult = nullptr;  // pinned copy of the LogUp multiplicities
+  uint32_t* h_mult = nullptr;  // coherent pinned copy of the LogUp multiplicities (written by k_u32_to_q)
   qm31* h_vec = nullptr;       // coherent pinned: vectors handed over by k_handover (2 x kHandMax)
   size_t h_mult_cap = 0;
   qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
@@ -173,13 +177,15 @@ struct gkr_ctx {
   std::map<uint64_t, std::vector<uint32_t>> tables;  // (tag << 32 | log) -> table outputs
   std::set<gkr_matrix*> matrices;  // live matrices; detached when the context is destroyed
   std::set<gkr_qvec*> qvecs;       // live QM31 vectors; detached likewise
-  uint64_t table_on_device = 0;    // (tag << 32 | log) of the table held in S_TABLE, 0 = none
+  uint64_t mult_zero_entries = 0;  // leading entries of S_MULT known to be zero once the queued work is done
+  std::map<uint64_t, uint32_t*> dev_tables;  // (tag << 32 | log) -> resident device copy of the table outputs
   MerkleConsts* merkle_consts = nullptr;  // device copy, built on first use
   bool fb_pending = false;  // f_b of the last restriction still as column-chunk partials (S_COLPART)
   uint64_t fb_rows = 0, fb_pk = 0;
   int fb_chunks = 0;
   uint32_t trip_count = 0;         // value of the fused trips' arrival counter (S_TRIPCNT) after the queued launches
   bool trip_count_valid = false;   // false: zero the counter before the next fused trip
+  bool tripmb_valid = false;       // false: zero the flags of the trips launched ahead (S_TRIPMB) before use
   bool int8_weights = false;       // GKR_INT8_WEIGHTS=1 at creation: int8 weight-side restriction
   // allocation-free mode (gkr_sumcheck_product_noalloc): ensure() hands out
   // the partial rows and the arrival counter from the device's static
@@ -272,6 +278,10 @@ static inline unsigned partial_grid(uint64_t n) {
 }
 
 PointArg make_point(const qm31* r, int n);
+int eq_split(gkr_ctx* c, const qm31* r, int n, qm31** hi, qm31** lo, int* h);
+int arrival_counter(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base);
+int deliver_args(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base);
+int dot2_evals(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uint32_t* v1, qm31 out[2]);
 
 // eq(r, x) for x < count (r[0] on the most significant bit of x).
 int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out);
@@ -300,6 +310,12 @@ static int launch_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks) {
   hipLaunchKernelGGL(k_finish<NQ>, dim3(1), dim3(kBlock), 0, c->stream, sk, (uint32_t)nblocks);
   return check_launch();
 }
+// The finisher of a launch made with deliver_args (none when it delivers itself).
+template <int NQ>
+static int deliver_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks, const uint32_t* counter) {
+  if (counter) return check_launch();
+  return launch_finish<NQ>(c, sk, nblocks);
+}
 // Wait until result `seq` has been published and copy NQ values.  The wait
 // spins on the coherent flag and never blocks on the stream (a hand-over
 // kernel queued behind the result may be waiting for the host): from time to
@@ -319,7 +335,7 @@ static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_H
   // the flag only moves forward (mod 2^32): a later delivery implies this one
   for (uint64_t spins = 0; (int32_t)(*flag - seq) < 0; spins++) {
     if (hand_mb && *expired == hand_mb)
-      return fail(GKR_ERR_DEVICE, "hand-over kernel stopped waiting for the challenges (mailbox %u)", hand_mb);
+      return fail(GKR_ERR_DEVICE, "kernel launched ahead stopped waiting for its challenges (mailbox %u)", hand_mb);
     if ((spins & 0xFFFF) != 0xFFFF) continue;
     if (spins == 0xFFFF) t0 = std::chrono::steady_clock::now();
     const hipError_t e = hipStreamQuery(c->stream);
@@ -338,6 +354,11 @@ static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_H
 template <int NQ>
 static int wait_sink(gkr_ctx* c, const RoundSink& sk, qm31* host_out) {
   return wait_result<NQ>(c, sk.seq, host_out, K_HOST_WAIT, (int)(sk.out - c->h_out));
+}
+// Post k challenges into the mailbox under sequence `want`.
+inline void post_mailbox(gkr_ctx* c, uint32_t want, const qm31* chal, int k) {
+  for (int r = 0; r < k; r++) c->mailbox->alpha[r] = chal[r];
+  __atomic_store_n(&c->mailbox->seq, want, __ATOMIC_RELEASE);
 }
 // Host side of a k_handover launch: posts the last trip's challenges into
 // the mailbox and receives the folded vectors.  If the host leaves before
@@ -382,8 +403,7 @@ struct HandoverSession {
       while (*expired != mb_seq && std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() < 10.0) {
       }
     }
-    for (int r = 0; r < k; r++) c->mailbox->alpha[r] = chal[r];
-    __atomic_store_n(&c->mailbox->seq, mb_seq, __ATOMIC_RELEASE);
+    post_mailbox(c, mb_seq, chal, k);
     return GKR_OK;
   }
   // Wait for the folded vectors: count vectors of len entries each.
@@ -466,11 +486,58 @@ void trip_round_gram(const qm31* G, int K, int j, const qm31* r, int nx, const q
                             const qm31* zt, const qm31& cpre);
 // Round j of a degree-1 trip from its 2^K sums S: p(0), p(1).
 void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out);
+// tw given: the trip is launched ahead of its np pending challenges, which
+// it takes from the mailbox (pend unused).
 int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
                        const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
-                       RoundSink* sk, uint64_t b_rows = 0, int b_chunks = 0);
-// Wait for a trip's nq sums.
-int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out);
+                       RoundSink* sk, uint64_t b_rows = 0, int b_chunks = 0, const TripWait* tw = nullptr);
+// Wait for a trip's nq sums (want: the mailbox sequence of a trip launched
+// ahead, whose expired wait is then reported at once).
+int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out, uint32_t want = 0);
+
+// The trips of one sumcheck launched ahead of their challenges, all at once
+// behind the first: make() gives the next launch its mailbox wait, post()
+// delivers its challenges (in launch order: one mailbox serves them all,
+// since a trip has read its challenges before the host, having received its
+// sums, posts the next).  Leaving with posts outstanding (an error) cancels
+// the waiting kernels, drains the stream and forgets the arrival counter's
+// value (cancelled trips do not arrive).  Off in the allocation-free mode,
+// whose device memory is shared by every context.
+struct AheadTrips {
+  gkr_ctx* c;
+  int outstanding = 0;
+  explicit AheadTrips(gkr_ctx* c_) : c(c_) {}
+  bool enabled() const { return !c->noalloc; }
+  int make(TripWait* tw) {
+    uint32_t* words;
+    TRY(ensureT(c, S_TRIPMB, 16, &words));  // flags[0..1], then kTripMaxK challenges at 16-byte offset
+    if (!c->tripmb_valid) {  // fresh memory: no flag may hold a future sequence number
+      hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, c->stream, words, 16u);
+      TRY(check_launch());
+      c->tripmb_valid = true;
+    }
+    tw->mb = c->mailbox;
+    tw->want = alloc_seq(&c->mb_seq, 1);
+    tw->spin_limit = kWaitSpinLimit;
+    tw->flags = words;
+    tw->chal = reinterpret_cast<qm31*>(words + 4);
+    outstanding++;
+    return GKR_OK;
+  }
+  int post(const TripWait& tw, const qm31* chal, int np) {
+    post_mailbox(c, tw.want, chal, np);
+    outstanding--;
+    return GKR_OK;
+  }
+  ~AheadTrips() {
+    if (outstanding > 0) {
+      __atomic_store_n(&c->mailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
+      (void)hipStreamSynchronize(c->stream);
+      __atomic_store_n(&c->mailbox->seq, 0u, __ATOMIC_RELEASE);
+      c->trip_count_valid = false;
+    }
+  }
+};
 
 int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out);
 
@@ -565,11 +632,26 @@ struct Eq3Plan {
 
 // A new matrix handle (owned: freed with the handle).
 gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t cols, bool owned);
+// Trip 0 of a product sumcheck as product_sumcheck launches it: the
+// weight-side column-chunk partials it adds into in_b on the way
+// (b_chunks > 0), and a hook called with its sums before the first round
+// (the walk's fresh matmul claim, whose value is the trace of those sums).
+struct FirstTrip {
+  const qm31* b_partials = nullptr;
+  uint64_t b_rows = 0;
+  int b_chunks = 0;
+  std::function<int(const qm31* g, int K)> on_sums;
+};
+// The walk's matmul step with a fresh claim (matmul.hip): the claim value
+// and the layer proof in one pass, k > 1.
+int walk_matmul_fresh(gkr_ctx* c, const gkr_qm31* point, uint32_t n_point, gkr_qm31* value, const gkr_matrix* a,
+                      const gkr_matrix* b, gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys,
+                      gkr_qm31* final_a, gkr_qm31* final_b, gkr_qm31* next_point, gkr_qm31* next_value);
 // Degree-2 product sumcheck over 2^T entries (matmul.hip).
 int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, const qm31* in_b,
                             qm31* const bufs_a[2], qm31* const bufs_b[2], const qm31* g0, int k0,
                             gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b,
-                            const qm31* scale3 = nullptr);
+                            const qm31* scale3 = nullptr, const FirstTrip* ft = nullptr);
 // Eq-weighted degree-3 sumcheck sum_x eq(z, x) w(x) d(x) (logup.hip): plan and eq tables,
 int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl);
 // one trip,

@@ -168,6 +168,74 @@ __device__ __forceinline__ void wait_memory() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Result delivery by the reducing kernel itself (no finisher launch): each
+// workgroup stores its row of NQ sums with device-scope stores and counts
+// itself on `counter`; the last to arrive (the counter reaches
+// base + gridDim.x, mod 2^32; the host tracks the value) adds the rows and
+// delivers the NQ results to sk like k_finish.  The arrival count is an
+// acquire-release operation at agent scope: its release publishes the row
+// (ordered before it by the barrier), and in the last workgroup its acquire,
+// extended to every wave by the barrier and an agent-scope fence, makes all
+// rows visible.
+// Same-address atomics serialize (about 20 ns each on MI355X), so the host
+// uses the counted delivery only for small grids (kTripFusedMax).
+constexpr int kCountedMaxRows = 1024;  // workgroups of a kernel that delivers through sink_finish_counted
+template <int NQ>
+__device__ __forceinline__ void sink_finish_counted(qm31 (&v)[NQ], const RoundSink& sk, uint32_t* counter,
+                                                    uint32_t base) {
+  __shared__ qm31 row[NQ];
+  __shared__ bool last;
+  block_sum_store<NQ>(v, row);
+  __syncthreads();
+  if (threadIdx.x < NQ) st_q_dev(sk.partials + (uint64_t)NQ * blockIdx.x + threadIdx.x, row[threadIdx.x]);
+  wait_memory();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == base + gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // every row load in flight at once (they bypass the caches), then the sums
+  constexpr int R = kCountedMaxRows / kBlock;
+  qm31 rv[R][NQ];
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const uint32_t b = threadIdx.x + (uint32_t)i * kBlock;
+#pragma unroll
+    for (int q = 0; q < NQ; q++) rv[i][q] = b < gridDim.x ? ld_q_dev(sk.partials + (uint64_t)NQ * b + q) : qm31_zero();
+  }
+  qacc acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) acc[q].zero();
+#pragma unroll
+  for (int i = 0; i < R; i++)
+#pragma unroll
+    for (int q = 0; q < NQ; q++) acc[q].add(rv[i][q]);
+  qm31 tot[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; q++) tot[q] = acc[q].reduce();
+  __shared__ qm31 res[NQ];
+  block_sum_store<NQ>(tot, res);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int q = 0; q < NQ; q++) sk.out[q] = res[q];
+    publish_flag(sk.flag, sk.seq);
+  }
+}
+// counter given: the kernel delivers its sums itself; null: it stores its
+// partial row and the host launches k_finish behind it.  The choice is the
+// same for every workgroup of a launch.
+template <int NQ>
+__device__ __forceinline__ void sink_deliver(qm31 (&v)[NQ], const RoundSink& sk, uint32_t* counter, uint32_t base) {
+  if (counter)
+    sink_finish_counted<NQ>(v, sk, counter, base);
+  else
+    sink_finish<NQ>(v, sk);
+}
+
 // ------------------------------------------------------------------ multi-round trips
 // One launch serves K consecutive rounds of a sumcheck (K <= kTripMaxK).
 // Seen through its top K variables (MSB first), a vector f of length n splits
@@ -202,6 +270,73 @@ constexpr int kTripMaxK = 3;
 struct TripChal {
   qm31 c[kTripMaxK];
 };
+
+// Host -> device challenge delivery for kernels launched before their
+// challenges are known (k_handover, trips launched ahead).  Waits on it are
+// bounded: after kWaitSpinLimit polls, or on the cancel code, the waiting
+// kernel gives up, writes its `want` into `expired` and returns without
+// delivering results.
+constexpr uint32_t kWaitSpinLimit = 1u << 22;
+constexpr uint32_t kWaitCancel = 0xFFFFFFFEu;
+struct Mailbox {
+  uint32_t seq;      // host -> device: sequence number of the posted challenges
+  uint32_t expired;  // device -> host: the `want` of the last wait that ended without them
+  uint32_t pad[2];
+  qm31 alpha[kTripMaxK];
+};
+// A trip launched ahead: workgroup 0 waits for mailbox sequence `want`, copies
+// the np challenges to `chal` (device memory) and releases flags[0] = want,
+// or flags[1] = want when its wait ended without them; the other workgroups
+// wait for either flag (device memory, so the host mailbox sees one poller).
+// Each context's wants are distinct, so a flag left by an earlier launch
+// never matches.  mb == nullptr: the challenges are the kernel's arguments.
+struct TripWait {
+  const Mailbox* mb;
+  uint32_t want, spin_limit;
+  uint32_t* flags;
+  qm31* chal;
+};
+// Thread 0 of a workgroup: the np challenges of a trip launched ahead into
+// out[0 .. np); false when the wait ended without them.
+static __device__ __noinline__ bool trip_wait(const TripWait& tw, int np, qm31* out) {
+  if (blockIdx.x == 0) {
+    bool ok = false;
+    for (uint32_t spins = 0; spins < tw.spin_limit; spins++) {
+      const uint32_t got = __hip_atomic_load(&tw.mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+      if (got == tw.want) {
+        ok = true;
+        break;
+      }
+      if (got == kWaitCancel) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (ok) {
+      for (int r = 0; r < np; r++) {  // read after the acquiring read of seq
+        const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&tw.mb->alpha[r]));
+        out[r] = qm31{q[0], q[1], q[2], q[3]};
+        st_q_dev(tw.chal + r, out[r]);
+      }
+      wait_memory();
+      __hip_atomic_store(&tw.flags[0], tw.want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      __hip_atomic_store(const_cast<uint32_t*>(&tw.mb->expired), tw.want, __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&tw.flags[1], tw.want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    return ok;
+  }
+  // twice workgroup 0's poll count: workgroup 0 always releases one of the
+  // flags within its own limit
+  for (uint32_t spins = 0; spins / 2 < tw.spin_limit; spins++) {
+    if (__hip_atomic_load(&tw.flags[0], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == tw.want) {
+      for (int r = 0; r < np; r++) out[r] = ld_q_dev(tw.chal + r);
+      return true;
+    }
+    if (__hip_atomic_load(&tw.flags[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == tw.want) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
 
 // t + (t of lane l ^ m), for every lane.  m = 8: DPP row rotation by 8 (the
 // other half of the 16-lane row); m = 16 / 32: the gfx950 row swaps, whose
@@ -287,7 +422,15 @@ static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__
                                                  qm31* __restrict__ db, const qm31* __restrict__ eq_hi,
                                                  const qm31* __restrict__ eq_lo, int eq_h, RoundSink sk,
                                                  uint32_t* counter, uint32_t count_base, uint64_t b_rows,
-                                                 int b_chunks) {
+                                                 int b_chunks, TripWait tw) {
+  if (tw.mb) {  // launched ahead: the pending challenges come through the mailbox
+    __shared__ qm31 s_al[kTripMaxK];
+    __shared__ bool s_ok;
+    if (threadIdx.x == 0) s_ok = trip_wait(tw, np, s_al);
+    __syncthreads();
+    if (!s_ok) return;  // the whole workgroup: the host has given up on this trip
+    for (int r = 0; r < np; r++) al.c[r] = s_al[r];
+  }
   using S = TripShape<KIND, K, SPLIT>;
   constexpr int G = S::G, LX = S::LX, NA = S::NA;
   const uint64_t nb = n >> K;
@@ -490,15 +633,6 @@ static __global__ void __launch_bounds__(kFinishBlock) k_finish_wide(RoundSink s
 // the mailbox's `expired` word and returns without publishing, so every wave
 // always exits and the shared result flag only ever holds sequence numbers.
 constexpr int kHandMax = 2048;
-constexpr uint32_t kWaitSpinLimit = 1u << 22;
-constexpr uint32_t kWaitCancel = 0xFFFFFFFEu;
-
-struct Mailbox {
-  uint32_t seq;      // host -> device: sequence number of the posted challenges
-  uint32_t expired;  // device -> host: the `want` of the last wait that ended without them
-  uint32_t pad[2];
-  qm31 alpha[kTripMaxK];
-};
 
 template <int NV>
 static __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a, const qm31* __restrict__ b,
@@ -1212,9 +1346,11 @@ struct dot_acc {
 // sum_p x_p * eq[p] (prover.rs:6411-6417), into a 2-value sink.
 static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
-    const uint32_t* __restrict__ table_out, uint32_t mask, qm31 gamma, qm31 beta, const qm31* __restrict__ eq,
-    uint32_t* __restrict__ masked_in, uint32_t* __restrict__ masked_out, qm31* __restrict__ d_out,
-    qm31* __restrict__ w_out, uint32_t* __restrict__ mult, RoundSink sink) {
+    const uint32_t* __restrict__ table_out, uint32_t mask, qm31 gamma, qm31 beta, const qm31* __restrict__ eq_hi,
+    const qm31* __restrict__ eq_lo, int eq_h, uint32_t* __restrict__ masked_in, uint32_t* __restrict__ masked_out,
+    qm31* __restrict__ d_out, qm31* __restrict__ w_out, uint32_t* __restrict__ mult, RoundSink sink,
+    uint32_t* counter, uint32_t count_base) {
+  const uint64_t lo_mask = (1ull << eq_h) - 1;
   qacc acc;
   acc.zero();
   dot_acc ie;
@@ -1234,16 +1370,17 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     // zero padding all lands in bin 0; it is counted once below
     if (r < rows && c < cols) atomicAdd(&mult[mi], 1u);
     acc.add(w);
-    ie.add(m31_from_u32(x), ld_q(eq, p));
+    ie.add(m31_from_u32(x), qm31_mul(ld_q(eq_hi, p >> eq_h), ld_q(eq_lo, p & lo_mask)));
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
   qm31 v[2] = {acc.reduce(), ie.reduce()};
-  sink_finish<2>(v, sink);
+  sink_deliver<2>(v, sink, counter, count_base);
 }
 // Table side: sum_j mult_j / (gamma - j - beta*f(j)) over entries with mult_j > 0.
 static __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __restrict__ table_out,
                                                             const uint32_t* __restrict__ mult, uint64_t size,
-                                                            qm31 gamma, qm31 beta, RoundSink sink) {
+                                                            qm31 gamma, qm31 beta, RoundSink sink,
+                                                            uint32_t* counter, uint32_t count_base) {
   qacc acc;
   acc.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -1255,7 +1392,7 @@ static __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_
     acc.add(qm31_mul_m31(qm31_inv(d), m31_from_u32(m)));
   }
   qm31 v[1] = {acc.reduce()};
-  sink_finish<1>(v, sink);
+  sink_deliver<1>(v, sink, counter, count_base);
 }
 
 // pad_matrix_pow2 + matrix_to_mle (components/matmul.rs:649-664, 174-187):
@@ -1267,9 +1404,17 @@ static __global__ void k_pad_q(const uint32_t* __restrict__ X, uint64_t rows, ui
   const uint64_t r = p >> log_pcol, c = p & ((1ull << log_pcol) - 1);
   st_q(out, p, qm31_from_m31((r < rows && c < cols) ? m31_from_u32(X[r * cols + c]) : 0u));
 }
-static __global__ void k_u32_to_q(const uint32_t* __restrict__ in, uint64_t n, qm31* __restrict__ out) {
+// out[i] = in[i] lifted to QM31; with host_copy (coherent pinned host memory)
+// the raw values are also written there, and with clear_in the input is
+// zeroed behind the read (a histogram left ready for its next use).
+static __global__ void k_u32_to_q(uint32_t* __restrict__ in, uint64_t n, qm31* __restrict__ out,
+                                  uint32_t* __restrict__ host_copy, int clear_in) {
   uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) st_q(out, i, qm31_from_m31(m31_from_u32(in[i])));
+  if (i >= n) return;
+  const uint32_t v = in[i];
+  st_q(out, i, qm31_from_m31(m31_from_u32(v)));
+  if (host_copy) host_copy[i] = v;
+  if (clear_in) in[i] = 0;
 }
 
 // ------------------------------------------------------------------ MLE evaluation helpers
@@ -1286,19 +1431,24 @@ static __global__ void __launch_bounds__(kBlock) k_dot_m31(const uint32_t* __res
 }
 // Two M31 vectors against one eq table in one pass (the masked input and
 // output MLEs at the eq-sumcheck challenges, prover.rs:6558-6579).
+// Two M31 vectors' MLEs at one point: sum_i v_k[i] eq(z, i) with eq kept as
+// the product of its tables over the high and the low eq_h coordinates.
 static __global__ void __launch_bounds__(kBlock) k_dot2_m31(const uint32_t* __restrict__ v0, const uint32_t* __restrict__ v1,
-                                                     const qm31* __restrict__ eq, uint64_t n, RoundSink sink) {
+                                                     const qm31* __restrict__ eq_hi, const qm31* __restrict__ eq_lo,
+                                                     int eq_h, uint64_t n, RoundSink sink, uint32_t* counter,
+                                                     uint32_t count_base) {
   dot_acc a0, a1;
   a0.zero();
   a1.zero();
+  const uint64_t lo_mask = (1ull << eq_h) - 1;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const qm31 e = ld_q(eq, i);
+    const qm31 e = qm31_mul(ld_q(eq_hi, i >> eq_h), ld_q(eq_lo, i & lo_mask));
     a0.add(m31_from_u32(v0[i]), e);
     a1.add(m31_from_u32(v1[i]), e);
   }
   qm31 q[2] = {a0.reduce(), a1.reduce()};
-  sink_finish<2>(q, sink);
+  sink_deliver<2>(q, sink, counter, count_base);
 }
 // Partial dot products sum_i v[i] * eq[i] for a QM31-valued v.
 static __global__ void __launch_bounds__(kBlock) k_dot_q(const qm31* __restrict__ v, const qm31* __restrict__ eq,

@@ -16,6 +16,27 @@ const std::vector<uint32_t>& cached_table(gkr_ctx* c, uint32_t tag, uint32_t log
   if (it == c->tables.end()) it = c->tables.emplace(key, act_table(tag, log_size)).first;
   return it->second;
 }
+// The table's outputs resident on the device, uploaded on first use and kept
+// for the context's lifetime (a model alternates between a few tables).
+static int device_table(gkr_ctx* c, uint32_t tag, uint32_t log_size, uint32_t** out) {
+  const uint64_t key = ((uint64_t)tag << 32) | log_size;
+  auto it = c->dev_tables.find(key);
+  if (it != c->dev_tables.end()) {
+    *out = it->second;
+    return GKR_OK;
+  }
+  const std::vector<uint32_t>& t = cached_table(c, tag, log_size);
+  uint32_t* d = nullptr;
+  HIP_TRY(hipMalloc(&d, t.size() * sizeof(uint32_t)));
+  const hipError_t e = hipMemcpy(d, t.data(), t.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(d);
+    return fail(GKR_ERR_DEVICE, "table upload: %s", hipGetErrorString(e));
+  }
+  c->dev_tables.emplace(key, d);
+  *out = d;
+  return GKR_OK;
+}
 
 // Eq-weighted degree-3 sumcheck over n = 2^nv entries (the eq-sumcheck of
 // reduce_activation_layer, gkr/prover.rs:6501-6556, and of reduce_mul_layer,
@@ -140,7 +161,10 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
     TRY(wait_trip(c, sk, trip_nq(1, tr.K), g));
     for (int i = 0; i < tr.K; i++) {
       qm31 sums[4];
-      trip_round_gram(g, tr.K, i, chal + tr.t, 4, xs, sums, z + tr.t, cpre);
+      {
+        HostTimer hg(c, K_HOST_GRAM);
+        trip_round_gram(g, tr.K, i, chal + tr.t, 4, xs, sums, z + tr.t, cpre);
+      }
       absorb3(tr.t + i, sums);
     }
     for (int i = 0; i < tr.K; i++) cpre = qm31_mul(cpre, eqlin(z[tr.t + i], chal[tr.t + i]));
@@ -226,11 +250,9 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   PoseidonChannel& C = ch->ch;
   const uint64_t tsize = 1ull << table_log;
   const uint32_t mask = (uint32_t)(tsize - 1);
-  const std::vector<uint32_t>& table = cached_table(c, tag, table_log);
 
   uint32_t *d_table, *d_mult, *d_min, *d_mout;
-  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *d_e0, *m0, *m1;
-  TRY(ensureT(c, S_TABLE, tsize, &d_table));
+  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *m0, *m1;
   TRY(ensureT(c, S_MULT, tsize, &d_mult));
   TRY(ensureT(c, S_MIN, n, &d_min));
   TRY(ensureT(c, S_MOUT, n, &d_mout));
@@ -238,20 +260,19 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(ensureT(c, S_D1, n / 2 + 1, &d_d1));
   TRY(ensureT(c, S_W0, n, &d_w0));
   TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
-  TRY(ensureT(c, S_E0, n, &d_e0));
   TRY(ensureT(c, S_M0, tsize, &m0));
   TRY(ensureT(c, S_M1, tsize / 2 + 1, &m1));
   TRY(ensure_host_mult(c, tsize));
-  const uint64_t table_key = ((uint64_t)tag << 32) | table_log;
-  if (c->table_on_device != table_key) {
-    c->table_on_device = 0;
-    HIP_TRY(hipMemcpyAsync(d_table, table.data(), tsize * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
-    c->table_on_device = table_key;
-  }
-  HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
-  // eq(claim point, x): the input MLE at the claim point (accumulated by the
-  // prepare pass) and the eq vector of the eq-sumcheck
-  TRY(eq_table(c, cpt.data(), nv, n, d_e0));
+  TRY(device_table(c, tag, table_log, &d_table));
+  // the histogram starts from zero: the previous layer's conversion kernel
+  // cleared it, or it is cleared here
+  if (c->mult_zero_entries < tsize) HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
+  c->mult_zero_entries = 0;
+  // eq(claim point, x) as the product of its high and low tables: the input
+  // MLE at the claim point is accumulated by the prepare pass
+  qm31 *eq_hi, *eq_lo;
+  int eq_h;
+  TRY(eq_split(c, cpt.data(), nv, &eq_hi, &eq_lo, &eq_h));
 
   // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
   C.mix_u64(0x4C4F47ull);
@@ -272,20 +293,31 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   {
     HostTimer ht(c, K_HOST_LAUNCH);
     TRY(make_sink(c, &sk_prep, kSlotPrep));
+    uint32_t* counter;
+    uint32_t base;
     {
-      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 16 * n + 8 * n + 32 * n);
-      hipLaunchKernelGGL(k_logup_prepare, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, input->dev,
-                         input->rows, input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, d_e0, d_min,
-                         d_mout, d_d0, d_w0, d_mult, sk_prep);
+      const unsigned grid = partial_grid(n);
+      TRY(deliver_args(c, grid, &counter, &base));
+      // algorithmic bytes: the input, masked input and output written (8 per entry), d and w written
+      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 8 * n + 32 * n);
+      hipLaunchKernelGGL(k_logup_prepare, dim3(grid), dim3(kBlock), 0, c->stream, input->dev, input->rows,
+                         input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, eq_hi, eq_lo, eq_h, d_min,
+                         d_mout, d_d0, d_w0, d_mult, sk_prep, counter, base);
+      TRY(deliver_finish<2>(c, sk_prep, grid, counter));
     }
-    TRY(launch_finish<2>(c, sk_prep, partial_grid(n)));
     TRY(make_sink(c, &sk_table, kSlotTable));
-    hipLaunchKernelGGL(k_logup_table_sum, dim3(partial_grid(tsize)), dim3(kBlock), 0, c->stream, d_table, d_mult,
-                       tsize, gamma, beta, sk_table);
-    TRY(launch_finish<1>(c, sk_table, partial_grid(tsize)));
-    HIP_TRY(hipMemcpyAsync(c->h_mult, d_mult, tsize * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
-    hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0);
+    {
+      const unsigned grid = partial_grid(tsize);
+      TRY(deliver_args(c, grid, &counter, &base));
+      hipLaunchKernelGGL(k_logup_table_sum, dim3(grid), dim3(kBlock), 0, c->stream, d_table, d_mult, tsize, gamma,
+                         beta, sk_table, counter, base);
+      TRY(deliver_finish<1>(c, sk_table, grid, counter));
+    }
+    // the multiplicities as QM31 for the sumcheck, and to the pinned host copy
+    hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0, c->h_mult,
+                       1);
     TRY(check_launch());
+    c->mult_zero_entries = tsize;
   }
   const std::vector<Trip> mtrips = plan_trips((int)table_log, kHostTailSum, kTripMaxK);
   TRY(launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
@@ -313,14 +345,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   const qm31 w_eval = fin[1];
   // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass
   qm31 io[2];
-  TRY(eq_table(c, chal.data(), nv, n, d_e0));
-  {
-    RoundSink sk;
-    TRY(make_sink(c, &sk));
-    hipLaunchKernelGGL(k_dot2_m31, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, d_min, d_mout, d_e0, n, sk);
-    TRY(launch_finish<2>(c, sk, partial_grid(n)));
-    TRY(wait_sink<2>(c, sk, io));
-  }
+  TRY(dot2_evals(c, chal.data(), nv, d_min, d_mout, io));
   const qm31 in_eval = io[0], out_eval = io[1];
   out->w_eval = G(w_eval);
   out->in_eval = G(in_eval);
@@ -368,7 +393,10 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       TRY(wait_trip(c, sk, trip_nq(2, tr.K), g));
       for (int i = 0; i < tr.K; i++) {
         qm31 sums[2];
-        trip_round_sum(g, tr.K, i, mchal.data() + tr.t, sums);
+        {
+          HostTimer hg(c, K_HOST_GRAM);
+          trip_round_sum(g, tr.K, i, mchal.data() + tr.t, sums);
+        }
         absorb1((uint32_t)(tr.t + i), sums);
         mchal[tr.t + i] = alpha;
       }
@@ -410,6 +438,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   out->output_eval = *claim_value;
 
   if (proof) {
+    HostTimer hp(c, K_HOST_PROOF);
     LayerRec L;
     L.tag = 3;
     L.act_type = tag;
@@ -426,7 +455,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     for (uint32_t t = 0; t < 2 * table_log; t++) L.mult_rp.push_back(Q(out->mult_round_polys[t]));
     L.mult_final = mfin[0];
     L.mult_sum = mult_sum;
-    proof->layers.push_back(L);
+    proof->layers.push_back(std::move(L));
   }
   return GKR_OK;
 }

@@ -229,7 +229,7 @@ static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* 
 int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, const qm31* in_b,
                             qm31* const bufs_a[2], qm31* const bufs_b[2], const qm31* g0, int k0,
                             gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b,
-                            const qm31* scale3) {
+                            const qm31* scale3, const FirstTrip* ft) {
   const qm31 inv2 = qm31_from_m31(1u << 30);  // 2^-1 mod P
   const uint64_t pk = 1ull << T;
   const std::vector<Trip> trips = plan_trips(T, kHostTailMM, g0 ? k0 : trip_k(1ull << T));
@@ -260,36 +260,70 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
   };
   const qm31 xs[3] = {qm31_zero(), qm31_one(), qm31_from_m31(2)};
   HandoverSession ho(c);
+  AheadTrips ahead(c);
+  const size_t nt = trips.size();
+  std::vector<RoundSink> sks(nt);
+  std::vector<TripWait> tws(nt);
+  // Every trip is launched up front (the first with its inputs, the others
+  // ahead of their challenges, which the host posts as it draws them), then
+  // the hand-over: no launch sits between a trip's sums and the next trip.
+  // Without launches ahead each trip is launched once its challenges are known.
+  const bool pre = ahead.enabled();
   const qm31* src_a = in_a;
   const qm31* src_b = in_b;
+  auto launch_j = [&](size_t j, const qm31* pend) -> int {
+    const Trip& tr = trips[j];
+    qm31* da = j == 0 ? nullptr : bufs_a[(j - 1) & 1];
+    qm31* db = j == 0 ? nullptr : bufs_b[(j - 1) & 1];
+    const int npj = j == 0 ? 0 : trips[j - 1].K;
+    const TripWait* tw = nullptr;
+    if (j > 0 && pre) {
+      TRY(ahead.make(&tws[j]));
+      tw = &tws[j];
+    }
+    if (j == 0 && ft && ft->b_chunks)  // add the weight-side chunk partials and store f_b (in_b)
+      TRY(launch_trip(c, 0, tr.K, src_a, ft->b_partials, tr.n, 0, nullptr, nullptr, const_cast<qm31*>(in_b),
+                      nullptr, nullptr, 0, 0, &sks[0], ft->b_rows, ft->b_chunks));
+    else
+      TRY(launch_trip(c, 0, tr.K, src_a, src_b, tr.n, npj, pend, da, db, nullptr, nullptr, 0, 0, &sks[j], 0, 0,
+                      tw));
+    if (j > 0) {
+      src_a = da;
+      src_b = db;
+    }
+    if (j + 1 == nt) TRY(ho.launch<2>(src_a, src_b, tr.n, tr.K));
+    return GKR_OK;
+  };
+  if (g0) {
+    if (nt == 1) TRY(ho.launch<2>(in_a, in_b, trips[0].n, trips[0].K));
+  } else {
+    TRY(launch_j(0, nullptr));
+  }
+  if (pre)
+    for (size_t j = 1; j < nt; j++) TRY(launch_j(j, nullptr));
   int np = 0;
   const qm31* pend = nullptr;
-  for (size_t j = 0; j < trips.size(); j++) {
+  for (size_t j = 0; j < nt; j++) {
     const Trip& tr = trips[j];
-    const bool last = j + 1 == trips.size();
     qm31 g[kMaxSums];
+    if (j > 0 && !pre) TRY(launch_j(j, pend));
     if (j == 0 && g0) {
       for (int q = 0; q < trip_nq(0, tr.K); q++) g[q] = g0[q];
-      if (last) TRY(ho.launch<2>(in_a, in_b, tr.n, tr.K));
     } else {
-      qm31* da = j == 0 ? nullptr : bufs_a[(j - 1) & 1];
-      qm31* db = j == 0 ? nullptr : bufs_b[(j - 1) & 1];
-      RoundSink sk;
-      TRY(launch_trip(c, 0, tr.K, src_a, src_b, tr.n, np, pend, da, db, nullptr, nullptr, 0, 0, &sk));
-      if (j > 0) {
-        src_a = da;
-        src_b = db;
-      }
-      if (last) TRY(ho.launch<2>(src_a, src_b, tr.n, tr.K));
-      TRY(wait_trip(c, sk, trip_nq(0, tr.K), g));
+      TRY(wait_trip(c, sks[j], trip_nq(0, tr.K), g, j > 0 && pre ? tws[j].want : 0));
     }
+    if (j == 0 && ft && ft->on_sums) TRY(ft->on_sums(g, tr.K));
     for (int i = 0; i < tr.K; i++) {
       qm31 sums[3];
-      trip_round_gram(g, tr.K, i, chal.data() + tr.t, 3, xs, sums, nullptr, qm31_zero());
+      {
+        HostTimer hg(c, K_HOST_GRAM);
+        trip_round_gram(g, tr.K, i, chal.data() + tr.t, 3, xs, sums, nullptr, qm31_zero());
+      }
       absorb(tr.t + i, sums);
     }
     np = tr.K;
     pend = chal.data() + tr.t;
+    if (pre && j + 1 < nt) TRY(ahead.post(tws[j + 1], pend, np));
   }
   const int t_end = trips.empty() ? 0 : trips.back().t + trips.back().K;
   const uint64_t hlen = pk >> t_end;
@@ -324,17 +358,19 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
   return GKR_OK;
 }
 
+// on_sums (T > 0 only): called with trip 0's sums before the first round.
 static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, uint32_t n_ri,
                               const gkr_qm31* r_j, uint32_t n_rj, uint64_t pk, PoseidonChannel& ch,
-                              gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b) {
+                              gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b,
+                              const std::function<int(const qm31*, int)>* on_sums = nullptr) {
   TRY(validate_matmul(c, a, b, n_ri, n_rj));
   if (pk != next_pow2(a->cols))
     return fail(GKR_ERR_INVALID, "pk=%llu but next_pow2(k)=%llu", (unsigned long long)pk,
                 (unsigned long long)next_pow2(a->cols));
   HIP_TRY(hipSetDevice(c->device));
   TRY(ensure_restricted(c, a, b, r_i, n_ri, r_j, n_rj));
-  if (!c->mm.have_trip0) TRY(finish_fb(c));  // the sumcheck reads f_b from S_FB0
   const int T = log2_exact(pk);
+  if (on_sums && T == 0) return fail(GKR_ERR_INVALID, "a claim from trip 0's sums needs k > 1");
   qm31 *fa0, *fa1, *fb0, *fb1, *fa2, *fb2;
   TRY(ensureT(c, S_FA0, pk, &fa0));
   TRY(ensureT(c, S_FB0, pk, &fb0));
@@ -345,6 +381,7 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
   // The trips write only S_FA1/S_FB1 and S_FA2/S_FB2; S_FA0/S_FB0 keep the
   // restricted vectors, so a cached restriction stays valid.
   if (T == 0) {
+    TRY(finish_fb(c));  // the sums read f_b from S_FB0
     qm31 v[1];
     TRY(fetch_q(c, fa0, 1, v));
     *final_a = G(v[0]);
@@ -356,8 +393,16 @@ static int reduce_matmul_impl(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix*
   qm31* bufs_b[2] = {fb1, fb2};
   const bool have = c->mm.have_trip0;
   c->mm.have_trip0 = false;  // used once: the transcript moves on
+  FirstTrip ft;
+  if (!have && c->fb_pending) {  // trip 0 adds the weight-side chunk partials and stores f_b (S_FB0)
+    ft.b_partials = (const qm31*)c->buf[S_COLPART];
+    ft.b_rows = c->fb_rows;
+    ft.b_chunks = c->fb_chunks;
+    c->fb_pending = false;
+  }
+  if (on_sums) ft.on_sums = *on_sums;
   return product_sumcheck(c, ch, T, fa0, fb0, bufs_a, bufs_b, have ? c->mm.trip0 : nullptr, c->mm.trip0_k,
-                          round_polys, challenges, final_a, final_b);
+                          round_polys, challenges, final_a, final_b, nullptr, &ft);
 }
 
 extern "C" int gkr_reduce_matmul_layer(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i,
@@ -400,14 +445,20 @@ extern "C" int gkr_matmul_output_claim(gkr_ctx* c, const gkr_matrix* a, const gk
   return GKR_OK;
 }
 
-extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
-                                      const gkr_qm31* claim_value, const gkr_matrix* a, const gkr_matrix* b,
-                                      gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys, gkr_qm31* final_a,
-                                      gkr_qm31* final_b, gkr_qm31* next_point, gkr_qm31* next_value) {
+// The matmul layer proof.  fresh: the claim value is not given but computed
+// as the trace of trip 0's sums (gkr_matmul_output_claim's value) once they
+// arrive, mixed as the walk mixes a fresh claim, and returned in
+// *claim_value; every trip of the sumcheck is then launched before the first
+// wait.  The transcript and the proof equal gkr_matmul_output_claim, the
+// walk's mix of the value, then gkr_prove_matmul_layer.  Needs k > 1.
+static int prove_matmul_impl(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, gkr_qm31* claim_value,
+                             bool fresh, const gkr_matrix* a, const gkr_matrix* b, gkr_channel* ch, gkr_proof* proof,
+                             gkr_qm31* round_polys, gkr_qm31* final_a, gkr_qm31* final_b, gkr_qm31* next_point,
+                             gkr_qm31* next_value) {
   CH_CHECK(ch);
   if (!c || !a || !b || !claim_value || !final_a || !final_b || !next_value || (!claim_point && n_point))
     return fail(GKR_ERR_INVALID, "null argument");
-  if (!canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
+  if (!fresh && !canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
   const uint64_t pm = next_pow2(a->rows), pk = next_pow2(a->cols), pn = next_pow2(b->cols);
   const uint32_t log_m = (uint32_t)log2_exact(pm), log_n = (uint32_t)log2_exact(pn);
   const int T = log2_exact(pk);
@@ -417,13 +468,24 @@ extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, u
   if (T > 0 && (!round_polys || !next_point)) return fail(GKR_ERR_INVALID, "null output buffer");
   TRY(validate_matmul(c, a, b, log_m, log_n));
   PoseidonChannel& C = ch->ch;
-  C.mix_u64(a->rows);
-  C.mix_u64(a->cols);
-  C.mix_u64(b->cols);
-  C.mix_secure_field(Q(*claim_value));
+  auto mix_head = [&](const qm31& v) {
+    C.mix_u64(a->rows);
+    C.mix_u64(a->cols);
+    C.mix_u64(b->cols);
+    C.mix_secure_field(v);
+  };
+  std::function<int(const qm31*, int)> claim_from_sums = [&](const qm31* g, int K) -> int {
+    qm31 v = qm31_zero();  // sum_x f_a(x) f_b(x) = trace of the cross sums
+    for (int q = 0; q < (1 << K); q++) v = qm31_add(v, g[q * ((1 << K) + 1)]);
+    *claim_value = G(v);
+    C.mix_secure_field(v);  // the walk's mix of a fresh claim
+    mix_head(v);
+    return GKR_OK;
+  };
+  if (!fresh) mix_head(Q(*claim_value));
   std::vector<gkr_qm31> chal(T > 0 ? T : 1);
   TRY(reduce_matmul_impl(c, a, b, claim_point, log_m, claim_point + log_m, log_n, pk, C, round_polys, chal.data(),
-                         final_a, final_b));
+                         final_a, final_b, fresh ? &claim_from_sums : nullptr));
   C.mix_secure_field(Q(*final_a));
   C.mix_secure_field(Q(*final_b));
   if (next_point) {
@@ -432,13 +494,14 @@ extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, u
   }
   *next_value = *final_a;
   if (proof) {
+    HostTimer hp(c, K_HOST_PROOF);
     LayerRec L;
     L.tag = 0;
     L.claim_value = Q(*claim_value);
     for (int t = 0; t < 3 * T; t++) L.rp.push_back(Q(round_polys[t]));
     L.final_a = Q(*final_a);
     L.final_b = Q(*final_b);
-    proof->layers.push_back(L);
+    proof->layers.push_back(std::move(L));
     WeightClaimRec w;
     w.b = b;
     for (uint32_t l = 0; l < log_n; l++) w.point.push_back(Q(claim_point[log_m + l]));
@@ -447,6 +510,24 @@ extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, u
     proof->weight_claims.push_back(std::move(w));
   }
   return GKR_OK;
+}
+
+extern "C" int gkr_prove_matmul_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
+                                      const gkr_qm31* claim_value, const gkr_matrix* a, const gkr_matrix* b,
+                                      gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys, gkr_qm31* final_a,
+                                      gkr_qm31* final_b, gkr_qm31* next_point, gkr_qm31* next_value) {
+  if (!claim_value) return fail(GKR_ERR_INVALID, "null argument");
+  gkr_qm31 v = *claim_value;
+  return prove_matmul_impl(c, claim_point, n_point, &v, false, a, b, ch, proof, round_polys, final_a, final_b,
+                           next_point, next_value);
+}
+// The walk's matmul step with a fresh claim at `point` (k > 1): claim value
+// and layer proof in one pass (prove_matmul_impl, fresh).
+int walk_matmul_fresh(gkr_ctx* c, const gkr_qm31* point, uint32_t n_point, gkr_qm31* value, const gkr_matrix* a,
+                      const gkr_matrix* b, gkr_channel* ch, gkr_proof* proof, gkr_qm31* round_polys,
+                      gkr_qm31* final_a, gkr_qm31* final_b, gkr_qm31* next_point, gkr_qm31* next_value) {
+  return prove_matmul_impl(c, point, n_point, value, true, a, b, ch, proof, round_polys, final_a, final_b, next_point,
+                           next_value);
 }
 
 // SIMD matmul layer with a shared weight: N activation blocks A_b (all m x k)
@@ -525,6 +606,7 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
   TRY(ensureT(c, S_FA2, pk / 4 + 1, &fa2));
   TRY(ensureT(c, S_FB2, pk / 4 + 1, &fb2));
   if (T == 0) {
+    TRY(finish_fb(c));  // the sums read f_b from S_FB0
     qm31 v[1];
     TRY(fetch_q(c, fa0, 1, v));
     *final_a = G(v[0]);
@@ -543,13 +625,14 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
   }
   *next_value = *final_a;
   if (proof) {
+    HostTimer hp(c, K_HOST_PROOF);
     LayerRec L;
     L.tag = 0;
     L.claim_value = Q(*claim_value);
     for (int t = 0; t < 3 * T; t++) L.rp.push_back(Q(round_polys[t]));
     L.final_a = Q(*final_a);
     L.final_b = Q(*final_b);
-    proof->layers.push_back(L);
+    proof->layers.push_back(std::move(L));
     WeightClaimRec w;
     w.b = b;
     for (uint32_t l = 0; l < log_n; l++) w.point.push_back(Q(claim_point[log_m + l]));
@@ -724,6 +807,7 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
   TRY(check_launch());
   std::vector<gkr_qm31> kchal(T > 0 ? T : 1);
   if (T == 0) {
+    TRY(finish_fb(c));  // the sums read f_b from S_FB0
     qm31 v[1];
     TRY(fetch_q(c, fa0, 1, v));
     *final_a = G(v[0]);

@@ -208,20 +208,15 @@ int norm_prepare(gkr_ctx* c, const gkr_matrix* X, const NormShape& S, const uint
   return sync(c);
 }
 
-// MLEs of the input (S_MIN) and output (S_MOUT) at z: one eq table, one pass.
+// MLEs of the input (S_MIN) and output (S_MOUT) at z: one eq split, one pass.
 int norm_evals(gkr_ctx* c, const NormShape& S, const qm31* z, qm31* in_eval, qm31* out_eval) {
-  qm31* eq;
   uint32_t *in_u, *out_u;
-  TRY(ensureT(c, S_EQ, S.n, &eq));
   TRY(ensureT(c, S_MIN, S.n, &in_u));
   TRY(ensureT(c, S_MOUT, S.n, &out_u));
-  TRY(eq_table(c, z, S.nv, S.n, eq));
-  RoundSink sk;
-  TRY(make_sink(c, &sk));
-  hipLaunchKernelGGL(k_dot2_m31, dim3(partial_grid(S.n)), dim3(kBlock), 0, c->stream, in_u, out_u, eq, S.n, sk);
-  TRY(launch_finish<2>(c, sk, partial_grid(S.n)));
+  if (S.n != (1ull << S.nv)) return fail(GKR_ERR_DEVICE, "norm vectors of %llu entries over %d variables",
+                                         (unsigned long long)S.n, S.nv);
   qm31 io[2];
-  TRY(wait_sink<2>(c, sk, io));
+  TRY(dot2_evals(c, z, S.nv, in_u, out_u, io));
   *in_eval = io[0];
   *out_eval = io[1];
   return GKR_OK;

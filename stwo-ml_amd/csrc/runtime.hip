@@ -32,8 +32,9 @@ int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
     return fail(GKR_ERR_NOMEM, "the allocation-free entry point needs device buffer %d (%zu bytes)", (int)s, bytes);
   }
   if (c->cap[s] < bytes) {
-    if (s == S_TABLE) c->table_on_device = 0;
     if (s == S_TRIPCNT) c->trip_count_valid = false;  // fresh memory must be zeroed
+    if (s == S_MULT) c->mult_zero_entries = 0;
+    if (s == S_TRIPMB) c->tripmb_valid = false;
     if (c->buf[s]) HIP_TRY(hipFree(c->buf[s]));
     c->buf[s] = nullptr;
     c->cap[s] = 0;
@@ -53,7 +54,7 @@ int ensure_host_mult(gkr_ctx* c, uint64_t n) {
     c->h_mult = nullptr;
     c->h_mult_cap = 0;
   }
-  HIP_TRY(hipHostMalloc((void**)&c->h_mult, n * sizeof(uint32_t), hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc((void**)&c->h_mult, n * sizeof(uint32_t), hipHostMallocCoherent | hipHostMallocMapped));
   c->h_mult_cap = n;
   return GKR_OK;
 }
@@ -116,6 +117,59 @@ int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out) {
   TRY(check_launch());
   hipLaunchKernelGGL(k_eq_combine, dim3(grid_for(count)), dim3(kBlock), 0, c->stream, hi, lo, h, count, out);
   return check_launch();
+}
+// The high / low factor tables of eq(r, .) over n coordinates (S_EQHI over
+// the first n - h, S_EQLO over the last h = n / 2), one launch.
+int eq_split(gkr_ctx* c, const qm31* r, int n, qm31** hi, qm31** lo, int* h) {
+  if (n > kMaxVars) return fail(GKR_ERR_INVALID, "eq table: %d variables exceeds %d", n, kMaxVars);
+  *h = n / 2;
+  const uint64_t n_hi = 1ull << (n - *h), n_lo = 1ull << *h;
+  TRY(ensureT(c, S_EQHI, n_hi, hi));
+  TRY(ensureT(c, S_EQLO, n_lo, lo));
+  PointArg pt = make_point(r, n);
+  TimedLaunch t(c, K_EQ_TABLE, 16 * (n_hi + n_lo));
+  hipLaunchKernelGGL(k_eq_tables, dim3(grid_for(n_hi + n_lo)), dim3(kBlock), 0, c->stream, pt, *h, *hi, *lo);
+  return check_launch();
+}
+// The arrival counter of kernels that deliver their own results
+// (sink_finish_counted, fused trips): the base value for a launch of `grid`
+// workgroups, zeroing the counter first when its value is unknown.
+int arrival_counter(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base) {
+  TRY(ensureT(c, S_TRIPCNT, 1, counter));
+  if (!c->trip_count_valid) {
+    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, c->stream, *counter, 1u);
+    TRY(check_launch());
+    c->trip_count = 0;
+    c->trip_count_valid = true;
+  }
+  *base = c->trip_count;
+  c->trip_count += grid;
+  return GKR_OK;
+}
+// Delivery of a reducing kernel's sums: by the kernel itself for grids of at
+// most kTripFusedMax workgroups (an arrival counter), else by k_finish
+// launched behind it (deliver_finish).
+int deliver_args(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base) {
+  *counter = nullptr;
+  *base = 0;
+  if (grid > kTripFusedMax) return GKR_OK;
+  return arrival_counter(c, grid, counter, base);
+}
+// MLEs of two M31 vectors of n = 2^nv entries at z (one eq split, one pass).
+int dot2_evals(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uint32_t* v1, qm31 out[2]) {
+  const uint64_t n = 1ull << nv;
+  qm31 *hi, *lo;
+  int h;
+  TRY(eq_split(c, z, nv, &hi, &lo, &h));
+  RoundSink sk;
+  TRY(make_sink(c, &sk));
+  const unsigned grid = partial_grid(n);
+  uint32_t* counter;
+  uint32_t base;
+  TRY(deliver_args(c, grid, &counter, &base));
+  hipLaunchKernelGGL(k_dot2_m31, dim3(grid), dim3(kBlock), 0, c->stream, v0, v1, hi, lo, h, n, sk, counter, base);
+  TRY(deliver_finish<2>(c, sk, grid, counter));
+  return wait_sink<2>(c, sk, out);
 }
 int make_sink(gkr_ctx* c, RoundSink* sk, int slot) {
   qm31* part;
@@ -204,22 +258,13 @@ void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out) {
 template <int KIND, int K, bool SPLIT>
 static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n, int np, const TripChal& al,
                          qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, const RoundSink& sk,
-                         unsigned grid, uint64_t b_rows, int b_chunks) {
+                         unsigned grid, uint64_t b_rows, int b_chunks, const TripWait& tw) {
   uint32_t* counter = nullptr;
   uint32_t base = 0;
-  if (GKR_TRIP_FUSED && grid <= kTripFusedMax) {  // one launch: the last workgroup finishes
-    TRY(ensureT(c, S_TRIPCNT, 1, &counter));
-    if (!c->trip_count_valid) {
-      hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, c->stream, counter, 1u);
-      TRY(check_launch());
-      c->trip_count = 0;
-      c->trip_count_valid = true;
-    }
-    base = c->trip_count;
-    c->trip_count += grid;
-  }
+  if (GKR_TRIP_FUSED && grid <= kTripFusedMax)  // one launch: the last workgroup finishes
+    TRY(arrival_counter(c, grid, &counter, &base));
   hipLaunchKernelGGL((k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
-                     sk, counter, base, b_rows, b_chunks);
+                     sk, counter, base, b_rows, b_chunks, tw);
   TRY(check_launch());
   if (counter) return GKR_OK;
   constexpr int NQ = TripShape<KIND, K, SPLIT>::NQ;
@@ -228,14 +273,19 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
 }
 int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
                        const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
-                       RoundSink* sk, uint64_t b_rows, int b_chunks) {
+                       RoundSink* sk, uint64_t b_rows, int b_chunks, const TripWait* tw) {
   if (np < 0 || np > kTripMaxK || K < 0 || K > kTripMaxK || (n >> K) == 0 || (kind == 1) != (hi != nullptr) ||
       (b_chunks && (kind != 0 || np != 0 || b_rows > n)))
     return fail(GKR_ERR_DEVICE, "bad trip (kind %d, K %d, np %d, n %llu)", kind, K, np, (unsigned long long)n);
   HostTimer ht(c, K_HOST_LAUNCH);
   TripChal al;
   memset(&al, 0, sizeof al);
-  for (int i = 0; i < np; i++) al.c[i] = pend[i];
+  TripWait w;
+  memset(&w, 0, sizeof w);
+  if (tw)
+    w = *tw;
+  else
+    for (int i = 0; i < np; i++) al.c[i] = pend[i];
   TRY(make_sink(c, sk, slot));
   // short vectors: one lane per entry and vector (KIND 0 / 1: 2n lanes, the
   // split layout of k_trip); long ones one lane per entry; up to
@@ -250,16 +300,16 @@ int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uin
                  16ull * nvec * ((n << np) + (da ? n : 0)));
 #define GKR_TRIP_CASE(KI, KK)                                                                                 \
   if (kind == KI && K == KK)                                                                                  \
-    return split ? launch_trip_k<KI, KK, true>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks) \
-                 : launch_trip_k<KI, KK, false>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks);
+    return split ? launch_trip_k<KI, KK, true>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks, w) \
+                 : launch_trip_k<KI, KK, false>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks, w);
   GKR_TRIP_CASE(0, 1) GKR_TRIP_CASE(0, 2) GKR_TRIP_CASE(0, 3)
   GKR_TRIP_CASE(1, 0) GKR_TRIP_CASE(1, 1) GKR_TRIP_CASE(1, 2) GKR_TRIP_CASE(1, 3)
   GKR_TRIP_CASE(2, 1) GKR_TRIP_CASE(2, 2) GKR_TRIP_CASE(2, 3)
 #undef GKR_TRIP_CASE
   return fail(GKR_ERR_DEVICE, "no trip kernel for kind %d, K %d", kind, K);
 }
-int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out) {
-  TRY(wait_result<0>(c, sk.seq, nullptr, K_HOST_WAIT, 0));
+int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out, uint32_t want) {
+  TRY(wait_result<0>(c, sk.seq, nullptr, K_HOST_WAIT, 0, want));
   const int slot = (int)(sk.out - c->h_out);
   for (int q = 0; q < nq; q++) out[q] = c->h_out[slot + q];
   return GKR_OK;
@@ -347,6 +397,7 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   }
   for (int s = 0; s < S_NSLOTS; s++)
     if (c->buf[s]) (void)hipFree(c->buf[s]);
+  for (auto& t : c->dev_tables) (void)hipFree(t.second);
   if (c->merkle_consts) (void)hipFree(c->merkle_consts);
   if (c->h_res) (void)hipHostFree(c->h_res);
   if (c->h_mult) (void)hipHostFree(c->h_mult);

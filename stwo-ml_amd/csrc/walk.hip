@@ -19,22 +19,30 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
     if (st.kind == GKR_STEP_MATMUL) {
       if (!st.b) return fail(GKR_ERR_INVALID, "step %zu: null weight matrix", si);
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.b->cols)));
+      const int T = log2_exact(next_pow2(st.a->cols));
+      // a fresh claim with k > 1: its value comes out of the layer proof's first trip
+      const bool fused = st.claim == GKR_CLAIM_FRESH && T > 0;
       if (st.claim == GKR_CLAIM_FRESH) {
         point.resize(nv);
         {
           HostTimer ht(c, K_HOST_DRAW);
           TRY(gkr_channel_draw_qm31s(ch, nv, point.data()));
         }
-        TRY(gkr_matmul_output_claim(c, st.a, st.b, point.data(), nv, &value));
-        ch->ch.mix_secure_field(Q(value));
+        if (!fused) {
+          TRY(gkr_matmul_output_claim(c, st.a, st.b, point.data(), nv, &value));
+          ch->ch.mix_secure_field(Q(value));
+        }
       } else if (!have_claim) {
         return fail(GKR_ERR_INVALID, "step %zu: chained claim but no previous claim", si);
       }
-      const int T = log2_exact(next_pow2(st.a->cols));
       rp.resize(3 * (size_t)(T > 0 ? T : 1));
       gkr_qm31 fa, fb, nval;
-      TRY(gkr_prove_matmul_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.b, ch, proof, rp.data(),
-                                 &fa, &fb, npnt.data(), &nval));
+      if (fused)
+        TRY(walk_matmul_fresh(c, point.data(), (uint32_t)point.size(), &value, st.a, st.b, ch, proof, rp.data(), &fa,
+                              &fb, npnt.data(), &nval));
+      else
+        TRY(gkr_prove_matmul_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.b, ch, proof,
+                                   rp.data(), &fa, &fb, npnt.data(), &nval));
       const uint32_t nn = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + T);
       point.assign(npnt.begin(), npnt.begin() + nn);
       value = nval;
