@@ -510,8 +510,8 @@ struct AheadTrips {
   bool enabled() const { return !c->noalloc; }
   int make(TripWait* tw) {
     uint32_t* words;
-    TRY(ensureT(c, S_TRIPMB, 16, &words));  // flags[0..1], then kTripMaxK challenges at 16-byte offset
-    if (!c->tripmb_valid) {  // fresh memory: no flag may hold a future sequence number
+    TRY(ensureT(c, S_TRIPMB, 16, &words));  // status word, then kTripMaxK challenges at 16-byte offset
+    if (!c->tripmb_valid) {  // fresh memory: the status may not hold a future sequence number
       hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, c->stream, words, 16u);
       TRY(check_launch());
       c->tripmb_valid = true;
@@ -519,7 +519,7 @@ struct AheadTrips {
     tw->mb = c->mailbox;
     tw->want = alloc_seq(&c->mb_seq, 1);
     tw->spin_limit = kWaitSpinLimit;
-    tw->flags = words;
+    tw->status = words;
     tw->chal = reinterpret_cast<qm31*>(words + 4);
     outstanding++;
     return GKR_OK;

@@ -284,58 +284,41 @@ struct Mailbox {
   uint32_t pad[2];
   qm31 alpha[kTripMaxK];
 };
-// A trip launched ahead: workgroup 0 waits for mailbox sequence `want`, copies
-// the np challenges to `chal` (device memory) and releases flags[0] = want,
-// or flags[1] = want when its wait ended without them; the other workgroups
-// wait for either flag (device memory, so the host mailbox sees one poller).
-// Each context's wants are distinct, so a flag left by an earlier launch
-// never matches.  mb == nullptr: the challenges are the kernel's arguments.
+// A trip launched ahead of its challenges: k_mailbox_wait, queued right
+// before it, waits for mailbox sequence `want`, copies the posted challenges
+// to `chal` (device memory) and sets status[0] = want; the trip reads them
+// there (the kernel boundary orders the copy before the trip).  When the wait
+// ends without them (cancel code or spin limit) the status is left alone and
+// the trip returns at once.  Each context's wants are distinct, so a status
+// left by an earlier launch never matches.  chal == nullptr: the challenges
+// are the trip's arguments.
 struct TripWait {
-  const Mailbox* mb;
+  Mailbox* mb;
   uint32_t want, spin_limit;
-  uint32_t* flags;
+  uint32_t* status;
   qm31* chal;
 };
-// Thread 0 of a workgroup: the np challenges of a trip launched ahead into
-// out[0 .. np); false when the wait ended without them.
-static __device__ __noinline__ bool trip_wait(const TripWait& tw, int np, qm31* out) {
-  if (blockIdx.x == 0) {
-    bool ok = false;
-    for (uint32_t spins = 0; spins < tw.spin_limit; spins++) {
-      const uint32_t got = __hip_atomic_load(&tw.mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-      if (got == tw.want) {
-        ok = true;
-        break;
-      }
-      if (got == kWaitCancel) break;
-      __builtin_amdgcn_s_sleep(1);
+static __global__ void k_mailbox_wait(TripWait tw, int np) {
+  if (threadIdx.x != 0) return;
+  bool ok = false;
+  for (uint32_t spins = 0; spins < tw.spin_limit; spins++) {
+    const uint32_t got = __hip_atomic_load(&tw.mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (got == tw.want) {
+      ok = true;
+      break;
     }
-    if (ok) {
-      for (int r = 0; r < np; r++) {  // read after the acquiring read of seq
-        const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&tw.mb->alpha[r]));
-        out[r] = qm31{q[0], q[1], q[2], q[3]};
-        st_q_dev(tw.chal + r, out[r]);
-      }
-      wait_memory();
-      __hip_atomic_store(&tw.flags[0], tw.want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      __hip_atomic_store(const_cast<uint32_t*>(&tw.mb->expired), tw.want, __ATOMIC_RELEASE,
-                         __HIP_MEMORY_SCOPE_SYSTEM);
-      __hip_atomic_store(&tw.flags[1], tw.want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    return ok;
-  }
-  // twice workgroup 0's poll count: workgroup 0 always releases one of the
-  // flags within its own limit
-  for (uint32_t spins = 0; spins / 2 < tw.spin_limit; spins++) {
-    if (__hip_atomic_load(&tw.flags[0], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == tw.want) {
-      for (int r = 0; r < np; r++) out[r] = ld_q_dev(tw.chal + r);
-      return true;
-    }
-    if (__hip_atomic_load(&tw.flags[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == tw.want) return false;
+    if (got == kWaitCancel) break;
     __builtin_amdgcn_s_sleep(1);
   }
-  return false;
+  if (!ok) {
+    __hip_atomic_store(&tw.mb->expired, tw.want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    return;
+  }
+  for (int r = 0; r < np; r++) {  // read after the acquiring read of seq
+    const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&tw.mb->alpha[r]));
+    tw.chal[r] = qm31{q[0], q[1], q[2], q[3]};
+  }
+  tw.status[0] = tw.want;
 }
 
 // t + (t of lane l ^ m), for every lane.  m = 8: DPP row rotation by 8 (the
@@ -423,13 +406,11 @@ static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__
                                                  const qm31* __restrict__ eq_lo, int eq_h, RoundSink sk,
                                                  uint32_t* counter, uint32_t count_base, uint64_t b_rows,
                                                  int b_chunks, TripWait tw) {
-  if (tw.mb) {  // launched ahead: the pending challenges come through the mailbox
-    __shared__ qm31 s_al[kTripMaxK];
-    __shared__ bool s_ok;
-    if (threadIdx.x == 0) s_ok = trip_wait(tw, np, s_al);
-    __syncthreads();
-    if (!s_ok) return;  // the whole workgroup: the host has given up on this trip
-    for (int r = 0; r < np; r++) al.c[r] = s_al[r];
+  if (tw.chal) {  // launched ahead: the pending challenges come from k_mailbox_wait
+    if (tw.status[0] != tw.want) return;  // the wait ended without them (every thread alike)
+#pragma unroll
+    for (int r = 0; r < kTripMaxK; r++)  // constant indices keep `al` in registers
+      if (r < np) al.c[r] = ld_q(tw.chal, r);
   }
   using S = TripShape<KIND, K, SPLIT>;
   constexpr int G = S::G, LX = S::LX, NA = S::NA;

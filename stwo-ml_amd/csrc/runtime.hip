@@ -263,6 +263,10 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
   uint32_t base = 0;
   if (GKR_TRIP_FUSED && grid <= kTripFusedMax)  // one launch: the last workgroup finishes
     TRY(arrival_counter(c, grid, &counter, &base));
+  if (tw.chal) {  // launched ahead: the challenges arrive through the mailbox
+    hipLaunchKernelGGL(k_mailbox_wait, dim3(1), dim3(64), 0, c->stream, tw, np);
+    TRY(check_launch());
+  }
   hipLaunchKernelGGL((k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
                      sk, counter, base, b_rows, b_chunks, tw);
   TRY(check_launch());
