@@ -80,7 +80,7 @@ inline bool felt_abi_canonical(const gkr_felt& f) {
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_TRIPMB, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW,
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_TRIPMB, S_LKINV, S_LKHIST, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW,
   S_LKARENA, S_LKFOLD, S_LKDESC, S_LKPART, S_LKRES, S_LKTAB,
   S_BIND, S_BINDEQ, S_BINDDESC, S_BINDPART, S_BINDRES, S_BINDVIRT, S_NSLOTS
 };

@@ -1320,57 +1320,175 @@ struct dot_acc {
   }
 };
 
+// The LogUp fractions of the table, inv[j] = 1 / (gamma - j - beta * f(j))
+// for j < size: an input entry whose masked value is j has exactly this
+// fraction, so the prepare pass gathers it and the table side weights it by
+// mult[j] (one inversion per table entry instead of one per input entry).
+static __global__ void k_logup_inv_table(const uint32_t* __restrict__ table_out, uint64_t size, qm31 gamma,
+                                         qm31 beta, qm31* __restrict__ inv) {
+  const uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= size) return;
+  const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(m31_from_u32((uint32_t)j))),
+                          qm31_mul_m31(beta, table_out[j]));
+  st_q(inv, j, qm31_inv(d));
+}
 // Pad the activation matrix to (prow x pcol), mask to the table range, look up
-// the table output, form d = gamma - in - beta*out and w = 1/d, count
-// multiplicities (gkr/prover.rs:6411-6475).  Per workgroup it accumulates
+// the table output, form d = gamma - in - beta*out and w = 1/d (gathered from
+// the inverted table), count multiplicities (gkr/prover.rs:6411-6475).  Per workgroup it accumulates
 // sum(w) and the MLE of the padded input at the claim point,
 // sum_p x_p * eq[p] (prover.rs:6411-6417), into a 2-value sink.
 static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
-    const uint32_t* __restrict__ table_out, uint32_t mask, qm31 gamma, qm31 beta, const qm31* __restrict__ eq_hi,
-    const qm31* __restrict__ eq_lo, int eq_h, uint32_t* __restrict__ masked_in, uint32_t* __restrict__ masked_out,
-    qm31* __restrict__ d_out, qm31* __restrict__ w_out, uint32_t* __restrict__ mult, RoundSink sink,
-    uint32_t* counter, uint32_t count_base) {
+    const uint32_t* __restrict__ table_out, const qm31* __restrict__ inv, uint32_t mask, qm31 gamma, qm31 beta,
+    const qm31* __restrict__ eq_hi, const qm31* __restrict__ eq_lo, int eq_h, uint32_t* __restrict__ masked_in,
+    uint32_t* __restrict__ masked_out, qm31* __restrict__ d_out, qm31* __restrict__ w_out,
+    uint32_t* __restrict__ mult, RoundSink sink, uint32_t* counter, uint32_t count_base) {
   const uint64_t lo_mask = (1ull << eq_h) - 1;
   qacc acc;
   acc.zero();
   dot_acc ie;
   ie.zero();
+  // kPrepBatch entries per thread and pass, every load of a pass in flight
+  // before its arithmetic (the entries of a thread are a grid stride apart)
+  constexpr int kPrepBatch = 4;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n; p += stride) {
-    const uint64_t r = p >> log_pcol, c = p & ((1ull << log_pcol) - 1);
-    const uint32_t x = (r < rows && c < cols) ? X[r * cols + c] : 0u;
-    const uint32_t mi = x & mask;
-    const uint32_t mo = table_out[mi];
-    masked_in[p] = mi;
-    masked_out[p] = mo;
-    const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(mi)), qm31_mul_m31(beta, mo));
-    const qm31 w = qm31_inv(d);
-    st_q(d_out, p, d);
-    st_q(w_out, p, w);
-    // zero padding all lands in bin 0; it is counted once below
-    if (r < rows && c < cols) atomicAdd(&mult[mi], 1u);
-    acc.add(w);
-    ie.add(m31_from_u32(x), qm31_mul(ld_q(eq_hi, p >> eq_h), ld_q(eq_lo, p & lo_mask)));
+  for (uint64_t p0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p0 < n; p0 += kPrepBatch * stride) {
+    uint32_t x[kPrepBatch];
+    bool real[kPrepBatch];
+#pragma unroll
+    for (int u = 0; u < kPrepBatch; u++) {
+      const uint64_t p = p0 + (uint64_t)u * stride;
+      const uint64_t r = p >> log_pcol, c = p & ((1ull << log_pcol) - 1);
+      real[u] = p < n && r < rows && c < cols;
+      x[u] = real[u] ? X[r * cols + c] : 0u;
+    }
+    uint32_t mo[kPrepBatch];
+    qm31 w[kPrepBatch], eh[kPrepBatch], el[kPrepBatch];
+#pragma unroll
+    for (int u = 0; u < kPrepBatch; u++) {
+      const uint64_t p = p0 + (uint64_t)u * stride;
+      const uint32_t mi = x[u] & mask;
+      mo[u] = table_out[mi];
+      w[u] = ld_q(inv, mi);
+      const uint64_t pe = p < n ? p : 0;
+      eh[u] = ld_q(eq_hi, pe >> eq_h);
+      el[u] = ld_q(eq_lo, pe & lo_mask);
+    }
+#pragma unroll
+    for (int u = 0; u < kPrepBatch; u++) {
+      const uint64_t p = p0 + (uint64_t)u * stride;
+      if (p < n) {
+        const uint32_t mi = x[u] & mask;
+        masked_in[p] = mi;
+        masked_out[p] = mo[u];
+        const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(mi)), qm31_mul_m31(beta, mo[u]));
+        st_q(d_out, p, d);
+        st_q(w_out, p, w[u]);
+        // zero padding all lands in bin 0; it is counted once below
+        if (mult && real[u]) atomicAdd(&mult[mi], 1u);
+        acc.add(w[u]);
+        ie.add(m31_from_u32(x[u]), qm31_mul(eh[u], el[u]));
+      }
+    }
   }
-  if (blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
+  if (mult && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
   qm31 v[2] = {acc.reduce(), ie.reduce()};
   sink_deliver<2>(v, sink, counter, count_base);
 }
-// Table side: sum_j mult_j / (gamma - j - beta*f(j)) over entries with mult_j > 0.
-static __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const uint32_t* __restrict__ table_out,
+// Multiplicities of a table of at most kHistBins entries without global
+// atomics (same-address atomics serialize; a uniform input has no repeats to
+// merge): workgroup g counts keys [g * kHistPerGroup, (g + 1) * kHistPerGroup)
+// in LDS, two 16-bit counters per word (a group has fewer than 2^16 keys, so
+// no counter carries into its neighbour), and writes its kHistBins / 2 words
+// to partial[g].  128 KB of LDS: one workgroup of kHistBlock threads per CU;
+// each thread has all its loads in flight before its LDS atomics.  n is a
+// multiple of 4.  Padding positions (row >= rows or column >= cols of the
+// rows x 2^log_pcol layout) are skipped: their key is 0, and counting them
+// here would serialize on one counter; the table pass adds them to bin 0.
+constexpr int kHistBins = 1 << 16;
+constexpr int kHistBlock = 1024;
+constexpr int kHistVecs = 8;  // u32x4 key loads per thread
+constexpr uint64_t kHistPerGroup = (uint64_t)kHistBlock * kHistVecs * 4;  // 32768 keys
+static_assert(kHistPerGroup < (1u << 16), "16-bit counters");
+static __global__ void __launch_bounds__(kHistBlock) k_logup_hist(const uint32_t* __restrict__ keys, uint64_t n,
+                                                           uint64_t rows, uint64_t cols, int log_pcol,
+                                                           uint32_t* __restrict__ partial) {
+  __shared__ uint32_t h[kHistBins / 2];
+  for (int i = threadIdx.x; i < kHistBins / 2; i += blockDim.x) h[i] = 0;
+  const u32x4* k4 = reinterpret_cast<const u32x4*>(keys);
+  const uint64_t q0 = (uint64_t)blockIdx.x * (kHistPerGroup / 4), nq = n / 4;
+  u32x4 k[kHistVecs];
+#pragma unroll
+  for (int v = 0; v < kHistVecs; v++) {
+    const uint64_t q = q0 + (uint64_t)v * kHistBlock + threadIdx.x;
+    k[v] = q < nq ? k4[q] : u32x4{0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};  // keys below kHistBins
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const uint64_t p = 4 * q + u;
+      if ((p >> log_pcol) >= rows || (p & ((1ull << log_pcol) - 1)) >= cols) k[v][u] = 0xffffffffu;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < kHistVecs; v++)
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (k[v][u] != 0xffffffffu) atomicAdd(&h[k[v][u] >> 1], (k[v][u] & 1) ? 0x10000u : 1u);
+  __syncthreads();
+  u32x4* out = reinterpret_cast<u32x4*>(partial + (uint64_t)blockIdx.x * (kHistBins / 2));
+  for (int i = threadIdx.x; i < kHistBins / 8; i += blockDim.x)
+    out[i] = u32x4{h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]};
+}
+// The table side in one pass over the size <= kHistBins bins (a thread takes
+// the two bins of one counter word): mult_j (the groups' counts added, eight
+// loads in flight at a time, and `pad` padding entries in bin 0), its QM31
+// copy for the multiplicity sumcheck,
+// the coherent host copy, and sum_j mult_j / (gamma - j - beta*f(j)).
+static __global__ void __launch_bounds__(kBlock) k_logup_table_pass(const uint32_t* __restrict__ partial, int groups,
+                                                             uint32_t pad, const qm31* __restrict__ inv, uint64_t size,
+                                                             qm31* __restrict__ mult_q, uint32_t* __restrict__ host_copy,
+                                                             RoundSink sink, uint32_t* counter, uint32_t count_base) {
+  qacc acc;
+  acc.zero();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t wi = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; 2 * wi < size; wi += stride) {
+    uint32_t m0 = 0, m1 = 0;
+    for (int g = 0; g < groups; g += 8) {
+      uint32_t w[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) w[u] = g + u < groups ? partial[(uint64_t)(g + u) * (kHistBins / 2) + wi] : 0u;
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        m0 += w[u] & 0xffffu;
+        m1 += w[u] >> 16;
+      }
+    }
+    if (wi == 0) m0 += pad;  // the padding entries, all in bin 0
+    const uint32_t m[2] = {m0, m1};
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const uint64_t j = 2 * wi + b;
+      if (j >= size) break;
+      st_q(mult_q, j, qm31_from_m31(m31_from_u32(m[b])));
+      host_copy[j] = m[b];
+      if (m[b]) acc.add(qm31_mul_m31(ld_q(inv, j), m31_from_u32(m[b])));
+    }
+  }
+  qm31 v[1] = {acc.reduce()};
+  sink_deliver<1>(v, sink, counter, count_base);
+}
+// Table side: sum_j mult_j / (gamma - j - beta*f(j)) over entries with mult_j > 0
+// (the fractions from k_logup_inv_table).
+static __global__ void __launch_bounds__(kBlock) k_logup_table_sum(const qm31* __restrict__ inv,
                                                             const uint32_t* __restrict__ mult, uint64_t size,
-                                                            qm31 gamma, qm31 beta, RoundSink sink,
-                                                            uint32_t* counter, uint32_t count_base) {
+                                                            RoundSink sink, uint32_t* counter, uint32_t count_base) {
   qacc acc;
   acc.zero();
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; j < size; j += stride) {
     const uint32_t m = mult[j];
     if (m == 0) continue;
-    const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(m31_from_u32((uint32_t)j))),
-                            qm31_mul_m31(beta, table_out[j]));
-    acc.add(qm31_mul_m31(qm31_inv(d), m31_from_u32(m)));
+    acc.add(qm31_mul_m31(ld_q(inv, j), m31_from_u32(m)));
   }
   qm31 v[1] = {acc.reduce()};
   sink_deliver<1>(v, sink, counter, count_base);

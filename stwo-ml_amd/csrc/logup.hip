@@ -252,7 +252,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   const uint32_t mask = (uint32_t)(tsize - 1);
 
   uint32_t *d_table, *d_mult, *d_min, *d_mout;
-  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *m0, *m1;
+  qm31 *d_d0, *d_d1, *d_w0, *d_w1, *m0, *m1, *d_inv;
   TRY(ensureT(c, S_MULT, tsize, &d_mult));
   TRY(ensureT(c, S_MIN, n, &d_min));
   TRY(ensureT(c, S_MOUT, n, &d_mout));
@@ -262,12 +262,18 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
   TRY(ensureT(c, S_M0, tsize, &m0));
   TRY(ensureT(c, S_M1, tsize / 2 + 1, &m1));
+  TRY(ensureT(c, S_LKINV, tsize, &d_inv));
   TRY(ensure_host_mult(c, tsize));
   TRY(device_table(c, tag, table_log, &d_table));
-  // the histogram starts from zero: the previous layer's conversion kernel
-  // cleared it, or it is cleared here
-  if (c->mult_zero_entries < tsize) HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
-  c->mult_zero_entries = 0;
+  // Multiplicities: tables of up to 2^16 entries are counted in LDS per
+  // workgroup (k_logup_hist) and added in the table pass; larger ones with
+  // global atomics into S_MULT, which starts from zero (the previous layer's
+  // conversion kernel cleared it, or it is cleared here).
+  const bool lds_hist = tsize <= (uint64_t)kHistBins && n >= 4;
+  if (!lds_hist) {
+    if (c->mult_zero_entries < tsize) HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
+    c->mult_zero_entries = 0;
+  }
   // eq(claim point, x) as the product of its high and low tables: the input
   // MLE at the claim point is accumulated by the prepare pass
   qm31 *eq_hi, *eq_lo;
@@ -292,6 +298,10 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   RoundSink sk_prep, sk_table, sk_mult0, sk_eq0;
   {
     HostTimer ht(c, K_HOST_LAUNCH);
+    // the table's fractions: one inversion per table entry
+    hipLaunchKernelGGL(k_logup_inv_table, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_table, tsize, gamma,
+                       beta, d_inv);
+    TRY(check_launch());
     TRY(make_sink(c, &sk_prep, kSlotPrep));
     uint32_t* counter;
     uint32_t base;
@@ -301,23 +311,39 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       // algorithmic bytes: the input, masked input and output written (8 per entry), d and w written
       TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 8 * n + 32 * n);
       hipLaunchKernelGGL(k_logup_prepare, dim3(grid), dim3(kBlock), 0, c->stream, input->dev, input->rows,
-                         input->cols, log2_exact(pcol), n, d_table, mask, gamma, beta, eq_hi, eq_lo, eq_h, d_min,
-                         d_mout, d_d0, d_w0, d_mult, sk_prep, counter, base);
+                         input->cols, log2_exact(pcol), n, d_table, d_inv, mask, gamma, beta, eq_hi, eq_lo, eq_h,
+                         d_min, d_mout, d_d0, d_w0, lds_hist ? nullptr : d_mult, sk_prep, counter, base);
       TRY(deliver_finish<2>(c, sk_prep, grid, counter));
     }
     TRY(make_sink(c, &sk_table, kSlotTable));
-    {
+    if (lds_hist) {
+      // counts of the masked input (the padding added to bin 0 afterwards),
+      // then one pass over the bins: multiplicities, their QM31 and host
+      // copies, table sum
+      const uint64_t groups = (n + kHistPerGroup - 1) / kHistPerGroup;
+      uint32_t* hist;
+      TRY(ensureT(c, S_LKHIST, groups * (kHistBins / 2), &hist));
+      hipLaunchKernelGGL(k_logup_hist, dim3((unsigned)groups), dim3(kHistBlock), 0, c->stream, d_min, n, input->rows,
+                         input->cols, log2_exact(pcol), hist);
+      TRY(check_launch());
+      const unsigned grid = partial_grid(tsize / 2);
+      TRY(deliver_args(c, grid, &counter, &base));
+      hipLaunchKernelGGL(k_logup_table_pass, dim3(grid), dim3(kBlock), 0, c->stream, hist, (int)groups,
+                         (uint32_t)(n - input->rows * input->cols), d_inv, tsize, m0, c->h_mult, sk_table, counter,
+                         base);
+      TRY(deliver_finish<1>(c, sk_table, grid, counter));
+    } else {
       const unsigned grid = partial_grid(tsize);
       TRY(deliver_args(c, grid, &counter, &base));
-      hipLaunchKernelGGL(k_logup_table_sum, dim3(grid), dim3(kBlock), 0, c->stream, d_table, d_mult, tsize, gamma,
-                         beta, sk_table, counter, base);
+      hipLaunchKernelGGL(k_logup_table_sum, dim3(grid), dim3(kBlock), 0, c->stream, d_inv, d_mult, tsize, sk_table,
+                         counter, base);
       TRY(deliver_finish<1>(c, sk_table, grid, counter));
+      // the multiplicities as QM31 for the sumcheck, and to the pinned host copy
+      hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0,
+                         c->h_mult, 1);
+      TRY(check_launch());
+      c->mult_zero_entries = tsize;
     }
-    // the multiplicities as QM31 for the sumcheck, and to the pinned host copy
-    hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0, c->h_mult,
-                       1);
-    TRY(check_launch());
-    c->mult_zero_entries = tsize;
   }
   const std::vector<Trip> mtrips = plan_trips((int)table_log, kHostTailSum, kTripMaxK);
   TRY(launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
