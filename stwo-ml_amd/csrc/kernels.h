@@ -1304,6 +1304,12 @@ struct dot_acc {
 #pragma unroll
     for (int c = 0; c < 4; c++) lo[c] = hi[c] = 0;
   }
+  __device__ __forceinline__ void add(const qm31& v) {  // a canonical QM31 term
+    lo[0] += v.a;
+    lo[1] += v.b;
+    lo[2] += v.c;
+    lo[3] += v.d;
+  }
   __device__ __forceinline__ void add(uint32_t x, const qm31& e) {
     const uint64_t t[4] = {(uint64_t)x * e.a, (uint64_t)x * e.b, (uint64_t)x * e.c, (uint64_t)x * e.d};
 #pragma unroll
@@ -1350,8 +1356,15 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
   ie.zero();
   // kPrepBatch entries per thread and pass, every load of a pass in flight
   // before its arithmetic (the entries of a thread are a grid stride apart)
-  constexpr int kPrepBatch = 4;
+  constexpr int kPrepBatch = 2;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  // eq(z, p) = hi[p >> eq_h] * lo[p & lo_mask]: when the grid stride is a
+  // multiple of 2^eq_h every entry of a thread has the same low index, so the
+  // thread adds x_p * hi[p >> eq_h] (M31 times QM31) and multiplies by its lo
+  // value once at the end
+  const bool lo_fixed = (stride & lo_mask) == 0;
+  dot_acc ih;
+  ih.zero();
   for (uint64_t p0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p0 < n; p0 += kPrepBatch * stride) {
     uint32_t x[kPrepBatch];
     bool real[kPrepBatch];
@@ -1372,7 +1385,7 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
       w[u] = ld_q(inv, mi);
       const uint64_t pe = p < n ? p : 0;
       eh[u] = ld_q(eq_hi, pe >> eq_h);
-      el[u] = ld_q(eq_lo, pe & lo_mask);
+      if (!lo_fixed) el[u] = ld_q(eq_lo, pe & lo_mask);
     }
 #pragma unroll
     for (int u = 0; u < kPrepBatch; u++) {
@@ -1387,9 +1400,16 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
         // zero padding all lands in bin 0; it is counted once below
         if (mult && real[u]) atomicAdd(&mult[mi], 1u);
         acc.add(w[u]);
-        ie.add(m31_from_u32(x[u]), qm31_mul(eh[u], el[u]));
+        if (lo_fixed)
+          ih.add(m31_from_u32(x[u]), eh[u]);
+        else
+          ie.add(m31_from_u32(x[u]), qm31_mul(eh[u], el[u]));
       }
     }
+  }
+  if (lo_fixed) {  // this thread's low index: its first entry's (a thread past n added nothing)
+    const uint64_t p0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p0 < n) ie.add(qm31_mul(ih.reduce(), ld_q(eq_lo, p0 & lo_mask)));
   }
   if (mult && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
   qm31 v[2] = {acc.reduce(), ie.reduce()};
