@@ -456,15 +456,23 @@ constexpr unsigned kTripMaxBlocks = GKR_TRIP_MAX_BLOCKS;  // partial rows per tr
 constexpr unsigned kTripMaxBlocksShort = GKR_TRIP_MAX_BLOCKS_SHORT;  // the same for trips of at most 2 rounds
 static_assert(GKR_TRIP_MAX_BLOCKS_SHORT <= kMaxPartialBlocks && GKR_TRIP_MAX_BLOCKS <= kMaxPartialBlocks,
               "trip partial rows exceed the partial buffer");
-// Trips whose one-entry-per-thread grid is at most kTripFusedGrid workgroups
-// run on at most kTripFusedMax workgroups and finish in the kernel itself.
+// Result delivery of the reducing kernels: k_finish / k_finish_wide launched
+// behind them.  With GKR_TRIP_FUSED=1, trips whose one-entry-per-thread grid
+// is at most kTripFusedGrid workgroups run on at most kTripFusedMax
+// workgroups and finish in the kernel itself (an arrival counter, the last
+// workgroup adds the rows); measured on MI355X this is slower than the
+// finisher kernel (the Qwen layer's trips: 450 us with fused trips of up to
+// 256 workgroups, 402 us plus one kernel boundary per trip without), so it
+// is off.  Vectors of at most kTripSplitLanes / 2 entries use the
+// two-lanes-per-entry layout.
 #ifndef GKR_TRIP_FUSED
-#define GKR_TRIP_FUSED 1
+#define GKR_TRIP_FUSED 0
 #endif
 #ifndef GKR_TRIP_FUSED_GRID
-#define GKR_TRIP_FUSED_GRID 256
+#define GKR_TRIP_FUSED_GRID 64
 #endif
 constexpr unsigned kTripFusedGrid = GKR_TRIP_FUSED_GRID;
+constexpr uint64_t kTripSplitLanes = 256ull * kBlock;
 std::vector<Trip> plan_trips(int T, uint64_t host_len, int k0);
 static inline int trip_nq(int kind, int K) { return kind == 2 ? (1 << K) : (1 << (2 * K)); }
 // eqlin(z, X) = (1 - z)(1 - X) + z X, the multilinear eq factor of one coordinate.

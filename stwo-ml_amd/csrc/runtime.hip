@@ -146,13 +146,13 @@ int arrival_counter(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* bas
   c->trip_count += grid;
   return GKR_OK;
 }
-// Delivery of a reducing kernel's sums: by the kernel itself for grids of at
-// most kTripFusedMax workgroups (an arrival counter), else by k_finish
-// launched behind it (deliver_finish).
+// Delivery of a reducing kernel's sums: by k_finish launched behind it
+// (deliver_finish), or, with GKR_TRIP_FUSED=1 and grids of at most
+// kTripFusedMax workgroups, by the kernel itself (an arrival counter).
 int deliver_args(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base) {
   *counter = nullptr;
   *base = 0;
-  if (grid > kTripFusedMax) return GKR_OK;
+  if (!GKR_TRIP_FUSED || grid > kTripFusedMax) return GKR_OK;
   return arrival_counter(c, grid, counter, base);
 }
 // MLEs of two M31 vectors of n = 2^nv entries at z (one eq split, one pass).
@@ -294,7 +294,7 @@ int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uin
   // short vectors: one lane per entry and vector (KIND 0 / 1: 2n lanes, the
   // split layout of k_trip); long ones one lane per entry; up to
   // kTripMaxBlocks workgroups
-  const bool split = kind != 2 && 2 * n <= (uint64_t)kTripFusedGrid * kBlock;
+  const bool split = kind != 2 && 2 * n <= kTripSplitLanes;
   unsigned grid = partial_grid(split ? 2 * n : n);
   const unsigned max_blocks = K <= 2 ? kTripMaxBlocksShort : kTripMaxBlocks;
   if (grid > max_blocks) grid = max_blocks;
