@@ -374,7 +374,7 @@ struct HandoverSession {
   explicit HandoverSession(gkr_ctx* c_) : c(c_) {}
   // Launch k_handover<NV> over the vectors a (, b) of length len, to be folded by k challenges.
   template <int NV>
-  int launch(const qm31* a, const qm31* b, uint64_t len, int k) {
+  int launch(const qm31* a, const qm31* b, uint64_t len, int k, const CarriedFinish* fin = nullptr) {
     HostTimer ht(c, K_HOST_LAUNCH);
     if (len > (uint64_t)kHandMax || k < 0 || k > kTripMaxK || (len >> k) == 0)
       return fail(GKR_ERR_DEVICE, "hand-over of %llu entries folded %d times", (unsigned long long)len, k);
@@ -390,8 +390,10 @@ struct HandoverSession {
       cancel_before_post = true;
       c->debug_handover_cancel = false;
     }
+    CarriedFinish none;
+    memset(&none, 0, sizeof none);
     hipLaunchKernelGGL(k_handover<NV>, dim3(1), dim3(kBlock), 0, c->stream, a, b, (uint32_t)len, k, c->mailbox,
-                       mb_seq, spin_limit, c->h_vec, c->h_flag, res_seq);
+                       mb_seq, spin_limit, c->h_vec, c->h_flag, res_seq, fin ? *fin : none);
     launched = true;
     return check_launch();
   }
@@ -496,9 +498,13 @@ void trip_round_gram(const qm31* G, int K, int j, const qm31* r, int nx, const q
 void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out);
 // tw given: the trip is launched ahead of its np pending challenges, which
 // it takes from the mailbox (pend unused).
+// carry_out given: no finisher is launched; the rows' finishing is described
+// there for the next kernel of the chain (carry_in of the next trip launched
+// ahead, or the hand-over), which adds them before it waits.
 int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
                        const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
-                       RoundSink* sk, uint64_t b_rows = 0, int b_chunks = 0, const TripWait* tw = nullptr);
+                       RoundSink* sk, uint64_t b_rows = 0, int b_chunks = 0, const TripWait* tw = nullptr,
+                       CarriedFinish* carry_out = nullptr, const CarriedFinish* carry_in = nullptr);
 // Wait for a trip's nq sums (want: the mailbox sequence of a trip launched
 // ahead, whose expired wait is then reported at once).
 int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out, uint32_t want = 0);

@@ -298,7 +298,53 @@ struct TripWait {
   uint32_t* status;
   qm31* chal;
 };
-static __global__ void k_mailbox_wait(TripWait tw, int np) {
+// A trip's finishing carried by the next kernel of the chain (the next trip's
+// mailbox wait or the hand-over): the work of k_finish_wide on nblocks partial
+// rows of nq values (nq a power of two <= 64; nblocks == 0: nothing carried).
+// status given (a trip launched ahead): the rows are delivered only if that
+// trip's wait ended with its challenges (status[0] == want); otherwise the
+// trip returned without computing them and nothing is published.
+struct CarriedFinish {
+  RoundSink sk;
+  uint32_t nblocks, nq;
+  const uint32_t* status;
+  uint32_t want;
+};
+// The whole block (NT threads, a multiple of nq) adds the rows and delivers
+// them to sk.out, then publishes sk.seq.
+template <int NT>
+__device__ __forceinline__ void finish_carried(const CarriedFinish& f) {
+  if (f.status && f.status[0] != f.want) return;  // every thread alike
+  const int nq = (int)f.nq, rg = NT / nq;
+  const int q = threadIdx.x % nq, g = threadIdx.x / nq;
+  qacc acc;
+  acc.zero();
+  uint32_t b = g;
+  for (; b + 3 * rg < f.nblocks; b += 4 * rg) {
+    const qm31 v0 = ld_q(f.sk.partials, (uint64_t)nq * b + q);
+    const qm31 v1 = ld_q(f.sk.partials, (uint64_t)nq * (b + rg) + q);
+    const qm31 v2 = ld_q(f.sk.partials, (uint64_t)nq * (b + 2 * rg) + q);
+    const qm31 v3 = ld_q(f.sk.partials, (uint64_t)nq * (b + 3 * rg) + q);
+    acc.add(v0);
+    acc.add(v1);
+    acc.add(v2);
+    acc.add(v3);
+  }
+  for (; b < f.nblocks; b += rg) acc.add(ld_q(f.sk.partials, (uint64_t)nq * b + q));
+  __shared__ qm31 fsh[NT];
+  fsh[threadIdx.x] = acc.reduce();
+  __syncthreads();
+  for (int step = rg / 2; step >= 1; step /= 2) {  // tree over the row groups
+    if (g < step) fsh[threadIdx.x] = qm31_add(fsh[threadIdx.x], fsh[threadIdx.x + step * nq]);
+    __syncthreads();
+  }
+  if (threadIdx.x < nq) f.sk.out[threadIdx.x] = fsh[threadIdx.x];
+  __syncthreads();
+  if (threadIdx.x == 0) publish_flag(f.sk.flag, f.sk.seq);
+}
+constexpr int kWaitBlock = 256;
+static __global__ void __launch_bounds__(kWaitBlock) k_mailbox_wait(TripWait tw, int np, CarriedFinish fin) {
+  if (fin.nblocks) finish_carried<kWaitBlock>(fin);  // the previous trip's sums first (the host needs them)
   if (threadIdx.x != 0) return;
   bool ok = false;
   for (uint32_t spins = 0; spins < tw.spin_limit; spins++) {
@@ -619,7 +665,8 @@ template <int NV>
 static __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restrict__ a, const qm31* __restrict__ b,
                                                      uint32_t len, int k, Mailbox* mb, uint32_t want,
                                                      uint32_t spin_limit, qm31* vec_out, uint32_t* flag,
-                                                     uint32_t seq) {
+                                                     uint32_t seq, CarriedFinish fin) {
+  if (fin.nblocks) finish_carried<kBlock>(fin);  // the last trip's sums first (the host needs them)
   __shared__ qm31 v[NV][kHandMax];
   __shared__ qm31 sh_al[kTripMaxK];
   __shared__ bool sh_ok;

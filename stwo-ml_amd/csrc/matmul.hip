@@ -271,6 +271,10 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
   const bool pre = ahead.enabled();
   const qm31* src_a = in_a;
   const qm31* src_b = in_b;
+  // Launched ahead, each trip's rows are added by the next kernel of the chain
+  // (the next trip's mailbox wait, or the hand-over) instead of a finisher.
+  CarriedFinish carry;
+  memset(&carry, 0, sizeof carry);
   auto launch_j = [&](size_t j, const qm31* pend) -> int {
     const Trip& tr = trips[j];
     qm31* da = j == 0 ? nullptr : bufs_a[(j - 1) & 1];
@@ -281,17 +285,19 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
       TRY(ahead.make(&tws[j]));
       tw = &tws[j];
     }
+    const CarriedFinish carry_in = carry;
+    CarriedFinish* carry_out = pre ? &carry : nullptr;
     if (j == 0 && ft && ft->b_chunks)  // add the weight-side chunk partials and store f_b (in_b)
       TRY(launch_trip(c, 0, tr.K, src_a, ft->b_partials, tr.n, 0, nullptr, nullptr, const_cast<qm31*>(in_b),
-                      nullptr, nullptr, 0, 0, &sks[0], ft->b_rows, ft->b_chunks));
+                      nullptr, nullptr, 0, 0, &sks[0], ft->b_rows, ft->b_chunks, nullptr, carry_out));
     else
       TRY(launch_trip(c, 0, tr.K, src_a, src_b, tr.n, npj, pend, da, db, nullptr, nullptr, 0, 0, &sks[j], 0, 0,
-                      tw));
+                      tw, carry_out, tw ? &carry_in : nullptr));
     if (j > 0) {
       src_a = da;
       src_b = db;
     }
-    if (j + 1 == nt) TRY(ho.launch<2>(src_a, src_b, tr.n, tr.K));
+    if (j + 1 == nt) TRY(ho.launch<2>(src_a, src_b, tr.n, tr.K, pre ? &carry : nullptr));
     return GKR_OK;
   };
   if (g0) {

@@ -258,26 +258,40 @@ void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out) {
 template <int KIND, int K, bool SPLIT>
 static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n, int np, const TripChal& al,
                          qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, const RoundSink& sk,
-                         unsigned grid, uint64_t b_rows, int b_chunks, const TripWait& tw) {
+                         unsigned grid, uint64_t b_rows, int b_chunks, const TripWait& tw, CarriedFinish* carry_out,
+                         const CarriedFinish* carry_in) {
+  constexpr int NQ = TripShape<KIND, K, SPLIT>::NQ;
   uint32_t* counter = nullptr;
   uint32_t base = 0;
-  if (GKR_TRIP_FUSED && grid <= kTripFusedMax)  // one launch: the last workgroup finishes
+  if (!carry_out && GKR_TRIP_FUSED && grid <= kTripFusedMax)  // one launch: the last workgroup finishes
     TRY(arrival_counter(c, grid, &counter, &base));
   if (tw.chal) {  // launched ahead: the challenges arrive through the mailbox
-    hipLaunchKernelGGL(k_mailbox_wait, dim3(1), dim3(64), 0, c->stream, tw, np);
+    CarriedFinish none;
+    memset(&none, 0, sizeof none);
+    hipLaunchKernelGGL(k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, c->stream, tw, np, carry_in ? *carry_in : none);
     TRY(check_launch());
   }
   hipLaunchKernelGGL((k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
                      sk, counter, base, b_rows, b_chunks, tw);
   TRY(check_launch());
   if (counter) return GKR_OK;
-  constexpr int NQ = TripShape<KIND, K, SPLIT>::NQ;
+  if (carry_out) {  // the next kernel of the chain adds the rows
+    carry_out->sk = sk;
+    carry_out->nblocks = grid;
+    carry_out->nq = NQ;
+    carry_out->status = tw.chal ? tw.status : nullptr;
+    carry_out->want = tw.want;
+    return GKR_OK;
+  }
   hipLaunchKernelGGL(k_finish_wide<NQ>, dim3(1), dim3(kFinishBlock), 0, c->stream, sk, grid);
   return check_launch();
 }
 int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
                        const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
-                       RoundSink* sk, uint64_t b_rows, int b_chunks, const TripWait* tw) {
+                       RoundSink* sk, uint64_t b_rows, int b_chunks, const TripWait* tw, CarriedFinish* carry_out,
+                       const CarriedFinish* carry_in) {
+  if (carry_in && carry_in->nblocks && !tw)
+    return fail(GKR_ERR_DEVICE, "a carried finish needs a trip launched ahead");
   if (np < 0 || np > kTripMaxK || K < 0 || K > kTripMaxK || (n >> K) == 0 || (kind == 1) != (hi != nullptr) ||
       (b_chunks && (kind != 0 || np != 0 || b_rows > n)))
     return fail(GKR_ERR_DEVICE, "bad trip (kind %d, K %d, np %d, n %llu)", kind, K, np, (unsigned long long)n);
@@ -304,8 +318,10 @@ int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uin
                  16ull * nvec * ((n << np) + (da ? n : 0)));
 #define GKR_TRIP_CASE(KI, KK)                                                                                 \
   if (kind == KI && K == KK)                                                                                  \
-    return split ? launch_trip_k<KI, KK, true>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks, w) \
-                 : launch_trip_k<KI, KK, false>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks, w);
+    return split ? launch_trip_k<KI, KK, true>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks, w, \
+                                               carry_out, carry_in)                                              \
+                 : launch_trip_k<KI, KK, false>(c, sa, sb, n, np, al, da, db, hi, lo, h, *sk, grid, b_rows, b_chunks, w, \
+                                                carry_out, carry_in);
   GKR_TRIP_CASE(0, 1) GKR_TRIP_CASE(0, 2) GKR_TRIP_CASE(0, 3)
   GKR_TRIP_CASE(1, 0) GKR_TRIP_CASE(1, 1) GKR_TRIP_CASE(1, 2) GKR_TRIP_CASE(1, 3)
   GKR_TRIP_CASE(2, 1) GKR_TRIP_CASE(2, 2) GKR_TRIP_CASE(2, 3)
