@@ -670,7 +670,9 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
 int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl);
 // one trip,
 int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, const qm31* d, int np,
-                           const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk);
+                           const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk,
+                           const TripWait* tw = nullptr, CarriedFinish* carry_out = nullptr,
+                           const CarriedFinish* carry_in = nullptr);
 // the whole sumcheck.
 int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& pl, qm31* w0, qm31* d0,
                         qm31* w1, qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3],

@@ -94,11 +94,12 @@ int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
 // Launch trip j of the plan over sources w, d (np pending challenges pend),
 // folded vectors to dw, dd when given.
 int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, const qm31* d, int np,
-                           const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk) {
+                           const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk, const TripWait* tw,
+                           CarriedFinish* carry_out, const CarriedFinish* carry_in) {
   qm31* parts = (qm31*)c->buf[S_EQPARTS];
   const Trip& tr = pl.trips[j];
   return launch_trip(c, 1, tr.K, w, d, tr.n, np, pend, dw, dd, parts + pl.hi_off[j], parts + pl.lo_off[j], pl.h[j],
-                     slot, sk);
+                     slot, sk, 0, 0, tw, carry_out, carry_in);
 }
 // The sumcheck for claim point z over w0, d0 (overwritten: the trips' folded
 // vectors go to w1/d1 (n/2 entries) and w0/d0 alternately).  pre0: trip 0
@@ -136,29 +137,52 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
   qm31* bw[2] = {w1, w0};
   qm31* bd[2] = {d1, d0};
   HandoverSession ho(c);
+  AheadTrips ahead(c);
+  const size_t nt = pl.trips.size();
+  std::vector<RoundSink> sks(nt);
+  std::vector<TripWait> tws(nt);
+  // One trip ahead: trip j + 1 is launched (behind its mailbox wait, which also
+  // adds trip j's rows) while trip j runs, before the host posts trip j's
+  // challenges; the hand-over follows the last trip the same way.
+  const bool pre = ahead.enabled();
+  CarriedFinish carry;
+  memset(&carry, 0, sizeof carry);
   const qm31* sw = w0;
   const qm31* sd = d0;
+  auto launch_j = [&](size_t j, const qm31* pend_j) -> int {
+    const Trip& tr = pl.trips[j];
+    qm31* dw = j == 0 ? nullptr : bw[(j - 1) & 1];
+    qm31* dd = j == 0 ? nullptr : bd[(j - 1) & 1];
+    const TripWait* tw = nullptr;
+    if (j > 0 && pre) {
+      TRY(ahead.make(&tws[j]));
+      tw = &tws[j];
+    }
+    const CarriedFinish carry_in = carry;
+    TRY(eq3_launch_trip(c, pl, j, sw, sd, j == 0 ? 0 : pl.trips[j - 1].K, pend_j, dw, dd, 0, &sks[j], tw,
+                        pre ? &carry : nullptr, tw ? &carry_in : nullptr));
+    if (j > 0) {
+      sw = dw;
+      sd = dd;
+    }
+    if (j + 1 == nt) TRY(ho.launch<2>(sw, sd, tr.n, tr.K, pre ? &carry : nullptr));
+    return GKR_OK;
+  };
+  if (pre0) {  // trip 0 launched earlier, with its own finisher
+    sks[0] = *pre0;
+    if (nt == 1) TRY(ho.launch<2>(sw, sd, pl.trips[0].n, pl.trips[0].K));
+  } else {
+    TRY(launch_j(0, nullptr));
+  }
+  if (pre && nt > 1) TRY(launch_j(1, nullptr));
   int np = 0;
   const qm31* pend = nullptr;
   qm31 cpre = qm31_one();  // prod of eqlin(z_l, r_l) over the rounds done
-  for (size_t j = 0; j < pl.trips.size(); j++) {
+  for (size_t j = 0; j < nt; j++) {
     const Trip& tr = pl.trips[j];
-    const bool last = j + 1 == pl.trips.size();
     qm31 g[kMaxSums];
-    RoundSink sk;
-    if (j == 0 && pre0) {
-      sk = *pre0;
-    } else {
-      qm31* dw = j == 0 ? nullptr : bw[(j - 1) & 1];
-      qm31* dd = j == 0 ? nullptr : bd[(j - 1) & 1];
-      TRY(eq3_launch_trip(c, pl, j, sw, sd, np, pend, dw, dd, 0, &sk));
-      if (j > 0) {
-        sw = dw;
-        sd = dd;
-      }
-    }
-    if (last) TRY(ho.launch<2>(sw, sd, tr.n, tr.K));
-    TRY(wait_trip(c, sk, trip_nq(1, tr.K), g));
+    if (j > 0 && !pre) TRY(launch_j(j, pend));
+    TRY(wait_trip(c, sks[j], trip_nq(1, tr.K), g, j > 0 && pre ? tws[j].want : 0));
     for (int i = 0; i < tr.K; i++) {
       qm31 sums[4];
       {
@@ -170,6 +194,10 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
     for (int i = 0; i < tr.K; i++) cpre = qm31_mul(cpre, eqlin(z[tr.t + i], chal[tr.t + i]));
     np = tr.K;
     pend = chal + tr.t;
+    if (pre && j + 1 < nt) {
+      TRY(ahead.post(tws[j + 1], pend, np));
+      if (j + 2 < nt) TRY(launch_j(j + 2, nullptr));  // while trip j + 1 runs
+    }
   }
   const int t_end = pl.trips.back().t + pl.trips.back().K;
   const uint64_t hlen = 1ull << (nv - t_end);
@@ -399,24 +427,41 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   {
     // trips of up to 3 rounds (the first launched ahead above), then the host
     HandoverSession ho(c);
+    AheadTrips ahead(c);
+    const size_t nt = mtrips.size();
+    std::vector<RoundSink> sks(nt);
+    std::vector<TripWait> tws(nt);
+    sks[0] = sk_mult0;  // launched above, with its own finisher
+    // one trip ahead, as in the eq-sumcheck
+    const bool pre = ahead.enabled();
+    CarriedFinish carry;
+    memset(&carry, 0, sizeof carry);
     const qm31* src = m0;
+    auto launch_j = [&](size_t j, const qm31* pend_j) -> int {  // j >= 1
+      const Trip& tr = mtrips[j];
+      qm31* dst = bm[(j - 1) & 1];
+      const TripWait* tw = nullptr;
+      if (pre) {
+        TRY(ahead.make(&tws[j]));
+        tw = &tws[j];
+      }
+      const CarriedFinish carry_in = carry;
+      TRY(launch_trip(c, 2, tr.K, src, nullptr, tr.n, mtrips[j - 1].K, pend_j, dst, nullptr, nullptr, nullptr, 0, 0,
+                      &sks[j], 0, 0, tw, pre ? &carry : nullptr, tw ? &carry_in : nullptr));
+      src = dst;
+      if (j + 1 == nt) TRY(ho.launch<1>(src, nullptr, tr.n, tr.K, pre ? &carry : nullptr));
+      return GKR_OK;
+    };
+    if (nt == 1) TRY(ho.launch<1>(src, nullptr, mtrips[0].n, mtrips[0].K));
+    if (pre && nt > 1) TRY(launch_j(1, nullptr));
     int np = 0;
     const qm31* pend = nullptr;
     std::vector<qm31> mchal(table_log);
-    for (size_t j = 0; j < mtrips.size(); j++) {
+    for (size_t j = 0; j < nt; j++) {
       const Trip& tr = mtrips[j];
-      const bool last = j + 1 == mtrips.size();
-      RoundSink sk;
-      if (j == 0) {
-        sk = sk_mult0;
-      } else {
-        qm31* dst = bm[(j - 1) & 1];
-        TRY(launch_trip(c, 2, tr.K, src, nullptr, tr.n, np, pend, dst, nullptr, nullptr, nullptr, 0, 0, &sk));
-        src = dst;
-      }
-      if (last) TRY(ho.launch<1>(src, nullptr, tr.n, tr.K));
+      if (j > 0 && !pre) TRY(launch_j(j, pend));
       qm31 g[kMaxSums];
-      TRY(wait_trip(c, sk, trip_nq(2, tr.K), g));
+      TRY(wait_trip(c, sks[j], trip_nq(2, tr.K), g, j > 0 && pre ? tws[j].want : 0));
       for (int i = 0; i < tr.K; i++) {
         qm31 sums[2];
         {
@@ -428,6 +473,10 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       }
       np = tr.K;
       pend = mchal.data() + tr.t;
+      if (pre && j + 1 < nt) {
+        TRY(ahead.post(tws[j + 1], pend, np));
+        if (j + 2 < nt) TRY(launch_j(j + 2, nullptr));  // while trip j + 1 runs
+      }
     }
     const int t_end = mtrips.back().t + mtrips.back().K;
     std::vector<qm31> v[1];
