@@ -101,6 +101,7 @@ constexpr int kSlotEq0 = 64;     // eq-sumcheck trip 0 (up to 64 values)
 constexpr int kSlotPrep = 128;   // LogUp prepare: trace sum, input MLE
 constexpr int kSlotTable = 130;  // LogUp table-side sum
 constexpr int kSlotMult0 = 136;  // multiplicity sumcheck trip 0 (up to 8 values)
+constexpr int kSlotIO = 144;     // LogUp input / output MLEs at the eq-sumcheck challenges
 constexpr int kOutSlots = 192;
 
 struct KernelStat {
@@ -282,6 +283,8 @@ int eq_split(gkr_ctx* c, const qm31* r, int n, qm31** hi, qm31** lo, int* h);
 int arrival_counter(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base);
 int deliver_args(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base);
 int dot2_evals(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uint32_t* v1, qm31 out[2]);
+// The same pass, launched only: its two values arrive in host slot `slot` (wait_sink<2>).
+int dot2_launch(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uint32_t* v1, int slot, RoundSink* sk);
 
 // eq(r, x) for x < count (r[0] on the most significant bit of x).
 int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out);

@@ -397,13 +397,12 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(eq3_sumcheck(c, C, cpt.data(), epl, d_w0, d_d0, d_w1, d_d1, out->eq_round_polys, chal.data(), fin,
                    eq_pre ? &sk_eq0 : nullptr));
   const qm31 w_eval = fin[1];
-  // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass
-  qm31 io[2];
-  TRY(dot2_evals(c, chal.data(), nv, d_min, d_mout, io));
-  const qm31 in_eval = io[0], out_eval = io[1];
+  // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass;
+  // the transcript does not use them before the multiplicity sumcheck, so they
+  // are read after it
+  RoundSink sk_io;
+  TRY(dot2_launch(c, chal.data(), nv, d_min, d_mout, kSlotIO, &sk_io));
   out->w_eval = G(w_eval);
-  out->in_eval = G(in_eval);
-  out->out_eval = G(out_eval);
 
   // Multiplicity sumcheck (prover.rs:9449-9511): degree-1 rounds over
   // 2^table_log entries.  The multiplicities reached the pinned copy before
@@ -500,6 +499,11 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     }
     mfin[0] = V[0];
   }
+  qm31 io[2];
+  TRY(wait_sink<2>(c, sk_io, io));  // delivered before the multiplicity trips' results
+  const qm31 in_eval = io[0], out_eval = io[1];
+  out->in_eval = G(in_eval);
+  out->out_eval = G(out_eval);
   out->mult_final_eval = G(mfin[0]);
   out->mult_claimed_sum = G(mult_sum);
 

@@ -156,19 +156,22 @@ int deliver_args(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base) 
   return arrival_counter(c, grid, counter, base);
 }
 // MLEs of two M31 vectors of n = 2^nv entries at z (one eq split, one pass).
-int dot2_evals(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uint32_t* v1, qm31 out[2]) {
+int dot2_launch(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uint32_t* v1, int slot, RoundSink* sk) {
   const uint64_t n = 1ull << nv;
   qm31 *hi, *lo;
   int h;
   TRY(eq_split(c, z, nv, &hi, &lo, &h));
-  RoundSink sk;
-  TRY(make_sink(c, &sk));
+  TRY(make_sink(c, sk, slot));
   const unsigned grid = partial_grid(n);
   uint32_t* counter;
   uint32_t base;
   TRY(deliver_args(c, grid, &counter, &base));
-  hipLaunchKernelGGL(k_dot2_m31, dim3(grid), dim3(kBlock), 0, c->stream, v0, v1, hi, lo, h, n, sk, counter, base);
-  TRY(deliver_finish<2>(c, sk, grid, counter));
+  hipLaunchKernelGGL(k_dot2_m31, dim3(grid), dim3(kBlock), 0, c->stream, v0, v1, hi, lo, h, n, *sk, counter, base);
+  return deliver_finish<2>(c, *sk, grid, counter);
+}
+int dot2_evals(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uint32_t* v1, qm31 out[2]) {
+  RoundSink sk;
+  TRY(dot2_launch(c, z, nv, v0, v1, 0, &sk));
   return wait_sink<2>(c, sk, out);
 }
 int make_sink(gkr_ctx* c, RoundSink* sk, int slot) {
