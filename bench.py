@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 P = (1 << 31) - 1  # M31
 (K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT,
  K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH, K_NORM, K_LOOKUP, K_HOST_GRAM,
- K_HOST_PROOF) = range(17)
+ K_HOST_PROOF, K_HOST_WALK_MM, K_HOST_WALK_ACT) = range(19)
 
 QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
 SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
@@ -962,7 +962,8 @@ def main():
     for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait"),
                       (K_HOST_WAIT_TAIL, "device_wait_handover"), (K_HOST_DRAW, "claim_draws"),
                       (K_HOST_LAUNCH, "launch_calls"), (K_HOST_FINISH, "host_finish"),
-                      (K_HOST_GRAM, "round_polys_from_trip_sums"), (K_HOST_PROOF, "proof_records")]:
+                      (K_HOST_GRAM, "round_polys_from_trip_sums"), (K_HOST_PROOF, "proof_records"),
+                      (K_HOST_WALK_MM, "walk_matmul_steps"), (K_HOST_WALK_ACT, "walk_activation_steps")]:
         ms, nl, _ = ctx.kernel_time(kid)
         if nl:
             host[name] = {"ms_per_step": round(ms / args.steps, 3), "avg_us": round(ms / nl * 1e3, 3), "calls": nl}

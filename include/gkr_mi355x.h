@@ -106,7 +106,8 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * the host-finish rounds' arithmetic (wall-clock, bytes = 0); 13 the norm
  * layers' row statistics and padded-vector kernels (device); 14 the LogUp-GKR
  * batch kernels (device); 15 host: round polynomials derived from a trip's
- * sums; 16 host: proof-record appends (wall-clock, bytes = 0). */
+ * sums; 16 host: proof-record appends; 17 / 18 host: the walk's matmul /
+ * activation steps, whole (wall-clock, bytes = 0). */
 /* level 0: off; 1: events on k_restrict_cols, the Merkle level kernel and
  * the norm kernels,
  * plus the host timers; 2: events on every timed kernel (adds an event pair

@@ -90,7 +90,8 @@ enum Slot {
 enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_ROUND = 3, K_LOGUP_PREP = 4,
                 K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
                 K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NORM = 13, K_LOOKUP = 14,
-                K_HOST_GRAM = 15, K_HOST_PROOF = 16, K_NKERNELS = 17 };
+                K_HOST_GRAM = 15, K_HOST_PROOF = 16, K_HOST_WALK_MM = 17, K_HOST_WALK_ACT = 18,
+                K_NKERNELS = 19 };
 constexpr int kMaxPartialBlocks = 1024;
 constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
 static_assert(kMaxPartialBlocks <= kCountedMaxRows && kCountedMaxRows % kBlock == 0,

@@ -17,6 +17,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
     const gkr_step& st = steps[si];
     if (!st.a) return fail(GKR_ERR_INVALID, "step %zu: null matrix", si);
     if (st.kind == GKR_STEP_MATMUL) {
+      HostTimer hw(c, K_HOST_WALK_MM);
       if (!st.b) return fail(GKR_ERR_INVALID, "step %zu: null weight matrix", si);
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.b->cols)));
       const int T = log2_exact(next_pow2(st.a->cols));
@@ -67,6 +68,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       TRY(gkr_prove_mul_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.b, ch, proof, &mo));
       value = mo.next_value;  // the claim point is unchanged (prover.rs:6260-6263)
     } else if (st.kind == GKR_STEP_ACTIVATION) {
+      HostTimer hw(c, K_HOST_WALK_ACT);
       const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
       if (st.claim == GKR_CLAIM_FRESH) {
         point.resize(nv);
