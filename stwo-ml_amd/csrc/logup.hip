@@ -307,6 +307,10 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   qm31 *eq_hi, *eq_lo;
   int eq_h;
   TRY(eq_split(c, cpt.data(), nv, &eq_hi, &eq_lo, &eq_h));
+  // the eq tables of the eq-sumcheck trips (the claim point only): built while
+  // the host draws gamma and beta
+  Eq3Plan epl;
+  TRY(eq3_prepare(c, cpt.data(), nv, &epl));
 
   // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
   C.mix_u64(0x4C4F47ull);
@@ -317,13 +321,15 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   out->gamma = G(gamma);
   out->beta = G(beta);
 
-  // Launched back to back, read when needed (each result in its own slot):
+  // Launched back to back, read when needed (each result in its own slot), in
+  // the order the host needs them:
   //   prepare -> (trace sum, input MLE at the claim point)      kSlotPrep
+  //   eq-sumcheck trip 0                                         kSlotEq0
   //   table-side sum over the multiplicities                     kSlotTable
   //   multiplicities -> pinned host copy
   //   multiplicity sumcheck trip 0 (no challenge needed)         kSlotMult0
-  //   eq tables of the eq-sumcheck trips, eq-sumcheck trip 0     kSlotEq0
   RoundSink sk_prep, sk_table, sk_mult0, sk_eq0;
+  const bool eq_pre = nv > 0;
   {
     HostTimer ht(c, K_HOST_LAUNCH);
     // the table's fractions: one inversion per table entry
@@ -343,6 +349,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
                          d_min, d_mout, d_d0, d_w0, lds_hist ? nullptr : d_mult, sk_prep, counter, base);
       TRY(deliver_finish<2>(c, sk_prep, grid, counter));
     }
+    if (eq_pre) TRY(eq3_launch_trip(c, epl, 0, d_w0, d_d0, 0, nullptr, nullptr, nullptr, kSlotEq0, &sk_eq0));
     TRY(make_sink(c, &sk_table, kSlotTable));
     if (lds_hist) {
       // counts of the masked input (the padding added to bin 0 afterwards),
@@ -376,10 +383,6 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   const std::vector<Trip> mtrips = plan_trips((int)table_log, kHostTailSum, kTripMaxK);
   TRY(launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
                   kSlotMult0, &sk_mult0));
-  Eq3Plan epl;
-  TRY(eq3_prepare(c, cpt.data(), nv, &epl));
-  const bool eq_pre = nv > 0;
-  if (eq_pre) TRY(eq3_launch_trip(c, epl, 0, d_w0, d_d0, 0, nullptr, nullptr, nullptr, kSlotEq0, &sk_eq0));
 
   qm31 prep[2], tsum[1];
   TRY(wait_sink<1>(c, sk_table, tsum));  // implies the prepare results (earlier on the stream)
