@@ -307,7 +307,7 @@ extern "C" int gkr_prove_aggregated_binding(gkr_ctx* c, gkr_channel* ch, const g
     a += len / 2 + 1;
     fb[1][k] = a;
     a += len / 2 + 1;
-    hipLaunchKernelGGL(k_bind_colmajor, dim3(grid_for(len)), dim3(kBlock), 0, c->stream, B[k].b->dev, B[k].b->rows,
+    GKR_LAUNCH(c, k_bind_colmajor, dim3(grid_for(len)), dim3(kBlock), 0, B[k].b->dev, B[k].b->rows,
                        B[k].b->cols, B[k].log_pk, len, F0[k]);
     TRY(check_launch());
   }
@@ -333,7 +333,7 @@ extern "C" int gkr_prove_aggregated_binding(gkr_ctx* c, gkr_channel* ch, const g
     dhi = dco + coords.size();
     dlo = dhi + (size_t)P * nhi;
     HIP_TRY(hipMemcpyAsync(dco, coords.data(), coords.size() * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
-    hipLaunchKernelGGL(k_bind_eq, dim3(grid_for((uint64_t)P * (nhi + nlo))), dim3(kBlock), 0, c->stream, dco, P, L, h,
+    GKR_LAUNCH(c, k_bind_eq, dim3(grid_for((uint64_t)P * (nhi + nlo))), dim3(kBlock), 0, dco, P, L, h,
                        dhi, dlo);
     TRY(check_launch());
     std::vector<BindDesc> d;
@@ -360,20 +360,20 @@ extern "C" int gkr_prove_aggregated_binding(gkr_ctx* c, gkr_channel* ch, const g
     const BindDesc* dd = static_cast<const BindDesc*>(dv);
     switch (NP) {
       case 1:
-        hipLaunchKernelGGL(k_bind_dots<1>, dim3(wg), dim3(kBlock), 0, c->stream, dd, (uint32_t)d.size(), P, h, dhi, nhi, dlo, part);
-        hipLaunchKernelGGL(k_bind_finish<1>, dim3((unsigned)d.size()), dim3(kBlock), 0, c->stream, dd, part, res);
+        GKR_LAUNCH(c, k_bind_dots<1>, dim3(wg), dim3(kBlock), 0, dd, (uint32_t)d.size(), P, h, dhi, nhi, dlo, part);
+        GKR_LAUNCH(c, k_bind_finish<1>, dim3((unsigned)d.size()), dim3(kBlock), 0, dd, part, res);
         break;
       case 2:
-        hipLaunchKernelGGL(k_bind_dots<2>, dim3(wg), dim3(kBlock), 0, c->stream, dd, (uint32_t)d.size(), P, h, dhi, nhi, dlo, part);
-        hipLaunchKernelGGL(k_bind_finish<2>, dim3((unsigned)d.size()), dim3(kBlock), 0, c->stream, dd, part, res);
+        GKR_LAUNCH(c, k_bind_dots<2>, dim3(wg), dim3(kBlock), 0, dd, (uint32_t)d.size(), P, h, dhi, nhi, dlo, part);
+        GKR_LAUNCH(c, k_bind_finish<2>, dim3((unsigned)d.size()), dim3(kBlock), 0, dd, part, res);
         break;
       case 4:
-        hipLaunchKernelGGL(k_bind_dots<4>, dim3(wg), dim3(kBlock), 0, c->stream, dd, (uint32_t)d.size(), P, h, dhi, nhi, dlo, part);
-        hipLaunchKernelGGL(k_bind_finish<4>, dim3((unsigned)d.size()), dim3(kBlock), 0, c->stream, dd, part, res);
+        GKR_LAUNCH(c, k_bind_dots<4>, dim3(wg), dim3(kBlock), 0, dd, (uint32_t)d.size(), P, h, dhi, nhi, dlo, part);
+        GKR_LAUNCH(c, k_bind_finish<4>, dim3((unsigned)d.size()), dim3(kBlock), 0, dd, part, res);
         break;
       default:
-        hipLaunchKernelGGL(k_bind_dots<8>, dim3(wg), dim3(kBlock), 0, c->stream, dd, (uint32_t)d.size(), P, h, dhi, nhi, dlo, part);
-        hipLaunchKernelGGL(k_bind_finish<8>, dim3((unsigned)d.size()), dim3(kBlock), 0, c->stream, dd, part, res);
+        GKR_LAUNCH(c, k_bind_dots<8>, dim3(wg), dim3(kBlock), 0, dd, (uint32_t)d.size(), P, h, dhi, nhi, dlo, part);
+        GKR_LAUNCH(c, k_bind_finish<8>, dim3((unsigned)d.size()), dim3(kBlock), 0, dd, part, res);
         break;
     }
     TRY(check_launch());
@@ -510,7 +510,7 @@ extern "C" int gkr_prove_aggregated_binding(gkr_ctx* c, gkr_channel* ch, const g
     vs.f[k] = F0[k];
     vs.len[k] = 1ull << B[k].nv;
   }
-  hipLaunchKernelGGL(k_bind_virtual, dim3(grid_for(vtotal)), dim3(kBlock), 0, c->stream, vs, P, cfg.n_max, vtotal, V);
+  GKR_LAUNCH(c, k_bind_virtual, dim3(grid_for(vtotal)), dim3(kBlock), 0, vs, P, cfg.n_max, vtotal, V);
   TRY(check_launch());
   std::vector<gkr_qm31> pt(chal.size());
   for (size_t k = 0; k < chal.size(); k++) pt[k] = G(chal[k]);

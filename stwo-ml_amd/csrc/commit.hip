@@ -164,14 +164,14 @@ static int merkle_roots(gkr_ctx* c, const std::vector<MerkleTreeSpec>& trees, gk
     uint64_t hashes = 0;  // the timer's byte counter holds the hash count of this kernel
     for (size_t k = L.first_step; k < L.first_step + L.n_steps; k++) hashes += steps[k].n_out * ((1ull << steps[k].d) - 1);
     TimedLaunch tl(c, K_MERKLE, hashes);
-    k_merkle_level<<<dim3((uint32_t)blocks), dim3(kMerkleBlock), 0, c->stream>>>(dsteps + L.first_step, (int)L.n_steps,
+    GKR_LAUNCH(c, k_merkle_level, dim3((uint32_t)blocks), dim3(kMerkleBlock), 0, dsteps + L.first_step, (int)L.n_steps,
                                                                               L.s, L.total, K);
     HIP_TRY(hipGetLastError());
   }
   std::vector<const f9::fe*> rp(nt);
   for (size_t i = 0; i < nt; i++) rp[i] = kept ? steps[root_at[i].second].out : root_nodes + i;
   HIP_TRY(hipMemcpyAsync(dptr, rp.data(), nt * sizeof(void*), hipMemcpyHostToDevice, c->stream));
-  k_merkle_roots<<<dim3((uint32_t)((nt + 63) / 64)), dim3(64), 0, c->stream>>>(dptr, (int)nt, K, dwords);
+  GKR_LAUNCH(c, k_merkle_roots, dim3((uint32_t)((nt + 63) / 64)), dim3(64), 0, dptr, (int)nt, K, dwords);
   HIP_TRY(hipGetLastError());
   HIP_TRY(hipMemcpyAsync(roots, dwords, nt * 32, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
@@ -274,12 +274,12 @@ int mle_opening(gkr_ctx* c, const OpenSrc& src, const gkr_qm31* point, uint32_t 
     const uint64_t mid = N >> (t + 1);
     const uint32_t blocks = (uint32_t)((mid + 255) / 256);
     if (t == 0 && b)
-      k_open_fold_matrix<<<dim3(blocks), dim3(256), 0, c->stream>>>(b->dev, b->rows, b->cols, log_pk, mid,
+      GKR_LAUNCH(c, k_open_fold_matrix, dim3(blocks), dim3(256), 0, b->dev, b->rows, b->cols, log_pk, mid,
                                                                     Q(point[0]), L[1]);
     else if (t == 0)
-      k_open_fold<<<dim3(blocks), dim3(256), 0, c->stream>>>(src.q, mid, Q(point[0]), L[1]);
+      GKR_LAUNCH(c, k_open_fold, dim3(blocks), dim3(256), 0, src.q, mid, Q(point[0]), L[1]);
     else
-      k_open_fold<<<dim3(blocks), dim3(256), 0, c->stream>>>(L[t], mid, Q(point[t]), L[t + 1]);
+      GKR_LAUNCH(c, k_open_fold, dim3(blocks), dim3(256), 0, L[t], mid, Q(point[t]), L[t + 1]);
     HIP_TRY(hipGetLastError());
   }
   // trees of layers 0..nv-1 (layer 0 also when nv == 0: one leaf padded to two)
@@ -357,7 +357,7 @@ int mle_opening(gkr_ctx* c, const OpenSrc& src, const gkr_qm31* point, uint32_t 
     HIP_TRY(hipMemcpyAsync(di, items.data(), ibytes, hipMemcpyHostToDevice, c->stream));
     const MerkleConsts* K;
     TRY(merkle_consts(c, &K));
-    k_merkle_gather<<<dim3((uint32_t)((items.size() + 63) / 64)), dim3(64), 0, c->stream>>>(dk, di, (int)items.size(),
+    GKR_LAUNCH(c, k_merkle_gather, dim3((uint32_t)((items.size() + 63) / 64)), dim3(64), 0, dk, di, (int)items.size(),
                                                                                           K, dout);
     HIP_TRY(hipGetLastError());
     HIP_TRY(hipMemcpyAsync(got.data(), dout, got.size() * 4, hipMemcpyDeviceToHost, c->stream));

@@ -12,7 +12,7 @@ static int digit_planes_needed(gkr_ctx* c, const uint32_t* X, uint64_t count, in
   TRY(ensureT(c, S_GEMMP, 1, &dmask));
   HIP_TRY(hipMemsetAsync(dmask, 0, 4, c->stream));
   const uint64_t blocks = std::min<uint64_t>((count + 255) / 256, 256);
-  k_digit_mask<<<dim3((uint32_t)std::max<uint64_t>(blocks, 1)), dim3(256), 0, c->stream>>>(X, count, dmask);
+  GKR_LAUNCH(c, k_digit_mask, dim3((uint32_t)std::max<uint64_t>(blocks, 1)), dim3(256), 0, X, count, dmask);
   HIP_TRY(hipGetLastError());
   uint32_t mask = 0;
   HIP_TRY(hipMemcpyAsync(&mask, dmask, 4, hipMemcpyDeviceToHost, c->stream));
@@ -28,7 +28,7 @@ static int pack_planes(gkr_ctx* c, const uint32_t* X, uint64_t outer, uint64_t K
                        uint32_t* mask = nullptr) {
   const uint64_t ntiles = (outer + kGemmTile - 1) / kGemmTile, nsteps = (K + kGemmK - 1) / kGemmK;
   const uint64_t slots = ntiles * nsteps * 64;
-  k_digit_pack<<<dim3((uint32_t)((slots + 255) / 256)), dim3(256), 0, c->stream>>>(X, outer, K, kmajor, np, ntiles,
+  GKR_LAUNCH(c, k_digit_pack, dim3((uint32_t)((slots + 255) / 256)), dim3(256), 0, X, outer, K, kmajor, np, ntiles,
                                                                                   nsteps, out, mask);
   HIP_TRY(hipGetLastError());
   return GKR_OK;
@@ -43,6 +43,7 @@ static int weight_planes(gkr_ctx* c, gkr_matrix* b) {
   HIP_TRY(hipMalloc(&d, (size_t)np * ntiles * nsteps * kGemmBlockBytes));
   const int rc = pack_planes(c, b->dev, b->cols, b->rows, true, np, d);
   if (rc != GKR_OK) {
+    drain(c);
     (void)hipFree(d);
     return rc;
   }
@@ -55,7 +56,7 @@ template <int PA, int PB, int U>
 static void launch_gemm(gkr_ctx* c, dim3 grid, const int8_t* ap, uint64_t apb, const uint32_t* amask,
                         const int8_t* bp, uint64_t bpb, uint64_t m, uint64_t n, uint64_t nsteps, uint64_t rt,
                         uint64_t ctl, uint64_t sps, uint32_t* out) {
-  k_gemm_m31<PA, PB, U><<<grid, dim3(256), 0, c->stream>>>(ap, apb, amask, bp, bpb, m, n, nsteps, rt, ctl, sps, out);
+  GKR_LAUNCH(c, (k_gemm_m31<PA, PB, U>), grid, dim3(256), 0, ap, apb, amask, bp, bpb, m, n, nsteps, rt, ctl, sps, out);
 }
 
 static int matmul_forward(gkr_ctx* c, const gkr_matrix* a, gkr_matrix* b, uint32_t* C) {
@@ -102,7 +103,7 @@ static int matmul_forward(gkr_ctx* c, const gkr_matrix* a, gkr_matrix* b, uint32
   HIP_TRY(hipGetLastError());
   if (splits > 1) {
     const uint64_t count = m * n;
-    k_gemm_reduce<<<dim3((uint32_t)((count + 255) / 256)), dim3(256), 0, c->stream>>>(part, count, (int)splits, C);
+    GKR_LAUNCH(c, k_gemm_reduce, dim3((uint32_t)((count + 255) / 256)), dim3(256), 0, part, count, (int)splits, C);
     HIP_TRY(hipGetLastError());
   }
   return GKR_OK;
@@ -141,6 +142,7 @@ extern "C" int gkr_matmul_forward(gkr_ctx* c, const gkr_matrix* a, const gkr_mat
   int rc = matmul_forward(c, a, const_cast<gkr_matrix*>(b), d);
   if (rc == GKR_OK) rc = sync(c);
   if (rc != GKR_OK) {
+    drain(c);
     (void)hipFree(d);
     return rc;
   }

@@ -24,6 +24,7 @@
 #include <functional>
 
 #include "kernels.h"
+#include "launcher.h"
 #include "poseidon.h"
 
 namespace gkr {
@@ -34,8 +35,11 @@ using namespace gkr;
 // ------------------------------------------------------------------ errors
 // Records the message of a failure for gkr_last_error() and returns code.
 int fail(int code, const char* fmt, ...);
+// Every HIP call made through HIP_TRY first drains the launch rings
+// (launcher.h), so it never overtakes a launch queued before it.
 #define HIP_TRY(expr)                                                                       \
   do {                                                                                      \
+    drain_launches();                                                                       \
     hipError_t e_ = (expr);                                                                 \
     if (e_ != hipSuccess) return fail(GKR_ERR_DEVICE, "%s: %s (%s:%d)", #expr,              \
                                       hipGetErrorString(e_), __FILE__, __LINE__);           \
@@ -195,6 +199,8 @@ struct gkr_ctx {
   // refuses every other slot
   uint8_t* scratch_dev = nullptr;
   bool noalloc = false;
+  // launches go through this thread's ring (null: GKR_ASYNC_LAUNCH=0, issued by the caller's thread)
+  std::unique_ptr<Launcher> launcher;
   // test hooks (gkr_ctx_debug), each consumed by the next hand-over
   bool debug_handover_cancel = false;  // the host leaves before posting the challenges
   uint32_t debug_handover_spins = 0;   // nonzero: the kernel's bounded wait, posted only after it expired
@@ -227,7 +233,26 @@ inline int ensureT(gkr_ctx* c, Slot s, size_t count, T** out) {
 
 int ensure_host_mult(gkr_ctx* c, uint64_t n);
 
+// Kernel launch on the context's stream: GKR_LAUNCH(c, kernel, grid, block,
+// shared bytes, kernel arguments...).  The arguments are evaluated and
+// converted to the kernel's parameter types at this point; the launch itself
+// is issued by the context's launcher thread when it has one.
+#define GKR_LAUNCH(ctx, KERN_, GRID_, BLOCK_, SHMEM_, ...)                                        \
+  (void)launch_kernel((ctx)->launcher.get(), KERN_, dim3(GRID_), dim3(BLOCK_), (uint32_t)(SHMEM_), \
+                      (ctx)->stream, __VA_ARGS__)
+// Waits until every launch queued on the context has been issued.
+inline void drain(const gkr_ctx* c) {
+  if (c && c->launcher) c->launcher->drain();
+}
 hipEvent_t get_event(gkr_ctx* c);
+// An event record in stream order (through the launcher when there is one).
+inline void record_event(gkr_ctx* c, hipEvent_t e) {
+  hipStream_t s = c->stream;
+  if (c->launcher)
+    c->launcher->submit([e, s]() -> hipError_t { return hipEventRecord(e, s); });
+  else
+    (void)hipEventRecord(e, s);
+}
 struct TimedLaunch {
   gkr_ctx* c;
   int kid;
@@ -238,12 +263,12 @@ struct TimedLaunch {
                                               kid == K_NORM || kid == K_LOOKUP))) {
       e0 = get_event(c);
       e1 = get_event(c);
-      if (e0) (void)hipEventRecord(e0, c->stream);
+      if (e0) record_event(c, e0);
     }
   }
   ~TimedLaunch() {
     if (e0 && e1) {
-      (void)hipEventRecord(e1, c->stream);
+      record_event(c, e1);
       c->pending.push_back({kid, e0, e1, bytes});
     }
   }
@@ -266,6 +291,7 @@ void collect_timing(gkr_ctx* c);
 int sync(gkr_ctx* c);
 inline int check_launch() {
   hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = launch_error();  // a launch the launcher thread issued
   if (e != hipSuccess) return fail(GKR_ERR_DEVICE, "kernel launch: %s", hipGetErrorString(e));
   return GKR_OK;
 }
@@ -311,7 +337,7 @@ int make_sink(gkr_ctx* c, RoundSink* sk, int slot = 0);
 template <int NQ>
 static int launch_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks) {
   TRY(check_launch());
-  hipLaunchKernelGGL(k_finish<NQ>, dim3(1), dim3(kBlock), 0, c->stream, sk, (uint32_t)nblocks);
+  GKR_LAUNCH(c, k_finish<NQ>, dim3(1), dim3(kBlock), 0, sk, (uint32_t)nblocks);
   return check_launch();
 }
 // The finisher of a launch made with deliver_args (none when it delivers itself).
@@ -342,7 +368,9 @@ static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_H
       return fail(GKR_ERR_DEVICE, "kernel launched ahead stopped waiting for its challenges (mailbox %u)", hand_mb);
     if ((spins & 0xFFFF) != 0xFFFF) continue;
     if (spins == 0xFFFF) t0 = std::chrono::steady_clock::now();
-    const hipError_t e = hipStreamQuery(c->stream);
+    TRY(check_launch());
+    // while launches are still being issued the stream has not drained
+    const hipError_t e = c->launcher && !c->launcher->idle() ? hipErrorNotReady : hipStreamQuery(c->stream);
     if (e == hipSuccess) {
       if ((int32_t)(*flag - seq) >= 0) break;
       return fail(GKR_ERR_DEVICE, "device result %u not delivered (stream drained)", seq);
@@ -396,7 +424,7 @@ struct HandoverSession {
     }
     CarriedFinish none;
     memset(&none, 0, sizeof none);
-    hipLaunchKernelGGL(k_handover<NV>, dim3(1), dim3(kBlock), 0, c->stream, a, b, (uint32_t)len, k, c->mailbox,
+    GKR_LAUNCH(c, k_handover<NV>, dim3(1), dim3(kBlock), 0, a, b, (uint32_t)len, k, c->mailbox,
                        mb_seq, spin_limit, c->h_vec, c->h_flag, res_seq, fin ? *fin : none);
     launched = true;
     return check_launch();
@@ -422,6 +450,7 @@ struct HandoverSession {
   ~HandoverSession() {
     if (launched && !done) {
       __atomic_store_n(&c->mailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
+      drain(c);  // kernels still queued see the cancel code when they run
       (void)hipStreamSynchronize(c->stream);
       __atomic_store_n(&c->mailbox->seq, 0u, __ATOMIC_RELEASE);  // 0 is never a wanted sequence
     }
@@ -530,7 +559,7 @@ struct AheadTrips {
     uint32_t* words;
     TRY(ensureT(c, S_TRIPMB, 16, &words));  // status word, then kTripMaxK challenges at 16-byte offset
     if (!c->tripmb_valid) {  // fresh memory: the status may not hold a future sequence number
-      hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, c->stream, words, 16u);
+      GKR_LAUNCH(c, k_zero_u32, dim3(1), dim3(64), 0, words, 16u);
       TRY(check_launch());
       c->tripmb_valid = true;
     }
@@ -550,6 +579,7 @@ struct AheadTrips {
   ~AheadTrips() {
     if (outstanding > 0) {
       __atomic_store_n(&c->mailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
+      drain(c);  // kernels still queued see the cancel code when they run
       (void)hipStreamSynchronize(c->stream);
       __atomic_store_n(&c->mailbox->seq, 0u, __ATOMIC_RELEASE);
       c->trip_count_valid = false;

@@ -87,7 +87,7 @@ int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
   TRY(ensureT(c, S_EQPARTS, total, &parts));
   {
     TimedLaunch tl(c, K_EQ_TABLE, 16ull * total);
-    hipLaunchKernelGGL(k_eq_parts, dim3(grid_for(total)), dim3(kBlock), 0, c->stream, arg, total, parts);
+    GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(total)), dim3(kBlock), 0, arg, total, parts);
   }
   return check_launch();
 }
@@ -333,7 +333,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   {
     HostTimer ht(c, K_HOST_LAUNCH);
     // the table's fractions: one inversion per table entry
-    hipLaunchKernelGGL(k_logup_inv_table, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_table, tsize, gamma,
+    GKR_LAUNCH(c, k_logup_inv_table, dim3(grid_for(tsize)), dim3(kBlock), 0, d_table, tsize, gamma,
                        beta, d_inv);
     TRY(check_launch());
     TRY(make_sink(c, &sk_prep, kSlotPrep));
@@ -344,7 +344,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       TRY(deliver_args(c, grid, &counter, &base));
       // algorithmic bytes: the input, masked input and output written (8 per entry), d and w written
       TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 8 * n + 32 * n);
-      hipLaunchKernelGGL(k_logup_prepare, dim3(grid), dim3(kBlock), 0, c->stream, input->dev, input->rows,
+      GKR_LAUNCH(c, k_logup_prepare, dim3(grid), dim3(kBlock), 0, input->dev, input->rows,
                          input->cols, log2_exact(pcol), n, d_table, d_inv, mask, gamma, beta, eq_hi, eq_lo, eq_h,
                          d_min, d_mout, d_d0, d_w0, lds_hist ? nullptr : d_mult, sk_prep, counter, base);
       TRY(deliver_finish<2>(c, sk_prep, grid, counter));
@@ -358,23 +358,23 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       const uint64_t groups = (n + kHistPerGroup - 1) / kHistPerGroup;
       uint32_t* hist;
       TRY(ensureT(c, S_LKHIST, groups * (kHistBins / 2), &hist));
-      hipLaunchKernelGGL(k_logup_hist, dim3((unsigned)groups), dim3(kHistBlock), 0, c->stream, d_min, n, input->rows,
+      GKR_LAUNCH(c, k_logup_hist, dim3((unsigned)groups), dim3(kHistBlock), 0, d_min, n, input->rows,
                          input->cols, log2_exact(pcol), hist);
       TRY(check_launch());
       const unsigned grid = partial_grid(tsize / 2);
       TRY(deliver_args(c, grid, &counter, &base));
-      hipLaunchKernelGGL(k_logup_table_pass, dim3(grid), dim3(kBlock), 0, c->stream, hist, (int)groups,
+      GKR_LAUNCH(c, k_logup_table_pass, dim3(grid), dim3(kBlock), 0, hist, (int)groups,
                          (uint32_t)(n - input->rows * input->cols), d_inv, tsize, m0, c->h_mult, sk_table, counter,
                          base);
       TRY(deliver_finish<1>(c, sk_table, grid, counter));
     } else {
       const unsigned grid = partial_grid(tsize);
       TRY(deliver_args(c, grid, &counter, &base));
-      hipLaunchKernelGGL(k_logup_table_sum, dim3(grid), dim3(kBlock), 0, c->stream, d_inv, d_mult, tsize, sk_table,
+      GKR_LAUNCH(c, k_logup_table_sum, dim3(grid), dim3(kBlock), 0, d_inv, d_mult, tsize, sk_table,
                          counter, base);
       TRY(deliver_finish<1>(c, sk_table, grid, counter));
       // the multiplicities as QM31 for the sumcheck, and to the pinned host copy
-      hipLaunchKernelGGL(k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, c->stream, d_mult, tsize, m0,
+      GKR_LAUNCH(c, k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, d_mult, tsize, m0,
                          c->h_mult, 1);
       TRY(check_launch());
       c->mult_zero_entries = tsize;

@@ -448,7 +448,7 @@ int lk_build(gkr_ctx* c, std::vector<Inst>& I) {
     HIP_TRY(hipMemcpyAsync(dd, h, d.size() * sizeof(LkTree), hipMemcpyHostToDevice, c->stream));
     {
       TimedLaunch tl(c, K_LOOKUP, bytes);
-      hipLaunchKernelGGL(k_lk_tree, dim3(wg), dim3(kBlock), 0, c->stream, dd, (uint32_t)d.size());
+      GKR_LAUNCH(c, k_lk_tree, dim3(wg), dim3(kBlock), 0, dd, (uint32_t)d.size());
     }
     TRY(check_launch());
     TRY(sync(c));  // the staging buffer is reused by the next stage
@@ -476,7 +476,7 @@ int lk_build(gkr_ctx* c, std::vector<Inst>& I) {
   TRY(ensure_host(c, H_LKDESC, td.size() * sizeof(LkTop), &h));
   memcpy(h, td.data(), td.size() * sizeof(LkTop));
   HIP_TRY(hipMemcpyAsync(dt, h, td.size() * sizeof(LkTop), hipMemcpyHostToDevice, c->stream));
-  hipLaunchKernelGGL(k_lk_top, dim3(grid_for(I.size())), dim3(kBlock), 0, c->stream, dt, (uint32_t)I.size(), top);
+  GKR_LAUNCH(c, k_lk_top, dim3(grid_for(I.size())), dim3(kBlock), 0, dt, (uint32_t)I.size(), top);
   TRY(check_launch());
   void* hr;
   TRY(ensure_host(c, H_LKRES, 6 * I.size() * sizeof(qm31), &hr));
@@ -643,11 +643,11 @@ extern "C" int gkr_prove_lookup_batch(gkr_ctx* c, gkr_channel* ch, const gkr_loo
           HIP_TRY(hipMemcpyAsync(dd, h, d.size() * sizeof(LkRound), hipMemcpyHostToDevice, c->stream));
           {
             TimedLaunch tl(c, K_LOOKUP, bytes);
-            hipLaunchKernelGGL(k_lk_round, dim3(wg), dim3(kBlock), 0, c->stream, dd, (uint32_t)d.size(), d_tab, d_y,
+            GKR_LAUNCH(c, k_lk_round, dim3(wg), dim3(kBlock), 0, dd, (uint32_t)d.size(), d_tab, d_y,
                                layer, part, res);
           }
           TRY(check_launch());
-          hipLaunchKernelGGL(k_lk_finish, dim3((unsigned)d.size()), dim3(kBlock), 0, c->stream, dd, part, res);
+          GKR_LAUNCH(c, k_lk_finish, dim3((unsigned)d.size()), dim3(kBlock), 0, dd, part, res);
           TRY(check_launch());
           HIP_TRY(hipMemcpyAsync(hr, res, (size_t)kLkRes * d.size() * sizeof(qm31), hipMemcpyDeviceToHost,
                                  c->stream));

@@ -10,8 +10,7 @@ static int finish_fb(gkr_ctx* c) {
   if (!c->fb_pending) return GKR_OK;
   qm31* fb;
   TRY(ensureT(c, S_FB0, c->fb_pk, &fb));
-  hipLaunchKernelGGL(k_restrict_cols_finish, dim3(grid_for(c->fb_pk)), dim3(kBlock), 0, c->stream,
-                     (const qm31*)c->buf[S_COLPART], c->fb_rows, c->fb_pk, c->fb_chunks, fb);
+  GKR_LAUNCH(c, k_restrict_cols_finish, dim3(grid_for(c->fb_pk)), dim3(kBlock), 0, (const qm31*)c->buf[S_COLPART], c->fb_rows, c->fb_pk, c->fb_chunks, fb);
   c->fb_pending = false;
   return check_launch();
 }
@@ -38,7 +37,7 @@ static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
   HIP_TRY(hipMemsetAsync(bad, 0, sizeof(uint32_t), c->stream));
   const uint64_t words = B->rows * stride / 4;
   const unsigned grid = (unsigned)std::min<uint64_t>((words + kBlock - 1) / kBlock, 4096);
-  hipLaunchKernelGGL(k_to_int8, dim3(grid), dim3(kBlock), 0, c->stream, B->dev, B->rows, B->cols, stride,
+  GKR_LAUNCH(c, k_to_int8, dim3(grid), dim3(kBlock), 0, B->dev, B->rows, B->cols, stride,
                      (uint32_t*)r8, bad);
   TRY(check_launch());
   uint32_t flag = 1;
@@ -80,7 +79,7 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     both.insert(both.end(), r_j, r_j + n_rj);
     PointArg pt = make_point(both.data(), n_ri + n_rj);
     TimedLaunch tl(c, K_EQ_TABLE, 16 * (m + n));
-    hipLaunchKernelGGL(k_eq_two, dim3(grid_for(m + n)), dim3(kBlock), 0, c->stream, pt, n_ri, m, n, Li, Lj, ldig);
+    GKR_LAUNCH(c, k_eq_two, dim3(grid_for(m + n)), dim3(kBlock), 0, pt, n_ri, m, n, Li, Lj, ldig);
     TRY(check_launch());
   } else {
     if (use8) return fail(GKR_ERR_DEVICE, "int8 restriction needs the combined eq launch");
@@ -128,18 +127,17 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
       if (act_blocks + gr8 * gc8 > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
       // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
       TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
-      hipLaunchKernelGGL(k_restrict_cols8, dim3((unsigned)(act_blocks + gr8 * gc8)), dim3(kBlock), 0, c->stream,
-                         B->r8, B->r8_stride, k, (const u32x4*)ldig, (n + 3) / 4, passes, (uint32_t*)part, rows,
+      GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(act_blocks + gr8 * gc8)), dim3(kBlock), 0, B->r8, B->r8_stride, k, (const u32x4*)ldig, (n + 3) / 4, passes, (uint32_t*)part, rows,
                          (uint32_t)act_blocks, (uint32_t)gr8);
       TRY(check_launch());
     } else {
       // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
       TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
       if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
-        hipLaunchKernelGGL(k_restrict_cols<true>, grid, dim3(kBlock), 0, c->stream, B->dev, k, n, chunk, Lj,
+        GKR_LAUNCH(c, k_restrict_cols<true>, grid, dim3(kBlock), 0, B->dev, k, n, chunk, Lj,
                            (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr);
       else
-        hipLaunchKernelGGL(k_restrict_cols<false>, grid, dim3(kBlock), 0, c->stream, B->dev, k, n, chunk, Lj,
+        GKR_LAUNCH(c, k_restrict_cols<false>, grid, dim3(kBlock), 0, B->dev, k, n, chunk, Lj,
                            (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr);
       TRY(check_launch());
     }
@@ -598,7 +596,7 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
     TRY(ensureT(c, S_FA0, pk, &fa));
     // algorithmic bytes: the blocks' activations, L_i, f_a written
     TimedLaunch t(c, K_RESTRICT_ROWS, 4ull * n_blocks * a->rows * a->cols + 16 * a->rows + 16 * pk);
-    hipLaunchKernelGGL(k_restrict_rows_simd, dim3((unsigned)((pk + 63) / 64)), dim3(kSimdWaves * 64), 0, c->stream, blk,
+    GKR_LAUNCH(c, k_restrict_rows_simd, dim3((unsigned)((pk + 63) / 64)), dim3(kSimdWaves * 64), 0, blk,
                        a->rows, a->cols, pk, (const qm31*)Li, fa);
     TRY(check_launch());
   }
@@ -725,15 +723,15 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
       pa.p[i] = a_blocks[i]->dev;
       pb.p[i] = b_blocks[i]->dev;
     }
-    hipLaunchKernelGGL(k_restrict_rows_blocks, dim3(grid_for(pk), n_blocks), dim3(kBlock), 0, c->stream, pa, a->rows,
+    GKR_LAUNCH(c, k_restrict_rows_blocks, dim3(grid_for(pk), n_blocks), dim3(kBlock), 0, pa, a->rows,
                        a->cols, pk, (const qm31*)Li, ea);
-    hipLaunchKernelGGL(k_restrict_cols_blocks, dim3((unsigned)((pk + kColWaves - 1) / kColWaves), n_blocks),
-                       dim3(kBlock), 0, c->stream, pb, b->rows, b->cols, pk, (const qm31*)Lj, eb);
+    GKR_LAUNCH(c, k_restrict_cols_blocks, dim3((unsigned)((pk + kColWaves - 1) / kColWaves), n_blocks),
+                       dim3(kBlock), 0, pb, b->rows, b->cols, pk, (const qm31*)Lj, eb);
     TRY(check_launch());
   }
   std::vector<qm31> D((size_t)n_blocks * n_blocks);
   if (nbv > 0) {
-    hipLaunchKernelGGL(k_block_gram, dim3(n_blocks * n_blocks), dim3(kBlock), 0, c->stream, (const qm31*)ea,
+    GKR_LAUNCH(c, k_block_gram, dim3(n_blocks * n_blocks), dim3(kBlock), 0, (const qm31*)ea,
                        (const qm31*)eb, n_blocks, pk, gram);
     TRY(check_launch());
     HIP_TRY(hipMemcpyAsync(D.data(), gram, D.size() * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
@@ -808,8 +806,8 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
   TRY(ensureT(c, S_FA2, pk / 4 + 1, &fa2));
   TRY(ensureT(c, S_FB2, pk / 4 + 1, &fb2));
   const dim3 gq((unsigned)((pk + kColWaves - 1) / kColWaves));  // one wave per entry
-  hipLaunchKernelGGL(k_combine_q, gq, dim3(kBlock), 0, c->stream, (const qm31*)ea, qw, n_blocks, pk, fa0);
-  hipLaunchKernelGGL(k_combine_q, gq, dim3(kBlock), 0, c->stream, (const qm31*)eb, qw, n_blocks, pk, fb0);
+  GKR_LAUNCH(c, k_combine_q, gq, dim3(kBlock), 0, (const qm31*)ea, qw, n_blocks, pk, fa0);
+  GKR_LAUNCH(c, k_combine_q, gq, dim3(kBlock), 0, (const qm31*)eb, qw, n_blocks, pk, fb0);
   TRY(check_launch());
   std::vector<gkr_qm31> kchal(T > 0 ? T : 1);
   if (T == 0) {
@@ -859,7 +857,7 @@ extern "C" int gkr_evaluate_mle_at_point(gkr_ctx* c, const gkr_qm31* mle, uint64
   TRY(eq_table(c, pt.data(), (int)n_vars, len, eq));
   RoundSink sk;
   TRY(make_sink(c, &sk));
-  hipLaunchKernelGGL(k_dot_q, dim3(partial_grid(len)), dim3(kBlock), 0, c->stream, dm, eq, len, sk);
+  GKR_LAUNCH(c, k_dot_q, dim3(partial_grid(len)), dim3(kBlock), 0, dm, eq, len, sk);
   TRY(launch_finish<1>(c, sk, partial_grid(len)));
   qm31 r[1];
   TRY(wait_sink<1>(c, sk, r));
@@ -884,7 +882,7 @@ extern "C" int gkr_restrict_mle(gkr_ctx* c, const gkr_qm31* mle, uint64_t len, c
   TRY(ensureT(c, S_OUT, rest, &dout));
   HIP_TRY(hipMemcpyAsync(dm, mle, len * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
   TRY(eq_table(c, pt.data(), (int)n_assign, nx, eq));
-  hipLaunchKernelGGL(k_restrict_q, dim3(grid_for(rest)), dim3(kBlock), 0, c->stream, dm, eq, nx, rest, dout);
+  GKR_LAUNCH(c, k_restrict_q, dim3(grid_for(rest)), dim3(kBlock), 0, dm, eq, nx, rest, dout);
   TRY(check_launch());
   HIP_TRY(hipMemcpyAsync(out, dout, rest * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
   return sync(c);
@@ -899,6 +897,7 @@ extern "C" int gkr_qvec_upload(gkr_ctx* c, const gkr_qm31* host, uint64_t n, gkr
   HIP_TRY(hipSetDevice(c->device));
   qm31* d = nullptr;
   HIP_TRY(hipMalloc(&d, n * sizeof(qm31)));
+  drain(c);
   hipError_t e = hipMemcpyAsync(d, host, n * sizeof(qm31), hipMemcpyHostToDevice, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) {
@@ -915,10 +914,11 @@ extern "C" int gkr_qvec_synthetic(gkr_ctx* c, uint64_t n, uint64_t seed, gkr_qve
   HIP_TRY(hipSetDevice(c->device));
   qm31* d = nullptr;
   HIP_TRY(hipMalloc(&d, n * sizeof(qm31)));
-  hipLaunchKernelGGL(k_fill_synth_q, dim3(partial_grid(n) * 8), dim3(kBlock), 0, c->stream, d, n, seed);
+  GKR_LAUNCH(c, k_fill_synth_q, dim3(partial_grid(n) * 8), dim3(kBlock), 0, d, n, seed);
   int rc = check_launch();
   if (rc == GKR_OK) rc = sync(c);
   if (rc != GKR_OK) {
+    drain(c);
     (void)hipFree(d);
     return rc;
   }
@@ -940,6 +940,7 @@ extern "C" void gkr_qvec_free(gkr_qvec* v) {
   if (v->ctx) {
     v->ctx->qvecs.erase(v);
     if (v->dev) {
+      drain(v->ctx);
       (void)hipStreamSynchronize(v->ctx->stream);
       (void)hipFree(v->dev);
     }

@@ -68,10 +68,10 @@ static int mul_stage_matrices(gkr_ctx* c, const gkr_matrix* lhs, const gkr_matri
   qm31 *d_w0, *d_d0;
   TRY(ensureT(c, S_W0, nl, &d_w0));
   TRY(ensureT(c, S_D0, nl, &d_d0));
-  hipLaunchKernelGGL(k_pad_q, dim3(grid_for(nl)), dim3(kBlock), 0, c->stream, lhs->dev, lhs->rows, lhs->cols,
+  GKR_LAUNCH(c, k_pad_q, dim3(grid_for(nl)), dim3(kBlock), 0, lhs->dev, lhs->rows, lhs->cols,
                      log2_exact(next_pow2(lhs->cols)), nl, d_w0);
   TRY(check_launch());
-  hipLaunchKernelGGL(k_pad_q, dim3(grid_for(nl)), dim3(kBlock), 0, c->stream, rhs->dev, rhs->rows, rhs->cols,
+  GKR_LAUNCH(c, k_pad_q, dim3(grid_for(nl)), dim3(kBlock), 0, rhs->dev, rhs->rows, rhs->cols,
                      log2_exact(next_pow2(rhs->cols)), nl, d_d0);
   TRY(check_launch());
   *nv_out = nv;
@@ -148,7 +148,7 @@ extern "C" int gkr_mul_output_claim(gkr_ctx* c, const gkr_matrix* lhs, const gkr
   const uint32_t total = arg.off[1] + (1u << h);
   qm31* parts;
   TRY(ensureT(c, S_EQPARTS, total, &parts));
-  hipLaunchKernelGGL(k_eq_parts, dim3(grid_for(total)), dim3(kBlock), 0, c->stream, arg, total, parts);
+  GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(total)), dim3(kBlock), 0, arg, total, parts);
   TRY(check_launch());
   RoundSink sk;
   TRY(launch_trip(c, 1, 0, d_w0, d_d0, n, 0, nullptr, nullptr, nullptr, parts, parts + arg.off[1], h, 0, &sk));

@@ -135,7 +135,7 @@ int norm_stats(gkr_ctx* c, const gkr_matrix* X, bool ln, uint64_t dim, NormShape
   const uint64_t act_real = S->active < X->cols ? S->active : X->cols;
   {
     TimedLaunch tl(c, K_NORM, 4 * X->rows * X->cols + 16 * X->rows);
-    hipLaunchKernelGGL(k_norm_rows, dim3((unsigned)X->rows), dim3(kBlock), 0, c->stream, X->dev, X->cols, act_real,
+    GKR_LAUNCH(c, k_norm_rows, dim3((unsigned)X->rows), dim3(kBlock), 0, X->dev, X->cols, act_real,
                        d_sums);
   }
   TRY(check_launch());
@@ -199,7 +199,7 @@ int norm_prepare(gkr_ctx* c, const gkr_matrix* X, const NormShape& S, const uint
     HIP_TRY(hipMemcpyAsync(d_gamma, gamma, ng * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream));
   {  // reads X once; writes w, d (and the LayerNorm input) as QM31, input and output as u32
     TimedLaunch tl(c, K_NORM, 4 * S.rows * S.cols + (S.ln ? 56 : 40) * S.n);
-    hipLaunchKernelGGL(k_norm_prepare, dim3(grid_for(S.n)), dim3(kBlock), 0, c->stream, X->dev, S.rows, S.cols,
+    GKR_LAUNCH(c, k_norm_prepare, dim3(grid_for(S.n)), dim3(kBlock), 0, X->dev, S.rows, S.cols,
                        log2_exact(S.pcol), S.n, S.ln ? 1 : 0, S.active, d_rowv, d_gamma, d_gamma ? ng : 0, w, d,
                        in_q, in_u, out_u);
   }

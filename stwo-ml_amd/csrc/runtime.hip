@@ -105,17 +105,17 @@ int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out) {
   PointArg pt = make_point(r, n);
   TimedLaunch t(c, K_EQ_TABLE, 16 * count);
   if (n <= 10) {
-    hipLaunchKernelGGL(k_eq_direct, dim3(grid_for(count)), dim3(kBlock), 0, c->stream, pt, count, out);
+    GKR_LAUNCH(c, k_eq_direct, dim3(grid_for(count)), dim3(kBlock), 0, pt, count, out);
     return check_launch();
   }
   const int h = n / 2;
   qm31 *hi, *lo;
   TRY(ensureT(c, S_EQHI, 1ull << (n - h), &hi));
   TRY(ensureT(c, S_EQLO, 1ull << h, &lo));
-  hipLaunchKernelGGL(k_eq_tables, dim3(grid_for((1ull << (n - h)) + (1ull << h))), dim3(kBlock), 0, c->stream, pt, h,
+  GKR_LAUNCH(c, k_eq_tables, dim3(grid_for((1ull << (n - h)) + (1ull << h))), dim3(kBlock), 0, pt, h,
                      hi, lo);
   TRY(check_launch());
-  hipLaunchKernelGGL(k_eq_combine, dim3(grid_for(count)), dim3(kBlock), 0, c->stream, hi, lo, h, count, out);
+  GKR_LAUNCH(c, k_eq_combine, dim3(grid_for(count)), dim3(kBlock), 0, hi, lo, h, count, out);
   return check_launch();
 }
 // The high / low factor tables of eq(r, .) over n coordinates (S_EQHI over
@@ -128,7 +128,7 @@ int eq_split(gkr_ctx* c, const qm31* r, int n, qm31** hi, qm31** lo, int* h) {
   TRY(ensureT(c, S_EQLO, n_lo, lo));
   PointArg pt = make_point(r, n);
   TimedLaunch t(c, K_EQ_TABLE, 16 * (n_hi + n_lo));
-  hipLaunchKernelGGL(k_eq_tables, dim3(grid_for(n_hi + n_lo)), dim3(kBlock), 0, c->stream, pt, *h, *hi, *lo);
+  GKR_LAUNCH(c, k_eq_tables, dim3(grid_for(n_hi + n_lo)), dim3(kBlock), 0, pt, *h, *hi, *lo);
   return check_launch();
 }
 // The arrival counter of kernels that deliver their own results
@@ -137,7 +137,7 @@ int eq_split(gkr_ctx* c, const qm31* r, int n, qm31** hi, qm31** lo, int* h) {
 int arrival_counter(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* base) {
   TRY(ensureT(c, S_TRIPCNT, 1, counter));
   if (!c->trip_count_valid) {
-    hipLaunchKernelGGL(k_zero_u32, dim3(1), dim3(64), 0, c->stream, *counter, 1u);
+    GKR_LAUNCH(c, k_zero_u32, dim3(1), dim3(64), 0, *counter, 1u);
     TRY(check_launch());
     c->trip_count = 0;
     c->trip_count_valid = true;
@@ -166,7 +166,7 @@ int dot2_launch(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uin
   uint32_t* counter;
   uint32_t base;
   TRY(deliver_args(c, grid, &counter, &base));
-  hipLaunchKernelGGL(k_dot2_m31, dim3(grid), dim3(kBlock), 0, c->stream, v0, v1, hi, lo, h, n, *sk, counter, base);
+  GKR_LAUNCH(c, k_dot2_m31, dim3(grid), dim3(kBlock), 0, v0, v1, hi, lo, h, n, *sk, counter, base);
   return deliver_finish<2>(c, *sk, grid, counter);
 }
 int dot2_evals(gkr_ctx* c, const qm31* z, int nv, const uint32_t* v0, const uint32_t* v1, qm31 out[2]) {
@@ -271,10 +271,10 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
   if (tw.chal) {  // launched ahead: the challenges arrive through the mailbox
     CarriedFinish none;
     memset(&none, 0, sizeof none);
-    hipLaunchKernelGGL(k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, c->stream, tw, np, carry_in ? *carry_in : none);
+    GKR_LAUNCH(c, k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, tw, np, carry_in ? *carry_in : none);
     TRY(check_launch());
   }
-  hipLaunchKernelGGL((k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, c->stream, sa, sb, n, np, al, da, db, hi, lo, h,
+  GKR_LAUNCH(c, (k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, sa, sb, n, np, al, da, db, hi, lo, h,
                      sk, counter, base, b_rows, b_chunks, tw);
   TRY(check_launch());
   if (counter) return GKR_OK;
@@ -286,7 +286,7 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
     carry_out->want = tw.want;
     return GKR_OK;
   }
-  hipLaunchKernelGGL(k_finish_wide<NQ>, dim3(1), dim3(kFinishBlock), 0, c->stream, sk, grid);
+  GKR_LAUNCH(c, k_finish_wide<NQ>, dim3(1), dim3(kFinishBlock), 0, sk, grid);
   return check_launch();
 }
 int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
@@ -347,11 +347,25 @@ int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out) {
 int dot_m31(gkr_ctx* c, const uint32_t* v, const qm31* eq, uint64_t n, qm31* out) {
   RoundSink sk;
   TRY(make_sink(c, &sk));
-  hipLaunchKernelGGL(k_dot_m31, dim3(partial_grid(n)), dim3(kBlock), 0, c->stream, v, eq, n, sk);
+  GKR_LAUNCH(c, k_dot_m31, dim3(partial_grid(n)), dim3(kBlock), 0, v, eq, n, sk);
   TRY(launch_finish<1>(c, sk, partial_grid(n)));
   return wait_sink<1>(c, sk, out);
 }
 // ------------------------------------------------------------------ context ABI
+std::atomic<Launcher*> gkr::g_launchers[kMaxLaunchers];
+void gkr::register_launcher(Launcher* l) {
+  for (int i = 0; i < kMaxLaunchers; i++) {
+    Launcher* none = nullptr;
+    if (g_launchers[i].compare_exchange_strong(none, l)) return;
+  }
+}
+void gkr::unregister_launcher(Launcher* l) {
+  for (int i = 0; i < kMaxLaunchers; i++) {
+    Launcher* mine = l;
+    if (g_launchers[i].compare_exchange_strong(mine, nullptr)) return;
+  }
+}
+
 extern "C" void gkr_ctx_destroy(gkr_ctx* c);
 extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   if (!out) return fail(GKR_ERR_INVALID, "null out");
@@ -392,12 +406,29 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   c->mailbox = reinterpret_cast<Mailbox*>(reinterpret_cast<char*>(c->h_out) + kOutSlots * sizeof(qm31) + 128);
   c->mailbox->seq = 0;
   c->mailbox->expired = 0;
+  // Launches are issued by a thread of their own unless GKR_ASYNC_LAUNCH=0
+  // (the launch cost then falls on the caller's thread).  A context beyond
+  // the registry's kMaxLaunchers live launchers issues its own launches.
+  const char* al = getenv("GKR_ASYNC_LAUNCH");
+  if (!(al && al[0] == '0' && al[1] == 0)) {
+    int live = 0;
+    for (int i = 0; i < kMaxLaunchers; i++) live += g_launchers[i].load() != nullptr;
+    if (live < kMaxLaunchers) {
+      c->launcher.reset(new Launcher(device));
+      register_launcher(c->launcher.get());
+    }
+  }
   *out = c;
   return GKR_OK;
 }
 extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
+  if (c->launcher) {  // issue what is queued, then stop the thread
+    c->launcher->drain();
+    unregister_launcher(c->launcher.get());
+    c->launcher.reset();
+  }
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   for (auto& p : c->pending) {
     (void)hipEventDestroy(p.e0);
@@ -480,6 +511,7 @@ extern "C" int gkr_matrix_upload(gkr_ctx* c, const uint32_t* host, uint64_t rows
                                   (unsigned long long)i);
   uint32_t* d = nullptr;
   HIP_TRY(hipMalloc(&d, n * sizeof(uint32_t)));
+  drain(c);
   hipError_t e = hipMemcpyAsync(d, host, n * sizeof(uint32_t), hipMemcpyHostToDevice, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) {
@@ -503,10 +535,11 @@ extern "C" int gkr_matrix_synthetic(gkr_ctx* c, uint64_t rows, uint64_t cols, in
   const uint64_t n = rows * cols;
   uint32_t* d = nullptr;
   HIP_TRY(hipMalloc(&d, n * sizeof(uint32_t)));
-  hipLaunchKernelGGL(k_fill_synth, dim3(partial_grid(n) * 8), dim3(kBlock), 0, c->stream, d, n, kind, seed);
+  GKR_LAUNCH(c, k_fill_synth, dim3(partial_grid(n) * 8), dim3(kBlock), 0, d, n, kind, seed);
   int rc = check_launch();
   if (rc == GKR_OK) rc = sync(c);
   if (rc != GKR_OK) {
+    drain(c);
     (void)hipFree(d);
     return rc;
   }
@@ -524,6 +557,7 @@ extern "C" void gkr_matrix_free(gkr_matrix* m) {
   if (m->ctx) {
     if (m->ctx->mm.a == m || m->ctx->mm.b == m) m->ctx->mm.valid = false;
     m->ctx->matrices.erase(m);
+    drain(m->ctx);
     if ((m->owned && m->dev) || m->bplanes || m->r8) (void)hipStreamSynchronize(m->ctx->stream);
     if (m->owned && m->dev) (void)hipFree(m->dev);
     if (m->bplanes) (void)hipFree(m->bplanes);
@@ -553,25 +587,28 @@ extern "C" int gkr_bench_copy(gkr_ctx* c, uint64_t bytes, int iters, double* cop
   hipEvent_t e0 = nullptr, e1 = nullptr;
   float ms = 0;
   const unsigned g = 256 * 8;  // 8 workgroups per CU, grid-stride
+  drain(c);
   if (hipMemsetAsync(src, 1, n * 16, c->stream) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
       hipEventCreate(&e1) != hipSuccess) {
     rc = fail(GKR_ERR_DEVICE, "copy setup");
   } else {
-    hipLaunchKernelGGL(k_copy16, dim3(g), dim3(kBlock), 0, c->stream, src, dst, n);  // warm-up
-    (void)hipEventRecord(e0, c->stream);
-    for (int i = 0; i < iters; i++) hipLaunchKernelGGL(k_copy16, dim3(g), dim3(kBlock), 0, c->stream, src, dst, n);
-    (void)hipEventRecord(e1, c->stream);
+    GKR_LAUNCH(c, k_copy16, dim3(g), dim3(kBlock), 0, src, dst, n);  // warm-up
+    record_event(c, e0);
+    for (int i = 0; i < iters; i++) GKR_LAUNCH(c, k_copy16, dim3(g), dim3(kBlock), 0, src, dst, n);
+    record_event(c, e1);
+    drain(c);
     (void)hipEventSynchronize(e1);
     (void)hipEventElapsedTime(&ms, e0, e1);
     *copy_gbps = 2.0 * n * 16 * iters / (ms * 1e-3) / 1e9;
-    (void)hipEventRecord(e0, c->stream);
+    record_event(c, e0);
     for (int i = 0; i < iters; i++)
-      hipLaunchKernelGGL(k_read16, dim3(g), dim3(kBlock), 0, c->stream, src, n, (uint32_t*)dst);
-    (void)hipEventRecord(e1, c->stream);
+      GKR_LAUNCH(c, k_read16, dim3(g), dim3(kBlock), 0, src, n, (uint32_t*)dst);
+    record_event(c, e1);
+    drain(c);
     (void)hipEventSynchronize(e1);
     (void)hipEventElapsedTime(&ms, e0, e1);
     *read_gbps = (double)n * 16 * iters / (ms * 1e-3) / 1e9;
-    if (hipGetLastError() != hipSuccess) rc = fail(GKR_ERR_DEVICE, "copy kernels failed");
+    if (check_launch() != GKR_OK) rc = fail(GKR_ERR_DEVICE, "copy kernels failed");
   }
   if (e0) (void)hipEventDestroy(e0);
   if (e1) (void)hipEventDestroy(e1);
