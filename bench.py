@@ -873,9 +873,8 @@ def main():
     ap.add_argument("--no-timing", action="store_true", help="no HIP events and no host timers")
     ap.add_argument("--timing-all", action="store_true",
                     help="HIP events on every timed kernel (default: only the roofline kernel k_restrict_cols)")
-    ap.add_argument("--int8-weights", action="store_true",
-                    help="int8 weight-side restriction (GKR_INT8_WEIGHTS=1): a quarter of the weight bytes, "
-                         "bound by v_dot4 issue rather than HBM")
+    ap.add_argument("--u32-weights", action="store_true",
+                    help="u32 weight-side restriction (GKR_INT8_WEIGHTS=0) instead of the default int8 weight copy")
     ap.add_argument("--driver", default="walk", choices=["walk", "calls"],
                     help="walk: one gkr_prove_walk call per proof; calls: one library call per layer")
     args = ap.parse_args()
@@ -887,8 +886,8 @@ def main():
     if args.cpu_configs:
         print(json.dumps({"cpu_configs": cpu_configs()}), flush=True)
         return
-    if args.int8_weights:
-        os.environ["GKR_INT8_WEIGHTS"] = "1"
+    if args.u32_weights:
+        os.environ["GKR_INT8_WEIGHTS"] = "0"
     ctx = G.Context(0)
     if args.config == "c2":
         return bench_c2(ctx, args)
@@ -972,11 +971,13 @@ def main():
     if rc:
         ms, nl, nb = ctx.kernel_time(K_RESTRICT_COLS)
         ach = nb / (ms * 1e-3) / 1e9
-        traffic = measured_traffic() if cfg is QWEN and not args.int8_weights else None  # u32 restriction
+        prof = "restrict_cols_traffic.md" if args.u32_weights else "restrict_cols8_traffic.md"
+        traffic = measured_traffic(prof) if cfg is QWEN else None
         roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "k_restrict_cols",
+                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+                    "kernel": "k_restrict_cols" if args.u32_weights else "k_restrict_cols8",
                     "avg_launch_us": rc["avg_us"], "bytes_per_launch": nb // nl,
-                    "traffic_source": "profiles/restrict_cols_traffic.md (rocprofv3 PMC, qwen1)" if traffic else None}
+                    "traffic_source": f"profiles/{prof} (rocprofv3 PMC, qwen1)" if traffic else None}
 
     result = {
         "metric": METRIC,
@@ -992,7 +993,7 @@ def main():
         "dtype": "u32-m31",
         "data": "synthetic (counter-mode SplitMix64; int8-range weights/activations, uniform-M31 LogUp inputs)",
         "config": {"workload": workload, "layers": n_layers, "tokens": tokens,
-                   "weight_restriction": "int8" if args.int8_weights else "u32",
+                   "weight_restriction": "u32" if args.u32_weights else "int8",
                    "matmul_elements_per_step": elems, "logup_tables": "2^16 (SiLU, softmax-exp)"},
         "proved_tokens_per_s": round(tokens / (ms_per_step * 1e-3), 3) if tokens else None,
         "roofline": roofline,

@@ -86,10 +86,11 @@ int gkr_channel_import(gkr_channel* ch, const uint32_t state[11]);
 /* ------------------------------------------------------------------ device context */
 typedef struct gkr_ctx gkr_ctx;
 int gkr_ctx_create(int device, gkr_ctx** out);  /* replaces GpuSumcheckExecutor::new/cached, gpu_sumcheck.rs:1309-1380 */
-/* With GKR_INT8_WEIGHTS=1 in the environment when the context is created, a
- * weight matrix whose entries are all int8-range gets an int8 copy on first
+/* A weight matrix whose entries are all int8-range gets an int8 copy on first
  * use and the weight-side restriction reads that copy (one byte per weight,
- * v_dot4 digit sums); otherwise the u32 matrix is read.  Proofs are identical. */
+ * digit sums on the matrix cores); other matrices, and every matrix of a
+ * context created with GKR_INT8_WEIGHTS=0 in the environment, are read as
+ * u32.  Proofs are identical. */
 void gkr_ctx_destroy(gkr_ctx* ctx);
 int gkr_ctx_synchronize(gkr_ctx* ctx);
 /* Per-kernel timing (HIP events on the context stream), for benchmarks.

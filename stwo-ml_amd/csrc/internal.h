@@ -141,12 +141,12 @@ struct gkr_matrix {
   // (gemm.h), built on first use; the contents of a matrix never change
   int8_t* bplanes = nullptr;
   int bnplanes = 0;
-  // int8 copy for the weight-side restriction (rows of kR8Block-byte
-  // blocks in k_restrict_cols8's permuted order, padded to r8_stride bytes),
-  // built on first use when every entry is int8-range;
+  // int8 copy for the weight-side restriction (1 KB tiles of 16 rows x 64
+  // columns, the MFMA operand layout of k_restrict_cols8; r8_nst column
+  // steps per row tile), built on first use when every entry is int8-range;
   // r8_state: 0 not yet checked, 1 copy present, -1 not int8-range
   int8_t* r8 = nullptr;
-  uint64_t r8_stride = 0;
+  uint64_t r8_nst = 0;
   int r8_state = 0;
 };
 
@@ -192,7 +192,7 @@ struct gkr_ctx {
   uint32_t trip_count = 0;         // value of the fused trips' arrival counter (S_TRIPCNT) after the queued launches
   bool trip_count_valid = false;   // false: zero the counter before the next fused trip
   bool tripmb_valid = false;       // false: zero the flags of the trips launched ahead (S_TRIPMB) before use
-  bool int8_weights = false;       // GKR_INT8_WEIGHTS=1 at creation: int8 weight-side restriction
+  bool int8_weights = true;        // int8 weight-side restriction for int8-range weights (GKR_INT8_WEIGHTS=0: off)
   // allocation-free mode (gkr_sumcheck_product_noalloc): ensure() hands out
   // the partial rows and the arrival counter from the device's static
   // scratch array (scratch_dev: its address on this context's device) and

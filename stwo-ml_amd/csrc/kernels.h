@@ -765,42 +765,50 @@ __device__ __forceinline__ void m31_digits(uint32_t x, int32_t (&d)[4]) {
   }
 }
 
+// Tiles of the int8 weight copy and of the digit blocks (k_restrict_cols8).
+constexpr int kR8TileRows = 16, kR8TileCols = 64;
+constexpr uint64_t kR8Tile = 1024;
 // Both Lagrange tables of a matmul restriction in one launch: out1[x] over
-// coordinates [0, n1) of pt (count1 entries), out2[x] over [n1, pt.n)
-// (count2 entries), one thread per entry.  With ldig, the second table is
-// also written as digits for the int8 weight-side restriction, in four
-// planes (one per component c) of nq = ceil(count2 / 4) 16-byte entries: for
-// column x, byte x % 4 of word q of entry c * nq + x / 4 holds digit q of
-// component c, so one word carries a digit of four consecutive columns (a
-// v_dot4 operand) and a wave reads 64 consecutive entries of a plane.
-static __global__ void k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2, qm31* __restrict__ out1,
-                         qm31* __restrict__ out2, uint8_t* __restrict__ ldig) {
+// coordinates [0, n1) of pt (count1 entries) on the first eq_two_lead(count1)
+// threads, then out2[x] over [n1, pt.n) (count2 entries), one thread per
+// entry; the second table starts on a workgroup boundary.  With ldig, the
+// second table is also written as the digit blocks of the int8 weight-side
+// restriction (k_restrict_cols8): a wave's 64 columns are one 1 KB block,
+// whose 16 digits per column (digit q of component c of column x at byte
+// x % 16 of lane slot 16 ((x % 64) / 16) + 4 c + q) are transposed in LDS and
+// stored as one 16-byte lane slot per thread; the launch then covers whole
+// blocks, columns >= count2 with zero digits.
+__host__ __device__ inline uint64_t eq_two_lead(uint64_t count1) { return (count1 + kBlock - 1) / kBlock * kBlock; }
+static __global__ void __launch_bounds__(kBlock) k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2,
+                                                   qm31* __restrict__ out1, qm31* __restrict__ out2,
+                                                   uint8_t* __restrict__ ldig) {
   __shared__ PointLds sp;
+  __shared__ __align__(16) uint8_t sd[kBlock / 64][kR8Tile];
   stage_point(pt, &sp);
-  uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  int s = 0, n = n1;
-  qm31* out = out1;
-  if (x >= count1) {
-    x -= count1;
-    if (x >= count2) return;
-    s = n1;
-    n = pt.n - n1;
-    out = out2;
+  const uint64_t lead = eq_two_lead(count1);
+  const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < lead) {  // whole workgroups
+    if (t < count1) st_q(out1, t, eq_prod(sp, 0, n1, t));
+    return;
   }
-  const qm31 acc = eq_prod(sp, s, n, x);
-  st_q(out, x, acc);
-  if (ldig && out == out2) {
-    const uint32_t comp[4] = {acc.a, acc.b, acc.c, acc.d};
-    const uint64_t nq = (count2 + 3) >> 2;
+  const uint64_t x = t - lead;
+  const bool valid = x < count2;
+  const qm31 acc = valid ? eq_prod(sp, n1, pt.n - n1, x) : qm31_zero();
+  if (valid) st_q(out2, x, acc);
+  if (!ldig) return;
+  const int lane = threadIdx.x & 63;
+  uint8_t* sdw = sd[threadIdx.x >> 6];
+  const uint32_t comp[4] = {acc.a, acc.b, acc.c, acc.d};
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      uint8_t* base = ldig + ((uint64_t)c * nq + (x >> 2)) * 16 + (x & 3);
-      int32_t d[4];
-      m31_digits(comp[c], d);
+  for (int c = 0; c < 4; c++) {
+    int32_t d[4];
+    m31_digits(comp[c], d);
 #pragma unroll
-      for (int q = 0; q < 4; q++) base[q * 4] = (uint8_t)d[q];
-    }
+    for (int q = 0; q < 4; q++) sdw[16 * (16 * (lane >> 4) + 4 * c + q) + (lane & 15)] = (uint8_t)d[q];
   }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  *reinterpret_cast<u32x4*>(ldig + (x >> 6) * kR8Tile + 16 * lane) = *reinterpret_cast<const u32x4*>(sdw + 16 * lane);
 }
 // Split construction: hi table over variables [0, n-h), lo over [n-h, n).
 static __global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __restrict__ lo) {
@@ -884,23 +892,33 @@ struct RowsJob {
 // consecutive columns; wave w adds the rows i = w, w + kColWaves, ... (each
 // row read is 64 consecutive words), and the waves' sums meet in LDS.
 __device__ __forceinline__ void restrict_rows_block(const RowsJob& act, uint64_t col0, qm31 (*part)[64]) {
+  constexpr int kAhead = 8;  // rows of A a wave has in flight
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t j = col0 + lane;
   uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
   if (j < act.k) {
-    for (uint64_t i = wave; i < act.m; i += 4 * kColWaves) {
-      uint64_t t[4] = {0, 0, 0, 0};  // up to 4 rows: 4 * (P-1)^2 < 2^64
+    for (uint64_t i0 = wave; i0 < act.m; i0 += (uint64_t)kAhead * kColWaves) {
+      uint32_t v[kAhead];
 #pragma unroll
-      for (int u = 0; u < 4; u++) {
-        const uint64_t iu = i + (uint64_t)u * kColWaves;
-        if (iu < act.m) {
-          const uint64_t v = act.A[iu * act.k + j];
-          const qm31 l = ld_q(act.L, iu);
-          t[0] += v * l.a; t[1] += v * l.b; t[2] += v * l.c; t[3] += v * l.d;
-        }
+      for (int u = 0; u < kAhead; u++) {
+        const uint64_t iu = i0 + (uint64_t)u * kColWaves;
+        v[u] = iu < act.m ? act.A[iu * act.k + j] : 0u;
       }
 #pragma unroll
-      for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+      for (int g = 0; g < kAhead / 4; g++) {
+        uint64_t t[4] = {0, 0, 0, 0};  // up to 4 rows: 4 * (P-1)^2 < 2^64
+#pragma unroll
+        for (int u = 4 * g; u < 4 * g + 4; u++) {
+          const uint64_t iu = i0 + (uint64_t)u * kColWaves;
+          if (iu < act.m) {
+            const qm31 l = ld_q(act.L, iu);
+            t[0] += (uint64_t)v[u] * l.a; t[1] += (uint64_t)v[u] * l.b;
+            t[2] += (uint64_t)v[u] * l.c; t[3] += (uint64_t)v[u] * l.d;
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+      }
     }
   }
   uint32_t r[4];
@@ -998,40 +1016,45 @@ static __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t*
 // A weight whose entries are all int8-range (centered |v| <= 127: the
 // configs' weights) keeps an int8 copy, built once, that the weight-side
 // restriction streams at one byte per entry.  With L_j's components in
-// balanced base-256 digits,
+// balanced base-256 digits d_q (q < 4),
 //   sum_j B[i][j] L_j.c = sum_q 256^q sum_j B[i][j] d_q(L_j.c),
-// each inner sum is v_dot4_i32_i8 over four columns; |B d| <= 127 * 128, so
-// an int32 lane holds the sum of any chunk below 2^17 columns.
+// so the 16 inner sums (4 components x 4 digits) of the rows are one int8
+// product of B with a 16-column digit matrix: v_mfma_i32_16x16x64_i8 takes
+// 16 rows x 64 columns of B against 64 columns x 16 digit planes per
+// instruction, far below the matrix cores' rate, so the kernel streams B at
+// HBM speed.  |B d| <= 127 * 128, so an int32 sum of up to 2^17 columns is
+// exact.
 //
-// Layout: rows of kR8Block-byte blocks (stride a multiple of kR8Block, zero
-// padded).  Block b of a row holds the 256 four-column groups ("quads")
-// 256 b .. 256 b + 255 permuted so that lane l's 16 bytes at offset 16 l are
-// quads l, l + 64, l + 128, l + 192: one coalesced 16-byte load per lane
-// gives each lane four quads whose L digits sit at consecutive LDS entries
-// across the wave.
-constexpr uint64_t kR8Block = 1024;
-constexpr int kR8Rows = 4;       // rows a wave carries through one pass
-constexpr int kR8ChunkBlocks = 2;  // column chunk: 2 blocks (2048 columns), L digits 32 KB of LDS
-constexpr int kR8MaxPasses = 8;  // row passes per wave
+// Layout of the int8 copy: tiles of kR8TileRows x kR8TileCols, 1 KB each,
+// tile (rt, s) at (rt * nst + s) * 1 KB (nst = ceil(n / 64) column steps);
+// lane slot l (16 bytes at 16 l) holds row 16 rt + l % 16, columns
+// 64 s + 16 (l / 16) .. + 15 (zero beyond k or n): the A operand of one MFMA,
+// one coalesced 16-byte load per lane.  The digit blocks (k_eq_two): block s
+// holds in lane slot l = 16 g + j digit j % 4 of component j / 4 of L at
+// columns 64 s + 16 g .. + 15: the B operand.  A and B keep the same column
+// order within a lane slot, so the sum pairs the right bytes whatever K order
+// the instruction uses inside a slot.
 
 static __global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __restrict__ B, uint64_t k, uint64_t n,
-                                                    uint64_t stride, uint32_t* __restrict__ out,
+                                                    uint64_t nst, uint64_t slots, u32x4* __restrict__ out,
                                                     uint32_t* __restrict__ bad) {
-  const uint64_t wpr = stride / 4, words = k * wpr;
   uint32_t any = 0;
-  for (uint64_t w = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; w < words;
-       w += (uint64_t)gridDim.x * blockDim.x) {
-    const uint64_t i = w / wpr, wr = w - i * wpr;
-    const uint64_t blk = wr >> 8, l = (wr & 255) >> 2, t = wr & 3;  // word 4 l + t of the block
-    const uint64_t j0 = 4 * (blk * 256 + t * 64 + l);
-    uint32_t packed = 0;
+  for (uint64_t sl = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; sl < slots;
+       sl += (uint64_t)gridDim.x * blockDim.x) {
+    const uint64_t t = sl >> 6;
+    const int l = (int)(sl & 63);
+    const uint64_t rt = t / nst, s = t - rt * nst;
+    const uint64_t row = rt * kR8TileRows + (l & 15), col0 = s * kR8TileCols + 16 * (l >> 4);
+    uint32_t w[4] = {0, 0, 0, 0};
+    if (row < k) {
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int32_t v = j0 + u < n ? m31_centered(B[i * n + j0 + u]) : 0;
-      any |= (v < -127 || v > 127) ? 1u : 0u;
-      packed |= ((uint32_t)v & 0xffu) << (8 * u);
+      for (int b = 0; b < 16; b++) {
+        const int32_t v = col0 + b < n ? m31_centered(B[row * n + col0 + b]) : 0;
+        any |= (v < -127 || v > 127) ? 1u : 0u;
+        w[b >> 2] |= ((uint32_t)v & 0xffu) << (8 * (b & 3));
+      }
     }
-    out[w] = packed;
+    out[sl] = u32x4{w[0], w[1], w[2], w[3]};
   }
   __shared__ uint32_t sh_any;
   if (threadIdx.x == 0) sh_any = 0;
@@ -1042,120 +1065,80 @@ static __global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __res
 }
 
 // Weight side of the fused restriction over the int8 copy.  The grid is the
-// activation side's act_blocks workgroups, then row_blocks x chunks
-// workgroups; a workgroup copies its chunk's L digits (4 planes x 512
-// entries) into LDS, and each wave then runs `passes` passes of kR8Rows rows
-// over the chunk's blocks: per block and row one 16-byte weight load (the
-// next block's loads are issued before the current block is multiplied) and
-// 64 v_dot4 against digits read from LDS.  After each pass the 16 digit sums
-// per (row, component) recombine (sum_q 256^q acc_q, reduced once) and the
-// wave reduction of k_restrict_cols leaves one value per (row, component),
-// kept in LDS until the wave writes its partial rows at the end.
-static __global__ void __launch_bounds__(kBlock) k_restrict_cols8(const int8_t* __restrict__ B8, uint64_t stride, uint64_t k,
-                                                           const u32x4* __restrict__ ldig, uint64_t nq, int passes,
-                                                           uint32_t* __restrict__ partial, RowsJob act,
-                                                           uint32_t act_blocks, uint32_t row_blocks) {
-  constexpr int QCH = kR8ChunkBlocks * 256;  // quads per chunk
-  __shared__ u32x4 sl[4][QCH];
-  __shared__ uint32_t sh[kColWaves][64][17];  // epilogue transpose, one region per wave
-  __shared__ uint32_t sres[kColWaves][kR8MaxPasses][16];
+// activation side's act_blocks workgroups, then row_tiles x chunks
+// workgroups.  A workgroup takes one row tile (16 rows) and `chunk` column
+// steps of it; wave w takes steps w, w + 4, ... of the chunk, with the
+// weight and digit loads of kR8Ahead steps in flight (one 16-byte load each
+// per lane and step) and one MFMA per step.  The four waves' 16 x 16 sums
+// are added in LDS; wave 0 recombines each row's digit sums
+// (sum_q 256^q acc_q, reduced once) and writes the 64 (row, component)
+// values as the chunk's partial rows.
+#ifndef GKR_R8_AHEAD
+#define GKR_R8_AHEAD 8
+#endif
+constexpr int kR8Ahead = GKR_R8_AHEAD;
+typedef int v4i32 __attribute__((ext_vector_type(4)));
+static __global__ void __launch_bounds__(kBlock) k_restrict_cols8(const u32x4* __restrict__ W8, uint64_t k,
+                                                           uint64_t nst, const u32x4* __restrict__ ldig,
+                                                           uint32_t chunk, uint32_t* __restrict__ partial,
+                                                           RowsJob act, uint32_t act_blocks, uint32_t row_tiles) {
+  __shared__ union {
+    v4i32 acc[kColWaves][64];
+    qm31 part[kColWaves][64];  // activation side
+  } lds;
   if (blockIdx.x < act_blocks) {
-    restrict_rows_block(act, (uint64_t)blockIdx.x * 64, reinterpret_cast<qm31(*)[64]>(&sh[0][0][0]));
+    restrict_rows_block(act, (uint64_t)blockIdx.x * 64, lds.part);
     return;
   }
   const uint32_t wb = blockIdx.x - act_blocks;
-  const uint32_t row_block = wb % row_blocks, chunk_id = wb / row_blocks;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint64_t q0 = (uint64_t)chunk_id * QCH;
-  const uint64_t nblocks = stride / kR8Block, blk0 = (uint64_t)chunk_id * kR8ChunkBlocks;
-  const int nb = (int)((nblocks - blk0) < (uint64_t)kR8ChunkBlocks ? (nblocks - blk0) : (uint64_t)kR8ChunkBlocks);
-  for (int idx = threadIdx.x; idx < 4 * QCH; idx += kBlock) {
-    const int c = idx / QCH, q = idx - c * QCH;
-    sl[c][q] = (q0 + q < nq) ? ldig[c * nq + q0 + q] : u32x4{0, 0, 0, 0};
-  }
-  __syncthreads();
-  const uint64_t wrow0 = ((uint64_t)row_block * kColWaves + wave) * (uint64_t)(kR8Rows * passes);
-  if (wrow0 >= k) return;  // whole wave leaves; no workgroup barrier follows
-  const uint64_t left = (k - wrow0 + kR8Rows - 1) / kR8Rows;
-  const int npass = (int)(left < (uint64_t)passes ? left : (uint64_t)passes);
-  const int iters = npass * nb;
-  const int8_t* base = B8 + blk0 * kR8Block;
-  const uint32_t loff = 16 * lane;
-  // weights of iteration it (pass it / nb, block it % nb); rows past k re-read row k - 1 (not stored)
-  auto load = [&](int it, u32x4 (&w)[kR8Rows]) {
-    const int pass = it / nb, b = it - pass * nb;
+  const uint32_t rt = wb % row_tiles, chunk_id = wb / row_tiles;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t s0 = (uint64_t)chunk_id * chunk + wave;
+  const uint64_t s_end = ((uint64_t)chunk_id + 1) * chunk < nst ? ((uint64_t)chunk_id + 1) * chunk : nst;
+  const int ns = s0 < s_end ? (int)((s_end - s0 + kColWaves - 1) / kColWaves) : 0;  // this wave's steps
+  const u32x4* wt = W8 + (uint64_t)rt * nst * 64 + lane;  // step s: wt[64 s]
+  const u32x4* dg = ldig + lane;                          // step s: dg[64 s]
+  v4i32 acc = {0, 0, 0, 0};
+  u32x4 wv[kR8Ahead], dv[kR8Ahead];
 #pragma unroll
-    for (int r = 0; r < kR8Rows; r++) {
-      uint64_t row = wrow0 + (uint64_t)pass * kR8Rows + r;
-      row = row < k ? row : k - 1;
-      w[r] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(base + row * stride + (uint64_t)b * kR8Block + loff));
+  for (int u = 0; u < kR8Ahead; u++)
+    if (u < ns) {
+      const uint64_t s = s0 + (uint64_t)kColWaves * u;
+      wv[u] = __builtin_nontemporal_load(wt + 64 * s);
+      dv[u] = dg[64 * s];
     }
-  };
-  int32_t acc[kR8Rows][16];
+  for (int i = 0; i < ns; i += kR8Ahead) {
 #pragma unroll
-  for (int r = 0; r < kR8Rows; r++)
-#pragma unroll
-    for (int i = 0; i < 16; i++) acc[r][i] = 0;
-  constexpr uint64_t kOffset = (uint64_t)P << 26;  // > |sum_q 256^q acc_q|, a multiple of P
-  const int vi = lane & 15, g = lane >> 4;
-  auto step = [&](int it, const u32x4 (&w)[kR8Rows]) {
-    const int pass = it / nb, b = it - pass * nb;
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-      u32x4 l[4];
-#pragma unroll
-      for (int c = 0; c < 4; c++) l[c] = sl[c][b * 256 + t * 64 + lane];
-#pragma unroll
-      for (int r = 0; r < kR8Rows; r++)
-#pragma unroll
-        for (int i = 0; i < 16; i++)
-          acc[r][i] = __builtin_amdgcn_sdot4((int)w[r][t], (int)l[i >> 2][i & 3], acc[r][i], false);
-    }
-    if (b != nb - 1) return;
-    // end of a pass: lane l adds value (l & 15) over the 16 lanes of group (l >> 4),
-    // two shuffles add the four groups, lanes 0-15 hold the (row, component) totals
-#pragma unroll
-    for (int r = 0; r < kR8Rows; r++)
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        const int64_t v = (int64_t)acc[r][4 * c] + ((int64_t)acc[r][4 * c + 1] << 8) +
-                          ((int64_t)acc[r][4 * c + 2] << 16) + ((int64_t)acc[r][4 * c + 3] << 24);
-        sh[wave][lane][4 * r + c] = m31_reduce64((uint64_t)(v + (int64_t)kOffset));
+    for (int u = 0; u < kR8Ahead; u++) {
+      if (i + u < ns) {
+        const v4i32 a = {(int)wv[u][0], (int)wv[u][1], (int)wv[u][2], (int)wv[u][3]};
+        const v4i32 b = {(int)dv[u][0], (int)dv[u][1], (int)dv[u][2], (int)dv[u][3]};
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+        const int nx = i + u + kR8Ahead;
+        if (nx < ns) {
+          const uint64_t s = s0 + (uint64_t)kColWaves * nx;
+          wv[u] = __builtin_nontemporal_load(wt + 64 * s);
+          dv[u] = dg[64 * s];
+        }
       }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    uint64_t sum = 0;
-#pragma unroll
-    for (int i = 0; i < 16; i++) sum += sh[wave][g * 16 + i][vi];
-    uint32_t x = m31_reduce64(sum);
-    x = m31_add(x, shfl_xor_u32(x, 16));
-    x = m31_add(x, shfl_xor_u32(x, 32));
-    if (lane < 16) sres[wave][pass][lane] = x;
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-    for (int r = 0; r < kR8Rows; r++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) acc[r][i] = 0;
-  };
-  // two weight register sets alternate, so a block's loads are in flight
-  // while the previous block is multiplied (the last load repeats a valid block)
-  u32x4 wa[kR8Rows], wb2[kR8Rows];
-  load(0, wa);
-  for (int it = 0; it < iters; it += 2) {
-    load(it + 1 < iters ? it + 1 : iters - 1, wb2);
-    step(it, wa);
-    if (it + 1 >= iters) break;
-    load(it + 2 < iters ? it + 2 : iters - 1, wa);
-    step(it + 1, wb2);
+    }
   }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  for (int e = lane; e < npass * 16; e += 64) {
-    const int pass = e >> 4, rc = e & 15;
-    const uint64_t row = wrow0 + (uint64_t)pass * kR8Rows + (rc >> 2);
-    if (row < k) partial[((uint64_t)chunk_id * k + row) * 4 + (rc & 3)] = sres[wave][pass][rc];
+  lds.acc[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  v4i32 t = lds.acc[0][lane];
+#pragma unroll
+  for (int w = 1; w < kColWaves; w++) t += lds.acc[w][lane];
+  // lane l, element v: row 4 (l / 16) + v of the tile, digit plane j = l % 16 = 4 c + q
+  constexpr int64_t kOffset = (int64_t)P << 26;  // > |sum_q 256^q acc_q| (< 2^53), a multiple of P
+  const int j = lane & 15, q = j & 3, c = j >> 2;
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    int64_t x = (int64_t)t[v] * ((int64_t)1 << (8 * q));
+    x += __shfl_xor(x, 1, 64);
+    x += __shfl_xor(x, 2, 64);
+    const uint64_t row = (uint64_t)rt * kR8TileRows + 4 * (lane >> 4) + v;
+    if (q == 0 && row < k) partial[((uint64_t)chunk_id * k + row) * 4 + c] = m31_reduce64((uint64_t)(x + kOffset));
   }
 }
 

@@ -15,19 +15,18 @@ static int finish_fb(gkr_ctx* c) {
   return check_launch();
 }
 // The int8 copy of weight B for the restriction (k_to_int8), on first use:
-// one pass over B and a 4-byte read-back of the range flag.  Used only when
-// the context was created with GKR_INT8_WEIGHTS=1 in the environment: the
-// int8 restriction moves a quarter of the bytes but is bound by v_dot4 issue
-// (about 2.8 TB/s of int8 weights on the config shapes), the u32 one by HBM.
+// one pass over B and a 4-byte read-back of the range flag.  Skipped when
+// the context was created with GKR_INT8_WEIGHTS=0 in the environment.
 static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
   if (B->r8_state || !c->int8_weights) return GKR_OK;
-  const uint64_t stride = (B->cols + kR8Block - 1) / kR8Block * kR8Block;
-  if (B->rows == 0 || stride == 0 || B->rows * stride > (1ull << 40)) {
+  const uint64_t nst = (B->cols + kR8TileCols - 1) / kR8TileCols;
+  const uint64_t nrt = (B->rows + kR8TileRows - 1) / kR8TileRows;
+  if (B->rows == 0 || nst == 0 || nrt * nst * kR8Tile > (1ull << 40)) {
     B->r8_state = -1;
     return GKR_OK;
   }
   int8_t* r8 = nullptr;
-  if (hipMalloc(&r8, B->rows * stride) != hipSuccess) {  // no room: keep the u32 path
+  if (hipMalloc(&r8, nrt * nst * kR8Tile) != hipSuccess) {  // no room: keep the u32 path
     (void)hipGetLastError();
     B->r8_state = -1;
     return GKR_OK;
@@ -35,21 +34,21 @@ static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
   uint32_t* bad;
   TRY(ensureT(c, S_R8FLAG, 1, &bad));
   HIP_TRY(hipMemsetAsync(bad, 0, sizeof(uint32_t), c->stream));
-  const uint64_t words = B->rows * stride / 4;
-  const unsigned grid = (unsigned)std::min<uint64_t>((words + kBlock - 1) / kBlock, 4096);
-  GKR_LAUNCH(c, k_to_int8, dim3(grid), dim3(kBlock), 0, B->dev, B->rows, B->cols, stride,
-                     (uint32_t*)r8, bad);
+  const uint64_t slots = nrt * nst * 64;  // 16-byte lane slots
+  const unsigned grid = (unsigned)std::min<uint64_t>((slots + kBlock - 1) / kBlock, 4096);
+  GKR_LAUNCH(c, k_to_int8, dim3(grid), dim3(kBlock), 0, B->dev, B->rows, B->cols, nst, slots, (u32x4*)r8, bad);
   TRY(check_launch());
   uint32_t flag = 1;
   HIP_TRY(hipMemcpyAsync(c->h_res, bad, sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
   TRY(sync(c));
   memcpy(&flag, c->h_res, sizeof flag);
   if (flag) {
+    drain(c);
     (void)hipFree(r8);
     B->r8_state = -1;
   } else {
     B->r8 = r8;
-    B->r8_stride = stride;
+    B->r8_nst = nst;
     B->r8_state = 1;
   }
   return GKR_OK;
@@ -67,7 +66,7 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
   const uint64_t m = A->rows, k = A->cols, n = B->cols;
   const bool use8 = B->r8_state == 1 && n < (1ull << 17);  // int32 digit sums stay exact below 2^17 columns
   uint8_t* ldig = nullptr;
-  if (use8) TRY(ensureT(c, S_LDIG, ((n + 3) / 4) * 64, &ldig));
+  if (use8) TRY(ensureT(c, S_LDIG, (n + kR8TileCols - 1) / kR8TileCols * kR8Tile, &ldig));
   qm31 *Li, *Lj, *fa, *fb;
   TRY(ensureT(c, S_LI, m, &Li));
   TRY(ensureT(c, S_LJ, n, &Lj));
@@ -79,7 +78,8 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     both.insert(both.end(), r_j, r_j + n_rj);
     PointArg pt = make_point(both.data(), n_ri + n_rj);
     TimedLaunch tl(c, K_EQ_TABLE, 16 * (m + n));
-    GKR_LAUNCH(c, k_eq_two, dim3(grid_for(m + n)), dim3(kBlock), 0, pt, n_ri, m, n, Li, Lj, ldig);
+    const uint64_t threads = eq_two_lead(m) + (ldig ? (n + kR8TileCols - 1) / kR8TileCols * kR8TileCols : n);
+    GKR_LAUNCH(c, k_eq_two, dim3(grid_for(threads)), dim3(kBlock), 0, pt, n_ri, m, n, Li, Lj, ldig);
     TRY(check_launch());
   } else {
     if (use8) return fail(GKR_ERR_DEVICE, "int8 restriction needs the combined eq launch");
@@ -115,20 +115,25 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     if (act_blocks + gr * gc > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
     const dim3 grid((unsigned)(act_blocks + gr * gc));
     if (use8) {
-      // column chunks of kR8ChunkBlocks blocks; passes per wave chosen for
-      // about 512 weight-side workgroups (measured best on the config shapes)
-      const uint64_t nblocks = B->r8_stride / kR8Block;
-      const uint64_t gc8 = (nblocks + kR8ChunkBlocks - 1) / kR8ChunkBlocks;
-      const uint64_t groups = (k + kColWaves * kR8Rows - 1) / (kColWaves * kR8Rows);
-      const int passes = (int)std::max<uint64_t>(1, std::min<uint64_t>(kR8MaxPasses, groups * gc8 / 512));
-      const uint64_t gr8 = (k + (uint64_t)kColWaves * kR8Rows * passes - 1) / ((uint64_t)kColWaves * kR8Rows * passes);
-      if (gc8 > gc) TRY(ensureT(c, S_COLPART, (size_t)gc8 * k, &part));
-      gc = gc8;
-      if (act_blocks + gr8 * gc8 > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
+      // row tiles x column chunks: as many chunks (at most 8: the first trip
+      // adds the chunk partials) as keep the grid within about GKR_R8_WGS
+      // workgroups, one round of resident workgroups
+#ifndef GKR_R8_WGS
+#define GKR_R8_WGS 1280
+#endif
+      const uint64_t nst = B->r8_nst, nrt = (k + kR8TileRows - 1) / kR8TileRows;
+      const uint64_t room = GKR_R8_WGS > act_blocks + nrt ? GKR_R8_WGS - act_blocks : nrt;
+      const uint64_t gc8 = std::max<uint64_t>(1, std::min<uint64_t>({8, room / nrt, nst}));
+      const uint64_t chunk8 = (nst + gc8 - 1) / gc8;
+      const uint64_t gc_used = (nst + chunk8 - 1) / chunk8;
+      if (gc_used > gc) TRY(ensureT(c, S_COLPART, (size_t)gc_used * k, &part));
+      gc = gc_used;
+      if (act_blocks + nrt * gc > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
       // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
       TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
-      GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(act_blocks + gr8 * gc8)), dim3(kBlock), 0, B->r8, B->r8_stride, k, (const u32x4*)ldig, (n + 3) / 4, passes, (uint32_t*)part, rows,
-                         (uint32_t)act_blocks, (uint32_t)gr8);
+      GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(act_blocks + nrt * gc)), dim3(kBlock), 0, (const u32x4*)B->r8,
+                 k, nst, (const u32x4*)ldig, (uint32_t)chunk8, (uint32_t*)part, rows, (uint32_t)act_blocks,
+                 (uint32_t)nrt);
       TRY(check_launch());
     } else {
       // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written

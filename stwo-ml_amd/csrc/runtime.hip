@@ -376,7 +376,7 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   gkr_ctx* c = new gkr_ctx();
   c->device = device;
   const char* i8 = getenv("GKR_INT8_WEIGHTS");
-  c->int8_weights = i8 && i8[0] == '1' && i8[1] == 0;
+  c->int8_weights = !(i8 && i8[0] == '0' && i8[1] == 0);  // default on; GKR_INT8_WEIGHTS=0: u32 restriction
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
     delete c;
     return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");

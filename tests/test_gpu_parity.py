@@ -129,6 +129,22 @@ def int8_ctx():
     ctx.close()
 
 
+@pytest.fixture(scope="module")
+def u32_ctx():
+    """A context created with GKR_INT8_WEIGHTS=0: every weight takes the u32 restriction."""
+    old = os.environ.get("GKR_INT8_WEIGHTS")
+    os.environ["GKR_INT8_WEIGHTS"] = "0"
+    try:
+        ctx = G.Context(0)
+    finally:
+        if old is None:
+            del os.environ["GKR_INT8_WEIGHTS"]
+        else:
+            os.environ["GKR_INT8_WEIGHTS"] = old
+    yield ctx
+    ctx.close()
+
+
 @pytest.mark.parametrize("m,k,n", [(1, 576, 576), (1, 1536, 576), (64, 512, 1024)])
 def test_matmul_layer_int8_range(gpu_ctx, m, k, n):
     A = O.synthetic(m, k, 1, 11)
@@ -136,11 +152,19 @@ def test_matmul_layer_int8_range(gpu_ctx, m, k, n):
     _compare_layer(gpu_ctx, A, B, 3, "int8")
 
 
+@pytest.mark.parametrize("m,k,n", [(1, 576, 576), (64, 512, 1024), (3, 700, 3000), (64, 5120, 1024)])
+def test_matmul_layer_u32_restriction(u32_ctx, m, k, n):
+    """int8-range weights under GKR_INT8_WEIGHTS=0 take the u32 restriction (k_restrict_cols)."""
+    A = O.synthetic(m, k, 1, 13)
+    B = O.synthetic(k, n, 1, 14)
+    _compare_layer(u32_ctx, A, B, 4, "u32 path")
+
+
 @pytest.mark.parametrize("m,k,n", [(1, 576, 576), (1, 1536, 576), (64, 512, 1024), (3, 700, 3000), (2, 33, 5),
                                    (5, 4100, 2048), (1, 16, 9000)])
 def test_matmul_layer_int8_weight_path(int8_ctx, m, k, n):
-    """The int8 weight copy (permuted blocks, digit planes, LDS-staged v_dot4 restriction) gives the
-    same proof as the oracle, including ragged rows, partial blocks and chunks."""
+    """The int8 weight copy (16 x 64 tiles, digit blocks, MFMA restriction) gives the same proof as
+    the oracle, including ragged row tiles, partial column steps and several chunks."""
     A = O.synthetic(m, k, 1, 21)
     B = O.synthetic(k, n, 1, 22)
     _compare_layer(int8_ctx, A, B, 5, "int8 path")
