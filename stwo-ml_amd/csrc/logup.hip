@@ -384,13 +384,13 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
                   kSlotMult0, &sk_mult0));
 
-  qm31 prep[2], tsum[1];
-  TRY(wait_sink<1>(c, sk_table, tsum));  // implies the prepare results (earlier on the stream)
-  for (int q = 0; q < 2; q++) prep[q] = c->h_out[kSlotPrep + q];
-  const qm31 trace_sum = prep[0], input_eval = prep[1], table_sum = tsum[0];
-  if (!qm31_eq(trace_sum, table_sum))
-    return fail(GKR_ERR_LOGUP, "Activation LogUp sum mismatch: trace=(%u,%u,%u,%u) table=(%u,%u,%u,%u)", trace_sum.a,
-                trace_sum.b, trace_sum.c, trace_sum.d, table_sum.a, table_sum.b, table_sum.c, table_sum.d);
+  // The trace sum goes into the transcript now; the table-side sum it must
+  // equal is checked before the multiplicity sumcheck, so the histogram and
+  // table pass run on the device while the host works through the first
+  // eq-sumcheck rounds.
+  qm31 prep[2];
+  TRY(wait_sink<2>(c, sk_prep, prep));
+  const qm31 trace_sum = prep[0], input_eval = prep[1];
   C.mix_secure_field(trace_sum);
   out->claimed_sum = G(trace_sum);
 
@@ -407,11 +407,16 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TRY(dot2_launch(c, chal.data(), nv, d_min, d_mout, kSlotIO, &sk_io));
   out->w_eval = G(w_eval);
 
+  qm31 tsum[1];
+  TRY(wait_sink<1>(c, sk_table, tsum));
+  const qm31 table_sum = tsum[0];
+  if (!qm31_eq(trace_sum, table_sum))
+    return fail(GKR_ERR_LOGUP, "Activation LogUp sum mismatch: trace=(%u,%u,%u,%u) table=(%u,%u,%u,%u)", trace_sum.a,
+                trace_sum.b, trace_sum.c, trace_sum.d, table_sum.a, table_sum.b, table_sum.c, table_sum.d);
+
   // Multiplicity sumcheck (prover.rs:9449-9511): degree-1 rounds over
-  // 2^table_log entries.  The multiplicities reached the pinned copy before
-  // the kernels whose results were waited for above; they count every padded
-  // input once, so their sum is n.
-  memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
+  // 2^table_log entries.  The multiplicities count every padded input once,
+  // so their sum is n.
   const qm31 mult_sum = qm31_from_m31(m31_reduce64(n));
   qm31* bm[2] = {m1, m0};
   qm31 alpha = qm31_zero();
@@ -502,6 +507,9 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     }
     mfin[0] = V[0];
   }
+  // the kernels whose results were waited for in the multiplicity sumcheck
+  // were queued after the one writing the multiplicities' pinned copy
+  memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
   qm31 io[2];
   TRY(wait_sink<2>(c, sk_io, io));  // delivered before the multiplicity trips' results
   const qm31 in_eval = io[0], out_eval = io[1];
