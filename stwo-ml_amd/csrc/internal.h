@@ -84,7 +84,7 @@ inline bool felt_abi_canonical(const gkr_felt& f) {
 enum Slot {
   S_LI, S_LJ, S_FA0, S_FA1, S_FB0, S_FB1, S_PART, S_RES, S_EQHI, S_EQLO, S_MLE, S_EQ, S_OUT,
   S_MULT, S_MIN, S_MOUT, S_D0, S_D1, S_W0, S_W1, S_E0, S_M0, S_M1, S_COLPART,
-  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_TRIPMB, S_LKINV, S_LKHIST, S_LDIG, S_R8FLAG, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW,
+  S_MK0, S_MK1, S_MKSTEP, S_MKROOT, S_OPL, S_OPI, S_GEMMA, S_GEMMB, S_GEMMP, S_FA2, S_FB2, S_EQPARTS, S_TRIPCNT, S_TRIPMB, S_LKINV, S_LKHIST, S_LDIG, S_R8FLAG, S_PTWAIT, S_EXTA, S_EXTB, S_GRAM, S_NORMSUM, S_NORMROW,
   S_LKARENA, S_LKFOLD, S_LKDESC, S_LKPART, S_LKRES, S_LKTAB,
   S_BIND, S_BINDEQ, S_BINDDESC, S_BINDPART, S_BINDRES, S_BINDVIRT, S_NSLOTS
 };
@@ -201,6 +201,17 @@ struct gkr_ctx {
   bool noalloc = false;
   // launches go through this thread's ring (null: GKR_ASYNC_LAUNCH=0, issued by the caller's thread)
   std::unique_ptr<Launcher> launcher;
+  // a matmul restriction launched ahead of its claim point (prelaunch_matmul):
+  // k_point_wait waits for mailbox sequence `want`
+  struct {
+    bool active = false;
+    uint32_t want = 0;
+    const gkr_matrix* a = nullptr;
+    const gkr_matrix* b = nullptr;
+  } pre;
+  uint32_t point_mb = 0;  // the posted point's sequence, until the first trip's results confirm it arrived
+  // set by the walk for one step: called at that step's last launch
+  std::function<int()> prelaunch;
   // test hooks (gkr_ctx_debug), each consumed by the next hand-over
   bool debug_handover_cancel = false;  // the host leaves before posting the challenges
   uint32_t debug_handover_spins = 0;   // nonzero: the kernel's bounded wait, posted only after it expired
@@ -588,6 +599,39 @@ struct AheadTrips {
 };
 
 int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out);
+
+// ------------------------------------------------------------------ launches ahead of a walk step
+int prelaunch_matmul(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, bool* launched);
+// The current step's last launch is done: launch what the walk queued for the next step.
+inline int run_prelaunch(gkr_ctx* c) {
+  if (!c->prelaunch) return GKR_OK;
+  std::function<int()> f = std::move(c->prelaunch);
+  c->prelaunch = nullptr;
+  return f();
+}
+// After the first results of a restriction launched ahead: its point wait saw the post.
+inline int check_point_wait(gkr_ctx* c) {
+  if (!c->point_mb) return GKR_OK;
+  const uint32_t w = c->point_mb;
+  c->point_mb = 0;
+  if (__atomic_load_n(&c->mailbox->expired, __ATOMIC_ACQUIRE) == w)
+    return fail(GKR_ERR_DEVICE, "restriction launched ahead stopped waiting for its claim point (mailbox %u)", w);
+  return GKR_OK;
+}
+// Drops a restriction launched ahead that will not be used: the cancel code
+// ends its wait, the stream drains, the mailbox is cleared.
+inline void cancel_prelaunch(gkr_ctx* c) {
+  c->prelaunch = nullptr;
+  if (!c->pre.active) return;
+  __atomic_store_n(&c->mailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
+  drain(c);
+  (void)hipStreamSynchronize(c->stream);
+  __atomic_store_n(&c->mailbox->seq, 0u, __ATOMIC_RELEASE);
+  c->pre.active = false;
+  c->point_mb = 0;
+  c->fb_pending = false;
+  c->mm.valid = false;
+}
 
 // sum_i v[i] * eq[i] (v M31-valued, length n).
 int dot_m31(gkr_ctx* c, const uint32_t* v, const qm31* eq, uint64_t n, qm31* out);

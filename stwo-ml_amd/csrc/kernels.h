@@ -283,6 +283,7 @@ struct Mailbox {
   uint32_t expired;  // device -> host: the `want` of the last wait that ended without them
   uint32_t pad[2];
   qm31 alpha[kTripMaxK];
+  qm31 point[kMaxVars];  // a claim point (k_point_wait)
 };
 // A trip launched ahead of its challenges: k_mailbox_wait, queued right
 // before it, waits for mailbox sequence `want`, copies the posted challenges
@@ -365,6 +366,41 @@ static __global__ void __launch_bounds__(kWaitBlock) k_mailbox_wait(TripWait tw,
     tw.chal[r] = qm31{q[0], q[1], q[2], q[3]};
   }
   tw.status[0] = tw.want;
+}
+
+// A matmul restriction launched ahead of its claim point: k_point_wait (one
+// wave), queued first, waits for mailbox sequence `want`, copies the posted
+// point (n coordinates, with 1 - r) to *out in device memory and sets
+// status[0] = want; k_eq_two reads the point there and returns at once
+// unless the status holds `want`.  A wait that ends without the point
+// (cancel code or spin limit) writes `want` into mb->expired.
+static __global__ void __launch_bounds__(64) k_point_wait(Mailbox* mb, uint32_t want, uint32_t spin_limit, int n,
+                                                   PointArg* out, uint32_t* status) {
+  int ok = 0;
+  if (threadIdx.x == 0) {
+    for (uint32_t spins = 0; spins < spin_limit; spins++) {
+      const uint32_t got = __hip_atomic_load(&mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+      if (got == want) {
+        ok = 1;
+        break;
+      }
+      if (got == kWaitCancel) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    if (!ok) __hip_atomic_store(&mb->expired, want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  ok = __shfl(ok, 0, 64);  // the wave's later loads follow lane 0's acquiring read
+  if (!ok) return;
+  for (int l = threadIdx.x; l < n; l += 64) {
+    const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&mb->point[l]));
+    const qm31 r{q[0], q[1], q[2], q[3]};
+    out->r[l] = r;
+    out->omr[l] = qm31_sub(qm31_one(), r);
+  }
+  if (threadIdx.x == 0) {
+    out->n = n;
+    status[0] = want;  // read by the next kernels of the stream only
+  }
 }
 
 // t + (t of lane l ^ m), for every lane.  m = 8: DPP row rotation by 8 (the
@@ -779,12 +815,22 @@ constexpr uint64_t kR8Tile = 1024;
 // stored as one 16-byte lane slot per thread; the launch then covers whole
 // blocks, columns >= count2 with zero digits.
 __host__ __device__ inline uint64_t eq_two_lead(uint64_t count1) { return (count1 + kBlock - 1) / kBlock * kBlock; }
-static __global__ void __launch_bounds__(kBlock) k_eq_two(PointArg pt, int n1, uint64_t count1, uint64_t count2,
-                                                   qm31* __restrict__ out1, qm31* __restrict__ out2,
-                                                   uint8_t* __restrict__ ldig) {
+// dpt given (a restriction launched ahead of its point): the point is read
+// from device memory, and the kernel returns unless *status == want.
+static __global__ void __launch_bounds__(kBlock) k_eq_two(PointArg pt, const PointArg* __restrict__ dpt,
+                                                   const uint32_t* __restrict__ status, uint32_t want, int n1,
+                                                   uint64_t count1, uint64_t count2, qm31* __restrict__ out1,
+                                                   qm31* __restrict__ out2, uint8_t* __restrict__ ldig) {
   __shared__ PointLds sp;
   __shared__ __align__(16) uint8_t sd[kBlock / 64][kR8Tile];
-  stage_point(pt, &sp);
+  int ntot = pt.n;
+  if (dpt) {
+    if (status[0] != want) return;  // every thread alike
+    stage_point(*dpt, &sp);
+    ntot = dpt->n;
+  } else {
+    stage_point(pt, &sp);
+  }
   const uint64_t lead = eq_two_lead(count1);
   const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t < lead) {  // whole workgroups
@@ -793,7 +839,7 @@ static __global__ void __launch_bounds__(kBlock) k_eq_two(PointArg pt, int n1, u
   }
   const uint64_t x = t - lead;
   const bool valid = x < count2;
-  const qm31 acc = valid ? eq_prod(sp, n1, pt.n - n1, x) : qm31_zero();
+  const qm31 acc = valid ? eq_prod(sp, n1, ntot - n1, x) : qm31_zero();
   if (valid) st_q(out2, x, acc);
   if (!ldig) return;
   const int lane = threadIdx.x & 63;

@@ -456,10 +456,16 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       TRY(launch_trip(c, 2, tr.K, src, nullptr, tr.n, mtrips[j - 1].K, pend_j, dst, nullptr, nullptr, nullptr, 0, 0,
                       &sks[j], 0, 0, tw, pre ? &carry : nullptr, tw ? &carry_in : nullptr));
       src = dst;
-      if (j + 1 == nt) TRY(ho.launch<1>(src, nullptr, tr.n, tr.K, pre ? &carry : nullptr));
+      if (j + 1 == nt) {
+        TRY(ho.launch<1>(src, nullptr, tr.n, tr.K, pre ? &carry : nullptr));
+        TRY(run_prelaunch(c));  // the activation step's last launch
+      }
       return GKR_OK;
     };
-    if (nt == 1) TRY(ho.launch<1>(src, nullptr, mtrips[0].n, mtrips[0].K));
+    if (nt == 1) {
+      TRY(ho.launch<1>(src, nullptr, mtrips[0].n, mtrips[0].K));
+      TRY(run_prelaunch(c));
+    }
     if (pre && nt > 1) TRY(launch_j(1, nullptr));
     int np = 0;
     const qm31* pend = nullptr;

@@ -59,37 +59,9 @@ static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
 // f_b as column-chunk partials in S_COLPART, pending until added).
 // weight_only: f_a is left to the caller (the SIMD layer combines its blocks'
 // activation sides itself); L_i is still built.
-static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, const qm31* r_i, int n_ri,
-                         const qm31* r_j, int n_rj, uint64_t pk, bool weight_only = false) {
-  TRY(prepare_r8(c, const_cast<gkr_matrix*>(B)));  // the matrix's contents never change; r8 is derived
-  HostTimer ht(c, K_HOST_LAUNCH);
-  const uint64_t m = A->rows, k = A->cols, n = B->cols;
-  const bool use8 = B->r8_state == 1 && n < (1ull << 17);  // int32 digit sums stay exact below 2^17 columns
-  uint8_t* ldig = nullptr;
-  if (use8) TRY(ensureT(c, S_LDIG, (n + kR8TileCols - 1) / kR8TileCols * kR8Tile, &ldig));
-  qm31 *Li, *Lj, *fa, *fb;
-  TRY(ensureT(c, S_LI, m, &Li));
-  TRY(ensureT(c, S_LJ, n, &Lj));
-  TRY(ensureT(c, S_FA0, pk, &fa));
-  TRY(ensureT(c, S_FB0, pk, &fb));
-  c->fb_pending = false;
-  if (n_ri + n_rj <= kMaxVars) {
-    std::vector<qm31> both(r_i, r_i + n_ri);
-    both.insert(both.end(), r_j, r_j + n_rj);
-    PointArg pt = make_point(both.data(), n_ri + n_rj);
-    TimedLaunch tl(c, K_EQ_TABLE, 16 * (m + n));
-    const uint64_t threads = eq_two_lead(m) + (ldig ? (n + kR8TileCols - 1) / kR8TileCols * kR8TileCols : n);
-    GKR_LAUNCH(c, k_eq_two, dim3(grid_for(threads)), dim3(kBlock), 0, pt, n_ri, m, n, Li, Lj, ldig);
-    TRY(check_launch());
-  } else {
-    if (use8) return fail(GKR_ERR_DEVICE, "int8 restriction needs the combined eq launch");
-    TRY(eq_table(c, r_i, n_ri, m, Li));
-    TRY(eq_table(c, r_j, n_rj, n, Lj));
-  }
-  {
-    // column chunks: chunks a multiple of one wave sweep (256 columns), at
-    // least GKR_RC_MIN_CHUNK columns, and at most GKR_RC_TARGET workgroups in
-    // all (GKR_RC_CEIL: at least that many)
+// The launch shape of one restriction, worked out before anything is
+// allocated or launched (so a restriction launched ahead of its claim point
+// can first check that no buffer has to grow).
 #ifndef GKR_RC_TARGET
 #define GKR_RC_TARGET 2560
 #endif
@@ -99,58 +71,188 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
 #ifndef GKR_RC_CEIL
 #define GKR_RC_CEIL 1
 #endif
+#ifndef GKR_R8_WGS
+#define GKR_R8_WGS 1280
+#endif
+struct RestrictPlan {
+  uint64_t m, k, n, pk;
+  bool use8;
+  uint64_t ldig_bytes;  // int8 digit blocks (use8)
+  uint64_t act_blocks;
+  uint64_t gr, gc, chunk;  // u32 path: row blocks, column chunks, chunk columns
+  uint64_t nst, nrt;       // int8 path: column steps, row tiles (gc chunks of `chunk` steps)
+};
+static int plan_restrict(const gkr_matrix* A, const gkr_matrix* B, uint64_t pk, bool weight_only, RestrictPlan* p) {
+  p->m = A->rows;
+  p->k = A->cols;
+  p->n = B->cols;
+  p->pk = pk;
+  const uint64_t k = p->k, n = p->n;
+  // int32 digit sums stay exact below 2^17 columns; the digits come from the combined eq launch
+  p->use8 = B->r8_state == 1 && n < (1ull << 17) &&
+            log2_exact(next_pow2(p->m)) + log2_exact(next_pow2(n)) <= kMaxVars;
+  p->ldig_bytes = p->use8 ? (n + kR8TileCols - 1) / kR8TileCols * kR8Tile : 0;
+  p->act_blocks = weight_only ? 0 : (pk + 63) / 64;  // 64 columns of A per workgroup
+  if (p->use8) {
+    // row tiles x column chunks: as many chunks (at most 8: the first trip
+    // adds the chunk partials) as keep the grid within about GKR_R8_WGS
+    // workgroups, one round of resident workgroups
+    p->nst = B->r8_nst;
+    p->nrt = (k + kR8TileRows - 1) / kR8TileRows;
+    const uint64_t room = GKR_R8_WGS > p->act_blocks + p->nrt ? GKR_R8_WGS - p->act_blocks : p->nrt;
+    const uint64_t gc8 = std::max<uint64_t>(1, std::min<uint64_t>({8, room / p->nrt, p->nst}));
+    p->chunk = (p->nst + gc8 - 1) / gc8;
+    p->gc = (p->nst + p->chunk - 1) / p->chunk;
+    p->gr = p->nrt;
+  } else {
+    // column chunks: chunks a multiple of one wave sweep (256 columns), at
+    // least GKR_RC_MIN_CHUNK columns, and at most GKR_RC_TARGET workgroups in
+    // all (GKR_RC_CEIL: at least that many)
     const uint64_t rows_per_block = (uint64_t)kColRows * kColWaves;
-    const uint64_t gr = (k + rows_per_block - 1) / rows_per_block;
-    uint64_t gc = GKR_RC_CEIL ? (GKR_RC_TARGET + gr - 1) / gr : GKR_RC_TARGET / gr;
+    p->gr = (k + rows_per_block - 1) / rows_per_block;
+    uint64_t gc = GKR_RC_CEIL ? (GKR_RC_TARGET + p->gr - 1) / p->gr : GKR_RC_TARGET / p->gr;
     if (gc < 1) gc = 1;
     uint64_t chunk = (n + gc - 1) / gc;
     chunk = (chunk + 255) / 256 * 256;
     if (chunk < GKR_RC_MIN_CHUNK) chunk = GKR_RC_MIN_CHUNK;
-    gc = (n + chunk - 1) / chunk;
-    qm31* part;
-    TRY(ensureT(c, S_COLPART, (size_t)gc * k, &part));
-    // the activation side rides in one more column-chunk slice (one column per thread)
-    RowsJob rows{A->dev, m, k, pk, Li, fa};
-    const uint64_t act_blocks = weight_only ? 0 : (pk + 63) / 64;  // 64 columns of A per workgroup
-    if (act_blocks + gr * gc > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
-    const dim3 grid((unsigned)(act_blocks + gr * gc));
-    if (use8) {
-      // row tiles x column chunks: as many chunks (at most 8: the first trip
-      // adds the chunk partials) as keep the grid within about GKR_R8_WGS
-      // workgroups, one round of resident workgroups
-#ifndef GKR_R8_WGS
-#define GKR_R8_WGS 1280
-#endif
-      const uint64_t nst = B->r8_nst, nrt = (k + kR8TileRows - 1) / kR8TileRows;
-      const uint64_t room = GKR_R8_WGS > act_blocks + nrt ? GKR_R8_WGS - act_blocks : nrt;
-      const uint64_t gc8 = std::max<uint64_t>(1, std::min<uint64_t>({8, room / nrt, nst}));
-      const uint64_t chunk8 = (nst + gc8 - 1) / gc8;
-      const uint64_t gc_used = (nst + chunk8 - 1) / chunk8;
-      if (gc_used > gc) TRY(ensureT(c, S_COLPART, (size_t)gc_used * k, &part));
-      gc = gc_used;
-      if (act_blocks + nrt * gc > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
-      // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
-      TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
-      GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(act_blocks + nrt * gc)), dim3(kBlock), 0, (const u32x4*)B->r8,
-                 k, nst, (const u32x4*)ldig, (uint32_t)chunk8, (uint32_t*)part, rows, (uint32_t)act_blocks,
-                 (uint32_t)nrt);
-      TRY(check_launch());
-    } else {
-      // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
-      TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
-      if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
-        GKR_LAUNCH(c, k_restrict_cols<true>, grid, dim3(kBlock), 0, B->dev, k, n, chunk, Lj,
-                           (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr);
-      else
-        GKR_LAUNCH(c, k_restrict_cols<false>, grid, dim3(kBlock), 0, B->dev, k, n, chunk, Lj,
-                           (uint32_t*)part, rows, (uint32_t)act_blocks, (uint32_t)gr);
-      TRY(check_launch());
-    }
-    c->fb_pending = true;
-    c->fb_rows = k;
-    c->fb_pk = pk;
-    c->fb_chunks = (int)gc;
+    p->chunk = chunk;
+    p->gc = (n + chunk - 1) / chunk;
   }
+  if (p->act_blocks + p->gr * p->gc > 0x7fffffffull) return fail(GKR_ERR_INVALID, "matrix too large for one restriction");
+  return GKR_OK;
+}
+// Device buffers of a restriction: {slot, bytes}.
+static void restrict_buffers(const RestrictPlan& p, std::vector<std::pair<Slot, size_t>>* out) {
+  out->clear();
+  if (p.use8) out->push_back({S_LDIG, p.ldig_bytes});
+  out->push_back({S_LI, p.m * sizeof(qm31)});
+  out->push_back({S_LJ, p.n * sizeof(qm31)});
+  out->push_back({S_FA0, p.pk * sizeof(qm31)});
+  out->push_back({S_FB0, p.pk * sizeof(qm31)});
+  out->push_back({S_COLPART, p.gc * p.k * sizeof(qm31)});
+}
+// The claim point of a restriction launched ahead of it: in device memory,
+// written by k_point_wait, valid when *status == want.
+struct DevicePoint {
+  const PointArg* pt;
+  const uint32_t* status;
+  uint32_t want;
+};
+
+// Restrict A rows by r_i and B columns by r_j into f_a (S_FA0) and f_b (S_FB0),
+// each of length pk (components/matmul.rs:470-565, backend.rs:127-134): one
+// launch for both Lagrange tables, one for both restrictions (f_a directly,
+// f_b as column-chunk partials in S_COLPART, pending until added).
+// weight_only: f_a is left to the caller (the SIMD layer combines its blocks'
+// activation sides itself); L_i is still built.  dp given: the point (n_ri +
+// n_rj coordinates) comes from device memory (r_i, r_j unused) and the int8
+// copy must already exist or be ruled out (no synchronisation here).
+static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, const qm31* r_i, int n_ri,
+                         const qm31* r_j, int n_rj, uint64_t pk, bool weight_only = false,
+                         const DevicePoint* dp = nullptr) {
+  if (!dp) TRY(prepare_r8(c, const_cast<gkr_matrix*>(B)));  // the matrix's contents never change; r8 is derived
+  HostTimer ht(c, K_HOST_LAUNCH);
+  RestrictPlan p;
+  TRY(plan_restrict(A, B, pk, weight_only, &p));
+  const uint64_t m = p.m, k = p.k, n = p.n;
+  if ((p.use8 || dp) && n_ri + n_rj > kMaxVars)
+    return fail(GKR_ERR_DEVICE, "the combined eq launch takes at most %d point coordinates", kMaxVars);
+  uint8_t* ldig = nullptr;
+  if (p.use8) TRY(ensureT(c, S_LDIG, p.ldig_bytes, &ldig));
+  qm31 *Li, *Lj, *fa, *fb, *part;
+  TRY(ensureT(c, S_LI, m, &Li));
+  TRY(ensureT(c, S_LJ, n, &Lj));
+  TRY(ensureT(c, S_FA0, pk, &fa));
+  TRY(ensureT(c, S_FB0, pk, &fb));
+  TRY(ensureT(c, S_COLPART, (size_t)p.gc * k, &part));
+  c->fb_pending = false;
+  if (n_ri + n_rj <= kMaxVars) {
+    PointArg pt;
+    if (dp) {
+      memset(&pt, 0, sizeof pt);
+    } else {
+      std::vector<qm31> both(r_i, r_i + n_ri);
+      both.insert(both.end(), r_j, r_j + n_rj);
+      pt = make_point(both.data(), n_ri + n_rj);
+    }
+    TimedLaunch tl(c, K_EQ_TABLE, 16 * (m + n));
+    const uint64_t threads = eq_two_lead(m) + (ldig ? (n + kR8TileCols - 1) / kR8TileCols * kR8TileCols : n);
+    GKR_LAUNCH(c, k_eq_two, dim3(grid_for(threads)), dim3(kBlock), 0, pt, dp ? dp->pt : nullptr,
+               dp ? dp->status : nullptr, dp ? dp->want : 0u, n_ri, m, n, Li, Lj, ldig);
+    TRY(check_launch());
+  } else {
+    TRY(eq_table(c, r_i, n_ri, m, Li));
+    TRY(eq_table(c, r_j, n_rj, n, Lj));
+  }
+  // the activation side rides in act_blocks more workgroups (64 columns of A each)
+  RowsJob rows{A->dev, m, k, pk, Li, fa};
+  if (p.use8) {
+    // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
+    TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
+    GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(p.act_blocks + p.nrt * p.gc)), dim3(kBlock), 0,
+               (const u32x4*)B->r8, k, p.nst, (const u32x4*)ldig, (uint32_t)p.chunk, (uint32_t*)part, rows,
+               (uint32_t)p.act_blocks, (uint32_t)p.nrt);
+    TRY(check_launch());
+  } else {
+    // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
+    TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
+    const dim3 grid((unsigned)(p.act_blocks + p.gr * p.gc));
+    if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
+      GKR_LAUNCH(c, k_restrict_cols<true>, grid, dim3(kBlock), 0, B->dev, k, n, p.chunk, Lj, (uint32_t*)part, rows,
+                 (uint32_t)p.act_blocks, (uint32_t)p.gr);
+    else
+      GKR_LAUNCH(c, k_restrict_cols<false>, grid, dim3(kBlock), 0, B->dev, k, n, p.chunk, Lj, (uint32_t*)part, rows,
+                 (uint32_t)p.act_blocks, (uint32_t)p.gr);
+    TRY(check_launch());
+  }
+  c->fb_pending = true;
+  c->fb_rows = k;
+  c->fb_pk = pk;
+  c->fb_chunks = (int)p.gc;
+  return GKR_OK;
+}
+
+// A walk's next matmul restriction launched ahead of its claim point (at the
+// current step's last launch): k_point_wait, then the restriction reading
+// the point from device memory.  Launched only when every buffer it needs is
+// already large enough and the weight's int8 copy question is settled, since
+// growing a buffer or building the copy synchronises with the stream, whose
+// earlier kernels wait for the current step's challenges.  *launched reports
+// whether it was.
+int prelaunch_matmul(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, bool* launched) {
+  *launched = false;
+  if (c->noalloc || c->pre.active || !A || !B || A->ctx != c || B->ctx != c || A->cols != B->rows) return GKR_OK;
+  if (c->int8_weights && B->r8_state == 0) return GKR_OK;
+  const uint64_t pk = next_pow2(A->cols);
+  const int n_ri = log2_exact(next_pow2(A->rows)), n_rj = log2_exact(next_pow2(B->cols));
+  if (log2_exact(pk) == 0 || n_ri + n_rj > kMaxVars) return GKR_OK;
+  RestrictPlan p;
+  if (plan_restrict(A, B, pk, false, &p) != GKR_OK) return GKR_OK;
+  std::vector<std::pair<Slot, size_t>> bufs;
+  restrict_buffers(p, &bufs);
+  bufs.push_back({S_PTWAIT, sizeof(PointArg) + 256});
+  for (const auto& sb : bufs)
+    if (c->cap[sb.first] < sb.second) return GKR_OK;
+  uint8_t* pw;
+  TRY(ensureT(c, S_PTWAIT, sizeof(PointArg) + 256, &pw));
+  DevicePoint dp;
+  dp.pt = reinterpret_cast<const PointArg*>(pw + 256);
+  dp.status = reinterpret_cast<const uint32_t*>(pw);
+  dp.want = alloc_seq(&c->mb_seq, 1);
+  {
+    HostTimer ht(c, K_HOST_LAUNCH);
+    GKR_LAUNCH(c, k_point_wait, dim3(1), dim3(64), 0, c->mailbox, dp.want, kWaitSpinLimit, n_ri + n_rj,
+               reinterpret_cast<PointArg*>(pw + 256), reinterpret_cast<uint32_t*>(pw));
+    TRY(check_launch());
+  }
+  c->pre.active = true;  // from here on a failure leaves a wait that the walk cancels
+  c->pre.want = dp.want;
+  c->pre.a = A;
+  c->pre.b = B;
+  c->mm.valid = false;
+  c->mm.have_trip0 = false;
+  TRY(restrict_pair(c, A, B, nullptr, n_ri, nullptr, n_rj, pk, false, &dp));
+  *launched = true;
   return GKR_OK;
 }
 
@@ -197,6 +299,23 @@ static int validate_matmul(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b,
 
 static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, uint32_t n_ri,
                              const gkr_qm31* r_j, uint32_t n_rj) {
+  if (c->pre.active && c->pre.a == a && c->pre.b == b) {  // launched ahead: post the point
+    for (uint32_t l = 0; l < n_ri + n_rj; l++) {
+      const gkr_qm31& x = l < n_ri ? r_i[l] : r_j[l - n_ri];
+      if (!canonical_q(x)) return fail(GKR_ERR_INVALID, "claim point coordinate %u not canonical", l);
+    }
+    for (uint32_t l = 0; l < n_ri + n_rj; l++) c->mailbox->point[l] = Q(l < n_ri ? r_i[l] : r_j[l - n_ri]);
+    __atomic_store_n(&c->mailbox->seq, c->pre.want, __ATOMIC_RELEASE);
+    c->point_mb = c->pre.want;  // checked once the first trip's results are in
+    c->pre.active = false;
+    c->mm.valid = true;
+    c->mm.a = a;
+    c->mm.b = b;
+    c->mm.r_i.assign(r_i, r_i + n_ri);
+    c->mm.r_j.assign(r_j, r_j + n_rj);
+    c->mm.have_trip0 = false;
+    return GKR_OK;
+  }
   if (cache_matches(c, a, b, r_i, (int)n_ri, r_j, (int)n_rj)) return GKR_OK;
   std::vector<qm31> ri(n_ri), rj(n_rj);
   for (uint32_t l = 0; l < n_ri; l++) {
@@ -308,8 +427,10 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
   } else {
     TRY(launch_j(0, nullptr));
   }
-  if (pre)
+  if (pre) {
     for (size_t j = 1; j < nt; j++) TRY(launch_j(j, nullptr));
+    TRY(run_prelaunch(c));  // every launch of this sumcheck is queued
+  }
   int np = 0;
   const qm31* pend = nullptr;
   for (size_t j = 0; j < nt; j++) {
@@ -321,6 +442,7 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
     } else {
       TRY(wait_trip(c, sks[j], trip_nq(0, tr.K), g, j > 0 && pre ? tws[j].want : 0));
     }
+    if (j == 0) TRY(check_point_wait(c));
     if (j == 0 && ft && ft->on_sums) TRY(ft->on_sums(g, tr.K));
     for (int i = 0; i < tr.K; i++) {
       qm31 sums[3];

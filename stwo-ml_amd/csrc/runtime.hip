@@ -382,7 +382,7 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
     return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");
   }
   if (hipHostMalloc((void**)&c->h_res, 64 * sizeof(qm31), hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&c->h_out, kOutSlots * sizeof(qm31) + 256, hipHostMallocCoherent | hipHostMallocMapped) !=
+      hipHostMalloc((void**)&c->h_out, kOutSlots * sizeof(qm31) + 128 + sizeof(Mailbox), hipHostMallocCoherent | hipHostMallocMapped) !=
           hipSuccess) {
     gkr_ctx_destroy(c);
     return fail(GKR_ERR_DEVICE, "context buffer allocation failed");

@@ -13,9 +13,35 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
   bool have_claim = init_value != nullptr;
   std::vector<gkr_qm31> rp, npnt(64);
   std::vector<uint32_t> mults;
+  // A fresh matmul step whose predecessor is a matmul or activation step has
+  // its restriction launched ahead, at the predecessor's last launch, waiting
+  // on the device for its claim point (prelaunch_matmul): the host then only
+  // posts the point.  Whatever is left of it on any exit is cancelled.
+  struct PreGuard {
+    gkr_ctx* c;
+    ~PreGuard() { cancel_prelaunch(c); }
+  } pre_guard{c};
+  auto fused_matmul = [](const gkr_step& s) {
+    return s.kind == GKR_STEP_MATMUL && s.claim == GKR_CLAIM_FRESH && s.a && s.b && s.a->cols > 1;
+  };
+  if (n_steps > 1) {
+    uint8_t* pw;
+    TRY(ensureT(c, S_PTWAIT, sizeof(PointArg) + 256, &pw));
+  }
   for (size_t si = 0; si < n_steps; si++) {
     const gkr_step& st = steps[si];
     if (!st.a) return fail(GKR_ERR_INVALID, "step %zu: null matrix", si);
+    if (c->pre.active && !(fused_matmul(st) && c->pre.a == st.a && c->pre.b == st.b)) cancel_prelaunch(c);
+    c->prelaunch = nullptr;
+    if (si + 1 < n_steps && fused_matmul(steps[si + 1]) &&
+        (fused_matmul(st) || st.kind == GKR_STEP_ACTIVATION)) {
+      const gkr_matrix* na = steps[si + 1].a;
+      const gkr_matrix* nb = steps[si + 1].b;
+      c->prelaunch = [c, na, nb]() -> int {
+        bool launched;
+        return prelaunch_matmul(c, na, nb, &launched);
+      };
+    }
     if (st.kind == GKR_STEP_MATMUL) {
       HostTimer hw(c, K_HOST_WALK_MM);
       if (!st.b) return fail(GKR_ERR_INVALID, "step %zu: null weight matrix", si);
@@ -130,6 +156,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
     } else {
       return fail(GKR_ERR_INVALID, "step %zu: unknown kind %u", si, st.kind);
     }
+    c->prelaunch = nullptr;
     have_claim = true;
   }
   if (point.size() > 64) return fail(GKR_ERR_BUFFER, "final claim has %zu variables", point.size());
