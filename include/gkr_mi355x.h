@@ -109,10 +109,11 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * batch kernels (device); 15 host: round polynomials derived from a trip's
  * sums; 16 host: proof-record appends; 17 / 18 host: the walk's matmul /
  * activation steps, whole (wall-clock, bytes = 0). */
-/* level 0: off; 1: events on k_restrict_cols, the Merkle level kernel and
- * the norm kernels,
- * plus the host timers; 2: events on every timed kernel (adds an event pair
- * per launch). */
+/* level 0: off; 1: events on every 8th launch of restrict_cols (id 0; only
+ * those launches are counted) and on every launch of ids 1, 9, 13 and 14,
+ * plus the host timers; 2: events on every launch of every timed kernel (an
+ * event pair per launch, each record a queue packet of its own that delays
+ * the next kernel by a few microseconds). */
 int gkr_ctx_set_timing(gkr_ctx* ctx, int level);
 int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);
 int gkr_ctx_reset_timing(gkr_ctx* ctx);

@@ -175,7 +175,8 @@ struct gkr_ctx {
   Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
   uint32_t seq = 0;            // last result sequence number handed out
   uint32_t mb_seq = 0;         // last mailbox sequence number handed out
-  int timing = 0;  // 0 off; 1: k_restrict_cols events + host timers; 2: events on every timed kernel
+  int timing = 0;  // 0 off; 1: sampled events on the roofline kernels + host timers; 2: events on every timed kernel
+  uint64_t event_seq[32] = {};  // launches of each timed kernel id since the last reset (level-1 sampling)
   KernelStat stats[K_NKERNELS];
   std::vector<PendingTiming> pending;
   std::vector<hipEvent_t> free_events;
@@ -256,6 +257,7 @@ inline void drain(const gkr_ctx* c) {
   if (c && c->launcher) c->launcher->drain();
 }
 hipEvent_t get_event(gkr_ctx* c);
+constexpr uint64_t kEventSample = 8;
 // An event record in stream order (through the launcher when there is one).
 inline void record_event(gkr_ctx* c, hipEvent_t e) {
   hipStream_t s = c->stream;
@@ -270,8 +272,14 @@ struct TimedLaunch {
   uint64_t bytes;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
-    if (c->timing >= 2 || (c->timing == 1 && (kid == K_RESTRICT_COLS || kid == K_RESTRICT_ROWS || kid == K_MERKLE ||
-                                              kid == K_NORM || kid == K_LOOKUP))) {
+    // level 1 brackets every kEventSample-th restriction launch (and every
+    // launch of the other level-1 kernels): each event record is a packet of
+    // its own in the queue, about 4 us between the kernels it separates, on
+    // the matmul's critical path
+    bool on = c->timing >= 2;
+    if (c->timing == 1 && kid == K_RESTRICT_COLS) on = c->event_seq[kid]++ % kEventSample == 0;
+    if (c->timing == 1 && (kid == K_RESTRICT_ROWS || kid == K_MERKLE || kid == K_NORM || kid == K_LOOKUP)) on = true;
+    if (on) {
       e0 = get_event(c);
       e1 = get_event(c);
       if (e0) record_event(c, e0);

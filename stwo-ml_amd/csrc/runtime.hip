@@ -496,6 +496,7 @@ extern "C" int gkr_ctx_reset_timing(gkr_ctx* c) {
   if (!c) return fail(GKR_ERR_INVALID, "null ctx");
   TRY(sync(c));
   for (auto& s : c->stats) s = KernelStat();
+  for (auto& e : c->event_seq) e = 0;
   return GKR_OK;
 }
 
