@@ -759,10 +759,12 @@ int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, cons
                            const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk,
                            const TripWait* tw = nullptr, CarriedFinish* carry_out = nullptr,
                            const CarriedFinish* carry_in = nullptr);
-// the whole sumcheck.
+// the whole sumcheck; after_last, when given, is called right after its last
+// launch (the hand-over), to queue work that must not sit between its trips
+// and may not allocate.
 int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& pl, qm31* w0, qm31* d0,
                         qm31* w1, qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3],
-                        const RoundSink* pre0 = nullptr);
+                        const RoundSink* pre0 = nullptr, const std::function<int()>* after_last = nullptr);
 // LayerNorm (ln) or RMSNorm layer reducer (norm.hip); commit_gamma: fill
 // gamma_commitment (one Poseidon mix per scale entry; the walk, which neither
 // mixes nor serializes it, skips it).

@@ -107,7 +107,7 @@ int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, cons
 // coefficients, nv challenges and the final (eq, w, d) values.
 int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& pl, qm31* w0, qm31* d0,
                         qm31* w1, qm31* d1, gkr_qm31* rp_out, qm31* chal, qm31 fin[3],
-                        const RoundSink* pre0) {
+                        const RoundSink* pre0, const std::function<int()>* after_last) {
   const int nv = pl.nv;
   if (nv == 0) {
     fin[0] = qm31_one();
@@ -165,12 +165,18 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
       sw = dw;
       sd = dd;
     }
-    if (j + 1 == nt) TRY(ho.launch<2>(sw, sd, tr.n, tr.K, pre ? &carry : nullptr));
+    if (j + 1 == nt) {
+      TRY(ho.launch<2>(sw, sd, tr.n, tr.K, pre ? &carry : nullptr));
+      if (after_last) TRY((*after_last)());
+    }
     return GKR_OK;
   };
   if (pre0) {  // trip 0 launched earlier, with its own finisher
     sks[0] = *pre0;
-    if (nt == 1) TRY(ho.launch<2>(sw, sd, pl.trips[0].n, pl.trips[0].K));
+    if (nt == 1) {
+      TRY(ho.launch<2>(sw, sd, pl.trips[0].n, pl.trips[0].K));
+      if (after_last) TRY((*after_last)());
+    }
   } else {
     TRY(launch_j(0, nullptr));
   }
@@ -350,39 +356,52 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       TRY(deliver_finish<2>(c, sk_prep, grid, counter));
     }
     if (eq_pre) TRY(eq3_launch_trip(c, epl, 0, d_w0, d_d0, 0, nullptr, nullptr, nullptr, kSlotEq0, &sk_eq0));
+  }
+  // The table side (multiplicities, their copies, the table-side sum) and the
+  // multiplicity sumcheck's first trip are needed only after the eq-sumcheck:
+  // they are queued behind its last launch (the hand-over), so they run while
+  // the host finishes the eq-sumcheck's last rounds instead of between its
+  // trips.  Their buffers are set up here: nothing queued after the
+  // eq-sumcheck's trips may allocate (a free would wait for those trips, which
+  // wait for the host).
+  const uint64_t hgroups = (n + kHistPerGroup - 1) / kHistPerGroup;
+  uint32_t* hist = nullptr;
+  if (lds_hist) TRY(ensureT(c, S_LKHIST, hgroups * (kHistBins / 2), &hist));
+  const std::vector<Trip> mtrips = plan_trips((int)table_log, kHostTailSum, kTripMaxK);
+  bool table_side_done = false;
+  std::function<int()> table_side = [&]() -> int {
+    table_side_done = true;
+    HostTimer ht(c, K_HOST_LAUNCH);
+    // the sink's sequence number is taken now: deliveries publish increasing
+    // numbers in stream order, and a wait takes any later number as proof
     TRY(make_sink(c, &sk_table, kSlotTable));
+    uint32_t* counter;
+    uint32_t base;
     if (lds_hist) {
       // counts of the masked input (the padding added to bin 0 afterwards),
       // then one pass over the bins: multiplicities, their QM31 and host
       // copies, table sum
-      const uint64_t groups = (n + kHistPerGroup - 1) / kHistPerGroup;
-      uint32_t* hist;
-      TRY(ensureT(c, S_LKHIST, groups * (kHistBins / 2), &hist));
-      GKR_LAUNCH(c, k_logup_hist, dim3((unsigned)groups), dim3(kHistBlock), 0, d_min, n, input->rows,
-                         input->cols, log2_exact(pcol), hist);
+      GKR_LAUNCH(c, k_logup_hist, dim3((unsigned)hgroups), dim3(kHistBlock), 0, d_min, n, input->rows,
+                 input->cols, log2_exact(pcol), hist);
       TRY(check_launch());
       const unsigned grid = partial_grid(tsize / 2);
       TRY(deliver_args(c, grid, &counter, &base));
-      GKR_LAUNCH(c, k_logup_table_pass, dim3(grid), dim3(kBlock), 0, hist, (int)groups,
-                         (uint32_t)(n - input->rows * input->cols), d_inv, tsize, m0, c->h_mult, sk_table, counter,
-                         base);
+      GKR_LAUNCH(c, k_logup_table_pass, dim3(grid), dim3(kBlock), 0, hist, (int)hgroups,
+                 (uint32_t)(n - input->rows * input->cols), d_inv, tsize, m0, c->h_mult, sk_table, counter, base);
       TRY(deliver_finish<1>(c, sk_table, grid, counter));
     } else {
       const unsigned grid = partial_grid(tsize);
       TRY(deliver_args(c, grid, &counter, &base));
-      GKR_LAUNCH(c, k_logup_table_sum, dim3(grid), dim3(kBlock), 0, d_inv, d_mult, tsize, sk_table,
-                         counter, base);
+      GKR_LAUNCH(c, k_logup_table_sum, dim3(grid), dim3(kBlock), 0, d_inv, d_mult, tsize, sk_table, counter, base);
       TRY(deliver_finish<1>(c, sk_table, grid, counter));
       // the multiplicities as QM31 for the sumcheck, and to the pinned host copy
-      GKR_LAUNCH(c, k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, d_mult, tsize, m0,
-                         c->h_mult, 1);
+      GKR_LAUNCH(c, k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, d_mult, tsize, m0, c->h_mult, 1);
       TRY(check_launch());
       c->mult_zero_entries = tsize;
     }
-  }
-  const std::vector<Trip> mtrips = plan_trips((int)table_log, kHostTailSum, kTripMaxK);
-  TRY(launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
-                  kSlotMult0, &sk_mult0));
+    return launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,
+                       kSlotMult0, &sk_mult0);
+  };
 
   // The trace sum goes into the transcript now; the table-side sum it must
   // equal is checked before the multiplicity sumcheck, so the histogram and
@@ -398,7 +417,8 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   std::vector<qm31> chal(nv);
   qm31 fin[3];
   TRY(eq3_sumcheck(c, C, cpt.data(), epl, d_w0, d_d0, d_w1, d_d1, out->eq_round_polys, chal.data(), fin,
-                   eq_pre ? &sk_eq0 : nullptr));
+                   eq_pre ? &sk_eq0 : nullptr, &table_side));
+  if (!table_side_done) TRY(table_side());
   const qm31 w_eval = fin[1];
   // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass;
   // the transcript does not use them before the multiplicity sumcheck, so they
