@@ -425,6 +425,9 @@ template <int M>
 __device__ __forceinline__ qm31 qm31_add_xor(qm31 t) {
   return qm31{m31_add_xor<M>(t.a), m31_add_xor<M>(t.b), m31_add_xor<M>(t.c), m31_add_xor<M>(t.d)};
 }
+__device__ __forceinline__ qm31 shfl_xor_q(qm31 q, int m) {
+  return qm31{shfl_xor_u32(q.a, m), shfl_xor_u32(q.b, m), shfl_xor_u32(q.c, m), shfl_xor_u32(q.d, m)};
+}
 __device__ __forceinline__ qm31 shfl_q(qm31 q, int src) {
   return qm31{(uint32_t)__shfl((int)q.a, src, 64), (uint32_t)__shfl((int)q.b, src, 64),
               (uint32_t)__shfl((int)q.c, src, 64), (uint32_t)__shfl((int)q.d, src, 64)};
@@ -805,16 +808,23 @@ __device__ __forceinline__ void m31_digits(uint32_t x, int32_t (&d)[4]) {
 constexpr int kR8TileRows = 16, kR8TileCols = 64;
 constexpr uint64_t kR8Tile = 1024;
 // Both Lagrange tables of a matmul restriction in one launch: out1[x] over
-// coordinates [0, n1) of pt (count1 entries) on the first eq_two_lead(count1)
-// threads, then out2[x] over [n1, pt.n) (count2 entries), one thread per
-// entry; the second table starts on a workgroup boundary.  With ldig, the
-// second table is also written as the digit blocks of the int8 weight-side
-// restriction (k_restrict_cols8): a wave's 64 columns are one 1 KB block,
-// whose 16 digits per column (digit q of component c of column x at byte
-// x % 16 of lane slot 16 ((x % 64) / 16) + 4 c + q) are transposed in LDS and
-// stored as one 16-byte lane slot per thread; the launch then covers whole
-// blocks, columns >= count2 with zero digits.
-__host__ __device__ inline uint64_t eq_two_lead(uint64_t count1) { return (count1 + kBlock - 1) / kBlock * kBlock; }
+// coordinates [0, n1) of pt (count1 entries), then out2[x] over [n1, pt.n)
+// (count2 entries) from entry eq_two_lead(count1) on (a workgroup boundary).
+// Four lanes take one entry: lane q multiplies the factors l = q mod 4 (the
+// products are issue-bound QM31 multiplications, so a quarter of the chain
+// per lane, two shuffle-and-multiply steps to join) and writes component q.
+// With ldig, the second table is also written as the digit blocks of the
+// int8 weight-side restriction (k_restrict_cols8): a workgroup's 64 columns
+// are one 1 KB block, whose 16 digits per column (digit d of component c of
+// column x at byte x % 16 of lane slot 16 ((x % 64) / 16) + 4 c + d; lane q
+// writes component q's four) are transposed in LDS and stored as one 16-byte
+// lane slot per thread of the first wave; the launch then covers whole blocks,
+// columns >= count2 with zero digits.
+constexpr int kEqLanes = 4;
+__host__ __device__ inline uint64_t eq_two_lead(uint64_t count1) {
+  constexpr uint64_t per_wg = kBlock / kEqLanes;  // entries per workgroup
+  return (count1 + per_wg - 1) / per_wg * per_wg;
+}
 // dpt given (a restriction launched ahead of its point): the point is read
 // from device memory, and the kernel returns unless *status == want.
 static __global__ void __launch_bounds__(kBlock) k_eq_two(PointArg pt, const PointArg* __restrict__ dpt,
@@ -822,7 +832,7 @@ static __global__ void __launch_bounds__(kBlock) k_eq_two(PointArg pt, const Poi
                                                    uint64_t count1, uint64_t count2, qm31* __restrict__ out1,
                                                    qm31* __restrict__ out2, uint8_t* __restrict__ ldig) {
   __shared__ PointLds sp;
-  __shared__ __align__(16) uint8_t sd[kBlock / 64][kR8Tile];
+  __shared__ __align__(16) uint8_t sd[kR8Tile];
   int ntot = pt.n;
   if (dpt) {
     if (status[0] != want) return;  // every thread alike
@@ -833,28 +843,35 @@ static __global__ void __launch_bounds__(kBlock) k_eq_two(PointArg pt, const Poi
   }
   const uint64_t lead = eq_two_lead(count1);
   const uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < lead) {  // whole workgroups
-    if (t < count1) st_q(out1, t, eq_prod(sp, 0, n1, t));
-    return;
-  }
-  const uint64_t x = t - lead;
-  const bool valid = x < count2;
-  const qm31 acc = valid ? eq_prod(sp, n1, ntot - n1, x) : qm31_zero();
-  if (valid) st_q(out2, x, acc);
-  if (!ldig) return;
-  const int lane = threadIdx.x & 63;
-  uint8_t* sdw = sd[threadIdx.x >> 6];
-  const uint32_t comp[4] = {acc.a, acc.b, acc.c, acc.d};
+  const uint64_t e = t / kEqLanes;
+  const int q = (int)(t % kEqLanes);
+  // lane q's part of prod_{l < m} (bit m-1-l of x ? r[s0+l] : 1 - r[s0+l]), then the join
+  const bool first = e < lead;  // whole workgroups
+  const uint64_t x = first ? e : e - lead;
+  const int s0 = first ? 0 : n1, m = first ? n1 : ntot - n1;
+  const bool valid = x < (first ? count1 : count2);
+  qm31 v = qm31_one();
+  if (valid)
+    for (int l = q; l < m; l += kEqLanes) v = qm31_mul(v, ((x >> (m - 1 - l)) & 1ull) ? sp.r[s0 + l] : sp.omr[s0 + l]);
+  v = qm31_mul(v, shfl_xor_q(v, 1));
+  v = qm31_mul(v, shfl_xor_q(v, 2));
+  const uint32_t comp[4] = {v.a, v.b, v.c, v.d};
+  uint32_t mine = comp[0];
 #pragma unroll
-  for (int c = 0; c < 4; c++) {
-    int32_t d[4];
-    m31_digits(comp[c], d);
+  for (int c = 1; c < 4; c++)
+    if (q == c) mine = comp[c];
+  if (!valid) mine = 0;
+  if (valid) reinterpret_cast<uint32_t*>(first ? out1 : out2)[4 * x + q] = mine;
+  if (first || !ldig) return;  // uniform per workgroup
+  int32_t d[4];
+  m31_digits(mine, d);
+  const int col = (int)(x & 63);  // the workgroup's 64 columns form block x / 64
 #pragma unroll
-    for (int q = 0; q < 4; q++) sdw[16 * (16 * (lane >> 4) + 4 * c + q) + (lane & 15)] = (uint8_t)d[q];
-  }
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  *reinterpret_cast<u32x4*>(ldig + (x >> 6) * kR8Tile + 16 * lane) = *reinterpret_cast<const u32x4*>(sdw + 16 * lane);
+  for (int j = 0; j < 4; j++) sd[16 * (16 * (col >> 4) + 4 * q + j) + (col & 15)] = (uint8_t)d[j];
+  __syncthreads();
+  if (threadIdx.x < 64)
+    *reinterpret_cast<u32x4*>(ldig + (x >> 6) * kR8Tile + 16 * threadIdx.x) =
+        *reinterpret_cast<const u32x4*>(sd + 16 * threadIdx.x);
 }
 // Split construction: hi table over variables [0, n-h), lo over [n-h, n).
 static __global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm31* __restrict__ lo) {

@@ -176,7 +176,8 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
       pt = make_point(both.data(), n_ri + n_rj);
     }
     TimedLaunch tl(c, K_EQ_TABLE, 16 * (m + n));
-    const uint64_t threads = eq_two_lead(m) + (ldig ? (n + kR8TileCols - 1) / kR8TileCols * kR8TileCols : n);
+    const uint64_t threads =
+        kEqLanes * (eq_two_lead(m) + (ldig ? (n + kR8TileCols - 1) / kR8TileCols * kR8TileCols : n));
     GKR_LAUNCH(c, k_eq_two, dim3(grid_for(threads)), dim3(kBlock), 0, pt, dp ? dp->pt : nullptr,
                dp ? dp->status : nullptr, dp ? dp->want : 0u, n_ri, m, n, Li, Lj, ldig);
     TRY(check_launch());
