@@ -755,6 +755,26 @@ static __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restri
   if (threadIdx.x == 0) publish_flag(flag, seq);
 }
 
+// ------------------------------------------------------------------ eq products, four lanes per entry
+// The eq-table kernels give each entry kEqLanes consecutive lanes: lane q
+// multiplies the factors l = q mod kEqLanes of prod_{l < m} (bit m-1-l of x ?
+// r[s+l] : 1 - r[s+l]) and two shuffle-and-multiply steps join them, so every
+// lane of the group holds the product (the QM31 products are issue-bound: a
+// quarter of the chain per lane).  Every lane of a group calls it, valid or
+// not (an invalid group returns 1); lane q then stores component q.
+constexpr int kEqLanes = 4;
+__device__ __forceinline__ qm31 eq_prod4(const PointLds& sp, int s, int m, uint64_t x, int q, bool valid) {
+  qm31 v = qm31_one();
+  if (valid)
+    for (int l = q; l < m; l += kEqLanes) v = qm31_mul(v, ((x >> (m - 1 - l)) & 1ull) ? sp.r[s + l] : sp.omr[s + l]);
+  v = qm31_mul(v, shfl_xor_q(v, 1));
+  v = qm31_mul(v, shfl_xor_q(v, 2));
+  return v;
+}
+__device__ __forceinline__ uint32_t qm31_comp(const qm31& v, int q) {
+  return q == 0 ? v.a : q == 1 ? v.b : q == 2 ? v.c : v.d;
+}
+
 // ------------------------------------------------------------------ eq parts
 // Small eq tables over runs of the claim point: table i covers coordinates
 // z[s_i .. s_i + m_i) (the first on the most significant bit) and has 2^m_i
@@ -771,13 +791,15 @@ struct EqPartsArg {
 static __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out) {
   __shared__ PointLds sp;
   stage_point(a.z, &sp);
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
+  const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t i = (uint32_t)(g / kEqLanes);
+  const int q = (int)(g % kEqLanes);
+  const bool valid = i < total;
   int t = 0;
-  while (t + 1 < a.count && i >= a.off[t + 1]) t++;
-  const uint32_t x = i - a.off[t];
-  const int s = a.s[t], m = a.m[t];
-  out[i] = eq_prod(sp, s, m, x);
+  while (valid && t + 1 < a.count && i >= a.off[t + 1]) t++;
+  const uint32_t x = valid ? i - a.off[t] : 0;
+  const qm31 v = eq_prod4(sp, a.s[t], a.m[t], x, q, valid);
+  if (valid) reinterpret_cast<uint32_t*>(out)[4 * (uint64_t)i + q] = qm31_comp(v, q);
 }
 
 // ------------------------------------------------------------------ eq / Lagrange
@@ -786,9 +808,11 @@ static __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict
 static __global__ void k_eq_direct(PointArg pt, uint64_t count, qm31* __restrict__ out) {
   __shared__ PointLds sp;
   stage_point(pt, &sp);
-  uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (x >= count) return;
-  st_q(out, x, eq_prod(sp, 0, pt.n, x));
+  const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t x = g / kEqLanes;
+  const int q = (int)(g % kEqLanes);
+  const qm31 v = eq_prod4(sp, 0, pt.n, x, q, x < count);
+  if (x < count) reinterpret_cast<uint32_t*>(out)[4 * x + q] = qm31_comp(v, q);
 }
 // Balanced base-256 digits of a canonical M31 value: centered to
 // v in (-P/2, P/2], v = sum_q d_q 256^q with d_q in [-128, 127].
@@ -820,7 +844,6 @@ constexpr uint64_t kR8Tile = 1024;
 // writes component q's four) are transposed in LDS and stored as one 16-byte
 // lane slot per thread of the first wave; the launch then covers whole blocks,
 // columns >= count2 with zero digits.
-constexpr int kEqLanes = 4;
 __host__ __device__ inline uint64_t eq_two_lead(uint64_t count1) {
   constexpr uint64_t per_wg = kBlock / kEqLanes;  // entries per workgroup
   return (count1 + per_wg - 1) / per_wg * per_wg;
@@ -878,13 +901,13 @@ static __global__ void k_eq_tables(PointArg pt, int h, qm31* __restrict__ hi, qm
   __shared__ PointLds sp;
   stage_point(pt, &sp);
   const uint64_t n_hi = 1ull << (pt.n - h), n_lo = 1ull << h;
-  uint64_t x = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (x < n_hi) {
-    st_q(hi, x, eq_prod(sp, 0, pt.n - h, x));
-  } else if (x < n_hi + n_lo) {
-    const uint64_t y = x - n_hi;
-    st_q(lo, y, eq_prod(sp, pt.n - h, h, y));
-  }
+  const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const uint64_t x = g / kEqLanes;
+  const int q = (int)(g % kEqLanes);
+  const bool in_hi = x < n_hi, valid = x < n_hi + n_lo;
+  const uint64_t y = in_hi ? x : x - n_hi;
+  const qm31 v = eq_prod4(sp, in_hi ? 0 : pt.n - h, in_hi ? pt.n - h : h, y, q, valid);
+  if (valid) reinterpret_cast<uint32_t*>(in_hi ? hi : lo)[4 * y + q] = qm31_comp(v, q);
 }
 static __global__ void k_eq_combine(const qm31* __restrict__ hi, const qm31* __restrict__ lo, int h, uint64_t count,
                              qm31* __restrict__ out) {

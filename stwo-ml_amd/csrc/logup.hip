@@ -87,7 +87,7 @@ int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
   TRY(ensureT(c, S_EQPARTS, total, &parts));
   {
     TimedLaunch tl(c, K_EQ_TABLE, 16ull * total);
-    GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(total)), dim3(kBlock), 0, arg, total, parts);
+    GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(kEqLanes * (uint64_t)total)), dim3(kBlock), 0, arg, total, parts);
   }
   return check_launch();
 }

@@ -105,14 +105,14 @@ int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out) {
   PointArg pt = make_point(r, n);
   TimedLaunch t(c, K_EQ_TABLE, 16 * count);
   if (n <= 10) {
-    GKR_LAUNCH(c, k_eq_direct, dim3(grid_for(count)), dim3(kBlock), 0, pt, count, out);
+    GKR_LAUNCH(c, k_eq_direct, dim3(grid_for(kEqLanes * count)), dim3(kBlock), 0, pt, count, out);
     return check_launch();
   }
   const int h = n / 2;
   qm31 *hi, *lo;
   TRY(ensureT(c, S_EQHI, 1ull << (n - h), &hi));
   TRY(ensureT(c, S_EQLO, 1ull << h, &lo));
-  GKR_LAUNCH(c, k_eq_tables, dim3(grid_for((1ull << (n - h)) + (1ull << h))), dim3(kBlock), 0, pt, h,
+  GKR_LAUNCH(c, k_eq_tables, dim3(grid_for(kEqLanes * ((1ull << (n - h)) + (1ull << h)))), dim3(kBlock), 0, pt, h,
                      hi, lo);
   TRY(check_launch());
   GKR_LAUNCH(c, k_eq_combine, dim3(grid_for(count)), dim3(kBlock), 0, hi, lo, h, count, out);
@@ -128,7 +128,7 @@ int eq_split(gkr_ctx* c, const qm31* r, int n, qm31** hi, qm31** lo, int* h) {
   TRY(ensureT(c, S_EQLO, n_lo, lo));
   PointArg pt = make_point(r, n);
   TimedLaunch t(c, K_EQ_TABLE, 16 * (n_hi + n_lo));
-  GKR_LAUNCH(c, k_eq_tables, dim3(grid_for(n_hi + n_lo)), dim3(kBlock), 0, pt, *h, *hi, *lo);
+  GKR_LAUNCH(c, k_eq_tables, dim3(grid_for(kEqLanes * (n_hi + n_lo))), dim3(kBlock), 0, pt, *h, *hi, *lo);
   return check_launch();
 }
 // The arrival counter of kernels that deliver their own results
