@@ -44,6 +44,7 @@ class Launcher {
   // (a sleeping thread takes a futex wake-up, several us, to resume).
   static constexpr double kSpinSeconds = 0.005;
 
+  // device < 0: the thread makes no HIP call of its own (the host-only tests)
   explicit Launcher(int device) : ring_(new Slot[kSlots]) {
     th_ = std::thread([this, device] { loop(device); });
   }
@@ -105,7 +106,7 @@ class Launcher {
   std::thread th_;
 
   void loop(int device) {
-    (void)hipSetDevice(device);
+    if (device >= 0) (void)hipSetDevice(device);
     uint64_t t = 0;
     for (;;) {
       if (head_.load(std::memory_order_acquire) == t) {
