@@ -389,6 +389,44 @@ def test_native_walk_fresh_claims(gpu_ctx):
     assert proof.serialize() == ref
 
 
+def test_walk_cancel_with_restriction_launched_ahead(gpu_ctx):
+    """A walk that fails after the next matmul's restriction was launched ahead of its claim point
+    (step 0's hand-over left by the test hook) cancels that queued wait: the context stays usable
+    and the same walk then gives the same proof as before, equal to the oracle's."""
+    log("case walk cancel with restriction launched ahead")
+    A1, B1 = O.synthetic(4, 64, 1, 51), O.synthetic(64, 32, 1, 52)
+    A2, B2 = O.synthetic(4, 32, 1, 53), O.synthetic(32, 16, 1, 54)
+    gs = [gpu_ctx.upload(M) for M in (A1, B1, A2, B2)]
+    F = G.CLAIM_FRESH
+    steps = [(G.STEP_MATMUL, F, gs[0], gs[1], 0, 0), (G.STEP_MATMUL, F, gs[2], gs[3], 0, 0)]
+
+    def run():
+        ch = G.PoseidonChannel()
+        ch.mix_u64(5)
+        proof = G.Proof()
+        fp, fv = G.prove_walk(gpu_ctx, ch, steps, proof)
+        proof.set_input_claim(fp, fv)
+        return ch.digest(), proof.serialize()
+
+    first = run()  # sizes the context's buffers, so the next walks launch step 1's restriction ahead
+    gpu_ctx.debug(G.DEBUG_HANDOVER_CANCEL, 0)
+    with pytest.raises(G.GkrError):
+        run()
+    assert run() == first
+    och = O.Channel()
+    och.mix_u64(5)
+    ref = [2]
+    for a, b in ((A1, B1), (A2, B2)):
+        r = och.draw_qm31s(lg(a.shape[0]) + lg(b.shape[1]))
+        v = O.matmul_output_claim(a, b, r)
+        och.mix_secure_field(v)
+        o = O.prove_matmul_layer(r, v, a, b, och)
+        O.serialize_matmul_layer(ref, o["round_polys"], o["final_a_eval"], o["final_b_eval"])
+        last = (o["next_point"], o["next_value"])
+    O.serialize_tail(ref, last[0], last[1], [], 0)
+    assert first == (och.digest(), ref)
+
+
 def test_native_walk_errors(gpu_ctx):
     """A chained first step without an initial claim and an unknown step kind are rejected."""
     log("case native walk errors")
