@@ -427,6 +427,41 @@ def test_walk_cancel_with_restriction_launched_ahead(gpu_ctx):
     assert first == (och.digest(), ref)
 
 
+def test_walk_without_launcher_thread(gpu_ctx):
+    """A context created with GKR_ASYNC_LAUNCH=0 (the calling thread issues every launch) proves
+    the same fresh-claim walk, bit for bit, as the default context (launches issued by the
+    context's launcher thread)."""
+    log("case walk without launcher thread")
+    old = os.environ.get("GKR_ASYNC_LAUNCH")
+    os.environ["GKR_ASYNC_LAUNCH"] = "0"
+    try:
+        sctx = G.Context(0)
+    finally:
+        if old is None:
+            del os.environ["GKR_ASYNC_LAUNCH"]
+        else:
+            os.environ["GKR_ASYNC_LAUNCH"] = old
+    try:
+        mats = [O.synthetic(4, 96, 1, 61), O.synthetic(96, 40, 1, 62), O.synthetic(4, 40, 1, 63),
+                O.synthetic(40, 24, 1, 64), O.synthetic(8, 40, 0, 65)]
+        F = G.CLAIM_FRESH
+        proofs = []
+        for ctx in (gpu_ctx, sctx):
+            gs = [ctx.upload(M) for M in mats]
+            steps = [(G.STEP_MATMUL, F, gs[0], gs[1], 0, 0), (G.STEP_ACTIVATION, F, gs[4], None, 5, 10),
+                     (G.STEP_MATMUL, F, gs[2], gs[3], 0, 0), (G.STEP_MATMUL, F, gs[2], gs[3], 0, 0)]
+            for _ in range(2):  # the second walk launches restrictions ahead of their points
+                ch = G.PoseidonChannel()
+                ch.mix_u64(9)
+                proof = G.Proof()
+                fp, fv = G.prove_walk(ctx, ch, steps, proof)
+                proof.set_input_claim(fp, fv)
+                proofs.append((ch.digest(), proof.serialize()))
+        assert proofs[0] == proofs[1] == proofs[2] == proofs[3]
+    finally:
+        sctx.close()
+
+
 def test_native_walk_errors(gpu_ctx):
     """A chained first step without an initial claim and an unknown step kind are rejected."""
     log("case native walk errors")
