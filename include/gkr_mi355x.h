@@ -135,9 +135,17 @@ int gkr_ctx_debug(gkr_ctx* ctx, int op, uint64_t arg);
 typedef struct gkr_matrix gkr_matrix;
 int gkr_matrix_upload(gkr_ctx* ctx, const uint32_t* host, uint64_t rows, uint64_t cols, gkr_matrix** out);
 /* Borrow device memory the caller owns (e.g. a torch tensor); not freed here.
- * The contents must stay unchanged while the matrix is in use.               */
+ * The library derives copies from a matrix's contents on first use and keeps
+ * them (the int8 copy of the weight-side restriction, the forward product's
+ * digit planes): a caller that writes to the memory afterwards must call
+ * gkr_matrix_invalidate before the matrix is used again.                    */
 int gkr_matrix_wrap_device(gkr_ctx* ctx, const uint32_t* device_ptr, uint64_t rows, uint64_t cols,
                            gkr_matrix** out);
+/* The contents of m changed outside the library (memory of
+ * gkr_matrix_wrap_device written by the caller): drops the copies derived
+ * from them, which the next use rebuilds.  No counterpart in the reference,
+ * which re-uploads its matrices on every call.                              */
+int gkr_matrix_invalidate(gkr_ctx* ctx, gkr_matrix* m);
 /* Fill a new resident matrix on the device from the documented synthetic
  * generator (counter-mode SplitMix64; kind 0 uniform M31, kind 1 int8-range). */
 int gkr_matrix_synthetic(gkr_ctx* ctx, uint64_t rows, uint64_t cols, int kind, uint64_t seed, gkr_matrix** out);
@@ -287,8 +295,9 @@ int gkr_sumcheck_product(gkr_ctx* ctx, const gkr_qvec* fa, const gkr_qvec* fb, g
  * Every device buffer the kernels need (fold levels, partial rows, arrival
  * counter) lives in a static 25 MiB device array, one per GPU, held until
  * the process ends; no hipMalloc or hipFree is called.  All calls on one GPU
- * share that array, so calls that overlap on one GPU (two contexts, two
- * threads) race.  Longer vectors fail with GKR_ERR_INVALID.               */
+ * share that array, so they take turns: a call holds a per-GPU lock until its
+ * kernels have finished, and a call from another context or thread on the
+ * same GPU waits for it.  Longer vectors fail with GKR_ERR_INVALID.       */
 int gkr_sumcheck_product_noalloc(gkr_ctx* ctx, const gkr_qm31* fa, const gkr_qm31* fb, uint64_t n, gkr_channel* ch,
                                  gkr_qm31* round_polys /* 3T */, gkr_qm31* challenges /* T */, gkr_qm31* final_a,
                                  gkr_qm31* final_b);

@@ -309,7 +309,7 @@ extern "C" int gkr_prove_aggregated_binding(gkr_ctx* c, gkr_channel* ch, const g
     a += len / 2 + 1;
     GKR_LAUNCH(c, k_bind_colmajor, dim3(grid_for(len)), dim3(kBlock), 0, B[k].b->dev, B[k].b->rows,
                        B[k].b->cols, B[k].log_pk, len, F0[k]);
-    TRY(check_launch());
+    TRY(check_launch(c));
   }
   int NP = 1;
   while (NP < P) NP *= 2;
@@ -335,7 +335,7 @@ extern "C" int gkr_prove_aggregated_binding(gkr_ctx* c, gkr_channel* ch, const g
     HIP_TRY(hipMemcpyAsync(dco, coords.data(), coords.size() * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
     GKR_LAUNCH(c, k_bind_eq, dim3(grid_for((uint64_t)P * (nhi + nlo))), dim3(kBlock), 0, dco, P, L, h,
                        dhi, dlo);
-    TRY(check_launch());
+    TRY(check_launch(c));
     std::vector<BindDesc> d;
     uint32_t wg = 0;
     for (size_t q = 0; q < ks.size(); q++) {
@@ -376,7 +376,7 @@ extern "C" int gkr_prove_aggregated_binding(gkr_ctx* c, gkr_channel* ch, const g
         GKR_LAUNCH(c, k_bind_finish<8>, dim3((unsigned)d.size()), dim3(kBlock), 0, dd, part, res);
         break;
     }
-    TRY(check_launch());
+    TRY(check_launch(c));
     std::vector<qm31> hres((size_t)2 * NP * d.size());
     HIP_TRY(hipMemcpyAsync(hres.data(), res, hres.size() * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
     TRY(sync(c));
@@ -511,7 +511,7 @@ extern "C" int gkr_prove_aggregated_binding(gkr_ctx* c, gkr_channel* ch, const g
     vs.len[k] = 1ull << B[k].nv;
   }
   GKR_LAUNCH(c, k_bind_virtual, dim3(grid_for(vtotal)), dim3(kBlock), 0, vs, P, cfg.n_max, vtotal, V);
-  TRY(check_launch());
+  TRY(check_launch(c));
   std::vector<gkr_qm31> pt(chal.size());
   for (size_t k = 0; k < chal.size(); k++) pt[k] = G(chal[k]);
   felt cm;

@@ -117,16 +117,7 @@ extern "C" int gkr_matmul_forward_into(gkr_ctx* c, const gkr_matrix* a, const gk
                 (unsigned long long)out->rows, (unsigned long long)out->cols);
   if (out == a || out == b) return fail(GKR_ERR_INVALID, "forward GEMM: output aliases an input");
   HIP_TRY(hipSetDevice(c->device));
-  if (out->bplanes || out->r8 || out->r8_state) {  // the contents change: drop the derived copies
-    HIP_TRY(hipStreamSynchronize(c->stream));
-    if (out->bplanes) (void)hipFree(out->bplanes);
-    if (out->r8) (void)hipFree(out->r8);
-    out->bplanes = nullptr;
-    out->bnplanes = 0;
-    out->r8 = nullptr;
-    out->r8_state = 0;
-  }
-  if (c->mm.a == out || c->mm.b == out) c->mm.valid = false;
+  TRY(drop_derived(c, out));  // the contents change
   return matmul_forward(c, a, const_cast<gkr_matrix*>(b), out->dev);
 }
 

@@ -35,14 +35,20 @@ using namespace gkr;
 // ------------------------------------------------------------------ errors
 // Records the message of a failure for gkr_last_error() and returns code.
 int fail(int code, const char* fmt, ...);
-// Every HIP call made through HIP_TRY first drains the launch rings
-// (launcher.h), so it never overtakes a launch queued before it.
-#define HIP_TRY(expr)                                                                       \
+// Every HIP call made through HIP_TRY first drains the launch ring of the
+// context `c` in scope (launcher.h), so it never overtakes a launch queued
+// before it on that context.  HIP_CHECK is for calls that touch no stream
+// or device memory (device queries), made where no context exists yet.
+#define HIP_CHECK(expr)                                                                     \
   do {                                                                                      \
-    drain_launches();                                                                       \
     hipError_t e_ = (expr);                                                                 \
     if (e_ != hipSuccess) return fail(GKR_ERR_DEVICE, "%s: %s (%s:%d)", #expr,              \
                                       hipGetErrorString(e_), __FILE__, __LINE__);           \
+  } while (0)
+#define HIP_TRY(expr) \
+  do {                \
+    drain(c);         \
+    HIP_CHECK(expr);  \
   } while (0)
 #define TRY(expr)             \
   do {                        \
@@ -138,7 +144,8 @@ struct gkr_matrix {
   uint64_t rows, cols;
   bool owned;
   // digit planes of the matrix as the B operand of the forward product
-  // (gemm.h), built on first use; the contents of a matrix never change
+  // (gemm.h), built on first use; kept until the contents change (written
+  // by gkr_matmul_forward_into, or declared changed by gkr_matrix_invalidate)
   int8_t* bplanes = nullptr;
   int bnplanes = 0;
   // int8 copy for the weight-side restriction (1 KB tiles of 16 rows x 64
@@ -149,6 +156,10 @@ struct gkr_matrix {
   uint64_t r8_nst = 0;
   int r8_state = 0;
 };
+
+// Drops the copies derived from m's contents (int8 copy, digit planes) and
+// a matmul claim computed over m; they are rebuilt on the next use.
+int drop_derived(gkr_ctx* c, gkr_matrix* m);
 
 struct gkr_qvec {
   gkr_ctx* ctx;
@@ -308,9 +319,11 @@ struct HostTimer {
 };
 void collect_timing(gkr_ctx* c);
 int sync(gkr_ctx* c);
-inline int check_launch() {
+// Launch errors of the calling thread and of c's launcher thread (the first
+// error its ring's launches returned), never another context's.
+inline int check_launch(gkr_ctx* c) {
   hipError_t e = hipGetLastError();
-  if (e == hipSuccess) e = launch_error();  // a launch the launcher thread issued
+  if (e == hipSuccess && c && c->launcher) e = c->launcher->take_error();
   if (e != hipSuccess) return fail(GKR_ERR_DEVICE, "kernel launch: %s", hipGetErrorString(e));
   return GKR_OK;
 }
@@ -355,14 +368,14 @@ int make_sink(gkr_ctx* c, RoundSink* sk, int slot = 0);
 // delivers the NQ results (after a multi-workgroup reducing kernel).
 template <int NQ>
 static int launch_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks) {
-  TRY(check_launch());
+  TRY(check_launch(c));
   GKR_LAUNCH(c, k_finish<NQ>, dim3(1), dim3(kBlock), 0, sk, (uint32_t)nblocks);
-  return check_launch();
+  return check_launch(c);
 }
 // The finisher of a launch made with deliver_args (none when it delivers itself).
 template <int NQ>
 static int deliver_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks, const uint32_t* counter) {
-  if (counter) return check_launch();
+  if (counter) return check_launch(c);
   return launch_finish<NQ>(c, sk, nblocks);
 }
 // Wait until result `seq` has been published and copy NQ values.  The wait
@@ -376,7 +389,7 @@ constexpr double kWaitWallSeconds = 60.0;
 template <int NQ>
 static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_HOST_WAIT_TAIL, int slot = 0,
                        uint32_t hand_mb = 0) {
-  TRY(check_launch());
+  TRY(check_launch(c));
   HostTimer ht(c, timer);
   volatile uint32_t* flag = c->h_flag;
   volatile uint32_t* expired = &c->mailbox->expired;
@@ -387,7 +400,7 @@ static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_H
       return fail(GKR_ERR_DEVICE, "kernel launched ahead stopped waiting for its challenges (mailbox %u)", hand_mb);
     if ((spins & 0xFFFF) != 0xFFFF) continue;
     if (spins == 0xFFFF) t0 = std::chrono::steady_clock::now();
-    TRY(check_launch());
+    TRY(check_launch(c));
     // while launches are still being issued the stream has not drained
     const hipError_t e = c->launcher && !c->launcher->idle() ? hipErrorNotReady : hipStreamQuery(c->stream);
     if (e == hipSuccess) {
@@ -446,7 +459,7 @@ struct HandoverSession {
     GKR_LAUNCH(c, k_handover<NV>, dim3(1), dim3(kBlock), 0, a, b, (uint32_t)len, k, c->mailbox,
                        mb_seq, spin_limit, c->h_vec, c->h_flag, res_seq, fin ? *fin : none);
     launched = true;
-    return check_launch();
+    return check_launch(c);
   }
   int post(const qm31* chal, int k) {
     if (cancel_before_post) return fail(GKR_ERR_DEVICE, "hand-over cancelled before the challenges were posted");
@@ -579,7 +592,7 @@ struct AheadTrips {
     TRY(ensureT(c, S_TRIPMB, 16, &words));  // status word, then kTripMaxK challenges at 16-byte offset
     if (!c->tripmb_valid) {  // fresh memory: the status may not hold a future sequence number
       GKR_LAUNCH(c, k_zero_u32, dim3(1), dim3(64), 0, words, 16u);
-      TRY(check_launch());
+      TRY(check_launch(c));
       c->tripmb_valid = true;
     }
     tw->mb = c->mailbox;

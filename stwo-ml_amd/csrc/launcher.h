@@ -12,9 +12,10 @@
 //
 // Ordering rule: every other HIP call of the library that touches memory or
 // a stream (copies, fills, frees, synchronisations, stream queries, event
-// records outside the ring) first drains the ring (drain_launches()), so it
-// never overtakes a launch queued before it.  Launch errors are recorded by
-// the launcher thread and reported by check_launch() and by the waits.
+// records outside the ring) first drains the ring of the context it works
+// on, so it never overtakes a launch queued before it on that context.
+// Launch errors are recorded by the launcher thread and reported, for that
+// context only, by check_launch(c) and by the waits.
 //
 // One producer per ring: the thread that calls the library on the context.
 #pragma once
@@ -142,29 +143,6 @@ class Launcher {
     }
   }
 };
-
-// Launchers of the live contexts, for drain_launches() (HIP calls made where
-// no context is in reach, e.g. inside HIP_TRY).
-constexpr int kMaxLaunchers = 64;
-extern std::atomic<Launcher*> g_launchers[kMaxLaunchers];
-void register_launcher(Launcher* l);
-void unregister_launcher(Launcher* l);
-inline void drain_launches() {
-  for (int i = 0; i < kMaxLaunchers; i++) {
-    const Launcher* l = g_launchers[i].load(std::memory_order_acquire);
-    if (l) l->drain();
-  }
-}
-inline hipError_t launch_error() {
-  for (int i = 0; i < kMaxLaunchers; i++) {
-    Launcher* l = g_launchers[i].load(std::memory_order_acquire);
-    if (l) {
-      const hipError_t e = l->take_error();
-      if (e != hipSuccess) return e;
-    }
-  }
-  return hipSuccess;
-}
 
 // A kernel launch with its arguments converted to the kernel's parameter
 // types now, issued through l (or at once when l is null).

@@ -89,7 +89,7 @@ int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
     TimedLaunch tl(c, K_EQ_TABLE, 16ull * total);
     GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(kEqLanes * (uint64_t)total)), dim3(kBlock), 0, arg, total, parts);
   }
-  return check_launch();
+  return check_launch(c);
 }
 // Launch trip j of the plan over sources w, d (np pending challenges pend),
 // folded vectors to dw, dd when given.
@@ -341,7 +341,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     // the table's fractions: one inversion per table entry
     GKR_LAUNCH(c, k_logup_inv_table, dim3(grid_for(tsize)), dim3(kBlock), 0, d_table, tsize, gamma,
                        beta, d_inv);
-    TRY(check_launch());
+    TRY(check_launch(c));
     TRY(make_sink(c, &sk_prep, kSlotPrep));
     uint32_t* counter;
     uint32_t base;
@@ -383,7 +383,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       // copies, table sum
       GKR_LAUNCH(c, k_logup_hist, dim3((unsigned)hgroups), dim3(kHistBlock), 0, d_min, n, input->rows,
                  input->cols, log2_exact(pcol), hist);
-      TRY(check_launch());
+      TRY(check_launch(c));
       const unsigned grid = partial_grid(tsize / 2);
       TRY(deliver_args(c, grid, &counter, &base));
       GKR_LAUNCH(c, k_logup_table_pass, dim3(grid), dim3(kBlock), 0, hist, (int)hgroups,
@@ -396,7 +396,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       TRY(deliver_finish<1>(c, sk_table, grid, counter));
       // the multiplicities as QM31 for the sumcheck, and to the pinned host copy
       GKR_LAUNCH(c, k_u32_to_q, dim3(grid_for(tsize)), dim3(kBlock), 0, d_mult, tsize, m0, c->h_mult, 1);
-      TRY(check_launch());
+      TRY(check_launch(c));
       c->mult_zero_entries = tsize;
     }
     return launch_trip(c, 2, mtrips[0].K, m0, nullptr, tsize, 0, nullptr, nullptr, nullptr, nullptr, nullptr, 0,

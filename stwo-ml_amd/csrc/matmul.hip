@@ -2,6 +2,8 @@
 // sumcheck, reduce_matmul_layer_with_backend, the SIMD variants, the ZkmlOps
 // MLE helpers and the product sumcheck over resident QM31 vectors.
 #include "internal.h"
+
+#include <mutex>
 // ------------------------------------------------------------------ matmul reduction
 // The weight-side restriction leaves f_b as column-chunk partials; the first
 // product trip adds them (and stores f_b), or finish_fb does when another
@@ -12,7 +14,7 @@ static int finish_fb(gkr_ctx* c) {
   TRY(ensureT(c, S_FB0, c->fb_pk, &fb));
   GKR_LAUNCH(c, k_restrict_cols_finish, dim3(grid_for(c->fb_pk)), dim3(kBlock), 0, (const qm31*)c->buf[S_COLPART], c->fb_rows, c->fb_pk, c->fb_chunks, fb);
   c->fb_pending = false;
-  return check_launch();
+  return check_launch(c);
 }
 // The int8 copy of weight B for the restriction (k_to_int8), on first use:
 // one pass over B and a 4-byte read-back of the range flag.  Skipped when
@@ -37,7 +39,7 @@ static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
   const uint64_t slots = nrt * nst * 64;  // 16-byte lane slots
   const unsigned grid = (unsigned)std::min<uint64_t>((slots + kBlock - 1) / kBlock, 4096);
   GKR_LAUNCH(c, k_to_int8, dim3(grid), dim3(kBlock), 0, B->dev, B->rows, B->cols, nst, slots, (u32x4*)r8, bad);
-  TRY(check_launch());
+  TRY(check_launch(c));
   uint32_t flag = 1;
   HIP_TRY(hipMemcpyAsync(c->h_res, bad, sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
   TRY(sync(c));
@@ -181,7 +183,7 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
         kEqLanes * (eq_two_lead(m) + (ldig ? (n + kR8TileCols - 1) / kR8TileCols * kR8TileCols : n));
     GKR_LAUNCH(c, k_eq_two, dim3(grid_for(threads)), dim3(kBlock), 0, pt, dp ? dp->pt : nullptr,
                dp ? dp->status : nullptr, dp ? dp->want : 0u, n_ri, m, n, Li, Lj, ldig);
-    TRY(check_launch());
+    TRY(check_launch(c));
   } else {
     TRY(eq_table(c, r_i, n_ri, m, Li));
     TRY(eq_table(c, r_j, n_rj, n, Lj));
@@ -194,7 +196,7 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(p.act_blocks + p.nrt * p.gc)), dim3(kBlock), 0,
                (const u32x4*)B->r8, k, p.nst, (const u32x4*)ldig, (uint32_t)p.chunk, (uint32_t*)part, rows,
                (uint32_t)p.act_blocks, (uint32_t)p.nrt);
-    TRY(check_launch());
+    TRY(check_launch(c));
   } else {
     // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
     TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
@@ -205,7 +207,7 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
     else
       GKR_LAUNCH(c, k_restrict_cols<false>, grid, dim3(kBlock), 0, B->dev, k, n, p.chunk, Lj, (uint32_t*)part, rows,
                  (uint32_t)p.act_blocks, (uint32_t)p.gr);
-    TRY(check_launch());
+    TRY(check_launch(c));
   }
   c->fb_pending = true;
   c->fb_rows = k;
@@ -245,7 +247,7 @@ int prelaunch_matmul(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, bool*
     HostTimer ht(c, K_HOST_LAUNCH);
     GKR_LAUNCH(c, k_point_wait, dim3(1), dim3(64), 0, c->mailbox, dp.want, kWaitSpinLimit, n_ri + n_rj,
                reinterpret_cast<PointArg*>(pw + 256), reinterpret_cast<uint32_t*>(pw));
-    TRY(check_launch());
+    TRY(check_launch(c));
   }
   c->pre.active = true;  // from here on a failure leaves a wait that the walk cancels
   c->pre.want = dp.want;
@@ -727,7 +729,7 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
     TimedLaunch t(c, K_RESTRICT_ROWS, 4ull * n_blocks * a->rows * a->cols + 16 * a->rows + 16 * pk);
     GKR_LAUNCH(c, k_restrict_rows_simd, dim3((unsigned)((pk + 63) / 64)), dim3(kSimdWaves * 64), 0, blk,
                        a->rows, a->cols, pk, (const qm31*)Li, fa);
-    TRY(check_launch());
+    TRY(check_launch(c));
   }
   TRY(finish_fb(c));
   std::vector<gkr_qm31> chal(T > 0 ? T : 1);
@@ -856,13 +858,13 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
                        a->cols, pk, (const qm31*)Li, ea);
     GKR_LAUNCH(c, k_restrict_cols_blocks, dim3((unsigned)((pk + kColWaves - 1) / kColWaves), n_blocks),
                        dim3(kBlock), 0, pb, b->rows, b->cols, pk, (const qm31*)Lj, eb);
-    TRY(check_launch());
+    TRY(check_launch(c));
   }
   std::vector<qm31> D((size_t)n_blocks * n_blocks);
   if (nbv > 0) {
     GKR_LAUNCH(c, k_block_gram, dim3(n_blocks * n_blocks), dim3(kBlock), 0, (const qm31*)ea,
                        (const qm31*)eb, n_blocks, pk, gram);
-    TRY(check_launch());
+    TRY(check_launch(c));
     HIP_TRY(hipMemcpyAsync(D.data(), gram, D.size() * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
     TRY(sync(c));
   }
@@ -937,7 +939,7 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
   const dim3 gq((unsigned)((pk + kColWaves - 1) / kColWaves));  // one wave per entry
   GKR_LAUNCH(c, k_combine_q, gq, dim3(kBlock), 0, (const qm31*)ea, qw, n_blocks, pk, fa0);
   GKR_LAUNCH(c, k_combine_q, gq, dim3(kBlock), 0, (const qm31*)eb, qw, n_blocks, pk, fb0);
-  TRY(check_launch());
+  TRY(check_launch(c));
   std::vector<gkr_qm31> kchal(T > 0 ? T : 1);
   if (T == 0) {
     TRY(finish_fb(c));  // the sums read f_b from S_FB0
@@ -1012,7 +1014,7 @@ extern "C" int gkr_restrict_mle(gkr_ctx* c, const gkr_qm31* mle, uint64_t len, c
   HIP_TRY(hipMemcpyAsync(dm, mle, len * sizeof(qm31), hipMemcpyHostToDevice, c->stream));
   TRY(eq_table(c, pt.data(), (int)n_assign, nx, eq));
   GKR_LAUNCH(c, k_restrict_q, dim3(grid_for(rest)), dim3(kBlock), 0, dm, eq, nx, rest, dout);
-  TRY(check_launch());
+  TRY(check_launch(c));
   HIP_TRY(hipMemcpyAsync(out, dout, rest * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
   return sync(c);
 }
@@ -1044,7 +1046,7 @@ extern "C" int gkr_qvec_synthetic(gkr_ctx* c, uint64_t n, uint64_t seed, gkr_qve
   qm31* d = nullptr;
   HIP_TRY(hipMalloc(&d, n * sizeof(qm31)));
   GKR_LAUNCH(c, k_fill_synth_q, dim3(partial_grid(n) * 8), dim3(kBlock), 0, d, n, seed);
-  int rc = check_launch();
+  int rc = check_launch(c);
   if (rc == GKR_OK) rc = sync(c);
   if (rc != GKR_OK) {
     drain(c);
@@ -1114,6 +1116,11 @@ extern "C" int gkr_sumcheck_product(gkr_ctx* c, const gkr_qvec* fa, const gkr_qv
 // every device buffer comes from the static scratch array.  The arrival
 // counter's expected value belongs to the scratch copy, so the context's
 // own counter state is set aside for the call and restored afterwards.
+// Every call on one GPU shares that GPU's static scratch array, so the calls
+// on a device take turns: each holds its device's lock from its first device
+// call until its stream has drained.
+constexpr int kNoAllocMaxDevices = 64;
+static std::mutex g_noalloc_mu[kNoAllocMaxDevices];
 extern "C" int gkr_sumcheck_product_noalloc(gkr_ctx* c, const gkr_qm31* fa, const gkr_qm31* fb, uint64_t n,
                                             gkr_channel* ch, gkr_qm31* round_polys, gkr_qm31* challenges,
                                             gkr_qm31* final_a, gkr_qm31* final_b) {
@@ -1125,6 +1132,8 @@ extern "C" int gkr_sumcheck_product_noalloc(gkr_ctx* c, const gkr_qm31* fa, cons
                 (unsigned long long)n, (unsigned long long)kNoAllocMaxN);
   const int T = log2_exact(n);
   if (T > 0 && (!round_polys || !challenges)) return fail(GKR_ERR_INVALID, "null output arrays");
+  if (c->device >= kNoAllocMaxDevices) return fail(GKR_ERR_INVALID, "device %d beyond the lock table", c->device);
+  std::lock_guard<std::mutex> turn(g_noalloc_mu[c->device]);
   HIP_TRY(hipSetDevice(c->device));
   for (const gkr_qm31* p : {fa, fb}) {  // device memory of this context's GPU, or the kernels would fault
     hipPointerAttribute_t at;
@@ -1160,6 +1169,7 @@ extern "C" int gkr_sumcheck_product_noalloc(gkr_ctx* c, const gkr_qm31* fa, cons
   c->trip_count = saved_count;
   c->trip_count_valid = saved_valid;
   c->timing = saved_timing;
-  return rc;
+  const int rs = sync(c);  // nothing of this call still touches the scratch array when the lock is released
+  return rc != GKR_OK ? rc : rs;
 }
 

@@ -70,10 +70,10 @@ static int mul_stage_matrices(gkr_ctx* c, const gkr_matrix* lhs, const gkr_matri
   TRY(ensureT(c, S_D0, nl, &d_d0));
   GKR_LAUNCH(c, k_pad_q, dim3(grid_for(nl)), dim3(kBlock), 0, lhs->dev, lhs->rows, lhs->cols,
                      log2_exact(next_pow2(lhs->cols)), nl, d_w0);
-  TRY(check_launch());
+  TRY(check_launch(c));
   GKR_LAUNCH(c, k_pad_q, dim3(grid_for(nl)), dim3(kBlock), 0, rhs->dev, rhs->rows, rhs->cols,
                      log2_exact(next_pow2(rhs->cols)), nl, d_d0);
-  TRY(check_launch());
+  TRY(check_launch(c));
   *nv_out = nv;
   return GKR_OK;
 }
@@ -149,7 +149,7 @@ extern "C" int gkr_mul_output_claim(gkr_ctx* c, const gkr_matrix* lhs, const gkr
   qm31* parts;
   TRY(ensureT(c, S_EQPARTS, total, &parts));
   GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(kEqLanes * (uint64_t)total)), dim3(kBlock), 0, arg, total, parts);
-  TRY(check_launch());
+  TRY(check_launch(c));
   RoundSink sk;
   TRY(launch_trip(c, 1, 0, d_w0, d_d0, n, 0, nullptr, nullptr, nullptr, parts, parts + arg.off[1], h, 0, &sk));
   qm31 v[1];

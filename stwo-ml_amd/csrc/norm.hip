@@ -138,7 +138,7 @@ int norm_stats(gkr_ctx* c, const gkr_matrix* X, bool ln, uint64_t dim, NormShape
     GKR_LAUNCH(c, k_norm_rows, dim3((unsigned)X->rows), dim3(kBlock), 0, X->dev, X->cols, act_real,
                        d_sums);
   }
-  TRY(check_launch());
+  TRY(check_launch(c));
   HIP_TRY(hipMemcpyAsync(sums.data(), d_sums, sums.size() * sizeof(uint32_t), hipMemcpyDeviceToHost, c->stream));
   TRY(sync(c));
   const uint32_t act_m = m31_from_u32((uint32_t)(S->active % P));
@@ -203,7 +203,7 @@ int norm_prepare(gkr_ctx* c, const gkr_matrix* X, const NormShape& S, const uint
                        log2_exact(S.pcol), S.n, S.ln ? 1 : 0, S.active, d_rowv, d_gamma, d_gamma ? ng : 0, w, d,
                        in_q, in_u, out_u);
   }
-  TRY(check_launch());
+  TRY(check_launch(c));
   // the host copies of rowv / gamma must outlive the copies
   return sync(c);
 }

@@ -106,7 +106,7 @@ int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out) {
   TimedLaunch t(c, K_EQ_TABLE, 16 * count);
   if (n <= 10) {
     GKR_LAUNCH(c, k_eq_direct, dim3(grid_for(kEqLanes * count)), dim3(kBlock), 0, pt, count, out);
-    return check_launch();
+    return check_launch(c);
   }
   const int h = n / 2;
   qm31 *hi, *lo;
@@ -114,9 +114,9 @@ int eq_table(gkr_ctx* c, const qm31* r, int n, uint64_t count, qm31* out) {
   TRY(ensureT(c, S_EQLO, 1ull << h, &lo));
   GKR_LAUNCH(c, k_eq_tables, dim3(grid_for(kEqLanes * ((1ull << (n - h)) + (1ull << h)))), dim3(kBlock), 0, pt, h,
                      hi, lo);
-  TRY(check_launch());
+  TRY(check_launch(c));
   GKR_LAUNCH(c, k_eq_combine, dim3(grid_for(count)), dim3(kBlock), 0, hi, lo, h, count, out);
-  return check_launch();
+  return check_launch(c);
 }
 // The high / low factor tables of eq(r, .) over n coordinates (S_EQHI over
 // the first n - h, S_EQLO over the last h = n / 2), one launch.
@@ -129,7 +129,7 @@ int eq_split(gkr_ctx* c, const qm31* r, int n, qm31** hi, qm31** lo, int* h) {
   PointArg pt = make_point(r, n);
   TimedLaunch t(c, K_EQ_TABLE, 16 * (n_hi + n_lo));
   GKR_LAUNCH(c, k_eq_tables, dim3(grid_for(kEqLanes * (n_hi + n_lo))), dim3(kBlock), 0, pt, *h, *hi, *lo);
-  return check_launch();
+  return check_launch(c);
 }
 // The arrival counter of kernels that deliver their own results
 // (sink_finish_counted, fused trips): the base value for a launch of `grid`
@@ -138,7 +138,7 @@ int arrival_counter(gkr_ctx* c, unsigned grid, uint32_t** counter, uint32_t* bas
   TRY(ensureT(c, S_TRIPCNT, 1, counter));
   if (!c->trip_count_valid) {
     GKR_LAUNCH(c, k_zero_u32, dim3(1), dim3(64), 0, *counter, 1u);
-    TRY(check_launch());
+    TRY(check_launch(c));
     c->trip_count = 0;
     c->trip_count_valid = true;
   }
@@ -272,11 +272,11 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
     CarriedFinish none;
     memset(&none, 0, sizeof none);
     GKR_LAUNCH(c, k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, tw, np, carry_in ? *carry_in : none);
-    TRY(check_launch());
+    TRY(check_launch(c));
   }
   GKR_LAUNCH(c, (k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, sa, sb, n, np, al, da, db, hi, lo, h,
                      sk, counter, base, b_rows, b_chunks, tw);
-  TRY(check_launch());
+  TRY(check_launch(c));
   if (counter) return GKR_OK;
   if (carry_out) {  // the next kernel of the chain adds the rows
     carry_out->sk = sk;
@@ -287,7 +287,7 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
     return GKR_OK;
   }
   GKR_LAUNCH(c, k_finish_wide<NQ>, dim3(1), dim3(kFinishBlock), 0, sk, grid);
-  return check_launch();
+  return check_launch(c);
 }
 int launch_trip(gkr_ctx* c, int kind, int K, const qm31* sa, const qm31* sb, uint64_t n, int np,
                        const qm31* pend, qm31* da, qm31* db, const qm31* hi, const qm31* lo, int h, int slot,
@@ -352,27 +352,13 @@ int dot_m31(gkr_ctx* c, const uint32_t* v, const qm31* eq, uint64_t n, qm31* out
   return wait_sink<1>(c, sk, out);
 }
 // ------------------------------------------------------------------ context ABI
-std::atomic<Launcher*> gkr::g_launchers[kMaxLaunchers];
-void gkr::register_launcher(Launcher* l) {
-  for (int i = 0; i < kMaxLaunchers; i++) {
-    Launcher* none = nullptr;
-    if (g_launchers[i].compare_exchange_strong(none, l)) return;
-  }
-}
-void gkr::unregister_launcher(Launcher* l) {
-  for (int i = 0; i < kMaxLaunchers; i++) {
-    Launcher* mine = l;
-    if (g_launchers[i].compare_exchange_strong(mine, nullptr)) return;
-  }
-}
-
 extern "C" void gkr_ctx_destroy(gkr_ctx* c);
 extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   if (!out) return fail(GKR_ERR_INVALID, "null out");
   int n = 0;
-  HIP_TRY(hipGetDeviceCount(&n));
+  HIP_CHECK(hipGetDeviceCount(&n));
   if (device < 0 || device >= n) return fail(GKR_ERR_INVALID, "device %d not present (%d devices)", device, n);
-  HIP_TRY(hipSetDevice(device));
+  HIP_CHECK(hipSetDevice(device));
   gkr_ctx* c = new gkr_ctx();
   c->device = device;
   const char* i8 = getenv("GKR_INT8_WEIGHTS");
@@ -407,17 +393,9 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   c->mailbox->seq = 0;
   c->mailbox->expired = 0;
   // Launches are issued by a thread of their own unless GKR_ASYNC_LAUNCH=0
-  // (the launch cost then falls on the caller's thread).  A context beyond
-  // the registry's kMaxLaunchers live launchers issues its own launches.
+  // (the launch cost then falls on the caller's thread).
   const char* al = getenv("GKR_ASYNC_LAUNCH");
-  if (!(al && al[0] == '0' && al[1] == 0)) {
-    int live = 0;
-    for (int i = 0; i < kMaxLaunchers; i++) live += g_launchers[i].load() != nullptr;
-    if (live < kMaxLaunchers) {
-      c->launcher.reset(new Launcher(device));
-      register_launcher(c->launcher.get());
-    }
-  }
+  if (!(al && al[0] == '0' && al[1] == 0)) c->launcher.reset(new Launcher(device));
   *out = c;
   return GKR_OK;
 }
@@ -426,7 +404,6 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   (void)hipSetDevice(c->device);
   if (c->launcher) {  // issue what is queued, then stop the thread
     c->launcher->drain();
-    unregister_launcher(c->launcher.get());
     c->launcher.reset();
   }
   if (c->stream) (void)hipStreamSynchronize(c->stream);
@@ -537,7 +514,7 @@ extern "C" int gkr_matrix_synthetic(gkr_ctx* c, uint64_t rows, uint64_t cols, in
   uint32_t* d = nullptr;
   HIP_TRY(hipMalloc(&d, n * sizeof(uint32_t)));
   GKR_LAUNCH(c, k_fill_synth, dim3(partial_grid(n) * 8), dim3(kBlock), 0, d, n, kind, seed);
-  int rc = check_launch();
+  int rc = check_launch(c);
   if (rc == GKR_OK) rc = sync(c);
   if (rc != GKR_OK) {
     drain(c);
@@ -565,6 +542,26 @@ extern "C" void gkr_matrix_free(gkr_matrix* m) {
     if (m->r8) (void)hipFree(m->r8);
   }
   delete m;
+}
+int drop_derived(gkr_ctx* c, gkr_matrix* m) {
+  if (c->mm.a == m || c->mm.b == m) c->mm.valid = false;
+  if (m->bplanes || m->r8) {
+    HIP_TRY(hipStreamSynchronize(c->stream));  // no queued kernel still reads them
+    if (m->bplanes) (void)hipFree(m->bplanes);
+    if (m->r8) (void)hipFree(m->r8);
+  }
+  m->bplanes = nullptr;
+  m->bnplanes = 0;
+  m->r8 = nullptr;
+  m->r8_nst = 0;
+  m->r8_state = 0;
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_invalidate(gkr_ctx* c, gkr_matrix* m) {
+  if (!c || !m) return fail(GKR_ERR_INVALID, "null argument");
+  if (m->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another (or a destroyed) context");
+  HIP_TRY(hipSetDevice(c->device));
+  return drop_derived(c, m);
 }
 gkr_matrix* new_matrix(gkr_ctx* c, uint32_t* dev, uint64_t rows, uint64_t cols, bool owned) {
   gkr_matrix* m = new gkr_matrix{c, dev, rows, cols, owned};
@@ -609,7 +606,7 @@ extern "C" int gkr_bench_copy(gkr_ctx* c, uint64_t bytes, int iters, double* cop
     (void)hipEventSynchronize(e1);
     (void)hipEventElapsedTime(&ms, e0, e1);
     *read_gbps = (double)n * 16 * iters / (ms * 1e-3) / 1e9;
-    if (check_launch() != GKR_OK) rc = fail(GKR_ERR_DEVICE, "copy kernels failed");
+    if (check_launch(c) != GKR_OK) rc = fail(GKR_ERR_DEVICE, "copy kernels failed");
   }
   if (e0) (void)hipEventDestroy(e0);
   if (e1) (void)hipEventDestroy(e1);

@@ -176,6 +176,7 @@ SIGNATURES = [
     ("gkr_qvec_free", None, [_P]),
     ("gkr_qvec_device_ptr", _P, [_P]),
     ("gkr_matrix_device_ptr", _P, [_P]),
+    ("gkr_matrix_invalidate", C.c_int, [_P, _P]),
     ("gkr_prove_aggregated_binding", C.c_int, [_P, _P, _P, C.c_size_t, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("gkr_proof_num_binding_groups", C.c_size_t, [_P]),
     ("gkr_proof_binding_group", C.c_int, [_P, C.c_size_t, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -888,6 +889,11 @@ class Matrix:
     def device_ptr(self) -> int:
         """Device address of the row-major u32 entries (gkr_matrix_device_ptr)."""
         return lib().gkr_matrix_device_ptr(self._h)
+
+    def invalidate(self) -> None:
+        """gkr_matrix_invalidate: the entries changed outside the library (wrapped device memory
+        written by the caller); the copies derived from them are rebuilt on the next use."""
+        _check(lib().gkr_matrix_invalidate(self.ctx.handle, self._h))
 
     @property
     def handle(self) -> int:

@@ -2,12 +2,12 @@
 // wrap-around, error reporting, sleep and wake-up, draining on destruction.
 // The closures do host work instead of HIP calls, so no GPU is needed.
 #include <chrono>
+#include <memory>
 #include <thread>
 #include <vector>
 
 #include "../../stwo-ml_amd/csrc/launcher.h"
 
-std::atomic<gkr::Launcher*> gkr::g_launchers[gkr::kMaxLaunchers];
 
 extern "C" int lt_order(int n) {
   std::vector<int> seen;
@@ -92,4 +92,17 @@ extern "C" int lt_big_closure() {
     l.drain();
   }
   return bad;
+}
+
+// Two rings: an error on one is taken from that ring only; the other's stays clear.
+extern "C" int lt_errors_per_ring() {
+  gkr::Launcher a(-1), b(-1);
+  a.submit([]() -> hipError_t { return hipErrorInvalidValue; });
+  b.submit([]() -> hipError_t { return hipSuccess; });
+  a.drain();
+  b.drain();
+  if (b.take_error() != hipSuccess) return 1;
+  if (a.take_error() != hipErrorInvalidValue) return 2;
+  if (a.take_error() != hipSuccess) return 3;
+  return 0;
 }

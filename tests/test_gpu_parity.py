@@ -59,9 +59,13 @@ def _random_point(rng, n):
     return [tuple(rng.randrange(P) for _ in range(4)) for _ in range(n)]
 
 
-def _compare_layer(ctx, A, B, seed, label):
+def _compare_layer(ctx, A, B, seed, label, a=None, b=None):
+    """One matmul layer (fresh output claim, then the reduction) on the GPU against the oracle; a, b:
+    resident matrices holding A and B (uploaded here when absent, and then freed)."""
     log(f"case {label} A{A.shape} B{B.shape}")
-    a, b = ctx.upload(A), ctx.upload(B)
+    own = a is None
+    if own:
+        a, b = ctx.upload(A), ctx.upload(B)
     m, k = A.shape
     n = B.shape[1]
     gch, och = G.PoseidonChannel(), O.Channel()
@@ -81,8 +85,9 @@ def _compare_layer(ctx, A, B, seed, label):
     assert rg["final_a_eval"] == ro["final_a_eval"] and rg["final_b_eval"] == ro["final_b_eval"]
     assert rg["next_point"] == ro["next_point"] and rg["next_value"] == ro["next_value"]
     assert gch.digest() == och.digest()
-    a.free()
-    b.free()
+    if own:
+        a.free()
+        b.free()
 
 
 def test_config1_uniform_256(gpu_ctx):
@@ -178,6 +183,27 @@ def test_int8_context_full_range_weights(int8_ctx, m, k, n):
     B = rng.integers(0, P, size=(k, n), dtype=np.uint32)
     B[0, 0] = 200  # out of int8 range even if the rest were small
     _compare_layer(int8_ctx, A, B, 7, "int8 ctx, full range")
+
+
+def test_wrapped_weight_changed_and_invalidated(gpu_ctx):
+    """A weight borrowed with gkr_matrix_wrap_device, proved once (which builds its int8 copy), then
+    written by the caller: the library keeps the copy it derived until gkr_matrix_invalidate, after
+    which the proof is the oracle's proof of the new entries."""
+    m, k, n = 8, 640, 512
+    A, B1, B2 = O.synthetic(m, k, 1, 31), O.synthetic(k, n, 1, 32), O.synthetic(k, n, 1, 33)
+    a, store = gpu_ctx.upload(A), gpu_ctx.upload(B1)
+    w = gpu_ctx.wrap_device(store.device_ptr, k, n)
+    _compare_layer(gpu_ctx, A, B1, 40, "wrapped weight", a, w)
+    # the caller writes new int8-range entries into the borrowed memory (B2 = I . B2)
+    ident, b2 = gpu_ctx.upload(np.eye(k, dtype=np.uint32)), gpu_ctx.upload(B2)
+    gpu_ctx.matmul_forward_into(ident, b2, store)
+    assert np.array_equal(w.download(), B2)
+    # as documented, the derived int8 copy still holds B1 until the caller invalidates it
+    _compare_layer(gpu_ctx, A, B1, 41, "wrapped weight, changed, not invalidated", a, w)
+    w.invalidate()
+    _compare_layer(gpu_ctx, A, B2, 42, "wrapped weight, invalidated", a, w)
+    _compare_layer(gpu_ctx, A, B2, 43, "wrapped weight, copy rebuilt", a, w)
+    assert G.lib().gkr_matrix_invalidate(None, w.handle) == 1  # GKR_ERR_INVALID
 
 
 def test_boundary_values(gpu_ctx):

@@ -2,7 +2,7 @@
 submitted closure runs once, in submission order, across ring wrap-around; the first
 error is kept and cleared once taken; the thread sleeps when idle and wakes on the next
 submission; destruction drains what is queued; a closure of almost a slot's size keeps
-its bytes.  Host work stands in for the HIP launches, so no GPU is needed."""
+its bytes; errors stay with the ring whose launch returned them.  Host work stands in for the HIP launches, so no GPU is needed."""
 import ctypes as C
 import os
 import subprocess
@@ -50,3 +50,8 @@ def test_destroy_drains(lt):
 
 def test_large_closure(lt):
     assert lt.lt_big_closure() == 0
+
+
+def test_errors_stay_with_their_ring(lt):
+    assert lt.lt_errors_per_ring() == 0
+
