@@ -15,9 +15,10 @@
  *   utils.rs:14-69          UnivariatePoly (leading zeros dropped), interpolate_lagrange
  *   backend/cpu/lookups/gkr.rs:17-288  gen_eq_evals, next_layer, the eval sums
  * The channel is the Poseidon252 channel (stwo core/channel/poseidon252.rs):
- * mix_felts packs pairs of QM31 and hashes [digest, packs...], draw_secure_felt
- * takes the low four 31-bit limbs of a draw, the same operations as
- * orc_mix_felts / orc_draw_qm31. */
+ * mix_felts packs pairs of QM31 and hashes [digest, packs...], also for an
+ * empty slice (a zero round polynomial has no coefficients left), and
+ * draw_secure_felt takes the low four 31-bit limbs of a draw: the operations
+ * of orc_mix_felts_stwo / orc_draw_qm31. */
 #include "oracle_internal.h"
 
 enum { L_GP = 0, L_GEN = 1, L_MULT = 2, L_SINGLE = 3 };
@@ -242,7 +243,7 @@ static qm draw(orc_channel* ch) {
 static void mix_q(orc_channel* ch, const qm* v, size_t n) {
   uint32_t* w = (uint32_t*)malloc((n ? n : 1) * 16);
   for (size_t i = 0; i < n; i++) q_store(w + 4 * i, v[i]);
-  orc_mix_felts(ch, w, n);
+  orc_mix_felts_stwo(ch, w, n);
   free(w);
 }
 /* random_linear_combination: v0 + a v1 + ... (Horner) */

@@ -45,6 +45,7 @@ void orc_mix_u64(orc_channel* ch, uint64_t v);
 void orc_mix_felt(orc_channel* ch, const uint32_t w[8]);
 void orc_mix_secure_field(orc_channel* ch, const uint32_t q[4]);
 void orc_mix_felts(orc_channel* ch, const uint32_t* q, size_t n);
+void orc_mix_felts_stwo(orc_channel* ch, const uint32_t* q, size_t n);
 void orc_mix_poly_coeffs(orc_channel* ch, const uint32_t c[12]);
 void orc_mix_poly_coeffs_deg3(orc_channel* ch, const uint32_t c[16]);
 void orc_draw_felt252(orc_channel* ch, uint32_t out[8]);
@@ -56,6 +57,7 @@ size_t orc_channel_size(void);
 
 /* ---------------------------------------------------------- MLE / matmul (matmul.c) */
 void orc_evaluate_mle(const uint32_t* evals, int n_vars, const uint32_t* point, uint32_t out[4]);
+void orc_inner_product_q(const uint32_t* fa, const uint32_t* fb, size_t n, uint32_t out[4]);
 void orc_restrict_mle(const uint32_t* evals, size_t len, const uint32_t* assign, int s, uint32_t* out);
 void orc_lagrange_basis(const uint32_t* c, int n, uint32_t* out);
 void orc_eq_evals(const uint32_t* r, int n, uint32_t* out);

@@ -365,6 +365,17 @@ void orc_mix_felts(orc_channel* ch, const uint32_t* q, size_t n) {
   ch_set(ch, fe_hash_many(in, m));
   free(in);
 }
+/* Poseidon252Channel::mix_felts (stwo core/channel/poseidon252.rs:70-84), the
+ * channel of STWO's LogUp-GKR batch: as orc_mix_felts, except that an empty
+ * slice still hashes [digest] (poseidon_hash_many of one felt) and resets n_draws. */
+void orc_mix_felts_stwo(orc_channel* ch, const uint32_t* q, size_t n) {
+  if (n) {
+    orc_mix_felts(ch, q, n);
+    return;
+  }
+  fe in[1] = {ch_digest(ch)};
+  ch_set(ch, fe_hash_many(in, 1));
+}
 /* draw_felt252: [digest, n_draws, 3] (poseidon_channel.rs:156-166) */
 static fe draw_fe(orc_channel* ch) {
   fe s[3] = {ch_digest(ch), fe_from_u64(ch->n_draws), fe_from_u64(3)};

@@ -450,7 +450,7 @@ int lk_build(gkr_ctx* c, std::vector<Inst>& I) {
       TimedLaunch tl(c, K_LOOKUP, bytes);
       GKR_LAUNCH(c, k_lk_tree, dim3(wg), dim3(kBlock), 0, dd, (uint32_t)d.size());
     }
-    TRY(check_launch());
+    TRY(check_launch(c));
     TRY(sync(c));  // the staging buffer is reused by the next stage
   }
   std::vector<LkTop> td(I.size());
@@ -477,7 +477,7 @@ int lk_build(gkr_ctx* c, std::vector<Inst>& I) {
   memcpy(h, td.data(), td.size() * sizeof(LkTop));
   HIP_TRY(hipMemcpyAsync(dt, h, td.size() * sizeof(LkTop), hipMemcpyHostToDevice, c->stream));
   GKR_LAUNCH(c, k_lk_top, dim3(grid_for(I.size())), dim3(kBlock), 0, dt, (uint32_t)I.size(), top);
-  TRY(check_launch());
+  TRY(check_launch(c));
   void* hr;
   TRY(ensure_host(c, H_LKRES, 6 * I.size() * sizeof(qm31), &hr));
   HIP_TRY(hipMemcpyAsync(hr, top, 6 * I.size() * sizeof(qm31), hipMemcpyDeviceToHost, c->stream));
@@ -562,7 +562,7 @@ extern "C" int gkr_prove_lookup_batch(gkr_ctx* c, gkr_channel* ch, const gkr_loo
     {
       HostTimer ht(c, K_HOST_FS);
       for (size_t i = 0; i < ni; i++)
-        if (I[i].active) C.mix_felts(I[i].claims, I[i].nclaims);
+        if (I[i].active) C.mix_felts_stwo(I[i].claims, I[i].nclaims);
     }
     const qm31 alpha = C.draw_qm31(), lambda = C.draw_qm31();
     // per active instance: layer variables lv, oracle variables k = lv - 1
@@ -646,9 +646,9 @@ extern "C" int gkr_prove_lookup_batch(gkr_ctx* c, gkr_channel* ch, const gkr_loo
             GKR_LAUNCH(c, k_lk_round, dim3(wg), dim3(kBlock), 0, dd, (uint32_t)d.size(), d_tab, d_y,
                                layer, part, res);
           }
-          TRY(check_launch());
+          TRY(check_launch(c));
           GKR_LAUNCH(c, k_lk_finish, dim3((unsigned)d.size()), dim3(kBlock), 0, dd, part, res);
-          TRY(check_launch());
+          TRY(check_launch(c));
           HIP_TRY(hipMemcpyAsync(hr, res, (size_t)kLkRes * d.size() * sizeof(qm31), hipMemcpyDeviceToHost,
                                  c->stream));
         }
@@ -694,7 +694,7 @@ extern "C" int gkr_prove_lookup_batch(gkr_ctx* c, gkr_channel* ch, const gkr_loo
       qm31 xr;
       {
         HostTimer ht(c, K_HOST_FS);
-        C.mix_felts(comb.c, comb.len);
+        C.mix_felts_stwo(comb.c, comb.len);
         xr = C.draw_qm31();
       }
       for (int q = 0; q < 4; q++) out->round_polys[4 * round + q] = G(q < comb.len ? comb.c[q] : qm31_zero());
@@ -732,7 +732,7 @@ extern "C" int gkr_prove_lookup_batch(gkr_ctx* c, gkr_channel* ch, const gkr_loo
           m[3] = d1;
         }
         const int nq = x.gp() ? 2 : 4;
-        C.mix_felts(m, nq);
+        C.mix_felts_stwo(m, nq);
         for (int q = 0; q < 4; q++)
           out->masks[4 * ((size_t)layer * ni + i) + q] = G(q < nq ? m[q] : qm31_zero());
       }
@@ -801,7 +801,7 @@ extern "C" int gkr_verify_lookup_batch(const uint32_t* gates, const uint32_t* n_
         }
       }
     for (size_t i = 0; i < ni; i++)
-      if (ncl[i]) C.mix_felts(&claims[2 * i], ncl[i]);
+      if (ncl[i]) C.mix_felts_stwo(&claims[2 * i], ncl[i]);
     const qm31 alpha = C.draw_qm31(), lambda = C.draw_qm31();
     std::vector<qm31> cl;
     for (size_t i = 0; i < ni; i++)
@@ -822,7 +822,7 @@ extern "C" int gkr_verify_lookup_batch(const uint32_t* gates, const uint32_t* n_
       }
       if (!qm31_eq(qm31_add(q.eval(qm31_zero()), q.eval(qm31_one())), sum))
         return fail(GKR_ERR_VERIFY, "layer %d round %d: p(0) + p(1) differs from the claim", layer, r);
-      C.mix_felts(q.c, q.len);
+      C.mix_felts_stwo(q.c, q.len);
       pt[r] = C.draw_qm31();
       sum = q.eval(pt[r]);
     }
@@ -855,7 +855,7 @@ extern "C" int gkr_verify_lookup_batch(const uint32_t* gates, const uint32_t* n_
         qm31 v[4];
         const int nv = gates[i] ? 4 : 2;
         for (int k = 0; k < nv; k++) v[k] = Q(m[k]);
-        C.mix_felts(v, nv);
+        C.mix_felts_stwo(v, nv);
       }
     const qm31 c = C.draw_qm31();
     ood = pt;

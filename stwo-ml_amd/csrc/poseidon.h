@@ -311,6 +311,17 @@ class PoseidonChannel {
     n_draws = 0;
     hash_count++;
   }
+  // Poseidon252Channel::mix_felts (stwo core/channel/poseidon252.rs:70-84),
+  // the channel of STWO's LogUp-GKR batch: the same packing as mix_felts, but
+  // an empty slice still hashes [digest] and resets n_draws.
+  void mix_felts_stwo(const qm31* q, int n) {
+    if (n > 0) return mix_felts(q, n);
+    digest = poseidon_hash_many(&digest, 1);
+    n_draws = 0;
+    hash_count++;
+  }
+  // PoseidonChannel::mix_felts (poseidon_channel.rs:261-297): an empty slice
+  // leaves the channel unchanged.
   void mix_felts(const qm31* q, int n) {
     if (n <= 0) return;
     felt* in = new felt[1 + (n + 1) / 2];

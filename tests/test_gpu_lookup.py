@@ -64,6 +64,18 @@ def _check(ctx, inst, seed):
     return got
 
 
+def test_lookup_zero_grand_product(gpu_ctx):
+    """A grand product over an all-zero column beside a LogUp instance: every round polynomial of
+    the grand product is zero, so the batch polynomial of the layers before the smaller LogUp
+    instance joins is mixed as an empty slice, which STWO's Poseidon252 channel still hashes."""
+    log("case lookup zero grand product")
+    rng = np.random.default_rng(77)
+    inst = [(0, None, np.zeros((1 << 6, 4), dtype=np.uint32))]
+    _check(gpu_ctx, inst, 77)
+    inst = _make(rng, [(1, 3)]) + inst
+    _check(gpu_ctx, inst, 78)
+
+
 SPECS = [[(0, 1)], [(1, 1)], [(3, 1)], [(2, 2)], [(0, 5)], [(1, 5)], [(2, 5)], [(3, 5)],
          [(1, 5), (2, 3), (3, 4), (0, 2)], [(2, 12)], [(3, 13), (0, 13)], [(1, 14), (2, 9), (3, 1)],
          [(2, 16)] * 6 + [(3, 16), (0, 10)]]

@@ -8,7 +8,8 @@ stwo-gpu/crates/stwo/src/prover/lookups/gkr_prover.rs:396-500) pinned on the CPU
 * every round polynomial of a one-instance proof against brute-force sums over the hypercube of
   eq((r, t, x), y) (num + lambda den)(r, t, x) at t = 0..3, from the input layer's MLE with the
   transcript replayed in Python (mix claims, draw alpha then lambda, mix the coefficients with the
-  leading zeros dropped, masks, the layer challenge);
+  leading zeros dropped, masks, the layer challenge), including a zero round polynomial mixed as
+  an empty slice (an all-zero grand-product column);
 * the restated partially_verify_batch accepts and ends on the prover's transcript; changed round
   polynomials, masks, output claims and gates are rejected.
 No reference-held vector covers this protocol (its tests run on the Blake2s channel and assert the
@@ -107,15 +108,34 @@ def _fold_point(vals, nv, pt_prefix, t, rest_bits, last):
     return Q.mle_bruteforce(vals, pt)
 
 
-@pytest.mark.parametrize("kind", [O.LOOKUP_GRAND_PRODUCT, O.LOOKUP_LOGUP_GENERIC, O.LOOKUP_LOGUP_SINGLES,
-                                  O.LOOKUP_LOGUP_MULTIPLICITIES])
-def test_lookup_round_polys_brute_force(kind):
+def stwo_mix(ch, qs):
+    """Poseidon252Channel::mix_felts (stwo core/channel/poseidon252.rs:70-84) on a replay channel:
+    digest = poseidon_hash_many([digest, packed pairs...]) with n_draws reset.  An empty slice
+    still hashes [digest], unlike PoseidonChannel::mix_felts (poseidon_channel.rs:261-264), which
+    returns at once; the empty case is spelled out here from hash_many."""
+    if qs:
+        ch.mix_felts(qs)
+        return
+    st = O.channel_state(ch)
+    d = O.hash_many([ch.digest()])
+    hc = (st[9] | (st[10] << 32)) + 1
+    O.set_channel_state(ch, [(d >> (32 * i)) & 0xFFFFFFFF for i in range(8)] + [0, hc & 0xFFFFFFFF, hc >> 32])
+
+
+@pytest.mark.parametrize("kind,zero", [(O.LOOKUP_GRAND_PRODUCT, False), (O.LOOKUP_LOGUP_GENERIC, False),
+                                       (O.LOOKUP_LOGUP_SINGLES, False), (O.LOOKUP_LOGUP_MULTIPLICITIES, False),
+                                       (O.LOOKUP_GRAND_PRODUCT, True)])
+def test_lookup_round_polys_brute_force(kind, zero):
     """One instance of 4 variables: replay the transcript in Python and check every round polynomial
     at t = 0..3 against sum_x eq((c, t, x), y) * (num(c,t,x) + lambda den(c,t,x)) where num/den are
-    the fraction sum (or product) of the layer below at (c, t, x, 0) and (c, t, x, 1)."""
+    the fraction sum (or product) of the layer below at (c, t, x, 0) and (c, t, x, 1).  zero: a
+    grand product over an all-zero column, so every round polynomial is zero and is mixed as an
+    empty slice (the transcript then depends on the empty-slice rule of the STWO channel)."""
     nv = 4
     rng = np.random.default_rng(40 + kind)
     inst = make(rng, [(kind, nv)])
+    if zero:
+        inst = [(kind, None, np.zeros_like(inst[0][2]))]
     ch = O.Channel()
     rep = ch.clone()
     d = O.prove_lookup_batch(ch, inst)
@@ -163,7 +183,8 @@ def test_lookup_round_polys_brute_force(kind):
                     val = Q.qadd(Q.qmul(val, qv(t)), c)
                 assert val == acc, (layer, r, t)
             assert not poly or poly[-1] != ZERO  # leading zeros dropped
-            rep.mix_felts(poly)
+            assert not zero or poly == []
+            stwo_mix(rep, poly)
             chal.append(rep.draw_qm31())
         mask = d["masks"][layer][0]
         rep.mix_felts(mask)
@@ -172,6 +193,10 @@ def test_lookup_round_polys_brute_force(kind):
         claims = [Q.qadd(mask[2 * k], Q.qmul(c, Q.qsub(mask[2 * k + 1], mask[2 * k]))) for k in range(len(mask) // 2)]
     assert ood == d["ood_point"] and claims == d["claims_to_verify"][0]
     assert rep.digest() == ch.digest()
+    if zero:  # the restated verifier takes the same transcript
+        vch = O.Channel()
+        st, vood, _ = O.verify_lookup_batch(d, vch)
+        assert st == 0 and vood == d["ood_point"] and vch.digest() == ch.digest()
 
 
 def test_lookup_verifier_rejects():
