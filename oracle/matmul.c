@@ -33,6 +33,23 @@ void orc_evaluate_mle(const uint32_t* evals, int n_vars, const uint32_t* point, 
   q_store(out, mle_evaluate((const qm*)evals, n_vars, (const qm*)point));
 }
 
+/* sum_i fa[i] * fb[i]: the claim the product round loop starts from
+ * (backend.rs:146-157 at round 0: s0 + s1 = the sum over the whole hypercube) */
+void orc_inner_product_q(const uint32_t* fa, const uint32_t* fb, size_t n, uint32_t out[4]) {
+  const qm* a = (const qm*)fa;
+  const qm* b = (const qm*)fb;
+  qm total = q_zero();
+#pragma omp parallel
+  {
+    qm part = q_zero();
+#pragma omp for schedule(static)
+    for (size_t i = 0; i < n; i++) part = q_add(part, q_mul(a[i], b[i]));
+#pragma omp critical
+    total = q_add(total, part);
+  }
+  q_store(out, total);
+}
+
 /* restrict_mle (matmul.rs:144-169): fold the first s variables; parallel when mid >= 8192 */
 static qm* restrict_mle(const qm* evals, size_t len, const qm* assign, int s) {
   qm* cur = (qm*)malloc(len * sizeof(qm));

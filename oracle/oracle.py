@@ -206,6 +206,16 @@ def evaluate_mle(evals: Sequence, point: Sequence):
     return _q(out)
 
 
+def inner_product_q(fa: np.ndarray, fb: np.ndarray):
+    """sum_i fa[i] * fb[i] over two QM31 vectors ((n, 4) arrays)."""
+    a = np.ascontiguousarray(fa, dtype=np.uint32).reshape(-1, 4)
+    b = np.ascontiguousarray(fb, dtype=np.uint32).reshape(-1, 4)
+    assert a.shape == b.shape
+    out = np.zeros(4, dtype=np.uint32)
+    lib().orc_inner_product_q(_p(a), _p(b), C.c_size_t(a.shape[0]), _p(out))
+    return _q(out)
+
+
 def restrict_mle(evals: Sequence, assign: Sequence):
     e = _qa(evals)
     out = np.zeros((len(evals) >> len(assign), 4), dtype=np.uint32)

@@ -83,8 +83,10 @@ def test_config3_smollm_30_layers_matches_oracle(gpu_ctx):
 
 def test_config2_product_sumcheck_2_28_chain(gpu_ctx):
     """Config 2 at its largest size: f_a, f_b of 2^28 QM31 each (4 GiB per vector).  The verifier's
-    chain p_t(0) + p_t(1) = p_{t-1}(r_{t-1}) with the transcript replayed on the CPU, ending at
-    final_a * final_b; final_a equals the oracle's MLE of the downloaded f_a at the challenges."""
+    chain with the transcript replayed on the CPU: p_0(0) + p_0(1) = sum_x f_a(x) f_b(x) (the
+    oracle's sum over the downloaded vectors), p_t(0) + p_t(1) = p_{t-1}(r_{t-1}), ending at
+    final_a * final_b; final_a and final_b equal the oracle's MLEs of the downloaded f_a and f_b at
+    the challenges."""
     n = 1 << 28
     log("case config2 2^28 chain")
     fa, fb = gpu_ctx.qvec_synthetic(n, 28), gpu_ctx.qvec_synthetic(n, 29)
@@ -94,19 +96,21 @@ def test_config2_product_sumcheck_2_28_chain(gpu_ctx):
     rep.mix_u64(28)
     got = gpu_ctx.sumcheck_product(fa, fb, gch)
     assert len(got["round_polys"]) == 28
-    cur = None
+    ha, hb = fa.download(), fb.download()
+    del fa, fb
+    t0 = time.time()
+    cur = O.inner_product_q(ha, hb)
+    log(f"  oracle sum {time.time() - t0:.1f} s")
     for (c0, c1, c2), r in zip(got["round_polys"], got["challenges"]):
-        if cur is not None:
-            assert Q.qadd(c0, Q.qadd(Q.qadd(c0, c1), c2)) == cur
+        assert Q.qadd(c0, Q.qadd(Q.qadd(c0, c1), c2)) == cur
         rep.mix_poly_coeffs(c0, c1, c2)
         assert rep.draw_qm31() == r
         cur = Q.qadd(Q.qadd(c0, Q.qmul(c1, r)), Q.qmul(c2, Q.qmul(r, r)))
     assert cur == Q.qmul(got["final_a_eval"], got["final_b_eval"])
     assert rep.digest() == gch.digest()
-    del fb
-    ha = fa.download()
-    del fa
     assert tuple(O.evaluate_mle(ha, got["challenges"])) == got["final_a_eval"]
+    assert tuple(O.evaluate_mle(hb, got["challenges"])) == got["final_b_eval"]
+    log(f"  oracle sum and MLEs {time.time() - t0:.1f} s")
 
 
 def test_softmax_reference_table_qwen_scores(gpu_ctx):

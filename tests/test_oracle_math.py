@@ -306,6 +306,7 @@ def test_sumcheck_product_identities(n):
     cur = (0, 0, 0, 0)
     for x, y in zip(A, B):
         cur = Q.qadd(cur, Q.qmul(x, y))
+    assert O.inner_product_q(fa, fb) == cur  # the parallel sum the 2^28 GPU test starts from
     for (c0, c1, c2), r in zip(res["round_polys"], res["challenges"]):
         assert Q.qadd(c0, Q.qadd(Q.qadd(c0, c1), c2)) == cur
         rep.mix_poly_coeffs(c0, c1, c2)
