@@ -13,6 +13,11 @@ ported to this build's verifier (the C ABI's host replay), the oracle's verifier
   table side; the reference's Rust verifier (verifier.rs:3058-3290) and this build's do, so the
   port takes all-zero multiplicities (table-side sum 0 = the claimed sum) and the matching
   all-zero multiplicity sumcheck; everything the Cairo case's acceptance depends on is kept.
+* The LogUp tail (multiplicity sumcheck and final mixes), which no reference vector covers: the
+  Cairo verifier's statement of it (layer_verifiers.cairo:53-95, :282-344, :431-485, parsed per
+  model_verifier.cairo:158-215, :298-372) spelled out in Python and run over the oracle's
+  serialized proof of a layer with a 4-entry table (two multiplicity rounds): accepted, ending on
+  the prover's channel state; a changed c1 rejected; the final mixes' order pinned.
 * Activation tables: engine/src/gadgets/lookup_table.rs:466-633 (GELU against its f64 formula
   at 200 points, known values, limits, monotonicity; SiLU(0) and SiLU(1.0))."""
 import math
@@ -202,3 +207,160 @@ def test_silu_cases():
     expected = round(1.0 / (1.0 + math.exp(-1.0)) * 65536.0)
     assert abs(int(silu[65536]) - expected) <= 1
     assert O.activation(5, 65536) == int(silu[65536])
+
+
+# ------------------------------------------------------------------ the LogUp tail, Cairo statement
+class _Reader:
+    """ProofReader over serialized felts (model_verifier.cairo: read_u32 / read_u64 / read_qm31 /
+    read_felt); a QM31 is four felts (a, b, c, d)."""
+
+    def __init__(self, felts, pos=0):
+        self.f, self.pos = felts, pos
+
+    def u(self):
+        v = int(self.f[self.pos])
+        self.pos += 1
+        return v
+
+    def q(self):
+        return tuple(self.u() for _ in range(4))
+
+
+def _eq_eval(r, s):
+    """eq(r, s) = prod_i (r_i s_i + (1 - r_i)(1 - s_i))."""
+    e = ONE
+    for a, b in zip(r, s):
+        e = Q.qmul(e, Q.qadd(Q.qmul(a, b), Q.qmul(Q.qsub(ONE, a), Q.qsub(ONE, b))))
+    return e
+
+
+def _poly3(c, x):
+    return Q.qadd(c[0], Q.qmul(x, Q.qadd(c[1], Q.qmul(x, Q.qadd(c[2], Q.qmul(x, c[3]))))))
+
+
+def cairo_dispatch_activation(felts, claim_point, ch, swap_final_mix=False):
+    """The Cairo verifier's statement of a tag-3 layer, spelled out step by step:
+    dispatch_activation's parse (elo-cairo-verifier/src/model_verifier.cairo:298-372, with
+    read_optional_logup :158-185 and read_optional_multiplicity_sumcheck :191-215), then
+    verify_activation_layer (layer_verifiers.cairo:431-485): mix 0x4C4F47 and the type tag, draw
+    gamma and beta, verify_logup_eq_sumcheck (:282-344: mix the claimed sum, degree-3 rounds from
+    sum 1 with c1 rebuilt, final eq * w * (gamma - in - beta out)), verify_multiplicity_sumcheck
+    (:53-95: per round p(0) + p(1) = sum, mix c0, mix c1, draw, sum = c0 + c1 r; final == sum),
+    then mix input_eval and output_eval.  Raises AssertionError with the Cairo panic message.
+    swap_final_mix mixes output_eval before input_eval (a transcript the reference does not use).
+    Returns (next claim value, felts read)."""
+    rd = _Reader(felts)
+    assert rd.u() == 3, "tag"
+    act_type = rd.u()
+    input_eval, output_eval = rd.q(), rd.q()
+    rd.u()  # table commitment (checked outside the walk)
+    assert rd.u() == 1, "has_logup"
+    claimed = rd.q()
+    polys = [(rd.q(), rd.q(), rd.q()) for _ in range(rd.u())]  # (c0, c2, c3)
+    w_e, in_e, out_e = rd.q(), rd.q(), rd.q()
+    for _ in range(rd.u()):
+        rd.u()  # multiplicities: consumed, not used
+    ms_has = rd.u() == 1
+    ms = [(rd.q(), rd.q()) for _ in range(rd.u())] if ms_has else []
+    ms_final, ms_claimed = (rd.q(), rd.q()) if ms_has else (ZERO, ZERO)
+    assert rd.u() == 0, "has_act_proof"
+    assert rd.u() == 0, "has_piecewise"
+    ch.mix_u64(0x4C4F47)
+    ch.mix_u64(act_type)
+    gamma = ch.draw_qm31()
+    beta = ch.draw_qm31()
+    ch.mix_secure_field(claimed)
+    cur, chal = ONE, []
+    for c0, c2, c3 in polys:
+        c1 = Q.qsub(Q.qsub(Q.qsub(cur, Q.qadd(c0, c0)), c2), c3)
+        ch.mix_poly_coeffs_deg3(c0, c1, c2, c3)
+        s = ch.draw_qm31()
+        chal.append(s)
+        cur = _poly3((c0, c1, c2, c3), s)
+    d_e = Q.qsub(Q.qsub(gamma, in_e), Q.qmul(beta, out_e))
+    assert cur == Q.qmul(_eq_eval(claim_point[:len(polys)], chal), Q.qmul(w_e, d_e)), "LOGUP_FINAL_MISMATCH"
+    if ms_has:
+        cur = ms_claimed
+        for c0, c1 in ms:
+            assert Q.qadd(c0, Q.qadd(c0, c1)) == cur, "MULT_SUMCHECK_ROUND_FAIL"
+            ch.mix_secure_field(c0)
+            ch.mix_secure_field(c1)
+            r = ch.draw_qm31()
+            cur = Q.qadd(c0, Q.qmul(c1, r))
+        assert cur == ms_final, "MULT_SUMCHECK_FINAL_EVAL_MISMATCH"
+    first, second = (output_eval, input_eval) if swap_final_mix else (input_eval, output_eval)
+    ch.mix_secure_field(first)
+    ch.mix_secure_field(second)
+    return input_eval, rd.pos
+
+
+def _activation_tail_case(tag=5, table_log=2, rows=2, cols=4, seed=61):
+    """A small activation layer whose multiplicity sumcheck has table_log rounds: the oracle's
+    reduce_activation_layer over a rows x cols input with a 2^table_log table, the claim value
+    the output MLE at a drawn point.  Returns (point, value, start channel, proof, end channel)."""
+    X = O.synthetic(rows, cols, 0, seed)
+    out = [[O.activation(tag, int(x) & ((1 << table_log) - 1)) for x in row] for row in X]
+    ch = O.Channel()
+    ch.mix_u64(seed)
+    nv = (rows - 1).bit_length() + (cols - 1).bit_length()
+    pt = ch.draw_qm31s(nv)
+    val = Q.mle_bruteforce([_q(v) for row in out for v in row], pt)
+    start = ch.clone()
+    proof = O.prove_activation_layer(pt, val, X, tag, ch, table_log)
+    return pt, val, start, proof, ch
+
+
+def test_logup_tail_cairo_statement_accepts_oracle_proof():
+    """The reference's second statement of the LogUp tail (the Cairo verifier: multiplicity
+    sumcheck after the eq-sumcheck, c0 and c1 mixed per round, then input_eval and output_eval
+    mixed) replayed over the oracle's serialized proof: accepted, ending on the prover's channel
+    state; two multiplicity rounds (a 4-entry table) with nonzero multiplicities.  The product's
+    walk verifier accepts the same calldata and ends on the same state."""
+    pt, val, start, proof, end = _activation_tail_case()
+    assert len(proof["mult_round_polys"]) == 2 and int(np.count_nonzero(proof["multiplicities"])) >= 2
+    assert proof["output_eval"] == val
+    cd = []
+    O.serialize_activation_layer(cd, 5, proof)
+    ch = start.clone()
+    nxt, used = cairo_dispatch_activation(cd, pt, ch)
+    assert used == len(cd) and nxt == proof["input_eval"]
+    assert ch.digest() == end.digest()
+    # the same layer as walk calldata, through the product's verifier
+    full = [1] + cd
+    O.serialize_tail(full, pt, proof["input_eval"], [], 0)
+    gch = G.PoseidonChannel()
+    gch.import_state(O.channel_state(start))
+    p2, v2, _ = G.verify_walk(full, [(G.STEP_ACTIVATION, 2, 4, 0, 5, 2)], pt, val, gch)
+    assert (p2, v2) == (pt, proof["input_eval"]) and gch.digest() == end.digest()
+
+
+def test_logup_tail_cairo_statement_rejections():
+    """A changed c1 of a multiplicity round is rejected by the Cairo statement
+    (MULT_SUMCHECK_ROUND_FAIL), by the product's verifier and by the oracle's; a prover that mixed
+    output_eval before input_eval ends on another channel state than the Cairo statement's, so the
+    final-mix order is pinned (the two evaluations differ here)."""
+    pt, val, start, proof, end = _activation_tail_case()
+    assert proof["input_eval"] != proof["output_eval"]
+    bad = dict(proof)
+    c0, c1 = proof["mult_round_polys"][1]
+    bad["mult_round_polys"] = [proof["mult_round_polys"][0], (c0, Q.qadd(c1, ONE))]
+    cd = []
+    O.serialize_activation_layer(cd, 5, bad)
+    with pytest.raises(AssertionError, match="MULT_SUMCHECK_ROUND_FAIL"):
+        cairo_dispatch_activation(cd, pt, start.clone())
+    full = [1] + cd
+    O.serialize_tail(full, pt, proof["input_eval"], [], 0)
+    gch = G.PoseidonChannel()
+    gch.import_state(O.channel_state(start))
+    with pytest.raises(G.GkrError) as e:
+        G.verify_walk(full, [(G.STEP_ACTIVATION, 2, 4, 0, 5, 2)], pt, val, gch)
+    assert e.value.code == 6
+    assert O.verify_activation_layer(pt, val, 5, 2, bad, start.clone()) != 0
+    good = []
+    O.serialize_activation_layer(good, 5, proof)
+    swapped = start.clone()
+    cairo_dispatch_activation(good, pt, swapped, swap_final_mix=True)
+    assert swapped.digest() != end.digest()
+    straight = start.clone()
+    cairo_dispatch_activation(good, pt, straight)
+    assert straight.digest() == end.digest()
