@@ -975,47 +975,53 @@ struct RowsJob {
   qm31* out;
 };
 // Activation side within the fused restriction: a workgroup takes 64
-// consecutive columns; wave w adds the rows i = w, w + kColWaves, ... (each
-// row read is 64 consecutive words), and the waves' sums meet in LDS.
-__device__ __forceinline__ void restrict_rows_block(const RowsJob& act, uint64_t col0, qm31 (*part)[64]) {
-  constexpr int kAhead = 8;  // rows of A a wave has in flight
+// consecutive columns and the rows in passes of 64: wave w loads rows
+// i0 + w, i0 + w + kColWaves, ... (16 per pass, each a 64-word coalesced
+// read) all at once, while the pass's 64 Lagrange weights are staged in LDS
+// by one coalesced load; the waves' sums meet in LDS.  One memory round trip
+// per pass: this side is latency-bound (it sets the time of the narrow
+// shapes), so every load of a pass is in flight together.
+struct RowsLds {
+  qm31 part[kColWaves][64];
+  qm31 l[64];
+};
+__device__ __forceinline__ void restrict_rows_block(const RowsJob& act, uint64_t col0, RowsLds& sh) {
+  constexpr int kRows = 16;  // rows per wave and pass
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t j = col0 + lane;
   uint64_t lo[4] = {0, 0, 0, 0}, hi[4] = {0, 0, 0, 0};
-  if (j < act.k) {
-    for (uint64_t i0 = wave; i0 < act.m; i0 += (uint64_t)kAhead * kColWaves) {
-      uint32_t v[kAhead];
+  for (uint64_t i0 = 0; i0 < act.m; i0 += (uint64_t)kRows * kColWaves) {  // same count in every wave
+    uint32_t v[kRows];
 #pragma unroll
-      for (int u = 0; u < kAhead; u++) {
-        const uint64_t iu = i0 + (uint64_t)u * kColWaves;
-        v[u] = iu < act.m ? act.A[iu * act.k + j] : 0u;
-      }
-#pragma unroll
-      for (int g = 0; g < kAhead / 4; g++) {
-        uint64_t t[4] = {0, 0, 0, 0};  // up to 4 rows: 4 * (P-1)^2 < 2^64
-#pragma unroll
-        for (int u = 4 * g; u < 4 * g + 4; u++) {
-          const uint64_t iu = i0 + (uint64_t)u * kColWaves;
-          if (iu < act.m) {
-            const qm31 l = ld_q(act.L, iu);
-            t[0] += (uint64_t)v[u] * l.a; t[1] += (uint64_t)v[u] * l.b;
-            t[2] += (uint64_t)v[u] * l.c; t[3] += (uint64_t)v[u] * l.d;
-          }
-        }
-#pragma unroll
-        for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
-      }
+    for (int u = 0; u < kRows; u++) {
+      const uint64_t iu = i0 + wave + (uint64_t)u * kColWaves;
+      v[u] = (j < act.k && iu < act.m) ? act.A[iu * act.k + j] : 0u;
     }
+    if (threadIdx.x < 64) sh.l[threadIdx.x] = i0 + threadIdx.x < act.m ? ld_q(act.L, i0 + threadIdx.x) : qm31_zero();
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kRows / 4; g++) {
+      uint64_t t[4] = {0, 0, 0, 0};  // 4 rows: 4 * (P-1)^2 < 2^64
+#pragma unroll
+      for (int u = 4 * g; u < 4 * g + 4; u++) {
+        const qm31 l = sh.l[wave + u * kColWaves];  // zero beyond m
+        t[0] += (uint64_t)v[u] * l.a; t[1] += (uint64_t)v[u] * l.b;
+        t[2] += (uint64_t)v[u] * l.c; t[3] += (uint64_t)v[u] * l.d;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) { lo[c] += (uint32_t)t[c]; hi[c] += t[c] >> 32; }
+    }
+    __syncthreads();  // the next pass stages its own weights
   }
   uint32_t r[4];
 #pragma unroll
   for (int c = 0; c < 4; c++) r[c] = m31_add(m31_reduce64(lo[c]), m31_mul(m31_reduce64(hi[c]), 2u));
-  part[wave][lane] = qm31{r[0], r[1], r[2], r[3]};
+  sh.part[wave][lane] = qm31{r[0], r[1], r[2], r[3]};
   __syncthreads();
   if (wave == 0 && j < act.pk) {
-    qm31 sum = part[0][lane];
+    qm31 sum = sh.part[0][lane];
 #pragma unroll
-    for (int w = 1; w < kColWaves; w++) sum = qm31_add(sum, part[w][lane]);
+    for (int w = 1; w < kColWaves; w++) sum = qm31_add(sum, sh.part[w][lane]);
     st_q(act.out, j, sum);  // columns k <= j < pk: zero padding (no rows added)
   }
 }
@@ -1025,9 +1031,12 @@ static __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t*
                                                           uint64_t chunk, const qm31* __restrict__ L,
                                                           uint32_t* __restrict__ partial, RowsJob act,
                                                           uint32_t act_blocks, uint32_t row_blocks) {
-  __shared__ uint32_t sh[kColWaves][64][17];  // epilogue transpose, one region per wave
+  __shared__ union {
+    uint32_t t[kColWaves][64][17];  // epilogue transpose, one region per wave
+    RowsLds act;
+  } sh;
   if (blockIdx.x < act_blocks) {
-    restrict_rows_block(act, (uint64_t)blockIdx.x * 64, reinterpret_cast<qm31(*)[64]>(&sh[0][0][0]));
+    restrict_rows_block(act, (uint64_t)blockIdx.x * 64, sh.act);
     return;
   }
   const uint32_t wb = blockIdx.x - act_blocks;
@@ -1083,13 +1092,13 @@ static __global__ void __launch_bounds__(kBlock) k_restrict_cols(const uint32_t*
 #pragma unroll
   for (int r = 0; r < kColRows; r++)
 #pragma unroll
-    for (int c = 0; c < 4; c++) sh[wave][lane][4 * r + c] = m31_reduce64(lo[r][c] + (hi[r][c] << 1));
+    for (int c = 0; c < 4; c++) sh.t[wave][lane][4 * r + c] = m31_reduce64(lo[r][c] + (hi[r][c] << 1));
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   const int vi = lane & 15, g = lane >> 4;
   uint64_t acc = 0;
 #pragma unroll
-  for (int i = 0; i < 16; i++) acc += sh[wave][g * 16 + i][vi];
+  for (int i = 0; i < 16; i++) acc += sh.t[wave][g * 16 + i][vi];
   uint32_t w = m31_reduce64(acc);
   w = m31_add(w, shfl_xor_u32(w, 16));
   w = m31_add(w, shfl_xor_u32(w, 32));
@@ -1151,70 +1160,86 @@ static __global__ void __launch_bounds__(kBlock) k_to_int8(const uint32_t* __res
 }
 
 // Weight side of the fused restriction over the int8 copy.  The grid is the
-// activation side's act_blocks workgroups, then row_tiles x chunks
-// workgroups.  A workgroup takes one row tile (16 rows) and `chunk` column
-// steps of it; wave w takes steps w, w + 4, ... of the chunk, with the
-// weight and digit loads of kR8Ahead steps in flight (one 16-byte load each
-// per lane and step) and one MFMA per step.  The four waves' 16 x 16 sums
-// are added in LDS; wave 0 recombines each row's digit sums
-// (sum_q 256^q acc_q, reduced once) and writes the 64 (row, component)
-// values as the chunk's partial rows.
+// activation side's act_blocks workgroups, then row_groups x chunks
+// workgroups.  A workgroup takes a group of kR8Rows row tiles (64 rows) and
+// `chunk` column steps; wave w takes steps w, w + 4, ... of the chunk.  Per
+// step a wave loads the digit block once and the kR8Rows weight tiles of the
+// group (one 16-byte load each per lane), and issues kR8Rows MFMAs: the
+// digit load is shared by four tiles.  The loads of kR8Ahead steps are in
+// flight.  The four waves' 16 x 16 sums per tile are added in LDS; wave w
+// recombines tile w's digit sums (sum_q 256^q acc_q, reduced once) and writes
+// its 64 (row, component) values as the chunk's partial rows.
 #ifndef GKR_R8_AHEAD
-#define GKR_R8_AHEAD 8
+#define GKR_R8_AHEAD 4
 #endif
 constexpr int kR8Ahead = GKR_R8_AHEAD;
+constexpr int kR8Rows = 4;  // row tiles per workgroup (== kColWaves: wave w finishes tile w)
+static_assert(kR8Rows <= kColWaves, "one finishing wave per row tile");
 typedef int v4i32 __attribute__((ext_vector_type(4)));
 static __global__ void __launch_bounds__(kBlock) k_restrict_cols8(const u32x4* __restrict__ W8, uint64_t k,
                                                            uint64_t nst, const u32x4* __restrict__ ldig,
                                                            uint32_t chunk, uint32_t* __restrict__ partial,
-                                                           RowsJob act, uint32_t act_blocks, uint32_t row_tiles) {
+                                                           RowsJob act, uint32_t act_blocks, uint32_t row_groups) {
   __shared__ union {
-    v4i32 acc[kColWaves][64];
-    qm31 part[kColWaves][64];  // activation side
+    v4i32 acc[kR8Rows][kColWaves][64];
+    RowsLds act;  // activation side
   } lds;
   if (blockIdx.x < act_blocks) {
-    restrict_rows_block(act, (uint64_t)blockIdx.x * 64, lds.part);
+    restrict_rows_block(act, (uint64_t)blockIdx.x * 64, lds.act);
     return;
   }
+  const uint64_t nrt = (k + kR8TileRows - 1) / kR8TileRows;
   const uint32_t wb = blockIdx.x - act_blocks;
-  const uint32_t rt = wb % row_tiles, chunk_id = wb / row_tiles;
+  const uint32_t rg = wb % row_groups, chunk_id = wb / row_groups;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint64_t s0 = (uint64_t)chunk_id * chunk + wave;
   const uint64_t s_end = ((uint64_t)chunk_id + 1) * chunk < nst ? ((uint64_t)chunk_id + 1) * chunk : nst;
   const int ns = s0 < s_end ? (int)((s_end - s0 + kColWaves - 1) / kColWaves) : 0;  // this wave's steps
-  const u32x4* wt = W8 + (uint64_t)rt * nst * 64 + lane;  // step s: wt[64 s]
-  const u32x4* dg = ldig + lane;                          // step s: dg[64 s]
-  v4i32 acc = {0, 0, 0, 0};
-  u32x4 wv[kR8Ahead], dv[kR8Ahead];
+  const uint64_t rt0 = (uint64_t)rg * kR8Rows;
+  const u32x4* wt[kR8Rows];  // step s of tile r: wt[r][64 s]; a group's missing tiles re-read the last one
+#pragma unroll
+  for (int r = 0; r < kR8Rows; r++) wt[r] = W8 + (rt0 + r < nrt ? rt0 + r : nrt - 1) * nst * 64 + lane;
+  const u32x4* dg = ldig + lane;  // step s: dg[64 s]
+  v4i32 acc[kR8Rows];
+#pragma unroll
+  for (int r = 0; r < kR8Rows; r++) acc[r] = v4i32{0, 0, 0, 0};
+  u32x4 wv[kR8Ahead][kR8Rows], dv[kR8Ahead];
 #pragma unroll
   for (int u = 0; u < kR8Ahead; u++)
     if (u < ns) {
       const uint64_t s = s0 + (uint64_t)kColWaves * u;
-      wv[u] = __builtin_nontemporal_load(wt + 64 * s);
+#pragma unroll
+      for (int r = 0; r < kR8Rows; r++) wv[u][r] = __builtin_nontemporal_load(wt[r] + 64 * s);
       dv[u] = dg[64 * s];
     }
   for (int i = 0; i < ns; i += kR8Ahead) {
 #pragma unroll
     for (int u = 0; u < kR8Ahead; u++) {
       if (i + u < ns) {
-        const v4i32 a = {(int)wv[u][0], (int)wv[u][1], (int)wv[u][2], (int)wv[u][3]};
         const v4i32 b = {(int)dv[u][0], (int)dv[u][1], (int)dv[u][2], (int)dv[u][3]};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < kR8Rows; r++) {
+          const v4i32 a = {(int)wv[u][r][0], (int)wv[u][r][1], (int)wv[u][r][2], (int)wv[u][r][3]};
+          acc[r] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[r], 0, 0, 0);
+        }
         const int nx = i + u + kR8Ahead;
         if (nx < ns) {
           const uint64_t s = s0 + (uint64_t)kColWaves * nx;
-          wv[u] = __builtin_nontemporal_load(wt + 64 * s);
+#pragma unroll
+          for (int r = 0; r < kR8Rows; r++) wv[u][r] = __builtin_nontemporal_load(wt[r] + 64 * s);
           dv[u] = dg[64 * s];
         }
       }
     }
   }
-  lds.acc[wave][lane] = acc;
-  __syncthreads();
-  if (wave != 0) return;
-  v4i32 t = lds.acc[0][lane];
 #pragma unroll
-  for (int w = 1; w < kColWaves; w++) t += lds.acc[w][lane];
+  for (int r = 0; r < kR8Rows; r++) lds.acc[r][wave][lane] = acc[r];
+  __syncthreads();
+  const uint64_t rt = rt0 + wave;  // this wave's tile
+  if (wave >= kR8Rows || rt >= nrt) return;
+  v4i32 t = lds.acc[wave][0][lane];
+#pragma unroll
+  for (int w = 1; w < kColWaves; w++) t += lds.acc[wave][w][lane];
   // lane l, element v: row 4 (l / 16) + v of the tile, digit plane j = l % 16 = 4 c + q
   constexpr int64_t kOffset = (int64_t)P << 26;  // > |sum_q 256^q acc_q| (< 2^53), a multiple of P
   const int j = lane & 15, q = j & 3, c = j >> 2;
@@ -1223,7 +1248,7 @@ static __global__ void __launch_bounds__(kBlock) k_restrict_cols8(const u32x4* _
     int64_t x = (int64_t)t[v] * ((int64_t)1 << (8 * q));
     x += __shfl_xor(x, 1, 64);
     x += __shfl_xor(x, 2, 64);
-    const uint64_t row = (uint64_t)rt * kR8TileRows + 4 * (lane >> 4) + v;
+    const uint64_t row = rt * kR8TileRows + 4 * (lane >> 4) + v;
     if (q == 0 && row < k) partial[((uint64_t)chunk_id * k + row) * 4 + c] = m31_reduce64((uint64_t)(x + kOffset));
   }
 }

@@ -74,7 +74,7 @@ static int prepare_r8(gkr_ctx* c, gkr_matrix* B) {
 #define GKR_RC_CEIL 1
 #endif
 #ifndef GKR_R8_WGS
-#define GKR_R8_WGS 2048
+#define GKR_R8_WGS 768
 #endif
 struct RestrictPlan {
   uint64_t m, k, n, pk;
@@ -83,6 +83,7 @@ struct RestrictPlan {
   uint64_t act_blocks;
   uint64_t gr, gc, chunk;  // u32 path: row blocks, column chunks, chunk columns
   uint64_t nst, nrt;       // int8 path: column steps, row tiles (gc chunks of `chunk` steps)
+  uint64_t ngroups;        // int8 path: groups of kR8Rows row tiles (gr == ngroups)
 };
 static int plan_restrict(const gkr_matrix* A, const gkr_matrix* B, uint64_t pk, bool weight_only, RestrictPlan* p) {
   p->m = A->rows;
@@ -96,17 +97,19 @@ static int plan_restrict(const gkr_matrix* A, const gkr_matrix* B, uint64_t pk, 
   p->ldig_bytes = p->use8 ? (n + kR8TileCols - 1) / kR8TileCols * kR8Tile : 0;
   p->act_blocks = weight_only ? 0 : (pk + 63) / 64;  // 64 columns of A per workgroup
   if (p->use8) {
-    // row tiles x column chunks: as many chunks (at most 8: the first trip
-    // adds the chunk partials) as keep the grid within about GKR_R8_WGS
-    // workgroups (2048: about 1.6 rounds of resident workgroups; measured
-    // 77 us of restriction per Qwen layer against 80 us with 1280 or 1536)
+    // row-tile groups x column chunks: as many chunks (at most 8: the first
+    // trip adds the chunk partials) as keep the grid within about GKR_R8_WGS
+    // workgroups (768: one round of resident workgroups at this kernel's
+    // occupancy; on cold weights the Qwen layer's seven restrictions took
+    // 68.8 us against 79.8 us for one row tile per workgroup at 2048)
     p->nst = B->r8_nst;
     p->nrt = (k + kR8TileRows - 1) / kR8TileRows;
-    const uint64_t room = GKR_R8_WGS > p->act_blocks + p->nrt ? GKR_R8_WGS - p->act_blocks : p->nrt;
-    const uint64_t gc8 = std::max<uint64_t>(1, std::min<uint64_t>({8, room / p->nrt, p->nst}));
+    p->ngroups = (p->nrt + kR8Rows - 1) / kR8Rows;
+    const uint64_t room = GKR_R8_WGS > p->act_blocks + p->ngroups ? GKR_R8_WGS - p->act_blocks : p->ngroups;
+    const uint64_t gc8 = std::max<uint64_t>(1, std::min<uint64_t>({8, room / p->ngroups, p->nst}));
     p->chunk = (p->nst + gc8 - 1) / gc8;
     p->gc = (p->nst + p->chunk - 1) / p->chunk;
-    p->gr = p->nrt;
+    p->gr = p->ngroups;
   } else {
     // column chunks: chunks a multiple of one wave sweep (256 columns), at
     // least GKR_RC_MIN_CHUNK columns, and at most GKR_RC_TARGET workgroups in
@@ -193,9 +196,9 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
   if (p.use8) {
     // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
     TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
-    GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(p.act_blocks + p.nrt * p.gc)), dim3(kBlock), 0,
+    GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(p.act_blocks + p.ngroups * p.gc)), dim3(kBlock), 0,
                (const u32x4*)B->r8, k, p.nst, (const u32x4*)ldig, (uint32_t)p.chunk, (uint32_t*)part, rows,
-               (uint32_t)p.act_blocks, (uint32_t)p.nrt);
+               (uint32_t)p.act_blocks, (uint32_t)p.ngroups);
     TRY(check_launch(c));
   } else {
     // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
