@@ -1,7 +1,8 @@
 """The BASELINE configurations at their full shapes on the GPU, checked against the CPU oracle
-(the reference's CPU algorithm): config 4 (one Qwen2.5-14B layer, the bench's workload), config 3
-(the 30-layer SmolLM2-135M walk), config 2 at 2^28, and the reference-default 2^20 softmax table on
-the Qwen score shape.  Inputs come from the bench's own generator (bench.LayerWeights), so these
+(the reference's CPU algorithm): config 5 (the 48-layer Qwen2.5-14B proof, every layer against the
+oracle's proof in tests/golden/config5_oracle.json), config 4 (one Qwen2.5-14B layer, the bench's
+workload), config 3 (the 30-layer SmolLM2-135M walk), config 2 at 2^28, and the reference-default
+2^20 softmax table on the Qwen score shape.  Inputs come from the bench's own generator (bench.LayerWeights), so these
 tests prove exactly what bench.py times."""
 import os
 import sys
@@ -146,42 +147,54 @@ def layer_shapes(cfg):
 
 
 def test_config5_qwen_48_layers(gpu_ctx):
-    """Config 5: the bench's 48-layer Qwen2.5-14B proof (52.9 GB of weights resident).  The proof
-    bytes equal the bench's recorded fingerprint; the whole serialized proof (432 layer proofs) is
-    replayed by the host verifier with the fresh-claim rule; layers 0, 23 and 47 are proved again
-    by the oracle from the channel state exported before each and equal the GPU's felts and the
-    state after them; a changed felt in layer 30 is rejected."""
+    """Config 5: the bench's 48-layer Qwen2.5-14B proof (52.9 GB of weights resident) against the CPU
+    oracle's proof of the same inputs (tests/golden/config5_oracle.json, written by
+    tests/golden/make_config5_fixture.py): every layer's serialized felts (SHA-256 of their words) and
+    the channel state after every layer equal the oracle's, and so does the whole proof's SHA-256.
+    Layer 23 is also proved again by the oracle on the box from the exported channel state.  The
+    whole proof is replayed by the host verifier with the fresh-claim rule, and a changed felt in
+    layer 30 is rejected."""
     import hashlib
+    import json
     log("case config5 48 layers")
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config5_oracle.json")) as f:
+        ref = json.load(f)
+    assert ref["n_layers"] == 48 and ref["seed"] == 7
     layers = [bench.LayerWeights(gpu_ctx, bench.QWEN, l, 0) for l in range(48)]
-    sample = (0, 23, 47)
+    live = 23
     ch = G.PoseidonChannel()
     ch.mix_u64(7)
     proof = G.Proof()
     states = {}
     for l, L in enumerate(layers):
-        if l in sample or l - 1 in sample:
+        if l == live:
             states[l] = ch.export_state()
         arr, n = bench.model_steps([L])
         fp, fv = G.prove_walk(gpu_ctx, ch, arr, proof, n_steps=n)
-    states[48] = ch.export_state()
+        states[l + 1] = ch.export_state()
     words = proof.serialize_words()
-    assert len(words) == 6368361
-    assert hashlib.sha256(words.tobytes()).hexdigest()[:16] == "7553e0f9af527f9a"  # bench.py's proof
+    assert len(words) == ref["n_felts"]
     # layer count, then 48 equal layers, then the tail: input claim (no point: 1 + 4 felts), commitment
     # count, opening count, IO commitment
     per, rem = divmod(len(words) - 1 - 8, 48)
     assert rem == 0
-    for l in sample:
-        t0 = time.time()
-        och = O.Channel()
-        O.set_channel_state(och, states[l])
-        ref = []
-        oracle_layer(och, bench.QWEN, l, ref)
-        log(f"  oracle layer {l}: {time.time() - t0:.1f} s")
-        assert len(ref) == per
-        assert np.array_equal(words[1 + l * per:1 + (l + 1) * per], G.felts_to_words(ref)), f"layer {l}"
-        assert O.channel_state(och) == list(states[l + 1]), f"channel after layer {l}"
+    for l in range(48):
+        want = ref["layers"][l]
+        assert per == want["felts"], f"layer {l} length"
+        got = hashlib.sha256(words[1 + l * per:1 + (l + 1) * per].tobytes()).hexdigest()
+        assert got == want["sha256"], f"layer {l} differs from the oracle's"
+        assert list(states[l + 1]) == want["state_after"], f"channel after layer {l}"
+    assert hashlib.sha256(words.tobytes()).hexdigest() == ref["proof_sha256"]
+    assert list(states[48]) == ref["final_state"]
+    log("  48 layers equal the oracle fixture")
+    t0 = time.time()
+    och = O.Channel()
+    O.set_channel_state(och, states[live])
+    out = []
+    oracle_layer(och, bench.QWEN, live, out)
+    log(f"  oracle layer {live}: {time.time() - t0:.1f} s")
+    assert np.array_equal(words[1 + live * per:1 + (live + 1) * per], G.felts_to_words(out))
+    assert O.channel_state(och) == list(states[live + 1])
     # host replay of the whole proof
     proof.set_input_claim(fp, fv)
     full = proof.serialize_words()
