@@ -143,6 +143,7 @@ int orc_prove_activation_layer(const uint32_t* claim_point, int n_point, const u
   orc_mix_u64(ch, tag);
   qm gamma = draw_q(ch);
   qm beta = draw_q(ch);
+  orc_trace(ch, "logup.gamma_beta", -1);
   /* d_i = gamma - in_i - beta out_i; w = batch_inverse(d) (6457-6464) */
   qm* d = (qm*)malloc(n * sizeof(qm));
   qm* w = (qm*)malloc(n * sizeof(qm));
@@ -202,6 +203,7 @@ int orc_prove_activation_layer(const uint32_t* claim_point, int n_point, const u
     fold_mle(d, r, mid);
     cur_n = mid;
   }
+  orc_trace(ch, "logup.eq", -1);
   qm w_eval = w[0];
   qm in_eval_s = mle_evaluate(masked_in, nv, chal);
   qm out_eval_s = mle_evaluate(masked_out, nv, chal);
@@ -231,6 +233,7 @@ int orc_prove_activation_layer(const uint32_t* claim_point, int n_point, const u
     for (size_t i = 0; i < half; i++) vals[i] = q_add(q_mul(omr, vals[i]), q_mul(r, vals[i + half]));
     cur = half;
   }
+  orc_trace(ch, "logup.mult", -1);
   q_store(mult_final, vals[0]);
   q_store(mult_sum, msum);
   free(vals);
@@ -243,6 +246,7 @@ int orc_prove_activation_layer(const uint32_t* claim_point, int n_point, const u
   /* final mixes (6578-6579) */
   mix_q(ch, in_eval_claim);
   orc_mix_secure_field(ch, claim_value);
+  orc_trace(ch, "logup", -1);
   q_store(input_eval, in_eval_claim);
   return 0;
 }

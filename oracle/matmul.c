@@ -265,8 +265,10 @@ int orc_prove_matmul_layer(const uint32_t* claim_point, int n_point, const uint3
     free(chal);
     return rc;
   }
+  orc_trace(ch, "matmul.rounds", -1);
   orc_mix_secure_field(ch, final_a);
   orc_mix_secure_field(ch, final_b);
+  orc_trace(ch, "matmul", -1);
   memcpy(next_point, claim_point, (size_t)log_m * 16);
   memcpy(next_point + 4 * log_m, chal, (size_t)T * 16);
   memcpy(next_value, final_a, 16);

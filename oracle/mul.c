@@ -75,9 +75,11 @@ int orc_reduce_mul_layer(const uint32_t* claim_point, int n_point, const uint32_
   }
   qm le = fa[0], re = fb[0];
   free(eq); free(fa); free(fb);
+  orc_trace(ch, "mul.eq", -1);
   mix_qv(ch, le);
   mix_qv(ch, re);
   qm alpha = draw_qv(ch);
+  orc_trace(ch, "mul", -1);
   qm comb = q_add(q_mul(alpha, le), q_mul(q_sub(q_one(), alpha), re));
   q_store(lhs_eval, le);
   q_store(rhs_eval, re);

@@ -393,6 +393,7 @@ int orc_prove_layernorm_layer(const uint32_t* claim_point, int n_point, const ui
   if (rc == 0) {
     mix_q(ch, input_eval); /* 8348-8349 */
     mix_q(ch, output_eval);
+    orc_trace(ch, "layernorm", -1);
     out->n_rows = (uint32_t)prow;
     for (size_t i = 0; i < prow; i++) {
       out->row_stats0[i] = mean[i];
@@ -543,6 +544,7 @@ int orc_prove_rmsnorm_layer(const uint32_t* claim_point, int n_point, const uint
   if (rc == 0) {
     mix_q(ch, input_eval); /* 8740-8741 */
     mix_q(ch, output_eval);
+    orc_trace(ch, "rmsnorm", -1);
     out->n_rows = (uint32_t)prow;
     for (size_t i = 0; i < prow; i++) {
       out->row_stats0[i] = ms[i];

@@ -46,6 +46,7 @@ void orc_mix_felt(orc_channel* ch, const uint32_t w[8]);
 void orc_mix_secure_field(orc_channel* ch, const uint32_t q[4]);
 void orc_mix_felts(orc_channel* ch, const uint32_t* q, size_t n);
 void orc_mix_felts_stwo(orc_channel* ch, const uint32_t* q, size_t n);
+void orc_trace(const orc_channel* ch, const char* label, long index);
 void orc_mix_poly_coeffs(orc_channel* ch, const uint32_t c[12]);
 void orc_mix_poly_coeffs_deg3(orc_channel* ch, const uint32_t c[16]);
 void orc_draw_felt252(orc_channel* ch, uint32_t out[8]);

@@ -140,6 +140,12 @@ class Channel:
         return felt_int(out)
 
 
+def trace_point(ch: "Channel", label: str, index: int = -1) -> None:
+    """orc_trace: one line of the ORACLE_CHANNEL_TRACE transcript trace (a walk's step boundaries are
+    marked from Python, the layers' own points from C)."""
+    lib().orc_trace(ch.buf, label.encode(), C.c_long(index))
+
+
 def channel_state(ch: "Channel") -> List[int]:
     """The channel in the reference's to_gpu_state layout (poseidon_channel.rs:109-135): 8 LE u32
     words of the canonical digest, n_draws, hash_count lo, hash_count hi."""

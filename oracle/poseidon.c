@@ -376,6 +376,26 @@ void orc_mix_felts_stwo(orc_channel* ch, const uint32_t* q, size_t n) {
   fe in[1] = {ch_digest(ch)};
   ch_set(ch, fe_hash_many(in, 1));
 }
+/* Transcript trace (test infrastructure): with ORACLE_CHANNEL_TRACE set to a
+ * path (or "-" for stderr), appends "<label>[ <index>] 0x<digest> <n_draws>"
+ * at the points where the product traces under GKR_CHANNEL_TRACE, so the two
+ * traces can be compared line by line.  The reference prints its channel at
+ * such points under STWO_CHANNEL_TRACE (gkr/prover.rs:1523-1541, 6002-6012). */
+void orc_trace(const orc_channel* ch, const char* label, long index) {
+  const char* path = getenv("ORACLE_CHANNEL_TRACE");
+  if (!path || !*path) return;
+  uint32_t d[8];
+  orc_digest(ch, d);
+  FILE* f = strcmp(path, "-") == 0 ? stderr : fopen(path, "a");
+  if (!f) return;
+  if (index >= 0)
+    fprintf(f, "%s %ld 0x", label, index);
+  else
+    fprintf(f, "%s 0x", label);
+  for (int w = 7; w >= 0; w--) fprintf(f, "%08x", d[w]);
+  fprintf(f, " %u\n", ch->n_draws);
+  if (f != stderr) fclose(f);
+}
 /* draw_felt252: [digest, n_draws, 3] (poseidon_channel.rs:156-166) */
 static fe draw_fe(orc_channel* ch) {
   fe s[3] = {ch_digest(ch), fe_from_u64(ch->n_draws), fe_from_u64(3)};

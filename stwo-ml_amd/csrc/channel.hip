@@ -32,6 +32,44 @@ extern "C" int gkr_poseidon_hash_many(const gkr_felt* in, size_t n, gkr_felt* ou
   return GKR_OK;
 }
 
+// ------------------------------------------------------------------ transcript trace
+namespace {
+thread_local int tl_trace_depth = 0;
+thread_local bool tl_trace_on = false;
+thread_local std::string tl_trace_path;  // empty: stderr
+std::mutex g_trace_mu;
+}  // namespace
+gkr::TraceScope::TraceScope() {
+  if (tl_trace_depth++ != 0) return;
+  const char* p = getenv("GKR_CHANNEL_TRACE");
+  tl_trace_on = false;
+  tl_trace_path.clear();
+  if (p && *p) {
+    tl_trace_on = true;
+    if (strcmp(p, "-") != 0 && strcmp(p, "stderr") != 0) tl_trace_path = p;
+  } else if (getenv("STWO_CHANNEL_TRACE")) {
+    tl_trace_on = true;
+  }
+}
+gkr::TraceScope::~TraceScope() { tl_trace_depth--; }
+bool gkr::trace_enabled() { return tl_trace_on && tl_trace_depth > 0; }
+void gkr::trace_point_impl(const PoseidonChannel& ch, const char* label, long index) {
+  const gkr_felt d = felt_to_abi(ch.digest);
+  char line[160];
+  int n = index >= 0 ? snprintf(line, sizeof line, "%s %ld 0x", label, index) : snprintf(line, sizeof line, "%s 0x", label);
+  for (int w = 7; w >= 0; w--) n += snprintf(line + n, sizeof line - n, "%08x", d.w[w]);
+  snprintf(line + n, sizeof line - n, " %u\n", ch.n_draws);
+  std::lock_guard<std::mutex> lk(g_trace_mu);
+  if (tl_trace_path.empty()) {
+    fputs(line, stderr);
+    return;
+  }
+  if (FILE* f = fopen(tl_trace_path.c_str(), "a")) {
+    fputs(line, f);
+    fclose(f);
+  }
+}
+
 // ------------------------------------------------------------------ channel ABI
 extern "C" int gkr_channel_new(gkr_channel** out) {
   if (!out) return fail(GKR_ERR_INVALID, "null out");

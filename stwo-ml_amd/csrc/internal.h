@@ -26,6 +26,7 @@
 #include "kernels.h"
 #include "launcher.h"
 #include "poseidon.h"
+#include "trace.h"
 
 namespace gkr {
 struct MerkleConsts;  // merkle.h

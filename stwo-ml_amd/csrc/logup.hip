@@ -281,6 +281,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   }
   HIP_TRY(hipSetDevice(c->device));
   c->mm.valid = false;
+  TraceScope trace;
   PoseidonChannel& C = ch->ch;
   const uint64_t tsize = 1ull << table_log;
   const uint32_t mask = (uint32_t)(tsize - 1);
@@ -324,6 +325,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   qm31 gb[2];
   C.draw_qm31s(gb, 2);
   const qm31 gamma = gb[0], beta = gb[1];
+  trace_point(C, "logup.gamma_beta");
   out->gamma = G(gamma);
   out->beta = G(beta);
 
@@ -418,6 +420,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   qm31 fin[3];
   TRY(eq3_sumcheck(c, C, cpt.data(), epl, d_w0, d_d0, d_w1, d_d1, out->eq_round_polys, chal.data(), fin,
                    eq_pre ? &sk_eq0 : nullptr, &table_side));
+  trace_point(C, "logup.eq");
   if (!table_side_done) TRY(table_side());
   const qm31 w_eval = fin[1];
   // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass;
@@ -533,6 +536,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     }
     mfin[0] = V[0];
   }
+  trace_point(C, "logup.mult");
   // the kernels whose results were waited for in the multiplicity sumcheck
   // were queued after the one writing the multiplicities' pinned copy
   memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
@@ -550,6 +554,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   out->table_commitment = felt_to_abi(tc);
   C.mix_secure_field(input_eval);
   C.mix_secure_field(Q(*claim_value));
+  trace_point(C, "logup");
   out->input_eval = G(input_eval);
   out->output_eval = *claim_value;
 

@@ -597,6 +597,7 @@ static int prove_matmul_impl(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n
   if (!c || !a || !b || !claim_value || !final_a || !final_b || !next_value || (!claim_point && n_point))
     return fail(GKR_ERR_INVALID, "null argument");
   if (!fresh && !canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
+  TraceScope trace;
   const uint64_t pm = next_pow2(a->rows), pk = next_pow2(a->cols), pn = next_pow2(b->cols);
   const uint32_t log_m = (uint32_t)log2_exact(pm), log_n = (uint32_t)log2_exact(pn);
   const int T = log2_exact(pk);
@@ -624,8 +625,10 @@ static int prove_matmul_impl(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n
   std::vector<gkr_qm31> chal(T > 0 ? T : 1);
   TRY(reduce_matmul_impl(c, a, b, claim_point, log_m, claim_point + log_m, log_n, pk, C, round_polys, chal.data(),
                          final_a, final_b, fresh ? &claim_from_sums : nullptr));
+  trace_point(C, "matmul.rounds");
   C.mix_secure_field(Q(*final_a));
   C.mix_secure_field(Q(*final_b));
+  trace_point(C, "matmul");
   if (next_point) {
     for (uint32_t l = 0; l < log_m; l++) next_point[l] = claim_point[l];
     for (int t = 0; t < T; t++) next_point[log_m + t] = chal[t];

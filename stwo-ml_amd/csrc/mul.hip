@@ -11,6 +11,7 @@ static int mul_layer_core(gkr_ctx* c, const std::vector<qm31>& cpt, const qm31& 
   TRY(ensureT(c, S_W1, n / 2 + 1, &d_w1));
   TRY(ensureT(c, S_D0, n, &d_d0));
   TRY(ensureT(c, S_D1, n / 2 + 1, &d_d1));
+  TraceScope trace;
   PoseidonChannel& C = ch->ch;
   Eq3Plan epl;  // eq over the first nv claim coordinates, kept factored
   TRY(eq3_prepare(c, cpt.data(), nv, &epl));
@@ -19,10 +20,12 @@ static int mul_layer_core(gkr_ctx* c, const std::vector<qm31>& cpt, const qm31& 
   std::vector<qm31> chal(nv);
   qm31 fin[3];
   TRY(eq3_sumcheck(c, C, cpt.data(), epl, d_w0, d_d0, d_w1, d_d1, out->eq_round_polys, chal.data(), fin));
+  trace_point(C, "mul.eq");
   const qm31 lhs = fin[1], rhs = fin[2];
   C.mix_secure_field(lhs);
   C.mix_secure_field(rhs);
   const qm31 alpha = C.draw_qm31();
+  trace_point(C, "mul");
   const qm31 comb = qm31_add(qm31_mul(alpha, lhs), qm31_mul(qm31_sub(qm31_one(), alpha), rhs));
   out->lhs_eval = G(lhs);
   out->rhs_eval = G(rhs);

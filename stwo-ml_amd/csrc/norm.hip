@@ -523,6 +523,7 @@ int prove_norm(gkr_ctx* c, bool ln, const gkr_qm31* claim_point, uint32_t n_poin
       if (gamma[i] >= P) return fail(GKR_ERR_INVALID, "gamma value %llu not canonical", (unsigned long long)i);
   HIP_TRY(hipSetDevice(c->device));
   c->mm.valid = false;
+  TraceScope trace;
   PoseidonChannel& C = ch->ch;
   NormShape S;
   TRY(norm_stats(c, X, ln, dim, &S));
@@ -632,6 +633,7 @@ int prove_norm(gkr_ctx* c, bool ln, const gkr_qm31* claim_point, uint32_t n_poin
   TRY(norm_logup(c, C, ln ? kNormTagRS : kNormTagRN, S, z.data(), out));
   C.mix_secure_field(input_eval);
   C.mix_secure_field(output_eval);
+  trace_point(C, ln ? "layernorm" : "rmsnorm");
   out->n_rows = (uint32_t)S.prow;
   for (uint64_t r = 0; r < S.prow; r++) {
     out->row_stats0[r] = ln ? S.mean[r] : S.key[r];

@@ -16,6 +16,7 @@
 #include "activations.h"
 #include "field.h"
 #include "poseidon.h"
+#include "trace.h"
 
 namespace gkr {
 
@@ -100,8 +101,10 @@ inline bool verify_matmul(const std::vector<qm31>& point, const qm31& value, uin
     err->why = "final eval check failed: sum=" + q_str(sum) + " != a*b=" + q_str(prod);
     return false;
   }
+  trace_point(ch, "matmul.rounds");
   ch.mix_secure_field(final_a);
   ch.mix_secure_field(final_b);
+  trace_point(ch, "matmul");
   next_point->assign(point.begin(), point.begin() + log_m);
   next_point->insert(next_point->end(), chal.begin(), chal.end());
   *next_value = final_a;
@@ -139,9 +142,11 @@ inline bool verify_mul(const std::vector<qm31>& point, const qm31& value, const 
     err->why = "mul final check failed: sum=" + q_str(sum) + " != eq*a*b=" + q_str(expected);
     return false;
   }
+  trace_point(ch, "mul.eq");
   ch.mix_secure_field(lhs);
   ch.mix_secure_field(rhs);
   const qm31 alpha = ch.draw_qm31();
+  trace_point(ch, "mul");
   *next_value = qm31_add(qm31_mul(alpha, lhs), qm31_mul(qm31_sub(qm31_one(), alpha), rhs));
   return true;
 }
@@ -179,6 +184,7 @@ inline bool verify_activation(const std::vector<qm31>& point, uint32_t tag, uint
   ch.mix_u64(tag);
   const qm31 gamma = ch.draw_qm31();
   const qm31 beta = ch.draw_qm31();
+  trace_point(ch, "logup.gamma_beta");
   felt tc_in[2] = {felt_from_u64(tag), felt_from_u64(table_log)};
   const felt expected_tc = felt_from_mont(poseidon_hash_many(tc_in, 2));
   if (!felt_eq(expected_tc, p.table_commitment)) {
@@ -224,6 +230,7 @@ inline bool verify_activation(const std::vector<qm31>& point, uint32_t tag, uint
     err->why = "activation final check failed: sum=" + q_str(sum) + " != eq*w*d=" + q_str(expected);
     return false;
   }
+  trace_point(ch, "logup.eq");
   // verify_multiplicity_sumcheck
   qm31 msum = p.mult_sum;
   for (size_t t = 0; t < p.mult_polys.size() / 2; t++) {
@@ -241,8 +248,10 @@ inline bool verify_activation(const std::vector<qm31>& point, uint32_t tag, uint
     err->why = "multiplicity sumcheck final eval mismatch";
     return false;
   }
+  trace_point(ch, "logup.mult");
   ch.mix_secure_field(p.input_eval);
   ch.mix_secure_field(p.output_eval);
+  trace_point(ch, "logup");
   *next_value = p.input_eval;
   return true;
 }
@@ -463,6 +472,7 @@ inline bool verify_norm(bool ln, const std::vector<qm31>& point, const qm31& val
   }
   ch.mix_secure_field(p.input_eval);
   ch.mix_secure_field(p.output_eval);
+  trace_point(ch, name);
   *next_value = p.input_eval;
   return true;
 }

@@ -21,6 +21,7 @@ extern "C" int gkr_verify_matmul_layer(const gkr_qm31* claim_point, uint32_t n_p
                                        gkr_channel* ch, gkr_qm31* next_point, uint32_t* n_next,
                                        gkr_qm31* next_value) {
   CH_CHECK(ch);
+  TraceScope trace;
   if (!claim_value || !final_a || !final_b || !next_point || !n_next || !next_value ||
       (!claim_point && n_point) || (!round_polys && n_rounds))
     return fail(GKR_ERR_INVALID, "null argument");
@@ -46,6 +47,7 @@ extern "C" int gkr_verify_mul_layer(const gkr_qm31* claim_point, uint32_t n_poin
                                     const gkr_qm31* eq_round_polys, uint32_t n_rounds, const gkr_qm31* lhs_eval,
                                     const gkr_qm31* rhs_eval, gkr_channel* ch, gkr_qm31* next_value) {
   CH_CHECK(ch);
+  TraceScope trace;
   if (!claim_value || !lhs_eval || !rhs_eval || !next_value || (!claim_point && n_point) ||
       (!eq_round_polys && n_rounds))
     return fail(GKR_ERR_INVALID, "null argument");
@@ -73,6 +75,7 @@ extern "C" int gkr_verify_activation_layer(const gkr_qm31* claim_point, uint32_t
                                            uint32_t table_log_size, uint32_t n_eq_rounds, const gkr_logup_out* proof,
                                            gkr_channel* ch, gkr_qm31* next_value) {
   CH_CHECK(ch);
+  TraceScope trace;
   if (!proof || !next_value || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
   if (!act_valid(activation_type)) return fail(GKR_ERR_INVALID, "unknown activation type %u", activation_type);
   if (!act_logup_valid(activation_type))
@@ -117,6 +120,7 @@ static const std::vector<uint32_t>& rsqrt_table() {
 static int verify_norm_abi(bool ln, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
                            uint64_t dim, const gkr_norm_out* o, gkr_channel* ch, gkr_qm31* next_value) {
   CH_CHECK(ch);
+  TraceScope trace;
   if (!o || !claim_value || !next_value || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
   if (!o->p0_round_polys || !o->lin_round_polys || !o->logup_round_polys || !o->multiplicities ||
       !o->mult_round_polys || (o->n_rows && (!o->row_stats0 || !o->row_stats1)))
@@ -184,6 +188,7 @@ extern "C" int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const g
                                gkr_channel* ch, gkr_qm31* final_point, uint32_t* n_final, gkr_qm31* final_value,
                                size_t* n_consumed) {
   CH_CHECK(ch);
+  TraceScope trace;
   if (!calldata || !layers || !final_point || !n_final || !final_value || (!init_point && n_init) ||
       (!fresh_values && n_fresh))
     return fail(GKR_ERR_INVALID, "null argument");
@@ -365,6 +370,7 @@ extern "C" int gkr_verify_walk(const gkr_felt* calldata, size_t n_felts, const g
     } else {
       return fail(GKR_ERR_INVALID, "layer %zu: unknown kind %u", li, L.kind);
     }
+    trace_point(ch->ch, "walk.step", (long)li);
   }
   // the input claim the proof states must be the one the walk arrived at
   const uint64_t npt = R.u(64);

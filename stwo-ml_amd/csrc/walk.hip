@@ -8,6 +8,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
   CH_CHECK(ch);
   if (!c || (!steps && n_steps) || !final_point || !n_final || !final_value)
     return fail(GKR_ERR_INVALID, "null argument");
+  TraceScope trace;
   std::vector<gkr_qm31> point(init_point ? init_point : nullptr, init_point ? init_point + n_init : nullptr);
   gkr_qm31 value = init_value ? *init_value : G(qm31_zero());
   bool have_claim = init_value != nullptr;
@@ -158,6 +159,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
     }
     c->prelaunch = nullptr;
     have_claim = true;
+    trace_point(ch->ch, "walk.step", (long)si);
   }
   if (point.size() > 64) return fail(GKR_ERR_BUFFER, "final claim has %zu variables", point.size());
   for (size_t l = 0; l < point.size(); l++) final_point[l] = point[l];

@@ -549,3 +549,39 @@ def test_matrix_outlives_context():
         other.reduce_matmul_layer(b, b, [(1, 0, 0, 0)], [(1, 0, 0, 0)], 2, ch)
     b.free()
     other.close()
+
+
+def test_walk_trace_equals_oracle_trace(gpu_ctx, tmp_path):
+    """GKR_CHANNEL_TRACE on the GPU prover: the chained MatMul -> Mul -> Activation -> MatMul walk of
+    tests/test_trace.py proved by gkr_prove_walk writes the same trace, line for line, as the oracle
+    proving it (ORACLE_CHANNEL_TRACE)."""
+    import test_trace as T
+    log("case walk transcript trace")
+    ot, gt = str(tmp_path / "oracle.trace"), str(tmp_path / "gpu.trace")
+    cd, shapes, start, r, v, end = T.chained_walk_proof(ot)
+    rng = np.random.default_rng(5)  # the walk's matrices, as chained_walk_proof draws them
+    X0 = rng.integers(0, P, size=(4, 12), dtype=np.uint32)
+    W0 = rng.integers(0, P, size=(12, 16), dtype=np.uint32)
+    H = O.matmul_forward(X0, W0)
+    L = np.vectorize(lambda x: O.activation(3, int(x)), otypes=[np.uint32])(H)
+    R = rng.integers(0, P, size=(4, 16), dtype=np.uint32)
+    X = ((L.astype(np.uint64) * R) % P).astype(np.uint32)
+    W = rng.integers(0, P, size=(16, 8), dtype=np.uint32)
+    dev = {k: gpu_ctx.upload(m) for k, m in dict(X0=X0, W0=W0, H=H, L=L, R=R, X=X, W=W).items()}
+    Ch = G.CLAIM_CHAINED
+    arr = G.make_steps([(G.STEP_MATMUL, Ch, dev["X"], dev["W"], 0, 0), (G.STEP_MUL, Ch, dev["L"], dev["R"], 0, 0),
+                        (G.STEP_ACTIVATION, Ch, dev["H"], None, 3, 8), (G.STEP_MATMUL, Ch, dev["X0"], dev["W0"], 0, 0)])
+    gch = G.PoseidonChannel()
+    gch.import_state(start)
+    old = os.environ.get("GKR_CHANNEL_TRACE")
+    os.environ["GKR_CHANNEL_TRACE"] = gt
+    try:
+        G.prove_walk(gpu_ctx, gch, arr, G.Proof(), n_steps=4, init_point=r, init_value=v)
+    finally:
+        if old is None:
+            os.environ.pop("GKR_CHANNEL_TRACE", None)
+        else:
+            os.environ["GKR_CHANNEL_TRACE"] = old
+    assert gch.digest() == end
+    assert T.read(gt) == T.read(ot)
+    assert [x[0] for x in T.read(gt)] == T.EXPECTED_LABELS
