@@ -219,26 +219,49 @@ def measured_traffic(name="restrict_cols_traffic.md"):
     return None
 
 
-def cpu_baseline(budget_s=25.0):
-    """The oracle (reference CPU algorithm) on a bounded sample: Qwen q_proj layer reduction."""
+def cpu_baseline(config="qwen48"):
+    """The oracle (the reference's CPU algorithm) on the host cores, on a bounded unit of the bench's
+    own workload: for the Qwen configs one whole config-4 layer (layer 0 of the bench's model: 7
+    matmul reductions with their fresh claims, the SiLU and softmax-exp LogUp reductions; config 5
+    is reported as 48 times that layer, labelled as an extrapolation), for smollm the whole 30-layer
+    proof, for cfg1 the 256^3 layer."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    m, k, n = 64, 5120, 5120
-    A = O.synthetic(m, k, 1, 1)
-    B = O.synthetic(k, n, 1, 2)
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    info = host_info()
+    base = {"unit": "Melem/s", "cores": info["omp_threads"], "kind": "port", "host": info}
     t0 = time.perf_counter()
-    ch = O.Channel()
-    r = ch.draw_qm31s(lg(m) + lg(n))
-    v = O.matmul_output_claim(A, B, r)
-    ch.mix_secure_field(v)
-    O.prove_matmul_layer(r, v, A, B, ch)
+    if config == "cfg1":
+        A, B = O.synthetic(256, 256, 0, 0), O.synthetic(256, 256, 0, 1)
+        ch = O.Channel()
+        r = ch.draw_qm31s(16)
+        v = O.matmul_output_claim(A, B, r)
+        ch.mix_secure_field(v)
+        O.prove_matmul_layer(r, v, A, B, ch)
+        dt = time.perf_counter() - t0
+        return dict(base, value=round(2 * 256 * 256 / dt / 1e6, 3), s_per_proof=round(dt, 4),
+                    sample=f"BASELINE config 1 (256x256x256 uniform M31 layer) by the oracle: {dt:.3f} s")
+    och = O.Channel()
+    och.mix_u64(7)
+    out = []
+    if config == "smollm":
+        for layer in range(30):
+            oracle_layer(O, och, SMOL, layer, out)
+        dt = time.perf_counter() - t0
+        per_layer, _ = matmul_elems(SMOL)
+        return dict(base, value=round(30 * per_layer / dt / 1e6, 3), s_per_proof=round(dt, 3),
+                    proved_tokens_per_s=round(1 / dt, 3),
+                    sample=f"the whole BASELINE config 3 proof (30 SmolLM2-135M layers, 1 token) by the oracle: {dt:.2f} s")
+    oracle_layer(O, och, QWEN, 0, out)
     dt = time.perf_counter() - t0
-    elems = k * n + m * k
-    return {"value": round(elems / dt / 1e6, 3), "unit": "Melem/s", "cores": threads, "kind": "port",
-            "sample": f"one Qwen2.5-14B q_proj layer (64x5120 . 5120x5120, int8-range) by the reference CPU "
-                      f"algorithm (forward GEMM for the claim, pad, QM31 MLE, restrict_mle, rounds): "
-                      f"{dt:.2f} s"}
+    per_layer, _ = matmul_elems(QWEN)
+    return dict(base, value=round(per_layer / dt / 1e6, 3),
+                sample=f"one whole Qwen2.5-14B layer, 64 tokens (BASELINE config 4: 7 matmul reductions with fresh "
+                       f"claims, SiLU and softmax-exp LogUp reductions) by the oracle, the reference's CPU algorithm "
+                       f"(forward product for each claim, pad, QM31 MLE, restrict_mle, rounds; batch inversion, "
+                       f"eq-sumcheck and multiplicity rounds): {dt:.2f} s",
+                s_per_layer=round(dt, 3), proved_tokens_per_s=round(QWEN["tokens"] / dt, 3),
+                config5_extrapolated_s_per_proof=round(48 * dt, 1),
+                config5_note="48 x the measured layer (an extrapolation, not timed)")
 
 
 def oracle_host_layer(O, cfg, layer, seed_base=0):
@@ -301,7 +324,12 @@ def host_info():
     except (OSError, IndexError, subprocess.SubprocessError):
         cc = None
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
-    return {"cpu_model": model, "nproc": os.cpu_count(), "omp_threads": threads, "oracle_compiler": cc}
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = None
+    return {"cpu_model": model, "nproc": os.cpu_count(), "cpus_usable": usable, "omp_threads": threads,
+            "oracle_compiler": cc, "oracle_flags": "-O3 -march=x86-64-v3 -fopenmp (oracle/Makefile)"}
 
 
 def cpu_configs():
@@ -1028,7 +1056,9 @@ def main():
         result["roofline"]["frac_of_measured_read"] = round(rc["gbps"] / rd, 4)
     if not args.no_cpu_baseline:
         log("[bench] timing CPU baseline sample")
-        result["cpu_baseline"] = cpu_baseline()
+        cb = cpu_baseline(args.config)
+        cb["gpu_over_cpu"] = round(result["value"] / cb["value"], 1)  # same unit (Melem/s), same workload unit
+        result["cpu_baseline"] = cb
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
