@@ -324,10 +324,23 @@ int gkr_matmul_forward_into(gkr_ctx* ctx, const gkr_matrix* a, const gkr_matrix*
  * mle_opening.rs:630-641): B[i][j] at index j * next_pow2(rows) + i of the padded grid.
  * gkr_weight_commitments: the same for `count` matrices in one batch (one root each,
  * in order), the role of commit_mle_root_only_batch (mle_opening.rs:791-809).
- * gkr_mle_commitment: commit_mle_root_only over the n QM31 values of `evals`. */
+ * gkr_mle_commitment: commit_mle_root_only over the n QM31 values of `evals`.
+ * A weight's root is kept on its resident matrix once computed (the weight
+ * phase of every later proof takes it from there) until its contents change
+ * (gkr_matrix_invalidate, gkr_matmul_forward_into).                           */
 int gkr_weight_commitment(gkr_ctx* ctx, const gkr_matrix* b, gkr_felt* root);
 int gkr_weight_commitments(gkr_ctx* ctx, const gkr_matrix* const* mats, size_t count, gkr_felt* roots);
 int gkr_mle_commitment(gkr_ctx* ctx, const gkr_qvec* evals, gkr_felt* root);
+/* The weight-commitment cache kept on resident matrices, for a caller that
+ * persists roots across processes (the reference's WeightCommitmentCache,
+ * engine/src/weight_cache.rs:283-327: get_root / insert_root, saved to a file
+ * with a content fingerprint, :339-395, :646).
+ * gkr_matrix_commitment_cached: *cached = 1 and the root when m holds one.
+ * gkr_matrix_set_commitment: m holds `root` from now on (canonical felt); the
+ * caller vouches that it is m's weight commitment, as the reference trusts a
+ * cache file whose fingerprint matches.                                        */
+int gkr_matrix_commitment_cached(const gkr_matrix* m, gkr_felt* root, int* cached);
+int gkr_matrix_set_commitment(gkr_ctx* ctx, gkr_matrix* m, const gkr_felt* root);
 
 /* Weight openings: prove_mle_opening_with_commitment (mle_opening.rs:1654-1915)
  * over matrix_to_mle_col_major_padded(B) at eval_point (log2(next_pow2(rows)) +

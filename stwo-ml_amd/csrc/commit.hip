@@ -197,12 +197,52 @@ extern "C" int gkr_weight_commitment(gkr_ctx* c, const gkr_matrix* b, gkr_felt* 
   return gkr_weight_commitments(c, &b, 1, root);
 }
 
+// Roots already on a matrix (computed before, or supplied with
+// gkr_matrix_set_commitment) are taken from it; the others are computed in
+// one batch and kept on their matrices, until the contents change
+// (gkr_matrix_invalidate, gkr_matmul_forward_into).  The reference keeps the
+// same root per weight in WeightCommitmentCache (weight_cache.rs:283-327).
 extern "C" int gkr_weight_commitments(gkr_ctx* c, const gkr_matrix* const* mats, size_t count, gkr_felt* roots) {
   if (!c || (count && (!mats || !roots))) return fail(GKR_ERR_INVALID, "null argument");
   HIP_TRY(hipSetDevice(c->device));
-  std::vector<MerkleTreeSpec> trees(count);
-  for (size_t i = 0; i < count; i++) TRY(weight_tree(mats[i], &trees[i]));
-  return merkle_roots(c, trees, roots);
+  std::vector<MerkleTreeSpec> trees;
+  std::vector<size_t> todo;
+  for (size_t i = 0; i < count; i++) {
+    MerkleTreeSpec t;
+    TRY(weight_tree(mats[i], &t));  // validates every matrix, cached or not
+    if (mats[i]->have_root) {
+      roots[i] = mats[i]->root;
+      continue;
+    }
+    trees.push_back(t);
+    todo.push_back(i);
+  }
+  if (trees.empty()) return GKR_OK;
+  std::vector<gkr_felt> fresh(trees.size());
+  TRY(merkle_roots(c, trees, fresh.data()));
+  for (size_t j = 0; j < todo.size(); j++) {
+    gkr_matrix* m = const_cast<gkr_matrix*>(mats[todo[j]]);
+    roots[todo[j]] = fresh[j];
+    if (m->ctx == c) {
+      m->root = fresh[j];
+      m->have_root = true;
+    }
+  }
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_commitment_cached(const gkr_matrix* m, gkr_felt* root, int* cached) {
+  if (!m || !root || !cached) return fail(GKR_ERR_INVALID, "null argument");
+  *cached = m->have_root ? 1 : 0;
+  if (m->have_root) *root = m->root;
+  return GKR_OK;
+}
+extern "C" int gkr_matrix_set_commitment(gkr_ctx* c, gkr_matrix* m, const gkr_felt* root) {
+  if (!c || !m || !root) return fail(GKR_ERR_INVALID, "null argument");
+  if (m->ctx != c) return fail(GKR_ERR_INVALID, "matrix belongs to another (or a destroyed) context");
+  if (!felt_abi_canonical(*root)) return fail(GKR_ERR_INVALID, "commitment root not canonical");
+  m->root = *root;
+  m->have_root = true;
+  return GKR_OK;
 }
 
 extern "C" int gkr_mle_commitment(gkr_ctx* c, const gkr_qvec* evals, gkr_felt* root) {

@@ -156,10 +156,15 @@ struct gkr_matrix {
   int8_t* r8 = nullptr;
   uint64_t r8_nst = 0;
   int r8_state = 0;
+  // the weight commitment (Poseidon Merkle root of the column-major padded
+  // MLE, canonical words), once computed or supplied by the caller
+  bool have_root = false;
+  gkr_felt root;
 };
 
-// Drops the copies derived from m's contents (int8 copy, digit planes) and
-// a matmul claim computed over m; they are rebuilt on the next use.
+// Drops the copies derived from m's contents (int8 copy, digit planes, the
+// cached commitment root) and a matmul claim computed over m; they are
+// rebuilt on the next use.
 int drop_derived(gkr_ctx* c, gkr_matrix* m);
 
 struct gkr_qvec {

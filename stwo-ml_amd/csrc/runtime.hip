@@ -555,6 +555,7 @@ int drop_derived(gkr_ctx* c, gkr_matrix* m) {
   m->r8 = nullptr;
   m->r8_nst = 0;
   m->r8_state = 0;
+  m->have_root = false;
   return GKR_OK;
 }
 extern "C" int gkr_matrix_invalidate(gkr_ctx* c, gkr_matrix* m) {

@@ -177,6 +177,8 @@ SIGNATURES = [
     ("gkr_qvec_device_ptr", _P, [_P]),
     ("gkr_matrix_device_ptr", _P, [_P]),
     ("gkr_matrix_invalidate", C.c_int, [_P, _P]),
+    ("gkr_matrix_commitment_cached", C.c_int, [_P, _P, C.POINTER(C.c_int)]),
+    ("gkr_matrix_set_commitment", C.c_int, [_P, _P, _P]),
     ("gkr_prove_aggregated_binding", C.c_int, [_P, _P, _P, C.c_size_t, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("gkr_proof_num_binding_groups", C.c_size_t, [_P]),
     ("gkr_proof_binding_group", C.c_int, [_P, C.c_size_t, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
@@ -894,6 +896,17 @@ class Matrix:
         """gkr_matrix_invalidate: the entries changed outside the library (wrapped device memory
         written by the caller); the copies derived from them are rebuilt on the next use."""
         _check(lib().gkr_matrix_invalidate(self.ctx.handle, self._h))
+
+    def cached_commitment(self) -> Optional[int]:
+        """gkr_matrix_commitment_cached: the weight commitment kept on the matrix, or None."""
+        f = GkrFelt()
+        cached = C.c_int()
+        _check(lib().gkr_matrix_commitment_cached(self._h, C.byref(f), C.byref(cached)))
+        return felt_from_c(f) if cached.value else None
+
+    def set_commitment(self, root: int) -> None:
+        """gkr_matrix_set_commitment: keep `root` as this weight's commitment."""
+        _check(lib().gkr_matrix_set_commitment(self.ctx.handle, self._h, C.byref(felt_to_c(root))))
 
     @property
     def handle(self) -> int:

@@ -72,3 +72,34 @@ def test_explicit_zero_padding_gives_same_root(gpu_ctx, rows, cols):
     # a changed entry changes the root
     B[rows // 2, cols // 3] = (int(B[rows // 2, cols // 3]) + 1) % P
     assert gpu_ctx.weight_commitment(gpu_ctx.upload(B)) != ra
+
+
+def test_commitment_cache(gpu_ctx):
+    """The weight-commitment cache on resident matrices (the reference's WeightCommitmentCache,
+    weight_cache.rs:283-327): a computed root is kept on its matrix and returned again, a batch mixing
+    cached and uncached weights equals the uncached batch, a root seeded with set_commitment is
+    used as given, and invalidate / forward_into drop it."""
+    print("case commitment cache", flush=True)
+    rng = np.random.default_rng(21)
+    Bs = [rand_matrix(rng, 33, 20), rand_matrix(rng, 64, 64), rand_matrix(rng, 7, 300)]
+    ms = [gpu_ctx.upload(B) for B in Bs]
+    want = [O.weight_commitment(B) for B in Bs]
+    assert all(m.cached_commitment() is None for m in ms)
+    assert gpu_ctx.weight_commitment(ms[1]) == want[1]
+    assert ms[1].cached_commitment() == want[1] and ms[0].cached_commitment() is None
+    assert gpu_ctx.weight_commitments(ms) == want  # one cached, two computed
+    assert [m.cached_commitment() for m in ms] == want
+    assert gpu_ctx.weight_commitments(ms) == want  # all cached
+    # a root persisted elsewhere and seeded on a new handle of the same weight
+    again = gpu_ctx.upload(Bs[2])
+    again.set_commitment(want[2])
+    assert again.cached_commitment() == want[2] and gpu_ctx.weight_commitment(again) == want[2]
+    # the contents change: the root is dropped and the new one computed
+    ms[0].invalidate()
+    assert ms[0].cached_commitment() is None
+    assert gpu_ctx.weight_commitment(ms[0]) == want[0]
+    ident = gpu_ctx.upload(np.eye(64, dtype=np.uint32))
+    B2 = rand_matrix(rng, 64, 64)
+    gpu_ctx.matmul_forward_into(ident, gpu_ctx.upload(B2), ms[1])
+    assert ms[1].cached_commitment() is None
+    assert gpu_ctx.weight_commitment(ms[1]) == O.weight_commitment(B2)

@@ -177,3 +177,38 @@ def test_weight_binding_modes(gpu_ctx, mode):
         assert cd[n_before - 3:n_before - 3 + 4] == [3] + want and cd[-2] == 0
     else:
         assert cd[n_before - 3] == 0 and cd[-2] == 0
+
+
+@pytest.mark.parametrize("mode", [G.WEIGHT_AGGREGATED_RLC, G.WEIGHT_AGGREGATED_FULL])
+def test_weight_phase_with_cached_commitments(gpu_ctx, mode):
+    """Three proofs of the same MatMul layers and weight phase on the same resident weights: the
+    first computes the commitments, the second takes them from the matrices (the weight cache of
+    weight_cache.rs:283-327), the third recomputes them after invalidate.  All three proofs (and
+    binding groups) are identical, and the cached roots equal the oracle's."""
+    print(f"case weight phase with cached commitments, mode {mode}", flush=True)
+    rng = np.random.default_rng(12)
+    W1 = rng.integers(0, P, size=(24, 40), dtype=np.uint32)
+    W2 = rng.integers(0, P, size=(40, 9), dtype=np.uint32)
+    X = rng.integers(0, P, size=(3, 24), dtype=np.uint32)
+    x, w1, w2 = gpu_ctx.upload(X), gpu_ctx.upload(W1), gpu_ctx.upload(W2)
+    H = gpu_ctx.upload(O.matmul_forward(X, W1))
+
+    def prove():
+        ch = G.PoseidonChannel()
+        ch.mix_u64(4)
+        proof = G.Proof()
+        for a, b in [(H, w2), (x, w1), (x, w1)]:
+            r = ch.draw_qm31s(lg(a.rows) + lg(b.cols))
+            v = gpu_ctx.matmul_output_claim(a, b, r)
+            ch.mix_secure_field(v)
+            gpu_ctx.prove_matmul_layer(r, v, a, b, ch, proof)
+        gpu_ctx.prove_weight_binding(ch, proof, mode)
+        return proof.serialize(), proof.binding_groups(), ch.digest()
+
+    first = prove()
+    assert w1.cached_commitment() == O.weight_commitment(W1) and w2.cached_commitment() == O.weight_commitment(W2)
+    assert prove() == first
+    w1.invalidate()
+    w2.invalidate()
+    assert w1.cached_commitment() is None
+    assert prove() == first
