@@ -101,3 +101,29 @@ def test_handover_failure_leaves_context_usable(gpu_ctx, op, arg):
     v = gpu_ctx.matmul_output_claim(a, b, r)
     assert gpu_ctx.prove_matmul_layer(r, v, a, b, gch) == O.prove_matmul_layer(r, v, A, B, och)
     assert gch.digest() == och.digest()
+
+
+def test_bounded_wait_wall_clock(gpu_ctx):
+    """The wall-clock length of the device-side bounded wait (kWaitSpinLimit = 2^22 polls of the host
+    mailbox): hand-overs whose wait is cut to 2^12 and 2^15 polls expire before the host posts, and
+    the difference of the two failing calls' times gives the time per poll.  The full limit must
+    end well inside the host's own 60 s wait limit (so a waiting kernel always gives up first) and
+    last long enough (over 0.5 s) that a host thread descheduled for a moment does not lose the
+    proof."""
+    import time
+    log("case bounded wait wall clock")
+    n = 1 << 12
+    fa, fb = gpu_ctx.qvec_synthetic(n, 31), gpu_ctx.qvec_synthetic(n, 32)
+    times = {}
+    for spins in (1 << 12, 1 << 15):
+        gpu_ctx.debug(G.DEBUG_HANDOVER_EXPIRE, spins)
+        t0 = time.perf_counter()
+        with pytest.raises(G.GkrError):
+            gpu_ctx.sumcheck_product(fa, fb, G.PoseidonChannel())
+        times[spins] = time.perf_counter() - t0
+    per_poll = (times[1 << 15] - times[1 << 12]) / ((1 << 15) - (1 << 12))
+    full = per_poll * (1 << 22)
+    log(f"  {per_poll * 1e9:.0f} ns per poll; 2^22 polls = {full:.2f} s")
+    assert 0.5 < full < 30.0
+    ha, hb = O.synthetic_q(n, 31), O.synthetic_q(n, 32)
+    assert gpu_ctx.sumcheck_product(fa, fb, G.PoseidonChannel()) == O.sumcheck_product(ha, hb, O.Channel())
