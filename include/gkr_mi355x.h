@@ -108,7 +108,9 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * layers' row statistics and padded-vector kernels (device); 14 the LogUp-GKR
  * batch kernels (device); 15 host: round polynomials derived from a trip's
  * sums; 16 host: proof-record appends; 17 / 18 host: the walk's matmul /
- * activation steps, whole (wall-clock, bytes = 0). */
+ * activation steps, whole (wall-clock, bytes = 0); 19: walk steps proved a
+ * second time because a kernel's bounded wait for the host (about 5.5 s)
+ * expired (launches = the count, counted at every timing level). */
 /* level 0: off; 1: events on every 8th launch of restrict_cols (id 0; only
  * those launches are counted) and on every launch of ids 1, 9, 13 and 14,
  * plus the host timers; 2: events on every launch of every timed kernel (an
@@ -551,7 +553,10 @@ int gkr_prove_aggregated_binding(gkr_ctx* ctx, gkr_channel* ch, const gkr_bindin
  * with draw_qm31; a Mul, LayerNorm or RMSNorm draws its point (log2 of the
  * padded size), takes the MLE of its output there and mixes it.  On return
  * final_point/final_value hold the last input claim (final_point needs room
- * for 64 entries).                                                          */
+ * for 64 entries).  A step that fails because a kernel's bounded wait for the
+ * host expired (the host thread held up for about 5.5 s) is proved once more
+ * from the channel and claim it started from, giving the same proof (timer
+ * id 19 counts these).                                                      */
 enum { GKR_STEP_MATMUL = 0, GKR_STEP_MUL = 2, GKR_STEP_ACTIVATION = 3, GKR_STEP_LAYERNORM = 4, GKR_STEP_RMSNORM = 8 };
 enum { GKR_CLAIM_CHAINED = 0, GKR_CLAIM_FRESH = 1 };
 typedef struct {

@@ -102,7 +102,7 @@ enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_
                 K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
                 K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NORM = 13, K_LOOKUP = 14,
                 K_HOST_GRAM = 15, K_HOST_PROOF = 16, K_HOST_WALK_MM = 17, K_HOST_WALK_ACT = 18,
-                K_NKERNELS = 19 };
+                K_WALK_RETRY = 19, K_NKERNELS = 20 };
 constexpr int kMaxPartialBlocks = 1024;
 constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
 static_assert(kMaxPartialBlocks <= kCountedMaxRows && kCountedMaxRows % kBlock == 0,
@@ -233,6 +233,10 @@ struct gkr_ctx {
   // test hooks (gkr_ctx_debug), each consumed by the next hand-over
   bool debug_handover_cancel = false;  // the host leaves before posting the challenges
   uint32_t debug_handover_spins = 0;   // nonzero: the kernel's bounded wait, posted only after it expired
+  // set when a call failed because a kernel's bounded wait for the host gave
+  // up (the host fell more than the wait's length behind); the walk then
+  // proves the step again
+  bool wait_expired = false;
 };
 
 // ------------------------------------------------------------------ static scratch (allocation-free entry point)
@@ -402,8 +406,10 @@ static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_H
   std::chrono::steady_clock::time_point t0;
   // the flag only moves forward (mod 2^32): a later delivery implies this one
   for (uint64_t spins = 0; (int32_t)(*flag - seq) < 0; spins++) {
-    if (hand_mb && *expired == hand_mb)
+    if (hand_mb && *expired == hand_mb) {
+      c->wait_expired = true;
       return fail(GKR_ERR_DEVICE, "kernel launched ahead stopped waiting for its challenges (mailbox %u)", hand_mb);
+    }
     if ((spins & 0xFFFF) != 0xFFFF) continue;
     if (spins == 0xFFFF) t0 = std::chrono::steady_clock::now();
     TRY(check_launch(c));
@@ -641,8 +647,10 @@ inline int check_point_wait(gkr_ctx* c) {
   if (!c->point_mb) return GKR_OK;
   const uint32_t w = c->point_mb;
   c->point_mb = 0;
-  if (__atomic_load_n(&c->mailbox->expired, __ATOMIC_ACQUIRE) == w)
+  if (__atomic_load_n(&c->mailbox->expired, __ATOMIC_ACQUIRE) == w) {
+    c->wait_expired = true;
     return fail(GKR_ERR_DEVICE, "restriction launched ahead stopped waiting for its claim point (mailbox %u)", w);
+  }
   return GKR_OK;
 }
 // Drops a restriction launched ahead that will not be used: the cancel code

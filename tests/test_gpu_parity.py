@@ -453,6 +453,39 @@ def test_walk_cancel_with_restriction_launched_ahead(gpu_ctx):
     assert first == (och.digest(), ref)
 
 
+def test_walk_retries_a_step_whose_wait_expired(gpu_ctx):
+    """A walk step whose hand-over wait expires before the host posts (the test hook cuts the bounded
+    wait to 4 polls: a host held up longer than the wait) is proved again from the channel and
+    claim it started from: the walk succeeds with the same proof and transcript as an undisturbed
+    walk, and the retry is counted (timer id 19).  Steps: fresh MatMul (its hand-over expires, with
+    the next MatMul's restriction already launched ahead), MatMul, SiLU activation, chained MatMul."""
+    log("case walk retry after an expired wait")
+    A1, B1 = O.synthetic(4, 64, 1, 61), O.synthetic(64, 32, 1, 62)
+    A2, B2 = O.synthetic(4, 32, 1, 63), O.synthetic(32, 16, 1, 64)
+    X = O.synthetic(4, 16, 0, 65)
+    A3, B3 = O.synthetic(4, 8, 1, 66), O.synthetic(8, 16, 1, 67)
+    gs = [gpu_ctx.upload(M) for M in (A1, B1, A2, B2, X, A3, B3)]
+    F, Ch = G.CLAIM_FRESH, G.CLAIM_CHAINED
+    steps = [(G.STEP_MATMUL, F, gs[0], gs[1], 0, 0), (G.STEP_MATMUL, F, gs[2], gs[3], 0, 0),
+             (G.STEP_ACTIVATION, F, gs[4], None, 5, 10), (G.STEP_MATMUL, Ch, gs[5], gs[6], 0, 0)]
+
+    def run():
+        ch = G.PoseidonChannel()
+        ch.mix_u64(6)
+        proof = G.Proof()
+        fp, fv = G.prove_walk(gpu_ctx, ch, steps, proof)
+        proof.set_input_claim(fp, fv)
+        return ch.digest(), proof.serialize()
+
+    first = run()
+    gpu_ctx.reset_timing()
+    gpu_ctx.debug(G.DEBUG_HANDOVER_EXPIRE, 4)
+    assert run() == first
+    assert gpu_ctx.kernel_time(19)[1] == 1
+    assert run() == first
+    assert gpu_ctx.kernel_time(19)[1] == 1
+
+
 def test_walk_without_launcher_thread(gpu_ctx):
     """A context created with GKR_ASYNC_LAUNCH=0 (the calling thread issues every launch) proves
     the same fresh-claim walk, bit for bit, as the default context (launches issued by the
