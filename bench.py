@@ -87,6 +87,29 @@ def matmul_elems(cfg):
     return sum(k * n + mm * k for mm, k, n in shapes), shapes
 
 
+def restrict_launch_bytes(m, k, n, int8):
+    """Algorithmic bytes of one k_restrict_cols(8) launch over A (m x k) and B (k x n): B once (int8 copy:
+    1 byte an entry, u32: 4) and L_j's digits (16 per column) on the weight side; A (4 per entry), L_i
+    (16 per row) read and f_a (16 per padded column) written on the activation side."""
+    return (1 if int8 else 4) * k * n + 16 * n + 4 * m * k + 16 * m + 16 * (1 << lg(k))
+
+
+def restrict_by_shape(ctx, cfg, int8):
+    """The restriction's timed launches grouped by launch size, named by the model's matmul shapes that
+    share it: bytes, launches, average us and fraction of HBM peak per shape."""
+    names = {}
+    per_layer = list(zip(["q", "k", "v", "o", "gate", "up", "down"], matmul_elems(cfg)[1]))
+    for name, (m, k, n) in per_layer:
+        names.setdefault(restrict_launch_bytes(m, k, n, int8), []).append(f"{name} {k}x{n}")
+    out = []
+    for nb, ms, nl in ctx.kernel_time_by_size(K_RESTRICT_COLS):
+        us = ms / nl * 1e3
+        gbs = nb / (us * 1e-6) / 1e9
+        out.append({"shape": "/".join(names.get(nb, [f"{nb} bytes"])), "bytes": nb, "launches": nl,
+                    "avg_us": round(us, 3), "gbps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    return out
+
+
 CALL_TIME = {"matmul_claim": 0.0, "matmul_layer": 0.0, "activation_layer": 0.0, "walk": 0.0, "serialize": 0.0}
 
 
@@ -994,10 +1017,6 @@ def main():
     assert all(d == digests[0] for d in digests), "non-deterministic proof"
 
     kernels = {}
-    # at timing level 1 the restriction's events bracket every 8th launch
-    # (sampled_launches); its device time per step is the sampled mean times
-    # the matmuls per step
-    mm_per_step = 7 * n_layers if cfg is not None else 1
     for kid, name in [(K_RESTRICT_COLS, "restrict_cols"), (K_RESTRICT_ROWS, "restrict_rows"),
                       (K_MM_ROUND, "product_trip"), (K_EQ3_ROUND, "eq3_or_sum_trip"), (K_LOGUP_PREP, "logup_prepare"),
                       (K_EQ_TABLE, "eq_table")]:
@@ -1006,10 +1025,6 @@ def main():
             kernels[name] = {"launches": nl, "avg_us": round(ms / nl * 1e3, 3),
                              "gbps": round(nb / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
                              "ms_per_step": round(ms / args.steps, 3)}
-    if "restrict_cols" in kernels and not args.timing_all:
-        rk = kernels["restrict_cols"]
-        rk["sampled_launches"] = rk.pop("launches")
-        rk["ms_per_step"] = round(rk["avg_us"] * mm_per_step / 1e3, 3)
     host = {}
     for kid, name in [(K_HOST_FS, "fiat_shamir"), (K_HOST_WAIT, "device_wait"),
                       (K_HOST_WAIT_TAIL, "device_wait_handover"), (K_HOST_DRAW, "claim_draws"),
@@ -1030,7 +1045,9 @@ def main():
                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
                     "kernel": "k_restrict_cols" if args.u32_weights else "k_restrict_cols8",
                     "avg_launch_us": rc["avg_us"], "bytes_per_launch": nb // nl,
-                    "timed_launches": "every launch" if args.timing_all else "every 8th launch (HIP events)",
+                    "timed_launches": "every launch (start/end events carried in the kernel's dispatch)",
+                    "bytes_basis": "B as the int8 copy" if not args.u32_weights else "B as u32",
+                    "by_shape": restrict_by_shape(ctx, cfg, not args.u32_weights) if cfg is not None else None,
                     "traffic_source": f"profiles/{prof} (rocprofv3 PMC, qwen1)" if traffic else None}
 
     result = {

@@ -111,13 +111,20 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * activation steps, whole (wall-clock, bytes = 0); 19: walk steps proved a
  * second time because a kernel's bounded wait for the host (about 5.5 s)
  * expired (launches = the count, counted at every timing level). */
-/* level 0: off; 1: events on every 8th launch of restrict_cols (id 0; only
- * those launches are counted) and on every launch of ids 1, 9, 13 and 14,
- * plus the host timers; 2: events on every launch of every timed kernel (an
- * event pair per launch, each record a queue packet of its own that delays
+/* level 0: off; 1: every launch of ids 0, 1 and 4, timed by events carried in
+ * the kernel's own dispatch (hipExtLaunchKernel: nothing is added to the
+ * queue), every launch of ids 9, 13 and 14 between event records, plus the
+ * host timers; 2: every launch of every timed kernel (the multi-launch ones
+ * between event records, each record a queue packet of its own that delays
  * the next kernel by a few microseconds). */
 int gkr_ctx_set_timing(gkr_ctx* ctx, int level);
 int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);
+/* The same totals split by the bytes one launch moves (launches of one
+ * matrix shape share it), in increasing order of bytes: fills the first cap
+ * entries and sets *n to the number of distinct sizes.  No counterpart in
+ * the reference (benchmark instrumentation, as the totals above). */
+int gkr_ctx_kernel_time_by_size(gkr_ctx* ctx, int kernel_id, uint64_t* bytes, double* total_ms, uint64_t* launches,
+                                size_t cap, size_t* n);
 int gkr_ctx_reset_timing(gkr_ctx* ctx);
 /* Test hooks for the failure paths of the hand-over (no counterpart in the
  * reference).  Each applies to the next sumcheck hand-over on the context:

@@ -192,9 +192,9 @@ struct gkr_ctx {
   Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
   uint32_t seq = 0;            // last result sequence number handed out
   uint32_t mb_seq = 0;         // last mailbox sequence number handed out
-  int timing = 0;  // 0 off; 1: sampled events on the roofline kernels + host timers; 2: events on every timed kernel
-  uint64_t event_seq[32] = {};  // launches of each timed kernel id since the last reset (level-1 sampling)
+  int timing = 0;  // 0 off; 1: events on the single-launch kernels + host timers; 2: events on every timed kernel
   KernelStat stats[K_NKERNELS];
+  std::map<std::pair<int, uint64_t>, KernelStat> size_stats;  // per (timer id, bytes of one launch)
   std::vector<PendingTiming> pending;
   std::vector<hipEvent_t> free_events;
   MatMulCache mm;
@@ -219,6 +219,7 @@ struct gkr_ctx {
   bool noalloc = false;
   // launches go through this thread's ring (null: GKR_ASYNC_LAUNCH=0, issued by the caller's thread)
   std::unique_ptr<Launcher> launcher;
+  LaunchEvents armed;  // a TimedLaunch's events for the next launch (take_armed)
   // a matmul restriction launched ahead of its claim point (prelaunch_matmul):
   // k_point_wait waits for mailbox sequence `want`
   struct {
@@ -270,15 +271,20 @@ int ensure_host_mult(gkr_ctx* c, uint64_t n);
 // shared bytes, kernel arguments...).  The arguments are evaluated and
 // converted to the kernel's parameter types at this point; the launch itself
 // is issued by the context's launcher thread when it has one.
-#define GKR_LAUNCH(ctx, KERN_, GRID_, BLOCK_, SHMEM_, ...)                                        \
-  (void)launch_kernel((ctx)->launcher.get(), KERN_, dim3(GRID_), dim3(BLOCK_), (uint32_t)(SHMEM_), \
-                      (ctx)->stream, __VA_ARGS__)
+#define GKR_LAUNCH(ctx, KERN_, GRID_, BLOCK_, SHMEM_, ...)                                     \
+  (void)launch_kernel((ctx)->launcher.get(), take_armed(ctx), KERN_, dim3(GRID_), dim3(BLOCK_), \
+                      (uint32_t)(SHMEM_), (ctx)->stream, __VA_ARGS__)
+// The events a TimedLaunch armed for the next launch (consumed by it).
+inline LaunchEvents take_armed(gkr_ctx* c) {
+  const LaunchEvents ev = c->armed;
+  c->armed = LaunchEvents{};
+  return ev;
+}
 // Waits until every launch queued on the context has been issued.
 inline void drain(const gkr_ctx* c) {
   if (c && c->launcher) c->launcher->drain();
 }
 hipEvent_t get_event(gkr_ctx* c);
-constexpr uint64_t kEventSample = 8;
 // An event record in stream order (through the launcher when there is one).
 inline void record_event(gkr_ctx* c, hipEvent_t e) {
   hipStream_t s = c->stream;
@@ -287,30 +293,46 @@ inline void record_event(gkr_ctx* c, hipEvent_t e) {
   else
     (void)hipEventRecord(e, s);
 }
+// Times the launches of its scope for timer `kid`.  single: the scope makes
+// exactly one launch, which carries the events in its own dispatch
+// (hipExtLaunchKernel): no packet is added to the queue, so every launch is
+// timed at level 1.  Otherwise a pair of event records brackets the scope:
+// each record is a packet of its own, about 4 us between the kernels it
+// separates, so level 1 brackets those scopes only for kernels off the
+// walk's critical path (ids 1, 9, 13, 14).
 struct TimedLaunch {
   gkr_ctx* c;
   int kid;
   uint64_t bytes;
+  bool single;
   hipEvent_t e0 = nullptr, e1 = nullptr;
-  TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_) : c(c_), kid(kid_), bytes(bytes_) {
-    // level 1 brackets every kEventSample-th restriction launch (and every
-    // launch of the other level-1 kernels): each event record is a packet of
-    // its own in the queue, about 4 us between the kernels it separates, on
-    // the matmul's critical path
+  TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_, bool single_ = false)
+      : c(c_), kid(kid_), bytes(bytes_), single(single_) {
     bool on = c->timing >= 2;
-    if (c->timing == 1 && kid == K_RESTRICT_COLS) on = c->event_seq[kid]++ % kEventSample == 0;
-    if (c->timing == 1 && (kid == K_RESTRICT_ROWS || kid == K_MERKLE || kid == K_NORM || kid == K_LOOKUP)) on = true;
+    if (c->timing == 1 && (single || kid == K_RESTRICT_ROWS || kid == K_MERKLE || kid == K_NORM || kid == K_LOOKUP))
+      on = true;
     if (on) {
       e0 = get_event(c);
       e1 = get_event(c);
-      if (e0) record_event(c, e0);
+      if (!e0 || !e1) {
+        e0 = e1 = nullptr;
+      } else if (single) {
+        c->armed = LaunchEvents{e0, e1};
+      } else {
+        record_event(c, e0);
+      }
     }
   }
   ~TimedLaunch() {
-    if (e0 && e1) {
-      record_event(c, e1);
-      c->pending.push_back({kid, e0, e1, bytes});
+    if (!e0 || !e1) return;
+    if (single && c->armed.start == e0) {  // no launch took them (an error path)
+      c->armed = LaunchEvents{};
+      c->free_events.push_back(e0);
+      c->free_events.push_back(e1);
+      return;
     }
+    if (!single) record_event(c, e1);
+    c->pending.push_back({kid, e0, e1, bytes});
   }
 };
 struct HostTimer {
@@ -390,12 +412,22 @@ static int deliver_finish(gkr_ctx* c, const RoundSink& sk, unsigned nblocks, con
 }
 // Wait until result `seq` has been published and copy NQ values.  The wait
 // spins on the coherent flag and never blocks on the stream (a hand-over
-// kernel queued behind the result may be waiting for the host): from time to
-// time it queries the stream, so a device error, or a drained stream without
-// the result, is reported; after kWaitWallSeconds it gives up.  hand_mb != 0:
+// kernel queued behind the result may be waiting for the host): once it has
+// waited kWaitQuerySeconds it queries the stream, and again every
+// kWaitQuerySeconds, so a device error, or a drained stream without the
+// result, is reported; after kWaitWallSeconds it gives up.  hand_mb != 0:
 // the result comes from the hand-over waiting for mailbox sequence hand_mb,
 // whose expiry is reported at once.
+//
+// The query is kept off ordinary waits: a stream query puts a marker packet
+// behind the kernels already queued, and the command processor takes about
+// 5 us over it before the next kernel starts.  While the host waits for a
+// trip's sums, the queue already holds the next trip launched ahead, so a
+// query then delayed the following mailbox wait, and with it the trip after
+// (kernel trace: about 5 us before most eq-sumcheck mailbox waits, 1.4 ms per
+// 48-layer proof, when the stream was queried every 65536 spins).
 constexpr double kWaitWallSeconds = 60.0;
+constexpr double kWaitQuerySeconds = 0.002;
 template <int NQ>
 static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_HOST_WAIT_TAIL, int slot = 0,
                        uint32_t hand_mb = 0) {
@@ -403,15 +435,24 @@ static int wait_result(gkr_ctx* c, uint32_t seq, qm31* host_out, int timer = K_H
   HostTimer ht(c, timer);
   volatile uint32_t* flag = c->h_flag;
   volatile uint32_t* expired = &c->mailbox->expired;
-  std::chrono::steady_clock::time_point t0;
+  std::chrono::steady_clock::time_point t0, next_query;
   // the flag only moves forward (mod 2^32): a later delivery implies this one
   for (uint64_t spins = 0; (int32_t)(*flag - seq) < 0; spins++) {
     if (hand_mb && *expired == hand_mb) {
       c->wait_expired = true;
       return fail(GKR_ERR_DEVICE, "kernel launched ahead stopped waiting for its challenges (mailbox %u)", hand_mb);
     }
-    if ((spins & 0xFFFF) != 0xFFFF) continue;
-    if (spins == 0xFFFF) t0 = std::chrono::steady_clock::now();
+    if ((spins & 0xFFF) != 0xFFF) continue;
+    const auto now = std::chrono::steady_clock::now();
+    if (spins == 0xFFF) {
+      t0 = now;
+      next_query = now + std::chrono::duration_cast<std::chrono::steady_clock::duration>(
+                             std::chrono::duration<double>(kWaitQuerySeconds));
+      continue;
+    }
+    if (now < next_query) continue;
+    next_query = now + std::chrono::duration_cast<std::chrono::steady_clock::duration>(
+                           std::chrono::duration<double>(kWaitQuerySeconds));
     TRY(check_launch(c));
     // while launches are still being issued the stream has not drained
     const hipError_t e = c->launcher && !c->launcher->idle() ? hipErrorNotReady : hipStreamQuery(c->stream);

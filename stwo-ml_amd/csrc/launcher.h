@@ -19,6 +19,7 @@
 //
 // One producer per ring: the thread that calls the library on the context.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -144,17 +145,25 @@ class Launcher {
   }
 };
 
+// Start and stop events taken from the kernel's own dispatch
+// (hipExtLaunchKernel): timing without event-record packets between kernels.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
 // A kernel launch with its arguments converted to the kernel's parameter
-// types now, issued through l (or at once when l is null).
+// types now, issued through l (or at once when l is null); with ev set, the
+// kernel's start and end times go to those events.
 template <class... KArgs, class... Args>
-inline hipError_t launch_kernel(Launcher* l, void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem,
-                                hipStream_t stream, Args&&... args) {
+inline hipError_t launch_kernel(Launcher* l, LaunchEvents ev, void (*kernel)(KArgs...), dim3 grid, dim3 block,
+                                uint32_t shmem, hipStream_t stream, Args&&... args) {
   static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
-  auto issue = [kernel, grid, block, shmem, stream,
+  auto issue = [kernel, grid, block, shmem, stream, ev,
                 tup = std::tuple<std::decay_t<KArgs>...>(std::forward<Args>(args)...)]() mutable -> hipError_t {
     return std::apply(
         [&](auto&... a) -> hipError_t {
           void* argv[] = {(void*)&a..., nullptr};
+          if (ev.start || ev.stop)
+            return hipExtLaunchKernel((const void*)kernel, grid, block, argv, shmem, stream, ev.start, ev.stop, 0);
           return hipLaunchKernel((const void*)kernel, grid, block, argv, shmem, stream);
         },
         tup);

@@ -351,7 +351,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
       const unsigned grid = partial_grid(n);
       TRY(deliver_args(c, grid, &counter, &base));
       // algorithmic bytes: the input, masked input and output written (8 per entry), d and w written
-      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 8 * n + 32 * n);
+      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 8 * n + 32 * n, true);
       GKR_LAUNCH(c, k_logup_prepare, dim3(grid), dim3(kBlock), 0, input->dev, input->rows,
                          input->cols, log2_exact(pcol), n, d_table, d_inv, mask, gamma, beta, eq_hi, eq_lo, eq_h,
                          d_min, d_mout, d_d0, d_w0, lds_hist ? nullptr : d_mult, sk_prep, counter, base);

@@ -195,14 +195,14 @@ static int restrict_pair(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, c
   RowsJob rows{A->dev, m, k, pk, Li, fa};
   if (p.use8) {
     // algorithmic bytes: B as int8 and L_j's digits (weight side), A and L_i (activation side), f_a written
-    TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
+    TimedLaunch t(c, K_RESTRICT_COLS, k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk), true);
     GKR_LAUNCH(c, k_restrict_cols8, dim3((unsigned)(p.act_blocks + p.ngroups * p.gc)), dim3(kBlock), 0,
                (const u32x4*)B->r8, k, p.nst, (const u32x4*)ldig, (uint32_t)p.chunk, (uint32_t*)part, rows,
                (uint32_t)p.act_blocks, (uint32_t)p.ngroups);
     TRY(check_launch(c));
   } else {
     // algorithmic bytes: B and L_j (weight side) plus A and L_i (activation side), f_a written
-    TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk));
+    TimedLaunch t(c, K_RESTRICT_COLS, 4 * k * n + 16 * n + (weight_only ? 0 : 4 * m * k + 16 * m + 16 * pk), true);
     const dim3 grid((unsigned)(p.act_blocks + p.gr * p.gc));
     if (n % 4 == 0 && ((uintptr_t)B->dev & 15) == 0)
       GKR_LAUNCH(c, k_restrict_cols<true>, grid, dim3(kBlock), 0, B->dev, k, n, p.chunk, Lj, (uint32_t*)part, rows,
@@ -732,7 +732,7 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
     TRY(ensureT(c, S_LI, a->rows, &Li));
     TRY(ensureT(c, S_FA0, pk, &fa));
     // algorithmic bytes: the blocks' activations, L_i, f_a written
-    TimedLaunch t(c, K_RESTRICT_ROWS, 4ull * n_blocks * a->rows * a->cols + 16 * a->rows + 16 * pk);
+    TimedLaunch t(c, K_RESTRICT_ROWS, 4ull * n_blocks * a->rows * a->cols + 16 * a->rows + 16 * pk, true);
     GKR_LAUNCH(c, k_restrict_rows_simd, dim3((unsigned)((pk + 63) / 64)), dim3(kSimdWaves * 64), 0, blk,
                        a->rows, a->cols, pk, (const qm31*)Li, fa);
     TRY(check_launch(c));

@@ -78,6 +78,10 @@ void collect_timing(gkr_ctx* c) {
       c->stats[p.kid].ms += ms;
       c->stats[p.kid].launches++;
       c->stats[p.kid].bytes += p.bytes;
+      KernelStat& z = c->size_stats[{p.kid, p.bytes}];
+      z.ms += ms;
+      z.launches++;
+      z.bytes += p.bytes;
     }
     c->free_events.push_back(p.e0);
     c->free_events.push_back(p.e1);
@@ -469,11 +473,29 @@ extern "C" int gkr_ctx_kernel_time(gkr_ctx* c, int kid, double* total_ms, uint64
   if (bytes) *bytes = c->stats[kid].bytes;
   return GKR_OK;
 }
+extern "C" int gkr_ctx_kernel_time_by_size(gkr_ctx* c, int kid, uint64_t* bytes, double* total_ms,
+                                           uint64_t* launches, size_t cap, size_t* n) {
+  if (!c || kid < 0 || kid >= K_NKERNELS || !n || (cap && (!bytes || !total_ms || !launches)))
+    return fail(GKR_ERR_INVALID, "bad ctx, kernel id or output");
+  TRY(sync(c));
+  size_t k = 0;
+  for (const auto& e : c->size_stats) {  // ordered by (id, bytes)
+    if (e.first.first != kid) continue;
+    if (k < cap) {
+      bytes[k] = e.first.second;
+      total_ms[k] = e.second.ms;
+      launches[k] = e.second.launches;
+    }
+    k++;
+  }
+  *n = k;
+  return GKR_OK;
+}
 extern "C" int gkr_ctx_reset_timing(gkr_ctx* c) {
   if (!c) return fail(GKR_ERR_INVALID, "null ctx");
   TRY(sync(c));
   for (auto& s : c->stats) s = KernelStat();
-  for (auto& e : c->event_seq) e = 0;
+  c->size_stats.clear();
   return GKR_OK;
 }
 

@@ -139,6 +139,8 @@ SIGNATURES = [
     ("gkr_ctx_set_timing", C.c_int, [_P, C.c_int]),
     ("gkr_ctx_kernel_time", C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_uint64),
                                       C.POINTER(C.c_uint64)]),
+    ("gkr_ctx_kernel_time_by_size", C.c_int, [_P, C.c_int, C.POINTER(C.c_uint64), C.POINTER(C.c_double),
+                                              C.POINTER(C.c_uint64), C.c_size_t, C.POINTER(C.c_size_t)]),
     ("gkr_ctx_reset_timing", C.c_int, [_P]),
     ("gkr_ctx_debug", C.c_int, [_P, C.c_int, C.c_uint64]),
     ("gkr_matrix_upload", C.c_int, [_P, _U32P, C.c_uint64, C.c_uint64, C.POINTER(_P)]),
@@ -412,6 +414,15 @@ class Context:
         ms, n, b = C.c_double(), C.c_uint64(), C.c_uint64()
         _check(lib().gkr_ctx_kernel_time(self._h, kid, C.byref(ms), C.byref(n), C.byref(b)))
         return ms.value, n.value, b.value
+
+    def kernel_time_by_size(self, kid: int) -> List[Tuple[int, float, int]]:
+        """[(bytes of one launch, total ms, launches)] per distinct launch size, smallest first."""
+        n = C.c_size_t()
+        _check(lib().gkr_ctx_kernel_time_by_size(self._h, kid, None, None, None, 0, C.byref(n)))
+        k = n.value
+        b, ms, nl = (C.c_uint64 * max(k, 1))(), (C.c_double * max(k, 1))(), (C.c_uint64 * max(k, 1))()
+        _check(lib().gkr_ctx_kernel_time_by_size(self._h, kid, b, ms, nl, k, C.byref(n)))
+        return [(b[i], ms[i], nl[i]) for i in range(min(k, n.value))]
 
     def bench_copy(self, nbytes: int = 1 << 32, iters: int = 5) -> Tuple[float, float]:
         """(copy GB/s counting read + write, read-only GB/s) of plain 128-bit streaming kernels."""
