@@ -111,12 +111,12 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * activation steps, whole (wall-clock, bytes = 0); 19: walk steps proved a
  * second time because a kernel's bounded wait for the host (about 5.5 s)
  * expired (launches = the count, counted at every timing level). */
-/* level 0: off; 1: every launch of ids 0, 1 and 4, timed by events carried in
- * the kernel's own dispatch (hipExtLaunchKernel: nothing is added to the
- * queue), every launch of ids 9, 13 and 14 between event records, plus the
- * host timers; 2: every launch of every timed kernel (the multi-launch ones
- * between event records, each record a queue packet of its own that delays
- * the next kernel by a few microseconds). */
+/* level 0: off; 1: every 8th launch of ids 0 and 4 (the walk's critical
+ * path: a timed dispatch waits about 4 us for its events on each side) and
+ * every launch of ids 1, 9, 13 and 14, plus the host timers; 2: every launch
+ * of every timed kernel.  One-launch scopes (ids 0, 1, 4) carry their events
+ * in the kernel's own dispatch (hipExtLaunchKernel); the others are
+ * bracketed by event records. */
 int gkr_ctx_set_timing(gkr_ctx* ctx, int level);
 int gkr_ctx_kernel_time(gkr_ctx* ctx, int kernel_id, double* total_ms, uint64_t* launches, uint64_t* bytes);
 /* The same totals split by the bytes one launch moves (launches of one

@@ -192,7 +192,8 @@ struct gkr_ctx {
   Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
   uint32_t seq = 0;            // last result sequence number handed out
   uint32_t mb_seq = 0;         // last mailbox sequence number handed out
-  int timing = 0;  // 0 off; 1: events on the single-launch kernels + host timers; 2: events on every timed kernel
+  int timing = 0;  // 0 off; 1: sampled events on the critical-path kernels + host timers; 2: events on every timed kernel
+  uint64_t event_seq[K_NKERNELS] = {};  // launches of each timer id since the last reset (level-1 sampling)
   KernelStat stats[K_NKERNELS];
   std::map<std::pair<int, uint64_t>, KernelStat> size_stats;  // per (timer id, bytes of one launch)
   std::vector<PendingTiming> pending;
@@ -293,13 +294,16 @@ inline void record_event(gkr_ctx* c, hipEvent_t e) {
   else
     (void)hipEventRecord(e, s);
 }
-// Times the launches of its scope for timer `kid`.  single: the scope makes
-// exactly one launch, which carries the events in its own dispatch
-// (hipExtLaunchKernel): no packet is added to the queue, so every launch is
-// timed at level 1.  Otherwise a pair of event records brackets the scope:
-// each record is a packet of its own, about 4 us between the kernels it
-// separates, so level 1 brackets those scopes only for kernels off the
-// walk's critical path (ids 1, 9, 13, 14).
+// Times the launches of its scope for timer `kid`.  Timing a dispatch costs
+// the queue about 4 us next to each neighbouring kernel (kernel trace of the
+// 48-layer walk: 3.9-4.0 us gaps on both sides of every timed dispatch,
+// whether its events are records or carried in the dispatch), so level 1
+// times every kEventSample-th launch of the kernels on the walk's critical
+// path (ids 0 and 4) and every launch of ids 1, 9, 13 and 14.
+// single: the scope makes exactly one launch, which carries the events in
+// its own dispatch (hipExtLaunchKernel); otherwise a pair of event records
+// brackets the scope.
+constexpr uint64_t kEventSample = 8;
 struct TimedLaunch {
   gkr_ctx* c;
   int kid;
@@ -309,8 +313,12 @@ struct TimedLaunch {
   TimedLaunch(gkr_ctx* c_, int kid_, uint64_t bytes_, bool single_ = false)
       : c(c_), kid(kid_), bytes(bytes_), single(single_) {
     bool on = c->timing >= 2;
-    if (c->timing == 1 && (single || kid == K_RESTRICT_ROWS || kid == K_MERKLE || kid == K_NORM || kid == K_LOOKUP))
-      on = true;
+    if (c->timing == 1) {
+      if (kid == K_RESTRICT_COLS || kid == K_LOGUP_PREP)
+        on = c->event_seq[kid]++ % kEventSample == 0;
+      else if (kid == K_RESTRICT_ROWS || kid == K_MERKLE || kid == K_NORM || kid == K_LOOKUP)
+        on = true;
+    }
     if (on) {
       e0 = get_event(c);
       e1 = get_event(c);

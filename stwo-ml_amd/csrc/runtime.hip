@@ -496,6 +496,7 @@ extern "C" int gkr_ctx_reset_timing(gkr_ctx* c) {
   TRY(sync(c));
   for (auto& s : c->stats) s = KernelStat();
   c->size_stats.clear();
+  for (auto& e : c->event_seq) e = 0;
   return GKR_OK;
 }
 
