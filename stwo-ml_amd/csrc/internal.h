@@ -804,6 +804,11 @@ struct Eq3Plan {
   std::vector<Trip> trips;
   std::vector<uint32_t> hi_off, lo_off;  // per trip, offsets into S_EQPARTS
   std::vector<int> h;                    // per trip, variables in the lower table
+  // with_split: eq(z, .) as the product of a table over z[0, nv - split_h)
+  // and one over z[nv - split_h, nv) (split_h = nv / 2, as eq_split), offsets
+  // into S_EQPARTS
+  int split_h = 0;
+  uint32_t split_hi_off = 0, split_lo_off = 0;
 };
 
 // A new matrix handle (owned: freed with the handle).
@@ -829,7 +834,7 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
                             gkr_qm31* round_polys, gkr_qm31* challenges, gkr_qm31* final_a, gkr_qm31* final_b,
                             const qm31* scale3 = nullptr, const FirstTrip* ft = nullptr);
 // Eq-weighted degree-3 sumcheck sum_x eq(z, x) w(x) d(x) (logup.hip): plan and eq tables,
-int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl);
+int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl, bool with_split = false);
 // one trip,
 int eq3_launch_trip(gkr_ctx* c, const Eq3Plan& pl, size_t j, const qm31* w, const qm31* d, int np,
                            const qm31* pend, qm31* dw, qm31* dd, int slot, RoundSink* sk,

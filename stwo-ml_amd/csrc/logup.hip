@@ -52,14 +52,15 @@ static int device_table(gkr_ctx* c, uint32_t tag, uint32_t log_size, uint32_t** 
 // final values equal those of folding eq like w and d (the polynomial of each
 // round is unique).
 // Plan the trips of an eq-sumcheck over 2^nv entries for claim point z and
-// launch the kernel that builds their eq tables (S_EQPARTS).
-int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
+// launch the kernel that builds their eq tables (S_EQPARTS); with_split, the
+// same launch builds the two halves of eq(z, .) (Eq3Plan::split_*).
+int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl, bool with_split) {
   pl->nv = nv;
   pl->trips = plan_trips(nv, kHostTailEq3, trip_k(1ull << nv));
   pl->hi_off.clear();
   pl->lo_off.clear();
   pl->h.clear();
-  if (pl->trips.empty()) return GKR_OK;
+  if (pl->trips.empty() && !with_split) return GKR_OK;
   EqPartsArg arg;
   memset(&arg, 0, sizeof arg);
   arg.z = make_point(z, nv);
@@ -81,6 +82,12 @@ int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl) {
     pl->hi_off.push_back(table(tr.t + tr.K, m - h));
     pl->lo_off.push_back(table(nv - h, h));
     pl->h.push_back(h);
+  }
+  if (with_split) {
+    if (arg.count + 2 > kEqPartsMax) return fail(GKR_ERR_DEVICE, "too many eq tables");
+    pl->split_h = nv / 2;
+    pl->split_hi_off = table(0, nv - pl->split_h);
+    pl->split_lo_off = table(nv - pl->split_h, pl->split_h);
   }
   HostTimer ht(c, K_HOST_LAUNCH);
   qm31* parts;
@@ -309,15 +316,15 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     if (c->mult_zero_entries < tsize) HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
     c->mult_zero_entries = 0;
   }
-  // eq(claim point, x) as the product of its high and low tables: the input
-  // MLE at the claim point is accumulated by the prepare pass
-  qm31 *eq_hi, *eq_lo;
-  int eq_h;
-  TRY(eq_split(c, cpt.data(), nv, &eq_hi, &eq_lo, &eq_h));
-  // the eq tables of the eq-sumcheck trips (the claim point only): built while
-  // the host draws gamma and beta
+  // One launch builds the eq tables of the eq-sumcheck trips and eq(claim
+  // point, x) as the product of its high and low halves (for the input MLE at
+  // the claim point, accumulated by the prepare pass): the claim point only,
+  // so it runs while the host draws gamma and beta
   Eq3Plan epl;
-  TRY(eq3_prepare(c, cpt.data(), nv, &epl));
+  TRY(eq3_prepare(c, cpt.data(), nv, &epl, true));
+  const qm31* eq_hi = (const qm31*)c->buf[S_EQPARTS] + epl.split_hi_off;
+  const qm31* eq_lo = (const qm31*)c->buf[S_EQPARTS] + epl.split_lo_off;
+  const int eq_h = epl.split_h;
 
   // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
   C.mix_u64(0x4C4F47ull);
