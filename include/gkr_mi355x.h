@@ -133,8 +133,10 @@ int gkr_ctx_reset_timing(gkr_ctx* ctx);
  *     kernel ends on the cancel code;
  *   GKR_DEBUG_HANDOVER_EXPIRE: the kernel's bounded wait is `arg` polls and
  *     the host posts only after it expired; the call fails with GKR_ERR_DEVICE.
+ *   GKR_DEBUG_TRIP_EXPIRE: the same for the next sumcheck trip launched ahead
+ *     of its challenges (that trip's wait expires).
  * Every kernel exits normally and the context stays usable.                 */
-enum { GKR_DEBUG_HANDOVER_CANCEL = 1, GKR_DEBUG_HANDOVER_EXPIRE = 2 };
+enum { GKR_DEBUG_HANDOVER_CANCEL = 1, GKR_DEBUG_HANDOVER_EXPIRE = 2, GKR_DEBUG_TRIP_EXPIRE = 3 };
 int gkr_ctx_debug(gkr_ctx* ctx, int op, uint64_t arg);
 
 /* ------------------------------------------------------------------ resident matrices

@@ -232,9 +232,10 @@ struct gkr_ctx {
   uint32_t point_mb = 0;  // the posted point's sequence, until the first trip's results confirm it arrived
   // set by the walk for one step: called at that step's last launch
   std::function<int()> prelaunch;
-  // test hooks (gkr_ctx_debug), each consumed by the next hand-over
+  // test hooks (gkr_ctx_debug), each consumed by the next hand-over (or trip launched ahead)
   bool debug_handover_cancel = false;  // the host leaves before posting the challenges
   uint32_t debug_handover_spins = 0;   // nonzero: the kernel's bounded wait, posted only after it expired
+  uint32_t debug_trip_spins = 0;       // the same for the next trip launched ahead of its challenges
   // set when a call failed because a kernel's bounded wait for the host gave
   // up (the host fell more than the wait's length behind); the walk then
   // proves the step again
@@ -646,6 +647,7 @@ int wait_trip(gkr_ctx* c, const RoundSink& sk, int nq, qm31* out, uint32_t want 
 struct AheadTrips {
   gkr_ctx* c;
   int outstanding = 0;
+  uint32_t hold_want = 0;  // test hook (gkr_ctx_debug): this wait is posted only after it expired
   explicit AheadTrips(gkr_ctx* c_) : c(c_) {}
   bool enabled() const { return !c->noalloc; }
   int make(TripWait* tw) {
@@ -659,12 +661,24 @@ struct AheadTrips {
     tw->mb = c->mailbox;
     tw->want = alloc_seq(&c->mb_seq, 1);
     tw->spin_limit = kWaitSpinLimit;
+    if (c->debug_trip_spins) {  // test hook: a short bounded wait that expires before the post
+      tw->spin_limit = c->debug_trip_spins;
+      c->debug_trip_spins = 0;
+      hold_want = tw->want;
+    }
     tw->status = words;
     tw->chal = reinterpret_cast<qm31*>(words + 4);
     outstanding++;
     return GKR_OK;
   }
   int post(const TripWait& tw, const qm31* chal, int np) {
+    if (tw.want == hold_want) {
+      const auto t0 = std::chrono::steady_clock::now();
+      volatile uint32_t* expired = &c->mailbox->expired;
+      while (*expired != tw.want &&
+             std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() < 10.0) {
+      }
+    }
     post_mailbox(c, tw.want, chal, np);
     outstanding--;
     return GKR_OK;

@@ -451,6 +451,10 @@ extern "C" int gkr_ctx_debug(gkr_ctx* c, int op, uint64_t arg) {
       if (arg == 0 || arg > kWaitSpinLimit) return fail(GKR_ERR_INVALID, "spin limit %llu", (unsigned long long)arg);
       c->debug_handover_spins = (uint32_t)arg;
       return GKR_OK;
+    case GKR_DEBUG_TRIP_EXPIRE:
+      if (arg == 0 || arg > kWaitSpinLimit) return fail(GKR_ERR_INVALID, "spin limit %llu", (unsigned long long)arg);
+      c->debug_trip_spins = (uint32_t)arg;
+      return GKR_OK;
     default: return fail(GKR_ERR_INVALID, "unknown debug op %d", op);
   }
 }

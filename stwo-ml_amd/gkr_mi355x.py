@@ -220,7 +220,7 @@ SIGNATURES = [
     ("gkr_prove_weight_binding", C.c_int, [_P, _P, _P, C.c_int]),
 ]
 WEIGHT_SEQUENTIAL, WEIGHT_AGGREGATED_RLC, WEIGHT_RLC_DIRECT, WEIGHT_AGGREGATED_FULL = 0, 1, 2, 3
-DEBUG_HANDOVER_CANCEL, DEBUG_HANDOVER_EXPIRE = 1, 2
+DEBUG_HANDOVER_CANCEL, DEBUG_HANDOVER_EXPIRE, DEBUG_TRIP_EXPIRE = 1, 2, 3
 
 
 def lib() -> C.CDLL:
@@ -407,7 +407,8 @@ class Context:
         _check(lib().gkr_ctx_reset_timing(self._h))
 
     def debug(self, op: int, arg: int = 0) -> None:
-        """Test hook for the hand-over failure paths (DEBUG_HANDOVER_CANCEL / DEBUG_HANDOVER_EXPIRE)."""
+        """Test hook for the failure paths of the device waits (DEBUG_HANDOVER_CANCEL / DEBUG_HANDOVER_EXPIRE /
+        DEBUG_TRIP_EXPIRE)."""
         _check(lib().gkr_ctx_debug(self._h, op, arg))
 
     def kernel_time(self, kid: int) -> Tuple[float, int, int]:

@@ -486,6 +486,40 @@ def test_walk_retries_a_step_whose_wait_expired(gpu_ctx):
     assert gpu_ctx.kernel_time(19)[1] == 1
 
 
+def _trip_walk(ctx, mats):
+    """Fresh MatMul (k = 4096: its second trip is launched ahead), SiLU LogUp over 2^16 entries (eq and
+    multiplicity trips launched ahead), MatMul; returns (digest, serialized proof)."""
+    gs = [ctx.upload(M) for M in mats]
+    F = G.CLAIM_FRESH
+    steps = [(G.STEP_MATMUL, F, gs[0], gs[1], 0, 0), (G.STEP_ACTIVATION, F, gs[2], None, 5, 16),
+             (G.STEP_MATMUL, F, gs[3], gs[4], 0, 0)]
+    ch = G.PoseidonChannel()
+    ch.mix_u64(12)
+    proof = G.Proof()
+    fp, fv = G.prove_walk(ctx, ch, steps, proof)
+    proof.set_input_claim(fp, fv)
+    return ch.digest(), proof.serialize()
+
+
+TRIP_MATS = [O.synthetic(4, 4096, 1, 71), O.synthetic(4096, 16, 1, 72), O.synthetic(64, 1024, 0, 73),
+             O.synthetic(8, 2048, 1, 74), O.synthetic(2048, 64, 1, 75)]
+
+
+def test_walk_retries_a_step_whose_trip_wait_expired(gpu_ctx):
+    """The first trip launched ahead in a walk (the MatMul's second trip, behind k_mailbox_wait) stops
+    waiting after 4 polls, before the host posts its challenges (test hook): the step is proved
+    again and the walk gives the same proof as an undisturbed one; the retry is counted (timer id
+    19), and the next walk runs undisturbed."""
+    log("case walk retry after an expired trip wait")
+    first = _trip_walk(gpu_ctx, TRIP_MATS)
+    gpu_ctx.reset_timing()
+    gpu_ctx.debug(G.DEBUG_TRIP_EXPIRE, 4)
+    assert _trip_walk(gpu_ctx, TRIP_MATS) == first
+    assert gpu_ctx.kernel_time(19)[1] == 1
+    assert _trip_walk(gpu_ctx, TRIP_MATS) == first
+    assert gpu_ctx.kernel_time(19)[1] == 1
+
+
 def test_walk_without_launcher_thread(gpu_ctx):
     """A context created with GKR_ASYNC_LAUNCH=0 (the calling thread issues every launch) proves
     the same fresh-claim walk, bit for bit, as the default context (launches issued by the
