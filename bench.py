@@ -137,8 +137,9 @@ def prove_logup(ctx, ch, x, tag, tlog, proof):
 class SerialBuffer:
     """Reused output buffer for the serialized proof (felt252 calldata)."""
 
-    def __init__(self):
+    def __init__(self, stream=True):
         self.buf, self.cap, self.n = None, 0, 0
+        self.stream = stream
 
     def serialize(self, proof) -> int:
         n = C.c_size_t()
@@ -150,6 +151,12 @@ class SerialBuffer:
         G._check(rc)
         self.n = n.value
         return self.n
+
+    def attach(self, proof) -> None:
+        """Once the buffer exists: the proof's layers are written into it while the walk proves
+        (gkr_proof_stream_to), so serialize() then writes only the layer count and the tail."""
+        if self.stream and self.buf is not None:
+            G._check(G.lib().gkr_proof_stream_to(proof.handle, self.buf, self.cap))
 
     def fingerprint(self) -> str:
         view = (C.c_uint8 * (32 * self.n)).from_address(C.addressof(self.buf))
@@ -197,6 +204,7 @@ def prove_model_walk(ctx, steps, seed, sbuf):
     ch = G.PoseidonChannel()
     ch.mix_u64(seed)
     proof = G.Proof()
+    sbuf.attach(proof)
     t0 = time.perf_counter()
     G.prove_walk(ctx, ch, arr, proof, n_steps=n)
     t1 = time.perf_counter()

@@ -205,6 +205,15 @@ int gkr_proof_set_io_commitment(gkr_proof* p, const gkr_felt* c);
  * not produced by this library) and the IO commitment.  Writes up to `cap`
  * felts; *n_out receives the full length (GKR_ERR_BUFFER when cap is short). */
 int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out);
+/* Serialization while proving (no counterpart in the reference, which
+ * serializes the finished proof): from this call on, a thread of the proof
+ * writes each layer record, as the reducers append it, into out (the layout
+ * gkr_proof_serialize writes, layer 0 at felt 1).  gkr_proof_serialize with
+ * the same out and cap then writes only the layer count and the tail; with
+ * another buffer, or when a layer did not fit in cap, it writes everything
+ * itself, as without streaming.  out must stay valid until the proof is
+ * freed, serialized or streamed elsewhere; out == NULL ends the streaming.   */
+int gkr_proof_stream_to(gkr_proof* p, gkr_felt* out, size_t cap);
 
 /* GKR driver seeding (gkr/prover.rs:1527-1560): mix_u64(num_layers),
  * mix_u64(in_rows), mix_u64(in_cols), then mix_felt(policy_commitment) when

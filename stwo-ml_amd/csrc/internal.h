@@ -11,6 +11,7 @@
 #include <string.h>
 
 #include <chrono>
+#include <deque>
 
 #include <map>
 #include <memory>
@@ -781,8 +782,14 @@ struct WeightClaimRec {
   std::vector<qm31> point;
   qm31 value;
 };
+// Serialization of a proof's layers while the proof is built
+// (gkr_proof_stream_to); defined with the serializer.
+struct ProofStream;
 struct gkr_proof {
-  std::vector<LayerRec> layers;
+  gkr_proof();
+  ~gkr_proof();
+  // a deque: appending keeps earlier records in place (the stream's thread reads them)
+  std::deque<LayerRec> layers;
   std::vector<qm31> in_point;
   qm31 in_value = {0, 0, 0, 0};
   std::vector<felt> weight_commitments;
@@ -790,7 +797,12 @@ struct gkr_proof {
   std::vector<std::vector<felt>> weight_openings;  // serialized opening records (claim + MleOpeningProof)
   std::vector<std::vector<gkr_felt>> binding_groups;  // serialized aggregated binding proofs
   felt io_commitment = {{0, 0, 0, 0}};
+  std::unique_ptr<ProofStream> stream;
 };
+// Appends a layer record (and hands it to the proof's stream, if any).
+void proof_add_layer(gkr_proof* p, LayerRec&& L);
+// Drops the records after the first n (a walk step proved again).
+void proof_truncate(gkr_proof* p, size_t n);
 
 // ------------------------------------------------------------------ provided by one unit to the others
 // The last rounds of each sumcheck run on the host once the vectors are this

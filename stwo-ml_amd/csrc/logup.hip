@@ -583,7 +583,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     for (uint32_t t = 0; t < 2 * table_log; t++) L.mult_rp.push_back(Q(out->mult_round_polys[t]));
     L.mult_final = mfin[0];
     L.mult_sum = mult_sum;
-    proof->layers.push_back(std::move(L));
+    proof_add_layer(proof, std::move(L));
   }
   return GKR_OK;
 }

@@ -642,7 +642,7 @@ static int prove_matmul_impl(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n
     for (int t = 0; t < 3 * T; t++) L.rp.push_back(Q(round_polys[t]));
     L.final_a = Q(*final_a);
     L.final_b = Q(*final_b);
-    proof->layers.push_back(std::move(L));
+    proof_add_layer(proof, std::move(L));
     WeightClaimRec w;
     w.b = b;
     for (uint32_t l = 0; l < log_n; l++) w.point.push_back(Q(claim_point[log_m + l]));
@@ -773,7 +773,7 @@ extern "C" int gkr_prove_matmul_layer_simd(gkr_ctx* c, const gkr_qm31* claim_poi
     for (int t = 0; t < 3 * T; t++) L.rp.push_back(Q(round_polys[t]));
     L.final_a = Q(*final_a);
     L.final_b = Q(*final_b);
-    proof->layers.push_back(std::move(L));
+    proof_add_layer(proof, std::move(L));
     WeightClaimRec w;
     w.b = b;
     for (uint32_t l = 0; l < log_n; l++) w.point.push_back(Q(claim_point[log_m + l]));
@@ -970,7 +970,7 @@ extern "C" int gkr_prove_matmul_layer_dual_simd(gkr_ctx* c, const gkr_qm31* clai
     for (int t = 0; t < 4 * (nbv + T); t++) L.rp.push_back(Q(round_polys[t]));
     L.final_a = Q(*final_a);
     L.final_b = Q(*final_b);
-    proof->layers.push_back(L);
+    proof_add_layer(proof, LayerRec(L));
   }
   return GKR_OK;
 }

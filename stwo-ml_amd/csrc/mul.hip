@@ -40,7 +40,7 @@ static int mul_layer_core(gkr_ctx* c, const std::vector<qm31>& cpt, const qm31& 
     for (size_t i = 0; i < L.rp.size(); i++) L.rp[i] = Q(out->eq_round_polys[i]);
     L.final_a = lhs;
     L.final_b = rhs;
-    proof->layers.push_back(std::move(L));
+    proof_add_layer(proof, std::move(L));
   }
   return GKR_OK;
 }

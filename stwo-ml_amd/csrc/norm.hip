@@ -505,7 +505,7 @@ void record_norm(gkr_proof* proof, bool ln, const qm31& claim, const NormShape& 
   N.table_commitment = felt_canon_from_words(o->table_commitment.w);
   N.rows0.assign(o->row_stats0, o->row_stats0 + o->n_rows);
   N.rows1.assign(o->row_stats1, o->row_stats1 + o->n_rows);
-  proof->layers.push_back(std::move(L));
+  proof_add_layer(proof, std::move(L));
 }
 
 }  // namespace

@@ -2,8 +2,12 @@
 #include "internal.h"
 
 #include <algorithm>
+#include <condition_variable>
+#include <mutex>
 #include <thread>
 // ------------------------------------------------------------------ proof container
+gkr_proof::gkr_proof() = default;
+gkr_proof::~gkr_proof() = default;  // a stream's thread is stopped and joined first (~ProofStream)
 extern "C" int gkr_proof_new(gkr_proof** out) {
   if (!out) return fail(GKR_ERR_INVALID, "null out");
   *out = new gkr_proof();
@@ -220,9 +224,113 @@ static void serialize_tail(const gkr_proof* p, Ser& s) {
     for (const felt& f : rec) s.f(f);
   s.f(p->io_commitment);
 }
+// ------------------------------------------------------------------ serialization while proving
+// A thread of the proof writes each layer record, as the reducers append it,
+// into the caller's buffer at the offset the records before it leave (layer
+// 0 at felt 1, after the layer count), so that serializing the finished
+// proof only writes the count and the tail.  A layer that does not fit ends
+// the streaming (gkr_proof_serialize then writes every layer itself).
+struct ProofStream {
+  gkr_felt* out;
+  size_t cap;
+  std::mutex m;
+  std::condition_variable work, idle;
+  std::vector<const LayerRec*> queue;  // records handed over, in proof order
+  size_t written = 0;                  // queue entries written (or counted, after an overflow)
+  std::vector<size_t> off{1};          // off[i]: first felt of layer i, for i <= written
+  bool overflow = false, stop = false;
+  std::thread th;
+  ProofStream(gkr_felt* o, size_t c) : out(o), cap(c) { th = std::thread([this] { run(); }); }
+  ~ProofStream() {
+    {
+      std::lock_guard<std::mutex> lk(m);
+      stop = true;
+    }
+    work.notify_all();
+    th.join();
+  }
+  void run() {
+    std::unique_lock<std::mutex> lk(m);
+    for (;;) {
+      work.wait(lk, [&] { return stop || written < queue.size(); });
+      if (stop) return;
+      const LayerRec* L = queue[written];
+      const size_t at = off[written];
+      bool fits = !overflow;
+      lk.unlock();
+      Ser count{nullptr};
+      serialize_layer(*L, count);
+      fits = fits && at + count.n <= cap;
+      if (fits) {
+        Ser w{out};
+        w.n = at;
+        serialize_layer(*L, w);
+      }
+      lk.lock();
+      if (!fits) overflow = true;
+      off.push_back(at + count.n);
+      written++;
+      idle.notify_all();
+    }
+  }
+  void add(const LayerRec* L) {
+    {
+      std::lock_guard<std::mutex> lk(m);
+      queue.push_back(L);
+    }
+    work.notify_one();
+  }
+  // Returns once every record handed over is written.
+  void sync() {
+    std::unique_lock<std::mutex> lk(m);
+    idle.wait(lk, [&] { return written == queue.size(); });
+  }
+  void truncate(size_t n) {
+    sync();
+    std::lock_guard<std::mutex> lk(m);
+    if (n < queue.size()) {
+      queue.resize(n);
+      written = n;
+      off.resize(n + 1);
+    }
+  }
+};
+void proof_add_layer(gkr_proof* p, LayerRec&& L) {
+  p->layers.push_back(std::move(L));
+  if (p->stream) p->stream->add(&p->layers.back());
+}
+void proof_truncate(gkr_proof* p, size_t n) {
+  if (p->stream) p->stream->truncate(n);
+  if (n < p->layers.size()) p->layers.resize(n);
+}
+extern "C" int gkr_proof_stream_to(gkr_proof* p, gkr_felt* out, size_t cap) {
+  if (!p || (!out && cap)) return fail(GKR_ERR_INVALID, "null argument");
+  p->stream.reset();
+  if (!out) return GKR_OK;
+  p->stream.reset(new ProofStream(out, cap));
+  for (const LayerRec& L : p->layers) p->stream->add(&L);
+  return GKR_OK;
+}
+
 extern "C" int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n_out) {
   if (!p || !n_out || (!out && cap)) return fail(GKR_ERR_INVALID, "null argument");
   const size_t nl = p->layers.size();
+  if (p->stream) {
+    ProofStream& st = *p->stream;
+    st.sync();  // nothing is appended while serializing: the stream is idle from here on
+    if (st.out == out && st.cap == cap && !st.overflow && st.written == nl) {
+      Ser tail_count{nullptr};
+      serialize_tail(p, tail_count);
+      *n_out = st.off[nl] + tail_count.n;
+      if (cap < *n_out) return fail(GKR_ERR_BUFFER, "need %zu felts, have %zu", *n_out, cap);
+      Ser head{out};
+      head.u(nl);
+      Ser tail{out};
+      tail.n = st.off[nl];
+      serialize_tail(p, tail);
+      return GKR_OK;
+    }
+  }
   std::vector<size_t> off(nl + 1);
   off[0] = 1;  // the layer count
   for (size_t l = 0; l < nl; l++) {

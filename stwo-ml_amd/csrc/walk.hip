@@ -179,7 +179,7 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
       point = point_before;
       value = value_before;
       if (proof) {
-        proof->layers.resize(layers_before);
+        proof_truncate(proof, layers_before);
         proof->weight_claims.resize(claims_before);
       }
       c->wait_expired = false;

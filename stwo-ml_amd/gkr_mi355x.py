@@ -161,6 +161,7 @@ SIGNATURES = [
     ("gkr_proof_add_weight_commitment", C.c_int, [_P, _PF]),
     ("gkr_proof_set_io_commitment", C.c_int, [_P, _PF]),
     ("gkr_proof_serialize", C.c_int, [_P, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
+    ("gkr_proof_stream_to", C.c_int, [_P, _PF, C.c_size_t]),
     ("gkr_seed_channel", C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_uint64, _PF]),
     ("gkr_matmul_output_claim", C.c_int, [_P, _P, _P, _PQ, C.c_uint32, _PQ]),
     ("gkr_prove_matmul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ, _PQ]),
@@ -1002,6 +1003,25 @@ class Proof:
         arr = (GkrFelt * max(1, n.value))()
         _check(lib().gkr_proof_serialize(self._h, arr, n.value, C.byref(n)))
         return [felt_from_c(arr[i]) for i in range(n.value)]
+
+    def stream_to(self, out: Optional[np.ndarray]) -> None:
+        """Serialize each layer into out, an (cap, 8) uint32 array of felt words, as the reducers append
+        it (gkr_proof_stream_to); serialize_into(out) then writes only the count and the tail.  None
+        ends the streaming.  The proof keeps a reference to out."""
+        if out is None:
+            _check(lib().gkr_proof_stream_to(self._h, None, 0))
+            self._stream_buf = None
+            return
+        assert out.dtype == np.uint32 and out.ndim == 2 and out.shape[1] == 8 and out.flags["C_CONTIGUOUS"]
+        self._stream_buf = out
+        _check(lib().gkr_proof_stream_to(self._h, out.ctypes.data_as(C.POINTER(GkrFelt)), out.shape[0]))
+
+    def serialize_into(self, out: np.ndarray) -> int:
+        """gkr_proof_serialize into out ((cap, 8) uint32); returns the felt count."""
+        assert out.dtype == np.uint32 and out.ndim == 2 and out.shape[1] == 8 and out.flags["C_CONTIGUOUS"]
+        n = C.c_size_t()
+        _check(lib().gkr_proof_serialize(self._h, out.ctypes.data_as(C.POINTER(GkrFelt)), out.shape[0], C.byref(n)))
+        return n.value
 
     def serialize_words(self) -> np.ndarray:
         """The serialized proof as an (n, 8) array of little-endian u32 felt words (no int conversion)."""
