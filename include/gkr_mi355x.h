@@ -215,6 +215,26 @@ int gkr_proof_serialize(const gkr_proof* p, gkr_felt* out, size_t cap, size_t* n
  * freed, serialized or streamed elsewhere; out == NULL ends the streaming.   */
 int gkr_proof_stream_to(gkr_proof* p, gkr_felt* out, size_t cap);
 
+/* Proof-generation policy (PolicyConfig, engine/src/policy.rs:48-121): every
+ * field is 0 or 1 except weight_binding_mode (0 Individual, 1 Aggregated,
+ * 2 TrustlessMode2, 3 TrustlessMode3, policy.rs:30-43).                      */
+typedef struct {
+  uint8_t allow_missing_norm_proof, allow_logup_activation, allow_missing_segment_binding;
+  uint8_t skip_rms_sq_proof, piecewise_activation, skip_batch_tokens, skip_unified_stark;
+  uint8_t weight_binding_mode;
+  uint8_t aggregated_full_binding, aggregated_rlc_only;
+  uint8_t io_packing, packed_proof, double_packed_proof;
+  uint8_t validate_decode_chain;
+} gkr_policy;
+/* The presets PolicyConfig::strict / standard / relaxed (policy.rs:131-203),
+ * by name, case-insensitive (from_preset_name, policy.rs:288-295); an
+ * unknown name is GKR_ERR_INVALID.                                           */
+int gkr_policy_preset(const char* name, gkr_policy* out);
+/* PolicyConfig::policy_commitment (policy.rs:236-254): poseidon_hash_many of
+ * the domain separator 0x504F4C01 and the 14 fields in declaration order, the
+ * value gkr_seed_channel mixes.  A field out of range is GKR_ERR_INVALID.    */
+int gkr_policy_commitment(const gkr_policy* policy, gkr_felt* out);
+
 /* GKR driver seeding (gkr/prover.rs:1527-1560): mix_u64(num_layers),
  * mix_u64(in_rows), mix_u64(in_cols), then mix_felt(policy_commitment) when
  * policy != NULL and non-zero (prover.rs:1533-1537).                         */

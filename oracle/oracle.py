@@ -91,6 +91,36 @@ def felt_int(w) -> int:
     return sum(int(w[i]) << (32 * i) for i in range(8))
 
 
+# PolicyConfig (engine/src/policy.rs:48-121): its fields in declaration order,
+# the presets strict / standard / relaxed (policy.rs:131-203), and
+# policy_commitment (policy.rs:236-254): poseidon_hash_many of the domain
+# separator "POL" + version 1 (policy.rs:28) and the fields as integers
+# (weight_binding_mode: Individual 0, Aggregated 1, TrustlessMode2 2,
+# TrustlessMode3 3, policy.rs:30-43).
+POLICY_FIELDS = ("allow_missing_norm_proof", "allow_logup_activation", "allow_missing_segment_binding",
+                 "skip_rms_sq_proof", "piecewise_activation", "skip_batch_tokens", "skip_unified_stark",
+                 "weight_binding_mode", "aggregated_full_binding", "aggregated_rlc_only", "io_packing", "packed_proof",
+                 "double_packed_proof", "validate_decode_chain")
+POLICY_PRESETS = {
+    "strict": dict(allow_missing_norm_proof=0, allow_logup_activation=0, allow_missing_segment_binding=0,
+                   skip_rms_sq_proof=0, piecewise_activation=1, skip_batch_tokens=0, skip_unified_stark=0,
+                   weight_binding_mode=1, aggregated_full_binding=1, aggregated_rlc_only=0, io_packing=1,
+                   packed_proof=1, double_packed_proof=1, validate_decode_chain=1),
+    "standard": dict(allow_missing_norm_proof=1, allow_logup_activation=1, allow_missing_segment_binding=0,
+                     skip_rms_sq_proof=1, piecewise_activation=0, skip_batch_tokens=1, skip_unified_stark=1,
+                     weight_binding_mode=1, aggregated_full_binding=1, aggregated_rlc_only=0, io_packing=1,
+                     packed_proof=1, double_packed_proof=1, validate_decode_chain=1),
+    "relaxed": dict(allow_missing_norm_proof=1, allow_logup_activation=1, allow_missing_segment_binding=1,
+                    skip_rms_sq_proof=1, piecewise_activation=1, skip_batch_tokens=1, skip_unified_stark=1,
+                    weight_binding_mode=1, aggregated_full_binding=0, aggregated_rlc_only=0, io_packing=1,
+                    packed_proof=1, double_packed_proof=1, validate_decode_chain=0),
+}
+
+
+def policy_commitment(policy: dict) -> int:
+    return hash_many([0x504F4C01] + [int(policy[f]) for f in POLICY_FIELDS])
+
+
 class Channel:
     """Oracle PoseidonChannel (engine/src/crypto/poseidon_channel.rs:83-308)."""
 

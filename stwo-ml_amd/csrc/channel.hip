@@ -168,6 +168,38 @@ extern "C" int gkr_channel_import(gkr_channel* ch, const uint32_t state[11]) {
   ch->ch.import_state(state);
   return GKR_OK;
 }
+// ------------------------------------------------------------------ proof-generation policy
+extern "C" int gkr_policy_preset(const char* name, gkr_policy* out) {
+  if (!name || !out) return fail(GKR_ERR_INVALID, "null argument");
+  std::string n(name);
+  for (char& ch : n) ch = (char)tolower((unsigned char)ch);
+  // field order: norm, logup, segment | rms_sq, piecewise, batch, stark | mode | full, rlc | io, packed, double | chain
+  if (n == "strict")  // policy.rs:131-155
+    *out = gkr_policy{0, 0, 0, 0, 1, 0, 0, 1, 1, 0, 1, 1, 1, 1};
+  else if (n == "standard")  // policy.rs:160-184
+    *out = gkr_policy{1, 1, 0, 1, 0, 1, 1, 1, 1, 0, 1, 1, 1, 1};
+  else if (n == "relaxed")  // policy.rs:189-203
+    *out = gkr_policy{1, 1, 1, 1, 1, 1, 1, 1, 0, 0, 1, 1, 1, 0};
+  else
+    return fail(GKR_ERR_INVALID, "unknown policy preset '%s'", name);
+  return GKR_OK;
+}
+extern "C" int gkr_policy_commitment(const gkr_policy* p, gkr_felt* out) {
+  if (!p || !out) return fail(GKR_ERR_INVALID, "null argument");
+  const uint8_t v[14] = {p->allow_missing_norm_proof, p->allow_logup_activation, p->allow_missing_segment_binding,
+                         p->skip_rms_sq_proof,        p->piecewise_activation,   p->skip_batch_tokens,
+                         p->skip_unified_stark,       p->weight_binding_mode,    p->aggregated_full_binding,
+                         p->aggregated_rlc_only,      p->io_packing,             p->packed_proof,
+                         p->double_packed_proof,      p->validate_decode_chain};
+  felt in[15];
+  in[0] = felt_from_u64(0x504F4C01ull);  // "POL" + version 1 (policy.rs:28)
+  for (int i = 0; i < 14; i++) {
+    if (v[i] > (i == 7 ? 3 : 1)) return fail(GKR_ERR_INVALID, "policy field %d out of range (%u)", i, v[i]);
+    in[1 + i] = felt_from_u64(v[i]);
+  }
+  *out = felt_to_abi(poseidon_hash_many(in, 15));
+  return GKR_OK;
+}
 extern "C" int gkr_seed_channel(gkr_channel* ch, uint64_t num_layers, uint64_t in_rows, uint64_t in_cols,
                                 const gkr_felt* policy_commitment) {
   CH_CHECK(ch);

@@ -33,6 +33,16 @@ class GkrFelt(C.Structure):
     _fields_ = [("w", C.c_uint32 * 8)]
 
 
+POLICY_FIELDS = ("allow_missing_norm_proof", "allow_logup_activation", "allow_missing_segment_binding",
+                 "skip_rms_sq_proof", "piecewise_activation", "skip_batch_tokens", "skip_unified_stark",
+                 "weight_binding_mode", "aggregated_full_binding", "aggregated_rlc_only", "io_packing", "packed_proof",
+                 "double_packed_proof", "validate_decode_chain")
+
+
+class GkrPolicy(C.Structure):
+    _fields_ = [(f, C.c_uint8) for f in POLICY_FIELDS]
+
+
 class GkrMulOut(C.Structure):
     _fields_ = [("eq_round_polys", C.POINTER(GkrQM31)), ("lhs_eval", GkrQM31), ("rhs_eval", GkrQM31),
                 ("alpha", GkrQM31), ("next_value", GkrQM31), ("n_vars", C.c_uint32)]
@@ -163,6 +173,8 @@ SIGNATURES = [
     ("gkr_proof_serialize", C.c_int, [_P, _PF, C.c_size_t, C.POINTER(C.c_size_t)]),
     ("gkr_proof_stream_to", C.c_int, [_P, _PF, C.c_size_t]),
     ("gkr_seed_channel", C.c_int, [_P, C.c_uint64, C.c_uint64, C.c_uint64, _PF]),
+    ("gkr_policy_preset", C.c_int, [C.c_char_p, C.POINTER(GkrPolicy)]),
+    ("gkr_policy_commitment", C.c_int, [C.POINTER(GkrPolicy), _PF]),
     ("gkr_matmul_output_claim", C.c_int, [_P, _P, _P, _PQ, C.c_uint32, _PQ]),
     ("gkr_prove_matmul_layer", C.c_int, [_P, _PQ, C.c_uint32, _PQ, _P, _P, _P, _P, _PQ, _PQ, _PQ, _PQ, _PQ]),
     ("gkr_prove_matmul_layer_dual_simd", C.c_int,
@@ -293,6 +305,21 @@ def poseidon_hash_many(xs: Sequence[int]) -> int:
     arr = (GkrFelt * max(1, len(xs)))(*[felt_to_c(v) for v in xs])
     out = GkrFelt()
     _check(lib().gkr_poseidon_hash_many(arr, len(xs), C.byref(out)))
+    return felt_from_c(out)
+
+
+def policy_preset(name: str) -> dict:
+    """PolicyConfig::strict / standard / relaxed (engine/src/policy.rs:131-203) as a field dict."""
+    p = GkrPolicy()
+    _check(lib().gkr_policy_preset(name.encode(), C.byref(p)))
+    return {f: int(getattr(p, f)) for f in POLICY_FIELDS}
+
+
+def policy_commitment(policy: dict) -> int:
+    """PolicyConfig::policy_commitment (engine/src/policy.rs:236-254)."""
+    p = GkrPolicy(*[int(policy[f]) for f in POLICY_FIELDS])
+    out = GkrFelt()
+    _check(lib().gkr_policy_commitment(C.byref(p), C.byref(out)))
     return felt_from_c(out)
 
 

@@ -15,6 +15,9 @@ tests and artifacts hold.  Sources:
     SHA-256 digest of the decimal list and the first/last value are kept)
   - engine/tests/artifacts/d10_verify_gkr_calldata.txt and d10_onchain_summary.json
     (MatMul -> LayerNorm -> MatMul on-chain calldata, e2e_cairo_verify.rs:312, 1479)
+  - engine/scripts/deploy_policy_upgrade.mjs, engine/docs/ENV_VARS.md and
+    elo-cairo-verifier/tests/test_model_gkr_contract.cairo (the policy
+    presets' commitments)
 """
 import hashlib
 import json
@@ -95,6 +98,21 @@ def main() -> None:
                  "[[7,9,11,13],[17,19,21,23]], identity 4x4 W0, W2[i][j] = i+j+1 (4x2)",
         "verify_calldata": [int(x, 16) if x.startswith("0x") else int(x) for x in d10],
         "summary": json.loads(read("engine/tests/artifacts/d10_onchain_summary.json")),
+    }
+    # PolicyConfig::policy_commitment of the three presets, as the reference
+    # records them in three places (the deployment script's table, the
+    # environment-variable documentation, the Cairo contract tests)
+    dep = read("engine/scripts/deploy_policy_upgrade.mjs")
+    pol = {k: v for k, v in re.findall(r'^\s*(strict|standard|relaxed):\s*"(0x[0-9a-f]{64})"', dep, re.M)}
+    doc = dict(re.findall(r"^(strict|standard|relaxed):\s+(0x[0-9a-f]{64})$", read("engine/docs/ENV_VARS.md"), re.M))
+    cairo_t = read("elo-cairo-verifier/tests/test_model_gkr_contract.cairo")
+    assert pol == doc and set(pol) == {"strict", "standard", "relaxed"}
+    assert pol["strict"] in cairo_t and pol["standard"] in cairo_t
+    out["policy"] = {
+        "commitments": pol,
+        "source": "engine/scripts/deploy_policy_upgrade.mjs:44-48, engine/docs/ENV_VARS.md:36-42, "
+                  "elo-cairo-verifier/tests/test_model_gkr_contract.cairo:189, 249 "
+                  "(PolicyConfig::policy_commitment, engine/src/policy.rs:236-254)",
     }
     with open(os.path.join(HERE, "reference_vectors.json"), "w") as f:
         json.dump(out, f, indent=1)

@@ -212,3 +212,33 @@ def test_parallel_draw_batches_equal_sequential_draws():
     for t in ts:
         t.join()
     assert not errs
+
+
+def test_policy_presets_and_commitment(golden):
+    """gkr_policy_preset / gkr_policy_commitment: the presets equal the oracle's restatement of
+    policy.rs:131-203 and their commitments the reference's recorded values; 60 random policies
+    equal the oracle; names are case-insensitive; out-of-range fields and unknown names are
+    rejected; seeding with the strict commitment mixes it like the oracle."""
+    want = {k: int(v, 16) for k, v in golden["policy"]["commitments"].items()}
+    for name in ("strict", "standard", "relaxed"):
+        p = G.policy_preset(name)
+        assert p == O.POLICY_PRESETS[name]
+        assert G.policy_preset(name.upper()) == p
+        assert G.policy_commitment(p) == want[name]
+    rng = random.Random(3)
+    for _ in range(60):
+        p = {f: rng.randrange(4 if f == "weight_binding_mode" else 2) for f in G.POLICY_FIELDS}
+        assert G.policy_commitment(p) == O.policy_commitment(p)
+    with pytest.raises(G.GkrError):
+        G.policy_preset("paranoid")
+    bad = dict(G.policy_preset("strict"), weight_binding_mode=4)
+    with pytest.raises(G.GkrError):
+        G.policy_commitment(bad)
+    with pytest.raises(G.GkrError):
+        G.policy_commitment(dict(G.policy_preset("strict"), io_packing=2))
+    a, b = G.PoseidonChannel(), O.Channel()
+    a.seed_gkr(48, 64, 5120, policy_commitment=want["strict"])
+    for v in (48, 64, 5120):
+        b.mix_u64(v)
+    b.mix_felt(want["strict"])
+    assert a.digest() == b.digest()

@@ -257,3 +257,18 @@ def test_oracle_opening_round_trip():
         vch = start.clone()
         assert O.verify_mle_opening(cm, proof, point, vch)
         assert vch.digest() == ch.digest()
+
+
+def test_policy_commitments_of_the_presets(golden):
+    """PolicyConfig::policy_commitment (policy.rs:236-254) of the strict / standard / relaxed presets
+    equals the values the reference records (deployment script, env-var docs, Cairo contract tests);
+    a flipped field, a changed binding mode or a field order swapped gives another value."""
+    want = {k: int(v, 16) for k, v in golden["policy"]["commitments"].items()}
+    for name, pol in O.POLICY_PRESETS.items():
+        assert O.policy_commitment(pol) == want[name], name
+    s = dict(O.POLICY_PRESETS["strict"])
+    assert O.policy_commitment(dict(s, validate_decode_chain=0)) != want["strict"]
+    assert O.policy_commitment(dict(s, weight_binding_mode=2)) != want["strict"]
+    swapped = [0x504F4C01] + [int(s[f]) for f in O.POLICY_FIELDS]
+    swapped[5], swapped[6] = swapped[6], swapped[5]  # piecewise_activation <-> skip_batch_tokens
+    assert O.hash_many(swapped) != want["strict"]
