@@ -18,6 +18,18 @@ ported to this build's verifier (the C ABI's host replay), the oracle's verifier
   model_verifier.cairo:158-215, :298-372) spelled out in Python and run over the oracle's
   serialized proof of a layer with a 4-entry table (two multiplicity rounds): accepted, ending on
   the prover's channel state; a changed c1 rejected; the final mixes' order pinned.
+* RMSNorm layer: the Cairo verifier's statement of it (dispatch_rmsnorm, model_verifier.cairo:483-573,
+  then verify_rmsnorm_layer, layer_verifiers.cairo:605-680 with verify_linear_eq_sumcheck :358-410,
+  verify_logup_eq_sumcheck :282-344 and verify_multiplicity_sumcheck :53-95), replayed over the
+  oracle's serialized RMSNorm layer: Part 0 ("RQ", n_active, sum of squares, its rounds, the
+  final evaluation), Part 1 ("RN", rms^2 and rsqrt evaluations, the claim value, the linear
+  eq-sumcheck, both finals), the rsqrt LogUp ("LOG", "RN", gamma, beta, claimed sum, rounds), the
+  multiplicity sumcheck, then input and output evaluations: accepted, ending on the prover's
+  channel state; a changed Part-0 or linear round and two swapped Part-1 mixes rejected or parted.
+  The reference's Rust serializer writes no multiplicity sumcheck for RMSNorm
+  (cairo_serde.rs:1648-1720) while the Cairo dispatcher reads an optional one before the per-row
+  statistics; the replay reads the Rust layout and takes the multiplicity rounds from the proof
+  record, where that optional field would carry them.
 * Activation tables: engine/src/gadgets/lookup_table.rs:466-633 (GELU against its f64 formula
   at 200 points, known values, limits, monotonicity; SiLU(0) and SiLU(1.0))."""
 import math
@@ -364,3 +376,164 @@ def test_logup_tail_cairo_statement_rejections():
     straight = start.clone()
     cairo_dispatch_activation(good, pt, straight)
     assert straight.digest() == end.digest()
+
+
+# ------------------------------------------------------------------ RMSNorm, Cairo statement
+def cairo_rmsnorm(felts, claim_point, claim_value, mult, ch, swap_part1_mix=False):
+    """The Cairo verifier's statement of a tag-8 layer, spelled out step by step over the Rust
+    layout of LayerProof::RMSNorm (cairo_serde.rs:1648-1720):
+    dispatch_rmsnorm (model_verifier.cairo:483-573): Part 0 -- mix_u64(0x5251), mix_u64(n_active),
+    mix(sum of squares), per round c1 rebuilt from the running sum, mix_poly_coeffs_deg3, draw,
+    sum = p(challenge); then mix(final evaluation);
+    verify_rmsnorm_layer (layer_verifiers.cairo:605-680): mix_u64(0x524E), mix(rms_sq_eval),
+    mix(rsqrt_eval), mix(claim value); verify_linear_eq_sumcheck (:358-410: rounds from the claim
+    value, final == eq(r, s) * input_final * rsqrt_final, LINEAR_FINAL_MISMATCH); mix both finals;
+    with a LogUp part: mix_u64(0x4C4F47), mix_u64(0x524E), draw gamma, beta,
+    verify_logup_eq_sumcheck (:282-344); verify_multiplicity_sumcheck (:53-95) over `mult`
+    ((rounds, final, claimed sum), the multiplicity sumcheck the Rust format does not write);
+    mix(input_eval), mix(output_eval).  Returns (next claim value, felts read)."""
+    rd = _Reader(felts)
+    assert rd.u() == 8, "tag"
+    input_eval, output_eval, rms_sq, rsqrt_eval = rd.q(), rd.q(), rd.q(), rd.q()
+    rd.u()  # rsqrt table commitment (checked outside the walk)
+    assert rd.u() == 0, "simd_combined"
+    if rd.u() == 1:  # Part 0b
+        n_active = rd.u()
+        sq_sum = rd.q()
+        rounds = [(rd.q(), rd.q(), rd.q()) for _ in range(rd.u())]
+        ch.mix_u64(0x5251)
+        ch.mix_u64(n_active)
+        ch.mix_secure_field(sq_sum)
+        cur = sq_sum
+        for c0, c2, c3 in rounds:
+            c1 = Q.qsub(Q.qsub(Q.qsub(cur, Q.qadd(c0, c0)), c2), c3)
+            ch.mix_poly_coeffs_deg3(c0, c1, c2, c3)
+            cur = _poly3((c0, c1, c2, c3), ch.draw_qm31())
+        ch.mix_secure_field(rd.q())  # rms_sq_final
+    lin = [(rd.q(), rd.q(), rd.q()) for _ in range(rd.u())]
+    in_final, rsqrt_final = rd.q(), rd.q()
+    has_logup = rd.u() == 1
+    if has_logup:
+        claimed = rd.q()
+        lpolys = [(rd.q(), rd.q(), rd.q()) for _ in range(rd.u())]
+        w_e, in_e, out_e = rd.q(), rd.q(), rd.q()
+        for _ in range(rd.u()):
+            rd.u()  # multiplicities: consumed, not used
+    if rd.u() == 1:  # per-row statistics: consumed
+        for _ in range(rd.u()):
+            rd.u()
+    first = [rms_sq, rsqrt_eval] if not swap_part1_mix else [rsqrt_eval, rms_sq]
+    ch.mix_u64(0x524E)
+    for v in first:
+        ch.mix_secure_field(v)
+    ch.mix_secure_field(claim_value)
+    cur, chal = claim_value, []
+    for c0, c2, c3 in lin:
+        c1 = Q.qsub(Q.qsub(Q.qsub(cur, Q.qadd(c0, c0)), c2), c3)
+        ch.mix_poly_coeffs_deg3(c0, c1, c2, c3)
+        x = ch.draw_qm31()
+        chal.append(x)
+        cur = _poly3((c0, c1, c2, c3), x)
+    assert cur == Q.qmul(_eq_eval(claim_point[:len(lin)], chal), Q.qmul(in_final, rsqrt_final)), \
+        "LINEAR_FINAL_MISMATCH"
+    ch.mix_secure_field(in_final)
+    ch.mix_secure_field(rsqrt_final)
+    if has_logup:
+        ch.mix_u64(0x4C4F47)
+        ch.mix_u64(0x524E)
+        gamma = ch.draw_qm31()
+        beta = ch.draw_qm31()
+        ch.mix_secure_field(claimed)
+        cur, chal = ONE, []
+        for c0, c2, c3 in lpolys:
+            c1 = Q.qsub(Q.qsub(Q.qsub(cur, Q.qadd(c0, c0)), c2), c3)
+            ch.mix_poly_coeffs_deg3(c0, c1, c2, c3)
+            x = ch.draw_qm31()
+            chal.append(x)
+            cur = _poly3((c0, c1, c2, c3), x)
+        d_e = Q.qsub(Q.qsub(gamma, in_e), Q.qmul(beta, out_e))
+        assert cur == Q.qmul(_eq_eval(claim_point[:len(lpolys)], chal), Q.qmul(w_e, d_e)), "LOGUP_FINAL_MISMATCH"
+    ms_rounds, ms_final, ms_claimed = mult
+    cur = ms_claimed
+    for c0, c1 in ms_rounds:
+        assert Q.qadd(c0, Q.qadd(c0, c1)) == cur, "MULT_SUMCHECK_ROUND_FAIL"
+        ch.mix_secure_field(c0)
+        ch.mix_secure_field(c1)
+        cur = Q.qadd(c0, Q.qmul(c1, ch.draw_qm31()))
+    assert cur == ms_final, "MULT_SUMCHECK_FINAL_EVAL_MISMATCH"
+    ch.mix_secure_field(input_eval)
+    ch.mix_secure_field(output_eval)
+    return input_eval, rd.pos
+
+
+def _rmsnorm_case(rows=2, cols=8, dim=8, seed=71):
+    """The oracle's RMSNorm reduction of a rows x cols input, claim = the output MLE at a drawn point.
+    Returns (point, value, start channel, proof, end channel, serialized layer)."""
+    X = O.synthetic(rows, cols, 1, seed)
+    out = O.rmsnorm_forward(X, dim)
+    ch = O.Channel()
+    ch.mix_u64(seed)
+    flat = [_q(int(x)) for x in out.reshape(-1)]
+    pt = ch.draw_qm31s((len(flat) - 1).bit_length())
+    val = O.evaluate_mle(flat, pt)
+    start = ch.clone()
+    proof = O.prove_rmsnorm_layer(pt, val, X, dim, ch)
+    cd = []
+    O.serialize_rmsnorm_layer(cd, proof)
+    return pt, val, start, proof, ch, cd
+
+
+def _mult(proof):
+    return proof["mult_round_polys"], proof["mult_final"], proof["mult_sum"]
+
+
+def test_rmsnorm_cairo_statement_accepts_oracle_proof():
+    """The reference's Cairo statement of the RMSNorm layer, replayed over the oracle's serialized
+    proof (two padded rows, so the per-row statistics are present), accepts it and ends on the
+    prover's channel state; the whole layer is read.  The product's RMSNorm verifier accepts the
+    same proof and ends on the same state (its walk verifier refuses RMSNorm calldata, which lacks
+    the multiplicity sumcheck)."""
+    pt, val, start, proof, end, cd = _rmsnorm_case()
+    ch = start.clone()
+    nxt, used = cairo_rmsnorm(cd, pt, val, _mult(proof), ch)
+    assert used == len(cd) and nxt == proof["input_eval"]
+    assert ch.digest() == end.digest()
+    gch = G.PoseidonChannel()
+    gch.import_state(O.channel_state(start))
+    assert G.verify_norm_layer(G.STEP_RMSNORM, pt, val, 8, dict(proof), gch) == proof["input_eval"]
+    assert gch.digest() == end.digest()
+    full = [1] + cd
+    O.serialize_tail(full, pt, proof["input_eval"], [], 0)
+    with pytest.raises(G.GkrError, match="multiplicity sumcheck"):
+        G.verify_walk(full, [(G.STEP_RMSNORM, 2, 8, 0, 0, 8)], pt, val, G.PoseidonChannel())
+
+
+def test_rmsnorm_cairo_statement_rejections():
+    """A changed c0 of the linear eq-sumcheck's last round fails LINEAR_FINAL_MISMATCH.  A changed
+    Part-0 round (Part 0 is replayed, not checked, by the Cairo statement; the Rust verifier checks
+    it) changes every later challenge, and so does mixing rsqrt_eval before rms_sq_eval: the
+    linear or LogUp eq-sumcheck's final check then fails, so Part 0's transcript and the Part-1
+    mix order are pinned."""
+    pt, val, start, proof, end, cd = _rmsnorm_case()
+    bad = dict(proof)
+    lr = list(proof["lin_round_polys"])
+    c0, c1, c2, c3 = lr[-1]
+    lr[-1] = (Q.qadd(c0, ONE), c1, c2, c3)
+    bad["lin_round_polys"] = lr
+    bcd = []
+    O.serialize_rmsnorm_layer(bcd, bad)
+    with pytest.raises(AssertionError, match="LINEAR_FINAL_MISMATCH"):
+        cairo_rmsnorm(bcd, pt, val, _mult(proof), start.clone())
+    bad0 = dict(proof)
+    p0 = list(proof["p0_round_polys"])
+    c0, c1, c2, c3 = p0[0]
+    p0[0] = (Q.qadd(c0, ONE), c1, c2, c3)
+    bad0["p0_round_polys"] = p0
+    b0 = []
+    O.serialize_rmsnorm_layer(b0, bad0)
+    ch = start.clone()
+    with pytest.raises(AssertionError):
+        cairo_rmsnorm(b0, pt, val, _mult(proof), ch)
+    sw = start.clone()
+    with pytest.raises(AssertionError):
+        cairo_rmsnorm(cd, pt, val, _mult(proof), sw, swap_part1_mix=True)
