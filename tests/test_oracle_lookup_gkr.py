@@ -13,7 +13,8 @@ stwo-gpu/crates/stwo/src/prover/lookups/gkr_prover.rs:396-500) pinned on the CPU
 * the restated partially_verify_batch accepts and ends on the prover's transcript; changed round
   polynomials, masks, output claims and gates are rejected.
 No reference-held vector covers this protocol (its tests run on the Blake2s channel and assert the
-properties above), so the transcript itself is pinned by the replay only."""
+properties above); the Poseidon transcript is pinned by the reference's Cairo statement of the
+verifier (tests/test_reference_lookup_gkr.py)."""
 import numpy as np
 import oracle as O
 import pytest
