@@ -11,7 +11,8 @@ aggregated_opening.rs:681-730 and the streaming variant :1647-1720) pinned on th
   hypercube of R(t) = sum_i beta_i eq(g_i, t) (W(t) - v_i), W the unified oracle, with the
   transcript replayed in Python;
 * the serialization layout (config, round polynomials, oracle value, roots, opening).
-No reference vector covers this protocol; the transcript is pinned by the replay."""
+No reference vector covers this protocol; the transcript is pinned by the reference's Cairo statement
+of the verifier (tests/test_reference_binding.py)."""
 import numpy as np
 import oracle as O
 import pytest
