@@ -537,3 +537,58 @@ def test_rmsnorm_cairo_statement_rejections():
     sw = start.clone()
     with pytest.raises(AssertionError):
         cairo_rmsnorm(cd, pt, val, _mult(proof), sw, swap_part1_mix=True)
+
+
+# ------------------------------------------------------------------ RLC weight binding, verifier statement
+def rust_verify_batched_rlc(claims, weights, ch):
+    """The Rust verifier's batched RLC weight binding (engine/src/gkr/verifier.rs:1170-1223, no
+    deferred proofs): draw rho; combined_expected = sum rho^i expected_i and combined_actual =
+    sum rho^i MLE_i(point_i), each weight's MLE the column-major padded matrix
+    (evaluate_weight_claim_against_matrix); mix combined_expected; the two must be equal."""
+    rho = ch.draw_qm31()
+    pw, exp, act = ONE, ZERO, ZERO
+    for (point, expected), W in zip(claims, weights):
+        mle = [tuple(int(x) for x in v) for v in O.col_major_mle(W)]
+        exp = Q.qadd(exp, Q.qmul(pw, expected))
+        act = Q.qadd(act, Q.qmul(pw, O.evaluate_mle(mle, point)))
+        pw = Q.qmul(pw, rho)
+    ch.mix_secure_field(exp)
+    assert exp == act, "batched RLC weight-binding mismatch"
+
+
+def _rlc_walk(seed=11):
+    """Three MatMul layers by the oracle (one weight used twice); returns the weight claims (point =
+    r_j followed by the reduction's challenges, value = final_b), the weights, the channel before the
+    binding and after the prover's RLC binding."""
+    rng = np.random.default_rng(seed)
+    W1 = rng.integers(0, P, size=(24, 40), dtype=np.uint32)
+    W2 = rng.integers(0, P, size=(40, 9), dtype=np.uint32)
+    X = rng.integers(0, P, size=(3, 24), dtype=np.uint32)
+    H = O.matmul_forward(X, W1)
+    ch = O.Channel()
+    ch.mix_u64(3)
+    claims, weights = [], []
+    for a, b in [(H, W2), (X, W1), (X, W1)]:
+        lm = (a.shape[0] - 1).bit_length()
+        r = ch.draw_qm31s(lm + (b.shape[1] - 1).bit_length())
+        v = O.matmul_output_claim(a, b, r)
+        ch.mix_secure_field(v)
+        o = O.prove_matmul_layer(r, v, a, b, ch)
+        claims.append((list(r[lm:]) + list(o["next_point"][lm:]), o["final_b_eval"]))
+        weights.append(b)
+    before = ch.clone()
+    O.rlc_weight_binding([c[1] for c in claims], ch)
+    return claims, weights, before, ch
+
+
+def test_rlc_weight_binding_by_the_rust_verifier_statement():
+    """The oracle's RLC binding after three MatMul layers: the Rust verifier's statement accepts the
+    claims (every final_b is the weight's MLE at its point), ends on the prover's channel state, and
+    rejects a changed claim value."""
+    claims, weights, before, after = _rlc_walk()
+    ch = before.clone()
+    rust_verify_batched_rlc(claims, weights, ch)
+    assert ch.digest() == after.digest()
+    bad = [claims[0], (claims[1][0], Q.qadd(claims[1][1], ONE)), claims[2]]
+    with pytest.raises(AssertionError, match="batched RLC weight-binding mismatch"):
+        rust_verify_batched_rlc(bad, weights, before.clone())
