@@ -28,11 +28,18 @@
 #include "launcher.h"
 #include "poseidon.h"
 #include "trace.h"
+#include "hostfield.h"
 
 namespace gkr {
 struct MerkleConsts;  // merkle.h
 }
 using namespace gkr;
+
+// The words of QM31 values, for the host-side AVX2 rounds (hostfield.h), which
+// take the array-of-structs layout as plain u32 words.
+static_assert(sizeof(qm31) == 16 && alignof(qm31) == 4, "qm31 is four packed u32 words");
+inline uint32_t* qwords(qm31* q) { return reinterpret_cast<uint32_t*>(q); }
+inline const uint32_t* qwords(const qm31* q) { return reinterpret_cast<const uint32_t*>(q); }
 
 // ------------------------------------------------------------------ errors
 // Records the message of a failure for gkr_last_error() and returns code.
@@ -612,16 +619,74 @@ static inline qm31 eqlin(const qm31& z, const qm31& x) {
 }
 // Lagrange weights E[u] (u < 2^j, first challenge on the MSB) of r[0..j).
 void lagrange_weights(const qm31* r, int j, qm31* E);
-// Round j (0-based within the trip) of a product-type trip from its cross sums
-// G (4^K, row-major over sub-vectors c, c'), evaluated at the nx points xs:
+// The K rounds of a product-type trip from its cross sums G (4^K, row-major
+// over sub-vectors c, c'), one after another.  Round j's polynomial is
 //   p(X) = sum_v sum_{u,u',b,b'} E[u] E[u'] eqlin(X,b) eqlin(X,b') G[(u,b,v)][(u',b',v)]
-// with E the Lagrange weights of the trip's challenges r[0..j) and v running
-// over the trip's later variables.  For the eq-sumcheck (zt given: the claim
-// coordinates of the trip's variables; cpre: prod of eqlin(z_l, r_l) over all
-// earlier rounds) the eq factors are applied:
-//   p(X) *= cpre * prod_{i<j} eqlin(zt_i, r_i) * eqlin(zt_j, X),  v weighted by eqlin(zt, v).
-void trip_round_gram(const qm31* G, int K, int j, const qm31* r, int nx, const qm31* xs, qm31* out,
-                            const qm31* zt, const qm31& cpre);
+// with E the Lagrange weights of the trip's challenges r_0 .. r_{j-1} (the
+// first on the most significant bit) and v over the trip's later variables.
+// Applying E on both sides is folding the rows and the columns of G on their
+// top bit by each challenge as it is drawn, so round j reads a 2^(K-j) x
+// 2^(K-j) matrix F:
+//   p(X) = sum_v eqv(v) sum_{b,b'} eqlin(X,b) eqlin(X,b') F[(b,v)][(b',v)].
+// For the eq-sumcheck (zt: the claim coordinates of the trip's variables;
+// cpre: prod of eqlin(z_l, r_l) over the earlier rounds) v is weighted by
+// eq(zt_{>j}, v) and p(X) multiplied by cpre * prod_{i<j} eqlin(zt_i, r_i) *
+// eqlin(zt_j, X).
+struct TripGram {
+  int K, j = 0, dim;
+  qm31 F[kMaxSums];
+  const qm31* zt;
+  qm31 pre;
+  TripGram(const qm31* G, int K_, const qm31* zt_, const qm31& cpre) : K(K_), dim(1 << K_), zt(zt_), pre(cpre) {
+    for (int q = 0; q < dim * dim; q++) F[q] = G[q];
+  }
+  // p(xs[k]) for the current round
+  void values(int nx, const qm31* xs, qm31* out) const {
+    const int h = dim / 2;
+    qm31 H00 = qm31_zero(), H01 = qm31_zero(), H10 = qm31_zero(), H11 = qm31_zero();
+    for (int v = 0; v < h; v++) {
+      qm31 f00 = F[v * dim + v], f01 = F[v * dim + h + v], f10 = F[(h + v) * dim + v], f11 = F[(h + v) * dim + h + v];
+      if (zt) {
+        qm31 ez = qm31_one();
+        for (int i = 0; i < K - j - 1; i++)
+          ez = qm31_mul(ez, ((v >> (K - j - 2 - i)) & 1) ? zt[j + 1 + i] : qm31_sub(qm31_one(), zt[j + 1 + i]));
+        f00 = qm31_mul(ez, f00);
+        f01 = qm31_mul(ez, f01);
+        f10 = qm31_mul(ez, f10);
+        f11 = qm31_mul(ez, f11);
+      }
+      H00 = qm31_add(H00, f00);
+      H01 = qm31_add(H01, f01);
+      H10 = qm31_add(H10, f10);
+      H11 = qm31_add(H11, f11);
+    }
+    const qm31 Hx = qm31_add(H01, H10);
+    for (int k = 0; k < nx; k++) {
+      const qm31 e1 = xs[k], e0 = qm31_sub(qm31_one(), e1);
+      qm31 p = qm31_add(qm31_mul(qm31_mul(e0, e0), H00),
+                        qm31_add(qm31_mul(qm31_mul(e0, e1), Hx), qm31_mul(qm31_mul(e1, e1), H11)));
+      if (zt) p = qm31_mul(p, qm31_mul(pre, eqlin(zt[j], e1)));
+      out[k] = p;
+    }
+  }
+  // the current round's challenge r: fold to the next round's matrix
+  void fold(const qm31& r) {
+    const int h = dim / 2;
+    const qm31 omr = qm31_sub(qm31_one(), r);
+    const qm31 w00 = qm31_mul(omr, omr), w01 = qm31_mul(omr, r), w11 = qm31_mul(r, r);
+    qm31 N[kMaxSums];
+    for (int a = 0; a < h; a++)
+      for (int b = 0; b < h; b++) {
+        const qm31 cross = qm31_add(F[a * dim + b + h], F[(a + h) * dim + b]);
+        N[a * h + b] = qm31_add(qm31_add(qm31_mul(w00, F[a * dim + b]), qm31_mul(w01, cross)),
+                                qm31_mul(w11, F[(a + h) * dim + b + h]));
+      }
+    for (int q = 0; q < h * h; q++) F[q] = N[q];
+    if (zt) pre = qm31_mul(pre, eqlin(zt[j], r));
+    j++;
+    dim = h;
+  }
+};
 // Round j of a degree-1 trip from its 2^K sums S: p(0), p(1).
 void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out);
 // tw given: the trip is launched ahead of its np pending challenges, which

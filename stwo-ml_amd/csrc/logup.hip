@@ -196,13 +196,18 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
     qm31 g[kMaxSums];
     if (j > 0 && !pre) TRY(launch_j(j, pend));
     TRY(wait_trip(c, sks[j], trip_nq(1, tr.K), g, j > 0 && pre ? tws[j].want : 0));
+    TripGram tg(g, tr.K, z + tr.t, cpre);
     for (int i = 0; i < tr.K; i++) {
       qm31 sums[4];
       {
         HostTimer hg(c, K_HOST_GRAM);
-        trip_round_gram(g, tr.K, i, chal + tr.t, 4, xs, sums, z + tr.t, cpre);
+        tg.values(4, xs, sums);
       }
       absorb3(tr.t + i, sums);
+      if (i + 1 < tr.K) {
+        HostTimer hg(c, K_HOST_GRAM);
+        tg.fold(chal[tr.t + i]);
+      }
     }
     for (int i = 0; i < tr.K; i++) cpre = qm31_mul(cpre, eqlin(z[tr.t + i], chal[tr.t + i]));
     np = tr.K;
@@ -231,26 +236,17 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
   }
   for (int t = t_end; t < nv; t++) {
     const size_t half = E.size() / 2;
-    qm31 sums[4] = {qm31_zero(), qm31_zero(), qm31_zero(), qm31_zero()};
+    qm31 sums[4];
     {
       HostTimer ht(c, K_HOST_FINISH);
-      for (size_t i = 0; i < half; i++) {
-        const qm31 e0 = E[i], e1 = E[i + half], w0v = W[i], w1v = W[i + half], d0v = D[i], d1v = D[i + half];
-        sums[0] = qm31_add(sums[0], qm31_mul(qm31_mul(e0, w0v), d0v));
-        sums[1] = qm31_add(sums[1], qm31_mul(qm31_mul(e1, w1v), d1v));
-        const qm31 de = qm31_sub(e1, e0), dw = qm31_sub(w1v, w0v), dd = qm31_sub(d1v, d0v);
-        const qm31 e2 = qm31_add(e1, de), w2 = qm31_add(w1v, dw), d2 = qm31_add(d1v, dd);
-        sums[2] = qm31_add(sums[2], qm31_mul(qm31_mul(e2, w2), d2));
-        sums[3] = qm31_add(sums[3], qm31_mul(qm31_mul(qm31_add(e2, de), qm31_add(w2, dw)), qm31_add(d2, dd)));
-      }
+      hostfield::eq3_round(qwords(E.data()), qwords(W.data()), qwords(D.data()), half,
+                           reinterpret_cast<uint32_t(*)[4]>(sums));
     }
     absorb3(t, sums);
     HostTimer ht(c, K_HOST_FINISH);
-    for (size_t i = 0; i < half; i++) {
-      E[i] = qm31_fold(E[i], E[i + half], chal[t]);
-      W[i] = qm31_fold(W[i], W[i + half], chal[t]);
-      D[i] = qm31_fold(D[i], D[i + half], chal[t]);
-    }
+    hostfield::fold(qwords(E.data()), half, qwords(&chal[t]));
+    hostfield::fold(qwords(W.data()), half, qwords(&chal[t]));
+    hostfield::fold(qwords(D.data()), half, qwords(&chal[t]));
     E.resize(half);
     W.resize(half);
     D.resize(half);
@@ -528,17 +524,14 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     std::vector<qm31>& V = v[0];
     for (int t = t_end; t < (int)table_log; t++) {
       const size_t half = V.size() / 2;
-      qm31 sums[2] = {qm31_zero(), qm31_zero()};
+      qm31 sums[2];
       {
         HostTimer ht(c, K_HOST_FINISH);
-        for (size_t i = 0; i < half; i++) {
-          sums[0] = qm31_add(sums[0], V[i]);
-          sums[1] = qm31_add(sums[1], V[i + half]);
-        }
+        hostfield::halves_sum(qwords(V.data()), half, reinterpret_cast<uint32_t(*)[4]>(sums));
       }
       absorb1((uint32_t)t, sums);
       HostTimer ht(c, K_HOST_FINISH);
-      for (size_t i = 0; i < half; i++) V[i] = qm31_fold(V[i], V[i + half], alpha);
+      hostfield::fold(qwords(V.data()), half, qwords(&alpha));
       V.resize(half);
     }
     mfin[0] = V[0];

@@ -451,13 +451,18 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
     }
     if (j == 0) TRY(check_point_wait(c));
     if (j == 0 && ft && ft->on_sums) TRY(ft->on_sums(g, tr.K));
+    TripGram tg(g, tr.K, nullptr, qm31_zero());
     for (int i = 0; i < tr.K; i++) {
       qm31 sums[3];
       {
         HostTimer hg(c, K_HOST_GRAM);
-        trip_round_gram(g, tr.K, i, chal.data() + tr.t, 3, xs, sums, nullptr, qm31_zero());
+        tg.values(3, xs, sums);
       }
       absorb(tr.t + i, sums);
+      if (i + 1 < tr.K) {
+        HostTimer hg(c, K_HOST_GRAM);
+        tg.fold(chal[tr.t + i]);
+      }
     }
     np = tr.K;
     pend = chal.data() + tr.t;
@@ -472,22 +477,15 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
   std::vector<qm31>& B = v[1];
   for (int t = t_end; t < T; t++) {
     const size_t half = A.size() / 2;
-    qm31 sums[3] = {qm31_zero(), qm31_zero(), qm31_zero()};
+    qm31 sums[3];
     {
       HostTimer ht(c, K_HOST_FINISH);
-      for (size_t i = 0; i < half; i++) {
-        const qm31 a0 = A[i], a1 = A[i + half], b0 = B[i], b1 = B[i + half];
-        sums[0] = qm31_add(sums[0], qm31_mul(a0, b0));
-        sums[1] = qm31_add(sums[1], qm31_mul(a1, b1));
-        sums[2] = qm31_add(sums[2], qm31_mul(qm31_sub(qm31_add(a1, a1), a0), qm31_sub(qm31_add(b1, b1), b0)));
-      }
+      hostfield::product_round(qwords(A.data()), qwords(B.data()), half, reinterpret_cast<uint32_t(*)[4]>(sums));
     }
     absorb(t, sums);
     HostTimer ht(c, K_HOST_FINISH);
-    for (size_t i = 0; i < half; i++) {
-      A[i] = qm31_fold(A[i], A[i + half], chal[t]);
-      B[i] = qm31_fold(B[i], B[i + half], chal[t]);
-    }
+    hostfield::fold(qwords(A.data()), half, qwords(&chal[t]));
+    hostfield::fold(qwords(B.data()), half, qwords(&chal[t]));
     A.resize(half);
     B.resize(half);
   }

@@ -280,9 +280,11 @@ int mean_var_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* cen, c
     qm31 Gm[kMaxSums];
     const int slot_q = (int)(skq.out - c->h_out);
     for (int q = 0; q < trip_nq(0, tr.K); q++) Gm[q] = c->h_out[slot_q + q];
+    TripGram tg(Gm, tr.K, nullptr, qm31_zero());
     for (int i = 0; i < tr.K; i++) {
       qm31 qv[3], lv[2], s[3];
-      trip_round_gram(Gm, tr.K, i, chal + tr.t, 3, xs, qv, nullptr, qm31_zero());
+      if (i) tg.fold(chal[tr.t + i - 1]);
+      tg.values(3, xs, qv);
       trip_round_sum(L, tr.K, i, chal + tr.t, lv);
       const qm31 l2 = qm31_sub(qm31_add(lv[1], lv[1]), lv[0]);
       s[0] = qm31_add(qm31_mul(eta0, lv[0]), qm31_mul(eta1, qv[0]));

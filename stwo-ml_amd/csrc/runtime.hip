@@ -212,44 +212,6 @@ void lagrange_weights(const qm31* r, int j, qm31* E) {
     }
   }
 }
-void trip_round_gram(const qm31* G, int K, int j, const qm31* r, int nx, const qm31* xs, qm31* out,
-                            const qm31* zt, const qm31& cpre) {
-  const int nu = 1 << j, nv = 1 << (K - j - 1), sh_b = K - j - 1, dim = 1 << K;
-  qm31 E[8];
-  lagrange_weights(r, j, E);
-  qm31 H[2][2] = {{qm31_zero(), qm31_zero()}, {qm31_zero(), qm31_zero()}};
-  for (int v = 0; v < nv; v++) {
-    qm31 ez = qm31_one();
-    if (zt)
-      for (int i = 0; i < K - j - 1; i++)
-        ez = qm31_mul(ez, ((v >> (K - j - 2 - i)) & 1) ? zt[j + 1 + i] : qm31_sub(qm31_one(), zt[j + 1 + i]));
-    for (int b = 0; b < 2; b++)
-      for (int b2 = 0; b2 < 2; b2++) {
-        qm31 acc = qm31_zero();
-        for (int u = 0; u < nu; u++) {
-          const int row = (u << (K - j)) | (b << sh_b) | v;
-          qm31 inner = qm31_zero();
-          for (int u2 = 0; u2 < nu; u2++) {
-            const int col = (u2 << (K - j)) | (b2 << sh_b) | v;
-            inner = qm31_add(inner, qm31_mul(E[u2], G[row * dim + col]));
-          }
-          acc = qm31_add(acc, qm31_mul(E[u], inner));
-        }
-        H[b][b2] = qm31_add(H[b][b2], zt ? qm31_mul(ez, acc) : acc);
-      }
-  }
-  qm31 pre = cpre;
-  if (zt)
-    for (int i = 0; i < j; i++) pre = qm31_mul(pre, eqlin(zt[i], r[i]));
-  for (int k = 0; k < nx; k++) {
-    const qm31 x = xs[k];
-    const qm31 e0 = qm31_sub(qm31_one(), x), e1 = x;
-    qm31 p = qm31_add(qm31_mul(qm31_mul(e0, e0), H[0][0]),
-                      qm31_add(qm31_mul(qm31_mul(e0, e1), qm31_add(H[0][1], H[1][0])), qm31_mul(qm31_mul(e1, e1), H[1][1])));
-    if (zt) p = qm31_mul(p, qm31_mul(pre, eqlin(zt[j], x)));
-    out[k] = p;
-  }
-}
 void trip_round_sum(const qm31* S, int K, int j, const qm31* r, qm31* out) {
   qm31 E[8];
   lagrange_weights(r, j, E);
