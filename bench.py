@@ -43,7 +43,7 @@ HBM_PEAK_GBS = 8000.0
 P = (1 << 31) - 1  # M31
 (K_RESTRICT_COLS, K_RESTRICT_ROWS, K_MM_ROUND, K_EQ3_ROUND, K_LOGUP_PREP, K_EQ_TABLE, K_HOST_FS, K_HOST_WAIT,
  K_HOST_WAIT_TAIL, K_MERKLE, K_HOST_DRAW, K_HOST_LAUNCH, K_HOST_FINISH, K_NORM, K_LOOKUP, K_HOST_GRAM,
- K_HOST_PROOF, K_HOST_WALK_MM, K_HOST_WALK_ACT) = range(19)
+ K_HOST_PROOF, K_HOST_WALK_MM, K_HOST_WALK_ACT, K_WALK_RETRY, K_ACT_AHEAD) = range(21)
 
 QWEN = dict(hidden=5120, inter=13824, q=40 * 128, kv=8 * 128, heads=40, tokens=64)
 SMOL = dict(hidden=576, inter=1536, q=9 * 64, kv=3 * 64, heads=9, tokens=1)
@@ -1054,6 +1054,11 @@ def main():
         ms, nl, _ = ctx.kernel_time(kid)
         if nl:
             host[name] = {"ms_per_step": round(ms / args.steps, 3), "avg_us": round(ms / nl * 1e3, 3), "calls": nl}
+    # counts over the timed steps: activation layers whose first kernels were
+    # launched ahead of their claim point, walk steps proved a second time
+    for kid, name in [(K_ACT_AHEAD, "activations_launched_ahead"), (K_WALK_RETRY, "walk_steps_retried")]:
+        _, nl, _ = ctx.kernel_time(kid)
+        host[name] = nl
     rc = kernels.get("restrict_cols")
     roofline = None
     if rc:

@@ -110,7 +110,9 @@ int gkr_ctx_synchronize(gkr_ctx* ctx);
  * sums; 16 host: proof-record appends; 17 / 18 host: the walk's matmul /
  * activation steps, whole (wall-clock, bytes = 0); 19: walk steps proved a
  * second time because a kernel's bounded wait for the host (about 5.5 s)
- * expired (launches = the count, counted at every timing level). */
+ * expired (launches = the count, counted at every timing level); 20:
+ * activation layers whose first kernels were launched ahead of their claim
+ * point and gamma, beta (launches = the count, at every timing level). */
 /* level 0: off; 1: every 8th launch of ids 0 and 4 (the walk's critical
  * path: a timed dispatch waits about 4 us for its events on each side) and
  * every launch of ids 1, 9, 13 and 14, plus the host timers; 2: every launch
@@ -133,8 +135,10 @@ int gkr_ctx_reset_timing(gkr_ctx* ctx);
  *     kernel ends on the cancel code;
  *   GKR_DEBUG_HANDOVER_EXPIRE: the kernel's bounded wait is `arg` polls and
  *     the host posts only after it expired; the call fails with GKR_ERR_DEVICE.
- *   GKR_DEBUG_TRIP_EXPIRE: the same for the next sumcheck trip launched ahead
- *     of its challenges (that trip's wait expires).
+ *   GKR_DEBUG_TRIP_EXPIRE: the same for the next wait launched ahead of
+ *     its values: a sumcheck trip's challenges, or an activation layer's
+ *     gamma and beta when its first kernels were launched ahead (that wait
+ *     expires).
  * Every kernel exits normally and the context stays usable.                 */
 enum { GKR_DEBUG_HANDOVER_CANCEL = 1, GKR_DEBUG_HANDOVER_EXPIRE = 2, GKR_DEBUG_TRIP_EXPIRE = 3 };
 int gkr_ctx_debug(gkr_ctx* ctx, int op, uint64_t arg);

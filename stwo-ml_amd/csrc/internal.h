@@ -110,7 +110,7 @@ enum KernelId { K_RESTRICT_COLS = 0, K_RESTRICT_ROWS = 1, K_MM_ROUND = 2, K_EQ3_
                 K_EQ_TABLE = 5, K_HOST_FS = 6, K_HOST_WAIT = 7, K_HOST_WAIT_TAIL = 8, K_MERKLE = 9,
                 K_HOST_DRAW = 10, K_HOST_LAUNCH = 11, K_HOST_FINISH = 12, K_NORM = 13, K_LOOKUP = 14,
                 K_HOST_GRAM = 15, K_HOST_PROOF = 16, K_HOST_WALK_MM = 17, K_HOST_WALK_ACT = 18,
-                K_WALK_RETRY = 19, K_NKERNELS = 20 };
+                K_WALK_RETRY = 19, K_ACT_AHEAD = 20, K_NKERNELS = 21 };
 constexpr int kMaxPartialBlocks = 1024;
 constexpr int kMaxSums = 64;  // values per partial row (a 3-round trip's 4^3 cross sums)
 static_assert(kMaxPartialBlocks <= kCountedMaxRows && kCountedMaxRows % kBlock == 0,
@@ -198,6 +198,9 @@ struct gkr_ctx {
   qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
   uint32_t* h_flag = nullptr; // coherent pinned: sequence number of the last delivery
   Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
+  // coherent pinned: values posted after a claim point to kernels launched
+  // ahead of both (an activation layer's gamma and beta, prelaunch_activation)
+  Mailbox* vmailbox = nullptr;
   uint32_t seq = 0;            // last result sequence number handed out
   uint32_t mb_seq = 0;         // last mailbox sequence number handed out
   int timing = 0;  // 0 off; 1: sampled events on the critical-path kernels + host timers; 2: events on every timed kernel
@@ -229,15 +232,26 @@ struct gkr_ctx {
   // launches go through this thread's ring (null: GKR_ASYNC_LAUNCH=0, issued by the caller's thread)
   std::unique_ptr<Launcher> launcher;
   LaunchEvents armed;  // a TimedLaunch's events for the next launch (take_armed)
-  // a matmul restriction launched ahead of its claim point (prelaunch_matmul):
-  // k_point_wait waits for mailbox sequence `want`
+  // kernels launched ahead of their claim point, behind a k_point_wait for
+  // mailbox sequence `want`: a matmul restriction (prelaunch_matmul; a, b the
+  // operands) or an activation layer's first kernels (prelaunch_activation,
+  // act; a the input, with its table and the sinks of its first results)
   struct {
     bool active = false;
+    bool act = false;
     uint32_t want = 0;
     const gkr_matrix* a = nullptr;
     const gkr_matrix* b = nullptr;
+    uint32_t tag = 0, table_log = 0;
+    RoundSink sk_prep, sk_eq0;
+    uint32_t want_vals = 0;  // act: vmailbox sequence of gamma and beta
+    bool hold_vals = false;  // test hook: gamma, beta posted only after that wait expired
   } pre;
+  // (variables, table_log) of the activation layers proved on this context:
+  // their buffers exist, so such a layer's first kernels can be launched ahead
+  std::set<std::pair<int, uint32_t>> act_shapes;
   uint32_t point_mb = 0;  // the posted point's sequence, until the first trip's results confirm it arrived
+  uint32_t vals_mb = 0;   // likewise for values posted through vmailbox
   // set by the walk for one step: called at that step's last launch
   std::function<int()> prelaunch;
   // test hooks (gkr_ctx_debug), each consumed by the next hand-over (or trip launched ahead)
@@ -764,6 +778,12 @@ int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out);
 
 // ------------------------------------------------------------------ launches ahead of a walk step
 int prelaunch_matmul(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, bool* launched);
+int prelaunch_activation(gkr_ctx* c, const gkr_matrix* input, uint32_t tag, uint32_t table_log, bool* launched);
+// S_PTWAIT: k_point_wait's status word at 0, the values' wait status at 64
+// (prelaunch_activation), the copied point at 256, posted values (gamma,
+// beta) at kPtWaitVals
+constexpr size_t kPtWaitVals = 256 + ((sizeof(PointArg) + 15) & ~(size_t)15);
+constexpr size_t kPtWaitBytes = kPtWaitVals + 4 * sizeof(qm31);
 // The current step's last launch is done: launch what the walk queued for the next step.
 inline int run_prelaunch(gkr_ctx* c) {
   if (!c->prelaunch) return GKR_OK;
@@ -773,26 +793,35 @@ inline int run_prelaunch(gkr_ctx* c) {
 }
 // After the first results of a restriction launched ahead: its point wait saw the post.
 inline int check_point_wait(gkr_ctx* c) {
-  if (!c->point_mb) return GKR_OK;
-  const uint32_t w = c->point_mb;
+  const uint32_t w = c->point_mb, v = c->vals_mb;
   c->point_mb = 0;
-  if (__atomic_load_n(&c->mailbox->expired, __ATOMIC_ACQUIRE) == w) {
+  c->vals_mb = 0;
+  if (w && __atomic_load_n(&c->mailbox->expired, __ATOMIC_ACQUIRE) == w) {
     c->wait_expired = true;
-    return fail(GKR_ERR_DEVICE, "restriction launched ahead stopped waiting for its claim point (mailbox %u)", w);
+    return fail(GKR_ERR_DEVICE, "kernels launched ahead stopped waiting for their claim point (mailbox %u)", w);
+  }
+  if (v && __atomic_load_n(&c->vmailbox->expired, __ATOMIC_ACQUIRE) == v) {
+    c->wait_expired = true;
+    return fail(GKR_ERR_DEVICE, "kernels launched ahead stopped waiting for their posted values (mailbox %u)", v);
   }
   return GKR_OK;
 }
-// Drops a restriction launched ahead that will not be used: the cancel code
-// ends its wait, the stream drains, the mailbox is cleared.
+// Drops kernels launched ahead that will not be used: the cancel code ends
+// their waits, the stream drains, the mailboxes are cleared.
 inline void cancel_prelaunch(gkr_ctx* c) {
   c->prelaunch = nullptr;
   if (!c->pre.active) return;
   __atomic_store_n(&c->mailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
+  __atomic_store_n(&c->vmailbox->seq, kWaitCancel, __ATOMIC_RELEASE);
   drain(c);
   (void)hipStreamSynchronize(c->stream);
   __atomic_store_n(&c->mailbox->seq, 0u, __ATOMIC_RELEASE);
+  __atomic_store_n(&c->vmailbox->seq, 0u, __ATOMIC_RELEASE);
   c->pre.active = false;
+  c->pre.act = false;
+  c->pre.hold_vals = false;
   c->point_mb = 0;
+  c->vals_mb = 0;
   c->fb_pending = false;
   c->mm.valid = false;
 }

@@ -368,12 +368,13 @@ static __global__ void __launch_bounds__(kWaitBlock) k_mailbox_wait(TripWait tw,
   tw.status[0] = tw.want;
 }
 
-// A matmul restriction launched ahead of its claim point: k_point_wait (one
-// wave), queued first, waits for mailbox sequence `want`, copies the posted
-// point (n coordinates, with 1 - r) to *out in device memory and sets
-// status[0] = want; k_eq_two reads the point there and returns at once
-// unless the status holds `want`.  A wait that ends without the point
-// (cancel code or spin limit) writes `want` into mb->expired.
+// Kernels launched ahead of their claim point (a matmul's restriction, an
+// activation layer's eq tables): k_point_wait (one wave), queued first, waits
+// for mailbox sequence `want`, copies the posted point (n coordinates, with
+// 1 - r) to *out in device memory and sets status[0] = want; the kernels
+// behind it read the point there and return at once unless the status holds
+// `want`.  A wait that ends without the point (cancel code or spin limit)
+// writes `want` into mb->expired.
 static __global__ void __launch_bounds__(64) k_point_wait(Mailbox* mb, uint32_t want, uint32_t spin_limit, int n,
                                                    PointArg* out, uint32_t* status) {
   int ok = 0;
@@ -402,6 +403,16 @@ static __global__ void __launch_bounds__(64) k_point_wait(Mailbox* mb, uint32_t 
     status[0] = want;  // read by the next kernels of the stream only
   }
 }
+// The values a kernel launched ahead takes from device memory, where a wait
+// queued before it (k_point_wait, k_mailbox_wait) copied them and set
+// status[0] = want (status == nullptr: from its own arguments).
+struct Posted {
+  const uint32_t* status;
+  uint32_t want;
+  const PointArg* pt;  // the claim point
+  const qm31* vals;    // posted values (gamma, beta)
+  __device__ __forceinline__ bool missing() const { return status && status[0] != want; }
+};
 
 // t + (t of lane l ^ m), for every lane.  m = 8: DPP row rotation by 8 (the
 // other half of the 16-lane row); m = 16 / 32: the gfx950 row swaps, whose
@@ -788,17 +799,35 @@ struct EqPartsArg {
   int m[kEqPartsMax];
   uint32_t off[kEqPartsMax];
 };
-static __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out) {
+// The table list is staged in LDS with the point and each entry finds its
+// table by binary search over the (ascending) offsets: a scan of the kernel
+// arguments is one dependent load per table passed.
+// ps.status given: launched ahead, the point comes from ps.pt.
+static __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out, Posted ps) {
+  if (ps.missing()) return;  // the wait ended without the point (every thread alike)
   __shared__ PointLds sp;
-  stage_point(a.z, &sp);
+  __shared__ uint32_t toff[kEqPartsMax];
+  __shared__ int ts[kEqPartsMax], tm[kEqPartsMax];
+  for (int l = threadIdx.x; l < a.count; l += blockDim.x) {
+    toff[l] = a.off[l];
+    ts[l] = a.s[l];
+    tm[l] = a.m[l];
+  }
+  stage_point(ps.status ? *ps.pt : a.z, &sp);  // its barrier also covers the table list
   const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const uint32_t i = (uint32_t)(g / kEqLanes);
   const int q = (int)(g % kEqLanes);
   const bool valid = i < total;
-  int t = 0;
-  while (valid && t + 1 < a.count && i >= a.off[t + 1]) t++;
-  const uint32_t x = valid ? i - a.off[t] : 0;
-  const qm31 v = eq_prod4(sp, a.s[t], a.m[t], x, q, valid);
+  int t = 0, hi = a.count - 1;  // the last table whose offset is <= i
+  while (valid && t < hi) {
+    const int mid = (t + hi + 1) >> 1;
+    if (toff[mid] <= i)
+      t = mid;
+    else
+      hi = mid - 1;
+  }
+  const uint32_t x = valid ? i - toff[t] : 0;
+  const qm31 v = eq_prod4(sp, ts[t], tm[t], x, q, valid);
   if (valid) reinterpret_cast<uint32_t*>(out)[4 * (uint64_t)i + q] = qm31_comp(v, q);
 }
 
@@ -1471,10 +1500,15 @@ struct dot_acc {
 // for j < size: an input entry whose masked value is j has exactly this
 // fraction, so the prepare pass gathers it and the table side weights it by
 // mult[j] (one inversion per table entry instead of one per input entry).
+// ps.status given: launched ahead, gamma and beta are ps.vals[0], ps.vals[1].
 static __global__ void k_logup_inv_table(const uint32_t* __restrict__ table_out, uint64_t size, qm31 gamma,
-                                         qm31 beta, qm31* __restrict__ inv) {
+                                         qm31 beta, qm31* __restrict__ inv, Posted ps) {
   const uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= size) return;
+  if (j >= size || ps.missing()) return;
+  if (ps.status) {
+    gamma = ld_q(ps.vals, 0);
+    beta = ld_q(ps.vals, 1);
+  }
   const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(m31_from_u32((uint32_t)j))),
                           qm31_mul_m31(beta, table_out[j]));
   st_q(inv, j, qm31_inv(d));
@@ -1483,13 +1517,21 @@ static __global__ void k_logup_inv_table(const uint32_t* __restrict__ table_out,
 // the table output, form d = gamma - in - beta*out and w = 1/d (gathered from
 // the inverted table), count multiplicities (gkr/prover.rs:6411-6475).  Per workgroup it accumulates
 // sum(w) and the MLE of the padded input at the claim point,
-// sum_p x_p * eq[p] (prover.rs:6411-6417), into a 2-value sink.
+// sum_p x_p * eq[p] (prover.rs:6411-6417), into a 2-value sink.  ps.status
+// given: launched ahead, gamma and beta are ps.vals[0], ps.vals[1]; when its
+// wait ended without them the pass adds nothing but still delivers (the host
+// reads the wait's expiry before the sums).
 static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
     const uint32_t* __restrict__ table_out, const qm31* __restrict__ inv, uint32_t mask, qm31 gamma, qm31 beta,
     const qm31* __restrict__ eq_hi, const qm31* __restrict__ eq_lo, int eq_h, uint32_t* __restrict__ masked_in,
     uint32_t* __restrict__ masked_out, qm31* __restrict__ d_out, qm31* __restrict__ w_out,
-    uint32_t* __restrict__ mult, RoundSink sink, uint32_t* counter, uint32_t count_base) {
+    uint32_t* __restrict__ mult, RoundSink sink, uint32_t* counter, uint32_t count_base, Posted ps) {
+  const bool go = !ps.missing();
+  if (ps.status && go) {
+    gamma = ld_q(ps.vals, 0);
+    beta = ld_q(ps.vals, 1);
+  }
   const uint64_t lo_mask = (1ull << eq_h) - 1;
   qacc acc;
   acc.zero();
@@ -1506,7 +1548,7 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
   const bool lo_fixed = (stride & lo_mask) == 0;
   dot_acc ih;
   ih.zero();
-  for (uint64_t p0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p0 < n; p0 += kPrepBatch * stride) {
+  for (uint64_t p0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; go && p0 < n; p0 += kPrepBatch * stride) {
     uint32_t x[kPrepBatch];
     bool real[kPrepBatch];
 #pragma unroll
@@ -1550,9 +1592,9 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
   }
   if (lo_fixed) {  // this thread's low index: its first entry's (a thread past n added nothing)
     const uint64_t p0 = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p0 < n) ie.add(qm31_mul(ih.reduce(), ld_q(eq_lo, p0 & lo_mask)));
+    if (go && p0 < n) ie.add(qm31_mul(ih.reduce(), ld_q(eq_lo, p0 & lo_mask)));
   }
-  if (mult && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
+  if (go && mult && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
   qm31 v[2] = {acc.reduce(), ie.reduce()};
   sink_deliver<2>(v, sink, counter, count_base);
 }

@@ -51,20 +51,21 @@ static int device_table(gkr_ctx* c, uint32_t tag, uint32_t log_size, uint32_t** 
 // the eq vector of the remaining variables.  The polynomials, challenges and
 // final values equal those of folding eq like w and d (the polynomial of each
 // round is unique).
-// Plan the trips of an eq-sumcheck over 2^nv entries for claim point z and
-// launch the kernel that builds their eq tables (S_EQPARTS); with_split, the
-// same launch builds the two halves of eq(z, .) (Eq3Plan::split_*).
-int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl, bool with_split) {
+// Plan the trips of an eq-sumcheck over 2^nv entries and the eq tables they
+// read (with_split, also the two halves of eq(z, .), Eq3Plan::split_*): the
+// tables' list for k_eq_parts (its point left to the caller), offsets into
+// S_EQPARTS.  arg->count == 0: no tables.
+static int eq3_plan(int nv, bool with_split, Eq3Plan* pl, EqPartsArg* arg_out, uint32_t* total_out) {
   pl->nv = nv;
   pl->trips = plan_trips(nv, kHostTailEq3, trip_k(1ull << nv));
   pl->hi_off.clear();
   pl->lo_off.clear();
   pl->h.clear();
-  if (pl->trips.empty() && !with_split) return GKR_OK;
-  EqPartsArg arg;
+  EqPartsArg& arg = *arg_out;
   memset(&arg, 0, sizeof arg);
-  arg.z = make_point(z, nv);
-  uint32_t total = 0;
+  uint32_t& total = *total_out;
+  total = 0;
+  if (pl->trips.empty() && !with_split) return GKR_OK;
   auto table = [&](int s0, int m) -> uint32_t {
     for (int i = 0; i < arg.count; i++)
       if (arg.s[i] == s0 && arg.m[i] == m) return arg.off[i];
@@ -89,14 +90,30 @@ int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl, bool with_split)
     pl->split_hi_off = table(0, nv - pl->split_h);
     pl->split_lo_off = table(nv - pl->split_h, pl->split_h);
   }
+  return GKR_OK;
+}
+// The eq tables of a plan (ps.status given: the point from k_point_wait).
+static int launch_eq_parts(gkr_ctx* c, const EqPartsArg& arg, uint32_t total, const Posted& ps) {
   HostTimer ht(c, K_HOST_LAUNCH);
   qm31* parts;
   TRY(ensureT(c, S_EQPARTS, total, &parts));
   {
     TimedLaunch tl(c, K_EQ_TABLE, 16ull * total);
-    GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(kEqLanes * (uint64_t)total)), dim3(kBlock), 0, arg, total, parts);
+    GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(kEqLanes * (uint64_t)total)), dim3(kBlock), 0, arg, total, parts, ps);
   }
   return check_launch(c);
+}
+// Plan an eq-sumcheck over 2^nv entries for claim point z and launch the
+// kernel that builds its eq tables (S_EQPARTS).
+int eq3_prepare(gkr_ctx* c, const qm31* z, int nv, Eq3Plan* pl, bool with_split) {
+  EqPartsArg arg;
+  uint32_t total;
+  TRY(eq3_plan(nv, with_split, pl, &arg, &total));
+  if (!arg.count) return GKR_OK;
+  arg.z = make_point(z, nv);
+  Posted ps;
+  memset(&ps, 0, sizeof ps);
+  return launch_eq_parts(c, arg, total, ps);
 }
 // Launch trip j of the plan over sources w, d (np pending challenges pend),
 // folded vectors to dw, dd when given.
@@ -257,6 +274,126 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
   return GKR_OK;
 }
 
+// The activation layer's first launches, in the order the host reads their
+// results: the table's fractions (one inversion per table entry), the prepare
+// pass (trace sum and input MLE at the claim point, slot kSlotPrep) and the
+// eq-sumcheck's first trip (slot kSlotEq0).  ps.status given: launched ahead,
+// gamma and beta come from k_point_wait's copies.  The buffers exist.
+static int logup_first_launches(gkr_ctx* c, const gkr_matrix* input, uint64_t n, const uint32_t* d_table,
+                                uint32_t table_log, bool lds_hist, qm31 gamma, qm31 beta, const Eq3Plan& epl,
+                                const Posted& ps, RoundSink* sk_prep, RoundSink* sk_eq0) {
+  const uint64_t tsize = 1ull << table_log;
+  const uint64_t pcol = next_pow2(input->cols);
+  uint32_t *d_mult, *d_min, *d_mout;
+  qm31 *d_d0, *d_w0, *d_inv;
+  TRY(ensureT(c, S_MULT, tsize, &d_mult));
+  TRY(ensureT(c, S_MIN, n, &d_min));
+  TRY(ensureT(c, S_MOUT, n, &d_mout));
+  TRY(ensureT(c, S_D0, n, &d_d0));
+  TRY(ensureT(c, S_W0, n, &d_w0));
+  TRY(ensureT(c, S_LKINV, tsize, &d_inv));
+  const qm31* eq_hi = (const qm31*)c->buf[S_EQPARTS] + epl.split_hi_off;
+  const qm31* eq_lo = (const qm31*)c->buf[S_EQPARTS] + epl.split_lo_off;
+  HostTimer ht(c, K_HOST_LAUNCH);
+  GKR_LAUNCH(c, k_logup_inv_table, dim3(grid_for(tsize)), dim3(kBlock), 0, d_table, tsize, gamma, beta, d_inv, ps);
+  TRY(check_launch(c));
+  TRY(make_sink(c, sk_prep, kSlotPrep));
+  {
+    uint32_t* counter;
+    uint32_t base;
+    const unsigned grid = partial_grid(n);
+    TRY(deliver_args(c, grid, &counter, &base));
+    // algorithmic bytes: the input, masked input and output written (8 per entry), d and w written
+    TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 8 * n + 32 * n, true);
+    GKR_LAUNCH(c, k_logup_prepare, dim3(grid), dim3(kBlock), 0, input->dev, input->rows, input->cols,
+               log2_exact(pcol), n, d_table, d_inv, (uint32_t)(tsize - 1), gamma, beta, eq_hi, eq_lo, epl.split_h,
+               d_min, d_mout, d_d0, d_w0, lds_hist ? nullptr : d_mult, *sk_prep, counter, base, ps);
+    TRY(deliver_finish<2>(c, *sk_prep, grid, counter));
+  }
+  if (epl.nv > 0) TRY(eq3_launch_trip(c, epl, 0, d_w0, d_d0, 0, nullptr, nullptr, nullptr, kSlotEq0, sk_eq0));
+  return GKR_OK;
+}
+
+// An activation layer's first kernels launched ahead of its claim point and
+// gamma, beta: k_point_wait and the eq tables (the point only), then
+// k_mailbox_wait on vmailbox, the table's inversion, the prepare pass and the
+// eq-sumcheck's first trip, reading the posted values from device memory.
+// gkr_prove_activation_layer posts the point as it starts and gamma, beta once
+// drawn, so the eq tables are built while the host draws.  Launched only
+// when nothing has to be allocated or uploaded on the way (growing a buffer
+// synchronises with the stream, whose earlier kernels may wait for the host):
+// this context has proved an activation of the same size before (buffers
+// only grow), the table is resident and small enough for the LDS
+// multiplicities.  *launched reports whether it was.
+int prelaunch_activation(gkr_ctx* c, const gkr_matrix* input, uint32_t tag, uint32_t table_log, bool* launched) {
+  *launched = false;
+  if (c->noalloc || c->pre.active || !input || input->ctx != c || !act_logup_valid(tag)) return GKR_OK;
+  if (table_log == 0) table_log = act_default_log_size(tag);
+  const uint64_t n = next_pow2(input->rows) * next_pow2(input->cols);
+  const int nv = log2_exact(n);
+  const uint64_t tsize = 1ull << table_log;
+  if (nv == 0 || nv > kMaxVars || table_log > 24 || tsize > (uint64_t)kHistBins || n < 4) return GKR_OK;
+  if (!c->act_shapes.count(std::make_pair(nv, table_log))) return GKR_OK;
+  const auto it = c->dev_tables.find(((uint64_t)tag << 32) | table_log);
+  if (it == c->dev_tables.end()) return GKR_OK;
+  if (c->cap[S_PTWAIT] < kPtWaitBytes) return GKR_OK;
+  Eq3Plan epl;
+  EqPartsArg arg;
+  uint32_t total;
+  TRY(eq3_plan(nv, true, &epl, &arg, &total));
+  uint8_t* pw;
+  TRY(ensureT(c, S_PTWAIT, kPtWaitBytes, &pw));
+  Posted pp;  // the point
+  memset(&pp, 0, sizeof pp);
+  pp.status = reinterpret_cast<const uint32_t*>(pw);
+  pp.want = alloc_seq(&c->mb_seq, 1);
+  pp.pt = reinterpret_cast<const PointArg*>(pw + 256);
+  {
+    HostTimer ht(c, K_HOST_LAUNCH);
+    GKR_LAUNCH(c, k_point_wait, dim3(1), dim3(64), 0, c->mailbox, pp.want, kWaitSpinLimit, nv,
+               reinterpret_cast<PointArg*>(pw + 256), reinterpret_cast<uint32_t*>(pw));
+    TRY(check_launch(c));
+  }
+  c->pre.active = true;  // from here on a failure leaves a wait that the walk cancels
+  c->pre.act = true;
+  c->pre.want = pp.want;
+  c->pre.a = input;
+  c->pre.b = nullptr;
+  c->pre.tag = tag;
+  c->pre.table_log = table_log;
+  c->pre.hold_vals = false;
+  c->mm.valid = false;
+  TRY(launch_eq_parts(c, arg, total, pp));
+  TripWait tw;  // gamma and beta, copied to device memory for the kernels behind it
+  tw.mb = c->vmailbox;
+  tw.want = alloc_seq(&c->mb_seq, 1);
+  tw.spin_limit = kWaitSpinLimit;
+  if (c->debug_trip_spins) {  // test hook: a short bounded wait that expires before the post
+    tw.spin_limit = c->debug_trip_spins;
+    c->debug_trip_spins = 0;
+    c->pre.hold_vals = true;
+  }
+  tw.status = reinterpret_cast<uint32_t*>(pw + 64);
+  tw.chal = reinterpret_cast<qm31*>(pw + kPtWaitVals);
+  c->pre.want_vals = tw.want;
+  {
+    HostTimer ht(c, K_HOST_LAUNCH);
+    CarriedFinish none;
+    memset(&none, 0, sizeof none);
+    GKR_LAUNCH(c, k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, tw, 2, none);
+    TRY(check_launch(c));
+  }
+  Posted pv;  // gamma and beta
+  memset(&pv, 0, sizeof pv);
+  pv.status = tw.status;
+  pv.want = tw.want;
+  pv.vals = tw.chal;
+  TRY(logup_first_launches(c, input, n, it->second, table_log, true, qm31_zero(), qm31_zero(), epl, pv,
+                           &c->pre.sk_prep, &c->pre.sk_eq0));
+  *launched = true;
+  return GKR_OK;
+}
+
 extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
                                           const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t tag,
                                           uint32_t table_log, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out) {
@@ -287,7 +424,6 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   TraceScope trace;
   PoseidonChannel& C = ch->ch;
   const uint64_t tsize = 1ull << table_log;
-  const uint32_t mask = (uint32_t)(tsize - 1);
 
   uint32_t *d_table, *d_mult, *d_min, *d_mout;
   qm31 *d_d0, *d_d1, *d_w0, *d_w1, *m0, *m1, *d_inv;
@@ -312,15 +448,33 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     if (c->mult_zero_entries < tsize) HIP_TRY(hipMemsetAsync(d_mult, 0, tsize * sizeof(uint32_t), c->stream));
     c->mult_zero_entries = 0;
   }
-  // One launch builds the eq tables of the eq-sumcheck trips and eq(claim
-  // point, x) as the product of its high and low halves (for the input MLE at
-  // the claim point, accumulated by the prepare pass): the claim point only,
-  // so it runs while the host draws gamma and beta
+  // The layer's first kernels (the eq tables, the table's inversion, the
+  // prepare pass and the eq-sumcheck's first trip) are launched ahead when
+  // they can be: by the walk at the previous step's last launch, or here,
+  // before the host draws gamma and beta (the launch calls then overlap the
+  // draws); they wait on the device for the claim point and gamma, beta.
+  // Otherwise one launch builds the eq tables of the eq-sumcheck trips and
+  // eq(claim point, x) as the product of its high and low halves (for the
+  // input MLE at the claim point, accumulated by the prepare pass) while the
+  // host draws gamma and beta, and the rest follows the draws.
+  bool pre = c->pre.active && c->pre.act && c->pre.a == input && c->pre.tag == tag && c->pre.table_log == table_log;
+  if (!pre && !c->pre.active) {  // nothing queued waits for the host: the wait's buffer may be allocated
+    uint8_t* pw;
+    TRY(ensureT(c, S_PTWAIT, kPtWaitBytes, &pw));
+    TRY(prelaunch_activation(c, input, tag, table_log, &pre));
+  }
   Eq3Plan epl;
-  TRY(eq3_prepare(c, cpt.data(), nv, &epl, true));
-  const qm31* eq_hi = (const qm31*)c->buf[S_EQPARTS] + epl.split_hi_off;
-  const qm31* eq_lo = (const qm31*)c->buf[S_EQPARTS] + epl.split_lo_off;
-  const int eq_h = epl.split_h;
+  if (pre) {  // post the claim point: the eq tables are built while the host draws gamma and beta
+    Mailbox* mb = c->mailbox;
+    for (int l = 0; l < nv; l++) mb->point[l] = cpt[l];
+    __atomic_store_n(&mb->seq, c->pre.want, __ATOMIC_RELEASE);
+    c->point_mb = c->pre.want;  // checked once the prepare sums are in
+    EqPartsArg arg;
+    uint32_t total;
+    TRY(eq3_plan(nv, true, &epl, &arg, &total));
+  } else {
+    TRY(eq3_prepare(c, cpt.data(), nv, &epl, true));
+  }
 
   // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
   C.mix_u64(0x4C4F47ull);
@@ -341,26 +495,29 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   //   multiplicity sumcheck trip 0 (no challenge needed)         kSlotMult0
   RoundSink sk_prep, sk_table, sk_mult0, sk_eq0;
   const bool eq_pre = nv > 0;
-  {
-    HostTimer ht(c, K_HOST_LAUNCH);
-    // the table's fractions: one inversion per table entry
-    GKR_LAUNCH(c, k_logup_inv_table, dim3(grid_for(tsize)), dim3(kBlock), 0, d_table, tsize, gamma,
-                       beta, d_inv);
-    TRY(check_launch(c));
-    TRY(make_sink(c, &sk_prep, kSlotPrep));
-    uint32_t* counter;
-    uint32_t base;
-    {
-      const unsigned grid = partial_grid(n);
-      TRY(deliver_args(c, grid, &counter, &base));
-      // algorithmic bytes: the input, masked input and output written (8 per entry), d and w written
-      TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 8 * n + 32 * n, true);
-      GKR_LAUNCH(c, k_logup_prepare, dim3(grid), dim3(kBlock), 0, input->dev, input->rows,
-                         input->cols, log2_exact(pcol), n, d_table, d_inv, mask, gamma, beta, eq_hi, eq_lo, eq_h,
-                         d_min, d_mout, d_d0, d_w0, lds_hist ? nullptr : d_mult, sk_prep, counter, base);
-      TRY(deliver_finish<2>(c, sk_prep, grid, counter));
+  if (pre) {  // post gamma and beta
+    Mailbox* vmb = c->vmailbox;
+    const uint32_t want = c->pre.want_vals;
+    if (c->pre.hold_vals) {  // test hook: post only after the bounded wait gave up
+      const auto t0 = std::chrono::steady_clock::now();
+      volatile uint32_t* expired = &vmb->expired;
+      while (*expired != want && std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() < 10.0) {
+      }
+      c->pre.hold_vals = false;
     }
-    if (eq_pre) TRY(eq3_launch_trip(c, epl, 0, d_w0, d_d0, 0, nullptr, nullptr, nullptr, kSlotEq0, &sk_eq0));
+    vmb->alpha[0] = gamma;
+    vmb->alpha[1] = beta;
+    __atomic_store_n(&vmb->seq, want, __ATOMIC_RELEASE);
+    c->vals_mb = want;  // checked once the prepare sums are in
+    sk_prep = c->pre.sk_prep;
+    sk_eq0 = c->pre.sk_eq0;
+    c->pre.active = false;
+    c->pre.act = false;
+    c->stats[K_ACT_AHEAD].launches++;
+  } else {
+    Posted ps;
+    memset(&ps, 0, sizeof ps);
+    TRY(logup_first_launches(c, input, n, d_table, table_log, lds_hist, gamma, beta, epl, ps, &sk_prep, &sk_eq0));
   }
   // The table side (multiplicities, their copies, the table-side sum) and the
   // multiplicity sumcheck's first trip are needed only after the eq-sumcheck:
@@ -414,6 +571,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   // eq-sumcheck rounds.
   qm31 prep[2];
   TRY(wait_sink<2>(c, sk_prep, prep));
+  TRY(check_point_wait(c));
   const qm31 trace_sum = prep[0], input_eval = prep[1];
   C.mix_secure_field(trace_sum);
   out->claimed_sum = G(trace_sum);
@@ -578,6 +736,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     L.mult_sum = mult_sum;
     proof_add_layer(proof, std::move(L));
   }
+  c->act_shapes.insert(std::make_pair(nv, table_log));
   return GKR_OK;
 }
 

@@ -237,11 +237,11 @@ int prelaunch_matmul(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, bool*
   if (plan_restrict(A, B, pk, false, &p) != GKR_OK) return GKR_OK;
   std::vector<std::pair<Slot, size_t>> bufs;
   restrict_buffers(p, &bufs);
-  bufs.push_back({S_PTWAIT, sizeof(PointArg) + 256});
+  bufs.push_back({S_PTWAIT, kPtWaitBytes});
   for (const auto& sb : bufs)
     if (c->cap[sb.first] < sb.second) return GKR_OK;
   uint8_t* pw;
-  TRY(ensureT(c, S_PTWAIT, sizeof(PointArg) + 256, &pw));
+  TRY(ensureT(c, S_PTWAIT, kPtWaitBytes, &pw));
   DevicePoint dp;
   dp.pt = reinterpret_cast<const PointArg*>(pw + 256);
   dp.status = reinterpret_cast<const uint32_t*>(pw);
@@ -253,6 +253,7 @@ int prelaunch_matmul(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, bool*
     TRY(check_launch(c));
   }
   c->pre.active = true;  // from here on a failure leaves a wait that the walk cancels
+  c->pre.act = false;
   c->pre.want = dp.want;
   c->pre.a = A;
   c->pre.b = B;
@@ -306,7 +307,7 @@ static int validate_matmul(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b,
 
 static int ensure_restricted(gkr_ctx* c, const gkr_matrix* a, const gkr_matrix* b, const gkr_qm31* r_i, uint32_t n_ri,
                              const gkr_qm31* r_j, uint32_t n_rj) {
-  if (c->pre.active && c->pre.a == a && c->pre.b == b) {  // launched ahead: post the point
+  if (c->pre.active && !c->pre.act && c->pre.a == a && c->pre.b == b) {  // launched ahead: post the point
     for (uint32_t l = 0; l < n_ri + n_rj; l++) {
       const gkr_qm31& x = l < n_ri ? r_i[l] : r_j[l - n_ri];
       if (!canonical_q(x)) return fail(GKR_ERR_INVALID, "claim point coordinate %u not canonical", l);

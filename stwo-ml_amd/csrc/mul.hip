@@ -151,7 +151,9 @@ extern "C" int gkr_mul_output_claim(gkr_ctx* c, const gkr_matrix* lhs, const gkr
   const uint32_t total = arg.off[1] + (1u << h);
   qm31* parts;
   TRY(ensureT(c, S_EQPARTS, total, &parts));
-  GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(kEqLanes * (uint64_t)total)), dim3(kBlock), 0, arg, total, parts);
+  Posted ps;
+  memset(&ps, 0, sizeof ps);
+  GKR_LAUNCH(c, k_eq_parts, dim3(grid_for(kEqLanes * (uint64_t)total)), dim3(kBlock), 0, arg, total, parts, ps);
   TRY(check_launch(c));
   RoundSink sk;
   TRY(launch_trip(c, 1, 0, d_w0, d_d0, n, 0, nullptr, nullptr, nullptr, parts, parts + arg.off[1], h, 0, &sk));

@@ -334,7 +334,8 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
     return fail(GKR_ERR_DEVICE, "hipStreamCreate failed");
   }
   if (hipHostMalloc((void**)&c->h_res, 64 * sizeof(qm31), hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&c->h_out, kOutSlots * sizeof(qm31) + 128 + sizeof(Mailbox), hipHostMallocCoherent | hipHostMallocMapped) !=
+      hipHostMalloc((void**)&c->h_out, kOutSlots * sizeof(qm31) + 128 + 2 * sizeof(Mailbox),
+                    hipHostMallocCoherent | hipHostMallocMapped) !=
           hipSuccess) {
     gkr_ctx_destroy(c);
     return fail(GKR_ERR_DEVICE, "context buffer allocation failed");
@@ -358,6 +359,9 @@ extern "C" int gkr_ctx_create(int device, gkr_ctx** out) {
   c->mailbox = reinterpret_cast<Mailbox*>(reinterpret_cast<char*>(c->h_out) + kOutSlots * sizeof(qm31) + 128);
   c->mailbox->seq = 0;
   c->mailbox->expired = 0;
+  c->vmailbox = c->mailbox + 1;
+  c->vmailbox->seq = 0;
+  c->vmailbox->expired = 0;
   // Launches are issued by a thread of their own unless GKR_ASYNC_LAUNCH=0
   // (the launch cost then falls on the caller's thread).
   const char* al = getenv("GKR_ASYNC_LAUNCH");

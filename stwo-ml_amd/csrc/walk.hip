@@ -17,7 +17,10 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
   // A fresh matmul step whose predecessor is a matmul or activation step has
   // its restriction launched ahead, at the predecessor's last launch, waiting
   // on the device for its claim point (prelaunch_matmul): the host then only
-  // posts the point.  Whatever is left of it on any exit is cancelled.
+  // posts the point.  A LogUp activation step after such a step has its first
+  // kernels launched the same way (prelaunch_activation), waiting for its
+  // claim point and gamma, beta.  Whatever is left of it on any exit is
+  // cancelled.
   struct PreGuard {
     gkr_ctx* c;
     ~PreGuard() { cancel_prelaunch(c); }
@@ -25,24 +28,45 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
   auto fused_matmul = [](const gkr_step& s) {
     return s.kind == GKR_STEP_MATMUL && s.claim == GKR_CLAIM_FRESH && s.a && s.b && s.a->cols > 1;
   };
+  auto table_log_of = [](const gkr_step& s) {
+    return s.table_log_size ? s.table_log_size : act_default_log_size(s.activation_type);
+  };
+  auto logup_act = [](const gkr_step& s) {
+    return s.kind == GKR_STEP_ACTIVATION && s.a && act_valid(s.activation_type) && act_logup_valid(s.activation_type);
+  };
+  // the kernels launched ahead are the ones step s needs
+  auto pre_matches = [&](const gkr_step& s) {
+    if (c->pre.act)
+      return logup_act(s) && c->pre.a == s.a && c->pre.tag == s.activation_type && c->pre.table_log == table_log_of(s);
+    return fused_matmul(s) && c->pre.a == s.a && c->pre.b == s.b;
+  };
   if (n_steps > 1) {
     uint8_t* pw;
-    TRY(ensureT(c, S_PTWAIT, sizeof(PointArg) + 256, &pw));
+    TRY(ensureT(c, S_PTWAIT, kPtWaitBytes, &pw));
   }
   for (size_t si = 0; si < n_steps; si++) {
     const gkr_step& st = steps[si];
     if (!st.a) return fail(GKR_ERR_INVALID, "step %zu: null matrix", si);
-    if (c->pre.active && !(fused_matmul(st) && c->pre.a == st.a && c->pre.b == st.b)) cancel_prelaunch(c);
+    if (c->pre.active && !pre_matches(st)) cancel_prelaunch(c);
     auto prove_step = [&]() -> int {
       c->prelaunch = nullptr;
-      if (si + 1 < n_steps && fused_matmul(steps[si + 1]) &&
-          (fused_matmul(st) || st.kind == GKR_STEP_ACTIVATION)) {
-        const gkr_matrix* na = steps[si + 1].a;
-        const gkr_matrix* nb = steps[si + 1].b;
-        c->prelaunch = [c, na, nb]() -> int {
-          bool launched;
-          return prelaunch_matmul(c, na, nb, &launched);
-        };
+      if (si + 1 < n_steps && (fused_matmul(st) || st.kind == GKR_STEP_ACTIVATION)) {
+        const gkr_step& ns = steps[si + 1];
+        if (fused_matmul(ns)) {
+          const gkr_matrix* na = ns.a;
+          const gkr_matrix* nb = ns.b;
+          c->prelaunch = [c, na, nb]() -> int {
+            bool launched;
+            return prelaunch_matmul(c, na, nb, &launched);
+          };
+        } else if (logup_act(ns)) {
+          const gkr_matrix* na = ns.a;
+          const uint32_t tag = ns.activation_type, tl = table_log_of(ns);
+          c->prelaunch = [c, na, tag, tl]() -> int {
+            bool launched;
+            return prelaunch_activation(c, na, tag, tl, &launched);
+          };
+        }
       }
       if (st.kind == GKR_STEP_MATMUL) {
         HostTimer hw(c, K_HOST_WALK_MM);

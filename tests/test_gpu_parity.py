@@ -486,6 +486,144 @@ def test_walk_retries_a_step_whose_wait_expired(gpu_ctx):
     assert gpu_ctx.kernel_time(19)[1] == 1
 
 
+ACT_KEYS = ("claimed_sum", "eq_round_polys", "final_evals", "mult_round_polys", "mult_final_eval",
+            "mult_claimed_sum", "input_eval", "output_eval", "table_commitment")
+
+
+def test_activation_layer_launched_ahead():
+    """An activation layer of a size its context has proved before has its first kernels (eq tables,
+    the table's inversion, the prepare pass, the eq-sumcheck's first trip) launched before the host
+    draws gamma and beta; they wait on the device for the posted claim point and gamma, beta.  Five
+    layers in a row on one context (two sizes of table, different inputs and claims): every output
+    and the transcript equal the oracle's, and counter id 20 counts the three launched ahead."""
+    log("case activation layer launched ahead")
+    ctx = G.Context(0)
+    try:
+        for i, (tag, tlog) in enumerate([(5, 12), (5, 12), (5, 12), (3, 10), (3, 10)]):
+            X = O.synthetic(12, 40, 0, 700 + i)
+            nv = lg(12) + lg(40)
+            gch, och = G.PoseidonChannel(), O.Channel()
+            gch.mix_u64(i)
+            och.mix_u64(i)
+            pt = gch.draw_qm31s(nv)
+            val = gch.draw_qm31()
+            assert pt == och.draw_qm31s(nv) and val == och.draw_qm31()
+            pg = ctx.prove_activation_layer(pt, val, ctx.upload(X), tag, gch, tlog)
+            po = O.prove_activation_layer(pt, val, X, tag, och, tlog)
+            for key in ACT_KEYS:
+                assert pg[key] == po[key], (i, key)
+            assert (pg["multiplicities"] == po["multiplicities"]).all()
+            assert gch.digest() == och.digest()
+        assert ctx.kernel_time(20)[1] == 3
+    finally:
+        ctx.close()
+
+
+def test_walk_activation_launched_ahead():
+    """Walk steps MatMul, activation (fresh claim), MatMul, activation (chained claim), MatMul: once
+    the context has proved an activation of that size, an activation step's first kernels are
+    launched at the previous step's last launch and wait on the device for the claim point and
+    gamma, beta, which the step posts.  Two walks on one context (one and two steps launched ahead,
+    counter id 20) both equal the oracle's transcript and serialized proof."""
+    log("case walk activation launched ahead")
+    A1, B1 = O.synthetic(4, 64, 1, 81), O.synthetic(64, 32, 1, 82)
+    A2, B2 = O.synthetic(4, 32, 1, 83), O.synthetic(32, 16, 1, 84)
+    A3, B3 = O.synthetic(2, 48, 1, 85), O.synthetic(48, 8, 1, 86)
+    S = O.synthetic(8, 16, 0, 87)  # 2^7 entries, as A2
+    och = O.Channel()
+    och.mix_u64(21)
+    ref = [5]
+    last = None
+    for kind, a, b in [(0, A1, B1), (3, S, None), (0, A2, B2), (4, A2, None), (0, A3, B3)]:
+        if kind == 0:
+            r = och.draw_qm31s(lg(a.shape[0]) + lg(b.shape[1]))
+            v = O.matmul_output_claim(a, b, r)
+            och.mix_secure_field(v)
+            o = O.prove_matmul_layer(r, v, a, b, och)
+            O.serialize_matmul_layer(ref, o["round_polys"], o["final_a_eval"], o["final_b_eval"])
+            last = (o["next_point"], o["next_value"])
+        else:
+            if kind == 3:
+                r = och.draw_qm31s(lg(a.shape[0]) + lg(a.shape[1]))
+                v = och.draw_qm31()
+            else:
+                r, v = last
+            o = O.prove_activation_layer(r, v, a, 5, och, 12)
+            O.serialize_activation_layer(ref, 5, o)
+            last = (r, o["input_eval"])
+    O.serialize_tail(ref, last[0], last[1], [], 0)
+    ctx = G.Context(0)
+    try:
+        gs = [ctx.upload(M) for M in (A1, B1, A2, B2, A3, B3, S)]
+        F, Ch = G.CLAIM_FRESH, G.CLAIM_CHAINED
+        steps = [(G.STEP_MATMUL, F, gs[0], gs[1], 0, 0), (G.STEP_ACTIVATION, F, gs[6], None, 5, 12),
+                 (G.STEP_MATMUL, F, gs[2], gs[3], 0, 0), (G.STEP_ACTIVATION, Ch, gs[2], None, 5, 12),
+                 (G.STEP_MATMUL, F, gs[4], gs[5], 0, 0)]
+        for ahead in (1, 3):
+            ch = G.PoseidonChannel()
+            ch.mix_u64(21)
+            proof = G.Proof()
+            fp, fv = G.prove_walk(ctx, ch, steps, proof)
+            assert (fp, fv) == last
+            assert ch.digest() == och.digest()
+            proof.set_input_claim(fp, fv)
+            assert proof.serialize() == ref
+            assert ctx.kernel_time(20)[1] == ahead
+    finally:
+        ctx.close()
+
+
+def test_activation_values_wait_expired():
+    """An activation layer whose first kernels were launched ahead, with the test hook cutting the
+    bounded wait for its gamma and beta to 4 polls (it expires before the host posts them): a walk
+    proves that step again (counter id 19) and gives the same proof as an undisturbed walk; a direct
+    call fails with GKR_ERR_DEVICE, and the next call equals the oracle's layer."""
+    log("case activation values wait expired")
+    S = O.synthetic(8, 16, 0, 91)
+    A, B = O.synthetic(4, 32, 1, 92), O.synthetic(32, 16, 1, 93)
+    ctx = G.Context(0)
+    try:
+        gs, ga, gb = ctx.upload(S), ctx.upload(A), ctx.upload(B)
+        F = G.CLAIM_FRESH
+        steps = [(G.STEP_ACTIVATION, F, gs, None, 5, 12), (G.STEP_MATMUL, F, ga, gb, 0, 0)]
+
+        def walk():
+            ch = G.PoseidonChannel()
+            ch.mix_u64(31)
+            proof = G.Proof()
+            fp, fv = G.prove_walk(ctx, ch, steps, proof)
+            proof.set_input_claim(fp, fv)
+            return ch.digest(), proof.serialize()
+
+        first = walk()  # the context's first activation of this size: proved the ordinary way
+        assert walk() == first and ctx.kernel_time(20)[1] == 1
+        ctx.reset_timing()
+        ctx.debug(G.DEBUG_TRIP_EXPIRE, 4)
+        assert walk() == first
+        assert ctx.kernel_time(19)[1] == 1
+        assert walk() == first
+        assert ctx.kernel_time(19)[1] == 1
+        nv = lg(8) + lg(16)
+        for expire in (True, False):
+            gch, och = G.PoseidonChannel(), O.Channel()
+            pt = gch.draw_qm31s(nv)
+            val = gch.draw_qm31()
+            assert pt == och.draw_qm31s(nv) and val == och.draw_qm31()
+            if expire:
+                ctx.debug(G.DEBUG_TRIP_EXPIRE, 4)
+                with pytest.raises(G.GkrError) as e:
+                    ctx.prove_activation_layer(pt, val, gs, 5, gch, 12)
+                assert e.value.code == 2 and "posted values" in str(e.value)
+                continue
+            pg = ctx.prove_activation_layer(pt, val, gs, 5, gch, 12)
+            po = O.prove_activation_layer(pt, val, S, 5, och, 12)
+            for key in ACT_KEYS:
+                assert pg[key] == po[key], key
+            assert gch.digest() == och.digest()
+    finally:
+        ctx.close()
+
+
 def _trip_walk(ctx, mats):
     """Fresh MatMul (k = 4096: its second trip is launched ahead), SiLU LogUp over 2^16 entries (eq and
     multiplicity trips launched ahead), MatMul; returns (digest, serialized proof)."""
