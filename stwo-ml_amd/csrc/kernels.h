@@ -36,6 +36,33 @@ __device__ __forceinline__ void stage_point(const PointArg& pt, PointLds* sp) {
   }
   __syncthreads();
 }
+static_assert(kMaxVars <= kBlock, "one lane per coordinate slot");
+// A point that k_point_wait copied to device memory (valid when
+// status[0] == want), staged like stage_point: the status, the length and
+// every coordinate slot are loaded together, one memory round trip, and
+// checked afterwards.  false (every thread alike, before any barrier): the
+// wait ended without the point.  Workgroups of at least kMaxVars threads.
+__device__ __forceinline__ bool stage_posted_point(const PointArg* __restrict__ dpt,
+                                                   const uint32_t* __restrict__ status, uint32_t want,
+                                                   PointLds* sp, int* n_out) {
+  const uint32_t st = status[0];
+  const int n = dpt->n;
+  const int l = threadIdx.x;
+  qm31 r = qm31_zero(), omr = qm31_zero();
+  if (l < kMaxVars) {
+    r = dpt->r[l];
+    omr = dpt->omr[l];
+  }
+  __asm__ volatile("" ::: "memory");  // keeps the loads above the branch
+  if (st != want) return false;
+  if (l < n) {
+    sp->r[l] = r;
+    sp->omr[l] = omr;
+  }
+  __syncthreads();
+  *n_out = n;
+  return true;
+}
 
 // eq factor product prod_{l < m} (bit m-1-l of x ? r[s+l] : 1 - r[s+l]) from
 // the staged point, as two interleaved chains (even and odd l) so one wave
@@ -287,8 +314,9 @@ struct Mailbox {
 };
 // A trip launched ahead of its challenges: k_mailbox_wait, queued right
 // before it, waits for mailbox sequence `want`, copies the posted challenges
-// to `chal` (device memory) and sets status[0] = want; the trip reads them
-// there (the kernel boundary orders the copy before the trip).  When the wait
+// (all kTripMaxK slots) to `chal` (device memory) and sets status[0] = want;
+// the trip reads them there (the kernel boundary orders the copy before the
+// trip).  When the wait
 // ends without them (cancel code or spin limit) the status is left alone and
 // the trip returns at once.  Each context's wants are distinct, so a status
 // left by an earlier launch never matches.  chal == nullptr: the challenges
@@ -315,7 +343,9 @@ struct CarriedFinish {
 // them to sk.out, then publishes sk.seq.
 template <int NT>
 __device__ __forceinline__ void finish_carried(const CarriedFinish& f) {
-  if (f.status && f.status[0] != f.want) return;  // every thread alike
+  // the status is loaded with the rows and checked once they are in (the
+  // rows' buffer is always readable): one memory round trip, not two
+  const uint32_t st = f.status ? f.status[0] : f.want;
   const int nq = (int)f.nq, rg = NT / nq;
   const int q = threadIdx.x % nq, g = threadIdx.x / nq;
   qacc acc;
@@ -332,6 +362,7 @@ __device__ __forceinline__ void finish_carried(const CarriedFinish& f) {
     acc.add(v3);
   }
   for (; b < f.nblocks; b += rg) acc.add(ld_q(f.sk.partials, (uint64_t)nq * b + q));
+  if (st != f.want) return;  // that trip's wait ended without its challenges (every thread alike)
   __shared__ qm31 fsh[NT];
   fsh[threadIdx.x] = acc.reduce();
   __syncthreads();
@@ -344,7 +375,7 @@ __device__ __forceinline__ void finish_carried(const CarriedFinish& f) {
   if (threadIdx.x == 0) publish_flag(f.sk.flag, f.sk.seq);
 }
 constexpr int kWaitBlock = 256;
-static __global__ void __launch_bounds__(kWaitBlock) k_mailbox_wait(TripWait tw, int np, CarriedFinish fin) {
+static __global__ void __launch_bounds__(kWaitBlock) k_mailbox_wait(TripWait tw, CarriedFinish fin) {
   if (fin.nblocks) finish_carried<kWaitBlock>(fin);  // the previous trip's sums first (the host needs them)
   if (threadIdx.x != 0) return;
   bool ok = false;
@@ -361,10 +392,14 @@ static __global__ void __launch_bounds__(kWaitBlock) k_mailbox_wait(TripWait tw,
     __hip_atomic_store(&tw.mb->expired, tw.want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     return;
   }
-  for (int r = 0; r < np; r++) {  // read after the acquiring read of seq
-    const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&tw.mb->alpha[r]));
-    tw.chal[r] = qm31{q[0], q[1], q[2], q[3]};
-  }
+  // read after the acquiring read of seq, every slot at once (one round trip
+  // to host memory instead of one per challenge) and copied whole: tw.chal
+  // holds kTripMaxK slots, of which the kernels behind read np
+  u32x4 q[kTripMaxK];
+#pragma unroll
+  for (int r = 0; r < kTripMaxK; r++) q[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&tw.mb->alpha[r]));
+#pragma unroll
+  for (int r = 0; r < kTripMaxK; r++) tw.chal[r] = qm31{q[r][0], q[r][1], q[r][2], q[r][3]};
   tw.status[0] = tw.want;
 }
 
@@ -412,6 +447,18 @@ struct Posted {
   const PointArg* pt;  // the claim point
   const qm31* vals;    // posted values (gamma, beta)
   __device__ __forceinline__ bool missing() const { return status && status[0] != want; }
+  // vals[0], vals[1] into *a, *b when status is given, loaded with the status
+  // (one memory round trip); false when the wait ended without them
+  __device__ __forceinline__ bool take2(qm31* a, qm31* b) const {
+    if (!status) return true;
+    const uint32_t st = status[0];
+    const qm31 x = ld_q(vals, 0), y = ld_q(vals, 1);
+    __asm__ volatile("" ::: "memory");
+    if (st != want) return false;
+    *a = x;
+    *b = y;
+    return true;
+  }
 };
 
 // t + (t of lane l ^ m), for every lane.  m = 8: DPP row rotation by 8 (the
@@ -503,10 +550,17 @@ static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__
                                                  uint32_t* counter, uint32_t count_base, uint64_t b_rows,
                                                  int b_chunks, TripWait tw) {
   if (tw.chal) {  // launched ahead: the pending challenges come from k_mailbox_wait
-    if (tw.status[0] != tw.want) return;  // the wait ended without them (every thread alike)
+    // the status and all kTripMaxK challenge slots are loaded together (one
+    // memory round trip instead of one per value), then the status decides
+    const uint32_t st = tw.status[0];
+    qm31 ch[kTripMaxK];
+#pragma unroll
+    for (int r = 0; r < kTripMaxK; r++) ch[r] = ld_q(tw.chal, r);
+    __asm__ volatile("" ::: "memory");  // keeps the loads above the branch
+    if (st != tw.want) return;          // the wait ended without them (every thread alike)
 #pragma unroll
     for (int r = 0; r < kTripMaxK; r++)  // constant indices keep `al` in registers
-      if (r < np) al.c[r] = ld_q(tw.chal, r);
+      if (r < np) al.c[r] = ch[r];
   }
   using S = TripShape<KIND, K, SPLIT>;
   constexpr int G = S::G, LX = S::LX, NA = S::NA;
@@ -735,11 +789,12 @@ static __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restri
       if (got == kWaitCancel) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    if (ok) {  // the challenges, read after the acquiring read of seq
-      for (int r = 0; r < k; r++) {
-        const u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&mb->alpha[r]));
-        sh_al[r] = qm31{q[0], q[1], q[2], q[3]};
-      }
+    if (ok) {  // the challenges, read after the acquiring read of seq: every slot at once
+      u32x4 q[kTripMaxK];
+#pragma unroll
+      for (int r = 0; r < kTripMaxK; r++) q[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&mb->alpha[r]));
+#pragma unroll
+      for (int r = 0; r < kTripMaxK; r++) sh_al[r] = qm31{q[r][0], q[r][1], q[r][2], q[r][3]};  // k of them used
     } else {
       __hip_atomic_store(&mb->expired, want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
     }
@@ -804,7 +859,6 @@ struct EqPartsArg {
 // arguments is one dependent load per table passed.
 // ps.status given: launched ahead, the point comes from ps.pt.
 static __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict__ out, Posted ps) {
-  if (ps.missing()) return;  // the wait ended without the point (every thread alike)
   __shared__ PointLds sp;
   __shared__ uint32_t toff[kEqPartsMax];
   __shared__ int ts[kEqPartsMax], tm[kEqPartsMax];
@@ -813,7 +867,13 @@ static __global__ void k_eq_parts(EqPartsArg a, uint32_t total, qm31* __restrict
     ts[l] = a.s[l];
     tm[l] = a.m[l];
   }
-  stage_point(ps.status ? *ps.pt : a.z, &sp);  // its barrier also covers the table list
+  // the staging's barrier also covers the table list
+  if (ps.status) {
+    int n;
+    if (!stage_posted_point(ps.pt, ps.status, ps.want, &sp, &n)) return;  // the wait ended without the point
+  } else {
+    stage_point(a.z, &sp);
+  }
   const uint64_t g = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const uint32_t i = (uint32_t)(g / kEqLanes);
   const int q = (int)(g % kEqLanes);
@@ -887,9 +947,7 @@ static __global__ void __launch_bounds__(kBlock) k_eq_two(PointArg pt, const Poi
   __shared__ __align__(16) uint8_t sd[kR8Tile];
   int ntot = pt.n;
   if (dpt) {
-    if (status[0] != want) return;  // every thread alike
-    stage_point(*dpt, &sp);
-    ntot = dpt->n;
+    if (!stage_posted_point(dpt, status, want, &sp, &ntot)) return;  // every thread alike
   } else {
     stage_point(pt, &sp);
   }
@@ -1504,11 +1562,7 @@ struct dot_acc {
 static __global__ void k_logup_inv_table(const uint32_t* __restrict__ table_out, uint64_t size, qm31 gamma,
                                          qm31 beta, qm31* __restrict__ inv, Posted ps) {
   const uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= size || ps.missing()) return;
-  if (ps.status) {
-    gamma = ld_q(ps.vals, 0);
-    beta = ld_q(ps.vals, 1);
-  }
+  if (j >= size || !ps.take2(&gamma, &beta)) return;
   const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(m31_from_u32((uint32_t)j))),
                           qm31_mul_m31(beta, table_out[j]));
   st_q(inv, j, qm31_inv(d));
@@ -1527,11 +1581,7 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
     const qm31* __restrict__ eq_hi, const qm31* __restrict__ eq_lo, int eq_h, uint32_t* __restrict__ masked_in,
     uint32_t* __restrict__ masked_out, qm31* __restrict__ d_out, qm31* __restrict__ w_out,
     uint32_t* __restrict__ mult, RoundSink sink, uint32_t* counter, uint32_t count_base, Posted ps) {
-  const bool go = !ps.missing();
-  if (ps.status && go) {
-    gamma = ld_q(ps.vals, 0);
-    beta = ld_q(ps.vals, 1);
-  }
+  const bool go = ps.take2(&gamma, &beta);
   const uint64_t lo_mask = (1ull << eq_h) - 1;
   qacc acc;
   acc.zero();

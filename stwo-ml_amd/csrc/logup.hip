@@ -380,7 +380,7 @@ int prelaunch_activation(gkr_ctx* c, const gkr_matrix* input, uint32_t tag, uint
     HostTimer ht(c, K_HOST_LAUNCH);
     CarriedFinish none;
     memset(&none, 0, sizeof none);
-    GKR_LAUNCH(c, k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, tw, 2, none);
+    GKR_LAUNCH(c, k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, tw, none);
     TRY(check_launch(c));
   }
   Posted pv;  // gamma and beta

@@ -237,7 +237,7 @@ static int launch_trip_k(gkr_ctx* c, const qm31* sa, const qm31* sb, uint64_t n,
   if (tw.chal) {  // launched ahead: the challenges arrive through the mailbox
     CarriedFinish none;
     memset(&none, 0, sizeof none);
-    GKR_LAUNCH(c, k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, tw, np, carry_in ? *carry_in : none);
+    GKR_LAUNCH(c, k_mailbox_wait, dim3(1), dim3(kWaitBlock), 0, tw, carry_in ? *carry_in : none);
     TRY(check_launch(c));
   }
   GKR_LAUNCH(c, (k_trip<KIND, K, SPLIT>), dim3(grid), dim3(kBlock), 0, sa, sb, n, np, al, da, db, hi, lo, h,
