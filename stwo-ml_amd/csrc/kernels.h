@@ -519,6 +519,24 @@ __device__ __forceinline__ qm31 load_pending(const qm31* __restrict__ src, uint6
   }
 }
 
+// b[pos] of a matmul's first trip: the sum of the weight-side restriction's
+// column-chunk partials sb[ch * b_rows + pos] (0 at and above b_rows), eight
+// loads in flight at a time (a loop over one load at a time waits for each).
+__device__ __forceinline__ qm31 chunk_sum(const qm31* __restrict__ sb, uint64_t b_rows, int b_chunks, uint64_t pos) {
+  qacc bs;
+  bs.zero();
+  if (pos < b_rows) {
+    for (int c0 = 0; c0 < b_chunks; c0 += 8) {
+      qm31 v[8];  // chunks past the last read the last again (no branch per load) and add nothing
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = ld_q(sb, (uint64_t)min(c0 + u, b_chunks - 1) * b_rows + pos);
+#pragma unroll
+      for (int u = 0; u < 8; u++) bs.add(c0 + u < b_chunks ? v[u] : qm31_zero());
+    }
+  }
+  return bs.reduce();
+}
+
 template <int KIND, int K, bool SPLIT = true>
 struct TripShape {
   static constexpr int G = 1 << K;                                  // sub-vectors
@@ -584,11 +602,7 @@ static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__
       if (da) st_q(da, pos, a);
       qm31 b;
       if (b_chunks) {
-        qacc bs;
-        bs.zero();
-        if (pos < b_rows)
-          for (int ch = 0; ch < b_chunks; ch++) bs.add(ld_q(sb, (uint64_t)ch * b_rows + pos));
-        b = bs.reduce();
+        b = chunk_sum(sb, b_rows, b_chunks, pos);
       } else {
         b = load_pending(sb, pos, n, np, al);
       }
@@ -617,11 +631,7 @@ static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__
         }
       } else {
         if (b_chunks) {
-          qacc bs;
-          bs.zero();
-          if (pos < b_rows)
-            for (int ch = 0; ch < b_chunks; ch++) bs.add(ld_q(sb, (uint64_t)ch * b_rows + pos));
-          v = bs.reduce();
+          v = chunk_sum(sb, b_rows, b_chunks, pos);
         } else {
           v = load_pending(sb, pos, n, np, al);
         }
