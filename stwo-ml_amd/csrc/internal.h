@@ -779,6 +779,11 @@ int fetch_q(gkr_ctx* c, const qm31* dev, int count, qm31* host_out);
 // ------------------------------------------------------------------ launches ahead of a walk step
 int prelaunch_matmul(gkr_ctx* c, const gkr_matrix* A, const gkr_matrix* B, bool* launched);
 int prelaunch_activation(gkr_ctx* c, const gkr_matrix* input, uint32_t tag, uint32_t table_log, bool* launched);
+// gkr_prove_activation_layer without its copy of the multiplicities when
+// out->multiplicities is null (the walk: the proof record holds them)
+int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                     const gkr_matrix* input, uint32_t tag, uint32_t table_log, gkr_channel* ch, gkr_proof* proof,
+                     gkr_logup_out* out);
 // S_PTWAIT: k_point_wait's status word at 0, the values' wait status at 64
 // (prelaunch_activation), the copied point at 256, posted values (gamma,
 // beta) at kPtWaitVals

@@ -397,6 +397,12 @@ int prelaunch_activation(gkr_ctx* c, const gkr_matrix* input, uint32_t tag, uint
 extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point,
                                           const gkr_qm31* claim_value, const gkr_matrix* input, uint32_t tag,
                                           uint32_t table_log, gkr_channel* ch, gkr_proof* proof, gkr_logup_out* out) {
+  if (out && !out->multiplicities) return fail(GKR_ERR_INVALID, "null output arrays");
+  return prove_activation(c, claim_point, n_point, claim_value, input, tag, table_log, ch, proof, out);
+}
+int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, const gkr_qm31* claim_value,
+                     const gkr_matrix* input, uint32_t tag, uint32_t table_log, gkr_channel* ch, gkr_proof* proof,
+                     gkr_logup_out* out) {
   CH_CHECK(ch);
   if (!c || !input || !claim_value || !out || (!claim_point && n_point)) return fail(GKR_ERR_INVALID, "null argument");
   if (!act_valid(tag)) return fail(GKR_ERR_INVALID, "unknown activation type %u", tag);
@@ -412,7 +418,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     return fail(GKR_ERR_INVALID, "claim point has %u vars, activation MLE has %d", n_point, nv);
   if (nv > kMaxVars) return fail(GKR_ERR_INVALID, "activation too large");
   if (!out->eq_round_polys && nv > 0) return fail(GKR_ERR_INVALID, "null eq_round_polys");
-  if (!out->multiplicities || !out->mult_round_polys) return fail(GKR_ERR_INVALID, "null output arrays");
+  if (!out->mult_round_polys) return fail(GKR_ERR_INVALID, "null output arrays");
   if (!canonical_q(*claim_value)) return fail(GKR_ERR_INVALID, "claim value not canonical");
   std::vector<qm31> cpt(n_point);
   for (uint32_t l = 0; l < n_point; l++) {
@@ -697,7 +703,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
   trace_point(C, "logup.mult");
   // the kernels whose results were waited for in the multiplicity sumcheck
   // were queued after the one writing the multiplicities' pinned copy
-  memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
+  if (out->multiplicities) memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
   qm31 io[2];
   TRY(wait_sink<2>(c, sk_io, io));  // delivered before the multiplicity trips' results
   const qm31 in_eval = io[0], out_eval = io[1];
@@ -730,7 +736,7 @@ extern "C" int gkr_prove_activation_layer(gkr_ctx* c, const gkr_qm31* claim_poin
     L.w_eval = w_eval;
     L.in_eval = in_eval;
     L.out_eval = out_eval;
-    L.mults.assign(out->multiplicities, out->multiplicities + tsize);
+    L.mults.assign(c->h_mult, c->h_mult + tsize);
     for (uint32_t t = 0; t < 2 * table_log; t++) L.mult_rp.push_back(Q(out->mult_round_polys[t]));
     L.mult_final = mfin[0];
     L.mult_sum = mult_sum;

@@ -2,6 +2,8 @@
 #include "internal.h"
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <mutex>
 #include <thread>
@@ -230,7 +232,12 @@ static void serialize_tail(const gkr_proof* p, Ser& s) {
 // 0 at felt 1, after the layer count), so that serializing the finished
 // proof only writes the count and the tail.  A layer that does not fit ends
 // the streaming (gkr_proof_serialize then writes every layer itself).
+//
+// The thread spins on the queue length for a while before it sleeps, and the
+// reducer's thread notifies it only when it sleeps: a condition-variable wake
+// per record (a futex call) would land on the transcript's critical path.
 struct ProofStream {
+  static constexpr double kSpinSeconds = 0.005;
   gkr_felt* out;
   size_t cap;
   std::mutex m;
@@ -239,12 +246,15 @@ struct ProofStream {
   size_t written = 0;                  // queue entries written (or counted, after an overflow)
   std::vector<size_t> off{1};          // off[i]: first felt of layer i, for i <= written
   bool overflow = false, stop = false;
+  std::atomic<size_t> queued{0};       // queue.size(), read without the lock while spinning
+  std::atomic<bool> sleeping{false}, stopping{false};
   std::thread th;
   ProofStream(gkr_felt* o, size_t c) : out(o), cap(c) { th = std::thread([this] { run(); }); }
   ~ProofStream() {
     {
       std::lock_guard<std::mutex> lk(m);
       stop = true;
+      stopping.store(true, std::memory_order_release);
     }
     work.notify_all();
     th.join();
@@ -252,7 +262,22 @@ struct ProofStream {
   void run() {
     std::unique_lock<std::mutex> lk(m);
     for (;;) {
-      work.wait(lk, [&] { return stop || written < queue.size(); });
+      if (!stop && written == queue.size()) {  // spin, then sleep until add() or the destructor wakes it
+        const size_t w = written;
+        lk.unlock();
+        const auto t0 = std::chrono::steady_clock::now();
+        for (uint32_t i = 1;; i++) {
+          _mm_pause();
+          if (queued.load(std::memory_order_acquire) != w || stopping.load(std::memory_order_acquire)) break;
+          if ((i & 1023) == 0 &&
+              std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > kSpinSeconds)
+            break;
+        }
+        lk.lock();
+        sleeping.store(true, std::memory_order_seq_cst);
+        work.wait(lk, [&] { return stop || written < queue.size(); });
+        sleeping.store(false, std::memory_order_seq_cst);
+      }
       if (stop) return;
       const LayerRec* L = queue[written];
       const size_t at = off[written];
@@ -277,8 +302,11 @@ struct ProofStream {
     {
       std::lock_guard<std::mutex> lk(m);
       queue.push_back(L);
+      queued.store(queue.size(), std::memory_order_release);
     }
-    work.notify_one();
+    // the thread sets `sleeping` under the lock before its last look at the
+    // queue, so either it sees this record or this load sees it sleeping
+    if (sleeping.load(std::memory_order_seq_cst)) work.notify_one();
   }
   // Returns once every record handed over is written.
   void sync() {
@@ -292,6 +320,7 @@ struct ProofStream {
       queue.resize(n);
       written = n;
       off.resize(n + 1);
+      queued.store(n, std::memory_order_release);
     }
   }
 };

@@ -13,7 +13,6 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
   gkr_qm31 value = init_value ? *init_value : G(qm31_zero());
   bool have_claim = init_value != nullptr;
   std::vector<gkr_qm31> rp, npnt(64);
-  std::vector<uint32_t> mults;
   // A fresh matmul step whose predecessor is a matmul or activation step has
   // its restriction launched ahead, at the predecessor's last launch, waiting
   // on the device for its claim point (prelaunch_matmul): the host then only
@@ -135,15 +134,14 @@ extern "C" int gkr_prove_walk(gkr_ctx* c, gkr_channel* ch, const gkr_step* steps
         const uint32_t tl = st.table_log_size ? st.table_log_size : act_default_log_size(st.activation_type);
         if (tl == 0 || tl > 24) return fail(GKR_ERR_INVALID, "step %zu: bad table size", si);
         rp.resize(4 * (size_t)(nv ? nv : 1));
-        mults.resize((size_t)1 << tl);
         std::vector<gkr_qm31> mrp(2 * tl);
         gkr_logup_out out;
         memset(&out, 0, sizeof out);
         out.eq_round_polys = rp.data();
-        out.multiplicities = mults.data();
+        out.multiplicities = nullptr;  // the proof record holds them
         out.mult_round_polys = mrp.data();
-        TRY(gkr_prove_activation_layer(c, point.data(), (uint32_t)point.size(), &value, st.a, st.activation_type, tl,
-                                       ch, proof, &out));
+        TRY(prove_activation(c, point.data(), (uint32_t)point.size(), &value, st.a, st.activation_type, tl, ch,
+                             proof, &out));
         value = out.input_eval;  // the claim point is unchanged (prover.rs:6581-6584)
       } else if (st.kind == GKR_STEP_LAYERNORM || st.kind == GKR_STEP_RMSNORM) {
         const uint32_t nv = (uint32_t)(log2_exact(next_pow2(st.a->rows)) + log2_exact(next_pow2(st.a->cols)));
