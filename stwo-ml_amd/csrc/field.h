@@ -117,7 +117,9 @@ GKR_HD qm31 qm31_mul_m31(qm31 x, uint32_t s) {
 //   lo = x_lo*y_lo + (2+i) * x_hi*y_hi,  hi = x_lo*y_hi + x_hi*y_lo.
 // Each word is a signed combination of 32-bit products; subtractions are
 // turned into additions of (P - v) so every intermediate is a non-negative
-// u64 below 2^64.
+// u64 below 2^64.  Canonical inputs and P - v are at most P, so a product is
+// at most P^2 and four of them sum to at most 4P^2 = 2^64 - 2^34 + 4: each
+// output word takes a single reduction.
 GKR_HD qm31 qm31_mul(qm31 x, qm31 y) {
   // t = x_hi * y_hi (CM31), kept unreduced: t.re = x2y2 - x3y3, t.im = x2y3 + x3y2
   uint64_t tre = (uint64_t)x.c * y.c + (uint64_t)(P - x.d) * y.d;   // < 2^63
@@ -128,10 +130,10 @@ GKR_HD qm31 qm31_mul(qm31 x, qm31 y) {
                    + 2ull * tr + (uint64_t)(P - ti);                  // + < 2^33
   uint64_t lo_im = (uint64_t)x.a * y.b + (uint64_t)x.b * y.a
                    + (uint64_t)tr + 2ull * ti;
-  uint64_t hi_re = (uint64_t)x.a * y.c + (uint64_t)(P - x.b) * y.d;
-  hi_re = (uint64_t)m31_reduce64(hi_re) + (uint64_t)x.c * y.a + (uint64_t)(P - x.d) * y.b;
-  uint64_t hi_im = (uint64_t)x.a * y.d + (uint64_t)x.b * y.c;
-  hi_im = (uint64_t)m31_reduce64(hi_im) + (uint64_t)x.c * y.b + (uint64_t)x.d * y.a;
+  uint64_t hi_re = (uint64_t)x.a * y.c + (uint64_t)(P - x.b) * y.d    // <= 4P^2 < 2^64
+                   + (uint64_t)x.c * y.a + (uint64_t)(P - x.d) * y.b;
+  uint64_t hi_im = (uint64_t)x.a * y.d + (uint64_t)x.b * y.c
+                   + (uint64_t)x.c * y.b + (uint64_t)x.d * y.a;
   return {m31_reduce64(lo_re), m31_reduce64(lo_im), m31_reduce64(hi_re), m31_reduce64(hi_im)};
 }
 GKR_HD qm31 qm31_sqr(qm31 x) { return qm31_mul(x, x); }
