@@ -509,25 +509,32 @@ inline void post_mailbox(gkr_ctx* c, uint32_t want, const qm31* chal, int k) {
   __atomic_store_n(&c->mailbox->seq, want, __ATOMIC_RELEASE);
 }
 // Host side of a k_handover launch: posts the last trip's challenges into
-// the mailbox and receives the folded vectors.  If the host leaves before
-// posting (an error), the guard posts the cancel code so the kernel stops
-// waiting at once, drains the stream, and clears the mailbox so that the
-// next hand-over does not read the cancel code.
+// the mailbox, one at a time as the host draws them (post_one, so the kernel
+// folds each level while the host draws the next) or the rest at once
+// (post), and receives the folded vectors.  The session holds max(k, 1)
+// consecutive mailbox sequence numbers from mb_seq: challenge i is posted
+// under mb_seq + i.  If the host leaves before posting (an error), the guard
+// posts the cancel code so the kernel stops waiting at once, drains the
+// stream, and clears the mailbox so that the next hand-over does not read
+// the cancel code.
 struct HandoverSession {
   gkr_ctx* c;
   uint32_t res_seq = 0, mb_seq = 0;
+  int k = 0, posted = 0;
   bool launched = false, done = false;
   bool cancel_before_post = false;  // test hook (gkr_ctx_debug): leave without posting
   bool hold_post = false;           // test hook (gkr_ctx_debug): post only after the kernel's wait expired
   explicit HandoverSession(gkr_ctx* c_) : c(c_) {}
   // Launch k_handover<NV> over the vectors a (, b) of length len, to be folded by k challenges.
   template <int NV>
-  int launch(const qm31* a, const qm31* b, uint64_t len, int k, const CarriedFinish* fin = nullptr) {
+  int launch(const qm31* a, const qm31* b, uint64_t len, int k_, const CarriedFinish* fin = nullptr) {
     HostTimer ht(c, K_HOST_LAUNCH);
-    if (len > (uint64_t)kHandMax || k < 0 || k > kTripMaxK || (len >> k) == 0)
-      return fail(GKR_ERR_DEVICE, "hand-over of %llu entries folded %d times", (unsigned long long)len, k);
+    if (len > (uint64_t)kHandMax || k_ < 0 || k_ > kTripMaxK || (len >> k_) == 0)
+      return fail(GKR_ERR_DEVICE, "hand-over of %llu entries folded %d times", (unsigned long long)len, k_);
+    k = k_;
+    posted = 0;
     res_seq = alloc_seq(&c->seq, 1);
-    mb_seq = alloc_seq(&c->mb_seq, 1);
+    mb_seq = alloc_seq(&c->mb_seq, k > 0 ? k : 1);
     uint32_t spin_limit = kWaitSpinLimit;
     if (c->debug_handover_spins) {  // test hook: a short bounded wait that expires before the post
       spin_limit = c->debug_handover_spins;
@@ -545,15 +552,37 @@ struct HandoverSession {
     launched = true;
     return check_launch(c);
   }
-  int post(const qm31* chal, int k) {
+  // Checks before a post: the test hooks leave without posting, or post only
+  // once the kernel's wait has expired.
+  int before_post() {
+    if (!launched) return fail(GKR_ERR_DEVICE, "hand-over challenges posted before its launch");
     if (cancel_before_post) return fail(GKR_ERR_DEVICE, "hand-over cancelled before the challenges were posted");
-    if (hold_post) {
+    if (hold_post && posted == 0) {
       const auto t0 = std::chrono::steady_clock::now();
       volatile uint32_t* expired = &c->mailbox->expired;
       while (*expired != mb_seq && std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() < 10.0) {
       }
     }
-    post_mailbox(c, mb_seq, chal, k);
+    return GKR_OK;
+  }
+  // Post challenge i (i == the number posted so far) as soon as it is drawn.
+  int post_one(int i, const qm31& r) {
+    if (i != posted || i >= k) return fail(GKR_ERR_DEVICE, "hand-over challenge %d posted out of order", i);
+    TRY(before_post());
+    c->mailbox->alpha[i] = r;
+    posted = i + 1;
+    __atomic_store_n(&c->mailbox->seq, mb_seq + (uint32_t)i, __ATOMIC_RELEASE);
+    return GKR_OK;
+  }
+  // Post the challenges not yet posted (all of them, or the wanted sequence
+  // alone when k = 0): chal holds all k.
+  int post(const qm31* chal, int k_) {
+    if (k_ != k) return fail(GKR_ERR_DEVICE, "hand-over folded %d times, %d challenges posted", k, k_);
+    if (posted == (k > 0 ? k : 1)) return GKR_OK;
+    TRY(before_post());
+    for (int r = posted; r < k; r++) c->mailbox->alpha[r] = chal[r];
+    posted = k > 0 ? k : 1;
+    __atomic_store_n(&c->mailbox->seq, mb_seq + (uint32_t)(posted - 1), __ATOMIC_RELEASE);
     return GKR_OK;
   }
   // Wait for the folded vectors: count vectors of len entries each.

@@ -766,13 +766,18 @@ static __global__ void __launch_bounds__(kFinishBlock) k_finish_wide(RoundSink s
 // ------------------------------------------------------------------ hand-over to the host
 // The end of a sumcheck's device part: one workgroup loads the NV vectors the
 // last trip left (length len <= kHandMax, not yet folded by that trip's k
-// challenges) into LDS while the host works on the trip's rounds, waits for
-// the k challenges (mailbox seq `want`), folds, and hands the vectors
-// (len >> k entries each, one after another) to vec_out in coherent host
-// memory, then publishes `seq`.  The wait is bounded: after spin_limit
-// polls without `want` (or on the cancel code) the kernel writes `want` into
-// the mailbox's `expired` word and returns without publishing, so every wave
-// always exits and the shared result flag only ever holds sequence numbers.
+// challenges) into LDS while the host works on the trip's rounds, folds them
+// by the k challenges as the host draws them, and hands the vectors (len >> k
+// entries each, one after another) to vec_out in coherent host memory, then
+// publishes `seq`.  The host posts challenge r into mailbox slot alpha[r]
+// under sequence want + r (or several at once under the last of theirs), so
+// fold r needs seq in [want + r, want + max(k, 1) - 1] (mod 2^32): each fold
+// runs while the host draws the next challenge, and one poll that finds
+// several posted takes all of them.  With k = 0 the kernel still waits for
+// `want` before it hands over.  The wait is bounded: after spin_limit polls
+// in all (or on the cancel code) the kernel writes `want` into the mailbox's
+// `expired` word and returns without publishing, so every wave always exits
+// and the shared result flag only ever holds sequence numbers.
 constexpr int kHandMax = 2048;
 
 template <int NV>
@@ -783,37 +788,46 @@ static __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restri
   if (fin.nblocks) finish_carried<kBlock>(fin);  // the last trip's sums first (the host needs them)
   __shared__ qm31 v[NV][kHandMax];
   __shared__ qm31 sh_al[kTripMaxK];
-  __shared__ bool sh_ok;
+  __shared__ int sh_avail;  // challenges in sh_al, or -1 once the wait gave up
   for (uint32_t i = threadIdx.x; i < len; i += blockDim.x) {
     v[0][i] = ld_q(a, i);
     if constexpr (NV > 1) v[1][i] = ld_q(b, i);
   }
-  if (threadIdx.x == 0) {
-    bool ok = false;
-    for (uint32_t spins = 0; spins < spin_limit; spins++) {
-      const uint32_t got = __hip_atomic_load(&mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
-      if (got == want) {
-        ok = true;
-        break;
-      }
-      if (got == kWaitCancel) break;
-      __builtin_amdgcn_s_sleep(1);
-    }
-    if (ok) {  // the challenges, read after the acquiring read of seq: every slot at once
-      u32x4 q[kTripMaxK];
-#pragma unroll
-      for (int r = 0; r < kTripMaxK; r++) q[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&mb->alpha[r]));
-#pragma unroll
-      for (int r = 0; r < kTripMaxK; r++) sh_al[r] = qm31{q[r][0], q[r][1], q[r][2], q[r][3]};  // k of them used
-    } else {
-      __hip_atomic_store(&mb->expired, want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-    sh_ok = ok;
-  }
-  __syncthreads();
-  if (!sh_ok) return;
+  const int levels = k > 0 ? k : 1;
+  uint32_t spins = 0;  // thread 0's polls, over every level
+  int avail = 0;
   uint32_t l = len;
-  for (int r = 0; r < k; r++) {
+  for (int r = 0; r < levels; r++) {
+    if (r >= avail) {  // uniform: avail comes from LDS after a barrier
+      if (threadIdx.x == 0) {
+        int got_n = -1;
+        for (; spins < spin_limit; spins++) {
+          const uint32_t got = __hip_atomic_load(&mb->seq, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+          if (got == kWaitCancel) break;
+          const int32_t d = (int32_t)(got - want);
+          if (d >= r && d < levels) {
+            got_n = d + 1;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(1);
+        }
+        if (got_n > 0) {  // the challenges, read after the acquiring read of seq: every slot at once
+          u32x4 q[kTripMaxK];
+#pragma unroll
+          for (int s = 0; s < kTripMaxK; s++)
+            q[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(&mb->alpha[s]));
+#pragma unroll
+          for (int s = 0; s < kTripMaxK; s++) sh_al[s] = qm31{q[s][0], q[s][1], q[s][2], q[s][3]};  // got_n used
+        } else {
+          __hip_atomic_store(&mb->expired, want, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        sh_avail = got_n;
+      }
+      __syncthreads();
+      avail = sh_avail;
+      if (avail < 0) return;
+    }
+    if (r >= k) break;
     const uint32_t h = l / 2;
     const qm31 al = sh_al[r];
     for (uint32_t i = threadIdx.x; i < h; i += blockDim.x)

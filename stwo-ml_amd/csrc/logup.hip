@@ -221,6 +221,7 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
         tg.values(4, xs, sums);
       }
       absorb3(tr.t + i, sums);
+      if (j + 1 == nt) TRY(ho.post_one(i, chal[tr.t + i]));  // the hand-over folds it while the next is drawn
       if (i + 1 < tr.K) {
         HostTimer hg(c, K_HOST_GRAM);
         tg.fold(chal[tr.t + i]);
@@ -673,6 +674,7 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
         }
         absorb1((uint32_t)(tr.t + i), sums);
         mchal[tr.t + i] = alpha;
+        if (j + 1 == nt) TRY(ho.post_one(i, alpha));  // the hand-over folds it while the next is drawn
       }
       np = tr.K;
       pend = mchal.data() + tr.t;

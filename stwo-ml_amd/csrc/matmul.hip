@@ -460,6 +460,7 @@ int product_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* in_a, c
         tg.values(3, xs, sums);
       }
       absorb(tr.t + i, sums);
+      if (j + 1 == nt) TRY(ho.post_one(i, chal[tr.t + i]));  // the hand-over folds it while the next is drawn
       if (i + 1 < tr.K) {
         HostTimer hg(c, K_HOST_GRAM);
         tg.fold(chal[tr.t + i]);

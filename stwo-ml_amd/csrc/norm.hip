@@ -291,6 +291,7 @@ int mean_var_sumcheck(gkr_ctx* c, PoseidonChannel& ch, int T, const qm31* cen, c
       s[1] = qm31_add(qm31_mul(eta0, lv[1]), qm31_mul(eta1, qv[1]));
       s[2] = qm31_add(qm31_mul(eta0, l2), qm31_mul(eta1, qv[2]));
       absorb(tr.t + i, s);
+      if (j + 1 == trips.size()) TRY(ho.post_one(i, chal[tr.t + i]));  // the hand-over folds it while the next is drawn
     }
     np = tr.K;
     pend = chal + tr.t;
