@@ -1672,6 +1672,161 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
   qm31 v[2] = {acc.reduce(), ie.reduce()};
   sink_deliver<2>(v, sink, counter, count_base);
 }
+// The prepare pass fused with the eq-sumcheck's first trip (k_trip<1, K>,
+// long-vector layout, K <= 2 rounds, no pending folds): the trip reads the
+// w and d the pass writes, so one pass forms both from the same registers.
+// Seen through its top K variables the padded input splits into G = 2^K
+// sub-vectors; lane c of a group of G consecutive lanes takes entry
+// p = c * nb + x (nb = n >> K) of each group index x, forms w and d as
+// k_logup_prepare does (and stores them, with the masked input and output,
+// for the later trips), and with eq(x) = hi[x >> h] * lo[x & (2^h - 1)], the
+// first trip's table over the claim coordinates below the trip's variables:
+//   G[c][c'] = sum_x eq(x) w_c(x) d_c'(x)       the first trip's cross sums
+//   T = sum_p w_p                               the trace sum
+//   I_c = sum_x x_(c nb + x) eq(x)               the input MLE per sub-vector
+// The input MLE at the claim point z is sum_c eq(z_0 .. z_(K-1), c) I_c (the
+// host applies the top coordinates' factor).  One partial row per workgroup:
+// [G[c][c'] row-major | T | I_0 .. I_(G-1) | zeros], kPrepTripNQ<K> values,
+// added by k_finish_wide.  Entries of a thread are `groups` apart, kPrepBatch
+// of them per pass with every load in flight before the arithmetic.
+// ps.status given: launched ahead, gamma and beta are ps.vals[0], ps.vals[1];
+// when its wait ended without them the pass adds nothing but still delivers.
+template <int K>
+struct PrepTrip {
+  static constexpr int G = 1 << K;
+  static constexpr int NQ = K == 1 ? 8 : 32;  // G * G + 1 + G values, padded to a power of two
+  static_assert(K >= 1 && K <= 2 && G * G + 1 + G <= NQ, "fused prepare: one or two rounds");
+};
+template <int K>
+static __global__ void __launch_bounds__(kBlock) k_logup_prepare_trip(
+    const uint32_t* __restrict__ X, uint64_t rows, uint64_t cols, int log_pcol, uint64_t n,
+    const uint32_t* __restrict__ table_out, const qm31* __restrict__ inv, uint32_t mask, qm31 gamma, qm31 beta,
+    const qm31* __restrict__ eq_hi, const qm31* __restrict__ eq_lo, int eq_h, uint32_t* __restrict__ masked_in,
+    uint32_t* __restrict__ masked_out, qm31* __restrict__ d_out, qm31* __restrict__ w_out,
+    uint32_t* __restrict__ mult, RoundSink sink, Posted ps) {
+  constexpr int G = PrepTrip<K>::G, NQ = PrepTrip<K>::NQ;
+  constexpr int kBatch = 2;
+  const bool go = ps.take2(&gamma, &beta);
+  const uint64_t nb = n >> K;
+  const uint64_t lo_mask = (1ull << eq_h) - 1, col_mask = (1ull << log_pcol) - 1;
+  const int lane = threadIdx.x & 63;
+  const int c = lane & (G - 1);
+  const uint64_t groups = ((uint64_t)gridDim.x * blockDim.x) / G;
+  const int gb = threadIdx.x & ~(G - 1);
+  // when the stride of a thread's x is a multiple of 2^h, all its x share
+  // one low index: the thread weights by hi[x >> h] alone and multiplies its
+  // sums by that lo value once at the end
+  const bool lo_fixed = (groups & lo_mask) == 0;
+  qacc acc[G], tsum;
+#pragma unroll
+  for (int i = 0; i < G; i++) acc[i].zero();
+  tsum.zero();
+  dot_acc ie;
+  ie.zero();
+  __shared__ qm31 shv[kBatch][kBlock];  // the group's d values, for the cross products
+  for (uint64_t x0 = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / G; go && x0 < nb; x0 += kBatch * groups) {
+    uint32_t xv[kBatch];
+    bool valid[kBatch], real[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      const uint64_t x = x0 + (uint64_t)u * groups;
+      const uint64_t p = (uint64_t)c * nb + x;
+      const uint64_t r = p >> log_pcol, col = p & col_mask;
+      valid[u] = x < nb;  // the same for the G lanes of a group
+      real[u] = valid[u] && r < rows && col < cols;
+      xv[u] = real[u] ? X[r * cols + col] : 0u;
+    }
+    uint32_t mo[kBatch];
+    qm31 w[kBatch], eh[kBatch], el[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      const uint64_t x = valid[u] ? x0 + (uint64_t)u * groups : 0;
+      const uint32_t mi = xv[u] & mask;
+      mo[u] = table_out[mi];
+      w[u] = ld_q(inv, mi);
+      eh[u] = ld_q(eq_hi, x >> eq_h);
+      if (!lo_fixed) el[u] = ld_q(eq_lo, x & lo_mask);
+    }
+    qm31 a[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; u++) {
+      const uint64_t p = (uint64_t)c * nb + x0 + (uint64_t)u * groups;
+      const uint32_t mi = xv[u] & mask;
+      const qm31 d = qm31_sub(qm31_sub(gamma, qm31_from_m31(mi)), qm31_mul_m31(beta, mo[u]));
+      const qm31 e = lo_fixed ? eh[u] : qm31_mul(eh[u], el[u]);
+      a[u] = qm31_mul(w[u], e);
+      if (valid[u]) {
+        masked_in[p] = mi;
+        masked_out[p] = mo[u];
+        st_q(d_out, p, d);
+        st_q(w_out, p, w[u]);
+        // zero padding all lands in bin 0; it is counted once below
+        if (mult && real[u]) atomicAdd(&mult[mi], 1u);
+        tsum.add(w[u]);
+        ie.add(m31_from_u32(xv[u]), e);
+      }
+      shv[u][threadIdx.x] = d;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int u = 0; u < kBatch; u++)
+      if (valid[u]) {
+#pragma unroll
+        for (int j = 0; j < G; j++) acc[j].add(qm31_mul(a[u], shv[u][gb + j]));
+      }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  }
+  if (go && mult && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(&mult[0], (uint32_t)(n - rows * cols));
+  // across the wave: the cross sums and I_c over the lanes of one c (masks
+  // G .. 32), the trace sum over every lane
+  // this thread's lo value (a thread past nb added nothing: any value serves)
+  const qm31 lo = lo_fixed ? ld_q(eq_lo, (((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / G) & lo_mask) : qm31_one();
+  qm31 t[G];
+#pragma unroll
+  for (int i = 0; i < G; i++) {
+    t[i] = acc[i].reduce();
+    if (lo_fixed) t[i] = qm31_mul(t[i], lo);
+    if constexpr (G <= 2) t[i] = qm31_add_xor<2>(t[i]);
+    t[i] = qm31_add_xor<4>(t[i]);
+    t[i] = qm31_add_xor<8>(t[i]);
+    t[i] = qm31_add_xor<16>(t[i]);
+    t[i] = qm31_add_xor<32>(t[i]);
+  }
+  qm31 iv = ie.reduce();
+  if (lo_fixed) iv = qm31_mul(iv, lo);
+  if constexpr (G <= 2) iv = qm31_add_xor<2>(iv);
+  iv = qm31_add_xor<4>(iv);
+  iv = qm31_add_xor<8>(iv);
+  iv = qm31_add_xor<16>(iv);
+  iv = qm31_add_xor<32>(iv);
+  qm31 ts = tsum.reduce();
+  ts = qm31_add_xor<1>(ts);
+  ts = qm31_add_xor<2>(ts);
+  ts = qm31_add_xor<4>(ts);
+  ts = qm31_add_xor<8>(ts);
+  ts = qm31_add_xor<16>(ts);
+  ts = qm31_add_xor<32>(ts);
+  __shared__ qm31 sh[kBlock / 64][NQ];
+  const int wave = threadIdx.x >> 6;
+  if (lane < G) {
+#pragma unroll
+    for (int i = 0; i < G; i++) sh[wave][c * G + i] = t[i];
+    sh[wave][G * G + 1 + c] = iv;
+  }
+  if (lane == 0) sh[wave][G * G] = ts;
+  __syncthreads();
+  for (int q = threadIdx.x; q < NQ; q += blockDim.x) {
+    qm31 v = qm31_zero();
+    if (q < G * G + 1 + G) {
+      v = sh[0][q];
+#pragma unroll
+      for (int wv = 1; wv < kBlock / 64; wv++) v = qm31_add(v, sh[wv][q]);
+    }
+    st_q(sink.partials, (uint64_t)blockIdx.x * NQ + q, v);
+  }
+}
 // Multiplicities of a table of at most kHistBins entries without global
 // atomics (same-address atomics serialize; a uniform input has no repeats to
 // merge): workgroup g counts keys [g * kHistPerGroup, (g + 1) * kHistPerGroup)

@@ -280,6 +280,41 @@ int eq3_sumcheck(gkr_ctx* c, PoseidonChannel& C, const qm31* z, const Eq3Plan& p
 // pass (trace sum and input MLE at the claim point, slot kSlotPrep) and the
 // eq-sumcheck's first trip (slot kSlotEq0).  ps.status given: launched ahead,
 // gamma and beta come from k_point_wait's copies.  The buffers exist.
+// Rounds of the eq-sumcheck's first trip when the prepare pass computes its
+// sums (k_logup_prepare_trip: a long-vector trip of one or two rounds), else
+// 0: the prepare pass and the trip are separate kernels, and the pass takes
+// the input MLE from the split halves of eq(z, .).
+static int prep_trip_k(int nv) {
+  if (nv <= 0 || nv > 62) return 0;
+  const uint64_t n = 1ull << nv;
+  const int K = trip_k(n) < nv ? trip_k(n) : nv;  // plan_trips' first trip
+  return K <= 2 && 2 * n > kTripSplitLanes ? K : 0;
+}
+#ifndef GKR_PREP_TRIP_BLOCKS
+#define GKR_PREP_TRIP_BLOCKS 512
+#endif
+constexpr unsigned kPrepTripMaxBlocks = GKR_PREP_TRIP_BLOCKS;  // partial rows of the fused pass
+template <int K>
+static int launch_prepare_trip(gkr_ctx* c, const gkr_matrix* input, uint64_t n, const uint32_t* d_table,
+                               const qm31* d_inv, uint32_t tsize, qm31 gamma, qm31 beta, const Eq3Plan& epl,
+                               uint32_t* d_min, uint32_t* d_mout, qm31* d_d0, qm31* d_w0, uint32_t* d_mult,
+                               const Posted& ps, RoundSink* sk) {
+  const qm31* parts = (const qm31*)c->buf[S_EQPARTS];
+  TRY(make_sink(c, sk, kSlotEq0));
+  unsigned grid = partial_grid(n);
+  if (grid > kPrepTripMaxBlocks) grid = kPrepTripMaxBlocks;
+  {
+    // algorithmic bytes: the input, masked input and output written (8 per entry), d and w written
+    TimedLaunch tl(c, K_LOGUP_PREP, 4 * input->rows * input->cols + 8 * n + 32 * n, true);
+    GKR_LAUNCH(c, k_logup_prepare_trip<K>, dim3(grid), dim3(kBlock), 0, input->dev, input->rows, input->cols,
+               log2_exact(next_pow2(input->cols)), n, d_table, d_inv, tsize - 1, gamma, beta, parts + epl.hi_off[0],
+               parts + epl.lo_off[0], epl.h[0], d_min, d_mout, d_d0, d_w0, d_mult, *sk, ps);
+  }
+  TRY(check_launch(c));
+  GKR_LAUNCH(c, k_finish_wide<PrepTrip<K>::NQ>, dim3(1), dim3(kFinishBlock), 0, *sk, grid);
+  return check_launch(c);
+}
+
 static int logup_first_launches(gkr_ctx* c, const gkr_matrix* input, uint64_t n, const uint32_t* d_table,
                                 uint32_t table_log, bool lds_hist, qm31 gamma, qm31 beta, const Eq3Plan& epl,
                                 const Posted& ps, RoundSink* sk_prep, RoundSink* sk_eq0) {
@@ -298,6 +333,19 @@ static int logup_first_launches(gkr_ctx* c, const gkr_matrix* input, uint64_t n,
   HostTimer ht(c, K_HOST_LAUNCH);
   GKR_LAUNCH(c, k_logup_inv_table, dim3(grid_for(tsize)), dim3(kBlock), 0, d_table, tsize, gamma, beta, d_inv, ps);
   TRY(check_launch(c));
+  const int fk = prep_trip_k(epl.nv);
+  if (fk) {  // one pass and one finisher: the trip's sums first, then the prepare values (one sink)
+    uint32_t* mult = lds_hist ? nullptr : d_mult;
+    if (fk == 1)
+      TRY(launch_prepare_trip<1>(c, input, n, d_table, d_inv, (uint32_t)tsize, gamma, beta, epl, d_min, d_mout, d_d0,
+                                 d_w0, mult, ps, sk_eq0));
+    else
+      TRY(launch_prepare_trip<2>(c, input, n, d_table, d_inv, (uint32_t)tsize, gamma, beta, epl, d_min, d_mout, d_d0,
+                                 d_w0, mult, ps, sk_eq0));
+    *sk_prep = *sk_eq0;
+    sk_prep->out += 1 << (2 * fk);
+    return GKR_OK;
+  }
   TRY(make_sink(c, sk_prep, kSlotPrep));
   {
     uint32_t* counter;
@@ -341,7 +389,7 @@ int prelaunch_activation(gkr_ctx* c, const gkr_matrix* input, uint32_t tag, uint
   Eq3Plan epl;
   EqPartsArg arg;
   uint32_t total;
-  TRY(eq3_plan(nv, true, &epl, &arg, &total));
+  TRY(eq3_plan(nv, prep_trip_k(nv) == 0, &epl, &arg, &total));
   uint8_t* pw;
   TRY(ensureT(c, S_PTWAIT, kPtWaitBytes, &pw));
   Posted pp;  // the point
@@ -460,10 +508,11 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
   // they can be: by the walk at the previous step's last launch, or here,
   // before the host draws gamma and beta (the launch calls then overlap the
   // draws); they wait on the device for the claim point and gamma, beta.
-  // Otherwise one launch builds the eq tables of the eq-sumcheck trips and
-  // eq(claim point, x) as the product of its high and low halves (for the
-  // input MLE at the claim point, accumulated by the prepare pass) while the
-  // host draws gamma and beta, and the rest follows the draws.
+  // Otherwise one launch builds the eq tables of the eq-sumcheck trips (and,
+  // when the prepare pass runs apart from the first trip, eq(claim point, x)
+  // as the product of its high and low halves, for the input MLE at the
+  // claim point) while the host draws gamma and beta, and the rest follows
+  // the draws.
   bool pre = c->pre.active && c->pre.act && c->pre.a == input && c->pre.tag == tag && c->pre.table_log == table_log;
   if (!pre && !c->pre.active) {  // nothing queued waits for the host: the wait's buffer may be allocated
     uint8_t* pw;
@@ -478,9 +527,9 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
     c->point_mb = c->pre.want;  // checked once the prepare sums are in
     EqPartsArg arg;
     uint32_t total;
-    TRY(eq3_plan(nv, true, &epl, &arg, &total));
+    TRY(eq3_plan(nv, prep_trip_k(nv) == 0, &epl, &arg, &total));
   } else {
-    TRY(eq3_prepare(c, cpt.data(), nv, &epl, true));
+    TRY(eq3_prepare(c, cpt.data(), nv, &epl, prep_trip_k(nv) == 0));
   }
 
   // Fiat-Shamir: LOG tag, type tag, gamma, beta (prover.rs:6451-6454)
@@ -497,6 +546,8 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
   // the order the host needs them:
   //   prepare -> (trace sum, input MLE at the claim point)      kSlotPrep
   //   eq-sumcheck trip 0                                         kSlotEq0
+  //   (over more than 2^16 entries one fused pass delivers both to kSlotEq0:
+  //   the trip's sums, the trace sum, the input MLE per top sub-vector)
   //   table-side sum over the multiplicities                     kSlotTable
   //   multiplicities -> pinned host copy
   //   multiplicity sumcheck trip 0 (no challenge needed)         kSlotMult0
@@ -577,7 +628,23 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
   // table pass run on the device while the host works through the first
   // eq-sumcheck rounds.
   qm31 prep[2];
-  TRY(wait_sink<2>(c, sk_prep, prep));
+  if (const int fk = prep_trip_k(nv)) {
+    // the trace sum, then the input MLE per top sub-vector c, weighted here by
+    // eq(z_0 .. z_(fk-1), c) (z_0 on the most significant bit of c)
+    qm31 v[1 + (1 << kTripMaxK)];
+    TRY(wait_result<0>(c, sk_prep.seq, nullptr, K_HOST_WAIT));
+    const int slot = (int)(sk_prep.out - c->h_out);
+    for (int q = 0; q <= (1 << fk); q++) v[q] = c->h_out[slot + q];
+    prep[0] = v[0];
+    prep[1] = qm31_zero();
+    for (int cc = 0; cc < (1 << fk); cc++) {
+      qm31 e = qm31_one();
+      for (int l = 0; l < fk; l++) e = qm31_mul(e, eqlin(cpt[l], ((cc >> (fk - 1 - l)) & 1) ? qm31_one() : qm31_zero()));
+      prep[1] = qm31_add(prep[1], qm31_mul(e, v[1 + cc]));
+    }
+  } else {
+    TRY(wait_sink<2>(c, sk_prep, prep));
+  }
   TRY(check_point_wait(c));
   const qm31 trace_sum = prep[0], input_eval = prep[1];
   C.mix_secure_field(trace_sum);

@@ -255,8 +255,11 @@ def test_mle_ops(gpu_ctx):
             assert gpu_ctx.restrict_mle(evals, assign) == O.restrict_mle(evals, assign)
 
 
+# 48 x 1500 (2^17 padded entries) and 20 x 50000 (2^21): the prepare pass fused with the
+# eq-sumcheck's first trip (two rounds, then one), ragged rows and columns
 @pytest.mark.parametrize("rows,cols,tag,tlog", [(1, 8, 5, 8), (4, 16, 5, 10), (3, 5, 3, 6), (2, 32, 4, 8),
-                                                (1, 1536, 5, 16), (8, 96, 2, 12), (16, 64, 3, 16)])
+                                                (1, 1536, 5, 16), (8, 96, 2, 12), (16, 64, 3, 16),
+                                                (48, 1500, 5, 12), (20, 50000, 3, 10)])
 def test_activation_layer_parity(gpu_ctx, rows, cols, tag, tlog):
     log(f"case logup {rows}x{cols} tag={tag} table=2^{tlog}")
     X = O.synthetic(rows, cols, 0, rows * 1000 + cols)
