@@ -492,6 +492,13 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
   TRY(ensureT(c, S_M0, tsize, &m0));
   TRY(ensureT(c, S_M1, tsize / 2 + 1, &m1));
   TRY(ensureT(c, S_LKINV, tsize, &d_inv));
+  {  // the eq halves of the input and output MLEs' pass (dot2_launch), sized
+     // now: it is queued behind the multiplicity sumcheck's hand-over, where
+     // nothing may allocate
+    qm31 *hi, *lo;
+    TRY(ensureT(c, S_EQHI, 1ull << (nv - nv / 2), &hi));
+    TRY(ensureT(c, S_EQLO, 1ull << (nv / 2), &lo));
+  }
   TRY(ensure_host_mult(c, tsize));
   TRY(device_table(c, tag, table_log, &d_table));
   // Multiplicities: tables of up to 2^16 entries are counted in LDS per
@@ -659,10 +666,16 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
   if (!table_side_done) TRY(table_side());
   const qm31 w_eval = fin[1];
   // MLE(masked_in), MLE(masked_out) at the eq-sumcheck challenges, one pass;
-  // the transcript does not use them before the multiplicity sumcheck, so they
-  // are read after it
+  // the transcript does not use them before the multiplicity sumcheck, so the
+  // pass is queued behind that sumcheck's hand-over (it runs while the host
+  // finishes the last rounds; queued earlier it would delay the trips the
+  // host waits for) and read after it
   RoundSink sk_io;
-  TRY(dot2_launch(c, chal.data(), nv, d_min, d_mout, kSlotIO, &sk_io));
+  bool io_launched = false;
+  auto launch_io = [&]() -> int {
+    io_launched = true;
+    return dot2_launch(c, chal.data(), nv, d_min, d_mout, kSlotIO, &sk_io);
+  };
   out->w_eval = G(w_eval);
 
   qm31 tsum[1];
@@ -716,12 +729,14 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
       src = dst;
       if (j + 1 == nt) {
         TRY(ho.launch<1>(src, nullptr, tr.n, tr.K, pre ? &carry : nullptr));
+        TRY(launch_io());
         TRY(run_prelaunch(c));  // the activation step's last launch
       }
       return GKR_OK;
     };
     if (nt == 1) {
       TRY(ho.launch<1>(src, nullptr, mtrips[0].n, mtrips[0].K));
+      TRY(launch_io());
       TRY(run_prelaunch(c));
     }
     if (pre && nt > 1) TRY(launch_j(1, nullptr));
@@ -773,8 +788,9 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
   // the kernels whose results were waited for in the multiplicity sumcheck
   // were queued after the one writing the multiplicities' pinned copy
   if (out->multiplicities) memcpy(out->multiplicities, c->h_mult, tsize * sizeof(uint32_t));
+  if (!io_launched) TRY(launch_io());
   qm31 io[2];
-  TRY(wait_sink<2>(c, sk_io, io));  // delivered before the multiplicity trips' results
+  TRY(wait_sink<2>(c, sk_io, io));
   const qm31 in_eval = io[0], out_eval = io[1];
   out->in_eval = G(in_eval);
   out->out_eval = G(out_eval);
