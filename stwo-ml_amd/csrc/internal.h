@@ -10,6 +10,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <chrono>
 #include <deque>
 
@@ -184,6 +185,27 @@ struct gkr_qvec {
 // Pinned host staging buffers (grow-only, hipHostMalloc).
 enum HostSlot { H_LKDESC, H_LKRES, H_LKTAB, H_NSLOTS };
 
+// Coherent pinned buffers for the LogUp multiplicities, one per activation
+// layer in flight: a layer's table pass writes its slot, and the layer's proof
+// record copies the slot into the record (on the proof stream's thread when the
+// proof is streamed, so the transcript thread does not) and then frees it.  A
+// layer takes the next slot once its previous record has copied it.  Records
+// share ownership of the ring, so a slot outlives a context destroyed first.
+struct MultRing {
+  static constexpr int kSlots = 4;
+  uint32_t* buf[kSlots] = {};
+  size_t cap = 0;
+  std::atomic<int> busy[kSlots];  // 1 from the layer's table pass until its record copied the slot
+  int next = 0;
+  MultRing() {
+    for (auto& b : busy) b.store(0, std::memory_order_relaxed);
+  }
+  ~MultRing() {
+    for (uint32_t* b : buf)
+      if (b) (void)hipHostFree(b);
+  }
+};
+
 struct gkr_ctx {
   int device = 0;
   void* hbuf[H_NSLOTS] = {};
@@ -192,9 +214,10 @@ struct gkr_ctx {
   void* buf[S_NSLOTS] = {};
   size_t cap[S_NSLOTS] = {};
   qm31* h_res = nullptr;  // pinned result staging (64 QM31)
-  uint32_t* h_mult = nullptr;  // coherent pinned copy of the LogUp multiplicities (written by k_u32_to_q)
+  std::shared_ptr<MultRing> mring;  // LogUp multiplicities, host side (ensure_host_mult)
+  uint32_t* h_mult = nullptr;  // the current activation layer's slot of mring (written by its table pass)
+  int h_mult_slot = -1;
   qm31* h_vec = nullptr;       // coherent pinned: vectors handed over by k_handover (2 x kHandMax)
-  size_t h_mult_cap = 0;
   qm31* h_out = nullptr;      // coherent pinned: results delivered by kernels (RoundSink)
   uint32_t* h_flag = nullptr; // coherent pinned: sequence number of the last delivery
   Mailbox* mailbox = nullptr;  // coherent pinned: challenges posted to persistent tail kernels
@@ -289,6 +312,8 @@ inline int ensureT(gkr_ctx* c, Slot s, size_t count, T** out) {
   return GKR_OK;
 }
 
+// A multiplicity ring of n-entry slots, then the next slot: c->h_mult,
+// c->h_mult_slot, marked busy (waits until its previous record copied it).
 int ensure_host_mult(gkr_ctx* c, uint64_t n);
 
 // Kernel launch on the context's stream: GKR_LAUNCH(c, kernel, grid, block,
@@ -899,6 +924,11 @@ struct LayerRec {
   felt table_commitment;
   qm31 claimed_sum, w_eval, in_eval, out_eval;
   std::vector<uint32_t> mults;
+  // Activation: mults still in slot mult_slot of mult_ring (mult_count
+  // entries) until layer_take_mults copies them; -1: in mults
+  std::shared_ptr<MultRing> mult_ring;
+  int mult_slot = -1;
+  size_t mult_count = 0;
   std::vector<qm31> mult_rp;  // c0,c1 per round
   qm31 mult_final, mult_sum;
   NormRec norm;  // tags 4 (LayerNorm) and 8 (RMSNorm)
@@ -929,6 +959,8 @@ struct gkr_proof {
 };
 // Appends a layer record (and hands it to the proof's stream, if any).
 void proof_add_layer(gkr_proof* p, LayerRec&& L);
+// Copies an activation record's multiplicities out of its ring slot and frees the slot.
+void layer_take_mults(LayerRec& L);
 // Drops the records after the first n (a walk step proved again).
 void proof_truncate(gkr_proof* p, size_t n);
 

@@ -500,6 +500,14 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
     TRY(ensureT(c, S_EQLO, 1ull << (nv / 2), &lo));
   }
   TRY(ensure_host_mult(c, tsize));
+  // the layer's multiplicity slot: handed to its proof record, or freed when this call ends
+  struct SlotHold {
+    std::shared_ptr<MultRing> r;
+    int s;
+    ~SlotHold() {
+      if (r) r->busy[s].store(0, std::memory_order_release);
+    }
+  } mslot{c->mring, c->h_mult_slot};
   TRY(device_table(c, tag, table_log, &d_table));
   // Multiplicities: tables of up to 2^16 entries are counted in LDS per
   // workgroup (k_logup_hist) and added in the table pass; larger ones with
@@ -821,7 +829,9 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
     L.w_eval = w_eval;
     L.in_eval = in_eval;
     L.out_eval = out_eval;
-    L.mults.assign(c->h_mult, c->h_mult + tsize);
+    L.mult_ring = std::move(mslot.r);  // copied by layer_take_mults (the proof stream's thread)
+    L.mult_slot = mslot.s;
+    L.mult_count = tsize;
     for (uint32_t t = 0; t < 2 * table_log; t++) L.mult_rp.push_back(Q(out->mult_round_polys[t]));
     L.mult_final = mfin[0];
     L.mult_sum = mult_sum;

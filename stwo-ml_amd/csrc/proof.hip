@@ -258,6 +258,7 @@ struct ProofStream {
     }
     work.notify_all();
     th.join();
+    for (size_t i = written; i < queue.size(); i++) layer_take_mults(*const_cast<LayerRec*>(queue[i]));
   }
   void run() {
     std::unique_lock<std::mutex> lk(m);
@@ -283,6 +284,8 @@ struct ProofStream {
       const size_t at = off[written];
       bool fits = !overflow;
       lk.unlock();
+      // the record is this thread's until it is counted as written
+      layer_take_mults(*const_cast<LayerRec*>(L));
       Ser count{nullptr};
       serialize_layer(*L, count);
       fits = fits && at + count.n <= cap;
@@ -324,9 +327,20 @@ struct ProofStream {
     }
   }
 };
+void layer_take_mults(LayerRec& L) {
+  if (L.mult_slot < 0) return;
+  const uint32_t* src = L.mult_ring->buf[L.mult_slot];
+  L.mults.assign(src, src + L.mult_count);
+  L.mult_ring->busy[L.mult_slot].store(0, std::memory_order_release);
+  L.mult_slot = -1;
+  L.mult_ring.reset();
+}
 void proof_add_layer(gkr_proof* p, LayerRec&& L) {
   p->layers.push_back(std::move(L));
-  if (p->stream) p->stream->add(&p->layers.back());
+  if (p->stream)
+    p->stream->add(&p->layers.back());  // its thread copies the multiplicities before writing the record
+  else
+    layer_take_mults(p->layers.back());
 }
 void proof_truncate(gkr_proof* p, size_t n) {
   if (p->stream) p->stream->truncate(n);

@@ -47,15 +47,29 @@ int ensure(gkr_ctx* c, Slot s, size_t bytes, void** out) {
 }
 
 int ensure_host_mult(gkr_ctx* c, uint64_t n) {
-  if (c->h_mult_cap >= n) return GKR_OK;
-  if (c->h_mult) {
+  c->h_mult = nullptr;
+  c->h_mult_slot = -1;
+  if (!c->mring || c->mring->cap < n) {
+    // a larger ring; records still holding the old one keep it until they copied their slots
     HIP_TRY(hipStreamSynchronize(c->stream));
-    (void)hipHostFree(c->h_mult);
-    c->h_mult = nullptr;
-    c->h_mult_cap = 0;
+    auto r = std::make_shared<MultRing>();
+    for (int i = 0; i < MultRing::kSlots; i++)
+      HIP_TRY(hipHostMalloc((void**)&r->buf[i], n * sizeof(uint32_t), hipHostMallocCoherent | hipHostMallocMapped));
+    r->cap = n;
+    c->mring = std::move(r);
   }
-  HIP_TRY(hipHostMalloc((void**)&c->h_mult, n * sizeof(uint32_t), hipHostMallocCoherent | hipHostMallocMapped));
-  c->h_mult_cap = n;
+  MultRing& r = *c->mring;
+  const int s = r.next;
+  // the slot's last record copies it as the proof stream writes that record,
+  // normally long before the ring comes round again
+  const auto t0 = std::chrono::steady_clock::now();
+  for (uint32_t i = 0; r.busy[s].load(std::memory_order_acquire); i++)
+    if ((i & 1023) == 1023 && std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > 60.0)
+      return fail(GKR_ERR_DEVICE, "multiplicity slot %d still held by an unwritten proof record after 60 s", s);
+  r.busy[s].store(1, std::memory_order_relaxed);
+  r.next = (s + 1) % MultRing::kSlots;
+  c->h_mult = r.buf[s];
+  c->h_mult_slot = s;
   return GKR_OK;
 }
 
@@ -401,7 +415,7 @@ extern "C" void gkr_ctx_destroy(gkr_ctx* c) {
   for (auto& t : c->dev_tables) (void)hipFree(t.second);
   if (c->merkle_consts) (void)hipFree(c->merkle_consts);
   if (c->h_res) (void)hipHostFree(c->h_res);
-  if (c->h_mult) (void)hipHostFree(c->h_mult);
+  c->mring.reset();  // freed with the last proof record still holding a slot
   for (int s = 0; s < H_NSLOTS; s++)
     if (c->hbuf[s]) (void)hipHostFree(c->hbuf[s]);
   if (c->h_vec) (void)hipHostFree(c->h_vec);

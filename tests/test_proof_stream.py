@@ -103,3 +103,49 @@ def test_streamed_walk_with_a_step_proved_again(gpu_ctx):
     _walk(gpu_ctx, p)
     assert gpu_ctx.kernel_time(19)[1] == 1
     assert p.serialize_into(buf) == len(ref) and (buf == ref).all()
+
+
+@pytest.mark.gpu
+def test_streamed_walk_multiplicity_slots(gpu_ctx):
+    """Six SiLU LogUp steps (2^16 multiplicities each) in one streamed walk: each layer's
+    multiplicities go from a ring of four pinned slots into its record on the stream's thread, so the
+    ring comes round while records are still being written; the streamed words equal those of the
+    same walk without a stream.  A proof whose stream is ended, and a proof freed, right after their
+    walks give their slots back (their records are copied on the way): the next walk on the context
+    neither waits for a slot nor differs."""
+    import time
+    log("case streamed walk, multiplicity slots")
+    g = gpu_ctx.upload(MATS[2])
+    steps = [(G.STEP_ACTIVATION, G.CLAIM_FRESH, g, None, 5, 16)] * 6
+
+    def run(proof):
+        ch = G.PoseidonChannel()
+        ch.mix_u64(29)
+        fp, fv = G.prove_walk(gpu_ctx, ch, steps, proof)
+        proof.set_input_claim(fp, fv)
+        return ch.digest()
+
+    plain = G.Proof()
+    d0 = run(plain)
+    ref = plain.serialize_words()
+    buf = np.zeros((len(ref), 8), dtype=np.uint32)
+    p = G.Proof()
+    p.stream_to(buf)
+    assert run(p) == d0
+    assert p.serialize_into(buf) == len(ref) and (buf == ref).all()
+    buf_q = np.zeros((len(ref), 8), dtype=np.uint32)
+    q = G.Proof()
+    q.stream_to(buf_q)
+    assert run(q) == d0
+    q.stream_to(None)  # ends the stream with records possibly unwritten
+    assert (q.serialize_words() == ref).all()
+    buf_r = np.zeros((len(ref), 8), dtype=np.uint32)
+    r = G.Proof()
+    r.stream_to(buf_r)
+    assert run(r) == d0
+    del r  # freed with records possibly unwritten
+    t0 = time.time()
+    s = G.Proof()
+    assert run(s) == d0
+    assert time.time() - t0 < 30
+    assert (s.serialize_words() == ref).all()
