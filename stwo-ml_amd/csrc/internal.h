@@ -533,19 +533,21 @@ inline void post_mailbox(gkr_ctx* c, uint32_t want, const qm31* chal, int k) {
   for (int r = 0; r < k; r++) c->mailbox->alpha[r] = chal[r];
   __atomic_store_n(&c->mailbox->seq, want, __ATOMIC_RELEASE);
 }
-// Host side of a k_handover launch: posts the last trip's challenges into
-// the mailbox, one at a time as the host draws them (post_one, so the kernel
-// folds each level while the host draws the next) or the rest at once
-// (post), and receives the folded vectors.  The session holds max(k, 1)
-// consecutive mailbox sequence numbers from mb_seq: challenge i is posted
-// under mb_seq + i.  If the host leaves before posting (an error), the guard
-// posts the cancel code so the kernel stops waiting at once, drains the
-// stream, and clears the mailbox so that the next hand-over does not read
-// the cancel code.
+// Host side of a k_handover launch over the last trip's vectors, folded by
+// that trip's k challenges: the kernel folds the first kd = k - 1 levels as
+// the host posts their challenges (post_one, one at a time as they are drawn,
+// so each fold runs while the host draws the next; or post, the rest at once)
+// and hands the vectors over while the host draws the last challenge, which
+// the host folds itself (fetch).  The session holds kd consecutive mailbox
+// sequence numbers from mb_seq: challenge i < kd is posted under mb_seq + i.
+// If the host leaves before posting (an error), the guard posts the cancel
+// code so the kernel stops waiting at once, drains the stream, and clears the
+// mailbox so that the next hand-over does not read the cancel code.
 struct HandoverSession {
   gkr_ctx* c;
   uint32_t res_seq = 0, mb_seq = 0;
-  int k = 0, posted = 0;
+  int k = 0, kd = 0, posted = 0;
+  qm31 last = {0, 0, 0, 0};  // challenge k - 1, folded by the host
   bool launched = false, done = false;
   bool cancel_before_post = false;  // test hook (gkr_ctx_debug): leave without posting
   bool hold_post = false;           // test hook (gkr_ctx_debug): post only after the kernel's wait expired
@@ -557,14 +559,15 @@ struct HandoverSession {
     if (len > (uint64_t)kHandMax || k_ < 0 || k_ > kTripMaxK || (len >> k_) == 0)
       return fail(GKR_ERR_DEVICE, "hand-over of %llu entries folded %d times", (unsigned long long)len, k_);
     k = k_;
+    kd = k > 0 ? k - 1 : 0;
     posted = 0;
     res_seq = alloc_seq(&c->seq, 1);
-    mb_seq = alloc_seq(&c->mb_seq, k > 0 ? k : 1);
+    mb_seq = alloc_seq(&c->mb_seq, kd > 0 ? kd : 1);
     uint32_t spin_limit = kWaitSpinLimit;
     if (c->debug_handover_spins) {  // test hook: a short bounded wait that expires before the post
       spin_limit = c->debug_handover_spins;
       c->debug_handover_spins = 0;
-      hold_post = true;
+      hold_post = kd > 0;  // only a kernel that waits can expire
     }
     if (c->debug_handover_cancel) {
       cancel_before_post = true;
@@ -572,7 +575,7 @@ struct HandoverSession {
     }
     CarriedFinish none;
     memset(&none, 0, sizeof none);
-    GKR_LAUNCH(c, k_handover<NV>, dim3(1), dim3(kBlock), 0, a, b, (uint32_t)len, k, c->mailbox,
+    GKR_LAUNCH(c, k_handover<NV>, dim3(1), dim3(kBlock), 0, a, b, (uint32_t)len, kd, c->mailbox,
                        mb_seq, spin_limit, c->h_vec, c->h_flag, res_seq, fin ? *fin : none);
     launched = true;
     return check_launch(c);
@@ -594,27 +597,42 @@ struct HandoverSession {
   int post_one(int i, const qm31& r) {
     if (i != posted || i >= k) return fail(GKR_ERR_DEVICE, "hand-over challenge %d posted out of order", i);
     TRY(before_post());
-    c->mailbox->alpha[i] = r;
     posted = i + 1;
+    if (i == k - 1) {  // the host's own fold
+      last = r;
+      return GKR_OK;
+    }
+    c->mailbox->alpha[i] = r;
     __atomic_store_n(&c->mailbox->seq, mb_seq + (uint32_t)i, __ATOMIC_RELEASE);
     return GKR_OK;
   }
-  // Post the challenges not yet posted (all of them, or the wanted sequence
-  // alone when k = 0): chal holds all k.
+  // Post the challenges not yet posted: chal holds all k.
   int post(const qm31* chal, int k_) {
     if (k_ != k) return fail(GKR_ERR_DEVICE, "hand-over folded %d times, %d challenges posted", k, k_);
-    if (posted == (k > 0 ? k : 1)) return GKR_OK;
+    if (posted == k) return GKR_OK;
     TRY(before_post());
-    for (int r = posted; r < k; r++) c->mailbox->alpha[r] = chal[r];
-    posted = k > 0 ? k : 1;
-    __atomic_store_n(&c->mailbox->seq, mb_seq + (uint32_t)(posted - 1), __ATOMIC_RELEASE);
+    const int from = posted;
+    for (int r = from; r < kd; r++) c->mailbox->alpha[r] = chal[r];
+    if (from < kd) __atomic_store_n(&c->mailbox->seq, mb_seq + (uint32_t)(kd - 1), __ATOMIC_RELEASE);
+    last = chal[k - 1];
+    posted = k;
     return GKR_OK;
   }
-  // Wait for the folded vectors: count vectors of len entries each.
+  // The folded vectors: count vectors of len entries each (the kernel's
+  // vectors, twice as long, folded here by the last challenge).
   int fetch(uint64_t len, int count, std::vector<qm31>* out) {
-    TRY(wait_result<0>(c, res_seq, nullptr, K_HOST_WAIT_TAIL, 0, mb_seq));
-    for (int v = 0; v < count; v++) out[v].assign(c->h_vec + v * len, c->h_vec + (v + 1) * len);
+    if (posted != k) return fail(GKR_ERR_DEVICE, "hand-over fetched before its %d challenges were posted", k);
+    TRY(wait_result<0>(c, res_seq, nullptr, K_HOST_WAIT_TAIL, 0, kd > 0 ? mb_seq : 0));
+    const uint64_t dl = k > 0 ? 2 * len : len;
+    for (int v = 0; v < count; v++) out[v].assign(c->h_vec + v * dl, c->h_vec + (v + 1) * dl);
     done = true;
+    if (k > 0) {
+      HostTimer ht(c, K_HOST_FINISH);
+      for (int v = 0; v < count; v++) {
+        hostfield::fold(qwords(out[v].data()), len, qwords(&last));
+        out[v].resize(len);
+      }
+    }
     return GKR_OK;
   }
   ~HandoverSession() {

@@ -765,19 +765,20 @@ static __global__ void __launch_bounds__(kFinishBlock) k_finish_wide(RoundSink s
 
 // ------------------------------------------------------------------ hand-over to the host
 // The end of a sumcheck's device part: one workgroup loads the NV vectors the
-// last trip left (length len <= kHandMax, not yet folded by that trip's k
-// challenges) into LDS while the host works on the trip's rounds, folds them
-// by the k challenges as the host draws them, and hands the vectors (len >> k
-// entries each, one after another) to vec_out in coherent host memory, then
-// publishes `seq`.  The host posts challenge r into mailbox slot alpha[r]
-// under sequence want + r (or several at once under the last of theirs), so
-// fold r needs seq in [want + r, want + max(k, 1) - 1] (mod 2^32): each fold
-// runs while the host draws the next challenge, and one poll that finds
-// several posted takes all of them.  With k = 0 the kernel still waits for
-// `want` before it hands over.  The wait is bounded: after spin_limit polls
-// in all (or on the cancel code) the kernel writes `want` into the mailbox's
-// `expired` word and returns without publishing, so every wave always exits
-// and the shared result flag only ever holds sequence numbers.
+// last trip left (length len <= kHandMax) into LDS while the host works on the
+// trip's rounds, folds them by k of that trip's challenges as the host draws
+// them (the host folds the trip's last level itself: the vectors go out while
+// it draws the last challenge), and hands the vectors (len >> k entries each,
+// one after another) to vec_out in coherent host memory, then publishes
+// `seq`.  The host posts challenge r into mailbox slot alpha[r] under
+// sequence want + r (or several at once under the last of theirs), so fold r
+// needs seq in [want + r, want + k - 1] (mod 2^32): each fold runs while the
+// host draws the next challenge, and one poll that finds several posted takes
+// all of them.  With k = 0 the kernel hands over at once.  The wait is
+// bounded: after spin_limit polls in all (or on the cancel code) the kernel
+// writes `want` into the mailbox's `expired` word and returns without
+// publishing, so every wave always exits and the shared result flag only ever
+// holds sequence numbers.
 constexpr int kHandMax = 2048;
 
 template <int NV>
@@ -793,7 +794,8 @@ static __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restri
     v[0][i] = ld_q(a, i);
     if constexpr (NV > 1) v[1][i] = ld_q(b, i);
   }
-  const int levels = k > 0 ? k : 1;
+  __syncthreads();  // the vectors are in LDS (k = 0: the loop below does not run)
+  const int levels = k;
   uint32_t spins = 0;  // thread 0's polls, over every level
   int avail = 0;
   uint32_t l = len;
@@ -827,7 +829,6 @@ static __global__ void __launch_bounds__(kBlock) k_handover(const qm31* __restri
       avail = sh_avail;
       if (avail < 0) return;
     }
-    if (r >= k) break;
     const uint32_t h = l / 2;
     const qm31 al = sh_al[r];
     for (uint32_t i = threadIdx.x; i < h; i += blockDim.x)
