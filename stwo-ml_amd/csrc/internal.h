@@ -238,6 +238,7 @@ struct gkr_ctx {
   std::set<gkr_qvec*> qvecs;       // live QM31 vectors; detached likewise
   uint64_t mult_zero_entries = 0;  // leading entries of S_MULT known to be zero once the queued work is done
   std::map<uint64_t, uint32_t*> dev_tables;  // (tag << 32 | log) -> resident device copy of the table outputs
+  std::map<uint64_t, felt> table_commitments;  // (tag << 32 | log) -> poseidon_hash_many([tag, log])
   MerkleConsts* merkle_consts = nullptr;  // device copy, built on first use
   bool fb_pending = false;  // f_b of the last restriction still as column-chunk partials (S_COLPART)
   uint64_t fb_rows = 0, fb_pk = 0;

@@ -591,6 +591,10 @@ static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__
 #pragma unroll
   for (int i = 0; i < NA; i++) acc[i].zero();
   __shared__ qm31 shv[kBlock];  // the wave's folded values, for the products of a lane group
+  // KIND 1, long vectors: when the stride of a thread's x is a multiple of
+  // 2^eq_h, all its x share one low eq index, so the thread weights by
+  // hi[x >> eq_h] alone and multiplies its sums by that lo value at the end
+  const bool lo_fixed = KIND == 1 && !S::SIDES && (groups & ((1ull << eq_h) - 1)) == 0;
   for (uint64_t x = ((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / LX; x < nb; x += groups) {
     const uint64_t pos = (uint64_t)c * nb + x;
     if constexpr (KIND == 2) {
@@ -609,7 +613,7 @@ static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__
       if (db) st_q(db, pos, b);
       if constexpr (KIND == 1) {
         const uint64_t mask = (1ull << eq_h) - 1;
-        a = qm31_mul(a, qm31_mul(ld_q(eq_hi, x >> eq_h), ld_q(eq_lo, x & mask)));
+        a = qm31_mul(a, lo_fixed ? ld_q(eq_hi, x >> eq_h) : qm31_mul(ld_q(eq_hi, x >> eq_h), ld_q(eq_lo, x & mask)));
       }
       // the group's G values of b through LDS (one 16-byte write, G broadcast reads)
       shv[threadIdx.x] = b;
@@ -651,10 +655,13 @@ static __global__ void __launch_bounds__(kBlock) k_trip(const qm31* __restrict__
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
   }
+  qm31 lo = qm31_one();  // this thread's lo value (a thread past nb added nothing: any value serves)
+  if (lo_fixed) lo = ld_q(eq_lo, (((uint64_t)blockIdx.x * blockDim.x + threadIdx.x) / LX) & ((1ull << eq_h) - 1));
   qm31 t[NA];
 #pragma unroll
   for (int i = 0; i < NA; i++) {
     t[i] = acc[i].reduce();
+    if (lo_fixed) t[i] = qm31_mul(t[i], lo);
     // add the 64 / LX lane groups: masks LX .. 32
     if constexpr (LX <= 1) t[i] = qm31_add_xor<1>(t[i]);
     if constexpr (LX <= 2) t[i] = qm31_add_xor<2>(t[i]);

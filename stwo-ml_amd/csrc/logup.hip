@@ -805,9 +805,15 @@ int prove_activation(gkr_ctx* c, const gkr_qm31* claim_point, uint32_t n_point, 
   out->mult_final_eval = G(mfin[0]);
   out->mult_claimed_sum = G(mult_sum);
 
-  // Table commitment = poseidon_hash_many([type_tag, log_size]) (prover.rs:8365-8373)
-  felt tc_in[2] = {felt_from_u64(tag), felt_from_u64(table_log)};
-  const felt tc = poseidon_hash_many(tc_in, 2);
+  // Table commitment = poseidon_hash_many([type_tag, log_size]) (prover.rs:8365-8373), a
+  // function of the table alone: hashed once per context and table
+  const uint64_t tkey = ((uint64_t)tag << 32) | table_log;
+  auto tci = c->table_commitments.find(tkey);
+  if (tci == c->table_commitments.end()) {
+    felt tc_in[2] = {felt_from_u64(tag), felt_from_u64(table_log)};
+    tci = c->table_commitments.emplace(tkey, poseidon_hash_many(tc_in, 2)).first;
+  }
+  const felt tc = tci->second;
   out->table_commitment = felt_to_abi(tc);
   C.mix_secure_field(input_eval);
   C.mix_secure_field(Q(*claim_value));
