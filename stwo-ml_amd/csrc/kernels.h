@@ -1699,6 +1699,9 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare(
 // of them per pass with every load in flight before the arithmetic.
 // ps.status given: launched ahead, gamma and beta are ps.vals[0], ps.vals[1];
 // when its wait ended without them the pass adds nothing but still delivers.
+#ifndef GKR_PREP_BATCH
+#define GKR_PREP_BATCH 2  // entries per thread and pass of k_logup_prepare_trip
+#endif
 template <int K>
 struct PrepTrip {
   static constexpr int G = 1 << K;
@@ -1713,7 +1716,7 @@ static __global__ void __launch_bounds__(kBlock) k_logup_prepare_trip(
     uint32_t* __restrict__ masked_out, qm31* __restrict__ d_out, qm31* __restrict__ w_out,
     uint32_t* __restrict__ mult, RoundSink sink, Posted ps) {
   constexpr int G = PrepTrip<K>::G, NQ = PrepTrip<K>::NQ;
-  constexpr int kBatch = 2;
+  constexpr int kBatch = GKR_PREP_BATCH;
   const bool go = ps.take2(&gamma, &beta);
   const uint64_t nb = n >> K;
   const uint64_t lo_mask = (1ull << eq_h) - 1, col_mask = (1ull << log_pcol) - 1;
