@@ -134,7 +134,10 @@ int gkr_ctx_reset_timing(gkr_ctx* ctx);
  *     challenges, as on an error; the call fails with GKR_ERR_DEVICE and the
  *     kernel ends on the cancel code;
  *   GKR_DEBUG_HANDOVER_EXPIRE: the kernel's bounded wait is `arg` polls and
- *     the host posts only after it expired; the call fails with GKR_ERR_DEVICE.
+ *     the host posts only after it expired; the call fails with GKR_ERR_DEVICE
+ *     (when the last trip has two or more rounds: the kernel folds all of its
+ *     levels but the last, which the host folds, so a last trip of one round
+ *     waits for nothing and the hook has no effect on it).
  *   GKR_DEBUG_TRIP_EXPIRE: the same for the next wait launched ahead of
  *     its values: a sumcheck trip's challenges, or an activation layer's
  *     gamma and beta when its first kernels were launched ahead (that wait

@@ -649,7 +649,8 @@ struct HandoverSession {
 // ------------------------------------------------------------------ multi-round trips (host side)
 // A sumcheck over 2^T entries runs as a few device trips of K <= 3 rounds
 // each (k_trip: one launch plus the finisher per trip), then k_handover
-// folds the last trip's vectors and the host finishes the rounds on vectors
+// folds the last trip's vectors by all of that trip's challenges but the last
+// (the host folds the last one) and the host finishes the rounds on vectors
 // of at most host_len entries.  The first trip covers min(k0, T) rounds;
 // later trips cover trip_k(n) rounds: a trip's sums cost 2^K products per
 // entry, so trips over long vectors (bound by HBM and VALU, not by launch
