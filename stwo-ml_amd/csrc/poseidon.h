@@ -289,7 +289,7 @@ class PoseidonChannel {
     return felt_to_qm31(s[0]);
   }
   void draw_qm31s(qm31* out, size_t n) {
-    if (n >= 4 && DrawPool::instance().run(digest, n_draws, n, draw_at, out)) {
+    if (n >= 2 && DrawPool::instance().run(digest, n_draws, n, draw_at, out)) {
       n_draws += (uint32_t)n;
       hash_count += n;
       return;
