@@ -374,7 +374,11 @@ __device__ __forceinline__ void finish_carried(const CarriedFinish& f) {
   __syncthreads();
   if (threadIdx.x == 0) publish_flag(f.sk.flag, f.sk.seq);
 }
-constexpr int kWaitBlock = 256;
+#ifndef GKR_WAIT_BLOCK
+#define GKR_WAIT_BLOCK 1024
+#endif
+// threads of k_mailbox_wait: one polls, all add the carried rows of the trip before it
+constexpr int kWaitBlock = GKR_WAIT_BLOCK;
 static __global__ void __launch_bounds__(kWaitBlock) k_mailbox_wait(TripWait tw, CarriedFinish fin) {
   if (fin.nblocks) finish_carried<kWaitBlock>(fin);  // the previous trip's sums first (the host needs them)
   if (threadIdx.x != 0) return;
